@@ -1,0 +1,278 @@
+"""ctypes binding of libgarfield.so (include/garfield.h)."""
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+lib_path = os.path.join(_HERE, "libgarfield.so")
+
+NO_RESULT = 0x7FFFFFFF
+NCOUNTERS = 8
+VEC_F32 = 0
+VEC_F16 = 1
+COUNTER_NAMES = ("expand", "dist", "attr", "cross", "lrow", "scan", "pass", "route")
+
+
+class GarfieldError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"garfield status {status}: {msg}")
+        self.status = status
+
+
+class _Paths(C.Structure):
+    _fields_ = [("data_path", C.c_char_p), ("cagra_prefix", C.c_char_p), ("cagra_suffix", C.c_char_p),
+                ("global_graph", C.c_char_p), ("grid", C.c_char_p), ("attrs", C.c_char_p),
+                ("cluster", C.c_char_p)]
+
+
+class _OpenOpts(C.Structure):
+    _fields_ = [("degree", C.c_uint32), ("f2h_factor", C.c_float), ("vec_dtype", C.c_int32),
+                ("hist_contiguous", C.c_int32), ("device", C.c_int32)]
+
+
+class _Host(C.Structure):
+    _fields_ = [("N", C.c_uint32), ("D", C.c_uint32), ("a", C.c_uint32), ("P", C.c_uint32),
+                ("R", C.c_uint32), ("E", C.c_uint32),
+                ("vectors", C.c_void_p), ("attrs", C.c_void_p), ("grid_shape", C.c_void_p),
+                ("l_q", C.c_void_p), ("r_q", C.c_void_p), ("global_pid", C.c_void_p),
+                ("cell_graphs", C.c_void_p), ("cross", C.c_void_p), ("labels", C.c_void_p)]
+
+
+class _Info(C.Structure):
+    _fields_ = [("N", C.c_uint32), ("D", C.c_uint32), ("a", C.c_uint32), ("P", C.c_uint32),
+                ("R", C.c_uint32), ("E", C.c_uint32), ("C", C.c_uint32), ("vec_dtype", C.c_uint32),
+                ("f2h_factor", C.c_float), ("device_bytes", C.c_uint64)]
+
+
+class _SearchOpts(C.Structure):
+    _fields_ = [("L", C.c_uint32), ("K", C.c_uint32), ("rl", C.c_uint32), ("postfilter", C.c_uint32),
+                ("entry_points", C.c_void_p)]
+
+
+class SearchStats(C.Structure):
+    _fields_ = [("ms_traverse", C.c_double), ("ms_bruteforce", C.c_double), ("ms_total", C.c_double),
+                ("q_traverse", C.c_uint32), ("q_bruteforce", C.c_uint32), ("q_empty", C.c_uint32),
+                ("n_expand", C.c_uint64), ("n_dist", C.c_uint64), ("n_attr", C.c_uint64),
+                ("n_cross", C.c_uint64), ("n_lrow", C.c_uint64), ("n_scan", C.c_uint64),
+                ("n_pass", C.c_uint64), ("bytes_traverse", C.c_double), ("bytes_bruteforce", C.c_double)]
+
+    def as_dict(self):
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+_SYMBOLS = {
+    "gf_index_open": [C.POINTER(_Paths), C.POINTER(_OpenOpts), C.POINTER(C.c_void_p)],
+    "gf_index_create": [C.POINTER(_Host), C.POINTER(_OpenOpts), C.POINTER(C.c_void_p)],
+    "gf_index_close": [C.c_void_p],
+    "gf_index_get_info": [C.c_void_p, C.POINTER(_Info)],
+    "gf_batch_create": [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p)],
+    "gf_batch_free": [C.c_void_p],
+    "gf_mark_cells": [C.c_void_p, C.c_float, C.POINTER(C.c_double)],
+    "gf_order_cells": [C.c_void_p, C.c_uint32, C.POINTER(C.c_double)],
+    "gf_search": [C.c_void_p, C.POINTER(_SearchOpts), C.c_void_p, C.c_void_p, C.POINTER(SearchStats)],
+    "gf_batch_get_cells": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
+    "gf_batch_set_cells": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
+    "gf_batch_get_centroid": [C.c_void_p, C.c_void_p, C.c_void_p],
+    "gf_batch_get_counters": [C.c_void_p, C.c_void_p],
+    "gf_f2h": [C.c_void_p, C.c_size_t, C.c_float, C.c_void_p],
+    "gf_row_norms_f16": [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p],
+    "gf_entry_points": [C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p],
+    "gf_status_str": [C.c_int32],
+    "gf_last_error": [],
+}
+
+_lib = None
+
+
+def load():
+    """Load libgarfield.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(lib_path):
+            raise ImportError(f"{lib_path} is missing: run __graft_entry__.build() "
+                              "or python garfield_amd/build.py")
+        lib = C.CDLL(lib_path)
+        for name, args in _SYMBOLS.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = C.c_char_p if name in ("gf_status_str", "gf_last_error") else C.c_int32
+        _lib = lib
+    return _lib
+
+
+def _check(status):
+    if status != 0:
+        lib = load()
+        raise GarfieldError(status, lib.gf_last_error().decode(errors="replace"))
+
+
+def _ptr(a):
+    return a.ctypes.data_as(C.c_void_p) if a is not None else None
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def _opts(degree, f2h_factor, vec_dtype, hist_contiguous, device):
+    return _OpenOpts(degree=degree, f2h_factor=f2h_factor, vec_dtype=vec_dtype,
+                     hist_contiguous=int(hist_contiguous), device=device)
+
+
+class Index:
+    """A GMG index resident on one GPU."""
+
+    def __init__(self, handle):
+        self._h = handle
+        info = _Info()
+        _check(load().gf_index_get_info(self._h, C.byref(info)))
+        self.N, self.D, self.a, self.P = info.N, info.D, info.a, info.P
+        self.R, self.E, self.C = info.R, info.E, info.C
+        self.vec_dtype, self.f2h_factor = info.vec_dtype, info.f2h_factor
+        self.device_bytes = info.device_bytes
+
+    @classmethod
+    def open(cls, data_path, cagra_prefix, cagra_suffix, global_graph, grid, attrs, cluster=None,
+             degree=0, f2h_factor=1.0, vec_dtype=VEC_F32, hist_contiguous=False, device=0):
+        enc = lambda s: None if s is None else str(s).encode()
+        paths = _Paths(enc(data_path), enc(cagra_prefix), enc(cagra_suffix), enc(global_graph),
+                       enc(grid), enc(attrs), enc(cluster))
+        h = C.c_void_p()
+        _check(load().gf_index_open(C.byref(paths), C.byref(_opts(degree, f2h_factor, vec_dtype,
+                                                                    hist_contiguous, device)), C.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def from_arrays(cls, vectors, attrs, grid_shape, l_q, r_q, global_pid, cell_graphs, cross,
+                    labels=None, f2h_factor=1.0, vec_dtype=VEC_F32, hist_contiguous=False, device=0,
+                    degree=0):
+        """Arrays as in the files: vectors (N,D) point order, cell_graphs (N,R)
+        concatenated per cell in cell order, cross (N, P*E) point order."""
+        keep = dict(
+            vectors=_c(vectors, np.float32), attrs=_c(attrs, np.float32),
+            grid=_c(grid_shape, np.uint32), l_q=_c(l_q, np.float32), r_q=_c(r_q, np.float32),
+            pid=_c(global_pid, np.uint32), graphs=_c(cell_graphs, np.uint32), cross=_c(cross, np.uint32),
+            labels=None if labels is None else _c(labels, np.int32))
+        N, D = keep["vectors"].shape
+        a = keep["attrs"].shape[1]
+        P = int(np.prod(keep["grid"]))
+        R = keep["graphs"].shape[1]
+        E = keep["cross"].shape[1] // P
+        host = _Host(N, D, a, P, R, E, _ptr(keep["vectors"]), _ptr(keep["attrs"]), _ptr(keep["grid"]),
+                     _ptr(keep["l_q"]), _ptr(keep["r_q"]), _ptr(keep["pid"]), _ptr(keep["graphs"]),
+                     _ptr(keep["cross"]), _ptr(keep["labels"]))
+        h = C.c_void_p()
+        _check(load().gf_index_create(C.byref(host), C.byref(_opts(degree, f2h_factor, vec_dtype,
+                                                                     hist_contiguous, device)), C.byref(h)))
+        return cls(h)
+
+    def close(self):
+        if self._h:
+            _check(load().gf_index_close(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def batch(self, queries, lo, hi):
+        return Batch(self, queries, lo, hi)
+
+
+class Batch:
+    """A query batch (vectors + closed ranges) on the index's GPU."""
+
+    def __init__(self, index, queries, lo, hi):
+        self.index = index
+        q = _c(queries, np.float32)
+        lo = _c(lo, np.float32)
+        hi = _c(hi, np.float32)
+        if q.ndim != 2 or q.shape[1] != index.D:
+            raise ValueError("queries must be (Q, D)")
+        if lo.shape != (q.shape[0], index.a) or hi.shape != lo.shape:
+            raise ValueError("lo/hi must be (Q, a)")
+        self.Q = q.shape[0]
+        self._topc = 0
+        h = C.c_void_p()
+        _check(load().gf_batch_create(index._h, _ptr(q), self.Q, _ptr(lo), _ptr(hi), C.byref(h)))
+        self._h = h
+
+    def close(self):
+        if self._h:
+            _check(load().gf_batch_free(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def mark_cells(self, prefilter):
+        ms = C.c_double()
+        _check(load().gf_mark_cells(self._h, float(prefilter), C.byref(ms)))
+        return ms.value
+
+    def order_cells(self, topc=4):
+        ms = C.c_double()
+        _check(load().gf_order_cells(self._h, int(topc), C.byref(ms)))
+        self._topc = topc
+        return ms.value
+
+    def search(self, L, K=10, rl=10, postfilter=1 << 30, entry_points=None):
+        ids = np.empty((self.Q, K), np.uint32)
+        dists = np.empty((self.Q, K), np.float32)
+        ent = None if entry_points is None else _c(entry_points, np.uint32)
+        opts = _SearchOpts(L, K, rl, min(int(postfilter), 0xFFFFFFFF), _ptr(ent))
+        st = SearchStats()
+        _check(load().gf_search(self._h, C.byref(opts), _ptr(ids), _ptr(dists), C.byref(st)))
+        return ids, dists, st
+
+    def get_cells(self):
+        P = self.index.P
+        cells = np.empty((self.Q, P), np.uint32)
+        counts = np.empty(self.Q, np.uint32)
+        little = np.empty(self.Q, np.uint32)
+        sel = np.empty(self.Q, np.uint32)
+        _check(load().gf_batch_get_cells(self._h, _ptr(cells), _ptr(counts), _ptr(little), _ptr(sel)))
+        return cells, counts, little, sel
+
+    def set_cells(self, cells, counts, little):
+        cells = _c(cells, np.uint32)
+        counts = _c(counts, np.uint32)
+        little = _c(little, np.uint32)
+        _check(load().gf_batch_set_cells(self._h, _ptr(cells), _ptr(counts), _ptr(little)))
+
+    def get_centroid(self):
+        dist = np.empty((self.Q, self.index.C), np.float32)
+        topk = np.empty((self.Q, self._topc), np.uint32)
+        _check(load().gf_batch_get_centroid(self._h, _ptr(dist), _ptr(topk)))
+        return dist, topk
+
+    def get_counters(self):
+        c = np.empty((self.Q, NCOUNTERS), np.uint32)
+        _check(load().gf_batch_get_counters(self._h, _ptr(c)))
+        return c
+
+
+def f2h(x, alpha=1.0):
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    _check(load().gf_f2h(_ptr(x), x.size, float(alpha), _ptr(out)))
+    return out
+
+
+def row_norms_f16(x):
+    x = _c(x, np.uint16)
+    out = np.empty(x.shape[0], np.float32)
+    _check(load().gf_row_norms_f16(_ptr(x), x.shape[0], x.shape[1], _ptr(out)))
+    return out
+
+
+def entry_points(N, P, R):
+    out = np.empty(R, np.uint32)
+    _check(load().gf_entry_points(N, P, R, _ptr(out)))
+    return out

@@ -1,0 +1,53 @@
+"""Build recipe for libgarfield.so (gfx950) and the garfield_search CLI.
+
+Everything is compiled in-tree with hipcc so the built files travel with the
+repository snapshot.  Packed-fp32 instructions are disabled for all device
+code (-packed-fp32-ops).
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libgarfield.so")
+CLI = os.path.join(HERE, "garfield_search")
+ARCH = os.environ.get("GF_OFFLOAD_ARCH", "gfx950")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+COMMON = [
+    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-deprecated-declarations", "-I", os.path.join(ROOT, "include"),
+]
+LIB_SOURCES = ["gf_kernels.hip", "gf_host.cpp", "gf_io.cpp"]
+OBJ_DIR = os.path.join(HERE, "_build")
+
+
+def _run(cmd):
+    print("+", " ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def build(verbose=True):
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    objs = []
+    for src in LIB_SOURCES:
+        obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
+        lang = ["-x", "hip"]
+        _run([HIPCC, *COMMON, *lang, "-c", os.path.join(CSRC, src), "-o", obj])
+        objs.append(obj)
+    tmp = LIB + ".tmp"
+    _run([HIPCC, *COMMON, "-shared", *objs, "-o", tmp])
+    os.replace(tmp, LIB)
+    cli_src = os.path.join(CSRC, "gf_cli.cpp")
+    if os.path.exists(cli_src):
+        _run([HIPCC, *COMMON, "-x", "hip", cli_src, "-o", CLI, "-L", HERE, "-lgarfield",
+              "-Wl,-rpath,$ORIGIN"])
+    return LIB
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

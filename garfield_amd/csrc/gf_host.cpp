@@ -1,0 +1,732 @@
+// Host side of libgarfield.so: the C ABI declared in include/garfield.h.
+//
+// gf_index_create lays every per-point array out cell-major on the device
+// (row offset[c] + l is the l-th point of cell c in ascending point id order,
+// the reference's get_idx_mapper order, tools.cuh:862-915), validates every
+// id the kernels will dereference, and precomputes the cluster centres and
+// the cell x cluster histogram (tools.cuh:569-602).  The three stage calls
+// mirror the reference's host functions; see the header for the citations.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <numeric>
+#include <random>
+#include <string>
+#include <unordered_set>
+#include <vector>
+
+#include "gf_internal.h"
+
+using gf::Error;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+#define GF_HIP(x)                                                                              \
+    do {                                                                                       \
+        hipError_t e_ = (x);                                                                   \
+        if (e_ != hipSuccess)                                                                  \
+            throw Error{GF_E_DEVICE, std::string(#x) + ": " + hipGetErrorString(e_)};          \
+    } while (0)
+
+#define GF_REQUIRE(cond, code, msg)                  \
+    do {                                             \
+        if (!(cond)) throw Error{(code), (msg)};     \
+    } while (0)
+
+// Owning device buffer.
+template <typename T>
+struct DevBuf {
+    T* p = nullptr;
+    size_t n = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    ~DevBuf() { release(); }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    void alloc(size_t count) {
+        if (count == n && p) return;
+        release();
+        if (count == 0) return;
+        hipError_t e = hipMalloc(&p, count * sizeof(T));
+        if (e != hipSuccess) {
+            p = nullptr;
+            throw Error{GF_E_NOMEM, "hipMalloc of " + std::to_string(count * sizeof(T)) + " bytes failed"};
+        }
+        n = count;
+    }
+    void upload(const T* src, size_t count) {
+        alloc(count);
+        if (count) GF_HIP(hipMemcpy(p, src, count * sizeof(T), hipMemcpyHostToDevice));
+    }
+    void upload(const std::vector<T>& v) { upload(v.data(), v.size()); }
+    size_t bytes() const { return n * sizeof(T); }
+};
+
+uint32_t round_up(uint32_t x, uint32_t m) { return (x + m - 1) / m * m; }
+
+gf_status run_guarded(const std::function<void()>& fn);
+
+}  // namespace
+
+struct gf_index {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    uint32_t N = 0, D = 0, a = 0, P = 0, R = 0, E = 0, C = 0;
+    int32_t vdtype = GF_VEC_F32;
+    float alpha = 1.0f;
+    gf::RowShape rs{};
+    uint32_t rowbytes = 0, Cp = 0, Dp = 0;
+    std::vector<uint32_t> offset_h, grid_h;
+    DevBuf<char> vec;
+    DevBuf<float> attrs, l_q, r_q, cnorm;
+    DevBuf<uint32_t> graph, cross, offset, gidx, lrow, grid, doff, hist;
+    DevBuf<uint32_t> tile_cell, tile_row0, tile_n;
+    DevBuf<uint16_t> centres;
+    uint32_t ntiles = 0;
+    ~gf_index() {
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+    uint64_t device_bytes() const {
+        return vec.bytes() + attrs.bytes() + l_q.bytes() + r_q.bytes() + cnorm.bytes() + graph.bytes() +
+               cross.bytes() + offset.bytes() + gidx.bytes() + lrow.bytes() + grid.bytes() + doff.bytes() +
+               hist.bytes() + tile_cell.bytes() + tile_row0.bytes() + tile_n.bytes() + centres.bytes();
+    }
+};
+
+struct gf_batch {
+    gf_index* ix = nullptr;
+    uint32_t Q = 0, Qp = 0, topc = 0;
+    bool marked = false;
+    DevBuf<float> qf32, qnorm, lo, hi, cdist, out_dist;
+    DevBuf<uint16_t> q16, q16v;
+    DevBuf<uint32_t> cells, counts, little, selcount, cellq, ccount, cstart, cfill, topk;
+    DevBuf<uint32_t> out_ids, counters, sched, entry;
+};
+
+namespace {
+
+gf_status run_guarded(const std::function<void()>& fn) {
+    try {
+        fn();
+        return GF_OK;
+    } catch (const Error& e) {
+        g_last_error = e.msg;
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        g_last_error = "host allocation failed";
+        return GF_E_NOMEM;
+    } catch (const std::exception& e) {
+        g_last_error = e.what();
+        return GF_E_ARG;
+    }
+}
+
+struct Timer {
+    hipEvent_t a = nullptr, b = nullptr;
+    hipStream_t s;
+    explicit Timer(hipStream_t st) : s(st) {
+        GF_HIP(hipEventCreate(&a));
+        GF_HIP(hipEventCreate(&b));
+        GF_HIP(hipEventRecord(a, s));
+    }
+    double stop() {
+        GF_HIP(hipEventRecord(b, s));
+        GF_HIP(hipEventSynchronize(b));
+        float ms = 0;
+        GF_HIP(hipEventElapsedTime(&ms, a, b));
+        return ms;
+    }
+    ~Timer() {
+        if (a) (void)hipEventDestroy(a);
+        if (b) (void)hipEventDestroy(b);
+    }
+};
+
+void set_device(const gf_index* ix) { GF_HIP(hipSetDevice(ix->device)); }
+
+void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix) {
+    GF_REQUIRE(h.N > 0 && h.D > 0, GF_E_ARG, "N and D must be positive");
+    GF_REQUIRE(h.a >= 1 && h.a <= gf::kMaxAttr, GF_E_UNSUPPORTED, "attribute count must be in [1, 8]");
+    GF_REQUIRE(h.R >= 1 && h.R <= 64, GF_E_UNSUPPORTED, "graph degree must be in [1, 64]");
+    GF_REQUIRE(h.E >= 1 && h.E <= gf::kMaxE, GF_E_UNSUPPORTED, "cross edges per cell must be in [1, 4]");
+    GF_REQUIRE(h.N < (1u << 30), GF_E_UNSUPPORTED, "at most 2^30 points");
+    GF_REQUIRE(h.vectors && h.attrs && h.grid_shape && h.l_q && h.r_q && h.global_pid && h.cell_graphs && h.cross,
+               GF_E_ARG, "missing index array");
+    ix.device = opts ? opts->device : 0;
+    ix.vdtype = opts ? opts->vec_dtype : GF_VEC_F32;
+    ix.alpha = (opts && opts->f2h_factor != 0.0f) ? opts->f2h_factor : 1.0f;
+    GF_REQUIRE(ix.vdtype == GF_VEC_F32 || ix.vdtype == GF_VEC_F16, GF_E_ARG, "vec_dtype must be GF_VEC_F32 or GF_VEC_F16");
+    GF_REQUIRE(!(opts && opts->degree) || opts->degree == h.R, GF_E_FORMAT, "--degree does not match the graph files");
+    const uint32_t elems = ix.vdtype == GF_VEC_F16 ? 8u : 4u;
+    GF_REQUIRE(h.D % elems == 0, GF_E_UNSUPPORTED, "D must be a multiple of 4 (fp32) or 8 (fp16)");
+    ix.rs = gf::row_shape(h.D, ix.vdtype == GF_VEC_F16);
+    GF_REQUIRE(ix.rs.cpl <= (ix.rs.f16 ? 2u : 4u), GF_E_UNSUPPORTED, "D too large for this build");
+
+    const uint32_t N = h.N, D = h.D, a = h.a, R = h.R, E = h.E;
+    uint64_t P64 = 1;
+    for (uint32_t d = 0; d < a; ++d) {
+        GF_REQUIRE(h.grid_shape[d] >= 1, GF_E_FORMAT, "empty grid dimension");
+        P64 *= h.grid_shape[d];
+    }
+    GF_REQUIRE(P64 == h.P, GF_E_FORMAT, "grid shape product differs from P");
+    GF_REQUIRE(P64 <= 4096, GF_E_UNSUPPORTED, "at most 4096 cells");
+    const uint32_t P = uint32_t(P64);
+    ix.N = N; ix.D = D; ix.a = a; ix.P = P; ix.R = R; ix.E = E;
+
+    // idx mapper (tools.cuh:862-915)
+    std::vector<uint32_t> size(P, 0), fill(P, 0), gidx(N), lrow(N), local(N);
+    for (uint32_t i = 0; i < N; ++i) {
+        GF_REQUIRE(h.global_pid[i] < P, GF_E_FORMAT, "global_pid out of range");
+        size[h.global_pid[i]]++;
+    }
+    ix.offset_h.assign(P + 1, 0);
+    for (uint32_t c = 0; c < P; ++c) {
+        GF_REQUIRE(size[c] > 0, GF_E_UNSUPPORTED, "empty cell " + std::to_string(c));
+        ix.offset_h[c + 1] = ix.offset_h[c] + size[c];
+    }
+    for (uint32_t i = 0; i < N; ++i) {
+        const uint32_t c = h.global_pid[i];
+        const uint32_t r = ix.offset_h[c] + fill[c];
+        gidx[r] = i;
+        lrow[r] = fill[c];
+        local[i] = fill[c]++;
+    }
+    // Every id the kernels dereference is checked here once.
+    for (uint32_t c = 0; c < P; ++c)
+        for (size_t k = size_t(ix.offset_h[c]) * R; k < size_t(ix.offset_h[c + 1]) * R; ++k)
+            GF_REQUIRE(h.cell_graphs[k] < size[c], GF_E_FORMAT,
+                       "per-cell graph " + std::to_string(c) + " holds an id beyond the cell");
+    std::vector<uint32_t> cross_cm(size_t(N) * P * E);
+    for (uint32_t r = 0; r < N; ++r) {
+        const uint32_t* src = h.cross + size_t(gidx[r]) * P * E;
+        for (uint32_t c = 0; c < P; ++c)
+            for (uint32_t e = 0; e < E; ++e) {
+                const uint32_t v = src[c * E + e];
+                GF_REQUIRE(v < size[c], GF_E_FORMAT, "cross-cell graph holds an id beyond its cell");
+                cross_cm[(size_t(r) * P + c) * E + e] = v;
+            }
+    }
+    // All ids are validated; from here on the device is used.
+    GF_HIP(hipSetDevice(ix.device));
+    GF_HIP(hipStreamCreateWithFlags(&ix.stream, hipStreamNonBlocking));
+    ix.cross.upload(cross_cm);
+    std::vector<uint32_t>().swap(cross_cm);
+    ix.graph.upload(h.cell_graphs, size_t(N) * R);
+    ix.offset.upload(ix.offset_h);
+    ix.gidx.upload(gidx);
+    ix.lrow.upload(lrow);
+    {
+        std::vector<float> at(size_t(N) * a);
+        for (uint32_t r = 0; r < N; ++r)
+            for (uint32_t d = 0; d < a; ++d) at[size_t(r) * a + d] = h.attrs[size_t(gidx[r]) * a + d];
+        ix.attrs.upload(at);
+    }
+    {
+        std::vector<float> v(size_t(N) * D);
+        for (uint32_t r = 0; r < N; ++r)
+            std::memcpy(&v[size_t(r) * D], h.vectors + size_t(gidx[r]) * D, sizeof(float) * D);
+        if (ix.vdtype == GF_VEC_F32) {
+            ix.vec.upload(reinterpret_cast<const char*>(v.data()), v.size() * sizeof(float));
+            ix.rowbytes = D * 4;
+        } else {
+            DevBuf<float> tmp;
+            tmp.upload(v);
+            ix.vec.alloc(v.size() * sizeof(uint16_t));
+            GF_HIP(gf::launch_f2h(tmp.p, reinterpret_cast<uint16_t*>(ix.vec.p), v.size(), ix.alpha, ix.stream));
+            GF_HIP(hipStreamSynchronize(ix.stream));
+            ix.rowbytes = D * 2;
+        }
+    }
+    // Grid (real_dataset_adapter.cuh:563-619).
+    uint32_t gsum = 0;
+    std::vector<uint32_t> doff(a);
+    ix.grid_h.assign(h.grid_shape, h.grid_shape + a);
+    for (uint32_t d = 0; d < a; ++d) { doff[d] = gsum; gsum += h.grid_shape[d]; }
+    ix.l_q.upload(h.l_q, gsum);
+    ix.r_q.upload(h.r_q, gsum);
+    ix.grid.upload(ix.grid_h);
+    ix.doff.upload(doff);
+    // Selectivity tiles: kSelTile rows of one cell each.
+    {
+        std::vector<uint32_t> tc, tr, tn;
+        for (uint32_t c = 0; c < P; ++c)
+            for (uint32_t r = ix.offset_h[c]; r < ix.offset_h[c + 1]; r += gf::kSelTile) {
+                tc.push_back(c);
+                tr.push_back(r);
+                tn.push_back(std::min(gf::kSelTile, ix.offset_h[c + 1] - r));
+            }
+        ix.ntiles = uint32_t(tc.size());
+        ix.tile_cell.upload(tc);
+        ix.tile_row0.upload(tr);
+        ix.tile_n.upload(tn);
+    }
+    // Cluster centres + cell x cluster histogram (tools.cuh:569-602).
+    if (h.labels) {
+        int32_t cmax = -1;
+        for (uint32_t i = 0; i < N; ++i) {
+            GF_REQUIRE(h.labels[i] >= 0, GF_E_FORMAT, "negative cluster label");
+            cmax = std::max(cmax, h.labels[i]);
+        }
+        const uint32_t C = uint32_t(cmax) + 1;
+        GF_REQUIRE(C <= (1u << 20), GF_E_UNSUPPORTED, "too many clusters");
+        const bool contiguous = opts && opts->hist_contiguous;
+        const uint32_t avg = (N + P - 1) / P;
+        std::vector<float> cen(size_t(C) * D, 0.0f);
+        std::vector<uint32_t> num(C, 0), hist(size_t(P) * C, 0);
+        for (uint32_t i = 0; i < N; ++i) {
+            const uint32_t cid = uint32_t(h.labels[i]);
+            const uint32_t pid = contiguous ? std::min(i / avg, P - 1) : h.global_pid[i];
+            num[cid]++;
+            hist[size_t(pid) * C + cid]++;
+            const float* x = h.vectors + size_t(i) * D;
+            float* y = &cen[size_t(cid) * D];
+            for (uint32_t j = 0; j < D; ++j) y[j] += x[j];
+        }
+        for (uint32_t c = 0; c < C; ++c)
+            for (uint32_t j = 0; j < D; ++j) cen[size_t(c) * D + j] /= float(num[c]);
+        ix.C = C;
+        ix.Dp = round_up(D, 32);
+        ix.Cp = round_up(C, 64);
+        DevBuf<float> tmp;
+        tmp.upload(cen);
+        ix.centres.alloc(size_t(ix.Cp) * ix.Dp);
+        GF_HIP(gf::launch_f2h_pad(tmp.p, C, D, ix.centres.p, ix.Cp, ix.Dp, ix.alpha, ix.stream));
+        ix.cnorm.alloc(ix.Cp);
+        GF_HIP(gf::launch_norms_f16(ix.centres.p, ix.Cp, ix.Dp, ix.Dp, ix.cnorm.p, ix.stream));
+        GF_HIP(hipStreamSynchronize(ix.stream));
+        ix.hist.upload(hist);
+    }
+}
+
+void ensure_out(gf_batch& b, uint32_t K) {
+    const size_t n = size_t(b.Q) * K;
+    if (b.out_ids.n < n) { b.out_ids.alloc(n); b.out_dist.alloc(n); }
+    if (b.counters.n < size_t(b.Q) * GF_NCOUNTERS) b.counters.alloc(size_t(b.Q) * GF_NCOUNTERS);
+}
+
+uint32_t next_pow2(uint32_t x) {
+    uint32_t p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+
+void entry_points_ref(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
+    const uint32_t avg = (N + P - 1) / P;
+    const uint32_t rand_max = N - (P - 1) * avg;
+    GF_REQUIRE(rand_max >= 1, GF_E_ARG, "no room for entry points");
+    std::mt19937 rng;
+    std::uniform_int_distribution<> intd(0, int(rand_max) - 1);
+    const uint32_t want = std::min<uint32_t>(R * 10, rand_max);
+    std::vector<unsigned> v(want);
+    std::unordered_set<unsigned> seen;
+    uint32_t k = 0;
+    while (k < want) {
+        const unsigned t = unsigned(intd(rng));
+        if (!seen.count(t)) { seen.insert(t); v[k++] = t; }
+    }
+    std::srand(1);
+    std::random_shuffle(v.begin(), v.begin() + want);
+    for (uint32_t j = 0; j < R; ++j) out[j] = j < want ? v[j] : j;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* gf_status_str(gf_status s) {
+    switch (s) {
+        case GF_OK: return "ok";
+        case GF_E_ARG: return "invalid argument";
+        case GF_E_IO: return "i/o error";
+        case GF_E_FORMAT: return "bad index format";
+        case GF_E_DEVICE: return "device error";
+        case GF_E_NOMEM: return "out of memory";
+        case GF_E_UNSUPPORTED: return "unsupported";
+        case GF_E_STATE: return "call out of order";
+        default: return "unknown status";
+    }
+}
+
+const char* gf_last_error(void) { return g_last_error.c_str(); }
+
+gf_status gf_index_create(const gf_index_host* host, const gf_open_opts* opts, gf_index** out) {
+    return run_guarded([&] {
+        GF_REQUIRE(host && out, GF_E_ARG, "null argument");
+        *out = nullptr;
+        std::unique_ptr<gf_index> ix(new gf_index());
+        build_index(*host, opts, *ix);
+        *out = ix.release();
+    });
+}
+
+gf_status gf_index_open(const gf_index_paths* paths, const gf_open_opts* opts, gf_index** out) {
+    return run_guarded([&] {
+        GF_REQUIRE(paths && out, GF_E_ARG, "null argument");
+        *out = nullptr;
+        gf::HostIndex hi;
+        gf::read_index_files(*paths, opts ? opts->degree : 0, hi);
+        gf_index_host h{};
+        h.N = hi.N; h.D = hi.D; h.a = hi.a; h.P = hi.P; h.R = hi.R; h.E = hi.E;
+        h.vectors = hi.vectors.data();
+        h.attrs = hi.attrs.data();
+        h.grid_shape = hi.grid.data();
+        h.l_q = hi.l_q.data();
+        h.r_q = hi.r_q.data();
+        h.global_pid = hi.global_pid.data();
+        h.cell_graphs = hi.cell_graphs.data();
+        h.cross = hi.cross.data();
+        h.labels = hi.has_labels ? hi.labels.data() : nullptr;
+        std::unique_ptr<gf_index> ix(new gf_index());
+        build_index(h, opts, *ix);
+        *out = ix.release();
+    });
+}
+
+gf_status gf_index_close(gf_index* ix) {
+    return run_guarded([&] {
+        if (!ix) return;
+        (void)hipSetDevice(ix->device);
+        delete ix;
+    });
+}
+
+gf_status gf_index_get_info(const gf_index* ix, gf_index_info* out) {
+    return run_guarded([&] {
+        GF_REQUIRE(ix && out, GF_E_ARG, "null argument");
+        out->N = ix->N; out->D = ix->D; out->a = ix->a; out->P = ix->P;
+        out->R = ix->R; out->E = ix->E; out->C = ix->C;
+        out->vec_dtype = uint32_t(ix->vdtype);
+        out->f2h_factor = ix->alpha;
+        out->device_bytes = ix->device_bytes();
+    });
+}
+
+gf_status gf_batch_create(gf_index* ix, const float* queries, uint32_t Q, const float* lo, const float* hi,
+                          gf_batch** out) {
+    return run_guarded([&] {
+        GF_REQUIRE(ix && queries && lo && hi && out, GF_E_ARG, "null argument");
+        GF_REQUIRE(Q > 0, GF_E_ARG, "empty batch");
+        *out = nullptr;
+        set_device(ix);
+        std::unique_ptr<gf_batch> b(new gf_batch());
+        b->ix = ix;
+        b->Q = Q;
+        b->Qp = round_up(Q, 16);
+        b->qf32.upload(queries, size_t(Q) * ix->D);
+        b->lo.upload(lo, size_t(Q) * ix->a);
+        b->hi.upload(hi, size_t(Q) * ix->a);
+        if (ix->vdtype == GF_VEC_F16) {
+            b->q16v.alloc(size_t(Q) * ix->D);
+            GF_HIP(gf::launch_f2h(b->qf32.p, b->q16v.p, size_t(Q) * ix->D, ix->alpha, ix->stream));
+        }
+        if (ix->C) {
+            b->q16.alloc(size_t(b->Qp) * ix->Dp);
+            GF_HIP(gf::launch_f2h_pad(b->qf32.p, Q, ix->D, b->q16.p, b->Qp, ix->Dp, ix->alpha, ix->stream));
+            b->qnorm.alloc(b->Qp);
+            GF_HIP(gf::launch_norms_f16(b->q16.p, b->Qp, ix->Dp, ix->Dp, b->qnorm.p, ix->stream));
+        }
+        b->cells.alloc(size_t(Q) * ix->P);
+        b->counts.alloc(Q);
+        b->little.alloc(Q);
+        b->selcount.alloc(Q);
+        b->cellq.alloc(size_t(Q) * ix->P);
+        b->ccount.alloc(ix->P);
+        b->cstart.alloc(ix->P);
+        b->cfill.alloc(ix->P);
+        GF_HIP(hipStreamSynchronize(ix->stream));
+        *out = b.release();
+    });
+}
+
+gf_status gf_batch_free(gf_batch* b) {
+    return run_guarded([&] {
+        if (!b) return;
+        (void)hipSetDevice(b->ix->device);
+        delete b;
+    });
+}
+
+gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms) {
+    return run_guarded([&] {
+        GF_REQUIRE(b, GF_E_ARG, "null batch");
+        gf_index* ix = b->ix;
+        set_device(ix);
+        hipStream_t st = ix->stream;
+        Timer t(st);
+        GF_HIP(gf::launch_cells(b->Q, ix->a, b->lo.p, b->hi.p, ix->grid.p, ix->doff.p, ix->l_q.p, ix->r_q.p,
+                                ix->P, b->cells.p, b->counts.p, st));
+        GF_HIP(hipMemsetAsync(b->ccount.p, 0, ix->P * sizeof(uint32_t), st));
+        GF_HIP(hipMemsetAsync(b->cfill.p, 0, ix->P * sizeof(uint32_t), st));
+        GF_HIP(hipMemsetAsync(b->selcount.p, 0, b->Q * sizeof(uint32_t), st));
+        GF_HIP(gf::launch_cellq_count(b->Q, ix->P, b->cells.p, b->counts.p, b->ccount.p, st));
+        GF_HIP(gf::launch_scan_small(b->ccount.p, ix->P, b->cstart.p, st));
+        GF_HIP(gf::launch_cellq_fill(b->Q, ix->P, b->cells.p, b->counts.p, b->cstart.p, b->cfill.p,
+                                     b->cellq.p, st));
+        GF_HIP(gf::launch_selcount(ix->ntiles, ix->tile_cell.p, ix->tile_row0.p, ix->tile_n.p, ix->attrs.p,
+                                   ix->a, b->cstart.p, b->ccount.p, b->cellq.p, b->lo.p, b->hi.p,
+                                   b->selcount.p, st));
+        GF_HIP(gf::launch_route(b->Q, ix->N, prefilter, b->selcount.p, b->counts.p, b->little.p, st));
+        const double el = t.stop();
+        if (ms) *ms = el;
+        b->marked = true;
+    });
+}
+
+gf_status gf_order_cells(gf_batch* b, uint32_t topc, double* ms) {
+    return run_guarded([&] {
+        GF_REQUIRE(b, GF_E_ARG, "null batch");
+        GF_REQUIRE(b->marked, GF_E_STATE, "gf_order_cells before gf_mark_cells");
+        GF_REQUIRE(topc >= 1 && topc <= 16, GF_E_ARG, "topc must be in [1, 16]");
+        gf_index* ix = b->ix;
+        set_device(ix);
+        if (!ix->C) { if (ms) *ms = 0.0; return; }
+        hipStream_t st = ix->stream;
+        if (!b->cdist.p) b->cdist.alloc(size_t(b->Q) * ix->C);
+        b->topk.alloc(size_t(b->Q) * topc);
+        b->topc = topc;
+        Timer t(st);
+        GF_HIP(gf::launch_centroid(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp, ix->Cp,
+                                   ix->Dp, b->cdist.p, st));
+        GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, b->cdist.p, ix->hist.p, b->cells.p, b->counts.p,
+                                b->topk.p, st));
+        const double el = t.stop();
+        if (ms) *ms = el;
+    });
+}
+
+gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, float* dists,
+                    gf_search_stats* stats) {
+    return run_guarded([&] {
+        GF_REQUIRE(b && opts && ids, GF_E_ARG, "null argument");
+        GF_REQUIRE(b->marked, GF_E_STATE, "gf_search before gf_mark_cells");
+        gf_index* ix = b->ix;
+        const uint32_t L = opts->L, K = opts->K, rl = opts->rl;
+        GF_REQUIRE(L >= 1 && L < (1u << 16), GF_E_ARG, "L must be in [1, 65535]");
+        GF_REQUIRE(K >= 1 && K <= 64, GF_E_ARG, "K must be in [1, 64]");
+        GF_REQUIRE(rl >= 1 && rl <= 16, GF_E_ARG, "rl must be in [1, 16]");
+        set_device(ix);
+        hipStream_t st = ix->stream;
+        const uint32_t Q = b->Q, R = ix->R;
+
+        // Entry points: the caller's, or the reference's draw.
+        std::vector<uint32_t> ent(R);
+        if (opts->entry_points) std::copy(opts->entry_points, opts->entry_points + R, ent.begin());
+        else entry_points_ref(ix->N, ix->P, R, ent.data());
+        b->entry.upload(ent);
+
+        // Schedule (gpu_graph.cu:12485-12493): traversal queries by descending
+        // cell count, then brute-force queries by descending cell count.
+        std::vector<uint32_t> cnt(Q), lit(Q);
+        GF_HIP(hipMemcpyAsync(cnt.data(), b->counts.p, Q * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+        GF_HIP(hipMemcpyAsync(lit.data(), b->little.p, Q * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+        GF_HIP(hipStreamSynchronize(st));
+        std::vector<uint32_t> tq, bq;
+        uint32_t nempty = 0;
+        for (uint32_t q = 0; q < Q; ++q) {
+            if (cnt[q] < opts->postfilter && cnt[q] != lit[q]) tq.push_back(q);
+            else if (lit[q] > 0) bq.push_back(q);
+            else ++nempty;
+        }
+        auto by_count = [&](uint32_t x, uint32_t y) { return cnt[x] != cnt[y] ? cnt[x] > cnt[y] : x < y; };
+        std::sort(tq.begin(), tq.end(), by_count);
+        std::sort(bq.begin(), bq.end(), by_count);
+        std::vector<uint32_t> sched(tq);
+        sched.insert(sched.end(), bq.begin(), bq.end());
+        if (sched.empty()) sched.push_back(0);
+        b->sched.upload(sched);
+        ensure_out(*b, K);
+
+        const uint32_t hsize = std::max<uint32_t>(256, next_pow2(2 * (L + gf::kXSlots + 4 * R)));
+        uint32_t hbits = 0;
+        while ((1u << hbits) < hsize) ++hbits;
+        const uint32_t Lpad = round_up(L, 2);
+        const uint32_t lds = Lpad * 8 + gf::kXSlots * 8 + 128 * 4 + hsize * 4;
+        GF_REQUIRE(lds <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
+
+        gf::TravArgs a{};
+        a.vec = ix->vec.p;
+        a.rowbytes = ix->rowbytes;
+        a.nch = ix->rs.nch;
+        a.attrs = ix->attrs.p;
+        a.graph = ix->graph.p;
+        a.cross = ix->cross.p;
+        a.offset = ix->offset.p;
+        a.gidx = ix->gidx.p;
+        a.lrow = ix->lrow.p;
+        if (ix->vdtype == GF_VEC_F16) {
+            a.queries = reinterpret_cast<const char*>(b->q16v.p);
+            a.qbytes = ix->D * 2;
+        } else {
+            a.queries = reinterpret_cast<const char*>(b->qf32.p);
+            a.qbytes = ix->D * 4;
+        }
+        a.lo = b->lo.p;
+        a.hi = b->hi.p;
+        a.cells = b->cells.p;
+        a.counts = b->counts.p;
+        a.little = b->little.p;
+        a.entry = b->entry.p;
+        a.out_ids = b->out_ids.p;
+        a.out_dist = b->out_dist.p;
+        a.counters = b->counters.p;
+        a.a = ix->a; a.P = ix->P; a.R = R; a.E = ix->E; a.L = L; a.K = K; a.rl = rl;
+        a.hbits = hbits;
+        a.Lpad = Lpad;
+
+        GF_HIP(hipMemsetAsync(b->counters.p, 0, size_t(Q) * GF_NCOUNTERS * sizeof(uint32_t), st));
+        GF_HIP(gf::launch_fill_results(b->out_ids.p, b->out_dist.p, Q * K, st));
+        hipEvent_t ev[3];
+        for (auto& e : ev) GF_HIP(hipEventCreate(&e));
+        GF_HIP(hipEventRecord(ev[0], st));
+        gf::TravArgs at = a;
+        at.sched = b->sched.p;
+        at.nsched = uint32_t(tq.size());
+        GF_HIP(gf::launch_traverse(ix->rs, at, lds, st));
+        GF_HIP(hipEventRecord(ev[1], st));
+        gf::TravArgs ab = a;
+        ab.sched = b->sched.p + tq.size();
+        ab.nsched = uint32_t(bq.size());
+        GF_HIP(gf::launch_bruteforce(ix->rs, ab, st));
+        GF_HIP(hipEventRecord(ev[2], st));
+        GF_HIP(hipEventSynchronize(ev[2]));
+        float t_tr = 0, t_bf = 0;
+        GF_HIP(hipEventElapsedTime(&t_tr, ev[0], ev[1]));
+        GF_HIP(hipEventElapsedTime(&t_bf, ev[1], ev[2]));
+        for (auto& e : ev) (void)hipEventDestroy(e);
+
+        GF_HIP(hipMemcpy(ids, b->out_ids.p, size_t(Q) * K * sizeof(uint32_t), hipMemcpyDeviceToHost));
+        if (dists) GF_HIP(hipMemcpy(dists, b->out_dist.p, size_t(Q) * K * sizeof(float), hipMemcpyDeviceToHost));
+        if (stats) {
+            std::vector<uint32_t> ctr(size_t(Q) * GF_NCOUNTERS);
+            GF_HIP(hipMemcpy(ctr.data(), b->counters.p, ctr.size() * sizeof(uint32_t), hipMemcpyDeviceToHost));
+            std::memset(stats, 0, sizeof(*stats));
+            stats->ms_traverse = t_tr;
+            stats->ms_bruteforce = t_bf;
+            stats->ms_total = double(t_tr) + double(t_bf);
+            stats->q_traverse = uint32_t(tq.size());
+            stats->q_bruteforce = uint32_t(bq.size());
+            stats->q_empty = nempty;
+            for (uint32_t q = 0; q < Q; ++q) {
+                const uint32_t* c = &ctr[size_t(q) * GF_NCOUNTERS];
+                stats->n_expand += c[gf::C_EXPAND];
+                stats->n_dist += c[gf::C_DIST];
+                stats->n_attr += c[gf::C_ATTR];
+                stats->n_cross += c[gf::C_CROSS];
+                stats->n_lrow += c[gf::C_LROW];
+                stats->n_scan += c[gf::C_SCAN];
+                stats->n_pass += c[gf::C_PASS];
+            }
+            // Algorithmic bytes: what each kernel must read from HBM given
+            // its counters (rows gathered, graph rows, attributes, cross-edge
+            // slices, local-id lookups) plus its result writes.
+            uint64_t t_dist = 0, b_dist = 0;
+            for (uint32_t q = 0; q < Q; ++q) {
+                const uint32_t* c = &ctr[size_t(q) * GF_NCOUNTERS];
+                if (c[gf::C_ROUTE] == 1) t_dist += c[gf::C_DIST];
+                else b_dist += c[gf::C_DIST];
+            }
+            stats->bytes_traverse = double(t_dist) * ix->rowbytes + double(stats->n_expand) * R * 4.0 +
+                                    double(stats->n_attr) * ix->a * 4.0 + double(stats->n_cross) * ix->E * 4.0 +
+                                    double(stats->n_lrow) * 4.0 + double(tq.size()) * (K * 8.0 + ix->P * 4.0);
+            stats->bytes_bruteforce = double(stats->n_scan) * ix->a * 4.0 + double(b_dist) * ix->rowbytes +
+                                      double(bq.size()) * (K * 8.0 + ix->P * 4.0);
+        }
+    });
+}
+
+gf_status gf_batch_get_cells(const gf_batch* b, uint32_t* cells, uint32_t* counts, uint32_t* little,
+                             uint32_t* selcount) {
+    return run_guarded([&] {
+        GF_REQUIRE(b, GF_E_ARG, "null batch");
+        GF_REQUIRE(b->marked, GF_E_STATE, "cells not marked");
+        set_device(b->ix);
+        const size_t Q = b->Q;
+        if (cells) GF_HIP(hipMemcpy(cells, b->cells.p, Q * b->ix->P * 4, hipMemcpyDeviceToHost));
+        if (counts) GF_HIP(hipMemcpy(counts, b->counts.p, Q * 4, hipMemcpyDeviceToHost));
+        if (little) GF_HIP(hipMemcpy(little, b->little.p, Q * 4, hipMemcpyDeviceToHost));
+        if (selcount) GF_HIP(hipMemcpy(selcount, b->selcount.p, Q * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+gf_status gf_batch_set_cells(gf_batch* b, const uint32_t* cells, const uint32_t* counts, const uint32_t* little) {
+    return run_guarded([&] {
+        GF_REQUIRE(b && cells && counts && little, GF_E_ARG, "null argument");
+        set_device(b->ix);
+        const uint32_t P = b->ix->P;
+        for (uint32_t q = 0; q < b->Q; ++q) {
+            GF_REQUIRE(counts[q] <= P && little[q] <= counts[q], GF_E_ARG, "cell count out of range");
+            for (uint32_t i = 0; i < counts[q]; ++i)
+                GF_REQUIRE(cells[size_t(q) * P + i] < P, GF_E_ARG, "cell id out of range");
+        }
+        const size_t Q = b->Q;
+        GF_HIP(hipMemcpy(b->cells.p, cells, Q * P * 4, hipMemcpyHostToDevice));
+        GF_HIP(hipMemcpy(b->counts.p, counts, Q * 4, hipMemcpyHostToDevice));
+        GF_HIP(hipMemcpy(b->little.p, little, Q * 4, hipMemcpyHostToDevice));
+        b->marked = true;
+    });
+}
+
+gf_status gf_batch_get_centroid(const gf_batch* b, float* dist, uint32_t* topc) {
+    return run_guarded([&] {
+        GF_REQUIRE(b, GF_E_ARG, "null batch");
+        GF_REQUIRE(b->cdist.p && b->topk.p, GF_E_STATE, "gf_order_cells has not run");
+        set_device(b->ix);
+        if (dist) GF_HIP(hipMemcpy(dist, b->cdist.p, size_t(b->Q) * b->ix->C * 4, hipMemcpyDeviceToHost));
+        if (topc) GF_HIP(hipMemcpy(topc, b->topk.p, size_t(b->Q) * b->topc * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+gf_status gf_batch_get_counters(const gf_batch* b, uint32_t* counters) {
+    return run_guarded([&] {
+        GF_REQUIRE(b && counters, GF_E_ARG, "null argument");
+        GF_REQUIRE(b->counters.p, GF_E_STATE, "gf_search has not run");
+        set_device(b->ix);
+        GF_HIP(hipMemcpy(counters, b->counters.p, size_t(b->Q) * GF_NCOUNTERS * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+gf_status gf_f2h(const float* x, size_t n, float alpha, uint16_t* out) {
+    return run_guarded([&] {
+        GF_REQUIRE(x && out, GF_E_ARG, "null argument");
+        if (!n) return;
+        DevBuf<float> dx;
+        DevBuf<uint16_t> dy;
+        dx.upload(x, n);
+        dy.alloc(n);
+        GF_HIP(gf::launch_f2h(dx.p, dy.p, n, alpha, nullptr));
+        GF_HIP(hipMemcpy(out, dy.p, n * 2, hipMemcpyDeviceToHost));
+    });
+}
+
+gf_status gf_row_norms_f16(const uint16_t* x, uint32_t n, uint32_t D, float* out) {
+    return run_guarded([&] {
+        GF_REQUIRE(x && out, GF_E_ARG, "null argument");
+        if (!n) return;
+        DevBuf<uint16_t> dx;
+        DevBuf<float> dy;
+        dx.upload(x, size_t(n) * D);
+        dy.alloc(n);
+        GF_HIP(gf::launch_norms_f16(dx.p, n, D, D, dy.p, nullptr));
+        GF_HIP(hipMemcpy(out, dy.p, size_t(n) * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+gf_status gf_entry_points(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
+    return run_guarded([&] {
+        GF_REQUIRE(out && P >= 1 && N >= P, GF_E_ARG, "invalid arguments");
+        entry_points_ref(N, P, R, out);
+    });
+}
+
+}  // extern "C"

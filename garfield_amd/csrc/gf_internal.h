@@ -1,0 +1,115 @@
+// Internal declarations shared by the HIP kernels (gf_kernels.hip) and the
+// host side of libgarfield.so (gf_host.cpp, gf_io.cpp).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/garfield.h"
+
+namespace gf {
+
+constexpr uint32_t kMaxIter = 10000;  // per-cell iteration cap (gpu_graph.cu:39)
+constexpr uint32_t kHashReset = 4;    // visited-set reset period (gpu_graph.cu:34)
+constexpr uint32_t kXSlots = 128;     // cross-cell entry slots (gpu_graph.cu:42)
+constexpr uint32_t kXStep = 64;       // candidates feeding the slots (gpu_graph.cu:3564)
+constexpr uint32_t kMaxAttr = 8;      // attributes per point supported
+constexpr uint32_t kMaxE = 4;         // cross edges per (point, cell) supported
+constexpr uint32_t kSelTile = 1024;   // rows per selectivity tile
+constexpr uint32_t kEmpty = 0xFFFFFFFFu;
+
+// Candidate word: high 32 bits = fp32 distance bits (non-negative, so the
+// unsigned order is the float order), low 32 bits = row << 2 | explored << 1
+// | passes-filter.  Ordering uses the word with the two flag bits cleared,
+// i.e. (distance, cell-major row).
+constexpr uint32_t kRecSent = 0xFFFFFFFEu;  // row 0x3FFFFFFF, explored, not passing
+constexpr uint64_t kCandSent = (uint64_t(0x7F800000u) << 32) | kRecSent;
+constexpr uint32_t kRowSent = 0x3FFFFFFFu;
+
+// Per-query counter slots (same order as the oracle's ORC_C_*).
+enum { C_EXPAND = 0, C_DIST = 1, C_ATTR = 2, C_CROSS = 3, C_LROW = 4, C_SCAN = 5,
+       C_PASS = 6, C_ROUTE = 7 };
+
+// Distance kernel shape for a row of D elements: 16-byte chunks, LPR lanes
+// per row (power of two in [8, 64]), CPL chunks per lane.
+struct RowShape {
+    bool f16;
+    uint32_t nch, lpr, cpl;
+};
+RowShape row_shape(uint32_t D, bool f16);
+
+struct TravArgs {
+    const char* vec;          // N rows of rowbytes, cell-major
+    uint32_t rowbytes, nch;
+    const float* attrs;       // N*a, cell-major
+    const uint32_t* graph;    // N*R cell-local neighbour ids, cell-major rows
+    const uint32_t* cross;    // N*P*E cell-local ids, cell-major rows
+    const uint32_t* offset;   // P+1
+    const uint32_t* gidx;     // row -> point id
+    const uint32_t* lrow;     // row -> cell-local id
+    const char* queries;      // Q rows of qbytes (fp32, or fp16 in f16 mode)
+    uint32_t qbytes;
+    const float* lo;          // Q*a
+    const float* hi;
+    const uint32_t* cells;    // Q*P ordered cell lists
+    const uint32_t* counts;   // Q
+    const uint32_t* little;   // Q
+    const uint32_t* sched;    // queries handled by this launch
+    uint32_t nsched;
+    const uint32_t* entry;    // R entry ids
+    uint32_t* out_ids;        // Q*K
+    float* out_dist;          // Q*K
+    uint32_t* counters;       // Q*GF_NCOUNTERS
+    uint32_t a, P, R, E, L, K, rl, hbits, Lpad;
+};
+
+// Kernel launchers (gf_kernels.hip).  All are asynchronous on `st`.
+hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds_bytes, hipStream_t st);
+hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, hipStream_t st);
+hipError_t launch_fill_results(uint32_t* ids, float* dist, uint32_t n, hipStream_t st);
+hipError_t launch_f2h(const float* x, uint16_t* out, size_t n, float alpha, hipStream_t st);
+hipError_t launch_f2h_pad(const float* x, uint32_t rows, uint32_t D, uint16_t* out,
+                          uint32_t rows_pad, uint32_t Dp, float alpha, hipStream_t st);
+hipError_t launch_norms_f16(const uint16_t* x, uint32_t n, uint32_t D, uint32_t ld, float* out,
+                            hipStream_t st);
+hipError_t launch_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi,
+                        const uint32_t* grid, const uint32_t* doff, const float* l_q,
+                        const float* r_q, uint32_t P, uint32_t* cells, uint32_t* counts,
+                        hipStream_t st);
+hipError_t launch_cellq_count(uint32_t Q, uint32_t P, const uint32_t* cells,
+                              const uint32_t* counts, uint32_t* ccount, hipStream_t st);
+hipError_t launch_scan_small(const uint32_t* in, uint32_t n, uint32_t* out_excl, hipStream_t st);
+hipError_t launch_cellq_fill(uint32_t Q, uint32_t P, const uint32_t* cells,
+                             const uint32_t* counts, const uint32_t* cstart, uint32_t* cfill,
+                             uint32_t* cellq, hipStream_t st);
+hipError_t launch_selcount(uint32_t ntiles, const uint32_t* tile_cell, const uint32_t* tile_row0,
+                           const uint32_t* tile_n, const float* attrs, uint32_t a,
+                           const uint32_t* cstart, const uint32_t* ccount,
+                           const uint32_t* cellq, const float* lo, const float* hi,
+                           uint32_t* selcount, hipStream_t st);
+hipError_t launch_route(uint32_t Q, uint32_t N, float thr, const uint32_t* selcount,
+                        const uint32_t* counts, uint32_t* little, hipStream_t st);
+hipError_t launch_centroid(const uint16_t* qh, const uint16_t* ch, const float* qn,
+                           const float* cn, uint32_t Q, uint32_t C, uint32_t Qp, uint32_t Cp,
+                           uint32_t Dp, float* dist, hipStream_t st);
+hipError_t launch_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc, const float* dist,
+                        const uint32_t* hist, uint32_t* cells, const uint32_t* counts,
+                        uint32_t* topk, hipStream_t st);
+
+// Host-side file readers (gf_io.cpp).  Each throws gf::Error on failure.
+struct Error {
+    gf_status code;
+    std::string msg;
+};
+struct HostIndex {
+    uint32_t N = 0, D = 0, a = 0, P = 0, R = 0, E = 0;
+    std::vector<float> vectors, attrs, l_q, r_q;
+    std::vector<uint32_t> grid, global_pid, cell_graphs, cross;
+    std::vector<int32_t> labels;
+    bool has_labels = false;
+};
+void read_index_files(const gf_index_paths& p, uint32_t degree, HostIndex& out);
+
+}  // namespace gf

@@ -1,0 +1,1047 @@
+// HIP kernels of the MI355X Garfield query path (gfx950, wave64).
+//
+// Layout: every per-point array on the device is stored cell-major -- row r of
+// cell c is point global_idx[offset[c] + r_local] -- so a cell-local neighbour
+// id l of cell c is row offset[c] + l and no id indirection sits between a
+// graph row and the vector gathers.  One wavefront handles one query; its
+// candidate list, visited hash and scratch live in LDS and every step is
+// wave-synchronous, so the traversal needs no workgroup barriers.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "gf_internal.h"
+
+namespace gf {
+namespace {
+
+__device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
+
+__device__ __forceinline__ uint64_t make_cand(float d, uint32_t row, bool pass) {
+    return (uint64_t(__float_as_uint(d)) << 32) | (row << 2) | (pass ? 1u : 0u);
+}
+__device__ __forceinline__ uint64_t ckey(uint64_t c) { return c & ~uint64_t(3); }
+__device__ __forceinline__ uint32_t crow(uint64_t c) { return uint32_t(c) >> 2; }
+__device__ __forceinline__ bool cvalid(uint64_t c) { return (uint32_t(c) >> 2) != kRowSent; }
+__device__ __forceinline__ bool cexpl(uint64_t c) { return (c & 2u) != 0; }
+__device__ __forceinline__ bool cpass(uint64_t c) { return (c & 1u) != 0; }
+__device__ __forceinline__ float cdist(uint64_t c) { return __uint_as_float(uint32_t(c >> 32)); }
+
+__device__ __forceinline__ uint32_t readlane32(uint32_t v, uint32_t l) {
+    return uint32_t(__builtin_amdgcn_readlane(int(v), int(l)));
+}
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, uint32_t l) {
+    uint32_t lo = readlane32(uint32_t(v), l), hi = readlane32(uint32_t(v >> 32), l);
+    return (uint64_t(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi(uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0u));
+}
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+// ---------------------------------------------------------------- visited set
+// Open addressing with linear probing in LDS; set semantics identical to the
+// reference's 2048-slot table (gpu_graph.cu:677-711) as long as the table does
+// not fill up, which the host guarantees by sizing it to twice the keys that
+// can be live between two resets.
+__device__ __forceinline__ bool hash_insert(uint32_t* H, uint32_t hbits, uint32_t key) {
+    const uint32_t mask = (1u << hbits) - 1u;
+    uint32_t h = (key * 2654435761u) >> (32u - hbits);
+    for (uint32_t i = 0; i <= mask; ++i) {
+        uint32_t old = atomicCAS(&H[h], kEmpty, key);
+        if (old == kEmpty) return true;
+        if (old == key) return false;
+        h = (h + 1u) & mask;
+    }
+    return false;
+}
+__device__ __forceinline__ void hash_clear(uint32_t* H, uint32_t hsize) {
+    uint4* h4 = reinterpret_cast<uint4*>(H);
+    const uint4 e = make_uint4(kEmpty, kEmpty, kEmpty, kEmpty);
+    for (uint32_t i = lane_id(); i < hsize / 4u; i += 64u) h4[i] = e;
+}
+
+// ----------------------------------------------------------- row distances
+template <bool F16, int CPL>
+struct QReg {
+    float v[CPL][F16 ? 8 : 4];
+};
+
+template <bool F16>
+__device__ __forceinline__ void load_chunk(const char* base, uint32_t c, float (&x)[F16 ? 8 : 4]) {
+    const uint4 u = *reinterpret_cast<const uint4*>(base + size_t(c) * 16u);
+    if constexpr (F16) {
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __half lo = __ushort_as_half(uint16_t(w[i] & 0xFFFFu));
+            __half hi = __ushort_as_half(uint16_t(w[i] >> 16));
+            x[2 * i] = __half2float(lo);
+            x[2 * i + 1] = __half2float(hi);
+        }
+    } else {
+        x[0] = __uint_as_float(u.x);
+        x[1] = __uint_as_float(u.y);
+        x[2] = __uint_as_float(u.z);
+        x[3] = __uint_as_float(u.w);
+    }
+}
+
+template <bool F16, int LPR, int CPL>
+__device__ __forceinline__ void load_query(QReg<F16, CPL>& q, const char* qrow, uint32_t nch) {
+    const uint32_t l = lane_id() % LPR;
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) {
+        const uint32_t c = l + m * LPR;
+        if (c < nch) {
+            load_chunk<F16>(qrow, c, q.v[m]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < (F16 ? 8 : 4); ++e) q.v[m][e] = 0.0f;
+        }
+    }
+}
+
+// Partial sum of one lane over its chunks l, l+LPR, ... in element order
+// (fp32 fma), the canonical order the oracle restates.
+template <bool F16, int LPR, int CPL>
+__device__ __forceinline__ float row_partial(const QReg<F16, CPL>& q, const char* row, uint32_t nch) {
+    const uint32_t l = lane_id() % LPR;
+    float acc = 0.0f;
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) {
+        const uint32_t c = l + m * LPR;
+        if (c < nch) {
+            float x[F16 ? 8 : 4];
+            load_chunk<F16>(row, c, x);
+#pragma unroll
+            for (int e = 0; e < (F16 ? 8 : 4); ++e) {
+                const float d = q.v[m][e] - x[e];
+                acc = __builtin_fmaf(d, d, acc);
+            }
+        }
+    }
+    return acc;
+}
+
+// Distances of the n rows listed in S[0..n) (LDS).  Lane j with compact
+// index ci (< n) receives the distance of row S[ci] in `dist`.
+template <bool F16, int LPR, int CPL>
+__device__ __forceinline__ void eval_rows(const QReg<F16, CPL>& q, const char* vec, uint32_t rowbytes,
+                                          uint32_t nch, const uint32_t* S, uint32_t n, uint32_t ci,
+                                          float& dist) {
+    constexpr uint32_t RPI = 64 / LPR;                  // rows per pass
+    constexpr uint32_t NB = (8 / CPL) > 0 ? (8 / CPL) : 1;  // passes per batch
+    const uint32_t g = lane_id() / LPR;
+    const uint32_t npass = (n + RPI - 1) / RPI;
+    for (uint32_t k0 = 0; k0 < npass; k0 += NB) {
+        float acc[NB];
+#pragma unroll
+        for (uint32_t b = 0; b < NB; ++b) {
+            const uint32_t i = (k0 + b) * RPI + g;
+            acc[b] = 0.0f;
+            if (i < n) acc[b] = row_partial<F16, LPR, CPL>(q, vec + size_t(S[i]) * rowbytes, nch);
+        }
+#pragma unroll
+        for (uint32_t b = 0; b < NB; ++b) {
+            float v = acc[b];
+#pragma unroll
+            for (int m = LPR / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+            const float t = __shfl(v, int((ci % RPI) * LPR), 64);
+            if (ci < n && ci / RPI == k0 + b) dist = t;
+        }
+    }
+}
+
+__device__ __forceinline__ bool row_pass(const float* attrs, uint32_t a, uint32_t row,
+                                         const float (&lo)[kMaxAttr], const float (&hi)[kMaxAttr]) {
+    bool ok = true;
+#pragma unroll
+    for (uint32_t d = 0; d < kMaxAttr; ++d) {
+        if (d < a) {
+            const float v = attrs[size_t(row) * a + d];
+            ok = ok && (v >= lo[d]) && (v <= hi[d]);
+        }
+    }
+    return ok;
+}
+
+// Evaluate candidate rows held one per lane (lanes with need=false keep dist
+// = +inf).  Returns the number of rows gathered.
+template <bool F16, int LPR, int CPL>
+__device__ __forceinline__ uint32_t eval_lanes(const QReg<F16, CPL>& q, const TravArgs& p, uint32_t* S,
+                                               uint32_t row, bool need, float& dist) {
+    const uint64_t m = ballot(need);
+    const uint32_t ci = need ? lanes_below(m) : 0xFFFFFFFFu;
+    if (need) S[ci] = row;
+    const uint32_t n = __popcll(m);
+    dist = __int_as_float(0x7F800000);
+    if (n) eval_rows<F16, LPR, CPL>(q, p.vec, p.rowbytes, p.nch, S, n, ci, dist);
+    return n;
+}
+
+// ------------------------------------------------------------ list merges
+// Merge the candidates b (lane j < nb holds one) into the sorted list A[0..L):
+// A_i moves to i + #{b <= A_i}, b_j to j' + #{A < b_j} with j' its stable rank
+// among b (gpu_graph.cu:162-222).  A-origin entries pushed past L go to Bp
+// (as themselves if valid and passing, else the sentinel; quirk of
+// merge_top_with_recycle_list, gpu_graph.cu:224-315); Bp has nb slots and is
+// pre-filled with sentinels.  Returns the first position that received an
+// incoming candidate (L if none).
+__device__ uint32_t merge_into(uint64_t* A, uint32_t L, uint64_t b, uint32_t nb, uint64_t* Bp) {
+    const uint32_t lane = lane_id();
+    const bool mine = lane < nb;
+    const uint64_t kb = ckey(b);
+    uint32_t r = L;
+    if (mine) {
+        if (kb <= ckey(A[L - 1])) {
+            uint32_t lo = 0, hi = L - 1;
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (ckey(A[mid]) < kb) lo = mid + 1; else hi = mid;
+            }
+            r = lo;
+        }
+    }
+    if (Bp && mine) Bp[lane] = kCandSent;
+    const uint64_t ins = ballot(mine && r < L);
+    if (ins == 0) return L;
+    uint32_t rb = 0, rmin = L;
+    for (uint64_t m = ins; m; m &= m - 1) {
+        const uint32_t k = __builtin_ctzll(m);
+        const uint64_t kk = readlane64(kb, k);
+        const uint32_t rk = readlane32(r, k);
+        rb += (kk < kb) || (kk == kb && k < lane);
+        rmin = rk < rmin ? rk : rmin;
+    }
+    const uint32_t nA = L - rmin;
+    for (int ch = int((nA + 63u) / 64u) - 1; ch >= 0; --ch) {
+        const uint32_t i = rmin + uint32_t(ch) * 64u + lane;
+        uint64_t av = 0;
+        uint32_t np = 0;
+        if (i < L) {
+            av = A[i];
+            uint32_t s = 0;
+            for (uint64_t m = ins; m; m &= m - 1) s += (readlane32(r, __builtin_ctzll(m)) <= i);
+            np = i + s;
+        }
+        if (i < L) {
+            if (np < L) A[np] = av;
+            else if (Bp) Bp[np - L] = (cvalid(av) && cpass(av)) ? av : kCandSent;
+        }
+    }
+    const uint32_t pos = rb + r;
+    if (mine && r < L && pos < L) A[pos] = b;
+    return rmin;
+}
+
+// Recycle-list update (gpu_graph.cu:3412-3425, 3536-3546): rc (lane t < rl
+// holds entry t, sorted) takes the rl smallest of rc and the valid evictees in
+// Bp[0..nb); ties put the evictee first.  bleft receives everything else
+// (the reference's B region, re-hashed at the next reset).
+__device__ void recycle_update(uint64_t& rc, uint32_t rl, const uint64_t* Bp, uint32_t nb,
+                               uint64_t& bleft, uint64_t* T) {
+    const uint32_t lane = lane_id();
+    const uint64_t e = lane < nb ? Bp[lane] : kCandSent;
+    const uint64_t ev = ballot(lane < nb && cvalid(e));
+    if (ev == 0) { bleft = e; return; }
+    const uint64_t ke = ckey(e), kr = ckey(rc);
+    const bool is_e = (ev >> lane) & 1u;
+    const bool is_r = lane < rl;
+    uint32_t re = 0, rr = lane;
+    for (uint64_t m = ev; m; m &= m - 1) {
+        const uint32_t k = __builtin_ctzll(m);
+        const uint64_t kk = readlane64(ke, k);
+        re += (kk < ke) || (kk == ke && k < lane);
+        rr += (kk <= kr);
+    }
+    for (uint32_t t = 0; t < rl; ++t) re += (readlane64(kr, t) < ke);
+    // T[0..rl) new recycle, T[64..) leftovers
+    if (is_e) T[re < rl ? re : 64u + re - rl] = e;
+    if (is_r) T[rr < rl ? rr : 64u + rr - rl] = rc;
+    const uint32_t nleft = __popcll(ev);
+    rc = lane < rl ? T[lane] : kCandSent;
+    bleft = lane < nleft ? T[64u + lane] : kCandSent;
+}
+
+__device__ __forceinline__ uint32_t first_unexplored(const uint64_t* A, uint32_t L, uint32_t start) {
+    for (uint32_t base = start; base < L; base += 64u) {
+        const uint32_t i = base + lane_id();
+        const bool un = i < L && !cexpl(A[i]);
+        const uint64_t m = ballot(un);
+        if (m) return base + __builtin_ctzll(m);
+    }
+    return L;
+}
+
+// Cell-local key of a candidate row for the visited set: arithmetic inside
+// the cell [off, offn), a gather of lrow[] for rows of other cells.
+__device__ __forceinline__ uint32_t local_key(const TravArgs& p, uint32_t row, uint32_t off, uint32_t offn,
+                                              uint32_t& nlrow) {
+    if (row >= off && row < offn) return row - off;
+    ++nlrow;
+    return p.lrow[row];
+}
+
+// Insert the keys of A[0..L) (and optionally one candidate per lane).
+__device__ void hash_add_list(const TravArgs& p, uint32_t* H, const uint64_t* A, uint32_t L,
+                              uint32_t off, uint32_t offn, uint32_t& nlrow) {
+    for (uint32_t i = lane_id(); i < L; i += 64u) {
+        const uint64_t c = A[i];
+        if (cvalid(c)) hash_insert(H, p.hbits, local_key(p, crow(c), off, offn, nlrow));
+    }
+}
+
+// In-LDS bitonic sort of 128 candidates (ascending key).
+__device__ void sort128(uint64_t* W) {
+    const uint32_t lane = lane_id();
+    for (uint32_t k = 2; k <= 128; k <<= 1) {
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            const uint32_t idx = 2u * j * (lane / j) + (lane % j);
+            const uint32_t par = idx + j;
+            const uint64_t x = W[idx], y = W[par];
+            const bool asc = (idx & k) == 0;
+            if ((ckey(x) > ckey(y)) == asc) { W[idx] = y; W[par] = x; }
+        }
+    }
+}
+
+// ------------------------------------------------------------- traversal
+// One wavefront per query: the reference's fused kernel
+// select_path_contain_attr_filter_V2_without_output_with_post_pre_filter
+// (gpu_graph.cu:3266-4131), traversal branch.
+template <bool F16, int LPR, int CPL>
+__global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint64_t* A = reinterpret_cast<uint64_t*>(smem);   // Lpad
+    uint64_t* W = A + p.Lpad;                           // 128 (slots, evictees, scratch)
+    uint32_t* S = reinterpret_cast<uint32_t*>(W + kXSlots);  // 128 row list
+    uint32_t* H = S + 128;                              // visited set
+    const uint32_t lane = lane_id();
+    const uint32_t q = p.sched[blockIdx.x];
+    const uint32_t hsize = 1u << p.hbits;
+    const uint32_t L = p.L, R = p.R, P = p.P, E = p.E;
+
+    QReg<F16, CPL> qv;
+    load_query<F16, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
+    float lo[kMaxAttr], hi[kMaxAttr];
+#pragma unroll
+    for (uint32_t d = 0; d < kMaxAttr; ++d) {
+        lo[d] = d < p.a ? p.lo[size_t(q) * p.a + d] : 0.0f;
+        hi[d] = d < p.a ? p.hi[size_t(q) * p.a + d] : 0.0f;
+    }
+    for (uint32_t i = lane; i < L; i += 64u) A[i] = kCandSent;
+    hash_clear(H, hsize);
+    uint32_t n_expand = 0, n_dist = 0, n_attr = 0, n_cross = 0, n_lrow = 0;
+    uint64_t rc = kCandSent, bleft = kCandSent;
+
+    const uint32_t* cl = p.cells + size_t(q) * P;
+    const uint32_t cnt = p.counts[q];
+
+    // Entry points of the first cell; their point ids go into the visited set
+    // as in the reference (gpu_graph.cu:3347-3351).
+    uint64_t b = kCandSent;
+    {
+        const uint32_t c0 = cl[0];
+        const uint32_t off0 = p.offset[c0], sz0 = p.offset[c0 + 1] - off0;
+        const bool mine = lane < R;
+        uint32_t row = 0;
+        bool pass = false;
+        if (mine) {
+            row = off0 + p.entry[lane] % sz0;
+            hash_insert(H, p.hbits, p.gidx[row]);
+            pass = row_pass(p.attrs, p.a, row, lo, hi);
+        }
+        float d;
+        n_dist += eval_lanes<F16, LPR, CPL>(qv, p, S, row, mine, d);
+        n_attr += R;
+        if (mine) b = make_cand(d, row, pass);
+    }
+
+    for (uint32_t pi = 0; pi < cnt; ++pi) {
+        const uint32_t cur = cl[pi];
+        const uint32_t off = p.offset[cur], offn = p.offset[cur + 1];
+        uint32_t scan = merge_into(A, L, b, R, W);
+        recycle_update(rc, p.rl, W, R, bleft, W);
+
+        for (uint32_t it = 0; it < kMaxIter; ++it) {
+            if ((it + 1) % kHashReset == 0) {          // gpu_graph.cu:3441-3454
+                hash_clear(H, hsize);
+                hash_add_list(p, H, A, L, off, offn, n_lrow);
+                if (lane < R && cvalid(bleft))
+                    hash_insert(H, p.hbits, local_key(p, crow(bleft), off, offn, n_lrow));
+            }
+            const uint32_t sel = first_unexplored(A, L, scan);
+            if (sel == L) break;
+            const uint64_t sc = A[sel];
+            if (lane == 0) A[sel] = sc | 2u;
+            ++n_expand;
+            scan = sel + 1;
+            const uint32_t srow = crow(sc);
+            // Expand: neighbours of the selected row (gpu_graph.cu:3500-3530).
+            const bool mine = lane < R;
+            uint32_t nrow = 0;
+            bool isnew = false, pass = false;
+            if (mine) {
+                const uint32_t nl = p.graph[size_t(srow) * R + lane];
+                nrow = off + nl;
+                isnew = hash_insert(H, p.hbits, nl);
+                pass = row_pass(p.attrs, p.a, nrow, lo, hi);
+            }
+            n_attr += R;
+            float d;
+            n_dist += eval_lanes<F16, LPR, CPL>(qv, p, S, nrow, isnew, d);
+            b = mine ? make_cand(d, nrow, pass) : kCandSent;
+            const uint32_t ip = merge_into(A, L, b, R, W);
+            recycle_update(rc, p.rl, W, R, bleft, W);
+            scan = ip < scan ? ip : scan;
+        }
+        // End of cell (gpu_graph.cu:3555-3560).
+        for (uint32_t i = lane; i < L; i += 64u) A[i] = A[i] | 2u;
+        hash_clear(H, hsize);
+        if (pi + 1 < cnt) {                             // gpu_graph.cu:3564-3642
+            const uint32_t nxt = cl[pi + 1];
+            const uint32_t offx = p.offset[nxt], offxn = p.offset[nxt + 1], szx = offxn - offx;
+            const uint32_t ncand = L < kXStep ? L : kXStep;
+            const uint64_t ac = lane < ncand ? A[lane] : kCandSent;
+            const bool cv = lane < ncand && cvalid(ac);
+            const uint64_t cvm = ballot(cv);
+            n_cross += __popcll(cvm);
+            uint32_t keys[kMaxE];
+#pragma unroll
+            for (uint32_t e = 0; e < kMaxE; ++e) {
+                keys[e] = kEmpty;
+                if (cv && e < E) keys[e] = p.cross[(size_t(crow(ac)) * P + nxt) * E + e];
+            }
+            // Slots filled in order 0..127 (the reference fills them
+            // concurrently); slot i follows candidate i % 64 and takes its
+            // first cross edge not yet taken, else the first free local id.
+            uint32_t tk0 = kEmpty, tk1 = kEmpty;
+            for (uint32_t i = 0; i < kXSlots; ++i) {
+                const uint32_t c = i & 63u;
+                if (!((cvm >> c) & 1u)) continue;
+                uint32_t found = kEmpty;
+#pragma unroll
+                for (uint32_t e = 0; e < kMaxE; ++e) {
+                    if (e < E && found == kEmpty) {
+                        const uint32_t k = readlane32(keys[e], c);
+                        if (ballot(tk0 == k || tk1 == k) == 0) found = k;
+                    }
+                }
+                for (uint32_t rp = 0; found == kEmpty && rp < szx; ++rp)
+                    if (ballot(tk0 == rp || tk1 == rp) == 0) found = rp;
+                if (found != kEmpty) {
+                    if (i < 64u) tk0 = lane == i ? found : tk0;
+                    else tk1 = lane == i - 64u ? found : tk1;
+                }
+            }
+            uint64_t w0 = kCandSent, w1 = kCandSent;
+            {
+                const bool v0 = tk0 != kEmpty, v1 = tk1 != kEmpty;
+                const uint32_t r0 = offx + tk0, r1 = offx + tk1;
+                const bool p0 = v0 && row_pass(p.attrs, p.a, r0, lo, hi);
+                const bool p1 = v1 && row_pass(p.attrs, p.a, r1, lo, hi);
+                float d0, d1;
+                const uint32_t n0 = eval_lanes<F16, LPR, CPL>(qv, p, S, r0, v0, d0);
+                const uint32_t n1 = eval_lanes<F16, LPR, CPL>(qv, p, S, r1, v1, d1);
+                n_dist += n0 + n1;
+                n_attr += n0 + n1;
+                if (v0) w0 = make_cand(d0, r0, p0);
+                if (v1) w1 = make_cand(d1, r1, p1);
+            }
+            W[lane] = w0;
+            W[64u + lane] = w1;
+            sort128(W);
+            hash_clear(H, hsize);
+            b = lane < R ? W[lane] : kCandSent;
+            const uint64_t y = W[R + lane];
+            for (uint32_t h = 0; h < 2; ++h) {
+                const uint64_t c = W[h * 64u + lane];
+                if (cvalid(c)) hash_insert(H, p.hbits, crow(c) - offx);
+            }
+            merge_into(A, L, y, 64u, nullptr);
+            hash_add_list(p, H, A, L, offx, offxn, n_lrow);
+        }
+    }
+
+    // Post-filter, then merge the recycle list (gpu_graph.cu:4025-4047):
+    // failing entries become sentinels, i.e. the passing ones are compacted
+    // in order.
+    {
+        uint32_t wpos = 0;
+        for (uint32_t base = 0; base < L; base += 64u) {
+            const uint32_t i = base + lane;
+            const uint64_t c = i < L ? A[i] : kCandSent;
+            const bool keep = i < L && cvalid(c) && cpass(c);
+            const uint64_t m = ballot(keep);
+            if (keep) A[wpos + lanes_below(m)] = c;
+            wpos += __popcll(m);
+        }
+        for (uint32_t i = wpos + lane; i < L; i += 64u) A[i] = kCandSent;
+    }
+    if (cvalid(readlane64(rc, 0))) merge_into(A, L, rc, p.rl, nullptr);
+
+    // First K distinct ids (duplicates are adjacent: equal keys).
+    uint32_t n = 0;
+    for (uint32_t base = 0; base < L && n < p.K; base += 64u) {
+        const uint32_t i = base + lane;
+        const uint64_t c = i < L ? A[i] : kCandSent;
+        bool distinct = cvalid(c);
+        if (distinct && i > 0) distinct = crow(A[i - 1]) != crow(c);
+        const uint64_t m = ballot(distinct);
+        const uint32_t idx = n + lanes_below(m);
+        if (distinct && idx < p.K) {
+            p.out_ids[size_t(q) * p.K + idx] = p.gidx[crow(c)];
+            p.out_dist[size_t(q) * p.K + idx] = cdist(c);
+        }
+        n += __popcll(m);
+        if (!cvalid(readlane64(c, 63))) break;
+    }
+    for (uint32_t j = n + lane; j < p.K; j += 64u) {
+        p.out_ids[size_t(q) * p.K + j] = GF_NO_RESULT;
+        p.out_dist[size_t(q) * p.K + j] = __int_as_float(0x7F800000);
+    }
+    if (lane == 0) {
+        uint32_t* ctr = p.counters + size_t(q) * GF_NCOUNTERS;
+        ctr[C_EXPAND] = n_expand;
+        ctr[C_DIST] = n_dist;
+        ctr[C_ATTR] = n_attr;
+        ctr[C_CROSS] = n_cross;
+        ctr[C_LROW] = n_lrow;
+        ctr[C_SCAN] = 0;
+        ctr[C_PASS] = 0;
+        ctr[C_ROUTE] = 1;
+    }
+}
+
+// ----------------------------------------------------------- brute force
+// Filtered brute force over the query's cells (gpu_graph.cu:3788-4022): an
+// attribute scan of each cell's contiguous rows, compaction of the passing
+// rows, distance evaluation and a wave-held top-K keyed by (distance, row).
+template <bool F16, int LPR, int CPL>
+__global__ __launch_bounds__(64) void k_bruteforce(TravArgs p) {
+    constexpr uint32_t U = 4;                 // 64-row chunks scanned per step
+    __shared__ uint32_t S[64 * U + 64];
+    __shared__ uint64_t T[64];
+    const uint32_t lane = lane_id();
+    const uint32_t q = p.sched[blockIdx.x];
+    const uint32_t K = p.K, P = p.P;
+    QReg<F16, CPL> qv;
+    load_query<F16, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
+    float lo[kMaxAttr], hi[kMaxAttr];
+#pragma unroll
+    for (uint32_t d = 0; d < kMaxAttr; ++d) {
+        lo[d] = d < p.a ? p.lo[size_t(q) * p.a + d] : 0.0f;
+        hi[d] = d < p.a ? p.hi[size_t(q) * p.a + d] : 0.0f;
+    }
+    uint64_t top = kCandSent;                 // lane t < K: t-th best
+    uint32_t n_scan = 0, n_pass = 0;
+    const uint32_t* cl = p.cells + size_t(q) * P;
+    const uint32_t lit = p.little[q];
+    uint32_t ns = 0;
+
+    auto flush = [&](uint32_t nrows) {
+        for (uint32_t base = 0; base < nrows; base += 64u) {
+            const uint32_t nb = nrows - base < 64u ? nrows - base : 64u;
+            const bool mine = lane < nb;
+            float d = 0.0f;
+            eval_rows<F16, LPR, CPL>(qv, p.vec, p.rowbytes, p.nch, S + base, nb,
+                                     mine ? lane : 0xFFFFFFFFu, d);
+            const uint64_t c = mine ? make_cand(d, S[base + lane], true) : kCandSent;
+            const uint64_t thr = ckey(readlane64(top, K - 1));
+            const bool surv = mine && ckey(c) < thr;
+            const uint64_t sm = ballot(surv);
+            if (sm == 0) continue;
+            const uint64_t kc = ckey(c), kt = ckey(top);
+            uint32_t rs = 0, rt = lane;
+            for (uint64_t m = sm; m; m &= m - 1) {
+                const uint64_t kk = readlane64(kc, __builtin_ctzll(m));
+                rs += kk < kc;
+                rt += kk < kt;
+            }
+            for (uint32_t t = 0; t < K; ++t) rs += readlane64(kt, t) < kc;
+            if (surv && rs < K) T[rs] = c;
+            if (lane < K && rt < K) T[rt] = top;
+            top = lane < K ? T[lane] : kCandSent;
+        }
+    };
+
+    for (uint32_t g = 0; g < lit; ++g) {
+        const uint32_t cc = cl[g];
+        const uint32_t off = p.offset[cc], end = p.offset[cc + 1];
+        n_scan += end - off;
+        for (uint32_t base = off; base < end; base += 64u * U) {
+            bool ps[U];
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                const uint32_t row = base + u * 64u + lane;
+                ps[u] = row < end && row_pass(p.attrs, p.a, row, lo, hi);
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                const uint64_t m = ballot(ps[u]);
+                if (ps[u]) S[ns + lanes_below(m)] = base + u * 64u + lane;
+                ns += __popcll(m);
+            }
+            if (ns >= 64u) {
+                const uint32_t full = ns & ~63u;
+                flush(full);
+                const uint32_t rest = ns - full;
+                const uint32_t tail = lane < rest ? S[full + lane] : 0u;
+                if (lane < rest) S[lane] = tail;
+                n_pass += full;
+                ns = rest;
+            }
+        }
+    }
+    if (ns) { flush(ns); n_pass += ns; }
+    if (lane < K) {
+        p.out_ids[size_t(q) * K + lane] = cvalid(top) ? p.gidx[crow(top)] : GF_NO_RESULT;
+        p.out_dist[size_t(q) * K + lane] = cdist(top);
+    }
+    if (lane == 0) {
+        uint32_t* ctr = p.counters + size_t(q) * GF_NCOUNTERS;
+        ctr[C_EXPAND] = 0;
+        ctr[C_DIST] = n_pass;
+        ctr[C_ATTR] = 0;
+        ctr[C_CROSS] = 0;
+        ctr[C_LROW] = 0;
+        ctr[C_SCAN] = n_scan;
+        ctr[C_PASS] = n_pass;
+        ctr[C_ROUTE] = lit ? 2u : 0u;
+    }
+}
+
+__global__ void k_fill_results(uint32_t* ids, float* dist, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) { ids[i] = GF_NO_RESULT; dist[i] = __int_as_float(0x7F800000); }
+}
+
+// ---------------------------------------------------------------- prep
+// f2h (tools.cuh:308-320): binary16 round-to-nearest-even of x*alpha.
+__global__ void k_f2h(const float* x, uint16_t* out, size_t n, float alpha) {
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+        out[i] = __half_as_ushort(__float2half_rn(x[i] * alpha));
+}
+
+__global__ void k_f2h_pad(const float* x, uint32_t rows, uint32_t D, uint16_t* out, uint32_t rows_pad,
+                          uint32_t Dp, float alpha) {
+    const size_t n = size_t(rows_pad) * Dp;
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+        const uint32_t r = uint32_t(i / Dp), c = uint32_t(i % Dp);
+        float v = (r < rows && c < D) ? x[size_t(r) * D + c] * alpha : 0.0f;
+        out[i] = __half_as_ushort(__float2half_rn(v));
+    }
+}
+
+// find_norm (tools.cuh:1561-1586): one wave per row, lane-strided fp32 fma
+// partial sums, xor butterfly.
+__global__ __launch_bounds__(64) void k_norms_f16(const uint16_t* x, uint32_t n, uint32_t D, uint32_t ld,
+                                                  float* out) {
+    const uint32_t r = blockIdx.x, lane = lane_id();
+    if (r >= n) return;
+    float acc = 0.0f;
+    for (uint32_t j = lane; j < D; j += 64u) {
+        const float v = __half2float(__ushort_as_half(x[size_t(r) * ld + j]));
+        acc = __builtin_fmaf(v, v, acc);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+    if (lane == 0) out[r] = acc;
+}
+
+// Cells each range intersects (real_dataset_adapter.cuh:126-216), ascending
+// cell id.  Per attribute: lo cell = first c with r_q[c] >= lo, hi cell =
+// (first c with l_q[c] > hi) - 1; the product is enumerated with the last
+// attribute fastest (gpu_graph.cu:10965-10973).  A range beyond every cell
+// (quirk Q16) selects nothing; an empty interval between two cells selects
+// the next cell, as the reference's do-while does.
+__global__ void k_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi, const uint32_t* grid,
+                        const uint32_t* doff, const float* l_q, const float* r_q, uint32_t P,
+                        uint32_t* cells, uint32_t* counts) {
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= Q) return;
+    uint32_t cl[kMaxAttr], ch[kMaxAttr], idx[kMaxAttr], g[kMaxAttr];
+    bool empty = false;
+#pragma unroll
+    for (uint32_t d = 0; d < kMaxAttr; ++d) {
+        if (d >= a) break;
+        g[d] = grid[d];
+        const float* rq = r_q + doff[d];
+        const float* lq = l_q + doff[d];
+        const float vl = lo[size_t(q) * a + d], vh = hi[size_t(q) * a + d];
+        uint32_t i = 0;
+        while (i < g[d] && rq[i] < vl) ++i;
+        uint32_t j = 0;
+        while (j < g[d] && lq[j] <= vh) ++j;
+        if (i >= g[d] || j == 0) empty = true;
+        cl[d] = i;
+        ch[d] = (j == 0) ? i : ((j - 1) > i ? (j - 1) : i);
+        idx[d] = i;
+    }
+    uint32_t n = 0;
+    if (!empty) {
+        while (true) {
+            uint32_t pid = 0, f = 1;
+            for (int d = int(a) - 1; d >= 0; --d) { pid += idx[d] * f; f *= g[d]; }
+            cells[size_t(q) * P + n++] = pid;
+            int d = int(a) - 1;
+            for (; d >= 0; --d) {
+                if (++idx[d] <= ch[d]) break;
+                idx[d] = cl[d];
+            }
+            if (d < 0) break;
+        }
+    }
+    counts[q] = n;
+}
+
+__global__ void k_cellq_count(uint32_t Q, uint32_t P, const uint32_t* cells, const uint32_t* counts,
+                              uint32_t* ccount) {
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= Q) return;
+    for (uint32_t i = 0; i < counts[q]; ++i) atomicAdd(&ccount[cells[size_t(q) * P + i]], 1u);
+}
+
+__global__ void k_cellq_fill(uint32_t Q, uint32_t P, const uint32_t* cells, const uint32_t* counts,
+                             const uint32_t* cstart, uint32_t* cfill, uint32_t* cellq) {
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= Q) return;
+    for (uint32_t i = 0; i < counts[q]; ++i) {
+        const uint32_t c = cells[size_t(q) * P + i];
+        cellq[cstart[c] + atomicAdd(&cfill[c], 1u)] = q;
+    }
+}
+
+// Exclusive scan of a short array (n <= a few thousand) by one workgroup.
+__global__ __launch_bounds__(256) void k_scan_small(const uint32_t* in, uint32_t n, uint32_t* out) {
+    __shared__ uint32_t part[256];
+    const uint32_t t = threadIdx.x;
+    const uint32_t per = (n + 255u) / 256u;
+    uint32_t s = 0;
+    for (uint32_t i = t * per; i < (t + 1) * per && i < n; ++i) s += in[i];
+    part[t] = s;
+    __syncthreads();
+    if (t == 0) {
+        uint32_t acc = 0;
+        for (uint32_t i = 0; i < 256; ++i) { const uint32_t v = part[i]; part[i] = acc; acc += v; }
+    }
+    __syncthreads();
+    uint32_t acc = part[t];
+    for (uint32_t i = t * per; i < (t + 1) * per && i < n; ++i) { out[i] = acc; acc += in[i]; }
+}
+
+// Exact selectivity counts (real_dataset_adapter.cuh:346-383), tiled: a tile
+// of one cell's rows is staged in LDS once and tested against every query
+// that selects the cell; points outside a query's selected cells cannot pass
+// its range, so they need no test.
+__global__ __launch_bounds__(256) void k_selcount(const uint32_t* tile_cell, const uint32_t* tile_row0,
+                                                  const uint32_t* tile_n, const float* attrs, uint32_t a,
+                                                  const uint32_t* cstart, const uint32_t* ccount,
+                                                  const uint32_t* cellq, const float* lo, const float* hi,
+                                                  uint32_t* selcount) {
+    extern __shared__ float sa[];
+    const uint32_t t = blockIdx.x;
+    const uint32_t c = tile_cell[t], r0 = tile_row0[t], n = tile_n[t];
+    for (uint32_t i = threadIdx.x; i < n * a; i += blockDim.x) sa[i] = attrs[size_t(r0) * a + i];
+    __syncthreads();
+    const uint32_t qs = cstart[c], qn = ccount[c];
+    for (uint32_t k = threadIdx.x; k < qn; k += blockDim.x) {
+        const uint32_t q = cellq[qs + k];
+        float l[kMaxAttr], h[kMaxAttr];
+#pragma unroll
+        for (uint32_t d = 0; d < kMaxAttr; ++d) {
+            l[d] = d < a ? lo[size_t(q) * a + d] : 0.0f;
+            h[d] = d < a ? hi[size_t(q) * a + d] : 0.0f;
+        }
+        uint32_t cnt = 0;
+        if (a == 2) {
+            for (uint32_t j = 0; j < n; ++j) {
+                const float v0 = sa[2 * j], v1 = sa[2 * j + 1];
+                cnt += (v0 >= l[0]) & (v0 <= h[0]) & (v1 >= l[1]) & (v1 <= h[1]);
+            }
+        } else {
+            for (uint32_t j = 0; j < n; ++j) {
+                bool ok = true;
+#pragma unroll
+                for (uint32_t d = 0; d < kMaxAttr; ++d)
+                    if (d < a) { const float v = sa[j * a + d]; ok = ok && v >= l[d] && v <= h[d]; }
+                cnt += ok;
+            }
+        }
+        if (cnt) atomicAdd(&selcount[q], cnt);
+    }
+}
+
+// Prefilter routing (real_dataset_adapter.cuh:374-381): the selectivity is
+// computed in double, stored as float and compared with the threshold.
+__global__ void k_route(uint32_t Q, uint32_t N, float thr, const uint32_t* selcount, const uint32_t* counts,
+                        uint32_t* little) {
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= Q) return;
+    const float proportion = float((1.0 * selcount[q]) / (1.0 * N));
+    little[q] = proportion <= thr ? counts[q] : 0u;
+}
+
+// Query x centre squared distances |q|^2 + |c|^2 - 2 q.c with the dot
+// products on MFMA (v_mfma_f32_16x16x32_f16, fp32 accumulation) -- the
+// reference's dis_cal_tensor_core<16> (tools.cuh:1493-1559).  A workgroup of
+// four waves takes 16 queries x 64 centres; each wave one 16x16 tile.
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void k_centroid(const uint16_t* qh, const uint16_t* ch, const float* qn,
+                                                  const float* cn, uint32_t Q, uint32_t C, uint32_t Dp,
+                                                  float* dist) {
+    const uint32_t lane = lane_id(), wave = threadIdx.x >> 6;
+    const uint32_t q0 = blockIdx.x * 16u;
+    const uint32_t c0 = (blockIdx.y * 4u + wave) * 16u;
+    const uint32_t r = lane & 15u, kq = (lane >> 4) * 8u;
+    const half8_t* ap = reinterpret_cast<const half8_t*>(qh + size_t(q0 + r) * Dp + kq);
+    const half8_t* bp = reinterpret_cast<const half8_t*>(ch + size_t(c0 + r) * Dp + kq);
+    float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t k = 0; k < Dp; k += 32u) {
+        const half8_t av = ap[k / 8u];
+        const half8_t bv = bp[k / 8u];
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+    }
+    const uint32_t col = c0 + (lane & 15u);
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t row = q0 + (lane >> 4) * 4u + i;
+        if (row < Q && col < C) dist[size_t(row) * C + col] = qn[row] + cn[col] - 2.0f * acc[i];
+    }
+}
+
+// Cluster-guided cell order (tools.cuh:1398-1491 top clusters, then
+// gpu_graph.cu:11343-11396): one wave per query picks its topc nearest centres
+// by (distance, index) -- NaN (empty cluster) counts as +inf -- scores every
+// selected cell by the sum of its histogram entries over those centres and
+// sorts the cells by (score descending, cell ascending).
+__global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc,
+                                              const float* dist, const uint32_t* hist, uint32_t* cells,
+                                              const uint32_t* counts, uint32_t* topk) {
+    extern __shared__ uint32_t so[];
+    uint32_t* tk = so;             // topc
+    uint32_t* sc = so + 16;        // P scores
+    uint32_t* cc = sc + P;         // P cells
+    const uint32_t q = blockIdx.x, lane = lane_id();
+    const float* dq = dist + size_t(q) * C;
+    float pd = -1.0f;
+    uint32_t pi = 0xFFFFFFFFu;
+    for (uint32_t t = 0; t < topc; ++t) {
+        float bd = __int_as_float(0x7F800000);
+        uint32_t bi = 0xFFFFFFFFu;
+        for (uint32_t c = lane; c < C; c += 64u) {
+            float v = dq[c];
+            if (v != v) v = __int_as_float(0x7F800000);
+            const bool after = (v > pd) || (v == pd && (pi == 0xFFFFFFFFu || c > pi));
+            const bool before = (v < bd) || (v == bd && c < bi);
+            if (after && before) { bd = v; bi = c; }
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const float od = __shfl_xor(bd, m, 64);
+            const uint32_t oi = __shfl_xor(bi, m, 64);
+            if (od < bd || (od == bd && oi < bi)) { bd = od; bi = oi; }
+        }
+        pd = bd;
+        pi = bi;
+        if (lane == 0) { tk[t] = bi < C ? bi : 0u; topk[size_t(q) * topc + t] = bi < C ? bi : 0u; }
+    }
+    __syncthreads();
+    const uint32_t n = counts[q];
+    uint32_t* cl = cells + size_t(q) * P;
+    for (uint32_t i = lane; i < n; i += 64u) {
+        const uint32_t cell = cl[i];
+        uint32_t s = 0;
+        for (uint32_t t = 0; t < topc; ++t) s += hist[size_t(cell) * C + tk[t]];
+        sc[i] = s;
+        cc[i] = cell;
+    }
+    __syncthreads();
+    for (uint32_t i = lane; i < n; i += 64u) {
+        const uint32_t s = sc[i], cell = cc[i];
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < n; ++j) rank += (sc[j] > s) || (sc[j] == s && cc[j] < cell);
+        cl[rank] = cell;
+    }
+}
+
+template <bool F16, int LPR, int CPL>
+hipError_t launch_trav_t(const TravArgs& a, uint32_t lds, hipStream_t st) {
+    if (a.nsched == 0) return hipSuccess;
+    hipLaunchKernelGGL((k_traverse<F16, LPR, CPL>), dim3(a.nsched), dim3(64), lds, st, a);
+    return hipGetLastError();
+}
+template <bool F16, int LPR, int CPL>
+hipError_t launch_bf_t(const TravArgs& a, hipStream_t st) {
+    if (a.nsched == 0) return hipSuccess;
+    hipLaunchKernelGGL((k_bruteforce<F16, LPR, CPL>), dim3(a.nsched), dim3(64), 0, st, a);
+    return hipGetLastError();
+}
+
+template <bool F16, template <bool, int, int> class Fn, typename... Args>
+hipError_t dispatch_shape(const RowShape& rs, Args&&... args);
+
+}  // namespace
+
+RowShape row_shape(uint32_t D, bool f16) {
+    RowShape r;
+    r.f16 = f16;
+    const uint32_t elems = f16 ? 8u : 4u;
+    r.nch = (D + elems - 1) / elems;
+    r.lpr = 8;
+    while (r.lpr < r.nch && r.lpr < 64) r.lpr <<= 1;
+    r.cpl = (r.nch + r.lpr - 1) / r.lpr;
+    return r;
+}
+
+#define GF_SHAPES(F16, X)                                                       \
+    if (rs.lpr == 8 && rs.cpl == 1) return X<F16, 8, 1>;                       \
+    if (rs.lpr == 16 && rs.cpl == 1) return X<F16, 16, 1>;                     \
+    if (rs.lpr == 32 && rs.cpl == 1) return X<F16, 32, 1>;                     \
+    if (rs.lpr == 64 && rs.cpl == 1) return X<F16, 64, 1>;                     \
+    if (rs.lpr == 64 && rs.cpl == 2) return X<F16, 64, 2>;                     \
+    if (rs.lpr == 64 && rs.cpl == 3) return X<F16, 64, 3>;                     \
+    if (rs.lpr == 64 && rs.cpl == 4) return X<F16, 64, 4>;
+
+hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds, hipStream_t st) {
+#define X(F, L_, C_) launch_trav_t<F, L_, C_>(a, lds, st)
+#define XT(F, L_, C_) X(F, L_, C_)
+    if (rs.f16) {
+        if (rs.lpr == 8 && rs.cpl == 1) return XT(true, 8, 1);
+        if (rs.lpr == 16 && rs.cpl == 1) return XT(true, 16, 1);
+        if (rs.lpr == 32 && rs.cpl == 1) return XT(true, 32, 1);
+        if (rs.lpr == 64 && rs.cpl == 1) return XT(true, 64, 1);
+        if (rs.lpr == 64 && rs.cpl == 2) return XT(true, 64, 2);
+    } else {
+        if (rs.lpr == 8 && rs.cpl == 1) return XT(false, 8, 1);
+        if (rs.lpr == 16 && rs.cpl == 1) return XT(false, 16, 1);
+        if (rs.lpr == 32 && rs.cpl == 1) return XT(false, 32, 1);
+        if (rs.lpr == 64 && rs.cpl == 1) return XT(false, 64, 1);
+        if (rs.lpr == 64 && rs.cpl == 2) return XT(false, 64, 2);
+        if (rs.lpr == 64 && rs.cpl == 3) return XT(false, 64, 3);
+        if (rs.lpr == 64 && rs.cpl == 4) return XT(false, 64, 4);
+    }
+#undef XT
+#undef X
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, hipStream_t st) {
+#define XT(F, L_, C_) launch_bf_t<F, L_, C_>(a, st)
+    if (rs.f16) {
+        if (rs.lpr == 8 && rs.cpl == 1) return XT(true, 8, 1);
+        if (rs.lpr == 16 && rs.cpl == 1) return XT(true, 16, 1);
+        if (rs.lpr == 32 && rs.cpl == 1) return XT(true, 32, 1);
+        if (rs.lpr == 64 && rs.cpl == 1) return XT(true, 64, 1);
+        if (rs.lpr == 64 && rs.cpl == 2) return XT(true, 64, 2);
+    } else {
+        if (rs.lpr == 8 && rs.cpl == 1) return XT(false, 8, 1);
+        if (rs.lpr == 16 && rs.cpl == 1) return XT(false, 16, 1);
+        if (rs.lpr == 32 && rs.cpl == 1) return XT(false, 32, 1);
+        if (rs.lpr == 64 && rs.cpl == 1) return XT(false, 64, 1);
+        if (rs.lpr == 64 && rs.cpl == 2) return XT(false, 64, 2);
+        if (rs.lpr == 64 && rs.cpl == 3) return XT(false, 64, 3);
+        if (rs.lpr == 64 && rs.cpl == 4) return XT(false, 64, 4);
+    }
+#undef XT
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_fill_results(uint32_t* ids, float* dist, uint32_t n, hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_fill_results, dim3((n + 255) / 256), dim3(256), 0, st, ids, dist, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_f2h(const float* x, uint16_t* out, size_t n, float alpha, hipStream_t st) {
+    if (!n) return hipSuccess;
+    const uint32_t blocks = uint32_t(std::min<size_t>((n + 255) / 256, 65536));
+    hipLaunchKernelGGL(k_f2h, dim3(blocks), dim3(256), 0, st, x, out, n, alpha);
+    return hipGetLastError();
+}
+
+hipError_t launch_f2h_pad(const float* x, uint32_t rows, uint32_t D, uint16_t* out, uint32_t rows_pad,
+                          uint32_t Dp, float alpha, hipStream_t st) {
+    const size_t n = size_t(rows_pad) * Dp;
+    if (!n) return hipSuccess;
+    const uint32_t blocks = uint32_t(std::min<size_t>((n + 255) / 256, 65536));
+    hipLaunchKernelGGL(k_f2h_pad, dim3(blocks), dim3(256), 0, st, x, rows, D, out, rows_pad, Dp, alpha);
+    return hipGetLastError();
+}
+
+hipError_t launch_norms_f16(const uint16_t* x, uint32_t n, uint32_t D, uint32_t ld, float* out,
+                            hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_norms_f16, dim3(n), dim3(64), 0, st, x, n, D, ld, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi, const uint32_t* grid,
+                        const uint32_t* doff, const float* l_q, const float* r_q, uint32_t P,
+                        uint32_t* cells, uint32_t* counts, hipStream_t st) {
+    if (!Q) return hipSuccess;
+    hipLaunchKernelGGL(k_cells, dim3((Q + 63) / 64), dim3(64), 0, st, Q, a, lo, hi, grid, doff, l_q, r_q,
+                       P, cells, counts);
+    return hipGetLastError();
+}
+
+hipError_t launch_cellq_count(uint32_t Q, uint32_t P, const uint32_t* cells, const uint32_t* counts,
+                              uint32_t* ccount, hipStream_t st) {
+    if (!Q) return hipSuccess;
+    hipLaunchKernelGGL(k_cellq_count, dim3((Q + 255) / 256), dim3(256), 0, st, Q, P, cells, counts, ccount);
+    return hipGetLastError();
+}
+
+hipError_t launch_scan_small(const uint32_t* in, uint32_t n, uint32_t* out, hipStream_t st) {
+    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(256), 0, st, in, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_cellq_fill(uint32_t Q, uint32_t P, const uint32_t* cells, const uint32_t* counts,
+                             const uint32_t* cstart, uint32_t* cfill, uint32_t* cellq, hipStream_t st) {
+    if (!Q) return hipSuccess;
+    hipLaunchKernelGGL(k_cellq_fill, dim3((Q + 255) / 256), dim3(256), 0, st, Q, P, cells, counts, cstart,
+                       cfill, cellq);
+    return hipGetLastError();
+}
+
+hipError_t launch_selcount(uint32_t ntiles, const uint32_t* tile_cell, const uint32_t* tile_row0,
+                           const uint32_t* tile_n, const float* attrs, uint32_t a, const uint32_t* cstart,
+                           const uint32_t* ccount, const uint32_t* cellq, const float* lo, const float* hi,
+                           uint32_t* selcount, hipStream_t st) {
+    if (!ntiles) return hipSuccess;
+    const uint32_t lds = kSelTile * a * sizeof(float);
+    hipLaunchKernelGGL(k_selcount, dim3(ntiles), dim3(256), lds, st, tile_cell, tile_row0, tile_n, attrs, a,
+                       cstart, ccount, cellq, lo, hi, selcount);
+    return hipGetLastError();
+}
+
+hipError_t launch_route(uint32_t Q, uint32_t N, float thr, const uint32_t* selcount, const uint32_t* counts,
+                        uint32_t* little, hipStream_t st) {
+    if (!Q) return hipSuccess;
+    hipLaunchKernelGGL(k_route, dim3((Q + 255) / 256), dim3(256), 0, st, Q, N, thr, selcount, counts, little);
+    return hipGetLastError();
+}
+
+hipError_t launch_centroid(const uint16_t* qh, const uint16_t* ch, const float* qn, const float* cn,
+                           uint32_t Q, uint32_t C, uint32_t Qp, uint32_t Cp, uint32_t Dp, float* dist,
+                           hipStream_t st) {
+    if (!Q || !C) return hipSuccess;
+    // Cp is a multiple of 64 and Qp of 16, so every tile read stays inside the
+    // zero-padded operands.
+    hipLaunchKernelGGL(k_centroid, dim3(Qp / 16, Cp / 64), dim3(256), 0, st, qh, ch, qn, cn, Q, C, Dp, dist);
+    return hipGetLastError();
+}
+
+hipError_t launch_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc, const float* dist,
+                        const uint32_t* hist, uint32_t* cells, const uint32_t* counts, uint32_t* topk,
+                        hipStream_t st) {
+    if (!Q) return hipSuccess;
+    const uint32_t lds = (16 + 2 * P) * sizeof(uint32_t);
+    hipLaunchKernelGGL(k_order, dim3(Q), dim3(64), lds, st, Q, C, P, topc, dist, hist, cells, counts, topk);
+    return hipGetLastError();
+}
+
+}  // namespace gf

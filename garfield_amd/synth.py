@@ -1,0 +1,241 @@
+"""Synthetic workloads and GMG index construction for tests and bench.py.
+
+The reference builds its index with cuVS (CAGRA per cell, CAGRA search for
+cross edges, k-means), which is not available here; this module builds the
+same files from exact nearest neighbours instead (a stronger stand-in):
+
+- grid: rank-quantile cells per attribute, row-major global cell id
+  (grid_scatter_V2, indexbuild/tools.py:88-125);
+- per-cell graph: exact R nearest neighbours inside the cell, self excluded,
+  cell-local ids (cagra_build.py:94-127 writes the same layout);
+- cross-cell graph: for every point and every cell, the E nearest points of
+  that cell (global_graph_build.py:106-176);
+- labels: Lloyd k-means (clustering.py:68-87 writes per-point labels).
+
+Distances run as torch matrix products in fp32 (exact for the integer-valued
+configs) on whatever device is given: "cpu" in the tests, "cuda" on the GPU
+box for the 1M-point bench.  This is index *construction*, outside the query
+path the library implements.
+"""
+import math
+
+import numpy as np
+
+DOMAIN = 10000  # attribute values are integers in [0, DOMAIN)
+
+
+def _torch():
+    import torch
+    return torch
+
+
+# ------------------------------------------------------------------ data
+def uniform_int_vectors(n, d, seed, hi=256):
+    rng = np.random.default_rng(seed)
+    return rng.integers(0, hi, size=(n, d)).astype(np.float32)
+
+
+def gaussian_unit_vectors(n, d, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, d)).astype(np.float32)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    return x
+
+
+def uniform_attrs(n, a, seed, hi=DOMAIN):
+    rng = np.random.default_rng(seed)
+    return rng.integers(0, hi, size=(n, a)).astype(np.int32)
+
+
+def zipf_attrs(n, a, seed, s=1.1, hi=DOMAIN):
+    rng = np.random.default_rng(seed)
+    return np.minimum(rng.zipf(s, size=(n, a)) - 1, hi - 1).astype(np.int32)
+
+
+def ranges_for_selectivity(q, a, sel, seed, hi=DOMAIN):
+    """Closed integer ranges whose per-attribute width is sel**(1/a) of the domain."""
+    rng = np.random.default_rng(seed)
+    sel = np.broadcast_to(np.asarray(sel, np.float64), (q,))
+    w = np.clip(np.round(hi * sel ** (1.0 / a)), 1, hi).astype(np.int64)
+    lo = np.empty((q, a), np.int64)
+    for d in range(a):
+        lo[:, d] = (rng.random(q) * (hi - w + 1)).astype(np.int64)
+    hi_ = lo + w[:, None] - 1
+    return lo.astype(np.int32), hi_.astype(np.int32)
+
+
+def log_uniform(q, lo, hi, seed):
+    rng = np.random.default_rng(seed)
+    return np.exp(rng.uniform(math.log(lo), math.log(hi), size=q))
+
+
+# ------------------------------------------------------------------ grid
+def grid_scatter(attrs, grid):
+    """grid_scatter_V2: stable rank quantiles per attribute (indexbuild/tools.py:88-125)."""
+    attrs = np.asarray(attrs)
+    n, a = attrs.shape
+    l_q, r_q, pid_lists = [], [], []
+    for d in range(a):
+        col = attrs[:, d]
+        order = np.argsort(col, kind="stable")
+        srt = col[order]
+        g = int(grid[d])
+        avg = (n + g - 1) // g
+        left = [j * avg for j in range(g)]
+        right = [((j + 1) * avg - 1) if j < g - 1 else (n - 1) for j in range(g)]
+        idx = np.zeros(n, np.int32)
+        for j in range(g):
+            idx[order[j * avg:((j + 1) * avg if j < g - 1 else n)]] = j
+        l_q.append(srt[left].astype(np.int32))
+        r_q.append(srt[right].astype(np.int32))
+        pid_lists.append(idx)
+    factors = np.ones(a, np.int64)
+    for d in range(a - 2, -1, -1):
+        factors[d] = factors[d + 1] * int(grid[d + 1])
+    global_pid = np.zeros(n, np.int64)
+    for d in range(a):
+        global_pid += factors[d] * pid_lists[d]
+    return l_q, r_q, pid_lists, global_pid.astype(np.int32)
+
+
+def cell_members(global_pid, P):
+    """Point ids of each cell in ascending id order (cell-local id = position)."""
+    order = np.argsort(global_pid, kind="stable")
+    sizes = np.bincount(global_pid, minlength=P)
+    bounds = np.concatenate([[0], np.cumsum(sizes)])
+    return [order[bounds[c]:bounds[c + 1]] for c in range(P)]
+
+
+# ------------------------------------------------------------------ graphs
+def _sqdist(torch, x, y, ynorm):
+    xn = (x * x).sum(1, keepdim=True)
+    return (xn + ynorm[None, :] - 2.0 * (x @ y.T)).clamp_min_(0.0)
+
+
+def knn_cell_graphs(vectors, members, R, device="cpu", chunk=4096):
+    """Exact R nearest neighbours within each cell, self excluded (cell-local ids)."""
+    torch = _torch()
+    out = []
+    for mem in members:
+        xc = torch.as_tensor(vectors[mem], device=device)
+        n = xc.shape[0]
+        k = min(R + 1, n)
+        yn = (xc * xc).sum(1)
+        g = torch.empty((n, R), dtype=torch.int64, device=device)
+        for s in range(0, n, chunk):
+            e = min(n, s + chunk)
+            d = _sqdist(torch, xc[s:e], xc, yn)
+            ar = torch.arange(s, e, device=device)
+            d[ar - s, ar] = float("inf")
+            idx = torch.topk(d, k, dim=1, largest=False, sorted=True).indices[:, :R]
+            if idx.shape[1] < R:  # tiny cells: pad by repeating the nearest
+                idx = torch.cat([idx, idx[:, :1].expand(-1, R - idx.shape[1])], 1)
+            g[s:e] = idx
+        out.append(g.cpu().numpy().astype(np.uint32))
+    return np.concatenate(out, 0)
+
+
+def cross_edges(vectors, members, E, device="cpu", chunk=8192):
+    """For every point and every cell, the E nearest points of that cell (local ids)."""
+    torch = _torch()
+    N = vectors.shape[0]
+    P = len(members)
+    out = np.zeros((N, P * E), np.uint32)
+    xall = torch.as_tensor(vectors, device=device)
+    for c, mem in enumerate(members):
+        yc = torch.as_tensor(vectors[mem], device=device)
+        yn = (yc * yc).sum(1)
+        k = min(E, yc.shape[0])
+        for s in range(0, N, chunk):
+            e = min(N, s + chunk)
+            d = _sqdist(torch, xall[s:e], yc, yn)
+            idx = torch.topk(d, k, dim=1, largest=False, sorted=True).indices
+            if k < E:
+                idx = torch.cat([idx, idx[:, :1].expand(-1, E - k)], 1)
+            out[s:e, c * E:(c + 1) * E] = idx.cpu().numpy().astype(np.uint32)
+    return out
+
+
+def kmeans_labels(vectors, C, iters, seed, device="cpu", chunk=65536):
+    torch = _torch()
+    rng = np.random.default_rng(seed)
+    x = torch.as_tensor(vectors, device=device)
+    N = x.shape[0]
+    cen = x[torch.as_tensor(rng.choice(N, size=C, replace=False), device=device)].clone()
+    labels = torch.empty(N, dtype=torch.int64, device=device)
+    for _ in range(iters):
+        cn = (cen * cen).sum(1)
+        for s in range(0, N, chunk):
+            e = min(N, s + chunk)
+            labels[s:e] = _sqdist(torch, x[s:e], cen, cn).argmin(1)
+        sums = torch.zeros_like(cen).index_add_(0, labels, x)
+        cnt = torch.bincount(labels, minlength=C).to(x.dtype)
+        nz = cnt > 0
+        cen[nz] = sums[nz] / cnt[nz, None]
+    return labels.cpu().numpy().astype(np.int32)
+
+
+def build_index(vectors, attrs, grid, R, E, C=0, kmeans_iters=8, seed=5, device="cpu"):
+    """All index arrays, in the layout the files hold."""
+    grid = np.asarray(grid, np.int64)
+    P = int(np.prod(grid))
+    l_q, r_q, pid_lists, global_pid = grid_scatter(attrs, grid)
+    members = cell_members(global_pid, P)
+    graphs = knn_cell_graphs(vectors, members, R, device=device)
+    cross = cross_edges(vectors, members, E, device=device)
+    labels = kmeans_labels(vectors, C, kmeans_iters, seed, device=device) if C else None
+    return dict(vectors=vectors, attrs=attrs, grid=grid.astype(np.int32), l_q=l_q, r_q=r_q,
+                pid_lists=pid_lists, global_pid=global_pid, cell_graphs=graphs, cross=cross, labels=labels,
+                P=P, R=R, E=E)
+
+
+def write_index(ix, prefix):
+    """Write the App. A files: {prefix}.fvecs, {prefix}_cell{i}.graph, {prefix}.cross, .grid, .attrs, .cluster"""
+    from . import formats
+    formats.write_fvecs(prefix + ".fvecs", ix["vectors"])
+    members = cell_members(ix["global_pid"], ix["P"])
+    start = 0
+    for c, mem in enumerate(members):
+        formats.write_graph(f"{prefix}_cell{c}.graph", ix["cell_graphs"][start:start + len(mem)])
+        start += len(mem)
+    formats.write_graph(prefix + ".cross", ix["cross"])
+    formats.write_grid(prefix + ".grid", ix["grid"], ix["l_q"], ix["r_q"], ix["pid_lists"], ix["global_pid"])
+    formats.write_attrs(prefix + ".attrs", ix["attrs"])
+    if ix["labels"] is not None:
+        formats.write_labels(prefix + ".cluster", ix["labels"])
+    return dict(data_path=prefix + ".fvecs", cagra_prefix=prefix + "_cell", cagra_suffix=".graph",
+                global_graph=prefix + ".cross", grid=prefix + ".grid", attrs=prefix + ".attrs",
+                cluster=prefix + ".cluster" if ix["labels"] is not None else None)
+
+
+def quantile_arrays(ix):
+    """Flattened float l_q / r_q, attribute-major, as the library takes them."""
+    return (np.concatenate(ix["l_q"]).astype(np.float32), np.concatenate(ix["r_q"]).astype(np.float32))
+
+
+def open_device_index(ix, **kw):
+    """Index.from_arrays on an index dict from build_index."""
+    from ._lib import Index
+    l_q, r_q = quantile_arrays(ix)
+    return Index.from_arrays(ix["vectors"], ix["attrs"].astype(np.float32), ix["grid"], l_q, r_q,
+                             ix["global_pid"], ix["cell_graphs"], ix["cross"], labels=ix["labels"], **kw)
+
+
+# ------------------------------------------------------------- workloads
+def config_small(N=100_000, Q=1000, R=16, C=100, sel=0.3, seed=1):
+    """BASELINE config 1 (optionally shrunk): 128-d integer vectors, 2 attributes, 4x4 grid."""
+    vec = uniform_int_vectors(N, 128, seed)
+    att = uniform_attrs(N, 2, seed + 1)
+    qv = uniform_int_vectors(Q, 128, seed + 2)
+    lo, hi = ranges_for_selectivity(Q, 2, sel, seed + 3)
+    return dict(vectors=vec, attrs=att, grid=[4, 4], R=R, E=2, C=C, queries=qv, lo=lo, hi=hi)
+
+
+def config_headline(N=1_000_000, Q=10_000, R=32, C=1000, seed=11):
+    """1M x 128 integers, 2 attributes on 4x4, selectivity log-U[1%, 50%]."""
+    vec = uniform_int_vectors(N, 128, seed)
+    att = uniform_attrs(N, 2, seed + 1)
+    qv = uniform_int_vectors(Q, 128, seed + 2)
+    sel = log_uniform(Q, 0.01, 0.5, seed + 3)
+    lo, hi = ranges_for_selectivity(Q, 2, sel, seed + 4)
+    return dict(vectors=vec, attrs=att, grid=[4, 4], R=R, E=2, C=C, queries=qv, lo=lo, hi=hi, sel=sel)

@@ -1,0 +1,163 @@
+/*
+ * garfield.h -- C ABI of the MI355X-native Garfield query path (libgarfield.so).
+ *
+ * The reference (ZJU-DAILY/Garfield) has no FFI: its query path sits behind
+ * three host C++ functions, a CLI and a set of index files.  This header is the
+ * plain-C replacement a binding (ctypes, cgo, JNI) attaches to.  Every entry
+ * point names the reference interface it replaces (file:line under
+ * indexsearch/ or indexbuild/).
+ *
+ * Conventions: all pointers are host pointers; sizes are element counts;
+ * every call returns a gf_status (0 = success) and never exits the process;
+ * gf_last_error() gives a message for the last failure on the calling thread.
+ * One gf_index per device; calls on one handle must be serialised by the
+ * caller.  Result ids are point ids (positions in the .fvecs file); a missing
+ * result is GF_NO_RESULT, as the reference's top & 0x7FFFFFFF sentinel.
+ */
+#ifndef GARFIELD_H
+#define GARFIELD_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t gf_status;
+#define GF_OK 0
+#define GF_E_ARG 1          /* invalid argument or inconsistent sizes */
+#define GF_E_IO 2           /* file cannot be opened or is truncated */
+#define GF_E_FORMAT 3       /* file contents violate the index format */
+#define GF_E_DEVICE 4       /* HIP runtime error */
+#define GF_E_NOMEM 5        /* device or host allocation failed */
+#define GF_E_UNSUPPORTED 6  /* valid input outside what this build supports */
+#define GF_E_STATE 7        /* call out of order (e.g. search before mark) */
+
+#define GF_NO_RESULT 0x7FFFFFFFu
+
+#define GF_VEC_F32 0        /* traversal distances on fp32 vectors */
+#define GF_VEC_F16 1        /* on binary16 copies half(x * f2h_factor), fp32 accumulation */
+
+typedef struct gf_index gf_index;
+typedef struct gf_batch gf_batch;
+
+/* Index files: the realdataset_search flags that name them
+ * (realdataset_search.cu:2712-2751; formats in README.md:101-170). */
+typedef struct {
+    const char* data_path;     /* --data_path    .fvecs base vectors */
+    const char* cagra_prefix;  /* --cagra_prefix per-cell graph i is prefix + i + suffix */
+    const char* cagra_suffix;  /* --cagra_suffix */
+    const char* global_graph;  /* --global_graph cross-cell graph */
+    const char* grid;          /* --grid         rank-quantile grid */
+    const char* attrs;         /* --attrs        per-point attributes */
+    const char* cluster;       /* --cluster      per-point k-means labels; NULL = no labels */
+} gf_index_paths;
+
+typedef struct {
+    uint32_t degree;          /* --degree: per-cell graph degree R; 0 = from the files */
+    float f2h_factor;         /* --f2h_factor: scale before fp16 conversion (0 means 1) */
+    int32_t vec_dtype;        /* GF_VEC_F32 or GF_VEC_F16 */
+    int32_t hist_contiguous;  /* 1: cell x cluster histogram by i / ceil(N/P) as the
+                                 reference (tools.cuh:587-590); 0: by grid cell */
+    int32_t device;           /* HIP device ordinal */
+} gf_open_opts;
+
+/* The same content as the files, in host memory (no files needed). */
+typedef struct {
+    uint32_t N, D, a, P, R, E;
+    const float* vectors;        /* N*D fp32, point-id order */
+    const float* attrs;          /* N*a attribute values (integers converted to float) */
+    const uint32_t* grid_shape;  /* a cells per attribute; P = product */
+    const float* l_q;            /* sum(grid) lower quantile values, attribute-major */
+    const float* r_q;            /* sum(grid) upper quantile values */
+    const uint32_t* global_pid;  /* N cell of each point (row-major, last attribute fastest) */
+    const uint32_t* cell_graphs; /* N*R per-cell graphs concatenated in cell order, cell-local ids */
+    const uint32_t* cross;       /* N*(P*E) cross-cell graph rows, cell-local ids, point-id order */
+    const int32_t* labels;       /* N k-means labels, or NULL */
+} gf_index_host;
+
+typedef struct {
+    uint32_t N, D, a, P, R, E, C;  /* C = number of cluster centres (0 without labels) */
+    uint32_t vec_dtype;
+    float f2h_factor;
+    uint64_t device_bytes;         /* device memory held by the index */
+} gf_index_info;
+
+/* Loaders: load_data (tools.cuh:85-106), get_graph_info (check.cu:406-484),
+ * load_result (tools.cuh:205-223), load_grid_infos + load2GPU
+ * (real_dataset_adapter.cuh:563-619), load_attrs (tools.cuh:746-765),
+ * get_idx_mapper (tools.cuh:862-915), load_clustering (tools.cuh:569-602). */
+gf_status gf_index_open(const gf_index_paths* paths, const gf_open_opts* opts, gf_index** out);
+gf_status gf_index_create(const gf_index_host* host, const gf_open_opts* opts, gf_index** out);
+gf_status gf_index_close(gf_index* ix);
+gf_status gf_index_get_info(const gf_index* ix, gf_index_info* out);
+
+/* A query batch: Q query vectors (Q*D fp32) and closed ranges lo/hi (Q*a),
+ * uploaded to the device (realdataset_search.cu:2198-2245 load + f2h). */
+gf_status gf_batch_create(gf_index* ix, const float* queries, uint32_t Q,
+                          const float* lo, const float* hi, gf_batch** out);
+gf_status gf_batch_free(gf_batch* b);
+
+/* Stage A -- intersection_area_mark_little_seg_V2<A,T>
+ * (real_dataset_adapter.cuh:388-519): the cells each range intersects and the
+ * prefilter routing: a query whose exact selectivity is <= prefilter is sent
+ * to filtered brute force.  ms (may be NULL) receives the device time. */
+gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms);
+
+/* Stage B -- get_partitions_access_order_V2 (gpu_graph.cu:11742-11845):
+ * orders each query's cells by overlap with its topc nearest cluster centres
+ * (the reference uses topc = 4).  Without labels the order is left as is. */
+gf_status gf_order_cells(gf_batch* b, uint32_t topc, double* ms);
+
+/* Stage C -- batch_graph_search_gpu_with_prefilter_and_postfilter<T>
+ * (gpu_graph.cu:12463-12616) and its kernel (gpu_graph.cu:3266-4131). */
+typedef struct {
+    uint32_t L;            /* candidate list length (the reference's ef / TOPM) */
+    uint32_t K;            /* results per query (reference: 10) */
+    uint32_t rl;           /* recycle list length (reference: 10), <= 16 */
+    uint32_t postfilter;   /* --postfilter: queries with >= this many cells skip traversal */
+    const uint32_t* entry_points;  /* R cell-local entry ids, or NULL for the
+                                      reference's mt19937 draw (gpu_graph.cu:12503-12526) */
+} gf_search_opts;
+
+#define GF_NCOUNTERS 8  /* per-query counters, same order as the oracle's */
+typedef struct {
+    double ms_traverse;      /* device time of the traversal kernel */
+    double ms_bruteforce;    /* device time of the brute-force kernel */
+    double ms_total;         /* device time of the whole search stage */
+    uint32_t q_traverse, q_bruteforce, q_empty;
+    uint64_t n_expand, n_dist, n_attr, n_cross, n_lrow, n_scan, n_pass;
+    double bytes_traverse;   /* algorithmic HBM bytes of the traversal kernel */
+    double bytes_bruteforce; /* algorithmic HBM bytes of the brute-force kernel */
+} gf_search_stats;
+
+gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids /*Q*K*/,
+                    float* dists /*Q*K or NULL*/, gf_search_stats* stats /*or NULL*/);
+
+/* Inspection / injection of the batch's intermediate state, for parity
+ * tests and for callers that compute cell lists themselves.
+ * cells is Q*P (row q holds counts[q] cell ids), the reference's
+ * partition_infos[0..3] without compaction. */
+gf_status gf_batch_get_cells(const gf_batch* b, uint32_t* cells, uint32_t* counts,
+                             uint32_t* little, uint32_t* selcount);
+gf_status gf_batch_set_cells(gf_batch* b, const uint32_t* cells, const uint32_t* counts,
+                             const uint32_t* little);
+gf_status gf_batch_get_centroid(const gf_batch* b, float* dist /*Q*C*/, uint32_t* topc /*Q*topc*/);
+gf_status gf_batch_get_counters(const gf_batch* b, uint32_t* counters /*Q*GF_NCOUNTERS*/);
+
+/* f2h (tools.cuh:308-320) on the device: out[i] = binary16(x[i]*alpha), RNE. */
+gf_status gf_f2h(const float* x, size_t n, float alpha, uint16_t* out);
+/* find_norm (tools.cuh:1561-1586) on the device: squared norms of fp16 rows. */
+gf_status gf_row_norms_f16(const uint16_t* x, uint32_t n, uint32_t D, float* out);
+/* Entry points of the reference's host wrapper (gpu_graph.cu:12503-12526):
+ * mt19937 default seed, distinct uniform draws in [0, N-(P-1)*ceil(N/P)),
+ * std::random_shuffle after srand(1) (this reseeds the process's rand()). */
+gf_status gf_entry_points(uint32_t N, uint32_t P, uint32_t R, uint32_t* out);
+
+const char* gf_status_str(gf_status s);
+const char* gf_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GARFIELD_H */

@@ -1,0 +1,676 @@
+// CPU oracle for the Garfield query path -- TEST INFRASTRUCTURE ONLY.
+// Restates the reference (ZJU-DAILY/Garfield indexsearch/*.cu) in plain C++;
+// see garfield_oracle.h for the rules that replace the reference's races and
+// out-of-bounds reads.  Only tests/, __graft_entry__.smoke() and bench.py's
+// cpu_baseline leg load this library; the product (libgarfield.so) never does.
+#include "garfield_oracle.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <limits>
+#include <random>
+#include <unordered_set>
+#include <vector>
+#include <omp.h>
+
+namespace {
+
+const uint32_t SENT = 0xFFFFFFFFu;   // reference's empty candidate id
+const uint32_t EXPL = 0x80000000u;   // reference's "explored" bit
+const uint32_t IDM = 0x7FFFFFFFu;
+const float INF = std::numeric_limits<float>::infinity();
+const uint32_t MAX_ITER = 10000;     // gpu_graph.cu:39
+const uint32_t HASH_RESET = 4;       // gpu_graph.cu:34
+const uint32_t XSLOTS = 128;         // gpu_graph.cu:42 EXTEND_POINTS_NUM
+const uint32_t XSTEP = 64;           // 128 / base_number(2), gpu_graph.cu:3267
+
+uint32_t f32_bits(float f) { uint32_t u; std::memcpy(&u, &f, 4); return u; }
+
+// Lanes per row of the HIP distance kernels: a row is split in 16-byte chunks,
+// LPR = next power of two >= chunk count, clamped to [8, 64].
+uint32_t lanes_per_row(uint32_t D, int vdtype) {
+    uint32_t elems = vdtype ? 8u : 4u;
+    uint32_t nch = (D + elems - 1) / elems;
+    uint32_t lpr = 8;
+    while (lpr < nch && lpr < 64) lpr <<= 1;
+    return lpr;
+}
+
+// Canonical distance: lane l of LPR accumulates chunks l, l+LPR, ... with fp32
+// fma in element order; the lane sums are combined by an xor butterfly.
+float canon_dist(const float* q, const float* x, uint32_t D, int vdtype) {
+    const uint32_t ce = vdtype ? 8u : 4u;
+    const uint32_t nch = D / ce;
+    const uint32_t lpr = lanes_per_row(D, vdtype);
+    float s[64];
+    for (uint32_t l = 0; l < lpr; ++l) {
+        float acc = 0.0f;
+        for (uint32_t c = l; c < nch; c += lpr)
+            for (uint32_t e = 0; e < ce; ++e) {
+                float d = q[c * ce + e] - x[c * ce + e];
+                acc = std::fmaf(d, d, acc);
+            }
+        s[l] = acc;
+    }
+    for (uint32_t m = lpr / 2; m >= 1; m >>= 1) {
+        float t[64];
+        for (uint32_t l = 0; l < lpr; ++l) t[l] = s[l] + s[l ^ m];
+        std::memcpy(s, t, sizeof(float) * lpr);
+    }
+    return s[0];
+}
+
+struct Cand { float d; uint32_t id; };
+
+struct Ctx {
+    const orc_index* ix;
+    const uint32_t* cmpos;   // point id -> cell-major position (tie key)
+    const uint32_t* cellof;  // point id -> cell
+};
+
+inline uint32_t tiekey(const Ctx& c, uint32_t id) {
+    return id == SENT ? 0xFFFFFFFFu : c.cmpos[id & IDM];
+}
+inline bool cless(const Ctx& c, const Cand& x, const Cand& y) {
+    if (x.d != y.d) return x.d < y.d;
+    return tiekey(c, x.id) < tiekey(c, y.id);
+}
+
+void sort_stable(const Ctx& c, Cand* v, size_t n) {
+    std::stable_sort(v, v + n, [&](const Cand& x, const Cand& y) { return cless(c, x, y); });
+}
+
+// Merged position of every element of sorted X (n) and sorted Y (m):
+// X_i -> i + #{Y <= X_i}, Y_j -> j + #{X < Y_j}  (gpu_graph.cu:162-222).
+void merge_positions(const Ctx& c, const Cand* X, size_t n, const Cand* Y, size_t m,
+                     std::vector<size_t>& px, std::vector<size_t>& py) {
+    px.resize(n); py.resize(m);
+    auto lt = [&](const Cand& a, const Cand& b) { return cless(c, a, b); };
+    for (size_t i = 0; i < n; ++i)
+        px[i] = i + (std::upper_bound(Y, Y + m, X[i], lt) - Y);
+    for (size_t j = 0; j < m; ++j)
+        py[j] = j + (std::lower_bound(X, X + n, Y[j], lt) - X);
+}
+
+// merge_top (gpu_graph.cu:162-222): X keeps the n smallest, Y the next m.
+void merge_plain(const Ctx& c, Cand* X, size_t n, Cand* Y, size_t m) {
+    std::vector<size_t> px, py;
+    merge_positions(c, X, n, Y, m, px, py);
+    std::vector<Cand> out(n + m);
+    for (size_t i = 0; i < n; ++i) out[px[i]] = X[i];
+    for (size_t j = 0; j < m; ++j) out[py[j]] = Y[j];
+    std::copy(out.begin(), out.begin() + n, X);
+    std::copy(out.begin() + n, out.end(), Y);
+}
+
+struct QueryState {
+    const Ctx* c;
+    const float* q;          // query as fp32 values (fp16 path: converted)
+    const float* lo;
+    const float* hi;
+    std::vector<float> xbuf;
+    uint32_t ctr[ORC_NCNT];
+};
+
+bool passes(const QueryState& s, uint32_t gid) {
+    const orc_index* ix = s.c->ix;
+    for (uint32_t d = 0; d < ix->a; ++d) {
+        float v = ix->attrs[(size_t)gid * ix->a + d];
+        if (!(v >= s.lo[d] && v <= s.hi[d])) return false;
+    }
+    return true;
+}
+
+float point_dist(QueryState& s, uint32_t gid) {
+    const orc_index* ix = s.c->ix;
+    const uint32_t D = ix->D;
+    if (ix->vdtype == 0)
+        return canon_dist(s.q, ix->vec_f32 + (size_t)gid * D, D, 0);
+    s.xbuf.resize(D);
+    for (uint32_t i = 0; i < D; ++i) s.xbuf[i] = orc_h2f(ix->vec_f16[(size_t)gid * D + i]);
+    return canon_dist(s.q, s.xbuf.data(), D, 1);
+}
+
+// merge_top_with_recycle_list (gpu_graph.cu:224-315) followed by the
+// evictee sort and merge into the recycle list (gpu_graph.cu:3412-3425,
+// 3536-3546).  B holds the leftovers afterwards (the reference's B region).
+void merge_with_recycle(QueryState& s, Cand* A, size_t L, Cand* B, size_t R,
+                        Cand* Rc, size_t rl) {
+    const Ctx& c = *s.c;
+    std::vector<size_t> px, py;
+    merge_positions(c, A, L, B, R, px, py);
+    std::vector<Cand> nA(L), nB(R);
+    for (size_t i = 0; i < L; ++i) {
+        if (px[i] < L) { nA[px[i]] = A[i]; continue; }
+        Cand x = A[i];
+        if (x.id != SENT && !passes(s, x.id & 0x3FFFFFFFu)) x = {INF, SENT};
+        nB[px[i] - L] = x;
+    }
+    for (size_t j = 0; j < R; ++j) {
+        if (py[j] < L) nA[py[j]] = B[j];
+        else nB[py[j] - L] = {INF, SENT};
+    }
+    std::copy(nA.begin(), nA.end(), A);
+    std::copy(nB.begin(), nB.end(), B);
+    sort_stable(c, B, R);
+    if (B[0].id != SENT) merge_plain(c, Rc, rl, B, R);
+}
+
+bool in_cell(const Ctx& c, uint32_t gid, uint32_t cell) { return c.cellof[gid] == cell; }
+
+void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_all,
+                const float* hi_all, const uint32_t* cells, const uint32_t* counts,
+                const uint32_t* little, const uint32_t* entry, uint32_t L, uint32_t K,
+                uint32_t rl, uint32_t postfilter, uint32_t* out_ids, float* out_dist,
+                uint32_t* counters) {
+    const orc_index* ix = c.ix;
+    const uint32_t D = ix->D, R = ix->R, E = ix->E, P = ix->P, a = ix->a;
+    std::vector<float> qv(D);
+    if (ix->vdtype == 0) {
+        std::memcpy(qv.data(), (const float*)queries + (size_t)qi * D, sizeof(float) * D);
+    } else {
+        const uint16_t* qh = (const uint16_t*)queries + (size_t)qi * D;
+        for (uint32_t i = 0; i < D; ++i) qv[i] = orc_h2f(qh[i]);
+    }
+    QueryState s;
+    s.c = &c; s.q = qv.data(); s.lo = lo_all + (size_t)qi * a; s.hi = hi_all + (size_t)qi * a;
+    std::memset(s.ctr, 0, sizeof(s.ctr));
+
+    const uint32_t* cl = cells + (size_t)qi * P;
+    const uint32_t cnt = counts[qi], lit = little[qi];
+    const bool traverse = (cnt < postfilter && cnt != lit);   // gpu_graph.cu:3377
+    std::vector<Cand> out;
+
+    auto cell_size = [&](uint32_t cc) { return ix->offset[cc + 1] - ix->offset[cc]; };
+
+    if (traverse) {
+        s.ctr[ORC_C_ROUTE] = 1;
+        std::vector<Cand> A(L, Cand{INF, SENT}), B(R, Cand{INF, SENT}), Rc(rl, Cand{INF, SENT});
+        std::vector<Cand> W(XSLOTS);
+        std::unordered_set<uint32_t> H;
+        H.reserve(4 * (L + XSLOTS + 4 * R));
+        // Entry points of the first cell (gpu_graph.cu:3347-3351).  The
+        // reference inserts their *point ids* into the visited set, which is
+        // otherwise keyed by cell-local ids; kept as is.  entry[j] is reduced
+        // modulo the cell size (quirk Q2 reads past the cell otherwise).
+        {
+            const uint32_t c0 = cl[0], sz0 = cell_size(c0);
+            for (uint32_t j = 0; j < R; ++j) {
+                uint32_t gid = ix->global_idx[ix->offset[c0] + entry[j] % sz0];
+                B[j] = {INF, gid};
+                H.insert(gid);
+            }
+        }
+        for (uint32_t p_i = 0; p_i < cnt; ++p_i) {
+            const uint32_t cur = cl[p_i];
+            const uint32_t base = ix->offset[cur];
+            // Distances of the cell's entries (gpu_graph.cu:3384-3405).  For
+            // later cells the entries come from the sorted cross-edge slots,
+            // whose distances were just computed; the reference recomputes the
+            // same values, here they are reused.
+            for (uint32_t j = 0; j < R; ++j) {
+                if (B[j].id == SENT) { B[j].d = INF; continue; }
+                if (p_i > 0) continue;
+                B[j].d = point_dist(s, B[j].id);
+                s.ctr[ORC_C_DIST]++; s.ctr[ORC_C_ATTR]++;
+            }
+            sort_stable(c, B.data(), R);
+            merge_with_recycle(s, A.data(), L, B.data(), R, Rc.data(), rl);
+
+            for (uint32_t it = 0; it < MAX_ITER; ++it) {
+                if ((it + 1) % HASH_RESET == 0) {            // gpu_graph.cu:3441-3454
+                    H.clear();
+                    for (const auto* arr : {&A, &B})
+                        for (const Cand& x : *arr) {
+                            if (x.id == SENT) continue;
+                            uint32_t g = x.id & IDM;
+                            H.insert(ix->local_idx[g]);
+                            if (!in_cell(c, g, cur)) s.ctr[ORC_C_LROW]++;
+                        }
+                }
+                uint32_t sel = L;                            // gpu_graph.cu:3457-3485
+                for (uint32_t j = 0; j < L; ++j)
+                    if ((A[j].id & EXPL) == 0) { sel = j; break; }
+                if (sel == L) break;
+                A[sel].id |= EXPL;
+                s.ctr[ORC_C_EXPAND]++;
+                const uint32_t tl = ix->local_idx[A[sel].id & IDM];
+                for (uint32_t j = 0; j < R; ++j) {           // gpu_graph.cu:3500-3530
+                    uint32_t nl = ix->graph[(size_t)(base + tl) * R + j];
+                    uint32_t gid = ix->global_idx[base + nl];
+                    bool isnew = H.insert(nl).second;
+                    B[j] = {INF, gid};
+                    s.ctr[ORC_C_ATTR]++;
+                    if (isnew) { B[j].d = point_dist(s, gid); s.ctr[ORC_C_DIST]++; }
+                }
+                sort_stable(c, B.data(), R);
+                if (B[0].id != SENT)
+                    merge_with_recycle(s, A.data(), L, B.data(), R, Rc.data(), rl);
+            }
+            // End of cell (gpu_graph.cu:3555-3560).
+            for (Cand& x : A) x.id |= EXPL;
+            H.clear();
+            if (p_i + 1 < cnt) {                             // gpu_graph.cu:3564-3642
+                const uint32_t nxt = cl[p_i + 1];
+                const uint32_t nbase = ix->offset[nxt], nsz = cell_size(nxt);
+                for (uint32_t i = 0; i < XSLOTS; ++i) W[i] = {INF, SENT};
+                for (uint32_t i = 0; i < std::min(XSTEP, L); ++i)
+                    if (A[i].id != SENT) s.ctr[ORC_C_CROSS]++;
+                for (uint32_t i = 0; i < XSLOTS; ++i) {
+                    const uint32_t ci = i % XSTEP;
+                    if (ci >= L || A[ci].id == SENT) continue;  // quirk Q7: ci >= L, not ci > L
+                    const uint32_t g = A[ci].id & IDM;
+                    bool got = false;
+                    for (uint32_t j = 0; j < E && !got; ++j) {
+                        uint32_t nl = ix->cross[(size_t)g * P * E + (size_t)nxt * E + j];
+                        if (H.insert(nl).second) { W[i].id = ix->global_idx[nbase + nl]; got = true; }
+                    }
+                    if (!got)                                // quirk Q6: scan [0, |cell|)
+                        for (uint32_t rp = 0; rp < nsz; ++rp)
+                            if (H.insert(rp).second) { W[i].id = ix->global_idx[nbase + rp]; break; }
+                }
+                for (uint32_t i = 0; i < XSLOTS; ++i) {
+                    if (W[i].id == SENT) continue;
+                    W[i].d = point_dist(s, W[i].id);
+                    s.ctr[ORC_C_DIST]++; s.ctr[ORC_C_ATTR]++;
+                }
+                sort_stable(c, W.data(), XSLOTS);
+                H.clear();
+                for (uint32_t j = 0; j < R; ++j) B[j] = W[j];
+                for (uint32_t i = 0; i < XSLOTS; ++i)
+                    if (W[i].id != SENT) H.insert(ix->local_idx[W[i].id]);
+                merge_plain(c, A.data(), L, W.data() + R, XSTEP);
+                for (const Cand& x : A) {
+                    if (x.id == SENT) continue;
+                    uint32_t g = x.id & IDM;
+                    H.insert(ix->local_idx[g]);
+                    if (!in_cell(c, g, nxt)) s.ctr[ORC_C_LROW]++;
+                }
+            }
+        }
+        // Post-filter + recycle merge (gpu_graph.cu:4025-4047).
+        for (Cand& x : A)
+            if (x.id != SENT && !passes(s, x.id & IDM)) x = {INF, SENT};
+        sort_stable(c, A.data(), L);
+        if (Rc[0].id != SENT) merge_plain(c, A.data(), L, Rc.data(), rl);
+        out = A;
+    } else {
+        // Filtered brute force over the first `little` cells (gpu_graph.cu:3788-4022).
+        s.ctr[ORC_C_ROUTE] = lit ? 2 : 0;
+        std::vector<Cand> found;
+        for (uint32_t g = 0; g < lit; ++g) {
+            const uint32_t cc = cl[g];
+            const uint32_t b = ix->offset[cc], sz = cell_size(cc);
+            s.ctr[ORC_C_SCAN] += sz;
+            for (uint32_t l = 0; l < sz; ++l) {
+                uint32_t gid = ix->global_idx[b + l];
+                if (!passes(s, gid)) continue;
+                s.ctr[ORC_C_PASS]++;
+                found.push_back({point_dist(s, gid), gid});
+            }
+        }
+        size_t kk = std::min<size_t>(K, found.size());
+        std::partial_sort(found.begin(), found.begin() + kk, found.end(),
+                          [&](const Cand& x, const Cand& y) { return cless(c, x, y); });
+        found.resize(kk);
+        out = found;
+    }
+    // Output: the first K distinct ids (quirk Q8: the reference may repeat ids).
+    uint32_t n = 0, prev = SENT;
+    for (const Cand& x : out) {
+        if (n >= K) break;
+        if (x.id == SENT) break;
+        uint32_t id = x.id & IDM;
+        if (n > 0 && id == prev) continue;
+        out_ids[(size_t)qi * K + n] = id;
+        out_dist[(size_t)qi * K + n] = x.d;
+        prev = id; ++n;
+    }
+    for (; n < K; ++n) {
+        out_ids[(size_t)qi * K + n] = ORC_SENTINEL_ID;
+        out_dist[(size_t)qi * K + n] = INF;
+    }
+    if (counters) std::memcpy(counters + (size_t)qi * ORC_NCNT, s.ctr, sizeof(s.ctr));
+}
+
+}  // namespace
+
+extern "C" {
+
+void orc_idx_mapper(uint32_t N, uint32_t P, const uint32_t* global_pid,
+                    uint32_t* global_idx, uint32_t* local_idx, uint32_t* offset) {
+    std::vector<uint32_t> sz(P, 0), fill(P, 0);
+    for (uint32_t i = 0; i < N; ++i) sz[global_pid[i]]++;
+    offset[0] = 0;
+    for (uint32_t c = 0; c < P; ++c) offset[c + 1] = offset[c] + sz[c];
+    for (uint32_t i = 0; i < N; ++i) {
+        uint32_t c = global_pid[i];
+        global_idx[offset[c] + fill[c]] = i;
+        local_idx[i] = fill[c]++;
+    }
+}
+
+uint16_t orc_f2h_one(float x, float alpha) {
+    float f = x * alpha;
+    uint32_t u = f32_bits(f);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    uint32_t ex = (u >> 23) & 0xFFu, man = u & 0x7FFFFFu;
+    if (ex == 0xFFu) return (uint16_t)(sign | 0x7C00u | (man ? (0x200u | (man >> 13)) : 0u));
+    if (ex == 0 && man == 0) return sign;
+    int e = (int)ex - 127 + 15;
+    if (e <= 0) {                       // binary16 subnormal (or zero)
+        uint32_t m = man | (ex ? 0x800000u : 0u);
+        int shift = 14 - e;
+        if (shift > 24) return sign;
+        uint32_t hm = m >> shift, rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (hm & 1u))) hm++;
+        return (uint16_t)(sign | hm);
+    }
+    uint32_t hm = man >> 13, rem = man & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (hm & 1u))) {
+        hm++;
+        if (hm == 0x400u) { hm = 0; e++; }
+    }
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    return (uint16_t)(sign | ((uint32_t)e << 10) | hm);
+}
+
+void orc_f2h(const float* x, size_t n, float alpha, uint16_t* out) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_f2h_one(x[i], alpha);
+}
+
+float orc_h2f(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t ex = (h >> 10) & 0x1Fu, man = h & 0x3FFu;
+    uint32_t u;
+    if (ex == 0) {
+        if (man == 0) u = sign;
+        else {                           // subnormal: normalise
+            int e = -1;
+            do { man <<= 1; ++e; } while ((man & 0x400u) == 0);
+            u = sign | ((uint32_t)(127 - 15 - e) << 23) | ((man & 0x3FFu) << 13);
+        }
+    } else if (ex == 0x1Fu) {
+        u = sign | 0x7F800000u | (man << 13);
+    } else {
+        u = sign | ((ex - 15 + 127) << 23) | (man << 13);
+    }
+    float f; std::memcpy(&f, &u, 4); return f;
+}
+
+void orc_row_norms_f16(const uint16_t* x, uint32_t n, uint32_t D, float* out) {
+    for (uint32_t r = 0; r < n; ++r) {
+        float s[64];
+        for (uint32_t l = 0; l < 64; ++l) {
+            float acc = 0.0f;
+            for (uint32_t j = l; j < D; j += 64) {
+                float v = orc_h2f(x[(size_t)r * D + j]);
+                acc = std::fmaf(v, v, acc);
+            }
+            s[l] = acc;
+        }
+        for (uint32_t m = 32; m >= 1; m >>= 1) {
+            float t[64];
+            for (uint32_t l = 0; l < 64; ++l) t[l] = s[l] + s[l ^ m];
+            std::memcpy(s, t, sizeof(s));
+        }
+        out[r] = s[0];
+    }
+}
+
+void orc_centres_hist(uint32_t N, uint32_t D, uint32_t C, uint32_t P,
+                      const float* data, const int32_t* labels,
+                      const uint32_t* global_pid, int32_t contiguous,
+                      float* centres, uint32_t* hist) {
+    std::vector<uint32_t> num(C, 0);
+    std::fill(centres, centres + (size_t)C * D, 0.0f);
+    std::fill(hist, hist + (size_t)P * C, 0u);
+    const uint32_t avg = (N + P - 1) / P;
+    for (uint32_t i = 0; i < N; ++i) {
+        uint32_t pid = contiguous ? std::min(i / avg, P - 1) : global_pid[i];
+        uint32_t cid = (uint32_t)labels[i];
+        num[cid]++; hist[(size_t)pid * C + cid]++;
+        for (uint32_t j = 0; j < D; ++j) centres[(size_t)cid * D + j] += data[(size_t)i * D + j];
+    }
+    for (uint32_t c = 0; c < C; ++c)
+        for (uint32_t j = 0; j < D; ++j) centres[(size_t)c * D + j] /= (float)num[c];
+}
+
+void orc_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi,
+               const uint32_t* grid, const float* l_q, const float* r_q,
+               uint32_t* cells, uint32_t* counts) {
+    uint32_t P = 1;
+    for (uint32_t d = 0; d < a; ++d) P *= grid[d];
+    std::vector<uint32_t> doff(a, 0);
+    for (uint32_t d = 1; d < a; ++d) doff[d] = doff[d - 1] + grid[d - 1];
+    for (uint32_t q = 0; q < Q; ++q) {
+        std::vector<int64_t> cl(a), ch(a);
+        bool empty = false;
+        for (uint32_t d = 0; d < a; ++d) {
+            const uint32_t g = grid[d];
+            const float* rq = r_q + doff[d];
+            const float* lq = l_q + doff[d];
+            int64_t i = 0;                           // to_lower_bound_linear_scan
+            while (i < g && rq[i] < lo[(size_t)q * a + d]) ++i;
+            int64_t j = 0;                           // to_upper_bound_linear_scan
+            while (j < g && lq[j] <= hi[(size_t)q * a + d]) ++j;
+            cl[d] = i; ch[d] = j - 1;
+            if (cl[d] >= g || ch[d] < 0) empty = true;   // quirk Q16
+            ch[d] = std::max(ch[d], cl[d]);
+        }
+        std::vector<char> sel(P, 0);
+        if (!empty) {
+            std::vector<int64_t> idx(cl);
+            while (true) {
+                uint32_t pid = 0, f = 1;
+                for (int d = (int)a - 1; d >= 0; --d) { pid += (uint32_t)idx[d] * f; f *= grid[d]; }
+                sel[pid] = 1;
+                uint32_t pos = 0;
+                while (pos < a) {
+                    idx[pos]++;
+                    if (idx[pos] <= ch[pos]) break;
+                    idx[pos] = cl[pos];
+                    ++pos;
+                }
+                if (pos >= a) break;
+            }
+        }
+        uint32_t n = 0;
+        for (uint32_t p = 0; p < P; ++p)
+            if (sel[p]) cells[(size_t)q * P + n++] = p;
+        counts[q] = n;
+    }
+}
+
+void orc_selectivity(uint32_t Q, uint32_t N, uint32_t a, const float* attrs,
+                     const float* lo, const float* hi, float threshold,
+                     const uint32_t* counts, uint32_t* selcount, uint32_t* little,
+                     int nthreads) {
+#pragma omp parallel for schedule(dynamic, 4) num_threads(nthreads > 0 ? nthreads : omp_get_max_threads())
+    for (int64_t q = 0; q < (int64_t)Q; ++q) {
+        uint32_t cnt = 0;
+        for (uint32_t i = 0; i < N; ++i) {
+            bool ok = true;
+            for (uint32_t d = 0; d < a && ok; ++d) {
+                float v = attrs[(size_t)i * a + d];
+                ok = v >= lo[q * a + d] && v <= hi[q * a + d];
+            }
+            cnt += ok;
+        }
+        selcount[q] = cnt;
+        float proportion = (float)((1.0 * cnt) / (1.0 * N));   // real_dataset_adapter.cuh:378
+        little[q] = proportion <= threshold ? counts[q] : 0u;
+    }
+}
+
+void orc_centroid_dist_f64(uint32_t Q, uint32_t C, uint32_t D,
+                           const uint16_t* qh, const uint16_t* ch, double* out) {
+    for (uint32_t q = 0; q < Q; ++q)
+        for (uint32_t c = 0; c < C; ++c) {
+            double qq = 0, cc = 0, qc = 0;
+            for (uint32_t j = 0; j < D; ++j) {
+                double x = orc_h2f(qh[(size_t)q * D + j]), y = orc_h2f(ch[(size_t)c * D + j]);
+                qq += x * x; cc += y * y; qc += x * y;
+            }
+            out[(size_t)q * C + c] = qq + cc - 2.0 * qc;
+        }
+}
+
+void orc_topk_clusters(uint32_t Q, uint32_t C, uint32_t k, const float* dist, uint32_t* out) {
+    std::vector<uint32_t> idx(C);
+    for (uint32_t q = 0; q < Q; ++q) {
+        const float* d = dist + (size_t)q * C;
+        for (uint32_t c = 0; c < C; ++c) idx[c] = c;
+        auto key = [&](uint32_t c) { float v = d[c]; return std::isnan(v) ? INF : v; };
+        uint32_t kk = std::min(k, C);
+        std::partial_sort(idx.begin(), idx.begin() + kk, idx.end(), [&](uint32_t x, uint32_t y) {
+            float a = key(x), b = key(y);
+            return a != b ? a < b : x < y;
+        });
+        for (uint32_t t = 0; t < k; ++t) out[(size_t)q * k + t] = t < kk ? idx[t] : 0u;
+    }
+}
+
+void orc_sort_cells(uint32_t Q, uint32_t P, uint32_t C, uint32_t k, uint32_t* cells,
+                    const uint32_t* counts, const uint32_t* topk, const uint32_t* hist) {
+    for (uint32_t q = 0; q < Q; ++q) {
+        uint32_t* cl = cells + (size_t)q * P;
+        const uint32_t n = counts[q];
+        std::vector<std::pair<int64_t, uint32_t>> v(n);
+        for (uint32_t i = 0; i < n; ++i) {
+            int64_t sc = 0;
+            for (uint32_t t = 0; t < k; ++t) sc += hist[(size_t)cl[i] * C + topk[(size_t)q * k + t]];
+            v[i] = {sc, cl[i]};
+        }
+        std::sort(v.begin(), v.end(), [](const std::pair<int64_t, uint32_t>& x,
+                                         const std::pair<int64_t, uint32_t>& y) {
+            return x.first != y.first ? x.first > y.first : x.second < y.second;
+        });
+        for (uint32_t i = 0; i < n; ++i) cl[i] = v[i].second;
+    }
+}
+
+void orc_entry_points(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
+    const uint32_t avg = (N + P - 1) / P;
+    const uint32_t rand_max = N - (P - 1) * avg;
+    std::mt19937 rng;
+    std::uniform_int_distribution<> intd(0, (int)rand_max - 1);
+    const uint32_t want = std::min<uint32_t>(R * 10, rand_max);
+    std::vector<unsigned> v(want);
+    std::unordered_set<unsigned> seen;
+    uint32_t k = 0;
+    while (k < want) {
+        unsigned t = (unsigned)intd(rng);
+        if (!seen.count(t)) { seen.insert(t); v[k++] = t; }
+    }
+    std::srand(1);
+    std::random_shuffle(v.begin(), v.begin() + want);
+    for (uint32_t j = 0; j < R; ++j) out[j] = j < want ? v[j] : j;
+}
+
+float orc_distance(const orc_index* ix, const void* q, uint32_t gid) {
+    std::vector<float> qv(ix->D), xv(ix->D);
+    if (ix->vdtype == 0)
+        return canon_dist((const float*)q, ix->vec_f32 + (size_t)gid * ix->D, ix->D, 0);
+    for (uint32_t i = 0; i < ix->D; ++i) {
+        qv[i] = orc_h2f(((const uint16_t*)q)[i]);
+        xv[i] = orc_h2f(ix->vec_f16[(size_t)gid * ix->D + i]);
+    }
+    return canon_dist(qv.data(), xv.data(), ix->D, 1);
+}
+
+void orc_search(const orc_index* ix, const void* queries, uint32_t Q,
+                const float* lo, const float* hi,
+                const uint32_t* cells, const uint32_t* counts, const uint32_t* little,
+                const uint32_t* entry, uint32_t L, uint32_t K, uint32_t rl,
+                uint32_t postfilter, uint32_t* out_ids, float* out_dist,
+                uint32_t* counters, int nthreads) {
+    std::vector<uint32_t> cmpos(ix->N), cellof(ix->N);
+    for (uint32_t c = 0; c < ix->P; ++c)
+        for (uint32_t r = ix->offset[c]; r < ix->offset[c + 1]; ++r) {
+            cmpos[ix->global_idx[r]] = r;
+            cellof[ix->global_idx[r]] = c;
+        }
+    Ctx c{ix, cmpos.data(), cellof.data()};
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads > 0 ? nthreads : omp_get_max_threads())
+    for (int64_t q = 0; q < (int64_t)Q; ++q)
+        search_one(c, queries, (uint32_t)q, lo, hi, cells, counts, little, entry, L, K, rl,
+                   postfilter, out_ids, out_dist, counters);
+}
+
+void orc_ground_truth(uint32_t N, uint32_t D, uint32_t a, const float* data,
+                      const float* attrs, uint32_t Q, const float* queries,
+                      const float* lo, const float* hi, uint32_t K,
+                      uint32_t* gt_ids, double* gt_dist, int nthreads) {
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads > 0 ? nthreads : omp_get_max_threads())
+    for (int64_t q = 0; q < (int64_t)Q; ++q) {
+        std::vector<std::pair<double, uint32_t>> best;   // max-heap of size K
+        auto cmp = [](const std::pair<double, uint32_t>& x, const std::pair<double, uint32_t>& y) {
+            return x.first != y.first ? x.first < y.first : x.second < y.second;
+        };
+        const float* qv = queries + (size_t)q * D;
+        for (uint32_t i = 0; i < N; ++i) {
+            bool ok = true;
+            for (uint32_t d = 0; d < a && ok; ++d) {
+                float v = attrs[(size_t)i * a + d];
+                ok = v >= lo[q * a + d] && v <= hi[q * a + d];
+            }
+            if (!ok) continue;
+            double s = 0;
+            const float* x = data + (size_t)i * D;
+            for (uint32_t j = 0; j < D; ++j) { double t = (double)qv[j] - (double)x[j]; s += t * t; }
+            std::pair<double, uint32_t> e{s, i};
+            if (best.size() < K) { best.push_back(e); std::push_heap(best.begin(), best.end(), cmp); }
+            else if (cmp(e, best.front())) {
+                std::pop_heap(best.begin(), best.end(), cmp);
+                best.back() = e;
+                std::push_heap(best.begin(), best.end(), cmp);
+            }
+        }
+        std::sort(best.begin(), best.end(), cmp);
+        for (uint32_t k = 0; k < K; ++k) {
+            gt_ids[(size_t)q * K + k] = k < best.size() ? best[k].second : ORC_SENTINEL_ID;
+            gt_dist[(size_t)q * K + k] = k < best.size() ? best[k].first : (double)INF;
+        }
+    }
+}
+
+double orc_recall(uint32_t Q, uint32_t K, const uint32_t* res, const uint32_t* gt,
+                  const double* gt_dist, const double* res_dist_exact, int tie_aware) {
+    double total = 0;
+    for (uint32_t q = 0; q < Q; ++q) {
+        std::vector<uint32_t> g, r;
+        double kth = -1;
+        for (uint32_t k = 0; k < K; ++k) {
+            if (gt[(size_t)q * K + k] != ORC_SENTINEL_ID) {
+                g.push_back(gt[(size_t)q * K + k]);
+                kth = gt_dist[(size_t)q * K + k];
+            }
+        }
+        if (g.empty()) { total += 1.0; continue; }
+        uint32_t hit = 0;
+        if (!tie_aware) {
+            for (uint32_t k = 0; k < K; ++k) r.push_back(res[(size_t)q * K + k]);
+            std::sort(r.begin(), r.end());
+            std::sort(g.begin(), g.end());
+            std::vector<uint32_t> inter;
+            std::set_intersection(r.begin(), r.end(), g.begin(), g.end(), std::back_inserter(inter));
+            hit = (uint32_t)inter.size();
+        } else {
+            std::unordered_set<uint32_t> seen;
+            for (uint32_t k = 0; k < K; ++k) {
+                uint32_t id = res[(size_t)q * K + k];
+                if (id == ORC_SENTINEL_ID || seen.count(id)) continue;
+                seen.insert(id);
+                if (res_dist_exact[(size_t)q * K + k] <= kth) hit++;
+            }
+            hit = std::min<uint32_t>(hit, (uint32_t)g.size());
+        }
+        total += (double)hit / (double)g.size();
+    }
+    return total / Q;
+}
+
+}  // extern "C"

@@ -1,0 +1,126 @@
+"""CPU checks of the boundary: libgarfield.so loads and exports every entry
+point include/garfield.h declares, the file formats round-trip, and the C++
+loaders reject malformed index files with status codes (no GPU needed: the
+files are validated before any device call)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from garfield_amd import formats, synth
+import garfield_amd._lib as gl
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "garfield.h")).read()
+    return sorted(set(re.findall(r"^(?:gf_status|const char\*)\s+(gf_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(gl.lib_path)
+    names = _declared()
+    assert len(names) >= 18
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(gl._SYMBOLS)
+
+
+def test_status_strings():
+    lib = gl.load()
+    assert lib.gf_status_str(0) == b"ok"
+    assert lib.gf_status_str(2) == b"i/o error"
+
+
+def test_entry_points_match_oracle():
+    from oracle import oracle as orc
+    for N, P, R in ((1_000_000, 16, 32), (100_000, 16, 16), (6000, 16, 16)):
+        assert np.array_equal(gl.entry_points(N, P, R), orc.entry_points(N, P, R))
+
+
+def test_format_round_trips(tmp_path):
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((50, 24)).astype(np.float32)
+    formats.write_fvecs(tmp_path / "a.fvecs", x)
+    assert np.array_equal(formats.read_fvecs(tmp_path / "a.fvecs"), x)
+    g = rng.integers(0, 50, (50, 8)).astype(np.uint32)
+    formats.write_graph(tmp_path / "g", g)
+    assert np.array_equal(formats.read_graph(tmp_path / "g"), g)
+    att = synth.uniform_attrs(50, 2, 1, hi=30)
+    formats.write_attrs(tmp_path / "at", att)
+    assert np.array_equal(formats.read_attrs(tmp_path / "at"), att)
+    l_q, r_q, pl, gp = synth.grid_scatter(att, [2, 3])
+    formats.write_grid(tmp_path / "grid", [2, 3], l_q, r_q, pl, gp)
+    grid, l2, r2, p2, g2 = formats.read_grid(tmp_path / "grid")
+    assert list(grid) == [2, 3] and np.array_equal(g2, gp)
+    assert all(np.array_equal(u, v) for u, v in zip(l2, l_q))
+    lo, hi = synth.ranges_for_selectivity(7, 2, 0.3, 2, hi=30)
+    formats.write_ranges(tmp_path / "r", lo, hi)
+    l3, h3 = formats.read_ranges(tmp_path / "r", 2)
+    assert np.array_equal(l3, lo) and np.array_equal(h3, hi)
+    gt = rng.integers(0, 50, (7, 10)).astype(np.uint32)
+    formats.write_gt(tmp_path / "gt", gt)
+    assert np.array_equal(formats.read_gt(tmp_path / "gt"), gt)
+    lab = rng.integers(0, 5, 50).astype(np.int32)
+    formats.write_labels(tmp_path / "lab", lab)
+    assert np.array_equal(formats.read_labels(tmp_path / "lab"), lab)
+
+
+def test_grid_matches_reference_layout():
+    # grid_scatter_V2: cell j of a dimension holds ranks [j*avg, (j+1)*avg)
+    att = np.array([[5, 0], [1, 0], [3, 0], [9, 0], [7, 0]], np.int32)
+    l_q, r_q, pl, gp = synth.grid_scatter(att, [2, 1])
+    assert list(l_q[0]) == [1, 7] and list(r_q[0]) == [5, 9]
+    assert list(pl[0]) == [0, 0, 0, 1, 1]
+    assert list(gp) == [0, 0, 0, 1, 1]
+
+
+@pytest.fixture(scope="module")
+def files(tmp_path_factory):
+    d = tmp_path_factory.mktemp("ix")
+    cfg = synth.config_small(N=1200, Q=4, R=8, C=6, sel=0.3, seed=3)
+    ix = synth.build_index(cfg["vectors"], cfg["attrs"], [2, 2], 8, 2, 6)
+    paths = synth.write_index(ix, str(d / "ix"))
+    return d, ix, paths
+
+
+def _open(paths, **kw):
+    try:
+        gl.Index.open(**paths, **kw)
+    except gl.GarfieldError as e:
+        return e.status
+    return 0
+
+
+def test_loader_rejects_missing_and_truncated_files(files):
+    d, ix, paths = files
+    p = dict(paths)
+    p["global_graph"] = str(d / "nope")
+    assert _open(p) == 2                                    # GF_E_IO
+    raw = open(paths["global_graph"], "rb").read()
+    bad = d / "trunc.cross"
+    bad.write_bytes(raw[:-12])
+    p = dict(paths)
+    p["global_graph"] = str(bad)
+    assert _open(p) == 3                                    # GF_E_FORMAT (size mismatch)
+    assert _open(paths, degree=4) == 3                      # --degree mismatch
+    att = formats.read_attrs(paths["attrs"])
+    formats.write_attrs(d / "att3", np.concatenate([att, att[:, :1]], 1))
+    p = dict(paths)
+    p["attrs"] = str(d / "att3")
+    assert _open(p) == 3                                    # attribute count differs from grid
+
+
+def test_loader_rejects_out_of_cell_ids(files):
+    d, ix, paths = files
+    g = formats.read_graph(paths["cagra_prefix"] + "0" + paths["cagra_suffix"])
+    g[3, 2] = g.shape[0] + 5
+    formats.write_graph(d / "bad_cell0.graph", g)
+    for c in range(1, 4):
+        os.link(paths["cagra_prefix"] + f"{c}" + paths["cagra_suffix"], d / f"bad_cell{c}.graph")
+    p = dict(paths)
+    p["cagra_prefix"] = str(d / "bad_cell")
+    assert _open(p) == 3   # GF_E_FORMAT, raised before the device is touched

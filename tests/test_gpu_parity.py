@@ -1,0 +1,198 @@
+"""Parity of the HIP path (libgarfield.so through its C ABI) with the CPU oracle.
+
+Bar: bit-exact for ids, cells, counts, routing, counters and fp32 traversal
+distances (the oracle restates the kernels' summation order); the MFMA
+centroid distances, whose accumulation order is the hardware's, are checked
+against an fp64 reference within a stated tolerance, and every stage after
+them is checked exactly on the GPU's own distances.
+"""
+import numpy as np
+import pytest
+
+from garfield_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _print_case(name, **kw):
+    print(f"[case] {name} " + " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def _oracle_pipeline(cfg, ix, prefilter, topc=4, gpu_topk=None):
+    from oracle import oracle as orc
+    l_q, r_q = synth.quantile_arrays(ix)
+    lo = cfg["lo"].astype(np.float32)
+    hi = cfg["hi"].astype(np.float32)
+    cells, cnt = orc.cells(lo, hi, ix["grid"], l_q, r_q)
+    sel, little = orc.selectivity(ix["attrs"], lo, hi, prefilter, cnt)
+    return lo, hi, cells, cnt, sel, little
+
+
+def _device(ix, **kw):
+    return synth.open_device_index(ix, **kw)
+
+
+def test_f2h_bit_exact():
+    import garfield_amd as gf
+    from oracle import oracle as orc
+    _print_case("f2h")
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2 ** 32, size=1 << 18, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = np.concatenate([x, np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e-8, 5.96e-8, 2.98e-8,
+                                     np.inf, -np.inf, 6.1e-5, 255.0, 0.1], np.float32)])
+    x = x[np.isfinite(x) | np.isinf(x)]
+    for alpha in (1.0, 0.01, 3.0):
+        g = gf.f2h(x, alpha)
+        o = orc.f2h(x, alpha)
+        assert np.array_equal(g, o), f"alpha={alpha}: {np.count_nonzero(g != o)} mismatches"
+
+
+def test_row_norms_f16_bit_exact():
+    import garfield_amd as gf
+    from oracle import oracle as orc
+    _print_case("norms")
+    rng = np.random.default_rng(1)
+    for D in (96, 128, 768):
+        x = orc.f2h(rng.standard_normal((300, D)).astype(np.float32) * 10)
+        assert np.array_equal(gf.row_norms_f16(x), orc.row_norms_f16(x)), D
+
+
+def test_cells_selectivity_routing(small_world):
+    cfg, ix = small_world
+    _print_case("cells", N=ix["vectors"].shape[0], Q=cfg["queries"].shape[0])
+    dev = _device(ix)
+    for prefilter in (0.0, 0.05, 0.3, 1.0):
+        lo, hi, cells, cnt, sel, little = _oracle_pipeline(cfg, ix, prefilter)
+        b = dev.batch(cfg["queries"], lo, hi)
+        b.mark_cells(prefilter)
+        gc, gcnt, glit, gsel = b.get_cells()
+        assert np.array_equal(gcnt, cnt)
+        for q in range(len(cnt)):
+            assert np.array_equal(gc[q, :cnt[q]], cells[q, :cnt[q]]), q
+        assert np.array_equal(gsel, sel)
+        assert np.array_equal(glit, little)
+        b.close()
+    dev.close()
+
+
+def test_centroid_order(small_world):
+    from oracle import oracle as orc
+    cfg, ix = small_world
+    _print_case("centroid")
+    dev = _device(ix)
+    lo, hi, cells, cnt, sel, little = _oracle_pipeline(cfg, ix, 0.0)
+    b = dev.batch(cfg["queries"], lo, hi)
+    b.mark_cells(0.0)
+    b.order_cells(4)
+    gdist, gtop = b.get_centroid()
+    cen, hist = orc.centres_hist(ix["vectors"], ix["labels"], ix["global_pid"], ix["P"])
+    qh = orc.f2h(cfg["queries"])
+    ch = orc.f2h(cen)
+    ref = orc.centroid_dist_f64(qh, ch)
+    qn = (orc.row_norms_f16(qh).astype(np.float64))
+    cn = (orc.row_norms_f16(ch).astype(np.float64))
+    # fp16 products are exact in fp32; the fp32 accumulation error is bounded
+    # by D * 2^-24 * sum|q_i c_i| <= D * 2^-24 * (|q|^2 + |c|^2) / 2, plus the
+    # rounding of the final sum.
+    tol = (128 * 2.0 ** -24 + 4 * 2.0 ** -24) * (qn[:, None] + cn[None, :]) + 1e-3
+    assert np.all(np.abs(gdist.astype(np.float64) - ref) <= tol)
+    # exact from here on, on the GPU's distances
+    assert np.array_equal(gtop, orc.topk_clusters(gdist, 4))
+    gc, gcnt, _, _ = b.get_cells()
+    ocells = orc.sort_cells(cells, cnt, gtop, hist)
+    for q in range(len(cnt)):
+        assert np.array_equal(gc[q, :cnt[q]], ocells[q, :cnt[q]]), q
+    b.close()
+    dev.close()
+
+
+def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, postfilter=1 << 30, Q=None):
+    import garfield_amd as gf
+    from oracle import oracle as orc
+    dev = _device(ix, vec_dtype=vec_dtype, f2h_factor=f2h_factor)
+    lo, hi, cells, cnt, sel, little = _oracle_pipeline(cfg, ix, prefilter)
+    queries = cfg["queries"] if Q is None else cfg["queries"][:Q]
+    lo, hi = lo[:len(queries)], hi[:len(queries)]
+    b = dev.batch(queries, lo, hi)
+    b.mark_cells(prefilter)
+    if ix["labels"] is not None:
+        b.order_cells(4)
+    gc, gcnt, glit, _ = b.get_cells()
+    ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], ix["R"])
+    ids, dists, st = b.search(L=L, K=10, rl=10, postfilter=postfilter, entry_points=ent)
+    ctr = b.get_counters()
+    vec16 = orc.f2h(ix["vectors"], f2h_factor) if vec_dtype == 1 else None
+    O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"],
+                        ix["cross"], vec_f16=vec16)
+    oq = orc.f2h(queries, f2h_factor) if vec_dtype == 1 else queries
+    oids, odist, octr = O.search(oq, lo, hi, gc, gcnt, glit, ent, L, K=10, rl=10, postfilter=postfilter)
+    b.close()
+    dev.close()
+    return ids, dists, ctr, oids, odist, octr, st
+
+
+def _assert_same(ids, dists, ctr, oids, odist, octr):
+    bad = np.nonzero(np.any(ids != oids, axis=1))[0]
+    assert bad.size == 0, f"{bad.size} queries differ, first q={bad[:5]}: gpu={ids[bad[0]]} oracle={oids[bad[0]]}"
+    assert np.array_equal(dists.view(np.uint32), odist.view(np.uint32))
+    cbad = np.nonzero(np.any(ctr != octr, axis=1))[0]
+    assert cbad.size == 0, f"counters differ for q={cbad[:5]}: gpu={ctr[cbad[0]]} oracle={octr[cbad[0]]}"
+
+
+@pytest.mark.parametrize("L", [10, 32, 64, 100, 256])
+def test_traversal_parity_r16(small_world, L):
+    cfg, ix = small_world
+    _print_case("traverse-r16", L=L)
+    _assert_same(*_traversal_case(cfg, ix, L)[:6])
+
+
+@pytest.mark.parametrize("L", [16, 80, 200])
+def test_traversal_parity_r32_mixed(world32, L):
+    cfg, ix = world32
+    _print_case("traverse-r32", L=L)
+    _assert_same(*_traversal_case(cfg, ix, L)[:6])
+
+
+def test_traversal_parity_fp16(world32):
+    cfg, ix = world32
+    _print_case("traverse-fp16")
+    _assert_same(*_traversal_case(cfg, ix, 64, vec_dtype=1, f2h_factor=0.01)[:6])
+
+
+@pytest.mark.parametrize("prefilter", [0.05, 1.0])
+def test_bruteforce_parity(world32, prefilter):
+    cfg, ix = world32
+    _print_case("bruteforce", prefilter=prefilter)
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 64, prefilter=prefilter)
+    _assert_same(ids, dists, ctr, oids, odist, octr)
+    assert st.q_bruteforce > 0
+
+
+def test_postfilter_routes_to_empty(small_world):
+    cfg, ix = small_world
+    _print_case("postfilter")
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 32, postfilter=12)
+    _assert_same(ids, dists, ctr, oids, odist, octr)
+    assert st.q_empty > 0
+
+
+def test_recall_against_ground_truth(world32):
+    from oracle import oracle as orc
+    cfg, ix = world32
+    _print_case("recall")
+    ids, dists, *_ = _traversal_case(cfg, ix, 200)
+    lo = cfg["lo"].astype(np.float32)
+    hi = cfg["hi"].astype(np.float32)
+    gt, gtd = orc.ground_truth(ix["vectors"], ix["attrs"], cfg["queries"], lo, hi, 10)
+    assert orc.recall(ids, gt, gtd) > 0.8
+    # every returned id passes the filter and its distance is the exact one
+    for q in range(ids.shape[0]):
+        for j in range(10):
+            i = ids[q, j]
+            if i == 0x7FFFFFFF:
+                continue
+            a = ix["attrs"][i]
+            assert np.all(a >= cfg["lo"][q]) and np.all(a <= cfg["hi"][q])
+            d = np.sum((cfg["queries"][q].astype(np.float64) - ix["vectors"][i]) ** 2)
+            assert abs(d - dists[q, j]) <= 1e-5 * max(d, 1.0)

@@ -1,0 +1,258 @@
+"""Pins the CPU oracle against library routines, closed forms and brute force.
+
+Each check is chosen so that a plausible mistake in the restatement (a wrong
+rounding, an off-by-one cell bound, a swapped index, a dropped tie rule)
+fails: numpy's IEEE binary16 conversion for f2h, numpy's MT19937 plus the
+published nearly-divisionless bounded draw and glibc's additive-feedback
+rand() for the entry points, exhaustive box intersection for the cells, and
+exact filtered brute force for the search results.
+"""
+import numpy as np
+import pytest
+
+from garfield_amd import synth
+from oracle import oracle as orc
+
+
+def test_f2h_matches_numpy_binary16():
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2 ** 32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[~np.isnan(x)]
+    edge = np.array([0.0, -0.0, 65504.0, 65519.996, 65520.0, 2.0 ** -24, 2.0 ** -25, 1.5 * 2.0 ** -25,
+                     2.0 ** -14, 2.0 ** -14 - 2.0 ** -25, 1e30, -1e30, np.inf, -np.inf], np.float32)
+    x = np.concatenate([x, edge])
+    for alpha in (1.0, 0.01, 3.0):
+        with np.errstate(over="ignore"):
+            ref = (x * np.float32(alpha)).astype(np.float16).view(np.uint16)
+        assert np.array_equal(orc.f2h(x, alpha), ref)
+
+
+def test_h2f_all_halves():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = h.view(np.float16).astype(np.float32)
+    lib = orc.load()
+    got = np.array([lib.orc_h2f(int(v)) for v in h[::7]], np.float32)
+    r = ref[::7]
+    ok = (got == r) | (np.isnan(got) & np.isnan(r))
+    assert ok.all()
+
+
+def test_norms_close_to_fp64():
+    rng = np.random.default_rng(1)
+    x = orc.f2h(rng.standard_normal((64, 768)).astype(np.float32))
+    ref = np.sum(x.view(np.float16).astype(np.float64) ** 2, axis=1)
+    got = orc.row_norms_f16(x)
+    assert np.all(np.abs(got - ref) <= 768 * 2.0 ** -23 * ref)
+    xi = orc.f2h(rng.integers(0, 256, (16, 128)).astype(np.float32))
+    assert np.array_equal(orc.row_norms_f16(xi), np.sum(xi.view(np.float16).astype(np.float64) ** 2, 1))
+
+
+def test_idx_mapper_invariants():
+    rng = np.random.default_rng(2)
+    pid = rng.integers(0, 9, 5000).astype(np.uint32)
+    gi, li, off = orc.idx_mapper(pid, 9)
+    assert np.array_equal(np.diff(off), np.bincount(pid, minlength=9))
+    assert np.array_equal(np.sort(gi), np.arange(5000))
+    for c in range(9):
+        seg = gi[off[c]:off[c + 1]]
+        assert np.all(np.diff(seg) > 0) and np.all(pid[seg] == c)
+        assert np.array_equal(li[seg], np.arange(len(seg)))
+
+
+def _cells_bruteforce(lo, hi, grid, l_q, r_q):
+    a = len(grid)
+    offs = np.concatenate([[0], np.cumsum(grid)[:-1]])
+    out = []
+    for q in range(lo.shape[0]):
+        ranges = []
+        for d in range(a):
+            lq = l_q[offs[d]:offs[d] + grid[d]]
+            rq = r_q[offs[d]:offs[d] + grid[d]]
+            ranges.append([c for c in range(grid[d]) if rq[c] >= lo[q, d] and lq[c] <= hi[q, d]])
+        sel = []
+        for idx in np.ndindex(*grid):
+            if all(idx[d] in ranges[d] for d in range(a)):
+                pid = 0
+                for d in range(a):
+                    pid = pid * grid[d] + idx[d]
+                sel.append(pid)
+        out.append(sorted(sel))
+    return out
+
+
+def test_cells_match_box_intersection():
+    rng = np.random.default_rng(3)
+    att = synth.uniform_attrs(4000, 3, 4, hi=200)
+    grid = np.array([3, 4, 2])
+    l_q, r_q, _, gpid = synth.grid_scatter(att, grid)
+    l_q = np.concatenate(l_q).astype(np.float32)
+    r_q = np.concatenate(r_q).astype(np.float32)
+    lo, hi = synth.ranges_for_selectivity(300, 3, rng.uniform(0.001, 0.8, 300), 5, hi=200)
+    cells, cnt = orc.cells(lo, hi, grid, l_q, r_q)
+    ref = _cells_bruteforce(lo, hi, grid, l_q, r_q)
+    for q in range(300):
+        assert list(cells[q, :cnt[q]]) == ref[q]
+    # every point passing a range lies in a selected cell
+    for q in range(0, 300, 7):
+        ok = np.all((att >= lo[q]) & (att <= hi[q]), axis=1)
+        assert set(gpid[ok].tolist()) <= set(cells[q, :cnt[q]].tolist())
+
+
+def test_cells_out_of_domain_select_nothing():
+    att = synth.uniform_attrs(1000, 2, 6, hi=100)
+    l_q, r_q, _, _ = synth.grid_scatter(att, [4, 4])
+    lo = np.array([[150, 0], [0, -50], [10, 10]], np.float32)
+    hi = np.array([[160, 99], [99, -10], [20, 20]], np.float32)
+    cells, cnt = orc.cells(lo, hi, np.array([4, 4]), np.concatenate(l_q).astype(np.float32),
+                           np.concatenate(r_q).astype(np.float32))
+    assert cnt[0] == 0 and cnt[1] == 0 and cnt[2] >= 1
+
+
+def test_selectivity_counts_and_threshold():
+    rng = np.random.default_rng(7)
+    att = rng.integers(0, 1000, (20000, 2)).astype(np.float32)
+    lo, hi = synth.ranges_for_selectivity(50, 2, rng.uniform(0.001, 0.5, 50), 8, hi=1000)
+    counts = np.arange(50, dtype=np.uint32) % 16 + 1
+    sel, little = orc.selectivity(att, lo, hi, 0.05, counts)
+    ref = np.array([np.count_nonzero(np.all((att >= lo[q]) & (att <= hi[q]), 1)) for q in range(50)])
+    assert np.array_equal(sel, ref)
+    prop = (ref / 20000.0).astype(np.float32)
+    assert np.array_equal(little, np.where(prop <= np.float32(0.05), counts, 0))
+
+
+def test_topk_clusters_and_cell_sort():
+    rng = np.random.default_rng(9)
+    d = rng.integers(0, 50, (40, 30)).astype(np.float32)  # many ties
+    d[0, 5] = np.nan
+    top = orc.topk_clusters(d, 4)
+    for q in range(40):
+        key = np.where(np.isnan(d[q]), np.inf, d[q])
+        ref = np.lexsort((np.arange(30), key))[:4]
+        assert np.array_equal(top[q], ref)
+    hist = rng.integers(0, 5, (16, 30)).astype(np.uint32)
+    cells = np.tile(np.arange(16, dtype=np.uint32), (40, 1))
+    counts = rng.integers(1, 17, 40).astype(np.uint32)
+    out = orc.sort_cells(cells, counts, top, hist)
+    for q in range(40):
+        cl = list(range(counts[q]))
+        sc = {c: int(hist[c, top[q]].sum()) for c in cl}
+        assert list(out[q, :counts[q]]) == sorted(cl, key=lambda c: (-sc[c], c))
+
+
+def _glibc_rand_seed1():
+    """glibc random() TYPE_3 (additive feedback, deg 31, sep 3) seeded with 1."""
+    r = [0] * 34
+    r[0] = 1
+    for i in range(1, 31):
+        hi_, lo_ = divmod(r[i - 1], 127773)
+        word = 16807 * lo_ - 2836 * hi_
+        if word < 0:
+            word += 2147483647
+        r[i] = word
+    for i in range(31, 34):
+        r[i] = r[i - 31]
+    i = 34
+    while True:
+        r.append((r[i - 31] + r[i - 3]) & 0xFFFFFFFF)
+        if i >= 344:
+            yield r[i] >> 1
+        i += 1
+
+
+def test_entry_points_restate_libstdcxx_draws():
+    N, P, R = 1_000_000, 16, 32
+    avg = (N + P - 1) // P
+    rand_max = N - (P - 1) * avg
+    assert rand_max == 62500
+    # std::mt19937 default seed 5489 == numpy's MT19937 init_genrand(5489)
+    mt = np.random.RandomState(5489)
+    want, seen, vals = R * 10, set(), []
+    urange = rand_max          # uniform_int_distribution<>(0, rand_max - 1)
+    while len(vals) < want:
+        # bounded draw by 64-bit multiply (Lemire 2019), as libstdc++ does
+        # for a 32-bit engine and a range below 2^32
+        prod = int(mt.randint(0, 2 ** 32, dtype=np.uint64)) * urange
+        low = prod & 0xFFFFFFFF
+        if low < urange:
+            thr = (-urange) % urange
+            while low < thr:
+                prod = int(mt.randint(0, 2 ** 32, dtype=np.uint64)) * urange
+                low = prod & 0xFFFFFFFF
+        t = prod >> 32
+        if t not in seen:
+            seen.add(t)
+            vals.append(t)
+    rnd = _glibc_rand_seed1()
+    for i in range(1, want):       # std::random_shuffle
+        j = next(rnd) % (i + 1)
+        vals[i], vals[j] = vals[j], vals[i]
+    assert list(orc.entry_points(N, P, R)) == vals[:R]
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    cfg = synth.config_small(N=4000, Q=120, R=16, C=12, sel=0.25, seed=31)
+    ix = synth.build_index(cfg["vectors"], cfg["attrs"], cfg["grid"], 16, 2, 12, seed=2)
+    l_q, r_q = synth.quantile_arrays(ix)
+    lo = cfg["lo"].astype(np.float32)
+    hi = cfg["hi"].astype(np.float32)
+    cells, cnt = orc.cells(lo, hi, ix["grid"], l_q, r_q)
+    O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], 16, ix["cell_graphs"], ix["cross"])
+    gt, gtd = orc.ground_truth(ix["vectors"], ix["attrs"], cfg["queries"], lo, hi, 10)
+    return cfg, ix, lo, hi, cells, cnt, O, gt, gtd
+
+
+def test_bruteforce_route_is_exact_topk(tiny):
+    cfg, ix, lo, hi, cells, cnt, O, gt, gtd = tiny
+    ent = orc.entry_points(4000, 16, 16)
+    little = cnt.copy()
+    ids, dist, ctr = O.search(cfg["queries"], lo, hi, cells, cnt, little, ent, 32)
+    assert orc.recall(ids, gt, gtd) == 1.0
+    assert np.all(ctr[:, 7] == 2)
+    # distances are the exact squared distances (integer data: fp32 is exact)
+    for q in range(0, 120, 11):
+        for j in range(10):
+            if ids[q, j] != orc.SENTINEL:
+                ref = np.sum((cfg["queries"][q].astype(np.float64) - ix["vectors"][ids[q, j]]) ** 2)
+                assert dist[q, j] == ref == gtd[q, j]
+
+
+def test_traversal_invariants_and_recall(tiny):
+    cfg, ix, lo, hi, cells, cnt, O, gt, gtd = tiny
+    ent = orc.entry_points(4000, 16, 16)
+    little = np.zeros_like(cnt)
+    recs = []
+    for L in (10, 40, 160):
+        ids, dist, ctr = O.search(cfg["queries"], lo, hi, cells, cnt, little, ent, L)
+        recs.append(orc.recall(ids, gt, gtd))
+        for q in range(120):
+            row = ids[q][ids[q] != orc.SENTINEL]
+            assert len(set(row.tolist())) == len(row)                     # unique
+            assert np.all(np.diff(dist[q][:len(row)]) >= 0)                # ascending
+            if len(row):
+                a = ix["attrs"][row]
+                assert np.all((a >= lo[q]) & (a <= hi[q]))                 # filter
+            for j, i in enumerate(row):
+                assert dist[q, j] == np.sum((cfg["queries"][q].astype(np.float64) - ix["vectors"][i]) ** 2)
+        assert np.all(ctr[:, 0] > 0)
+    assert recs[0] < recs[1] < recs[2] and recs[2] > 0.85
+
+
+def test_traversal_deterministic_across_threads(tiny):
+    cfg, ix, lo, hi, cells, cnt, O, gt, gtd = tiny
+    ent = orc.entry_points(4000, 16, 16)
+    z = np.zeros_like(cnt)
+    a = O.search(cfg["queries"], lo, hi, cells, cnt, z, ent, 64, nthreads=1)
+    b = O.search(cfg["queries"], lo, hi, cells, cnt, z, ent, 64, nthreads=8)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+
+
+def test_postfilter_and_empty_routes(tiny):
+    cfg, ix, lo, hi, cells, cnt, O, gt, gtd = tiny
+    ent = orc.entry_points(4000, 16, 16)
+    z = np.zeros_like(cnt)
+    ids, dist, ctr = O.search(cfg["queries"], lo, hi, cells, cnt, z, ent, 32, postfilter=int(cnt.min()))
+    routed = cnt >= cnt.min()
+    assert np.all(ids[routed] == orc.SENTINEL) and np.all(ctr[routed, 7] == 0)
