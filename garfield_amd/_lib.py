@@ -5,7 +5,7 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-lib_path = os.path.join(_HERE, "libgarfield.so")
+lib_path = os.environ.get("GARFIELD_LIB") or os.path.join(_HERE, "libgarfield.so")
 
 NO_RESULT = 0x7FFFFFFF
 NCOUNTERS = 8

@@ -38,6 +38,14 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
 }
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
+// Lanes of one wave exchange data through LDS between the phases below.
+// Program order alone does not order one lane's LDS store before another
+// lane's load: the compiler assumes no cross-thread communication without
+// synchronisation and may move accesses.  Every hand-off therefore goes
+// through a workgroup barrier, which for these one-wave workgroups costs a
+// wait on outstanding LDS operations.
+__device__ __forceinline__ void wave_sync() { __syncthreads(); }
+
 // ---------------------------------------------------------------- visited set
 // Open addressing with linear probing in LDS; set semantics identical to the
 // reference's 2048-slot table (gpu_graph.cu:677-711) as long as the table does
@@ -58,6 +66,7 @@ __device__ __forceinline__ void hash_clear(uint32_t* H, uint32_t hsize) {
     uint4* h4 = reinterpret_cast<uint4*>(H);
     const uint4 e = make_uint4(kEmpty, kEmpty, kEmpty, kEmpty);
     for (uint32_t i = lane_id(); i < hsize / 4u; i += 64u) h4[i] = e;
+    wave_sync();
 }
 
 // ----------------------------------------------------------- row distances
@@ -172,10 +181,13 @@ __device__ __forceinline__ uint32_t eval_lanes(const QReg<F16, CPL>& q, const Tr
                                                uint32_t row, bool need, float& dist) {
     const uint64_t m = ballot(need);
     const uint32_t ci = need ? lanes_below(m) : 0xFFFFFFFFu;
+    wave_sync();
     if (need) S[ci] = row;
+    wave_sync();
     const uint32_t n = __popcll(m);
     dist = __int_as_float(0x7F800000);
     if (n) eval_rows<F16, LPR, CPL>(q, p.vec, p.rowbytes, p.nch, S, n, ci, dist);
+    wave_sync();
     return n;
 }
 
@@ -192,6 +204,7 @@ __device__ uint32_t merge_into(uint64_t* A, uint32_t L, uint64_t b, uint32_t nb,
     const bool mine = lane < nb;
     const uint64_t kb = ckey(b);
     uint32_t r = L;
+    wave_sync();
     if (mine) {
         if (kb <= ckey(A[L - 1])) {
             uint32_t lo = 0, hi = L - 1;
@@ -203,6 +216,7 @@ __device__ uint32_t merge_into(uint64_t* A, uint32_t L, uint64_t b, uint32_t nb,
         }
     }
     if (Bp && mine) Bp[lane] = kCandSent;
+    wave_sync();
     const uint64_t ins = ballot(mine && r < L);
     if (ins == 0) return L;
     uint32_t rb = 0, rmin = L;
@@ -224,13 +238,16 @@ __device__ uint32_t merge_into(uint64_t* A, uint32_t L, uint64_t b, uint32_t nb,
             for (uint64_t m = ins; m; m &= m - 1) s += (readlane32(r, __builtin_ctzll(m)) <= i);
             np = i + s;
         }
+        wave_sync();
         if (i < L) {
             if (np < L) A[np] = av;
             else if (Bp) Bp[np - L] = (cvalid(av) && cpass(av)) ? av : kCandSent;
         }
+        wave_sync();
     }
     const uint32_t pos = rb + r;
     if (mine && r < L && pos < L) A[pos] = b;
+    wave_sync();
     return rmin;
 }
 
@@ -241,9 +258,11 @@ __device__ uint32_t merge_into(uint64_t* A, uint32_t L, uint64_t b, uint32_t nb,
 __device__ void recycle_update(uint64_t& rc, uint32_t rl, const uint64_t* Bp, uint32_t nb,
                                uint64_t& bleft, uint64_t* T) {
     const uint32_t lane = lane_id();
+    wave_sync();
     const uint64_t e = lane < nb ? Bp[lane] : kCandSent;
     const uint64_t ev = ballot(lane < nb && cvalid(e));
     if (ev == 0) { bleft = e; return; }
+    wave_sync();
     const uint64_t ke = ckey(e), kr = ckey(rc);
     const bool is_e = (ev >> lane) & 1u;
     const bool is_r = lane < rl;
@@ -258,9 +277,11 @@ __device__ void recycle_update(uint64_t& rc, uint32_t rl, const uint64_t* Bp, ui
     // T[0..rl) new recycle, T[64..) leftovers
     if (is_e) T[re < rl ? re : 64u + re - rl] = e;
     if (is_r) T[rr < rl ? rr : 64u + rr - rl] = rc;
+    wave_sync();
     const uint32_t nleft = __popcll(ev);
     rc = lane < rl ? T[lane] : kCandSent;
     bleft = lane < nleft ? T[64u + lane] : kCandSent;
+    wave_sync();
 }
 
 __device__ __forceinline__ uint32_t first_unexplored(const uint64_t* A, uint32_t L, uint32_t start) {
@@ -289,6 +310,7 @@ __device__ void hash_add_list(const TravArgs& p, uint32_t* H, const uint64_t* A,
         const uint64_t c = A[i];
         if (cvalid(c)) hash_insert(H, p.hbits, local_key(p, crow(c), off, offn, nlrow));
     }
+    wave_sync();
 }
 
 // In-LDS bitonic sort of 128 candidates (ascending key).
@@ -300,7 +322,9 @@ __device__ void sort128(uint64_t* W) {
             const uint32_t par = idx + j;
             const uint64_t x = W[idx], y = W[par];
             const bool asc = (idx & k) == 0;
+            wave_sync();
             if ((ckey(x) > ckey(y)) == asc) { W[idx] = y; W[par] = x; }
+            wave_sync();
         }
     }
 }
@@ -330,7 +354,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
         hi[d] = d < p.a ? p.hi[size_t(q) * p.a + d] : 0.0f;
     }
     for (uint32_t i = lane; i < L; i += 64u) A[i] = kCandSent;
-    hash_clear(H, hsize);
+    hash_clear(H, hsize);   // ends with a wave_sync
     uint32_t n_expand = 0, n_dist = 0, n_attr = 0, n_cross = 0, n_lrow = 0;
     uint64_t rc = kCandSent, bleft = kCandSent;
 
@@ -351,6 +375,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
             hash_insert(H, p.hbits, p.gidx[row]);
             pass = row_pass(p.attrs, p.a, row, lo, hi);
         }
+        wave_sync();
         float d;
         n_dist += eval_lanes<F16, LPR, CPL>(qv, p, S, row, mine, d);
         n_attr += R;
@@ -369,11 +394,14 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
                 hash_add_list(p, H, A, L, off, offn, n_lrow);
                 if (lane < R && cvalid(bleft))
                     hash_insert(H, p.hbits, local_key(p, crow(bleft), off, offn, n_lrow));
+                wave_sync();
             }
             const uint32_t sel = first_unexplored(A, L, scan);
             if (sel == L) break;
             const uint64_t sc = A[sel];
+            wave_sync();
             if (lane == 0) A[sel] = sc | 2u;
+            wave_sync();
             ++n_expand;
             scan = sel + 1;
             const uint32_t srow = crow(sc);
@@ -397,6 +425,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
         }
         // End of cell (gpu_graph.cu:3555-3560).
         for (uint32_t i = lane; i < L; i += 64u) A[i] = A[i] | 2u;
+        wave_sync();
         hash_clear(H, hsize);
         if (pi + 1 < cnt) {                             // gpu_graph.cu:3564-3642
             const uint32_t nxt = cl[pi + 1];
@@ -448,8 +477,10 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
                 if (v0) w0 = make_cand(d0, r0, p0);
                 if (v1) w1 = make_cand(d1, r1, p1);
             }
+            wave_sync();
             W[lane] = w0;
             W[64u + lane] = w1;
+            wave_sync();
             sort128(W);
             hash_clear(H, hsize);
             b = lane < R ? W[lane] : kCandSent;
@@ -458,6 +489,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
                 const uint64_t c = W[h * 64u + lane];
                 if (cvalid(c)) hash_insert(H, p.hbits, crow(c) - offx);
             }
+            wave_sync();
             merge_into(A, L, y, 64u, nullptr);
             hash_add_list(p, H, A, L, offx, offxn, n_lrow);
         }
@@ -470,13 +502,17 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
         uint32_t wpos = 0;
         for (uint32_t base = 0; base < L; base += 64u) {
             const uint32_t i = base + lane;
+            wave_sync();
             const uint64_t c = i < L ? A[i] : kCandSent;
             const bool keep = i < L && cvalid(c) && cpass(c);
             const uint64_t m = ballot(keep);
+            wave_sync();
             if (keep) A[wpos + lanes_below(m)] = c;
             wpos += __popcll(m);
         }
+        wave_sync();
         for (uint32_t i = wpos + lane; i < L; i += 64u) A[i] = kCandSent;
+        wave_sync();
     }
     if (cvalid(readlane64(rc, 0))) merge_into(A, L, rc, p.rl, nullptr);
 
@@ -500,6 +536,8 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
         p.out_ids[size_t(q) * p.K + j] = GF_NO_RESULT;
         p.out_dist[size_t(q) * p.K + j] = __int_as_float(0x7F800000);
     }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) n_lrow += __shfl_xor(n_lrow, m, 64);  // per-lane count
     if (lane == 0) {
         uint32_t* ctr = p.counters + size_t(q) * GF_NCOUNTERS;
         ctr[C_EXPAND] = n_expand;
@@ -559,8 +597,10 @@ __global__ __launch_bounds__(64) void k_bruteforce(TravArgs p) {
                 rt += kk < kt;
             }
             for (uint32_t t = 0; t < K; ++t) rs += readlane64(kt, t) < kc;
+            wave_sync();
             if (surv && rs < K) T[rs] = c;
             if (lane < K && rt < K) T[rt] = top;
+            wave_sync();
             top = lane < K ? T[lane] : kCandSent;
         }
     };
@@ -582,12 +622,15 @@ __global__ __launch_bounds__(64) void k_bruteforce(TravArgs p) {
                 if (ps[u]) S[ns + lanes_below(m)] = base + u * 64u + lane;
                 ns += __popcll(m);
             }
+            wave_sync();
             if (ns >= 64u) {
                 const uint32_t full = ns & ~63u;
                 flush(full);
                 const uint32_t rest = ns - full;
                 const uint32_t tail = lane < rest ? S[full + lane] : 0u;
+                wave_sync();
                 if (lane < rest) S[lane] = tail;
+                wave_sync();
                 n_pass += full;
                 ns = rest;
             }
@@ -617,10 +660,20 @@ __global__ void k_fill_results(uint32_t* ids, float* dist, uint32_t n) {
 }
 
 // ---------------------------------------------------------------- prep
-// f2h (tools.cuh:308-320): binary16 round-to-nearest-even of x*alpha.
+// f2h (tools.cuh:308-320): binary16 round-to-nearest-even of the fp32
+// product x*alpha.  The empty asm pins the fp32 product in a register so the
+// compiler cannot fold multiply and conversion into one mixed-precision fma,
+// which would round once (not twice, as the reference does) and turn
+// -0 * a + 0 into +0.
+__device__ __forceinline__ uint16_t f2h_scaled(float x, float alpha) {
+    float v = x * alpha;
+    asm volatile("" : "+v"(v));
+    return __half_as_ushort(__float2half_rn(v));
+}
+
 __global__ void k_f2h(const float* x, uint16_t* out, size_t n, float alpha) {
     for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
-        out[i] = __half_as_ushort(__float2half_rn(x[i] * alpha));
+        out[i] = f2h_scaled(x[i], alpha);
 }
 
 __global__ void k_f2h_pad(const float* x, uint32_t rows, uint32_t D, uint16_t* out, uint32_t rows_pad,
@@ -628,8 +681,7 @@ __global__ void k_f2h_pad(const float* x, uint32_t rows, uint32_t D, uint16_t* o
     const size_t n = size_t(rows_pad) * Dp;
     for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
         const uint32_t r = uint32_t(i / Dp), c = uint32_t(i % Dp);
-        float v = (r < rows && c < D) ? x[size_t(r) * D + c] * alpha : 0.0f;
-        out[i] = __half_as_ushort(__float2half_rn(v));
+        out[i] = (r < rows && c < D) ? f2h_scaled(x[size_t(r) * D + c], alpha) : uint16_t(0);
     }
 }
 

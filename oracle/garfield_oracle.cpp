@@ -308,6 +308,7 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
                 uint32_t gid = ix->global_idx[b + l];
                 if (!passes(s, gid)) continue;
                 s.ctr[ORC_C_PASS]++;
+                s.ctr[ORC_C_DIST]++;
                 found.push_back({point_dist(s, gid), gid});
             }
         }

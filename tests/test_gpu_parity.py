@@ -6,6 +6,8 @@ centroid distances, whose accumulation order is the hardware's, are checked
 against an fp64 reference within a stated tolerance, and every stage after
 them is checked exactly on the GPU's own distances.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -45,7 +47,10 @@ def test_f2h_bit_exact():
     for alpha in (1.0, 0.01, 3.0):
         g = gf.f2h(x, alpha)
         o = orc.f2h(x, alpha)
-        assert np.array_equal(g, o), f"alpha={alpha}: {np.count_nonzero(g != o)} mismatches"
+        bad = np.nonzero(g != o)[0]
+        assert bad.size == 0, (f"alpha={alpha}: {bad.size} mismatches, first x={x[bad[:4]].tolist()} "
+                               f"bits={x[bad[:4]].view(np.uint32).tolist()} gpu={g[bad[:4]].tolist()} "
+                               f"oracle={o[bad[:4]].tolist()}")
 
 
 def test_row_norms_f16_bit_exact():
@@ -129,6 +134,12 @@ def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, post
     oids, odist, octr = O.search(oq, lo, hi, gc, gcnt, glit, ent, L, K=10, rl=10, postfilter=postfilter)
     b.close()
     dev.close()
+    dump = os.environ.get("GF_DUMP_DIR")
+    if dump and (not np.array_equal(ids, oids) or not np.array_equal(ctr, octr)):
+        os.makedirs(dump, exist_ok=True)
+        np.savez_compressed(os.path.join(dump, f"parity_L{L}_pf{prefilter}_v{vec_dtype}_Q{len(queries)}.npz"),
+                            cells=gc, counts=gcnt, little=glit, ent=ent, ids=ids, ctr=ctr, oids=oids, octr=octr,
+                            L=L, postfilter=postfilter)
     return ids, dists, ctr, oids, odist, octr, st
 
 
