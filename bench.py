@@ -1,0 +1,228 @@
+#!/usr/bin/env python
+"""Headline benchmark: QPS at recall@10 >= 0.95 on BASELINE config 2.
+
+Workload (synthetic, generated here): 1M x 128 fp32 integer vectors in
+[0,255], 2 uint32 attributes uniform in [0,10000) on a 4x4 rank-quantile grid,
+per-cell exact kNN graphs of degree 32 plus 2 exact cross edges per (point,
+cell), 1000 k-means centres, 10k queries with range selectivity log-uniform in
+[1%, 50%], k = 10.  The index and the exact filtered ground truth are built on
+the GPU with torch before any timing (index construction is not the product).
+
+A "step" is one pass of the hot path over the 10k-query batch with inputs
+resident in HBM: stage A (cells + prefilter routing), stage B (cluster-guided
+cell order) and stage C (traversal / brute force, results copied to the host).
+The (L, prefilter) operating point is the one with the highest QPS among the
+reference's L sweep (realdataset_search.cu:2757) whose tie-aware recall@10
+reaches the target.  Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "QPS at recall@10≥0.95, 1M×128 fp32, 2-attr range filter, 1 MI355X"
+L_SWEEP = [10, 15, 20, 25, 30, 35, 40, 45, 50, 55, 60, 70, 80, 90, 100, 120, 140, 160, 180, 200, 250,
+           300, 400, 500, 600, 700, 800, 900, 1000, 1100, 1400, 1700]
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", choices=["headline", "small"], default="headline")
+    ap.add_argument("--recall", type=float, default=0.95)
+    ap.add_argument("--prefilters", default="1.0,0.05,0.0")
+    ap.add_argument("--postfilter", type=int, default=1 << 30)
+    ap.add_argument("--L", type=int, default=0, help="fixed L (skip the sweep)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the query path shards over "
+              "queries with no exchange, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import garfield_amd as gf
+    from garfield_amd import synth
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+
+    t0 = time.time()
+    if args.config == "headline":
+        cfg = synth.config_headline()
+        workload = ("C2 headline: 1M x 128 fp32 (integers 0-255), 2 uint32 attrs on a 4x4 grid, "
+                    "R=32 exact per-cell kNN + E=2 cross edges, C=1000, 10k queries, selectivity log-U[1%,50%], k=10")
+    else:
+        cfg = synth.config_small()
+        workload = "C1: 100k x 128 fp32 (integers 0-255), 2 attrs on 4x4, R=16, E=2, C=100, 1k queries at 30%, k=10"
+    N, D = cfg["vectors"].shape
+    Q = cfg["queries"].shape[0]
+    log(f"data generated N={N} D={D} Q={Q} ({time.time() - t0:.1f}s)")
+    t1 = time.time()
+    ix = synth.build_index(cfg["vectors"], cfg["attrs"], cfg["grid"], cfg["R"], cfg["E"], cfg["C"],
+                           device="cuda")
+    log(f"index built on GPU in {time.time() - t1:.1f}s")
+    lo = cfg["lo"].astype(np.float32)
+    hi = cfg["hi"].astype(np.float32)
+    t1 = time.time()
+    gt_ids, gt_dist = synth.ground_truth_torch(cfg["vectors"], cfg["attrs"], cfg["queries"], lo, hi, 10)
+    log(f"ground truth in {time.time() - t1:.1f}s")
+    torch.cuda.empty_cache()
+
+    t1 = time.time()
+    dev = synth.open_device_index(ix)
+    b = dev.batch(cfg["queries"], lo, hi)
+    log(f"library index resident ({dev.device_bytes / 2**30:.2f} GiB) in {time.time() - t1:.1f}s")
+
+    def step(prefilter, L):
+        ms_a = b.mark_cells(prefilter)
+        ms_b = b.order_cells(4)
+        ids, dists, st = b.search(L=L, K=10, rl=10, postfilter=args.postfilter)
+        return ids, dists, st, ms_a, ms_b
+
+    def recall(ids):
+        ex = synth.exact_result_dist(cfg["vectors"], cfg["queries"], ids)
+        return synth.recall_at_k(ids, ex, gt_ids, gt_dist)
+
+    # Calibration: for each prefilter, the smallest L of the sweep reaching the target.
+    points = []
+    for pf in [float(x) for x in args.prefilters.split(",")]:
+        sweep = [args.L] if args.L else L_SWEEP
+        for L in sweep:
+            t = time.perf_counter()
+            ids, dists, st, ms_a, ms_b = step(pf, L)
+            wall = time.perf_counter() - t
+            strict, tie = recall(ids)
+            gbs = st.bytes_traverse / max(st.ms_traverse, 1e-9) / 1e6
+            log(f"prefilter={pf} L={L}: recall={tie:.4f} (strict {strict:.4f}) step={wall * 1e3:.1f}ms "
+                f"trav_GBs={gbs:.0f} "
+                f"trav={st.ms_traverse:.1f}ms bf={st.ms_bruteforce:.1f}ms A={ms_a:.2f}ms B={ms_b:.2f}ms "
+                f"q_trav={st.q_traverse} q_bf={st.q_bruteforce}")
+            if tie >= args.recall or args.L:
+                points.append(dict(prefilter=pf, L=L, recall=tie, strict=strict, wall=wall))
+                break
+            if points and wall > 2 * min(p["wall"] for p in points):
+                break   # slower than a known operating point already
+    if not points:
+        raise SystemExit("no operating point reached the recall target")
+    best = min(points, key=lambda p: p["wall"])
+    pf, L = best["prefilter"], best["L"]
+    log(f"operating point: prefilter={pf} L={L} recall={best['recall']:.4f}")
+
+    for _ in range(args.warmup):
+        step(pf, L)
+    torch.cuda.synchronize()
+    ms_a_sum = ms_b_sum = ms_tr = ms_bf = bytes_tr = bytes_bf = 0.0
+    last = None
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        ids, dists, st, ms_a, ms_b = step(pf, L)
+        ms_a_sum += ms_a
+        ms_b_sum += ms_b
+        ms_tr += st.ms_traverse
+        ms_bf += st.ms_bruteforce
+        bytes_tr += st.bytes_traverse
+        bytes_bf += st.bytes_bruteforce
+        last = st
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t
+    K = args.steps
+    strict, tie = recall(ids)
+    qps = Q * K / elapsed
+    ms_per_step = elapsed * 1e3 / K
+    qps_ref = Q / ((ms_a_sum + ms_b_sum + ms_tr + ms_bf) / K / 1e3)
+    # Dominant kernel: the one with the larger device time in the timed steps.
+    if ms_tr >= ms_bf:
+        dom, dom_bytes, dom_ms = "k_traverse", bytes_tr, ms_tr
+    else:
+        dom, dom_bytes, dom_ms = "k_bruteforce", bytes_bf, ms_bf
+    achieved = (dom_bytes / K) / (dom_ms / K / 1e3) / 1e9 if dom_ms > 0 else 0.0
+    log(f"timed: {qps:.0f} QPS end-to-end, {qps_ref:.0f} QPS (reference definition), "
+        f"{dom} {dom_ms / K:.2f} ms at {achieved:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cfg, ix, b, L, pf, args)
+
+    out = {
+        "metric": METRIC,
+        "value": round(qps, 1),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (generated in bench.py; exact kNN index built on the GPU)",
+        "config": {
+            "workload": workload,
+            "N": N, "D": D, "Q": Q, "K": 10, "L": L,
+            "prefilter": pf, "postfilter": args.postfilter, "f2h_factor": 1.0, "degree": cfg["R"],
+            "recall_at_10": round(tie, 4), "recall_at_10_strict": round(strict, 4),
+            "qps_reference_definition": round(qps_ref, 1),
+            "ms_stage_a": round(ms_a_sum / K, 3), "ms_stage_b": round(ms_b_sum / K, 3),
+            "ms_traverse": round(ms_tr / K, 3), "ms_bruteforce": round(ms_bf / K, 3),
+            "q_traverse": last.q_traverse, "q_bruteforce": last.q_bruteforce, "q_empty": last.q_empty,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom,
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": round(dom_bytes / K),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(cfg, ix, batch, L, prefilter, args):
+    """The oracle's traversal / brute force (OpenMP over queries) on a sample of
+    the same batch, same routing, same L, on the host's cores."""
+    from oracle import oracle as orc
+    import garfield_amd as gf
+    cells, counts, little, _ = batch.get_cells()
+    O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"], ix["cross"])
+    ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], ix["R"])
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
+    lo = cfg["lo"].astype(np.float32)
+    hi = cfg["hi"].astype(np.float32)
+    Q = cfg["queries"].shape[0]
+    rng = np.random.default_rng(0)
+    order = rng.permutation(Q)
+    n = min(64, Q)
+    while True:
+        sel = np.sort(order[:n])
+        t = time.perf_counter()
+        O.search(cfg["queries"][sel], lo[sel], hi[sel], cells[sel], counts[sel], little[sel], ent, L,
+                 postfilter=args.postfilter, nthreads=threads)
+        dt = time.perf_counter() - t
+        if dt >= args.cpu_seconds or n >= Q:
+            break
+        n = min(Q, max(n * 2, int(n * args.cpu_seconds / max(dt, 1e-3) * 1.1)))
+    log(f"cpu baseline: {n} queries in {dt:.1f}s on {threads} threads")
+    return {"value": round(n / dt, 1), "unit": "queries/s", "cores": threads, "kind": "port",
+            "sample": f"{n} random queries of the same batch (same cells, routing, L={L}, "
+                      f"prefilter={prefilter}), traversal/brute force only (stages A/B not timed)"}
+
+
+if __name__ == "__main__":
+    main()

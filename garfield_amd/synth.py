@@ -239,3 +239,66 @@ def config_headline(N=1_000_000, Q=10_000, R=32, C=1000, seed=11):
     sel = log_uniform(Q, 0.01, 0.5, seed + 3)
     lo, hi = ranges_for_selectivity(Q, 2, sel, seed + 4)
     return dict(vectors=vec, attrs=att, grid=[4, 4], R=R, E=2, C=C, queries=qv, lo=lo, hi=hi, sel=sel)
+
+
+def ground_truth_torch(vectors, attrs, queries, lo, hi, K, device="cuda", chunk=256):
+    """Exact filtered kNN (naive_brute_force_with_filter, gpu_graph.cu:10782-10812)
+    in fp64 on `device`; returns ids (missing = 0x7FFFFFFF) and squared distances."""
+    torch = _torch()
+    x = torch.as_tensor(vectors, device=device, dtype=torch.float64)
+    xn = (x * x).sum(1)
+    at = torch.as_tensor(attrs, device=device)
+    Q = queries.shape[0]
+    ids = np.full((Q, K), 0x7FFFFFFF, np.uint32)
+    dist = np.full((Q, K), np.inf, np.float64)
+    for s in range(0, Q, chunk):
+        e = min(Q, s + chunk)
+        q = torch.as_tensor(queries[s:e], device=device, dtype=torch.float64)
+        d = (q * q).sum(1, keepdim=True) + xn[None, :] - 2.0 * (q @ x.T)
+        l = torch.as_tensor(lo[s:e], device=device)
+        h = torch.as_tensor(hi[s:e], device=device)
+        ok = torch.ones_like(d, dtype=torch.bool)
+        for j in range(at.shape[1]):
+            ok &= (at[None, :, j] >= l[:, None, j]) & (at[None, :, j] <= h[:, None, j])
+        d = torch.where(ok, d, torch.full_like(d, float("inf")))
+        v, i = torch.topk(d, K, dim=1, largest=False, sorted=True)
+        v = v.cpu().numpy()
+        i = i.cpu().numpy().astype(np.uint32)
+        i[~np.isfinite(v)] = 0x7FFFFFFF
+        ids[s:e] = i
+        dist[s:e] = v
+    return ids, dist
+
+
+def recall_at_k(res_ids, res_exact_dist, gt_ids, gt_dist):
+    """(strict, tie-aware) recall: strict is |res ∩ gt| / |gt| (tools.cuh:384-453,
+    1 when the filter passes nothing); tie-aware also counts a result whose exact
+    distance is <= the K-th ground-truth distance."""
+    Q, K = gt_ids.shape
+    strict = np.empty(Q)
+    tie = np.empty(Q)
+    for q in range(Q):
+        g = gt_ids[q][gt_ids[q] != 0x7FFFFFFF]
+        if g.size == 0:
+            strict[q] = tie[q] = 1.0
+            continue
+        r = res_ids[q]
+        valid = r != 0x7FFFFFFF
+        strict[q] = np.intersect1d(r[valid], g).size / g.size
+        kth = gt_dist[q][g.size - 1]
+        _, first = np.unique(r, return_index=True)
+        uniq = np.zeros(K, bool)
+        uniq[first] = True
+        tie[q] = min(np.count_nonzero(valid & uniq & (res_exact_dist[q] <= kth)), g.size) / g.size
+    return float(strict.mean()), float(tie.mean())
+
+
+def exact_result_dist(vectors, queries, ids, device="cuda"):
+    torch = _torch()
+    safe = np.where(ids == 0x7FFFFFFF, 0, ids).astype(np.int64)
+    x = torch.as_tensor(vectors, device=device, dtype=torch.float64)
+    q = torch.as_tensor(queries, device=device, dtype=torch.float64)
+    g = x[torch.as_tensor(safe, device=device)]
+    d = ((g - q[:, None, :]) ** 2).sum(-1).cpu().numpy()
+    d[ids == 0x7FFFFFFF] = np.inf
+    return d
