@@ -55,7 +55,8 @@ class SearchStats(C.Structure):
                 ("q_traverse", C.c_uint32), ("q_bruteforce", C.c_uint32), ("q_empty", C.c_uint32),
                 ("n_expand", C.c_uint64), ("n_dist", C.c_uint64), ("n_attr", C.c_uint64),
                 ("n_cross", C.c_uint64), ("n_lrow", C.c_uint64), ("n_scan", C.c_uint64),
-                ("n_pass", C.c_uint64), ("bytes_traverse", C.c_double), ("bytes_bruteforce", C.c_double)]
+                ("n_pass", C.c_uint64), ("bytes_traverse", C.c_double), ("bytes_bruteforce", C.c_double),
+                ("ops_bruteforce", C.c_double), ("bf_mfma", C.c_uint32)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}

@@ -94,13 +94,21 @@ struct gf_index {
     DevBuf<uint32_t> tile_cell, tile_row0, tile_n;
     DevBuf<uint16_t> centres;
     uint32_t ntiles = 0;
+    // Query-batch MFMA brute force (integer data in [0, 255], D a multiple of 64).
+    bool i8 = false;
+    DevBuf<int8_t> vt;
+    DevBuf<int32_t> nxt;
+    DevBuf<float> attrt;
+    DevBuf<uint32_t> tbase;
+    std::vector<uint32_t> tbase_h;
     ~gf_index() {
         if (stream) (void)hipStreamDestroy(stream);
     }
     uint64_t device_bytes() const {
         return vec.bytes() + attrs.bytes() + l_q.bytes() + r_q.bytes() + cnorm.bytes() + graph.bytes() +
                cross.bytes() + offset.bytes() + gidx.bytes() + lrow.bytes() + grid.bytes() + doff.bytes() +
-               hist.bytes() + tile_cell.bytes() + tile_row0.bytes() + tile_n.bytes() + centres.bytes();
+               hist.bytes() + tile_cell.bytes() + tile_row0.bytes() + tile_n.bytes() + centres.bytes() +
+               vt.bytes() + nxt.bytes() + attrt.bytes() + tbase.bytes();
     }
 };
 
@@ -108,6 +116,12 @@ struct gf_batch {
     gf_index* ix = nullptr;
     uint32_t Q = 0, Qp = 0, topc = 0;
     bool marked = false;
+    bool i8 = false;
+    DevBuf<int8_t> q8;
+    DevBuf<int32_t> nq;
+    DevBuf<uint32_t> pq, ppos, part_off, bfq;
+    DevBuf<gf::BfItem> items;
+    DevBuf<uint64_t> part;
     DevBuf<float> qf32, qnorm, lo, hi, cdist, out_dist;
     DevBuf<uint16_t> q16, q16v;
     DevBuf<uint32_t> cells, counts, little, selcount, cellq, ccount, cstart, cfill, topk;
@@ -191,10 +205,7 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
         size[h.global_pid[i]]++;
     }
     ix.offset_h.assign(P + 1, 0);
-    for (uint32_t c = 0; c < P; ++c) {
-        GF_REQUIRE(size[c] > 0, GF_E_UNSUPPORTED, "empty cell " + std::to_string(c));
-        ix.offset_h[c + 1] = ix.offset_h[c] + size[c];
-    }
+    for (uint32_t c = 0; c < P; ++c) ix.offset_h[c + 1] = ix.offset_h[c] + size[c];
     for (uint32_t i = 0; i < N; ++i) {
         const uint32_t c = h.global_pid[i];
         const uint32_t r = ix.offset_h[c] + fill[c];
@@ -213,7 +224,8 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
         for (uint32_t c = 0; c < P; ++c)
             for (uint32_t e = 0; e < E; ++e) {
                 const uint32_t v = src[c * E + e];
-                GF_REQUIRE(v < size[c], GF_E_FORMAT, "cross-cell graph holds an id beyond its cell");
+                // edges into an empty cell are never followed (no query selects it)
+                GF_REQUIRE(v < size[c] || size[c] == 0, GF_E_FORMAT, "cross-cell graph holds an id beyond its cell");
                 cross_cm[(size_t(r) * P + c) * E + e] = v;
             }
     }
@@ -236,17 +248,36 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
         std::vector<float> v(size_t(N) * D);
         for (uint32_t r = 0; r < N; ++r)
             std::memcpy(&v[size_t(r) * D], h.vectors + size_t(gidx[r]) * D, sizeof(float) * D);
+        DevBuf<float> tmp;
+        const float* vec_f32_dev = nullptr;
         if (ix.vdtype == GF_VEC_F32) {
             ix.vec.upload(reinterpret_cast<const char*>(v.data()), v.size() * sizeof(float));
             ix.rowbytes = D * 4;
+            vec_f32_dev = reinterpret_cast<const float*>(ix.vec.p);
         } else {
-            DevBuf<float> tmp;
             tmp.upload(v);
             ix.vec.alloc(v.size() * sizeof(uint16_t));
             GF_HIP(gf::launch_f2h(tmp.p, reinterpret_cast<uint16_t*>(ix.vec.p), v.size(), ix.alpha, ix.stream));
-            GF_HIP(hipStreamSynchronize(ix.stream));
             ix.rowbytes = D * 2;
+            vec_f32_dev = tmp.p;
         }
+        // Integer-valued data in [0, 255]: build the int8 tiles of the MFMA brute force.
+        bool ints = ix.vdtype == GF_VEC_F32 && D % 64 == 0 && D <= 256;
+        for (size_t i = 0; ints && i < v.size(); ++i) ints = v[i] >= 0.0f && v[i] <= 255.0f && v[i] == std::floor(v[i]);
+        if (ints) {
+            ix.tbase_h.assign(P + 1, 0);
+            for (uint32_t c = 0; c < P; ++c)
+                ix.tbase_h[c + 1] = ix.tbase_h[c] + (size[c] + gf::kBfTile - 1) / gf::kBfTile;
+            const uint32_t nt = ix.tbase_h[P];
+            ix.tbase.upload(ix.tbase_h);
+            ix.vt.alloc(size_t(nt) * (D / 64) * 1024);
+            ix.nxt.alloc(size_t(nt) * 16);
+            ix.attrt.alloc(size_t(nt) * 16 * a);
+            GF_HIP(gf::launch_tile_i8(vec_f32_dev, D, ix.offset.p, ix.tbase.p, ix.attrs.p, a, P, nt, ix.vt.p,
+                                      ix.nxt.p, ix.attrt.p, ix.stream));
+            ix.i8 = true;
+        }
+        GF_HIP(hipStreamSynchronize(ix.stream));
     }
     // Grid (real_dataset_adapter.cuh:563-619).
     uint32_t gsum = 0;
@@ -436,6 +467,18 @@ gf_status gf_batch_create(gf_index* ix, const float* queries, uint32_t Q, const 
             b->qnorm.alloc(b->Qp);
             GF_HIP(gf::launch_norms_f16(b->q16.p, b->Qp, ix->Dp, ix->Dp, b->qnorm.p, ix->stream));
         }
+        if (ix->i8) {
+            bool ints = true;
+            const size_t nq = size_t(Q) * ix->D;
+            for (size_t i = 0; ints && i < nq; ++i)
+                ints = queries[i] >= 0.0f && queries[i] <= 255.0f && queries[i] == std::floor(queries[i]);
+            if (ints) {
+                b->q8.alloc(nq);
+                b->nq.alloc(Q);
+                GF_HIP(gf::launch_q_i8(b->qf32.p, Q, ix->D, b->q8.p, b->nq.p, ix->stream));
+                b->i8 = true;
+            }
+        }
         b->cells.alloc(size_t(Q) * ix->P);
         b->counts.alloc(Q);
         b->little.alloc(Q);
@@ -465,7 +508,7 @@ gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms) {
         hipStream_t st = ix->stream;
         Timer t(st);
         GF_HIP(gf::launch_cells(b->Q, ix->a, b->lo.p, b->hi.p, ix->grid.p, ix->doff.p, ix->l_q.p, ix->r_q.p,
-                                ix->P, b->cells.p, b->counts.p, st));
+                                ix->P, ix->offset.p, b->cells.p, b->counts.p, st));
         GF_HIP(hipMemsetAsync(b->ccount.p, 0, ix->P * sizeof(uint32_t), st));
         GF_HIP(hipMemsetAsync(b->cfill.p, 0, ix->P * sizeof(uint32_t), st));
         GF_HIP(hipMemsetAsync(b->selcount.p, 0, b->Q * sizeof(uint32_t), st));
@@ -584,6 +627,66 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         a.hbits = hbits;
         a.Lpad = Lpad;
 
+        // Brute-force route on MFMA when vectors and queries are int8-exact:
+        // work items of (cell, 16 queries, chunk of the cell's tiles).
+        const bool gemm = ix->i8 && b->i8 && !bq.empty();
+        double bf_ops = 0.0, bf_bytes_gemm = 0.0;
+        gf::BfGemmArgs ga{};
+        gf::BfFinalArgs fa{};
+        if (gemm) {
+            const uint32_t P = ix->P;
+            std::vector<uint32_t> cellsh(size_t(Q) * P);
+            GF_HIP(hipMemcpy(cellsh.data(), b->cells.p, cellsh.size() * 4, hipMemcpyDeviceToHost));
+            uint32_t maxch = 0;
+            for (uint32_t c = 0; c < P; ++c)
+                maxch = std::max(maxch, (ix->tbase_h[c + 1] - ix->tbase_h[c] + gf::kBfChunk - 1) / gf::kBfChunk);
+            std::vector<std::vector<std::pair<uint32_t, uint32_t>>> lists(P);
+            std::vector<uint32_t> poff(Q, 0);
+            uint64_t tot = 0;
+            for (uint32_t q : bq) {
+                poff[q] = uint32_t(tot);
+                tot += uint64_t(cnt[q]) * maxch * K;
+                for (uint32_t i = 0; i < cnt[q]; ++i) lists[cellsh[size_t(q) * P + i]].push_back({q, i});
+            }
+            GF_REQUIRE(tot < (1ull << 32), GF_E_UNSUPPORTED, "brute-force batch too large");
+            std::vector<uint32_t> pq, ppos;
+            std::vector<gf::BfItem> items;
+            const uint32_t KS = ix->D / 64;
+            for (uint32_t c = 0; c < P; ++c) {
+                const uint32_t base = uint32_t(pq.size());
+                const uint32_t nlist = uint32_t(lists[c].size());
+                for (auto& pr : lists[c]) { pq.push_back(pr.first); ppos.push_back(pr.second); }
+                const uint32_t t0c = ix->tbase_h[c], t1c = ix->tbase_h[c + 1];
+                for (uint32_t ch = 0; t0c + ch * gf::kBfChunk < t1c; ++ch) {
+                    const uint32_t ts = t0c + ch * gf::kBfChunk, te = std::min(t1c, ts + gf::kBfChunk);
+                    for (uint32_t qb = 0; qb < nlist; qb += 16) {
+                        const uint32_t nq = std::min(16u, nlist - qb);
+                        items.push_back({c, base + qb, nq, ts, te, ch});
+                        bf_ops += 2.0 * double(te - ts) * 16.0 * nq * ix->D;
+                        bf_bytes_gemm += double(te - ts) * (KS * 1024.0 + 64.0);
+                    }
+                }
+            }
+            b->pq.upload(pq);
+            b->ppos.upload(ppos);
+            b->items.upload(items);
+            b->part_off.upload(poff);
+            b->bfq.upload(bq);
+            if (b->part.n < tot) b->part.alloc(tot);
+            GF_HIP(hipMemsetAsync(b->part.p, 0xFF, tot * sizeof(uint64_t), st));
+            ga.vt = ix->vt.p; ga.nxt = ix->nxt.p; ga.attrt = ix->attrt.p; ga.tbase = ix->tbase.p;
+            ga.offset = ix->offset.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p; ga.hi = b->hi.p;
+            ga.items = b->items.p; ga.nitems = uint32_t(items.size()); ga.pq = b->pq.p; ga.ppos = b->ppos.p;
+            ga.part_off = b->part_off.p; ga.part = b->part.p; ga.maxch = maxch; ga.K = K; ga.a = ix->a;
+            ga.D = ix->D;
+            fa.bfq = b->bfq.p; fa.nbf = uint32_t(bq.size()); fa.part_off = b->part_off.p; fa.part = b->part.p;
+            fa.counts = b->counts.p; fa.cells = b->cells.p; fa.offset = ix->offset.p;
+            fa.selcount = b->selcount.p; fa.gidx = ix->gidx.p; fa.out_ids = b->out_ids.p;
+            fa.out_dist = b->out_dist.p; fa.counters = b->counters.p; fa.maxch = maxch; fa.K = K; fa.P = P;
+            // final merge reads every partial list and writes the results
+            bf_bytes_gemm += double(tot) * 8.0 + double(bq.size()) * K * 8.0;
+        }
+
         GF_HIP(hipMemsetAsync(b->counters.p, 0, size_t(Q) * GF_NCOUNTERS * sizeof(uint32_t), st));
         GF_HIP(gf::launch_fill_results(b->out_ids.p, b->out_dist.p, Q * K, st));
         hipEvent_t ev[3];
@@ -597,7 +700,12 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         gf::TravArgs ab = a;
         ab.sched = b->sched.p + tq.size();
         ab.nsched = uint32_t(bq.size());
-        GF_HIP(gf::launch_bruteforce(ix->rs, ab, st));
+        if (gemm) {
+            GF_HIP(gf::launch_bf_i8(ga, st));
+            GF_HIP(gf::launch_bf_final(fa, st));
+        } else {
+            GF_HIP(gf::launch_bruteforce(ix->rs, ab, st));
+        }
         GF_HIP(hipEventRecord(ev[2], st));
         GF_HIP(hipEventSynchronize(ev[2]));
         float t_tr = 0, t_bf = 0;
@@ -639,8 +747,15 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             stats->bytes_traverse = double(t_dist) * ix->rowbytes + double(stats->n_expand) * R * 4.0 +
                                     double(stats->n_attr) * ix->a * 4.0 + double(stats->n_cross) * ix->E * 4.0 +
                                     double(stats->n_lrow) * 4.0 + double(tq.size()) * (K * 8.0 + ix->P * 4.0);
-            stats->bytes_bruteforce = double(stats->n_scan) * ix->a * 4.0 + double(b_dist) * ix->rowbytes +
-                                      double(bq.size()) * (K * 8.0 + ix->P * 4.0);
+            if (gemm) {
+                stats->bytes_bruteforce = bf_bytes_gemm;
+                stats->ops_bruteforce = bf_ops;
+            } else {
+                stats->bytes_bruteforce = double(stats->n_scan) * ix->a * 4.0 + double(b_dist) * ix->rowbytes +
+                                          double(bq.size()) * (K * 8.0 + ix->P * 4.0);
+                stats->ops_bruteforce = 3.0 * double(b_dist) * ix->D;
+            }
+            stats->bf_mfma = gemm ? 1u : 0u;
         }
     });
 }

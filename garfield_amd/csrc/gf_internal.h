@@ -65,10 +65,59 @@ struct TravArgs {
     uint32_t a, P, R, E, L, K, rl, hbits, Lpad;
 };
 
+// Query-batch brute force on int8 MFMA (integer-valued data in [0, 255]).
+// Vectors are stored shifted by -128 as int8, per cell in tiles of 16 points
+// laid out in MFMA operand order: tile t, k-step s holds 64 lanes x 16 bytes,
+// lane l carrying bytes [64 s + 16 (l / 16), +16) of point l % 16.
+constexpr uint32_t kBfTile = 16;      // points per tile
+constexpr uint32_t kBfChunk = 512;    // tiles per work item (8192 points)
+struct BfItem {
+    uint32_t cell, qbase, nq, t0, t1, chunk;
+};
+struct BfGemmArgs {
+    const int8_t* vt;          // tiled int8 vectors
+    const int32_t* nxt;        // |x - 128|^2 per tiled point
+    const float* attrt;        // attributes per tiled point
+    const uint32_t* tbase;     // P+1 first tile of each cell
+    const uint32_t* offset;    // P+1 first row of each cell
+    const int8_t* q8;          // Q*D queries shifted by -128
+    const int32_t* nq;         // |q - 128|^2
+    const float* lo;
+    const float* hi;
+    const BfItem* items;
+    uint32_t nitems;
+    const uint32_t* pq;        // query of each (query, cell) pair, grouped by cell
+    const uint32_t* ppos;      // position of the cell in that query's list
+    const uint32_t* part_off;  // per query: first partial slot entry
+    uint64_t* part;            // partial top-K keys: (d << 32) | row
+    uint32_t maxch, K, a, D;
+};
+struct BfFinalArgs {
+    const uint32_t* bfq;       // brute-force queries
+    uint32_t nbf;
+    const uint32_t* part_off;
+    const uint64_t* part;
+    const uint32_t* counts;
+    const uint32_t* cells;
+    const uint32_t* offset;
+    const uint32_t* selcount;
+    const uint32_t* gidx;
+    uint32_t* out_ids;
+    float* out_dist;
+    uint32_t* counters;
+    uint32_t maxch, K, P;
+};
+
 // Kernel launchers (gf_kernels.hip).  All are asynchronous on `st`.
 hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds_bytes, hipStream_t st);
 hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, hipStream_t st);
 hipError_t launch_fill_results(uint32_t* ids, float* dist, uint32_t n, hipStream_t st);
+hipError_t launch_bf_i8(const BfGemmArgs& a, hipStream_t st);
+hipError_t launch_bf_final(const BfFinalArgs& a, hipStream_t st);
+hipError_t launch_tile_i8(const float* vec_cm, uint32_t D, const uint32_t* offset, const uint32_t* tbase,
+                          const float* attrs_cm, uint32_t a, uint32_t P, uint32_t ntiles, int8_t* vt,
+                          int32_t* nxt, float* attrt, hipStream_t st);
+hipError_t launch_q_i8(const float* q, uint32_t Q, uint32_t D, int8_t* q8, int32_t* nq, hipStream_t st);
 hipError_t launch_f2h(const float* x, uint16_t* out, size_t n, float alpha, hipStream_t st);
 hipError_t launch_f2h_pad(const float* x, uint32_t rows, uint32_t D, uint16_t* out,
                           uint32_t rows_pad, uint32_t Dp, float alpha, hipStream_t st);
@@ -76,8 +125,8 @@ hipError_t launch_norms_f16(const uint16_t* x, uint32_t n, uint32_t D, uint32_t 
                             hipStream_t st);
 hipError_t launch_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi,
                         const uint32_t* grid, const uint32_t* doff, const float* l_q,
-                        const float* r_q, uint32_t P, uint32_t* cells, uint32_t* counts,
-                        hipStream_t st);
+                        const float* r_q, uint32_t P, const uint32_t* offset, uint32_t* cells,
+                        uint32_t* counts, hipStream_t st);
 hipError_t launch_cellq_count(uint32_t Q, uint32_t P, const uint32_t* cells,
                               const uint32_t* counts, uint32_t* ccount, hipStream_t st);
 hipError_t launch_scan_small(const uint32_t* in, uint32_t n, uint32_t* out_excl, hipStream_t st);

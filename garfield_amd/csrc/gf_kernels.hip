@@ -706,10 +706,11 @@ __global__ __launch_bounds__(64) void k_norms_f16(const uint16_t* x, uint32_t n,
 // (first c with l_q[c] > hi) - 1; the product is enumerated with the last
 // attribute fastest (gpu_graph.cu:10965-10973).  A range beyond every cell
 // (quirk Q16) selects nothing; an empty interval between two cells selects
-// the next cell, as the reference's do-while does.
+// the next cell, as the reference's do-while does.  Cells holding no point
+// are never selected (the reference would read past them).
 __global__ void k_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi, const uint32_t* grid,
                         const uint32_t* doff, const float* l_q, const float* r_q, uint32_t P,
-                        uint32_t* cells, uint32_t* counts) {
+                        const uint32_t* offset, uint32_t* cells, uint32_t* counts) {
     const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
     if (q >= Q) return;
     uint32_t cl[kMaxAttr], ch[kMaxAttr], idx[kMaxAttr], g[kMaxAttr];
@@ -735,7 +736,7 @@ __global__ void k_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi
         while (true) {
             uint32_t pid = 0, f = 1;
             for (int d = int(a) - 1; d >= 0; --d) { pid += idx[d] * f; f *= g[d]; }
-            cells[size_t(q) * P + n++] = pid;
+            if (offset[pid + 1] > offset[pid]) cells[size_t(q) * P + n++] = pid;
             int d = int(a) - 1;
             for (; d >= 0; --d) {
                 if (++idx[d] <= ch[d]) break;
@@ -919,6 +920,255 @@ __global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P
     }
 }
 
+// ------------------------------------------ query-batch brute force (MFMA)
+// Filtered brute force for queries routed to it when every vector and query
+// is an integer in [0, 255]: with q' = q - 128 and x' = x - 128 (int8),
+// |q - x|^2 = |q'|^2 + |x'|^2 - 2 q'.x' holds exactly in int32, so the
+// distances are bit-identical to the canonical fp32 ones (all sums < 2^24).
+// A wave takes 16 queries that select one cell and one chunk of that cell's
+// tiles; v_mfma_i32_16x16x64_i8 produces a 16 x 16 distance block per tile.
+// A per-query threshold (the current K-th distance) rejects almost every
+// pair; the range filter runs only on the few survivors, which are buffered
+// in LDS and merged into a per-query top-K keyed by (distance, row).
+typedef int v4i32_t __attribute__((ext_vector_type(4)));
+constexpr uint32_t kBfBuf = 64;      // survivors buffered per query
+constexpr uint32_t kBfMergeAt = 48;  // a tile adds at most 16 per query
+constexpr uint64_t kKeySent = ~uint64_t(0);
+
+// LDS ordering between the lanes of one wave of a multi-wave workgroup:
+// the fences stop the compiler from moving LDS accesses across this point,
+// and the wave executes its LDS instructions in order.
+__device__ __forceinline__ void wave_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Merge buf[0..n) (unsorted, unique keys) into the sorted top[0..K).
+__device__ void bf_merge_row(const uint64_t* buf, uint64_t* top, uint32_t n, uint32_t K) {
+    const uint32_t lane = lane_id();
+    const uint64_t c = lane < n ? buf[lane] : kKeySent;
+    const uint64_t tv = lane < K ? top[lane] : kKeySent;
+    uint32_t rc = 0, rt = lane;
+    for (uint32_t k = 0; k < n; ++k) {
+        const uint64_t kk = readlane64(c, k);
+        rc += kk < c;
+        rt += kk < tv;
+    }
+    for (uint32_t t = 0; t < K; ++t) rc += readlane64(tv, t) < c;
+    wave_fence();
+    if (lane < n && rc < K) top[rc] = c;
+    if (lane < K && rt < K) top[rt] = tv;
+    wave_fence();
+}
+
+template <int KS>
+__global__ __launch_bounds__(256) void k_bf_i8(BfGemmArgs p) {
+    __shared__ uint64_t sbuf[4][16][kBfBuf];
+    __shared__ uint64_t stop[4][16][16];
+    __shared__ uint32_t scnt[4][16];
+    const uint32_t wave = threadIdx.x >> 6, lane = lane_id();
+    const uint32_t item_id = blockIdx.x * 4u + wave;
+    if (item_id >= p.nitems) return;
+    const BfItem it = p.items[item_id];
+    const uint32_t K = p.K;
+    uint64_t(*buf)[kBfBuf] = sbuf[wave];
+    uint64_t(*top)[16] = stop[wave];
+    uint32_t* cnt = scnt[wave];
+    for (uint32_t i = lane; i < 256u; i += 64u) top[i >> 4][i & 15u] = kKeySent;
+    if (lane < 16) cnt[lane] = 0;
+    wave_fence();
+
+    // A operand: query row lane % 16 (padding rows repeat row 0, results unused).
+    const uint32_t arow = lane & 15u;
+    const uint32_t aq = p.pq[it.qbase + (arow < it.nq ? arow : 0u)];
+    v4i32_t A[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+        A[s] = *reinterpret_cast<const v4i32_t*>(p.q8 + size_t(aq) * p.D + s * 64 + (lane >> 4) * 16);
+    // Output rows of this lane: 4 * (lane / 16) + i.
+    uint32_t qr[4];
+    int32_t nqr[4], thr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = 4u * (lane >> 4) + i;
+        const bool live = r < it.nq;
+        qr[i] = live ? p.pq[it.qbase + r] : 0u;
+        nqr[i] = live ? p.nq[qr[i]] : 0;
+        thr[i] = live ? 0x7FFFFFFF : -1;
+    }
+    const uint32_t cell = it.cell;
+    const uint32_t tb = p.tbase[cell];
+    const uint32_t off = p.offset[cell], csz = p.offset[cell + 1] - off;
+    const uint32_t col = lane & 15u;
+
+    auto merge_all = [&]() {
+        for (uint32_t r = 0; r < 16; ++r) {
+            const uint32_t n = cnt[r];
+            if (n) bf_merge_row(buf[r], top[r], n, K);
+        }
+        wave_fence();
+        if (lane < 16) cnt[lane] = 0;
+        wave_fence();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = 4u * (lane >> 4) + i;
+            if (r < it.nq) {
+                const uint64_t kth = top[r][K - 1];
+                thr[i] = kth == kKeySent ? 0x7FFFFFFF : int32_t(kth >> 32);
+            }
+        }
+    };
+
+    for (uint32_t t = it.t0; t < it.t1; ++t) {
+        const v4i32_t* bp = reinterpret_cast<const v4i32_t*>(p.vt + size_t(t) * KS * 1024u) + lane;
+        v4i32_t acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[s], bp[s * 64], acc, 0, 0, 0);
+        const uint32_t lp = (t - tb) * 16u + col;
+        const bool valid = lp < csz;
+        const int32_t nx = p.nxt[size_t(t) * 16u + col];
+        int32_t d[4];
+        uint32_t surv = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            d[i] = nqr[i] + nx - 2 * acc[i];
+            if (valid && d[i] <= thr[i]) surv |= 1u << i;
+        }
+        if (ballot(surv != 0) == 0) continue;
+        if (surv) {
+            float at[kMaxAttr];
+#pragma unroll
+            for (uint32_t dd = 0; dd < kMaxAttr; ++dd)
+                at[dd] = dd < p.a ? p.attrt[(size_t(t) * 16u + col) * p.a + dd] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (!((surv >> i) & 1u)) continue;
+                bool ok = true;
+#pragma unroll
+                for (uint32_t dd = 0; dd < kMaxAttr; ++dd)
+                    if (dd < p.a)
+                        ok = ok && at[dd] >= p.lo[size_t(qr[i]) * p.a + dd] && at[dd] <= p.hi[size_t(qr[i]) * p.a + dd];
+                if (ok) {
+                    const uint32_t r = 4u * (lane >> 4) + i;
+                    const uint32_t slot = atomicAdd(&cnt[r], 1u);
+                    buf[r][slot] = (uint64_t(uint32_t(d[i])) << 32) | (off + lp);
+                }
+            }
+        }
+        wave_fence();
+        if (ballot(lane < 16 && cnt[lane] >= kBfMergeAt)) merge_all();
+    }
+    merge_all();
+    for (uint32_t idx = lane; idx < it.nq * K; idx += 64u) {
+        const uint32_t r = idx / K, j = idx % K;
+        const uint32_t q = p.pq[it.qbase + r];
+        const size_t slot = size_t(p.part_off[q]) + (size_t(p.ppos[it.qbase + r]) * p.maxch + it.chunk) * K;
+        p.part[slot + j] = top[r][j];
+    }
+}
+
+// Per-query merge of the partial top-K lists of every (cell, chunk).
+__global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
+    __shared__ uint64_t T[64];
+    const uint32_t lane = lane_id();
+    const uint32_t q = p.bfq[blockIdx.x];
+    const uint32_t K = p.K;
+    const uint32_t n = p.counts[q] * p.maxch * K;
+    const uint64_t* part = p.part + p.part_off[q];
+    uint64_t top = kKeySent;
+    for (uint32_t s0 = 0; s0 < n; s0 += 64u) {
+        const uint64_t c = s0 + lane < n ? part[s0 + lane] : kKeySent;
+        const uint64_t thr = readlane64(top, K - 1);
+        const bool surv = c < thr;
+        const uint64_t sm = ballot(surv);
+        if (!sm) continue;
+        uint32_t rs = 0, rt = lane;
+        for (uint64_t m = sm; m; m &= m - 1) {
+            const uint64_t kk = readlane64(c, __builtin_ctzll(m));
+            rs += kk < c;
+            rt += kk < top;
+        }
+        for (uint32_t t = 0; t < K; ++t) rs += readlane64(top, t) < c;
+        __syncthreads();
+        if (surv && rs < K) T[rs] = c;
+        if (lane < K && rt < K) T[rt] = top;
+        __syncthreads();
+        top = lane < K ? T[lane] : kKeySent;
+        __syncthreads();
+    }
+    if (lane < K) {
+        const bool v = top != kKeySent;
+        p.out_ids[size_t(q) * K + lane] = v ? p.gidx[uint32_t(top)] : GF_NO_RESULT;
+        p.out_dist[size_t(q) * K + lane] = v ? float(uint32_t(top >> 32)) : __int_as_float(0x7F800000);
+    }
+    if (lane == 0) {
+        uint32_t scan = 0;
+        for (uint32_t i = 0; i < p.counts[q]; ++i) {
+            const uint32_t c = p.cells[size_t(q) * p.P + i];
+            scan += p.offset[c + 1] - p.offset[c];
+        }
+        uint32_t* ctr = p.counters + size_t(q) * GF_NCOUNTERS;
+        ctr[C_EXPAND] = 0;
+        ctr[C_DIST] = scan;
+        ctr[C_ATTR] = 0;
+        ctr[C_CROSS] = 0;
+        ctr[C_LROW] = 0;
+        ctr[C_SCAN] = scan;
+        ctr[C_PASS] = p.selcount[q];
+        ctr[C_ROUTE] = 2;
+    }
+}
+
+// Index build: int8 tiles (see BfGemmArgs), |x'|^2 and attributes per tile slot.
+__global__ __launch_bounds__(64) void k_tile_i8(const float* vec, uint32_t D, const uint32_t* offset,
+                                               const uint32_t* tbase, const float* attrs, uint32_t a, uint32_t P,
+                                               int8_t* vt, int32_t* nxt, float* attrt) {
+    const uint32_t t = blockIdx.x, lane = lane_id();
+    uint32_t lo = 0, hi = P;   // cell c with tbase[c] <= t < tbase[c+1]
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (tbase[mid] <= t) lo = mid; else hi = mid;
+    }
+    const uint32_t c = lo;
+    const uint32_t col = lane & 15u;
+    const uint32_t lp = (t - tbase[c]) * 16u + col;
+    const uint32_t csz = offset[c + 1] - offset[c];
+    const bool valid = lp < csz;
+    const size_t row = size_t(offset[c]) + lp;
+    const uint32_t KS = D / 64u;
+    for (uint32_t s = 0; s < KS; ++s) {
+        int8_t* dst = vt + (size_t(t) * KS + s) * 1024u + lane * 16u;
+        for (uint32_t j = 0; j < 16; ++j) {
+            const uint32_t k = s * 64u + (lane >> 4) * 16u + j;
+            dst[j] = valid ? int8_t(int32_t(vec[row * D + k]) - 128) : int8_t(0);
+        }
+    }
+    if (lane < 16) {
+        int32_t n = 0;
+        if (valid)
+            for (uint32_t k = 0; k < D; ++k) {
+                const int32_t v = int32_t(vec[row * D + k]) - 128;
+                n += v * v;
+            }
+        nxt[size_t(t) * 16u + col] = n;
+        for (uint32_t d = 0; d < a; ++d) attrt[(size_t(t) * 16u + col) * a + d] = valid ? attrs[row * a + d] : 0.0f;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_q_i8(const float* q, uint32_t D, int8_t* q8, int32_t* nq) {
+    const uint32_t r = blockIdx.x, lane = lane_id();
+    int32_t n = 0;
+    for (uint32_t k = lane; k < D; k += 64u) {
+        const int32_t v = int32_t(q[size_t(r) * D + k]) - 128;
+        q8[size_t(r) * D + k] = int8_t(v);
+        n += v * v;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) n += __shfl_xor(n, m, 64);
+    if (lane == 0) nq[r] = n;
+}
+
 template <bool F16, int LPR, int CPL>
 hipError_t launch_trav_t(const TravArgs& a, uint32_t lds, hipStream_t st) {
     if (a.nsched == 0) return hipSuccess;
@@ -1001,6 +1251,40 @@ hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, hipStream_t 
     return hipErrorInvalidValue;
 }
 
+hipError_t launch_bf_i8(const BfGemmArgs& a, hipStream_t st) {
+    if (!a.nitems) return hipSuccess;
+    const uint32_t blocks = (a.nitems + 3) / 4;
+    switch (a.D / 64) {
+        case 1: hipLaunchKernelGGL(k_bf_i8<1>, dim3(blocks), dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL(k_bf_i8<2>, dim3(blocks), dim3(256), 0, st, a); break;
+        case 3: hipLaunchKernelGGL(k_bf_i8<3>, dim3(blocks), dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL(k_bf_i8<4>, dim3(blocks), dim3(256), 0, st, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_bf_final(const BfFinalArgs& a, hipStream_t st) {
+    if (!a.nbf) return hipSuccess;
+    hipLaunchKernelGGL(k_bf_final, dim3(a.nbf), dim3(64), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_i8(const float* vec_cm, uint32_t D, const uint32_t* offset, const uint32_t* tbase,
+                          const float* attrs_cm, uint32_t a, uint32_t P, uint32_t ntiles, int8_t* vt, int32_t* nxt,
+                          float* attrt, hipStream_t st) {
+    if (!ntiles) return hipSuccess;
+    hipLaunchKernelGGL(k_tile_i8, dim3(ntiles), dim3(64), 0, st, vec_cm, D, offset, tbase, attrs_cm, a, P, vt, nxt,
+                       attrt);
+    return hipGetLastError();
+}
+
+hipError_t launch_q_i8(const float* q, uint32_t Q, uint32_t D, int8_t* q8, int32_t* nq, hipStream_t st) {
+    if (!Q) return hipSuccess;
+    hipLaunchKernelGGL(k_q_i8, dim3(Q), dim3(64), 0, st, q, D, q8, nq);
+    return hipGetLastError();
+}
+
 hipError_t launch_fill_results(uint32_t* ids, float* dist, uint32_t n, hipStream_t st) {
     if (!n) return hipSuccess;
     hipLaunchKernelGGL(k_fill_results, dim3((n + 255) / 256), dim3(256), 0, st, ids, dist, n);
@@ -1032,10 +1316,10 @@ hipError_t launch_norms_f16(const uint16_t* x, uint32_t n, uint32_t D, uint32_t 
 
 hipError_t launch_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi, const uint32_t* grid,
                         const uint32_t* doff, const float* l_q, const float* r_q, uint32_t P,
-                        uint32_t* cells, uint32_t* counts, hipStream_t st) {
+                        const uint32_t* offset, uint32_t* cells, uint32_t* counts, hipStream_t st) {
     if (!Q) return hipSuccess;
     hipLaunchKernelGGL(k_cells, dim3((Q + 63) / 64), dim3(64), 0, st, Q, a, lo, hi, grid, doff, l_q, r_q,
-                       P, cells, counts);
+                       P, offset, cells, counts);
     return hipGetLastError();
 }
 

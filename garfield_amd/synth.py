@@ -98,6 +98,10 @@ def grid_scatter(attrs, grid):
     return l_q, r_q, pid_lists, global_pid.astype(np.int32)
 
 
+def cell_sizes(ix):
+    return np.bincount(ix["global_pid"], minlength=ix["P"]).astype(np.uint32)
+
+
 def cell_members(global_pid, P):
     """Point ids of each cell in ascending id order (cell-local id = position)."""
     order = np.argsort(global_pid, kind="stable")
@@ -117,6 +121,8 @@ def knn_cell_graphs(vectors, members, R, device="cpu", chunk=4096):
     torch = _torch()
     out = []
     for mem in members:
+        if len(mem) == 0:
+            continue
         xc = torch.as_tensor(vectors[mem], device=device)
         n = xc.shape[0]
         k = min(R + 1, n)
@@ -143,6 +149,8 @@ def cross_edges(vectors, members, E, device="cpu", chunk=8192):
     out = np.zeros((N, P * E), np.uint32)
     xall = torch.as_tensor(vectors, device=device)
     for c, mem in enumerate(members):
+        if len(mem) == 0:   # empty cell: edges into it are never followed
+            continue
         yc = torch.as_tensor(vectors[mem], device=device)
         yn = (yc * yc).sum(1)
         k = min(E, yc.shape[0])

@@ -129,6 +129,8 @@ typedef struct {
     uint64_t n_expand, n_dist, n_attr, n_cross, n_lrow, n_scan, n_pass;
     double bytes_traverse;   /* algorithmic HBM bytes of the traversal kernel */
     double bytes_bruteforce; /* algorithmic HBM bytes of the brute-force kernel */
+    double ops_bruteforce;   /* arithmetic of the brute-force kernel (int8 MACs x 2 on MFMA) */
+    uint32_t bf_mfma;        /* 1 if the brute force ran as the int8 MFMA query-batch kernel */
 } gf_search_stats;
 
 gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids /*Q*K*/,

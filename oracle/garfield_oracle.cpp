@@ -441,7 +441,7 @@ void orc_centres_hist(uint32_t N, uint32_t D, uint32_t C, uint32_t P,
 
 void orc_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi,
                const uint32_t* grid, const float* l_q, const float* r_q,
-               uint32_t* cells, uint32_t* counts) {
+               const uint32_t* cell_size, uint32_t* cells, uint32_t* counts) {
     uint32_t P = 1;
     for (uint32_t d = 0; d < a; ++d) P *= grid[d];
     std::vector<uint32_t> doff(a, 0);
@@ -480,7 +480,7 @@ void orc_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi,
         }
         uint32_t n = 0;
         for (uint32_t p = 0; p < P; ++p)
-            if (sel[p]) cells[(size_t)q * P + n++] = p;
+            if (sel[p] && (!cell_size || cell_size[p] > 0)) cells[(size_t)q * P + n++] = p;
         counts[q] = n;
     }
 }

@@ -67,6 +67,7 @@ void orc_centres_hist(uint32_t N, uint32_t D, uint32_t C, uint32_t P,
  * of each query in ascending cell id order.  cells is Q*P (stride P). */
 void orc_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi,
                const uint32_t* grid, const float* l_q, const float* r_q,
+               const uint32_t* cell_size /* P or NULL: cells with no point are skipped */,
                uint32_t* cells, uint32_t* counts);
 
 /* real_dataset_adapter.cuh:346-383 prefiltering_tag_elements: exact count of

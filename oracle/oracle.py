@@ -89,7 +89,7 @@ def centres_hist(data, labels, global_pid, P, contiguous=False):
     return cen, hist
 
 
-def cells(lo, hi, grid, l_q, r_q):
+def cells(lo, hi, grid, l_q, r_q, cell_size=None):
     lo = _c(lo, np.float32)
     hi = _c(hi, np.float32)
     grid = _c(grid, np.uint32)
@@ -97,8 +97,9 @@ def cells(lo, hi, grid, l_q, r_q):
     P = int(np.prod(grid))
     out = np.zeros((Q, P), np.uint32)
     cnt = np.empty(Q, np.uint32)
+    cs = None if cell_size is None else _c(cell_size, np.uint32)
     load().orc_cells(C.c_uint32(Q), C.c_uint32(a), _p(lo), _p(hi), _p(grid), _p(_c(l_q, np.float32)),
-                     _p(_c(r_q, np.float32)), _p(out), _p(cnt))
+                     _p(_c(r_q, np.float32)), _p(cs) if cs is not None else None, _p(out), _p(cnt))
     return out, cnt
 
 

@@ -25,7 +25,7 @@ def _oracle_pipeline(cfg, ix, prefilter, topc=4, gpu_topk=None):
     l_q, r_q = synth.quantile_arrays(ix)
     lo = cfg["lo"].astype(np.float32)
     hi = cfg["hi"].astype(np.float32)
-    cells, cnt = orc.cells(lo, hi, ix["grid"], l_q, r_q)
+    cells, cnt = orc.cells(lo, hi, ix["grid"], l_q, r_q, synth.cell_sizes(ix))
     sel, little = orc.selectivity(ix["attrs"], lo, hi, prefilter, cnt)
     return lo, hi, cells, cnt, sel, little
 
@@ -143,7 +143,13 @@ def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, post
     return ids, dists, ctr, oids, odist, octr, st
 
 
-def _assert_same(ids, dists, ctr, oids, odist, octr):
+def _assert_same(ids, dists, ctr, oids, odist, octr, st=None):
+    if st is not None and st.bf_mfma:
+        # the MFMA brute force evaluates every scanned point, the oracle only
+        # the passing ones
+        octr = octr.copy()
+        rows = octr[:, 7] == 2
+        octr[rows, 1] = octr[rows, 5]
     bad = np.nonzero(np.any(ids != oids, axis=1))[0]
     assert bad.size == 0, f"{bad.size} queries differ, first q={bad[:5]}: gpu={ids[bad[0]]} oracle={oids[bad[0]]}"
     assert np.array_equal(dists.view(np.uint32), odist.view(np.uint32))
@@ -176,15 +182,15 @@ def test_bruteforce_parity(world32, prefilter):
     cfg, ix = world32
     _print_case("bruteforce", prefilter=prefilter)
     ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 64, prefilter=prefilter)
-    _assert_same(ids, dists, ctr, oids, odist, octr)
-    assert st.q_bruteforce > 0
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+    assert st.q_bruteforce > 0 and st.bf_mfma == 1
 
 
 def test_postfilter_routes_to_empty(small_world):
     cfg, ix = small_world
     _print_case("postfilter")
     ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 32, postfilter=12)
-    _assert_same(ids, dists, ctr, oids, odist, octr)
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
     assert st.q_empty > 0
 
 
@@ -207,3 +213,29 @@ def test_recall_against_ground_truth(world32):
             assert np.all(a >= cfg["lo"][q]) and np.all(a <= cfg["hi"][q])
             d = np.sum((cfg["queries"][q].astype(np.float64) - ix["vectors"][i]) ** 2)
             assert abs(d - dists[q, j]) <= 1e-5 * max(d, 1.0)
+
+
+@pytest.mark.parametrize("L,prefilter", [(32, 0.0), (100, 0.0), (64, 0.01), (64, 1.0)])
+def test_gaussian_parity(world_gauss, L, prefilter):
+    """Non-integer 96-d data: canonical fp32 summation order, gather brute force, 3 attributes."""
+    cfg, ix = world_gauss
+    _print_case("gauss", L=L, prefilter=prefilter)
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, L, prefilter=prefilter)
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+    assert st.bf_mfma == 0
+    if prefilter == 1.0:
+        assert st.q_traverse == 0
+
+
+def test_mfma_bruteforce_all_queries(world32):
+    """Every query on the int8 MFMA brute force: exact filtered top-10."""
+    from oracle import oracle as orc
+    cfg, ix = world32
+    _print_case("mfma-bf")
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 10, prefilter=1.0)
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+    assert st.bf_mfma == 1 and st.q_traverse == 0
+    lo = cfg["lo"].astype(np.float32)
+    hi = cfg["hi"].astype(np.float32)
+    gt, gtd = orc.ground_truth(ix["vectors"], ix["attrs"], cfg["queries"], lo, hi, 10)
+    assert orc.recall(ids, gt, gtd) == 1.0

@@ -109,6 +109,20 @@ def test_cells_out_of_domain_select_nothing():
     assert cnt[0] == 0 and cnt[1] == 0 and cnt[2] >= 1
 
 
+def test_cells_skip_empty_cells():
+    att = np.array([[0, 0], [0, 1], [9, 9], [9, 8]], np.int32)   # cells (0,1) and (1,0) stay empty
+    l_q, r_q, _, gp = synth.grid_scatter(att, [2, 2])
+    sizes = np.bincount(gp, minlength=4).astype(np.uint32)
+    assert sizes[1] == 0 and sizes[2] == 0
+    lo = np.array([[0, 0]], np.float32)
+    hi = np.array([[9, 9]], np.float32)
+    lq = np.concatenate(l_q).astype(np.float32)
+    rq = np.concatenate(r_q).astype(np.float32)
+    full, n_full = orc.cells(lo, hi, np.array([2, 2]), lq, rq)
+    skip, n_skip = orc.cells(lo, hi, np.array([2, 2]), lq, rq, sizes)
+    assert n_full[0] == 4 and list(skip[0, :n_skip[0]]) == [0, 3]
+
+
 def test_selectivity_counts_and_threshold():
     rng = np.random.default_rng(7)
     att = rng.integers(0, 1000, (20000, 2)).astype(np.float32)
