@@ -705,7 +705,7 @@ __global__ __launch_bounds__(64) void k_norms_f16(const uint16_t* x, uint32_t n,
 // cell id.  Per attribute: lo cell = first c with r_q[c] >= lo, hi cell =
 // (first c with l_q[c] > hi) - 1; the product is enumerated with the last
 // attribute fastest (gpu_graph.cu:10965-10973).  A range beyond every cell
-// (quirk Q16) selects nothing; an empty interval between two cells selects
+// (the reference computes cell -1 or g there) selects nothing; an empty interval between two cells selects
 // the next cell, as the reference's do-while does.  Cells holding no point
 // are never selected (the reference would read past them).
 __global__ void k_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi, const uint32_t* grid,

@@ -198,7 +198,7 @@ def build_index(vectors, attrs, grid, R, E, C=0, kmeans_iters=8, seed=5, device=
 
 
 def write_index(ix, prefix):
-    """Write the App. A files: {prefix}.fvecs, {prefix}_cell{i}.graph, {prefix}.cross, .grid, .attrs, .cluster"""
+    """Write the index files (formats of README.md:101-170): {prefix}.fvecs, {prefix}_cell{i}.graph, {prefix}.cross, .grid, .attrs, .cluster"""
     from . import formats
     formats.write_fvecs(prefix + ".fvecs", ix["vectors"])
     members = cell_members(ix["global_pid"], ix["P"])
@@ -231,7 +231,7 @@ def open_device_index(ix, **kw):
 
 # ------------------------------------------------------------- workloads
 def config_small(N=100_000, Q=1000, R=16, C=100, sel=0.3, seed=1):
-    """BASELINE config 1 (optionally shrunk): 128-d integer vectors, 2 attributes, 4x4 grid."""
+    """Config C1 (optionally shrunk): 128-d integer vectors, 2 attributes, 4x4 grid."""
     vec = uniform_int_vectors(N, 128, seed)
     att = uniform_attrs(N, 2, seed + 1)
     qv = uniform_int_vectors(Q, 128, seed + 2)
@@ -240,7 +240,7 @@ def config_small(N=100_000, Q=1000, R=16, C=100, sel=0.3, seed=1):
 
 
 def config_headline(N=1_000_000, Q=10_000, R=32, C=1000, seed=11):
-    """1M x 128 integers, 2 attributes on 4x4, selectivity log-U[1%, 50%]."""
+    """Config C2 (headline): 1M x 128 integers, 2 attributes on 4x4, selectivity log-U[1%, 50%]."""
     vec = uniform_int_vectors(N, 128, seed)
     att = uniform_attrs(N, 2, seed + 1)
     qv = uniform_int_vectors(Q, 128, seed + 2)

@@ -194,7 +194,8 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
         // Entry points of the first cell (gpu_graph.cu:3347-3351).  The
         // reference inserts their *point ids* into the visited set, which is
         // otherwise keyed by cell-local ids; kept as is.  entry[j] is reduced
-        // modulo the cell size (quirk Q2 reads past the cell otherwise).
+        // modulo the cell size (the reference draws them from
+        // [0, N-(P-1)*ceil(N/P)) and reads past a smaller first cell).
         {
             const uint32_t c0 = cl[0], sz0 = cell_size(c0);
             for (uint32_t j = 0; j < R; ++j) {
@@ -260,14 +261,14 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
                     if (A[i].id != SENT) s.ctr[ORC_C_CROSS]++;
                 for (uint32_t i = 0; i < XSLOTS; ++i) {
                     const uint32_t ci = i % XSTEP;
-                    if (ci >= L || A[ci].id == SENT) continue;  // quirk Q7: ci >= L, not ci > L
+                    if (ci >= L || A[ci].id == SENT) continue;  // in-bounds guard (the reference tests ci > L)
                     const uint32_t g = A[ci].id & IDM;
                     bool got = false;
                     for (uint32_t j = 0; j < E && !got; ++j) {
                         uint32_t nl = ix->cross[(size_t)g * P * E + (size_t)nxt * E + j];
                         if (H.insert(nl).second) { W[i].id = ix->global_idx[nbase + nl]; got = true; }
                     }
-                    if (!got)                                // quirk Q6: scan [0, |cell|)
+                    if (!got)                                // fallback: scan [0, |cell|), not [0, 62500)
                         for (uint32_t rp = 0; rp < nsz; ++rp)
                             if (H.insert(rp).second) { W[i].id = ix->global_idx[nbase + rp]; break; }
                 }
@@ -318,7 +319,8 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
         found.resize(kk);
         out = found;
     }
-    // Output: the first K distinct ids (quirk Q8: the reference may repeat ids).
+    // Output: the first K distinct ids (the reference merges top and recycle
+    // without deduplication and may repeat an id, gpu_graph.cu:4044-4047).
     uint32_t n = 0, prev = SENT;
     for (const Cand& x : out) {
         if (n >= K) break;
@@ -458,7 +460,7 @@ void orc_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi,
             int64_t j = 0;                           // to_upper_bound_linear_scan
             while (j < g && lq[j] <= hi[(size_t)q * a + d]) ++j;
             cl[d] = i; ch[d] = j - 1;
-            if (cl[d] >= g || ch[d] < 0) empty = true;   // quirk Q16
+            if (cl[d] >= g || ch[d] < 0) empty = true;   // range outside every cell
             ch[d] = std::max(ch[d], cl[d]);
         }
         std::vector<char> sel(P, 0);

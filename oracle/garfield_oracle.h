@@ -15,7 +15,9 @@
  *     the reference orders equal distances by sorting-network position;
  *   - cross-cell entry slots are filled in slot order 0..127;
  *   - the +inf distance replaces the reference's 1e9 stand-in;
- *   - out-of-bounds reads of the reference (App. B quirks Q2, Q6, Q7, Q16) are
+ *   - out-of-bounds reads of the reference (entry ids past a small first cell,
+ *     the cross-edge fallback scan to 62500, the ci > L guard, ranges outside
+ *     the grid) are
  *     replaced by the in-bounds rule named at each function.
  */
 #ifndef GARFIELD_ORACLE_H
@@ -57,7 +59,7 @@ void orc_row_norms_f16(const uint16_t* x, uint32_t n, uint32_t D, float* out);
 
 /* tools.cuh:569-602 load_clustering: fp32 centres (sequential sums, then divide)
  * and the cell x cluster histogram.  contiguous=1 reproduces the reference's
- * i / ceil(N/P) cell assignment (quirk Q1); 0 uses global_pid. */
+ * i / ceil(N/P) cell assignment (tools.cuh:587-590); 0 uses global_pid. */
 void orc_centres_hist(uint32_t N, uint32_t D, uint32_t C, uint32_t P,
                       const float* data, const int32_t* labels,
                       const uint32_t* global_pid, int32_t contiguous,
