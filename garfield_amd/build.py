@@ -2,7 +2,9 @@
 
 Everything is compiled in-tree with hipcc so the built files travel with the
 repository snapshot.  Packed-fp32 instructions are disabled for all device
-code (-packed-fp32-ops).
+code (-packed-fp32-ops).  MFMA results are kept in ordinary VGPRs
+(-amdgpu-mfma-vgpr-form): the brute-force epilogue reads every accumulator
+with VALU compares, and AGPR results would cost one v_accvgpr_read each.
 """
 import os
 import subprocess
@@ -19,6 +21,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 COMMON = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-deprecated-declarations", "-I", os.path.join(ROOT, "include"),
 ]
 LIB_SOURCES = ["gf_kernels.hip", "gf_host.cpp", "gf_io.cpp"]

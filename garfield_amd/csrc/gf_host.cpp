@@ -94,11 +94,11 @@ struct gf_index {
     DevBuf<uint32_t> tile_cell, tile_row0, tile_n;
     DevBuf<uint16_t> centres;
     uint32_t ntiles = 0;
-    // Query-batch MFMA brute force (integer data in [0, 255], D a multiple of 64).
+    // Query-batch MFMA brute force (integer data in [0, 255], D a multiple of
+    // 64, at most 4 integer attributes spread by less than 65534 in each cell).
     bool i8 = false;
     DevBuf<int8_t> vt;
-    DevBuf<int32_t> nxt;
-    DevBuf<float> attrt;
+    DevBuf<int32_t> nxt, meta, abase;
     DevBuf<uint32_t> tbase;
     std::vector<uint32_t> tbase_h;
     ~gf_index() {
@@ -108,7 +108,7 @@ struct gf_index {
         return vec.bytes() + attrs.bytes() + l_q.bytes() + r_q.bytes() + cnorm.bytes() + graph.bytes() +
                cross.bytes() + offset.bytes() + gidx.bytes() + lrow.bytes() + grid.bytes() + doff.bytes() +
                hist.bytes() + tile_cell.bytes() + tile_row0.bytes() + tile_n.bytes() + centres.bytes() +
-               vt.bytes() + nxt.bytes() + attrt.bytes() + tbase.bytes();
+               vt.bytes() + nxt.bytes() + meta.bytes() + abase.bytes() + tbase.bytes();
     }
 };
 
@@ -125,7 +125,7 @@ struct gf_batch {
     DevBuf<float> qf32, qnorm, lo, hi, cdist, out_dist;
     DevBuf<uint16_t> q16, q16v;
     DevBuf<uint32_t> cells, counts, little, selcount, cellq, ccount, cstart, cfill, topk;
-    DevBuf<uint32_t> out_ids, counters, sched, entry;
+    DevBuf<uint32_t> out_ids, counters, sched, entry, gbound;
 };
 
 namespace {
@@ -261,9 +261,23 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
             ix.rowbytes = D * 2;
             vec_f32_dev = tmp.p;
         }
-        // Integer-valued data in [0, 255]: build the int8 tiles of the MFMA brute force.
-        bool ints = ix.vdtype == GF_VEC_F32 && D % 64 == 0 && D <= 256;
+        // Integer-valued data in [0, 255] and integer attributes packable as
+        // 16-bit offsets from a per-cell base: build the MFMA brute-force tiles.
+        bool ints = ix.vdtype == GF_VEC_F32 && D % 64 == 0 && D <= 256 && a >= 1 && a <= 4;
         for (size_t i = 0; ints && i < v.size(); ++i) ints = v[i] >= 0.0f && v[i] <= 255.0f && v[i] == std::floor(v[i]);
+        std::vector<int32_t> abase(size_t(P) * a, 0);
+        for (uint32_t c = 0; ints && c < P; ++c)
+            for (uint32_t d = 0; ints && d < a; ++d) {
+                double mn = 0.0, mx = 0.0;
+                for (uint32_t r = ix.offset_h[c]; r < ix.offset_h[c + 1]; ++r) {
+                    const double x = h.attrs[size_t(gidx[r]) * a + d];
+                    ints = ints && x == std::floor(x) && x >= -2147483648.0 && x < 2147483648.0;
+                    mn = r == ix.offset_h[c] ? x : std::min(mn, x);
+                    mx = r == ix.offset_h[c] ? x : std::max(mx, x);
+                }
+                ints = ints && mx - mn <= 65533.0;
+                abase[size_t(c) * a + d] = int32_t(mn);
+            }
         if (ints) {
             ix.tbase_h.assign(P + 1, 0);
             for (uint32_t c = 0; c < P; ++c)
@@ -272,9 +286,10 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
             ix.tbase.upload(ix.tbase_h);
             ix.vt.alloc(size_t(nt) * (D / 64) * 1024);
             ix.nxt.alloc(size_t(nt) * 16);
-            ix.attrt.alloc(size_t(nt) * 16 * a);
-            GF_HIP(gf::launch_tile_i8(vec_f32_dev, D, ix.offset.p, ix.tbase.p, ix.attrs.p, a, P, nt, ix.vt.p,
-                                      ix.nxt.p, ix.attrt.p, ix.stream));
+            ix.meta.alloc(size_t(nt) * 16 * (1 + (a + 1) / 2));
+            ix.abase.upload(abase);
+            GF_HIP(gf::launch_tile_i8(vec_f32_dev, D, ix.offset.p, ix.tbase.p, ix.attrs.p, a, ix.abase.p, P, nt,
+                                      ix.vt.p, ix.nxt.p, ix.meta.p, ix.stream));
             ix.i8 = true;
         }
         GF_HIP(hipStreamSynchronize(ix.stream));
@@ -628,8 +643,9 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         a.Lpad = Lpad;
 
         // Brute-force route on MFMA when vectors and queries are int8-exact:
-        // work items of (cell, 16 queries, chunk of the cell's tiles).
-        const bool gemm = ix->i8 && b->i8 && !bq.empty();
+        // work items of (cell, 64 queries, chunk of the cell's tiles), ordered
+        // chunk-major so that the query blocks of one chunk run together.
+        const bool gemm = ix->i8 && b->i8 && !bq.empty() && K <= gf::kBfKMax;
         double bf_ops = 0.0, bf_bytes_gemm = 0.0;
         gf::BfGemmArgs ga{};
         gf::BfFinalArgs fa{};
@@ -659,11 +675,11 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 const uint32_t t0c = ix->tbase_h[c], t1c = ix->tbase_h[c + 1];
                 for (uint32_t ch = 0; t0c + ch * gf::kBfChunk < t1c; ++ch) {
                     const uint32_t ts = t0c + ch * gf::kBfChunk, te = std::min(t1c, ts + gf::kBfChunk);
-                    for (uint32_t qb = 0; qb < nlist; qb += 16) {
-                        const uint32_t nq = std::min(16u, nlist - qb);
+                    for (uint32_t qb = 0; qb < nlist; qb += gf::kBfQB) {
+                        const uint32_t nq = std::min(gf::kBfQB, nlist - qb);
                         items.push_back({c, base + qb, nq, ts, te, ch});
                         bf_ops += 2.0 * double(te - ts) * 16.0 * nq * ix->D;
-                        bf_bytes_gemm += double(te - ts) * (KS * 1024.0 + 64.0);
+                        bf_bytes_gemm += double(te - ts) * (KS * 1024.0 + 64.0 * (1 + (ix->a + 1) / 2));
                     }
                 }
             }
@@ -674,7 +690,10 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             b->bfq.upload(bq);
             if (b->part.n < tot) b->part.alloc(tot);
             GF_HIP(hipMemsetAsync(b->part.p, 0xFF, tot * sizeof(uint64_t), st));
-            ga.vt = ix->vt.p; ga.nxt = ix->nxt.p; ga.attrt = ix->attrt.p; ga.tbase = ix->tbase.p;
+            if (b->gbound.n < Q) b->gbound.alloc(Q);
+            GF_HIP(hipMemsetAsync(b->gbound.p, 0xFF, size_t(Q) * sizeof(uint32_t), st));
+            ga.vt = ix->vt.p; ga.nxt = ix->nxt.p; ga.meta = ix->meta.p; ga.abase = ix->abase.p;
+            ga.tbase = ix->tbase.p; ga.gbound = b->gbound.p;
             ga.offset = ix->offset.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p; ga.hi = b->hi.p;
             ga.items = b->items.p; ga.nitems = uint32_t(items.size()); ga.pq = b->pq.p; ga.ppos = b->ppos.p;
             ga.part_off = b->part_off.p; ga.part = b->part.p; ga.maxch = maxch; ga.K = K; ga.a = ix->a;

@@ -65,19 +65,23 @@ struct TravArgs {
     uint32_t a, P, R, E, L, K, rl, hbits, Lpad;
 };
 
-// Query-batch brute force on int8 MFMA (integer-valued data in [0, 255]).
-// Vectors are stored shifted by -128 as int8, per cell in tiles of 16 points
-// laid out in MFMA operand order: tile t, k-step s holds 64 lanes x 16 bytes,
-// lane l carrying bytes [64 s + 16 (l / 16), +16) of point l % 16.
+// Query-batch brute force on int8 MFMA (integer data in [0, 255], integer
+// attributes whose spread inside each cell is below 65534).  Vectors are
+// stored shifted by -128 as int8, per cell in tiles of 16 points laid out in
+// MFMA operand order: tile t, k-step s holds 64 lanes x 16 bytes, lane l
+// carrying bytes [64 s + 16 (l / 16), +16) of point l % 16.
 constexpr uint32_t kBfTile = 16;      // points per tile
 constexpr uint32_t kBfChunk = 512;    // tiles per work item (8192 points)
+constexpr uint32_t kBfKMax = 16;      // largest K of the MFMA route
+constexpr uint32_t kBfQB = 64;        // queries per work item
 struct BfItem {
     uint32_t cell, qbase, nq, t0, t1, chunk;
 };
 struct BfGemmArgs {
     const int8_t* vt;          // tiled int8 vectors
     const int32_t* nxt;        // |x - 128|^2 per tiled point
-    const float* attrt;        // attributes per tiled point
+    const int32_t* meta;       // per tile: -floor(|x'|^2/2) x 16, then AW attribute words x 16
+    const int32_t* abase;      // P*a smallest attribute value of each cell
     const uint32_t* tbase;     // P+1 first tile of each cell
     const uint32_t* offset;    // P+1 first row of each cell
     const int8_t* q8;          // Q*D queries shifted by -128
@@ -90,6 +94,7 @@ struct BfGemmArgs {
     const uint32_t* ppos;      // position of the cell in that query's list
     const uint32_t* part_off;  // per query: first partial slot entry
     uint64_t* part;            // partial top-K keys: (d << 32) | row
+    uint32_t* gbound;          // per query: smallest K-th distance of any chunk so far
     uint32_t maxch, K, a, D;
 };
 struct BfFinalArgs {
@@ -115,8 +120,8 @@ hipError_t launch_fill_results(uint32_t* ids, float* dist, uint32_t n, hipStream
 hipError_t launch_bf_i8(const BfGemmArgs& a, hipStream_t st);
 hipError_t launch_bf_final(const BfFinalArgs& a, hipStream_t st);
 hipError_t launch_tile_i8(const float* vec_cm, uint32_t D, const uint32_t* offset, const uint32_t* tbase,
-                          const float* attrs_cm, uint32_t a, uint32_t P, uint32_t ntiles, int8_t* vt,
-                          int32_t* nxt, float* attrt, hipStream_t st);
+                          const float* attrs_cm, uint32_t a, const int32_t* abase, uint32_t P, uint32_t ntiles,
+                          int8_t* vt, int32_t* nxt, int32_t* meta, hipStream_t st);
 hipError_t launch_q_i8(const float* q, uint32_t Q, uint32_t D, int8_t* q8, int32_t* nq, hipStream_t st);
 hipError_t launch_f2h(const float* x, uint16_t* out, size_t n, float alpha, hipStream_t st);
 hipError_t launch_f2h_pad(const float* x, uint32_t rows, uint32_t D, uint16_t* out,

@@ -921,19 +921,35 @@ __global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P
 }
 
 // ------------------------------------------ query-batch brute force (MFMA)
-// Filtered brute force for queries routed to it when every vector and query
-// is an integer in [0, 255]: with q' = q - 128 and x' = x - 128 (int8),
-// |q - x|^2 = |q'|^2 + |x'|^2 - 2 q'.x' holds exactly in int32, so the
-// distances are bit-identical to the canonical fp32 ones (all sums < 2^24).
-// A wave takes 16 queries that select one cell and one chunk of that cell's
-// tiles; v_mfma_i32_16x16x64_i8 produces a 16 x 16 distance block per tile.
-// A per-query threshold (the current K-th distance) rejects almost every
-// pair; the range filter runs only on the few survivors, which are buffered
-// in LDS and merged into a per-query top-K keyed by (distance, row).
+// Filtered brute force for the queries routed to it, when every vector and
+// query is an integer in [0, 255] and every attribute an integer whose spread
+// inside a cell is below 65534.  With x' = x - 128 and q' = q - 128 (int8),
+// |q - x|^2 = |q'|^2 + |x'|^2 - 2 q'.x' holds exactly in int32, so distances
+// are bit-identical to the canonical fp32 ones (all sums < 2^24).
+//
+// A wave owns 64 queries that select one cell (the stationary B operand, four
+// 16-query column tiles) and streams a chunk of that cell's 16-point tiles as
+// the A operand of v_mfma_i32_16x16x64_i8; lane l receives points
+// 4 (l / 16) + i, i < 4, of query 16 j + l % 16 for each column tile j.  The
+// accumulator starts at -floor(|x'|^2 / 2), so "d <= thr" becomes the single
+// compare acc >= ceil((|q'|^2 - thr) / 2) (exact up to the parity of |x'|^2,
+// which the owner's exact test settles).  The range test runs on every pair as
+// a packed u16 clamp: per cell, attributes are stored as value - base in
+// [0, 65533] (tile padding 65535) and a query's range becomes [lo', hi'] in the
+// same units (an empty range is [65534, 65534]); a point passes iff clamping
+// its packed word leaves it unchanged.  Survivors (rare once the threshold has
+// settled) go to a per-query LDS buffer; lane q of the wave owns query q of
+// the block and keeps its sorted top-K (distance, row) in LDS.  Thresholds
+// tighten from the wave's own top-K and from a per-query global bound that
+// every chunk of the query lowers with atomicMin: a point farther than some
+// chunk's K-th distance cannot be in the final top-K.
 typedef int v4i32_t __attribute__((ext_vector_type(4)));
-constexpr uint32_t kBfBuf = 64;      // survivors buffered per query
-constexpr uint32_t kBfMergeAt = 48;  // a tile adds at most 16 per query
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+constexpr uint32_t kQB = 64;        // queries per wave
+constexpr uint32_t kBfBufQ = 16;    // survivor slots per query (one tile adds <= 16)
+constexpr uint32_t kBfRefresh = 32; // tiles between reads of the global bounds
 constexpr uint64_t kKeySent = ~uint64_t(0);
+constexpr int32_t kTpOpen = INT32_MIN;  // acc threshold while fewer than K are known
 
 // LDS ordering between the lanes of one wave of a multi-wave workgroup:
 // the fences stop the compiler from moving LDS accesses across this point,
@@ -944,127 +960,196 @@ __device__ __forceinline__ void wave_fence() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Merge buf[0..n) (unsorted, unique keys) into the sorted top[0..K).
-__device__ void bf_merge_row(const uint64_t* buf, uint64_t* top, uint32_t n, uint32_t K) {
-    const uint32_t lane = lane_id();
-    const uint64_t c = lane < n ? buf[lane] : kKeySent;
-    const uint64_t tv = lane < K ? top[lane] : kKeySent;
-    uint32_t rc = 0, rt = lane;
-    for (uint32_t k = 0; k < n; ++k) {
-        const uint64_t kk = readlane64(c, k);
-        rc += kk < c;
-        rt += kk < tv;
-    }
-    for (uint32_t t = 0; t < K; ++t) rc += readlane64(tv, t) < c;
-    wave_fence();
-    if (lane < n && rc < K) top[rc] = c;
-    if (lane < K && rt < K) top[rt] = tv;
-    wave_fence();
+__device__ __forceinline__ uint32_t clamp16(uint32_t x, uint32_t lo, uint32_t hi) {
+    u16x2_t v = __builtin_bit_cast(u16x2_t, x);
+    v = __builtin_elementwise_min(__builtin_elementwise_max(v, __builtin_bit_cast(u16x2_t, lo)),
+                                  __builtin_bit_cast(u16x2_t, hi));
+    return __builtin_bit_cast(uint32_t, v);
 }
 
-template <int KS>
+// One attribute range [lo, hi] (floats holding integers) in the units of a
+// cell whose attribute values are base + [0, 65533].
+__device__ __forceinline__ void range16(float lo, float hi, int32_t base, uint32_t& l16, uint32_t& h16) {
+    const float lc = ceilf(fmaxf(lo, -4.0e9f)), hc = floorf(fminf(hi, 4.0e9f));
+    const int64_t l = int64_t(lc) - base, h = int64_t(hc) - base;
+    if (!(lc <= hc) || h < 0 || l > 65533) { l16 = h16 = 65534u; return; }
+    l16 = uint32_t(l < 0 ? 0 : l);
+    h16 = uint32_t(h > 65533 ? 65533 : h);
+}
+
+__device__ __forceinline__ int32_t acc_threshold(int32_t nq, uint32_t thr) {
+    if (thr == 0xFFFFFFFFu) return kTpOpen;
+    return int32_t((int64_t(nq) - int64_t(thr) + 1) >> 1);   // ceil((nq - thr) / 2)
+}
+
+template <int KS, int AW>
 __global__ __launch_bounds__(256) void k_bf_i8(BfGemmArgs p) {
-    __shared__ uint64_t sbuf[4][16][kBfBuf];
-    __shared__ uint64_t stop[4][16][16];
-    __shared__ uint32_t scnt[4][16];
+    __shared__ uint64_t s_buf[4][kQB * kBfBufQ];
+    __shared__ uint64_t s_top[4][kBfKMax * kQB];
+    __shared__ uint32_t s_cnt[4][kQB];
+    __shared__ int32_t s_tp[4][kQB];
+    __shared__ int32_t s_nq[4][kQB];
+    __shared__ uint32_t s_bnd[4][2 * AW][kQB];
     const uint32_t wave = threadIdx.x >> 6, lane = lane_id();
-    const uint32_t item_id = blockIdx.x * 4u + wave;
-    if (item_id >= p.nitems) return;
+    // XCD-aware order: workgroups go round-robin to the 8 XCDs, so XCD x gets
+    // a contiguous run of items (neighbouring query blocks of one chunk share
+    // that XCD's L2).
+    const uint32_t nwg = gridDim.x, xcd = blockIdx.x & 7u, k8 = blockIdx.x >> 3;
+    const uint32_t wg = xcd * (nwg >> 3) + min(xcd, nwg & 7u) + k8;
+    const uint32_t item_id = wg * 4u + wave;
+    if (item_id >= p.nitems) return;   // waves are independent: no workgroup barrier below
     const BfItem it = p.items[item_id];
     const uint32_t K = p.K;
-    uint64_t(*buf)[kBfBuf] = sbuf[wave];
-    uint64_t(*top)[16] = stop[wave];
-    uint32_t* cnt = scnt[wave];
-    for (uint32_t i = lane; i < 256u; i += 64u) top[i >> 4][i & 15u] = kKeySent;
-    if (lane < 16) cnt[lane] = 0;
+    uint64_t* buf = s_buf[wave];
+    uint64_t* top = s_top[wave];
+    uint32_t* cnt = s_cnt[wave];
+    int32_t* stp = s_tp[wave];
+    int32_t* snq = s_nq[wave];
+    const uint32_t cell = it.cell;
+
+    // Owner state: lane q owns query q of the block.
+    const bool own_live = lane < it.nq;
+    const uint32_t own_q = p.pq[it.qbase + (own_live ? lane : 0u)];
+    const int32_t own_nq = p.nq[own_q];
+    uint32_t own_thr = own_live ? p.gbound[own_q] : 0u;
+    for (uint32_t k = 0; k < K; ++k) top[k * kQB + lane] = kKeySent;
+    cnt[lane] = 0;
+    snq[lane] = own_nq;
+    stp[lane] = own_live ? acc_threshold(own_nq, own_thr) : INT32_MAX;
+#pragma unroll
+    for (int w = 0; w < AW; ++w) {
+        uint32_t l0 = 65534u, h0 = 65534u, l1 = 0u, h1 = 0u;
+        if (own_live) {
+            const uint32_t d0 = 2u * w, d1 = 2u * w + 1u;
+            range16(p.lo[size_t(own_q) * p.a + d0], p.hi[size_t(own_q) * p.a + d0], p.abase[cell * p.a + d0], l0, h0);
+            if (d1 < p.a)
+                range16(p.lo[size_t(own_q) * p.a + d1], p.hi[size_t(own_q) * p.a + d1], p.abase[cell * p.a + d1], l1,
+                        h1);
+        }
+        s_bnd[wave][2 * w][lane] = l0 | (l1 << 16);
+        s_bnd[wave][2 * w + 1][lane] = h0 | (h1 << 16);
+    }
     wave_fence();
 
-    // A operand: query row lane % 16 (padding rows repeat row 0, results unused).
-    const uint32_t arow = lane & 15u;
-    const uint32_t aq = p.pq[it.qbase + (arow < it.nq ? arow : 0u)];
-    v4i32_t A[KS];
+    // Column data: query 16 j + col of the block (a dead column repeats the
+    // first query; its empty range keeps it from producing survivors).
+    const uint32_t col = lane & 15u, grp = lane >> 4;
+    v4i32_t B[4][KS];
+    uint32_t blo[4][AW], bhi[4][AW];
+    int32_t tp[4];
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-        A[s] = *reinterpret_cast<const v4i32_t*>(p.q8 + size_t(aq) * p.D + s * 64 + (lane >> 4) * 16);
-    // Output rows of this lane: 4 * (lane / 16) + i.
-    uint32_t qr[4];
-    int32_t nqr[4], thr[4];
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t ql = 16u * j + col;
+        const uint32_t q = p.pq[it.qbase + (ql < it.nq ? ql : 0u)];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t r = 4u * (lane >> 4) + i;
-        const bool live = r < it.nq;
-        qr[i] = live ? p.pq[it.qbase + r] : 0u;
-        nqr[i] = live ? p.nq[qr[i]] : 0;
-        thr[i] = live ? 0x7FFFFFFF : -1;
+        for (int s = 0; s < KS; ++s)
+            B[j][s] = *reinterpret_cast<const v4i32_t*>(p.q8 + size_t(q) * p.D + s * 64 + grp * 16);
+#pragma unroll
+        for (int w = 0; w < AW; ++w) {
+            blo[j][w] = s_bnd[wave][2 * w][ql];
+            bhi[j][w] = s_bnd[wave][2 * w + 1][ql];
+        }
+        tp[j] = stp[ql];
     }
-    const uint32_t cell = it.cell;
-    const uint32_t tb = p.tbase[cell];
-    const uint32_t off = p.offset[cell], csz = p.offset[cell + 1] - off;
-    const uint32_t col = lane & 15u;
 
-    auto merge_all = [&]() {
-        for (uint32_t r = 0; r < 16; ++r) {
-            const uint32_t n = cnt[r];
-            if (n) bf_merge_row(buf[r], top[r], n, K);
-        }
-        wave_fence();
-        if (lane < 16) cnt[lane] = 0;
-        wave_fence();
+    const uint32_t tb = p.tbase[cell];
+    const uint32_t off = p.offset[cell];
+    constexpr uint32_t kMeta = 16u * (1u + AW);
+    auto reload_tp = [&]() {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t r = 4u * (lane >> 4) + i;
-            if (r < it.nq) {
-                const uint64_t kth = top[r][K - 1];
-                thr[i] = kth == kKeySent ? 0x7FFFFFFF : int32_t(kth >> 32);
-            }
-        }
+        for (int j = 0; j < 4; ++j) tp[j] = stp[16u * j + col];
     };
 
+    // Operands of tile t + 1 are loaded while tile t is computed.
+    v4i32_t A[KS], mh, ma[AW];
+    auto load_tile = [&](uint32_t t) {
+        const v4i32_t* vp = reinterpret_cast<const v4i32_t*>(p.vt + size_t(t) * KS * 1024u) + lane;
+        const int32_t* mt = p.meta + size_t(t) * kMeta;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) A[s] = vp[s * 64];
+        mh = *reinterpret_cast<const v4i32_t*>(mt + 4u * grp);
+#pragma unroll
+        for (int w = 0; w < AW; ++w) ma[w] = *reinterpret_cast<const v4i32_t*>(mt + 16u * (1 + w) + 4u * grp);
+    };
+    load_tile(it.t0);
     for (uint32_t t = it.t0; t < it.t1; ++t) {
-        const v4i32_t* bp = reinterpret_cast<const v4i32_t*>(p.vt + size_t(t) * KS * 1024u) + lane;
-        v4i32_t acc = {0, 0, 0, 0};
+        v4i32_t acc[4];
 #pragma unroll
-        for (int s = 0; s < KS; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[s], bp[s * 64], acc, 0, 0, 0);
-        const uint32_t lp = (t - tb) * 16u + col;
-        const bool valid = lp < csz;
-        const int32_t nx = p.nxt[size_t(t) * 16u + col];
-        int32_t d[4];
-        uint32_t surv = 0;
+        for (int j = 0; j < 4; ++j) {
+            acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B[j][0], mh, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            d[i] = nqr[i] + nx - 2 * acc[i];
-            if (valid && d[i] <= thr[i]) surv |= 1u << i;
+            for (int s = 1; s < KS; ++s) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[s], B[j][s], acc[j], 0, 0, 0);
         }
-        if (ballot(surv != 0) == 0) continue;
-        if (surv) {
-            float at[kMaxAttr];
+        const v4i32_t cmh = mh, cma0 = ma[0], cma1 = ma[AW - 1];
+        if (t + 1 < it.t1) load_tile(t + 1);
+        // Branch-free test of one (point i, query column j) pair.
+        auto pass = [&](int j, int i) {
+            bool ok = acc[j][i] >= tp[j];
+            const uint32_t x0 = uint32_t(cma0[i]);
+            ok &= clamp16(x0, blo[j][0], bhi[j][0]) == x0;
+            if (AW > 1) {
+                const uint32_t x1 = uint32_t(cma1[i]);
+                ok &= clamp16(x1, blo[j][AW - 1], bhi[j][AW - 1]) == x1;
+            }
+            return ok;
+        };
+        bool anyl = false;   // lane-mask OR: no per-pair ballot
 #pragma unroll
-            for (uint32_t dd = 0; dd < kMaxAttr; ++dd)
-                at[dd] = dd < p.a ? p.attrt[(size_t(t) * 16u + col) * p.a + dd] : 0.0f;
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (!((surv >> i) & 1u)) continue;
-                bool ok = true;
+            for (int i = 0; i < 4; ++i) anyl |= pass(j, i);
+        if (__builtin_amdgcn_ballot_w64(anyl)) {
+            const v4i32_t nx = *reinterpret_cast<const v4i32_t*>(p.nxt + size_t(t) * 16u + 4u * grp);
+            const uint32_t row0 = off + (t - tb) * 16u + 4u * grp;
 #pragma unroll
-                for (uint32_t dd = 0; dd < kMaxAttr; ++dd)
-                    if (dd < p.a)
-                        ok = ok && at[dd] >= p.lo[size_t(qr[i]) * p.a + dd] && at[dd] <= p.hi[size_t(qr[i]) * p.a + dd];
-                if (ok) {
-                    const uint32_t r = 4u * (lane >> 4) + i;
-                    const uint32_t slot = atomicAdd(&cnt[r], 1u);
-                    buf[r][slot] = (uint64_t(uint32_t(d[i])) << 32) | (off + lp);
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (pass(j, i)) {
+                        const uint32_t ql = 16u * j + col;
+                        const int32_t d = snq[ql] + nx[i] - 2 * (acc[j][i] - cmh[i]);
+                        const uint32_t slot = atomicAdd(&cnt[ql], 1u);
+                        buf[ql * kBfBufQ + slot] = (uint64_t(uint32_t(d)) << 32) | (row0 + i);
+                    }
+            wave_fence();
+            const uint32_t n = cnt[lane];
+            if (n) {
+                uint64_t kth = top[(K - 1) * kQB + lane];
+                for (uint32_t e = 0; e < n; ++e) {
+                    uint64_t c = buf[lane * kBfBufQ + e];
+                    if (c >= kth) continue;
+                    for (uint32_t k = 0; k < K; ++k) {
+                        const uint64_t v = top[k * kQB + lane];
+                        if (c < v) { top[k * kQB + lane] = c; c = v; }
+                    }
+                    kth = top[(K - 1) * kQB + lane];
+                }
+                cnt[lane] = 0;
+                if (kth != kKeySent && uint32_t(kth >> 32) < own_thr) {
+                    own_thr = uint32_t(kth >> 32);
+                    atomicMin(&p.gbound[own_q], own_thr);
+                    stp[lane] = acc_threshold(own_nq, own_thr);
                 }
             }
+            wave_fence();
+            reload_tp();
         }
-        wave_fence();
-        if (ballot(lane < 16 && cnt[lane] >= kBfMergeAt)) merge_all();
+        if ((t - it.t0) % kBfRefresh == kBfRefresh - 1) {
+            // other chunks of the same queries may have lowered their bounds
+            if (own_live) {
+                const uint32_t g = __hip_atomic_load(&p.gbound[own_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (g < own_thr) {
+                    own_thr = g;
+                    stp[lane] = acc_threshold(own_nq, own_thr);
+                }
+            }
+            wave_fence();
+            reload_tp();
+        }
     }
-    merge_all();
-    for (uint32_t idx = lane; idx < it.nq * K; idx += 64u) {
-        const uint32_t r = idx / K, j = idx % K;
-        const uint32_t q = p.pq[it.qbase + r];
-        const size_t slot = size_t(p.part_off[q]) + (size_t(p.ppos[it.qbase + r]) * p.maxch + it.chunk) * K;
-        p.part[slot + j] = top[r][j];
+    if (own_live) {
+        const size_t slot = size_t(p.part_off[own_q]) + (size_t(p.ppos[it.qbase + lane]) * p.maxch + it.chunk) * K;
+        for (uint32_t k = 0; k < K; ++k) p.part[slot + k] = top[k * kQB + lane];
     }
 }
 
@@ -1120,10 +1205,14 @@ __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
     }
 }
 
-// Index build: int8 tiles (see BfGemmArgs), |x'|^2 and attributes per tile slot.
+// Index build: int8 tiles (operand layout of BfGemmArgs::vt), |x'|^2 per tiled
+// point, and per tile the meta block [-floor(|x'|^2 / 2) x 16][attribute words
+// x 16] x AW, attribute word w of a point = (a_{2w} - base) | (a_{2w+1} - base) << 16
+// (padding points: 65535 in the low half, so they never pass a range).
 __global__ __launch_bounds__(64) void k_tile_i8(const float* vec, uint32_t D, const uint32_t* offset,
-                                               const uint32_t* tbase, const float* attrs, uint32_t a, uint32_t P,
-                                               int8_t* vt, int32_t* nxt, float* attrt) {
+                                               const uint32_t* tbase, const float* attrs, uint32_t a,
+                                               const int32_t* abase, uint32_t P, int8_t* vt, int32_t* nxt,
+                                               int32_t* meta) {
     const uint32_t t = blockIdx.x, lane = lane_id();
     uint32_t lo = 0, hi = P;   // cell c with tbase[c] <= t < tbase[c+1]
     while (hi - lo > 1) {
@@ -1137,6 +1226,7 @@ __global__ __launch_bounds__(64) void k_tile_i8(const float* vec, uint32_t D, co
     const bool valid = lp < csz;
     const size_t row = size_t(offset[c]) + lp;
     const uint32_t KS = D / 64u;
+    const uint32_t AW = (a + 1u) / 2u;
     for (uint32_t s = 0; s < KS; ++s) {
         int8_t* dst = vt + (size_t(t) * KS + s) * 1024u + lane * 16u;
         for (uint32_t j = 0; j < 16; ++j) {
@@ -1152,7 +1242,17 @@ __global__ __launch_bounds__(64) void k_tile_i8(const float* vec, uint32_t D, co
                 n += v * v;
             }
         nxt[size_t(t) * 16u + col] = n;
-        for (uint32_t d = 0; d < a; ++d) attrt[(size_t(t) * 16u + col) * a + d] = valid ? attrs[row * a + d] : 0.0f;
+        int32_t* mt = meta + size_t(t) * 16u * (1u + AW);
+        mt[col] = -(n >> 1);
+        for (uint32_t w = 0; w < AW; ++w) {
+            uint32_t word = 65535u;
+            if (valid) {
+                const uint32_t d0 = 2u * w, d1 = 2u * w + 1u;
+                word = uint32_t(int32_t(attrs[row * a + d0]) - abase[c * a + d0]);
+                if (d1 < a) word |= uint32_t(int32_t(attrs[row * a + d1]) - abase[c * a + d1]) << 16;
+            }
+            mt[16u * (1u + w) + col] = int32_t(word);
+        }
     }
 }
 
@@ -1253,14 +1353,22 @@ hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, hipStream_t 
 
 hipError_t launch_bf_i8(const BfGemmArgs& a, hipStream_t st) {
     if (!a.nitems) return hipSuccess;
+    if (a.K > kBfKMax || a.a < 1 || a.a > 4) return hipErrorInvalidValue;
     const uint32_t blocks = (a.nitems + 3) / 4;
-    switch (a.D / 64) {
-        case 1: hipLaunchKernelGGL(k_bf_i8<1>, dim3(blocks), dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL(k_bf_i8<2>, dim3(blocks), dim3(256), 0, st, a); break;
-        case 3: hipLaunchKernelGGL(k_bf_i8<3>, dim3(blocks), dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL(k_bf_i8<4>, dim3(blocks), dim3(256), 0, st, a); break;
+    const uint32_t AW = (a.a + 1) / 2;
+#define BF(KS, AW_) hipLaunchKernelGGL((k_bf_i8<KS, AW_>), dim3(blocks), dim3(256), 0, st, a)
+    switch ((a.D / 64) * 4 + AW) {
+        case 1 * 4 + 1: BF(1, 1); break;
+        case 2 * 4 + 1: BF(2, 1); break;
+        case 3 * 4 + 1: BF(3, 1); break;
+        case 4 * 4 + 1: BF(4, 1); break;
+        case 1 * 4 + 2: BF(1, 2); break;
+        case 2 * 4 + 2: BF(2, 2); break;
+        case 3 * 4 + 2: BF(3, 2); break;
+        case 4 * 4 + 2: BF(4, 2); break;
         default: return hipErrorInvalidValue;
     }
+#undef BF
     return hipGetLastError();
 }
 
@@ -1271,11 +1379,11 @@ hipError_t launch_bf_final(const BfFinalArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_tile_i8(const float* vec_cm, uint32_t D, const uint32_t* offset, const uint32_t* tbase,
-                          const float* attrs_cm, uint32_t a, uint32_t P, uint32_t ntiles, int8_t* vt, int32_t* nxt,
-                          float* attrt, hipStream_t st) {
+                          const float* attrs_cm, uint32_t a, const int32_t* abase, uint32_t P, uint32_t ntiles,
+                          int8_t* vt, int32_t* nxt, int32_t* meta, hipStream_t st) {
     if (!ntiles) return hipSuccess;
-    hipLaunchKernelGGL(k_tile_i8, dim3(ntiles), dim3(64), 0, st, vec_cm, D, offset, tbase, attrs_cm, a, P, vt, nxt,
-                       attrt);
+    hipLaunchKernelGGL(k_tile_i8, dim3(ntiles), dim3(64), 0, st, vec_cm, D, offset, tbase, attrs_cm, a, abase, P, vt,
+                       nxt, meta);
     return hipGetLastError();
 }
 
