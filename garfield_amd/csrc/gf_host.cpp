@@ -286,7 +286,7 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
             ix.tbase.upload(ix.tbase_h);
             ix.vt.alloc(size_t(nt) * (D / 64) * 1024);
             ix.nxt.alloc(size_t(nt) * 16);
-            ix.meta.alloc(size_t(nt) * 16 * (1 + (a + 1) / 2));
+            ix.meta.alloc(size_t(nt) * 16 * (2 + (a + 1) / 2));
             ix.abase.upload(abase);
             GF_HIP(gf::launch_tile_i8(vec_f32_dev, D, ix.offset.p, ix.tbase.p, ix.attrs.p, a, ix.abase.p, P, nt,
                                       ix.vt.p, ix.nxt.p, ix.meta.p, ix.stream));
@@ -679,7 +679,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                         const uint32_t nq = std::min(gf::kBfQB, nlist - qb);
                         items.push_back({c, base + qb, nq, ts, te, ch});
                         bf_ops += 2.0 * double(te - ts) * 16.0 * nq * ix->D;
-                        bf_bytes_gemm += double(te - ts) * (KS * 1024.0 + 64.0 * (1 + (ix->a + 1) / 2));
+                        bf_bytes_gemm += double(te - ts) * (KS * 1024.0 + 64.0 * (2 + (ix->a + 1) / 2));
                     }
                 }
             }

@@ -80,7 +80,7 @@ struct BfItem {
 struct BfGemmArgs {
     const int8_t* vt;          // tiled int8 vectors
     const int32_t* nxt;        // |x - 128|^2 per tiled point
-    const int32_t* meta;       // per tile: -floor(|x'|^2/2) x 16, then AW attribute words x 16
+    const int32_t* meta;       // per tile: -floor(|x'|^2/2) x 16, |x'|^2 x 16, AW attribute words x 16
     const int32_t* abase;      // P*a smallest attribute value of each cell
     const uint32_t* tbase;     // P+1 first tile of each cell
     const uint32_t* offset;    // P+1 first row of each cell

@@ -939,14 +939,16 @@ __global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P
 // same units (an empty range is [65534, 65534]); a point passes iff clamping
 // its packed word leaves it unchanged.  Survivors (rare once the threshold has
 // settled) go to a per-query LDS buffer; lane q of the wave owns query q of
-// the block and keeps its sorted top-K (distance, row) in LDS.  Thresholds
+// the block, keeps its sorted top-K (distance, row) in registers and merges
+// its buffer once some query's buffer holds kBfDrainAt entries.  Thresholds
 // tighten from the wave's own top-K and from a per-query global bound that
 // every chunk of the query lowers with atomicMin: a point farther than some
 // chunk's K-th distance cannot be in the final top-K.
 typedef int v4i32_t __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 constexpr uint32_t kQB = 64;        // queries per wave
-constexpr uint32_t kBfBufQ = 16;    // survivor slots per query (one tile adds <= 16)
+constexpr uint32_t kBfBufQ = 24;    // survivor slots per query
+constexpr uint32_t kBfDrainAt = 8;  // drain once a query holds this many (+ <= 16 per tile < 24)
 constexpr uint32_t kBfRefresh = 32; // tiles between reads of the global bounds
 constexpr uint64_t kKeySent = ~uint64_t(0);
 constexpr int32_t kTpOpen = INT32_MIN;  // acc threshold while fewer than K are known
@@ -982,13 +984,11 @@ __device__ __forceinline__ int32_t acc_threshold(int32_t nq, uint32_t thr) {
     return int32_t((int64_t(nq) - int64_t(thr) + 1) >> 1);   // ceil((nq - thr) / 2)
 }
 
-template <int KS, int AW>
+template <int KS, int AW, int KT>
 __global__ __launch_bounds__(256) void k_bf_i8(BfGemmArgs p) {
     __shared__ uint64_t s_buf[4][kQB * kBfBufQ];
-    __shared__ uint64_t s_top[4][kBfKMax * kQB];
     __shared__ uint32_t s_cnt[4][kQB];
     __shared__ int32_t s_tp[4][kQB];
-    __shared__ int32_t s_nq[4][kQB];
     __shared__ uint32_t s_bnd[4][2 * AW][kQB];
     const uint32_t wave = threadIdx.x >> 6, lane = lane_id();
     // XCD-aware order: workgroups go round-robin to the 8 XCDs, so XCD x gets
@@ -1001,20 +1001,21 @@ __global__ __launch_bounds__(256) void k_bf_i8(BfGemmArgs p) {
     const BfItem it = p.items[item_id];
     const uint32_t K = p.K;
     uint64_t* buf = s_buf[wave];
-    uint64_t* top = s_top[wave];
     uint32_t* cnt = s_cnt[wave];
     int32_t* stp = s_tp[wave];
-    int32_t* snq = s_nq[wave];
     const uint32_t cell = it.cell;
 
-    // Owner state: lane q owns query q of the block.
+    // Owner state: lane q owns query q of the block; its sorted top-K of
+    // (distance << 32 | row) keys lives in registers.
     const bool own_live = lane < it.nq;
     const uint32_t own_q = p.pq[it.qbase + (own_live ? lane : 0u)];
     const int32_t own_nq = p.nq[own_q];
     uint32_t own_thr = own_live ? p.gbound[own_q] : 0u;
-    for (uint32_t k = 0; k < K; ++k) top[k * kQB + lane] = kKeySent;
+    uint64_t tk[KT];
+#pragma unroll
+    for (int k = 0; k < KT; ++k) tk[k] = kKeySent;
+    uint64_t kth = kKeySent;
     cnt[lane] = 0;
-    snq[lane] = own_nq;
     stp[lane] = own_live ? acc_threshold(own_nq, own_thr) : INT32_MAX;
 #pragma unroll
     for (int w = 0; w < AW; ++w) {
@@ -1054,24 +1055,64 @@ __global__ __launch_bounds__(256) void k_bf_i8(BfGemmArgs p) {
 
     const uint32_t tb = p.tbase[cell];
     const uint32_t off = p.offset[cell];
-    constexpr uint32_t kMeta = 16u * (1u + AW);
+    constexpr uint32_t kMeta = 16u * (2u + AW);
     auto reload_tp = [&]() {
 #pragma unroll
         for (int j = 0; j < 4; ++j) tp[j] = stp[16u * j + col];
     };
+    auto set_thr = [&](uint32_t thr) {
+        own_thr = thr;
+        stp[lane] = acc_threshold(own_nq, own_thr);
+    };
+    // Owner: merge the buffered survivors of its query, publish the new
+    // threshold and lower the query's global bound.
+    auto drain = [&]() {
+        wave_fence();
+        const uint32_t n = cnt[lane];
+        if (n) {
+            uint64_t nxt = buf[lane * kBfBufQ];
+            for (uint32_t e = 0; e < n; ++e) {
+                const uint64_t cur = nxt;
+                if (e + 1 < n) nxt = buf[lane * kBfBufQ + e + 1];
+                const int32_t d = own_nq + int32_t(uint32_t(cur >> 32));
+                uint64_t c = (uint64_t(uint32_t(d)) << 32) | uint32_t(cur);
+                if (c < kth) {
+#pragma unroll
+                    for (int k = 0; k < KT; ++k) {
+                        const bool lt = c < tk[k];
+                        const uint64_t v = tk[k];
+                        tk[k] = lt ? c : v;
+                        c = lt ? v : c;
+                    }
+#pragma unroll
+                    for (int k = 0; k < KT; ++k)
+                        if (uint32_t(k) == K - 1) kth = tk[k];
+                }
+            }
+            cnt[lane] = 0;
+            if (kth != kKeySent && uint32_t(kth >> 32) < own_thr) {
+                set_thr(uint32_t(kth >> 32));
+                atomicMin(&p.gbound[own_q], own_thr);
+            }
+        }
+        wave_fence();
+        reload_tp();
+    };
 
     // Operands of tile t + 1 are loaded while tile t is computed.
-    v4i32_t A[KS], mh, ma[AW];
+    v4i32_t A[KS], mh, mn, ma[AW];
     auto load_tile = [&](uint32_t t) {
         const v4i32_t* vp = reinterpret_cast<const v4i32_t*>(p.vt + size_t(t) * KS * 1024u) + lane;
         const int32_t* mt = p.meta + size_t(t) * kMeta;
 #pragma unroll
         for (int s = 0; s < KS; ++s) A[s] = vp[s * 64];
         mh = *reinterpret_cast<const v4i32_t*>(mt + 4u * grp);
+        mn = *reinterpret_cast<const v4i32_t*>(mt + 16u + 4u * grp);
 #pragma unroll
-        for (int w = 0; w < AW; ++w) ma[w] = *reinterpret_cast<const v4i32_t*>(mt + 16u * (1 + w) + 4u * grp);
+        for (int w = 0; w < AW; ++w) ma[w] = *reinterpret_cast<const v4i32_t*>(mt + 16u * (2 + w) + 4u * grp);
     };
     load_tile(it.t0);
+    uint32_t gb_next = 0xFFFFFFFFu;   // global bound loaded one refresh period earlier
     for (uint32_t t = it.t0; t < it.t1; ++t) {
         v4i32_t acc[4];
 #pragma unroll
@@ -1080,7 +1121,7 @@ __global__ __launch_bounds__(256) void k_bf_i8(BfGemmArgs p) {
 #pragma unroll
             for (int s = 1; s < KS; ++s) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[s], B[j][s], acc[j], 0, 0, 0);
         }
-        const v4i32_t cmh = mh, cma0 = ma[0], cma1 = ma[AW - 1];
+        const v4i32_t cmh = mh, cmn = mn, cma0 = ma[0], cma1 = ma[AW - 1];
         if (t + 1 < it.t1) load_tile(t + 1);
         // Branch-free test of one (point i, query column j) pair.
         auto pass = [&](int j, int i) {
@@ -1099,57 +1140,41 @@ __global__ __launch_bounds__(256) void k_bf_i8(BfGemmArgs p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) anyl |= pass(j, i);
         if (__builtin_amdgcn_ballot_w64(anyl)) {
-            const v4i32_t nx = *reinterpret_cast<const v4i32_t*>(p.nxt + size_t(t) * 16u + 4u * grp);
+            // Append: the owner adds |q'|^2 to nx - 2 q'.x' later.
             const uint32_t row0 = off + (t - tb) * 16u + 4u * grp;
+            bool full = false;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     if (pass(j, i)) {
                         const uint32_t ql = 16u * j + col;
-                        const int32_t d = snq[ql] + nx[i] - 2 * (acc[j][i] - cmh[i]);
+                        const int32_t v = cmn[i] - 2 * (acc[j][i] - cmh[i]);
                         const uint32_t slot = atomicAdd(&cnt[ql], 1u);
-                        buf[ql * kBfBufQ + slot] = (uint64_t(uint32_t(d)) << 32) | (row0 + i);
+                        buf[ql * kBfBufQ + slot] = (uint64_t(uint32_t(v)) << 32) | (row0 + i);
+                        full |= slot + 1u >= kBfDrainAt;
                     }
-            wave_fence();
-            const uint32_t n = cnt[lane];
-            if (n) {
-                uint64_t kth = top[(K - 1) * kQB + lane];
-                for (uint32_t e = 0; e < n; ++e) {
-                    uint64_t c = buf[lane * kBfBufQ + e];
-                    if (c >= kth) continue;
-                    for (uint32_t k = 0; k < K; ++k) {
-                        const uint64_t v = top[k * kQB + lane];
-                        if (c < v) { top[k * kQB + lane] = c; c = v; }
-                    }
-                    kth = top[(K - 1) * kQB + lane];
-                }
-                cnt[lane] = 0;
-                if (kth != kKeySent && uint32_t(kth >> 32) < own_thr) {
-                    own_thr = uint32_t(kth >> 32);
-                    atomicMin(&p.gbound[own_q], own_thr);
-                    stp[lane] = acc_threshold(own_nq, own_thr);
-                }
-            }
-            wave_fence();
-            reload_tp();
+            if (__builtin_amdgcn_ballot_w64(full)) drain();
         }
         if ((t - it.t0) % kBfRefresh == kBfRefresh - 1) {
-            // other chunks of the same queries may have lowered their bounds
-            if (own_live) {
-                const uint32_t g = __hip_atomic_load(&p.gbound[own_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (g < own_thr) {
-                    own_thr = g;
-                    stp[lane] = acc_threshold(own_nq, own_thr);
-                }
+            // Other chunks of the same queries may have lowered their bounds;
+            // the value used now was loaded one period ago (no wait on it).
+            const bool lower = own_live && gb_next < own_thr;
+            if (__builtin_amdgcn_ballot_w64(lower)) {
+                if (lower) set_thr(gb_next);
+                wave_fence();
+                reload_tp();
             }
-            wave_fence();
-            reload_tp();
+            gb_next = own_live ? __hip_atomic_load(&p.gbound[own_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                               : 0xFFFFFFFFu;
         }
     }
+    drain();
     if (own_live) {
         const size_t slot = size_t(p.part_off[own_q]) + (size_t(p.ppos[it.qbase + lane]) * p.maxch + it.chunk) * K;
-        for (uint32_t k = 0; k < K; ++k) p.part[slot + k] = top[k * kQB + lane];
+#pragma unroll
+        for (int k = 0; k < KT; ++k)
+            if (uint32_t(k) < K) p.part[slot + k] = tk[k];
     }
 }
 
@@ -1206,8 +1231,8 @@ __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
 }
 
 // Index build: int8 tiles (operand layout of BfGemmArgs::vt), |x'|^2 per tiled
-// point, and per tile the meta block [-floor(|x'|^2 / 2) x 16][attribute words
-// x 16] x AW, attribute word w of a point = (a_{2w} - base) | (a_{2w+1} - base) << 16
+// point, and per tile the meta block [-floor(|x'|^2 / 2) x 16][|x'|^2 x 16]
+// [attribute words x 16] x AW, attribute word w of a point = (a_{2w} - base) | (a_{2w+1} - base) << 16
 // (padding points: 65535 in the low half, so they never pass a range).
 __global__ __launch_bounds__(64) void k_tile_i8(const float* vec, uint32_t D, const uint32_t* offset,
                                                const uint32_t* tbase, const float* attrs, uint32_t a,
@@ -1242,8 +1267,9 @@ __global__ __launch_bounds__(64) void k_tile_i8(const float* vec, uint32_t D, co
                 n += v * v;
             }
         nxt[size_t(t) * 16u + col] = n;
-        int32_t* mt = meta + size_t(t) * 16u * (1u + AW);
+        int32_t* mt = meta + size_t(t) * 16u * (2u + AW);
         mt[col] = -(n >> 1);
+        mt[16u + col] = n;
         for (uint32_t w = 0; w < AW; ++w) {
             uint32_t word = 65535u;
             if (valid) {
@@ -1251,7 +1277,7 @@ __global__ __launch_bounds__(64) void k_tile_i8(const float* vec, uint32_t D, co
                 word = uint32_t(int32_t(attrs[row * a + d0]) - abase[c * a + d0]);
                 if (d1 < a) word |= uint32_t(int32_t(attrs[row * a + d1]) - abase[c * a + d1]) << 16;
             }
-            mt[16u * (1u + w) + col] = int32_t(word);
+            mt[16u * (2u + w) + col] = int32_t(word);
         }
     }
 }
@@ -1356,7 +1382,13 @@ hipError_t launch_bf_i8(const BfGemmArgs& a, hipStream_t st) {
     if (a.K > kBfKMax || a.a < 1 || a.a > 4) return hipErrorInvalidValue;
     const uint32_t blocks = (a.nitems + 3) / 4;
     const uint32_t AW = (a.a + 1) / 2;
-#define BF(KS, AW_) hipLaunchKernelGGL((k_bf_i8<KS, AW_>), dim3(blocks), dim3(256), 0, st, a)
+#define BF(KS, AW_)                                                                     \
+    do {                                                                                \
+        if (a.K <= 10)                                                                  \
+            hipLaunchKernelGGL((k_bf_i8<KS, AW_, 10>), dim3(blocks), dim3(256), 0, st, a); \
+        else                                                                            \
+            hipLaunchKernelGGL((k_bf_i8<KS, AW_, 16>), dim3(blocks), dim3(256), 0, st, a); \
+    } while (0)
     switch ((a.D / 64) * 4 + AW) {
         case 1 * 4 + 1: BF(1, 1); break;
         case 2 * 4 + 1: BF(2, 1); break;
