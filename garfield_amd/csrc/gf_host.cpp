@@ -94,13 +94,21 @@ struct gf_index {
     DevBuf<uint32_t> tile_cell, tile_row0, tile_n;
     DevBuf<uint16_t> centres;
     uint32_t ntiles = 0;
-    // Query-batch MFMA brute force (integer data in [0, 255], D a multiple of
-    // 64, at most 4 integer attributes spread by less than 65534 in each cell).
+    // Sub-cells (integer attributes spread by less than 65534 inside every
+    // cell, a <= 4): each cell is split by a rank grid of S bins per
+    // attribute; tiles of 16 points are grouped by sub-cell and carry the
+    // cell-major row and the packed 16-bit attribute offsets of each point.
+    bool sub = false;
+    uint32_t AW = 0, NS = 0, ntile = 0;
+    std::vector<uint32_t> ssize_h, stile_h;
+    DevBuf<uint32_t> sbase, scell, ssize, stile, tmeta;
+    DevBuf<int32_t> sbox, abase;
+    // Query-batch MFMA brute force (additionally: vectors integers in
+    // [0, 255], D a multiple of 64 up to 256): int8 tiles and norms.
     bool i8 = false;
     DevBuf<int8_t> vt;
-    DevBuf<int32_t> nxt, meta, abase;
-    DevBuf<uint32_t> tbase;
-    std::vector<uint32_t> tbase_h;
+    DevBuf<int32_t> tnorm;
+    int ncu = 0;
     ~gf_index() {
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -108,7 +116,8 @@ struct gf_index {
         return vec.bytes() + attrs.bytes() + l_q.bytes() + r_q.bytes() + cnorm.bytes() + graph.bytes() +
                cross.bytes() + offset.bytes() + gidx.bytes() + lrow.bytes() + grid.bytes() + doff.bytes() +
                hist.bytes() + tile_cell.bytes() + tile_row0.bytes() + tile_n.bytes() + centres.bytes() +
-               vt.bytes() + nxt.bytes() + meta.bytes() + abase.bytes() + tbase.bytes();
+               sbase.bytes() + scell.bytes() + ssize.bytes() + stile.bytes() + tmeta.bytes() + sbox.bytes() +
+               abase.bytes() + vt.bytes() + tnorm.bytes();
     }
 };
 
@@ -119,7 +128,9 @@ struct gf_batch {
     bool i8 = false;
     DevBuf<int8_t> q8;
     DevBuf<int32_t> nq;
-    DevBuf<uint32_t> pq, ppos, part_off, bfq;
+    // brute-force schedule of stage C (tot: device totals and fit flags)
+    DevBuf<uint32_t> tot;
+    DevBuf<uint32_t> bcnt, bstart, pcnt, bq, nsub, part_off, icnt, ioff, bfq;
     DevBuf<gf::BfItem> items;
     DevBuf<uint64_t> part;
     DevBuf<float> qf32, qnorm, lo, hi, cdist, out_dist;
@@ -168,6 +179,97 @@ struct Timer {
 };
 
 void set_device(const gf_index* ix) { GF_HIP(hipSetDevice(ix->device)); }
+
+// Sub-cells of every cell, built when all attributes are integers whose
+// spread inside each cell is below 65534 and a <= 4 (otherwise ix.sub stays
+// false and stage A / the brute force use the per-cell kernels).  A cell of n
+// points gets S = round((n / 1024)^(1/a)) bins per attribute (S^a <= 4096):
+// bin of a point = rank of its value among the cell's (ties by row) * S / n,
+// sub-cell = row-major bin tuple.  Tiles list each sub-cell's points in
+// ascending row order, padded to 16 (row 0xFFFFFFFF, low attribute half
+// 65535, which no range accepts).
+void build_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, const std::vector<uint32_t>& size,
+                    gf_index& ix) {
+    const uint32_t a = ix.a, P = ix.P;
+    if (a > 4) return;
+    std::vector<int32_t> abase(size_t(P) * a, 0);
+    for (uint32_t c = 0; c < P; ++c)
+        for (uint32_t d = 0; d < a; ++d) {
+            double mn = 0.0, mx = 0.0;
+            for (uint32_t r = ix.offset_h[c]; r < ix.offset_h[c + 1]; ++r) {
+                const double x = h.attrs[size_t(gidx[r]) * a + d];
+                if (!(x == std::floor(x) && x >= -2147483648.0 && x < 2147483648.0)) return;
+                mn = r == ix.offset_h[c] ? x : std::min(mn, x);
+                mx = r == ix.offset_h[c] ? x : std::max(mx, x);
+            }
+            if (mx - mn > 65533.0) return;
+            abase[size_t(c) * a + d] = int32_t(mn);
+        }
+    const uint32_t AW = (a + 1) / 2, MW = 16 * (1 + AW);
+    std::vector<uint32_t> sbase(P + 1, 0), scell, ssize, stile, tmeta;
+    std::vector<int32_t> sbox;
+    auto attr = [&](uint32_t r, uint32_t d) { return int32_t(h.attrs[size_t(gidx[r]) * a + d]); };
+    for (uint32_t c = 0; c < P; ++c) {
+        const uint32_t off = ix.offset_h[c], n = size[c];
+        uint32_t S = n ? std::max<uint32_t>(1u, uint32_t(std::lround(std::pow(n / 1024.0, 1.0 / a)))) : 1u;
+        while (S > 1 && std::pow(double(S), double(a)) > 4096.0) --S;
+        uint32_t nsc = 1;
+        for (uint32_t d = 0; d < a; ++d) nsc *= S;
+        std::vector<uint32_t> sid(n, 0), ord(n);
+        for (uint32_t d = 0; d < a; ++d) {
+            for (uint32_t i = 0; i < n; ++i) ord[i] = i;
+            std::stable_sort(ord.begin(), ord.end(),
+                             [&](uint32_t x, uint32_t y) { return attr(off + x, d) < attr(off + y, d); });
+            for (uint32_t k = 0; k < n; ++k) sid[ord[k]] = sid[ord[k]] * S + uint32_t(uint64_t(k) * S / n);
+        }
+        std::vector<std::vector<uint32_t>> members(nsc);
+        for (uint32_t i = 0; i < n; ++i) members[sid[i]].push_back(off + i);
+        for (uint32_t k = 0; k < nsc; ++k) {
+            const auto& m = members[k];
+            scell.push_back(c);
+            ssize.push_back(uint32_t(m.size()));
+            stile.push_back(uint32_t(tmeta.size() / MW));
+            for (uint32_t d = 0; d < a; ++d) {
+                int32_t mn = INT32_MAX, mx = INT32_MIN;
+                for (uint32_t r : m) { mn = std::min(mn, attr(r, d)); mx = std::max(mx, attr(r, d)); }
+                sbox.push_back(mn);
+                sbox.push_back(mx);
+            }
+            for (size_t t0 = 0; t0 < m.size(); t0 += 16) {
+                const size_t base = tmeta.size();
+                tmeta.resize(base + MW, 0);
+                for (uint32_t j = 0; j < 16; ++j) {
+                    const bool valid = t0 + j < m.size();
+                    const uint32_t r = valid ? m[t0 + j] : 0xFFFFFFFFu;
+                    tmeta[base + j] = r;
+                    for (uint32_t w = 0; w < AW; ++w) {
+                        uint32_t word = 65535u;
+                        if (valid) {
+                            word = uint32_t(attr(r, 2 * w) - abase[size_t(c) * a + 2 * w]);
+                            if (2 * w + 1 < a) word |= uint32_t(attr(r, 2 * w + 1) - abase[size_t(c) * a + 2 * w + 1]) << 16;
+                        }
+                        tmeta[base + 16 * (1 + w) + j] = word;
+                    }
+                }
+            }
+        }
+        sbase[c + 1] = sbase[c] + nsc;
+    }
+    stile.push_back(uint32_t(tmeta.size() / MW));
+    ix.AW = AW;
+    ix.NS = sbase[P];
+    ix.ntile = stile.back();
+    ix.ssize_h = ssize;
+    ix.stile_h = stile;
+    ix.abase.upload(abase);
+    ix.sbase.upload(sbase);
+    ix.scell.upload(scell);
+    ix.ssize.upload(ssize);
+    ix.stile.upload(stile);
+    ix.sbox.upload(sbox);
+    ix.tmeta.upload(tmeta);
+    ix.sub = true;
+}
 
 void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix) {
     GF_REQUIRE(h.N > 0 && h.D > 0, GF_E_ARG, "N and D must be positive");
@@ -232,6 +334,8 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
     // All ids are validated; from here on the device is used.
     GF_HIP(hipSetDevice(ix.device));
     GF_HIP(hipStreamCreateWithFlags(&ix.stream, hipStreamNonBlocking));
+    GF_HIP(hipDeviceGetAttribute(&ix.ncu, hipDeviceAttributeMultiprocessorCount, ix.device));
+    ix.ncu = std::max(ix.ncu, 1);
     ix.cross.upload(cross_cm);
     std::vector<uint32_t>().swap(cross_cm);
     ix.graph.upload(h.cell_graphs, size_t(N) * R);
@@ -261,35 +365,14 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
             ix.rowbytes = D * 2;
             vec_f32_dev = tmp.p;
         }
-        // Integer-valued data in [0, 255] and integer attributes packable as
-        // 16-bit offsets from a per-cell base: build the MFMA brute-force tiles.
-        bool ints = ix.vdtype == GF_VEC_F32 && D % 64 == 0 && D <= 256 && a >= 1 && a <= 4;
+        build_subcells(h, gidx, size, ix);
+        // Integer-valued data in [0, 255]: int8 tiles of the MFMA brute force.
+        bool ints = ix.sub && ix.vdtype == GF_VEC_F32 && D % 64 == 0 && D <= 256;
         for (size_t i = 0; ints && i < v.size(); ++i) ints = v[i] >= 0.0f && v[i] <= 255.0f && v[i] == std::floor(v[i]);
-        std::vector<int32_t> abase(size_t(P) * a, 0);
-        for (uint32_t c = 0; ints && c < P; ++c)
-            for (uint32_t d = 0; ints && d < a; ++d) {
-                double mn = 0.0, mx = 0.0;
-                for (uint32_t r = ix.offset_h[c]; r < ix.offset_h[c + 1]; ++r) {
-                    const double x = h.attrs[size_t(gidx[r]) * a + d];
-                    ints = ints && x == std::floor(x) && x >= -2147483648.0 && x < 2147483648.0;
-                    mn = r == ix.offset_h[c] ? x : std::min(mn, x);
-                    mx = r == ix.offset_h[c] ? x : std::max(mx, x);
-                }
-                ints = ints && mx - mn <= 65533.0;
-                abase[size_t(c) * a + d] = int32_t(mn);
-            }
         if (ints) {
-            ix.tbase_h.assign(P + 1, 0);
-            for (uint32_t c = 0; c < P; ++c)
-                ix.tbase_h[c + 1] = ix.tbase_h[c] + (size[c] + gf::kBfTile - 1) / gf::kBfTile;
-            const uint32_t nt = ix.tbase_h[P];
-            ix.tbase.upload(ix.tbase_h);
-            ix.vt.alloc(size_t(nt) * (D / 64) * 1024);
-            ix.nxt.alloc(size_t(nt) * 16);
-            ix.meta.alloc(size_t(nt) * 16 * (2 + (a + 1) / 2));
-            ix.abase.upload(abase);
-            GF_HIP(gf::launch_tile_i8(vec_f32_dev, D, ix.offset.p, ix.tbase.p, ix.attrs.p, a, ix.abase.p, P, nt,
-                                      ix.vt.p, ix.nxt.p, ix.meta.p, ix.stream));
+            ix.vt.alloc(size_t(ix.ntile) * (D / 64) * 1024);
+            ix.tnorm.alloc(size_t(ix.ntile) * 32);
+            GF_HIP(gf::launch_tile_i8(vec_f32_dev, D, ix.tmeta.p, ix.AW, ix.ntile, ix.vt.p, ix.tnorm.p, ix.stream));
             ix.i8 = true;
         }
         GF_HIP(hipStreamSynchronize(ix.stream));
@@ -359,6 +442,14 @@ void ensure_out(gf_batch& b, uint32_t K) {
     const size_t n = size_t(b.Q) * K;
     if (b.out_ids.n < n) { b.out_ids.alloc(n); b.out_dist.alloc(n); }
     if (b.counters.n < size_t(b.Q) * GF_NCOUNTERS) b.counters.alloc(size_t(b.Q) * GF_NCOUNTERS);
+}
+
+gf::SubArgs sub_args(const gf_index& ix) {
+    gf::SubArgs sa{};
+    sa.sbase = ix.sbase.p; sa.scell = ix.scell.p; sa.ssize = ix.ssize.p; sa.stile = ix.stile.p;
+    sa.sbox = ix.sbox.p; sa.tmeta = ix.tmeta.p; sa.abase = ix.abase.p;
+    sa.a = ix.a; sa.AW = ix.AW; sa.P = ix.P; sa.NS = ix.NS;
+    return sa;
 }
 
 uint32_t next_pow2(uint32_t x) {
@@ -498,10 +589,13 @@ gf_status gf_batch_create(gf_index* ix, const float* queries, uint32_t Q, const 
         b->counts.alloc(Q);
         b->little.alloc(Q);
         b->selcount.alloc(Q);
-        b->cellq.alloc(size_t(Q) * ix->P);
-        b->ccount.alloc(ix->P);
-        b->cstart.alloc(ix->P);
-        b->cfill.alloc(ix->P);
+        b->tot.alloc(8);
+        if (!ix->sub) {
+            b->cellq.alloc(size_t(Q) * ix->P);
+            b->ccount.alloc(ix->P);
+            b->cstart.alloc(ix->P);
+            b->cfill.alloc(ix->P);
+        }
         GF_HIP(hipStreamSynchronize(ix->stream));
         *out = b.release();
     });
@@ -522,18 +616,26 @@ gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms) {
         set_device(ix);
         hipStream_t st = ix->stream;
         Timer t(st);
-        GF_HIP(gf::launch_cells(b->Q, ix->a, b->lo.p, b->hi.p, ix->grid.p, ix->doff.p, ix->l_q.p, ix->r_q.p,
-                                ix->P, ix->offset.p, b->cells.p, b->counts.p, st));
-        GF_HIP(hipMemsetAsync(b->ccount.p, 0, ix->P * sizeof(uint32_t), st));
-        GF_HIP(hipMemsetAsync(b->cfill.p, 0, ix->P * sizeof(uint32_t), st));
+        GF_HIP(gf::launch_cells(b->Q, ix->a, b->lo.p, b->hi.p, ix->grid.p, ix->doff.p, ix->l_q.p, ix->r_q.p, ix->P,
+                                ix->offset.p, b->cells.p, b->counts.p, st));
         GF_HIP(hipMemsetAsync(b->selcount.p, 0, b->Q * sizeof(uint32_t), st));
-        GF_HIP(gf::launch_cellq_count(b->Q, ix->P, b->cells.p, b->counts.p, b->ccount.p, st));
-        GF_HIP(gf::launch_scan_small(b->ccount.p, ix->P, b->cstart.p, st));
-        GF_HIP(gf::launch_cellq_fill(b->Q, ix->P, b->cells.p, b->counts.p, b->cstart.p, b->cfill.p,
-                                     b->cellq.p, st));
-        GF_HIP(gf::launch_selcount(ix->ntiles, ix->tile_cell.p, ix->tile_row0.p, ix->tile_n.p, ix->attrs.p,
-                                   ix->a, b->cstart.p, b->ccount.p, b->cellq.p, b->lo.p, b->hi.p,
-                                   b->selcount.p, st));
+        if (ix->sub) {
+            // Sub-cells inside a range count whole; partially covered ones are
+            // scanned exactly.
+            gf::SubSelArgs sl{};
+            sl.sa = sub_args(*ix);
+            sl.Q = b->Q; sl.lo = b->lo.p; sl.hi = b->hi.p; sl.selcount = b->selcount.p;
+            GF_HIP(gf::launch_subsel(sl, st));
+        } else {
+            GF_HIP(hipMemsetAsync(b->ccount.p, 0, ix->P * sizeof(uint32_t), st));
+            GF_HIP(hipMemsetAsync(b->cfill.p, 0, ix->P * sizeof(uint32_t), st));
+            GF_HIP(gf::launch_cellq_count(b->Q, ix->P, b->cells.p, b->counts.p, b->ccount.p, st));
+            GF_HIP(gf::launch_scan_small(b->ccount.p, ix->P, b->cstart.p, st));
+            GF_HIP(gf::launch_cellq_fill(b->Q, ix->P, b->cells.p, b->counts.p, b->cstart.p, b->cfill.p, b->cellq.p,
+                                         st));
+            GF_HIP(gf::launch_selcount(ix->ntiles, ix->tile_cell.p, ix->tile_row0.p, ix->tile_n.p, ix->attrs.p, ix->a,
+                                       b->cstart.p, b->ccount.p, b->cellq.p, b->lo.p, b->hi.p, b->selcount.p, st));
+        }
         GF_HIP(gf::launch_route(b->Q, ix->N, prefilter, b->selcount.p, b->counts.p, b->little.p, st));
         const double el = t.stop();
         if (ms) *ms = el;
@@ -643,68 +745,59 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         a.Lpad = Lpad;
 
         // Brute-force route on MFMA when vectors and queries are int8-exact:
-        // work items of (cell, 64 queries, chunk of the cell's tiles), ordered
-        // chunk-major so that the query blocks of one chunk run together.
+        // work items of (sub-cell, <= 64 queries whose range reaches it),
+        // scheduled on the device.
         const bool gemm = ix->i8 && b->i8 && !bq.empty() && K <= gf::kBfKMax;
-        double bf_ops = 0.0, bf_bytes_gemm = 0.0;
-        gf::BfGemmArgs ga{};
-        gf::BfFinalArgs fa{};
+        const uint32_t NS = ix->NS;
         if (gemm) {
-            const uint32_t P = ix->P;
-            std::vector<uint32_t> cellsh(size_t(Q) * P);
-            GF_HIP(hipMemcpy(cellsh.data(), b->cells.p, cellsh.size() * 4, hipMemcpyDeviceToHost));
-            uint32_t maxch = 0;
-            for (uint32_t c = 0; c < P; ++c)
-                maxch = std::max(maxch, (ix->tbase_h[c + 1] - ix->tbase_h[c] + gf::kBfChunk - 1) / gf::kBfChunk);
-            std::vector<std::vector<std::pair<uint32_t, uint32_t>>> lists(P);
-            std::vector<uint32_t> poff(Q, 0);
-            uint64_t tot = 0;
-            for (uint32_t q : bq) {
-                poff[q] = uint32_t(tot);
-                tot += uint64_t(cnt[q]) * maxch * K;
-                for (uint32_t i = 0; i < cnt[q]; ++i) lists[cellsh[size_t(q) * P + i]].push_back({q, i});
-            }
-            GF_REQUIRE(tot < (1ull << 32), GF_E_UNSUPPORTED, "brute-force batch too large");
-            std::vector<uint32_t> pq, ppos;
-            std::vector<gf::BfItem> items;
-            const uint32_t KS = ix->D / 64;
-            for (uint32_t c = 0; c < P; ++c) {
-                const uint32_t base = uint32_t(pq.size());
-                const uint32_t nlist = uint32_t(lists[c].size());
-                for (auto& pr : lists[c]) { pq.push_back(pr.first); ppos.push_back(pr.second); }
-                const uint32_t t0c = ix->tbase_h[c], t1c = ix->tbase_h[c + 1];
-                for (uint32_t ch = 0; t0c + ch * gf::kBfChunk < t1c; ++ch) {
-                    const uint32_t ts = t0c + ch * gf::kBfChunk, te = std::min(t1c, ts + gf::kBfChunk);
-                    for (uint32_t qb = 0; qb < nlist; qb += gf::kBfQB) {
-                        const uint32_t nq = std::min(gf::kBfQB, nlist - qb);
-                        items.push_back({c, base + qb, nq, ts, te, ch});
-                        bf_ops += 2.0 * double(te - ts) * 16.0 * nq * ix->D;
-                        bf_bytes_gemm += double(te - ts) * (KS * 1024.0 + 64.0 * (2 + (ix->a + 1) / 2));
-                    }
-                }
-            }
-            b->pq.upload(pq);
-            b->ppos.upload(ppos);
-            b->items.upload(items);
-            b->part_off.upload(poff);
             b->bfq.upload(bq);
-            if (b->part.n < tot) b->part.alloc(tot);
-            GF_HIP(hipMemsetAsync(b->part.p, 0xFF, tot * sizeof(uint64_t), st));
+            if (!b->bcnt.n) {
+                b->bcnt.alloc(NS); b->bstart.alloc(NS); b->icnt.alloc(NS); b->ioff.alloc(NS);
+                b->nsub.alloc(Q); b->part_off.alloc(Q); b->pcnt.alloc(Q);
+            }
+            if (!b->bq.n) {
+                const size_t cap = size_t(Q) * 64;
+                b->bq.alloc(cap); b->part.alloc(cap * K);
+                b->items.alloc(cap / gf::kBfQB + NS + 1);
+            }
+            if (b->part.n < b->bq.n * K) b->part.alloc(b->bq.n * K);
             if (b->gbound.n < Q) b->gbound.alloc(Q);
-            GF_HIP(hipMemsetAsync(b->gbound.p, 0xFF, size_t(Q) * sizeof(uint32_t), st));
-            ga.vt = ix->vt.p; ga.nxt = ix->nxt.p; ga.meta = ix->meta.p; ga.abase = ix->abase.p;
-            ga.tbase = ix->tbase.p; ga.gbound = b->gbound.p;
-            ga.offset = ix->offset.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p; ga.hi = b->hi.p;
-            ga.items = b->items.p; ga.nitems = uint32_t(items.size()); ga.pq = b->pq.p; ga.ppos = b->ppos.p;
-            ga.part_off = b->part_off.p; ga.part = b->part.p; ga.maxch = maxch; ga.K = K; ga.a = ix->a;
-            ga.D = ix->D;
-            fa.bfq = b->bfq.p; fa.nbf = uint32_t(bq.size()); fa.part_off = b->part_off.p; fa.part = b->part.p;
-            fa.counts = b->counts.p; fa.cells = b->cells.p; fa.offset = ix->offset.p;
-            fa.selcount = b->selcount.p; fa.gidx = ix->gidx.p; fa.out_ids = b->out_ids.p;
-            fa.out_dist = b->out_dist.p; fa.counters = b->counters.p; fa.maxch = maxch; fa.K = K; fa.P = P;
-            // final merge reads every partial list and writes the results
-            bf_bytes_gemm += double(tot) * 8.0 + double(bq.size()) * K * 8.0;
         }
+        auto launch_gemm = [&]() {
+            gf::BfSchedArgs sc{};
+            sc.sa = sub_args(*ix);
+            sc.Q = Q; sc.postfilter = opts->postfilter; sc.counts = b->counts.p;
+            sc.little = b->little.p; sc.lo = b->lo.p; sc.hi = b->hi.p; sc.nsub = b->nsub.p; sc.bcnt = b->bcnt.p;
+            sc.bstart = b->bstart.p; sc.bq = b->bq.p;
+            sc.ok = b->tot.p + 3;
+            GF_HIP(hipMemsetAsync(b->nsub.p, 0, size_t(Q) * sizeof(uint32_t), st));
+            GF_HIP(hipMemsetAsync(b->pcnt.p, 0, size_t(Q) * sizeof(uint32_t), st));
+            GF_HIP(hipMemsetAsync(b->gbound.p, 0xFF, size_t(Q) * sizeof(uint32_t), st));
+            GF_HIP(gf::launch_bfsched(sc, false, st));
+            GF_HIP(gf::launch_scan_small(b->bcnt.p, NS, b->bstart.p, st));
+            GF_HIP(gf::launch_scan_small(b->nsub.p, Q, b->part_off.p, st));
+            GF_HIP(gf::launch_total(b->nsub.p, b->part_off.p, Q, uint32_t(std::min<size_t>(b->bq.n, UINT32_MAX)), K,
+                                    b->part.n, b->tot.p + 2, st));
+            GF_HIP(gf::launch_bfsched(sc, true, st));
+            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bstart.p, NS, b->icnt.p, b->ioff.p, b->items.p, b->tot.p + 4,
+                                      b->tot.p + 3, false, st));
+            GF_HIP(gf::launch_scan_small(b->icnt.p, NS, b->ioff.p, st));
+            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bstart.p, NS, b->icnt.p, b->ioff.p, b->items.p, b->tot.p + 4,
+                                      b->tot.p + 3, true, st));
+            gf::BfGemmArgs ga{};
+            ga.sa = sub_args(*ix);
+            ga.vt = ix->vt.p; ga.tnorm = ix->tnorm.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p;
+            ga.hi = b->hi.p; ga.items = b->items.p; ga.nitems = b->tot.p + 4; ga.bq = b->bq.p; ga.pcnt = b->pcnt.p;
+            ga.part_off = b->part_off.p; ga.part = b->part.p; ga.gbound = b->gbound.p; ga.ok = b->tot.p + 3;
+            ga.K = K; ga.D = ix->D;
+            GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu) * 3u, st));
+            gf::BfFinalArgs fa{};
+            fa.bfq = b->bfq.p; fa.nbf = uint32_t(bq.size()); fa.part_off = b->part_off.p; fa.pcnt = b->pcnt.p;
+            fa.ok = b->tot.p + 3; fa.part = b->part.p; fa.counts = b->counts.p; fa.cells = b->cells.p;
+            fa.offset = ix->offset.p; fa.selcount = b->selcount.p; fa.gidx = ix->gidx.p; fa.out_ids = b->out_ids.p;
+            fa.out_dist = b->out_dist.p; fa.counters = b->counters.p; fa.K = K; fa.P = ix->P;
+            GF_HIP(gf::launch_bf_final(fa, st));
+        };
 
         GF_HIP(hipMemsetAsync(b->counters.p, 0, size_t(Q) * GF_NCOUNTERS * sizeof(uint32_t), st));
         GF_HIP(gf::launch_fill_results(b->out_ids.p, b->out_dist.p, Q * K, st));
@@ -720,13 +813,28 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         ab.sched = b->sched.p + tq.size();
         ab.nsched = uint32_t(bq.size());
         if (gemm) {
-            GF_HIP(gf::launch_bf_i8(ga, st));
-            GF_HIP(gf::launch_bf_final(fa, st));
+            launch_gemm();
         } else {
             GF_HIP(gf::launch_bruteforce(ix->rs, ab, st));
         }
         GF_HIP(hipEventRecord(ev[2], st));
         GF_HIP(hipEventSynchronize(ev[2]));
+        uint32_t gtot[3] = {0, 1, 0};
+        if (gemm) {
+            GF_HIP(hipMemcpy(gtot, b->tot.p + 2, sizeof(gtot), hipMemcpyDeviceToHost));
+            if (!gtot[1]) {
+                // the pair lists outgrew their buffers: grow them and run the brute force again
+                const size_t cap = size_t(gtot[0]) + gtot[0] / 4 + 1024;
+                b->bq.alloc(cap); b->part.alloc(cap * K);
+                b->items.alloc(cap / gf::kBfQB + NS + 1);
+                GF_HIP(hipEventRecord(ev[1], st));
+                launch_gemm();
+                GF_HIP(hipEventRecord(ev[2], st));
+                GF_HIP(hipEventSynchronize(ev[2]));
+                GF_HIP(hipMemcpy(gtot, b->tot.p + 2, sizeof(gtot), hipMemcpyDeviceToHost));
+                GF_REQUIRE(gtot[1], GF_E_STATE, "brute-force schedule does not fit after growing");
+            }
+        }
         float t_tr = 0, t_bf = 0;
         GF_HIP(hipEventElapsedTime(&t_tr, ev[0], ev[1]));
         GF_HIP(hipEventElapsedTime(&t_bf, ev[1], ev[2]));
@@ -767,8 +875,20 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                                     double(stats->n_attr) * ix->a * 4.0 + double(stats->n_cross) * ix->E * 4.0 +
                                     double(stats->n_lrow) * 4.0 + double(tq.size()) * (K * 8.0 + ix->P * 4.0);
             if (gemm) {
-                stats->bytes_bruteforce = bf_bytes_gemm;
-                stats->ops_bruteforce = bf_ops;
+                // Algorithmic work of the item schedule: every pair (query,
+                // sub-cell) costs 2 D ops per point; every item streams its
+                // sub-cell's tiles once; the final merge reads all partials.
+                std::vector<uint32_t> bc(NS);
+                GF_HIP(hipMemcpy(bc.data(), b->bcnt.p, NS * sizeof(uint32_t), hipMemcpyDeviceToHost));
+                const double tile_bytes = (ix->D / 64) * 1024.0 + 32 * 4.0 + 16.0 * (1 + ix->AW) * 4.0;
+                double ops = 0.0, bytes = 0.0;
+                for (uint32_t sc = 0; sc < NS; ++sc) {
+                    ops += 2.0 * ix->D * double(bc[sc]) * ix->ssize_h[sc];
+                    bytes += double((bc[sc] + gf::kBfQB - 1) / gf::kBfQB) * (ix->stile_h[sc + 1] - ix->stile_h[sc]) *
+                             tile_bytes;
+                }
+                stats->bytes_bruteforce = bytes + double(gtot[0]) * K * 16.0;
+                stats->ops_bruteforce = ops;
             } else {
                 stats->bytes_bruteforce = double(stats->n_scan) * ix->a * 4.0 + double(b_dist) * ix->rowbytes +
                                           double(bq.size()) * (K * 8.0 + ix->P * 4.0);

@@ -65,42 +65,56 @@ struct TravArgs {
     uint32_t a, P, R, E, L, K, rl, hbits, Lpad;
 };
 
-// Query-batch brute force on int8 MFMA (integer data in [0, 255], integer
-// attributes whose spread inside each cell is below 65534).  Vectors are
-// stored shifted by -128 as int8, per cell in tiles of 16 points laid out in
+// Sub-cells: per cell a rank grid of attribute bins (host build in
+// gf_host.cpp).  Tiles of 16 points are grouped by sub-cell; tile t of the
+// tmeta array holds [row x 16][attribute word x 16] x AW (AW = ceil(a/2)
+// 32-bit words of two 16-bit offsets from the cell's smallest value).
+struct SubArgs {
+    const uint32_t* sbase;     // P+1 first sub-cell of each cell
+    const uint32_t* scell;     // cell of each sub-cell
+    const uint32_t* ssize;     // points per sub-cell
+    const uint32_t* stile;     // NS+1 first tile of each sub-cell
+    const int32_t* sbox;       // NS*2a: per attribute min, max
+    const uint32_t* tmeta;     // per tile: rows, attribute words
+    const int32_t* abase;      // P*a smallest attribute value of each cell
+    uint32_t a, AW, P, NS;
+};
+
+// Query-batch brute force on int8 MFMA (integer data in [0, 255]).  Vectors
+// are stored shifted by -128 as int8 in the sub-cell tile order, each tile in
 // MFMA operand order: tile t, k-step s holds 64 lanes x 16 bytes, lane l
-// carrying bytes [64 s + 16 (l / 16), +16) of point l % 16.
+// carrying bytes [64 s + 16 (l / 16), +16) of point l % 16.  tnorm holds per
+// tile [-floor(|x'|^2 / 2) x 16][|x'|^2 x 16].
 constexpr uint32_t kBfTile = 16;      // points per tile
-constexpr uint32_t kBfChunk = 512;    // tiles per work item (8192 points)
 constexpr uint32_t kBfKMax = 16;      // largest K of the MFMA route
 constexpr uint32_t kBfQB = 64;        // queries per work item
 struct BfItem {
-    uint32_t cell, qbase, nq, t0, t1, chunk;
+    uint32_t sub, qbase, nq;           // sub-cell, first entry of its query list, queries
 };
 struct BfGemmArgs {
+    SubArgs sa;
     const int8_t* vt;          // tiled int8 vectors
-    const int32_t* nxt;        // |x - 128|^2 per tiled point
-    const int32_t* meta;       // per tile: -floor(|x'|^2/2) x 16, |x'|^2 x 16, AW attribute words x 16
-    const int32_t* abase;      // P*a smallest attribute value of each cell
-    const uint32_t* tbase;     // P+1 first tile of each cell
-    const uint32_t* offset;    // P+1 first row of each cell
+    const int32_t* tnorm;      // per tile norms
     const int8_t* q8;          // Q*D queries shifted by -128
     const int32_t* nq;         // |q - 128|^2
     const float* lo;
     const float* hi;
     const BfItem* items;
-    uint32_t nitems;
-    const uint32_t* pq;        // query of each (query, cell) pair, grouped by cell
-    const uint32_t* ppos;      // position of the cell in that query's list
-    const uint32_t* part_off;  // per query: first partial slot entry
-    uint64_t* part;            // partial top-K keys: (d << 32) | row
-    uint32_t* gbound;          // per query: smallest K-th distance of any chunk so far
-    uint32_t maxch, K, a, D;
+    const uint32_t* nitems;    // device scalar
+    const uint32_t* bq;        // query of each (query, sub-cell) pair, grouped by sub-cell
+    const uint32_t* part_off;  // per query: first pair (its partial area holds pairs * K keys)
+    uint32_t* pcnt;            // per query: keys appended so far (zeroed before)
+    uint64_t* part;            // partial keys: (d << 32) | row
+    uint32_t* gbound;          // per query: smallest K-th distance of any item so far
+    const uint32_t* ok;        // schedule fits its buffers (else the kernel does nothing)
+    uint32_t K, D;
 };
 struct BfFinalArgs {
     const uint32_t* bfq;       // brute-force queries
     uint32_t nbf;
-    const uint32_t* part_off;
+    const uint32_t* part_off;  // per query: first pair (partial area = pairs * K keys)
+    const uint32_t* pcnt;      // keys appended for each query
+    const uint32_t* ok;
     const uint64_t* part;
     const uint32_t* counts;
     const uint32_t* cells;
@@ -110,18 +124,52 @@ struct BfFinalArgs {
     uint32_t* out_ids;
     float* out_dist;
     uint32_t* counters;
-    uint32_t maxch, K, P;
+    uint32_t K, P;
+};
+// Stage A on sub-cells: one workgroup per sub-cell over all queries.  A point
+// that passes a range lies in a cell the range selects, so the relation of a
+// range to a sub-cell's attribute box alone decides what the sub-cell adds to
+// the query's exact count.
+struct SubSelArgs {
+    SubArgs sa;
+    uint32_t Q;
+    const float* lo;
+    const float* hi;
+    uint32_t* selcount;        // zeroed before; receives atomic sums
+};
+// Stage C schedule of the MFMA brute force: per sub-cell, the brute-force
+// queries whose range reaches it, in query order.
+struct BfSchedArgs {
+    SubArgs sa;
+    uint32_t Q, postfilter;
+    const uint32_t* counts;
+    const uint32_t* little;
+    const float* lo;
+    const float* hi;
+    uint32_t* nsub;            // pairs per query (pass 1, zeroed before)
+    uint32_t* bcnt;            // pairs per sub-cell (pass 1)
+    const uint32_t* bstart;    // exclusive scan of bcnt (pass 2)
+    uint32_t* bq;
+    const uint32_t* ok;        // bq and part are large enough (pass 2)
 };
 
 // Kernel launchers (gf_kernels.hip).  All are asynchronous on `st`.
 hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds_bytes, hipStream_t st);
 hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, hipStream_t st);
 hipError_t launch_fill_results(uint32_t* ids, float* dist, uint32_t n, hipStream_t st);
-hipError_t launch_bf_i8(const BfGemmArgs& a, hipStream_t st);
+hipError_t launch_bf_i8(const BfGemmArgs& a, uint32_t nwg, hipStream_t st);
 hipError_t launch_bf_final(const BfFinalArgs& a, hipStream_t st);
-hipError_t launch_tile_i8(const float* vec_cm, uint32_t D, const uint32_t* offset, const uint32_t* tbase,
-                          const float* attrs_cm, uint32_t a, const int32_t* abase, uint32_t P, uint32_t ntiles,
-                          int8_t* vt, int32_t* nxt, int32_t* meta, hipStream_t st);
+hipError_t launch_tile_i8(const float* vec_cm, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
+                          int8_t* vt, int32_t* tnorm, hipStream_t st);
+hipError_t launch_subsel(const SubSelArgs& a, hipStream_t st);
+hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st);
+hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bstart, uint32_t NS, uint32_t* icnt,
+                          uint32_t* ioff, BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill,
+                          hipStream_t st);
+// out[0] = start[n-1] + cnt[n-1] (total of an exclusive scan); out[1] = out[0] <= cap
+// (with cap2 != 0 also out[0] * mul <= cap2).
+hipError_t launch_total(const uint32_t* cnt, const uint32_t* start, uint32_t n, uint32_t cap, uint32_t mul,
+                        uint64_t cap2, uint32_t* out, hipStream_t st);
 hipError_t launch_q_i8(const float* q, uint32_t Q, uint32_t D, int8_t* q8, int32_t* nq, hipStream_t st);
 hipError_t launch_f2h(const float* x, uint16_t* out, size_t n, float alpha, hipStream_t st);
 hipError_t launch_f2h_pad(const float* x, uint32_t rows, uint32_t D, uint16_t* out,

@@ -927,9 +927,10 @@ __global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P
 // |q - x|^2 = |q'|^2 + |x'|^2 - 2 q'.x' holds exactly in int32, so distances
 // are bit-identical to the canonical fp32 ones (all sums < 2^24).
 //
-// A wave owns 64 queries that select one cell (the stationary B operand, four
-// 16-query column tiles) and streams a chunk of that cell's 16-point tiles as
-// the A operand of v_mfma_i32_16x16x64_i8; lane l receives points
+// A work item is one sub-cell and up to 64 queries whose range reaches it;
+// persistent waves take items in turn.  The queries are the stationary B
+// operand (four 16-query column tiles); the sub-cell's 16-point tiles stream
+// as the A operand of v_mfma_i32_16x16x64_i8; lane l receives points
 // 4 (l / 16) + i, i < 4, of query 16 j + l % 16 for each column tile j.  The
 // accumulator starts at -floor(|x'|^2 / 2), so "d <= thr" becomes the single
 // compare acc >= ceil((|q'|^2 - thr) / 2) (exact up to the parity of |x'|^2,
@@ -942,14 +943,14 @@ __global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P
 // the block, keeps its sorted top-K (distance, row) in registers and merges
 // its buffer once some query's buffer holds kBfDrainAt entries.  Thresholds
 // tighten from the wave's own top-K and from a per-query global bound that
-// every chunk of the query lowers with atomicMin: a point farther than some
-// chunk's K-th distance cannot be in the final top-K.
+// every item lowers with atomicMin when it ends and reads when it starts: a
+// point farther than some item's K-th distance cannot be in the final top-K,
+// and only keys within the bound are appended for the final merge.
 typedef int v4i32_t __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 constexpr uint32_t kQB = 64;        // queries per wave
 constexpr uint32_t kBfBufQ = 24;    // survivor slots per query
 constexpr uint32_t kBfDrainAt = 8;  // drain once a query holds this many (+ <= 16 per tile < 24)
-constexpr uint32_t kBfRefresh = 32; // tiles between reads of the global bounds
 constexpr uint64_t kKeySent = ~uint64_t(0);
 constexpr int32_t kTpOpen = INT32_MIN;  // acc threshold while fewer than K are known
 
@@ -972,6 +973,7 @@ __device__ __forceinline__ uint32_t clamp16(uint32_t x, uint32_t lo, uint32_t hi
 // One attribute range [lo, hi] (floats holding integers) in the units of a
 // cell whose attribute values are base + [0, 65533].
 __device__ __forceinline__ void range16(float lo, float hi, int32_t base, uint32_t& l16, uint32_t& h16) {
+    if (!(lo <= hi)) { l16 = h16 = 65534u; return; }   // empty or NaN bound: nothing passes
     const float lc = ceilf(fmaxf(lo, -4.0e9f)), hc = floorf(fminf(hi, 4.0e9f));
     const int64_t l = int64_t(lc) - base, h = int64_t(hc) - base;
     if (!(lc <= hc) || h < 0 || l > 65533) { l16 = h16 = 65534u; return; }
@@ -984,208 +986,447 @@ __device__ __forceinline__ int32_t acc_threshold(int32_t nq, uint32_t thr) {
     return int32_t((int64_t(nq) - int64_t(thr) + 1) >> 1);   // ceil((nq - thr) / 2)
 }
 
+// ------------------------------------------------------------ sub-cells
+// Attribute box of one sub-cell as floats (attribute values are integers and
+// the conversion is monotone, so comparing the float bounds with the box ends
+// decides every point's float comparison of the reference).
+struct SubBox {
+    float mn[4], mx[4];
+};
+__device__ __forceinline__ SubBox load_box(const SubArgs& sa, uint32_t s) {
+    SubBox b;
+#pragma unroll
+    for (uint32_t d = 0; d < 4; ++d) {
+        b.mn[d] = d < sa.a ? float(sa.sbox[size_t(s) * 2 * sa.a + 2 * d]) : 0.0f;
+        b.mx[d] = d < sa.a ? float(sa.sbox[size_t(s) * 2 * sa.a + 2 * d + 1]) : 0.0f;
+    }
+    return b;
+}
+// A query's range held in registers.
+struct QRange {
+    float l[4], h[4];
+};
+__device__ __forceinline__ QRange load_range(uint32_t a, const float* lo, const float* hi, uint32_t q) {
+    QRange r;
+#pragma unroll
+    for (uint32_t d = 0; d < 4; ++d) {
+        r.l[d] = d < a ? lo[size_t(q) * a + d] : 0.0f;
+        r.h[d] = d < a ? hi[size_t(q) * a + d] : 0.0f;
+    }
+    return r;
+}
+// Relation of a range to a (non-empty) sub-cell: 0 no point can pass,
+// 1 partially covered, 2 every point passes.
+__device__ __forceinline__ uint32_t sub_relation(const SubBox& b, uint32_t a, const QRange& r) {
+    bool inside = true, outside = false;
+#pragma unroll
+    for (uint32_t d = 0; d < 4; ++d) {
+        if (d < a) {
+            inside = inside && r.l[d] <= b.mn[d] && b.mx[d] <= r.h[d];
+            outside = outside || !(r.h[d] >= b.mn[d]) || !(b.mx[d] >= r.l[d]);
+        }
+    }
+    return outside ? 0u : inside ? 2u : 1u;
+}
+
+// Stage A exact counts, one workgroup per sub-cell, over all queries in
+// chunks of 256: a query covering the whole box adds the sub-cell's size; the
+// partially covered ones are compacted in LDS and tested point by point (each
+// lane holds 16 points' packed attribute words, 1024 points per pass; lane k
+// of a wave loads the packed range of the k-th such query, then the wave
+// tests the queries one by one with the range broadcast from lane k).
+// Global atomics are collected in LDS and issued once per workgroup (or when
+// the list fills): a device-scope atomic takes microseconds, and later loads
+// of the same wave would wait for it.
+constexpr uint32_t kFlushCap = 2048;
+
+template <int AW>
+__global__ __launch_bounds__(256) void k_subsel(SubSelArgs p) {
+    __shared__ uint32_t cutl[256];
+    __shared__ uint32_t ncut, fn;
+    __shared__ uint32_t fq[kFlushCap], fv[kFlushCap];
+    const SubArgs& sa = p.sa;
+    const uint32_t s = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+    const uint32_t size = sa.ssize[s];
+    if (size == 0) return;
+    const SubBox box = load_box(sa, s);
+    const uint32_t c = sa.scell[s], t0 = sa.stile[s], t1 = sa.stile[s + 1];
+    constexpr uint32_t MW = 16u * (1u + AW);
+    if (tid == 0) fn = 0;
+    auto flush = [&]() {   // all threads; between barriers
+        for (uint32_t i = tid; i < fn; i += 256u) atomicAdd(&p.selcount[fq[i]], fv[i]);
+    };
+    for (uint32_t tb = t0; tb < t1; tb += 64u) {
+        uint32_t w[16][AW];
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            const uint32_t t = tb + 4u * g + (lane >> 4);
+#pragma unroll
+            for (int k = 0; k < AW; ++k)
+                w[g][k] = t < t1 ? sa.tmeta[size_t(t) * MW + 16u * (1 + k) + (lane & 15u)] : 65535u;
+        }
+        // Each sub-cell starts at its own chunk, so the per-query atomics of
+        // concurrent workgroups land on different queries.
+        const uint32_t nch = (p.Q + 255u) / 256u;
+        // ranges of the next chunk are loaded while the current one is scanned
+        uint32_t qn = (s % nch) * 256u + tid;
+        QRange rn = load_range(sa.a, p.lo, p.hi, qn < p.Q ? qn : 0u);
+        for (uint32_t ci = 0; ci < nch; ++ci) {
+            const uint32_t q = qn;
+            const QRange rq = rn;
+            qn = ((ci + 1 + s) % nch) * 256u + tid;
+            if (ci + 1 < nch) rn = load_range(sa.a, p.lo, p.hi, qn < p.Q ? qn : 0u);
+            __syncthreads();
+            if (fn + 512u > kFlushCap) {   // a chunk adds at most 2 x 256 entries
+                flush();
+                __syncthreads();
+                if (tid == 0) fn = 0;
+            }
+            if (tid == 0) ncut = 0;
+            __syncthreads();
+            const uint32_t rel = q < p.Q ? sub_relation(box, sa.a, rq) : 0u;
+            if (rel == 2 && tb == t0) {
+                const uint32_t i = atomicAdd(&fn, 1u);
+                fq[i] = q;
+                fv[i] = size;
+            }
+            if (rel == 1) cutl[atomicAdd(&ncut, 1u)] = q;
+            __syncthreads();
+            // The waves split the partial queries: wave w takes entries w, w + 4, ...
+            const uint32_t n = ncut, nw = n > wave ? (n - wave + 3u) / 4u : 0u;
+            for (uint32_t base = 0; base < nw; base += 64u) {
+                const uint32_t k = base + lane;
+                const uint32_t qq = k < nw ? cutl[wave + 4u * k] : cutl[wave];
+                uint32_t lo16[AW], hi16[AW];
+#pragma unroll
+                for (int x = 0; x < AW; ++x) {
+                    uint32_t l0, h0, l1 = 0u, h1 = 0u;
+                    const uint32_t d0 = 2u * x, d1 = 2u * x + 1u;
+                    range16(p.lo[size_t(qq) * sa.a + d0], p.hi[size_t(qq) * sa.a + d0], sa.abase[c * sa.a + d0], l0,
+                            h0);
+                    if (d1 < sa.a)
+                        range16(p.lo[size_t(qq) * sa.a + d1], p.hi[size_t(qq) * sa.a + d1], sa.abase[c * sa.a + d1],
+                                l1, h1);
+                    lo16[x] = l0 | (l1 << 16);
+                    hi16[x] = h0 | (h1 << 16);
+                }
+                const uint32_t nb = min(64u, nw - base);
+                for (uint32_t u = 0; u < nb; ++u) {
+                    uint32_t bl[AW], bh[AW];
+#pragma unroll
+                    for (int x = 0; x < AW; ++x) {
+                        bl[x] = readlane32(lo16[x], u);
+                        bh[x] = readlane32(hi16[x], u);
+                    }
+                    uint32_t cnt = 0;
+#pragma unroll
+                    for (int g = 0; g < 16; ++g) {
+                        bool ok = true;
+#pragma unroll
+                        for (int x = 0; x < AW; ++x) ok &= clamp16(w[g][x], bl[x], bh[x]) == w[g][x];
+                        cnt += __builtin_popcountll(__builtin_amdgcn_ballot_w64(ok));
+                    }
+                    if (cnt && lane == u) {
+                        const uint32_t i = atomicAdd(&fn, 1u);
+                        fq[i] = qq;
+                        fv[i] = cnt;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    __syncthreads();
+    flush();
+}
+
+// Stage C schedule, one workgroup per sub-cell over all queries: the
+// brute-force queries (not traversed, little > 0) whose range reaches the
+// sub-cell, in query order starting at a chunk that depends on the sub-cell
+// (spreading the per-query atomics of concurrent workgroups).  Pass 1 counts
+// per sub-cell and per query; pass 2 writes the lists at their scanned
+// offsets in the same order.
+__global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
+    __shared__ uint32_t wcnt[4];
+    __shared__ uint32_t fq[kFlushCap];
+    const SubArgs& sa = p.sa;
+    const uint32_t s = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+    if (fill && !*p.ok) return;
+    if (sa.ssize[s] == 0) {
+        if (!fill && tid == 0) p.bcnt[s] = 0;
+        return;
+    }
+    const SubBox box = load_box(sa, s);
+    const uint32_t base = fill ? p.bstart[s] : 0u;
+    uint32_t running = 0, fn = 0;   // fn: queries listed since the last flush (uniform)
+    const uint32_t nch = (p.Q + 255u) / 256u;
+    for (uint32_t ci = 0; ci < nch; ++ci) {
+        if (!fill && fn + 256u > kFlushCap) {
+            for (uint32_t i = tid; i < fn; i += 256u) atomicAdd(&p.nsub[fq[i]], 1u);
+            __syncthreads();
+            fn = 0;
+        }
+        const uint32_t q = ((ci + s) % nch) * 256u + tid;
+        bool hit = false;
+        if (q < p.Q) {
+            const uint32_t cnt = p.counts[q], lit = p.little[q];
+            const bool trav = cnt < p.postfilter && cnt != lit;
+            hit = !trav && lit > 0 && sub_relation(box, sa.a, load_range(sa.a, p.lo, p.hi, q)) != 0;
+        }
+        const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
+        if (lane == 0) wcnt[wave] = uint32_t(__builtin_popcountll(m));
+        __syncthreads();
+        uint32_t woff = 0, tot = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < 4; ++w) {
+            woff += w < wave ? wcnt[w] : 0u;
+            tot += wcnt[w];
+        }
+        if (hit) {
+            if (!fill) fq[fn + woff + lanes_below(m)] = q;
+            else p.bq[base + running + woff + lanes_below(m)] = q;
+        }
+        running += tot;
+        fn += tot;
+        __syncthreads();
+    }
+    if (!fill) {
+        for (uint32_t i = tid; i < fn; i += 256u) atomicAdd(&p.nsub[fq[i]], 1u);
+        if (tid == 0) p.bcnt[s] = running;
+    }
+}
+
+// Work items of the MFMA brute force: ceil(n / 64) blocks per sub-cell.
+__global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bstart, uint32_t NS, uint32_t* icnt,
+                          const uint32_t* ioff, BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill) {
+    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= NS) return;
+    if (fill && !*ok) {
+        if (s == NS - 1) *nitems = 0;
+        return;
+    }
+    const uint32_t n = bcnt[s], nb = (n + kBfQB - 1) / kBfQB;
+    if (!fill) { icnt[s] = nb; return; }
+    for (uint32_t b = 0; b < nb; ++b)
+        items[ioff[s] + b] = BfItem{s, bstart[s] + b * kBfQB, min(kBfQB, n - b * kBfQB)};
+    if (s == NS - 1) *nitems = ioff[s] + nb;
+}
+
+// out[0] = start[n-1] + cnt[n-1], the total of an exclusive scan; out[1] =
+// whether it fits a buffer of cap entries (and, times mul, one of cap2).
+__global__ void k_total(const uint32_t* cnt, const uint32_t* start, uint32_t n, uint32_t cap, uint32_t mul,
+                        uint64_t cap2, uint32_t* out) {
+    if (threadIdx.x != 0) return;
+    const uint32_t t = n ? start[n - 1] + cnt[n - 1] : 0u;
+    out[0] = t;
+    out[1] = (t <= cap && (cap2 == 0 || uint64_t(t) * mul <= cap2)) ? 1u : 0u;
+}
+
 template <int KS, int AW, int KT>
-__global__ __launch_bounds__(256) void k_bf_i8(BfGemmArgs p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_bf_i8(BfGemmArgs p) {
     __shared__ uint64_t s_buf[4][kQB * kBfBufQ];
     __shared__ uint32_t s_cnt[4][kQB];
     __shared__ int32_t s_tp[4][kQB];
     __shared__ uint32_t s_bnd[4][2 * AW][kQB];
     const uint32_t wave = threadIdx.x >> 6, lane = lane_id();
-    // XCD-aware order: workgroups go round-robin to the 8 XCDs, so XCD x gets
-    // a contiguous run of items (neighbouring query blocks of one chunk share
-    // that XCD's L2).
+    const SubArgs& sa = p.sa;
+    // Persistent waves, XCD-aware: workgroups go round-robin to the 8 XCDs and
+    // XCD x works through the x-th eighth of the item list (items of one
+    // sub-cell are adjacent, so its tiles stay in that XCD's L2).
     const uint32_t nwg = gridDim.x, xcd = blockIdx.x & 7u, k8 = blockIdx.x >> 3;
-    const uint32_t wg = xcd * (nwg >> 3) + min(xcd, nwg & 7u) + k8;
-    const uint32_t item_id = wg * 4u + wave;
-    if (item_id >= p.nitems) return;   // waves are independent: no workgroup barrier below
-    const BfItem it = p.items[item_id];
-    const uint32_t K = p.K;
+    const uint32_t nwg_x = (nwg - xcd + 7u) >> 3;
+    const uint32_t n_items = *p.ok ? *p.nitems : 0u;
+    const uint32_t i_lo = uint32_t(uint64_t(n_items) * xcd / 8u), i_hi = uint32_t(uint64_t(n_items) * (xcd + 1u) / 8u);
     uint64_t* buf = s_buf[wave];
     uint32_t* cnt = s_cnt[wave];
     int32_t* stp = s_tp[wave];
-    const uint32_t cell = it.cell;
-
-    // Owner state: lane q owns query q of the block; its sorted top-K of
-    // (distance << 32 | row) keys lives in registers.
-    const bool own_live = lane < it.nq;
-    const uint32_t own_q = p.pq[it.qbase + (own_live ? lane : 0u)];
-    const int32_t own_nq = p.nq[own_q];
-    uint32_t own_thr = own_live ? p.gbound[own_q] : 0u;
-    uint64_t tk[KT];
-#pragma unroll
-    for (int k = 0; k < KT; ++k) tk[k] = kKeySent;
-    uint64_t kth = kKeySent;
-    cnt[lane] = 0;
-    stp[lane] = own_live ? acc_threshold(own_nq, own_thr) : INT32_MAX;
-#pragma unroll
-    for (int w = 0; w < AW; ++w) {
-        uint32_t l0 = 65534u, h0 = 65534u, l1 = 0u, h1 = 0u;
-        if (own_live) {
-            const uint32_t d0 = 2u * w, d1 = 2u * w + 1u;
-            range16(p.lo[size_t(own_q) * p.a + d0], p.hi[size_t(own_q) * p.a + d0], p.abase[cell * p.a + d0], l0, h0);
-            if (d1 < p.a)
-                range16(p.lo[size_t(own_q) * p.a + d1], p.hi[size_t(own_q) * p.a + d1], p.abase[cell * p.a + d1], l1,
-                        h1);
-        }
-        s_bnd[wave][2 * w][lane] = l0 | (l1 << 16);
-        s_bnd[wave][2 * w + 1][lane] = h0 | (h1 << 16);
-    }
-    wave_fence();
-
-    // Column data: query 16 j + col of the block (a dead column repeats the
-    // first query; its empty range keeps it from producing survivors).
+    const uint32_t K = p.K;
     const uint32_t col = lane & 15u, grp = lane >> 4;
-    v4i32_t B[4][KS];
-    uint32_t blo[4][AW], bhi[4][AW];
-    int32_t tp[4];
+    constexpr uint32_t MW = 16u * (1u + AW);
+
+    for (uint32_t item_id = i_lo + k8 * 4u + wave; item_id < i_hi; item_id += nwg_x * 4u) {
+        const BfItem it = p.items[item_id];
+        const uint32_t s = it.sub, cell = sa.scell[s];
+        const uint32_t t0 = sa.stile[s], t1 = sa.stile[s + 1];
+
+        // Owner state: lane q owns query q of the block; its sorted top-K of
+        // (distance << 32 | row) keys lives in registers.
+        const bool own_live = lane < it.nq;
+        const uint32_t own_q = p.bq[it.qbase + (own_live ? lane : 0u)];
+        const int32_t own_nq = p.nq[own_q];
+        uint32_t own_thr =
+            own_live ? __hip_atomic_load(&p.gbound[own_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        uint64_t tk[KT];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t ql = 16u * j + col;
-        const uint32_t q = p.pq[it.qbase + (ql < it.nq ? ql : 0u)];
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-            B[j][s] = *reinterpret_cast<const v4i32_t*>(p.q8 + size_t(q) * p.D + s * 64 + grp * 16);
+        for (int k = 0; k < KT; ++k) tk[k] = kKeySent;
+        uint64_t kth = kKeySent;
+        wave_fence();
+        cnt[lane] = 0;
+        stp[lane] = own_live ? acc_threshold(own_nq, own_thr) : INT32_MAX;
 #pragma unroll
         for (int w = 0; w < AW; ++w) {
-            blo[j][w] = s_bnd[wave][2 * w][ql];
-            bhi[j][w] = s_bnd[wave][2 * w + 1][ql];
-        }
-        tp[j] = stp[ql];
-    }
-
-    const uint32_t tb = p.tbase[cell];
-    const uint32_t off = p.offset[cell];
-    constexpr uint32_t kMeta = 16u * (2u + AW);
-    auto reload_tp = [&]() {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) tp[j] = stp[16u * j + col];
-    };
-    auto set_thr = [&](uint32_t thr) {
-        own_thr = thr;
-        stp[lane] = acc_threshold(own_nq, own_thr);
-    };
-    // Owner: merge the buffered survivors of its query, publish the new
-    // threshold and lower the query's global bound.
-    auto drain = [&]() {
-        wave_fence();
-        const uint32_t n = cnt[lane];
-        if (n) {
-            uint64_t nxt = buf[lane * kBfBufQ];
-            for (uint32_t e = 0; e < n; ++e) {
-                const uint64_t cur = nxt;
-                if (e + 1 < n) nxt = buf[lane * kBfBufQ + e + 1];
-                const int32_t d = own_nq + int32_t(uint32_t(cur >> 32));
-                uint64_t c = (uint64_t(uint32_t(d)) << 32) | uint32_t(cur);
-                if (c < kth) {
-#pragma unroll
-                    for (int k = 0; k < KT; ++k) {
-                        const bool lt = c < tk[k];
-                        const uint64_t v = tk[k];
-                        tk[k] = lt ? c : v;
-                        c = lt ? v : c;
-                    }
-#pragma unroll
-                    for (int k = 0; k < KT; ++k)
-                        if (uint32_t(k) == K - 1) kth = tk[k];
-                }
+            uint32_t l0 = 65534u, h0 = 65534u, l1 = 0u, h1 = 0u;
+            if (own_live) {
+                const uint32_t d0 = 2u * w, d1 = 2u * w + 1u;
+                range16(p.lo[size_t(own_q) * sa.a + d0], p.hi[size_t(own_q) * sa.a + d0],
+                        sa.abase[cell * sa.a + d0], l0, h0);
+                if (d1 < sa.a)
+                    range16(p.lo[size_t(own_q) * sa.a + d1], p.hi[size_t(own_q) * sa.a + d1],
+                            sa.abase[cell * sa.a + d1], l1, h1);
             }
-            cnt[lane] = 0;
-            if (kth != kKeySent && uint32_t(kth >> 32) < own_thr) {
-                set_thr(uint32_t(kth >> 32));
-                atomicMin(&p.gbound[own_q], own_thr);
-            }
+            s_bnd[wave][2 * w][lane] = l0 | (l1 << 16);
+            s_bnd[wave][2 * w + 1][lane] = h0 | (h1 << 16);
         }
         wave_fence();
-        reload_tp();
-    };
 
-    // Operands of tile t + 1 are loaded while tile t is computed.
-    v4i32_t A[KS], mh, mn, ma[AW];
-    auto load_tile = [&](uint32_t t) {
-        const v4i32_t* vp = reinterpret_cast<const v4i32_t*>(p.vt + size_t(t) * KS * 1024u) + lane;
-        const int32_t* mt = p.meta + size_t(t) * kMeta;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) A[s] = vp[s * 64];
-        mh = *reinterpret_cast<const v4i32_t*>(mt + 4u * grp);
-        mn = *reinterpret_cast<const v4i32_t*>(mt + 16u + 4u * grp);
-#pragma unroll
-        for (int w = 0; w < AW; ++w) ma[w] = *reinterpret_cast<const v4i32_t*>(mt + 16u * (2 + w) + 4u * grp);
-    };
-    load_tile(it.t0);
-    uint32_t gb_next = 0xFFFFFFFFu;   // global bound loaded one refresh period earlier
-    for (uint32_t t = it.t0; t < it.t1; ++t) {
-        v4i32_t acc[4];
+        // Column data: query 16 j + col of the block (a dead column repeats
+        // the first query; its empty range keeps it from producing survivors).
+        v4i32_t B[4][KS];
+        uint32_t blo[4][AW], bhi[4][AW];
+        int32_t tp[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B[j][0], mh, 0, 0, 0);
+            const uint32_t ql = 16u * j + col;
+            const uint32_t q = p.bq[it.qbase + (ql < it.nq ? ql : 0u)];
 #pragma unroll
-            for (int s = 1; s < KS; ++s) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[s], B[j][s], acc[j], 0, 0, 0);
-        }
-        const v4i32_t cmh = mh, cmn = mn, cma0 = ma[0], cma1 = ma[AW - 1];
-        if (t + 1 < it.t1) load_tile(t + 1);
-        // Branch-free test of one (point i, query column j) pair.
-        auto pass = [&](int j, int i) {
-            bool ok = acc[j][i] >= tp[j];
-            const uint32_t x0 = uint32_t(cma0[i]);
-            ok &= clamp16(x0, blo[j][0], bhi[j][0]) == x0;
-            if (AW > 1) {
-                const uint32_t x1 = uint32_t(cma1[i]);
-                ok &= clamp16(x1, blo[j][AW - 1], bhi[j][AW - 1]) == x1;
+            for (int k = 0; k < KS; ++k)
+                B[j][k] = *reinterpret_cast<const v4i32_t*>(p.q8 + size_t(q) * p.D + k * 64 + grp * 16);
+#pragma unroll
+            for (int w = 0; w < AW; ++w) {
+                blo[j][w] = s_bnd[wave][2 * w][ql];
+                bhi[j][w] = s_bnd[wave][2 * w + 1][ql];
             }
-            return ok;
+            tp[j] = stp[ql];
+        }
+
+        auto reload_tp = [&]() {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) tp[j] = stp[16u * j + col];
         };
-        bool anyl = false;   // lane-mask OR: no per-pair ballot
+        auto set_thr = [&](uint32_t thr) {
+            own_thr = thr;
+            stp[lane] = acc_threshold(own_nq, own_thr);
+        };
+        // Owner: merge the buffered survivors of its query, publish the new
+        // threshold and lower the query's global bound.
+        auto drain = [&]() {
+            wave_fence();
+            const uint32_t n = cnt[lane];
+            if (n) {
+                uint64_t nxt = buf[lane * kBfBufQ];
+                for (uint32_t e = 0; e < n; ++e) {
+                    const uint64_t cur = nxt;
+                    if (e + 1 < n) nxt = buf[lane * kBfBufQ + e + 1];
+                    const int32_t d = own_nq + int32_t(uint32_t(cur >> 32));
+                    uint64_t c = (uint64_t(uint32_t(d)) << 32) | uint32_t(cur);
+                    if (c < kth) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+                        for (int k = 0; k < KT; ++k) {
+                            const bool lt = c < tk[k];
+                            const uint64_t v = tk[k];
+                            tk[k] = lt ? c : v;
+                            c = lt ? v : c;
+                        }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) anyl |= pass(j, i);
-        if (__builtin_amdgcn_ballot_w64(anyl)) {
-            // Append: the owner adds |q'|^2 to nx - 2 q'.x' later.
-            const uint32_t row0 = off + (t - tb) * 16u + 4u * grp;
-            bool full = false;
+                        for (int k = 0; k < KT; ++k)
+                            if (uint32_t(k) == K - 1) kth = tk[k];
+                    }
+                }
+                cnt[lane] = 0;
+                if (kth != kKeySent && uint32_t(kth >> 32) < own_thr) set_thr(uint32_t(kth >> 32));
+            }
+            wave_fence();
+            reload_tp();
+        };
+
+        // Operands of tile t + 1 are loaded while tile t is computed.
+        v4i32_t A[KS], mh, mn, mr, ma[AW];
+        auto load_tile = [&](uint32_t t) {
+            const v4i32_t* vp = reinterpret_cast<const v4i32_t*>(p.vt + size_t(t) * KS * 1024u) + lane;
+            const int32_t* nt = p.tnorm + size_t(t) * 32u;
+            const uint32_t* mt = sa.tmeta + size_t(t) * MW;
+#pragma unroll
+            for (int k = 0; k < KS; ++k) A[k] = vp[k * 64];
+            mh = *reinterpret_cast<const v4i32_t*>(nt + 4u * grp);
+            mn = *reinterpret_cast<const v4i32_t*>(nt + 16u + 4u * grp);
+            mr = *reinterpret_cast<const v4i32_t*>(mt + 4u * grp);
+#pragma unroll
+            for (int w = 0; w < AW; ++w) ma[w] = *reinterpret_cast<const v4i32_t*>(mt + 16u * (1 + w) + 4u * grp);
+        };
+        load_tile(t0);
+        for (uint32_t t = t0; t < t1; ++t) {
+            v4i32_t acc[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B[j][0], mh, 0, 0, 0);
+#pragma unroll
+                for (int k = 1; k < KS; ++k)
+                    acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[k], B[j][k], acc[j], 0, 0, 0);
+            }
+            const v4i32_t cmh = mh, cmn = mn, cmr = mr, cma0 = ma[0], cma1 = ma[AW - 1];
+            if (t + 1 < t1) load_tile(t + 1);
+            // Branch-free test of one (point i, query column j) pair.
+            auto pass = [&](int j, int i) {
+                bool ok = acc[j][i] >= tp[j];
+                const uint32_t x0 = uint32_t(cma0[i]);
+                ok &= clamp16(x0, blo[j][0], bhi[j][0]) == x0;
+                if (AW > 1) {
+                    const uint32_t x1 = uint32_t(cma1[i]);
+                    ok &= clamp16(x1, blo[j][AW - 1], bhi[j][AW - 1]) == x1;
+                }
+                return ok;
+            };
+            bool anyl = false;   // lane-mask OR: no per-pair ballot
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (pass(j, i)) {
-                        const uint32_t ql = 16u * j + col;
-                        const int32_t v = cmn[i] - 2 * (acc[j][i] - cmh[i]);
-                        const uint32_t slot = atomicAdd(&cnt[ql], 1u);
-                        buf[ql * kBfBufQ + slot] = (uint64_t(uint32_t(v)) << 32) | (row0 + i);
-                        full |= slot + 1u >= kBfDrainAt;
-                    }
-            if (__builtin_amdgcn_ballot_w64(full)) drain();
-        }
-        if ((t - it.t0) % kBfRefresh == kBfRefresh - 1) {
-            // Other chunks of the same queries may have lowered their bounds;
-            // the value used now was loaded one period ago (no wait on it).
-            const bool lower = own_live && gb_next < own_thr;
-            if (__builtin_amdgcn_ballot_w64(lower)) {
-                if (lower) set_thr(gb_next);
-                wave_fence();
-                reload_tp();
-            }
-            gb_next = own_live ? __hip_atomic_load(&p.gbound[own_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                               : 0xFFFFFFFFu;
-        }
-    }
-    drain();
-    if (own_live) {
-        const size_t slot = size_t(p.part_off[own_q]) + (size_t(p.ppos[it.qbase + lane]) * p.maxch + it.chunk) * K;
+                for (int i = 0; i < 4; ++i) anyl |= pass(j, i);
+            if (__builtin_amdgcn_ballot_w64(anyl)) {
+                // Append: the owner adds |q'|^2 to nx - 2 q'.x' later.
+                bool full = false;
 #pragma unroll
-        for (int k = 0; k < KT; ++k)
-            if (uint32_t(k) < K) p.part[slot + k] = tk[k];
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (pass(j, i)) {
+                            const uint32_t ql = 16u * j + col;
+                            const int32_t v = cmn[i] - 2 * (acc[j][i] - cmh[i]);
+                            const uint32_t slot = atomicAdd(&cnt[ql], 1u);
+                            buf[ql * kBfBufQ + slot] = (uint64_t(uint32_t(v)) << 32) | uint32_t(cmr[i]);
+                            full |= slot + 1u >= kBfDrainAt;
+                        }
+                if (__builtin_amdgcn_ballot_w64(full)) drain();
+            }
+        }
+        drain();
+        if (own_live) {
+            // The query's bound is read at item start and lowered at item end:
+            // device-scope atomics inside the tile loop would stall its loads.
+            if (own_thr != 0xFFFFFFFFu) atomicMin(&p.gbound[own_q], own_thr);
+            // Only keys within the query's bound can reach its final top-K.
+            uint32_t keep = 0;
+#pragma unroll
+            for (int k = 0; k < KT; ++k)
+                keep += (uint32_t(k) < K && tk[k] != kKeySent && uint32_t(tk[k] >> 32) <= own_thr) ? 1u : 0u;
+            if (keep) {
+                const size_t slot = size_t(p.part_off[own_q]) * K + atomicAdd(&p.pcnt[own_q], keep);
+#pragma unroll
+                for (int k = 0; k < KT; ++k)
+                    if (uint32_t(k) < keep) p.part[slot + k] = tk[k];
+            }
+        }
     }
 }
 
-// Per-query merge of the partial top-K lists of every (cell, chunk).
+// Per-query merge of the keys the brute-force items appended for the query.
 __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
     __shared__ uint64_t T[64];
     const uint32_t lane = lane_id();
+    if (!*p.ok) return;
     const uint32_t q = p.bfq[blockIdx.x];
     const uint32_t K = p.K;
-    const uint32_t n = p.counts[q] * p.maxch * K;
-    const uint64_t* part = p.part + p.part_off[q];
+    const uint32_t n = p.pcnt[q];
+    const uint64_t* part = p.part + size_t(p.part_off[q]) * K;
     uint64_t top = kKeySent;
     for (uint32_t s0 = 0; s0 < n; s0 += 64u) {
         const uint64_t c = s0 + lane < n ? part[s0 + lane] : kKeySent;
@@ -1230,55 +1471,32 @@ __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
     }
 }
 
-// Index build: int8 tiles (operand layout of BfGemmArgs::vt), |x'|^2 per tiled
-// point, and per tile the meta block [-floor(|x'|^2 / 2) x 16][|x'|^2 x 16]
-// [attribute words x 16] x AW, attribute word w of a point = (a_{2w} - base) | (a_{2w+1} - base) << 16
-// (padding points: 65535 in the low half, so they never pass a range).
-__global__ __launch_bounds__(64) void k_tile_i8(const float* vec, uint32_t D, const uint32_t* offset,
-                                               const uint32_t* tbase, const float* attrs, uint32_t a,
-                                               const int32_t* abase, uint32_t P, int8_t* vt, int32_t* nxt,
-                                               int32_t* meta) {
+// Index build: int8 tiles (operand layout of BfGemmArgs::vt) of the sub-cell
+// tile order and per tile [-floor(|x'|^2 / 2) x 16][|x'|^2 x 16] (padding
+// points are all zero).
+__global__ __launch_bounds__(64) void k_tile_i8(const float* vec, uint32_t D, const uint32_t* tmeta, uint32_t AW,
+                                               int8_t* vt, int32_t* tnorm) {
     const uint32_t t = blockIdx.x, lane = lane_id();
-    uint32_t lo = 0, hi = P;   // cell c with tbase[c] <= t < tbase[c+1]
-    while (hi - lo > 1) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (tbase[mid] <= t) lo = mid; else hi = mid;
-    }
-    const uint32_t c = lo;
     const uint32_t col = lane & 15u;
-    const uint32_t lp = (t - tbase[c]) * 16u + col;
-    const uint32_t csz = offset[c + 1] - offset[c];
-    const bool valid = lp < csz;
-    const size_t row = size_t(offset[c]) + lp;
+    const uint32_t row = tmeta[size_t(t) * 16u * (1u + AW) + col];
+    const bool valid = row != 0xFFFFFFFFu;
     const uint32_t KS = D / 64u;
-    const uint32_t AW = (a + 1u) / 2u;
     for (uint32_t s = 0; s < KS; ++s) {
         int8_t* dst = vt + (size_t(t) * KS + s) * 1024u + lane * 16u;
         for (uint32_t j = 0; j < 16; ++j) {
             const uint32_t k = s * 64u + (lane >> 4) * 16u + j;
-            dst[j] = valid ? int8_t(int32_t(vec[row * D + k]) - 128) : int8_t(0);
+            dst[j] = valid ? int8_t(int32_t(vec[size_t(row) * D + k]) - 128) : int8_t(0);
         }
     }
     if (lane < 16) {
         int32_t n = 0;
         if (valid)
             for (uint32_t k = 0; k < D; ++k) {
-                const int32_t v = int32_t(vec[row * D + k]) - 128;
+                const int32_t v = int32_t(vec[size_t(row) * D + k]) - 128;
                 n += v * v;
             }
-        nxt[size_t(t) * 16u + col] = n;
-        int32_t* mt = meta + size_t(t) * 16u * (2u + AW);
-        mt[col] = -(n >> 1);
-        mt[16u + col] = n;
-        for (uint32_t w = 0; w < AW; ++w) {
-            uint32_t word = 65535u;
-            if (valid) {
-                const uint32_t d0 = 2u * w, d1 = 2u * w + 1u;
-                word = uint32_t(int32_t(attrs[row * a + d0]) - abase[c * a + d0]);
-                if (d1 < a) word |= uint32_t(int32_t(attrs[row * a + d1]) - abase[c * a + d1]) << 16;
-            }
-            mt[16u * (2u + w) + col] = int32_t(word);
-        }
+        tnorm[size_t(t) * 32u + col] = -(n >> 1);
+        tnorm[size_t(t) * 32u + 16u + col] = n;
     }
 }
 
@@ -1377,17 +1595,15 @@ hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, hipStream_t 
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_bf_i8(const BfGemmArgs& a, hipStream_t st) {
-    if (!a.nitems) return hipSuccess;
-    if (a.K > kBfKMax || a.a < 1 || a.a > 4) return hipErrorInvalidValue;
-    const uint32_t blocks = (a.nitems + 3) / 4;
-    const uint32_t AW = (a.a + 1) / 2;
-#define BF(KS, AW_)                                                                     \
-    do {                                                                                \
-        if (a.K <= 10)                                                                  \
-            hipLaunchKernelGGL((k_bf_i8<KS, AW_, 10>), dim3(blocks), dim3(256), 0, st, a); \
-        else                                                                            \
-            hipLaunchKernelGGL((k_bf_i8<KS, AW_, 16>), dim3(blocks), dim3(256), 0, st, a); \
+hipError_t launch_bf_i8(const BfGemmArgs& a, uint32_t nwg, hipStream_t st) {
+    if (a.K > kBfKMax || a.sa.a < 1 || a.sa.a > 4 || nwg == 0) return hipErrorInvalidValue;
+    const uint32_t AW = a.sa.AW;
+#define BF(KS, AW_)                                                                   \
+    do {                                                                              \
+        if (a.K <= 10)                                                                \
+            hipLaunchKernelGGL((k_bf_i8<KS, AW_, 10>), dim3(nwg), dim3(256), 0, st, a); \
+        else                                                                          \
+            hipLaunchKernelGGL((k_bf_i8<KS, AW_, 16>), dim3(nwg), dim3(256), 0, st, a); \
     } while (0)
     switch ((a.D / 64) * 4 + AW) {
         case 1 * 4 + 1: BF(1, 1); break;
@@ -1410,12 +1626,39 @@ hipError_t launch_bf_final(const BfFinalArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_tile_i8(const float* vec_cm, uint32_t D, const uint32_t* offset, const uint32_t* tbase,
-                          const float* attrs_cm, uint32_t a, const int32_t* abase, uint32_t P, uint32_t ntiles,
-                          int8_t* vt, int32_t* nxt, int32_t* meta, hipStream_t st) {
-    if (!ntiles) return hipSuccess;
-    hipLaunchKernelGGL(k_tile_i8, dim3(ntiles), dim3(64), 0, st, vec_cm, D, offset, tbase, attrs_cm, a, abase, P, vt,
-                       nxt, meta);
+hipError_t launch_tile_i8(const float* vec_cm, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
+                          int8_t* vt, int32_t* tnorm, hipStream_t st) {
+    if (!ntile) return hipSuccess;
+    hipLaunchKernelGGL(k_tile_i8, dim3(ntile), dim3(64), 0, st, vec_cm, D, tmeta, AW, vt, tnorm);
+    return hipGetLastError();
+}
+
+hipError_t launch_subsel(const SubSelArgs& a, hipStream_t st) {
+    if (!a.sa.NS || !a.Q) return hipSuccess;
+    if (a.sa.AW == 1) hipLaunchKernelGGL(k_subsel<1>, dim3(a.sa.NS), dim3(256), 0, st, a);
+    else if (a.sa.AW == 2) hipLaunchKernelGGL(k_subsel<2>, dim3(a.sa.NS), dim3(256), 0, st, a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st) {
+    if (!a.sa.NS) return hipSuccess;
+    hipLaunchKernelGGL(k_bfsched, dim3(a.sa.NS), dim3(256), 0, st, a, fill);
+    return hipGetLastError();
+}
+
+hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bstart, uint32_t NS, uint32_t* icnt,
+                          uint32_t* ioff, BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill,
+                          hipStream_t st) {
+    if (!NS) return hipSuccess;
+    hipLaunchKernelGGL(k_bfitems, dim3((NS + 255) / 256), dim3(256), 0, st, bcnt, bstart, NS, icnt, ioff, items,
+                       nitems, ok, fill);
+    return hipGetLastError();
+}
+
+hipError_t launch_total(const uint32_t* cnt, const uint32_t* start, uint32_t n, uint32_t cap, uint32_t mul,
+                        uint64_t cap2, uint32_t* out, hipStream_t st) {
+    hipLaunchKernelGGL(k_total, dim3(1), dim3(64), 0, st, cnt, start, n, cap, mul, cap2, out);
     return hipGetLastError();
 }
 

@@ -51,3 +51,32 @@ def world_gauss():
     cfg = dict(vectors=vec, attrs=att, grid=[4, 4, 4], R=16, E=2, C=16, queries=qv, lo=lo, hi=hi)
     ix = synth.build_index(vec, att, cfg["grid"], 16, 2, 16, seed=6)
     return cfg, ix
+
+
+def _sub_world(N, D, a, grid, hi_attr, Q, seed):
+    from garfield_amd import synth
+    vec = synth.uniform_int_vectors(N, D, seed)
+    att = synth.uniform_attrs(N, a, seed + 1, hi=hi_attr)
+    qv = synth.uniform_int_vectors(Q, D, seed + 2)
+    sel = synth.log_uniform(Q, 0.002, 0.6, seed + 3)
+    lo, hi = synth.ranges_for_selectivity(Q, a, sel, seed + 4, hi=hi_attr)
+    # edge cases: an empty range, ranges beyond the domain, one covering all
+    lo[0], hi[0] = 5, 4
+    lo[1], hi[1] = hi_attr + 10, hi_attr + 20
+    lo[2], hi[2] = -50, -1
+    lo[3], hi[3] = -5, hi_attr + 5
+    cfg = dict(vectors=vec, attrs=att, grid=grid, R=16, E=2, C=16, queries=qv, lo=lo, hi=hi)
+    ix = synth.build_index(vec, att, grid, 16, 2, 16, seed=seed + 5)
+    return cfg, ix
+
+
+@pytest.fixture(scope="session")
+def world_sub2():
+    """Cells of 15k points (16 sub-cells each), 2 attributes, 64-d integer data."""
+    return _sub_world(60000, 64, 2, [2, 2], 10000, 160, 60)
+
+
+@pytest.fixture(scope="session")
+def world_sub3():
+    """3 attributes (two packed words) with many ties, 2x2x2 cells of 5k points."""
+    return _sub_world(40000, 128, 3, [2, 2, 2], 400, 128, 70)

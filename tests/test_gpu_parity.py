@@ -239,3 +239,61 @@ def test_mfma_bruteforce_all_queries(world32):
     hi = cfg["hi"].astype(np.float32)
     gt, gtd = orc.ground_truth(ix["vectors"], ix["attrs"], cfg["queries"], lo, hi, 10)
     assert orc.recall(ids, gt, gtd) == 1.0
+
+
+def _bf_case(cfg, ix, K, prefilter=1.0):
+    import garfield_amd as gf
+    from oracle import oracle as orc
+    dev = _device(ix)
+    lo, hi, cells, cnt, sel, little = _oracle_pipeline(cfg, ix, prefilter)
+    b = dev.batch(cfg["queries"], lo, hi)
+    b.mark_cells(prefilter)
+    gc, gcnt, glit, gsel = b.get_cells()
+    assert np.array_equal(gcnt, cnt) and np.array_equal(gsel, sel) and np.array_equal(glit, little)
+    if ix["labels"] is not None:
+        b.order_cells(4)
+    gc, gcnt, glit, _ = b.get_cells()
+    ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], ix["R"])
+    ids, dists, st = b.search(L=32, K=K, rl=10, entry_points=ent)
+    ctr = b.get_counters()
+    O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"], ix["cross"])
+    oids, odist, octr = O.search(cfg["queries"], lo, hi, gc, gcnt, glit, ent, 32, K=K, rl=10)
+    b.close()
+    dev.close()
+    return ids, dists, ctr, oids, odist, octr, st
+
+
+@pytest.mark.parametrize("prefilter", [0.0, 0.05, 0.3, 1.0])
+def test_subcell_selectivity(world_sub2, prefilter):
+    """Sub-cell classification + partial scans give the exact selectivity counts."""
+    cfg, ix = world_sub2
+    _print_case("subcell-sel", prefilter=prefilter)
+    dev = _device(ix)
+    lo, hi, cells, cnt, sel, little = _oracle_pipeline(cfg, ix, prefilter)
+    b = dev.batch(cfg["queries"], lo, hi)
+    b.mark_cells(prefilter)
+    gc, gcnt, glit, gsel = b.get_cells()
+    assert np.array_equal(gcnt, cnt)
+    bad = np.nonzero(gsel != sel)[0]
+    assert bad.size == 0, f"selcount differs for q={bad[:5]}: gpu={gsel[bad[:5]]} oracle={sel[bad[:5]]}"
+    assert np.array_equal(glit, little)
+    b.close()
+    dev.close()
+
+
+@pytest.mark.parametrize("K", [5, 10, 16])
+def test_subcell_mfma_bruteforce(world_sub2, K):
+    cfg, ix = world_sub2
+    _print_case("subcell-bf", K=K)
+    ids, dists, ctr, oids, odist, octr, st = _bf_case(cfg, ix, K)
+    assert st.bf_mfma == 1 and st.q_traverse == 0
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+
+
+@pytest.mark.parametrize("prefilter", [0.05, 1.0])
+def test_subcell_three_attributes(world_sub3, prefilter):
+    cfg, ix = world_sub3
+    _print_case("subcell-a3", prefilter=prefilter)
+    ids, dists, ctr, oids, odist, octr, st = _bf_case(cfg, ix, 10, prefilter)
+    assert st.bf_mfma == 1
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
