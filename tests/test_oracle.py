@@ -270,3 +270,60 @@ def test_postfilter_and_empty_routes(tiny):
     ids, dist, ctr = O.search(cfg["queries"], lo, hi, cells, cnt, z, ent, 32, postfilter=int(cnt.min()))
     routed = cnt >= cnt.min()
     assert np.all(ids[routed] == orc.SENTINEL) and np.all(ctr[routed, 7] == 0)
+
+
+def test_centres_hist_closed_form():
+    """Centres = sequential fp32 sums per label / count (np.add.at sums in index
+    order); histogram = label counts per cell, by grid cell or by i / ceil(N/P)."""
+    rng = np.random.default_rng(5)
+    N, D, C, P = 3000, 24, 7, 16
+    x = rng.standard_normal((N, D)).astype(np.float32) * 10
+    lab = rng.integers(0, C, N).astype(np.int32)
+    pid = rng.integers(0, P, N).astype(np.uint32)
+    cen, hist = orc.centres_hist(x, lab, pid, P)
+    s = np.zeros((C, D), np.float32)
+    np.add.at(s, lab, x)
+    cnt = np.bincount(lab, minlength=C).astype(np.float32)
+    assert np.array_equal(cen, s / cnt[:, None])
+    h = np.zeros((P, C), np.uint32)
+    np.add.at(h, (pid, lab), 1)
+    assert np.array_equal(hist, h)
+    _, hc = orc.centres_hist(x, lab, pid, P, contiguous=True)
+    avg = -(-N // P)
+    h2 = np.zeros((P, C), np.uint32)
+    np.add.at(h2, (np.minimum(np.arange(N) // avg, P - 1), lab), 1)
+    assert np.array_equal(hc, h2)
+
+
+def test_ground_truth_brute_force():
+    """Exact filtered kNN: fp64 distances, ties by ascending id, sentinel padding."""
+    rng = np.random.default_rng(6)
+    N, D, a, Q, K = 700, 16, 2, 40, 10
+    x = rng.integers(0, 4, (N, D)).astype(np.float32)        # many distance ties
+    att = rng.integers(0, 50, (N, a)).astype(np.float32)
+    q = rng.integers(0, 4, (Q, D)).astype(np.float32)
+    lo = rng.integers(0, 40, (Q, a)).astype(np.float32)
+    hi = lo + rng.integers(0, 12, (Q, a)).astype(np.float32)
+    ids, dist = orc.ground_truth(x, att, q, lo, hi, K)
+    for i in range(Q):
+        ok = np.all((att >= lo[i]) & (att <= hi[i]), axis=1)
+        cand = np.nonzero(ok)[0]
+        d = np.sum((x[cand].astype(np.float64) - q[i]) ** 2, axis=1)
+        order = np.lexsort((cand, d))[:K]
+        n = len(order)
+        assert np.array_equal(ids[i, :n], cand[order])
+        assert np.array_equal(dist[i, :n], d[order])
+        assert np.all(ids[i, n:] == orc.SENTINEL) and np.all(np.isinf(dist[i, n:]))
+
+
+def test_recall_known_answers():
+    gt = np.array([[1, 2, 3], [4, 5, 6]], np.uint32)
+    gtd = np.array([[1.0, 2.0, 3.0], [1.0, 1.0, 1.0]])
+    res = np.array([[3, 2, 9], [6, 7, 8]], np.uint32)
+    assert orc.recall(res, gt, gtd) == pytest.approx((2 / 3 + 1 / 3) / 2)
+    # tie-aware: id 9 at distance 3.0 (= the 3rd ground-truth distance) counts
+    rd = np.array([[3.0, 2.0, 3.0], [1.0, 5.0, 1.0]])
+    assert orc.recall(res, gt, gtd, rd, tie_aware=True) == pytest.approx((1.0 + 2 / 3) / 2)
+    # an empty ground truth counts as recall 1
+    e = np.full((1, 3), orc.SENTINEL, np.uint32)
+    assert orc.recall(e, e, np.full((1, 3), np.inf)) == 1.0
