@@ -91,6 +91,7 @@ struct gf_index {
     DevBuf<char> vec;
     DevBuf<float> attrs, l_q, r_q, cnorm;
     DevBuf<uint32_t> graph, cross, offset, gidx, lrow, grid, doff, hist;
+    DevBuf<uint32_t> entry_ref;   // the reference's entry-point draw, made on first use
     DevBuf<uint32_t> tile_cell, tile_row0, tile_n;
     DevBuf<uint16_t> centres;
     uint32_t ntiles = 0;
@@ -133,6 +134,7 @@ struct gf_batch {
     DevBuf<uint32_t> bcnt, bstart, pcnt, bq, nsub, part_off, icnt, ioff, bfq;
     DevBuf<gf::BfItem> items;
     DevBuf<uint64_t> part;
+    DevBuf<unsigned long long> stats;
     DevBuf<float> qf32, qnorm, lo, hi, cdist, out_dist;
     DevBuf<uint16_t> q16, q16v;
     DevBuf<uint32_t> cells, counts, little, selcount, cellq, ccount, cstart, cfill, topk;
@@ -589,7 +591,7 @@ gf_status gf_batch_create(gf_index* ix, const float* queries, uint32_t Q, const 
         b->counts.alloc(Q);
         b->little.alloc(Q);
         b->selcount.alloc(Q);
-        b->tot.alloc(8);
+        b->tot.alloc(16);
         if (!ix->sub) {
             b->cellq.alloc(size_t(Q) * ix->P);
             b->ccount.alloc(ix->P);
@@ -679,33 +681,20 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         hipStream_t st = ix->stream;
         const uint32_t Q = b->Q, R = ix->R;
 
-        // Entry points: the caller's, or the reference's draw.
-        std::vector<uint32_t> ent(R);
-        if (opts->entry_points) std::copy(opts->entry_points, opts->entry_points + R, ent.begin());
-        else entry_points_ref(ix->N, ix->P, R, ent.data());
-        b->entry.upload(ent);
-
-        // Schedule (gpu_graph.cu:12485-12493): traversal queries by descending
-        // cell count, then brute-force queries by descending cell count.
-        std::vector<uint32_t> cnt(Q), lit(Q);
-        GF_HIP(hipMemcpyAsync(cnt.data(), b->counts.p, Q * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-        GF_HIP(hipMemcpyAsync(lit.data(), b->little.p, Q * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-        GF_HIP(hipStreamSynchronize(st));
-        std::vector<uint32_t> tq, bq;
-        uint32_t nempty = 0;
-        for (uint32_t q = 0; q < Q; ++q) {
-            if (cnt[q] < opts->postfilter && cnt[q] != lit[q]) tq.push_back(q);
-            else if (lit[q] > 0) bq.push_back(q);
-            else ++nempty;
+        // Entry points: the caller's, or the reference's draw (computed once per index).
+        if (opts->entry_points) {
+            b->entry.upload(opts->entry_points, R);
+        } else {
+            if (!ix->entry_ref.n) {
+                std::vector<uint32_t> ent(R);
+                entry_points_ref(ix->N, ix->P, R, ent.data());
+                ix->entry_ref.upload(ent);
+            }
+            if (b->entry.n < R) b->entry.alloc(R);
+            GF_HIP(hipMemcpyAsync(b->entry.p, ix->entry_ref.p, R * sizeof(uint32_t), hipMemcpyDeviceToDevice, st));
         }
-        auto by_count = [&](uint32_t x, uint32_t y) { return cnt[x] != cnt[y] ? cnt[x] > cnt[y] : x < y; };
-        std::sort(tq.begin(), tq.end(), by_count);
-        std::sort(bq.begin(), bq.end(), by_count);
-        std::vector<uint32_t> sched(tq);
-        sched.insert(sched.end(), bq.begin(), bq.end());
-        if (sched.empty()) sched.push_back(0);
-        b->sched.upload(sched);
         ensure_out(*b, K);
+        if (b->sched.n < Q) b->sched.alloc(Q);
 
         const uint32_t hsize = std::max<uint32_t>(256, next_pow2(2 * (L + gf::kXSlots + 4 * R)));
         uint32_t hbits = 0;
@@ -714,6 +703,9 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         const uint32_t lds = Lpad * 8 + gf::kXSlots * 8 + 128 * 4 + hsize * 4;
         GF_REQUIRE(lds <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
 
+        // device scalars: tot[2] pairs, [3] fits, [4] items, [8..10] traversal /
+        // brute-force / empty counts, [12..13] traversal range, [14..15] brute-force range
+        uint32_t* tot = b->tot.p;
         gf::TravArgs a{};
         a.vec = ix->vec.p;
         a.rowbytes = ix->rowbytes;
@@ -736,6 +728,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         a.cells = b->cells.p;
         a.counts = b->counts.p;
         a.little = b->little.p;
+        a.sched = b->sched.p;
         a.entry = b->entry.p;
         a.out_ids = b->out_ids.p;
         a.out_dist = b->out_dist.p;
@@ -747,10 +740,9 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         // Brute-force route on MFMA when vectors and queries are int8-exact:
         // work items of (sub-cell, <= 64 queries whose range reaches it),
         // scheduled on the device.
-        const bool gemm = ix->i8 && b->i8 && !bq.empty() && K <= gf::kBfKMax;
+        const bool gemm = ix->i8 && b->i8 && K <= gf::kBfKMax;
         const uint32_t NS = ix->NS;
         if (gemm) {
-            b->bfq.upload(bq);
             if (!b->bcnt.n) {
                 b->bcnt.alloc(NS); b->bstart.alloc(NS); b->icnt.alloc(NS); b->ioff.alloc(NS);
                 b->nsub.alloc(Q); b->part_off.alloc(Q); b->pcnt.alloc(Q);
@@ -769,7 +761,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             sc.Q = Q; sc.postfilter = opts->postfilter; sc.counts = b->counts.p;
             sc.little = b->little.p; sc.lo = b->lo.p; sc.hi = b->hi.p; sc.nsub = b->nsub.p; sc.bcnt = b->bcnt.p;
             sc.bstart = b->bstart.p; sc.bq = b->bq.p;
-            sc.ok = b->tot.p + 3;
+            sc.ok = tot + 3; sc.nbf = tot + 9;
             GF_HIP(hipMemsetAsync(b->nsub.p, 0, size_t(Q) * sizeof(uint32_t), st));
             GF_HIP(hipMemsetAsync(b->pcnt.p, 0, size_t(Q) * sizeof(uint32_t), st));
             GF_HIP(hipMemsetAsync(b->gbound.p, 0xFF, size_t(Q) * sizeof(uint32_t), st));
@@ -777,63 +769,64 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             GF_HIP(gf::launch_scan_small(b->bcnt.p, NS, b->bstart.p, st));
             GF_HIP(gf::launch_scan_small(b->nsub.p, Q, b->part_off.p, st));
             GF_HIP(gf::launch_total(b->nsub.p, b->part_off.p, Q, uint32_t(std::min<size_t>(b->bq.n, UINT32_MAX)), K,
-                                    b->part.n, b->tot.p + 2, st));
+                                    b->part.n, tot + 2, st));
             GF_HIP(gf::launch_bfsched(sc, true, st));
-            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bstart.p, NS, b->icnt.p, b->ioff.p, b->items.p, b->tot.p + 4,
-                                      b->tot.p + 3, false, st));
+            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bstart.p, NS, b->icnt.p, b->ioff.p, b->items.p, tot + 4, tot + 3,
+                                      false, st));
             GF_HIP(gf::launch_scan_small(b->icnt.p, NS, b->ioff.p, st));
-            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bstart.p, NS, b->icnt.p, b->ioff.p, b->items.p, b->tot.p + 4,
-                                      b->tot.p + 3, true, st));
+            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bstart.p, NS, b->icnt.p, b->ioff.p, b->items.p, tot + 4, tot + 3,
+                                      true, st));
             gf::BfGemmArgs ga{};
             ga.sa = sub_args(*ix);
             ga.vt = ix->vt.p; ga.tnorm = ix->tnorm.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p;
-            ga.hi = b->hi.p; ga.items = b->items.p; ga.nitems = b->tot.p + 4; ga.bq = b->bq.p; ga.pcnt = b->pcnt.p;
-            ga.part_off = b->part_off.p; ga.part = b->part.p; ga.gbound = b->gbound.p; ga.ok = b->tot.p + 3;
+            ga.hi = b->hi.p; ga.items = b->items.p; ga.nitems = tot + 4; ga.bq = b->bq.p; ga.pcnt = b->pcnt.p;
+            ga.part_off = b->part_off.p; ga.part = b->part.p; ga.gbound = b->gbound.p; ga.ok = tot + 3;
             ga.K = K; ga.D = ix->D;
             GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu) * 3u, st));
             gf::BfFinalArgs fa{};
-            fa.bfq = b->bfq.p; fa.nbf = uint32_t(bq.size()); fa.part_off = b->part_off.p; fa.pcnt = b->pcnt.p;
-            fa.ok = b->tot.p + 3; fa.part = b->part.p; fa.counts = b->counts.p; fa.cells = b->cells.p;
+            fa.bfq = b->sched.p; fa.srange = tot + 14; fa.part_off = b->part_off.p; fa.pcnt = b->pcnt.p;
+            fa.ok = tot + 3; fa.part = b->part.p; fa.counts = b->counts.p; fa.cells = b->cells.p;
             fa.offset = ix->offset.p; fa.selcount = b->selcount.p; fa.gidx = ix->gidx.p; fa.out_ids = b->out_ids.p;
             fa.out_dist = b->out_dist.p; fa.counters = b->counters.p; fa.K = K; fa.P = ix->P;
-            GF_HIP(gf::launch_bf_final(fa, st));
+            GF_HIP(gf::launch_bf_final(fa, Q, st));
         };
 
+        // Schedule (gpu_graph.cu:12485-12493) on the device.
+        gf::SchedArgs sa{};
+        sa.Q = Q; sa.P = ix->P; sa.postfilter = opts->postfilter; sa.counts = b->counts.p; sa.little = b->little.p;
+        sa.sched = b->sched.p; sa.tot = tot + 8; sa.ranges = tot + 12;
         GF_HIP(hipMemsetAsync(b->counters.p, 0, size_t(Q) * GF_NCOUNTERS * sizeof(uint32_t), st));
         GF_HIP(gf::launch_fill_results(b->out_ids.p, b->out_dist.p, Q * K, st));
+        GF_HIP(gf::launch_sched(sa, st));
         hipEvent_t ev[3];
         for (auto& e : ev) GF_HIP(hipEventCreate(&e));
         GF_HIP(hipEventRecord(ev[0], st));
         gf::TravArgs at = a;
-        at.sched = b->sched.p;
-        at.nsched = uint32_t(tq.size());
-        GF_HIP(gf::launch_traverse(ix->rs, at, lds, st));
+        at.srange = tot + 12;
+        GF_HIP(gf::launch_traverse(ix->rs, at, lds, Q, st));
         GF_HIP(hipEventRecord(ev[1], st));
-        gf::TravArgs ab = a;
-        ab.sched = b->sched.p + tq.size();
-        ab.nsched = uint32_t(bq.size());
         if (gemm) {
             launch_gemm();
         } else {
-            GF_HIP(gf::launch_bruteforce(ix->rs, ab, st));
+            gf::TravArgs ab = a;
+            ab.srange = tot + 14;
+            GF_HIP(gf::launch_bruteforce(ix->rs, ab, Q, st));
         }
         GF_HIP(hipEventRecord(ev[2], st));
         GF_HIP(hipEventSynchronize(ev[2]));
-        uint32_t gtot[3] = {0, 1, 0};
-        if (gemm) {
-            GF_HIP(hipMemcpy(gtot, b->tot.p + 2, sizeof(gtot), hipMemcpyDeviceToHost));
-            if (!gtot[1]) {
-                // the pair lists outgrew their buffers: grow them and run the brute force again
-                const size_t cap = size_t(gtot[0]) + gtot[0] / 4 + 1024;
-                b->bq.alloc(cap); b->part.alloc(cap * K);
-                b->items.alloc(cap / gf::kBfQB + NS + 1);
-                GF_HIP(hipEventRecord(ev[1], st));
-                launch_gemm();
-                GF_HIP(hipEventRecord(ev[2], st));
-                GF_HIP(hipEventSynchronize(ev[2]));
-                GF_HIP(hipMemcpy(gtot, b->tot.p + 2, sizeof(gtot), hipMemcpyDeviceToHost));
-                GF_REQUIRE(gtot[1], GF_E_STATE, "brute-force schedule does not fit after growing");
-            }
+        uint32_t dt[16];
+        GF_HIP(hipMemcpy(dt, tot, sizeof(dt), hipMemcpyDeviceToHost));
+        if (gemm && !dt[3]) {
+            // the pair lists outgrew their buffers: grow them and run the brute force again
+            const size_t cap = size_t(dt[2]) + dt[2] / 4 + 1024;
+            b->bq.alloc(cap); b->part.alloc(cap * K);
+            b->items.alloc(cap / gf::kBfQB + NS + 1);
+            GF_HIP(hipEventRecord(ev[1], st));
+            launch_gemm();
+            GF_HIP(hipEventRecord(ev[2], st));
+            GF_HIP(hipEventSynchronize(ev[2]));
+            GF_HIP(hipMemcpy(dt, tot, sizeof(dt), hipMemcpyDeviceToHost));
+            GF_REQUIRE(dt[3], GF_E_STATE, "brute-force schedule does not fit after growing");
         }
         float t_tr = 0, t_bf = 0;
         GF_HIP(hipEventElapsedTime(&t_tr, ev[0], ev[1]));
@@ -843,58 +836,45 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         GF_HIP(hipMemcpy(ids, b->out_ids.p, size_t(Q) * K * sizeof(uint32_t), hipMemcpyDeviceToHost));
         if (dists) GF_HIP(hipMemcpy(dists, b->out_dist.p, size_t(Q) * K * sizeof(float), hipMemcpyDeviceToHost));
         if (stats) {
-            std::vector<uint32_t> ctr(size_t(Q) * GF_NCOUNTERS);
-            GF_HIP(hipMemcpy(ctr.data(), b->counters.p, ctr.size() * sizeof(uint32_t), hipMemcpyDeviceToHost));
+            if (b->stats.n < 16) b->stats.alloc(16);
+            GF_HIP(hipMemsetAsync(b->stats.p, 0, 16 * sizeof(unsigned long long), st));
+            gf::StatsArgs sa2{};
+            sa2.Q = Q; sa2.NS = gemm ? NS : 0; sa2.counters = b->counters.p; sa2.bcnt = gemm ? b->bcnt.p : nullptr;
+            sa2.ssize = ix->ssize.p; sa2.stile = ix->stile.p; sa2.out = b->stats.p;
+            GF_HIP(gf::launch_stats(sa2, st));
+            unsigned long long sm[16];
+            GF_HIP(hipMemcpyAsync(sm, b->stats.p, sizeof(sm), hipMemcpyDeviceToHost, st));
+            GF_HIP(hipStreamSynchronize(st));
             std::memset(stats, 0, sizeof(*stats));
             stats->ms_traverse = t_tr;
             stats->ms_bruteforce = t_bf;
             stats->ms_total = double(t_tr) + double(t_bf);
-            stats->q_traverse = uint32_t(tq.size());
-            stats->q_bruteforce = uint32_t(bq.size());
-            stats->q_empty = nempty;
-            for (uint32_t q = 0; q < Q; ++q) {
-                const uint32_t* c = &ctr[size_t(q) * GF_NCOUNTERS];
-                stats->n_expand += c[gf::C_EXPAND];
-                stats->n_dist += c[gf::C_DIST];
-                stats->n_attr += c[gf::C_ATTR];
-                stats->n_cross += c[gf::C_CROSS];
-                stats->n_lrow += c[gf::C_LROW];
-                stats->n_scan += c[gf::C_SCAN];
-                stats->n_pass += c[gf::C_PASS];
-            }
+            stats->q_traverse = dt[8];
+            stats->q_bruteforce = dt[9];
+            stats->q_empty = dt[10];
+            stats->n_expand = sm[0]; stats->n_dist = sm[1]; stats->n_attr = sm[2]; stats->n_cross = sm[3];
+            stats->n_lrow = sm[4]; stats->n_scan = sm[5]; stats->n_pass = sm[6];
             // Algorithmic bytes: what each kernel must read from HBM given
             // its counters (rows gathered, graph rows, attributes, cross-edge
             // slices, local-id lookups) plus its result writes.
-            uint64_t t_dist = 0, b_dist = 0;
-            for (uint32_t q = 0; q < Q; ++q) {
-                const uint32_t* c = &ctr[size_t(q) * GF_NCOUNTERS];
-                if (c[gf::C_ROUTE] == 1) t_dist += c[gf::C_DIST];
-                else b_dist += c[gf::C_DIST];
-            }
-            stats->bytes_traverse = double(t_dist) * ix->rowbytes + double(stats->n_expand) * R * 4.0 +
+            const double t_dist = double(sm[7]), b_dist = double(sm[8]);
+            stats->bytes_traverse = t_dist * ix->rowbytes + double(stats->n_expand) * R * 4.0 +
                                     double(stats->n_attr) * ix->a * 4.0 + double(stats->n_cross) * ix->E * 4.0 +
-                                    double(stats->n_lrow) * 4.0 + double(tq.size()) * (K * 8.0 + ix->P * 4.0);
-            if (gemm) {
-                // Algorithmic work of the item schedule: every pair (query,
-                // sub-cell) costs 2 D ops per point; every item streams its
-                // sub-cell's tiles once; the final merge reads all partials.
-                std::vector<uint32_t> bc(NS);
-                GF_HIP(hipMemcpy(bc.data(), b->bcnt.p, NS * sizeof(uint32_t), hipMemcpyDeviceToHost));
+                                    double(stats->n_lrow) * 4.0 + double(dt[8]) * (K * 8.0 + ix->P * 4.0);
+            if (gemm && dt[9]) {
+                // Item schedule: every (query, sub-cell) pair costs 2 D ops per
+                // point; every item streams its sub-cell's tiles once; the final
+                // merge reads the appended keys.
                 const double tile_bytes = (ix->D / 64) * 1024.0 + 32 * 4.0 + 16.0 * (1 + ix->AW) * 4.0;
-                double ops = 0.0, bytes = 0.0;
-                for (uint32_t sc = 0; sc < NS; ++sc) {
-                    ops += 2.0 * ix->D * double(bc[sc]) * ix->ssize_h[sc];
-                    bytes += double((bc[sc] + gf::kBfQB - 1) / gf::kBfQB) * (ix->stile_h[sc + 1] - ix->stile_h[sc]) *
-                             tile_bytes;
-                }
-                stats->bytes_bruteforce = bytes + double(gtot[0]) * K * 16.0;
-                stats->ops_bruteforce = ops;
+                stats->ops_bruteforce = 2.0 * ix->D * double(sm[9]);
+                stats->bytes_bruteforce = double(sm[10]) * tile_bytes + double(dt[9]) * K * 16.0;
+                stats->bf_mfma = 1;
             } else {
-                stats->bytes_bruteforce = double(stats->n_scan) * ix->a * 4.0 + double(b_dist) * ix->rowbytes +
-                                          double(bq.size()) * (K * 8.0 + ix->P * 4.0);
-                stats->ops_bruteforce = 3.0 * double(b_dist) * ix->D;
+                stats->bytes_bruteforce = double(stats->n_scan) * ix->a * 4.0 + b_dist * ix->rowbytes +
+                                          double(dt[9]) * (K * 8.0 + ix->P * 4.0);
+                stats->ops_bruteforce = 3.0 * b_dist * ix->D;
+                stats->bf_mfma = 0;
             }
-            stats->bf_mfma = gemm ? 1u : 0u;
         }
     });
 }

@@ -56,8 +56,8 @@ struct TravArgs {
     const uint32_t* cells;    // Q*P ordered cell lists
     const uint32_t* counts;   // Q
     const uint32_t* little;   // Q
-    const uint32_t* sched;    // queries handled by this launch
-    uint32_t nsched;
+    const uint32_t* sched;    // schedule: traversal queries, then brute-force queries
+    const uint32_t* srange;   // device [begin, end) of this launch's queries in sched
     const uint32_t* entry;    // R entry ids
     uint32_t* out_ids;        // Q*K
     float* out_dist;          // Q*K
@@ -110,8 +110,8 @@ struct BfGemmArgs {
     uint32_t K, D;
 };
 struct BfFinalArgs {
-    const uint32_t* bfq;       // brute-force queries
-    uint32_t nbf;
+    const uint32_t* bfq;       // schedule
+    const uint32_t* srange;    // device [begin, end) of the brute-force queries in bfq
     const uint32_t* part_off;  // per query: first pair (partial area = pairs * K keys)
     const uint32_t* pcnt;      // keys appended for each query
     const uint32_t* ok;
@@ -151,14 +151,40 @@ struct BfSchedArgs {
     const uint32_t* bstart;    // exclusive scan of bcnt (pass 2)
     uint32_t* bq;
     const uint32_t* ok;        // bq and part are large enough (pass 2)
+    const uint32_t* nbf;       // device count of brute-force queries (0: nothing to do)
+};
+// Query schedule (gpu_graph.cu:12485-12493): traversal queries by descending
+// cell count, then brute-force queries.  tot[0..2] = traversal, brute-force,
+// empty query counts; ranges[0..3] = traversal [begin, end), brute force [begin, end).
+struct SchedArgs {
+    uint32_t Q, P, postfilter;
+    const uint32_t* counts;
+    const uint32_t* little;
+    uint32_t* sched;
+    uint32_t* tot;
+    uint32_t* ranges;
+};
+// Sums of the per-query counters and of the brute-force schedule for the
+// search statistics: out[0..6] counter sums, out[7] traversal DIST, out[8]
+// brute-force DIST, out[9] sum of pairs x sub-cell size, out[10] sum of
+// items x tiles per item.
+struct StatsArgs {
+    uint32_t Q, NS;
+    const uint32_t* counters;
+    const uint32_t* bcnt;      // null without the MFMA schedule
+    const uint32_t* ssize;
+    const uint32_t* stile;
+    unsigned long long* out;   // zeroed before
 };
 
 // Kernel launchers (gf_kernels.hip).  All are asynchronous on `st`.
-hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds_bytes, hipStream_t st);
-hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, hipStream_t st);
+// The search launches take a grid of `grid` workgroups (an upper bound of
+// their query range, which is read on the device).
+hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds_bytes, uint32_t grid, hipStream_t st);
+hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, uint32_t grid, hipStream_t st);
 hipError_t launch_fill_results(uint32_t* ids, float* dist, uint32_t n, hipStream_t st);
 hipError_t launch_bf_i8(const BfGemmArgs& a, uint32_t nwg, hipStream_t st);
-hipError_t launch_bf_final(const BfFinalArgs& a, hipStream_t st);
+hipError_t launch_bf_final(const BfFinalArgs& a, uint32_t grid, hipStream_t st);
 hipError_t launch_tile_i8(const float* vec_cm, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
                           int8_t* vt, int32_t* tnorm, hipStream_t st);
 hipError_t launch_subsel(const SubSelArgs& a, hipStream_t st);
@@ -168,6 +194,8 @@ hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bstart, uint32_t
                           hipStream_t st);
 // out[0] = start[n-1] + cnt[n-1] (total of an exclusive scan); out[1] = out[0] <= cap
 // (with cap2 != 0 also out[0] * mul <= cap2).
+hipError_t launch_sched(const SchedArgs& a, hipStream_t st);
+hipError_t launch_stats(const StatsArgs& a, hipStream_t st);
 hipError_t launch_total(const uint32_t* cnt, const uint32_t* start, uint32_t n, uint32_t cap, uint32_t mul,
                         uint64_t cap2, uint32_t* out, hipStream_t st);
 hipError_t launch_q_i8(const float* q, uint32_t Q, uint32_t D, int8_t* q8, int32_t* nq, hipStream_t st);

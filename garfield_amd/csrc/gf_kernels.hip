@@ -341,7 +341,9 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
     uint32_t* S = reinterpret_cast<uint32_t*>(W + kXSlots);  // 128 row list
     uint32_t* H = S + 128;                              // visited set
     const uint32_t lane = lane_id();
-    const uint32_t q = p.sched[blockIdx.x];
+    const uint32_t si = p.srange[0] + blockIdx.x;
+    if (si >= p.srange[1]) return;
+    const uint32_t q = p.sched[si];
     const uint32_t hsize = 1u << p.hbits;
     const uint32_t L = p.L, R = p.R, P = p.P, E = p.E;
 
@@ -561,7 +563,9 @@ __global__ __launch_bounds__(64) void k_bruteforce(TravArgs p) {
     __shared__ uint32_t S[64 * U + 64];
     __shared__ uint64_t T[64];
     const uint32_t lane = lane_id();
-    const uint32_t q = p.sched[blockIdx.x];
+    const uint32_t si = p.srange[0] + blockIdx.x;
+    if (si >= p.srange[1]) return;
+    const uint32_t q = p.sched[si];
     const uint32_t K = p.K, P = p.P;
     QReg<F16, CPL> qv;
     load_query<F16, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
@@ -1152,7 +1156,7 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
     const SubArgs& sa = p.sa;
     const uint32_t s = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
     if (fill && !*p.ok) return;
-    if (sa.ssize[s] == 0) {
+    if (sa.ssize[s] == 0 || *p.nbf == 0) {
         if (!fill && tid == 0) p.bcnt[s] = 0;
         return;
     }
@@ -1194,6 +1198,76 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
         for (uint32_t i = tid; i < fn; i += 256u) atomicAdd(&p.nsub[fq[i]], 1u);
         if (tid == 0) p.bcnt[s] = running;
     }
+}
+
+// Query schedule on the device, one workgroup: routes (traversal if
+// counts < postfilter and counts != little; brute force if otherwise little >
+// 0; else empty), a counting sort of the traversal queries by descending cell
+// count (order inside one count is arbitrary: it only affects load balance),
+// then the brute-force queries.
+__global__ __launch_bounds__(1024) void k_sched(SchedArgs p) {
+    extern __shared__ uint32_t bins[];   // P + 1 counters, then P + 1 offsets
+    __shared__ uint32_t nbf, nempty, bffill;
+    const uint32_t tid = threadIdx.x, nb = p.P + 1;
+    uint32_t* off = bins + nb;
+    for (uint32_t i = tid; i < nb; i += blockDim.x) bins[i] = 0;
+    if (tid == 0) { nbf = 0; nempty = 0; bffill = 0; }
+    __syncthreads();
+    auto route = [&](uint32_t q) -> uint32_t {
+        const uint32_t c = p.counts[q], l = p.little[q];
+        if (c < p.postfilter && c != l) return 1u;
+        return l > 0 ? 2u : 0u;
+    };
+    for (uint32_t q = tid; q < p.Q; q += blockDim.x) {
+        const uint32_t r = route(q);
+        if (r == 1) atomicAdd(&bins[min(p.counts[q], p.P)], 1u);
+        else if (r == 2) atomicAdd(&nbf, 1u);
+        else atomicAdd(&nempty, 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t acc = 0;
+        for (uint32_t i = nb; i-- > 0;) { off[i] = acc; acc += bins[i]; bins[i] = 0; }
+        p.tot[0] = acc; p.tot[1] = nbf; p.tot[2] = nempty;
+        p.ranges[0] = 0; p.ranges[1] = acc; p.ranges[2] = acc; p.ranges[3] = acc + nbf;
+    }
+    __syncthreads();
+    const uint32_t ntrav = p.ranges[1];
+    for (uint32_t q = tid; q < p.Q; q += blockDim.x) {
+        const uint32_t r = route(q);
+        if (r == 1) {
+            const uint32_t c = min(p.counts[q], p.P);
+            p.sched[off[c] + atomicAdd(&bins[c], 1u)] = q;
+        } else if (r == 2) {
+            p.sched[ntrav + atomicAdd(&bffill, 1u)] = q;
+        }
+    }
+}
+
+// Statistics sums (see StatsArgs), one thread per query and per sub-cell.
+__global__ __launch_bounds__(256) void k_stats(StatsArgs p) {
+    __shared__ unsigned long long acc[11];
+    const uint32_t tid = threadIdx.x, i = blockIdx.x * 256u + tid;
+    if (tid < 11) acc[tid] = 0;
+    __syncthreads();
+    if (i < p.Q) {
+        const uint32_t* c = p.counters + size_t(i) * GF_NCOUNTERS;
+        const uint32_t map[7] = {C_EXPAND, C_DIST, C_ATTR, C_CROSS, C_LROW, C_SCAN, C_PASS};
+#pragma unroll
+        for (int k = 0; k < 7; ++k)
+            if (c[map[k]]) atomicAdd(&acc[k], (unsigned long long)c[map[k]]);
+        if (c[C_ROUTE] == 1) atomicAdd(&acc[7], (unsigned long long)c[C_DIST]);
+        if (c[C_ROUTE] == 2) atomicAdd(&acc[8], (unsigned long long)c[C_DIST]);
+    }
+    if (p.bcnt && i < p.NS) {
+        const uint32_t n = p.bcnt[i];
+        if (n) {
+            atomicAdd(&acc[9], (unsigned long long)n * p.ssize[i]);
+            atomicAdd(&acc[10], (unsigned long long)((n + kBfQB - 1) / kBfQB) * (p.stile[i + 1] - p.stile[i]));
+        }
+    }
+    __syncthreads();
+    if (tid < 11 && acc[tid]) atomicAdd(&p.out[tid], acc[tid]);
 }
 
 // Work items of the MFMA brute force: ceil(n / 64) blocks per sub-cell.
@@ -1423,7 +1497,9 @@ __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
     __shared__ uint64_t T[64];
     const uint32_t lane = lane_id();
     if (!*p.ok) return;
-    const uint32_t q = p.bfq[blockIdx.x];
+    const uint32_t si = p.srange[0] + blockIdx.x;
+    if (si >= p.srange[1]) return;
+    const uint32_t q = p.bfq[si];
     const uint32_t K = p.K;
     const uint32_t n = p.pcnt[q];
     const uint64_t* part = p.part + size_t(p.part_off[q]) * K;
@@ -1514,15 +1590,15 @@ __global__ __launch_bounds__(64) void k_q_i8(const float* q, uint32_t D, int8_t*
 }
 
 template <bool F16, int LPR, int CPL>
-hipError_t launch_trav_t(const TravArgs& a, uint32_t lds, hipStream_t st) {
-    if (a.nsched == 0) return hipSuccess;
-    hipLaunchKernelGGL((k_traverse<F16, LPR, CPL>), dim3(a.nsched), dim3(64), lds, st, a);
+hipError_t launch_trav_t(const TravArgs& a, uint32_t lds, uint32_t grid, hipStream_t st) {
+    if (grid == 0) return hipSuccess;
+    hipLaunchKernelGGL((k_traverse<F16, LPR, CPL>), dim3(grid), dim3(64), lds, st, a);
     return hipGetLastError();
 }
 template <bool F16, int LPR, int CPL>
-hipError_t launch_bf_t(const TravArgs& a, hipStream_t st) {
-    if (a.nsched == 0) return hipSuccess;
-    hipLaunchKernelGGL((k_bruteforce<F16, LPR, CPL>), dim3(a.nsched), dim3(64), 0, st, a);
+hipError_t launch_bf_t(const TravArgs& a, uint32_t grid, hipStream_t st) {
+    if (grid == 0) return hipSuccess;
+    hipLaunchKernelGGL((k_bruteforce<F16, LPR, CPL>), dim3(grid), dim3(64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -1551,8 +1627,8 @@ RowShape row_shape(uint32_t D, bool f16) {
     if (rs.lpr == 64 && rs.cpl == 3) return X<F16, 64, 3>;                     \
     if (rs.lpr == 64 && rs.cpl == 4) return X<F16, 64, 4>;
 
-hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds, hipStream_t st) {
-#define X(F, L_, C_) launch_trav_t<F, L_, C_>(a, lds, st)
+hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds, uint32_t grid, hipStream_t st) {
+#define X(F, L_, C_) launch_trav_t<F, L_, C_>(a, lds, grid, st)
 #define XT(F, L_, C_) X(F, L_, C_)
     if (rs.f16) {
         if (rs.lpr == 8 && rs.cpl == 1) return XT(true, 8, 1);
@@ -1574,8 +1650,8 @@ hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds, 
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, hipStream_t st) {
-#define XT(F, L_, C_) launch_bf_t<F, L_, C_>(a, st)
+hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, uint32_t grid, hipStream_t st) {
+#define XT(F, L_, C_) launch_bf_t<F, L_, C_>(a, grid, st)
     if (rs.f16) {
         if (rs.lpr == 8 && rs.cpl == 1) return XT(true, 8, 1);
         if (rs.lpr == 16 && rs.cpl == 1) return XT(true, 16, 1);
@@ -1620,9 +1696,22 @@ hipError_t launch_bf_i8(const BfGemmArgs& a, uint32_t nwg, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_bf_final(const BfFinalArgs& a, hipStream_t st) {
-    if (!a.nbf) return hipSuccess;
-    hipLaunchKernelGGL(k_bf_final, dim3(a.nbf), dim3(64), 0, st, a);
+hipError_t launch_bf_final(const BfFinalArgs& a, uint32_t grid, hipStream_t st) {
+    if (!grid) return hipSuccess;
+    hipLaunchKernelGGL(k_bf_final, dim3(grid), dim3(64), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_sched(const SchedArgs& a, hipStream_t st) {
+    if (!a.Q) return hipSuccess;
+    hipLaunchKernelGGL(k_sched, dim3(1), dim3(1024), size_t(a.P + 1) * 2 * sizeof(uint32_t), st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_stats(const StatsArgs& a, hipStream_t st) {
+    const uint32_t n = a.Q > a.NS ? a.Q : a.NS;
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_stats, dim3((n + 255) / 256), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
