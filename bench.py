@@ -49,6 +49,12 @@ def main():
     ap.add_argument("--L", type=int, default=0, help="fixed L (skip the sweep)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-traverse", action="store_true", help="skip the traversal roofline line")
+    ap.add_argument("--traverse-L", type=int, default=100)
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="after the run, stream this many MiB through y = x + 1 (fp32) three times: a kernel "
+                         "of known traffic (reads and writes that many bytes) to scale rocprofv3's "
+                         "FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the query path shards over "
@@ -125,7 +131,7 @@ def main():
     for _ in range(args.warmup):
         step(pf, L)
     torch.cuda.synchronize()
-    ms_a_sum = ms_b_sum = ms_tr = ms_bf = bytes_tr = bytes_bf = ops_bf = 0.0
+    ms_a_sum = ms_b_sum = ms_tr = ms_bf = ms_bfk = bytes_tr = bytes_bf = ops_bf = 0.0
     last = None
     t = time.perf_counter()
     for _ in range(args.steps):
@@ -137,6 +143,7 @@ def main():
         bytes_tr += st.bytes_traverse
         bytes_bf += st.bytes_bruteforce
         ops_bf += st.ops_bruteforce
+        ms_bfk += st.ms_bf_kernel
         last = st
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t
@@ -152,7 +159,8 @@ def main():
         dom, dom_bytes, dom_ms, mfma = "k_traverse", bytes_tr, ms_tr, False
     else:
         mfma = bool(last.bf_mfma)
-        dom, dom_bytes, dom_ms = ("k_bf_i8" if mfma else "k_bruteforce"), bytes_bf, ms_bf
+        # the MFMA kernel alone (its schedule and the final merge are timed in ms_bruteforce)
+        dom, dom_bytes, dom_ms = ("k_bf_i8" if mfma else "k_bruteforce"), bytes_bf, (ms_bfk if mfma else ms_bf)
     if mfma:
         achieved = (ops_bf / K) / (dom_ms / K / 1e3) / 1e12 if dom_ms > 0 else 0.0
         roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
@@ -173,6 +181,21 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, ix, b, L, pf, args)
+
+    # The traversal kernel priced against HBM on the same batch: every query
+    # traversed (prefilter 0), at the sweep's L for recall >= 0.5 or L=100.
+    trav = None
+    if not args.no_traverse:
+        Lt = args.traverse_L
+        _, _, stt, _, _ = step(0.0, Lt)
+        ms_t = stt.ms_traverse
+        gbs = stt.bytes_traverse / (ms_t / 1e3) / 1e9 if ms_t > 0 else 0.0
+        trav = {"bound": "hbm", "kernel": "k_traverse", "L": Lt, "prefilter": 0.0,
+                "queries": stt.q_traverse, "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": round(stt.bytes_traverse),
+                "ms_per_launch": round(ms_t, 4), "traffic": None}
+        log(f"traversal at L={Lt}: {ms_t:.2f} ms, {gbs:.0f} GB/s algorithmic ({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+
 
     out = {
         "metric": METRIC,
@@ -198,9 +221,18 @@ def main():
             "q_traverse": last.q_traverse, "q_bruteforce": last.q_bruteforce, "q_empty": last.q_empty,
         },
         "roofline": roofline,
+        "roofline_traverse": trav,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+    if args.calib_copy_mb:
+        n = args.calib_copy_mb * (1 << 20) // 4
+        x = torch.zeros(n, dtype=torch.float32, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            torch.add(x, 1.0, out=y)
+        torch.cuda.synchronize()
+        log(f"calibration: 3 x y = x + 1 over {args.calib_copy_mb} MiB (reads and writes {n * 4} bytes each)")
 
 
 def cpu_baseline(cfg, ix, batch, L, prefilter, args):
@@ -208,6 +240,8 @@ def cpu_baseline(cfg, ix, batch, L, prefilter, args):
     the same batch, same routing, same L, on the host's cores."""
     from oracle import oracle as orc
     import garfield_amd as gf
+    batch.mark_cells(prefilter)          # the operating point's cells and routing
+    batch.order_cells(4)
     cells, counts, little, _ = batch.get_cells()
     O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"], ix["cross"])
     ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], ix["R"])

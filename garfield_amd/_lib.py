@@ -56,7 +56,7 @@ class SearchStats(C.Structure):
                 ("n_expand", C.c_uint64), ("n_dist", C.c_uint64), ("n_attr", C.c_uint64),
                 ("n_cross", C.c_uint64), ("n_lrow", C.c_uint64), ("n_scan", C.c_uint64),
                 ("n_pass", C.c_uint64), ("bytes_traverse", C.c_double), ("bytes_bruteforce", C.c_double),
-                ("ops_bruteforce", C.c_double), ("bf_mfma", C.c_uint32)]
+                ("ops_bruteforce", C.c_double), ("bf_mfma", C.c_uint32), ("ms_bf_kernel", C.c_double)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}

@@ -755,6 +755,8 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             if (b->part.n < b->bq.n * K) b->part.alloc(b->bq.n * K);
             if (b->gbound.n < Q) b->gbound.alloc(Q);
         }
+        hipEvent_t evg[2];   // around the MFMA kernel alone
+        for (auto& e : evg) GF_HIP(hipEventCreate(&e));
         auto launch_gemm = [&]() {
             gf::BfSchedArgs sc{};
             sc.sa = sub_args(*ix);
@@ -782,7 +784,9 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             ga.hi = b->hi.p; ga.items = b->items.p; ga.nitems = tot + 4; ga.bq = b->bq.p; ga.pcnt = b->pcnt.p;
             ga.part_off = b->part_off.p; ga.part = b->part.p; ga.gbound = b->gbound.p; ga.ok = tot + 3;
             ga.K = K; ga.D = ix->D;
+            GF_HIP(hipEventRecord(evg[0], st));
             GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu) * 3u, st));
+            GF_HIP(hipEventRecord(evg[1], st));
             gf::BfFinalArgs fa{};
             fa.bfq = b->sched.p; fa.srange = tot + 14; fa.part_off = b->part_off.p; fa.pcnt = b->pcnt.p;
             fa.ok = tot + 3; fa.part = b->part.p; fa.counts = b->counts.p; fa.cells = b->cells.p;
@@ -828,10 +832,12 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             GF_HIP(hipMemcpy(dt, tot, sizeof(dt), hipMemcpyDeviceToHost));
             GF_REQUIRE(dt[3], GF_E_STATE, "brute-force schedule does not fit after growing");
         }
-        float t_tr = 0, t_bf = 0;
+        float t_tr = 0, t_bf = 0, t_g = 0;
         GF_HIP(hipEventElapsedTime(&t_tr, ev[0], ev[1]));
         GF_HIP(hipEventElapsedTime(&t_bf, ev[1], ev[2]));
+        if (gemm) GF_HIP(hipEventElapsedTime(&t_g, evg[0], evg[1]));
         for (auto& e : ev) (void)hipEventDestroy(e);
+        for (auto& e : evg) (void)hipEventDestroy(e);
 
         GF_HIP(hipMemcpy(ids, b->out_ids.p, size_t(Q) * K * sizeof(uint32_t), hipMemcpyDeviceToHost));
         if (dists) GF_HIP(hipMemcpy(dists, b->out_dist.p, size_t(Q) * K * sizeof(float), hipMemcpyDeviceToHost));
@@ -849,6 +855,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             stats->ms_traverse = t_tr;
             stats->ms_bruteforce = t_bf;
             stats->ms_total = double(t_tr) + double(t_bf);
+            stats->ms_bf_kernel = t_g;
             stats->q_traverse = dt[8];
             stats->q_bruteforce = dt[9];
             stats->q_empty = dt[10];

@@ -131,6 +131,7 @@ typedef struct {
     double bytes_bruteforce; /* algorithmic HBM bytes of the brute-force kernel */
     double ops_bruteforce;   /* arithmetic of the brute-force kernel (int8 MACs x 2 on MFMA) */
     uint32_t bf_mfma;        /* 1 if the brute force ran as the int8 MFMA query-batch kernel */
+    double ms_bf_kernel;     /* device time of the MFMA brute-force kernel alone (no schedule, no merge) */
 } gf_search_stats;
 
 gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids /*Q*K*/,
