@@ -23,10 +23,12 @@ struct File {
     ~File() {
         if (f) std::fclose(f);
     }
+    // File size in bytes; the read position is left where it was.
     size_t size() {
+        const long pos = std::ftell(f);
         std::fseek(f, 0, SEEK_END);
-        long s = std::ftell(f);
-        std::fseek(f, 0, SEEK_SET);
+        const long s = std::ftell(f);
+        std::fseek(f, pos, SEEK_SET);
         return s < 0 ? 0 : size_t(s);
     }
     void read(void* dst, size_t bytes) {
@@ -106,6 +108,7 @@ void read_index_files(const gf_index_paths& p, uint32_t degree, HostIndex& out) 
             f.read(tmp.data(), tmp.size() * 4);  // per-attribute cell index (unused)
         }
         f.read(tmp.data(), tmp.size() * 4);
+        if (std::ftell(f.f) != long(f.size())) throw Error{GF_E_FORMAT, "grid file has trailing bytes: " + f.path};
         out.global_pid.resize(out.N);
         for (uint32_t i = 0; i < out.N; ++i) {
             if (tmp[i] < 0 || uint32_t(tmp[i]) >= out.P) throw Error{GF_E_FORMAT, "global_pid out of range"};

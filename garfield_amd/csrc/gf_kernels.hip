@@ -1297,7 +1297,7 @@ __global__ void k_total(const uint32_t* cnt, const uint32_t* start, uint32_t n, 
 }
 
 template <int KS, int AW, int KT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_bf_i8(BfGemmArgs p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3 : 2))) void k_bf_i8(BfGemmArgs p) {
     __shared__ uint64_t s_buf[4][kQB * kBfBufQ];
     __shared__ uint32_t s_cnt[4][kQB];
     __shared__ int32_t s_tp[4][kQB];

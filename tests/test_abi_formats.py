@@ -124,3 +124,60 @@ def test_loader_rejects_out_of_cell_ids(files):
     p = dict(paths)
     p["cagra_prefix"] = str(d / "bad_cell")
     assert _open(p) == 3   # GF_E_FORMAT, raised before the device is touched
+
+
+CLI = os.path.join(ROOT, "garfield_amd", "garfield_search")
+
+
+def test_cli_usage_and_argument_errors():
+    """The driver parses the reference's flags; errors exit 1 before any device call."""
+    import subprocess
+    assert os.path.exists(CLI), "garfield_search is built with the library"
+    r = subprocess.run([CLI, "--help"], capture_output=True, text=True)
+    assert r.returncode == 0 and "--prefilter" in r.stdout and "--postfilter" in r.stdout
+    r = subprocess.run([CLI, "--data_path", "x"], capture_output=True, text=True)
+    assert r.returncode == 1 and "required" in r.stderr
+    r = subprocess.run([CLI, "--bogus", "1"], capture_output=True, text=True)
+    assert r.returncode == 1 and "unknown flag" in r.stderr
+    r = subprocess.run([CLI, "--vec_dtype", "f8"], capture_output=True, text=True)
+    assert r.returncode == 1
+
+
+def test_file_reader_returns_the_written_arrays(files, tmp_path):
+    """The C++ index-file reader, built for the CPU, gives back exactly the
+    arrays the files were written from (attributes point-major, the grid's
+    quantiles as floats, per-cell graphs concatenated in cell order)."""
+    import shutil
+    import subprocess
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not found")
+    d, ix, paths = files
+    exe = tmp_path / "io_dump"
+    subprocess.run([gxx, "-O1", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                    os.path.join(ROOT, "tests", "native", "io_dump.cpp"),
+                    os.path.join(ROOT, "garfield_amd", "csrc", "gf_io.cpp"), "-o", str(exe)],
+                   check=True, capture_output=True)
+    r = subprocess.run([str(exe), paths["data_path"][:-len(".fvecs")], str(tmp_path)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    P = int(np.prod(ix["grid"]))
+    assert [int(v) for v in r.stdout.split()] == [ix["vectors"].shape[0], ix["vectors"].shape[1],
+                                                  ix["attrs"].shape[1], P, ix["R"], ix["cross"].shape[1] // P]
+    l_q, r_q = synth.quantile_arrays(ix)
+    want = dict(vectors=(ix["vectors"], np.float32), attrs=(ix["attrs"], np.float32), l_q=(l_q, np.float32),
+                r_q=(r_q, np.float32), global_pid=(ix["global_pid"], np.uint32),
+                cell_graphs=(ix["cell_graphs"], np.uint32), cross=(ix["cross"], np.uint32),
+                labels=(ix["labels"], np.int32))
+    for name, (ref, t) in want.items():
+        got = np.fromfile(tmp_path / name, t)
+        np.testing.assert_array_equal(got, np.ascontiguousarray(ref, t).ravel(), err_msg=name)
+    # a grid file with trailing bytes is rejected
+    bad = tmp_path / "bad"
+    for ext in (".fvecs", ".cross", ".attrs", ".cluster"):
+        os.link(paths["data_path"][:-len(".fvecs")] + ext, str(bad) + ext)
+    for c in range(P):
+        os.link(paths["cagra_prefix"] + f"{c}" + paths["cagra_suffix"], f"{bad}_cell{c}.graph")
+    open(str(bad) + ".grid", "wb").write(open(paths["grid"], "rb").read() + b"\0\0\0\0")
+    r = subprocess.run([str(exe), str(bad), str(tmp_path)], capture_output=True, text=True)
+    assert r.returncode == 1 and "trailing" in r.stderr

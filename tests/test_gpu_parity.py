@@ -297,3 +297,72 @@ def test_subcell_three_attributes(world_sub3, prefilter):
     ids, dists, ctr, oids, odist, octr, st = _bf_case(cfg, ix, 10, prefilter)
     assert st.bf_mfma == 1
     _assert_same(ids, dists, ctr, oids, odist, octr, st)
+
+
+def test_index_opened_from_files(small_world, tmp_path):
+    """gf_index_open on the written index files: stage A matches the oracle and
+    the search gives the same bits as the index built from the arrays."""
+    import garfield_amd._lib as gl
+    cfg, ix = small_world
+    _print_case("open-files", N=ix["vectors"].shape[0])
+    p = synth.write_index(ix, str(tmp_path / "w"))
+    lo, hi, cells, cnt, sel, little = _oracle_pipeline(cfg, ix, 0.05)
+    out = []
+    for dev in (gl.Index.open(**p, degree=ix["R"]), _device(ix)):
+        b = dev.batch(cfg["queries"], lo, hi)
+        b.mark_cells(0.05)
+        b.order_cells(4)
+        gc, gcnt, glit, gsel = b.get_cells()
+        assert np.array_equal(gcnt, cnt) and np.array_equal(gsel, sel) and np.array_equal(glit, little)
+        ids, dists, _ = b.search(L=64, K=10, rl=10)
+        # entries past a query's cell count are not defined
+        live = np.arange(gc.shape[1])[None, :] < gcnt[:, None]
+        out.append((np.where(live, gc, 0), ids, dists, b.get_counters()))
+        b.close()
+        dev.close()
+    for x, y in zip(out[0], out[1]):
+        assert np.array_equal(x, y)
+
+
+def test_cli_matches_library(small_world, tmp_path):
+    """garfield_search on the index files: the reference's CSV, and the same
+    recall as the library on the same batch."""
+    import csv
+    import subprocess
+    from garfield_amd import formats
+    from oracle import oracle as orc
+    cfg, ix = small_world
+    _print_case("cli")
+    p = synth.write_index(ix, str(tmp_path / "w"))
+    formats.write_fvecs(str(tmp_path / "q.fvecs"), cfg["queries"])
+    formats.write_ranges(str(tmp_path / "q.range"), cfg["lo"], cfg["hi"])
+    lo = cfg["lo"].astype(np.float32)
+    hi = cfg["hi"].astype(np.float32)
+    gt, gtd = orc.ground_truth(ix["vectors"], ix["attrs"], cfg["queries"], lo, hi, 10)
+    formats.write_gt(str(tmp_path / "q.gt"), gt)
+    cli = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "garfield_amd", "garfield_search")
+    args = [cli, "--data_path", p["data_path"], "--query_path", str(tmp_path / "q.fvecs"), "--range",
+            str(tmp_path / "q.range"), "--gt", str(tmp_path / "q.gt"), "--cagra_prefix", p["cagra_prefix"],
+            "--cagra_suffix", p["cagra_suffix"], "--global_graph", p["global_graph"], "--grid", p["grid"],
+            "--attrs", p["attrs"], "--cluster", p["cluster"], "--result", str(tmp_path / "r.csv"),
+            "--prefilter", "0.05", "--f2h_factor", "1.0", "--degree", str(ix["R"]), "--L", "32,64",
+            "--vec_dtype", "f32"]
+    r = subprocess.run(args, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    rows = list(csv.DictReader(open(tmp_path / "r.csv")))
+    assert [int(x["ef"]) for x in rows] == [32, 64]
+    for x in rows:
+        tot = float(x["cost1"]) + float(x["cost2"]) + float(x["cost3"])
+        assert abs(float(x["total_cost"]) - tot) < 1e-5 and float(x["qps"]) > 0
+    # the library on the same files, batch and L gives the same recall
+    dev = synth.open_device_index(ix)
+    b = dev.batch(cfg["queries"], lo, hi)
+    b.mark_cells(0.05)
+    b.order_cells(4)
+    for x in rows:
+        ids, _, _ = b.search(L=int(x["ef"]), K=10, rl=10)
+        rec = np.mean([len(set(ids[q]) & set(gt[q][gt[q] != 0x7FFFFFFF])) / max(1, np.sum(gt[q] != 0x7FFFFFFF))
+                       if np.any(gt[q] != 0x7FFFFFFF) else 1.0 for q in range(len(gt))])
+        assert abs(rec - float(x["recall"])) < 1e-5, (x, rec)
+    b.close()
+    dev.close()
