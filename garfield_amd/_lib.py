@@ -11,6 +11,7 @@ NO_RESULT = 0x7FFFFFFF
 NCOUNTERS = 8
 VEC_F32 = 0
 VEC_F16 = 1
+VEC_U8 = 2
 COUNTER_NAMES = ("expand", "dist", "attr", "cross", "lrow", "scan", "pass", "route")
 
 
@@ -50,13 +51,19 @@ class _SearchOpts(C.Structure):
                 ("entry_points", C.c_void_p)]
 
 
+class _StreamPlan(C.Structure):
+    _fields_ = [("device_budget", C.c_uint64), ("nbatch", C.c_uint32), ("batch_cells", C.c_uint32),
+                ("sizes", C.c_void_p), ("cells", C.c_void_p)]
+
+
 class SearchStats(C.Structure):
     _fields_ = [("ms_traverse", C.c_double), ("ms_bruteforce", C.c_double), ("ms_total", C.c_double),
                 ("q_traverse", C.c_uint32), ("q_bruteforce", C.c_uint32), ("q_empty", C.c_uint32),
                 ("n_expand", C.c_uint64), ("n_dist", C.c_uint64), ("n_attr", C.c_uint64),
                 ("n_cross", C.c_uint64), ("n_lrow", C.c_uint64), ("n_scan", C.c_uint64),
                 ("n_pass", C.c_uint64), ("bytes_traverse", C.c_double), ("bytes_bruteforce", C.c_double),
-                ("ops_bruteforce", C.c_double), ("bf_mfma", C.c_uint32), ("ms_bf_kernel", C.c_double)]
+                ("ops_bruteforce", C.c_double), ("bf_mfma", C.c_uint32), ("ms_bf_kernel", C.c_double),
+                ("n_batches", C.c_uint32), ("bytes_h2d", C.c_double), ("ms_h2d", C.c_double)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -65,17 +72,23 @@ class SearchStats(C.Structure):
 _SYMBOLS = {
     "gf_index_open": [C.POINTER(_Paths), C.POINTER(_OpenOpts), C.POINTER(C.c_void_p)],
     "gf_index_create": [C.POINTER(_Host), C.POINTER(_OpenOpts), C.POINTER(C.c_void_p)],
+    "gf_index_create_streamed": [C.POINTER(_Host), C.POINTER(_OpenOpts), C.POINTER(_StreamPlan),
+                                 C.POINTER(C.c_void_p)],
+    "gf_index_open_streamed": [C.POINTER(_Paths), C.POINTER(_OpenOpts), C.POINTER(_StreamPlan),
+                               C.POINTER(C.c_void_p)],
     "gf_index_close": [C.c_void_p],
     "gf_index_get_info": [C.c_void_p, C.POINTER(_Info)],
     "gf_batch_create": [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p)],
     "gf_batch_free": [C.c_void_p],
     "gf_mark_cells": [C.c_void_p, C.c_float, C.POINTER(C.c_double)],
     "gf_order_cells": [C.c_void_p, C.c_uint32, C.POINTER(C.c_double)],
+    "gf_mark_cells_grid": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_double, C.POINTER(C.c_double)],
     "gf_search": [C.c_void_p, C.POINTER(_SearchOpts), C.c_void_p, C.c_void_p, C.POINTER(SearchStats)],
     "gf_batch_get_cells": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
     "gf_batch_set_cells": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
     "gf_batch_get_centroid": [C.c_void_p, C.c_void_p, C.c_void_p],
     "gf_batch_get_counters": [C.c_void_p, C.c_void_p],
+    "gf_batch_get_cell_flags": [C.c_void_p, C.c_void_p],
     "gf_f2h": [C.c_void_p, C.c_size_t, C.c_float, C.c_void_p],
     "gf_row_norms_f16": [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p],
     "gf_entry_points": [C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p],
@@ -168,6 +181,53 @@ class Index:
                                                                      hist_contiguous, device)), C.byref(h)))
         return cls(h)
 
+    @staticmethod
+    def _plan(device_budget, plan, batch_cells):
+        keep = None
+        if plan is None:
+            sp = _StreamPlan(int(device_budget), 0, int(batch_cells), None, None)
+        else:
+            sizes = _c([len(b) for b in plan], np.uint32)
+            cells = _c([c for b in plan for c in b], np.uint32)
+            keep = (sizes, cells)
+            sp = _StreamPlan(int(device_budget), len(plan), int(batch_cells), _ptr(sizes), _ptr(cells))
+        return sp, keep
+
+    @classmethod
+    def create_streamed(cls, vectors, attrs, grid_shape, l_q, r_q, global_pid, cell_graphs, cross,
+                        plan=None, device_budget=0, batch_cells=16, vec_dtype=VEC_U8, device=0, degree=0):
+        """A streamed (out-of-core) index: plan is a list of batches of cell
+        ids (None: consecutive cells, batch_cells per batch)."""
+        keep = dict(
+            vectors=_c(vectors, np.float32), attrs=_c(attrs, np.float32),
+            grid=_c(grid_shape, np.uint32), l_q=_c(l_q, np.float32), r_q=_c(r_q, np.float32),
+            pid=_c(global_pid, np.uint32), graphs=_c(cell_graphs, np.uint32), cross=_c(cross, np.uint32))
+        N, D = keep["vectors"].shape
+        a = keep["attrs"].shape[1]
+        P = int(np.prod(keep["grid"]))
+        R = keep["graphs"].shape[1]
+        E = keep["cross"].shape[1] // P
+        host = _Host(N, D, a, P, R, E, _ptr(keep["vectors"]), _ptr(keep["attrs"]), _ptr(keep["grid"]),
+                     _ptr(keep["l_q"]), _ptr(keep["r_q"]), _ptr(keep["pid"]), _ptr(keep["graphs"]),
+                     _ptr(keep["cross"]), None)
+        sp, _keep = cls._plan(device_budget, plan, batch_cells)
+        h = C.c_void_p()
+        _check(load().gf_index_create_streamed(C.byref(host), C.byref(_opts(degree, 1.0, vec_dtype, False, device)),
+                                               C.byref(sp), C.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def open_streamed(cls, data_path, cagra_prefix, cagra_suffix, global_graph, grid, attrs, cluster=None,
+                      plan=None, device_budget=0, batch_cells=16, degree=0, vec_dtype=VEC_U8, device=0):
+        enc = lambda s: None if s is None else str(s).encode()
+        paths = _Paths(enc(data_path), enc(cagra_prefix), enc(cagra_suffix), enc(global_graph),
+                       enc(grid), enc(attrs), enc(cluster))
+        sp, _keep = cls._plan(device_budget, plan, batch_cells)
+        h = C.c_void_p()
+        _check(load().gf_index_open_streamed(C.byref(paths), C.byref(_opts(degree, 1.0, vec_dtype, False, device)),
+                                             C.byref(sp), C.byref(h)))
+        return cls(h)
+
     def close(self):
         if self._h:
             _check(load().gf_index_close(self._h))
@@ -216,6 +276,18 @@ class Batch:
         ms = C.c_double()
         _check(load().gf_mark_cells(self._h, float(prefilter), C.byref(ms)))
         return ms.value
+
+    def mark_cells_grid(self, attr_min, attr_width, threshold):
+        amin = _c(attr_min, np.float32)
+        width = _c(attr_width, np.float32)
+        ms = C.c_double()
+        _check(load().gf_mark_cells_grid(self._h, _ptr(amin), _ptr(width), float(threshold), C.byref(ms)))
+        return ms.value
+
+    def get_cell_flags(self):
+        f = np.empty((self.Q, self.index.P), np.uint8)
+        _check(load().gf_batch_get_cell_flags(self._h, _ptr(f)))
+        return f
 
     def order_cells(self, topc=4):
         ms = C.c_double()

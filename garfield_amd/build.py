@@ -24,7 +24,7 @@ COMMON = [
     "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-deprecated-declarations", "-I", os.path.join(ROOT, "include"),
 ]
-LIB_SOURCES = ["gf_kernels.hip", "gf_host.cpp", "gf_io.cpp"]
+LIB_SOURCES = ["gf_kernels.hip", "gf_host.cpp", "gf_stream.cpp", "gf_io.cpp"]
 OBJ_DIR = os.path.join(HERE, "_build")
 
 
@@ -35,12 +35,16 @@ def _run(cmd):
 
 def build(verbose=True):
     os.makedirs(OBJ_DIR, exist_ok=True)
-    objs = []
-    for src in LIB_SOURCES:
+    objs, procs = [], []
+    for src in LIB_SOURCES:   # compiled concurrently, one hipcc per source
         obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
-        lang = ["-x", "hip"]
-        _run([HIPCC, *COMMON, *lang, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmd = [HIPCC, *COMMON, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+        print("+", " ".join(cmd), flush=True)
+        procs.append((cmd, subprocess.Popen(cmd)))
         objs.append(obj)
+    failed = [cmd for cmd, pr in procs if pr.wait() != 0]
+    if failed:
+        raise subprocess.CalledProcessError(1, failed[0])
     tmp = LIB + ".tmp"
     _run([HIPCC, *COMMON, "-shared", *objs, "-o", tmp])
     os.replace(tmp, LIB)

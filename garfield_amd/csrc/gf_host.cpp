@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <functional>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -20,7 +21,7 @@
 #include <unordered_set>
 #include <vector>
 
-#include "gf_internal.h"
+#include "gf_state.h"
 
 using gf::Error;
 
@@ -28,118 +29,14 @@ namespace {
 
 thread_local std::string g_last_error;
 
-#define GF_HIP(x)                                                                              \
-    do {                                                                                       \
-        hipError_t e_ = (x);                                                                   \
-        if (e_ != hipSuccess)                                                                  \
-            throw Error{GF_E_DEVICE, std::string(#x) + ": " + hipGetErrorString(e_)};          \
-    } while (0)
-
-#define GF_REQUIRE(cond, code, msg)                  \
-    do {                                             \
-        if (!(cond)) throw Error{(code), (msg)};     \
-    } while (0)
-
-// Owning device buffer.
-template <typename T>
-struct DevBuf {
-    T* p = nullptr;
-    size_t n = 0;
-    DevBuf() = default;
-    DevBuf(const DevBuf&) = delete;
-    DevBuf& operator=(const DevBuf&) = delete;
-    ~DevBuf() { release(); }
-    void release() {
-        if (p) (void)hipFree(p);
-        p = nullptr;
-        n = 0;
-    }
-    void alloc(size_t count) {
-        if (count == n && p) return;
-        release();
-        if (count == 0) return;
-        hipError_t e = hipMalloc(&p, count * sizeof(T));
-        if (e != hipSuccess) {
-            p = nullptr;
-            throw Error{GF_E_NOMEM, "hipMalloc of " + std::to_string(count * sizeof(T)) + " bytes failed"};
-        }
-        n = count;
-    }
-    void upload(const T* src, size_t count) {
-        alloc(count);
-        if (count) GF_HIP(hipMemcpy(p, src, count * sizeof(T), hipMemcpyHostToDevice));
-    }
-    void upload(const std::vector<T>& v) { upload(v.data(), v.size()); }
-    size_t bytes() const { return n * sizeof(T); }
-};
-
-uint32_t round_up(uint32_t x, uint32_t m) { return (x + m - 1) / m * m; }
-
 gf_status run_guarded(const std::function<void()>& fn);
 
 }  // namespace
 
-struct gf_index {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    uint32_t N = 0, D = 0, a = 0, P = 0, R = 0, E = 0, C = 0;
-    int32_t vdtype = GF_VEC_F32;
-    float alpha = 1.0f;
-    gf::RowShape rs{};
-    uint32_t rowbytes = 0, Cp = 0, Dp = 0;
-    std::vector<uint32_t> offset_h, grid_h;
-    DevBuf<char> vec;
-    DevBuf<float> attrs, l_q, r_q, cnorm;
-    DevBuf<uint32_t> graph, cross, offset, gidx, lrow, grid, doff, hist;
-    DevBuf<uint32_t> entry_ref;   // the reference's entry-point draw, made on first use
-    DevBuf<uint32_t> tile_cell, tile_row0, tile_n;
-    DevBuf<uint16_t> centres;
-    uint32_t ntiles = 0;
-    // Sub-cells (integer attributes spread by less than 65534 inside every
-    // cell, a <= 4): each cell is split by a rank grid of S bins per
-    // attribute; tiles of 16 points are grouped by sub-cell and carry the
-    // cell-major row and the packed 16-bit attribute offsets of each point.
-    bool sub = false;
-    uint32_t AW = 0, NS = 0, ntile = 0;
-    std::vector<uint32_t> ssize_h, stile_h;
-    DevBuf<uint32_t> sbase, scell, ssize, stile, tmeta;
-    DevBuf<int32_t> sbox, abase;
-    // Query-batch MFMA brute force (additionally: vectors integers in
-    // [0, 255], D a multiple of 64 up to 256): int8 tiles and norms.
-    bool i8 = false;
-    DevBuf<int8_t> vt;
-    DevBuf<int32_t> tnorm;
-    int ncu = 0;
-    ~gf_index() {
-        if (stream) (void)hipStreamDestroy(stream);
-    }
-    uint64_t device_bytes() const {
-        return vec.bytes() + attrs.bytes() + l_q.bytes() + r_q.bytes() + cnorm.bytes() + graph.bytes() +
-               cross.bytes() + offset.bytes() + gidx.bytes() + lrow.bytes() + grid.bytes() + doff.bytes() +
-               hist.bytes() + tile_cell.bytes() + tile_row0.bytes() + tile_n.bytes() + centres.bytes() +
-               sbase.bytes() + scell.bytes() + ssize.bytes() + stile.bytes() + tmeta.bytes() + sbox.bytes() +
-               abase.bytes() + vt.bytes() + tnorm.bytes();
-    }
-};
-
-struct gf_batch {
-    gf_index* ix = nullptr;
-    uint32_t Q = 0, Qp = 0, topc = 0;
-    bool marked = false;
-    bool i8 = false;
-    DevBuf<int8_t> q8;
-    DevBuf<int32_t> nq;
-    // brute-force schedule of stage C (tot: device totals and fit flags)
-    DevBuf<uint32_t> tot;
-    DevBuf<uint32_t> bcnt, bstart, pcnt, bq, nsub, part_off, icnt, ioff, bfq;
-    DevBuf<gf::BfItem> items;
-    DevBuf<uint64_t> part;
-    DevBuf<unsigned long long> stats;
-    DevBuf<float> qf32, qnorm, lo, hi, cdist, out_dist;
-    DevBuf<uint16_t> q16, q16v;
-    DevBuf<uint32_t> cells, counts, little, selcount, cellq, ccount, cstart, cfill, topk;
-    DevBuf<uint32_t> out_ids, counters, sched, entry, gbound;
-};
+using gf::DevBuf;
+using gf::Timer;
+using gf::round_up;
+using gf::set_device;
 
 namespace {
 
@@ -159,28 +56,6 @@ gf_status run_guarded(const std::function<void()>& fn) {
     }
 }
 
-struct Timer {
-    hipEvent_t a = nullptr, b = nullptr;
-    hipStream_t s;
-    explicit Timer(hipStream_t st) : s(st) {
-        GF_HIP(hipEventCreate(&a));
-        GF_HIP(hipEventCreate(&b));
-        GF_HIP(hipEventRecord(a, s));
-    }
-    double stop() {
-        GF_HIP(hipEventRecord(b, s));
-        GF_HIP(hipEventSynchronize(b));
-        float ms = 0;
-        GF_HIP(hipEventElapsedTime(&ms, a, b));
-        return ms;
-    }
-    ~Timer() {
-        if (a) (void)hipEventDestroy(a);
-        if (b) (void)hipEventDestroy(b);
-    }
-};
-
-void set_device(const gf_index* ix) { GF_HIP(hipSetDevice(ix->device)); }
 
 // Sub-cells of every cell, built when all attributes are integers whose
 // spread inside each cell is below 65534 and a <= 4 (otherwise ix.sub stays
@@ -273,7 +148,12 @@ void build_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, c
     ix.sub = true;
 }
 
-void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix) {
+}  // namespace
+
+namespace gf {
+
+void map_cells(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix, std::vector<uint32_t>& size,
+               std::vector<uint32_t>& gidx, std::vector<uint32_t>& lrow) {
     GF_REQUIRE(h.N > 0 && h.D > 0, GF_E_ARG, "N and D must be positive");
     GF_REQUIRE(h.a >= 1 && h.a <= gf::kMaxAttr, GF_E_UNSUPPORTED, "attribute count must be in [1, 8]");
     GF_REQUIRE(h.R >= 1 && h.R <= 64, GF_E_UNSUPPORTED, "graph degree must be in [1, 64]");
@@ -284,12 +164,14 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
     ix.device = opts ? opts->device : 0;
     ix.vdtype = opts ? opts->vec_dtype : GF_VEC_F32;
     ix.alpha = (opts && opts->f2h_factor != 0.0f) ? opts->f2h_factor : 1.0f;
-    GF_REQUIRE(ix.vdtype == GF_VEC_F32 || ix.vdtype == GF_VEC_F16, GF_E_ARG, "vec_dtype must be GF_VEC_F32 or GF_VEC_F16");
+    GF_REQUIRE(ix.vdtype == GF_VEC_F32 || ix.vdtype == GF_VEC_F16 || ix.vdtype == GF_VEC_U8, GF_E_ARG,
+               "vec_dtype must be GF_VEC_F32, GF_VEC_F16 or GF_VEC_U8");
     GF_REQUIRE(!(opts && opts->degree) || opts->degree == h.R, GF_E_FORMAT, "--degree does not match the graph files");
-    const uint32_t elems = ix.vdtype == GF_VEC_F16 ? 8u : 4u;
-    GF_REQUIRE(h.D % elems == 0, GF_E_UNSUPPORTED, "D must be a multiple of 4 (fp32) or 8 (fp16)");
-    ix.rs = gf::row_shape(h.D, ix.vdtype == GF_VEC_F16);
-    GF_REQUIRE(ix.rs.cpl <= (ix.rs.f16 ? 2u : 4u), GF_E_UNSUPPORTED, "D too large for this build");
+    const uint32_t elems = ix.vdtype == GF_VEC_F32 ? 4u : (ix.vdtype == GF_VEC_F16 ? 8u : 16u);
+    GF_REQUIRE(h.D % elems == 0, GF_E_UNSUPPORTED, "D must be a multiple of 4 (fp32), 8 (fp16) or 16 (u8)");
+    ix.rs = gf::row_shape(h.D, ix.vdtype);
+    GF_REQUIRE(ix.rs.cpl <= gf::row_shape_max_cpl(ix.vdtype), GF_E_UNSUPPORTED, "D too large for this build");
+    ix.rowbytes = h.D * (ix.vdtype == GF_VEC_F32 ? 4u : (ix.vdtype == GF_VEC_F16 ? 2u : 1u));
 
     const uint32_t N = h.N, D = h.D, a = h.a, R = h.R, E = h.E;
     uint64_t P64 = 1;
@@ -301,9 +183,13 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
     GF_REQUIRE(P64 <= 4096, GF_E_UNSUPPORTED, "at most 4096 cells");
     const uint32_t P = uint32_t(P64);
     ix.N = N; ix.D = D; ix.a = a; ix.P = P; ix.R = R; ix.E = E;
+    ix.grid_h.assign(h.grid_shape, h.grid_shape + a);
 
     // idx mapper (tools.cuh:862-915)
-    std::vector<uint32_t> size(P, 0), fill(P, 0), gidx(N), lrow(N), local(N);
+    size.assign(P, 0);
+    gidx.assign(N, 0);
+    lrow.assign(N, 0);
+    std::vector<uint32_t> fill(P, 0);
     for (uint32_t i = 0; i < N; ++i) {
         GF_REQUIRE(h.global_pid[i] < P, GF_E_FORMAT, "global_pid out of range");
         size[h.global_pid[i]]++;
@@ -314,25 +200,59 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
         const uint32_t c = h.global_pid[i];
         const uint32_t r = ix.offset_h[c] + fill[c];
         gidx[r] = i;
-        lrow[r] = fill[c];
-        local[i] = fill[c]++;
+        lrow[r] = fill[c]++;
     }
     // Every id the kernels dereference is checked here once.
     for (uint32_t c = 0; c < P; ++c)
         for (size_t k = size_t(ix.offset_h[c]) * R; k < size_t(ix.offset_h[c + 1]) * R; ++k)
             GF_REQUIRE(h.cell_graphs[k] < size[c], GF_E_FORMAT,
                        "per-cell graph " + std::to_string(c) + " holds an id beyond the cell");
-    std::vector<uint32_t> cross_cm(size_t(N) * P * E);
-    for (uint32_t r = 0; r < N; ++r) {
-        const uint32_t* src = h.cross + size_t(gidx[r]) * P * E;
+    for (uint32_t i = 0; i < N; ++i) {
+        const uint32_t* src = h.cross + size_t(i) * P * E;
         for (uint32_t c = 0; c < P; ++c)
-            for (uint32_t e = 0; e < E; ++e) {
-                const uint32_t v = src[c * E + e];
+            for (uint32_t e = 0; e < E; ++e)
                 // edges into an empty cell are never followed (no query selects it)
-                GF_REQUIRE(v < size[c] || size[c] == 0, GF_E_FORMAT, "cross-cell graph holds an id beyond its cell");
-                cross_cm[(size_t(r) * P + c) * E + e] = v;
-            }
+                GF_REQUIRE(src[c * E + e] < size[c] || size[c] == 0, GF_E_FORMAT,
+                           "cross-cell graph holds an id beyond its cell");
     }
+    if (ix.vdtype == GF_VEC_U8) {
+        const size_t n = size_t(N) * D;
+        for (size_t i = 0; i < n; ++i) {
+            const float x = h.vectors[i];
+            GF_REQUIRE(x >= 0.0f && x <= 255.0f && x == std::floor(x), GF_E_ARG,
+                       "GF_VEC_U8 needs vectors of integers in [0, 255]");
+        }
+    }
+}
+
+void entry_points_draw(uint32_t range, uint32_t ndraw, uint32_t R, uint32_t* out) {
+    GF_REQUIRE(range >= 1, GF_E_ARG, "no room for entry points");
+    std::mt19937 rng;
+    std::uniform_int_distribution<> intd(0, int(range) - 1);
+    const uint32_t want = std::min<uint32_t>(ndraw, range);
+    std::vector<unsigned> v(want);
+    std::unordered_set<unsigned> seen;
+    uint32_t k = 0;
+    while (k < want) {
+        const unsigned t = unsigned(intd(rng));
+        if (!seen.count(t)) { seen.insert(t); v[k++] = t; }
+    }
+    std::srand(1);
+    std::random_shuffle(v.begin(), v.begin() + want);
+    for (uint32_t j = 0; j < R; ++j) out[j] = j < want ? v[j] : j;
+}
+
+}  // namespace gf
+
+namespace {
+
+void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix) {
+    std::vector<uint32_t> size, gidx, lrow;
+    gf::map_cells(h, opts, ix, size, gidx, lrow);
+    const uint32_t N = ix.N, D = ix.D, a = ix.a, P = ix.P, R = ix.R, E = ix.E;
+    std::vector<uint32_t> cross_cm(size_t(N) * P * E);
+    for (uint32_t r = 0; r < N; ++r)
+        std::memcpy(&cross_cm[size_t(r) * P * E], h.cross + size_t(gidx[r]) * P * E, sizeof(uint32_t) * P * E);
     // All ids are validated; from here on the device is used.
     GF_HIP(hipSetDevice(ix.device));
     GF_HIP(hipStreamCreateWithFlags(&ix.stream, hipStreamNonBlocking));
@@ -358,18 +278,22 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
         const float* vec_f32_dev = nullptr;
         if (ix.vdtype == GF_VEC_F32) {
             ix.vec.upload(reinterpret_cast<const char*>(v.data()), v.size() * sizeof(float));
-            ix.rowbytes = D * 4;
             vec_f32_dev = reinterpret_cast<const float*>(ix.vec.p);
-        } else {
+        } else if (ix.vdtype == GF_VEC_F16) {
             tmp.upload(v);
             ix.vec.alloc(v.size() * sizeof(uint16_t));
             GF_HIP(gf::launch_f2h(tmp.p, reinterpret_cast<uint16_t*>(ix.vec.p), v.size(), ix.alpha, ix.stream));
-            ix.rowbytes = D * 2;
+            vec_f32_dev = tmp.p;
+        } else {
+            std::vector<char> u(v.size());
+            for (size_t i = 0; i < v.size(); ++i) u[i] = char(uint8_t(v[i]));
+            ix.vec.upload(u);
+            tmp.upload(v);
             vec_f32_dev = tmp.p;
         }
         build_subcells(h, gidx, size, ix);
         // Integer-valued data in [0, 255]: int8 tiles of the MFMA brute force.
-        bool ints = ix.sub && ix.vdtype == GF_VEC_F32 && D % 64 == 0 && D <= 256;
+        bool ints = ix.sub && ix.vdtype != GF_VEC_F16 && D % 64 == 0 && D <= 256;
         for (size_t i = 0; ints && i < v.size(); ++i) ints = v[i] >= 0.0f && v[i] <= 255.0f && v[i] == std::floor(v[i]);
         if (ints) {
             ix.vt.alloc(size_t(ix.ntile) * (D / 64) * 1024);
@@ -382,7 +306,6 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
     // Grid (real_dataset_adapter.cuh:563-619).
     uint32_t gsum = 0;
     std::vector<uint32_t> doff(a);
-    ix.grid_h.assign(h.grid_shape, h.grid_shape + a);
     for (uint32_t d = 0; d < a; ++d) { doff[d] = gsum; gsum += h.grid_shape[d]; }
     ix.l_q.upload(h.l_q, gsum);
     ix.r_q.upload(h.r_q, gsum);
@@ -464,19 +387,7 @@ void entry_points_ref(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
     const uint32_t avg = (N + P - 1) / P;
     const uint32_t rand_max = N - (P - 1) * avg;
     GF_REQUIRE(rand_max >= 1, GF_E_ARG, "no room for entry points");
-    std::mt19937 rng;
-    std::uniform_int_distribution<> intd(0, int(rand_max) - 1);
-    const uint32_t want = std::min<uint32_t>(R * 10, rand_max);
-    std::vector<unsigned> v(want);
-    std::unordered_set<unsigned> seen;
-    uint32_t k = 0;
-    while (k < want) {
-        const unsigned t = unsigned(intd(rng));
-        if (!seen.count(t)) { seen.insert(t); v[k++] = t; }
-    }
-    std::srand(1);
-    std::random_shuffle(v.begin(), v.begin() + want);
-    for (uint32_t j = 0; j < R; ++j) out[j] = j < want ? v[j] : j;
+    gf::entry_points_draw(rand_max, R * 10, R, out);
 }
 
 }  // namespace
@@ -528,6 +439,41 @@ gf_status gf_index_open(const gf_index_paths* paths, const gf_open_opts* opts, g
         h.labels = hi.has_labels ? hi.labels.data() : nullptr;
         std::unique_ptr<gf_index> ix(new gf_index());
         build_index(h, opts, *ix);
+        *out = ix.release();
+    });
+}
+
+gf_status gf_index_create_streamed(const gf_index_host* host, const gf_open_opts* opts, const gf_stream_plan* plan,
+                                   gf_index** out) {
+    return run_guarded([&] {
+        GF_REQUIRE(host && plan && out, GF_E_ARG, "null argument");
+        *out = nullptr;
+        std::unique_ptr<gf_index> ix(new gf_index());
+        gf::build_streamed(*host, opts, plan, *ix);
+        *out = ix.release();
+    });
+}
+
+gf_status gf_index_open_streamed(const gf_index_paths* paths, const gf_open_opts* opts, const gf_stream_plan* plan,
+                                 gf_index** out) {
+    return run_guarded([&] {
+        GF_REQUIRE(paths && plan && out, GF_E_ARG, "null argument");
+        *out = nullptr;
+        gf::HostIndex hi;
+        gf::read_index_files(*paths, opts ? opts->degree : 0, hi);
+        gf_index_host h{};
+        h.N = hi.N; h.D = hi.D; h.a = hi.a; h.P = hi.P; h.R = hi.R; h.E = hi.E;
+        h.vectors = hi.vectors.data();
+        h.attrs = hi.attrs.data();
+        h.grid_shape = hi.grid.data();
+        h.l_q = hi.l_q.data();
+        h.r_q = hi.r_q.data();
+        h.global_pid = hi.global_pid.data();
+        h.cell_graphs = hi.cell_graphs.data();
+        h.cross = hi.cross.data();
+        h.labels = nullptr;
+        std::unique_ptr<gf_index> ix(new gf_index());
+        gf::build_streamed(h, opts, plan, *ix);
         *out = ix.release();
     });
 }
@@ -615,6 +561,9 @@ gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms) {
     return run_guarded([&] {
         GF_REQUIRE(b, GF_E_ARG, "null batch");
         gf_index* ix = b->ix;
+        GF_REQUIRE(!ix->sx, GF_E_UNSUPPORTED,
+                   "a streamed index has no resident attributes: use gf_mark_cells_grid or gf_batch_set_cells");
+        b->flags_ready = false;
         set_device(ix);
         hipStream_t st = ix->stream;
         Timer t(st);
@@ -642,6 +591,31 @@ gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms) {
         const double el = t.stop();
         if (ms) *ms = el;
         b->marked = true;
+    });
+}
+
+gf_status gf_mark_cells_grid(gf_batch* b, const float* attr_min, const float* attr_width, double threshold,
+                             double* ms) {
+    return run_guarded([&] {
+        GF_REQUIRE(b && attr_min && attr_width, GF_E_ARG, "null argument");
+        gf_index* ix = b->ix;
+        for (uint32_t d = 0; d < ix->a; ++d)
+            GF_REQUIRE(attr_width[d] > 0.0f && std::isfinite(attr_width[d]) && std::isfinite(attr_min[d]), GF_E_ARG,
+                       "attr_width must be positive and finite, attr_min finite");
+        set_device(ix);
+        hipStream_t st = ix->stream;
+        if (b->flags.n < size_t(b->Q) * ix->P) b->flags.alloc(size_t(b->Q) * ix->P);
+        DevBuf<float> amin, width;
+        amin.upload(attr_min, ix->a);
+        width.upload(attr_width, ix->a);
+        Timer t(st);
+        GF_HIP(gf::launch_cells_grid(b->Q, ix->a, b->lo.p, b->hi.p, amin.p, width.p, ix->grid.p, ix->P, ix->offset.p,
+                                     threshold, b->cells.p, b->counts.p, b->little.p, b->flags.p, st));
+        GF_HIP(hipMemsetAsync(b->selcount.p, 0, b->Q * sizeof(uint32_t), st));
+        const double el = t.stop();
+        if (ms) *ms = el;
+        b->marked = true;
+        b->flags_ready = true;
     });
 }
 
@@ -678,6 +652,10 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         GF_REQUIRE(K >= 1 && K <= 64, GF_E_ARG, "K must be in [1, 64]");
         GF_REQUIRE(rl >= 1 && rl <= 16, GF_E_ARG, "rl must be in [1, 16]");
         set_device(ix);
+        if (ix->sx) {
+            gf::stream_search(*b, *opts, ids, dists, stats);
+            return;
+        }
         hipStream_t st = ix->stream;
         const uint32_t Q = b->Q, R = ix->R;
 
@@ -713,6 +691,8 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         a.attrs = ix->attrs.p;
         a.graph = ix->graph.p;
         a.cross = ix->cross.p;
+        a.xrow = uint64_t(ix->P) * ix->E;
+        a.xcell = ix->E;
         a.offset = ix->offset.p;
         a.gidx = ix->gidx.p;
         a.lrow = ix->lrow.p;
@@ -907,14 +887,19 @@ gf_status gf_batch_set_cells(gf_batch* b, const uint32_t* cells, const uint32_t*
         const uint32_t P = b->ix->P;
         for (uint32_t q = 0; q < b->Q; ++q) {
             GF_REQUIRE(counts[q] <= P && little[q] <= counts[q], GF_E_ARG, "cell count out of range");
-            for (uint32_t i = 0; i < counts[q]; ++i)
-                GF_REQUIRE(cells[size_t(q) * P + i] < P, GF_E_ARG, "cell id out of range");
+            for (uint32_t i = 0; i < counts[q]; ++i) {
+                const uint32_t c = cells[size_t(q) * P + i];
+                GF_REQUIRE(c < P, GF_E_ARG, "cell id out of range");
+                // the kernels draw entry points inside the first cell and read every listed cell
+                GF_REQUIRE(b->ix->offset_h[c + 1] > b->ix->offset_h[c], GF_E_ARG, "cell list names a cell with no point");
+            }
         }
         const size_t Q = b->Q;
         GF_HIP(hipMemcpy(b->cells.p, cells, Q * P * 4, hipMemcpyHostToDevice));
         GF_HIP(hipMemcpy(b->counts.p, counts, Q * 4, hipMemcpyHostToDevice));
         GF_HIP(hipMemcpy(b->little.p, little, Q * 4, hipMemcpyHostToDevice));
         b->marked = true;
+        b->flags_ready = false;
     });
 }
 
@@ -925,6 +910,23 @@ gf_status gf_batch_get_centroid(const gf_batch* b, float* dist, uint32_t* topc) 
         set_device(b->ix);
         if (dist) GF_HIP(hipMemcpy(dist, b->cdist.p, size_t(b->Q) * b->ix->C * 4, hipMemcpyDeviceToHost));
         if (topc) GF_HIP(hipMemcpy(topc, b->topk.p, size_t(b->Q) * b->topc * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+gf_status gf_batch_get_cell_flags(const gf_batch* b, uint8_t* flags) {
+    return run_guarded([&] {
+        GF_REQUIRE(b && flags, GF_E_ARG, "null argument");
+        GF_REQUIRE(b->marked, GF_E_STATE, "cells not marked");
+        gf_batch* mb = const_cast<gf_batch*>(b);
+        set_device(b->ix);
+        const size_t n = size_t(b->Q) * b->ix->P;
+        if (!b->flags_ready) {
+            if (mb->flags.n < n) mb->flags.alloc(n);
+            GF_HIP(gf::launch_cell_flags(b->Q, b->ix->P, b->cells.p, b->counts.p, b->little.p, mb->flags.p,
+                                         b->ix->stream));
+            GF_HIP(hipStreamSynchronize(b->ix->stream));
+        }
+        GF_HIP(hipMemcpy(flags, b->flags.p, n, hipMemcpyDeviceToHost));
     });
 }
 

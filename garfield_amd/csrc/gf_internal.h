@@ -34,18 +34,22 @@ enum { C_EXPAND = 0, C_DIST = 1, C_ATTR = 2, C_CROSS = 3, C_LROW = 4, C_SCAN = 5
 
 // Distance kernel shape for a row of D elements: 16-byte chunks, LPR lanes
 // per row (power of two in [8, 64]), CPL chunks per lane.
+// Row layout of the distance kernels: vt 0 = fp32, 1 = binary16, 2 = uint8
+// vectors; a row is nch 16-byte chunks, LPR lanes per row, cpl chunks per lane.
 struct RowShape {
-    bool f16;
+    int vt;
     uint32_t nch, lpr, cpl;
 };
-RowShape row_shape(uint32_t D, bool f16);
+RowShape row_shape(uint32_t D, int vt);
+uint32_t row_shape_max_cpl(int vt);
 
 struct TravArgs {
     const char* vec;          // N rows of rowbytes, cell-major
     uint32_t rowbytes, nch;
     const float* attrs;       // N*a, cell-major
     const uint32_t* graph;    // N*R cell-local neighbour ids, cell-major rows
-    const uint32_t* cross;    // N*P*E cell-local ids, cell-major rows
+    const uint32_t* cross;    // cell-local ids: edge e of row r into cell c at r*xrow + c*xcell + e
+    uint64_t xrow, xcell;     // resident index: P*E, E; a streamed batch ("T" layout): E, rows*E
     const uint32_t* offset;   // P+1
     const uint32_t* gidx;     // row -> point id
     const uint32_t* lrow;     // row -> cell-local id
@@ -221,6 +225,17 @@ hipError_t launch_selcount(uint32_t ntiles, const uint32_t* tile_cell, const uin
                            uint32_t* selcount, hipStream_t st);
 hipError_t launch_route(uint32_t Q, uint32_t N, float thr, const uint32_t* selcount,
                         const uint32_t* counts, uint32_t* little, hipStream_t st);
+hipError_t launch_cells_grid(uint32_t Q, uint32_t a, const float* lo, const float* hi, const float* amin,
+                             const float* width, const uint32_t* grid, uint32_t P, const uint32_t* offset,
+                             double thr, uint32_t* cells, uint32_t* counts, uint32_t* little, uint8_t* flags,
+                             hipStream_t st);
+hipError_t launch_cell_flags(uint32_t Q, uint32_t P, const uint32_t* cells, const uint32_t* counts,
+                             const uint32_t* little, uint8_t* flags, hipStream_t st);
+hipError_t launch_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_t* bcell, const uint8_t* flags,
+                               uint32_t* lists, uint32_t* counts, uint32_t* little, hipStream_t st);
+hipError_t launch_merge_stream(uint32_t Q, uint32_t K, uint32_t* run_ids, float* run_dist, const uint32_t* ids,
+                               const float* dist, uint32_t* run_ctr, const uint32_t* ctr, bool first,
+                               hipStream_t st);
 hipError_t launch_centroid(const uint16_t* qh, const uint16_t* ch, const float* qn,
                            const float* cn, uint32_t Q, uint32_t C, uint32_t Qp, uint32_t Cp,
                            uint32_t Dp, float* dist, hipStream_t st);

@@ -70,60 +70,78 @@ __device__ __forceinline__ void hash_clear(uint32_t* H, uint32_t hsize) {
 }
 
 // ----------------------------------------------------------- row distances
-template <bool F16, int CPL>
+// Vector types: VT 0 = fp32, 1 = binary16, 2 = uint8.  A row is read in
+// 16-byte chunks of kEpc<VT> elements; queries are fp32 rows for VT 2 and
+// rows of the data's type otherwise.
+template <int VT>
+constexpr int kEpc = VT == 0 ? 4 : (VT == 1 ? 8 : 16);
+
+template <int VT, int CPL>
 struct QReg {
-    float v[CPL][F16 ? 8 : 4];
+    float v[CPL][kEpc<VT>];
 };
 
-template <bool F16>
-__device__ __forceinline__ void load_chunk(const char* base, uint32_t c, float (&x)[F16 ? 8 : 4]) {
+template <int VT>
+__device__ __forceinline__ void load_chunk(const char* base, uint32_t c, float (&x)[kEpc<VT>]) {
     const uint4 u = *reinterpret_cast<const uint4*>(base + size_t(c) * 16u);
-    if constexpr (F16) {
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    if constexpr (VT == 1) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            __half lo = __ushort_as_half(uint16_t(w[i] & 0xFFFFu));
-            __half hi = __ushort_as_half(uint16_t(w[i] >> 16));
-            x[2 * i] = __half2float(lo);
-            x[2 * i + 1] = __half2float(hi);
+            x[2 * i] = __half2float(__ushort_as_half(uint16_t(w[i] & 0xFFFFu)));
+            x[2 * i + 1] = __half2float(__ushort_as_half(uint16_t(w[i] >> 16)));
         }
+    } else if constexpr (VT == 2) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) x[4 * i + k] = float((w[i] >> (8 * k)) & 0xFFu);
     } else {
-        x[0] = __uint_as_float(u.x);
-        x[1] = __uint_as_float(u.y);
-        x[2] = __uint_as_float(u.z);
-        x[3] = __uint_as_float(u.w);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = __uint_as_float(w[i]);
     }
 }
 
-template <bool F16, int LPR, int CPL>
-__device__ __forceinline__ void load_query(QReg<F16, CPL>& q, const char* qrow, uint32_t nch) {
+template <int VT, int LPR, int CPL>
+__device__ __forceinline__ void load_query(QReg<VT, CPL>& q, const char* qrow, uint32_t nch) {
     const uint32_t l = lane_id() % LPR;
 #pragma unroll
     for (int m = 0; m < CPL; ++m) {
         const uint32_t c = l + m * LPR;
         if (c < nch) {
-            load_chunk<F16>(qrow, c, q.v[m]);
+            if constexpr (VT == 2) {
+                // fp32 query: one 16-element chunk is four 16-byte loads
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    float x[4];
+                    load_chunk<0>(qrow, 4 * c + k, x);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) q.v[m][4 * k + e] = x[e];
+                }
+            } else {
+                load_chunk<VT>(qrow, c, q.v[m]);
+            }
         } else {
 #pragma unroll
-            for (int e = 0; e < (F16 ? 8 : 4); ++e) q.v[m][e] = 0.0f;
+            for (int e = 0; e < kEpc<VT>; ++e) q.v[m][e] = 0.0f;
         }
     }
 }
 
 // Partial sum of one lane over its chunks l, l+LPR, ... in element order
 // (fp32 fma), the canonical order the oracle restates.
-template <bool F16, int LPR, int CPL>
-__device__ __forceinline__ float row_partial(const QReg<F16, CPL>& q, const char* row, uint32_t nch) {
+template <int VT, int LPR, int CPL>
+__device__ __forceinline__ float row_partial(const QReg<VT, CPL>& q, const char* row, uint32_t nch) {
     const uint32_t l = lane_id() % LPR;
     float acc = 0.0f;
 #pragma unroll
     for (int m = 0; m < CPL; ++m) {
         const uint32_t c = l + m * LPR;
         if (c < nch) {
-            float x[F16 ? 8 : 4];
-            load_chunk<F16>(row, c, x);
+            float x[kEpc<VT>];
+            load_chunk<VT>(row, c, x);
 #pragma unroll
-            for (int e = 0; e < (F16 ? 8 : 4); ++e) {
+            for (int e = 0; e < kEpc<VT>; ++e) {
                 const float d = q.v[m][e] - x[e];
                 acc = __builtin_fmaf(d, d, acc);
             }
@@ -134,8 +152,8 @@ __device__ __forceinline__ float row_partial(const QReg<F16, CPL>& q, const char
 
 // Distances of the n rows listed in S[0..n) (LDS).  Lane j with compact
 // index ci (< n) receives the distance of row S[ci] in `dist`.
-template <bool F16, int LPR, int CPL>
-__device__ __forceinline__ void eval_rows(const QReg<F16, CPL>& q, const char* vec, uint32_t rowbytes,
+template <int VT, int LPR, int CPL>
+__device__ __forceinline__ void eval_rows(const QReg<VT, CPL>& q, const char* vec, uint32_t rowbytes,
                                           uint32_t nch, const uint32_t* S, uint32_t n, uint32_t ci,
                                           float& dist) {
     constexpr uint32_t RPI = 64 / LPR;                  // rows per pass
@@ -148,7 +166,7 @@ __device__ __forceinline__ void eval_rows(const QReg<F16, CPL>& q, const char* v
         for (uint32_t b = 0; b < NB; ++b) {
             const uint32_t i = (k0 + b) * RPI + g;
             acc[b] = 0.0f;
-            if (i < n) acc[b] = row_partial<F16, LPR, CPL>(q, vec + size_t(S[i]) * rowbytes, nch);
+            if (i < n) acc[b] = row_partial<VT, LPR, CPL>(q, vec + size_t(S[i]) * rowbytes, nch);
         }
 #pragma unroll
         for (uint32_t b = 0; b < NB; ++b) {
@@ -176,8 +194,8 @@ __device__ __forceinline__ bool row_pass(const float* attrs, uint32_t a, uint32_
 
 // Evaluate candidate rows held one per lane (lanes with need=false keep dist
 // = +inf).  Returns the number of rows gathered.
-template <bool F16, int LPR, int CPL>
-__device__ __forceinline__ uint32_t eval_lanes(const QReg<F16, CPL>& q, const TravArgs& p, uint32_t* S,
+template <int VT, int LPR, int CPL>
+__device__ __forceinline__ uint32_t eval_lanes(const QReg<VT, CPL>& q, const TravArgs& p, uint32_t* S,
                                                uint32_t row, bool need, float& dist) {
     const uint64_t m = ballot(need);
     const uint32_t ci = need ? lanes_below(m) : 0xFFFFFFFFu;
@@ -186,7 +204,7 @@ __device__ __forceinline__ uint32_t eval_lanes(const QReg<F16, CPL>& q, const Tr
     wave_sync();
     const uint32_t n = __popcll(m);
     dist = __int_as_float(0x7F800000);
-    if (n) eval_rows<F16, LPR, CPL>(q, p.vec, p.rowbytes, p.nch, S, n, ci, dist);
+    if (n) eval_rows<VT, LPR, CPL>(q, p.vec, p.rowbytes, p.nch, S, n, ci, dist);
     wave_sync();
     return n;
 }
@@ -333,7 +351,7 @@ __device__ void sort128(uint64_t* W) {
 // One wavefront per query: the reference's fused kernel
 // select_path_contain_attr_filter_V2_without_output_with_post_pre_filter
 // (gpu_graph.cu:3266-4131), traversal branch.
-template <bool F16, int LPR, int CPL>
+template <int VT, int LPR, int CPL>
 __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
     extern __shared__ __align__(16) unsigned char smem[];
     uint64_t* A = reinterpret_cast<uint64_t*>(smem);   // Lpad
@@ -347,8 +365,8 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
     const uint32_t hsize = 1u << p.hbits;
     const uint32_t L = p.L, R = p.R, P = p.P, E = p.E;
 
-    QReg<F16, CPL> qv;
-    load_query<F16, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
+    QReg<VT, CPL> qv;
+    load_query<VT, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
     float lo[kMaxAttr], hi[kMaxAttr];
 #pragma unroll
     for (uint32_t d = 0; d < kMaxAttr; ++d) {
@@ -379,7 +397,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
         }
         wave_sync();
         float d;
-        n_dist += eval_lanes<F16, LPR, CPL>(qv, p, S, row, mine, d);
+        n_dist += eval_lanes<VT, LPR, CPL>(qv, p, S, row, mine, d);
         n_attr += R;
         if (mine) b = make_cand(d, row, pass);
     }
@@ -419,7 +437,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
             }
             n_attr += R;
             float d;
-            n_dist += eval_lanes<F16, LPR, CPL>(qv, p, S, nrow, isnew, d);
+            n_dist += eval_lanes<VT, LPR, CPL>(qv, p, S, nrow, isnew, d);
             b = mine ? make_cand(d, nrow, pass) : kCandSent;
             const uint32_t ip = merge_into(A, L, b, R, W);
             recycle_update(rc, p.rl, W, R, bleft, W);
@@ -441,7 +459,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
 #pragma unroll
             for (uint32_t e = 0; e < kMaxE; ++e) {
                 keys[e] = kEmpty;
-                if (cv && e < E) keys[e] = p.cross[(size_t(crow(ac)) * P + nxt) * E + e];
+                if (cv && e < E) keys[e] = p.cross[size_t(crow(ac)) * p.xrow + size_t(nxt) * p.xcell + e];
             }
             // Slots filled in order 0..127 (the reference fills them
             // concurrently); slot i follows candidate i % 64 and takes its
@@ -472,8 +490,8 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
                 const bool p0 = v0 && row_pass(p.attrs, p.a, r0, lo, hi);
                 const bool p1 = v1 && row_pass(p.attrs, p.a, r1, lo, hi);
                 float d0, d1;
-                const uint32_t n0 = eval_lanes<F16, LPR, CPL>(qv, p, S, r0, v0, d0);
-                const uint32_t n1 = eval_lanes<F16, LPR, CPL>(qv, p, S, r1, v1, d1);
+                const uint32_t n0 = eval_lanes<VT, LPR, CPL>(qv, p, S, r0, v0, d0);
+                const uint32_t n1 = eval_lanes<VT, LPR, CPL>(qv, p, S, r1, v1, d1);
                 n_dist += n0 + n1;
                 n_attr += n0 + n1;
                 if (v0) w0 = make_cand(d0, r0, p0);
@@ -557,7 +575,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
 // Filtered brute force over the query's cells (gpu_graph.cu:3788-4022): an
 // attribute scan of each cell's contiguous rows, compaction of the passing
 // rows, distance evaluation and a wave-held top-K keyed by (distance, row).
-template <bool F16, int LPR, int CPL>
+template <int VT, int LPR, int CPL>
 __global__ __launch_bounds__(64) void k_bruteforce(TravArgs p) {
     constexpr uint32_t U = 4;                 // 64-row chunks scanned per step
     __shared__ uint32_t S[64 * U + 64];
@@ -567,8 +585,8 @@ __global__ __launch_bounds__(64) void k_bruteforce(TravArgs p) {
     if (si >= p.srange[1]) return;
     const uint32_t q = p.sched[si];
     const uint32_t K = p.K, P = p.P;
-    QReg<F16, CPL> qv;
-    load_query<F16, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
+    QReg<VT, CPL> qv;
+    load_query<VT, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
     float lo[kMaxAttr], hi[kMaxAttr];
 #pragma unroll
     for (uint32_t d = 0; d < kMaxAttr; ++d) {
@@ -586,7 +604,7 @@ __global__ __launch_bounds__(64) void k_bruteforce(TravArgs p) {
             const uint32_t nb = nrows - base < 64u ? nrows - base : 64u;
             const bool mine = lane < nb;
             float d = 0.0f;
-            eval_rows<F16, LPR, CPL>(qv, p.vec, p.rowbytes, p.nch, S + base, nb,
+            eval_rows<VT, LPR, CPL>(qv, p.vec, p.rowbytes, p.nch, S + base, nb,
                                      mine ? lane : 0xFFFFFFFFu, d);
             const uint64_t c = mine ? make_cand(d, S[base + lane], true) : kCandSent;
             const uint64_t thr = ckey(readlane64(top, K - 1));
@@ -837,6 +855,143 @@ __global__ void k_route(uint32_t Q, uint32_t N, float thr, const uint32_t* selco
     if (q >= Q) return;
     const float proportion = float((1.0 * selcount[q]) / (1.0 * N));
     little[q] = proportion <= thr ? counts[q] : 0u;
+}
+
+// Arithmetic-grid cells (intersection_area_batch_mark_little_seg,
+// gpu_graph.cu:11095-11188): cell index of a value v on attribute d is
+// trunc((v - min_d) / width_d) (fp32), clamped to [0, g_d - 1] -- the
+// reference clamps only the upper index and writes past its flag array for
+// a range starting beyond the grid; clamping both ends selects the edge
+// cells, where a builder that clamps puts out-of-grid points.  Every
+// selected cell is "little" when the product over attributes of its overlap
+// with the range, in units of the cell width, is <= thr (fp64, no fused
+// operations, as the reference's double expression).  Cells come out in
+// ascending id; flags[q * P + c] = 1 (selected) | 2 (little); little[q] =
+// number of little cells.  An empty range (lo > hi) selects nothing, and
+// cells holding no point are never selected.
+__device__ __forceinline__ uint32_t grid_index(float v, float m, float w, uint32_t g) {
+    const float x = __fdiv_rn(__fsub_rn(v, m), w);
+    if (!(x > 0.0f)) return 0u;
+    if (x >= float(g)) return g - 1;
+    return uint32_t(x);
+}
+
+__global__ void k_cells_grid(uint32_t Q, uint32_t a, const float* lo, const float* hi, const float* amin,
+                             const float* width, const uint32_t* grid, uint32_t P, const uint32_t* offset,
+                             double thr, uint32_t* cells, uint32_t* counts, uint32_t* little, uint8_t* flags) {
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= Q) return;
+    uint8_t* fl = flags + size_t(q) * P;
+    for (uint32_t c = 0; c < P; ++c) fl[c] = 0;
+    uint32_t cl[kMaxAttr], ch[kMaxAttr], idx[kMaxAttr], g[kMaxAttr];
+    bool empty = false;
+#pragma unroll
+    for (uint32_t d = 0; d < kMaxAttr; ++d) {
+        if (d >= a) break;
+        g[d] = grid[d];
+        const float vl = lo[size_t(q) * a + d], vh = hi[size_t(q) * a + d];
+        if (!(vl <= vh)) empty = true;
+        cl[d] = grid_index(vl, amin[d], width[d], g[d]);
+        ch[d] = grid_index(vh, amin[d], width[d], g[d]);
+        idx[d] = cl[d];
+    }
+    uint32_t n = 0, nl = 0;
+    if (!empty) {
+        while (true) {
+            uint32_t pid = 0, f = 1;
+            for (int d = int(a) - 1; d >= 0; --d) { pid += idx[d] * f; f *= g[d]; }
+            if (offset[pid + 1] > offset[pid]) {
+                double area = 1.0;
+                for (uint32_t d = 0; d < a; ++d) {
+                    const double step = double(idx[d]), w = double(width[d]), m = double(amin[d]);
+                    const double cl0 = __dadd_rn(m, __dmul_rn(step, w));
+                    const double ch0 = __dadd_rn(m, __dmul_rn(__dadd_rn(step, 1.0), w));
+                    const double lb = fmax(cl0, double(lo[size_t(q) * a + d]));
+                    const double rb = fmin(ch0, double(hi[size_t(q) * a + d]));
+                    area = __dmul_rn(area, __ddiv_rn(__dsub_rn(rb, lb), w));
+                }
+                const bool lit = area <= thr;
+                cells[size_t(q) * P + n++] = pid;
+                nl += lit;
+                fl[pid] = uint8_t(1u | (lit ? 2u : 0u));
+            }
+            int d = int(a) - 1;
+            for (; d >= 0; --d) {
+                if (++idx[d] <= ch[d]) break;
+                idx[d] = cl[d];
+            }
+            if (d < 0) break;
+        }
+    }
+    counts[q] = n;
+    little[q] = nl;
+}
+
+// Per-cell flags from ordered cell lists: the first little[q] cells of a
+// query's list are little (the cells the brute-force branch scans).
+__global__ void k_cell_flags(uint32_t Q, uint32_t P, const uint32_t* cells, const uint32_t* counts,
+                             const uint32_t* little, uint8_t* flags) {
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= Q) return;
+    uint8_t* fl = flags + size_t(q) * P;
+    for (uint32_t c = 0; c < P; ++c) fl[c] = 0;
+    const uint32_t n = counts[q], l = little[q];
+    for (uint32_t i = 0; i < n; ++i) fl[cells[size_t(q) * P + i]] = uint8_t(1u | (i < l ? 2u : 0u));
+}
+
+// Cell lists of one streamed batch (fill_partition_info03, tools.cuh:1646-1670):
+// the query's selected cells among the batch's, in batch order, as batch
+// positions; the query takes the brute-force branch on this batch when all
+// of them are little (little = count), else it traverses them (little = 0).
+__global__ void k_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_t* bcell, const uint8_t* flags,
+                               uint32_t* lists, uint32_t* counts, uint32_t* little) {
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= Q) return;
+    const uint8_t* fl = flags + size_t(q) * P;
+    uint32_t n = 0;
+    bool all = true;
+    for (uint32_t i = 0; i < B; ++i) {
+        const uint8_t f = fl[bcell[i]];
+        if (f & 1u) {
+            lists[size_t(q) * B + n++] = i;
+            all = all && (f & 2u);
+        }
+    }
+    counts[q] = n;
+    little[q] = (n > 0 && all) ? n : 0u;
+}
+
+// Running top-K of a streamed search: merge the batch's sorted K results
+// into the running ones (a batch's entry goes first at equal distance, as
+// the reference's host merge, big_dataset_adapterV3.cuh:3785-3795) and add
+// its counters.  Batches hold disjoint cells, so ids never repeat.
+__global__ void k_merge_stream(uint32_t Q, uint32_t K, uint32_t* run_ids, float* run_dist, const uint32_t* ids,
+                               const float* dist, uint32_t* run_ctr, const uint32_t* ctr, uint32_t first) {
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= Q) return;
+    uint32_t* ri = run_ids + size_t(q) * K;
+    float* rd = run_dist + size_t(q) * K;
+    const uint32_t* ni = ids + size_t(q) * K;
+    const float* nd = dist + size_t(q) * K;
+    // counters add up; the route counter becomes (traversed batches) |
+    // (brute-force batches << 16)
+    uint32_t* rc = run_ctr + size_t(q) * GF_NCOUNTERS;
+    const uint32_t* nc = ctr + size_t(q) * GF_NCOUNTERS;
+    const uint32_t route = nc[C_ROUTE] == 1u ? 1u : (nc[C_ROUTE] == 2u ? 0x10000u : 0u);
+    if (first) {
+        for (uint32_t k = 0; k < K; ++k) { ri[k] = ni[k]; rd[k] = nd[k]; }
+        for (uint32_t c = 0; c < GF_NCOUNTERS; ++c) rc[c] = c == C_ROUTE ? route : nc[c];
+        return;
+    }
+    uint32_t oi[kBfKMax * 4];
+    float od[kBfKMax * 4];
+    for (uint32_t k = 0; k < K; ++k) { oi[k] = ri[k]; od[k] = rd[k]; }
+    uint32_t i = 0, j = 0;
+    for (uint32_t t = 0; t < K; ++t) {
+        if (od[i] < nd[j]) { ri[t] = oi[i]; rd[t] = od[i]; ++i; }
+        else { ri[t] = ni[j]; rd[t] = nd[j]; ++j; }
+    }
+    for (uint32_t c = 0; c < GF_NCOUNTERS; ++c) rc[c] += c == C_ROUTE ? route : nc[c];
 }
 
 // Query x centre squared distances |q|^2 + |c|^2 - 2 q.c with the dot
@@ -1589,28 +1744,25 @@ __global__ __launch_bounds__(64) void k_q_i8(const float* q, uint32_t D, int8_t*
     if (lane == 0) nq[r] = n;
 }
 
-template <bool F16, int LPR, int CPL>
+template <int VT, int LPR, int CPL>
 hipError_t launch_trav_t(const TravArgs& a, uint32_t lds, uint32_t grid, hipStream_t st) {
     if (grid == 0) return hipSuccess;
-    hipLaunchKernelGGL((k_traverse<F16, LPR, CPL>), dim3(grid), dim3(64), lds, st, a);
+    hipLaunchKernelGGL((k_traverse<VT, LPR, CPL>), dim3(grid), dim3(64), lds, st, a);
     return hipGetLastError();
 }
-template <bool F16, int LPR, int CPL>
+template <int VT, int LPR, int CPL>
 hipError_t launch_bf_t(const TravArgs& a, uint32_t grid, hipStream_t st) {
     if (grid == 0) return hipSuccess;
-    hipLaunchKernelGGL((k_bruteforce<F16, LPR, CPL>), dim3(grid), dim3(64), 0, st, a);
+    hipLaunchKernelGGL((k_bruteforce<VT, LPR, CPL>), dim3(grid), dim3(64), 0, st, a);
     return hipGetLastError();
 }
-
-template <bool F16, template <bool, int, int> class Fn, typename... Args>
-hipError_t dispatch_shape(const RowShape& rs, Args&&... args);
 
 }  // namespace
 
-RowShape row_shape(uint32_t D, bool f16) {
+RowShape row_shape(uint32_t D, int vt) {
     RowShape r;
-    r.f16 = f16;
-    const uint32_t elems = f16 ? 8u : 4u;
+    r.vt = vt;
+    const uint32_t elems = vt == 0 ? 4u : (vt == 1 ? 8u : 16u);
     r.nch = (D + elems - 1) / elems;
     r.lpr = 8;
     while (r.lpr < r.nch && r.lpr < 64) r.lpr <<= 1;
@@ -1618,56 +1770,38 @@ RowShape row_shape(uint32_t D, bool f16) {
     return r;
 }
 
-#define GF_SHAPES(F16, X)                                                       \
-    if (rs.lpr == 8 && rs.cpl == 1) return X<F16, 8, 1>;                       \
-    if (rs.lpr == 16 && rs.cpl == 1) return X<F16, 16, 1>;                     \
-    if (rs.lpr == 32 && rs.cpl == 1) return X<F16, 32, 1>;                     \
-    if (rs.lpr == 64 && rs.cpl == 1) return X<F16, 64, 1>;                     \
-    if (rs.lpr == 64 && rs.cpl == 2) return X<F16, 64, 2>;                     \
-    if (rs.lpr == 64 && rs.cpl == 3) return X<F16, 64, 3>;                     \
-    if (rs.lpr == 64 && rs.cpl == 4) return X<F16, 64, 4>;
+uint32_t row_shape_max_cpl(int vt) { return vt == 0 ? 4u : 2u; }
+
+// Instantiated shapes: LPR 8..64 with one chunk per lane, and 64 lanes with
+// up to 4 (fp32) or 2 (fp16, u8) chunks per lane.
+#define GF_DISPATCH_VT(VT_, CALL)                                                  \
+    do {                                                                           \
+        if (rs.lpr == 8 && rs.cpl == 1) return CALL(VT_, 8, 1);                     \
+        if (rs.lpr == 16 && rs.cpl == 1) return CALL(VT_, 16, 1);                   \
+        if (rs.lpr == 32 && rs.cpl == 1) return CALL(VT_, 32, 1);                   \
+        if (rs.lpr == 64 && rs.cpl == 1) return CALL(VT_, 64, 1);                   \
+        if (rs.lpr == 64 && rs.cpl == 2) return CALL(VT_, 64, 2);                   \
+        if (VT_ == 0 && rs.lpr == 64 && rs.cpl == 3) return CALL(0, 64, 3);         \
+        if (VT_ == 0 && rs.lpr == 64 && rs.cpl == 4) return CALL(0, 64, 4);         \
+    } while (0)
+#define GF_DISPATCH(CALL)                          \
+    do {                                           \
+        if (rs.vt == 0) GF_DISPATCH_VT(0, CALL);   \
+        if (rs.vt == 1) GF_DISPATCH_VT(1, CALL);   \
+        if (rs.vt == 2) GF_DISPATCH_VT(2, CALL);   \
+    } while (0)
 
 hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds, uint32_t grid, hipStream_t st) {
-#define X(F, L_, C_) launch_trav_t<F, L_, C_>(a, lds, grid, st)
-#define XT(F, L_, C_) X(F, L_, C_)
-    if (rs.f16) {
-        if (rs.lpr == 8 && rs.cpl == 1) return XT(true, 8, 1);
-        if (rs.lpr == 16 && rs.cpl == 1) return XT(true, 16, 1);
-        if (rs.lpr == 32 && rs.cpl == 1) return XT(true, 32, 1);
-        if (rs.lpr == 64 && rs.cpl == 1) return XT(true, 64, 1);
-        if (rs.lpr == 64 && rs.cpl == 2) return XT(true, 64, 2);
-    } else {
-        if (rs.lpr == 8 && rs.cpl == 1) return XT(false, 8, 1);
-        if (rs.lpr == 16 && rs.cpl == 1) return XT(false, 16, 1);
-        if (rs.lpr == 32 && rs.cpl == 1) return XT(false, 32, 1);
-        if (rs.lpr == 64 && rs.cpl == 1) return XT(false, 64, 1);
-        if (rs.lpr == 64 && rs.cpl == 2) return XT(false, 64, 2);
-        if (rs.lpr == 64 && rs.cpl == 3) return XT(false, 64, 3);
-        if (rs.lpr == 64 && rs.cpl == 4) return XT(false, 64, 4);
-    }
-#undef XT
-#undef X
+#define CALL_T(V, L_, C_) launch_trav_t<V, L_, C_>(a, lds, grid, st)
+    GF_DISPATCH(CALL_T);
+#undef CALL_T
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, uint32_t grid, hipStream_t st) {
-#define XT(F, L_, C_) launch_bf_t<F, L_, C_>(a, grid, st)
-    if (rs.f16) {
-        if (rs.lpr == 8 && rs.cpl == 1) return XT(true, 8, 1);
-        if (rs.lpr == 16 && rs.cpl == 1) return XT(true, 16, 1);
-        if (rs.lpr == 32 && rs.cpl == 1) return XT(true, 32, 1);
-        if (rs.lpr == 64 && rs.cpl == 1) return XT(true, 64, 1);
-        if (rs.lpr == 64 && rs.cpl == 2) return XT(true, 64, 2);
-    } else {
-        if (rs.lpr == 8 && rs.cpl == 1) return XT(false, 8, 1);
-        if (rs.lpr == 16 && rs.cpl == 1) return XT(false, 16, 1);
-        if (rs.lpr == 32 && rs.cpl == 1) return XT(false, 32, 1);
-        if (rs.lpr == 64 && rs.cpl == 1) return XT(false, 64, 1);
-        if (rs.lpr == 64 && rs.cpl == 2) return XT(false, 64, 2);
-        if (rs.lpr == 64 && rs.cpl == 3) return XT(false, 64, 3);
-        if (rs.lpr == 64 && rs.cpl == 4) return XT(false, 64, 4);
-    }
-#undef XT
+#define CALL_B(V, L_, C_) launch_bf_t<V, L_, C_>(a, grid, st)
+    GF_DISPATCH(CALL_B);
+#undef CALL_B
     return hipErrorInvalidValue;
 }
 
@@ -1830,6 +1964,37 @@ hipError_t launch_route(uint32_t Q, uint32_t N, float thr, const uint32_t* selco
                         uint32_t* little, hipStream_t st) {
     if (!Q) return hipSuccess;
     hipLaunchKernelGGL(k_route, dim3((Q + 255) / 256), dim3(256), 0, st, Q, N, thr, selcount, counts, little);
+    return hipGetLastError();
+}
+
+hipError_t launch_cells_grid(uint32_t Q, uint32_t a, const float* lo, const float* hi, const float* amin,
+                             const float* width, const uint32_t* grid, uint32_t P, const uint32_t* offset,
+                             double thr, uint32_t* cells, uint32_t* counts, uint32_t* little, uint8_t* flags,
+                             hipStream_t st) {
+    hipLaunchKernelGGL(k_cells_grid, dim3((Q + 63) / 64), dim3(64), 0, st, Q, a, lo, hi, amin, width, grid, P,
+                       offset, thr, cells, counts, little, flags);
+    return hipGetLastError();
+}
+
+hipError_t launch_cell_flags(uint32_t Q, uint32_t P, const uint32_t* cells, const uint32_t* counts,
+                             const uint32_t* little, uint8_t* flags, hipStream_t st) {
+    hipLaunchKernelGGL(k_cell_flags, dim3((Q + 63) / 64), dim3(64), 0, st, Q, P, cells, counts, little, flags);
+    return hipGetLastError();
+}
+
+hipError_t launch_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_t* bcell, const uint8_t* flags,
+                               uint32_t* lists, uint32_t* counts, uint32_t* little, hipStream_t st) {
+    hipLaunchKernelGGL(k_stream_lists, dim3((Q + 63) / 64), dim3(64), 0, st, Q, P, B, bcell, flags, lists, counts,
+                       little);
+    return hipGetLastError();
+}
+
+hipError_t launch_merge_stream(uint32_t Q, uint32_t K, uint32_t* run_ids, float* run_dist, const uint32_t* ids,
+                               const float* dist, uint32_t* run_ctr, const uint32_t* ctr, bool first,
+                               hipStream_t st) {
+    if (K > kBfKMax * 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_merge_stream, dim3((Q + 63) / 64), dim3(64), 0, st, Q, K, run_ids, run_dist, ids, dist,
+                       run_ctr, ctr, uint32_t(first));
     return hipGetLastError();
 }
 

@@ -1,0 +1,247 @@
+// Host-side state of libgarfield.so shared by gf_host.cpp (resident
+// indexes, the C ABI) and gf_stream.cpp (streamed indexes): owning device
+// and pinned host buffers, error macros, and the opaque gf_index / gf_batch.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "gf_internal.h"
+
+#define GF_HIP(x)                                                                              \
+    do {                                                                                       \
+        hipError_t e_ = (x);                                                                   \
+        if (e_ != hipSuccess)                                                                  \
+            throw gf::Error{GF_E_DEVICE, std::string(#x) + ": " + hipGetErrorString(e_)};          \
+    } while (0)
+
+#define GF_REQUIRE(cond, code, msg)                  \
+    do {                                             \
+        if (!(cond)) throw gf::Error{(code), (msg)};     \
+    } while (0)
+
+namespace gf {
+
+// Owning device buffer.
+template <typename T>
+struct DevBuf {
+    T* p = nullptr;
+    size_t n = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    ~DevBuf() { release(); }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    void alloc(size_t count) {
+        if (count == n && p) return;
+        release();
+        if (count == 0) return;
+        hipError_t e = hipMalloc(&p, count * sizeof(T));
+        if (e != hipSuccess) {
+            p = nullptr;
+            throw gf::Error{GF_E_NOMEM, "hipMalloc of " + std::to_string(count * sizeof(T)) + " bytes failed"};
+        }
+        n = count;
+    }
+    void upload(const T* src, size_t count) {
+        alloc(count);
+        if (count) GF_HIP(hipMemcpy(p, src, count * sizeof(T), hipMemcpyHostToDevice));
+    }
+    void upload(const std::vector<T>& v) { upload(v.data(), v.size()); }
+    size_t bytes() const { return n * sizeof(T); }
+};
+
+inline uint32_t round_up(uint32_t x, uint32_t m) { return (x + m - 1) / m * m; }
+
+// Owning pinned host buffer (hipHostMalloc): the source of streamed copies.
+template <typename T>
+struct PinBuf {
+    T* p = nullptr;
+    size_t n = 0;
+    PinBuf() = default;
+    PinBuf(const PinBuf&) = delete;
+    PinBuf& operator=(const PinBuf&) = delete;
+    ~PinBuf() { release(); }
+    void release() {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    void alloc(size_t count) {
+        release();
+        if (count == 0) return;
+        hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&p), count * sizeof(T), hipHostMallocDefault);
+        if (e != hipSuccess) {
+            p = nullptr;
+            throw gf::Error{GF_E_NOMEM, "hipHostMalloc of " + std::to_string(count * sizeof(T)) + " bytes failed"};
+        }
+        n = count;
+    }
+    size_t bytes() const { return n * sizeof(T); }
+};
+
+struct Timer {
+    hipEvent_t a = nullptr, b = nullptr;
+    hipStream_t s;
+    explicit Timer(hipStream_t st) : s(st) {
+        GF_HIP(hipEventCreate(&a));
+        GF_HIP(hipEventCreate(&b));
+        GF_HIP(hipEventRecord(a, s));
+    }
+    double stop() {
+        GF_HIP(hipEventRecord(b, s));
+        GF_HIP(hipEventSynchronize(b));
+        float ms = 0;
+        GF_HIP(hipEventElapsedTime(&ms, a, b));
+        return ms;
+    }
+    ~Timer() {
+        if (a) (void)hipEventDestroy(a);
+        if (b) (void)hipEventDestroy(b);
+    }
+};
+
+
+// A streamed index keeps no per-point array on the device.  Its static plan
+// groups cells into batches; each batch is stored in pinned host memory as
+// one packed image that a single hipMemcpyAsync moves into one of two device
+// buffers ("turns"), laid out as a small index of the batch's cells:
+//   vec    rows x rowbytes (the batch's cells in plan order, cell-major rows)
+//   graph  rows x R   cell-local neighbour ids
+//   attrs  rows x a   fp32
+//   gidx   rows       point id of each row
+//   lrow   rows       cell-local id of each row
+//   cross  B x rows x E: edge e of row r into the batch's i-th cell at
+//          (i * rows + r) * E + e (the reference's per-pair "T" slices,
+//          big_dataset_adapterV3.cuh:3539-3541)
+//   offset B + 1      first row of each batch cell
+//   bcell  B          cell id of each batch cell
+// Every section starts on a 256-byte boundary.
+struct StreamBatch {
+    uint32_t B = 0, rows = 0;
+    size_t o_vec = 0, o_graph = 0, o_attrs = 0, o_gidx = 0, o_lrow = 0, o_cross = 0, o_offset = 0, o_bcell = 0;
+    size_t bytes = 0;      // image size
+    size_t host_off = 0;   // image start in the pinned arena
+};
+
+struct StreamIndex {
+    std::vector<StreamBatch> batches;
+    PinBuf<char> host;
+    DevBuf<char> turn[2];
+    size_t max_bytes = 0;
+    uint64_t budget = 0;
+    uint32_t Bmax = 0, min_cell = 0;
+    hipStream_t copy = nullptr;
+    hipEvent_t ready[2] = {nullptr, nullptr}, freed[2] = {nullptr, nullptr};
+    ~StreamIndex() {
+        for (auto& e : ready) if (e) (void)hipEventDestroy(e);
+        for (auto& e : freed) if (e) (void)hipEventDestroy(e);
+        if (copy) (void)hipStreamDestroy(copy);
+    }
+};
+
+}  // namespace gf
+
+using gf::DevBuf;
+
+struct gf_index {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    uint32_t N = 0, D = 0, a = 0, P = 0, R = 0, E = 0, C = 0;
+    int32_t vdtype = GF_VEC_F32;
+    float alpha = 1.0f;
+    gf::RowShape rs{};
+    uint32_t rowbytes = 0, Cp = 0, Dp = 0;
+    std::vector<uint32_t> offset_h, grid_h;
+    DevBuf<char> vec;
+    DevBuf<float> attrs, l_q, r_q, cnorm;
+    DevBuf<uint32_t> graph, cross, offset, gidx, lrow, grid, doff, hist;
+    DevBuf<uint32_t> entry_ref;   // the reference's entry-point draw, made on first use
+    DevBuf<uint32_t> tile_cell, tile_row0, tile_n;
+    DevBuf<uint16_t> centres;
+    uint32_t ntiles = 0;
+    // Sub-cells (integer attributes spread by less than 65534 inside every
+    // cell, a <= 4): each cell is split by a rank grid of S bins per
+    // attribute; tiles of 16 points are grouped by sub-cell and carry the
+    // cell-major row and the packed 16-bit attribute offsets of each point.
+    bool sub = false;
+    uint32_t AW = 0, NS = 0, ntile = 0;
+    std::vector<uint32_t> ssize_h, stile_h;
+    DevBuf<uint32_t> sbase, scell, ssize, stile, tmeta;
+    DevBuf<int32_t> sbox, abase;
+    // Query-batch MFMA brute force (additionally: vectors integers in
+    // [0, 255], D a multiple of 64 up to 256): int8 tiles and norms.
+    bool i8 = false;
+    DevBuf<int8_t> vt;
+    DevBuf<int32_t> tnorm;
+    int ncu = 0;
+    // Streamed index (gf_index_create_streamed / gf_index_open_streamed):
+    // the per-point arrays above stay empty.
+    std::unique_ptr<gf::StreamIndex> sx;
+    ~gf_index() {
+        sx.reset();
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+    uint64_t device_bytes() const {
+        return vec.bytes() + attrs.bytes() + l_q.bytes() + r_q.bytes() + cnorm.bytes() + graph.bytes() +
+               cross.bytes() + offset.bytes() + gidx.bytes() + lrow.bytes() + grid.bytes() + doff.bytes() +
+               hist.bytes() + tile_cell.bytes() + tile_row0.bytes() + tile_n.bytes() + centres.bytes() +
+               sbase.bytes() + scell.bytes() + ssize.bytes() + stile.bytes() + tmeta.bytes() + sbox.bytes() +
+               abase.bytes() + vt.bytes() + tnorm.bytes() +
+               (sx ? sx->turn[0].bytes() + sx->turn[1].bytes() : 0);
+    }
+};
+
+struct gf_batch {
+    gf_index* ix = nullptr;
+    uint32_t Q = 0, Qp = 0, topc = 0;
+    bool marked = false;
+    bool i8 = false;
+    DevBuf<int8_t> q8;
+    DevBuf<int32_t> nq;
+    // brute-force schedule of stage C (tot: device totals and fit flags)
+    DevBuf<uint32_t> tot;
+    DevBuf<uint32_t> bcnt, bstart, pcnt, bq, nsub, part_off, icnt, ioff, bfq;
+    DevBuf<gf::BfItem> items;
+    DevBuf<uint64_t> part;
+    DevBuf<unsigned long long> stats;
+    DevBuf<float> qf32, qnorm, lo, hi, cdist, out_dist;
+    DevBuf<uint16_t> q16, q16v;
+    DevBuf<uint32_t> cells, counts, little, selcount, cellq, ccount, cstart, cfill, topk;
+    DevBuf<uint32_t> out_ids, counters, sched, entry, gbound;
+    // Per (query, cell) flags, 1 = selected | 2 = little: written by the
+    // arithmetic-grid stage A, else derived from the cell lists on use.
+    DevBuf<uint8_t> flags;
+    bool flags_ready = false;
+    // Streamed search: per-batch cell lists and results.
+    DevBuf<uint32_t> slist, scount, slittle, s_ids, s_ctr;
+    DevBuf<float> s_dist;
+};
+
+
+namespace gf {
+inline void set_device(const gf_index* ix) { GF_HIP(hipSetDevice(ix->device)); }
+}  // namespace gf
+
+namespace gf {
+// Checks shared by resident and streamed indexes, and the idx mapper
+// (tools.cuh:862-915): size[c] points per cell, ix.offset_h, gidx (row ->
+// point id), lrow (row -> cell-local id).  Every id the kernels dereference
+// is validated here, before any device call.
+void map_cells(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix, std::vector<uint32_t>& size,
+               std::vector<uint32_t>& gidx, std::vector<uint32_t>& lrow);
+// Streamed index (gf_stream.cpp): packs the plan's batch images and sizes
+// the device buffers; then the streamed stage C.
+void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_stream_plan* plan, gf_index& ix);
+void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* dists, gf_search_stats* stats);
+// Entry-point draws (mt19937 default seed, distinct uniform_int_distribution
+// draws in [0, range), std::random_shuffle after srand(1)): the first R.
+void entry_points_draw(uint32_t range, uint32_t ndraw, uint32_t R, uint32_t* out);
+}  // namespace gf

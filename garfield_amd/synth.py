@@ -98,6 +98,29 @@ def grid_scatter(attrs, grid):
     return l_q, r_q, pid_lists, global_pid.astype(np.int32)
 
 
+def grid_scatter_arith(attrs, grid, attr_min, attr_width):
+    """Arithmetic grid (the out-of-core driver's cells: width = ceil((max - min) / g), bigdataset_experiment.cu:63-70):
+    cell of v on attribute d = min(max(floor((v - min_d) / width_d), 0), g_d - 1).
+    l_q / r_q hold each cell's value interval [min + j w, min + (j + 1) w - 1]."""
+    attrs = np.asarray(attrs)
+    n, a = attrs.shape
+    l_q, r_q, pid_lists = [], [], []
+    for d in range(a):
+        g = int(grid[d])
+        m, w = float(attr_min[d]), float(attr_width[d])
+        idx = np.clip(np.floor((attrs[:, d].astype(np.float64) - m) / w), 0, g - 1).astype(np.int32)
+        l_q.append(np.array([m + j * w for j in range(g)]).astype(np.int32))
+        r_q.append(np.array([m + (j + 1) * w - 1 for j in range(g)]).astype(np.int32))
+        pid_lists.append(idx)
+    factors = np.ones(a, np.int64)
+    for d in range(a - 2, -1, -1):
+        factors[d] = factors[d + 1] * int(grid[d + 1])
+    global_pid = np.zeros(n, np.int64)
+    for d in range(a):
+        global_pid += factors[d] * pid_lists[d]
+    return l_q, r_q, pid_lists, global_pid.astype(np.int32)
+
+
 def cell_sizes(ix):
     return np.bincount(ix["global_pid"], minlength=ix["P"]).astype(np.uint32)
 
@@ -183,11 +206,15 @@ def kmeans_labels(vectors, C, iters, seed, device="cpu", chunk=65536):
     return labels.cpu().numpy().astype(np.int32)
 
 
-def build_index(vectors, attrs, grid, R, E, C=0, kmeans_iters=8, seed=5, device="cpu"):
-    """All index arrays, in the layout the files hold."""
+def build_index(vectors, attrs, grid, R, E, C=0, kmeans_iters=8, seed=5, device="cpu", arith=None):
+    """All index arrays, in the layout the files hold.  arith = (attr_min,
+    attr_width) builds the cells on an arithmetic grid instead of rank quantiles."""
     grid = np.asarray(grid, np.int64)
     P = int(np.prod(grid))
-    l_q, r_q, pid_lists, global_pid = grid_scatter(attrs, grid)
+    if arith is None:
+        l_q, r_q, pid_lists, global_pid = grid_scatter(attrs, grid)
+    else:
+        l_q, r_q, pid_lists, global_pid = grid_scatter_arith(attrs, grid, arith[0], arith[1])
     members = cell_members(global_pid, P)
     graphs = knn_cell_graphs(vectors, members, R, device=device)
     cross = cross_edges(vectors, members, E, device=device)

@@ -37,6 +37,8 @@ typedef int32_t gf_status;
 
 #define GF_VEC_F32 0        /* traversal distances on fp32 vectors */
 #define GF_VEC_F16 1        /* on binary16 copies half(x * f2h_factor), fp32 accumulation */
+#define GF_VEC_U8 2         /* on uint8 copies (vectors must be integers in [0, 255], as the
+                               reference's u8 datasets, tools.cuh:134-150), fp32 accumulation */
 
 typedef struct gf_index gf_index;
 typedef struct gf_batch gf_batch;
@@ -56,7 +58,7 @@ typedef struct {
 typedef struct {
     uint32_t degree;          /* --degree: per-cell graph degree R; 0 = from the files */
     float f2h_factor;         /* --f2h_factor: scale before fp16 conversion (0 means 1) */
-    int32_t vec_dtype;        /* GF_VEC_F32 or GF_VEC_F16 */
+    int32_t vec_dtype;        /* GF_VEC_F32, GF_VEC_F16 or GF_VEC_U8 */
     int32_t hist_contiguous;  /* 1: cell x cluster histogram by i / ceil(N/P) as the
                                  reference (tools.cuh:587-590); 0: by grid cell */
     int32_t device;           /* HIP device ordinal */
@@ -92,6 +94,29 @@ gf_status gf_index_create(const gf_index_host* host, const gf_open_opts* opts, g
 gf_status gf_index_close(gf_index* ix);
 gf_status gf_index_get_info(const gf_index* ix, gf_index_info* out);
 
+/* Streamed (out-of-core) index: the cells' graphs, vectors, attributes and
+ * the cross edges between cells of one batch stay in pinned host memory, in
+ * one packed image per batch of a static plan, and gf_search streams the
+ * batches through two device buffers with hipMemcpyAsync on a side stream,
+ * overlapped with the search of the previous batch.  Replaces the
+ * out-of-core driver's host-pinned loaders (get_graph_info_host,
+ * check.cu:572-623; load_result_pined, tools.cuh:241-255), its static batch
+ * plan (bigdataset_experiment.cu:271-277, 746-756) and the device buffers it
+ * sizes from the largest batch (bigdataset_experiment.cu:776-793). */
+typedef struct {
+    uint64_t device_budget;   /* bytes the two batch buffers may use (the device cap); 0 = no cap */
+    uint32_t nbatch;          /* batches in cells/sizes; 0 = consecutive cells, batch_cells per batch */
+    uint32_t batch_cells;     /* cells per batch when nbatch == 0 (the reference's MAX_BATCH_SIZE: 16) */
+    const uint32_t* sizes;    /* nbatch batch sizes */
+    const uint32_t* cells;    /* sum(sizes) cell ids, batch after batch; each cell at most once
+                                 (a cell in no batch is never searched) */
+} gf_stream_plan;
+
+gf_status gf_index_create_streamed(const gf_index_host* host, const gf_open_opts* opts,
+                                   const gf_stream_plan* plan, gf_index** out);
+gf_status gf_index_open_streamed(const gf_index_paths* paths, const gf_open_opts* opts,
+                                 const gf_stream_plan* plan, gf_index** out);
+
 /* A query batch: Q query vectors (Q*D fp32) and closed ranges lo/hi (Q*a),
  * uploaded to the device (realdataset_search.cu:2198-2245 load + f2h). */
 gf_status gf_batch_create(gf_index* ix, const float* queries, uint32_t Q,
@@ -109,15 +134,30 @@ gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms);
  * (the reference uses topc = 4).  Without labels the order is left as is. */
 gf_status gf_order_cells(gf_batch* b, uint32_t topc, double* ms);
 
+/* Stage A on an arithmetic grid -- intersection_area_mark_little_seg_batch_process
+ * (gpu_graph.cu:12066-12187) and its kernel intersection_area_batch_mark_little_seg
+ * (gpu_graph.cu:11095-11188), the out-of-core driver's stage A: attribute d
+ * has cells of width attr_width[d] from attr_min[d] (the index's grid shape);
+ * a selected cell is "little" when its overlap with the range, as a fraction
+ * of a cell, is <= threshold.  little[q] = number of little cells. */
+gf_status gf_mark_cells_grid(gf_batch* b, const float* attr_min /*a*/, const float* attr_width /*a*/,
+                             double threshold, double* ms);
+
 /* Stage C -- batch_graph_search_gpu_with_prefilter_and_postfilter<T>
- * (gpu_graph.cu:12463-12616) and its kernel (gpu_graph.cu:3266-4131). */
+ * (gpu_graph.cu:12463-12616) and its kernel (gpu_graph.cu:3266-4131).  On a
+ * streamed index: batch_graph_search_gpu_with_prefilter_batch_process_compressed_graph_T_dataset_resident_u8
+ * (big_dataset_adapterV3.cuh:3719-4117) and its kernel (:2674-3316): per batch,
+ * each query searches its selected cells of the batch, in plan order (brute
+ * force when all of them are little), from fresh entry points, and its K
+ * results merge into a running top-K; postfilter does not apply. */
 typedef struct {
     uint32_t L;            /* candidate list length (the reference's ef / TOPM) */
     uint32_t K;            /* results per query (reference: 10) */
     uint32_t rl;           /* recycle list length (reference: 10), <= 16 */
     uint32_t postfilter;   /* --postfilter: queries with >= this many cells skip traversal */
     const uint32_t* entry_points;  /* R cell-local entry ids, or NULL for the
-                                      reference's mt19937 draw (gpu_graph.cu:12503-12526) */
+                                      reference's mt19937 draw (gpu_graph.cu:12503-12526;
+                                      streamed: big_dataset_adapterV3.cuh:3862-3875) */
 } gf_search_opts;
 
 #define GF_NCOUNTERS 8  /* per-query counters, same order as the oracle's */
@@ -132,6 +172,10 @@ typedef struct {
     double ops_bruteforce;   /* arithmetic of the brute-force kernel (int8 MACs x 2 on MFMA) */
     uint32_t bf_mfma;        /* 1 if the brute force ran as the int8 MFMA query-batch kernel */
     double ms_bf_kernel;     /* device time of the MFMA brute-force kernel alone (no schedule, no merge) */
+    /* streamed index only */
+    uint32_t n_batches;      /* batches of the plan */
+    double bytes_h2d;        /* bytes copied host -> device */
+    double ms_h2d;           /* sum of the copies' device times */
 } gf_search_stats;
 
 gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids /*Q*K*/,
@@ -146,6 +190,11 @@ gf_status gf_batch_get_cells(const gf_batch* b, uint32_t* cells, uint32_t* count
 gf_status gf_batch_set_cells(gf_batch* b, const uint32_t* cells, const uint32_t* counts,
                              const uint32_t* little);
 gf_status gf_batch_get_centroid(const gf_batch* b, float* dist /*Q*C*/, uint32_t* topc /*Q*topc*/);
+/* Per (query, cell) flags, Q*P bytes: 1 = selected, 2 = little (the
+ * reference's partition_is_selected and is_little_seg, gpu_graph.cu:12066-12187).
+ * After gf_mark_cells or gf_batch_set_cells the first little[q] cells of a
+ * query's list are the little ones. */
+gf_status gf_batch_get_cell_flags(const gf_batch* b, uint8_t* flags);
 gf_status gf_batch_get_counters(const gf_batch* b, uint32_t* counters /*Q*GF_NCOUNTERS*/);
 
 /* f2h (tools.cuh:308-320) on the device: out[i] = binary16(x[i]*alpha), RNE. */

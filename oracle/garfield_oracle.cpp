@@ -28,10 +28,13 @@ const uint32_t XSTEP = 64;           // 128 / base_number(2), gpu_graph.cu:3267
 
 uint32_t f32_bits(float f) { uint32_t u; std::memcpy(&u, &f, 4); return u; }
 
-// Lanes per row of the HIP distance kernels: a row is split in 16-byte chunks,
-// LPR = next power of two >= chunk count, clamped to [8, 64].
+// Lanes per row of the HIP distance kernels: a row is split in 16-byte chunks
+// (4 fp32, 8 fp16 or 16 u8 elements), LPR = next power of two >= chunk
+// count, clamped to [8, 64].
+uint32_t chunk_elems(int vdtype) { return vdtype == 0 ? 4u : (vdtype == 1 ? 8u : 16u); }
+
 uint32_t lanes_per_row(uint32_t D, int vdtype) {
-    uint32_t elems = vdtype ? 8u : 4u;
+    const uint32_t elems = chunk_elems(vdtype);
     uint32_t nch = (D + elems - 1) / elems;
     uint32_t lpr = 8;
     while (lpr < nch && lpr < 64) lpr <<= 1;
@@ -40,16 +43,18 @@ uint32_t lanes_per_row(uint32_t D, int vdtype) {
 
 // Canonical distance: lane l of LPR accumulates chunks l, l+LPR, ... with fp32
 // fma in element order; the lane sums are combined by an xor butterfly.
+// Elements past D (row padding) are zero in both operands.
 float canon_dist(const float* q, const float* x, uint32_t D, int vdtype) {
-    const uint32_t ce = vdtype ? 8u : 4u;
-    const uint32_t nch = D / ce;
+    const uint32_t ce = chunk_elems(vdtype);
+    const uint32_t nch = (D + ce - 1) / ce;
     const uint32_t lpr = lanes_per_row(D, vdtype);
     float s[64];
     for (uint32_t l = 0; l < lpr; ++l) {
         float acc = 0.0f;
         for (uint32_t c = l; c < nch; c += lpr)
             for (uint32_t e = 0; e < ce; ++e) {
-                float d = q[c * ce + e] - x[c * ce + e];
+                const uint32_t k = c * ce + e;
+                float d = k < D ? q[k] - x[k] : 0.0f;
                 acc = std::fmaf(d, d, acc);
             }
         s[l] = acc;
@@ -126,8 +131,8 @@ bool passes(const QueryState& s, uint32_t gid) {
 float point_dist(QueryState& s, uint32_t gid) {
     const orc_index* ix = s.c->ix;
     const uint32_t D = ix->D;
-    if (ix->vdtype == 0)
-        return canon_dist(s.q, ix->vec_f32 + (size_t)gid * D, D, 0);
+    if (ix->vdtype != 1)
+        return canon_dist(s.q, ix->vec_f32 + (size_t)gid * D, D, ix->vdtype);
     s.xbuf.resize(D);
     for (uint32_t i = 0; i < D; ++i) s.xbuf[i] = orc_h2f(ix->vec_f16[(size_t)gid * D + i]);
     return canon_dist(s.q, s.xbuf.data(), D, 1);
@@ -168,7 +173,7 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
     const orc_index* ix = c.ix;
     const uint32_t D = ix->D, R = ix->R, E = ix->E, P = ix->P, a = ix->a;
     std::vector<float> qv(D);
-    if (ix->vdtype == 0) {
+    if (ix->vdtype != 1) {
         std::memcpy(qv.data(), (const float*)queries + (size_t)qi * D, sizeof(float) * D);
     } else {
         const uint16_t* qh = (const uint16_t*)queries + (size_t)qi * D;
@@ -487,6 +492,62 @@ void orc_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi,
     }
 }
 
+void orc_cells_grid(uint32_t Q, uint32_t a, const float* lo, const float* hi, const uint32_t* grid,
+                    const float* amin, const float* width, double thr, const uint32_t* cell_size,
+                    uint32_t* cells, uint32_t* counts, uint32_t* little, uint8_t* flags) {
+    uint32_t P = 1;
+    for (uint32_t d = 0; d < a; ++d) P *= grid[d];
+    for (uint32_t q = 0; q < Q; ++q) {
+        uint8_t* fl = flags + (size_t)q * P;
+        std::memset(fl, 0, P);
+        std::vector<int64_t> cl(a), ch(a);
+        bool empty = false;
+        for (uint32_t d = 0; d < a; ++d) {
+            const float vl = lo[(size_t)q * a + d], vh = hi[(size_t)q * a + d];
+            const int64_t g = grid[d];
+            if (!(vl <= vh)) empty = true;
+            // (unsigned)((l - min) / width) in fp32, both ends clamped to [0, g - 1]
+            auto index = [&](float v) -> int64_t {
+                const float x = (v - amin[d]) / width[d];
+                if (!(x > 0.0f)) return 0;
+                if (x >= (float)g) return g - 1;
+                return (int64_t)x;
+            };
+            cl[d] = index(vl);
+            ch[d] = index(vh);
+        }
+        uint32_t n = 0, nl = 0;
+        if (!empty) {
+            std::vector<int64_t> idx(cl);
+            while (true) {
+                uint32_t pid = 0, f = 1;
+                for (int d = (int)a - 1; d >= 0; --d) { pid += (uint32_t)idx[d] * f; f *= grid[d]; }
+                if (!cell_size || cell_size[pid] > 0) {
+                    double area = 1.0;                      // gpu_graph.cu:11158-11168
+                    for (uint32_t d = 0; d < a; ++d) {
+                        const double step = (double)idx[d], w = (double)width[d], m = (double)amin[d];
+                        const double lb = std::max(m + step * w, (double)lo[(size_t)q * a + d]);
+                        const double rb = std::min(m + (step + 1.0) * w, (double)hi[(size_t)q * a + d]);
+                        area *= (rb - lb) / w;
+                    }
+                    const bool lit = area <= thr;
+                    cells[(size_t)q * P + n++] = pid;
+                    nl += lit;
+                    fl[pid] = (uint8_t)(1u | (lit ? 2u : 0u));
+                }
+                int d = (int)a - 1;                           // last attribute fastest: ascending ids
+                for (; d >= 0; --d) {
+                    if (++idx[d] <= ch[d]) break;
+                    idx[d] = cl[d];
+                }
+                if (d < 0) break;
+            }
+        }
+        counts[q] = n;
+        little[q] = nl;
+    }
+}
+
 void orc_selectivity(uint32_t Q, uint32_t N, uint32_t a, const float* attrs,
                      const float* lo, const float* hi, float threshold,
                      const uint32_t* counts, uint32_t* selcount, uint32_t* little,
@@ -555,12 +616,10 @@ void orc_sort_cells(uint32_t Q, uint32_t P, uint32_t C, uint32_t k, uint32_t* ce
     }
 }
 
-void orc_entry_points(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
-    const uint32_t avg = (N + P - 1) / P;
-    const uint32_t rand_max = N - (P - 1) * avg;
+void orc_entry_draw(uint32_t range, uint32_t ndraw, uint32_t R, uint32_t* out) {
     std::mt19937 rng;
-    std::uniform_int_distribution<> intd(0, (int)rand_max - 1);
-    const uint32_t want = std::min<uint32_t>(R * 10, rand_max);
+    std::uniform_int_distribution<> intd(0, (int)range - 1);
+    const uint32_t want = std::min<uint32_t>(ndraw, range);
     std::vector<unsigned> v(want);
     std::unordered_set<unsigned> seen;
     uint32_t k = 0;
@@ -573,10 +632,15 @@ void orc_entry_points(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
     for (uint32_t j = 0; j < R; ++j) out[j] = j < want ? v[j] : j;
 }
 
+void orc_entry_points(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
+    const uint32_t avg = (N + P - 1) / P;
+    orc_entry_draw(N - (P - 1) * avg, R * 10, R, out);
+}
+
 float orc_distance(const orc_index* ix, const void* q, uint32_t gid) {
     std::vector<float> qv(ix->D), xv(ix->D);
-    if (ix->vdtype == 0)
-        return canon_dist((const float*)q, ix->vec_f32 + (size_t)gid * ix->D, ix->D, 0);
+    if (ix->vdtype != 1)
+        return canon_dist((const float*)q, ix->vec_f32 + (size_t)gid * ix->D, ix->D, ix->vdtype);
     for (uint32_t i = 0; i < ix->D; ++i) {
         qv[i] = orc_h2f(((const uint16_t*)q)[i]);
         xv[i] = orc_h2f(ix->vec_f16[(size_t)gid * ix->D + i]);

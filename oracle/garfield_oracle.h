@@ -33,8 +33,8 @@ extern "C" {
 /* Index in the reference's representation (point-id order, idx mapper). */
 typedef struct {
     uint32_t N, D, a, P, R, E;
-    int32_t vdtype;               /* 0: fp32 vectors, 1: fp16 bit patterns */
-    const float* vec_f32;         /* N*D, point-id order */
+    int32_t vdtype;               /* 0: fp32 vectors, 1: fp16 bit patterns, 2: u8 values (in vec_f32) */
+    const float* vec_f32;         /* N*D, point-id order (vdtype 0 and 2) */
     const uint16_t* vec_f16;      /* N*D, point-id order, binary16 bits */
     const float* attrs;           /* N*a */
     const uint32_t* graph;        /* N*R, per-cell graphs concatenated in cell order */
@@ -72,6 +72,16 @@ void orc_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi,
                const uint32_t* cell_size /* P or NULL: cells with no point are skipped */,
                uint32_t* cells, uint32_t* counts);
 
+/* gpu_graph.cu:11095-11188 intersection_area_batch_mark_little_seg (arithmetic
+ * grid): cell index trunc((v - min) / width) in fp32, clamped to [0, g - 1]
+ * (the reference clamps only the upper one); little when the product of
+ * per-attribute overlaps in cell widths (fp64, unfused) is <= thr.  An empty
+ * range (lo > hi) selects nothing.  flags Q*P: 1 selected |
+ * 2 little; little[q] = little cells; cells ascending (stride P). */
+void orc_cells_grid(uint32_t Q, uint32_t a, const float* lo, const float* hi, const uint32_t* grid,
+                    const float* amin, const float* width, double thr, const uint32_t* cell_size,
+                    uint32_t* cells, uint32_t* counts, uint32_t* little, uint8_t* flags);
+
 /* real_dataset_adapter.cuh:346-383 prefiltering_tag_elements: exact count of
  * points passing the range, and the routing value little[q]. */
 void orc_selectivity(uint32_t Q, uint32_t N, uint32_t a, const float* attrs,
@@ -100,6 +110,10 @@ void orc_sort_cells(uint32_t Q, uint32_t P, uint32_t C, uint32_t k,
  * uniform_int_distribution<>(0, rand_max-1) distinct draws, random_shuffle
  * after srand(1); rand_max = N - (P-1)*ceil(N/P). */
 void orc_entry_points(uint32_t N, uint32_t P, uint32_t R, uint32_t* out);
+/* The draw itself: min(ndraw, range) distinct values in [0, range), shuffled,
+ * the first R (big_dataset_adapterV3.cuh:3862-3875 draws 10 L below the
+ * smallest cell). */
+void orc_entry_draw(uint32_t range, uint32_t ndraw, uint32_t R, uint32_t* out);
 
 /* Canonical squared L2 distance between query q and point gid (the HIP
  * kernels' summation order). */

@@ -103,6 +103,24 @@ def cells(lo, hi, grid, l_q, r_q, cell_size=None):
     return out, cnt
 
 
+def cells_grid(lo, hi, grid, attr_min, attr_width, threshold, cell_size=None):
+    """Arithmetic-grid stage A: (cells Q x P, counts, little counts, flags Q x P)."""
+    lo = _c(lo, np.float32)
+    hi = _c(hi, np.float32)
+    grid = _c(grid, np.uint32)
+    Q, a = lo.shape
+    P = int(np.prod(grid))
+    out = np.zeros((Q, P), np.uint32)
+    cnt = np.empty(Q, np.uint32)
+    lit = np.empty(Q, np.uint32)
+    flags = np.empty((Q, P), np.uint8)
+    cs = None if cell_size is None else _c(cell_size, np.uint32)
+    load().orc_cells_grid(C.c_uint32(Q), C.c_uint32(a), _p(lo), _p(hi), _p(grid), _p(_c(attr_min, np.float32)),
+                          _p(_c(attr_width, np.float32)), C.c_double(threshold),
+                          _p(cs) if cs is not None else None, _p(out), _p(cnt), _p(lit), _p(flags))
+    return out, cnt, lit, flags
+
+
 def selectivity(attrs, lo, hi, threshold, counts, nthreads=0):
     attrs = _c(attrs, np.float32)
     lo = _c(lo, np.float32)
@@ -150,10 +168,17 @@ def entry_points(N, P, R):
     return out
 
 
+def entry_draw(range_, ndraw, R):
+    out = np.empty(R, np.uint32)
+    load().orc_entry_draw(C.c_uint32(range_), C.c_uint32(ndraw), C.c_uint32(R), _p(out))
+    return out
+
+
 class OracleIndex:
     """The index in the reference's representation (point-id order + idx mapper)."""
 
-    def __init__(self, vectors, attrs, global_pid, P, cell_graphs, cross, vec_f16=None):
+    def __init__(self, vectors, attrs, global_pid, P, cell_graphs, cross, vec_f16=None, u8=False):
+        """u8=True: the HIP path's uint8 vector mode (vectors hold the integer values)."""
         self.vectors = _c(vectors, np.float32)
         self.vec_f16 = None if vec_f16 is None else _c(vec_f16, np.uint16)
         self.attrs = _c(attrs, np.float32)
@@ -163,7 +188,7 @@ class OracleIndex:
         self.gidx, self.lidx, self.offset = idx_mapper(global_pid, P)
         N, D = self.vectors.shape
         self.s = _Index(N, D, self.attrs.shape[1], P, self.graph.shape[1], self.cross.shape[1] // P,
-                        0 if self.vec_f16 is None else 1, _p(self.vectors),
+                        (2 if u8 else 0) if self.vec_f16 is None else 1, _p(self.vectors),
                         None if self.vec_f16 is None else _p(self.vec_f16), _p(self.attrs), _p(self.graph),
                         _p(self.offset), _p(self.gidx), _p(self.lidx), _p(self.cross))
 

@@ -181,3 +181,31 @@ def test_file_reader_returns_the_written_arrays(files, tmp_path):
     open(str(bad) + ".grid", "wb").write(open(paths["grid"], "rb").read() + b"\0\0\0\0")
     r = subprocess.run([str(exe), str(bad), str(tmp_path)], capture_output=True, text=True)
     assert r.returncode == 1 and "trailing" in r.stderr
+
+
+def test_streamed_plan_validation(files):
+    """gf_index_create_streamed rejects bad plans and a device budget below
+    two batch images before any device call."""
+    d, ix, paths = files
+    l_q, r_q = synth.quantile_arrays(ix)
+    args = (ix["vectors"], ix["attrs"], ix["grid"], l_q, r_q, ix["global_pid"], ix["cell_graphs"], ix["cross"])
+
+    def status(**kw):
+        try:
+            gl.Index.create_streamed(*args, **kw)
+        except gl.GarfieldError as e:
+            return e.status
+        return 0
+
+    assert status(plan=[[0, 1], [1, 2]]) == 1          # cell twice
+    assert status(plan=[[0, 1], [4]]) == 1             # cell id beyond P = 4
+    assert status(plan=[[0, 1], []]) == 1              # empty batch
+    assert status(plan=[[0, 1, 2, 3]], device_budget=4096) == 6
+    assert status(vec_dtype=gl.VEC_F16) == 6
+    bad = ix["vectors"].copy()
+    bad[0, 0] = 0.5
+    try:
+        gl.Index.create_streamed(bad, *args[1:])
+        raise AssertionError("non-integer vectors accepted for GF_VEC_U8")
+    except gl.GarfieldError as e:
+        assert e.status == 1

@@ -1,0 +1,263 @@
+"""Streamed (out-of-core) search, the arithmetic-grid stage A and the uint8
+vector mode, through the C ABI, against the CPU oracle.
+
+The streamed search is checked bit-exactly (ids, fp32 distances, counters)
+against the oracle run batch by batch: for each batch of the plan the
+oracle searches the batch's selected cells in plan order (the batch's cells
+renumbered to come first, so its tie order is the batch's row order), and
+the per-batch top K are merged with the batch's entry first at equal
+distance.  With one batch holding every cell it must equal the resident
+search on the same cell lists and entry points.
+"""
+import numpy as np
+import pytest
+
+from garfield_amd import synth
+import garfield_amd._lib as gl
+
+pytestmark = pytest.mark.gpu
+
+GRID = [4, 4]
+AMIN = np.zeros(2, np.float32)
+WIDTH = np.full(2, 2500.0, np.float32)
+
+
+def _print_case(name, **kw):
+    print(f"[case] {name} " + " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+@pytest.fixture(scope="module")
+def world_stream():
+    N, D, Q = 24000, 64, 200
+    rng = np.random.default_rng(41)
+    vec = synth.uniform_int_vectors(N, D, 42)
+    att = rng.integers(0, 10000, (N, 2)).astype(np.int32)
+    queries = synth.uniform_int_vectors(Q, D, 43)
+    sel = synth.log_uniform(Q, 0.02, 0.3, 44)
+    lo, hi = synth.ranges_for_selectivity(Q, 2, sel, 45)
+    lo[0] = [20000, 20000]          # beyond the grid: the last cell
+    hi[0] = [30000, 30000]
+    lo[1] = [5000, 100]             # empty on attribute 0
+    hi[1] = [4000, 9000]
+    lo[2] = [0, 0]                  # everything
+    hi[2] = [9999, 9999]
+    ix = synth.build_index(vec, att, GRID, 16, 2, 0, arith=(AMIN, WIDTH))
+    cfg = dict(queries=queries, lo=lo.astype(np.float32), hi=hi.astype(np.float32))
+    return cfg, ix
+
+
+def _args(ix):
+    l_q, r_q = synth.quantile_arrays(ix)
+    return (ix["vectors"], ix["attrs"], ix["grid"], l_q, r_q, ix["global_pid"], ix["cell_graphs"], ix["cross"])
+
+
+def _oracle_stream(ix, plan, cfg, flags, ent, L, K=10, rl=10):
+    """Per-batch oracle searches merged into a running top K (see module doc)."""
+    from oracle import oracle as orc
+    P, E, N = ix["P"], ix["E"], ix["vectors"].shape[0]
+    sizes = synth.cell_sizes(ix)
+    goff = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    Q = cfg["queries"].shape[0]
+    run_ids = run_d = run_c = None
+    for batch in plan:
+        order = list(batch) + [c for c in range(P) if c not in batch]
+        new_of = np.empty(P, np.int64)
+        new_of[order] = np.arange(P)
+        graphs = np.concatenate([ix["cell_graphs"][goff[c]:goff[c + 1]] for c in order])
+        cross = ix["cross"].reshape(N, P, E)[:, order, :].reshape(N, P * E)
+        O = orc.OracleIndex(ix["vectors"], ix["attrs"], new_of[ix["global_pid"]].astype(np.uint32), P, graphs,
+                            cross, u8=True)
+        cells = np.zeros((Q, P), np.uint32)
+        cnt = np.zeros(Q, np.uint32)
+        lit = np.zeros(Q, np.uint32)
+        for q in range(Q):
+            mine = [i for i, c in enumerate(batch) if flags[q, c] & 1]
+            cells[q, :len(mine)] = mine
+            cnt[q] = len(mine)
+            lit[q] = len(mine) if mine and all(flags[q, batch[i]] & 2 for i in mine) else 0
+        ids, d, c = O.search(cfg["queries"], cfg["lo"], cfg["hi"], cells, cnt, lit, ent, L, K=K, rl=rl)
+        c = c.copy()
+        c[:, 7] = np.where(c[:, 7] == 1, 1, np.where(c[:, 7] == 2, 1 << 16, 0))
+        if run_ids is None:
+            run_ids, run_d, run_c = ids.copy(), d.copy(), c.astype(np.int64)
+            continue
+        for q in range(Q):
+            oi, od = run_ids[q].copy(), run_d[q].copy()
+            i = j = 0
+            for t in range(K):
+                if od[i] < d[q, j]:
+                    run_ids[q, t], run_d[q, t] = oi[i], od[i]
+                    i += 1
+                else:
+                    run_ids[q, t], run_d[q, t] = ids[q, j], d[q, j]
+                    j += 1
+        run_c += c
+    return run_ids, run_d, run_c
+
+
+def _shuffled_plan(P, per, seed):
+    cells = np.random.default_rng(seed).permutation(P)
+    return [[int(c) for c in cells[i:i + per]] for i in range(0, P, per)]
+
+
+def test_cells_grid_matches_oracle(world_stream):
+    from oracle import oracle as orc
+    cfg, ix = world_stream
+    _print_case("cells-grid")
+    sizes = synth.cell_sizes(ix)
+    dev = gl.Index.from_arrays(*_args(ix), vec_dtype=gl.VEC_U8)
+    sdev = gl.Index.create_streamed(*_args(ix), batch_cells=4)
+    for thr in (0.0, 0.05, 0.5, 2.0):
+        oc, on, ol, of = orc.cells_grid(cfg["lo"], cfg["hi"], GRID, AMIN, WIDTH, thr, sizes)
+        for d in (dev, sdev):
+            b = d.batch(cfg["queries"], cfg["lo"], cfg["hi"])
+            b.mark_cells_grid(AMIN, WIDTH, thr)
+            c, n, l, _ = b.get_cells()
+            assert np.array_equal(n, on) and np.array_equal(l, ol)
+            for q in range(len(n)):
+                assert np.array_equal(c[q, :n[q]], oc[q, :on[q]]), q
+            assert np.array_equal(b.get_cell_flags(), of)
+            b.close()
+    assert on[0] == 1 and oc[0, 0] == 15 and on[1] == 0 and on[2] == 16
+    sdev.close()
+    dev.close()
+
+
+@pytest.mark.parametrize("L", [32, 100])
+def test_u8_resident_traversal_parity(world_stream, L):
+    import garfield_amd as gf
+    from oracle import oracle as orc
+    cfg, ix = world_stream
+    _print_case("u8-traverse", L=L)
+    dev = gl.Index.from_arrays(*_args(ix), vec_dtype=gl.VEC_U8)
+    assert dev.vec_dtype == gl.VEC_U8
+    b = dev.batch(cfg["queries"], cfg["lo"], cfg["hi"])
+    b.mark_cells_grid(AMIN, WIDTH, 0.0)
+    gc, gn, gl_, _ = b.get_cells()
+    ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], ix["R"])
+    ids, dists, st = b.search(L=L, K=10, rl=10, entry_points=ent)
+    ctr = b.get_counters()
+    O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"], ix["cross"],
+                        u8=True)
+    oids, od, oc = O.search(cfg["queries"], cfg["lo"], cfg["hi"], gc, gn, gl_, ent, L)
+    assert np.array_equal(ids, oids)
+    assert np.array_equal(dists.view(np.uint32), od.view(np.uint32))
+    if st.bf_mfma:
+        # the MFMA brute force evaluates every scanned point, the oracle only the passing ones
+        rows = oc[:, 7] == 2
+        oc[rows, 1] = oc[rows, 5]
+    assert np.array_equal(ctr, oc)
+    b.close()
+    dev.close()
+
+
+def test_u8_resident_gather_bruteforce(world_stream):
+    """K = 20 (above the MFMA route's 16): the gather brute force on u8 rows."""
+    import garfield_amd as gf
+    from oracle import oracle as orc
+    cfg, ix = world_stream
+    _print_case("u8-bruteforce")
+    dev = gl.Index.from_arrays(*_args(ix), vec_dtype=gl.VEC_U8)
+    b = dev.batch(cfg["queries"], cfg["lo"], cfg["hi"])
+    b.mark_cells_grid(AMIN, WIDTH, 0.0)
+    gc, gn, _, _ = b.get_cells()
+    b.set_cells(gc, gn, gn)     # every query on the brute-force route
+    ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], ix["R"])
+    ids, dists, st = b.search(L=32, K=20, rl=10, entry_points=ent)
+    assert st.bf_mfma == 0
+    O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"], ix["cross"],
+                        u8=True)
+    oids, od, oc = O.search(cfg["queries"], cfg["lo"], cfg["hi"], gc, gn, gn, ent, 32, K=20)
+    assert np.array_equal(ids, oids)
+    assert np.array_equal(dists.view(np.uint32), od.view(np.uint32))
+    assert np.array_equal(b.get_counters(), oc)
+    b.close()
+    dev.close()
+
+
+def test_stream_one_batch_equals_resident(world_stream):
+    import garfield_amd as gf
+    cfg, ix = world_stream
+    _print_case("stream-one-batch")
+    P = ix["P"]
+    res = gl.Index.from_arrays(*_args(ix), vec_dtype=gl.VEC_U8)
+    sx = gl.Index.create_streamed(*_args(ix), plan=[list(range(P))])
+    ent = gf.entry_points(ix["vectors"].shape[0], P, ix["R"])
+    out = []
+    for d in (res, sx):
+        b = d.batch(cfg["queries"], cfg["lo"], cfg["hi"])
+        b.mark_cells_grid(AMIN, WIDTH, 0.02)
+        c, n, l, _ = b.get_cells()
+        l = np.where(np.arange(len(n)) % 3 == 0, n, 0).astype(np.uint32)   # every third query: brute force
+        b.set_cells(c, n, l)
+        ids, dists, st = b.search(L=64, K=10, rl=10, entry_points=ent)
+        out.append((ids, dists, b.get_counters(), l, n))
+        b.close()
+    (i0, d0, c0, l0, n0), (i1, d1, c1, _, _) = out
+    assert np.array_equal(i0, i1)
+    assert np.array_equal(d0.view(np.uint32), d1.view(np.uint32))
+    trav = (l0 == 0) & (n0 > 0)
+    assert trav.any() and (l0 > 0).any()
+    assert np.array_equal(c0[trav, :7], c1[trav, :7]) and np.all(c1[trav, 7] == 1)
+    assert np.all(c1[l0 > 0, 7] == 1 << 16)
+    sx.close()
+    res.close()
+
+
+@pytest.mark.parametrize("L,thr,per", [(16, 0.02, 4), (64, 0.1, 3), (100, 0.0, 16)])
+def test_stream_batches_match_oracle(world_stream, L, thr, per):
+    from oracle import oracle as orc
+    cfg, ix = world_stream
+    _print_case("stream-batches", L=L, thr=thr, per=per)
+    P = ix["P"]
+    plan = _shuffled_plan(P, per, seed=L)
+    sx = gl.Index.create_streamed(*_args(ix), plan=plan)
+    b = sx.batch(cfg["queries"], cfg["lo"], cfg["hi"])
+    b.mark_cells_grid(AMIN, WIDTH, thr)
+    flags = b.get_cell_flags()
+    ids, dists, st = b.search(L=L, K=10, rl=10)
+    ctr = b.get_counters()
+    assert st.n_batches == len(plan) and st.bytes_h2d > 0
+    sizes = synth.cell_sizes(ix)
+    ent = orc.entry_draw(int(sizes[sizes > 0].min()), 10 * L, ix["R"])
+    oids, od, oc = _oracle_stream(ix, plan, cfg, flags, ent, L)
+    bad = np.nonzero(np.any(ids != oids, axis=1))[0]
+    assert bad.size == 0, f"{bad.size} queries differ, first {bad[:5]}: {ids[bad[0]]} vs {oids[bad[0]]}"
+    assert np.array_equal(dists.view(np.uint32), od.view(np.uint32))
+    assert np.array_equal(ctr.astype(np.int64), oc)
+    # a second search on the same batch (state reuse), smaller L
+    ids2, _, _ = b.search(L=max(8, L // 2), K=10, rl=10)
+    ent2 = orc.entry_draw(int(sizes[sizes > 0].min()), 10 * max(8, L // 2), ix["R"])
+    oids2, _, _ = _oracle_stream(ix, plan, cfg, flags, ent2, max(8, L // 2))
+    assert np.array_equal(ids2, oids2)
+    b.close()
+    sx.close()
+
+
+def test_stream_under_device_budget(world_stream):
+    """A budget below half the resident index: the streamed index fits it and
+    still returns the resident brute-force results (recall 1 on the exact
+    route), with its device memory within the budget."""
+    cfg, ix = world_stream
+    _print_case("stream-budget")
+    P = ix["P"]
+    res = gl.Index.from_arrays(*_args(ix), vec_dtype=gl.VEC_U8)
+    budget = res.device_bytes // 2
+    sx = gl.Index.create_streamed(*_args(ix), plan=_shuffled_plan(P, 2, seed=9), device_budget=budget)
+    assert sx.device_bytes <= budget
+    out = []
+    for d in (res, sx):
+        b = d.batch(cfg["queries"], cfg["lo"], cfg["hi"])
+        b.mark_cells_grid(AMIN, WIDTH, 10.0)       # every cell little: exact brute force
+        ids, dists, st = b.search(L=32, K=10, rl=10)
+        out.append((ids, dists))
+        b.close()
+    (i0, d0), (i1, d1) = out
+    assert np.array_equal(d0.view(np.uint32), d1.view(np.uint32))
+    # ids agree wherever the distance is not tied (batches merge ties in plan order)
+    for q in range(i0.shape[0]):
+        vals, cnt = np.unique(d0[q], return_counts=True)
+        single = np.isin(d0[q], vals[cnt == 1]) & (d0[q] != d0[q, -1])
+        assert np.array_equal(i0[q, single], i1[q, single]), q
+    sx.close()
+    res.close()

@@ -174,15 +174,12 @@ def _glibc_rand_seed1():
         i += 1
 
 
-def test_entry_points_restate_libstdcxx_draws():
-    N, P, R = 1_000_000, 16, 32
-    avg = (N + P - 1) // P
-    rand_max = N - (P - 1) * avg
-    assert rand_max == 62500
+def _libstdcxx_draw(urange, want):
+    """std::mt19937 (default seed) + uniform_int_distribution<>(0, urange - 1)
+    distinct draws, then std::random_shuffle with glibc rand() after srand(1)."""
     # std::mt19937 default seed 5489 == numpy's MT19937 init_genrand(5489)
     mt = np.random.RandomState(5489)
-    want, seen, vals = R * 10, set(), []
-    urange = rand_max          # uniform_int_distribution<>(0, rand_max - 1)
+    seen, vals = set(), []
     while len(vals) < want:
         # bounded draw by 64-bit multiply (Lemire 2019), as libstdc++ does
         # for a 32-bit engine and a range below 2^32
@@ -201,7 +198,100 @@ def test_entry_points_restate_libstdcxx_draws():
     for i in range(1, want):       # std::random_shuffle
         j = next(rnd) % (i + 1)
         vals[i], vals[j] = vals[j], vals[i]
-    assert list(orc.entry_points(N, P, R)) == vals[:R]
+    return vals
+
+
+def test_entry_points_restate_libstdcxx_draws():
+    N, P, R = 1_000_000, 16, 32
+    avg = (N + P - 1) // P
+    rand_max = N - (P - 1) * avg
+    assert rand_max == 62500
+    assert list(orc.entry_points(N, P, R)) == _libstdcxx_draw(rand_max, R * 10)[:R]
+
+
+def test_entry_draw_streamed_rule():
+    # out-of-core host (big_dataset_adapterV3.cuh:3862-3875): 10 L distinct
+    # draws below the smallest cell; a range smaller than 10 L is exhausted
+    for rng_, L, R in ((3000, 64, 16), (500, 100, 32), (40, 8, 32)):
+        want = min(10 * L, rng_)
+        ref = _libstdcxx_draw(rng_, want)
+        ref = [ref[j] if j < want else j for j in range(R)]
+        assert list(orc.entry_draw(rng_, 10 * L, R)) == ref
+    # the resident rule is the same draw over N - (P - 1) ceil(N / P)
+    assert np.array_equal(orc.entry_points(100000, 16, 16), orc.entry_draw(100000 - 15 * 6250, 160, 16))
+
+
+def test_cells_grid_integer_brute_force():
+    """Arithmetic-grid cells against exhaustive enumeration of the integer
+    values in each range, the area formula against the closed form
+    sum over cells = prod_d (hi_d - lo_d) / w_d for ranges inside the grid,
+    and every little flag against exact rational arithmetic."""
+    from fractions import Fraction
+    rng = np.random.default_rng(7)
+    for a, grid in ((1, [7]), (2, [4, 5]), (3, [3, 2, 4])):
+        P = int(np.prod(grid))
+        amin = rng.integers(-50, 50, a).astype(np.float32)
+        width = rng.integers(1, 40, a).astype(np.float32)
+        Q = 300
+        lo = (amin + rng.integers(-60, 200, (Q, a))).astype(np.float32)
+        hi = (lo + rng.integers(-5, 120, (Q, a))).astype(np.float32)   # some empty (hi < lo)
+        thr = 0.3
+        cells, cnt, lit, flags = orc.cells_grid(lo, hi, grid, amin, width, thr)
+        for q in range(Q):
+            per_dim = []
+            for d in range(a):
+                m, w, g = int(amin[d]), int(width[d]), grid[d]
+                cellof = lambda v: min(max((v - m) // w, 0), g - 1)
+                per_dim.append(sorted({cellof(v) for v in range(int(lo[q, d]), int(hi[q, d]) + 1)}))
+            want = []
+            if all(per_dim):
+                idx = np.stack(np.meshgrid(*per_dim, indexing="ij"), -1).reshape(-1, a)
+                mult = np.array([int(np.prod(grid[d + 1:])) for d in range(a)])
+                want = sorted(int(x) for x in idx @ mult)
+            assert cnt[q] == len(want) and list(cells[q, :cnt[q]]) == want, q
+            assert np.array_equal(np.nonzero(flags[q] & 1)[0], want)
+            areas = []
+            for pid in want:
+                rem, t = pid, []
+                for d in range(a - 1, -1, -1):
+                    t.append(rem % grid[d])
+                    rem //= grid[d]
+                t = t[::-1]
+                ar = Fraction(1)
+                for d in range(a):
+                    m, w = int(amin[d]), int(width[d])
+                    lb = max(m + t[d] * w, int(lo[q, d]))
+                    rb = min(m + (t[d] + 1) * w, int(hi[q, d]))
+                    ar *= Fraction(rb - lb, w)
+                areas.append(ar)
+                if abs(ar - Fraction(thr)) > Fraction(1, 10 ** 9):
+                    assert bool(flags[q, pid] & 2) == (ar <= Fraction(thr)), (q, pid)
+            assert lit[q] == int(np.count_nonzero(flags[q] & 2))
+            inside = all(lo[q, d] >= amin[d] and hi[q, d] < amin[d] + grid[d] * width[d] and lo[q, d] <= hi[q, d]
+                         for d in range(a))
+            if inside and want:
+                closed = Fraction(1)
+                for d in range(a):
+                    closed *= Fraction(int(hi[q, d]) - int(lo[q, d]), int(width[d]))
+                assert sum(areas) == closed
+
+
+def test_u8_mode_distance():
+    """u8 vector mode: 16-element chunks; exact on integer queries (any
+    order), within the fp32 bound of fp64 on fractional ones."""
+    rng = np.random.default_rng(3)
+    N, D = 200, 128
+    x = rng.integers(0, 256, (N, D)).astype(np.float32)
+    pid = rng.integers(0, 4, N).astype(np.uint32)
+    members = synth.cell_members(pid, 4)
+    graphs = np.concatenate([np.zeros((len(m), 4), np.uint32) for m in members])
+    O = orc.OracleIndex(x, np.zeros((N, 1), np.float32), pid, 4, graphs, np.zeros((N, 4), np.uint32), u8=True)
+    qi = rng.integers(0, 256, D).astype(np.float32)
+    qf = (rng.random(D) * 255).astype(np.float32)
+    for g in range(0, N, 17):
+        assert O.distance(qi, g) == float(np.sum((qi.astype(np.int64) - x[g].astype(np.int64)) ** 2))
+        ref = np.sum((qf.astype(np.float64) - x[g]) ** 2)
+        assert abs(O.distance(qf, g) - ref) <= 1e-6 * ref + 1e-3
 
 
 @pytest.fixture(scope="module")
