@@ -67,19 +67,41 @@ gf_status run_guarded(const std::function<void()>& fn) {
 // 65535, which no range accepts).
 void build_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, const std::vector<uint32_t>& size,
                     gf_index& ix) {
-    const uint32_t a = ix.a, P = ix.P;
-    if (a > 4) return;
+    gf::SubHost sh;
+    if (!gf::compute_subcells(h, gidx, size, ix.offset_h, ix.a, ix.P, sh)) return;
+    ix.AW = sh.AW;
+    ix.NS = sh.NS;
+    ix.ntile = sh.ntile;
+    ix.ssize_h = sh.ssize;
+    ix.stile_h = sh.stile;
+    ix.abase.upload(sh.abase);
+    ix.sbase.upload(sh.sbase);
+    ix.scell.upload(sh.scell);
+    ix.ssize.upload(sh.ssize);
+    ix.stile.upload(sh.stile);
+    ix.sbox.upload(sh.sbox);
+    ix.tmeta.upload(sh.tmeta);
+    ix.sub = true;
+}
+
+}  // namespace
+
+namespace gf {
+
+bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, const std::vector<uint32_t>& size,
+                      const std::vector<uint32_t>& offset_h, uint32_t a, uint32_t P, SubHost& out) {
+    if (a > 4) return false;
     std::vector<int32_t> abase(size_t(P) * a, 0);
     for (uint32_t c = 0; c < P; ++c)
         for (uint32_t d = 0; d < a; ++d) {
             double mn = 0.0, mx = 0.0;
-            for (uint32_t r = ix.offset_h[c]; r < ix.offset_h[c + 1]; ++r) {
+            for (uint32_t r = offset_h[c]; r < offset_h[c + 1]; ++r) {
                 const double x = h.attrs[size_t(gidx[r]) * a + d];
-                if (!(x == std::floor(x) && x >= -2147483648.0 && x < 2147483648.0)) return;
-                mn = r == ix.offset_h[c] ? x : std::min(mn, x);
-                mx = r == ix.offset_h[c] ? x : std::max(mx, x);
+                if (!(x == std::floor(x) && x >= -2147483648.0 && x < 2147483648.0)) return false;
+                mn = r == offset_h[c] ? x : std::min(mn, x);
+                mx = r == offset_h[c] ? x : std::max(mx, x);
             }
-            if (mx - mn > 65533.0) return;
+            if (mx - mn > 65533.0) return false;
             abase[size_t(c) * a + d] = int32_t(mn);
         }
     const uint32_t AW = (a + 1) / 2, MW = 16 * (1 + AW);
@@ -87,7 +109,7 @@ void build_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, c
     std::vector<int32_t> sbox;
     auto attr = [&](uint32_t r, uint32_t d) { return int32_t(h.attrs[size_t(gidx[r]) * a + d]); };
     for (uint32_t c = 0; c < P; ++c) {
-        const uint32_t off = ix.offset_h[c], n = size[c];
+        const uint32_t off = offset_h[c], n = size[c];
         uint32_t S = n ? std::max<uint32_t>(1u, uint32_t(std::lround(std::pow(n / 1024.0, 1.0 / a)))) : 1u;
         while (S > 1 && std::pow(double(S), double(a)) > 4096.0) --S;
         uint32_t nsc = 1;
@@ -133,24 +155,18 @@ void build_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, c
         sbase[c + 1] = sbase[c] + nsc;
     }
     stile.push_back(uint32_t(tmeta.size() / MW));
-    ix.AW = AW;
-    ix.NS = sbase[P];
-    ix.ntile = stile.back();
-    ix.ssize_h = ssize;
-    ix.stile_h = stile;
-    ix.abase.upload(abase);
-    ix.sbase.upload(sbase);
-    ix.scell.upload(scell);
-    ix.ssize.upload(ssize);
-    ix.stile.upload(stile);
-    ix.sbox.upload(sbox);
-    ix.tmeta.upload(tmeta);
-    ix.sub = true;
+    out.AW = AW;
+    out.NS = sbase[P];
+    out.ntile = stile.back();
+    out.sbase = std::move(sbase);
+    out.scell = std::move(scell);
+    out.ssize = std::move(ssize);
+    out.stile = std::move(stile);
+    out.sbox = std::move(sbox);
+    out.tmeta = std::move(tmeta);
+    out.abase = std::move(abase);
+    return true;
 }
-
-}  // namespace
-
-namespace gf {
 
 void map_cells(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix, std::vector<uint32_t>& size,
                std::vector<uint32_t>& gidx, std::vector<uint32_t>& lrow) {
@@ -298,7 +314,8 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
         if (ints) {
             ix.vt.alloc(size_t(ix.ntile) * (D / 64) * 1024);
             ix.tnorm.alloc(size_t(ix.ntile) * 32);
-            GF_HIP(gf::launch_tile_i8(vec_f32_dev, D, ix.tmeta.p, ix.AW, ix.ntile, ix.vt.p, ix.tnorm.p, ix.stream));
+            GF_HIP(gf::launch_tile_i8(vec_f32_dev, false, D, ix.tmeta.p, ix.AW, ix.ntile, ix.vt.p, ix.tnorm.p,
+                                      ix.stream));
             ix.i8 = true;
         }
         GF_HIP(hipStreamSynchronize(ix.stream));
@@ -564,6 +581,7 @@ gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms) {
         GF_REQUIRE(!ix->sx, GF_E_UNSUPPORTED,
                    "a streamed index has no resident attributes: use gf_mark_cells_grid or gf_batch_set_cells");
         b->flags_ready = false;
+        b->bf_all = true;
         set_device(ix);
         hipStream_t st = ix->stream;
         Timer t(st);
@@ -616,6 +634,7 @@ gf_status gf_mark_cells_grid(gf_batch* b, const float* attr_min, const float* at
         if (ms) *ms = el;
         b->marked = true;
         b->flags_ready = true;
+        b->bf_all = false;
     });
 }
 
@@ -744,6 +763,12 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             sc.little = b->little.p; sc.lo = b->lo.p; sc.hi = b->hi.p; sc.nsub = b->nsub.p; sc.bcnt = b->bcnt.p;
             sc.bstart = b->bstart.p; sc.bq = b->bq.p;
             sc.ok = tot + 3; sc.nbf = tot + 9;
+            if (!b->bf_all) {
+                if (b->bfmask.n < size_t(Q) * ix->P) b->bfmask.alloc(size_t(Q) * ix->P);
+                GF_HIP(gf::launch_cell_flags(Q, ix->P, b->cells.p, b->counts.p, b->little.p, b->bfmask.p, st));
+                sc.bfm = b->bfmask.p;
+                sc.bP = ix->P;
+            }
             GF_HIP(hipMemsetAsync(b->nsub.p, 0, size_t(Q) * sizeof(uint32_t), st));
             GF_HIP(hipMemsetAsync(b->pcnt.p, 0, size_t(Q) * sizeof(uint32_t), st));
             GF_HIP(hipMemsetAsync(b->gbound.p, 0xFF, size_t(Q) * sizeof(uint32_t), st));
@@ -900,6 +925,7 @@ gf_status gf_batch_set_cells(gf_batch* b, const uint32_t* cells, const uint32_t*
         GF_HIP(hipMemcpy(b->little.p, little, Q * 4, hipMemcpyHostToDevice));
         b->marked = true;
         b->flags_ready = false;
+        b->bf_all = false;
     });
 }
 

@@ -156,6 +156,10 @@ struct BfSchedArgs {
     uint32_t* bq;
     const uint32_t* ok;        // bq and part are large enough (pass 2)
     const uint32_t* nbf;       // device count of brute-force queries (0: nothing to do)
+    // Optional (null: every sub-cell a range reaches): per (query, cell),
+    // stride bP, bit 2 = the cell is one the query's brute force scans.
+    const uint8_t* bfm;
+    uint32_t bP;
 };
 // Query schedule (gpu_graph.cu:12485-12493): traversal queries by descending
 // cell count, then brute-force queries.  tot[0..2] = traversal, brute-force,
@@ -189,8 +193,9 @@ hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, uint32_t gri
 hipError_t launch_fill_results(uint32_t* ids, float* dist, uint32_t n, hipStream_t st);
 hipError_t launch_bf_i8(const BfGemmArgs& a, uint32_t nwg, hipStream_t st);
 hipError_t launch_bf_final(const BfFinalArgs& a, uint32_t grid, hipStream_t st);
-hipError_t launch_tile_i8(const float* vec_cm, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
+hipError_t launch_tile_i8(const void* vec_cm, bool u8, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
                           int8_t* vt, int32_t* tnorm, hipStream_t st);
+hipError_t launch_note_bf(const uint32_t* tot, uint32_t* note, hipStream_t st);
 hipError_t launch_subsel(const SubSelArgs& a, hipStream_t st);
 hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st);
 hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bstart, uint32_t NS, uint32_t* icnt,
@@ -233,6 +238,8 @@ hipError_t launch_cell_flags(uint32_t Q, uint32_t P, const uint32_t* cells, cons
                              const uint32_t* little, uint8_t* flags, hipStream_t st);
 hipError_t launch_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_t* bcell, const uint8_t* flags,
                                uint32_t* lists, uint32_t* counts, uint32_t* little, hipStream_t st);
+hipError_t launch_batch_need(uint32_t Q, uint32_t P, uint32_t nbatch, const uint32_t* plan_cells,
+                             const uint32_t* plan_off, const uint8_t* flags, uint32_t* need, hipStream_t st);
 hipError_t launch_merge_stream(uint32_t Q, uint32_t K, uint32_t* run_ids, float* run_dist, const uint32_t* ids,
                                const float* dist, uint32_t* run_ctr, const uint32_t* ctr, bool first,
                                hipStream_t st);

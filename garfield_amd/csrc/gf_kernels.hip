@@ -961,6 +961,33 @@ __global__ void k_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_
     little[q] = (n > 0 && all) ? n : 0u;
 }
 
+// What each batch of a streamed plan must do for this query batch (one
+// workgroup per batch): need[b] bit 0 = some query takes the brute force on
+// it (all its selected cells of the batch little), bit 1 = some query
+// traverses it; 0 = no query selects any of its cells.
+__global__ __launch_bounds__(256) void k_batch_need(uint32_t Q, uint32_t P, const uint32_t* plan_cells,
+                                                    const uint32_t* plan_off, const uint8_t* flags, uint32_t* need) {
+    __shared__ uint32_t acc;
+    const uint32_t bi = blockIdx.x;
+    if (threadIdx.x == 0) acc = 0;
+    __syncthreads();
+    const uint32_t c0 = plan_off[bi], c1 = plan_off[bi + 1];
+    uint32_t mine = 0;
+    for (uint32_t q = threadIdx.x; q < Q; q += blockDim.x) {
+        const uint8_t* fl = flags + size_t(q) * P;
+        uint32_t n = 0;
+        bool all = true;
+        for (uint32_t i = c0; i < c1; ++i) {
+            const uint8_t f = fl[plan_cells[i]];
+            if (f & 1u) { ++n; all = all && (f & 2u); }
+        }
+        if (n) mine |= all ? 1u : 2u;
+    }
+    if (mine) atomicOr(&acc, mine);
+    __syncthreads();
+    if (threadIdx.x == 0) need[bi] = acc;
+}
+
 // Running top-K of a streamed search: merge the batch's sorted K results
 // into the running ones (a batch's entry goes first at equal distance, as
 // the reference's host merge, big_dataset_adapterV3.cuh:3785-3795) and add
@@ -1330,7 +1357,8 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
         if (q < p.Q) {
             const uint32_t cnt = p.counts[q], lit = p.little[q];
             const bool trav = cnt < p.postfilter && cnt != lit;
-            hit = !trav && lit > 0 && sub_relation(box, sa.a, load_range(sa.a, p.lo, p.hi, q)) != 0;
+            hit = !trav && lit > 0 && (!p.bfm || (p.bfm[size_t(q) * p.bP + sa.scell[s]] & 2u)) &&
+                  sub_relation(box, sa.a, load_range(sa.a, p.lo, p.hi, q)) != 0;
         }
         const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
         if (lane == 0) wcnt[wave] = uint32_t(__builtin_popcountll(m));
@@ -1449,6 +1477,15 @@ __global__ void k_total(const uint32_t* cnt, const uint32_t* start, uint32_t n, 
     const uint32_t t = n ? start[n - 1] + cnt[n - 1] : 0u;
     out[0] = t;
     out[1] = (t <= cap && (cap2 == 0 || uint64_t(t) * mul <= cap2)) ? 1u : 0u;
+}
+
+// Keeps a streamed batch's brute-force schedule fit flag and pair total
+// (tot[3], tot[2]) past the next batch: note[0] = fits, note[1] = pairs.
+__global__ void k_note_bf(const uint32_t* tot, uint32_t* note) {
+    if (threadIdx.x == 0) {
+        note[0] = tot[3];
+        note[1] = tot[2];
+    }
 }
 
 template <int KS, int AW, int KT>
@@ -1705,7 +1742,8 @@ __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
 // Index build: int8 tiles (operand layout of BfGemmArgs::vt) of the sub-cell
 // tile order and per tile [-floor(|x'|^2 / 2) x 16][|x'|^2 x 16] (padding
 // points are all zero).
-__global__ __launch_bounds__(64) void k_tile_i8(const float* vec, uint32_t D, const uint32_t* tmeta, uint32_t AW,
+template <typename T>
+__global__ __launch_bounds__(64) void k_tile_i8(const T* vec, uint32_t D, const uint32_t* tmeta, uint32_t AW,
                                                int8_t* vt, int32_t* tnorm) {
     const uint32_t t = blockIdx.x, lane = lane_id();
     const uint32_t col = lane & 15u;
@@ -1849,10 +1887,20 @@ hipError_t launch_stats(const StatsArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_tile_i8(const float* vec_cm, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
+hipError_t launch_tile_i8(const void* vec_cm, bool u8, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
                           int8_t* vt, int32_t* tnorm, hipStream_t st) {
     if (!ntile) return hipSuccess;
-    hipLaunchKernelGGL(k_tile_i8, dim3(ntile), dim3(64), 0, st, vec_cm, D, tmeta, AW, vt, tnorm);
+    if (u8)
+        hipLaunchKernelGGL(k_tile_i8<uint8_t>, dim3(ntile), dim3(64), 0, st, static_cast<const uint8_t*>(vec_cm), D,
+                           tmeta, AW, vt, tnorm);
+    else
+        hipLaunchKernelGGL(k_tile_i8<float>, dim3(ntile), dim3(64), 0, st, static_cast<const float*>(vec_cm), D,
+                           tmeta, AW, vt, tnorm);
+    return hipGetLastError();
+}
+
+hipError_t launch_note_bf(const uint32_t* tot, uint32_t* note, hipStream_t st) {
+    hipLaunchKernelGGL(k_note_bf, dim3(1), dim3(64), 0, st, tot, note);
     return hipGetLastError();
 }
 
@@ -1986,6 +2034,13 @@ hipError_t launch_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_
                                uint32_t* lists, uint32_t* counts, uint32_t* little, hipStream_t st) {
     hipLaunchKernelGGL(k_stream_lists, dim3((Q + 63) / 64), dim3(64), 0, st, Q, P, B, bcell, flags, lists, counts,
                        little);
+    return hipGetLastError();
+}
+
+hipError_t launch_batch_need(uint32_t Q, uint32_t P, uint32_t nbatch, const uint32_t* plan_cells,
+                             const uint32_t* plan_off, const uint8_t* flags, uint32_t* need, hipStream_t st) {
+    if (!nbatch) return hipSuccess;
+    hipLaunchKernelGGL(k_batch_need, dim3(nbatch), dim3(256), 0, st, Q, P, plan_cells, plan_off, flags, need);
     return hipGetLastError();
 }
 

@@ -111,23 +111,33 @@ struct Timer {
 
 // A streamed index keeps no per-point array on the device.  Its static plan
 // groups cells into batches; each batch is stored in pinned host memory as
-// one packed image that a single hipMemcpyAsync moves into one of two device
-// buffers ("turns"), laid out as a small index of the batch's cells:
+// one packed image that hipMemcpyAsync moves into one of two device buffers
+// ("turns"), laid out as a small index of the batch's cells, with the
+// sections the brute force needs first so that a batch none of whose queries
+// traverses crosses PCIe as a prefix of its image:
 //   vec    rows x rowbytes (the batch's cells in plan order, cell-major rows)
-//   graph  rows x R   cell-local neighbour ids
-//   attrs  rows x a   fp32
 //   gidx   rows       point id of each row
+//   offset B + 1      first row of each batch cell
+//   bcell  B          cell id of each batch cell
+//   sub-cells (when the MFMA brute force applies: u8 vectors, D a multiple
+//   of 64 up to 256): sbase B + 1, scell / ssize NS, stile NS + 1,
+//   sbox NS * 2a, abase B * a, tmeta tiles * 16 (1 + AW), batch-local rows
+//   and cells; the int8 tiles are built on the device from the rows
+//                                      <- end of the MFMA brute-force prefix
+//   attrs  rows x a   fp32             <- end of the gather brute-force prefix
+//   graph  rows x R   cell-local neighbour ids
 //   lrow   rows       cell-local id of each row
 //   cross  B x rows x E: edge e of row r into the batch's i-th cell at
 //          (i * rows + r) * E + e (the reference's per-pair "T" slices,
 //          big_dataset_adapterV3.cuh:3539-3541)
-//   offset B + 1      first row of each batch cell
-//   bcell  B          cell id of each batch cell
 // Every section starts on a 256-byte boundary.
 struct StreamBatch {
-    uint32_t B = 0, rows = 0;
+    uint32_t B = 0, rows = 0, NS = 0, ntile = 0;
     size_t o_vec = 0, o_graph = 0, o_attrs = 0, o_gidx = 0, o_lrow = 0, o_cross = 0, o_offset = 0, o_bcell = 0;
+    size_t o_sbase = 0, o_scell = 0, o_ssize = 0, o_stile = 0, o_sbox = 0, o_abase = 0, o_tmeta = 0;
     size_t bytes = 0;      // image size
+    size_t bytes_mfma = 0;  // prefix the MFMA brute force reads
+    size_t bytes_bf = 0;    // prefix the gather brute force reads
     size_t host_off = 0;   // image start in the pinned arena
 };
 
@@ -138,6 +148,13 @@ struct StreamIndex {
     size_t max_bytes = 0;
     uint64_t budget = 0;
     uint32_t Bmax = 0, min_cell = 0;
+    // MFMA brute force: int8 tiles of the batch being searched
+    bool i8 = false;
+    uint32_t AW = 0, NSmax = 0, tmax = 0;
+    DevBuf<int8_t> vt;
+    DevBuf<int32_t> tnorm;
+    // the plan on the device (cells batch after batch, first of each batch)
+    DevBuf<uint32_t> plan_cells, plan_off;
     hipStream_t copy = nullptr;
     hipEvent_t ready[2] = {nullptr, nullptr}, freed[2] = {nullptr, nullptr};
     ~StreamIndex() {
@@ -195,7 +212,7 @@ struct gf_index {
                hist.bytes() + tile_cell.bytes() + tile_row0.bytes() + tile_n.bytes() + centres.bytes() +
                sbase.bytes() + scell.bytes() + ssize.bytes() + stile.bytes() + tmeta.bytes() + sbox.bytes() +
                abase.bytes() + vt.bytes() + tnorm.bytes() +
-               (sx ? sx->turn[0].bytes() + sx->turn[1].bytes() : 0);
+               (sx ? sx->turn[0].bytes() + sx->turn[1].bytes() + sx->vt.bytes() + sx->tnorm.bytes() : 0);
     }
 };
 
@@ -220,8 +237,14 @@ struct gf_batch {
     // arithmetic-grid stage A, else derived from the cell lists on use.
     DevBuf<uint8_t> flags;
     bool flags_ready = false;
+    // True after gf_mark_cells: every query's list holds every non-empty cell
+    // its range reaches and little is 0 or the count, so the MFMA brute force
+    // may pair a query with every sub-cell its range reaches; otherwise bfmask
+    // (Q*P, bit 2 = a cell the query's brute force scans) restricts it.
+    bool bf_all = false;
+    DevBuf<uint8_t> bfmask;
     // Streamed search: per-batch cell lists and results.
-    DevBuf<uint32_t> slist, scount, slittle, s_ids, s_ctr;
+    DevBuf<uint32_t> slist, scount, slittle, s_ids, s_ctr, note, need;
     DevBuf<float> s_dist;
 };
 
@@ -231,6 +254,16 @@ inline void set_device(const gf_index* ix) { GF_HIP(hipSetDevice(ix->device)); }
 }  // namespace gf
 
 namespace gf {
+// Sub-cells of every cell (host arrays; see build_subcells in gf_host.cpp):
+// false when the attributes do not allow them (a > 4, non-integer values, or
+// a spread of 65534 or more inside a cell).
+struct SubHost {
+    uint32_t AW = 0, NS = 0, ntile = 0;
+    std::vector<uint32_t> sbase, scell, ssize, stile, tmeta;
+    std::vector<int32_t> sbox, abase;
+};
+bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, const std::vector<uint32_t>& size,
+                      const std::vector<uint32_t>& offset_h, uint32_t a, uint32_t P, SubHost& out);
 // Checks shared by resident and streamed indexes, and the idx mapper
 // (tools.cuh:862-915): size[c] points per cell, ix.offset_h, gidx (row ->
 // point id), lrow (row -> cell-local id).  Every id the kernels dereference

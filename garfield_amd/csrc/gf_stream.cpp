@@ -73,6 +73,12 @@ void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_s
 
     std::unique_ptr<StreamIndex> sx(new StreamIndex());
     sx->budget = plan->device_budget;
+    // Sub-cells for the MFMA brute force (u8 vectors, D a multiple of 64 up to 256).
+    SubHost sh;
+    sx->i8 = ix.vdtype == GF_VEC_U8 && D % 64 == 0 && D <= 256 &&
+             compute_subcells(h, gidx, size, ix.offset_h, a, P, sh);
+    sx->AW = sh.AW;
+    const uint32_t MW = 16 * (1 + sh.AW);
     size_t total = 0;
     for (const auto& cl : plan_cells) {
         StreamBatch sb;
@@ -80,24 +86,47 @@ void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_s
         uint64_t rows = 0;
         for (uint32_t c : cl) rows += size[c];
         sb.rows = uint32_t(rows);
+        if (sx->i8)
+            for (uint32_t c : cl) {
+                sb.NS += sh.sbase[c + 1] - sh.sbase[c];
+                sb.ntile += sh.stile[sh.sbase[c + 1]] - sh.stile[sh.sbase[c]];
+            }
         sb.o_vec = 0;
-        sb.o_graph = align_up(sb.o_vec + rows * ix.rowbytes);
-        sb.o_attrs = align_up(sb.o_graph + rows * R * 4);
-        sb.o_gidx = align_up(sb.o_attrs + rows * a * 4);
-        sb.o_lrow = align_up(sb.o_gidx + rows * 4);
-        sb.o_cross = align_up(sb.o_lrow + rows * 4);
-        sb.o_offset = align_up(sb.o_cross + size_t(sb.B) * rows * E * 4);
+        sb.o_gidx = align_up(sb.o_vec + rows * ix.rowbytes);
+        sb.o_offset = align_up(sb.o_gidx + rows * 4);
         sb.o_bcell = align_up(sb.o_offset + (size_t(sb.B) + 1) * 4);
-        sb.bytes = align_up(sb.o_bcell + size_t(sb.B) * 4);
+        size_t end = sb.o_bcell + size_t(sb.B) * 4;
+        if (sx->i8) {
+            sb.o_sbase = align_up(end);
+            sb.o_scell = align_up(sb.o_sbase + (size_t(sb.B) + 1) * 4);
+            sb.o_ssize = align_up(sb.o_scell + size_t(sb.NS) * 4);
+            sb.o_stile = align_up(sb.o_ssize + size_t(sb.NS) * 4);
+            sb.o_sbox = align_up(sb.o_stile + (size_t(sb.NS) + 1) * 4);
+            sb.o_abase = align_up(sb.o_sbox + size_t(sb.NS) * 2 * a * 4);
+            sb.o_tmeta = align_up(sb.o_abase + size_t(sb.B) * a * 4);
+            end = sb.o_tmeta + size_t(sb.ntile) * MW * 4;
+        }
+        sb.bytes_mfma = align_up(end);
+        sb.o_attrs = sb.bytes_mfma;
+        sb.bytes_bf = align_up(sb.o_attrs + rows * a * 4);
+        sb.o_graph = sb.bytes_bf;
+        sb.o_lrow = align_up(sb.o_graph + rows * R * 4);
+        sb.o_cross = align_up(sb.o_lrow + rows * 4);
+        sb.bytes = align_up(sb.o_cross + size_t(sb.B) * rows * E * 4);
         sb.host_off = total;
         total += sb.bytes;
         sx->max_bytes = std::max(sx->max_bytes, sb.bytes);
         sx->Bmax = std::max(sx->Bmax, sb.B);
+        sx->NSmax = std::max(sx->NSmax, sb.NS);
+        sx->tmax = std::max(sx->tmax, sb.ntile);
         sx->batches.push_back(sb);
     }
-    GF_REQUIRE(sx->budget == 0 || 2 * sx->max_bytes <= sx->budget, GF_E_UNSUPPORTED,
-               "the largest batch needs 2 x " + std::to_string(sx->max_bytes) +
-                   " device bytes, over the device budget of " + std::to_string(sx->budget));
+    const size_t tile_bytes = size_t(D / 64) * 1024 + 32 * 4;
+    const uint64_t need = 2 * uint64_t(sx->max_bytes) + (sx->i8 ? uint64_t(sx->tmax) * tile_bytes : 0);
+    GF_REQUIRE(sx->budget == 0 || need <= sx->budget, GF_E_UNSUPPORTED,
+               "the largest batch needs " + std::to_string(need) + " device bytes (two images" +
+                   (sx->i8 ? std::string(" and its int8 tiles") : std::string()) + "), over the device budget of " +
+                   std::to_string(sx->budget));
     sx->min_cell = 0;
     for (uint32_t c = 0; c < P; ++c)
         if (size[c] && (sx->min_cell == 0 || size[c] < sx->min_cell)) sx->min_cell = size[c];
@@ -139,6 +168,36 @@ void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_s
         }
         std::memcpy(img + sb.o_offset, boff.data(), boff.size() * 4);
         std::memcpy(img + sb.o_bcell, cl.data(), cl.size() * 4);
+        if (sx->i8) {
+            uint32_t* g_sbase = reinterpret_cast<uint32_t*>(img + sb.o_sbase);
+            uint32_t* g_scell = reinterpret_cast<uint32_t*>(img + sb.o_scell);
+            uint32_t* g_ssize = reinterpret_cast<uint32_t*>(img + sb.o_ssize);
+            uint32_t* g_stile = reinterpret_cast<uint32_t*>(img + sb.o_stile);
+            int32_t* g_sbox = reinterpret_cast<int32_t*>(img + sb.o_sbox);
+            int32_t* g_abase = reinterpret_cast<int32_t*>(img + sb.o_abase);
+            uint32_t* g_tmeta = reinterpret_cast<uint32_t*>(img + sb.o_tmeta);
+            uint32_t ns = 0, nt = 0;
+            for (uint32_t i = 0; i < sb.B; ++i) {
+                const uint32_t c = cl[i];
+                g_sbase[i] = ns;
+                for (uint32_t d = 0; d < a; ++d) g_abase[size_t(i) * a + d] = sh.abase[size_t(c) * a + d];
+                for (uint32_t s0 = sh.sbase[c]; s0 < sh.sbase[c + 1]; ++s0, ++ns) {
+                    g_scell[ns] = i;
+                    g_ssize[ns] = sh.ssize[s0];
+                    g_stile[ns] = nt;
+                    for (uint32_t k = 0; k < 2 * a; ++k) g_sbox[size_t(ns) * 2 * a + k] = sh.sbox[size_t(s0) * 2 * a + k];
+                    for (uint32_t t = sh.stile[s0]; t < sh.stile[s0 + 1]; ++t, ++nt) {
+                        const uint32_t* src = &sh.tmeta[size_t(t) * MW];
+                        uint32_t* dst = g_tmeta + size_t(nt) * MW;
+                        std::memcpy(dst, src, MW * 4);
+                        for (uint32_t j = 0; j < 16; ++j)   // rows become batch rows
+                            if (src[j] != 0xFFFFFFFFu) dst[j] = src[j] - ix.offset_h[c] + boff[i];
+                    }
+                }
+            }
+            g_sbase[sb.B] = ns;
+            g_stile[ns] = nt;
+        }
     }
 
     GF_HIP(hipStreamCreateWithFlags(&ix.stream, hipStreamNonBlocking));
@@ -147,6 +206,21 @@ void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_s
         GF_HIP(hipEventCreateWithFlags(&sx->ready[t], hipEventDisableTiming));
         GF_HIP(hipEventCreateWithFlags(&sx->freed[t], hipEventDisableTiming));
         sx->turn[t].alloc(sx->max_bytes);
+    }
+    {
+        std::vector<uint32_t> pc, po(1, 0);
+        for (const auto& cl : plan_cells) {
+            pc.insert(pc.end(), cl.begin(), cl.end());
+            po.push_back(uint32_t(pc.size()));
+        }
+        if (pc.empty()) pc.push_back(0);
+        sx->plan_cells.upload(pc);
+        sx->plan_off.upload(po);
+    }
+    if (sx->i8) {
+        sx->vt.alloc(size_t(std::max(sx->tmax, 1u)) * (D / 64) * 1024);
+        sx->tnorm.alloc(size_t(std::max(sx->tmax, 1u)) * 32);
+        ix.i8 = true;   // gf_batch_create keeps int8 queries
     }
     GF_HIP(hipDeviceGetAttribute(&ix.ncu, hipDeviceAttributeMultiprocessorCount, ix.device));
     ix.offset.upload(ix.offset_h);
@@ -209,7 +283,8 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     uint32_t* tot = b.tot.p;
 
     const size_t nb = S.batches.size();
-    std::vector<hipEvent_t> ce(2 * nb, nullptr);
+    // per batch: copy start/end (copy stream), traversal start, brute-force start/end (compute stream)
+    std::vector<hipEvent_t> ce(5 * nb, nullptr);
     hipEvent_t t0 = nullptr, t1 = nullptr;
     struct Ev {
         std::vector<hipEvent_t>& v;
@@ -225,23 +300,103 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     GF_HIP(hipEventCreate(&t0));
     GF_HIP(hipEventCreate(&t1));
 
-    GF_HIP(hipEventRecord(t0, st));
-    // The copy stream starts after everything queued so far on the compute
-    // stream (flags, entries): a turn buffer is never in use at this point.
-    GF_HIP(hipEventRecord(S.freed[0], st));
-    GF_HIP(hipEventRecord(S.freed[1], st));
-    double bytes = 0.0;
-    for (size_t bi = 0; bi < nb; ++bi) {
-        const StreamBatch& sb = S.batches[bi];
-        const int t = int(bi & 1);
-        char* dev = S.turn[t].p;
-        GF_HIP(hipStreamWaitEvent(S.copy, S.freed[t], 0));
-        GF_HIP(hipEventRecord(ce[2 * bi], S.copy));
-        GF_HIP(hipMemcpyAsync(dev, S.host.p + sb.host_off, sb.bytes, hipMemcpyHostToDevice, S.copy));
-        GF_HIP(hipEventRecord(ce[2 * bi + 1], S.copy));
-        GF_HIP(hipEventRecord(S.ready[t], S.copy));
-        bytes += double(sb.bytes);
+    // MFMA brute force on the streamed batches: int8 queries, K within the
+    // route's limit; schedule buffers sized like the resident path's.
+    const bool gemm = S.i8 && b.i8 && K <= kBfKMax;
+    if (gemm) {
+        const uint32_t NS = std::max(S.NSmax, 1u);
+        if (b.bcnt.n < NS) { b.bcnt.alloc(NS); b.bstart.alloc(NS); b.icnt.alloc(NS); b.ioff.alloc(NS); }
+        if (b.nsub.n < Q) { b.nsub.alloc(Q); b.part_off.alloc(Q); b.pcnt.alloc(Q); b.gbound.alloc(Q); }
+        if (!b.bq.n) b.bq.alloc(size_t(Q) * 64);
+        if (b.part.n < b.bq.n * K) b.part.alloc(b.bq.n * K);
+        if (b.items.n < b.bq.n / kBfQB + NS + 1) b.items.alloc(b.bq.n / kBfQB + NS + 1);
+        if (b.bfmask.n < size_t(Q) * Bm) b.bfmask.alloc(size_t(Q) * Bm);
+        if (b.note.n < 2 * std::max<size_t>(nb, 1)) b.note.alloc(2 * std::max<size_t>(nb, 1));
+    }
+    std::vector<hipEvent_t> ge(2 * nb, nullptr);   // around each batch's MFMA kernel
+    struct EvG {
+        std::vector<hipEvent_t>& v;
+        ~EvG() { for (auto e : v) if (e) (void)hipEventDestroy(e); }
+    } gguard{ge};
+    if (gemm) for (auto& e : ge) GF_HIP(hipEventCreate(&e));
 
+    // Filtered brute force of one batch on int8 MFMA: the resident path's
+    // item schedule (k_bfsched / k_bfitems / k_bf_i8 / k_bf_final) on the
+    // batch's sub-cells, restricted by bfmask to the cells the batch lists.
+    auto mfma_bruteforce = [&](size_t bi, const StreamBatch& sb, char* dev) {
+        SubArgs sa{};
+        sa.sbase = reinterpret_cast<const uint32_t*>(dev + sb.o_sbase);
+        sa.scell = reinterpret_cast<const uint32_t*>(dev + sb.o_scell);
+        sa.ssize = reinterpret_cast<const uint32_t*>(dev + sb.o_ssize);
+        sa.stile = reinterpret_cast<const uint32_t*>(dev + sb.o_stile);
+        sa.sbox = reinterpret_cast<const int32_t*>(dev + sb.o_sbox);
+        sa.tmeta = reinterpret_cast<const uint32_t*>(dev + sb.o_tmeta);
+        sa.abase = reinterpret_cast<const int32_t*>(dev + sb.o_abase);
+        sa.a = ix.a; sa.AW = S.AW; sa.P = sb.B; sa.NS = sb.NS;
+        GF_HIP(launch_tile_i8(dev + sb.o_vec, true, ix.D, sa.tmeta, S.AW, sb.ntile, S.vt.p, S.tnorm.p, st));
+        // exact passing counts of the batch (the PASS counter)
+        GF_HIP(hipMemsetAsync(b.selcount.p, 0, size_t(Q) * sizeof(uint32_t), st));
+        SubSelArgs sl{};
+        sl.sa = sa; sl.Q = Q; sl.lo = b.lo.p; sl.hi = b.hi.p; sl.selcount = b.selcount.p;
+        if (sb.NS) GF_HIP(launch_subsel(sl, st));
+        GF_HIP(launch_cell_flags(Q, sb.B, b.slist.p, b.scount.p, b.slittle.p, b.bfmask.p, st));
+        BfSchedArgs sc{};
+        sc.sa = sa;
+        sc.Q = Q; sc.postfilter = 0xFFFFFFFFu; sc.counts = b.scount.p; sc.little = b.slittle.p;
+        sc.lo = b.lo.p; sc.hi = b.hi.p; sc.nsub = b.nsub.p; sc.bcnt = b.bcnt.p; sc.bstart = b.bstart.p;
+        sc.bq = b.bq.p; sc.ok = tot + 3; sc.nbf = tot + 9; sc.bfm = b.bfmask.p; sc.bP = sb.B;
+        GF_HIP(hipMemsetAsync(b.nsub.p, 0, size_t(Q) * sizeof(uint32_t), st));
+        GF_HIP(hipMemsetAsync(b.pcnt.p, 0, size_t(Q) * sizeof(uint32_t), st));
+        GF_HIP(hipMemsetAsync(b.gbound.p, 0xFF, size_t(Q) * sizeof(uint32_t), st));
+        if (sb.NS) {
+            GF_HIP(launch_bfsched(sc, false, st));
+            GF_HIP(launch_scan_small(b.bcnt.p, sb.NS, b.bstart.p, st));
+        }
+        GF_HIP(launch_scan_small(b.nsub.p, Q, b.part_off.p, st));
+        GF_HIP(launch_total(b.nsub.p, b.part_off.p, Q, uint32_t(std::min<size_t>(b.bq.n, UINT32_MAX)), K, b.part.n,
+                            tot + 2, st));
+        GF_HIP(hipMemsetAsync(tot + 4, 0, sizeof(uint32_t), st));
+        if (sb.NS) {
+            GF_HIP(launch_bfsched(sc, true, st));
+            GF_HIP(launch_bfitems(b.bcnt.p, b.bstart.p, sb.NS, b.icnt.p, b.ioff.p, b.items.p, tot + 4, tot + 3, false,
+                                  st));
+            GF_HIP(launch_scan_small(b.icnt.p, sb.NS, b.ioff.p, st));
+            GF_HIP(launch_bfitems(b.bcnt.p, b.bstart.p, sb.NS, b.icnt.p, b.ioff.p, b.items.p, tot + 4, tot + 3, true,
+                                  st));
+        }
+        BfGemmArgs ga{};
+        ga.sa = sa;
+        ga.vt = S.vt.p; ga.tnorm = S.tnorm.p; ga.q8 = b.q8.p; ga.nq = b.nq.p; ga.lo = b.lo.p; ga.hi = b.hi.p;
+        ga.items = b.items.p; ga.nitems = tot + 4; ga.bq = b.bq.p; ga.pcnt = b.pcnt.p; ga.part_off = b.part_off.p;
+        ga.part = b.part.p; ga.gbound = b.gbound.p; ga.ok = tot + 3; ga.K = K; ga.D = ix.D;
+        GF_HIP(hipEventRecord(ge[2 * bi], st));
+        GF_HIP(launch_bf_i8(ga, uint32_t(std::max(ix.ncu, 1)) * 3u, st));
+        GF_HIP(hipEventRecord(ge[2 * bi + 1], st));
+        BfFinalArgs fa{};
+        fa.bfq = b.sched.p; fa.srange = tot + 14; fa.part_off = b.part_off.p; fa.pcnt = b.pcnt.p; fa.ok = tot + 3;
+        fa.part = b.part.p; fa.counts = b.scount.p; fa.cells = b.slist.p;
+        fa.offset = reinterpret_cast<const uint32_t*>(dev + sb.o_offset); fa.selcount = b.selcount.p;
+        fa.gidx = reinterpret_cast<const uint32_t*>(dev + sb.o_gidx); fa.out_ids = b.s_ids.p;
+        fa.out_dist = b.s_dist.p; fa.counters = b.s_ctr.p; fa.K = K; fa.P = sb.B;
+        GF_HIP(launch_bf_final(fa, Q, st));
+        GF_HIP(launch_note_bf(tot, b.note.p + 2 * bi, st));
+    };
+
+    double bytes = 0.0;
+    auto enqueue_copy = [&](size_t bi, int t, size_t nbytes) {
+        const StreamBatch& sb = S.batches[bi];
+        GF_HIP(hipStreamWaitEvent(S.copy, S.freed[t], 0));
+        GF_HIP(hipEventRecord(ce[5 * bi], S.copy));
+        GF_HIP(hipMemcpyAsync(S.turn[t].p, S.host.p + sb.host_off, nbytes, hipMemcpyHostToDevice, S.copy));
+        GF_HIP(hipEventRecord(ce[5 * bi + 1], S.copy));
+        GF_HIP(hipEventRecord(S.ready[t], S.copy));
+        bytes += double(nbytes);
+    };
+    // One batch on the compute stream: its cell lists and routes, the
+    // traversal (unless skipped), the brute force, the merge.
+    auto enqueue_compute = [&](size_t bi, int t, bool traverse, bool first) {
+        const StreamBatch& sb = S.batches[bi];
+        char* dev = S.turn[t].p;
         GF_HIP(hipStreamWaitEvent(st, S.ready[t], 0));
         const uint32_t* bcell = reinterpret_cast<const uint32_t*>(dev + sb.o_bcell);
         GF_HIP(launch_stream_lists(Q, P, sb.B, bcell, b.flags.p, b.slist.p, b.scount.p, b.slittle.p, st));
@@ -263,17 +418,76 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         at.offset = reinterpret_cast<const uint32_t*>(dev + sb.o_offset);
         at.P = sb.B;
         at.srange = tot + 12;
-        GF_HIP(launch_traverse(ix.rs, at, lds, Q, st));
-        TravArgs ab = at;
-        ab.srange = tot + 14;
-        GF_HIP(launch_bruteforce(ix.rs, ab, Q, st));
+        GF_HIP(hipEventRecord(ce[5 * bi + 2], st));
+        if (traverse) GF_HIP(launch_traverse(ix.rs, at, lds, Q, st));
+        GF_HIP(hipEventRecord(ce[5 * bi + 3], st));
+        if (gemm) {
+            mfma_bruteforce(bi, sb, dev);
+        } else {
+            TravArgs ab = at;
+            ab.srange = tot + 14;
+            GF_HIP(launch_bruteforce(ix.rs, ab, Q, st));
+        }
+        GF_HIP(hipEventRecord(ce[5 * bi + 4], st));
         GF_HIP(launch_merge_stream(Q, K, b.out_ids.p, b.out_dist.p, b.s_ids.p, b.s_dist.p, b.counters.p, b.s_ctr.p,
-                                   bi == 0, st));
+                                   first, st));
         GF_HIP(hipEventRecord(S.freed[t], st));
+    };
+
+    GF_HIP(hipEventRecord(t0, st));
+    // Which batches this query batch needs, and which prefix of each image:
+    // skipped batches cost nothing; a batch no query traverses moves only
+    // its brute-force sections.
+    if (b.need.n < std::max<size_t>(nb, 1)) b.need.alloc(std::max<size_t>(nb, 1));
+    GF_HIP(launch_batch_need(Q, P, uint32_t(nb), S.plan_cells.p, S.plan_off.p, b.flags.p, b.need.p, st));
+    std::vector<uint32_t> need(nb, 0);
+    if (nb) {
+        GF_HIP(hipMemcpyAsync(need.data(), b.need.p, nb * 4, hipMemcpyDeviceToHost, st));
+        GF_HIP(hipStreamSynchronize(st));
     }
-    if (nb == 0) {
+    if (gemm) GF_HIP(hipMemsetAsync(b.note.p, 0xFF, 2 * nb * sizeof(uint32_t), st));
+    // The copy stream starts after everything queued so far on the compute
+    // stream (flags, entries): a turn buffer is never in use at this point.
+    GF_HIP(hipEventRecord(S.freed[0], st));
+    GF_HIP(hipEventRecord(S.freed[1], st));
+    std::vector<size_t> ran;
+    for (size_t bi = 0; bi < nb; ++bi) {
+        if (!need[bi]) continue;
+        const StreamBatch& sb = S.batches[bi];
+        const bool trav = (need[bi] & 2u) != 0;
+        const int t = int(ran.size() & 1);
+        enqueue_copy(bi, t, trav ? sb.bytes : (gemm ? sb.bytes_mfma : sb.bytes_bf));
+        enqueue_compute(bi, t, trav, ran.empty());
+        ran.push_back(bi);
+    }
+    if (ran.empty()) {
         GF_HIP(launch_fill_results(b.out_ids.p, b.out_dist.p, Q * K, st));
         GF_HIP(hipMemsetAsync(b.counters.p, 0, size_t(Q) * GF_NCOUNTERS * sizeof(uint32_t), st));
+    }
+    if (gemm && !ran.empty()) {
+        // A batch whose brute-force pairs outgrew the buffers skipped its
+        // brute force (its routed queries merged no result): grow the
+        // buffers and run the brute force of those batches again.
+        GF_HIP(hipStreamSynchronize(st));
+        std::vector<uint32_t> note(2 * nb);
+        GF_HIP(hipMemcpy(note.data(), b.note.p, note.size() * 4, hipMemcpyDeviceToHost));
+        size_t need = 0;
+        for (size_t bi = 0; bi < nb; ++bi)
+            if (!note[2 * bi]) need = std::max<size_t>(need, note[2 * bi + 1]);
+        if (need) {
+            const size_t cap = need + need / 4 + 1024;
+            const uint32_t NS = std::max(S.NSmax, 1u);
+            b.bq.alloc(cap); b.part.alloc(cap * K); b.items.alloc(cap / kBfQB + NS + 1);
+            for (size_t bi = 0; bi < nb; ++bi)
+                if (!note[2 * bi]) {
+                    enqueue_copy(bi, 0, S.batches[bi].bytes_mfma);
+                    enqueue_compute(bi, 0, false, false);
+                }
+            GF_HIP(hipStreamSynchronize(st));
+            GF_HIP(hipMemcpy(note.data(), b.note.p, note.size() * 4, hipMemcpyDeviceToHost));
+            for (size_t bi = 0; bi < nb; ++bi)
+                GF_REQUIRE(note[2 * bi], GF_E_STATE, "brute-force schedule does not fit after growing");
+        }
     }
     GF_HIP(hipEventRecord(t1, st));
     GF_HIP(hipEventSynchronize(t1));
@@ -284,17 +498,32 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     if (stats) {
         float ms = 0.0f;
         GF_HIP(hipEventElapsedTime(&ms, t0, t1));
-        double h2d = 0.0;
-        for (size_t bi = 0; bi < nb; ++bi) {
-            float c = 0.0f;
-            GF_HIP(hipEventElapsedTime(&c, ce[2 * bi], ce[2 * bi + 1]));
+        double h2d = 0.0, tr = 0.0, bf = 0.0;
+        for (size_t bi : ran) {
+            float c = 0.0f, t = 0.0f, f = 0.0f;
+            GF_HIP(hipEventElapsedTime(&c, ce[5 * bi], ce[5 * bi + 1]));
+            GF_HIP(hipEventElapsedTime(&t, ce[5 * bi + 2], ce[5 * bi + 3]));
+            GF_HIP(hipEventElapsedTime(&f, ce[5 * bi + 3], ce[5 * bi + 4]));
             h2d += c;
+            tr += t;
+            bf += f;
         }
         std::vector<uint32_t> ctr(size_t(Q) * GF_NCOUNTERS);
         GF_HIP(hipMemcpy(ctr.data(), b.counters.p, ctr.size() * 4, hipMemcpyDeviceToHost));
         std::memset(stats, 0, sizeof(*stats));
+        double g = 0.0;
+        if (gemm)
+            for (size_t bi : ran) {
+                float x = 0.0f;
+                GF_HIP(hipEventElapsedTime(&x, ge[2 * bi], ge[2 * bi + 1]));
+                g += x;
+            }
         stats->ms_total = ms;
-        stats->n_batches = uint32_t(nb);
+        stats->ms_traverse = tr;
+        stats->ms_bruteforce = bf;
+        stats->ms_bf_kernel = g;
+        stats->bf_mfma = gemm ? 1u : 0u;
+        stats->n_batches = uint32_t(ran.size());
         stats->bytes_h2d = bytes;
         stats->ms_h2d = h2d;
         uint64_t sum[GF_NCOUNTERS] = {0};
@@ -305,9 +534,11 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
             stats->q_traverse += (c[7] & 0xFFFFu) ? 1 : 0;
             stats->q_bruteforce += (c[7] >> 16) ? 1 : 0;
             stats->q_empty += c[7] ? 0 : 1;
-            // brute-force distances equal the passing points; the rest are traversal's
-            t_dist += double(c[1]) - double(c[6]);
-            b_dist += double(c[6]);
+            // the brute force's distances are its passing points (gather) or
+            // its scanned points (MFMA); the rest are traversal's
+            const double bd = gemm ? double(c[5]) : double(c[6]);
+            t_dist += double(c[1]) - bd;
+            b_dist += bd;
         }
         stats->n_expand = sum[0]; stats->n_dist = sum[1]; stats->n_attr = sum[2]; stats->n_cross = sum[3];
         stats->n_lrow = sum[4]; stats->n_scan = sum[5]; stats->n_pass = sum[6];

@@ -276,6 +276,31 @@ def config_headline(N=1_000_000, Q=10_000, R=32, C=1000, seed=11):
     return dict(vectors=vec, attrs=att, grid=[4, 4], R=R, E=2, C=C, queries=qv, lo=lo, hi=hi, sel=sel)
 
 
+def config_stream(N=1_000_000, Q=10_000, R=32, seed=21):
+    """Config C5 scaled to one GPU box's build time: N x 128 integer vectors
+    (stored as u8), 2 uint32 attributes uniform in [0,10000) on a 16x16
+    arithmetic grid (width 625), R=32, E=2, selectivity log-U[0.5%, 20%]."""
+    vec = uniform_int_vectors(N, 128, seed)
+    att = uniform_attrs(N, 2, seed + 1)
+    qv = uniform_int_vectors(Q, 128, seed + 2)
+    sel = log_uniform(Q, 0.005, 0.2, seed + 3)
+    lo, hi = ranges_for_selectivity(Q, 2, sel, seed + 4)
+    width = float((DOMAIN + 15) // 16)
+    return dict(vectors=vec, attrs=att, grid=[16, 16], R=R, E=2, C=0, queries=qv, lo=lo, hi=hi, sel=sel,
+                attr_min=np.zeros(2, np.float32), attr_width=np.full(2, width, np.float32))
+
+
+def block_plan(grid, block):
+    """Static plan of compact blocks of block x block cells on a 2-d grid (the
+    spatially grouped batches of bigdataset_experiment.cu:746-756)."""
+    g0, g1 = int(grid[0]), int(grid[1])
+    plan = []
+    for i0 in range(0, g0, block):
+        for j0 in range(0, g1, block):
+            plan.append([i * g1 + j for i in range(i0, min(g0, i0 + block)) for j in range(j0, min(g1, j0 + block))])
+    return plan
+
+
 def ground_truth_torch(vectors, attrs, queries, lo, hi, K, device="cuda", chunk=256):
     """Exact filtered kNN (naive_brute_force_with_filter, gpu_graph.cu:10782-10812)
     in fp64 on `device`; returns ids (missing = 0x7FFFFFFF) and squared distances."""

@@ -162,8 +162,8 @@ typedef struct {
 
 #define GF_NCOUNTERS 8  /* per-query counters, same order as the oracle's */
 typedef struct {
-    double ms_traverse;      /* device time of the traversal kernel */
-    double ms_bruteforce;    /* device time of the brute-force kernel */
+    double ms_traverse;      /* device time of the traversal kernel (streamed: summed over batches) */
+    double ms_bruteforce;    /* device time of the brute-force kernel (streamed: summed over batches) */
     double ms_total;         /* device time of the whole search stage */
     uint32_t q_traverse, q_bruteforce, q_empty;
     uint64_t n_expand, n_dist, n_attr, n_cross, n_lrow, n_scan, n_pass;
@@ -173,8 +173,8 @@ typedef struct {
     uint32_t bf_mfma;        /* 1 if the brute force ran as the int8 MFMA query-batch kernel */
     double ms_bf_kernel;     /* device time of the MFMA brute-force kernel alone (no schedule, no merge) */
     /* streamed index only */
-    uint32_t n_batches;      /* batches of the plan */
-    double bytes_h2d;        /* bytes copied host -> device */
+    uint32_t n_batches;      /* batches searched (a batch none of whose cells a query selects is skipped) */
+    double bytes_h2d;        /* bytes copied host -> device (a batch no query traverses: its brute-force sections only) */
     double ms_h2d;           /* sum of the copies' device times */
 } gf_search_stats;
 

@@ -51,8 +51,10 @@ def _args(ix):
     return (ix["vectors"], ix["attrs"], ix["grid"], l_q, r_q, ix["global_pid"], ix["cell_graphs"], ix["cross"])
 
 
-def _oracle_stream(ix, plan, cfg, flags, ent, L, K=10, rl=10):
-    """Per-batch oracle searches merged into a running top K (see module doc)."""
+def _oracle_stream(ix, plan, cfg, flags, ent, L, K=10, rl=10, mfma=False):
+    """Per-batch oracle searches merged into a running top K (see module doc).
+    mfma: the brute force ran on MFMA, which evaluates every scanned point
+    (its DIST counter is the SCAN counter)."""
     from oracle import oracle as orc
     P, E, N = ix["P"], ix["E"], ix["vectors"].shape[0]
     sizes = synth.cell_sizes(ix)
@@ -77,6 +79,8 @@ def _oracle_stream(ix, plan, cfg, flags, ent, L, K=10, rl=10):
             lit[q] = len(mine) if mine and all(flags[q, batch[i]] & 2 for i in mine) else 0
         ids, d, c = O.search(cfg["queries"], cfg["lo"], cfg["hi"], cells, cnt, lit, ent, L, K=K, rl=rl)
         c = c.copy()
+        if mfma:
+            c[c[:, 7] == 2, 1] = c[c[:, 7] == 2, 5]
         c[:, 7] = np.where(c[:, 7] == 1, 1, np.where(c[:, 7] == 2, 1 << 16, 0))
         if run_ids is None:
             run_ids, run_d, run_c = ids.copy(), d.copy(), c.astype(np.int64)
@@ -204,31 +208,33 @@ def test_stream_one_batch_equals_resident(world_stream):
     res.close()
 
 
-@pytest.mark.parametrize("L,thr,per", [(16, 0.02, 4), (64, 0.1, 3), (100, 0.0, 16)])
-def test_stream_batches_match_oracle(world_stream, L, thr, per):
+@pytest.mark.parametrize("L,thr,per,K", [(16, 0.02, 4, 10), (64, 0.1, 3, 10), (100, 0.0, 16, 10),
+                                         (32, 0.1, 4, 20), (48, 1.0, 5, 10), (48, 1.0, 5, 20)])
+def test_stream_batches_match_oracle(world_stream, L, thr, per, K):
     from oracle import oracle as orc
     cfg, ix = world_stream
-    _print_case("stream-batches", L=L, thr=thr, per=per)
+    _print_case("stream-batches", L=L, thr=thr, per=per, K=K)
     P = ix["P"]
     plan = _shuffled_plan(P, per, seed=L)
     sx = gl.Index.create_streamed(*_args(ix), plan=plan)
     b = sx.batch(cfg["queries"], cfg["lo"], cfg["hi"])
     b.mark_cells_grid(AMIN, WIDTH, thr)
     flags = b.get_cell_flags()
-    ids, dists, st = b.search(L=L, K=10, rl=10)
+    ids, dists, st = b.search(L=L, K=K, rl=10)
     ctr = b.get_counters()
-    assert st.n_batches == len(plan) and st.bytes_h2d > 0
+    assert 0 < st.n_batches <= len(plan) and st.bytes_h2d > 0
+    assert st.bf_mfma == (K <= 16)
     sizes = synth.cell_sizes(ix)
     ent = orc.entry_draw(int(sizes[sizes > 0].min()), 10 * L, ix["R"])
-    oids, od, oc = _oracle_stream(ix, plan, cfg, flags, ent, L)
+    oids, od, oc = _oracle_stream(ix, plan, cfg, flags, ent, L, K=K, mfma=bool(st.bf_mfma))
     bad = np.nonzero(np.any(ids != oids, axis=1))[0]
     assert bad.size == 0, f"{bad.size} queries differ, first {bad[:5]}: {ids[bad[0]]} vs {oids[bad[0]]}"
     assert np.array_equal(dists.view(np.uint32), od.view(np.uint32))
     assert np.array_equal(ctr.astype(np.int64), oc)
     # a second search on the same batch (state reuse), smaller L
-    ids2, _, _ = b.search(L=max(8, L // 2), K=10, rl=10)
+    ids2, _, _ = b.search(L=max(8, L // 2), K=K, rl=10)
     ent2 = orc.entry_draw(int(sizes[sizes > 0].min()), 10 * max(8, L // 2), ix["R"])
-    oids2, _, _ = _oracle_stream(ix, plan, cfg, flags, ent2, max(8, L // 2))
+    oids2, _, _ = _oracle_stream(ix, plan, cfg, flags, ent2, max(8, L // 2), K=K)
     assert np.array_equal(ids2, oids2)
     b.close()
     sx.close()
@@ -261,3 +267,39 @@ def test_stream_under_device_budget(world_stream):
         assert np.array_equal(i0[q, single], i1[q, single]), q
     sx.close()
     res.close()
+
+
+def test_stream_bruteforce_overflow_rerun():
+    """One cell of 80000 points (81 sub-cells) and full-range queries: the
+    brute-force pairs outgrow the initial buffers (64 per query), the
+    streamed search grows them and runs the brute force again; results are
+    the exact filtered top K (resident path and CPU ground truth)."""
+    from oracle import oracle as orc
+    _print_case("stream-overflow")
+    rng = np.random.default_rng(77)
+    N, D, Q, R = 80000, 64, 64, 8
+    vec = rng.integers(0, 256, (N, D)).astype(np.float32)
+    att = rng.integers(0, 10000, (N, 2)).astype(np.float32)
+    graphs = rng.integers(0, N, (N, R)).astype(np.uint32)     # any graph: every query takes brute force
+    cross = rng.integers(0, N, (N, 2)).astype(np.uint32)
+    args = (vec, att, np.array([1, 1], np.uint32), np.array([0, 0], np.float32),
+            np.array([9999, 9999], np.float32), np.zeros(N, np.uint32), graphs, cross)
+    queries = rng.integers(0, 256, (Q, D)).astype(np.float32)
+    lo = np.zeros((Q, 2), np.float32)
+    hi = np.full((Q, 2), 9999.0, np.float32)
+    lo[::3, 0] = 5000.0                                       # some narrower ranges too
+    gt, gtd = orc.ground_truth(vec, att, queries, lo, hi, 10)
+    out = []
+    for make in (lambda: gl.Index.from_arrays(*args, vec_dtype=gl.VEC_U8),
+                 lambda: gl.Index.create_streamed(*args, plan=[[0]])):
+        dev = make()
+        b = dev.batch(queries, lo, hi)
+        b.set_cells(np.zeros((Q, 1), np.uint32), np.ones(Q, np.uint32), np.ones(Q, np.uint32))
+        ids, dists, st = b.search(L=16, K=10, rl=10)
+        assert st.bf_mfma == 1
+        out.append((ids, dists))
+        b.close()
+        dev.close()
+    for ids, dists in out:
+        assert np.array_equal(dists, gtd.astype(np.float32))
+    assert np.array_equal(out[0][0], out[1][0])
