@@ -763,6 +763,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             sc.little = b->little.p; sc.lo = b->lo.p; sc.hi = b->hi.p; sc.nsub = b->nsub.p; sc.bcnt = b->bcnt.p;
             sc.bstart = b->bstart.p; sc.bq = b->bq.p;
             sc.ok = tot + 3; sc.nbf = tot + 9;
+            sc.qlist = b->sched.p; sc.qrange = tot + 14;   // the brute-force queries of the schedule
             if (!b->bf_all) {
                 if (b->bfmask.n < size_t(Q) * ix->P) b->bfmask.alloc(size_t(Q) * ix->P);
                 GF_HIP(gf::launch_cell_flags(Q, ix->P, b->cells.p, b->counts.p, b->little.p, b->bfmask.p, st));
@@ -778,11 +779,11 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             GF_HIP(gf::launch_total(b->nsub.p, b->part_off.p, Q, uint32_t(std::min<size_t>(b->bq.n, UINT32_MAX)), K,
                                     b->part.n, tot + 2, st));
             GF_HIP(gf::launch_bfsched(sc, true, st));
-            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bstart.p, NS, b->icnt.p, b->ioff.p, b->items.p, tot + 4, tot + 3,
-                                      false, st));
+            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bstart.p, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p, b->items.p,
+                                      tot + 4, tot + 3, false, st));
             GF_HIP(gf::launch_scan_small(b->icnt.p, NS, b->ioff.p, st));
-            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bstart.p, NS, b->icnt.p, b->ioff.p, b->items.p, tot + 4, tot + 3,
-                                      true, st));
+            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bstart.p, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p, b->items.p,
+                                      tot + 4, tot + 3, true, st));
             gf::BfGemmArgs ga{};
             ga.sa = sub_args(*ix);
             ga.vt = ix->vt.p; ga.tnorm = ix->tnorm.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p;

@@ -94,6 +94,7 @@ constexpr uint32_t kBfKMax = 16;      // largest K of the MFMA route
 constexpr uint32_t kBfQB = 64;        // queries per work item
 struct BfItem {
     uint32_t sub, qbase, nq;           // sub-cell, first entry of its query list, queries
+    uint32_t tb, te;                   // tiles [tb, te) of the sub-cell
 };
 struct BfGemmArgs {
     SubArgs sa;
@@ -160,6 +161,13 @@ struct BfSchedArgs {
     // stride bP, bit 2 = the cell is one the query's brute force scans.
     const uint8_t* bfm;
     uint32_t bP;
+    // Optional (null: queries 0..Q-1): candidate queries qlist[qrange[0] ..
+    // qrange[1]) (device range), e.g. the schedule's brute-force queries.
+    const uint32_t* qlist;
+    const uint32_t* qrange;
+    // Items cover at most tch tiles of a sub-cell (0: the whole sub-cell);
+    // nsub counts a pair once per such chunk, each of which appends <= K keys.
+    uint32_t tch;
 };
 // Query schedule (gpu_graph.cu:12485-12493): traversal queries by descending
 // cell count, then brute-force queries.  tot[0..2] = traversal, brute-force,
@@ -198,9 +206,9 @@ hipError_t launch_tile_i8(const void* vec_cm, bool u8, uint32_t D, const uint32_
 hipError_t launch_note_bf(const uint32_t* tot, uint32_t* note, hipStream_t st);
 hipError_t launch_subsel(const SubSelArgs& a, hipStream_t st);
 hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st);
-hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bstart, uint32_t NS, uint32_t* icnt,
-                          uint32_t* ioff, BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill,
-                          hipStream_t st);
+hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bstart, const uint32_t* stile, uint32_t tch,
+                          uint32_t NS, uint32_t* icnt, uint32_t* ioff, BfItem* items, uint32_t* nitems,
+                          const uint32_t* ok, bool fill, hipStream_t st);
 // out[0] = start[n-1] + cnt[n-1] (total of an exclusive scan); out[1] = out[0] <= cap
 // (with cap2 != 0 also out[0] * mul <= cap2).
 hipError_t launch_sched(const SchedArgs& a, hipStream_t st);
@@ -238,6 +246,8 @@ hipError_t launch_cell_flags(uint32_t Q, uint32_t P, const uint32_t* cells, cons
                              const uint32_t* little, uint8_t* flags, hipStream_t st);
 hipError_t launch_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_t* bcell, const uint8_t* flags,
                                uint32_t* lists, uint32_t* counts, uint32_t* little, hipStream_t st);
+hipError_t launch_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t* gbound, hipStream_t st);
+hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, hipStream_t st);
 hipError_t launch_batch_need(uint32_t Q, uint32_t P, uint32_t nbatch, const uint32_t* plan_cells,
                              const uint32_t* plan_off, const uint8_t* flags, uint32_t* need, hipStream_t st);
 hipError_t launch_merge_stream(uint32_t Q, uint32_t K, uint32_t* run_ids, float* run_dist, const uint32_t* ids,

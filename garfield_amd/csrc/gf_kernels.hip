@@ -961,6 +961,27 @@ __global__ void k_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_
     little[q] = (n > 0 && all) ? n : 0u;
 }
 
+__global__ void k_zero_u32(uint32_t* x, uint32_t n) {
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) x[i] = 0;
+}
+
+// Per-query state of the MFMA brute-force schedule, reset in one pass:
+// pairs and appended keys zeroed, bounds open.
+__global__ void k_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t* gbound) {
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= Q) return;
+    nsub[q] = 0;
+    pcnt[q] = 0;
+    gbound[q] = 0xFFFFFFFFu;
+}
+
+// Sentinel results and zero counters for a batch's searches.
+__global__ void k_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < Q * K) { ids[i] = GF_NO_RESULT; dist[i] = __int_as_float(0x7F800000); }
+    if (i < Q * GF_NCOUNTERS) ctr[i] = 0;
+}
+
 // What each batch of a streamed plan must do for this query batch (one
 // workgroup per batch): need[b] bit 0 = some query takes the brute force on
 // it (all its selected cells of the batch little), bit 1 = some query
@@ -973,7 +994,7 @@ __global__ __launch_bounds__(256) void k_batch_need(uint32_t Q, uint32_t P, cons
     __syncthreads();
     const uint32_t c0 = plan_off[bi], c1 = plan_off[bi + 1];
     uint32_t mine = 0;
-    for (uint32_t q = threadIdx.x; q < Q; q += blockDim.x) {
+    for (uint32_t q = blockIdx.y * blockDim.x + threadIdx.x; q < Q; q += gridDim.y * blockDim.x) {
         const uint8_t* fl = flags + size_t(q) * P;
         uint32_t n = 0;
         bool all = true;
@@ -985,7 +1006,7 @@ __global__ __launch_bounds__(256) void k_batch_need(uint32_t Q, uint32_t P, cons
     }
     if (mine) atomicOr(&acc, mine);
     __syncthreads();
-    if (threadIdx.x == 0) need[bi] = acc;
+    if (threadIdx.x == 0 && acc) atomicOr(&need[bi], acc);   // need[] zeroed before
 }
 
 // Running top-K of a streamed search: merge the batch's sorted K results
@@ -1332,6 +1353,13 @@ __global__ __launch_bounds__(256) void k_subsel(SubSelArgs p) {
 // (spreading the per-query atomics of concurrent workgroups).  Pass 1 counts
 // per sub-cell and per query; pass 2 writes the lists at their scanned
 // offsets in the same order.
+// Items per (query, sub-cell) pair: the sub-cell's tiles in chunks of tch
+// (0: one item).
+__device__ __forceinline__ uint32_t tile_chunks(const uint32_t* stile, uint32_t s, uint32_t tch) {
+    const uint32_t nt = stile[s + 1] - stile[s];
+    return tch ? (nt + tch - 1) / tch : 1u;
+}
+
 __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
     __shared__ uint32_t wcnt[4];
     __shared__ uint32_t fq[kFlushCap];
@@ -1344,15 +1372,20 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
     }
     const SubBox box = load_box(sa, s);
     const uint32_t base = fill ? p.bstart[s] : 0u;
+    const uint32_t nch_s = tile_chunks(sa.stile, s, p.tch);   // items per (query, sub-cell) pair
     uint32_t running = 0, fn = 0;   // fn: queries listed since the last flush (uniform)
-    const uint32_t nch = (p.Q + 255u) / 256u;
+    // candidates: every query, or the brute-force queries of the schedule
+    const uint32_t q0 = p.qlist ? p.qrange[0] : 0u;
+    const uint32_t nq = p.qlist ? p.qrange[1] - q0 : p.Q;
+    const uint32_t nch = (nq + 255u) / 256u;
     for (uint32_t ci = 0; ci < nch; ++ci) {
         if (!fill && fn + 256u > kFlushCap) {
-            for (uint32_t i = tid; i < fn; i += 256u) atomicAdd(&p.nsub[fq[i]], 1u);
+            for (uint32_t i = tid; i < fn; i += 256u) atomicAdd(&p.nsub[fq[i]], nch_s);
             __syncthreads();
             fn = 0;
         }
-        const uint32_t q = ((ci + s) % nch) * 256u + tid;
+        const uint32_t qi = ((ci + s) % nch) * 256u + tid;
+        const uint32_t q = qi < nq ? (p.qlist ? p.qlist[q0 + qi] : qi) : 0xFFFFFFFFu;
         bool hit = false;
         if (q < p.Q) {
             const uint32_t cnt = p.counts[q], lit = p.little[q];
@@ -1378,7 +1411,7 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
         __syncthreads();
     }
     if (!fill) {
-        for (uint32_t i = tid; i < fn; i += 256u) atomicAdd(&p.nsub[fq[i]], 1u);
+        for (uint32_t i = tid; i < fn; i += 256u) atomicAdd(&p.nsub[fq[i]], nch_s);
         if (tid == 0) p.bcnt[s] = running;
     }
 }
@@ -1454,8 +1487,11 @@ __global__ __launch_bounds__(256) void k_stats(StatsArgs p) {
 }
 
 // Work items of the MFMA brute force: ceil(n / 64) blocks per sub-cell.
-__global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bstart, uint32_t NS, uint32_t* icnt,
-                          const uint32_t* ioff, BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill) {
+// Work items of the MFMA brute force: per sub-cell, its query list in groups
+// of 64, times its tiles in chunks of tch (0: one chunk).
+__global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bstart, const uint32_t* stile, uint32_t tch,
+                          uint32_t NS, uint32_t* icnt, const uint32_t* ioff, BfItem* items, uint32_t* nitems,
+                          const uint32_t* ok, bool fill) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= NS) return;
     if (fill && !*ok) {
@@ -1463,10 +1499,16 @@ __global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bstart, uint32_t
         return;
     }
     const uint32_t n = bcnt[s], nb = (n + kBfQB - 1) / kBfQB;
-    if (!fill) { icnt[s] = nb; return; }
-    for (uint32_t b = 0; b < nb; ++b)
-        items[ioff[s] + b] = BfItem{s, bstart[s] + b * kBfQB, min(kBfQB, n - b * kBfQB)};
-    if (s == NS - 1) *nitems = ioff[s] + nb;
+    const uint32_t nc = n ? tile_chunks(stile, s, tch) : 0u;
+    if (!fill) { icnt[s] = nb * nc; return; }
+    const uint32_t t0 = stile[s], t1 = stile[s + 1], step = tch ? tch : (t1 - t0);
+    uint32_t k = ioff[s];
+    for (uint32_t c = 0; c < nc; ++c) {
+        const uint32_t tb = t0 + c * step, te = min(t1, tb + step);
+        for (uint32_t b = 0; b < nb; ++b)
+            items[k++] = BfItem{s, bstart[s] + b * kBfQB, min(kBfQB, n - b * kBfQB), tb, te};
+    }
+    if (s == NS - 1) *nitems = ioff[s] + nb * nc;
 }
 
 // out[0] = start[n-1] + cnt[n-1], the total of an exclusive scan; out[1] =
@@ -1513,7 +1555,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3
     for (uint32_t item_id = i_lo + k8 * 4u + wave; item_id < i_hi; item_id += nwg_x * 4u) {
         const BfItem it = p.items[item_id];
         const uint32_t s = it.sub, cell = sa.scell[s];
-        const uint32_t t0 = sa.stile[s], t1 = sa.stile[s + 1];
+        const uint32_t t0 = it.tb, t1 = it.te;
 
         // Owner state: lane q owns query q of the block; its sorted top-K of
         // (distance << 32 | row) keys lives in registers.
@@ -1750,6 +1792,33 @@ __global__ __launch_bounds__(64) void k_tile_i8(const T* vec, uint32_t D, const 
     const uint32_t row = tmeta[size_t(t) * 16u * (1u + AW) + col];
     const bool valid = row != 0xFFFFFFFFu;
     const uint32_t KS = D / 64u;
+    if constexpr (sizeof(T) == 1) {
+        // u8 rows: each lane moves its 16 bytes of a k-step with one load and
+        // one store (x - 128 as int8 is x ^ 0x80); the norm of a point is the
+        // sum over its four lanes (col, col + 16, col + 32, col + 48).
+        int32_t n = 0;
+        for (uint32_t s = 0; s < KS; ++s) {
+            uint4 v = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
+            if (valid) v = *reinterpret_cast<const uint4*>(vec + size_t(row) * D + s * 64u + (lane >> 4) * 16u);
+            v.x ^= 0x80808080u; v.y ^= 0x80808080u; v.z ^= 0x80808080u; v.w ^= 0x80808080u;
+            *reinterpret_cast<uint4*>(vt + (size_t(t) * KS + s) * 1024u + lane * 16u) = v;
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int32_t x = int32_t(int8_t(uint8_t(w[i] >> (8 * k))));
+                    n += x * x;
+                }
+        }
+        n += __shfl_xor(n, 16, 64);
+        n += __shfl_xor(n, 32, 64);
+        if (lane < 16) {
+            tnorm[size_t(t) * 32u + col] = -(n >> 1);
+            tnorm[size_t(t) * 32u + 16u + col] = n;
+        }
+        return;
+    }
     for (uint32_t s = 0; s < KS; ++s) {
         int8_t* dst = vt + (size_t(t) * KS + s) * 1024u + lane * 16u;
         for (uint32_t j = 0; j < 16; ++j) {
@@ -1918,12 +1987,12 @@ hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bstart, uint32_t NS, uint32_t* icnt,
-                          uint32_t* ioff, BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill,
-                          hipStream_t st) {
+hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bstart, const uint32_t* stile, uint32_t tch,
+                          uint32_t NS, uint32_t* icnt, uint32_t* ioff, BfItem* items, uint32_t* nitems,
+                          const uint32_t* ok, bool fill, hipStream_t st) {
     if (!NS) return hipSuccess;
-    hipLaunchKernelGGL(k_bfitems, dim3((NS + 255) / 256), dim3(256), 0, st, bcnt, bstart, NS, icnt, ioff, items,
-                       nitems, ok, fill);
+    hipLaunchKernelGGL(k_bfitems, dim3((NS + 255) / 256), dim3(256), 0, st, bcnt, bstart, stile, tch, NS, icnt, ioff,
+                       items, nitems, ok, fill);
     return hipGetLastError();
 }
 
@@ -2037,10 +2106,23 @@ hipError_t launch_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_
     return hipGetLastError();
 }
 
+hipError_t launch_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t* gbound, hipStream_t st) {
+    hipLaunchKernelGGL(k_bf_reset, dim3((Q + 255) / 256), dim3(256), 0, st, Q, nsub, pcnt, gbound);
+    return hipGetLastError();
+}
+
+hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, hipStream_t st) {
+    const uint32_t n = Q * (K > GF_NCOUNTERS ? K : GF_NCOUNTERS);
+    hipLaunchKernelGGL(k_reset_results, dim3((n + 255) / 256), dim3(256), 0, st, Q, K, ids, dist, ctr);
+    return hipGetLastError();
+}
+
 hipError_t launch_batch_need(uint32_t Q, uint32_t P, uint32_t nbatch, const uint32_t* plan_cells,
                              const uint32_t* plan_off, const uint8_t* flags, uint32_t* need, hipStream_t st) {
     if (!nbatch) return hipSuccess;
-    hipLaunchKernelGGL(k_batch_need, dim3(nbatch), dim3(256), 0, st, Q, P, plan_cells, plan_off, flags, need);
+    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(256), 0, st, need, nbatch);
+    const uint32_t gy = (Q + 255) / 256 < 64u ? (Q + 255) / 256 : 64u;
+    hipLaunchKernelGGL(k_batch_need, dim3(nbatch, gy), dim3(256), 0, st, Q, P, plan_cells, plan_off, flags, need);
     return hipGetLastError();
 }
 

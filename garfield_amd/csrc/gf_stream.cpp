@@ -27,6 +27,7 @@ namespace gf {
 namespace {
 
 constexpr size_t kAlign = 256;
+constexpr uint32_t kStreamTileChunk = 16;   // tiles per MFMA brute-force item on a streamed batch
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 uint32_t next_pow2(uint32_t x) {
@@ -309,7 +310,9 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         if (b.nsub.n < Q) { b.nsub.alloc(Q); b.part_off.alloc(Q); b.pcnt.alloc(Q); b.gbound.alloc(Q); }
         if (!b.bq.n) b.bq.alloc(size_t(Q) * 64);
         if (b.part.n < b.bq.n * K) b.part.alloc(b.bq.n * K);
-        if (b.items.n < b.bq.n / kBfQB + NS + 1) b.items.alloc(b.bq.n / kBfQB + NS + 1);
+        // items <= pairs x chunks / 64 + chunks of all sub-cells (k_bfitems)
+        const size_t ni = b.bq.n / kBfQB + S.tmax / kStreamTileChunk + NS + 2;
+        if (b.items.n < ni) b.items.alloc(ni);
         if (b.bfmask.n < size_t(Q) * Bm) b.bfmask.alloc(size_t(Q) * Bm);
         if (b.note.n < 2 * std::max<size_t>(nb, 1)) b.note.alloc(2 * std::max<size_t>(nb, 1));
     }
@@ -334,20 +337,17 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         sa.abase = reinterpret_cast<const int32_t*>(dev + sb.o_abase);
         sa.a = ix.a; sa.AW = S.AW; sa.P = sb.B; sa.NS = sb.NS;
         GF_HIP(launch_tile_i8(dev + sb.o_vec, true, ix.D, sa.tmeta, S.AW, sb.ntile, S.vt.p, S.tnorm.p, st));
-        // exact passing counts of the batch (the PASS counter)
-        GF_HIP(hipMemsetAsync(b.selcount.p, 0, size_t(Q) * sizeof(uint32_t), st));
-        SubSelArgs sl{};
-        sl.sa = sa; sl.Q = Q; sl.lo = b.lo.p; sl.hi = b.hi.p; sl.selcount = b.selcount.p;
-        if (sb.NS) GF_HIP(launch_subsel(sl, st));
         GF_HIP(launch_cell_flags(Q, sb.B, b.slist.p, b.scount.p, b.slittle.p, b.bfmask.p, st));
         BfSchedArgs sc{};
         sc.sa = sa;
         sc.Q = Q; sc.postfilter = 0xFFFFFFFFu; sc.counts = b.scount.p; sc.little = b.slittle.p;
         sc.lo = b.lo.p; sc.hi = b.hi.p; sc.nsub = b.nsub.p; sc.bcnt = b.bcnt.p; sc.bstart = b.bstart.p;
         sc.bq = b.bq.p; sc.ok = tot + 3; sc.nbf = tot + 9; sc.bfm = b.bfmask.p; sc.bP = sb.B;
-        GF_HIP(hipMemsetAsync(b.nsub.p, 0, size_t(Q) * sizeof(uint32_t), st));
-        GF_HIP(hipMemsetAsync(b.pcnt.p, 0, size_t(Q) * sizeof(uint32_t), st));
-        GF_HIP(hipMemsetAsync(b.gbound.p, 0xFF, size_t(Q) * sizeof(uint32_t), st));
+        sc.qlist = b.sched.p; sc.qrange = tot + 14;
+        // a batch holds few, small sub-cells: items of kStreamTileChunk tiles
+        // give the persistent kernel enough of them to fill the GPU
+        sc.tch = kStreamTileChunk;
+        GF_HIP(launch_bf_reset(Q, b.nsub.p, b.pcnt.p, b.gbound.p, st));
         if (sb.NS) {
             GF_HIP(launch_bfsched(sc, false, st));
             GF_HIP(launch_scan_small(b.bcnt.p, sb.NS, b.bstart.p, st));
@@ -358,11 +358,11 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         GF_HIP(hipMemsetAsync(tot + 4, 0, sizeof(uint32_t), st));
         if (sb.NS) {
             GF_HIP(launch_bfsched(sc, true, st));
-            GF_HIP(launch_bfitems(b.bcnt.p, b.bstart.p, sb.NS, b.icnt.p, b.ioff.p, b.items.p, tot + 4, tot + 3, false,
-                                  st));
+            GF_HIP(launch_bfitems(b.bcnt.p, b.bstart.p, sa.stile, kStreamTileChunk, sb.NS, b.icnt.p, b.ioff.p,
+                                  b.items.p, tot + 4, tot + 3, false, st));
             GF_HIP(launch_scan_small(b.icnt.p, sb.NS, b.ioff.p, st));
-            GF_HIP(launch_bfitems(b.bcnt.p, b.bstart.p, sb.NS, b.icnt.p, b.ioff.p, b.items.p, tot + 4, tot + 3, true,
-                                  st));
+            GF_HIP(launch_bfitems(b.bcnt.p, b.bstart.p, sa.stile, kStreamTileChunk, sb.NS, b.icnt.p, b.ioff.p,
+                                  b.items.p, tot + 4, tot + 3, true, st));
         }
         BfGemmArgs ga{};
         ga.sa = sa;
@@ -404,8 +404,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         sa.Q = Q; sa.P = sb.B; sa.postfilter = 0xFFFFFFFFu; sa.counts = b.scount.p; sa.little = b.slittle.p;
         sa.sched = b.sched.p; sa.tot = tot + 8; sa.ranges = tot + 12;
         GF_HIP(launch_sched(sa, st));
-        GF_HIP(launch_fill_results(b.s_ids.p, b.s_dist.p, Q * K, st));
-        GF_HIP(hipMemsetAsync(b.s_ctr.p, 0, size_t(Q) * GF_NCOUNTERS * sizeof(uint32_t), st));
+        GF_HIP(launch_reset_results(Q, K, b.s_ids.p, b.s_dist.p, b.s_ctr.p, st));
         TravArgs at = base;
         at.vec = dev + sb.o_vec;
         at.graph = reinterpret_cast<const uint32_t*>(dev + sb.o_graph);
@@ -445,7 +444,12 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         GF_HIP(hipMemcpyAsync(need.data(), b.need.p, nb * 4, hipMemcpyDeviceToHost, st));
         GF_HIP(hipStreamSynchronize(st));
     }
-    if (gemm) GF_HIP(hipMemsetAsync(b.note.p, 0xFF, 2 * nb * sizeof(uint32_t), st));
+    if (gemm) {
+        GF_HIP(hipMemsetAsync(b.note.p, 0xFF, 2 * nb * sizeof(uint32_t), st));
+        // the MFMA route does not count passing points on a streamed batch:
+        // its PASS counter stays 0
+        GF_HIP(hipMemsetAsync(b.selcount.p, 0, size_t(Q) * sizeof(uint32_t), st));
+    }
     // The copy stream starts after everything queued so far on the compute
     // stream (flags, entries): a turn buffer is never in use at this point.
     GF_HIP(hipEventRecord(S.freed[0], st));
@@ -477,7 +481,8 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         if (need) {
             const size_t cap = need + need / 4 + 1024;
             const uint32_t NS = std::max(S.NSmax, 1u);
-            b.bq.alloc(cap); b.part.alloc(cap * K); b.items.alloc(cap / kBfQB + NS + 1);
+            b.bq.alloc(cap); b.part.alloc(cap * K);
+            b.items.alloc(cap / kBfQB + S.tmax / kStreamTileChunk + NS + 2);
             for (size_t bi = 0; bi < nb; ++bi)
                 if (!note[2 * bi]) {
                     enqueue_copy(bi, 0, S.batches[bi].bytes_mfma);

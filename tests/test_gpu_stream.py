@@ -54,7 +54,8 @@ def _args(ix):
 def _oracle_stream(ix, plan, cfg, flags, ent, L, K=10, rl=10, mfma=False):
     """Per-batch oracle searches merged into a running top K (see module doc).
     mfma: the brute force ran on MFMA, which evaluates every scanned point
-    (its DIST counter is the SCAN counter)."""
+    (its DIST counter is the SCAN counter) and, on a streamed batch, does not
+    count passing points (PASS = 0)."""
     from oracle import oracle as orc
     P, E, N = ix["P"], ix["E"], ix["vectors"].shape[0]
     sizes = synth.cell_sizes(ix)
@@ -81,6 +82,7 @@ def _oracle_stream(ix, plan, cfg, flags, ent, L, K=10, rl=10, mfma=False):
         c = c.copy()
         if mfma:
             c[c[:, 7] == 2, 1] = c[c[:, 7] == 2, 5]
+            c[c[:, 7] == 2, 6] = 0     # the streamed MFMA route does not count passing points
         c[:, 7] = np.where(c[:, 7] == 1, 1, np.where(c[:, 7] == 2, 1 << 16, 0))
         if run_ids is None:
             run_ids, run_d, run_c = ids.copy(), d.copy(), c.astype(np.int64)
