@@ -7,12 +7,15 @@ stages (ZJU-DAILY/Garfield indexsearch/):
 - ``intersection_area_mark_little_seg_V2``  real_dataset_adapter.cuh:388-519
 - ``get_partitions_access_order_V2``        gpu_graph.cu:11742-11845
 - ``batch_graph_search_gpu_with_prefilter_and_postfilter``  gpu_graph.cu:12463-12616
+- ``intersection_area_mark_little_seg_batch_process``  gpu_graph.cu:12066-12187 (arithmetic grid)
+- ``batch_graph_search_gpu_with_prefilter_batch_process_compressed_graph_T_dataset_resident_u8``
+  big_dataset_adapterV3.cuh:3719-4117 (out-of-core; the index is ``Index.create_streamed``)
 
 All computation runs in the HIP library; every call raises if the library has
 not been built or cannot reach a GPU, and there is no CPU fallback.
 """
 from ._lib import (GarfieldError, Index, Batch, SearchStats, lib_path, f2h, row_norms_f16,
-                   entry_points, NO_RESULT, NCOUNTERS, VEC_F32, VEC_F16)
+                   entry_points, NO_RESULT, NCOUNTERS, VEC_F32, VEC_F16, VEC_U8)
 
 
 def intersection_area_mark_little_seg_V2(batch, prefilter):
@@ -32,9 +35,25 @@ def batch_graph_search_gpu_with_prefilter_and_postfilter(batch, L, K=10, recycle
                         entry_points=entry_points)
 
 
+def intersection_area_mark_little_seg_batch_process(batch, attr_min, attr_width, little_seg_threshold):
+    """Stage A on an arithmetic grid (per-cell overlap areas); returns device ms."""
+    return batch.mark_cells_grid(attr_min, attr_width, little_seg_threshold)
+
+
+def batch_graph_search_gpu_with_prefilter_batch_process_compressed_graph_T_dataset_resident_u8(
+        batch, L, K=10, recycle_list_size=10, entry_points=None):
+    """Out-of-core stage C on a streamed index (the batch plan is the index's);
+    returns (ids[Q,K], dists[Q,K], SearchStats)."""
+    if not batch.index.streamed:
+        raise GarfieldError(1, "not a streamed index: use batch_graph_search_gpu_with_prefilter_and_postfilter")
+    return batch.search(L=L, K=K, rl=recycle_list_size, entry_points=entry_points)
+
+
 __all__ = [
     "GarfieldError", "Index", "Batch", "SearchStats", "lib_path", "f2h", "row_norms_f16",
-    "entry_points", "NO_RESULT", "NCOUNTERS", "VEC_F32", "VEC_F16",
+    "entry_points", "NO_RESULT", "NCOUNTERS", "VEC_F32", "VEC_F16", "VEC_U8",
     "intersection_area_mark_little_seg_V2", "get_partitions_access_order_V2",
     "batch_graph_search_gpu_with_prefilter_and_postfilter",
+    "intersection_area_mark_little_seg_batch_process",
+    "batch_graph_search_gpu_with_prefilter_batch_process_compressed_graph_T_dataset_resident_u8",
 ]

@@ -43,7 +43,8 @@ class _Host(C.Structure):
 class _Info(C.Structure):
     _fields_ = [("N", C.c_uint32), ("D", C.c_uint32), ("a", C.c_uint32), ("P", C.c_uint32),
                 ("R", C.c_uint32), ("E", C.c_uint32), ("C", C.c_uint32), ("vec_dtype", C.c_uint32),
-                ("f2h_factor", C.c_float), ("device_bytes", C.c_uint64)]
+                ("f2h_factor", C.c_float), ("device_bytes", C.c_uint64), ("streamed", C.c_uint32),
+                ("nbatch", C.c_uint32)]
 
 
 class _SearchOpts(C.Structure):
@@ -145,6 +146,7 @@ class Index:
         self.R, self.E, self.C = info.R, info.E, info.C
         self.vec_dtype, self.f2h_factor = info.vec_dtype, info.f2h_factor
         self.device_bytes = info.device_bytes
+        self.streamed, self.nbatch = bool(info.streamed), info.nbatch
 
     @classmethod
     def open(cls, data_path, cagra_prefix, cagra_suffix, global_graph, grid, attrs, cluster=None,

@@ -511,6 +511,8 @@ gf_status gf_index_get_info(const gf_index* ix, gf_index_info* out) {
         out->vec_dtype = uint32_t(ix->vdtype);
         out->f2h_factor = ix->alpha;
         out->device_bytes = ix->device_bytes();
+        out->streamed = ix->sx ? 1u : 0u;
+        out->nbatch = ix->sx ? uint32_t(ix->sx->batches.size()) : 0u;
     });
 }
 
@@ -743,7 +745,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         const uint32_t NS = ix->NS;
         if (gemm) {
             if (!b->bcnt.n) {
-                b->bcnt.alloc(NS); b->bstart.alloc(NS); b->icnt.alloc(NS); b->ioff.alloc(NS);
+                b->bcnt.alloc(NS); b->bin.alloc(NS); b->bstart.alloc(NS); b->icnt.alloc(NS); b->ioff.alloc(NS);
                 b->nsub.alloc(Q); b->part_off.alloc(Q); b->pcnt.alloc(Q);
             }
             if (!b->bq.n) {
@@ -760,7 +762,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             gf::BfSchedArgs sc{};
             sc.sa = sub_args(*ix);
             sc.Q = Q; sc.postfilter = opts->postfilter; sc.counts = b->counts.p;
-            sc.little = b->little.p; sc.lo = b->lo.p; sc.hi = b->hi.p; sc.nsub = b->nsub.p; sc.bcnt = b->bcnt.p;
+            sc.little = b->little.p; sc.lo = b->lo.p; sc.hi = b->hi.p; sc.nsub = b->nsub.p; sc.bcnt = b->bcnt.p; sc.bin = b->bin.p;
             sc.bstart = b->bstart.p; sc.bq = b->bq.p;
             sc.ok = tot + 3; sc.nbf = tot + 9;
             sc.qlist = b->sched.p; sc.qrange = tot + 14;   // the brute-force queries of the schedule
@@ -770,25 +772,24 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 sc.bfm = b->bfmask.p;
                 sc.bP = ix->P;
             }
-            GF_HIP(hipMemsetAsync(b->nsub.p, 0, size_t(Q) * sizeof(uint32_t), st));
-            GF_HIP(hipMemsetAsync(b->pcnt.p, 0, size_t(Q) * sizeof(uint32_t), st));
-            GF_HIP(hipMemsetAsync(b->gbound.p, 0xFF, size_t(Q) * sizeof(uint32_t), st));
+            GF_HIP(gf::launch_bf_reset(Q, b->nsub.p, b->pcnt.p, b->gbound.p, st));
             GF_HIP(gf::launch_bfsched(sc, false, st));
             GF_HIP(gf::launch_scan_small(b->bcnt.p, NS, b->bstart.p, st));
             GF_HIP(gf::launch_scan_small(b->nsub.p, Q, b->part_off.p, st));
             GF_HIP(gf::launch_total(b->nsub.p, b->part_off.p, Q, uint32_t(std::min<size_t>(b->bq.n, UINT32_MAX)), K,
                                     b->part.n, tot + 2, st));
             GF_HIP(gf::launch_bfsched(sc, true, st));
-            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bstart.p, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p, b->items.p,
+            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p, b->items.p,
                                       tot + 4, tot + 3, false, st));
             GF_HIP(gf::launch_scan_small(b->icnt.p, NS, b->ioff.p, st));
-            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bstart.p, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p, b->items.p,
+            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p, b->items.p,
                                       tot + 4, tot + 3, true, st));
             gf::BfGemmArgs ga{};
             ga.sa = sub_args(*ix);
             ga.vt = ix->vt.p; ga.tnorm = ix->tnorm.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p;
             ga.hi = b->hi.p; ga.items = b->items.p; ga.nitems = tot + 4; ga.bq = b->bq.p; ga.pcnt = b->pcnt.p;
-            ga.part_off = b->part_off.p; ga.part = b->part.p; ga.gbound = b->gbound.p; ga.ok = tot + 3;
+            ga.part_off = b->part_off.p; ga.part = b->part.p; ga.gbound = b->gbound.p;
+            ga.ok = tot + 3;
             ga.K = K; ga.D = ix->D;
             GF_HIP(hipEventRecord(evg[0], st));
             GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu) * 3u, st));

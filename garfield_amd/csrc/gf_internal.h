@@ -95,6 +95,7 @@ constexpr uint32_t kBfQB = 64;        // queries per work item
 struct BfItem {
     uint32_t sub, qbase, nq;           // sub-cell, first entry of its query list, queries
     uint32_t tb, te;                   // tiles [tb, te) of the sub-cell
+    uint32_t inside;                   // 1: every query's range contains the sub-cell's box
 };
 struct BfGemmArgs {
     SubArgs sa;
@@ -153,6 +154,7 @@ struct BfSchedArgs {
     const float* hi;
     uint32_t* nsub;            // pairs per query (pass 1, zeroed before)
     uint32_t* bcnt;            // pairs per sub-cell (pass 1)
+    uint32_t* bin;             // of which the range contains the whole sub-cell box (pass 1)
     const uint32_t* bstart;    // exclusive scan of bcnt (pass 2)
     uint32_t* bq;
     const uint32_t* ok;        // bq and part are large enough (pass 2)
@@ -206,8 +208,8 @@ hipError_t launch_tile_i8(const void* vec_cm, bool u8, uint32_t D, const uint32_
 hipError_t launch_note_bf(const uint32_t* tot, uint32_t* note, hipStream_t st);
 hipError_t launch_subsel(const SubSelArgs& a, hipStream_t st);
 hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st);
-hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bstart, const uint32_t* stile, uint32_t tch,
-                          uint32_t NS, uint32_t* icnt, uint32_t* ioff, BfItem* items, uint32_t* nitems,
+hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, const uint32_t* stile,
+                          uint32_t tch, uint32_t NS, uint32_t* icnt, uint32_t* ioff, BfItem* items, uint32_t* nitems,
                           const uint32_t* ok, bool fill, hipStream_t st);
 // out[0] = start[n-1] + cnt[n-1] (total of an exclusive scan); out[1] = out[0] <= cap
 // (with cap2 != 0 also out[0] * mul <= cap2).

@@ -9,6 +9,8 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "gf_internal.h"
 
 namespace gf {
@@ -1159,7 +1161,12 @@ constexpr uint32_t kQB = 64;        // queries per wave
 constexpr uint32_t kBfBufQ = 24;    // survivor slots per query
 constexpr uint32_t kBfDrainAt = 8;  // drain once a query holds this many (+ <= 16 per tile < 24)
 constexpr uint64_t kKeySent = ~uint64_t(0);
-constexpr int32_t kTpOpen = INT32_MIN;  // acc threshold while fewer than K are known
+// acc threshold while fewer than K are known: every point passes it except
+// tile padding, whose accumulator is seeded with INT32_MIN (its int8 vector is
+// zero, so its accumulator stays there); padding never survives, with or
+// without the range test.
+constexpr int32_t kTpOpen = INT32_MIN + 1;
+constexpr int32_t kPadSeed = INT32_MIN;
 
 // LDS ordering between the lanes of one wave of a multi-wave workgroup:
 // the fences stop the compiler from moving LDS accesses across this point,
@@ -1361,19 +1368,22 @@ __device__ __forceinline__ uint32_t tile_chunks(const uint32_t* stile, uint32_t 
 }
 
 __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
-    __shared__ uint32_t wcnt[4];
+    __shared__ uint32_t wcnt[2][4];
     __shared__ uint32_t fq[kFlushCap];
     const SubArgs& sa = p.sa;
     const uint32_t s = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
     if (fill && !*p.ok) return;
     if (sa.ssize[s] == 0 || *p.nbf == 0) {
-        if (!fill && tid == 0) p.bcnt[s] = 0;
+        if (!fill && tid == 0) { p.bcnt[s] = 0; p.bin[s] = 0; }
         return;
     }
     const SubBox box = load_box(sa, s);
     const uint32_t base = fill ? p.bstart[s] : 0u;
     const uint32_t nch_s = tile_chunks(sa.stile, s, p.tch);   // items per (query, sub-cell) pair
-    uint32_t running = 0, fn = 0;   // fn: queries listed since the last flush (uniform)
+    // A sub-cell's list holds the queries whose range contains its whole box
+    // first (their items skip the range test), then the partial ones.
+    const uint32_t nin = fill ? p.bin[s] : 0u;
+    uint32_t run_in = 0, run_p = 0, fn = 0;   // fn: queries listed since the last flush (uniform)
     // candidates: every query, or the brute-force queries of the schedule
     const uint32_t q0 = p.qlist ? p.qrange[0] : 0u;
     const uint32_t nq = p.qlist ? p.qrange[1] - q0 : p.Q;
@@ -1386,33 +1396,44 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
         }
         const uint32_t qi = ((ci + s) % nch) * 256u + tid;
         const uint32_t q = qi < nq ? (p.qlist ? p.qlist[q0 + qi] : qi) : 0xFFFFFFFFu;
-        bool hit = false;
+        uint32_t rel = 0;
         if (q < p.Q) {
             const uint32_t cnt = p.counts[q], lit = p.little[q];
             const bool trav = cnt < p.postfilter && cnt != lit;
-            hit = !trav && lit > 0 && (!p.bfm || (p.bfm[size_t(q) * p.bP + sa.scell[s]] & 2u)) &&
-                  sub_relation(box, sa.a, load_range(sa.a, p.lo, p.hi, q)) != 0;
+            if (!trav && lit > 0 && (!p.bfm || (p.bfm[size_t(q) * p.bP + sa.scell[s]] & 2u)))
+                rel = sub_relation(box, sa.a, load_range(sa.a, p.lo, p.hi, q));
         }
-        const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
-        if (lane == 0) wcnt[wave] = uint32_t(__builtin_popcountll(m));
+        const uint64_t mi = __builtin_amdgcn_ballot_w64(rel == 2u);
+        const uint64_t mp = __builtin_amdgcn_ballot_w64(rel == 1u);
+        if (lane == 0) {
+            wcnt[0][wave] = uint32_t(__builtin_popcountll(mi));
+            wcnt[1][wave] = uint32_t(__builtin_popcountll(mp));
+        }
         __syncthreads();
-        uint32_t woff = 0, tot = 0;
+        uint32_t oi = 0, op = 0, ti = 0, tp = 0;
 #pragma unroll
         for (uint32_t w = 0; w < 4; ++w) {
-            woff += w < wave ? wcnt[w] : 0u;
-            tot += wcnt[w];
+            oi += w < wave ? wcnt[0][w] : 0u;
+            op += w < wave ? wcnt[1][w] : 0u;
+            ti += wcnt[0][w];
+            tp += wcnt[1][w];
         }
-        if (hit) {
-            if (!fill) fq[fn + woff + lanes_below(m)] = q;
-            else p.bq[base + running + woff + lanes_below(m)] = q;
+        if (rel) {
+            if (!fill) {
+                fq[fn + (rel == 2u ? oi + lanes_below(mi) : ti + op + lanes_below(mp))] = q;
+            } else {
+                const uint32_t pos = rel == 2u ? run_in + oi + lanes_below(mi) : nin + run_p + op + lanes_below(mp);
+                p.bq[base + pos] = q;
+            }
         }
-        running += tot;
-        fn += tot;
+        run_in += ti;
+        run_p += tp;
+        fn += ti + tp;
         __syncthreads();
     }
     if (!fill) {
         for (uint32_t i = tid; i < fn; i += 256u) atomicAdd(&p.nsub[fq[i]], nch_s);
-        if (tid == 0) p.bcnt[s] = running;
+        if (tid == 0) { p.bcnt[s] = run_in + run_p; p.bin[s] = run_in; }
     }
 }
 
@@ -1489,9 +1510,9 @@ __global__ __launch_bounds__(256) void k_stats(StatsArgs p) {
 // Work items of the MFMA brute force: ceil(n / 64) blocks per sub-cell.
 // Work items of the MFMA brute force: per sub-cell, its query list in groups
 // of 64, times its tiles in chunks of tch (0: one chunk).
-__global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bstart, const uint32_t* stile, uint32_t tch,
-                          uint32_t NS, uint32_t* icnt, const uint32_t* ioff, BfItem* items, uint32_t* nitems,
-                          const uint32_t* ok, bool fill) {
+__global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, const uint32_t* stile,
+                          uint32_t tch, uint32_t NS, uint32_t* icnt, const uint32_t* ioff, BfItem* items,
+                          uint32_t* nitems, const uint32_t* ok, bool fill) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= NS) return;
     if (fill && !*ok) {
@@ -1505,8 +1526,10 @@ __global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bstart, const ui
     uint32_t k = ioff[s];
     for (uint32_t c = 0; c < nc; ++c) {
         const uint32_t tb = t0 + c * step, te = min(t1, tb + step);
-        for (uint32_t b = 0; b < nb; ++b)
-            items[k++] = BfItem{s, bstart[s] + b * kBfQB, min(kBfQB, n - b * kBfQB), tb, te};
+        for (uint32_t b = 0; b < nb; ++b) {
+            const uint32_t m = min(kBfQB, n - b * kBfQB);
+            items[k++] = BfItem{s, bstart[s] + b * kBfQB, m, tb, te, b * kBfQB + m <= bin[s] ? 1u : 0u};
+        }
     }
     if (s == NS - 1) *nitems = ioff[s] + nb * nc;
 }
@@ -1661,51 +1684,62 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3
 #pragma unroll
             for (int w = 0; w < AW; ++w) ma[w] = *reinterpret_cast<const v4i32_t*>(mt + 16u * (1 + w) + 4u * grp);
         };
-        load_tile(t0);
-        for (uint32_t t = t0; t < t1; ++t) {
-            v4i32_t acc[4];
+        // The tile loop, with the range test, or without it for an item
+        // whose queries all contain the sub-cell's box (every point passes).
+        auto tiles = [&](auto filt) {
+            constexpr bool FILTER = decltype(filt)::value;
+            load_tile(t0);
+            for (uint32_t t = t0; t < t1; ++t) {
+                // k-outer: the four column tiles' MFMAs are independent, so a
+                // dependent MFMA (same accumulator) issues three MFMAs later
+                v4i32_t acc[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B[j][0], mh, 0, 0, 0);
+                for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B[j][0], mh, 0, 0, 0);
 #pragma unroll
                 for (int k = 1; k < KS; ++k)
-                    acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[k], B[j][k], acc[j], 0, 0, 0);
-            }
-            const v4i32_t cmh = mh, cmn = mn, cmr = mr, cma0 = ma[0], cma1 = ma[AW - 1];
-            if (t + 1 < t1) load_tile(t + 1);
-            // Branch-free test of one (point i, query column j) pair.
-            auto pass = [&](int j, int i) {
-                bool ok = acc[j][i] >= tp[j];
-                const uint32_t x0 = uint32_t(cma0[i]);
-                ok &= clamp16(x0, blo[j][0], bhi[j][0]) == x0;
-                if (AW > 1) {
-                    const uint32_t x1 = uint32_t(cma1[i]);
-                    ok &= clamp16(x1, blo[j][AW - 1], bhi[j][AW - 1]) == x1;
-                }
-                return ok;
-            };
-            bool anyl = false;   // lane-mask OR: no per-pair ballot
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) anyl |= pass(j, i);
-            if (__builtin_amdgcn_ballot_w64(anyl)) {
-                // Append: the owner adds |q'|^2 to nx - 2 q'.x' later.
-                bool full = false;
+                    for (int j = 0; j < 4; ++j)
+                        acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[k], B[j][k], acc[j], 0, 0, 0);
+                const v4i32_t cmh = mh, cmn = mn, cmr = mr, cma0 = ma[0], cma1 = ma[AW - 1];
+                if (t + 1 < t1) load_tile(t + 1);
+                // Branch-free test of one (point i, query column j) pair.
+                auto pass = [&](int j, int i) {
+                    bool ok = acc[j][i] >= tp[j];
+                    if constexpr (FILTER) {
+                        const uint32_t x0 = uint32_t(cma0[i]);
+                        ok &= clamp16(x0, blo[j][0], bhi[j][0]) == x0;
+                        if (AW > 1) {
+                            const uint32_t x1 = uint32_t(cma1[i]);
+                            ok &= clamp16(x1, blo[j][AW - 1], bhi[j][AW - 1]) == x1;
+                        }
+                    }
+                    return ok;
+                };
+                bool anyl = false;   // lane-mask OR: no per-pair ballot
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (pass(j, i)) {
-                            const uint32_t ql = 16u * j + col;
-                            const int32_t v = cmn[i] - 2 * (acc[j][i] - cmh[i]);
-                            const uint32_t slot = atomicAdd(&cnt[ql], 1u);
-                            buf[ql * kBfBufQ + slot] = (uint64_t(uint32_t(v)) << 32) | uint32_t(cmr[i]);
-                            full |= slot + 1u >= kBfDrainAt;
-                        }
-                if (__builtin_amdgcn_ballot_w64(full)) drain();
+                    for (int i = 0; i < 4; ++i) anyl |= pass(j, i);
+                if (__builtin_amdgcn_ballot_w64(anyl)) {
+                    // Append: the owner adds |q'|^2 to nx - 2 q'.x' later.
+                    bool full = false;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (pass(j, i)) {
+                                const uint32_t ql = 16u * j + col;
+                                const int32_t v = cmn[i] - 2 * (acc[j][i] - cmh[i]);
+                                const uint32_t slot = atomicAdd(&cnt[ql], 1u);
+                                buf[ql * kBfBufQ + slot] = (uint64_t(uint32_t(v)) << 32) | uint32_t(cmr[i]);
+                                full |= slot + 1u >= kBfDrainAt;
+                            }
+                    if (__builtin_amdgcn_ballot_w64(full)) drain();
+                }
             }
-        }
+        };
+        if (it.inside) tiles(std::false_type{});
+        else tiles(std::true_type{});
         drain();
         if (own_live) {
             // The query's bound is read at item start and lowered at item end:
@@ -1814,7 +1848,7 @@ __global__ __launch_bounds__(64) void k_tile_i8(const T* vec, uint32_t D, const 
         n += __shfl_xor(n, 16, 64);
         n += __shfl_xor(n, 32, 64);
         if (lane < 16) {
-            tnorm[size_t(t) * 32u + col] = -(n >> 1);
+            tnorm[size_t(t) * 32u + col] = valid ? -(n >> 1) : kPadSeed;
             tnorm[size_t(t) * 32u + 16u + col] = n;
         }
         return;
@@ -1833,7 +1867,7 @@ __global__ __launch_bounds__(64) void k_tile_i8(const T* vec, uint32_t D, const 
                 const int32_t v = int32_t(vec[size_t(row) * D + k]) - 128;
                 n += v * v;
             }
-        tnorm[size_t(t) * 32u + col] = -(n >> 1);
+        tnorm[size_t(t) * 32u + col] = valid ? -(n >> 1) : kPadSeed;
         tnorm[size_t(t) * 32u + 16u + col] = n;
     }
 }
@@ -1987,12 +2021,12 @@ hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bstart, const uint32_t* stile, uint32_t tch,
-                          uint32_t NS, uint32_t* icnt, uint32_t* ioff, BfItem* items, uint32_t* nitems,
+hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, const uint32_t* stile,
+                          uint32_t tch, uint32_t NS, uint32_t* icnt, uint32_t* ioff, BfItem* items, uint32_t* nitems,
                           const uint32_t* ok, bool fill, hipStream_t st) {
     if (!NS) return hipSuccess;
-    hipLaunchKernelGGL(k_bfitems, dim3((NS + 255) / 256), dim3(256), 0, st, bcnt, bstart, stile, tch, NS, icnt, ioff,
-                       items, nitems, ok, fill);
+    hipLaunchKernelGGL(k_bfitems, dim3((NS + 255) / 256), dim3(256), 0, st, bcnt, bin, bstart, stile, tch, NS, icnt,
+                       ioff, items, nitems, ok, fill);
     return hipGetLastError();
 }
 

@@ -225,7 +225,7 @@ struct gf_batch {
     DevBuf<int32_t> nq;
     // brute-force schedule of stage C (tot: device totals and fit flags)
     DevBuf<uint32_t> tot;
-    DevBuf<uint32_t> bcnt, bstart, pcnt, bq, nsub, part_off, icnt, ioff, bfq;
+    DevBuf<uint32_t> bcnt, bin, bstart, pcnt, bq, nsub, part_off, icnt, ioff, bfq;
     DevBuf<gf::BfItem> items;
     DevBuf<uint64_t> part;
     DevBuf<unsigned long long> stats;

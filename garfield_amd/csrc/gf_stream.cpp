@@ -306,7 +306,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     const bool gemm = S.i8 && b.i8 && K <= kBfKMax;
     if (gemm) {
         const uint32_t NS = std::max(S.NSmax, 1u);
-        if (b.bcnt.n < NS) { b.bcnt.alloc(NS); b.bstart.alloc(NS); b.icnt.alloc(NS); b.ioff.alloc(NS); }
+        if (b.bcnt.n < NS) { b.bcnt.alloc(NS); b.bin.alloc(NS); b.bstart.alloc(NS); b.icnt.alloc(NS); b.ioff.alloc(NS); }
         if (b.nsub.n < Q) { b.nsub.alloc(Q); b.part_off.alloc(Q); b.pcnt.alloc(Q); b.gbound.alloc(Q); }
         if (!b.bq.n) b.bq.alloc(size_t(Q) * 64);
         if (b.part.n < b.bq.n * K) b.part.alloc(b.bq.n * K);
@@ -341,7 +341,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         BfSchedArgs sc{};
         sc.sa = sa;
         sc.Q = Q; sc.postfilter = 0xFFFFFFFFu; sc.counts = b.scount.p; sc.little = b.slittle.p;
-        sc.lo = b.lo.p; sc.hi = b.hi.p; sc.nsub = b.nsub.p; sc.bcnt = b.bcnt.p; sc.bstart = b.bstart.p;
+        sc.lo = b.lo.p; sc.hi = b.hi.p; sc.nsub = b.nsub.p; sc.bcnt = b.bcnt.p; sc.bin = b.bin.p; sc.bstart = b.bstart.p;
         sc.bq = b.bq.p; sc.ok = tot + 3; sc.nbf = tot + 9; sc.bfm = b.bfmask.p; sc.bP = sb.B;
         sc.qlist = b.sched.p; sc.qrange = tot + 14;
         // a batch holds few, small sub-cells: items of kStreamTileChunk tiles
@@ -358,10 +358,10 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         GF_HIP(hipMemsetAsync(tot + 4, 0, sizeof(uint32_t), st));
         if (sb.NS) {
             GF_HIP(launch_bfsched(sc, true, st));
-            GF_HIP(launch_bfitems(b.bcnt.p, b.bstart.p, sa.stile, kStreamTileChunk, sb.NS, b.icnt.p, b.ioff.p,
+            GF_HIP(launch_bfitems(b.bcnt.p, b.bin.p, b.bstart.p, sa.stile, kStreamTileChunk, sb.NS, b.icnt.p, b.ioff.p,
                                   b.items.p, tot + 4, tot + 3, false, st));
             GF_HIP(launch_scan_small(b.icnt.p, sb.NS, b.ioff.p, st));
-            GF_HIP(launch_bfitems(b.bcnt.p, b.bstart.p, sa.stile, kStreamTileChunk, sb.NS, b.icnt.p, b.ioff.p,
+            GF_HIP(launch_bfitems(b.bcnt.p, b.bin.p, b.bstart.p, sa.stile, kStreamTileChunk, sb.NS, b.icnt.p, b.ioff.p,
                                   b.items.p, tot + 4, tot + 3, true, st));
         }
         BfGemmArgs ga{};

@@ -83,6 +83,8 @@ typedef struct {
     uint32_t vec_dtype;
     float f2h_factor;
     uint64_t device_bytes;         /* device memory held by the index */
+    uint32_t streamed;             /* 1: a streamed (out-of-core) index */
+    uint32_t nbatch;               /* streamed: batches of its plan */
 } gf_index_info;
 
 /* Loaders: load_data (tools.cuh:85-106), get_graph_info (check.cu:406-484),

@@ -218,11 +218,14 @@ def test_stream_batches_match_oracle(world_stream, L, thr, per, K):
     _print_case("stream-batches", L=L, thr=thr, per=per, K=K)
     P = ix["P"]
     plan = _shuffled_plan(P, per, seed=L)
+    import garfield_amd as gf
     sx = gl.Index.create_streamed(*_args(ix), plan=plan)
+    assert sx.streamed and sx.nbatch == len(plan)
     b = sx.batch(cfg["queries"], cfg["lo"], cfg["hi"])
-    b.mark_cells_grid(AMIN, WIDTH, thr)
+    gf.intersection_area_mark_little_seg_batch_process(b, AMIN, WIDTH, thr)
     flags = b.get_cell_flags()
-    ids, dists, st = b.search(L=L, K=K, rl=10)
+    ids, dists, st = gf.batch_graph_search_gpu_with_prefilter_batch_process_compressed_graph_T_dataset_resident_u8(
+        b, L, K=K)
     ctr = b.get_counters()
     assert 0 < st.n_batches <= len(plan) and st.bytes_h2d > 0
     assert st.bf_mfma == (K <= 16)
