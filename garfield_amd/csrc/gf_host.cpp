@@ -407,6 +407,36 @@ void entry_points_ref(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
     gf::entry_points_draw(rand_max, R * 10, R, out);
 }
 
+// Exact selectivity counts of the batch's ranges (prefiltering_tag_elements,
+// real_dataset_adapter.cuh:346-383): sub-cells inside a range count whole,
+// partially covered ones are scanned; without sub-cells, per-cell tiles.
+void count_selectivity(gf_batch& b, hipStream_t st) {
+    gf_index* ix = b.ix;
+    GF_HIP(hipMemsetAsync(b.selcount.p, 0, b.Q * sizeof(uint32_t), st));
+    if (ix->sub) {
+        gf::SubSelArgs sl{};
+        sl.sa = sub_args(*ix);
+        sl.Q = b.Q; sl.lo = b.lo.p; sl.hi = b.hi.p; sl.selcount = b.selcount.p;
+        GF_HIP(gf::launch_subsel(sl, st));
+    } else {
+        GF_HIP(hipMemsetAsync(b.ccount.p, 0, ix->P * sizeof(uint32_t), st));
+        GF_HIP(hipMemsetAsync(b.cfill.p, 0, ix->P * sizeof(uint32_t), st));
+        GF_HIP(gf::launch_cellq_count(b.Q, ix->P, b.cells.p, b.counts.p, b.ccount.p, st));
+        GF_HIP(gf::launch_scan_small(b.ccount.p, ix->P, b.cstart.p, st));
+        GF_HIP(gf::launch_cellq_fill(b.Q, ix->P, b.cells.p, b.counts.p, b.cstart.p, b.cfill.p, b.cellq.p, st));
+        GF_HIP(gf::launch_selcount(ix->ntiles, ix->tile_cell.p, ix->tile_row0.p, ix->tile_n.p, ix->attrs.p, ix->a,
+                                   b.cstart.p, b.ccount.p, b.cellq.p, b.lo.p, b.hi.p, b.selcount.p, st));
+    }
+}
+
+// The exact counts, when gf_mark_cells skipped them.
+void ensure_selcount(gf_batch& b) {
+    if (b.sel_exact) return;
+    count_selectivity(b, b.ix->stream);
+    GF_HIP(hipStreamSynchronize(b.ix->stream));
+    b.sel_exact = true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -589,23 +619,15 @@ gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms) {
         Timer t(st);
         GF_HIP(gf::launch_cells(b->Q, ix->a, b->lo.p, b->hi.p, ix->grid.p, ix->doff.p, ix->l_q.p, ix->r_q.p, ix->P,
                                 ix->offset.p, b->cells.p, b->counts.p, st));
-        GF_HIP(hipMemsetAsync(b->selcount.p, 0, b->Q * sizeof(uint32_t), st));
-        if (ix->sub) {
-            // Sub-cells inside a range count whole; partially covered ones are
-            // scanned exactly.
-            gf::SubSelArgs sl{};
-            sl.sa = sub_args(*ix);
-            sl.Q = b->Q; sl.lo = b->lo.p; sl.hi = b->hi.p; sl.selcount = b->selcount.p;
-            GF_HIP(gf::launch_subsel(sl, st));
+        if (prefilter >= 1.0f) {
+            // count / N <= prefilter holds for every count: every query is
+            // routed to the brute force without counting (the routing is the
+            // reference's); the exact counts are made when they are asked for.
+            GF_HIP(hipMemsetAsync(b->selcount.p, 0, b->Q * sizeof(uint32_t), st));
+            b->sel_exact = false;
         } else {
-            GF_HIP(hipMemsetAsync(b->ccount.p, 0, ix->P * sizeof(uint32_t), st));
-            GF_HIP(hipMemsetAsync(b->cfill.p, 0, ix->P * sizeof(uint32_t), st));
-            GF_HIP(gf::launch_cellq_count(b->Q, ix->P, b->cells.p, b->counts.p, b->ccount.p, st));
-            GF_HIP(gf::launch_scan_small(b->ccount.p, ix->P, b->cstart.p, st));
-            GF_HIP(gf::launch_cellq_fill(b->Q, ix->P, b->cells.p, b->counts.p, b->cstart.p, b->cfill.p, b->cellq.p,
-                                         st));
-            GF_HIP(gf::launch_selcount(ix->ntiles, ix->tile_cell.p, ix->tile_row0.p, ix->tile_n.p, ix->attrs.p, ix->a,
-                                       b->cstart.p, b->ccount.p, b->cellq.p, b->lo.p, b->hi.p, b->selcount.p, st));
+            count_selectivity(*b, st);
+            b->sel_exact = true;
         }
         GF_HIP(gf::launch_route(b->Q, ix->N, prefilter, b->selcount.p, b->counts.p, b->little.p, st));
         const double el = t.stop();
@@ -637,6 +659,7 @@ gf_status gf_mark_cells_grid(gf_batch* b, const float* attr_min, const float* at
         b->marked = true;
         b->flags_ready = true;
         b->bf_all = false;
+        b->sel_exact = true;   // the arithmetic-grid stage A counts nothing: selcount stays 0
     });
 }
 
@@ -743,6 +766,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         // scheduled on the device.
         const bool gemm = ix->i8 && b->i8 && K <= gf::kBfKMax;
         const uint32_t NS = ix->NS;
+        b->pass_pending = gemm && !b->sel_exact;
         if (gemm) {
             if (!b->bcnt.n) {
                 b->bcnt.alloc(NS); b->bin.alloc(NS); b->bstart.alloc(NS); b->icnt.alloc(NS); b->ioff.alloc(NS);
@@ -899,6 +923,7 @@ gf_status gf_batch_get_cells(const gf_batch* b, uint32_t* cells, uint32_t* count
         GF_REQUIRE(b, GF_E_ARG, "null batch");
         GF_REQUIRE(b->marked, GF_E_STATE, "cells not marked");
         set_device(b->ix);
+        if (selcount) ensure_selcount(*const_cast<gf_batch*>(b));
         const size_t Q = b->Q;
         if (cells) GF_HIP(hipMemcpy(cells, b->cells.p, Q * b->ix->P * 4, hipMemcpyDeviceToHost));
         if (counts) GF_HIP(hipMemcpy(counts, b->counts.p, Q * 4, hipMemcpyDeviceToHost));
@@ -964,6 +989,16 @@ gf_status gf_batch_get_counters(const gf_batch* b, uint32_t* counters) {
         GF_REQUIRE(b->counters.p, GF_E_STATE, "gf_search has not run");
         set_device(b->ix);
         GF_HIP(hipMemcpy(counters, b->counters.p, size_t(b->Q) * GF_NCOUNTERS * 4, hipMemcpyDeviceToHost));
+        if (b->pass_pending) {
+            // the MFMA brute force reports the exact count as PASS; it was
+            // not made by gf_mark_cells: make it now
+            gf_batch* mb = const_cast<gf_batch*>(b);
+            ensure_selcount(*mb);
+            std::vector<uint32_t> sel(b->Q);
+            GF_HIP(hipMemcpy(sel.data(), b->selcount.p, size_t(b->Q) * 4, hipMemcpyDeviceToHost));
+            for (uint32_t q = 0; q < b->Q; ++q)
+                if (counters[size_t(q) * GF_NCOUNTERS + 7] == 2u) counters[size_t(q) * GF_NCOUNTERS + 6] = sel[q];
+        }
     });
 }
 

@@ -243,6 +243,11 @@ struct gf_batch {
     // (Q*P, bit 2 = a cell the query's brute force scans) restricts it.
     bool bf_all = false;
     DevBuf<uint8_t> bfmask;
+    // selcount holds the exact counts (false after gf_mark_cells with
+    // prefilter >= 1, which routes without them); pass_pending: the last
+    // search's MFMA brute force reported PASS from counts not made yet.
+    bool sel_exact = true;
+    bool pass_pending = false;
     // Streamed search: per-batch cell lists and results.
     DevBuf<uint32_t> slist, scount, slittle, s_ids, s_ctr, note, need;
     DevBuf<float> s_dist;

@@ -128,7 +128,10 @@ gf_status gf_batch_free(gf_batch* b);
 /* Stage A -- intersection_area_mark_little_seg_V2<A,T>
  * (real_dataset_adapter.cuh:388-519): the cells each range intersects and the
  * prefilter routing: a query whose exact selectivity is <= prefilter is sent
- * to filtered brute force.  ms (may be NULL) receives the device time. */
+ * to filtered brute force.  With prefilter >= 1 every query is routed there
+ * without counting (count / N <= 1 always holds); the exact counts are then
+ * made when gf_batch_get_cells asks for selcount or counters are read.
+ * ms (may be NULL) receives the device time. */
 gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms);
 
 /* Stage B -- get_partitions_access_order_V2 (gpu_graph.cu:11742-11845):
