@@ -42,6 +42,23 @@ def gaussian_unit_vectors(n, d, seed):
     return x
 
 
+def gmm_vectors(n, d, ncomp, seed, sigma=0.1):
+    """Config C4's vectors: a mixture of ncomp Gaussians (sigma around unit-norm
+    centres); returns the vectors and each point's component."""
+    rng = np.random.default_rng(seed)
+    cen = rng.standard_normal((ncomp, d))
+    cen /= np.linalg.norm(cen, axis=1, keepdims=True)
+    comp = rng.integers(0, ncomp, size=n)
+    x = (cen[comp] + sigma * rng.standard_normal((n, d))).astype(np.float32)
+    return x, comp
+
+
+def component_attrs(comp, a, seed):
+    """Config C4's attributes: 10 * component + U{0..9} on every attribute."""
+    rng = np.random.default_rng(seed)
+    return (10 * np.asarray(comp)[:, None] + rng.integers(0, 10, size=(len(comp), a))).astype(np.int32)
+
+
 def uniform_attrs(n, a, seed, hi=DOMAIN):
     rng = np.random.default_rng(seed)
     return rng.integers(0, hi, size=(n, a)).astype(np.int32)

@@ -299,6 +299,26 @@ def test_subcell_three_attributes(world_sub3, prefilter):
     _assert_same(ids, dists, ctr, oids, odist, octr, st)
 
 
+@pytest.mark.parametrize("L", [32, 100])
+def test_c4_fp16_768d_traversal(world_c4, L):
+    """768-d fp16 rows (64 lanes x 2 chunks per lane) in the reference's half
+    path with f2h_factor 1."""
+    cfg, ix = world_c4
+    _print_case("c4-traverse", L=L)
+    _assert_same(*_traversal_case(cfg, ix, L, vec_dtype=1, f2h_factor=1.0)[:6])
+
+
+def test_c4_fp16_768d_bruteforce_and_order(world_c4):
+    """The gather brute force on 768-d fp16 rows (prefilter 1: every query),
+    after the cluster-guided order of stage B on 768-d centres."""
+    cfg, ix = world_c4
+    _print_case("c4-bruteforce")
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 32, prefilter=1.0, vec_dtype=1,
+                                                             f2h_factor=1.0)
+    assert st.bf_mfma == 0 and st.q_bruteforce > 0
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+
+
 def test_index_opened_from_files(small_world, tmp_path):
     """gf_index_open on the written index files: stage A matches the oracle and
     the search gives the same bits as the index built from the arrays."""
