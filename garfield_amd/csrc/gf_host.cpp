@@ -780,8 +780,11 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             if (b->part.n < b->bq.n * K) b->part.alloc(b->bq.n * K);
             if (b->gbound.n < Q) b->gbound.alloc(Q);
         }
-        hipEvent_t evg[2];   // around the MFMA kernel alone
-        for (auto& e : evg) GF_HIP(hipEventCreate(&e));
+        // events: [0] search start, [1] after traversal, [2] end, [3..4] around the MFMA kernel alone
+        if (!b->ev[0])
+            for (auto& e : b->ev) GF_HIP(hipEventCreate(&e));
+        hipEvent_t* ev = b->ev;
+        hipEvent_t* evg = b->ev + 3;
         auto launch_gemm = [&]() {
             gf::BfSchedArgs sc{};
             sc.sa = sub_args(*ix);
@@ -833,8 +836,6 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         GF_HIP(hipMemsetAsync(b->counters.p, 0, size_t(Q) * GF_NCOUNTERS * sizeof(uint32_t), st));
         GF_HIP(gf::launch_fill_results(b->out_ids.p, b->out_dist.p, Q * K, st));
         GF_HIP(gf::launch_sched(sa, st));
-        hipEvent_t ev[3];
-        for (auto& e : ev) GF_HIP(hipEventCreate(&e));
         GF_HIP(hipEventRecord(ev[0], st));
         gf::TravArgs at = a;
         at.srange = tot + 12;
@@ -848,9 +849,30 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             GF_HIP(gf::launch_bruteforce(ix->rs, ab, Q, st));
         }
         GF_HIP(hipEventRecord(ev[2], st));
-        GF_HIP(hipEventSynchronize(ev[2]));
-        uint32_t dt[16];
-        GF_HIP(hipMemcpy(dt, tot, sizeof(dt), hipMemcpyDeviceToHost));
+
+        // Results, statistics and the schedule's totals come back through
+        // pinned staging with one synchronisation.
+        const size_t nr = size_t(Q) * K;
+        if (b->h_ids.n < nr) { b->h_ids.alloc(nr); b->h_dist.alloc(nr); }
+        if (!b->h_tot.n) { b->h_tot.alloc(16); b->h_stats.alloc(16); }
+        if (stats && b->stats.n < 16) b->stats.alloc(16);
+        auto enqueue_tail = [&]() {
+            if (stats) {
+                GF_HIP(hipMemsetAsync(b->stats.p, 0, 16 * sizeof(unsigned long long), st));
+                gf::StatsArgs sa2{};
+                sa2.Q = Q; sa2.NS = gemm ? NS : 0; sa2.counters = b->counters.p; sa2.bcnt = gemm ? b->bcnt.p : nullptr;
+                sa2.ssize = ix->ssize.p; sa2.stile = ix->stile.p; sa2.out = b->stats.p;
+                GF_HIP(gf::launch_stats(sa2, st));
+                GF_HIP(hipMemcpyAsync(b->h_stats.p, b->stats.p, 16 * sizeof(unsigned long long), hipMemcpyDeviceToHost,
+                                      st));
+            }
+            GF_HIP(hipMemcpyAsync(b->h_tot.p, tot, 16 * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+            GF_HIP(hipMemcpyAsync(b->h_ids.p, b->out_ids.p, nr * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+            if (dists) GF_HIP(hipMemcpyAsync(b->h_dist.p, b->out_dist.p, nr * sizeof(float), hipMemcpyDeviceToHost, st));
+            GF_HIP(hipStreamSynchronize(st));
+        };
+        enqueue_tail();
+        const uint32_t* dt = b->h_tot.p;
         if (gemm && !dt[3]) {
             // the pair lists outgrew their buffers: grow them and run the brute force again
             const size_t cap = size_t(dt[2]) + dt[2] / 4 + 1024;
@@ -859,29 +881,17 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             GF_HIP(hipEventRecord(ev[1], st));
             launch_gemm();
             GF_HIP(hipEventRecord(ev[2], st));
-            GF_HIP(hipEventSynchronize(ev[2]));
-            GF_HIP(hipMemcpy(dt, tot, sizeof(dt), hipMemcpyDeviceToHost));
+            enqueue_tail();
             GF_REQUIRE(dt[3], GF_E_STATE, "brute-force schedule does not fit after growing");
         }
-        float t_tr = 0, t_bf = 0, t_g = 0;
-        GF_HIP(hipEventElapsedTime(&t_tr, ev[0], ev[1]));
-        GF_HIP(hipEventElapsedTime(&t_bf, ev[1], ev[2]));
-        if (gemm) GF_HIP(hipEventElapsedTime(&t_g, evg[0], evg[1]));
-        for (auto& e : ev) (void)hipEventDestroy(e);
-        for (auto& e : evg) (void)hipEventDestroy(e);
-
-        GF_HIP(hipMemcpy(ids, b->out_ids.p, size_t(Q) * K * sizeof(uint32_t), hipMemcpyDeviceToHost));
-        if (dists) GF_HIP(hipMemcpy(dists, b->out_dist.p, size_t(Q) * K * sizeof(float), hipMemcpyDeviceToHost));
+        std::memcpy(ids, b->h_ids.p, nr * sizeof(uint32_t));
+        if (dists) std::memcpy(dists, b->h_dist.p, nr * sizeof(float));
         if (stats) {
-            if (b->stats.n < 16) b->stats.alloc(16);
-            GF_HIP(hipMemsetAsync(b->stats.p, 0, 16 * sizeof(unsigned long long), st));
-            gf::StatsArgs sa2{};
-            sa2.Q = Q; sa2.NS = gemm ? NS : 0; sa2.counters = b->counters.p; sa2.bcnt = gemm ? b->bcnt.p : nullptr;
-            sa2.ssize = ix->ssize.p; sa2.stile = ix->stile.p; sa2.out = b->stats.p;
-            GF_HIP(gf::launch_stats(sa2, st));
-            unsigned long long sm[16];
-            GF_HIP(hipMemcpyAsync(sm, b->stats.p, sizeof(sm), hipMemcpyDeviceToHost, st));
-            GF_HIP(hipStreamSynchronize(st));
+            float t_tr = 0, t_bf = 0, t_g = 0;
+            GF_HIP(hipEventElapsedTime(&t_tr, ev[0], ev[1]));
+            GF_HIP(hipEventElapsedTime(&t_bf, ev[1], ev[2]));
+            if (gemm) GF_HIP(hipEventElapsedTime(&t_g, evg[0], evg[1]));
+            const unsigned long long* sm = b->h_stats.p;
             std::memset(stats, 0, sizeof(*stats));
             stats->ms_traverse = t_tr;
             stats->ms_bruteforce = t_bf;

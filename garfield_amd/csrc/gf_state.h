@@ -251,6 +251,14 @@ struct gf_batch {
     // Streamed search: per-batch cell lists and results.
     DevBuf<uint32_t> slist, scount, slittle, s_ids, s_ctr, note, need;
     DevBuf<float> s_dist;
+    // pinned staging of a resident search's results and its events
+    gf::PinBuf<uint32_t> h_ids, h_tot;
+    gf::PinBuf<float> h_dist;
+    gf::PinBuf<unsigned long long> h_stats;
+    hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+    ~gf_batch() {
+        for (auto& e : ev) if (e) (void)hipEventDestroy(e);
+    }
 };
 
 
