@@ -772,12 +772,8 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 b->bcnt.alloc(NS); b->bin.alloc(NS); b->bstart.alloc(NS); b->icnt.alloc(NS); b->ioff.alloc(NS);
                 b->nsub.alloc(Q); b->part_off.alloc(Q); b->pcnt.alloc(Q);
             }
-            if (!b->bq.n) {
-                const size_t cap = size_t(Q) * 64;
-                b->bq.alloc(cap); b->part.alloc(cap * K);
-                b->items.alloc(cap / gf::kBfQB + NS + 1);
-            }
-            if (b->part.n < b->bq.n * K) b->part.alloc(b->bq.n * K);
+            if (!b->part.n) b->alloc_pairs(size_t(Q) * 64, K, Q, NS, 0);
+            if (b->part.n < b->pair_cap * K) b->part.alloc(b->pair_cap * K);
             if (b->gbound.n < Q) b->gbound.alloc(Q);
         }
         // events: [0] search start, [1] after traversal, [2] end, [3..4] around the MFMA kernel alone
@@ -790,7 +786,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             sc.sa = sub_args(*ix);
             sc.Q = Q; sc.postfilter = opts->postfilter; sc.counts = b->counts.p;
             sc.little = b->little.p; sc.lo = b->lo.p; sc.hi = b->hi.p; sc.nsub = b->nsub.p; sc.bcnt = b->bcnt.p; sc.bin = b->bin.p;
-            sc.bstart = b->bstart.p; sc.bq = b->bq.p;
+            sc.bstart = b->bstart.p; sc.bq = b->bq.p; sc.qcap = b->qcap;
             sc.ok = tot + 3; sc.nbf = tot + 9;
             sc.qlist = b->sched.p; sc.qrange = tot + 14;   // the brute-force queries of the schedule
             if (!b->bf_all) {
@@ -801,16 +797,16 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             }
             GF_HIP(gf::launch_bf_reset(Q, b->nsub.p, b->pcnt.p, b->gbound.p, st));
             GF_HIP(gf::launch_bfsched(sc, false, st));
-            GF_HIP(gf::launch_scan_small(b->bcnt.p, NS, b->bstart.p, st));
+            if (!b->qcap) GF_HIP(gf::launch_scan_small(b->bcnt.p, NS, b->bstart.p, st));
             GF_HIP(gf::launch_scan_small(b->nsub.p, Q, b->part_off.p, st));
-            GF_HIP(gf::launch_total(b->nsub.p, b->part_off.p, Q, uint32_t(std::min<size_t>(b->bq.n, UINT32_MAX)), K,
+            GF_HIP(gf::launch_total(b->nsub.p, b->part_off.p, Q, uint32_t(std::min<size_t>(b->pair_cap, UINT32_MAX)), K,
                                     b->part.n, tot + 2, st));
-            GF_HIP(gf::launch_bfsched(sc, true, st));
-            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p, b->items.p,
-                                      tot + 4, tot + 3, false, st));
+            if (!b->qcap) GF_HIP(gf::launch_bfsched(sc, true, st));
+            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, b->qcap, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p,
+                                      b->items.p, tot + 4, tot + 3, false, st));
             GF_HIP(gf::launch_scan_small(b->icnt.p, NS, b->ioff.p, st));
-            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p, b->items.p,
-                                      tot + 4, tot + 3, true, st));
+            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, b->qcap, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p,
+                                      b->items.p, tot + 4, tot + 3, true, st));
             gf::BfGemmArgs ga{};
             ga.sa = sub_args(*ix);
             ga.vt = ix->vt.p; ga.tnorm = ix->tnorm.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p;
@@ -861,6 +857,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 GF_HIP(hipMemsetAsync(b->stats.p, 0, 16 * sizeof(unsigned long long), st));
                 gf::StatsArgs sa2{};
                 sa2.Q = Q; sa2.NS = gemm ? NS : 0; sa2.counters = b->counters.p; sa2.bcnt = gemm ? b->bcnt.p : nullptr;
+                sa2.bin = b->bin.p; sa2.split = b->qcap != 0;
                 sa2.ssize = ix->ssize.p; sa2.stile = ix->stile.p; sa2.out = b->stats.p;
                 GF_HIP(gf::launch_stats(sa2, st));
                 GF_HIP(hipMemcpyAsync(b->h_stats.p, b->stats.p, 16 * sizeof(unsigned long long), hipMemcpyDeviceToHost,
@@ -875,9 +872,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         const uint32_t* dt = b->h_tot.p;
         if (gemm && !dt[3]) {
             // the pair lists outgrew their buffers: grow them and run the brute force again
-            const size_t cap = size_t(dt[2]) + dt[2] / 4 + 1024;
-            b->bq.alloc(cap); b->part.alloc(cap * K);
-            b->items.alloc(cap / gf::kBfQB + NS + 1);
+            b->alloc_pairs(size_t(dt[2]) + dt[2] / 4 + 1024, K, Q, NS, 0);
             GF_HIP(hipEventRecord(ev[1], st));
             launch_gemm();
             GF_HIP(hipEventRecord(ev[2], st));

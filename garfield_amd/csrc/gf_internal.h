@@ -92,6 +92,7 @@ struct SubArgs {
 constexpr uint32_t kBfTile = 16;      // points per tile
 constexpr uint32_t kBfKMax = 16;      // largest K of the MFMA route
 constexpr uint32_t kBfQB = 64;        // queries per work item
+constexpr size_t kDirectListMax = size_t(64) << 20;   // NS x Q bound of one-pass sub-cell lists (256 MiB)
 struct BfItem {
     uint32_t sub, qbase, nq;           // sub-cell, first entry of its query list, queries
     uint32_t tb, te;                   // tiles [tb, te) of the sub-cell
@@ -170,6 +171,10 @@ struct BfSchedArgs {
     // Items cover at most tch tiles of a sub-cell (0: the whole sub-cell);
     // nsub counts a pair once per such chunk, each of which appends <= K keys.
     uint32_t tch;
+    // > 0: one pass writes each sub-cell's list into bq[s * qcap, (s + 1) * qcap)
+    // (inside queries from the front, partial ones from the back); 0: count
+    // and fill passes at the scan bstart of bcnt.
+    uint32_t qcap;
 };
 // Query schedule (gpu_graph.cu:12485-12493): traversal queries by descending
 // cell count, then brute-force queries.  tot[0..2] = traversal, brute-force,
@@ -190,6 +195,8 @@ struct StatsArgs {
     uint32_t Q, NS;
     const uint32_t* counters;
     const uint32_t* bcnt;      // null without the MFMA schedule
+    const uint32_t* bin;       // inside queries of each list, counted apart when split
+    bool split;                // items group inside and partial queries separately
     const uint32_t* ssize;
     const uint32_t* stile;
     unsigned long long* out;   // zeroed before
@@ -208,9 +215,9 @@ hipError_t launch_tile_i8(const void* vec_cm, bool u8, uint32_t D, const uint32_
 hipError_t launch_note_bf(const uint32_t* tot, uint32_t* note, hipStream_t st);
 hipError_t launch_subsel(const SubSelArgs& a, hipStream_t st);
 hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st);
-hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, const uint32_t* stile,
-                          uint32_t tch, uint32_t NS, uint32_t* icnt, uint32_t* ioff, BfItem* items, uint32_t* nitems,
-                          const uint32_t* ok, bool fill, hipStream_t st);
+hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, uint32_t qcap,
+                          const uint32_t* stile, uint32_t tch, uint32_t NS, uint32_t* icnt, uint32_t* ioff,
+                          BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill, hipStream_t st);
 // out[0] = start[n-1] + cnt[n-1] (total of an exclusive scan); out[1] = out[0] <= cap
 // (with cap2 != 0 also out[0] * mul <= cap2).
 hipError_t launch_sched(const SchedArgs& a, hipStream_t st);

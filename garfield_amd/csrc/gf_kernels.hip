@@ -1357,9 +1357,10 @@ __global__ __launch_bounds__(256) void k_subsel(SubSelArgs p) {
 // Stage C schedule, one workgroup per sub-cell over all queries: the
 // brute-force queries (not traversed, little > 0) whose range reaches the
 // sub-cell, in query order starting at a chunk that depends on the sub-cell
-// (spreading the per-query atomics of concurrent workgroups).  Pass 1 counts
-// per sub-cell and per query; pass 2 writes the lists at their scanned
-// offsets in the same order.
+// (spreading the per-query atomics of concurrent workgroups).  With qcap > 0
+// the count pass also writes each list into the sub-cell's own region of bq;
+// else pass 1 counts per sub-cell and per query and pass 2 writes the lists
+// at their scanned offsets in the same order.
 // Items per (query, sub-cell) pair: the sub-cell's tiles in chunks of tch
 // (0: one item).
 __device__ __forceinline__ uint32_t tile_chunks(const uint32_t* stile, uint32_t s, uint32_t tch) {
@@ -1378,7 +1379,11 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
         return;
     }
     const SubBox box = load_box(sa, s);
-    const uint32_t base = fill ? p.bstart[s] : 0u;
+    // direct (qcap > 0): one pass writes the list into the sub-cell's own
+    // region of qcap entries, inside queries from its front, partial ones
+    // from its back; else the fill pass writes at the scanned offsets.
+    const bool direct = p.qcap != 0u;
+    const uint32_t base = direct ? s * p.qcap : (fill ? p.bstart[s] : 0u);
     const uint32_t nch_s = tile_chunks(sa.stile, s, p.tch);   // items per (query, sub-cell) pair
     // A sub-cell's list holds the queries whose range contains its whole box
     // first (their items skip the range test), then the partial ones.
@@ -1419,9 +1424,12 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
             tp += wcnt[1][w];
         }
         if (rel) {
-            if (!fill) {
-                fq[fn + (rel == 2u ? oi + lanes_below(mi) : ti + op + lanes_below(mp))] = q;
-            } else {
+            if (!fill) fq[fn + (rel == 2u ? oi + lanes_below(mi) : ti + op + lanes_below(mp))] = q;
+            if (direct) {
+                const uint32_t pos = rel == 2u ? run_in + oi + lanes_below(mi)
+                                               : p.qcap - 1u - (run_p + op + lanes_below(mp));
+                p.bq[base + pos] = q;
+            } else if (fill) {
                 const uint32_t pos = rel == 2u ? run_in + oi + lanes_below(mi) : nin + run_p + op + lanes_below(mp);
                 p.bq[base + pos] = q;
             }
@@ -1500,38 +1508,51 @@ __global__ __launch_bounds__(256) void k_stats(StatsArgs p) {
         const uint32_t n = p.bcnt[i];
         if (n) {
             atomicAdd(&acc[9], (unsigned long long)n * p.ssize[i]);
-            atomicAdd(&acc[10], (unsigned long long)((n + kBfQB - 1) / kBfQB) * (p.stile[i + 1] - p.stile[i]));
+            const uint32_t ni = p.split ? p.bin[i] : 0u;
+            const uint32_t nb = (ni + kBfQB - 1) / kBfQB + (n - ni + kBfQB - 1) / kBfQB;
+            atomicAdd(&acc[10], (unsigned long long)nb * (p.stile[i + 1] - p.stile[i]));
         }
     }
     __syncthreads();
     if (tid < 11 && acc[tid]) atomicAdd(&p.out[tid], acc[tid]);
 }
 
-// Work items of the MFMA brute force: ceil(n / 64) blocks per sub-cell.
 // Work items of the MFMA brute force: per sub-cell, its query list in groups
 // of 64, times its tiles in chunks of tch (0: one chunk).
-__global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, const uint32_t* stile,
-                          uint32_t tch, uint32_t NS, uint32_t* icnt, const uint32_t* ioff, BfItem* items,
-                          uint32_t* nitems, const uint32_t* ok, bool fill) {
+__global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, uint32_t qcap,
+                          const uint32_t* stile, uint32_t tch, uint32_t NS, uint32_t* icnt, const uint32_t* ioff,
+                          BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= NS) return;
     if (fill && !*ok) {
         if (s == NS - 1) *nitems = 0;
         return;
     }
-    const uint32_t n = bcnt[s], nb = (n + kBfQB - 1) / kBfQB;
+    const uint32_t n = bcnt[s], ni = bin[s];
+    // direct lists (qcap > 0): inside and partial queries are separate runs,
+    // grouped by 64 each; else one run whose first ni entries are inside
+    const uint32_t gi = qcap ? (ni + kBfQB - 1) / kBfQB : 0u;
+    const uint32_t gp = qcap ? (n - ni + kBfQB - 1) / kBfQB : (n + kBfQB - 1) / kBfQB;
     const uint32_t nc = n ? tile_chunks(stile, s, tch) : 0u;
-    if (!fill) { icnt[s] = nb * nc; return; }
+    if (!fill) { icnt[s] = (gi + gp) * nc; return; }
     const uint32_t t0 = stile[s], t1 = stile[s + 1], step = tch ? tch : (t1 - t0);
     uint32_t k = ioff[s];
     for (uint32_t c = 0; c < nc; ++c) {
         const uint32_t tb = t0 + c * step, te = min(t1, tb + step);
-        for (uint32_t b = 0; b < nb; ++b) {
-            const uint32_t m = min(kBfQB, n - b * kBfQB);
-            items[k++] = BfItem{s, bstart[s] + b * kBfQB, m, tb, te, b * kBfQB + m <= bin[s] ? 1u : 0u};
+        if (qcap) {
+            const uint32_t np = n - ni;
+            for (uint32_t b = 0; b < gi; ++b)
+                items[k++] = BfItem{s, s * qcap + b * kBfQB, min(kBfQB, ni - b * kBfQB), tb, te, 1u};
+            for (uint32_t b = 0; b < gp; ++b)
+                items[k++] = BfItem{s, s * qcap + qcap - np + b * kBfQB, min(kBfQB, np - b * kBfQB), tb, te, 0u};
+        } else {
+            for (uint32_t b = 0; b < gp; ++b) {
+                const uint32_t m = min(kBfQB, n - b * kBfQB);
+                items[k++] = BfItem{s, bstart[s] + b * kBfQB, m, tb, te, b * kBfQB + m <= ni ? 1u : 0u};
+            }
         }
     }
-    if (s == NS - 1) *nitems = ioff[s] + nb * nc;
+    if (s == NS - 1) *nitems = ioff[s] + (gi + gp) * nc;
 }
 
 // out[0] = start[n-1] + cnt[n-1], the total of an exclusive scan; out[1] =
@@ -2021,12 +2042,12 @@ hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, const uint32_t* stile,
-                          uint32_t tch, uint32_t NS, uint32_t* icnt, uint32_t* ioff, BfItem* items, uint32_t* nitems,
-                          const uint32_t* ok, bool fill, hipStream_t st) {
+hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, uint32_t qcap,
+                          const uint32_t* stile, uint32_t tch, uint32_t NS, uint32_t* icnt, uint32_t* ioff,
+                          BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill, hipStream_t st) {
     if (!NS) return hipSuccess;
-    hipLaunchKernelGGL(k_bfitems, dim3((NS + 255) / 256), dim3(256), 0, st, bcnt, bin, bstart, stile, tch, NS, icnt,
-                       ioff, items, nitems, ok, fill);
+    hipLaunchKernelGGL(k_bfitems, dim3((NS + 255) / 256), dim3(256), 0, st, bcnt, bin, bstart, qcap, stile, tch, NS,
+                       icnt, ioff, items, nitems, ok, fill);
     return hipGetLastError();
 }
 

@@ -228,6 +228,23 @@ struct gf_batch {
     DevBuf<uint32_t> bcnt, bin, bstart, pcnt, bq, nsub, part_off, icnt, ioff, bfq;
     DevBuf<gf::BfItem> items;
     DevBuf<uint64_t> part;
+    // Capacity of the schedule in (query, sub-cell) pairs (part holds K
+    // partial results per pair) and, when NS x Q lists fit, the capacity of
+    // each sub-cell's own list (qcap = Q: k_bfsched fills the lists in one
+    // pass); qcap = 0 selects the count-scan-fill scheme with bq of pair_cap.
+    size_t pair_cap = 0;
+    uint32_t qcap = 0;
+    // slots: (sub-cell, tile chunk) combinations, bounding the items beyond
+    // one per 64 pairs.
+    void alloc_pairs(size_t pairs, uint32_t K, uint32_t Q, uint32_t NS, size_t slots) {
+        const bool direct = size_t(NS) * Q <= gf::kDirectListMax;
+        qcap = direct ? Q : 0u;
+        pair_cap = pairs;
+        const size_t nbq = direct ? size_t(NS) * Q : pairs;
+        if (bq.n < nbq) bq.alloc(nbq);
+        part.alloc(pairs * K);
+        items.alloc(pairs / gf::kBfQB + (direct ? 2 : 1) * slots + 2);
+    }
     DevBuf<unsigned long long> stats;
     DevBuf<float> qf32, qnorm, lo, hi, cdist, out_dist;
     DevBuf<uint16_t> q16, q16v;

@@ -308,11 +308,9 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         const uint32_t NS = std::max(S.NSmax, 1u);
         if (b.bcnt.n < NS) { b.bcnt.alloc(NS); b.bin.alloc(NS); b.bstart.alloc(NS); b.icnt.alloc(NS); b.ioff.alloc(NS); }
         if (b.nsub.n < Q) { b.nsub.alloc(Q); b.part_off.alloc(Q); b.pcnt.alloc(Q); b.gbound.alloc(Q); }
-        if (!b.bq.n) b.bq.alloc(size_t(Q) * 64);
-        if (b.part.n < b.bq.n * K) b.part.alloc(b.bq.n * K);
-        // items <= pairs x chunks / 64 + chunks of all sub-cells (k_bfitems)
-        const size_t ni = b.bq.n / kBfQB + S.tmax / kStreamTileChunk + NS + 2;
-        if (b.items.n < ni) b.items.alloc(ni);
+        // items <= pairs x chunks / 64 + (sub-cell, chunk) slots (k_bfitems)
+        if (!b.part.n) b.alloc_pairs(size_t(Q) * 64, K, Q, NS, S.tmax / kStreamTileChunk + NS);
+        if (b.part.n < b.pair_cap * K) b.part.alloc(b.pair_cap * K);
         if (b.bfmask.n < size_t(Q) * Bm) b.bfmask.alloc(size_t(Q) * Bm);
         if (b.note.n < 2 * std::max<size_t>(nb, 1)) b.note.alloc(2 * std::max<size_t>(nb, 1));
     }
@@ -342,7 +340,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         sc.sa = sa;
         sc.Q = Q; sc.postfilter = 0xFFFFFFFFu; sc.counts = b.scount.p; sc.little = b.slittle.p;
         sc.lo = b.lo.p; sc.hi = b.hi.p; sc.nsub = b.nsub.p; sc.bcnt = b.bcnt.p; sc.bin = b.bin.p; sc.bstart = b.bstart.p;
-        sc.bq = b.bq.p; sc.ok = tot + 3; sc.nbf = tot + 9; sc.bfm = b.bfmask.p; sc.bP = sb.B;
+        sc.bq = b.bq.p; sc.qcap = b.qcap; sc.ok = tot + 3; sc.nbf = tot + 9; sc.bfm = b.bfmask.p; sc.bP = sb.B;
         sc.qlist = b.sched.p; sc.qrange = tot + 14;
         // a batch holds few, small sub-cells: items of kStreamTileChunk tiles
         // give the persistent kernel enough of them to fill the GPU
@@ -350,19 +348,19 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         GF_HIP(launch_bf_reset(Q, b.nsub.p, b.pcnt.p, b.gbound.p, st));
         if (sb.NS) {
             GF_HIP(launch_bfsched(sc, false, st));
-            GF_HIP(launch_scan_small(b.bcnt.p, sb.NS, b.bstart.p, st));
+            if (!b.qcap) GF_HIP(launch_scan_small(b.bcnt.p, sb.NS, b.bstart.p, st));
         }
         GF_HIP(launch_scan_small(b.nsub.p, Q, b.part_off.p, st));
-        GF_HIP(launch_total(b.nsub.p, b.part_off.p, Q, uint32_t(std::min<size_t>(b.bq.n, UINT32_MAX)), K, b.part.n,
+        GF_HIP(launch_total(b.nsub.p, b.part_off.p, Q, uint32_t(std::min<size_t>(b.pair_cap, UINT32_MAX)), K, b.part.n,
                             tot + 2, st));
         GF_HIP(hipMemsetAsync(tot + 4, 0, sizeof(uint32_t), st));
         if (sb.NS) {
-            GF_HIP(launch_bfsched(sc, true, st));
-            GF_HIP(launch_bfitems(b.bcnt.p, b.bin.p, b.bstart.p, sa.stile, kStreamTileChunk, sb.NS, b.icnt.p, b.ioff.p,
-                                  b.items.p, tot + 4, tot + 3, false, st));
+            if (!b.qcap) GF_HIP(launch_bfsched(sc, true, st));
+            GF_HIP(launch_bfitems(b.bcnt.p, b.bin.p, b.bstart.p, b.qcap, sa.stile, kStreamTileChunk, sb.NS, b.icnt.p,
+                                  b.ioff.p, b.items.p, tot + 4, tot + 3, false, st));
             GF_HIP(launch_scan_small(b.icnt.p, sb.NS, b.ioff.p, st));
-            GF_HIP(launch_bfitems(b.bcnt.p, b.bin.p, b.bstart.p, sa.stile, kStreamTileChunk, sb.NS, b.icnt.p, b.ioff.p,
-                                  b.items.p, tot + 4, tot + 3, true, st));
+            GF_HIP(launch_bfitems(b.bcnt.p, b.bin.p, b.bstart.p, b.qcap, sa.stile, kStreamTileChunk, sb.NS, b.icnt.p,
+                                  b.ioff.p, b.items.p, tot + 4, tot + 3, true, st));
         }
         BfGemmArgs ga{};
         ga.sa = sa;
@@ -479,10 +477,8 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         for (size_t bi = 0; bi < nb; ++bi)
             if (!note[2 * bi]) need = std::max<size_t>(need, note[2 * bi + 1]);
         if (need) {
-            const size_t cap = need + need / 4 + 1024;
             const uint32_t NS = std::max(S.NSmax, 1u);
-            b.bq.alloc(cap); b.part.alloc(cap * K);
-            b.items.alloc(cap / kBfQB + S.tmax / kStreamTileChunk + NS + 2);
+            b.alloc_pairs(need + need / 4 + 1024, K, Q, NS, S.tmax / kStreamTileChunk + NS);
             for (size_t bi = 0; bi < nb; ++bi)
                 if (!note[2 * bi]) {
                     enqueue_copy(bi, 0, S.batches[bi].bytes_mfma);
