@@ -772,7 +772,9 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 b->bcnt.alloc(NS); b->bin.alloc(NS); b->bstart.alloc(NS); b->icnt.alloc(NS); b->ioff.alloc(NS);
                 b->nsub.alloc(Q); b->part_off.alloc(Q); b->pcnt.alloc(Q);
             }
-            if (!b->part.n) b->alloc_pairs(size_t(Q) * 64, K, Q, NS, 0);
+            if (!b->part.n) b->alloc_pairs(size_t(Q) * 64, K, Q, NS, NS);
+            if (b->seed.n < Q) b->seed.alloc(Q);
+            if (b->scnt.n < NS) { b->scnt.alloc(NS); b->sitems.alloc(size_t(Q) / gf::kBfQB + NS + 1); }
             if (b->part.n < b->pair_cap * K) b->part.alloc(b->pair_cap * K);
             if (b->gbound.n < Q) b->gbound.alloc(Q);
         }
@@ -795,7 +797,20 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 sc.bfm = b->bfmask.p;
                 sc.bP = ix->P;
             }
-            GF_HIP(gf::launch_bf_reset(Q, b->nsub.p, b->pcnt.p, b->gbound.p, st));
+            // Seeds (one-pass lists): each query's best-filled sub-cell runs first.
+            const bool seeds = b->qcap != 0;
+            GF_HIP(gf::launch_bf_reset(Q, b->nsub.p, b->pcnt.p, b->gbound.p, st, seeds ? NS : 0,
+                                       seeds ? b->scnt.p : nullptr, seeds ? tot + 5 : nullptr));
+            if (seeds) {
+                gf::BfSeedArgs sd{};
+                sd.sa = sc.sa; sd.postfilter = sc.postfilter; sd.counts = sc.counts; sd.little = sc.little;
+                sd.cells = b->cells.p; sd.lo = sc.lo; sd.hi = sc.hi; sd.bfm = sc.bfm; sd.bP = sc.bP;
+                sd.qlist = sc.qlist; sd.qrange = sc.qrange; sd.qcap = b->qcap; sd.tch = 0;
+                sd.seed = b->seed.p; sd.scnt = b->scnt.p; sd.bq = b->bq.p; sd.nsub = b->nsub.p;
+                GF_HIP(gf::launch_bfseed(sd, Q, st));
+                sc.seed = b->seed.p;
+                sc.scnt = b->scnt.p;
+            }
             GF_HIP(gf::launch_bfsched(sc, false, st));
             if (!b->qcap) GF_HIP(gf::launch_scan_small(b->bcnt.p, NS, b->bstart.p, st));
             GF_HIP(gf::launch_scan_small(b->nsub.p, Q, b->part_off.p, st));
@@ -805,14 +820,17 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, b->qcap, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p,
                                       b->items.p, tot + 4, tot + 3, false, st));
             GF_HIP(gf::launch_scan_small(b->icnt.p, NS, b->ioff.p, st));
+            const uint32_t scap = uint32_t(b->sitems.n);
             GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, b->qcap, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p,
-                                      b->items.p, tot + 4, tot + 3, true, st));
+                                      b->items.p, tot + 4, tot + 3, true, st, seeds ? b->scnt.p : nullptr,
+                                      b->sitems.p, tot + 5, scap));
             gf::BfGemmArgs ga{};
             ga.sa = sub_args(*ix);
             ga.vt = ix->vt.p; ga.tnorm = ix->tnorm.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p;
             ga.hi = b->hi.p; ga.items = b->items.p; ga.nitems = tot + 4; ga.bq = b->bq.p; ga.pcnt = b->pcnt.p;
             ga.part_off = b->part_off.p; ga.part = b->part.p; ga.gbound = b->gbound.p;
             ga.ok = tot + 3;
+            if (seeds) { ga.sitems = b->sitems.p; ga.nseed = tot + 5; ga.nseed_cap = scap; }
             ga.K = K; ga.D = ix->D;
             GF_HIP(hipEventRecord(evg[0], st));
             GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu) * 3u, st));
@@ -857,7 +875,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 GF_HIP(hipMemsetAsync(b->stats.p, 0, 16 * sizeof(unsigned long long), st));
                 gf::StatsArgs sa2{};
                 sa2.Q = Q; sa2.NS = gemm ? NS : 0; sa2.counters = b->counters.p; sa2.bcnt = gemm ? b->bcnt.p : nullptr;
-                sa2.bin = b->bin.p; sa2.split = b->qcap != 0;
+                sa2.bin = b->bin.p; sa2.split = b->qcap != 0; sa2.sseed = b->qcap ? b->scnt.p : nullptr;
                 sa2.ssize = ix->ssize.p; sa2.stile = ix->stile.p; sa2.out = b->stats.p;
                 GF_HIP(gf::launch_stats(sa2, st));
                 GF_HIP(hipMemcpyAsync(b->h_stats.p, b->stats.p, 16 * sizeof(unsigned long long), hipMemcpyDeviceToHost,

@@ -114,6 +114,11 @@ struct BfGemmArgs {
     uint64_t* part;            // partial keys: (d << 32) | row
     uint32_t* gbound;          // per query: smallest K-th distance of any item so far
     const uint32_t* ok;        // schedule fits its buffers (else the kernel does nothing)
+    // Optional seed items (null: none), run before every other item so that
+    // each query's bound is set from one well-filled sub-cell early.
+    const BfItem* sitems;
+    const uint32_t* nseed;     // device count of seed items
+    uint32_t nseed_cap;        // capacity of sitems
     uint32_t K, D;
 };
 struct BfFinalArgs {
@@ -175,6 +180,34 @@ struct BfSchedArgs {
     // (inside queries from the front, partial ones from the back); 0: count
     // and fill passes at the scan bstart of bcnt.
     uint32_t qcap;
+    // Optional (one-pass lists only): per query its seed sub-cell (k_bfseed),
+    // whose pair is listed, counted and run as a seed item instead; per
+    // sub-cell the seeds at the front of its region, before the inside run.
+    const uint32_t* seed;
+    const uint32_t* scnt;
+};
+
+// Seed choice (one-pass lists only): per brute-force query, the sub-cell its
+// brute force reaches that holds the most points of its range (whole
+// sub-cells by size, partial ones by box overlap), listed at the front of
+// that sub-cell's region and counted in nsub.
+struct BfSeedArgs {
+    SubArgs sa;
+    uint32_t postfilter;
+    const uint32_t* counts;
+    const uint32_t* little;
+    const uint32_t* cells;     // Q x P cell lists
+    const float* lo;
+    const float* hi;
+    const uint8_t* bfm;        // as BfSchedArgs
+    uint32_t bP;
+    const uint32_t* qlist;
+    const uint32_t* qrange;
+    uint32_t qcap, tch;
+    uint32_t* seed;
+    uint32_t* scnt;            // zeroed before
+    uint32_t* bq;
+    uint32_t* nsub;
 };
 // Query schedule (gpu_graph.cu:12485-12493): traversal queries by descending
 // cell count, then brute-force queries.  tot[0..2] = traversal, brute-force,
@@ -196,6 +229,7 @@ struct StatsArgs {
     const uint32_t* counters;
     const uint32_t* bcnt;      // null without the MFMA schedule
     const uint32_t* bin;       // inside queries of each list, counted apart when split
+    const uint32_t* sseed;     // seed queries of each sub-cell (null: none)
     bool split;                // items group inside and partial queries separately
     const uint32_t* ssize;
     const uint32_t* stile;
@@ -217,7 +251,10 @@ hipError_t launch_subsel(const SubSelArgs& a, hipStream_t st);
 hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st);
 hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, uint32_t qcap,
                           const uint32_t* stile, uint32_t tch, uint32_t NS, uint32_t* icnt, uint32_t* ioff,
-                          BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill, hipStream_t st);
+                          BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill, hipStream_t st,
+                          const uint32_t* scnt = nullptr, BfItem* sitems = nullptr, uint32_t* nseed = nullptr,
+                          uint32_t scap = 0);
+hipError_t launch_bfseed(const BfSeedArgs& a, uint32_t Q, hipStream_t st);
 // out[0] = start[n-1] + cnt[n-1] (total of an exclusive scan); out[1] = out[0] <= cap
 // (with cap2 != 0 also out[0] * mul <= cap2).
 hipError_t launch_sched(const SchedArgs& a, hipStream_t st);
@@ -255,7 +292,8 @@ hipError_t launch_cell_flags(uint32_t Q, uint32_t P, const uint32_t* cells, cons
                              const uint32_t* little, uint8_t* flags, hipStream_t st);
 hipError_t launch_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_t* bcell, const uint8_t* flags,
                                uint32_t* lists, uint32_t* counts, uint32_t* little, hipStream_t st);
-hipError_t launch_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t* gbound, hipStream_t st);
+hipError_t launch_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t* gbound, hipStream_t st,
+                          uint32_t NS = 0, uint32_t* scnt = nullptr, uint32_t* nseed = nullptr);
 hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, hipStream_t st);
 hipError_t launch_batch_need(uint32_t Q, uint32_t P, uint32_t nbatch, const uint32_t* plan_cells,
                              const uint32_t* plan_off, const uint8_t* flags, uint32_t* need, hipStream_t st);

@@ -969,8 +969,11 @@ __global__ void k_zero_u32(uint32_t* x, uint32_t n) {
 
 // Per-query state of the MFMA brute-force schedule, reset in one pass:
 // pairs and appended keys zeroed, bounds open.
-__global__ void k_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t* gbound) {
+__global__ void k_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t* gbound, uint32_t NS, uint32_t* scnt,
+                           uint32_t* nseed) {
     const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (scnt && q < NS) scnt[q] = 0;
+    if (nseed && q == 0) *nseed = 0;
     if (q >= Q) return;
     nsub[q] = 0;
     pcnt[q] = 0;
@@ -1368,6 +1371,62 @@ __device__ __forceinline__ uint32_t tile_chunks(const uint32_t* stile, uint32_t 
     return tch ? (nt + tch - 1) / tch : 1u;
 }
 
+// Seed choice, one wave per candidate query (see BfSeedArgs).  The same
+// route, mask and relation tests as k_bfsched pick among the sub-cells of the
+// query's listed cells; a score of points in range (whole sub-cells by size,
+// partial ones by size x box overlap per attribute) decides, ties to the
+// lowest sub-cell.
+__global__ __launch_bounds__(256) void k_bfseed(BfSeedArgs p) {
+    const SubArgs& sa = p.sa;
+    const uint32_t lane = lane_id();
+    const uint32_t q0 = p.qrange[0], nq = p.qrange[1] - q0;
+    const uint32_t ci = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (ci >= nq) return;
+    const uint32_t q = p.qlist[q0 + ci];
+    const uint32_t cnt = p.counts[q], lit = p.little[q];
+    uint64_t key = 0;   // (score bits << 32) | ~sub-cell: the largest wins
+    if (!(cnt < p.postfilter && cnt != lit) && lit > 0) {
+        const QRange r = load_range(sa.a, p.lo, p.hi, q);
+        for (uint32_t i = 0; i < cnt; ++i) {
+            const uint32_t c = p.cells[size_t(q) * sa.P + i];
+            if (p.bfm && !(p.bfm[size_t(q) * p.bP + c] & 2u)) continue;
+            for (uint32_t s = sa.sbase[c] + lane; s < sa.sbase[c + 1]; s += 64u) {
+                const uint32_t n = sa.ssize[s];
+                if (!n) continue;
+                const SubBox b = load_box(sa, s);
+                const uint32_t rel = sub_relation(b, sa.a, r);
+                if (!rel) continue;
+                float sc = float(n);
+                if (rel == 1u) {
+#pragma unroll
+                    for (uint32_t d = 0; d < 4; ++d)
+                        if (d < sa.a) {
+                            const float ov = fminf(r.h[d], b.mx[d]) - fmaxf(r.l[d], b.mn[d]) + 1.0f;
+                            sc *= fminf(1.0f, fmaxf(ov, 1.0f) / (b.mx[d] - b.mn[d] + 1.0f));
+                        }
+                }
+                const uint64_t k = (uint64_t(__float_as_uint(sc)) << 32) | (0xFFFFFFFFu - s);
+                key = k > key ? k : key;
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t o = 32; o; o >>= 1) {
+        const uint64_t other = (uint64_t(uint32_t(__shfl_xor(int(key >> 32), int(o)))) << 32) |
+                               uint32_t(__shfl_xor(int(uint32_t(key)), int(o)));
+        key = other > key ? other : key;
+    }
+    if (lane == 0) {
+        const uint32_t s = key ? 0xFFFFFFFFu - uint32_t(key) : kEmpty;
+        p.seed[q] = s;
+        if (s != kEmpty) {
+            const uint32_t slot = atomicAdd(&p.scnt[s], 1u);
+            p.bq[size_t(s) * p.qcap + slot] = q;
+            atomicAdd(&p.nsub[q], tile_chunks(sa.stile, s, p.tch));
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
     __shared__ uint32_t wcnt[2][4];
     __shared__ uint32_t fq[kFlushCap];
@@ -1384,6 +1443,7 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
     // from its back; else the fill pass writes at the scanned offsets.
     const bool direct = p.qcap != 0u;
     const uint32_t base = direct ? s * p.qcap : (fill ? p.bstart[s] : 0u);
+    const uint32_t nseed = direct && p.scnt ? p.scnt[s] : 0u;   // seeds hold the front of the region
     const uint32_t nch_s = tile_chunks(sa.stile, s, p.tch);   // items per (query, sub-cell) pair
     // A sub-cell's list holds the queries whose range contains its whole box
     // first (their items skip the range test), then the partial ones.
@@ -1405,7 +1465,8 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
         if (q < p.Q) {
             const uint32_t cnt = p.counts[q], lit = p.little[q];
             const bool trav = cnt < p.postfilter && cnt != lit;
-            if (!trav && lit > 0 && (!p.bfm || (p.bfm[size_t(q) * p.bP + sa.scell[s]] & 2u)))
+            if (!trav && lit > 0 && (!p.bfm || (p.bfm[size_t(q) * p.bP + sa.scell[s]] & 2u)) &&
+                !(p.seed && p.seed[q] == s))
                 rel = sub_relation(box, sa.a, load_range(sa.a, p.lo, p.hi, q));
         }
         const uint64_t mi = __builtin_amdgcn_ballot_w64(rel == 2u);
@@ -1426,7 +1487,7 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
         if (rel) {
             if (!fill) fq[fn + (rel == 2u ? oi + lanes_below(mi) : ti + op + lanes_below(mp))] = q;
             if (direct) {
-                const uint32_t pos = rel == 2u ? run_in + oi + lanes_below(mi)
+                const uint32_t pos = rel == 2u ? nseed + run_in + oi + lanes_below(mi)
                                                : p.qcap - 1u - (run_p + op + lanes_below(mp));
                 p.bq[base + pos] = q;
             } else if (fill) {
@@ -1505,11 +1566,12 @@ __global__ __launch_bounds__(256) void k_stats(StatsArgs p) {
         if (c[C_ROUTE] == 2) atomicAdd(&acc[8], (unsigned long long)c[C_DIST]);
     }
     if (p.bcnt && i < p.NS) {
-        const uint32_t n = p.bcnt[i];
+        const uint32_t ns = p.sseed ? p.sseed[i] : 0u, n = p.bcnt[i] + ns;
         if (n) {
             atomicAdd(&acc[9], (unsigned long long)n * p.ssize[i]);
             const uint32_t ni = p.split ? p.bin[i] : 0u;
-            const uint32_t nb = (ni + kBfQB - 1) / kBfQB + (n - ni + kBfQB - 1) / kBfQB;
+            const uint32_t nb = (ns + kBfQB - 1) / kBfQB + (ni + kBfQB - 1) / kBfQB +
+                                (n - ns - ni + kBfQB - 1) / kBfQB;
             atomicAdd(&acc[10], (unsigned long long)nb * (p.stile[i + 1] - p.stile[i]));
         }
     }
@@ -1521,12 +1583,25 @@ __global__ __launch_bounds__(256) void k_stats(StatsArgs p) {
 // of 64, times its tiles in chunks of tch (0: one chunk).
 __global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, uint32_t qcap,
                           const uint32_t* stile, uint32_t tch, uint32_t NS, uint32_t* icnt, const uint32_t* ioff,
-                          BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill) {
+                          BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill, const uint32_t* scnt,
+                          BfItem* sitems, uint32_t* nseed, uint32_t scap) {
     const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
     if (s >= NS) return;
     if (fill && !*ok) {
         if (s == NS - 1) *nitems = 0;
         return;
+    }
+    const uint32_t ns = qcap && scnt ? scnt[s] : 0u;   // seeds: the front of the region
+    if (fill && ns) {
+        // seed items go to their own list (order is free: each is one sub-cell)
+        const uint32_t nc = tile_chunks(stile, s, tch), gs = (ns + kBfQB - 1) / kBfQB;
+        const uint32_t t0 = stile[s], t1 = stile[s + 1], step = tch ? tch : (t1 - t0);
+        uint32_t k = atomicAdd(nseed, gs * nc);
+        for (uint32_t c = 0; c < nc; ++c) {
+            const uint32_t tb = t0 + c * step, te = min(t1, tb + step);
+            for (uint32_t b = 0; b < gs; ++b, ++k)
+                if (k < scap) sitems[k] = BfItem{s, s * qcap + b * kBfQB, min(kBfQB, ns - b * kBfQB), tb, te, 0u};
+        }
     }
     const uint32_t n = bcnt[s], ni = bin[s];
     // direct lists (qcap > 0): inside and partial queries are separate runs,
@@ -1542,7 +1617,7 @@ __global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint3
         if (qcap) {
             const uint32_t np = n - ni;
             for (uint32_t b = 0; b < gi; ++b)
-                items[k++] = BfItem{s, s * qcap + b * kBfQB, min(kBfQB, ni - b * kBfQB), tb, te, 1u};
+                items[k++] = BfItem{s, s * qcap + ns + b * kBfQB, min(kBfQB, ni - b * kBfQB), tb, te, 1u};
             for (uint32_t b = 0; b < gp; ++b)
                 items[k++] = BfItem{s, s * qcap + qcap - np + b * kBfQB, min(kBfQB, np - b * kBfQB), tb, te, 0u};
         } else {
@@ -1596,8 +1671,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3
     const uint32_t col = lane & 15u, grp = lane >> 4;
     constexpr uint32_t MW = 16u * (1u + AW);
 
-    for (uint32_t item_id = i_lo + k8 * 4u + wave; item_id < i_hi; item_id += nwg_x * 4u) {
-        const BfItem it = p.items[item_id];
+    // Seed items first (strided over every wave of the grid), then the XCD's
+    // range of the item list.
+    const uint32_t n_seed = p.sitems && *p.ok ? min(*p.nseed, p.nseed_cap) : 0u;
+    uint32_t seed_id = blockIdx.x * 4u + wave, item_id = i_lo + k8 * 4u + wave;
+    for (;;) {
+        BfItem it;
+        if (seed_id < n_seed) {
+            it = p.sitems[seed_id];
+            seed_id += nwg * 4u;
+        } else if (item_id < i_hi) {
+            it = p.items[item_id];
+            item_id += nwg_x * 4u;
+        } else {
+            break;
+        }
         const uint32_t s = it.sub, cell = sa.scell[s];
         const uint32_t t0 = it.tb, t1 = it.te;
 
@@ -2044,10 +2132,12 @@ hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st) {
 
 hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, uint32_t qcap,
                           const uint32_t* stile, uint32_t tch, uint32_t NS, uint32_t* icnt, uint32_t* ioff,
-                          BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill, hipStream_t st) {
+                          BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill, hipStream_t st,
+                          const uint32_t* scnt, BfItem* sitems, uint32_t* nseed, uint32_t scap) {
     if (!NS) return hipSuccess;
+    if (scnt && (!sitems || !nseed)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_bfitems, dim3((NS + 255) / 256), dim3(256), 0, st, bcnt, bin, bstart, qcap, stile, tch, NS,
-                       icnt, ioff, items, nitems, ok, fill);
+                       icnt, ioff, items, nitems, ok, fill, scnt, sitems, nseed, scap);
     return hipGetLastError();
 }
 
@@ -2161,8 +2251,16 @@ hipError_t launch_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_
     return hipGetLastError();
 }
 
-hipError_t launch_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t* gbound, hipStream_t st) {
-    hipLaunchKernelGGL(k_bf_reset, dim3((Q + 255) / 256), dim3(256), 0, st, Q, nsub, pcnt, gbound);
+hipError_t launch_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t* gbound, hipStream_t st, uint32_t NS,
+                          uint32_t* scnt, uint32_t* nseed) {
+    const uint32_t n = (Q > NS ? Q : NS) > 0u ? (Q > NS ? Q : NS) : 1u;
+    hipLaunchKernelGGL(k_bf_reset, dim3((n + 255) / 256), dim3(256), 0, st, Q, nsub, pcnt, gbound, NS, scnt, nseed);
+    return hipGetLastError();
+}
+
+hipError_t launch_bfseed(const BfSeedArgs& a, uint32_t Q, hipStream_t st) {
+    if (!Q || !a.qcap) return hipSuccess;
+    hipLaunchKernelGGL(k_bfseed, dim3((Q + 3) / 4), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

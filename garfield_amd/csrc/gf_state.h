@@ -234,6 +234,10 @@ struct gf_batch {
     // pass); qcap = 0 selects the count-scan-fill scheme with bq of pair_cap.
     size_t pair_cap = 0;
     uint32_t qcap = 0;
+    // Seed sub-cell per query, seeds per sub-cell and the seed items (one-pass
+    // lists of a resident index).
+    DevBuf<uint32_t> seed, scnt;
+    DevBuf<gf::BfItem> sitems;
     // slots: (sub-cell, tile chunk) combinations, bounding the items beyond
     // one per 64 pairs.
     void alloc_pairs(size_t pairs, uint32_t K, uint32_t Q, uint32_t NS, size_t slots) {
