@@ -64,7 +64,8 @@ class SearchStats(C.Structure):
                 ("n_cross", C.c_uint64), ("n_lrow", C.c_uint64), ("n_scan", C.c_uint64),
                 ("n_pass", C.c_uint64), ("bytes_traverse", C.c_double), ("bytes_bruteforce", C.c_double),
                 ("ops_bruteforce", C.c_double), ("bf_mfma", C.c_uint32), ("ms_bf_kernel", C.c_double),
-                ("n_batches", C.c_uint32), ("bytes_h2d", C.c_double), ("ms_h2d", C.c_double)]
+                ("n_batches", C.c_uint32), ("bytes_h2d", C.c_double), ("ms_h2d", C.c_double),
+                ("ms_stage_a", C.c_double), ("ms_stage_b", C.c_double)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -274,10 +275,12 @@ class Batch:
         except Exception:
             pass
 
-    def mark_cells(self, prefilter):
+    def mark_cells(self, prefilter, timed=True):
+        """Stage A; returns its device time in ms (timed=False: returns None
+        without waiting for the stage; the search statistics report it)."""
         ms = C.c_double()
-        _check(load().gf_mark_cells(self._h, float(prefilter), C.byref(ms)))
-        return ms.value
+        _check(load().gf_mark_cells(self._h, float(prefilter), C.byref(ms) if timed else None))
+        return ms.value if timed else None
 
     def mark_cells_grid(self, attr_min, attr_width, threshold):
         amin = _c(attr_min, np.float32)
@@ -291,11 +294,12 @@ class Batch:
         _check(load().gf_batch_get_cell_flags(self._h, _ptr(f)))
         return f
 
-    def order_cells(self, topc=4):
+    def order_cells(self, topc=4, timed=True):
+        """Stage B; returns its device time in ms (timed=False: as mark_cells)."""
         ms = C.c_double()
-        _check(load().gf_order_cells(self._h, int(topc), C.byref(ms)))
+        _check(load().gf_order_cells(self._h, int(topc), C.byref(ms) if timed else None))
         self._topc = topc
-        return ms.value
+        return ms.value if timed else None
 
     def search(self, L, K=10, rl=10, postfilter=1 << 30, entry_points=None):
         ids = np.empty((self.Q, K), np.uint32)

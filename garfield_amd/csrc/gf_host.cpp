@@ -34,7 +34,6 @@ gf_status run_guarded(const std::function<void()>& fn);
 }  // namespace
 
 using gf::DevBuf;
-using gf::Timer;
 using gf::round_up;
 using gf::set_device;
 
@@ -616,7 +615,7 @@ gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms) {
         b->bf_all = true;
         set_device(ix);
         hipStream_t st = ix->stream;
-        Timer t(st);
+        b->stage_event(0, st);
         GF_HIP(gf::launch_cells(b->Q, ix->a, b->lo.p, b->hi.p, ix->grid.p, ix->doff.p, ix->l_q.p, ix->r_q.p, ix->P,
                                 ix->offset.p, b->cells.p, b->counts.p, st));
         if (prefilter >= 1.0f) {
@@ -630,8 +629,9 @@ gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms) {
             b->sel_exact = true;
         }
         GF_HIP(gf::launch_route(b->Q, ix->N, prefilter, b->selcount.p, b->counts.p, b->little.p, st));
-        const double el = t.stop();
-        if (ms) *ms = el;
+        b->stage_event(1, st);
+        b->sev_a = true;
+        if (ms) *ms = b->stage_ms(0);
         b->marked = true;
     });
 }
@@ -650,11 +650,14 @@ gf_status gf_mark_cells_grid(gf_batch* b, const float* attr_min, const float* at
         DevBuf<float> amin, width;
         amin.upload(attr_min, ix->a);
         width.upload(attr_width, ix->a);
-        Timer t(st);
+        b->stage_event(0, st);
         GF_HIP(gf::launch_cells_grid(b->Q, ix->a, b->lo.p, b->hi.p, amin.p, width.p, ix->grid.p, ix->P, ix->offset.p,
                                      threshold, b->cells.p, b->counts.p, b->little.p, b->flags.p, st));
         GF_HIP(hipMemsetAsync(b->selcount.p, 0, b->Q * sizeof(uint32_t), st));
-        const double el = t.stop();
+        b->stage_event(1, st);
+        b->sev_a = true;
+        // amin and width are freed on return: their reads must be done first
+        const double el = b->stage_ms(0);
         if (ms) *ms = el;
         b->marked = true;
         b->flags_ready = true;
@@ -670,18 +673,19 @@ gf_status gf_order_cells(gf_batch* b, uint32_t topc, double* ms) {
         GF_REQUIRE(topc >= 1 && topc <= 16, GF_E_ARG, "topc must be in [1, 16]");
         gf_index* ix = b->ix;
         set_device(ix);
-        if (!ix->C) { if (ms) *ms = 0.0; return; }
+        if (!ix->C) { if (ms) *ms = 0.0; b->sev_b = false; return; }
         hipStream_t st = ix->stream;
         if (!b->cdist.p) b->cdist.alloc(size_t(b->Q) * ix->C);
         b->topk.alloc(size_t(b->Q) * topc);
         b->topc = topc;
-        Timer t(st);
+        b->stage_event(2, st);
         GF_HIP(gf::launch_centroid(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp, ix->Cp,
                                    ix->Dp, b->cdist.p, st));
         GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, b->cdist.p, ix->hist.p, b->cells.p, b->counts.p,
                                 b->topk.p, st));
-        const double el = t.stop();
-        if (ms) *ms = el;
+        b->stage_event(3, st);
+        b->sev_b = true;
+        if (ms) *ms = b->stage_ms(2);
     });
 }
 
@@ -696,8 +700,16 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         GF_REQUIRE(K >= 1 && K <= 64, GF_E_ARG, "K must be in [1, 64]");
         GF_REQUIRE(rl >= 1 && rl <= 16, GF_E_ARG, "rl must be in [1, 16]");
         set_device(ix);
+        // Device times of the latest stage calls (their events precede the
+        // search on the stream, which the search has waited for).
+        auto stage_times = [&]() {
+            if (!stats) return;
+            stats->ms_stage_a = b->sev_a ? b->stage_ms(0) : 0.0;
+            stats->ms_stage_b = b->sev_b ? b->stage_ms(2) : 0.0;
+        };
         if (ix->sx) {
             gf::stream_search(*b, *opts, ids, dists, stats);
+            stage_times();
             return;
         }
         hipStream_t st = ix->stream;
@@ -773,8 +785,14 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 b->nsub.alloc(Q); b->part_off.alloc(Q); b->pcnt.alloc(Q);
             }
             if (!b->part.n) b->alloc_pairs(size_t(Q) * 64, K, Q, NS, NS);
-            if (b->seed.n < Q) b->seed.alloc(Q);
-            if (b->scnt.n < NS) { b->scnt.alloc(NS); b->sitems.alloc(size_t(Q) / gf::kBfQB + NS + 1); }
+            if (b->rq.n < Q) {
+                b->rq.alloc(Q); b->rseed.alloc(Q);
+                b->rlo.alloc(size_t(Q) * ix->a); b->rhi.alloc(size_t(Q) * ix->a);
+            }
+            if (b->scnt.n < NS) {
+                b->scnt.alloc(NS);
+                b->sitems.alloc(size_t(Q) / gf::kBfQB + NS + 1);
+            }
             if (b->part.n < b->pair_cap * K) b->part.alloc(b->pair_cap * K);
             if (b->gbound.n < Q) b->gbound.alloc(Q);
         }
@@ -803,13 +821,14 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                                        seeds ? b->scnt.p : nullptr, seeds ? tot + 5 : nullptr));
             if (seeds) {
                 gf::BfSeedArgs sd{};
-                sd.sa = sc.sa; sd.postfilter = sc.postfilter; sd.counts = sc.counts; sd.little = sc.little;
+                sd.sa = sc.sa; sd.Q = Q; sd.postfilter = sc.postfilter; sd.counts = sc.counts; sd.little = sc.little;
                 sd.cells = b->cells.p; sd.lo = sc.lo; sd.hi = sc.hi; sd.bfm = sc.bfm; sd.bP = sc.bP;
                 sd.qlist = sc.qlist; sd.qrange = sc.qrange; sd.qcap = b->qcap; sd.tch = 0;
-                sd.seed = b->seed.p; sd.scnt = b->scnt.p; sd.bq = b->bq.p; sd.nsub = b->nsub.p;
+                sd.scnt = b->scnt.p; sd.bq = b->bq.p; sd.nsub = b->nsub.p;
+                sd.rq = b->rq.p; sd.rseed = b->rseed.p; sd.rlo = b->rlo.p; sd.rhi = b->rhi.p;
                 GF_HIP(gf::launch_bfseed(sd, Q, st));
-                sc.seed = b->seed.p;
                 sc.scnt = b->scnt.p;
+                sc.rq = b->rq.p; sc.rseed = b->rseed.p; sc.rlo = b->rlo.p; sc.rhi = b->rhi.p;
             }
             GF_HIP(gf::launch_bfsched(sc, false, st));
             if (!b->qcap) GF_HIP(gf::launch_scan_small(b->bcnt.p, NS, b->bstart.p, st));
@@ -836,7 +855,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu) * 3u, st));
             GF_HIP(hipEventRecord(evg[1], st));
             gf::BfFinalArgs fa{};
-            fa.bfq = b->sched.p; fa.srange = tot + 14; fa.part_off = b->part_off.p; fa.pcnt = b->pcnt.p;
+            fa.gbound = b->gbound.p; fa.bfq = b->sched.p; fa.srange = tot + 14; fa.part_off = b->part_off.p; fa.pcnt = b->pcnt.p;
             fa.ok = tot + 3; fa.part = b->part.p; fa.counts = b->counts.p; fa.cells = b->cells.p;
             fa.offset = ix->offset.p; fa.selcount = b->selcount.p; fa.gidx = ix->gidx.p; fa.out_ids = b->out_ids.p;
             fa.out_dist = b->out_dist.p; fa.counters = b->counters.p; fa.K = K; fa.P = ix->P;
@@ -936,6 +955,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 stats->ops_bruteforce = 3.0 * b_dist * ix->D;
                 stats->bf_mfma = 0;
             }
+            stage_times();
         }
     });
 }

@@ -122,6 +122,7 @@ struct BfGemmArgs {
     uint32_t K, D;
 };
 struct BfFinalArgs {
+    const uint32_t* gbound;    // optional: per query the bound the items reached
     const uint32_t* bfq;       // schedule
     const uint32_t* srange;    // device [begin, end) of the brute-force queries in bfq
     const uint32_t* part_off;  // per query: first pair (partial area = pairs * K keys)
@@ -180,20 +181,26 @@ struct BfSchedArgs {
     // (inside queries from the front, partial ones from the back); 0: count
     // and fill passes at the scan bstart of bcnt.
     uint32_t qcap;
-    // Optional (one-pass lists only): per query its seed sub-cell (k_bfseed),
-    // whose pair is listed, counted and run as a seed item instead; per
-    // sub-cell the seeds at the front of its region, before the inside run.
-    const uint32_t* seed;
+    // Optional (one-pass lists with qlist): the candidate records k_bfseed
+    // writes for candidate index ci: its query (kEmpty: not on the
+    // brute-force route), seed sub-cell (whose pair is listed, counted and run
+    // as a seed item instead) and range (rlo / rhi: attribute d at d * Q + ci);
+    // per sub-cell the seeds at the front of its region (scnt).
+    const uint32_t* rq;
+    const uint32_t* rseed;
+    const float* rlo;
+    const float* rhi;
     const uint32_t* scnt;
 };
 
 // Seed choice (one-pass lists only): per brute-force query, the sub-cell its
 // brute force reaches that holds the most points of its range (whole
 // sub-cells by size, partial ones by box overlap), listed at the front of
-// that sub-cell's region and counted in nsub.
+// that sub-cell's region and counted in nsub; also the candidate records
+// k_bfsched reads.
 struct BfSeedArgs {
     SubArgs sa;
-    uint32_t postfilter;
+    uint32_t Q, postfilter;
     const uint32_t* counts;
     const uint32_t* little;
     const uint32_t* cells;     // Q x P cell lists
@@ -204,10 +211,13 @@ struct BfSeedArgs {
     const uint32_t* qlist;
     const uint32_t* qrange;
     uint32_t qcap, tch;
-    uint32_t* seed;
     uint32_t* scnt;            // zeroed before
     uint32_t* bq;
     uint32_t* nsub;
+    uint32_t* rq;              // candidate records (BfSchedArgs), Q each
+    uint32_t* rseed;
+    float* rlo;                // a x Q
+    float* rhi;
 };
 // Query schedule (gpu_graph.cu:12485-12493): traversal queries by descending
 // cell count, then brute-force queries.  tot[0..2] = traversal, brute-force,
@@ -292,6 +302,7 @@ hipError_t launch_cell_flags(uint32_t Q, uint32_t P, const uint32_t* cells, cons
                              const uint32_t* little, uint8_t* flags, hipStream_t st);
 hipError_t launch_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_t* bcell, const uint8_t* flags,
                                uint32_t* lists, uint32_t* counts, uint32_t* little, hipStream_t st);
+// Also zeroes scnt (NS entries) and *nseed when given.
 hipError_t launch_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t* gbound, hipStream_t st,
                           uint32_t NS = 0, uint32_t* scnt = nullptr, uint32_t* nseed = nullptr);
 hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, hipStream_t st);

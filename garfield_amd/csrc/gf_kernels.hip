@@ -790,21 +790,38 @@ __global__ void k_cellq_fill(uint32_t Q, uint32_t P, const uint32_t* cells, cons
 }
 
 // Exclusive scan of a short array (n <= a few thousand) by one workgroup.
-__global__ __launch_bounds__(256) void k_scan_small(const uint32_t* in, uint32_t n, uint32_t* out) {
-    __shared__ uint32_t part[256];
-    const uint32_t t = threadIdx.x;
-    const uint32_t per = (n + 255u) / 256u;
-    uint32_t s = 0;
-    for (uint32_t i = t * per; i < (t + 1) * per && i < n; ++i) s += in[i];
-    part[t] = s;
-    __syncthreads();
-    if (t == 0) {
-        uint32_t acc = 0;
-        for (uint32_t i = 0; i < 256; ++i) { const uint32_t v = part[i]; part[i] = acc; acc += v; }
+__global__ __launch_bounds__(1024) void k_scan_small(const uint32_t* in, uint32_t n, uint32_t* out) {
+    // Chunks of 1024 elements: wave scans, then a scan of the 16 wave sums,
+    // carried across chunks.  Each chunk reads its inputs before any thread
+    // writes its outputs, so in and out may alias.
+    __shared__ uint32_t wsum[16];
+    const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+    uint32_t carry = 0;
+    for (uint32_t base = 0; base < n; base += 1024u) {
+        const uint32_t i = base + t;
+        const uint32_t v = i < n ? in[i] : 0u;
+        uint32_t x = v;
+#pragma unroll
+        for (uint32_t o = 1; o < 64u; o <<= 1) {
+            const uint32_t y = uint32_t(__shfl_up(int(x), o));
+            x += lane >= o ? y : 0u;
+        }
+        if (lane == 63u) wsum[w] = x;
+        __syncthreads();
+        if (w == 0) {
+            uint32_t z = lane < 16u ? wsum[lane] : 0u;
+#pragma unroll
+            for (uint32_t o = 1; o < 16u; o <<= 1) {
+                const uint32_t y = uint32_t(__shfl_up(int(z), o));
+                z += lane >= o ? y : 0u;
+            }
+            if (lane < 16u) wsum[lane] = z;
+        }
+        __syncthreads();
+        if (i < n) out[i] = carry + (w ? wsum[w - 1] : 0u) + x - v;
+        carry += wsum[15];
+        __syncthreads();
     }
-    __syncthreads();
-    uint32_t acc = part[t];
-    for (uint32_t i = t * per; i < (t + 1) * per && i < n; ++i) { out[i] = acc; acc += in[i]; }
 }
 
 // Exact selectivity counts (real_dataset_adapter.cuh:346-383), tiled: a tile
@@ -1174,6 +1191,14 @@ constexpr int32_t kPadSeed = INT32_MIN;
 // LDS ordering between the lanes of one wave of a multi-wave workgroup:
 // the fences stop the compiler from moving LDS accesses across this point,
 // and the wave executes its LDS instructions in order.
+// Workgroup barrier ordering LDS only: global loads in flight stay in
+// flight (a full __syncthreads waits for them).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ void wave_fence() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -1371,11 +1396,12 @@ __device__ __forceinline__ uint32_t tile_chunks(const uint32_t* stile, uint32_t 
     return tch ? (nt + tch - 1) / tch : 1u;
 }
 
-// Seed choice, one wave per candidate query (see BfSeedArgs).  The same
-// route, mask and relation tests as k_bfsched pick among the sub-cells of the
-// query's listed cells; a score of points in range (whole sub-cells by size,
-// partial ones by size x box overlap per attribute) decides, ties to the
-// lowest sub-cell.
+// Seed choice, one wave per candidate query (see BfSeedArgs): among the
+// sub-cells of the first cell of the query's list that its brute force
+// reaches (stage B puts the cell nearest the query's closest centres first),
+// the one with the most points in range, whole sub-cells by size and partial
+// ones by size x box overlap per attribute; ties go to the lowest sub-cell.
+// Also writes the candidate records and counts the seed pair in nsub.
 __global__ __launch_bounds__(256) void k_bfseed(BfSeedArgs p) {
     const SubArgs& sa = p.sa;
     const uint32_t lane = lane_id();
@@ -1384,41 +1410,47 @@ __global__ __launch_bounds__(256) void k_bfseed(BfSeedArgs p) {
     if (ci >= nq) return;
     const uint32_t q = p.qlist[q0 + ci];
     const uint32_t cnt = p.counts[q], lit = p.little[q];
+    const bool bf = !(cnt < p.postfilter && cnt != lit) && lit > 0;
+    const QRange r = load_range(sa.a, p.lo, p.hi, q);
     uint64_t key = 0;   // (score bits << 32) | ~sub-cell: the largest wins
-    if (!(cnt < p.postfilter && cnt != lit) && lit > 0) {
-        const QRange r = load_range(sa.a, p.lo, p.hi, q);
-        for (uint32_t i = 0; i < cnt; ++i) {
-            const uint32_t c = p.cells[size_t(q) * sa.P + i];
-            if (p.bfm && !(p.bfm[size_t(q) * p.bP + c] & 2u)) continue;
-            for (uint32_t s = sa.sbase[c] + lane; s < sa.sbase[c + 1]; s += 64u) {
-                const uint32_t n = sa.ssize[s];
-                if (!n) continue;
-                const SubBox b = load_box(sa, s);
-                const uint32_t rel = sub_relation(b, sa.a, r);
-                if (!rel) continue;
-                float sc = float(n);
-                if (rel == 1u) {
+    for (uint32_t i = 0; bf && i < cnt && key == 0; ++i) {
+        const uint32_t c = p.cells[size_t(q) * sa.P + i];
+        if (p.bfm && !(p.bfm[size_t(q) * p.bP + c] & 2u)) continue;
+        for (uint32_t s = sa.sbase[c] + lane; s < sa.sbase[c + 1]; s += 64u) {
+            const uint32_t n = sa.ssize[s];
+            if (!n) continue;
+            const SubBox b = load_box(sa, s);
+            const uint32_t rel = sub_relation(b, sa.a, r);
+            if (!rel) continue;
+            float sc = float(n);
+            if (rel == 1u) {
 #pragma unroll
-                    for (uint32_t d = 0; d < 4; ++d)
-                        if (d < sa.a) {
-                            const float ov = fminf(r.h[d], b.mx[d]) - fmaxf(r.l[d], b.mn[d]) + 1.0f;
-                            sc *= fminf(1.0f, fmaxf(ov, 1.0f) / (b.mx[d] - b.mn[d] + 1.0f));
-                        }
-                }
-                const uint64_t k = (uint64_t(__float_as_uint(sc)) << 32) | (0xFFFFFFFFu - s);
-                key = k > key ? k : key;
+                for (uint32_t d = 0; d < 4; ++d)
+                    if (d < sa.a) {
+                        const float ov = fminf(r.h[d], b.mx[d]) - fmaxf(r.l[d], b.mn[d]) + 1.0f;
+                        sc *= fminf(1.0f, fmaxf(ov, 1.0f) / (b.mx[d] - b.mn[d] + 1.0f));
+                    }
             }
+            const uint64_t k = (uint64_t(__float_as_uint(sc)) << 32) | (0xFFFFFFFFu - s);
+            key = k > key ? k : key;
+        }
+#pragma unroll
+        for (uint32_t o = 32; o; o >>= 1) {
+            const uint64_t other = (uint64_t(uint32_t(__shfl_xor(int(key >> 32), int(o)))) << 32) |
+                                   uint32_t(__shfl_xor(int(uint32_t(key)), int(o)));
+            key = other > key ? other : key;
         }
     }
-#pragma unroll
-    for (uint32_t o = 32; o; o >>= 1) {
-        const uint64_t other = (uint64_t(uint32_t(__shfl_xor(int(key >> 32), int(o)))) << 32) |
-                               uint32_t(__shfl_xor(int(uint32_t(key)), int(o)));
-        key = other > key ? other : key;
-    }
+    const uint32_t s = key ? 0xFFFFFFFFu - uint32_t(key) : kEmpty;
     if (lane == 0) {
-        const uint32_t s = key ? 0xFFFFFFFFu - uint32_t(key) : kEmpty;
-        p.seed[q] = s;
+#pragma unroll
+        for (uint32_t d = 0; d < 4; ++d)
+            if (d < sa.a) {
+                p.rlo[size_t(d) * p.Q + ci] = r.l[d];
+                p.rhi[size_t(d) * p.Q + ci] = r.h[d];
+            }
+        p.rq[ci] = bf ? q : kEmpty;
+        p.rseed[ci] = s;
         if (s != kEmpty) {
             const uint32_t slot = atomicAdd(&p.scnt[s], 1u);
             p.bq[size_t(s) * p.qcap + slot] = q;
@@ -1453,21 +1485,50 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
     const uint32_t q0 = p.qlist ? p.qrange[0] : 0u;
     const uint32_t nq = p.qlist ? p.qrange[1] - q0 : p.Q;
     const uint32_t nch = (nq + 255u) / 256u;
+    // With candidate records the next chunk's record is loaded while the
+    // current one is tested (one load level, no query-indexed gathers; the
+    // barriers order LDS only, so the loads stay in flight).
+    const bool recs = p.rq != nullptr;
+    uint32_t nx_q = kEmpty, nx_s = kEmpty;
+    QRange nx_r{};
+    auto fetch = [&](uint32_t ci) {
+        const uint32_t qi = ((ci + s) % nch) * 256u + tid;
+        nx_q = kEmpty;
+        if (qi < nq) {
+            nx_q = p.rq[qi];
+            nx_s = p.rseed[qi];
+#pragma unroll
+            for (uint32_t d = 0; d < 4; ++d)
+                if (d < sa.a) {
+                    nx_r.l[d] = p.rlo[size_t(d) * p.Q + qi];
+                    nx_r.h[d] = p.rhi[size_t(d) * p.Q + qi];
+                }
+        }
+    };
+    if (recs && nch) fetch(0);
     for (uint32_t ci = 0; ci < nch; ++ci) {
         if (!fill && fn + 256u > kFlushCap) {
             for (uint32_t i = tid; i < fn; i += 256u) atomicAdd(&p.nsub[fq[i]], nch_s);
-            __syncthreads();
+            lds_barrier();
             fn = 0;
         }
-        const uint32_t qi = ((ci + s) % nch) * 256u + tid;
-        const uint32_t q = qi < nq ? (p.qlist ? p.qlist[q0 + qi] : qi) : 0xFFFFFFFFu;
-        uint32_t rel = 0;
-        if (q < p.Q) {
-            const uint32_t cnt = p.counts[q], lit = p.little[q];
-            const bool trav = cnt < p.postfilter && cnt != lit;
-            if (!trav && lit > 0 && (!p.bfm || (p.bfm[size_t(q) * p.bP + sa.scell[s]] & 2u)) &&
-                !(p.seed && p.seed[q] == s))
-                rel = sub_relation(box, sa.a, load_range(sa.a, p.lo, p.hi, q));
+        uint32_t q, rel = 0;
+        if (recs) {
+            q = nx_q;
+            const uint32_t sd = nx_s;
+            const QRange r = nx_r;
+            if (ci + 1 < nch) fetch(ci + 1);
+            if (q != kEmpty && sd != s && (!p.bfm || (p.bfm[size_t(q) * p.bP + sa.scell[s]] & 2u)))
+                rel = sub_relation(box, sa.a, r);
+        } else {
+            const uint32_t qi = ((ci + s) % nch) * 256u + tid;
+            q = qi < nq ? (p.qlist ? p.qlist[q0 + qi] : qi) : 0xFFFFFFFFu;
+            if (q < p.Q) {
+                const uint32_t cnt = p.counts[q], lit = p.little[q];
+                const bool trav = cnt < p.postfilter && cnt != lit;
+                if (!trav && lit > 0 && (!p.bfm || (p.bfm[size_t(q) * p.bP + sa.scell[s]] & 2u)))
+                    rel = sub_relation(box, sa.a, load_range(sa.a, p.lo, p.hi, q));
+            }
         }
         const uint64_t mi = __builtin_amdgcn_ballot_w64(rel == 2u);
         const uint64_t mp = __builtin_amdgcn_ballot_w64(rel == 1u);
@@ -1475,7 +1536,7 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
             wcnt[0][wave] = uint32_t(__builtin_popcountll(mi));
             wcnt[1][wave] = uint32_t(__builtin_popcountll(mp));
         }
-        __syncthreads();
+        lds_barrier();
         uint32_t oi = 0, op = 0, ti = 0, tp = 0;
 #pragma unroll
         for (uint32_t w = 0; w < 4; ++w) {
@@ -1498,7 +1559,7 @@ __global__ __launch_bounds__(256) void k_bfsched(BfSchedArgs p, bool fill) {
         run_in += ti;
         run_p += tp;
         fn += ti + tp;
-        __syncthreads();
+        lds_barrier();
     }
     if (!fill) {
         for (uint32_t i = tid; i < fn; i += 256u) atomicAdd(&p.nsub[fq[i]], nch_s);
@@ -1880,10 +1941,15 @@ __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
     const uint32_t K = p.K;
     const uint32_t n = p.pcnt[q];
     const uint64_t* part = p.part + size_t(p.part_off[q]) * K;
+    // The query's final bound: some item held K keys within it, so no key
+    // beyond it reaches the top K.
+    const uint32_t g = p.gbound ? p.gbound[q] : 0xFFFFFFFFu;
+    const uint64_t cap = g == 0xFFFFFFFFu ? kKeySent : (uint64_t(g) + 1u) << 32;
     uint64_t top = kKeySent;
     for (uint32_t s0 = 0; s0 < n; s0 += 64u) {
         const uint64_t c = s0 + lane < n ? part[s0 + lane] : kKeySent;
-        const uint64_t thr = readlane64(top, K - 1);
+        const uint64_t t_k = readlane64(top, K - 1);
+        const uint64_t thr = t_k < cap ? t_k : cap;
         const bool surv = c < thr;
         const uint64_t sm = ballot(surv);
         if (!sm) continue;
@@ -1906,12 +1972,14 @@ __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
         p.out_ids[size_t(q) * K + lane] = v ? p.gidx[uint32_t(top)] : GF_NO_RESULT;
         p.out_dist[size_t(q) * K + lane] = v ? float(uint32_t(top >> 32)) : __int_as_float(0x7F800000);
     }
+    uint32_t scan = 0;
+    for (uint32_t i = lane; i < p.counts[q]; i += 64u) {
+        const uint32_t c = p.cells[size_t(q) * p.P + i];
+        scan += p.offset[c + 1] - p.offset[c];
+    }
+#pragma unroll
+    for (uint32_t o = 32; o; o >>= 1) scan += uint32_t(__shfl_xor(int(scan), int(o)));
     if (lane == 0) {
-        uint32_t scan = 0;
-        for (uint32_t i = 0; i < p.counts[q]; ++i) {
-            const uint32_t c = p.cells[size_t(q) * p.P + i];
-            scan += p.offset[c + 1] - p.offset[c];
-        }
         uint32_t* ctr = p.counters + size_t(q) * GF_NCOUNTERS;
         ctr[C_EXPAND] = 0;
         ctr[C_DIST] = scan;
@@ -2199,7 +2267,7 @@ hipError_t launch_cellq_count(uint32_t Q, uint32_t P, const uint32_t* cells, con
 }
 
 hipError_t launch_scan_small(const uint32_t* in, uint32_t n, uint32_t* out, hipStream_t st) {
-    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(256), 0, st, in, n, out);
+    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, st, in, n, out);
     return hipGetLastError();
 }
 

@@ -87,28 +87,6 @@ struct PinBuf {
     size_t bytes() const { return n * sizeof(T); }
 };
 
-struct Timer {
-    hipEvent_t a = nullptr, b = nullptr;
-    hipStream_t s;
-    explicit Timer(hipStream_t st) : s(st) {
-        GF_HIP(hipEventCreate(&a));
-        GF_HIP(hipEventCreate(&b));
-        GF_HIP(hipEventRecord(a, s));
-    }
-    double stop() {
-        GF_HIP(hipEventRecord(b, s));
-        GF_HIP(hipEventSynchronize(b));
-        float ms = 0;
-        GF_HIP(hipEventElapsedTime(&ms, a, b));
-        return ms;
-    }
-    ~Timer() {
-        if (a) (void)hipEventDestroy(a);
-        if (b) (void)hipEventDestroy(b);
-    }
-};
-
-
 // A streamed index keeps no per-point array on the device.  Its static plan
 // groups cells into batches; each batch is stored in pinned host memory as
 // one packed image that hipMemcpyAsync moves into one of two device buffers
@@ -234,9 +212,10 @@ struct gf_batch {
     // pass); qcap = 0 selects the count-scan-fill scheme with bq of pair_cap.
     size_t pair_cap = 0;
     uint32_t qcap = 0;
-    // Seed sub-cell per query, seeds per sub-cell and the seed items (one-pass
-    // lists of a resident index).
-    DevBuf<uint32_t> seed, scnt;
+    // Seed schedule of a resident index's one-pass lists: candidate records
+    // (query, seed sub-cell, range), seeds per sub-cell and the seed items.
+    DevBuf<uint32_t> scnt, rq, rseed;
+    DevBuf<float> rlo, rhi;
     DevBuf<gf::BfItem> sitems;
     // slots: (sub-cell, tile chunk) combinations, bounding the items beyond
     // one per 64 pairs.
@@ -277,8 +256,24 @@ struct gf_batch {
     gf::PinBuf<float> h_dist;
     gf::PinBuf<unsigned long long> h_stats;
     hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+    // Around the latest stage A ([0], [1]) and stage B ([2], [3]) calls.
+    hipEvent_t sev[4] = {nullptr, nullptr, nullptr, nullptr};
+    bool sev_a = false, sev_b = false;
+    // Records event i of sev (created on first use).
+    void stage_event(int i, hipStream_t st) {
+        if (!sev[i]) GF_HIP(hipEventCreate(&sev[i]));
+        GF_HIP(hipEventRecord(sev[i], st));
+    }
+    // Device time between sev[i] and sev[i + 1] (waits for the latter).
+    double stage_ms(int i) {
+        GF_HIP(hipEventSynchronize(sev[i + 1]));
+        float ms = 0;
+        GF_HIP(hipEventElapsedTime(&ms, sev[i], sev[i + 1]));
+        return ms;
+    }
     ~gf_batch() {
         for (auto& e : ev) if (e) (void)hipEventDestroy(e);
+        for (auto& e : sev) if (e) (void)hipEventDestroy(e);
     }
 };
 

@@ -371,7 +371,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         GF_HIP(launch_bf_i8(ga, uint32_t(std::max(ix.ncu, 1)) * 3u, st));
         GF_HIP(hipEventRecord(ge[2 * bi + 1], st));
         BfFinalArgs fa{};
-        fa.bfq = b.sched.p; fa.srange = tot + 14; fa.part_off = b.part_off.p; fa.pcnt = b.pcnt.p; fa.ok = tot + 3;
+        fa.gbound = b.gbound.p; fa.bfq = b.sched.p; fa.srange = tot + 14; fa.part_off = b.part_off.p; fa.pcnt = b.pcnt.p; fa.ok = tot + 3;
         fa.part = b.part.p; fa.counts = b.scount.p; fa.cells = b.slist.p;
         fa.offset = reinterpret_cast<const uint32_t*>(dev + sb.o_offset); fa.selcount = b.selcount.p;
         fa.gidx = reinterpret_cast<const uint32_t*>(dev + sb.o_gidx); fa.out_ids = b.s_ids.p;

@@ -131,7 +131,9 @@ gf_status gf_batch_free(gf_batch* b);
  * to filtered brute force.  With prefilter >= 1 every query is routed there
  * without counting (count / N <= 1 always holds); the exact counts are then
  * made when gf_batch_get_cells asks for selcount or counters are read.
- * ms (may be NULL) receives the device time. */
+ * ms (may be NULL) receives the device time; with ms NULL the call returns
+ * once the stage is enqueued, and gf_search_stats.ms_stage_a reports the
+ * device time after the search (the same holds for the other stage calls). */
 gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms);
 
 /* Stage B -- get_partitions_access_order_V2 (gpu_graph.cu:11742-11845):
@@ -181,6 +183,10 @@ typedef struct {
     uint32_t n_batches;      /* batches searched (a batch none of whose cells a query selects is skipped) */
     double bytes_h2d;        /* bytes copied host -> device (a batch no query traverses: its brute-force sections only) */
     double ms_h2d;           /* sum of the copies' device times */
+    /* device times of the batch's latest stage A (gf_mark_cells or
+       gf_mark_cells_grid) and stage B (gf_order_cells) calls; 0 if none ran */
+    double ms_stage_a;
+    double ms_stage_b;
 } gf_search_stats;
 
 gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids /*Q*K*/,
