@@ -675,14 +675,26 @@ gf_status gf_order_cells(gf_batch* b, uint32_t topc, double* ms) {
         set_device(ix);
         if (!ix->C) { if (ms) *ms = 0.0; b->sev_b = false; return; }
         hipStream_t st = ix->stream;
-        if (!b->cdist.p) b->cdist.alloc(size_t(b->Q) * ix->C);
-        b->topk.alloc(size_t(b->Q) * topc);
+        if (b->topk.n < size_t(b->Q) * topc) b->topk.alloc(size_t(b->Q) * topc);
         b->topc = topc;
         b->stage_event(2, st);
-        GF_HIP(gf::launch_centroid(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp, ix->Cp,
-                                   ix->Dp, b->cdist.p, st));
-        GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, b->cdist.p, ix->hist.p, b->cells.p, b->counts.p,
-                                b->topk.p, st));
+        if (topc <= 4) {
+            // nearest centres straight from the MFMA tiles; the distance
+            // matrix is made only if gf_batch_get_centroid asks for it
+            GF_HIP(gf::launch_centroid_top(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp,
+                                           ix->Cp, ix->Dp, topc, b->topk.p, st));
+            GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, nullptr, ix->hist.p, b->cells.p, b->counts.p,
+                                    b->topk.p, st, true));
+            b->cdist_ready = false;
+        } else {
+            if (!b->cdist.p) b->cdist.alloc(size_t(b->Q) * ix->C);
+            GF_HIP(gf::launch_centroid(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp, ix->Cp,
+                                       ix->Dp, b->cdist.p, st));
+            GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, b->cdist.p, ix->hist.p, b->cells.p, b->counts.p,
+                                    b->topk.p, st));
+            b->cdist_ready = true;
+        }
+        b->ordered = true;
         b->stage_event(3, st);
         b->sev_b = true;
         if (ms) *ms = b->stage_ms(2);
@@ -1002,9 +1014,19 @@ gf_status gf_batch_set_cells(gf_batch* b, const uint32_t* cells, const uint32_t*
 gf_status gf_batch_get_centroid(const gf_batch* b, float* dist, uint32_t* topc) {
     return run_guarded([&] {
         GF_REQUIRE(b, GF_E_ARG, "null batch");
-        GF_REQUIRE(b->cdist.p && b->topk.p, GF_E_STATE, "gf_order_cells has not run");
+        GF_REQUIRE(b->ordered, GF_E_STATE, "gf_order_cells has not run");
         set_device(b->ix);
-        if (dist) GF_HIP(hipMemcpy(dist, b->cdist.p, size_t(b->Q) * b->ix->C * 4, hipMemcpyDeviceToHost));
+        const gf_index* ix = b->ix;
+        if (dist && !b->cdist_ready) {
+            // the matrix the nearest centres were chosen from (same tiles, same rounding)
+            gf_batch* mb = const_cast<gf_batch*>(b);
+            if (!mb->cdist.p) mb->cdist.alloc(size_t(b->Q) * ix->C);
+            GF_HIP(gf::launch_centroid(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp, ix->Cp,
+                                       ix->Dp, mb->cdist.p, ix->stream));
+            GF_HIP(hipStreamSynchronize(ix->stream));
+            mb->cdist_ready = true;
+        }
+        if (dist) GF_HIP(hipMemcpy(dist, b->cdist.p, size_t(b->Q) * ix->C * 4, hipMemcpyDeviceToHost));
         if (topc) GF_HIP(hipMemcpy(topc, b->topk.p, size_t(b->Q) * b->topc * 4, hipMemcpyDeviceToHost));
     });
 }

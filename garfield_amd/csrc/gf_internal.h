@@ -314,9 +314,14 @@ hipError_t launch_merge_stream(uint32_t Q, uint32_t K, uint32_t* run_ids, float*
 hipError_t launch_centroid(const uint16_t* qh, const uint16_t* ch, const float* qn,
                            const float* cn, uint32_t Q, uint32_t C, uint32_t Qp, uint32_t Cp,
                            uint32_t Dp, float* dist, hipStream_t st);
+// chosen: topk already holds each query's topc nearest centres (dist unused).
 hipError_t launch_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc, const float* dist,
                         const uint32_t* hist, uint32_t* cells, const uint32_t* counts,
-                        uint32_t* topk, hipStream_t st);
+                        uint32_t* topk, hipStream_t st, bool chosen = false);
+// Each query's topc (<= 4) nearest centres without the distance matrix.
+hipError_t launch_centroid_top(const uint16_t* qh, const uint16_t* ch, const float* qn, const float* cn, uint32_t Q,
+                               uint32_t C, uint32_t Qp, uint32_t Cp, uint32_t Dp, uint32_t topc, uint32_t* topk,
+                               hipStream_t st);
 
 // Host-side file readers (gf_io.cpp).  Each throws gf::Error on failure.
 struct Error {

@@ -1071,6 +1071,12 @@ __global__ void k_merge_stream(uint32_t Q, uint32_t K, uint32_t* run_ids, float*
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
+// |q|^2 + |c|^2 - 2 q.c rounded step by step (no contraction), so the full
+// matrix and the fused nearest-centre selection agree bit for bit.
+__device__ __forceinline__ float centre_dist(float qn, float cn, float dot) {
+    return __fsub_rn(__fadd_rn(qn, cn), __fmul_rn(2.0f, dot));
+}
+
 __global__ __launch_bounds__(256) void k_centroid(const uint16_t* qh, const uint16_t* ch, const float* qn,
                                                   const float* cn, uint32_t Q, uint32_t C, uint32_t Dp,
                                                   float* dist) {
@@ -1090,7 +1096,124 @@ __global__ __launch_bounds__(256) void k_centroid(const uint16_t* qh, const uint
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
         const uint32_t row = q0 + (lane >> 4) * 4u + i;
-        if (row < Q && col < C) dist[size_t(row) * C + col] = qn[row] + cn[col] - 2.0f * acc[i];
+        if (row < Q && col < C) dist[size_t(row) * C + col] = centre_dist(qn[row], cn[col], acc[i]);
+    }
+}
+
+// (distance, centre) order of the nearest-centre choice; NaN counts as +inf.
+__device__ __forceinline__ bool ckey_lt(float d, uint32_t c, float e, uint32_t f) {
+    return d < e || (d == e && c < f);
+}
+__device__ __forceinline__ void ckey_ce(float& ad, uint32_t& ai, float& bd, uint32_t& bi) {
+    if (ckey_lt(bd, bi, ad, ai)) {
+        const float td = ad; ad = bd; bd = td;
+        const uint32_t t = ai; ai = bi; bi = t;
+    }
+}
+// a := the 4 smallest of sorted lists a and b: min(a[k], b[3 - k]) is
+// bitonic, then a half-cleaner sorts it.
+__device__ __forceinline__ void merge4(float (&ad)[4], uint32_t (&ai)[4], const float (&bd)[4],
+                                       const uint32_t (&bi)[4]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (ckey_lt(bd[3 - k], bi[3 - k], ad[k], ai[k])) { ad[k] = bd[3 - k]; ai[k] = bi[3 - k]; }
+    ckey_ce(ad[0], ai[0], ad[2], ai[2]);
+    ckey_ce(ad[1], ai[1], ad[3], ai[3]);
+    ckey_ce(ad[0], ai[0], ad[1], ai[1]);
+    ckey_ce(ad[2], ai[2], ad[3], ai[3]);
+}
+
+// Stage B's nearest centres without the Q x C matrix: a workgroup takes 16
+// queries against every centre tile (each of its kCtW waves every kCtW-th
+// tile, the MFMA tiles and distances of k_centroid); lane l keeps, for each of
+// its four query rows, the 4 smallest (distance, centre) it saw (its centres
+// come in ascending order, so a later equal distance never displaces an
+// earlier one), then the lists merge across the 16 lanes of a row and the
+// waves.  Writes the first topc (<= 4) centres of each query, as the
+// sequential arg-min rounds of k_order would pick them from the matrix.
+constexpr uint32_t kCtW = 16;
+__global__ __launch_bounds__(64 * kCtW) void k_centroid_top(const uint16_t* qh, const uint16_t* ch, const float* qn,
+                                                            const float* cn, uint32_t Q, uint32_t C, uint32_t Cp,
+                                                            uint32_t Dp, uint32_t topc, uint32_t* topk) {
+    __shared__ float sd[kCtW][16][4];
+    __shared__ uint32_t si[kCtW][16][4];
+    const uint32_t lane = lane_id(), wave = threadIdx.x >> 6;
+    const uint32_t q0 = blockIdx.x * 16u;
+    const uint32_t r = lane & 15u, kq = (lane >> 4) * 8u;
+    const half8_t* ap = reinterpret_cast<const half8_t*>(qh + size_t(q0 + r) * Dp + kq);
+    float td[4][4], qr[4];
+    uint32_t ti[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t row = q0 + (lane >> 4) * 4u + i;
+        qr[i] = row < Q ? qn[row] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { td[i][k] = __int_as_float(0x7F800000); ti[i][k] = 0xFFFFFFFFu; }
+    }
+    for (uint32_t ct = wave; ct < Cp / 16u; ct += kCtW) {
+        const uint32_t c0 = ct * 16u;
+        const half8_t* bp = reinterpret_cast<const half8_t*>(ch + size_t(c0 + r) * Dp + kq);
+        float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t k = 0; k < Dp; k += 32u) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap[k / 8u], bp[k / 8u], acc, 0, 0, 0);
+        const uint32_t col = c0 + (lane & 15u);
+        if (col < C) {
+            const float cc = cn[col];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float d = centre_dist(qr[i], cc, acc[i]);
+                if (d != d) d = __int_as_float(0x7F800000);
+                bool lt[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) lt[k] = ckey_lt(d, col, td[i][k], ti[i][k]);
+#pragma unroll
+                for (int k = 3; k >= 1; --k) {
+                    td[i][k] = lt[k - 1] ? td[i][k - 1] : (lt[k] ? d : td[i][k]);
+                    ti[i][k] = lt[k - 1] ? ti[i][k - 1] : (lt[k] ? col : ti[i][k]);
+                }
+                if (lt[0]) { td[i][0] = d; ti[i][0] = col; }
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t m = 1; m < 16u; m <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float od[4];
+            uint32_t oi[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                od[k] = __shfl_xor(td[i][k], int(m));
+                oi[k] = uint32_t(__shfl_xor(int(ti[i][k]), int(m)));
+            }
+            merge4(td[i], ti[i], od, oi);
+        }
+    }
+    if (r == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                sd[wave][(lane >> 4) * 4u + i][k] = td[i][k];
+                si[wave][(lane >> 4) * 4u + i][k] = ti[i][k];
+            }
+    }
+    __syncthreads();
+    const uint32_t t = threadIdx.x;
+    if (t < 16u && q0 + t < Q) {
+        float ad[4];
+        uint32_t ai[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { ad[k] = sd[0][t][k]; ai[k] = si[0][t][k]; }
+        for (uint32_t w = 1; w < kCtW; ++w) {
+            float bd[4];
+            uint32_t bi[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) { bd[k] = sd[w][t][k]; bi[k] = si[w][t][k]; }
+            merge4(ad, ai, bd, bi);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (uint32_t(k) < topc) topk[size_t(q0 + t) * topc + k] = ai[k] < C ? ai[k] : 0u;
     }
 }
 
@@ -1101,7 +1224,7 @@ __global__ __launch_bounds__(256) void k_centroid(const uint16_t* qh, const uint
 // sorts the cells by (score descending, cell ascending).
 __global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc,
                                               const float* dist, const uint32_t* hist, uint32_t* cells,
-                                              const uint32_t* counts, uint32_t* topk) {
+                                              const uint32_t* counts, uint32_t* topk, bool chosen) {
     extern __shared__ uint32_t so[];
     uint32_t* tk = so;             // topc
     uint32_t* sc = so + 16;        // P scores
@@ -1110,7 +1233,9 @@ __global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P
     const float* dq = dist + size_t(q) * C;
     float pd = -1.0f;
     uint32_t pi = 0xFFFFFFFFu;
-    for (uint32_t t = 0; t < topc; ++t) {
+    // chosen: the nearest centres are already in topk (k_centroid_top)
+    if (chosen && lane < topc) tk[lane] = topk[size_t(q) * topc + lane];
+    for (uint32_t t = 0; !chosen && t < topc; ++t) {
         float bd = __int_as_float(0x7F800000);
         uint32_t bi = 0xFFFFFFFFu;
         for (uint32_t c = lane; c < C; c += 64u) {
@@ -2368,10 +2493,20 @@ hipError_t launch_centroid(const uint16_t* qh, const uint16_t* ch, const float* 
 
 hipError_t launch_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc, const float* dist,
                         const uint32_t* hist, uint32_t* cells, const uint32_t* counts, uint32_t* topk,
-                        hipStream_t st) {
+                        hipStream_t st, bool chosen) {
     if (!Q) return hipSuccess;
     const uint32_t lds = (16 + 2 * P) * sizeof(uint32_t);
-    hipLaunchKernelGGL(k_order, dim3(Q), dim3(64), lds, st, Q, C, P, topc, dist, hist, cells, counts, topk);
+    hipLaunchKernelGGL(k_order, dim3(Q), dim3(64), lds, st, Q, C, P, topc, dist, hist, cells, counts, topk, chosen);
+    return hipGetLastError();
+}
+
+hipError_t launch_centroid_top(const uint16_t* qh, const uint16_t* ch, const float* qn, const float* cn, uint32_t Q,
+                               uint32_t C, uint32_t Qp, uint32_t Cp, uint32_t Dp, uint32_t topc, uint32_t* topk,
+                               hipStream_t st) {
+    if (!Q || !C) return hipSuccess;
+    if (topc < 1 || topc > 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_centroid_top, dim3(Qp / 16), dim3(64 * kCtW), 0, st, qh, ch, qn, cn, Q, C, Cp, Dp, topc,
+                       topk);
     return hipGetLastError();
 }
 

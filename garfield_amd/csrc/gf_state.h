@@ -255,6 +255,8 @@ struct gf_batch {
     gf::PinBuf<uint32_t> h_ids, h_tot;
     gf::PinBuf<float> h_dist;
     gf::PinBuf<unsigned long long> h_stats;
+    // Stage B ran; cdist holds the query x centre matrix of that run.
+    bool ordered = false, cdist_ready = false;
     hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
     // Around the latest stage A ([0], [1]) and stage B ([2], [3]) calls.
     hipEvent_t sev[4] = {nullptr, nullptr, nullptr, nullptr};
