@@ -1131,7 +1131,7 @@ __device__ __forceinline__ void merge4(float (&ad)[4], uint32_t (&ai)[4], const 
 // earlier one), then the lists merge across the 16 lanes of a row and the
 // waves.  Writes the first topc (<= 4) centres of each query, as the
 // sequential arg-min rounds of k_order would pick them from the matrix.
-constexpr uint32_t kCtW = 16;
+constexpr uint32_t kCtW = 4;
 __global__ __launch_bounds__(64 * kCtW) void k_centroid_top(const uint16_t* qh, const uint16_t* ch, const float* qn,
                                                             const float* cn, uint32_t Q, uint32_t C, uint32_t Cp,
                                                             uint32_t Dp, uint32_t topc, uint32_t* topk) {
