@@ -80,6 +80,8 @@ void build_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, c
     ix.stile.upload(sh.stile);
     ix.sbox.upload(sh.sbox);
     ix.tmeta.upload(sh.tmeta);
+    ix.sorder.upload(sh.sorder);
+    ix.ns1 = sh.ns1;
     ix.sub = true;
 }
 
@@ -104,7 +106,7 @@ bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx,
             abase[size_t(c) * a + d] = int32_t(mn);
         }
     const uint32_t AW = (a + 1) / 2, MW = 16 * (1 + AW);
-    std::vector<uint32_t> sbase(P + 1, 0), scell, ssize, stile, tmeta;
+    std::vector<uint32_t> sbase(P + 1, 0), scell, ssize, stile, tmeta, first;
     std::vector<int32_t> sbox;
     auto attr = [&](uint32_t r, uint32_t d) { return int32_t(h.attrs[size_t(gidx[r]) * a + d]); };
     for (uint32_t c = 0; c < P; ++c) {
@@ -124,6 +126,12 @@ bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx,
         for (uint32_t i = 0; i < n; ++i) members[sid[i]].push_back(off + i);
         for (uint32_t k = 0; k < nsc; ++k) {
             const auto& m = members[k];
+            // First-pass sub-cells: grid coordinates (s_0, ..., s_{a-1}) with
+            // s_0 + 3 s_1 + 5 s_2 + 7 s_3 = 0 (mod 8), one in eight of the grid
+            // and spread over every row and column of it.
+            uint32_t h = 0;
+            for (uint32_t d = 0, kk = k; d < a; ++d, kk /= S) h += (2u * (a - 1u - d) + 1u) * (kk % S);
+            first.push_back(h % 8u == 0u ? 1u : 0u);
             scell.push_back(c);
             ssize.push_back(uint32_t(m.size()));
             stile.push_back(uint32_t(tmeta.size() / MW));
@@ -156,6 +164,12 @@ bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx,
     stile.push_back(uint32_t(tmeta.size() / MW));
     out.AW = AW;
     out.NS = sbase[P];
+    out.sorder.clear();
+    for (uint32_t s = 0; s < out.NS; ++s)
+        if (first[s]) out.sorder.push_back(s);
+    out.ns1 = uint32_t(out.sorder.size());
+    for (uint32_t s = 0; s < out.NS; ++s)
+        if (!first[s]) out.sorder.push_back(s);
     out.ntile = stile.back();
     out.sbase = std::move(sbase);
     out.scell = std::move(scell);
@@ -796,14 +810,22 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 b->bcnt.alloc(NS); b->bin.alloc(NS); b->bstart.alloc(NS); b->icnt.alloc(NS); b->ioff.alloc(NS);
                 b->nsub.alloc(Q); b->part_off.alloc(Q); b->pcnt.alloc(Q);
             }
-            if (!b->part.n) b->alloc_pairs(size_t(Q) * 64, K, Q, NS, NS);
+            // item slots: a sub-cell adds up to two partial query blocks per
+            // tile chunk beyond pairs / 64
+            const size_t islots = size_t(NS) + ix->ntile / gf::kBfMaxItemTiles + 1;
+            if (!b->part.n) b->alloc_pairs(size_t(Q) * 64, K, Q, NS, islots);
             if (b->rq.n < Q) {
                 b->rq.alloc(Q); b->rseed.alloc(Q);
                 b->rlo.alloc(size_t(Q) * ix->a); b->rhi.alloc(size_t(Q) * ix->a);
             }
             if (b->scnt.n < NS) {
                 b->scnt.alloc(NS);
-                b->sitems.alloc(size_t(Q) / gf::kBfQB + NS + 1);
+                // a seed sub-cell s with ns queries makes ceil(ns / 64) items per
+                // chunk of kBfSeedTiles tiles; every query seeds one sub-cell
+                uint32_t tmax = 0;
+                for (uint32_t s = 0; s < NS; ++s) tmax = std::max(tmax, ix->stile_h[s + 1] - ix->stile_h[s]);
+                const size_t chunks = (tmax + gf::kBfSeedTiles - 1) / gf::kBfSeedTiles;
+                b->sitems.alloc((size_t(Q) / gf::kBfQB + NS + 1) * std::max<size_t>(chunks, 1));
             }
             if (b->part.n < b->pair_cap * K) b->part.alloc(b->pair_cap * K);
             if (b->gbound.n < Q) b->gbound.alloc(Q);
@@ -821,6 +843,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             sc.bstart = b->bstart.p; sc.bq = b->bq.p; sc.qcap = b->qcap;
             sc.ok = tot + 3; sc.nbf = tot + 9;
             sc.qlist = b->sched.p; sc.qrange = tot + 14;   // the brute-force queries of the schedule
+            sc.tch = gf::kBfMaxItemTiles;
             if (!b->bf_all) {
                 if (b->bfmask.n < size_t(Q) * ix->P) b->bfmask.alloc(size_t(Q) * ix->P);
                 GF_HIP(gf::launch_cell_flags(Q, ix->P, b->cells.p, b->counts.p, b->little.p, b->bfmask.p, st));
@@ -835,7 +858,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 gf::BfSeedArgs sd{};
                 sd.sa = sc.sa; sd.Q = Q; sd.postfilter = sc.postfilter; sd.counts = sc.counts; sd.little = sc.little;
                 sd.cells = b->cells.p; sd.lo = sc.lo; sd.hi = sc.hi; sd.bfm = sc.bfm; sd.bP = sc.bP;
-                sd.qlist = sc.qlist; sd.qrange = sc.qrange; sd.qcap = b->qcap; sd.tch = 0;
+                sd.qlist = sc.qlist; sd.qrange = sc.qrange; sd.qcap = b->qcap; sd.tch = gf::kBfSeedTiles;
                 sd.scnt = b->scnt.p; sd.bq = b->bq.p; sd.nsub = b->nsub.p;
                 sd.rq = b->rq.p; sd.rseed = b->rseed.p; sd.rlo = b->rlo.p; sd.rhi = b->rhi.p;
                 GF_HIP(gf::launch_bfseed(sd, Q, st));
@@ -848,29 +871,56 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             GF_HIP(gf::launch_total(b->nsub.p, b->part_off.p, Q, uint32_t(std::min<size_t>(b->pair_cap, UINT32_MAX)), K,
                                     b->part.n, tot + 2, st));
             if (!b->qcap) GF_HIP(gf::launch_bfsched(sc, true, st));
-            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, b->qcap, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p,
-                                      b->items.p, tot + 4, tot + 3, false, st));
+            // Two passes (resident index): the seeds and the items of the
+            // first-pass sub-cells, then a merge that lowers each query's
+            // bound to the K-th smallest distance found so far, then the rest
+            // of the items under those bounds.  Both k_bfitems launches take
+            // the sub-cells in the same order (counts, scan, fill).
+            const bool two = ix->sorder.n == NS && ix->ns1 > 0 && ix->ns1 < NS;
+            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, b->qcap, ix->stile.p, gf::kBfMaxItemTiles, NS, b->icnt.p, b->ioff.p,
+                                      b->items.p, tot + 4, tot + 3, false, st, nullptr, nullptr, nullptr, 0,
+                                      two ? ix->sorder.p : nullptr, two ? ix->ns1 : 0u, nullptr));
             GF_HIP(gf::launch_scan_small(b->icnt.p, NS, b->ioff.p, st));
             const uint32_t scap = uint32_t(b->sitems.n);
-            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, b->qcap, ix->stile.p, 0, NS, b->icnt.p, b->ioff.p,
+            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, b->qcap, ix->stile.p, gf::kBfMaxItemTiles, NS, b->icnt.p, b->ioff.p,
                                       b->items.p, tot + 4, tot + 3, true, st, seeds ? b->scnt.p : nullptr,
-                                      b->sitems.p, tot + 5, scap));
+                                      b->sitems.p, tot + 5, scap, two ? ix->sorder.p : nullptr, two ? ix->ns1 : 0u,
+                                      two ? tot + 6 : nullptr, gf::kBfSeedTiles));
             gf::BfGemmArgs ga{};
             ga.sa = sub_args(*ix);
             ga.vt = ix->vt.p; ga.tnorm = ix->tnorm.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p;
             ga.hi = b->hi.p; ga.items = b->items.p; ga.nitems = tot + 4; ga.bq = b->bq.p; ga.pcnt = b->pcnt.p;
             ga.part_off = b->part_off.p; ga.part = b->part.p; ga.gbound = b->gbound.p;
             ga.ok = tot + 3;
-            if (seeds) { ga.sitems = b->sitems.p; ga.nseed = tot + 5; ga.nseed_cap = scap; }
+            if (seeds) { ga.sitems = b->sitems.p; ga.nseed = tot + 5; ga.nseed_cap = scap; ga.seeds_on = 1; }
             ga.K = K; ga.D = ix->D;
-            GF_HIP(hipEventRecord(evg[0], st));
-            GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu) * 3u, st));
-            GF_HIP(hipEventRecord(evg[1], st));
             gf::BfFinalArgs fa{};
             fa.gbound = b->gbound.p; fa.bfq = b->sched.p; fa.srange = tot + 14; fa.part_off = b->part_off.p; fa.pcnt = b->pcnt.p;
             fa.ok = tot + 3; fa.part = b->part.p; fa.counts = b->counts.p; fa.cells = b->cells.p;
             fa.offset = ix->offset.p; fa.selcount = b->selcount.p; fa.gidx = ix->gidx.p; fa.out_ids = b->out_ids.p;
             fa.out_dist = b->out_dist.p; fa.counters = b->counters.p; fa.K = K; fa.P = ix->P;
+            GF_HIP(hipEventRecord(evg[0], st));
+            if (two) {
+                // the seeds alone, then a merge (each query's bound becomes the
+                // K-th of its seed sub-cell), the first pass under those
+                // bounds, a merge, the rest
+                ga.nitems_a = tot + 6;
+                if (seeds) {
+                    ga.irange = 3;
+                    GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu), st));
+                    fa.bound_only = 1;
+                    GF_HIP(gf::launch_bf_final(fa, Q, st));
+                    ga.seeds_on = 0;
+                }
+                ga.irange = 1;
+                GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu), st));
+                fa.bound_only = 1;
+                GF_HIP(gf::launch_bf_final(fa, Q, st));
+                fa.bound_only = 0;
+                ga.irange = 2;
+            }
+            GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu), st));
+            GF_HIP(hipEventRecord(evg[1], st));
             GF_HIP(gf::launch_bf_final(fa, Q, st));
         };
 
@@ -921,7 +971,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         const uint32_t* dt = b->h_tot.p;
         if (gemm && !dt[3]) {
             // the pair lists outgrew their buffers: grow them and run the brute force again
-            b->alloc_pairs(size_t(dt[2]) + dt[2] / 4 + 1024, K, Q, NS, 0);
+            b->alloc_pairs(size_t(dt[2]) + dt[2] / 4 + 1024, K, Q, NS, size_t(NS) + ix->ntile / gf::kBfMaxItemTiles + 1);
             GF_HIP(hipEventRecord(ev[1], st));
             launch_gemm();
             GF_HIP(hipEventRecord(ev[2], st));

@@ -92,6 +92,8 @@ struct SubArgs {
 constexpr uint32_t kBfTile = 16;      // points per tile
 constexpr uint32_t kBfKMax = 16;      // largest K of the MFMA route
 constexpr uint32_t kBfQB = 64;        // queries per work item
+constexpr uint32_t kBfMaxItemTiles = 65536;   // tiles per MFMA work item (keeps buffer offsets below 2^31)
+constexpr uint32_t kBfSeedTiles = 16;         // tiles per seed item: a seed sub-cell spreads over several waves
 constexpr size_t kDirectListMax = size_t(64) << 20;   // NS x Q bound of one-pass sub-cell lists (256 MiB)
 struct BfItem {
     uint32_t sub, qbase, nq;           // sub-cell, first entry of its query list, queries
@@ -120,9 +122,14 @@ struct BfGemmArgs {
     const uint32_t* nseed;     // device count of seed items
     uint32_t nseed_cap;        // capacity of sitems
     uint32_t K, D;
+    // What a launch runs: the seed items if seeds_on, and of the item list
+    // all (irange 0), the first *nitems_a (1), the rest (2) or none (3).
+    uint32_t seeds_on;
+    uint32_t irange;
+    const uint32_t* nitems_a;
 };
 struct BfFinalArgs {
-    const uint32_t* gbound;    // optional: per query the bound the items reached
+    uint32_t* gbound;          // optional: per query the bound the items reached
     const uint32_t* bfq;       // schedule
     const uint32_t* srange;    // device [begin, end) of the brute-force queries in bfq
     const uint32_t* part_off;  // per query: first pair (partial area = pairs * K keys)
@@ -138,6 +145,9 @@ struct BfFinalArgs {
     float* out_dist;
     uint32_t* counters;
     uint32_t K, P;
+    // Bound only: lower each query's gbound to the K-th smallest key appended
+    // so far and leave the keys, results and counters as they are.
+    uint32_t bound_only;
 };
 // Stage A on sub-cells: one workgroup per sub-cell over all queries.  A point
 // that passes a range lies in a cell the range selects, so the relation of a
@@ -252,7 +262,7 @@ struct StatsArgs {
 hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds_bytes, uint32_t grid, hipStream_t st);
 hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, uint32_t grid, hipStream_t st);
 hipError_t launch_fill_results(uint32_t* ids, float* dist, uint32_t n, hipStream_t st);
-hipError_t launch_bf_i8(const BfGemmArgs& a, uint32_t nwg, hipStream_t st);
+hipError_t launch_bf_i8(const BfGemmArgs& a, uint32_t ncu, hipStream_t st);   // grid: ncu x resident workgroups per CU
 hipError_t launch_bf_final(const BfFinalArgs& a, uint32_t grid, hipStream_t st);
 hipError_t launch_tile_i8(const void* vec_cm, bool u8, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
                           int8_t* vt, int32_t* tnorm, hipStream_t st);
@@ -263,7 +273,8 @@ hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint3
                           const uint32_t* stile, uint32_t tch, uint32_t NS, uint32_t* icnt, uint32_t* ioff,
                           BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill, hipStream_t st,
                           const uint32_t* scnt = nullptr, BfItem* sitems = nullptr, uint32_t* nseed = nullptr,
-                          uint32_t scap = 0);
+                          uint32_t scap = 0, const uint32_t* sorder = nullptr, uint32_t ns1 = 0,
+                          uint32_t* nitems_a = nullptr, uint32_t stch = 0);
 hipError_t launch_bfseed(const BfSeedArgs& a, uint32_t Q, hipStream_t st);
 // out[0] = start[n-1] + cnt[n-1] (total of an exclusive scan); out[1] = out[0] <= cap
 // (with cap2 != 0 also out[0] * mul <= cap2).

@@ -1766,22 +1766,28 @@ __global__ __launch_bounds__(256) void k_stats(StatsArgs p) {
 }
 
 // Work items of the MFMA brute force: per sub-cell, its query list in groups
-// of 64, times its tiles in chunks of tch (0: one chunk).
+// of 64, times its tiles in chunks of tch (0: one chunk).  Sub-cells are
+// taken in the order sorder (identity if null), so the items of its first
+// ns1 sub-cells come first: *nitems_a of them.
 __global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, uint32_t qcap,
                           const uint32_t* stile, uint32_t tch, uint32_t NS, uint32_t* icnt, const uint32_t* ioff,
                           BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill, const uint32_t* scnt,
-                          BfItem* sitems, uint32_t* nseed, uint32_t scap) {
-    const uint32_t s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= NS) return;
+                          BfItem* sitems, uint32_t* nseed, uint32_t scap, const uint32_t* sorder, uint32_t ns1,
+                          uint32_t* nitems_a, uint32_t stch) {
+    const uint32_t ks = blockIdx.x * blockDim.x + threadIdx.x;
+    if (ks >= NS) return;
+    const uint32_t s = sorder ? sorder[ks] : ks;
     if (fill && !*ok) {
-        if (s == NS - 1) *nitems = 0;
+        if (ks == NS - 1) *nitems = 0;
+        if (nitems_a && ks == 0) *nitems_a = 0;
         return;
     }
     const uint32_t ns = qcap && scnt ? scnt[s] : 0u;   // seeds: the front of the region
     if (fill && ns) {
-        // seed items go to their own list (order is free: each is one sub-cell)
-        const uint32_t nc = tile_chunks(stile, s, tch), gs = (ns + kBfQB - 1) / kBfQB;
-        const uint32_t t0 = stile[s], t1 = stile[s + 1], step = tch ? tch : (t1 - t0);
+        // seed items go to their own list (order is free: each is one
+        // sub-cell), in chunks of stch tiles
+        const uint32_t nc = tile_chunks(stile, s, stch), gs = (ns + kBfQB - 1) / kBfQB;
+        const uint32_t t0 = stile[s], t1 = stile[s + 1], step = stch ? stch : (t1 - t0);
         uint32_t k = atomicAdd(nseed, gs * nc);
         for (uint32_t c = 0; c < nc; ++c) {
             const uint32_t tb = t0 + c * step, te = min(t1, tb + step);
@@ -1795,9 +1801,13 @@ __global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint3
     const uint32_t gi = qcap ? (ni + kBfQB - 1) / kBfQB : 0u;
     const uint32_t gp = qcap ? (n - ni + kBfQB - 1) / kBfQB : (n + kBfQB - 1) / kBfQB;
     const uint32_t nc = n ? tile_chunks(stile, s, tch) : 0u;
-    if (!fill) { icnt[s] = (gi + gp) * nc; return; }
+    if (!fill) { icnt[ks] = (gi + gp) * nc; return; }
     const uint32_t t0 = stile[s], t1 = stile[s + 1], step = tch ? tch : (t1 - t0);
-    uint32_t k = ioff[s];
+    uint32_t k = ioff[ks];
+    if (nitems_a) {
+        if (ks + 1 == ns1) *nitems_a = ioff[ks] + (gi + gp) * nc;
+        else if (ns1 == 0 && ks == 0) *nitems_a = 0;
+    }
     for (uint32_t c = 0; c < nc; ++c) {
         const uint32_t tb = t0 + c * step, te = min(t1, tb + step);
         if (qcap) {
@@ -1813,7 +1823,7 @@ __global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint3
             }
         }
     }
-    if (s == NS - 1) *nitems = ioff[s] + (gi + gp) * nc;
+    if (ks == NS - 1) *nitems = ioff[ks] + (gi + gp) * nc;
 }
 
 // out[0] = start[n-1] + cnt[n-1], the total of an exclusive scan; out[1] =
@@ -1841,15 +1851,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3
     __shared__ uint32_t s_cnt[4][kQB];
     __shared__ int32_t s_tp[4][kQB];
     __shared__ uint32_t s_bnd[4][2 * AW][kQB];
-    const uint32_t wave = threadIdx.x >> 6, lane = lane_id();
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
     const SubArgs& sa = p.sa;
     // Persistent waves, XCD-aware: workgroups go round-robin to the 8 XCDs and
     // XCD x works through the x-th eighth of the item list (items of one
     // sub-cell are adjacent, so its tiles stay in that XCD's L2).
     const uint32_t nwg = gridDim.x, xcd = blockIdx.x & 7u, k8 = blockIdx.x >> 3;
     const uint32_t nwg_x = (nwg - xcd + 7u) >> 3;
-    const uint32_t n_items = *p.ok ? *p.nitems : 0u;
-    const uint32_t i_lo = uint32_t(uint64_t(n_items) * xcd / 8u), i_hi = uint32_t(uint64_t(n_items) * (xcd + 1u) / 8u);
+    uint32_t i_b = 0, i_e = *p.ok && p.irange != 3u ? *p.nitems : 0u;
+    if (p.irange == 1u) i_e = min(i_e, *p.nitems_a);
+    if (p.irange == 2u) i_b = min(i_e, *p.nitems_a);
+    const uint32_t n_items = i_e - i_b;
+    const uint32_t i_lo = i_b + uint32_t(uint64_t(n_items) * xcd / 8u);
+    const uint32_t i_hi = i_b + uint32_t(uint64_t(n_items) * (xcd + 1u) / 8u);
     uint64_t* buf = s_buf[wave];
     uint32_t* cnt = s_cnt[wave];
     int32_t* stp = s_tp[wave];
@@ -1859,7 +1873,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3
 
     // Seed items first (strided over every wave of the grid), then the XCD's
     // range of the item list.
-    const uint32_t n_seed = p.sitems && *p.ok ? min(*p.nseed, p.nseed_cap) : 0u;
+    const uint32_t n_seed = p.sitems && *p.ok && p.seeds_on ? min(*p.nseed, p.nseed_cap) : 0u;
     uint32_t seed_id = blockIdx.x * 4u + wave, item_id = i_lo + k8 * 4u + wave;
     for (;;) {
         BfItem it;
@@ -2092,6 +2106,11 @@ __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
         top = lane < K ? T[lane] : kKeySent;
         __syncthreads();
     }
+    if (p.bound_only) {
+        const uint64_t t_k = readlane64(top, K - 1);
+        if (lane == 0 && t_k != kKeySent && uint32_t(t_k >> 32) < g) p.gbound[q] = uint32_t(t_k >> 32);
+        return;
+    }
     if (lane < K) {
         const bool v = top != kKeySent;
         p.out_ids[size_t(q) * K + lane] = v ? p.gidx[uint32_t(top)] : GF_NO_RESULT;
@@ -2248,15 +2267,32 @@ hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, uint32_t gri
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_bf_i8(const BfGemmArgs& a, uint32_t nwg, hipStream_t st) {
-    if (a.K > kBfKMax || a.sa.a < 1 || a.sa.a > 4 || nwg == 0) return hipErrorInvalidValue;
+// The kernel's waves are persistent and split the items evenly, so the grid
+// is exactly the workgroups that fit on the device at once (a workgroup that
+// started late would run its share after the others finished).
+template <int KS, int AW, int KT>
+static hipError_t launch_bf_i8_t(const BfGemmArgs& a, uint32_t ncu, hipStream_t st) {
+    static int per_cu = 0;
+    if (!per_cu) {
+        int n = 0;
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_bf_i8<KS, AW, KT>, 256, 0);
+        if (e != hipSuccess) return e;
+        per_cu = n > 0 ? n : 1;
+    }
+    hipLaunchKernelGGL((k_bf_i8<KS, AW, KT>), dim3(ncu * uint32_t(per_cu)), dim3(256), 0, st, a);
+    return hipSuccess;
+}
+
+hipError_t launch_bf_i8(const BfGemmArgs& a, uint32_t ncu, hipStream_t st) {
+    if (a.K > kBfKMax || a.sa.a < 1 || a.sa.a > 4 || ncu == 0) return hipErrorInvalidValue;
     const uint32_t AW = a.sa.AW;
-#define BF(KS, AW_)                                                                   \
-    do {                                                                              \
-        if (a.K <= 10)                                                                \
-            hipLaunchKernelGGL((k_bf_i8<KS, AW_, 10>), dim3(nwg), dim3(256), 0, st, a); \
-        else                                                                          \
-            hipLaunchKernelGGL((k_bf_i8<KS, AW_, 16>), dim3(nwg), dim3(256), 0, st, a); \
+    hipError_t e = hipSuccess;
+#define BF(KS, AW_)                                                        \
+    do {                                                                   \
+        if (a.K <= 10)                                                     \
+            e = launch_bf_i8_t<KS, AW_, 10>(a, ncu, st);                   \
+        else                                                               \
+            e = launch_bf_i8_t<KS, AW_, 16>(a, ncu, st);                   \
     } while (0)
     switch ((a.D / 64) * 4 + AW) {
         case 1 * 4 + 1: BF(1, 1); break;
@@ -2270,6 +2306,7 @@ hipError_t launch_bf_i8(const BfGemmArgs& a, uint32_t nwg, hipStream_t st) {
         default: return hipErrorInvalidValue;
     }
 #undef BF
+    if (e != hipSuccess) return e;
     return hipGetLastError();
 }
 
@@ -2326,11 +2363,14 @@ hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st) {
 hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, uint32_t qcap,
                           const uint32_t* stile, uint32_t tch, uint32_t NS, uint32_t* icnt, uint32_t* ioff,
                           BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill, hipStream_t st,
-                          const uint32_t* scnt, BfItem* sitems, uint32_t* nseed, uint32_t scap) {
+                          const uint32_t* scnt, BfItem* sitems, uint32_t* nseed, uint32_t scap, const uint32_t* sorder,
+                          uint32_t ns1, uint32_t* nitems_a, uint32_t stch) {
     if (!NS) return hipSuccess;
     if (scnt && (!sitems || !nseed)) return hipErrorInvalidValue;
+    if (sorder && ns1 > NS) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_bfitems, dim3((NS + 255) / 256), dim3(256), 0, st, bcnt, bin, bstart, qcap, stile, tch, NS,
-                       icnt, ioff, items, nitems, ok, fill, scnt, sitems, nseed, scap);
+                       icnt, ioff, items, nitems, ok, fill, scnt, sitems, nseed, scap, sorder, ns1, nitems_a,
+                       scnt ? stch : tch);
     return hipGetLastError();
 }
 

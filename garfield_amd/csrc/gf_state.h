@@ -170,6 +170,8 @@ struct gf_index {
     uint32_t AW = 0, NS = 0, ntile = 0;
     std::vector<uint32_t> ssize_h, stile_h;
     DevBuf<uint32_t> sbase, scell, ssize, stile, tmeta;
+    DevBuf<uint32_t> sorder;   // sub-cells of the brute force's first pass (ns1 of them), then the rest
+    uint32_t ns1 = 0;
     DevBuf<int32_t> sbox, abase;
     // Query-batch MFMA brute force (additionally: vectors integers in
     // [0, 255], D a multiple of 64 up to 256): int8 tiles and norms.
@@ -189,7 +191,7 @@ struct gf_index {
                cross.bytes() + offset.bytes() + gidx.bytes() + lrow.bytes() + grid.bytes() + doff.bytes() +
                hist.bytes() + tile_cell.bytes() + tile_row0.bytes() + tile_n.bytes() + centres.bytes() +
                sbase.bytes() + scell.bytes() + ssize.bytes() + stile.bytes() + tmeta.bytes() + sbox.bytes() +
-               abase.bytes() + vt.bytes() + tnorm.bytes() +
+               sorder.bytes() + abase.bytes() + vt.bytes() + tnorm.bytes() +
                (sx ? sx->turn[0].bytes() + sx->turn[1].bytes() + sx->vt.bytes() + sx->tnorm.bytes() : 0);
     }
 };
@@ -290,6 +292,10 @@ namespace gf {
 // a spread of 65534 or more inside a cell).
 struct SubHost {
     uint32_t AW = 0, NS = 0, ntile = 0;
+    // Brute-force pass order: the ns1 sub-cells of the first pass (about one
+    // in eight of each cell's rank grid, spread over it), then the rest.
+    uint32_t ns1 = 0;
+    std::vector<uint32_t> sorder;
     std::vector<uint32_t> sbase, scell, ssize, stile, tmeta;
     std::vector<int32_t> sbox, abase;
 };

@@ -368,7 +368,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         ga.items = b.items.p; ga.nitems = tot + 4; ga.bq = b.bq.p; ga.pcnt = b.pcnt.p; ga.part_off = b.part_off.p;
         ga.part = b.part.p; ga.gbound = b.gbound.p; ga.ok = tot + 3; ga.K = K; ga.D = ix.D;
         GF_HIP(hipEventRecord(ge[2 * bi], st));
-        GF_HIP(launch_bf_i8(ga, uint32_t(std::max(ix.ncu, 1)) * 3u, st));
+        GF_HIP(launch_bf_i8(ga, uint32_t(std::max(ix.ncu, 1)), st));
         GF_HIP(hipEventRecord(ge[2 * bi + 1], st));
         BfFinalArgs fa{};
         fa.gbound = b.gbound.p; fa.bfq = b.sched.p; fa.srange = tot + 14; fa.part_off = b.part_off.p; fa.pcnt = b.pcnt.p; fa.ok = tot + 3;
