@@ -286,6 +286,8 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
     GF_HIP(hipSetDevice(ix.device));
     GF_HIP(hipStreamCreateWithFlags(&ix.stream, hipStreamNonBlocking));
     GF_HIP(hipDeviceGetAttribute(&ix.ncu, hipDeviceAttributeMultiprocessorCount, ix.device));
+    GF_HIP(hipDeviceGetAttribute(&ix.wclk_khz, hipDeviceAttributeWallClockRate, ix.device));
+    ix.wclk_khz = std::max(ix.wclk_khz, 1);
     ix.ncu = std::max(ix.ncu, 1);
     ix.cross.upload(cross_cm);
     std::vector<uint32_t>().swap(cross_cm);
@@ -829,12 +831,14 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             }
             if (b->part.n < b->pair_cap * K) b->part.alloc(b->pair_cap * K);
             if (b->gbound.n < Q) b->gbound.alloc(Q);
+            if (!b->bf_all && b->bfmask.n < size_t(Q) * ix->P) b->bfmask.alloc(size_t(Q) * ix->P);
         }
         // events: [0] search start, [1] after traversal, [2] end, [3..4] around the MFMA kernel alone
-        if (!b->ev[0])
-            for (auto& e : b->ev) GF_HIP(hipEventCreate(&e));
-        hipEvent_t* ev = b->ev;
-        hipEvent_t* evg = b->ev + 3;
+        // Device timestamps (wall clock, kernels on the stream, so that they
+        // time a replayed graph too): [0] search start, [1] after traversal,
+        // [2] end, [3..4] around the MFMA brute-force launches.
+        if (!b->stamps.n) { b->stamps.alloc(8); b->h_stamps.alloc(8); }
+        uint64_t* stamp = b->stamps.p;
         auto launch_gemm = [&]() {
             gf::BfSchedArgs sc{};
             sc.sa = sub_args(*ix);
@@ -845,7 +849,6 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             sc.qlist = b->sched.p; sc.qrange = tot + 14;   // the brute-force queries of the schedule
             sc.tch = gf::kBfMaxItemTiles;
             if (!b->bf_all) {
-                if (b->bfmask.n < size_t(Q) * ix->P) b->bfmask.alloc(size_t(Q) * ix->P);
                 GF_HIP(gf::launch_cell_flags(Q, ix->P, b->cells.p, b->counts.p, b->little.p, b->bfmask.p, st));
                 sc.bfm = b->bfmask.p;
                 sc.bP = ix->P;
@@ -899,7 +902,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             fa.ok = tot + 3; fa.part = b->part.p; fa.counts = b->counts.p; fa.cells = b->cells.p;
             fa.offset = ix->offset.p; fa.selcount = b->selcount.p; fa.gidx = ix->gidx.p; fa.out_ids = b->out_ids.p;
             fa.out_dist = b->out_dist.p; fa.counters = b->counters.p; fa.K = K; fa.P = ix->P;
-            GF_HIP(hipEventRecord(evg[0], st));
+            GF_HIP(gf::launch_stamp(stamp + 3, st));
             if (two) {
                 // the seeds alone, then a merge (each query's bound becomes the
                 // K-th of its seed sub-cell), the first pass under those
@@ -920,30 +923,9 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 ga.irange = 2;
             }
             GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu), st));
-            GF_HIP(hipEventRecord(evg[1], st));
+            GF_HIP(gf::launch_stamp(stamp + 4, st));
             GF_HIP(gf::launch_bf_final(fa, Q, st));
         };
-
-        // Schedule (gpu_graph.cu:12485-12493) on the device.
-        gf::SchedArgs sa{};
-        sa.Q = Q; sa.P = ix->P; sa.postfilter = opts->postfilter; sa.counts = b->counts.p; sa.little = b->little.p;
-        sa.sched = b->sched.p; sa.tot = tot + 8; sa.ranges = tot + 12;
-        GF_HIP(hipMemsetAsync(b->counters.p, 0, size_t(Q) * GF_NCOUNTERS * sizeof(uint32_t), st));
-        GF_HIP(gf::launch_fill_results(b->out_ids.p, b->out_dist.p, Q * K, st));
-        GF_HIP(gf::launch_sched(sa, st));
-        GF_HIP(hipEventRecord(ev[0], st));
-        gf::TravArgs at = a;
-        at.srange = tot + 12;
-        GF_HIP(gf::launch_traverse(ix->rs, at, lds, Q, st));
-        GF_HIP(hipEventRecord(ev[1], st));
-        if (gemm) {
-            launch_gemm();
-        } else {
-            gf::TravArgs ab = a;
-            ab.srange = tot + 14;
-            GF_HIP(gf::launch_bruteforce(ix->rs, ab, Q, st));
-        }
-        GF_HIP(hipEventRecord(ev[2], st));
 
         // Results, statistics and the schedule's totals come back through
         // pinned staging with one synchronisation.
@@ -951,9 +933,9 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         if (b->h_ids.n < nr) { b->h_ids.alloc(nr); b->h_dist.alloc(nr); }
         if (!b->h_tot.n) { b->h_tot.alloc(16); b->h_stats.alloc(16); }
         if (stats && b->stats.n < 16) b->stats.alloc(16);
-        auto enqueue_tail = [&]() {
+        auto enqueue_copies = [&]() {
             if (stats) {
-                GF_HIP(hipMemsetAsync(b->stats.p, 0, 16 * sizeof(unsigned long long), st));
+                GF_HIP(gf::launch_zero_u32(reinterpret_cast<uint32_t*>(b->stats.p), 32, st));
                 gf::StatsArgs sa2{};
                 sa2.Q = Q; sa2.NS = gemm ? NS : 0; sa2.counters = b->counters.p; sa2.bcnt = gemm ? b->bcnt.p : nullptr;
                 sa2.bin = b->bin.p; sa2.split = b->qcap != 0; sa2.sseed = b->qcap ? b->scnt.p : nullptr;
@@ -963,18 +945,62 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                                       st));
             }
             GF_HIP(hipMemcpyAsync(b->h_tot.p, tot, 16 * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+            GF_HIP(hipMemcpyAsync(b->h_stamps.p, b->stamps.p, 8 * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
             GF_HIP(hipMemcpyAsync(b->h_ids.p, b->out_ids.p, nr * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
             if (dists) GF_HIP(hipMemcpyAsync(b->h_dist.p, b->out_dist.p, nr * sizeof(float), hipMemcpyDeviceToHost, st));
+        };
+        auto enqueue_tail = [&]() {
+            enqueue_copies();
             GF_HIP(hipStreamSynchronize(st));
         };
-        enqueue_tail();
+        // The whole stage, schedule to copies: no allocation, no host wait.
+        auto enqueue = [&]() {
+            // Schedule (gpu_graph.cu:12485-12493) on the device.
+            gf::SchedArgs sa{};
+            sa.Q = Q; sa.P = ix->P; sa.postfilter = opts->postfilter; sa.counts = b->counts.p; sa.little = b->little.p;
+            sa.sched = b->sched.p; sa.tot = tot + 8; sa.ranges = tot + 12;
+            GF_HIP(gf::launch_reset_results(Q, K, b->out_ids.p, b->out_dist.p, b->counters.p, st));
+            GF_HIP(gf::launch_sched(sa, st));
+            GF_HIP(gf::launch_stamp(stamp + 0, st));
+            gf::TravArgs at = a;
+            at.srange = tot + 12;
+            GF_HIP(gf::launch_traverse(ix->rs, at, lds, Q, st));
+            GF_HIP(gf::launch_stamp(stamp + 1, st));
+            if (gemm) {
+                launch_gemm();
+            } else {
+                gf::TravArgs ab = a;
+                ab.srange = tot + 14;
+                GF_HIP(gf::launch_bruteforce(ix->rs, ab, Q, st));
+            }
+            GF_HIP(gf::launch_stamp(stamp + 2, st));
+            enqueue_copies();
+        };
+        // From a batch's second search on, the stage runs as a HIP graph,
+        // captured once per layout (buffers, options, route) and replayed:
+        // one launch instead of some twenty, no gaps between the kernels.
+        const uint64_t key[] = {uint64_t(L), K, rl, opts->postfilter, uint64_t(gemm), uint64_t(b->bf_all),
+                                uint64_t(b->qcap), uint64_t(stats != nullptr), uint64_t(dists != nullptr),
+                                uint64_t(uintptr_t(b->part.p)), uint64_t(uintptr_t(b->items.p)),
+                                uint64_t(uintptr_t(b->bq.p)), b->pair_cap, uint64_t(uintptr_t(b->out_ids.p)),
+                                uint64_t(uintptr_t(b->counters.p)), uint64_t(uintptr_t(b->sched.p)),
+                                uint64_t(uintptr_t(b->h_ids.p)), uint64_t(uintptr_t(b->h_dist.p)),
+                                uint64_t(uintptr_t(b->stats.p)), uint64_t(uintptr_t(b->bfmask.p)),
+                                uint64_t(uintptr_t(b->entry.p)), uint64_t(uintptr_t(b->sitems.p)),
+                                uint64_t(uintptr_t(b->out_dist.p)), uint64_t(uintptr_t(b->selcount.p)),
+                                uint64_t(uintptr_t(b->cells.p)), uint64_t(uintptr_t(b->gbound.p)),
+                                uint64_t(uintptr_t(b->scnt.p)), uint64_t(uintptr_t(b->rq.p)),
+                                uint64_t(uintptr_t(b->bcnt.p)), uint64_t(uintptr_t(b->h_tot.p)),
+                                uint64_t(uintptr_t(b->stamps.p)), uint64_t(uintptr_t(b->h_stamps.p))};
+        b->run_stage(std::vector<uint64_t>(std::begin(key), std::end(key)), st, enqueue);
+        GF_HIP(hipStreamSynchronize(st));
         const uint32_t* dt = b->h_tot.p;
         if (gemm && !dt[3]) {
             // the pair lists outgrew their buffers: grow them and run the brute force again
             b->alloc_pairs(size_t(dt[2]) + dt[2] / 4 + 1024, K, Q, NS, size_t(NS) + ix->ntile / gf::kBfMaxItemTiles + 1);
-            GF_HIP(hipEventRecord(ev[1], st));
+            GF_HIP(gf::launch_stamp(stamp + 1, st));
             launch_gemm();
-            GF_HIP(hipEventRecord(ev[2], st));
+            GF_HIP(gf::launch_stamp(stamp + 2, st));
             enqueue_tail();
             GF_REQUIRE(dt[3], GF_E_STATE, "brute-force schedule does not fit after growing");
         }
@@ -982,15 +1008,18 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         if (dists) std::memcpy(dists, b->h_dist.p, nr * sizeof(float));
         if (stats) {
             float t_tr = 0, t_bf = 0, t_g = 0;
-            GF_HIP(hipEventElapsedTime(&t_tr, ev[0], ev[1]));
-            GF_HIP(hipEventElapsedTime(&t_bf, ev[1], ev[2]));
-            if (gemm) GF_HIP(hipEventElapsedTime(&t_g, evg[0], evg[1]));
+            const uint64_t* ts = b->h_stamps.p;
+            const double tick_ms = 1.0 / double(ix->wclk_khz);
+            t_tr = float(double(ts[1] - ts[0]) * tick_ms);
+            t_bf = float(double(ts[2] - ts[1]) * tick_ms);
+            if (gemm) t_g = float(double(ts[4] - ts[3]) * tick_ms);
             const unsigned long long* sm = b->h_stats.p;
             std::memset(stats, 0, sizeof(*stats));
             stats->ms_traverse = t_tr;
             stats->ms_bruteforce = t_bf;
             stats->ms_total = double(t_tr) + double(t_bf);
             stats->ms_bf_kernel = t_g;
+            stats->graph = b->graph_replayed ? 1u : 0u;
             stats->q_traverse = dt[8];
             stats->q_bruteforce = dt[9];
             stats->q_empty = dt[10];

@@ -980,6 +980,12 @@ __global__ void k_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_
     little[q] = (n > 0 && all) ? n : 0u;
 }
 
+// The device wall clock (constant rate, hipDeviceAttributeWallClockRate).
+__global__ void k_stamp(uint64_t* t) {
+    const uint64_t now = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) *t = now;
+}
+
 __global__ void k_zero_u32(uint32_t* x, uint32_t n) {
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) x[i] = 0;
 }
@@ -2494,6 +2500,17 @@ hipError_t launch_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t*
 hipError_t launch_bfseed(const BfSeedArgs& a, uint32_t Q, hipStream_t st) {
     if (!Q || !a.qcap) return hipSuccess;
     hipLaunchKernelGGL(k_bfseed, dim3((Q + 3) / 4), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_stamp(uint64_t* t, hipStream_t st) {
+    hipLaunchKernelGGL(k_stamp, dim3(1), dim3(64), 0, st, t);
+    return hipGetLastError();
+}
+
+hipError_t launch_zero_u32(uint32_t* x, uint32_t n, hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(256), 0, st, x, n);
     return hipGetLastError();
 }
 

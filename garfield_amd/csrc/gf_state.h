@@ -4,6 +4,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -179,6 +180,7 @@ struct gf_index {
     DevBuf<int8_t> vt;
     DevBuf<int32_t> tnorm;
     int ncu = 0;
+    int wclk_khz = 100000;   // rate of the device wall clock the search's timestamps read
     // Streamed index (gf_index_create_streamed / gf_index_open_streamed):
     // the per-point arrays above stay empty.
     std::unique_ptr<gf::StreamIndex> sx;
@@ -253,13 +255,14 @@ struct gf_batch {
     // Streamed search: per-batch cell lists and results.
     DevBuf<uint32_t> slist, scount, slittle, s_ids, s_ctr, note, need;
     DevBuf<float> s_dist;
-    // pinned staging of a resident search's results and its events
+    // pinned staging of a resident search's results, totals and timestamps
     gf::PinBuf<uint32_t> h_ids, h_tot;
     gf::PinBuf<float> h_dist;
     gf::PinBuf<unsigned long long> h_stats;
+    DevBuf<uint64_t> stamps;
+    gf::PinBuf<uint64_t> h_stamps;
     // Stage B ran; cdist holds the query x centre matrix of that run.
     bool ordered = false, cdist_ready = false;
-    hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
     // Around the latest stage A ([0], [1]) and stage B ([2], [3]) calls.
     hipEvent_t sev[4] = {nullptr, nullptr, nullptr, nullptr};
     bool sev_a = false, sev_b = false;
@@ -275,8 +278,66 @@ struct gf_batch {
         GF_HIP(hipEventElapsedTime(&ms, sev[i], sev[i + 1]));
         return ms;
     }
+    // The search stage as a HIP graph: captured on a batch's second search
+    // and replayed while its key (the buffers it touches, the options, the
+    // route) is unchanged.  If capture or instantiation fails the batch runs
+    // every later search eagerly.  GARFIELD_NO_GRAPH=1 turns replay off.
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    std::vector<uint64_t> gkey;
+    uint32_t nruns = 0;
+    bool graph_off = false, graph_replayed = false;
+    void drop_graph() {
+        if (gexec) (void)hipGraphExecDestroy(gexec);
+        if (graph) (void)hipGraphDestroy(graph);
+        gexec = nullptr;
+        graph = nullptr;
+        gkey.clear();
+    }
+    // Enqueues the stage on st: replays the graph, captures and launches a
+    // new one, or calls enqueue() directly.  enqueue must not allocate or
+    // wait on the host.
+    template <class F>
+    void run_stage(const std::vector<uint64_t>& key, hipStream_t st, F&& enqueue) {
+        graph_replayed = false;
+        ++nruns;
+        const char* off = std::getenv("GARFIELD_NO_GRAPH");
+        if (graph_off || nruns < 2 || (off && off[0] == '1')) {
+            enqueue();
+            return;
+        }
+        if (!(gexec && key == gkey)) {
+            drop_graph();
+            if (hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed) != hipSuccess) {
+                (void)hipGetLastError();
+                graph_off = true;
+                enqueue();
+                return;
+            }
+            bool ok = true;
+            try {
+                enqueue();
+            } catch (...) {
+                ok = false;
+            }
+            hipGraph_t g = nullptr;
+            const hipError_t e = hipStreamEndCapture(st, &g);
+            if (!ok || e != hipSuccess || !g || hipGraphInstantiate(&gexec, g, nullptr, nullptr, 0) != hipSuccess) {
+                if (g) (void)hipGraphDestroy(g);
+                gexec = nullptr;
+                (void)hipGetLastError();
+                graph_off = true;
+                enqueue();
+                return;
+            }
+            graph = g;
+            gkey = key;
+        }
+        GF_HIP(hipGraphLaunch(gexec, st));
+        graph_replayed = true;
+    }
     ~gf_batch() {
-        for (auto& e : ev) if (e) (void)hipEventDestroy(e);
+        drop_graph();
         for (auto& e : sev) if (e) (void)hipEventDestroy(e);
     }
 };

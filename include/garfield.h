@@ -187,6 +187,9 @@ typedef struct {
        gf_mark_cells_grid) and stage B (gf_order_cells) calls; 0 if none ran */
     double ms_stage_a;
     double ms_stage_b;
+    /* 1 if the search stage ran as a replayed HIP graph (a resident index's
+       second and later searches of a batch with the same buffers and options) */
+    uint32_t graph;
 } gf_search_stats;
 
 gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids /*Q*K*/,

@@ -1,0 +1,74 @@
+"""The resident search stage replayed as a HIP graph gives the eager bits.
+
+A batch's second and later searches run the stage (schedule, traversal,
+brute force, merges, statistics, result copies) as one captured graph.  Each
+case runs the stage once eagerly (GARFIELD_NO_GRAPH=1), then replays it
+several times with other eager work on the stream in between (stage A again,
+reading the cells back), and compares every replay's ids, distances and
+counters with the eager run; a change of options recaptures.
+"""
+import numpy as np
+import pytest
+
+from garfield_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _print_case(name, **kw):
+    print(f"[case] {name} " + " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def _replays(monkeypatch, cfg, ix, prefilter, Ls, reps=3, **dev_kw):
+    dev = synth.open_device_index(ix, **dev_kw)
+    b = dev.batch(cfg["queries"], cfg["lo"].astype(np.float32), cfg["hi"].astype(np.float32))
+    b.mark_cells(prefilter)
+    if ix["labels"] is not None:
+        b.order_cells(4)
+    try:
+        for L in Ls:
+            monkeypatch.setenv("GARFIELD_NO_GRAPH", "1")
+            ids0, d0, st0 = b.search(L=L, K=10, rl=10)
+            c0 = b.get_counters()
+            assert st0.graph == 0
+            monkeypatch.delenv("GARFIELD_NO_GRAPH")
+            for r in range(reps):
+                ids, d, st = b.search(L=L, K=10, rl=10)
+                c = b.get_counters()
+                assert st.graph == 1, f"L={L} run {r}: the search did not run as a graph"
+                assert np.array_equal(ids, ids0), f"L={L} replay {r}: ids differ"
+                assert np.array_equal(d.view(np.uint32), d0.view(np.uint32)), f"L={L} replay {r}: distances differ"
+                assert np.array_equal(c, c0), f"L={L} replay {r}: counters differ"
+                assert (st.q_traverse, st.q_bruteforce, st.q_empty) == (st0.q_traverse, st0.q_bruteforce,
+                                                                         st0.q_empty)
+                # eager work on the stream between replays
+                b.mark_cells(prefilter)
+                if ix["labels"] is not None:
+                    b.order_cells(4)
+                b.get_cells()
+    finally:
+        b.close()
+        dev.close()
+
+
+@pytest.mark.parametrize("prefilter", [1.0, 0.05])
+def test_graph_replay_mfma_bruteforce(monkeypatch, world_sub2, prefilter):
+    """Integer data: the MFMA brute force with its three launches and merges
+    (prefilter 1), or mixed with traversal (0.05)."""
+    cfg, ix = world_sub2
+    _print_case("graph-mfma", prefilter=prefilter)
+    _replays(monkeypatch, cfg, ix, prefilter, [32, 48])
+
+
+def test_graph_replay_traversal(monkeypatch, world32):
+    """Traversal only (prefilter 0), two L values (the second recaptures)."""
+    cfg, ix = world32
+    _print_case("graph-traverse")
+    _replays(monkeypatch, cfg, ix, 0.0, [40, 100])
+
+
+def test_graph_replay_gather_bruteforce(monkeypatch, world_gauss):
+    """Non-integer data: the gather brute force and traversal mixed."""
+    cfg, ix = world_gauss
+    _print_case("graph-gather")
+    _replays(monkeypatch, cfg, ix, 0.05, [32])
