@@ -101,12 +101,16 @@ def main():
     b = dev.batch(cfg["queries"], lo, hi)
     log(f"library index resident ({dev.device_bytes / 2**30:.2f} GiB) in {time.time() - t1:.1f}s")
 
+    out = (np.empty((Q, 10), np.uint32), np.empty((Q, 10), np.float32))
+
     def step(prefilter, L):
         # Stages A and B are enqueued without waiting; the search reports
-        # their device times after its one synchronisation.
+        # their device times after its one synchronisation.  The result
+        # arrays are reused from step to step (the host copies into pages
+        # already touched).
         b.mark_cells(prefilter, timed=False)
         b.order_cells(4, timed=False)
-        ids, dists, st = b.search(L=L, K=10, rl=10, postfilter=args.postfilter)
+        ids, dists, st = b.search(L=L, K=10, rl=10, postfilter=args.postfilter, out=out)
         return ids, dists, st, st.ms_stage_a, st.ms_stage_b
 
     def recall(ids):

@@ -301,9 +301,18 @@ class Batch:
         self._topc = topc
         return ms.value if timed else None
 
-    def search(self, L, K=10, rl=10, postfilter=1 << 30, entry_points=None):
-        ids = np.empty((self.Q, K), np.uint32)
-        dists = np.empty((self.Q, K), np.float32)
+    def search(self, L, K=10, rl=10, postfilter=1 << 30, entry_points=None, out=None):
+        """out: optional (ids, dists) arrays of shape (Q, K), uint32 and float32,
+        C-contiguous, that receive the results (a caller searching in a loop
+        reuses them instead of touching fresh pages every call)."""
+        if out is None:
+            ids = np.empty((self.Q, K), np.uint32)
+            dists = np.empty((self.Q, K), np.float32)
+        else:
+            ids, dists = out
+            for arr, dt in ((ids, np.uint32), (dists, np.float32)):
+                if arr.shape != (self.Q, K) or arr.dtype != dt or not arr.flags.c_contiguous:
+                    raise ValueError("out arrays must be C-contiguous (Q, K) uint32 and float32")
         ent = None if entry_points is None else _c(entry_points, np.uint32)
         opts = _SearchOpts(L, K, rl, min(int(postfilter), 0xFFFFFFFF), _ptr(ent))
         st = SearchStats()

@@ -1096,12 +1096,14 @@ __global__ __launch_bounds__(256) void k_centroid(const uint16_t* qh, const uint
     for (uint32_t k = 0; k < Dp; k += 32u) {
         const half8_t av = ap[k / 8u];
         const half8_t bv = bp[k / 8u];
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+        // centres as A, queries as B: the operand order of k_centroid_top,
+        // so both produce the same bits for every (query, centre)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(bv, av, acc, 0, 0, 0);
     }
-    const uint32_t col = c0 + (lane & 15u);
+    const uint32_t row = q0 + (lane & 15u);
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
-        const uint32_t row = q0 + (lane >> 4) * 4u + i;
+        const uint32_t col = c0 + (lane >> 4) * 4u + i;
         if (row < Q && col < C) dist[size_t(row) * C + col] = centre_dist(qn[row], cn[col], acc[i]);
     }
 }
@@ -1131,11 +1133,9 @@ __device__ __forceinline__ void merge4(float (&ad)[4], uint32_t (&ai)[4], const 
 
 // Stage B's nearest centres without the Q x C matrix: a workgroup takes 16
 // queries against every centre tile (each of its kCtW waves every kCtW-th
-// tile, the MFMA tiles and distances of k_centroid); lane l keeps, for each of
-// its four query rows, the 4 smallest (distance, centre) it saw (its centres
-// come in ascending order, so a later equal distance never displaces an
-// earlier one), then the lists merge across the 16 lanes of a row and the
-// waves.  Writes the first topc (<= 4) centres of each query, as the
+// tile, the MFMA tiles and distances of k_centroid); lane l keeps, for its
+// query, the 4 smallest (distance, centre) keys it saw, then the lists merge
+// across the four lanes of the query and the waves.  Writes the first topc (<= 4) centres of each query, as the
 // sequential arg-min rounds of k_order would pick them from the matrix.
 constexpr uint32_t kCtW = 4;
 __global__ __launch_bounds__(64 * kCtW) void k_centroid_top(const uint16_t* qh, const uint16_t* ch, const float* qn,
@@ -1145,63 +1145,78 @@ __global__ __launch_bounds__(64 * kCtW) void k_centroid_top(const uint16_t* qh, 
     __shared__ uint32_t si[kCtW][16][4];
     const uint32_t lane = lane_id(), wave = threadIdx.x >> 6;
     const uint32_t q0 = blockIdx.x * 16u;
-    const uint32_t r = lane & 15u, kq = (lane >> 4) * 8u;
-    const half8_t* ap = reinterpret_cast<const half8_t*>(qh + size_t(q0 + r) * Dp + kq);
-    float td[4][4], qr[4];
-    uint32_t ti[4][4];
+    const uint32_t r = lane & 15u, g = lane >> 4, kq = g * 8u;
+    // Centres are the A operand and queries the B operand: lane l holds the
+    // products of query q0 + l % 16 with centres 4 (l / 16) + i of the tile,
+    // so it keeps the top 4 of one query and only the four lanes sharing it
+    // merge at the end.
+    // The query operand stays in registers for up to kCtK k-steps of 32
+    // (256 dimensions); a tile's centre operands and norms are loaded
+    // together and waited for once.
+    constexpr uint32_t kCtK = 8;
+    const uint32_t nks = Dp / 32u;
+    const half8_t* qp = reinterpret_cast<const half8_t*>(qh + size_t(q0 + r) * Dp + kq);
+    half8_t qv[kCtK];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t row = q0 + (lane >> 4) * 4u + i;
-        qr[i] = row < Q ? qn[row] : 0.0f;
+    for (uint32_t k = 0; k < kCtK; ++k)
+        if (k < nks) qv[k] = qp[k * 4u];
+    const float qr = q0 + r < Q ? qn[q0 + r] : 0.0f;
+    float td[4];
+    uint32_t ti[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) { td[i][k] = __int_as_float(0x7F800000); ti[i][k] = 0xFFFFFFFFu; }
-    }
+    for (int k = 0; k < 4; ++k) { td[k] = __int_as_float(0x7F800000); ti[k] = 0xFFFFFFFFu; }
     for (uint32_t ct = wave; ct < Cp / 16u; ct += kCtW) {
         const uint32_t c0 = ct * 16u;
         const half8_t* bp = reinterpret_cast<const half8_t*>(ch + size_t(c0 + r) * Dp + kq);
+        half8_t cv[kCtK];
+#pragma unroll
+        for (uint32_t k = 0; k < kCtK; ++k)
+            if (k < nks) cv[k] = bp[k * 4u];
+        const float4_t cc = *reinterpret_cast<const float4_t*>(cn + c0 + g * 4u);   // cn holds Cp norms
         float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (uint32_t k = 0; k < Dp; k += 32u) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap[k / 8u], bp[k / 8u], acc, 0, 0, 0);
-        const uint32_t col = c0 + (lane & 15u);
-        if (col < C) {
-            const float cc = cn[col];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float d = centre_dist(qr[i], cc, acc[i]);
-                if (d != d) d = __int_as_float(0x7F800000);
-                bool lt[4];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) lt[k] = ckey_lt(d, col, td[i][k], ti[i][k]);
-#pragma unroll
-                for (int k = 3; k >= 1; --k) {
-                    td[i][k] = lt[k - 1] ? td[i][k - 1] : (lt[k] ? d : td[i][k]);
-                    ti[i][k] = lt[k - 1] ? ti[i][k - 1] : (lt[k] ? col : ti[i][k]);
-                }
-                if (lt[0]) { td[i][0] = d; ti[i][0] = col; }
-            }
-        }
-    }
-#pragma unroll
-    for (uint32_t m = 1; m < 16u; m <<= 1) {
+        for (uint32_t k = 0; k < kCtK; ++k)
+            if (k < nks) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(cv[k], qv[k], acc, 0, 0, 0);
+        for (uint32_t k = kCtK; k < nks; ++k)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(bp[k * 4u], qp[k * 4u], acc, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float od[4];
-            uint32_t oi[4];
+            const uint32_t col = c0 + g * 4u + uint32_t(i);
+            if (col < C) {
+                float d = centre_dist(qr, cc[i], acc[i]);
+                if (d != d) d = __int_as_float(0x7F800000);
+                // most centres lose to the current 4th: insert only past it
+                if (ckey_lt(d, col, td[3], ti[3])) {
+                    bool lt[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                od[k] = __shfl_xor(td[i][k], int(m));
-                oi[k] = uint32_t(__shfl_xor(int(ti[i][k]), int(m)));
+                    for (int k = 0; k < 4; ++k) lt[k] = ckey_lt(d, col, td[k], ti[k]);
+#pragma unroll
+                    for (int k = 3; k >= 1; --k) {
+                        td[k] = lt[k - 1] ? td[k - 1] : (lt[k] ? d : td[k]);
+                        ti[k] = lt[k - 1] ? ti[k - 1] : (lt[k] ? col : ti[k]);
+                    }
+                    if (lt[0]) { td[0] = d; ti[0] = col; }
+                }
             }
-            merge4(td[i], ti[i], od, oi);
         }
     }
-    if (r == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+    for (uint32_t m = 16; m < 64u; m <<= 1) {
+        float od[4];
+        uint32_t oi[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                sd[wave][(lane >> 4) * 4u + i][k] = td[i][k];
-                si[wave][(lane >> 4) * 4u + i][k] = ti[i][k];
-            }
+        for (int k = 0; k < 4; ++k) {
+            od[k] = __shfl_xor(td[k], int(m));
+            oi[k] = uint32_t(__shfl_xor(int(ti[k]), int(m)));
+        }
+        merge4(td, ti, od, oi);
+    }
+    if (g == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            sd[wave][r][k] = td[k];
+            si[wave][r][k] = ti[k];
+        }
     }
     __syncthreads();
     const uint32_t t = threadIdx.x;
