@@ -862,13 +862,15 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 sd.sa = sc.sa; sd.Q = Q; sd.postfilter = sc.postfilter; sd.counts = sc.counts; sd.little = sc.little;
                 sd.cells = b->cells.p; sd.lo = sc.lo; sd.hi = sc.hi; sd.bfm = sc.bfm; sd.bP = sc.bP;
                 sd.qlist = sc.qlist; sd.qrange = sc.qrange; sd.qcap = b->qcap; sd.tch = gf::kBfSeedTiles;
+                sd.itch = gf::kBfMaxItemTiles;
                 sd.scnt = b->scnt.p; sd.bq = b->bq.p; sd.nsub = b->nsub.p;
                 sd.rq = b->rq.p; sd.rseed = b->rseed.p; sd.rlo = b->rlo.p; sd.rhi = b->rhi.p;
                 GF_HIP(gf::launch_bfseed(sd, Q, st));
                 sc.scnt = b->scnt.p;
                 sc.rq = b->rq.p; sc.rseed = b->rseed.p; sc.rlo = b->rlo.p; sc.rhi = b->rhi.p;
             }
-            GF_HIP(gf::launch_bfsched(sc, false, st));
+            if (seeds) GF_HIP(gf::launch_bfsched_direct(sc, st));
+            else GF_HIP(gf::launch_bfsched(sc, false, st));
             if (!b->qcap) GF_HIP(gf::launch_scan_small(b->bcnt.p, NS, b->bstart.p, st));
             GF_HIP(gf::launch_scan_small(b->nsub.p, Q, b->part_off.p, st));
             GF_HIP(gf::launch_total(b->nsub.p, b->part_off.p, Q, uint32_t(std::min<size_t>(b->pair_cap, UINT32_MAX)), K,

@@ -220,10 +220,11 @@ struct BfSeedArgs {
     uint32_t bP;
     const uint32_t* qlist;
     const uint32_t* qrange;
-    uint32_t qcap, tch;
+    uint32_t qcap, tch;        // tch: tiles per seed item
+    uint32_t itch;             // tiles per regular item
     uint32_t* scnt;            // zeroed before
     uint32_t* bq;
-    uint32_t* nsub;
+    uint32_t* nsub;            // written: the query's seed and regular item chunks
     uint32_t* rq;              // candidate records (BfSchedArgs), Q each
     uint32_t* rseed;
     float* rlo;                // a x Q
@@ -269,6 +270,7 @@ hipError_t launch_tile_i8(const void* vec_cm, bool u8, uint32_t D, const uint32_
 hipError_t launch_note_bf(const uint32_t* tot, uint32_t* note, hipStream_t st);
 hipError_t launch_subsel(const SubSelArgs& a, hipStream_t st);
 hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st);
+hipError_t launch_bfsched_direct(const BfSchedArgs& a, hipStream_t st);   // one pass, after k_bfseed
 hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, uint32_t qcap,
                           const uint32_t* stile, uint32_t tch, uint32_t NS, uint32_t* icnt, uint32_t* ioff,
                           BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill, hipStream_t st,

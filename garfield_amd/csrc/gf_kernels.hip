@@ -1588,6 +1588,36 @@ __global__ __launch_bounds__(256) void k_bfseed(BfSeedArgs p) {
         }
     }
     const uint32_t s = key ? 0xFFFFFFFFu - uint32_t(key) : kEmpty;
+    // The query's regular pairs: every other non-empty sub-cell its range
+    // reaches in a cell its brute force scans (the pairs k_bfsched_direct
+    // lists), each in chunks of itch tiles.
+    uint32_t np = 0;
+    if (bf) {
+        // four sub-cells per lane per round, their loads issued together
+        for (uint32_t s0 = 0; s0 < sa.NS; s0 += 256u) {
+            uint32_t sz[4], t0[4], t1[4], cl[4];
+            SubBox bx[4];
+#pragma unroll
+            for (uint32_t u = 0; u < 4u; ++u) {
+                const uint32_t s2 = min(s0 + 64u * u + lane, sa.NS - 1u);
+                sz[u] = s0 + 64u * u + lane < sa.NS ? sa.ssize[s2] : 0u;
+                t0[u] = sa.stile[s2];
+                t1[u] = sa.stile[s2 + 1];
+                cl[u] = p.bfm ? sa.scell[s2] : 0u;
+                bx[u] = load_box(sa, s2);
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 4u; ++u) {
+                const uint32_t s2 = s0 + 64u * u + lane;
+                if (!sz[u] || s2 == s) continue;
+                if (p.bfm && !(p.bfm[size_t(q) * p.bP + cl[u]] & 2u)) continue;
+                if (sub_relation(bx[u], sa.a, r))
+                    np += p.itch ? (t1[u] - t0[u] + p.itch - 1u) / p.itch : 1u;
+            }
+        }
+#pragma unroll
+        for (uint32_t o = 32; o; o >>= 1) np += uint32_t(__shfl_xor(int(np), int(o)));
+    }
     if (lane == 0) {
 #pragma unroll
         for (uint32_t d = 0; d < 4; ++d)
@@ -1600,8 +1630,78 @@ __global__ __launch_bounds__(256) void k_bfseed(BfSeedArgs p) {
         if (s != kEmpty) {
             const uint32_t slot = atomicAdd(&p.scnt[s], 1u);
             p.bq[size_t(s) * p.qcap + slot] = q;
-            atomicAdd(&p.nsub[q], tile_chunks(sa.stile, s, p.tch));
         }
+        p.nsub[q] = np + (s != kEmpty ? tile_chunks(sa.stile, s, p.tch) : 0u);
+    }
+}
+
+// One-pass lists with candidate records (after k_bfseed): each sub-cell's
+// region of bq gets its inside queries after the seeds and its partial ones
+// from the back.  Waves take candidate chunks in turn and claim positions
+// with one LDS atomic per chunk and kind (the order inside a list only
+// groups queries into items; the brute force's results do not depend on
+// it); the next chunk's records load while the current one is tested.
+__global__ __launch_bounds__(256) void k_bfsched_direct(BfSchedArgs p) {
+    __shared__ uint32_t cnt[2];   // inside, partial
+    const SubArgs& sa = p.sa;
+    const uint32_t s = blockIdx.x, tid = threadIdx.x, lane = lane_id();
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (tid < 2u) cnt[tid] = 0;
+    __syncthreads();
+    if (sa.ssize[s] != 0 && *p.nbf != 0) {
+        const SubBox box = load_box(sa, s);
+        const uint32_t cell = sa.scell[s];
+        const size_t base = size_t(s) * p.qcap;
+        const uint32_t nseed = p.scnt[s];
+        const uint32_t nq = p.qrange[1] - p.qrange[0];
+        const uint32_t nch = (nq + 63u) / 64u;
+        // Four chunks per wave per round: their records load together.
+        for (uint32_t c0 = wave; c0 < nch; c0 += 16u) {
+            uint32_t rq4[4], rs4[4];
+            QRange rr4[4];
+#pragma unroll
+            for (uint32_t u = 0; u < 4u; ++u) {
+                const uint32_t c = c0 + 4u * u;
+                const uint32_t ci = ((c + s) % nch) * 64u + lane;
+                rq4[u] = kEmpty;
+                rs4[u] = kEmpty;
+                if (c < nch && ci < nq) {
+                    rq4[u] = p.rq[ci];
+                    rs4[u] = p.rseed[ci];
+#pragma unroll
+                    for (uint32_t d = 0; d < 4; ++d)
+                        if (d < sa.a) {
+                            rr4[u].l[d] = p.rlo[size_t(d) * p.Q + ci];
+                            rr4[u].h[d] = p.rhi[size_t(d) * p.Q + ci];
+                        }
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 4u; ++u) {
+                if (c0 + 4u * u >= nch) break;
+                const uint32_t q = rq4[u], sd = rs4[u];
+                const QRange r = rr4[u];
+                uint32_t rel = 0;
+                if (q != kEmpty && sd != s && (!p.bfm || (p.bfm[size_t(q) * p.bP + cell] & 2u)))
+                    rel = sub_relation(box, sa.a, r);
+                const uint64_t mi = __builtin_amdgcn_ballot_w64(rel == 2u);
+                const uint64_t mp = __builtin_amdgcn_ballot_w64(rel == 1u);
+                uint32_t bi = 0, bp = 0;
+                if (lane == 0) {
+                    if (mi) bi = atomicAdd(&cnt[0], uint32_t(__builtin_popcountll(mi)));
+                    if (mp) bp = atomicAdd(&cnt[1], uint32_t(__builtin_popcountll(mp)));
+                }
+                bi = __builtin_amdgcn_readfirstlane(bi);
+                bp = __builtin_amdgcn_readfirstlane(bp);
+                if (rel == 2u) p.bq[base + nseed + bi + lanes_below(mi)] = q;
+                if (rel == 1u) p.bq[base + p.qcap - 1u - (bp + lanes_below(mp))] = q;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        p.bcnt[s] = cnt[0] + cnt[1];
+        p.bin[s] = cnt[0];
     }
 }
 
@@ -2378,6 +2478,13 @@ hipError_t launch_subsel(const SubSelArgs& a, hipStream_t st) {
 hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st) {
     if (!a.sa.NS) return hipSuccess;
     hipLaunchKernelGGL(k_bfsched, dim3(a.sa.NS), dim3(256), 0, st, a, fill);
+    return hipGetLastError();
+}
+
+hipError_t launch_bfsched_direct(const BfSchedArgs& a, hipStream_t st) {
+    if (!a.sa.NS) return hipSuccess;
+    if (!a.qcap || !a.rq || !a.qrange || !a.scnt) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_bfsched_direct, dim3(a.sa.NS), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
