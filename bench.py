@@ -43,8 +43,9 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", choices=["headline", "small"], default="headline")
-    ap.add_argument("--workload", choices=["resident", "stream"], default="resident",
-                    help="stream: the C5-shaped out-of-core workload (a second JSON line, not the headline)")
+    ap.add_argument("--workload", choices=["resident", "stream", "build"], default="resident",
+                    help="stream: the C5-shaped out-of-core workload; build: the index builder on the "
+                         "headline index (each its own JSON line, not the headline)")
     ap.add_argument("--stream-n", type=int, default=1_000_000)
     ap.add_argument("--stream-q", type=int, default=10_000)
     ap.add_argument("--stream-budget-mb", type=int, default=64)
@@ -73,6 +74,8 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.workload == "stream":
         return stream_bench(args)
+    if args.workload == "build":
+        return build_bench(args)
 
     t0 = time.time()
     if args.config == "headline":
@@ -87,7 +90,7 @@ def main():
     log(f"data generated N={N} D={D} Q={Q} ({time.time() - t0:.1f}s)")
     t1 = time.time()
     ix = synth.build_index(cfg["vectors"], cfg["attrs"], cfg["grid"], cfg["R"], cfg["E"], cfg["C"],
-                           device="cuda")
+                           device="hip")
     log(f"index built on GPU in {time.time() - t1:.1f}s")
     lo = cfg["lo"].astype(np.float32)
     hi = cfg["hi"].astype(np.float32)
@@ -252,6 +255,78 @@ def main():
 PCIE_PEAK_GBS = 64.0   # PCIe 5.0 x16, one direction
 
 
+def build_bench(args):
+    """Index build of the headline index (1M x 128 u8, 4x4 rank-quantile
+    cells, R = 32, E = 2): a step is gf_grid_scatter plus gf_build_graphs from
+    host arrays to host arrays (uploads, int8 tiles, per-cell graphs, cross
+    edges, downloads).  The roofline is the cross-edge kernel's int8 MFMA rate
+    on its algorithmic work: D multiply-adds (2 D ops) per (point, candidate)
+    pair, N * N pairs."""
+    import garfield_amd._lib as gl
+    from garfield_amd import synth
+    cfg = synth.config_headline()
+    v = cfg["vectors"].astype(np.uint8)
+    att = cfg["attrs"].astype(np.float32)
+    N, D = v.shape
+    R, E, P = cfg["R"], cfg["E"], int(np.prod(cfg["grid"]))
+
+    def step():
+        _, _, _, gp = gl.grid_scatter(att, cfg["grid"])
+        g, x, st = gl.build_graphs(v, gp, P, R, E)
+        return gp, g, x, st
+
+    for _ in range(args.warmup):
+        step()
+    acc = dict(tiles=0.0, graph=0.0, cross=0.0)
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        gp, g, x, st = step()
+        acc["tiles"] += st.ms_tiles
+        acc["graph"] += st.ms_graph
+        acc["cross"] += st.ms_cross
+    elapsed = time.perf_counter() - t
+    K = args.steps
+    ms_cross = acc["cross"] / K
+    tops = 2.0 * st.dim * st.pairs_cross / (ms_cross * 1e-3) / 1e12
+    tops_g = 2.0 * st.dim * st.pairs_graph / (acc["graph"] / K * 1e-3) / 1e12
+    log(f"build: {elapsed * 1e3 / K:.1f} ms per step; kernels: tiles {acc['tiles'] / K:.2f} ms, graphs "
+        f"{acc['graph'] / K:.2f} ms ({tops_g:.0f} TOP/s), cross {ms_cross:.2f} ms ({tops:.0f} TOP/s)")
+    cpu = None
+    if not args.no_cpu:
+        # the oracle's exact rows (numpy, float64 BLAS dot products) for a
+        # sample of points: each row is the same work as in the full build
+        from oracle import oracle as orc
+        rng = np.random.default_rng(3)
+        S, t_cpu, done = 16, 0.0, 0
+        while t_cpu < args.cpu_seconds and done < 4096:
+            rows = rng.choice(N, S, replace=False)
+            t0 = time.perf_counter()
+            orc.cross_rows(v, gp, P, E, rows)
+            orc.graph_rows(v, gp, P, R, rows)
+            t_cpu += time.perf_counter() - t0
+            done += S
+            S *= 2
+        cpu = {"value": round(done / t_cpu, 1), "unit": "points/s", "cores": os.cpu_count(),
+               "kind": "port", "sample": f"{done} random points' cross-edge and graph rows (oracle, numpy + BLAS)"}
+    out = {
+        "metric": "index build throughput, headline index (exact per-cell kNN + cross edges), 1 MI355X",
+        "value": round(N * K / elapsed, 1), "unit": "points/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": round(elapsed * 1e3 / K, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (generated in bench.py; host arrays in and out, PCIe included)",
+        "config": {"workload": f"build: {N} x {D} u8 (integers 0-255), 2 attrs on a 4x4 rank-quantile grid, "
+                               f"R={R} exact per-cell kNN, E={E} cross edges",
+                   "N": N, "D": D, "P": P, "R": R, "E": E,
+                   "ms_tiles": round(acc["tiles"] / K, 3), "ms_graph": round(acc["graph"] / K, 3),
+                   "ms_cross": round(ms_cross, 3), "pairs_cross": st.pairs_cross, "pairs_graph": st.pairs_graph},
+        "roofline": {"bound": "mfma", "kernel": "k_knn_i8 (cross edges)", "achieved": round(tops, 1),
+                     "peak": INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
+                     "traffic": None, "ms_per_launch": round(ms_cross, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def stream_bench(args):
     """C5-shaped out-of-core search on one GPU: the index is streamed from
     pinned host memory under a device budget far below its size (config
@@ -266,7 +341,7 @@ def stream_bench(args):
     N, D = cfg["vectors"].shape
     Q = cfg["queries"].shape[0]
     amin, width = cfg["attr_min"], cfg["attr_width"]
-    ix = synth.build_index(cfg["vectors"], cfg["attrs"], cfg["grid"], cfg["R"], cfg["E"], 0, device="cuda",
+    ix = synth.build_index(cfg["vectors"], cfg["attrs"], cfg["grid"], cfg["R"], cfg["E"], 0, device="hip",
                            arith=(amin, width))
     lo = cfg["lo"].astype(np.float32)
     hi = cfg["hi"].astype(np.float32)

@@ -71,6 +71,14 @@ class SearchStats(C.Structure):
         return {name: getattr(self, name) for name, _ in self._fields_}
 
 
+class BuildStats(C.Structure):
+    _fields_ = [("ms_tiles", C.c_double), ("ms_graph", C.c_double), ("ms_cross", C.c_double),
+                ("pairs_graph", C.c_uint64), ("pairs_cross", C.c_uint64), ("dim", C.c_uint32)]
+
+    def as_dict(self):
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
 _SYMBOLS = {
     "gf_index_open": [C.POINTER(_Paths), C.POINTER(_OpenOpts), C.POINTER(C.c_void_p)],
     "gf_index_create": [C.POINTER(_Host), C.POINTER(_OpenOpts), C.POINTER(C.c_void_p)],
@@ -94,6 +102,10 @@ _SYMBOLS = {
     "gf_f2h": [C.c_void_p, C.c_size_t, C.c_float, C.c_void_p],
     "gf_row_norms_f16": [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p],
     "gf_entry_points": [C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p],
+    "gf_grid_scatter": [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                        C.c_void_p],
+    "gf_build_graphs": [C.c_void_p, C.c_int32, C.c_uint32, C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32,
+                        C.c_uint32, C.c_int32, C.c_void_p, C.c_void_p, C.POINTER(BuildStats)],
     "gf_status_str": [C.c_int32],
     "gf_last_error": [],
 }
@@ -364,3 +376,47 @@ def entry_points(N, P, R):
     out = np.empty(R, np.uint32)
     _check(load().gf_entry_points(N, P, R, _ptr(out)))
     return out
+
+
+def grid_scatter(attrs, grid):
+    """grid_scatter_V2 (indexbuild/tools.py:88-125) in the library: returns
+    (l_q, r_q, pid_lists, global_pid); l_q / r_q are lists of per-attribute
+    float32 arrays (attribute values are integers held as floats)."""
+    att = _c(attrs, np.float32)
+    if att.ndim != 2:
+        raise GarfieldError(1, "attrs must be N x a")
+    n, a = att.shape
+    g = _c(grid, np.uint32)
+    if g.shape != (a,):
+        raise GarfieldError(1, "grid must hold one size per attribute")
+    lq = np.empty(int(g.sum()), np.float32)
+    rq = np.empty(int(g.sum()), np.float32)
+    pl = np.empty((a, n), np.uint32)
+    gp = np.empty(n, np.uint32)
+    _check(load().gf_grid_scatter(_ptr(att), n, a, _ptr(g), _ptr(lq), _ptr(rq), _ptr(pl), _ptr(gp)))
+    cut = np.cumsum(g)[:-1]
+    return np.split(lq, cut), np.split(rq, cut), list(pl), gp
+
+
+def build_graphs(vectors, global_pid, P, R, E, device=0, graphs=True, cross=True):
+    """Exact per-cell graphs (N x R, cell-major) and cross-cell graph
+    (N x P*E, point-id order) on the GPU; returns (graphs, cross, BuildStats)
+    with None for a graph not asked for.  vectors: uint8, or float32 holding
+    integers in [0, 255]."""
+    v = np.asarray(vectors)
+    if v.ndim != 2:
+        raise GarfieldError(1, "vectors must be N x D")
+    if v.dtype == np.uint8:
+        v, vt = np.ascontiguousarray(v), VEC_U8
+    else:
+        v, vt = _c(v, np.float32), VEC_F32
+    n, d = v.shape
+    gp = _c(global_pid, np.uint32)
+    if gp.shape != (n,):
+        raise GarfieldError(1, "global_pid must hold one cell per vector")
+    g = np.empty((n, R), np.uint32) if graphs else None
+    x = np.empty((n, P * E), np.uint32) if cross else None
+    st = BuildStats()
+    _check(load().gf_build_graphs(_ptr(v), vt, n, d, _ptr(gp), P, R if graphs else 0, E if cross else 0,
+                                  device, _ptr(g), _ptr(x), C.byref(st)))
+    return g, x, st

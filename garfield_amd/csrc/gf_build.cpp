@@ -1,0 +1,229 @@
+// Index builder of libgarfield.so: the rank-quantile grid and the exact
+// per-cell and cross-cell graphs of a GMG index, in the layouts
+// gf_index_create (and the index files) take.
+//
+// The reference builds these with Python scripts over cuVS: grid_scatter_V2
+// (indexbuild/tools.py:88-125) for the grid, a CAGRA graph per cell
+// (indexbuild/cagra_build.py:94-127, cell-local ids) and, for the cross-cell
+// graph, a CAGRA search of every point against every cell's index
+// (indexbuild/global_graph_build.py:106-176, local ids, own cell included).
+// Here both graphs are exact: the distances are integer dot products on the
+// int8 MFMA units (k_knn_i8) over the brute force's tile layout, and every
+// list is ordered by (squared distance, cell-local id).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <numeric>
+#include <vector>
+
+#include "gf_state.h"
+
+namespace gf {
+
+void grid_scatter(const float* attrs, uint32_t N, uint32_t a, const uint32_t* grid, float* l_q, float* r_q,
+                  uint32_t* pid_lists, uint32_t* global_pid) {
+    GF_REQUIRE(attrs && grid && N > 0 && a > 0, GF_E_ARG, "grid_scatter: empty input");
+    uint64_t P = 1;
+    for (uint32_t d = 0; d < a; ++d) {
+        GF_REQUIRE(grid[d] > 0, GF_E_ARG, "grid_scatter: a grid dimension is 0");
+        const uint64_t avg = (uint64_t(N) + grid[d] - 1) / grid[d];
+        // the last cell's first rank must exist (tools.py:101 indexes it)
+        GF_REQUIRE((grid[d] - 1) * avg < N, GF_E_ARG, "grid_scatter: more cells than the points can fill");
+        P *= grid[d];
+        GF_REQUIRE(P <= 0x7FFFFFFFu, GF_E_ARG, "grid_scatter: too many cells");
+    }
+    std::vector<uint32_t> order(N), idx(size_t(a) * N);
+    std::vector<float> col(N);
+    uint32_t qoff = 0;
+    for (uint32_t d = 0; d < a; ++d) {
+        for (uint32_t i = 0; i < N; ++i) col[i] = attrs[size_t(i) * a + d];
+        std::iota(order.begin(), order.end(), 0u);
+        // stable argsort (tools.py:98): equal values keep point-id order
+        std::stable_sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) { return col[x] < col[y]; });
+        const uint32_t g = grid[d];
+        const uint32_t avg = uint32_t((uint64_t(N) + g - 1) / g);
+        for (uint32_t j = 0; j < g; ++j) {
+            const uint32_t s = j * avg, e = j + 1 < g ? (j + 1) * avg : N;
+            for (uint32_t r = s; r < e; ++r) idx[size_t(d) * N + order[r]] = j;
+            if (l_q) l_q[qoff + j] = col[order[s]];
+            if (r_q) r_q[qoff + j] = col[order[e - 1]];
+        }
+        qoff += g;
+    }
+    if (pid_lists) std::memcpy(pid_lists, idx.data(), idx.size() * sizeof(uint32_t));
+    if (global_pid) {
+        // row-major cell id, the last attribute fastest (tools.py:111-120)
+        for (uint32_t i = 0; i < N; ++i) {
+            uint64_t pid = 0;
+            for (uint32_t d = 0; d < a; ++d) pid = pid * grid[d] + idx[size_t(d) * N + i];
+            global_pid[i] = uint32_t(pid);
+        }
+    }
+}
+
+void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, const uint32_t* global_pid,
+                  uint32_t P, uint32_t R, uint32_t E, int32_t device, uint32_t* cell_graphs, uint32_t* cross,
+                  gf_build_stats* stats) {
+    GF_REQUIRE(vectors && global_pid && N > 0 && D > 0 && P > 0, GF_E_ARG, "build_graphs: empty input");
+    GF_REQUIRE(vec_dtype == GF_VEC_F32 || vec_dtype == GF_VEC_U8, GF_E_ARG,
+               "build_graphs: vectors must be GF_VEC_F32 or GF_VEC_U8");
+    GF_REQUIRE(!cell_graphs || (R > 0 && R + 1 <= kKnnKMax), GF_E_UNSUPPORTED,
+               "build_graphs: degree R must be in [1, " + std::to_string(kKnnKMax - 1) + "]");
+    GF_REQUIRE(!cross || (E > 0 && E <= kKnnKMax), GF_E_UNSUPPORTED,
+               "build_graphs: E must be in [1, " + std::to_string(kKnnKMax) + "]");
+    GF_REQUIRE(uint64_t(N) * P * (cross ? E : 0) < (uint64_t(1) << 40), GF_E_UNSUPPORTED,
+               "build_graphs: cross-cell graph too large");
+    const uint32_t Dp = round_up(D, 64);
+    GF_REQUIRE(Dp <= 256, GF_E_UNSUPPORTED, "build_graphs: dimension above 256");
+    const uint32_t KS = Dp / 64;
+
+    // Vectors as u8 rows of Dp (padding 128 is 0 after the -128 shift and
+    // adds nothing to norms or dot products); float input must hold integers
+    // in [0, 255], the data the int8 distances are exact for.
+    std::vector<uint8_t> v8(size_t(N) * Dp, uint8_t(128));
+    if (vec_dtype == GF_VEC_U8) {
+        const uint8_t* s = static_cast<const uint8_t*>(vectors);
+        for (uint32_t i = 0; i < N; ++i) std::memcpy(&v8[size_t(i) * Dp], s + size_t(i) * D, D);
+    } else {
+        const float* s = static_cast<const float*>(vectors);
+        for (uint32_t i = 0; i < N; ++i)
+            for (uint32_t k = 0; k < D; ++k) {
+                const float x = s[size_t(i) * D + k];
+                GF_REQUIRE(x >= 0.0f && x <= 255.0f && x == std::floor(x), GF_E_UNSUPPORTED,
+                           "build_graphs: vectors must be integers in [0, 255]");
+                v8[size_t(i) * Dp + k] = uint8_t(x);
+            }
+    }
+
+    // Cells: members in ascending point id (the cell-local id order of the
+    // index), each cell padded to whole 16-point tiles.
+    std::vector<uint32_t> size(P, 0), coff(P + 1, 0), ctile(P + 1, 0);
+    for (uint32_t i = 0; i < N; ++i) {
+        GF_REQUIRE(global_pid[i] < P, GF_E_ARG, "build_graphs: global_pid out of range");
+        ++size[global_pid[i]];
+    }
+    for (uint32_t c = 0; c < P; ++c) {
+        coff[c + 1] = coff[c] + size[c];
+        ctile[c + 1] = ctile[c] + (size[c] + 15) / 16;
+    }
+    const uint32_t ntile = ctile[P];
+    std::vector<uint32_t> trow(size_t(ntile) * 16, 0xFFFFFFFFu), fill(P, 0);
+    for (uint32_t i = 0; i < N; ++i) {
+        const uint32_t c = global_pid[i];
+        trow[size_t(ctile[c]) * 16 + fill[c]++] = i;
+    }
+    // Items: groups of four query tiles of a cell; the graph pass pairs each
+    // with its own cell, the cross pass with every non-empty cell, target
+    // cell outermost so that concurrent waves stream the same candidates.
+    std::vector<KnnItem> gitems, citems;
+    for (uint32_t c = 0; c < P; ++c)
+        for (uint32_t t = ctile[c]; t < ctile[c + 1]; t += 4) gitems.push_back(KnnItem{t, c, c});
+    if (cross) {
+        citems.reserve(gitems.size() * P);
+        for (uint32_t tc = 0; tc < P; ++tc) {
+            if (!size[tc]) continue;
+            for (const KnnItem& g : gitems) citems.push_back(KnnItem{g.qtile, g.qcell, tc});
+        }
+    }
+
+    GF_HIP(hipSetDevice(device));
+    int ncu = 0;
+    GF_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
+    hipStream_t st = nullptr;
+    hipEvent_t ev[4] = {};
+    struct Guard {
+        hipStream_t& st;
+        hipEvent_t* ev;
+        ~Guard() {
+            for (int i = 0; i < 4; ++i)
+                if (ev[i]) (void)hipEventDestroy(ev[i]);
+            if (st) (void)hipStreamDestroy(st);
+        }
+    } guard{st, ev};
+    GF_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    for (auto& e : ev) GF_HIP(hipEventCreate(&e));
+
+    DevBuf<uint8_t> dvec;
+    DevBuf<uint32_t> dtrow, dctile, dcoff, dout_g, dout_c;
+    DevBuf<int8_t> vt;
+    DevBuf<int32_t> tnorm;
+    DevBuf<KnnItem> dgi, dci;
+    dvec.upload(v8);
+    dtrow.upload(trow);
+    dctile.upload(ctile);
+    dcoff.upload(coff);
+    dgi.upload(gitems);
+    dci.upload(citems);
+    vt.alloc(size_t(ntile) * KS * 1024);
+    tnorm.alloc(size_t(ntile) * 32);
+    if (cell_graphs) dout_g.alloc(size_t(N) * R);
+    if (cross) {
+        dout_c.alloc(size_t(N) * P * E);
+        // rows into empty cells are never written by a kernel: zero them
+        GF_HIP(hipMemsetAsync(dout_c.p, 0, dout_c.bytes(), st));
+    }
+
+    GF_HIP(hipEventRecord(ev[0], st));
+    GF_HIP(launch_tile_i8(dvec.p, true, Dp, dtrow.p, 0, ntile, vt.p, tnorm.p, st));
+    GF_HIP(hipEventRecord(ev[1], st));
+    // Candidates stream in chunks of about 1 MiB of tiles per target cell, one
+    // launch per chunk, so that an XCD's share of a launch (items of one or
+    // two target cells) keeps its chunk in L2; the keys carry over between
+    // launches in `state`.
+    const uint32_t ctiles = 1024 / KS;
+    uint32_t tmax = 0;
+    for (uint32_t c = 0; c < P; ++c) tmax = std::max(tmax, ctile[c + 1] - ctile[c]);
+    const uint32_t nchunk = (tmax + ctiles - 1) / ctiles;
+    DevBuf<uint64_t> state;
+    state.alloc(std::max(cell_graphs ? size_t(N) * (R + 1) : 0, cross ? size_t(N) * P * E : 0));
+    KnnArgs ka{};
+    ka.vt = vt.p;
+    ka.tnorm = tnorm.p;
+    ka.trow = dtrow.p;
+    ka.ctile = dctile.p;
+    ka.coff = dcoff.p;
+    ka.P = P;
+    ka.ctiles = ctiles;
+    ka.state = state.p;
+    if (cell_graphs) {
+        ka.items = dgi.p;
+        ka.nitems = uint32_t(gitems.size());
+        ka.K = R + 1;
+        ka.R = R;
+        ka.out = dout_g.p;
+        for (ka.chunk = 0; ka.chunk < nchunk; ++ka.chunk) GF_HIP(launch_knn_i8(ka, KS, uint32_t(ncu), st));
+    }
+    GF_HIP(hipEventRecord(ev[2], st));
+    if (cross) {
+        GF_REQUIRE(citems.size() < 0xFFFFFFFFull, GF_E_UNSUPPORTED, "build_graphs: too many cross items");
+        ka.items = dci.p;
+        ka.nitems = uint32_t(citems.size());
+        ka.K = E;
+        ka.R = 0;
+        ka.out = dout_c.p;
+        for (ka.chunk = 0; ka.chunk < nchunk; ++ka.chunk) GF_HIP(launch_knn_i8(ka, KS, uint32_t(ncu), st));
+    }
+    GF_HIP(hipEventRecord(ev[3], st));
+    GF_HIP(hipStreamSynchronize(st));
+    if (cell_graphs) GF_HIP(hipMemcpy(cell_graphs, dout_g.p, dout_g.bytes(), hipMemcpyDeviceToHost));
+    if (cross) GF_HIP(hipMemcpy(cross, dout_c.p, dout_c.bytes(), hipMemcpyDeviceToHost));
+    if (stats) {
+        float ms = 0;
+        GF_HIP(hipEventElapsedTime(&ms, ev[0], ev[1]));
+        stats->ms_tiles = ms;
+        GF_HIP(hipEventElapsedTime(&ms, ev[1], ev[2]));
+        stats->ms_graph = ms;
+        GF_HIP(hipEventElapsedTime(&ms, ev[2], ev[3]));
+        stats->ms_cross = ms;
+        uint64_t gp = 0, cp = 0;
+        for (uint32_t c = 0; c < P; ++c) gp += uint64_t(size[c]) * size[c];
+        for (uint32_t c = 0; c < P; ++c) cp += uint64_t(N) * size[c];
+        stats->pairs_graph = cell_graphs ? gp : 0;
+        stats->pairs_cross = cross ? cp : 0;
+        stats->dim = Dp;
+    }
+}
+
+}  // namespace gf

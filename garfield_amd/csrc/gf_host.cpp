@@ -1174,6 +1174,19 @@ gf_status gf_row_norms_f16(const uint16_t* x, uint32_t n, uint32_t D, float* out
     });
 }
 
+gf_status gf_grid_scatter(const float* attrs, uint32_t N, uint32_t a, const uint32_t* grid_shape, float* l_q,
+                          float* r_q, uint32_t* pid_lists, uint32_t* global_pid) {
+    return run_guarded([&] { gf::grid_scatter(attrs, N, a, grid_shape, l_q, r_q, pid_lists, global_pid); });
+}
+
+gf_status gf_build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D,
+                          const uint32_t* global_pid, uint32_t P, uint32_t R, uint32_t E, int32_t device,
+                          uint32_t* cell_graphs, uint32_t* cross, gf_build_stats* stats) {
+    return run_guarded([&] {
+        gf::build_graphs(vectors, vec_dtype, N, D, global_pid, P, R, E, device, cell_graphs, cross, stats);
+    });
+}
+
 gf_status gf_entry_points(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
     return run_guarded([&] {
         GF_REQUIRE(out && P >= 1 && N >= P, GF_E_ARG, "invalid arguments");

@@ -128,6 +128,33 @@ struct BfGemmArgs {
     uint32_t irange;
     const uint32_t* nitems_a;
 };
+// Index build: exact nearest neighbours over int8 tiles (k_knn_i8).
+constexpr uint32_t kKnnKMax = 72;   // largest K (R + 1 for graphs, E for cross edges)
+struct KnnItem {
+    uint32_t qtile;   // first of up to four query tiles (64 points) of cell qcell
+    uint32_t qcell;
+    uint32_t tcell;   // the cell whose points are the candidates
+};
+struct KnnArgs {
+    const int8_t* vt;        // tiles of every cell, cell-major, members in id order
+    const int32_t* tnorm;    // per tile [-floor(|x'|^2 / 2) x 16][|x'|^2 x 16]
+    const uint32_t* trow;    // per tile row: point id, 0xFFFFFFFF = padding
+    const uint32_t* ctile;   // P + 1: first tile of each cell
+    const uint32_t* coff;    // P + 1: first member (cell-major position) of each cell
+    const KnnItem* items;
+    uint32_t nitems;
+    uint32_t K;              // keys kept per query
+    uint32_t R;              // > 0: graph rows of R ids (K = R + 1); 0: cross edges
+    uint32_t P;
+    uint32_t* out;           // graph: rows in cell-major order; cross: N x P x K
+    // A launch covers tiles [chunk * ctiles, (chunk + 1) * ctiles) of each
+    // target cell; the keys found so far carry over in state (graph: N x K,
+    // cross: N x P x K, cell-major rows).
+    uint32_t chunk, ctiles;
+    uint64_t* state;
+};
+hipError_t launch_knn_i8(const KnnArgs& a, uint32_t KS, uint32_t ncu, hipStream_t st);
+
 struct BfFinalArgs {
     uint32_t* gbound;          // optional: per query the bound the items reached
     const uint32_t* bfq;       // schedule

@@ -2327,6 +2327,233 @@ __global__ __launch_bounds__(64) void k_q_i8(const float* q, uint32_t D, int8_t*
     if (lane == 0) nq[r] = n;
 }
 
+// ------------------------------------------------------------ index build
+// Exact nearest neighbours for the index builder: the per-cell graphs (the
+// cell's own points, self included here and dropped when written) and the
+// cross-cell graph (every point against every cell).  One item is a group of
+// four query tiles (64 points, the MFMA B operand held in registers) of one
+// cell against every tile of a target cell (the A operand, streamed); the
+// tile layout is the brute force's (k_tile_i8).  Candidates pass a
+// per-query accumulator threshold, queue in LDS and are merged by the query's
+// owner lane into a register top-K of (distance << 32 | cell-local id) keys:
+// the result is the K smallest keys, ties broken by the smaller local id.
+template <int KS, int KT, int NB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KT > 40 ? 1 : 2))) void k_knn_i8(KnnArgs p) {
+    __shared__ uint64_t s_buf[4][kQB * kBfBufQ];
+    __shared__ uint32_t s_cnt[4][kQB];
+    __shared__ int32_t s_tp[4][kQB];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
+    uint64_t* buf = s_buf[wave];
+    uint32_t* cnt = s_cnt[wave];
+    int32_t* stp = s_tp[wave];
+    const uint32_t K = p.K;
+    const uint32_t col = lane & 15u, grp = lane >> 4;
+    // Persistent waves, XCD-aware: workgroups go round-robin to the 8 XCDs
+    // and XCD x works through the x-th eighth of the item list, whose items
+    // share few target cells, so that this launch's chunk of their tiles
+    // stays in that XCD's L2.
+    const uint32_t nwg = gridDim.x, xcd = blockIdx.x & 7u, k8 = blockIdx.x >> 3;
+    const uint32_t nwg_x = (nwg - xcd + 7u) >> 3;
+    const uint32_t i_lo = uint32_t(uint64_t(p.nitems) * xcd / 8u);
+    const uint32_t i_hi = uint32_t(uint64_t(p.nitems) * (xcd + 1u) / 8u);
+    for (uint32_t item = i_lo + k8 * 4u + wave; item < i_hi; item += nwg_x * 4u) {
+        const KnnItem it = p.items[item];
+        const uint32_t qc = it.qcell, tc = it.tcell;
+        const uint32_t qt = it.qtile, qt_end = min(qt + 4u, p.ctile[qc + 1]);
+        // candidates: this launch's chunk of the target cell's tiles
+        const uint32_t t0 = p.ctile[tc], tn = p.ctile[tc + 1];
+        const uint32_t tb = t0 + p.chunk * p.ctiles;
+        if (tb >= tn) continue;
+        const uint32_t t1 = min(tn, tb + p.ctiles);
+        const bool first = p.chunk == 0, last = t1 == tn;
+        const uint32_t q_lid = (qt - p.ctile[qc]) * 16u + lane;   // the owner's query, cell-local
+        const bool own_live = q_lid < p.coff[qc + 1] - p.coff[qc];
+        const uint32_t own_t = own_live ? qt + grp : qt;
+        const int32_t own_nq = p.tnorm[size_t(own_t) * 32u + 16u + col];
+        // the query's keys so far (earlier chunks), cell-major row order
+        uint64_t* kst = p.state + ((size_t(p.coff[qc]) + q_lid) * (p.R ? 1u : p.P) + (p.R ? 0u : tc)) * p.K;
+        uint64_t tk[KT];
+#pragma unroll
+        for (int k = 0; k < KT; ++k) tk[k] = own_live && !first && uint32_t(k) < K ? kst[k] : kKeySent;
+        uint64_t kth = kKeySent;
+#pragma unroll
+        for (int k = 0; k < KT; ++k)
+            if (uint32_t(k) == K - 1) kth = tk[k];
+        uint32_t own_thr = kth != kKeySent ? uint32_t(kth >> 32) : 0xFFFFFFFFu;
+        wave_fence();
+        cnt[lane] = 0;
+        stp[lane] = own_live ? acc_threshold(own_nq, own_thr) : INT32_MAX;
+        wave_fence();
+        v4i32_t B[4][KS];
+        int32_t tp[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t t = qt + j < qt_end ? qt + j : qt;
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
+                B[j][k] = *reinterpret_cast<const v4i32_t*>(p.vt + (size_t(t) * KS + k) * 1024u + lane * 16u);
+            tp[j] = stp[16u * j + col];
+        }
+        auto drain = [&]() {
+            wave_fence();
+            const uint32_t n = cnt[lane];
+            if (n) {
+                uint64_t nxt = buf[lane * kBfBufQ];
+                for (uint32_t e = 0; e < n; ++e) {
+                    const uint64_t cur = nxt;
+                    if (e + 1 < n) nxt = buf[lane * kBfBufQ + e + 1];
+                    const int32_t d = own_nq + int32_t(uint32_t(cur >> 32));
+                    uint64_t c = (uint64_t(uint32_t(d)) << 32) | uint32_t(cur);
+                    if (c < kth) {
+#pragma unroll
+                        for (int k = 0; k < KT; ++k) {
+                            const bool lt = c < tk[k];
+                            const uint64_t v = tk[k];
+                            tk[k] = lt ? c : v;
+                            c = lt ? v : c;
+                        }
+#pragma unroll
+                        for (int k = 0; k < KT; ++k)
+                            if (uint32_t(k) == K - 1) kth = tk[k];
+                    }
+                }
+                cnt[lane] = 0;
+                if (kth != kKeySent && uint32_t(kth >> 32) < own_thr) {
+                    own_thr = uint32_t(kth >> 32);
+                    stp[lane] = acc_threshold(own_nq, own_thr);
+                }
+            }
+            wave_fence();
+#pragma unroll
+            for (int j = 0; j < 4; ++j) tp[j] = stp[16u * j + col];
+        };
+        // Operands of the next NB - 1 tiles are in flight while a tile is
+        // computed (a ring of NB register stages, indexed statically; a
+        // stage is refilled once its tile is done).
+        v4i32_t A[NB][KS], mh[NB], mn[NB];
+        auto load_tile = [&](int b, uint32_t t) {
+            const v4i32_t* vp = reinterpret_cast<const v4i32_t*>(p.vt + size_t(t) * KS * 1024u) + lane;
+            const int32_t* nt = p.tnorm + size_t(t) * 32u;
+#pragma unroll
+            for (int k = 0; k < KS; ++k) A[b][k] = vp[k * 64];
+            mh[b] = *reinterpret_cast<const v4i32_t*>(nt + 4u * grp);
+            mn[b] = *reinterpret_cast<const v4i32_t*>(nt + 16u + 4u * grp);
+        };
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+            if (tb + b < t1) load_tile(b, tb + b);
+        for (uint32_t ts = tb; ts < t1; ts += NB) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const uint32_t t = ts + b;
+                if (t >= t1) break;
+                v4i32_t acc[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b][0], B[j][0], mh[b], 0, 0, 0);
+#pragma unroll
+                for (int k = 1; k < KS; ++k)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b][k], B[j][k], acc[j], 0, 0, 0);
+                // any pass in the tile: one compare per column on the max of its four rows
+                bool anyl = false;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    anyl |= max(max(acc[j][0], acc[j][1]), max(acc[j][2], acc[j][3])) >= tp[j];
+                if (__builtin_amdgcn_ballot_w64(anyl)) {
+                    // The owner adds |q'|^2 to |x'|^2 - 2 q'.x' when it merges.
+                    const uint32_t lid0 = (t - t0) * 16u + 4u * grp;
+                    const v4i32_t cmh = mh[b], cmn = mn[b];
+                    bool full = false;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (acc[j][i] >= tp[j]) {
+                                const uint32_t ql = 16u * j + col;
+                                const int32_t v = cmn[i] - 2 * (acc[j][i] - cmh[i]);
+                                const uint32_t slot = atomicAdd(&cnt[ql], 1u);
+                                buf[ql * kBfBufQ + slot] = (uint64_t(uint32_t(v)) << 32) | (lid0 + uint32_t(i));
+                                full |= slot + 1u >= kBfDrainAt;
+                            }
+                    if (__builtin_amdgcn_ballot_w64(full)) drain();
+                }
+                // the stage's registers are free: load the tile NB ahead
+                if (t + NB < t1) load_tile(b, t + NB);
+            }
+        }
+        drain();
+        if (!own_live) continue;
+        if (!last) {
+#pragma unroll
+            for (int k = 0; k < KT; ++k)
+                if (uint32_t(k) < K) kst[k] = tk[k];
+            continue;
+        }
+        if (p.R) {
+            // per-cell graph row of the query: its R nearest other points
+            uint32_t* row = p.out + (size_t(p.coff[qc]) + q_lid) * p.R;
+            uint32_t o = 0, first = q_lid;
+#pragma unroll
+            for (int k = 0; k < KT; ++k) {
+                const uint32_t lid = uint32_t(tk[k]);
+                if (uint32_t(k) < K && tk[k] != kKeySent && lid != q_lid && o < p.R) {
+                    if (o == 0) first = lid;
+                    row[o++] = lid;
+                }
+            }
+            for (; o < p.R; ++o) row[o] = first;   // fewer than R others: repeat the nearest
+        } else {
+            // cross-cell edges of the query's point into the target cell
+            const uint32_t pid = p.trow[size_t(own_t) * 16u + col];
+            uint32_t* row = p.out + (size_t(pid) * p.P + tc) * K;
+            const uint32_t first = uint32_t(tk[0]);
+#pragma unroll
+            for (int k = 0; k < KT; ++k)
+                if (uint32_t(k) < K) row[k] = tk[k] != kKeySent ? uint32_t(tk[k]) : first;
+        }
+    }
+}
+
+}  // namespace
+
+template <int KS, int KT, int NB = 1>
+static hipError_t launch_knn_i8_t(const KnnArgs& a, uint32_t ncu, hipStream_t st) {
+    static int per_cu = 0;
+    if (!per_cu) {
+        int n = 0;
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_knn_i8<KS, KT, NB>, 256, 0);
+        if (e != hipSuccess) return e;
+        per_cu = n > 0 ? n : 1;
+    }
+    // every XCD (workgroup id mod 8) needs a workgroup: it owns an eighth of the items
+    if (a.nitems == 0) return hipSuccess;
+    const uint32_t need = ((a.nitems + 3u) / 4u + 7u) / 8u * 8u;
+    const uint32_t grid = max(8u, min(ncu * uint32_t(per_cu), need));
+    hipLaunchKernelGGL((k_knn_i8<KS, KT, NB>), dim3(grid), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_knn_i8(const KnnArgs& a, uint32_t KS, uint32_t ncu, hipStream_t st) {
+    if (a.K == 0 || a.K > kKnnKMax || ncu == 0 || (a.R && a.K != a.R + 1)) return hipErrorInvalidValue;
+#define KNN(KS_)                                                          \
+    if (KS == KS_) {                                                      \
+        if (a.K <= 4) return launch_knn_i8_t<KS_, 4, 2>(a, ncu, st);     \
+        if (a.K <= 16) return launch_knn_i8_t<KS_, 16, 2>(a, ncu, st);   \
+        if (a.K <= 40) return launch_knn_i8_t<KS_, 40, 2>(a, ncu, st);   \
+        return launch_knn_i8_t<KS_, 72>(a, ncu, st);                     \
+    }
+    KNN(1)
+    KNN(2)
+    KNN(3)
+    KNN(4)
+#undef KNN
+    return hipErrorInvalidValue;
+}
+
+namespace {
+
 template <int VT, int LPR, int CPL>
 hipError_t launch_trav_t(const TravArgs& a, uint32_t lds, uint32_t grid, hipStream_t st) {
     if (grid == 0) return hipSuccess;

@@ -375,4 +375,10 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
 // Entry-point draws (mt19937 default seed, distinct uniform_int_distribution
 // draws in [0, range), std::random_shuffle after srand(1)): the first R.
 void entry_points_draw(uint32_t range, uint32_t ndraw, uint32_t R, uint32_t* out);
+// Index builder (gf_build.cpp): the rank-quantile grid and the exact graphs.
+void grid_scatter(const float* attrs, uint32_t N, uint32_t a, const uint32_t* grid, float* l_q, float* r_q,
+                  uint32_t* pid_lists, uint32_t* global_pid);
+void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, const uint32_t* global_pid,
+                  uint32_t P, uint32_t R, uint32_t E, int32_t device, uint32_t* cell_graphs, uint32_t* cross,
+                  gf_build_stats* stats);
 }  // namespace gf

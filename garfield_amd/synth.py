@@ -225,17 +225,30 @@ def kmeans_labels(vectors, C, iters, seed, device="cpu", chunk=65536):
 
 def build_index(vectors, attrs, grid, R, E, C=0, kmeans_iters=8, seed=5, device="cpu", arith=None):
     """All index arrays, in the layout the files hold.  arith = (attr_min,
-    attr_width) builds the cells on an arithmetic grid instead of rank quantiles."""
+    attr_width) builds the cells on an arithmetic grid instead of rank quantiles.
+    device "hip": the library's builder (gf_grid_scatter and the int8 MFMA
+    gf_build_graphs, integer data only; k-means labels still via torch on the
+    GPU); else torch on that device."""
     grid = np.asarray(grid, np.int64)
     P = int(np.prod(grid))
-    if arith is None:
-        l_q, r_q, pid_lists, global_pid = grid_scatter(attrs, grid)
-    else:
+    hip = device == "hip"
+    if arith is not None:
         l_q, r_q, pid_lists, global_pid = grid_scatter_arith(attrs, grid, arith[0], arith[1])
-    members = cell_members(global_pid, P)
-    graphs = knn_cell_graphs(vectors, members, R, device=device)
-    cross = cross_edges(vectors, members, E, device=device)
-    labels = kmeans_labels(vectors, C, kmeans_iters, seed, device=device) if C else None
+    elif hip:
+        from ._lib import grid_scatter as lib_grid_scatter
+        l_q, r_q, pid_lists, global_pid = lib_grid_scatter(np.asarray(attrs, np.float32), grid)
+        global_pid = global_pid.astype(np.int32)
+    else:
+        l_q, r_q, pid_lists, global_pid = grid_scatter(attrs, grid)
+    if hip:
+        from ._lib import build_graphs
+        v = vectors if vectors.dtype == np.uint8 else np.asarray(vectors, np.float32)
+        graphs, cross, _ = build_graphs(v, global_pid, P, R, E)
+    else:
+        members = cell_members(global_pid, P)
+        graphs = knn_cell_graphs(vectors, members, R, device=device)
+        cross = cross_edges(vectors, members, E, device=device)
+    labels = kmeans_labels(vectors, C, kmeans_iters, seed, device="cuda" if hip else device) if C else None
     return dict(vectors=vectors, attrs=attrs, grid=grid.astype(np.int32), l_q=l_q, r_q=r_q,
                 pid_lists=pid_lists, global_pid=global_pid, cell_graphs=graphs, cross=cross, labels=labels,
                 P=P, R=R, E=E)

@@ -220,6 +220,45 @@ gf_status gf_row_norms_f16(const uint16_t* x, uint32_t n, uint32_t D, float* out
  * std::random_shuffle after srand(1) (this reseeds the process's rand()). */
 gf_status gf_entry_points(uint32_t N, uint32_t P, uint32_t R, uint32_t* out);
 
+/* ---- Index build: the files the reference's indexbuild/ scripts write ---- */
+
+/* grid_scatter_V2 (indexbuild/tools.py:88-125): per attribute, the points in
+ * stable ascending order of value are cut into grid_shape[d] runs of
+ * ceil(N / g) (the last run takes the rest); l_q / r_q (sum(grid) values,
+ * attribute-major, as gf_index_host) hold each run's first and last value,
+ * pid_lists (a*N, attribute-major) each point's run, and global_pid the
+ * row-major cell id (last attribute fastest).  Host code.  Any output may be
+ * NULL.  GF_E_ARG when a last run would start beyond N (the reference's
+ * script fails there). */
+gf_status gf_grid_scatter(const float* attrs /*N*a*/, uint32_t N, uint32_t a, const uint32_t* grid_shape,
+                          float* l_q, float* r_q, uint32_t* pid_lists, uint32_t* global_pid);
+
+typedef struct {
+    double ms_tiles;        /* int8 tile build */
+    double ms_graph;        /* per-cell graphs (kernel time) */
+    double ms_cross;        /* cross-cell graph (kernel time) */
+    uint64_t pairs_graph;   /* distances evaluated: sum of |cell|^2 */
+    uint64_t pairs_cross;   /* N * sum of |cell| */
+    uint32_t dim;           /* dimension as computed (D rounded up to 64) */
+} gf_build_stats;
+
+/* The per-cell graphs (cagra_build.py:94-127 writes the layout: rows of R
+ * cell-local ids, cells concatenated in cell order, members in ascending
+ * point id) and the cross-cell graph (global_graph_build.py:106-176: for
+ * every point, in point-id order, and every cell c, the E nearest points of
+ * c as cell-local ids, the point's own cell included) of the points'
+ * cells global_pid, by exact nearest neighbours where the reference uses
+ * CAGRA: ordered by (squared L2 distance, cell-local id); a graph row
+ * excludes the point itself; a row with fewer candidates than it holds
+ * repeats its nearest (a point alone in its cell lists itself); edges into
+ * an empty cell are 0.  vectors: N*D in point-id order, GF_VEC_U8 bytes or
+ * GF_VEC_F32 integers in [0, 255] (other data is GF_E_UNSUPPORTED); D up to
+ * 256; R + 1 and E up to 72.  cell_graphs (N*R) or cross (N*P*E) may be NULL
+ * to skip that graph.  Runs on HIP device `device`; stats may be NULL. */
+gf_status gf_build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D,
+                          const uint32_t* global_pid, uint32_t P, uint32_t R, uint32_t E, int32_t device,
+                          uint32_t* cell_graphs, uint32_t* cross, gf_build_stats* stats);
+
 const char* gf_status_str(gf_status s);
 const char* gf_last_error(void);
 

@@ -242,3 +242,131 @@ def recall(res, gt, gt_dist, res_dist_exact=None, tie_aware=False):
     rd = _c(res_dist_exact if res_dist_exact is not None else np.zeros_like(gt_dist), np.float64)
     return load().orc_recall(C.c_uint32(Q), C.c_uint32(K), _p(res), _p(gt), _p(gt_dist), _p(rd),
                              C.c_int(int(tie_aware)))
+
+
+# ------------------------------------------------------------ index build
+# Restatements of the reference's index-build scripts (numpy), the checker
+# of gf_grid_scatter / gf_build_graphs.
+
+def grid_scatter(attrs, grid):
+    """grid_scatter_V2 (indexbuild/tools.py:88-125): per attribute a stable
+    argsort (:98), runs of avg = ceil(N / g) ranks (:100-107; the last run
+    takes the rest), quantiles = the sorted values at each run's first and
+    last rank (:101-102, :108), global pid = row-major with the last attribute
+    fastest (:111-120)."""
+    attrs = np.asarray(attrs, np.float64)
+    n, a = attrs.shape
+    l_q, r_q, pid_lists = [], [], []
+    for d in range(a):
+        order = np.argsort(attrs[:, d], kind="stable")
+        srt = attrs[order, d]
+        g = int(grid[d])
+        avg = (n + g - 1) // g
+        idx = np.zeros(n, np.int64)
+        left = [j * avg for j in range(g)]
+        right = [(j + 1) * avg - 1 if j < g - 1 else n - 1 for j in range(g)]
+        for j in range(g):
+            idx[order[left[j]:right[j] + 1]] = j
+        l_q.append(srt[left])
+        r_q.append(srt[right])
+        pid_lists.append(idx)
+    factors = np.concatenate([np.cumprod(np.asarray(grid, np.int64)[::-1])[::-1][1:], [1]])
+    global_pid = sum(factors[d] * pid_lists[d] for d in range(a))
+    return l_q, r_q, pid_lists, global_pid
+
+
+def _members(global_pid, P):
+    order = np.argsort(np.asarray(global_pid), kind="stable")
+    bounds = np.concatenate([[0], np.cumsum(np.bincount(global_pid, minlength=P))])
+    return [order[bounds[c]:bounds[c + 1]] for c in range(P)]
+
+
+def _sq(x, y):
+    """Exact squared distances of integer-valued rows (int64): the dot
+    products run in float64, exact while every partial sum stays below 2^53."""
+    xi = x.astype(np.int64)
+    yi = y.astype(np.int64)
+    dots = np.rint(x.astype(np.float64) @ y.astype(np.float64).T).astype(np.int64)
+    return (xi * xi).sum(1)[:, None] + (yi * yi).sum(1)[None, :] - 2 * dots
+
+
+def knn_cell_graphs(vectors, global_pid, P, R):
+    """Per-cell graphs in the layout of cagra_build.py:94-127 (rows of R
+    cell-local ids, cells concatenated in cell order, members by ascending
+    point id), exact: each point's R nearest other points of its cell by
+    (squared distance, local id); fewer than R others repeat the nearest; a
+    point alone in its cell lists itself."""
+    v = np.asarray(vectors)
+    rows = []
+    for mem in _members(global_pid, P):
+        n = len(mem)
+        if n == 0:
+            continue
+        # (distance, local id) order as one int64 key per pair; self last
+        key = _sq(v[mem], v[mem]) * n + np.arange(n)[None, :]
+        np.fill_diagonal(key, np.iinfo(np.int64).max)
+        o = np.argsort(key, axis=1, kind="stable")[:, :max(0, min(R, n - 1))]
+        g = np.empty((n, R), np.uint32)
+        if n == 1:
+            g[:] = 0
+        else:
+            g[:, :o.shape[1]] = o
+            g[:, o.shape[1]:] = o[:, :1]
+        rows.append(g)
+    return np.concatenate(rows, 0)
+
+
+def cross_graph(vectors, global_pid, P, E):
+    """Cross-cell graph of global_graph_build.py:106-176 (row p, columns
+    c*E .. c*E+E-1: the E nearest points of cell c to point p as cell-local
+    ids, p's own cell included), exact by (squared distance, local id);
+    a cell with fewer than E points repeats the nearest; edges into an empty
+    cell are 0."""
+    v = np.asarray(vectors)
+    N = v.shape[0]
+    out = np.zeros((N, P * E), np.uint32)
+    for c, mem in enumerate(_members(global_pid, P)):
+        n = len(mem)
+        if n == 0:
+            continue
+        key = _sq(v, v[mem]) * n + np.arange(n)[None, :]
+        o = np.argsort(key, axis=1, kind="stable")[:, :min(E, n)]
+        out[:, c * E:c * E + o.shape[1]] = o
+        out[:, c * E + o.shape[1]:(c + 1) * E] = o[:, :1]
+    return out
+
+
+def graph_rows(vectors, global_pid, P, R, rows):
+    """knn_cell_graphs' rows of the points `rows` only (row i = point rows[i])."""
+    v = np.asarray(vectors)
+    gp = np.asarray(global_pid)
+    mem = _members(gp, P)
+    out = np.empty((len(rows), R), np.uint32)
+    for i, p in enumerate(rows):
+        m = mem[gp[p]]
+        n = len(m)
+        self_lid = int(np.searchsorted(m, p))
+        if n == 1:
+            out[i] = self_lid
+            continue
+        key = _sq(v[p:p + 1], v[m])[0] * n + np.arange(n)
+        key[self_lid] = np.iinfo(np.int64).max
+        o = np.argsort(key, kind="stable")[:min(R, n - 1)]
+        out[i, :len(o)] = o
+        out[i, len(o):] = o[0]
+    return out
+
+
+def cross_rows(vectors, global_pid, P, E, rows):
+    """cross_graph's rows of the points `rows` only."""
+    v = np.asarray(vectors)
+    out = np.zeros((len(rows), P * E), np.uint32)
+    for c, m in enumerate(_members(np.asarray(global_pid), P)):
+        n = len(m)
+        if n == 0:
+            continue
+        d = _sq(v[np.asarray(rows)], v[m]) * n + np.arange(n)[None, :]
+        o = np.argsort(d, axis=1, kind="stable")[:, :min(E, n)]
+        out[:, c * E:c * E + o.shape[1]] = o
+        out[:, c * E + o.shape[1]:(c + 1) * E] = o[:, :1]
+    return out

@@ -1,0 +1,157 @@
+"""Index builder, CPU side: the oracle's restatements of the reference's
+build scripts pinned by hand-computed cases and by a brute force of a
+different form (Python tuple sorts), the library's grid (host code) against
+the oracle, and the builder's argument checks (which run before any device
+call)."""
+import numpy as np
+import pytest
+
+from garfield_amd import _lib
+from garfield_amd._lib import GarfieldError
+from oracle import oracle
+
+
+# ---------------------------------------------------------------- grid
+def test_oracle_grid_hand_case():
+    # N = 5, g = 2: avg = 3; stable order of (5, 1, 3, 1, 2) is ids 1, 3, 4, 2, 0
+    att = np.array([[5, 0], [1, 1], [3, 0], [1, 1], [2, 0]])
+    l_q, r_q, pl, gp = oracle.grid_scatter(att, [2, 2])
+    assert list(pl[0]) == [1, 0, 1, 0, 0]
+    assert list(l_q[0]) == [1, 3] and list(r_q[0]) == [2, 5]
+    # attribute 1 (0, 1, 0, 1, 0): stable ranks put ids 0, 2, 4 first
+    assert list(pl[1]) == [0, 1, 0, 1, 0]
+    assert list(l_q[1]) == [0, 1] and list(r_q[1]) == [0, 1]
+    # row-major, last attribute fastest
+    assert list(gp) == [2, 1, 2, 1, 0]
+
+
+def test_oracle_grid_three_attributes_factors():
+    rng = np.random.default_rng(3)
+    att = rng.integers(0, 50, (200, 3))
+    _, _, pl, gp = oracle.grid_scatter(att, [2, 3, 4])
+    assert np.array_equal(gp, pl[0] * 12 + pl[1] * 4 + pl[2])
+    # every run but the last holds ceil(N / g) points
+    for d, g in enumerate([2, 3, 4]):
+        cnt = np.bincount(pl[d], minlength=g)
+        avg = -(-200 // g)
+        assert np.all(cnt[:-1] == avg) and cnt[-1] == 200 - avg * (g - 1)
+
+
+@pytest.mark.parametrize("n,grid,hi,seed", [(1000, [4, 4], 10000, 1), (777, [3, 5], 20, 2),
+                                            (64, [2, 2, 2], 3, 3), (10, [1], 5, 4), (300, [7], 1, 5)])
+def test_library_grid_matches_oracle(n, grid, hi, seed):
+    rng = np.random.default_rng(seed)
+    att = rng.integers(0, hi, (n, len(grid))).astype(np.float32)
+    l_q, r_q, pl, gp = _lib.grid_scatter(att, grid)
+    ol, orr, opl, ogp = oracle.grid_scatter(att, grid)
+    for d in range(len(grid)):
+        assert np.array_equal(l_q[d], ol[d]) and np.array_equal(r_q[d], orr[d])
+        assert np.array_equal(pl[d], opl[d])
+    assert np.array_equal(gp, ogp)
+
+
+def test_library_grid_rejects_unfillable_grid():
+    # N = 5, g = 4: avg = 2 and the last run would start at rank 6
+    with pytest.raises(GarfieldError) as e:
+        _lib.grid_scatter(np.arange(5, dtype=np.float32)[:, None], [4])
+    assert e.value.status == 1
+
+
+# ---------------------------------------------------------------- graphs
+def _brute_graph(v, gpid, P, R):
+    rows = []
+    for c in range(P):
+        mem = [i for i in range(len(gpid)) if gpid[i] == c]
+        for i, p in enumerate(mem):
+            cand = sorted((int(((v[p].astype(int) - v[q].astype(int)) ** 2).sum()), j)
+                          for j, q in enumerate(mem) if j != i)
+            ids = [j for _, j in cand[:R]]
+            if not ids:
+                ids = [i]
+            rows.append(ids + [ids[0]] * (R - len(ids)))
+    return np.array(rows, np.uint32)
+
+
+def _brute_cross(v, gpid, P, E):
+    out = np.zeros((len(gpid), P * E), np.uint32)
+    for c in range(P):
+        mem = [i for i in range(len(gpid)) if gpid[i] == c]
+        if not mem:
+            continue
+        for p in range(len(gpid)):
+            cand = sorted((int(((v[p].astype(int) - v[q].astype(int)) ** 2).sum()), j) for j, q in enumerate(mem))
+            ids = [j for _, j in cand[:E]]
+            out[p, c * E:(c + 1) * E] = ids + [ids[0]] * (E - len(ids))
+    return out
+
+
+def test_oracle_graph_line_hand_case():
+    # one cell, points on a line at 0, 1, 3, 7
+    v = np.array([[0], [1], [3], [7]], np.uint8)
+    g = oracle.knn_cell_graphs(v, np.zeros(4, np.int64), 1, 2)
+    assert g.tolist() == [[1, 2], [0, 2], [1, 0], [2, 1]]
+    # the same points as a second cell's members, interleaved with cell 0's
+    v2 = np.array([[0], [50], [1], [60], [3], [7]], np.uint8)
+    gp = np.array([1, 0, 1, 0, 1, 1])
+    g2 = oracle.knn_cell_graphs(v2, gp, 2, 2)
+    assert g2.tolist() == [[1, 1], [0, 0], [1, 2], [0, 2], [1, 0], [2, 1]]
+    x = oracle.cross_graph(v2, gp, 2, 2)
+    # point 0 (value 0): cell 0 = (50, 60) -> 0, 1; cell 1 = (0, 1, 3, 7) -> 0, 1
+    assert x[0].tolist() == [0, 1, 0, 1]
+    # point 3 (value 60): cell 0 -> 1 (itself), 0; cell 1 -> 3, 2
+    assert x[3].tolist() == [1, 0, 3, 2]
+
+
+def test_oracle_graph_ties_and_tiny_cells():
+    rng = np.random.default_rng(9)
+    v = rng.integers(0, 2, (40, 8)).astype(np.uint8)   # many equal distances
+    gp = np.zeros(40, np.int64)
+    gp[30:37] = 2            # cell 2: 7 points
+    gp[37] = 3               # cell 3: alone
+    gp[38:] = 4              # cell 4: 2 points; cell 1: empty
+    for R in (1, 3, 8):
+        assert np.array_equal(oracle.knn_cell_graphs(v, gp, 5, R), _brute_graph(v, gp, 5, R))
+    for E in (1, 2, 5):
+        assert np.array_equal(oracle.cross_graph(v, gp, 5, E), _brute_cross(v, gp, 5, E))
+
+
+def test_oracle_graph_random_brute_force():
+    rng = np.random.default_rng(11)
+    v = rng.integers(0, 256, (60, 16)).astype(np.uint8)
+    gp = rng.integers(0, 3, 60)
+    assert np.array_equal(oracle.knn_cell_graphs(v, gp, 3, 5), _brute_graph(v, gp, 3, 5))
+    assert np.array_equal(oracle.cross_graph(v, gp, 3, 3), _brute_cross(v, gp, 3, 3))
+
+
+def test_oracle_rows_match_full():
+    rng = np.random.default_rng(12)
+    v = rng.integers(0, 4, (300, 32)).astype(np.uint8)
+    gp = rng.integers(0, 5, 300)
+    gp[gp == 3] = 4          # cell 3 empty
+    gp[7] = 3                # ... but for one point
+    rows = [0, 7, 50, 299, 123]
+    full_g = oracle.knn_cell_graphs(v, gp, 5, 6)
+    order = np.argsort(gp, kind="stable")
+    pos = np.empty(300, np.int64)
+    pos[order] = np.arange(300)   # cell-major row of each point
+    assert np.array_equal(oracle.graph_rows(v, gp, 5, 6, rows), full_g[pos[rows]])
+    assert np.array_equal(oracle.cross_rows(v, gp, 5, 3, rows), oracle.cross_graph(v, gp, 5, 3)[rows])
+
+
+# ---------------------------------------------------------------- argument checks (no device call)
+def test_builder_rejects_bad_input_before_device():
+    v = np.zeros((10, 64), np.float32)
+    gp = np.zeros(10, np.uint32)
+    v[3, 5] = 0.5
+    with pytest.raises(GarfieldError) as e:
+        _lib.build_graphs(v, gp, 1, 4, 2)
+    assert e.value.status == 6   # GF_E_UNSUPPORTED: not integers in [0, 255]
+    with pytest.raises(GarfieldError) as e:
+        _lib.build_graphs(np.zeros((10, 64), np.uint8), gp, 1, 72, 2)
+    assert e.value.status == 6   # R + 1 above 72
+    with pytest.raises(GarfieldError) as e:
+        _lib.build_graphs(np.zeros((10, 300), np.uint8), gp, 1, 4, 2)
+    assert e.value.status == 6   # dimension above 256
+    with pytest.raises(GarfieldError) as e:
+        _lib.build_graphs(np.zeros((10, 64), np.uint8), gp + 1, 1, 4, 2)
+    assert e.value.status == 1   # a cell id >= P
