@@ -277,20 +277,21 @@ def build_bench(args):
 
     for _ in range(args.warmup):
         step()
-    acc = dict(tiles=0.0, graph=0.0, cross=0.0)
+    acc = dict(tiles=0.0, graph=0.0, cross=0.0, prep=0.0, upload=0.0, run=0.0, download=0.0, total=0.0)
     t = time.perf_counter()
     for _ in range(args.steps):
         gp, g, x, st = step()
-        acc["tiles"] += st.ms_tiles
-        acc["graph"] += st.ms_graph
-        acc["cross"] += st.ms_cross
+        for k in acc:
+            acc[k] += getattr(st, "ms_" + k)
     elapsed = time.perf_counter() - t
     K = args.steps
     ms_cross = acc["cross"] / K
     tops = 2.0 * st.dim * st.pairs_cross / (ms_cross * 1e-3) / 1e12
     tops_g = 2.0 * st.dim * st.pairs_graph / (acc["graph"] / K * 1e-3) / 1e12
     log(f"build: {elapsed * 1e3 / K:.1f} ms per step; kernels: tiles {acc['tiles'] / K:.2f} ms, graphs "
-        f"{acc['graph'] / K:.2f} ms ({tops_g:.0f} TOP/s), cross {ms_cross:.2f} ms ({tops:.0f} TOP/s)")
+        f"{acc['graph'] / K:.2f} ms ({tops_g:.0f} TOP/s), cross {ms_cross:.2f} ms ({tops:.0f} TOP/s); "
+        f"gf_build_graphs {acc['total'] / K:.1f} ms = prep {acc['prep'] / K:.1f} + upload {acc['upload'] / K:.1f} "
+        f"+ run {acc['run'] / K:.1f} + download {acc['download'] / K:.1f}")
     cpu = None
     if not args.no_cpu:
         # the oracle's exact rows (numpy, float64 BLAS dot products) for a
@@ -318,7 +319,9 @@ def build_bench(args):
                                f"R={R} exact per-cell kNN, E={E} cross edges",
                    "N": N, "D": D, "P": P, "R": R, "E": E,
                    "ms_tiles": round(acc["tiles"] / K, 3), "ms_graph": round(acc["graph"] / K, 3),
-                   "ms_cross": round(ms_cross, 3), "pairs_cross": st.pairs_cross, "pairs_graph": st.pairs_graph},
+                   "ms_cross": round(ms_cross, 3), "pairs_cross": st.pairs_cross, "pairs_graph": st.pairs_graph,
+                   "ms_call": round(acc["total"] / K, 3), "ms_host_prep": round(acc["prep"] / K, 3),
+                   "ms_upload": round(acc["upload"] / K, 3), "ms_download": round(acc["download"] / K, 3)},
         "roofline": {"bound": "mfma", "kernel": "k_knn_i8 (cross edges)", "achieved": round(tops, 1),
                      "peak": INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
                      "traffic": None, "ms_per_launch": round(ms_cross, 4)},

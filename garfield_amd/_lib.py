@@ -73,7 +73,9 @@ class SearchStats(C.Structure):
 
 class BuildStats(C.Structure):
     _fields_ = [("ms_tiles", C.c_double), ("ms_graph", C.c_double), ("ms_cross", C.c_double),
-                ("pairs_graph", C.c_uint64), ("pairs_cross", C.c_uint64), ("dim", C.c_uint32)]
+                ("pairs_graph", C.c_uint64), ("pairs_cross", C.c_uint64), ("dim", C.c_uint32),
+                ("ms_prep", C.c_double), ("ms_upload", C.c_double), ("ms_run", C.c_double),
+                ("ms_download", C.c_double), ("ms_total", C.c_double)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}

@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstring>
 #include <numeric>
@@ -21,6 +22,37 @@
 #include "gf_state.h"
 
 namespace gf {
+
+namespace {
+
+// Stable ascending argsort of floats: LSD radix sort (three 11-bit digits)
+// of the order-preserving integer image of each value; -0 counts as +0, as
+// in a comparison sort.
+void stable_argsort(const std::vector<float>& v, std::vector<uint32_t>& order) {
+    const size_t n = v.size();
+    std::vector<uint32_t> key(n), k2(n), o2(n);
+    for (size_t i = 0; i < n; ++i) {
+        uint32_t u;
+        const float x = v[i] == 0.0f ? 0.0f : v[i];
+        std::memcpy(&u, &x, 4);
+        key[i] = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+        order[i] = uint32_t(i);
+    }
+    for (int shift = 0; shift < 33; shift += 11) {
+        std::vector<size_t> cnt(2049, 0);
+        for (size_t i = 0; i < n; ++i) ++cnt[((key[i] >> shift) & 2047u) + 1];
+        for (int b = 0; b < 2048; ++b) cnt[b + 1] += cnt[b];
+        for (size_t i = 0; i < n; ++i) {
+            const size_t d = cnt[(key[i] >> shift) & 2047u]++;
+            k2[d] = key[i];
+            o2[d] = order[i];
+        }
+        key.swap(k2);
+        order.swap(o2);
+    }
+}
+
+}  // namespace
 
 void grid_scatter(const float* attrs, uint32_t N, uint32_t a, const uint32_t* grid, float* l_q, float* r_q,
                   uint32_t* pid_lists, uint32_t* global_pid) {
@@ -39,9 +71,8 @@ void grid_scatter(const float* attrs, uint32_t N, uint32_t a, const uint32_t* gr
     uint32_t qoff = 0;
     for (uint32_t d = 0; d < a; ++d) {
         for (uint32_t i = 0; i < N; ++i) col[i] = attrs[size_t(i) * a + d];
-        std::iota(order.begin(), order.end(), 0u);
         // stable argsort (tools.py:98): equal values keep point-id order
-        std::stable_sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) { return col[x] < col[y]; });
+        stable_argsort(col, order);
         const uint32_t g = grid[d];
         const uint32_t avg = uint32_t((uint64_t(N) + g - 1) / g);
         for (uint32_t j = 0; j < g; ++j) {
@@ -79,11 +110,19 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
     GF_REQUIRE(Dp <= 256, GF_E_UNSUPPORTED, "build_graphs: dimension above 256");
     const uint32_t KS = Dp / 64;
 
+    using clock = std::chrono::steady_clock;
+    const auto c0 = clock::now();
+    auto ms_since = [](clock::time_point a) {
+        return std::chrono::duration<double, std::milli>(clock::now() - a).count();
+    };
     // Vectors as u8 rows of Dp (padding 128 is 0 after the -128 shift and
     // adds nothing to norms or dot products); float input must hold integers
-    // in [0, 255], the data the int8 distances are exact for.
-    std::vector<uint8_t> v8(size_t(N) * Dp, uint8_t(128));
-    if (vec_dtype == GF_VEC_U8) {
+    // in [0, 255], the data the int8 distances are exact for.  u8 rows of a
+    // multiple of 64 are uploaded as they are.
+    const bool direct = vec_dtype == GF_VEC_U8 && D == Dp;
+    std::vector<uint8_t> v8(direct ? 0 : size_t(N) * Dp, uint8_t(128));
+    if (direct) {
+    } else if (vec_dtype == GF_VEC_U8) {
         const uint8_t* s = static_cast<const uint8_t*>(vectors);
         for (uint32_t i = 0; i < N; ++i) std::memcpy(&v8[size_t(i) * Dp], s + size_t(i) * D, D);
     } else {
@@ -128,6 +167,8 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
         }
     }
 
+    const double ms_prep = ms_since(c0);
+    const auto c1 = clock::now();
     GF_HIP(hipSetDevice(device));
     int ncu = 0;
     GF_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
@@ -150,7 +191,10 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
     DevBuf<int8_t> vt;
     DevBuf<int32_t> tnorm;
     DevBuf<KnnItem> dgi, dci;
-    dvec.upload(v8);
+    if (direct)
+        dvec.upload(static_cast<const uint8_t*>(vectors), size_t(N) * D);
+    else
+        dvec.upload(v8);
     dtrow.upload(trow);
     dctile.upload(ctile);
     dcoff.upload(coff);
@@ -165,6 +209,9 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
         GF_HIP(hipMemsetAsync(dout_c.p, 0, dout_c.bytes(), st));
     }
 
+    GF_HIP(hipStreamSynchronize(st));
+    const double ms_upload = ms_since(c1);
+    const auto c2 = clock::now();
     GF_HIP(hipEventRecord(ev[0], st));
     GF_HIP(launch_tile_i8(dvec.p, true, Dp, dtrow.p, 0, ntile, vt.p, tnorm.p, st));
     GF_HIP(hipEventRecord(ev[1], st));
@@ -207,9 +254,16 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
     }
     GF_HIP(hipEventRecord(ev[3], st));
     GF_HIP(hipStreamSynchronize(st));
+    const double ms_run = ms_since(c2);
+    const auto c3 = clock::now();
     if (cell_graphs) GF_HIP(hipMemcpy(cell_graphs, dout_g.p, dout_g.bytes(), hipMemcpyDeviceToHost));
     if (cross) GF_HIP(hipMemcpy(cross, dout_c.p, dout_c.bytes(), hipMemcpyDeviceToHost));
     if (stats) {
+        stats->ms_prep = ms_prep;
+        stats->ms_upload = ms_upload;
+        stats->ms_run = ms_run;
+        stats->ms_download = ms_since(c3);
+        stats->ms_total = ms_since(c0);
         float ms = 0;
         GF_HIP(hipEventElapsedTime(&ms, ev[0], ev[1]));
         stats->ms_tiles = ms;

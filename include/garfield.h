@@ -240,6 +240,11 @@ typedef struct {
     uint64_t pairs_graph;   /* distances evaluated: sum of |cell|^2 */
     uint64_t pairs_cross;   /* N * sum of |cell| */
     uint32_t dim;           /* dimension as computed (D rounded up to 64) */
+    double ms_prep;         /* host: input checks, cell layout, item lists */
+    double ms_upload;       /* device set-up, allocations and uploads */
+    double ms_run;          /* wall time of the kernels */
+    double ms_download;     /* results to the caller's arrays */
+    double ms_total;        /* the whole call */
 } gf_build_stats;
 
 /* The per-cell graphs (cagra_build.py:94-127 writes the layout: rows of R

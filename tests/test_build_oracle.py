@@ -50,6 +50,17 @@ def test_library_grid_matches_oracle(n, grid, hi, seed):
     assert np.array_equal(gp, ogp)
 
 
+def test_library_grid_signed_values_and_zeros():
+    # negative values, -0.0 next to +0.0 (equal: they keep point-id order)
+    rng = np.random.default_rng(6)
+    att = rng.integers(-5, 6, (400, 2)).astype(np.float32)
+    att[rng.random((400, 2)) < 0.2] = -0.0
+    l_q, r_q, pl, gp = _lib.grid_scatter(att, [3, 4])
+    ol, orr, opl, ogp = oracle.grid_scatter(att, [3, 4])
+    assert all(np.array_equal(pl[d], opl[d]) for d in range(2)) and np.array_equal(gp, ogp)
+    assert all(np.array_equal(l_q[d], ol[d]) and np.array_equal(r_q[d], orr[d]) for d in range(2))
+
+
 def test_library_grid_rejects_unfillable_grid():
     # N = 5, g = 4: avg = 2 and the last run would start at rank 6
     with pytest.raises(GarfieldError) as e:
