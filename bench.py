@@ -259,7 +259,7 @@ def build_bench(args):
     """Index build of the headline index (1M x 128 u8, 4x4 rank-quantile
     cells, R = 32, E = 2): a step is gf_grid_scatter plus gf_build_graphs from
     host arrays to host arrays (uploads, int8 tiles, per-cell graphs, cross
-    edges, downloads).  The roofline is the cross-edge kernel's int8 MFMA rate
+    edges, downloads), plus gf_kmeans labels (C = 1000, 8 rounds).  The roofline is the cross-edge kernel's int8 MFMA rate
     on its algorithmic work: D multiply-adds (2 D ops) per (point, candidate)
     pair, N * N pairs."""
     import garfield_amd._lib as gl
@@ -273,14 +273,17 @@ def build_bench(args):
     def step():
         _, _, _, gp = gl.grid_scatter(att, cfg["grid"])
         g, x, st = gl.build_graphs(v, gp, P, R, E)
-        return gp, g, x, st
+        lab, _, ms_km = gl.kmeans(v, cfg["C"], 8, seed=5)
+        return gp, g, x, st, ms_km
 
     for _ in range(args.warmup):
         step()
     acc = dict(tiles=0.0, graph=0.0, cross=0.0, prep=0.0, upload=0.0, run=0.0, download=0.0, total=0.0)
+    ms_kmeans = 0.0
     t = time.perf_counter()
     for _ in range(args.steps):
-        gp, g, x, st = step()
+        gp, g, x, st, ms_km = step()
+        ms_kmeans += ms_km
         for k in acc:
             acc[k] += getattr(st, "ms_" + k)
     elapsed = time.perf_counter() - t
@@ -291,7 +294,8 @@ def build_bench(args):
     log(f"build: {elapsed * 1e3 / K:.1f} ms per step; kernels: tiles {acc['tiles'] / K:.2f} ms, graphs "
         f"{acc['graph'] / K:.2f} ms ({tops_g:.0f} TOP/s), cross {ms_cross:.2f} ms ({tops:.0f} TOP/s); "
         f"gf_build_graphs {acc['total'] / K:.1f} ms = prep {acc['prep'] / K:.1f} + upload {acc['upload'] / K:.1f} "
-        f"+ run {acc['run'] / K:.1f} + download {acc['download'] / K:.1f}")
+        f"+ run {acc['run'] / K:.1f} + download {acc['download'] / K:.1f}; gf_kmeans (C={cfg['C']}, 8 rounds) "
+        f"{ms_kmeans / K:.1f} ms")
     cpu = None
     if not args.no_cpu:
         # the oracle's exact rows (numpy, float64 BLAS dot products) for a
@@ -310,18 +314,19 @@ def build_bench(args):
         cpu = {"value": round(done / t_cpu, 1), "unit": "points/s", "cores": os.cpu_count(),
                "kind": "port", "sample": f"{done} random points' cross-edge and graph rows (oracle, numpy + BLAS)"}
     out = {
-        "metric": "index build throughput, headline index (exact per-cell kNN + cross edges), 1 MI355X",
+        "metric": "index build throughput, headline index (grid, exact per-cell kNN + cross edges, k-means labels), 1 MI355X",
         "value": round(N * K / elapsed, 1), "unit": "points/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": round(elapsed * 1e3 / K, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic (generated in bench.py; host arrays in and out, PCIe included)",
         "config": {"workload": f"build: {N} x {D} u8 (integers 0-255), 2 attrs on a 4x4 rank-quantile grid, "
-                               f"R={R} exact per-cell kNN, E={E} cross edges",
+                               f"R={R} exact per-cell kNN, E={E} cross edges, k-means labels C={cfg['C']}",
                    "N": N, "D": D, "P": P, "R": R, "E": E,
                    "ms_tiles": round(acc["tiles"] / K, 3), "ms_graph": round(acc["graph"] / K, 3),
                    "ms_cross": round(ms_cross, 3), "pairs_cross": st.pairs_cross, "pairs_graph": st.pairs_graph,
                    "ms_call": round(acc["total"] / K, 3), "ms_host_prep": round(acc["prep"] / K, 3),
-                   "ms_upload": round(acc["upload"] / K, 3), "ms_download": round(acc["download"] / K, 3)},
+                   "ms_upload": round(acc["upload"] / K, 3), "ms_download": round(acc["download"] / K, 3),
+                   "C": cfg["C"], "kmeans_rounds": 8, "ms_kmeans": round(ms_kmeans / K, 3)},
         "roofline": {"bound": "mfma", "kernel": "k_knn_i8 (cross edges)", "achieved": round(tops, 1),
                      "peak": INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
                      "traffic": None, "ms_per_launch": round(ms_cross, 4)},

@@ -108,6 +108,8 @@ _SYMBOLS = {
                         C.c_void_p],
     "gf_build_graphs": [C.c_void_p, C.c_int32, C.c_uint32, C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32,
                         C.c_uint32, C.c_int32, C.c_void_p, C.c_void_p, C.POINTER(BuildStats)],
+    "gf_kmeans": [C.c_void_p, C.c_int32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p, C.c_int32,
+                  C.c_void_p, C.c_void_p, C.POINTER(C.c_double)],
     "gf_status_str": [C.c_int32],
     "gf_last_error": [],
 }
@@ -422,3 +424,29 @@ def build_graphs(vectors, global_pid, P, R, E, device=0, graphs=True, cross=True
     _check(load().gf_build_graphs(_ptr(v), vt, n, d, _ptr(gp), P, R if graphs else 0, E if cross else 0,
                                   device, _ptr(g), _ptr(x), C.byref(st)))
     return g, x, st
+
+
+def kmeans(vectors, ncent, iters, init_ids=None, seed=5, device=0):
+    """Cluster labels (gf_kmeans): integer Lloyd rounds from the points
+    init_ids (default: ncent distinct points drawn with numpy's
+    default_rng(seed)); returns (labels int32[N], centres uint8[ncent, D],
+    wall ms)."""
+    v = np.asarray(vectors)
+    if v.ndim != 2:
+        raise GarfieldError(1, "vectors must be N x D")
+    if v.dtype == np.uint8:
+        v, vt = np.ascontiguousarray(v), VEC_U8
+    else:
+        v, vt = _c(v, np.float32), VEC_F32
+    n, d = v.shape
+    if init_ids is None:
+        init_ids = np.random.default_rng(seed).choice(n, size=ncent, replace=False)
+    ids = _c(init_ids, np.uint32)
+    if ids.shape != (ncent,):
+        raise GarfieldError(1, "init_ids must hold ncent point ids")
+    lab = np.empty(n, np.int32)
+    cen = np.empty((ncent, d), np.uint8)
+    ms = C.c_double()
+    _check(load().gf_kmeans(_ptr(v), vt, n, d, ncent, iters, _ptr(ids), device, _ptr(lab), _ptr(cen),
+                            C.byref(ms)))
+    return lab, cen, ms.value

@@ -280,4 +280,110 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
     }
 }
 
+void kmeans_labels(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, uint32_t C, uint32_t iters,
+                   const uint32_t* init_ids, int32_t device, int32_t* labels, uint8_t* centres, double* ms) {
+    GF_REQUIRE(vectors && init_ids && labels && N > 0 && D > 0, GF_E_ARG, "kmeans: empty input");
+    GF_REQUIRE(vec_dtype == GF_VEC_F32 || vec_dtype == GF_VEC_U8, GF_E_ARG,
+               "kmeans: vectors must be GF_VEC_F32 or GF_VEC_U8");
+    GF_REQUIRE(C > 0 && C <= N, GF_E_ARG, "kmeans: need 0 < C <= N");
+    GF_REQUIRE(uint64_t(N) + C < 0xFFFFFFF0ull, GF_E_UNSUPPORTED, "kmeans: too many points");
+    const uint32_t Dp = round_up(D, 64);
+    GF_REQUIRE(Dp <= 256, GF_E_UNSUPPORTED, "kmeans: dimension above 256");
+    const uint32_t KS = Dp / 64;
+    for (uint32_t c = 0; c < C; ++c) GF_REQUIRE(init_ids[c] < N, GF_E_ARG, "kmeans: init id out of range");
+    const auto c0 = std::chrono::steady_clock::now();
+
+    // Rows: the N points, then the C centres (u8, Dp wide, padding 128).
+    std::vector<uint8_t> v8(size_t(N + C) * Dp, uint8_t(128));
+    if (vec_dtype == GF_VEC_U8) {
+        const uint8_t* s = static_cast<const uint8_t*>(vectors);
+        for (uint32_t i = 0; i < N; ++i) std::memcpy(&v8[size_t(i) * Dp], s + size_t(i) * D, D);
+    } else {
+        const float* s = static_cast<const float*>(vectors);
+        for (uint32_t i = 0; i < N; ++i)
+            for (uint32_t k = 0; k < D; ++k) {
+                const float x = s[size_t(i) * D + k];
+                GF_REQUIRE(x >= 0.0f && x <= 255.0f && x == std::floor(x), GF_E_UNSUPPORTED,
+                           "kmeans: vectors must be integers in [0, 255]");
+                v8[size_t(i) * Dp + k] = uint8_t(x);
+            }
+    }
+    for (uint32_t c = 0; c < C; ++c)
+        std::memcpy(&v8[size_t(N + c) * Dp], &v8[size_t(init_ids[c]) * Dp], Dp);
+    // Two "cells": the points (queries) and the centres (candidates); an
+    // assignment is the cross-edge pass with E = 1 (nearest centre, ties to
+    // the smaller centre index).
+    const uint32_t Tp = (N + 15) / 16, Tc = (C + 15) / 16, ntile = Tp + Tc;
+    std::vector<uint32_t> trow(size_t(ntile) * 16, 0xFFFFFFFFu);
+    for (uint32_t i = 0; i < N; ++i) trow[i] = i;
+    for (uint32_t c = 0; c < C; ++c) trow[size_t(Tp) * 16 + c] = N + c;
+    const std::vector<uint32_t> ctile{0, Tp, ntile}, coff{0, N, N + C};
+    std::vector<KnnItem> items;
+    for (uint32_t t = 0; t < Tp; t += 4) items.push_back(KnnItem{t, 0, 1});
+
+    GF_HIP(hipSetDevice(device));
+    int ncu = 0;
+    GF_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
+    hipStream_t st = nullptr;
+    struct Guard {
+        hipStream_t& st;
+        ~Guard() {
+            if (st) (void)hipStreamDestroy(st);
+        }
+    } guard{st};
+    GF_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    DevBuf<uint8_t> dvec;
+    DevBuf<uint32_t> dtrow, dctile, dcoff, out2, cnt;
+    DevBuf<int32_t> tnorm, sums;
+    DevBuf<int8_t> vt;
+    DevBuf<KnnItem> ditems;
+    DevBuf<uint64_t> state;
+    dvec.upload(v8);
+    dtrow.upload(trow);
+    dctile.upload(ctile);
+    dcoff.upload(coff);
+    ditems.upload(items);
+    vt.alloc(size_t(ntile) * KS * 1024);
+    tnorm.alloc(size_t(ntile) * 32);
+    out2.alloc(size_t(N) * 2);
+    state.alloc(size_t(N) * 2);
+    sums.alloc(size_t(C) * Dp);
+    cnt.alloc(C);
+    const uint32_t ctiles = 1024 / KS, nchunk = (Tc + ctiles - 1) / ctiles;
+    KnnArgs ka{};
+    ka.vt = vt.p;
+    ka.tnorm = tnorm.p;
+    ka.trow = dtrow.p;
+    ka.ctile = dctile.p;
+    ka.coff = dcoff.p;
+    ka.items = ditems.p;
+    ka.nitems = uint32_t(items.size());
+    ka.K = 1;
+    ka.R = 0;
+    ka.P = 2;
+    ka.out = out2.p;
+    ka.ctiles = ctiles;
+    ka.state = state.p;
+    GF_HIP(launch_tile_i8(dvec.p, true, Dp, dtrow.p, 0, ntile, vt.p, tnorm.p, st));
+    for (uint32_t it = 0;; ++it) {
+        for (ka.chunk = 0; ka.chunk < nchunk; ++ka.chunk) GF_HIP(launch_knn_i8(ka, KS, uint32_t(ncu), st));
+        if (it == iters) break;
+        GF_HIP(hipMemsetAsync(sums.p, 0, sums.bytes(), st));
+        GF_HIP(hipMemsetAsync(cnt.p, 0, cnt.bytes(), st));
+        GF_HIP(launch_kmeans_update(dvec.p, Dp, out2.p, N, C, sums.p, cnt.p, dvec.p + size_t(N) * Dp, st));
+        GF_HIP(launch_tile_i8(dvec.p, true, Dp, dtrow.p + size_t(Tp) * 16, 0, Tc, vt.p + size_t(Tp) * KS * 1024,
+                              tnorm.p + size_t(Tp) * 32, st));
+    }
+    GF_HIP(hipStreamSynchronize(st));
+    std::vector<uint32_t> h2(size_t(N) * 2);
+    GF_HIP(hipMemcpy(h2.data(), out2.p, out2.bytes(), hipMemcpyDeviceToHost));
+    for (uint32_t i = 0; i < N; ++i) labels[i] = int32_t(h2[size_t(i) * 2 + 1]);
+    if (centres) {
+        std::vector<uint8_t> hc(size_t(C) * Dp);
+        GF_HIP(hipMemcpy(hc.data(), dvec.p + size_t(N) * Dp, hc.size(), hipMemcpyDeviceToHost));
+        for (uint32_t c = 0; c < C; ++c) std::memcpy(centres + size_t(c) * D, &hc[size_t(c) * Dp], D);
+    }
+    if (ms) *ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - c0).count();
+}
+
 }  // namespace gf

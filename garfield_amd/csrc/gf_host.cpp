@@ -1187,6 +1187,13 @@ gf_status gf_build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, ui
     });
 }
 
+gf_status gf_kmeans(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, uint32_t C, uint32_t iters,
+                    const uint32_t* init_ids, int32_t device, int32_t* labels, uint8_t* centres, double* ms) {
+    return run_guarded([&] {
+        gf::kmeans_labels(vectors, vec_dtype, N, D, C, iters, init_ids, device, labels, centres, ms);
+    });
+}
+
 gf_status gf_entry_points(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
     return run_guarded([&] {
         GF_REQUIRE(out && P >= 1 && N >= P, GF_E_ARG, "invalid arguments");

@@ -2516,6 +2516,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KT > 40 ? 1
     }
 }
 
+// k-means update of the index builder (integer Lloyd step): per-cluster
+// sums of the u8 rows and member counts, then each centre the rounded mean
+// floor((2 sum + n) / (2 n)) of its members (an empty cluster keeps its
+// centre).  lab2 holds the assignment as (point, 2) pairs, label second.
+__global__ void k_kmeans_accum(const uint8_t* vec, uint32_t Dp, const uint32_t* lab2, uint32_t N, int32_t* sums,
+                               uint32_t* cnt) {
+    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= size_t(N) * Dp) return;
+    const uint32_t pt = uint32_t(i / Dp), d = uint32_t(i % Dp);
+    const uint32_t l = lab2[size_t(pt) * 2u + 1u];
+    atomicAdd(&sums[size_t(l) * Dp + d], int32_t(vec[i]));
+    if (d == 0) atomicAdd(&cnt[l], 1u);
+}
+
+__global__ void k_kmeans_centres(const int32_t* sums, const uint32_t* cnt, uint32_t C, uint32_t Dp, uint8_t* centres) {
+    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= size_t(C) * Dp) return;
+    const uint32_t n = cnt[i / Dp];
+    if (n) centres[i] = uint8_t((2 * int64_t(sums[i]) + n) / (2 * int64_t(n)));
+}
+
 }  // namespace
 
 template <int KS, int KT, int NB = 1>
@@ -2550,6 +2571,17 @@ hipError_t launch_knn_i8(const KnnArgs& a, uint32_t KS, uint32_t ncu, hipStream_
     KNN(4)
 #undef KNN
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_kmeans_update(const uint8_t* vec, uint32_t Dp, const uint32_t* lab2, uint32_t N, uint32_t C,
+                                int32_t* sums, uint32_t* cnt, uint8_t* centres, hipStream_t st) {
+    const size_t n1 = size_t(N) * Dp, n2 = size_t(C) * Dp;
+    if (n1 == 0 || n2 == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_kmeans_accum, dim3(uint32_t((n1 + 255) / 256)), dim3(256), 0, st, vec, Dp, lab2, N, sums,
+                       cnt);
+    hipLaunchKernelGGL(k_kmeans_centres, dim3(uint32_t((n2 + 255) / 256)), dim3(256), 0, st, sums, cnt, C, Dp,
+                       centres);
+    return hipGetLastError();
 }
 
 namespace {

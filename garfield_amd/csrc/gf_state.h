@@ -381,4 +381,6 @@ void grid_scatter(const float* attrs, uint32_t N, uint32_t a, const uint32_t* gr
 void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, const uint32_t* global_pid,
                   uint32_t P, uint32_t R, uint32_t E, int32_t device, uint32_t* cell_graphs, uint32_t* cross,
                   gf_build_stats* stats);
+void kmeans_labels(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, uint32_t C, uint32_t iters,
+                   const uint32_t* init_ids, int32_t device, int32_t* labels, uint8_t* centres, double* ms);
 }  // namespace gf

@@ -226,9 +226,9 @@ def kmeans_labels(vectors, C, iters, seed, device="cpu", chunk=65536):
 def build_index(vectors, attrs, grid, R, E, C=0, kmeans_iters=8, seed=5, device="cpu", arith=None):
     """All index arrays, in the layout the files hold.  arith = (attr_min,
     attr_width) builds the cells on an arithmetic grid instead of rank quantiles.
-    device "hip": the library's builder (gf_grid_scatter and the int8 MFMA
-    gf_build_graphs, integer data only; k-means labels still via torch on the
-    GPU); else torch on that device."""
+    device "hip": the library's builder (gf_grid_scatter, the int8 MFMA
+    gf_build_graphs and gf_kmeans; integer data only); else torch on that
+    device."""
     grid = np.asarray(grid, np.int64)
     P = int(np.prod(grid))
     hip = device == "hip"
@@ -248,7 +248,12 @@ def build_index(vectors, attrs, grid, R, E, C=0, kmeans_iters=8, seed=5, device=
         members = cell_members(global_pid, P)
         graphs = knn_cell_graphs(vectors, members, R, device=device)
         cross = cross_edges(vectors, members, E, device=device)
-    labels = kmeans_labels(vectors, C, kmeans_iters, seed, device="cuda" if hip else device) if C else None
+    if C and hip:
+        from ._lib import kmeans
+        v = vectors if vectors.dtype == np.uint8 else np.asarray(vectors, np.float32)
+        labels = kmeans(v, C, kmeans_iters, seed=seed)[0]
+    else:
+        labels = kmeans_labels(vectors, C, kmeans_iters, seed, device=device) if C else None
     return dict(vectors=vectors, attrs=attrs, grid=grid.astype(np.int32), l_q=l_q, r_q=r_q,
                 pid_lists=pid_lists, global_pid=global_pid, cell_graphs=graphs, cross=cross, labels=labels,
                 P=P, R=R, E=E)

@@ -264,6 +264,19 @@ gf_status gf_build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, ui
                           const uint32_t* global_pid, uint32_t P, uint32_t R, uint32_t E, int32_t device,
                           uint32_t* cell_graphs, uint32_t* cross, gf_build_stats* stats);
 
+/* Per-point cluster labels for the index (the .cluster file; the reference
+ * fits cuVS k-means and predicts, clustering.py:68-87).  Integer Lloyd
+ * iterations: centres start as the points init_ids (C of them); an
+ * assignment gives each point its nearest centre by exact squared L2
+ * distance (ties to the smaller centre index); an update moves each centre
+ * to the rounded mean floor((2 sum + n) / (2 n)) of its n members (an empty
+ * cluster keeps its centre).  `iters` assign + update rounds, then a final
+ * assignment gives the labels.  Same data limits as gf_build_graphs;
+ * centres (C*D bytes) may be NULL; ms (wall time of the call) may be NULL. */
+gf_status gf_kmeans(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, uint32_t C, uint32_t iters,
+                    const uint32_t* init_ids, int32_t device, int32_t* labels /*N*/, uint8_t* centres /*C*D*/,
+                    double* ms);
+
 const char* gf_status_str(gf_status s);
 const char* gf_last_error(void);
 

@@ -370,3 +370,23 @@ def cross_rows(vectors, global_pid, P, E, rows):
         out[:, c * E:c * E + o.shape[1]] = o
         out[:, c * E + o.shape[1]:(c + 1) * E] = o[:, :1]
     return out
+
+
+def kmeans(vectors, C, iters, init_ids):
+    """gf_kmeans' definition (the reference fits cuVS k-means, absent here,
+    clustering.py:68-87): integer Lloyd rounds from the points init_ids;
+    assignment = nearest centre by exact squared distance, the smaller centre
+    index on ties (np.argmin); update = floor((2 sum + n) / (2 n)) per
+    dimension, an empty cluster kept; `iters` rounds, then a final
+    assignment.  Returns (labels, centres)."""
+    x = np.asarray(vectors).astype(np.int64)
+    cen = x[np.asarray(init_ids)].copy()
+    for it in range(iters + 1):
+        lab = np.argmin(_sq(x, cen), axis=1)
+        if it == iters:
+            return lab.astype(np.int32), cen.astype(np.uint8)
+        n = np.bincount(lab, minlength=C).astype(np.int64)
+        sums = np.zeros_like(cen)
+        np.add.at(sums, lab, x)
+        nz = n > 0
+        cen[nz] = (2 * sums[nz] + n[nz, None]) // (2 * n[nz, None])

@@ -149,6 +149,49 @@ def test_oracle_rows_match_full():
     assert np.array_equal(oracle.cross_rows(v, gp, 5, 3, rows), oracle.cross_graph(v, gp, 5, 3)[rows])
 
 
+# ---------------------------------------------------------------- k-means labels
+def _brute_kmeans(v, C, iters, init):
+    x = [list(map(int, r)) for r in v]
+    cen = [list(x[i]) for i in init]
+    for it in range(iters + 1):
+        lab = []
+        for p in x:
+            best = min(range(C), key=lambda c: (sum((a - b) ** 2 for a, b in zip(p, cen[c])), c))
+            lab.append(best)
+        if it == iters:
+            return np.array(lab), np.array(cen)
+        for c in range(C):
+            mem = [x[i] for i in range(len(x)) if lab[i] == c]
+            if mem:
+                n = len(mem)
+                cen[c] = [(2 * sum(col) + n) // (2 * n) for col in zip(*mem)]
+
+
+def test_oracle_kmeans_hand_cases():
+    v = np.array([[0], [1], [2], [10], [11], [12]], np.uint8)
+    lab, cen = oracle.kmeans(v, 2, 2, [0, 3])
+    assert lab.tolist() == [0, 0, 0, 1, 1, 1] and cen.ravel().tolist() == [1, 11]
+    # a mean of 0.5 rounds up; a point between two centres takes the smaller index
+    lab, cen = oracle.kmeans(np.array([[0], [1]], np.uint8), 1, 1, [0])
+    assert cen.ravel().tolist() == [1]
+    lab, _ = oracle.kmeans(np.array([[0], [2], [1]], np.uint8), 2, 0, [0, 1])
+    assert lab.tolist() == [0, 1, 0]
+    # equal initial centres: the second cluster stays empty in the first
+    # assignment and keeps its centre (3); the update moves the first to
+    # floor((2 * 17 + 3) / 6) = 6, and the final assignment takes 3 back
+    lab, cen = oracle.kmeans(np.array([[3], [5], [9]], np.uint8), 2, 1, [0, 0])
+    assert lab.tolist() == [1, 0, 0] and cen.ravel().tolist() == [6, 3]
+
+
+def test_oracle_kmeans_brute_force():
+    rng = np.random.default_rng(21)
+    v = rng.integers(0, 6, (50, 5)).astype(np.uint8)
+    init = rng.choice(50, 6, replace=False)
+    lab, cen = oracle.kmeans(v, 6, 4, init)
+    blab, bcen = _brute_kmeans(v, 6, 4, init)
+    assert np.array_equal(lab, blab) and np.array_equal(cen, bcen)
+
+
 # ---------------------------------------------------------------- argument checks (no device call)
 def test_builder_rejects_bad_input_before_device():
     v = np.zeros((10, 64), np.float32)
@@ -166,3 +209,10 @@ def test_builder_rejects_bad_input_before_device():
     with pytest.raises(GarfieldError) as e:
         _lib.build_graphs(np.zeros((10, 64), np.uint8), gp + 1, 1, 4, 2)
     assert e.value.status == 1   # a cell id >= P
+
+    with pytest.raises(GarfieldError) as e:
+        _lib.kmeans(np.zeros((10, 64), np.uint8), 3, 2, init_ids=[0, 1, 10])
+    assert e.value.status == 1   # an initial centre id >= N
+    with pytest.raises(GarfieldError) as e:
+        _lib.kmeans(np.zeros((10, 64), np.uint8), 11, 2, init_ids=list(range(10)) + [0])
+    assert e.value.status == 1   # more centres than points

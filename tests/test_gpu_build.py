@@ -97,3 +97,34 @@ def test_built_index_searches():
         rec.append(oracle.recall(ids, gt, gtd))
     print(f"[build-search] recall hip {rec[0]:.4f} torch {rec[1]:.4f}", flush=True)
     assert rec[0] > 0.85 and abs(rec[0] - rec[1]) < 0.01
+
+
+@pytest.mark.parametrize("N,D,C,iters,hi,u8", [
+    (5000, 128, 40, 5, 256, True),
+    (3000, 100, 17, 3, 256, False),   # D padded, float input
+    (2000, 64, 64, 4, 3, True),       # many equal distances
+])
+def test_kmeans_matches_oracle(N, D, C, iters, hi, u8):
+    _print_case("kmeans", N=N, D=D, C=C, iters=iters, hi=hi)
+    rng = np.random.default_rng(N + C)
+    v = rng.integers(0, hi, (N, D))
+    v = v.astype(np.uint8) if u8 else v.astype(np.float32)
+    init = rng.choice(N, C, replace=False)
+    lab, cen, _ = _lib.kmeans(v, C, iters, init_ids=init)
+    olab, ocen = oracle.kmeans(v, C, iters, init)
+    assert np.array_equal(cen, ocen), "centres differ"
+    assert np.array_equal(lab, olab), "labels differ"
+
+
+def test_kmeans_headline_size_property():
+    """1M x 128, C = 1000 (the headline index's clusters): every sampled
+    point's label is its nearest returned centre, ties to the smaller index."""
+    N, D, C = 1_000_000, 128, 1000
+    _print_case("kmeans-headline", N=N, C=C)
+    v = synth.uniform_int_vectors(N, D, 11).astype(np.uint8)
+    lab, cen, ms = _lib.kmeans(v, C, 8, seed=5)
+    print(f"[kmeans] {ms:.1f} ms", flush=True)
+    pts = np.random.default_rng(17).choice(N, 2000, replace=False)
+    d = oracle._sq(v[pts], cen)
+    assert np.array_equal(lab[pts], np.argmin(d, axis=1))
+    assert len(np.unique(lab)) > C // 2
