@@ -2145,11 +2145,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3
                     }
                     return ok;
                 };
-                bool anyl = false;   // lane-mask OR: no per-pair ballot
+                // Distance first, on the max of each column's four rows (one
+                // compare per column); the range test only runs for a tile
+                // where some pair is within the threshold.
+                bool anyd = false;
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
+                    anyd |= max(max(acc[j][0], acc[j][1]), max(acc[j][2], acc[j][3])) >= tp[j];
+                if (!__builtin_amdgcn_ballot_w64(anyd)) continue;
+                bool anyl = !FILTER;   // lane-mask OR: no per-pair ballot
+                if constexpr (FILTER) {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) anyl |= pass(j, i);
+                    for (int j = 0; j < 4; ++j)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) anyl |= pass(j, i);
+                }
                 if (__builtin_amdgcn_ballot_w64(anyl)) {
                     // Append: the owner adds |q'|^2 to nx - 2 q'.x' later.
                     bool full = false;
