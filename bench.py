@@ -104,13 +104,15 @@ def main():
     b = dev.batch(cfg["queries"], lo, hi)
     log(f"library index resident ({dev.device_bytes / 2**30:.2f} GiB) in {time.time() - t1:.1f}s")
 
-    out = (np.empty((Q, 10), np.uint32), np.empty((Q, 10), np.float32))
+    # page-locked result arrays: the search copies into them directly
+    out = (torch.empty((Q, 10), dtype=torch.int32, pin_memory=True).numpy().view(np.uint32),
+           torch.empty((Q, 10), dtype=torch.float32, pin_memory=True).numpy())
 
     def step(prefilter, L):
         # Stages A and B are enqueued without waiting; the search reports
         # their device times after its one synchronisation.  The result
-        # arrays are reused from step to step (the host copies into pages
-        # already touched).
+        # arrays are reused from step to step, page-locked, so the search's
+        # device-to-host copies land in them directly.
         b.mark_cells(prefilter, timed=False)
         b.order_cells(4, timed=False)
         ids, dists, st = b.search(L=L, K=10, rl=10, postfilter=args.postfilter, out=out)

@@ -935,6 +935,21 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         if (b->h_ids.n < nr) { b->h_ids.alloc(nr); b->h_dist.alloc(nr); }
         if (!b->h_tot.n) { b->h_tot.alloc(16); b->h_stats.alloc(16); }
         if (stats && b->stats.n < 16) b->stats.alloc(16);
+        // Results go straight into the caller's arrays when HIP knows them as
+        // page-locked host memory; otherwise through the batch's pinned
+        // buffers and a host copy after the wait.
+        auto page_locked = [](const void* ptr) {
+            if (!ptr) return false;
+            hipPointerAttribute_t at{};
+            if (hipPointerGetAttributes(&at, ptr) != hipSuccess) {
+                (void)hipGetLastError();
+                return false;
+            }
+            return at.type == hipMemoryTypeHost;
+        };
+        const bool ids_direct = page_locked(ids), dist_direct = page_locked(dists);
+        uint32_t* ids_dst = ids_direct ? ids : b->h_ids.p;
+        float* dist_dst = dist_direct ? dists : b->h_dist.p;
         auto enqueue_copies = [&]() {
             if (stats) {
                 GF_HIP(gf::launch_zero_u32(reinterpret_cast<uint32_t*>(b->stats.p), 32, st));
@@ -948,8 +963,8 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             }
             GF_HIP(hipMemcpyAsync(b->h_tot.p, tot, 16 * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
             GF_HIP(hipMemcpyAsync(b->h_stamps.p, b->stamps.p, 8 * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
-            GF_HIP(hipMemcpyAsync(b->h_ids.p, b->out_ids.p, nr * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-            if (dists) GF_HIP(hipMemcpyAsync(b->h_dist.p, b->out_dist.p, nr * sizeof(float), hipMemcpyDeviceToHost, st));
+            GF_HIP(hipMemcpyAsync(ids_dst, b->out_ids.p, nr * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+            if (dists) GF_HIP(hipMemcpyAsync(dist_dst, b->out_dist.p, nr * sizeof(float), hipMemcpyDeviceToHost, st));
         };
         auto enqueue_tail = [&]() {
             enqueue_copies();
@@ -986,7 +1001,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                                 uint64_t(uintptr_t(b->part.p)), uint64_t(uintptr_t(b->items.p)),
                                 uint64_t(uintptr_t(b->bq.p)), b->pair_cap, uint64_t(uintptr_t(b->out_ids.p)),
                                 uint64_t(uintptr_t(b->counters.p)), uint64_t(uintptr_t(b->sched.p)),
-                                uint64_t(uintptr_t(b->h_ids.p)), uint64_t(uintptr_t(b->h_dist.p)),
+                                uint64_t(uintptr_t(ids_dst)), uint64_t(uintptr_t(dist_dst)),
                                 uint64_t(uintptr_t(b->stats.p)), uint64_t(uintptr_t(b->bfmask.p)),
                                 uint64_t(uintptr_t(b->entry.p)), uint64_t(uintptr_t(b->sitems.p)),
                                 uint64_t(uintptr_t(b->out_dist.p)), uint64_t(uintptr_t(b->selcount.p)),
@@ -1006,8 +1021,8 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             enqueue_tail();
             GF_REQUIRE(dt[3], GF_E_STATE, "brute-force schedule does not fit after growing");
         }
-        std::memcpy(ids, b->h_ids.p, nr * sizeof(uint32_t));
-        if (dists) std::memcpy(dists, b->h_dist.p, nr * sizeof(float));
+        if (!ids_direct) std::memcpy(ids, b->h_ids.p, nr * sizeof(uint32_t));
+        if (dists && !dist_direct) std::memcpy(dists, b->h_dist.p, nr * sizeof(float));
         if (stats) {
             float t_tr = 0, t_bf = 0, t_g = 0;
             const uint64_t* ts = b->h_stamps.p;

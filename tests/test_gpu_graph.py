@@ -72,3 +72,34 @@ def test_graph_replay_gather_bruteforce(monkeypatch, world_gauss):
     cfg, ix = world_gauss
     _print_case("graph-gather")
     _replays(monkeypatch, cfg, ix, 0.05, [32])
+
+
+def test_graph_replay_into_page_locked_arrays(monkeypatch, world_sub2):
+    """Result arrays in page-locked memory receive the device copies
+    directly (no staging); every replay gives the eager bits, and a switch
+    between pageable and page-locked arrays recaptures."""
+    import torch
+    cfg, ix = world_sub2
+    _print_case("graph-pinned-out")
+    dev = synth.open_device_index(ix)
+    b = dev.batch(cfg["queries"], cfg["lo"].astype(np.float32), cfg["hi"].astype(np.float32))
+    Q = cfg["queries"].shape[0]
+    pinned = (torch.empty((Q, 10), dtype=torch.int32, pin_memory=True).numpy().view(np.uint32),
+              torch.empty((Q, 10), dtype=torch.float32, pin_memory=True).numpy())
+    try:
+        b.mark_cells(1.0)
+        monkeypatch.setenv("GARFIELD_NO_GRAPH", "1")
+        ids0, d0, _ = b.search(L=32, K=10, rl=10)
+        monkeypatch.delenv("GARFIELD_NO_GRAPH")
+        for r in range(4):
+            out = pinned if r % 2 == 0 else None
+            ids, d, st = b.search(L=32, K=10, rl=10, out=out)
+            assert st.graph == 1
+            assert np.array_equal(ids, ids0), f"run {r}: ids differ"
+            assert np.array_equal(d.view(np.uint32), d0.view(np.uint32)), f"run {r}: distances differ"
+            if out is not None:
+                assert ids is out[0] or np.shares_memory(ids, out[0])
+            b.mark_cells(1.0)
+    finally:
+        b.close()
+        dev.close()
