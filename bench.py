@@ -105,8 +105,7 @@ def main():
     log(f"library index resident ({dev.device_bytes / 2**30:.2f} GiB) in {time.time() - t1:.1f}s")
 
     # page-locked result arrays: the search copies into them directly
-    out = (torch.empty((Q, 10), dtype=torch.int32, pin_memory=True).numpy().view(np.uint32),
-           torch.empty((Q, 10), dtype=torch.float32, pin_memory=True).numpy())
+    out = (gf.pinned_empty((Q, 10), np.uint32), gf.pinned_empty((Q, 10), np.float32))
 
     def step(prefilter, L):
         # Stages A and B are enqueued without waiting; the search reports

@@ -110,6 +110,8 @@ _SYMBOLS = {
                         C.c_uint32, C.c_int32, C.c_void_p, C.c_void_p, C.POINTER(BuildStats)],
     "gf_kmeans": [C.c_void_p, C.c_int32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p, C.c_int32,
                   C.c_void_p, C.c_void_p, C.POINTER(C.c_double)],
+    "gf_host_alloc": [C.c_size_t, C.POINTER(C.c_void_p)],
+    "gf_host_free": [C.c_void_p],
     "gf_status_str": [C.c_int32],
     "gf_last_error": [],
 }
@@ -450,3 +452,17 @@ def kmeans(vectors, ncent, iters, init_ids=None, seed=5, device=0):
     _check(load().gf_kmeans(_ptr(v), vt, n, d, ncent, iters, _ptr(ids), device, _ptr(lab), _ptr(cen),
                             C.byref(ms)))
     return lab, cen, ms.value
+
+
+def pinned_empty(shape, dtype):
+    """An uninitialised numpy array in page-locked host memory (gf_host_alloc),
+    freed when the array is collected; Batch.search(out=...) copies into such
+    arrays directly."""
+    import weakref
+    dt = np.dtype(dtype)
+    n = int(np.prod(shape)) * dt.itemsize
+    ptr = C.c_void_p()
+    _check(load().gf_host_alloc(max(n, 1), C.byref(ptr)))
+    buf = (C.c_uint8 * max(n, 1)).from_address(ptr.value)
+    weakref.finalize(buf, load().gf_host_free, C.c_void_p(ptr.value))
+    return np.frombuffer(buf, dtype=dt, count=int(np.prod(shape))).reshape(shape)

@@ -1209,6 +1209,20 @@ gf_status gf_kmeans(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t
     });
 }
 
+gf_status gf_host_alloc(size_t bytes, void** out) {
+    return run_guarded([&] {
+        GF_REQUIRE(out && bytes > 0, GF_E_ARG, "gf_host_alloc: null output or zero size");
+        *out = nullptr;
+        GF_HIP(hipHostMalloc(out, bytes, hipHostMallocDefault));
+    });
+}
+
+gf_status gf_host_free(void* ptr) {
+    return run_guarded([&] {
+        if (ptr) GF_HIP(hipHostFree(ptr));
+    });
+}
+
 gf_status gf_entry_points(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
     return run_guarded([&] {
         GF_REQUIRE(out && P >= 1 && N >= P, GF_E_ARG, "invalid arguments");

@@ -211,6 +211,12 @@ gf_status gf_batch_get_centroid(const gf_batch* b, float* dist /*Q*C*/, uint32_t
 gf_status gf_batch_get_cell_flags(const gf_batch* b, uint8_t* flags);
 gf_status gf_batch_get_counters(const gf_batch* b, uint32_t* counters /*Q*GF_NCOUNTERS*/);
 
+/* Page-locked host memory (hipHostMalloc).  No counterpart in the reference:
+ * result arrays allocated here receive gf_search's device-to-host copies
+ * directly, without a staging copy on the host.  Free with gf_host_free. */
+gf_status gf_host_alloc(size_t bytes, void** out);
+gf_status gf_host_free(void* ptr);
+
 /* f2h (tools.cuh:308-320) on the device: out[i] = binary16(x[i]*alpha), RNE. */
 gf_status gf_f2h(const float* x, size_t n, float alpha, uint16_t* out);
 /* find_norm (tools.cuh:1561-1586) on the device: squared norms of fp16 rows. */

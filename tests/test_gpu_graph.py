@@ -78,14 +78,13 @@ def test_graph_replay_into_page_locked_arrays(monkeypatch, world_sub2):
     """Result arrays in page-locked memory receive the device copies
     directly (no staging); every replay gives the eager bits, and a switch
     between pageable and page-locked arrays recaptures."""
-    import torch
+    from garfield_amd import pinned_empty
     cfg, ix = world_sub2
     _print_case("graph-pinned-out")
     dev = synth.open_device_index(ix)
     b = dev.batch(cfg["queries"], cfg["lo"].astype(np.float32), cfg["hi"].astype(np.float32))
     Q = cfg["queries"].shape[0]
-    pinned = (torch.empty((Q, 10), dtype=torch.int32, pin_memory=True).numpy().view(np.uint32),
-              torch.empty((Q, 10), dtype=torch.float32, pin_memory=True).numpy())
+    pinned = (pinned_empty((Q, 10), np.uint32), pinned_empty((Q, 10), np.float32))
     try:
         b.mark_cells(1.0)
         monkeypatch.setenv("GARFIELD_NO_GRAPH", "1")
