@@ -172,18 +172,21 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
     GF_HIP(hipSetDevice(device));
     int ncu = 0;
     GF_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
-    hipStream_t st = nullptr;
+    hipStream_t st = nullptr, st2 = nullptr;
     hipEvent_t ev[4] = {};
     struct Guard {
         hipStream_t& st;
+        hipStream_t& st2;
         hipEvent_t* ev;
         ~Guard() {
             for (int i = 0; i < 4; ++i)
                 if (ev[i]) (void)hipEventDestroy(ev[i]);
+            if (st2) (void)hipStreamDestroy(st2);
             if (st) (void)hipStreamDestroy(st);
         }
-    } guard{st, ev};
+    } guard{st, st2, ev};
     GF_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    GF_HIP(hipStreamCreateWithFlags(&st2, hipStreamNonBlocking));
     for (auto& e : ev) GF_HIP(hipEventCreate(&e));
 
     DevBuf<uint8_t> dvec;
@@ -253,10 +256,16 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
         for (ka.chunk = 0; ka.chunk < nchunk; ++ka.chunk) GF_HIP(launch_knn_i8(ka, KS, uint32_t(ncu), st));
     }
     GF_HIP(hipEventRecord(ev[3], st));
+    // The graphs travel to the caller on a second stream while the cross
+    // edges are computed.
+    if (cell_graphs) {
+        GF_HIP(hipStreamWaitEvent(st2, ev[2], 0));
+        GF_HIP(hipMemcpyAsync(cell_graphs, dout_g.p, dout_g.bytes(), hipMemcpyDeviceToHost, st2));
+        GF_HIP(hipStreamSynchronize(st2));
+    }
     GF_HIP(hipStreamSynchronize(st));
     const double ms_run = ms_since(c2);
     const auto c3 = clock::now();
-    if (cell_graphs) GF_HIP(hipMemcpy(cell_graphs, dout_g.p, dout_g.bytes(), hipMemcpyDeviceToHost));
     if (cross) GF_HIP(hipMemcpy(cross, dout_c.p, dout_c.bytes(), hipMemcpyDeviceToHost));
     if (stats) {
         stats->ms_prep = ms_prep;
@@ -333,8 +342,8 @@ void kmeans_labels(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t 
     } guard{st};
     GF_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
     DevBuf<uint8_t> dvec;
-    DevBuf<uint32_t> dtrow, dctile, dcoff, out2, cnt;
-    DevBuf<int32_t> tnorm, sums;
+    DevBuf<uint32_t> dtrow, dctile, dcoff, out2, cnt, cstart, cfill, cmem;
+    DevBuf<int32_t> tnorm;
     DevBuf<int8_t> vt;
     DevBuf<KnnItem> ditems;
     DevBuf<uint64_t> state;
@@ -347,8 +356,10 @@ void kmeans_labels(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t 
     tnorm.alloc(size_t(ntile) * 32);
     out2.alloc(size_t(N) * 2);
     state.alloc(size_t(N) * 2);
-    sums.alloc(size_t(C) * Dp);
     cnt.alloc(C);
+    cstart.alloc(C);
+    cfill.alloc(C);
+    cmem.alloc(N);
     const uint32_t ctiles = 1024 / KS, nchunk = (Tc + ctiles - 1) / ctiles;
     KnnArgs ka{};
     ka.vt = vt.p;
@@ -368,9 +379,10 @@ void kmeans_labels(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t 
     for (uint32_t it = 0;; ++it) {
         for (ka.chunk = 0; ka.chunk < nchunk; ++ka.chunk) GF_HIP(launch_knn_i8(ka, KS, uint32_t(ncu), st));
         if (it == iters) break;
-        GF_HIP(hipMemsetAsync(sums.p, 0, sums.bytes(), st));
         GF_HIP(hipMemsetAsync(cnt.p, 0, cnt.bytes(), st));
-        GF_HIP(launch_kmeans_update(dvec.p, Dp, out2.p, N, C, sums.p, cnt.p, dvec.p + size_t(N) * Dp, st));
+        GF_HIP(hipMemsetAsync(cfill.p, 0, cfill.bytes(), st));
+        GF_HIP(launch_kmeans_update(dvec.p, Dp, out2.p, N, C, cnt.p, cstart.p, cfill.p, cmem.p,
+                                    dvec.p + size_t(N) * Dp, st));
         GF_HIP(launch_tile_i8(dvec.p, true, Dp, dtrow.p + size_t(Tp) * 16, 0, Tc, vt.p + size_t(Tp) * KS * 1024,
                               tnorm.p + size_t(Tp) * 32, st));
     }

@@ -154,10 +154,12 @@ struct KnnArgs {
     uint64_t* state;
 };
 hipError_t launch_knn_i8(const KnnArgs& a, uint32_t KS, uint32_t ncu, hipStream_t st);
-// k-means update: sums (C x Dp) and cnt (C) must start at zero; centres
-// (C x Dp u8) are rewritten where a cluster has members.
+// k-means update: cnt and fill (C each) must start at zero; start (C) and
+// mem (N) are scratch; centres (C x Dp u8) are rewritten where a cluster
+// has members.
 hipError_t launch_kmeans_update(const uint8_t* vec, uint32_t Dp, const uint32_t* lab2, uint32_t N, uint32_t C,
-                                int32_t* sums, uint32_t* cnt, uint8_t* centres, hipStream_t st);
+                                uint32_t* cnt, uint32_t* start, uint32_t* fill, uint32_t* mem, uint8_t* centres,
+                                hipStream_t st);
 
 struct BfFinalArgs {
     uint32_t* gbound;          // optional: per query the bound the items reached

@@ -2526,25 +2526,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KT > 40 ? 1
     }
 }
 
-// k-means update of the index builder (integer Lloyd step): per-cluster
-// sums of the u8 rows and member counts, then each centre the rounded mean
-// floor((2 sum + n) / (2 n)) of its members (an empty cluster keeps its
-// centre).  lab2 holds the assignment as (point, 2) pairs, label second.
-__global__ void k_kmeans_accum(const uint8_t* vec, uint32_t Dp, const uint32_t* lab2, uint32_t N, int32_t* sums,
-                               uint32_t* cnt) {
-    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= size_t(N) * Dp) return;
-    const uint32_t pt = uint32_t(i / Dp), d = uint32_t(i % Dp);
-    const uint32_t l = lab2[size_t(pt) * 2u + 1u];
-    atomicAdd(&sums[size_t(l) * Dp + d], int32_t(vec[i]));
-    if (d == 0) atomicAdd(&cnt[l], 1u);
+// k-means update of the index builder (integer Lloyd step): the members of
+// each cluster are listed (count, scan, scatter), then one workgroup per
+// cluster sums its members' u8 rows, a thread per dimension, and moves the
+// centre to the rounded mean floor((2 sum + n) / (2 n)) (an empty cluster
+// keeps its centre).  lab2 holds the assignment as (point, 2) pairs, label
+// second.
+__global__ void k_kmeans_count(const uint32_t* lab2, uint32_t N, uint32_t* cnt) {
+    const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p < N) atomicAdd(&cnt[lab2[size_t(p) * 2u + 1u]], 1u);
 }
 
-__global__ void k_kmeans_centres(const int32_t* sums, const uint32_t* cnt, uint32_t C, uint32_t Dp, uint8_t* centres) {
-    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= size_t(C) * Dp) return;
-    const uint32_t n = cnt[i / Dp];
-    if (n) centres[i] = uint8_t((2 * int64_t(sums[i]) + n) / (2 * int64_t(n)));
+__global__ void k_kmeans_scatter(const uint32_t* lab2, uint32_t N, const uint32_t* start, uint32_t* fill,
+                                 uint32_t* mem) {
+    const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= N) return;
+    const uint32_t l = lab2[size_t(p) * 2u + 1u];
+    mem[start[l] + atomicAdd(&fill[l], 1u)] = p;
+}
+
+__global__ __launch_bounds__(256) void k_kmeans_mean(const uint8_t* vec, uint32_t Dp, const uint32_t* cnt,
+                                                     const uint32_t* start, const uint32_t* mem, uint8_t* centres) {
+    const uint32_t c = blockIdx.x, d = threadIdx.x;
+    const uint32_t n = cnt[c], s0 = start[c];
+    if (n == 0 || d >= Dp) return;
+    // eight members' rows in flight at a time
+    uint32_t sum8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint32_t k = 0;
+    for (; k + 8u <= n; k += 8u) {
+        uint32_t m[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m[i] = mem[s0 + k + i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum8[i] += vec[size_t(m[i]) * Dp + d];
+    }
+    uint64_t sum = 0;
+    for (; k < n; ++k) sum += vec[size_t(mem[s0 + k]) * Dp + d];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sum += sum8[i];
+    centres[size_t(c) * Dp + d] = uint8_t((2 * sum + n) / (2 * uint64_t(n)));
 }
 
 }  // namespace
@@ -2584,13 +2604,15 @@ hipError_t launch_knn_i8(const KnnArgs& a, uint32_t KS, uint32_t ncu, hipStream_
 }
 
 hipError_t launch_kmeans_update(const uint8_t* vec, uint32_t Dp, const uint32_t* lab2, uint32_t N, uint32_t C,
-                                int32_t* sums, uint32_t* cnt, uint8_t* centres, hipStream_t st) {
-    const size_t n1 = size_t(N) * Dp, n2 = size_t(C) * Dp;
-    if (n1 == 0 || n2 == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_kmeans_accum, dim3(uint32_t((n1 + 255) / 256)), dim3(256), 0, st, vec, Dp, lab2, N, sums,
-                       cnt);
-    hipLaunchKernelGGL(k_kmeans_centres, dim3(uint32_t((n2 + 255) / 256)), dim3(256), 0, st, sums, cnt, C, Dp,
-                       centres);
+                                uint32_t* cnt, uint32_t* start, uint32_t* fill, uint32_t* mem, uint8_t* centres,
+                                hipStream_t st) {
+    if (N == 0 || C == 0 || Dp > 256) return N == 0 || C == 0 ? hipSuccess : hipErrorInvalidValue;
+    const uint32_t g = (N + 255) / 256;
+    hipLaunchKernelGGL(k_kmeans_count, dim3(g), dim3(256), 0, st, lab2, N, cnt);
+    hipError_t e = launch_scan_small(cnt, C, start, st);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_kmeans_scatter, dim3(g), dim3(256), 0, st, lab2, N, start, fill, mem);
+    hipLaunchKernelGGL(k_kmeans_mean, dim3(C), dim3(256), 0, st, vec, Dp, cnt, start, mem, centres);
     return hipGetLastError();
 }
 

@@ -248,8 +248,8 @@ typedef struct {
     uint32_t dim;           /* dimension as computed (D rounded up to 64) */
     double ms_prep;         /* host: input checks, cell layout, item lists */
     double ms_upload;       /* device set-up, allocations and uploads */
-    double ms_run;          /* wall time of the kernels */
-    double ms_download;     /* results to the caller's arrays */
+    double ms_run;          /* wall time of the kernels (the graphs' download overlaps the cross pass) */
+    double ms_download;     /* the cross edges to the caller's array */
     double ms_total;        /* the whole call */
 } gf_build_stats;
 
