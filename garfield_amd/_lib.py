@@ -8,6 +8,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 lib_path = os.environ.get("GARFIELD_LIB") or os.path.join(_HERE, "libgarfield.so")
 
 NO_RESULT = 0x7FFFFFFF
+NOALLOC_SCRATCH_MB = 32   # GF_NOALLOC_SCRATCH_MB
 NCOUNTERS = 8
 VEC_F32 = 0
 VEC_F16 = 1
@@ -50,6 +51,10 @@ class _Info(C.Structure):
 class _SearchOpts(C.Structure):
     _fields_ = [("L", C.c_uint32), ("K", C.c_uint32), ("rl", C.c_uint32), ("postfilter", C.c_uint32),
                 ("entry_points", C.c_void_p)]
+
+
+class _NoallocOpts(C.Structure):
+    _fields_ = [("prefilter", C.c_float), ("topc", C.c_uint32), ("search", _SearchOpts)]
 
 
 class _StreamPlan(C.Structure):
@@ -110,6 +115,8 @@ _SYMBOLS = {
                         C.c_uint32, C.c_int32, C.c_void_p, C.c_void_p, C.POINTER(BuildStats)],
     "gf_kmeans": [C.c_void_p, C.c_int32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p, C.c_int32,
                   C.c_void_p, C.c_void_p, C.POINTER(C.c_double)],
+    "gf_search_noalloc": [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.POINTER(_NoallocOpts),
+                          C.c_void_p, C.c_void_p],
     "gf_host_alloc": [C.c_size_t, C.POINTER(C.c_void_p)],
     "gf_host_free": [C.c_void_p],
     "gf_status_str": [C.c_int32],
@@ -362,6 +369,30 @@ class Batch:
         c = np.empty((self.Q, NCOUNTERS), np.uint32)
         _check(load().gf_batch_get_counters(self._h, _ptr(c)))
         return c
+
+
+def search_noalloc(index, queries, lo, hi, prefilter, topc=4, L=64, K=10, rl=10, postfilter=1 << 30,
+                   entry_points=None, out=None):
+    """Stages A, B and C in one call that allocates no device memory
+    (gf_search_noalloc): the same ids and distances as
+    Batch.mark_cells(prefilter) + order_cells(topc) + search(...)."""
+    q = _c(queries, np.float32)
+    lo = _c(lo, np.float32)
+    hi = _c(hi, np.float32)
+    if q.ndim != 2 or q.shape[1] != index.D or lo.shape != (q.shape[0], index.a) or hi.shape != lo.shape:
+        raise ValueError("queries must be (Q, D) and lo/hi (Q, a)")
+    Q = q.shape[0]
+    if out is None:
+        ids = np.empty((Q, K), np.uint32)
+        dists = np.empty((Q, K), np.float32)
+    else:
+        ids, dists = out
+    ent = None if entry_points is None else _c(entry_points, np.uint32)
+    opts = _NoallocOpts(float(prefilter), int(topc),
+                        _SearchOpts(L, K, rl, min(int(postfilter), 0xFFFFFFFF), _ptr(ent)))
+    _check(load().gf_search_noalloc(index._h, _ptr(q), Q, _ptr(lo), _ptr(hi), C.byref(opts), _ptr(ids),
+                                    _ptr(dists)))
+    return ids, dists
 
 
 def f2h(x, alpha=1.0):

@@ -24,7 +24,8 @@ COMMON = [
     "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-deprecated-declarations", "-I", os.path.join(ROOT, "include"),
 ]
-LIB_SOURCES = ["gf_kernels.hip", "gf_host.cpp", "gf_stream.cpp", "gf_io.cpp", "gf_build.cpp"]
+LIB_SOURCES = ["gf_kernels.hip", "gf_host.cpp", "gf_stream.cpp", "gf_io.cpp", "gf_build.cpp",
+               "gf_noalloc.cpp"]
 OBJ_DIR = os.path.join(HERE, "_build")
 
 

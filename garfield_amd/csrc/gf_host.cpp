@@ -89,6 +89,8 @@ void build_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, c
 
 namespace gf {
 
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+
 bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, const std::vector<uint32_t>& size,
                       const std::vector<uint32_t>& offset_h, uint32_t a, uint32_t P, SubHost& out) {
     if (a > 4) return false;
@@ -340,6 +342,17 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
     std::vector<uint32_t> doff(a);
     for (uint32_t d = 0; d < a; ++d) { doff[d] = gsum; gsum += h.grid_shape[d]; }
     ix.l_q.upload(h.l_q, gsum);
+    // The reference's entry-point draw (gpu_graph.cu:12503-12526), made once
+    // per index; an index with no room for it (N <= (P - 1) * ceil(N / P))
+    // searches with the caller's entry points only.
+    {
+        const uint32_t avg = (N + P - 1) / P;
+        if (N > (P - 1) * avg) {
+            std::vector<uint32_t> ent(R);
+            gf::entry_points_draw(N - (P - 1) * avg, R * 10, R, ent.data());
+            ix.entry_ref.upload(ent);
+        }
+    }
     ix.r_q.upload(h.r_q, gsum);
     ix.grid.upload(ix.grid_h);
     ix.doff.upload(doff);

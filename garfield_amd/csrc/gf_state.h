@@ -159,7 +159,7 @@ struct gf_index {
     DevBuf<char> vec;
     DevBuf<float> attrs, l_q, r_q, cnorm;
     DevBuf<uint32_t> graph, cross, offset, gidx, lrow, grid, doff, hist;
-    DevBuf<uint32_t> entry_ref;   // the reference's entry-point draw, made on first use
+    DevBuf<uint32_t> entry_ref;   // the reference's entry-point draw (resident index: made when it is built)
     DevBuf<uint32_t> tile_cell, tile_row0, tile_n;
     DevBuf<uint16_t> centres;
     uint32_t ntiles = 0;
@@ -345,6 +345,8 @@ struct gf_batch {
 
 namespace gf {
 inline void set_device(const gf_index* ix) { GF_HIP(hipSetDevice(ix->device)); }
+// The message gf_last_error() returns on the calling thread.
+void set_last_error(const std::string& msg);
 }  // namespace gf
 
 namespace gf {

@@ -211,6 +211,28 @@ gf_status gf_batch_get_centroid(const gf_batch* b, float* dist /*Q*C*/, uint32_t
 gf_status gf_batch_get_cell_flags(const gf_batch* b, uint8_t* flags);
 gf_status gf_batch_get_counters(const gf_batch* b, uint32_t* counters /*Q*GF_NCOUNTERS*/);
 
+/* One query batch through stages A, B and C in one call that allocates
+ * nothing.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It runs the kernels of gf_batch_create,
+ * gf_mark_cells(prefilter), gf_order_cells(topc) and gf_search(search) on a
+ * resident index and returns the same ids and distances; routed queries take
+ * the gather brute force, whose results equal the MFMA route's.  Every
+ * per-batch buffer is carved from a per-device static array of
+ * GF_NOALLOC_SCRATCH_MB MiB that each GPU holds until the process ends; a
+ * batch whose buffers do not fit (about Q * (4 D + 4 P + 8 K + 64) bytes, plus
+ * 2 D per query with labels) is GF_E_UNSUPPORTED.  The array keeps the last
+ * call's contents and is shared by every call on that GPU: calls that overlap
+ * on one GPU race.  Host arrays need not be page-locked. */
+#define GF_NOALLOC_SCRATCH_MB 32
+typedef struct {
+    float prefilter;         /* as gf_mark_cells */
+    uint32_t topc;           /* as gf_order_cells, 1..4 (unused without labels) */
+    gf_search_opts search;   /* as gf_search */
+} gf_noalloc_opts;
+gf_status gf_search_noalloc(gf_index* ix, const float* queries, uint32_t Q, const float* lo, const float* hi,
+                            const gf_noalloc_opts* opts, uint32_t* ids /*Q*K*/, float* dists /*Q*K or NULL*/);
+
 /* Page-locked host memory (hipHostMalloc).  No counterpart in the reference:
  * result arrays allocated here receive gf_search's device-to-host copies
  * directly, without a staging copy on the host.  Free with gf_host_free. */
