@@ -51,10 +51,14 @@ def main():
     ap.add_argument("--stream-budget-mb", type=int, default=64)
     ap.add_argument("--stream-thresholds", default="1.0,0.25,0.0")
     ap.add_argument("--recall", type=float, default=0.95)
-    ap.add_argument("--prefilters", default="1.0,0.05,0.0")
+    ap.add_argument("--prefilters", default="1.0,0.3,0.2,0.1,0.05,0.0",
+                    help="1.0 = every query to the filtered brute force; below 1, queries whose "
+                         "selectivity is at most the value take the brute force, the rest traverse")
     ap.add_argument("--postfilter", type=int, default=1 << 30)
     ap.add_argument("--L", type=int, default=0, help="fixed L (skip the sweep)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--graph", choices=["knn", "cagra"], default="cagra",
+                    help="per-cell graphs: exact kNN, or optimised (pruned + reverse edges) as cagra.build returns")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traverse", action="store_true", help="skip the traversal roofline line")
     ap.add_argument("--traverse-L", type=int, default=100)
@@ -81,7 +85,8 @@ def main():
     if args.config == "headline":
         cfg = synth.config_headline()
         workload = ("C2 headline: 1M x 128 fp32 (integers 0-255), 2 uint32 attrs on a 4x4 grid, "
-                    "R=32 exact per-cell kNN + E=2 cross edges, C=1000, 10k queries, selectivity log-U[1%,50%], k=10")
+                    f"R=32 per-cell graphs ({'exact 64-NN optimised to 32 (pruned + reverse edges)' if args.graph == 'cagra' else 'exact 32-NN'})"
+                    " + E=2 exact cross edges, C=1000, 10k queries, selectivity log-U[1%,50%], k=10")
     else:
         cfg = synth.config_small()
         workload = "C1: 100k x 128 fp32 (integers 0-255), 2 attrs on 4x4, R=16, E=2, C=100, 1k queries at 30%, k=10"
@@ -90,8 +95,8 @@ def main():
     log(f"data generated N={N} D={D} Q={Q} ({time.time() - t0:.1f}s)")
     t1 = time.time()
     ix = synth.build_index(cfg["vectors"], cfg["attrs"], cfg["grid"], cfg["R"], cfg["E"], cfg["C"],
-                           device="hip")
-    log(f"index built on GPU in {time.time() - t1:.1f}s")
+                           device="hip", graph=args.graph)
+    log(f"index built on GPU in {time.time() - t1:.1f}s ({args.graph} graphs)")
     lo = cfg["lo"].astype(np.float32)
     hi = cfg["hi"].astype(np.float32)
     t1 = time.time()
@@ -121,99 +126,154 @@ def main():
         ex = synth.exact_result_dist(cfg["vectors"], cfg["queries"], ids)
         return synth.recall_at_k(ids, ex, gt_ids, gt_dist)
 
-    # Calibration: for each prefilter, the smallest L of the sweep reaching the target.
-    points = []
+    def timed(prefilter, L, steps, warmup):
+        """steps timed passes after warmup; sums of the device times and the
+        algorithmic work the search statistics report."""
+        for _ in range(warmup):
+            step(prefilter, L)
+        torch.cuda.synchronize()
+        acc = dict(a=0.0, b=0.0, tr=0.0, bf=0.0, bfk=0.0, btr=0.0, bbf=0.0, obf=0.0)
+        t = time.perf_counter()
+        for _ in range(steps):
+            ids, dists, st, ms_a, ms_b = step(prefilter, L)
+            acc["a"] += ms_a
+            acc["b"] += ms_b
+            acc["tr"] += st.ms_traverse
+            acc["bf"] += st.ms_bruteforce
+            acc["bfk"] += st.ms_bf_kernel
+            acc["btr"] += st.bytes_traverse
+            acc["bbf"] += st.bytes_bruteforce
+            acc["obf"] += st.ops_bruteforce
+        torch.cuda.synchronize()
+        acc["elapsed"] = time.perf_counter() - t
+        return ids, st, acc
+
+    # Operating points.  The brute-force route (prefilter 1: every query to
+    # the filtered brute force, exact at any L) and, for each traversal
+    # prefilter, the smallest L of the reference's sweep reaching the target,
+    # read off a full sweep (no early stop), which is reported as the
+    # traversal curve.
+    candidates = []
+    curves = {}
     for pf in [float(x) for x in args.prefilters.split(",")]:
-        sweep = [args.L] if args.L else L_SWEEP
-        for L in sweep:
+        if pf >= 1.0:
+            ids, dists, st, _, _ = step(pf, 10)
+            strict, tie = recall(ids)
+            log(f"prefilter={pf}: recall={tie:.4f} (strict {strict:.4f}) q_bf={st.q_bruteforce}")
+            if tie >= args.recall:
+                candidates.append(dict(prefilter=pf, L=10, recall=tie, strict=strict, route="bruteforce"))
+            continue
+        curve = []
+        for L in ([args.L] if args.L else L_SWEEP):
             t = time.perf_counter()
             ids, dists, st, ms_a, ms_b = step(pf, L)
             wall = time.perf_counter() - t
             strict, tie = recall(ids)
             gbs = st.bytes_traverse / max(st.ms_traverse, 1e-9) / 1e6
+            curve.append({"L": L, "recall": round(tie, 4), "recall_strict": round(strict, 4),
+                          "qps_step": round(Q / wall, 1), "ms_traverse": round(st.ms_traverse, 3),
+                          "ms_bruteforce": round(st.ms_bruteforce, 3), "traverse_GBs": round(gbs, 1),
+                          "traverse_frac": round(gbs / HBM_PEAK_GBS, 4), "q_traverse": st.q_traverse,
+                          "q_bruteforce": st.q_bruteforce})
             log(f"prefilter={pf} L={L}: recall={tie:.4f} (strict {strict:.4f}) step={wall * 1e3:.1f}ms "
-                f"trav_GBs={gbs:.0f} "
-                f"trav={st.ms_traverse:.1f}ms bf={st.ms_bruteforce:.1f}ms A={ms_a:.2f}ms B={ms_b:.2f}ms "
-                f"q_trav={st.q_traverse} q_bf={st.q_bruteforce}")
-            if tie >= args.recall or args.L:
-                points.append(dict(prefilter=pf, L=L, recall=tie, strict=strict, wall=wall))
-                break
-            if points and wall > 2 * min(p["wall"] for p in points):
-                break   # slower than a known operating point already
-    if not points:
+                f"trav={st.ms_traverse:.1f}ms ({gbs:.0f} GB/s) bf={st.ms_bruteforce:.1f}ms A={ms_a:.2f}ms "
+                f"B={ms_b:.2f}ms q_trav={st.q_traverse} q_bf={st.q_bruteforce}")
+        curves[str(pf)] = curve
+        reach = [c for c in curve if c["recall"] >= args.recall]
+        if reach:
+            c = reach[0]
+            candidates.append(dict(prefilter=pf, L=c["L"], recall=c["recall"], strict=c["recall_strict"],
+                                   route="traversal"))
+    if not candidates:
         raise SystemExit("no operating point reached the recall target")
-    best = min(points, key=lambda p: p["wall"])
+    for c in candidates:
+        _, _, acc = timed(c["prefilter"], c["L"], max(3, args.steps // 4), 1)
+        c["qps"] = Q * max(3, args.steps // 4) / acc["elapsed"]
+        log(f"candidate {c['route']} prefilter={c['prefilter']} L={c['L']}: {c['qps']:.0f} QPS")
+    best = max(candidates, key=lambda c: c["qps"])
     pf, L = best["prefilter"], best["L"]
-    log(f"operating point: prefilter={pf} L={L} recall={best['recall']:.4f}")
+    log(f"operating point: {best['route']} prefilter={pf} L={L} recall={best['recall']:.4f}")
 
-    for _ in range(args.warmup):
-        step(pf, L)
-    torch.cuda.synchronize()
-    ms_a_sum = ms_b_sum = ms_tr = ms_bf = ms_bfk = bytes_tr = bytes_bf = ops_bf = 0.0
-    last = None
-    t = time.perf_counter()
-    for _ in range(args.steps):
-        ids, dists, st, ms_a, ms_b = step(pf, L)
-        ms_a_sum += ms_a
-        ms_b_sum += ms_b
-        ms_tr += st.ms_traverse
-        ms_bf += st.ms_bruteforce
-        bytes_tr += st.bytes_traverse
-        bytes_bf += st.bytes_bruteforce
-        ops_bf += st.ops_bruteforce
-        ms_bfk += st.ms_bf_kernel
-        last = st
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t
+    ids, last, acc = timed(pf, L, args.steps, args.warmup)
+    elapsed = acc["elapsed"]
     K = args.steps
     strict, tie = recall(ids)
     qps = Q * K / elapsed
     ms_per_step = elapsed * 1e3 / K
+    ms_a_sum, ms_b_sum, ms_tr, ms_bf, ms_bfk = acc["a"], acc["b"], acc["tr"], acc["bf"], acc["bfk"]
     qps_ref = Q / ((ms_a_sum + ms_b_sum + ms_tr + ms_bf) / K / 1e3)
     # Dominant kernel: the one with the larger device time in the timed steps.
-    # The int8 query-batch brute force is a GEMM and is priced against the
-    # int8 MFMA peak; the traversal and gather brute force against HBM.
+    traffic = profiled_traffic()
     if ms_tr >= ms_bf:
-        dom, dom_bytes, dom_ms, mfma = "k_traverse", bytes_tr, ms_tr, False
+        dom, dom_bytes, dom_ms, mfma = "k_traverse", acc["btr"], ms_tr, False
     else:
         mfma = bool(last.bf_mfma)
         # the MFMA kernel alone (its schedule and the final merge are timed in ms_bruteforce)
-        dom, dom_bytes, dom_ms = ("k_bf_i8" if mfma else "k_bruteforce"), bytes_bf, (ms_bfk if mfma else ms_bf)
+        dom, dom_bytes, dom_ms = ("k_bf_i8" if mfma else "k_bruteforce"), acc["bbf"], (ms_bfk if mfma else ms_bf)
     if mfma:
-        achieved = (ops_bf / K) / (dom_ms / K / 1e3) / 1e12 if dom_ms > 0 else 0.0
+        # Algorithmic work of the int8 brute force: D multiply-adds (2 D ops)
+        # per (query, point) pair that passes the query's filter.  The
+        # kernel evaluates every point of every sub-cell a range reaches
+        # (ops_scheduled); the pairs that pass come from the exact counts,
+        # made once after the timed steps (with prefilter >= 1 stage A routes
+        # without them).
+        ctr = b.get_counters()
+        n_pass = int(ctr[ctr[:, 7] == 2, 6].sum(dtype=np.int64))
+        ops_alg = 2.0 * D * n_pass
+        achieved = ops_alg / (dom_ms / K / 1e3) / 1e12 if dom_ms > 0 else 0.0
+        tr = traffic.get("k_bf_i8")
         roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                     "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "op_kind": "int8 MAC x2 (TOP/s)",
-                    "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": None,
-                    "ops_per_launch": round(ops_bf / K), "bytes_per_launch": round(dom_bytes / K),
-                    "ms_per_launch": round(dom_ms / K, 4)}
+                    "frac": round(achieved / INT8_PEAK_TOPS, 4),
+                    "traffic": tr["bytes"] if tr else None,
+                    "traffic_source": tr["source"] if tr else None,
+                    "ops_per_launch": round(ops_alg), "pairs_passing": n_pass,
+                    "ops_scheduled_per_launch": round(acc["obf"] / K),
+                    "bytes_per_launch": round(dom_bytes / K), "ms_per_launch": round(dom_ms / K, 4),
+                    "launch": "one search: three k_bf_i8 launches and the two bound merges between them"}
         dom_desc = f"{achieved:.1f} TOP/s"
     else:
         achieved = (dom_bytes / K) / (dom_ms / K / 1e3) / 1e9 if dom_ms > 0 else 0.0
+        tr = traffic.get(dom)
         roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": tr["bytes"] if tr else None, "traffic_source": tr["source"] if tr else None,
                     "bytes_per_launch": round(dom_bytes / K), "ms_per_launch": round(dom_ms / K, 4)}
         dom_desc = f"{achieved:.0f} GB/s"
     log(f"timed: {qps:.0f} QPS end-to-end, {qps_ref:.0f} QPS (reference definition), "
         f"{dom} {dom_ms / K:.2f} ms at {dom_desc}")
 
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(cfg, ix, b, L, pf, args)
-
-    # The traversal kernel priced against HBM on the same batch: every query
-    # traversed (prefilter 0), at the sweep's L for recall >= 0.5 or L=100.
+    # The traversal route at its own operating point (the smallest L reaching
+    # the target with prefilter 0, else with the other traversal prefilter),
+    # timed, with k_traverse priced against HBM.
     trav = None
     if not args.no_traverse:
-        Lt = args.traverse_L
-        _, _, stt, _, _ = step(0.0, Lt)
-        ms_t = stt.ms_traverse
-        gbs = stt.bytes_traverse / (ms_t / 1e3) / 1e9 if ms_t > 0 else 0.0
-        trav = {"bound": "hbm", "kernel": "k_traverse", "L": Lt, "prefilter": 0.0,
-                "queries": stt.q_traverse, "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": round(stt.bytes_traverse),
-                "ms_per_launch": round(ms_t, 4), "traffic": None}
-        log(f"traversal at L={Lt}: {ms_t:.2f} ms, {gbs:.0f} GB/s algorithmic ({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+        tc = [c for c in candidates if c["route"] == "traversal"]
+        if tc:
+            tp = max(tc, key=lambda c: c["qps"])
+            tpf, tL, trec = tp["prefilter"], tp["L"], tp["recall"]
+        else:
+            tpf, tL, trec = 0.0, args.traverse_L, None
+        tsteps = max(3, args.steps // 4)
+        tids, stt, tacc = timed(tpf, tL, tsteps, 1)
+        ms_t = tacc["tr"] / tsteps
+        gbs = tacc["btr"] / tsteps / (ms_t / 1e3) / 1e9 if ms_t > 0 else 0.0
+        tr = traffic.get(f"k_traverse@{tpf}:{tL}")
+        trav = {"bound": "hbm", "kernel": "k_traverse", "prefilter": tpf, "L": tL,
+                "recall_at_10": round(recall(tids)[1], 4), "reaches_target": trec is not None,
+                "qps": round(Q * tsteps / tacc["elapsed"], 1), "queries_traversed": stt.q_traverse,
+                "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": round(tacc["btr"] / tsteps),
+                "ms_per_launch": round(ms_t, 4), "traffic": tr["bytes"] if tr else None,
+                "traffic_source": tr["source"] if tr else None}
+        log(f"traversal route: prefilter={tpf} L={tL}: {trav['qps']:.0f} QPS, recall {trav['recall_at_10']}, "
+            f"k_traverse {ms_t:.2f} ms, {gbs:.0f} GB/s algorithmic ({gbs / HBM_PEAK_GBS:.1%} of HBM)")
 
+    cpu = cpu_trav = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cfg, ix, b, L, pf, args)
+        if trav is not None and best["route"] != "traversal":
+            cpu_trav = cpu_baseline(cfg, ix, b, trav["L"], trav["prefilter"], args)
 
     out = {
         "metric": METRIC,
@@ -227,20 +287,28 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "i8" if (last.bf_mfma and ms_bf > ms_tr) else "f32",
-        "data": "synthetic (generated in bench.py; exact kNN index built on the GPU)",
+        "data": "synthetic (generated in bench.py; index built on the GPU by the library's builder)",
         "config": {
             "workload": workload,
+            "route": ("filtered brute force (int8 MFMA query-batch kernel)" if best["route"] == "bruteforce"
+                      else "cell-by-cell graph traversal (queries at or below the prefilter selectivity "
+                           "to filtered brute force)"),
             "N": N, "D": D, "Q": Q, "K": 10, "L": L,
             "prefilter": pf, "postfilter": args.postfilter, "f2h_factor": 1.0, "degree": cfg["R"],
+            "graph": args.graph,
             "recall_at_10": round(tie, 4), "recall_at_10_strict": round(strict, 4),
             "qps_reference_definition": round(qps_ref, 1),
             "ms_stage_a": round(ms_a_sum / K, 3), "ms_stage_b": round(ms_b_sum / K, 3),
             "ms_traverse": round(ms_tr / K, 3), "ms_bruteforce": round(ms_bf / K, 3),
             "q_traverse": last.q_traverse, "q_bruteforce": last.q_bruteforce, "q_empty": last.q_empty,
+            "candidates": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in c.items()}
+                           for c in candidates],
         },
         "roofline": roofline,
-        "roofline_traverse": trav,
+        "traverse_operating_point": trav,
+        "traverse_curve": curves,
         "cpu_baseline": cpu,
+        "cpu_baseline_traverse": cpu_trav,
     }
     print(json.dumps(out), flush=True)
     if args.calib_copy_mb:
@@ -251,6 +319,22 @@ def main():
             torch.add(x, 1.0, out=y)
         torch.cuda.synchronize()
         log(f"calibration: 3 x y = x + 1 over {args.calib_copy_mb} MiB (reads and writes {n * 4} bytes each)")
+
+
+def profiled_traffic():
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE, then
+    WRITE_SIZE, each scaled by a copy kernel of known size) and committed in
+    profiles/traffic_C2.md as lines `traffic <kernel> <bytes>`; bench.py
+    cannot read hardware counters from inside its own process."""
+    path = os.path.join(ROOT, "profiles", "traffic_C2.md")
+    out = {}
+    if not os.path.exists(path):
+        return out
+    for line in open(path):
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == "traffic":
+            out[parts[1]] = {"bytes": int(float(parts[2])), "source": "profiles/traffic_C2.md"}
+    return out
 
 
 PCIE_PEAK_GBS = 64.0   # PCIe 5.0 x16, one direction
@@ -462,6 +546,8 @@ def cpu_baseline(cfg, ix, batch, L, prefilter, args):
     cells, counts, little, _ = batch.get_cells()
     O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"], ix["cross"])
     ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], ix["R"])
+    # The GPU box allots 16 host cores to its one GPU (OMP_NUM_THREADS is
+    # set to that share there); os.cpu_count() sees the whole host.
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
     lo = cfg["lo"].astype(np.float32)
     hi = cfg["hi"].astype(np.float32)
@@ -478,10 +564,24 @@ def cpu_baseline(cfg, ix, batch, L, prefilter, args):
         if dt >= args.cpu_seconds or n >= Q:
             break
         n = min(Q, max(n * 2, int(n * args.cpu_seconds / max(dt, 1e-3) * 1.1)))
-    log(f"cpu baseline: {n} queries in {dt:.1f}s on {threads} threads")
+    routed = int(np.sum((little[sel] == counts[sel]) & (counts[sel] > 0)))
+    log(f"cpu baseline (prefilter {prefilter}, L {L}): {n} queries in {dt:.1f}s on {threads} threads")
     return {"value": round(n / dt, 1), "unit": "queries/s", "cores": threads, "kind": "port",
-            "sample": f"{n} random queries of the same batch (same cells, routing, L={L}, "
-                      f"prefilter={prefilter}), traversal/brute force only (stages A/B not timed)"}
+            "route": "filtered brute force" if prefilter >= 1.0 else "traversal (+ brute force below the prefilter)",
+            "host_cpu": host_cpu_model(), "host_nproc": os.cpu_count(),
+            "sample": f"{n} random queries of the same batch ({routed} on the brute force; same cells, routing, "
+                      f"L={L}, prefilter={prefilter}), search stage only (stages A/B not timed), OpenMP over "
+                      f"queries on {threads} threads (the GPU box's host-core share for one GPU)"}
+
+
+def host_cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 if __name__ == "__main__":

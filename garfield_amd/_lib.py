@@ -30,7 +30,7 @@ class _Paths(C.Structure):
 
 class _OpenOpts(C.Structure):
     _fields_ = [("degree", C.c_uint32), ("f2h_factor", C.c_float), ("vec_dtype", C.c_int32),
-                ("hist_contiguous", C.c_int32), ("device", C.c_int32)]
+                ("hist_contiguous", C.c_int32), ("device", C.c_int32), ("ref_ties", C.c_int32)]
 
 
 class _Host(C.Structure):
@@ -113,6 +113,8 @@ _SYMBOLS = {
                         C.c_void_p],
     "gf_build_graphs": [C.c_void_p, C.c_int32, C.c_uint32, C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32,
                         C.c_uint32, C.c_int32, C.c_void_p, C.c_void_p, C.POINTER(BuildStats)],
+    "gf_optimize_graphs": [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32, C.c_int32,
+                           C.c_void_p, C.POINTER(C.c_double)],
     "gf_kmeans": [C.c_void_p, C.c_int32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p, C.c_int32,
                   C.c_void_p, C.c_void_p, C.POINTER(C.c_double)],
     "gf_search_noalloc": [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.POINTER(_NoallocOpts),
@@ -156,9 +158,9 @@ def _c(a, dtype):
     return np.ascontiguousarray(a, dtype=dtype)
 
 
-def _opts(degree, f2h_factor, vec_dtype, hist_contiguous, device):
+def _opts(degree, f2h_factor, vec_dtype, hist_contiguous, device, ref_ties=False):
     return _OpenOpts(degree=degree, f2h_factor=f2h_factor, vec_dtype=vec_dtype,
-                     hist_contiguous=int(hist_contiguous), device=device)
+                     hist_contiguous=int(hist_contiguous), device=device, ref_ties=int(ref_ties))
 
 
 class Index:
@@ -176,19 +178,20 @@ class Index:
 
     @classmethod
     def open(cls, data_path, cagra_prefix, cagra_suffix, global_graph, grid, attrs, cluster=None,
-             degree=0, f2h_factor=1.0, vec_dtype=VEC_F32, hist_contiguous=False, device=0):
+             degree=0, f2h_factor=1.0, vec_dtype=VEC_F32, hist_contiguous=False, device=0, ref_ties=False):
         enc = lambda s: None if s is None else str(s).encode()
         paths = _Paths(enc(data_path), enc(cagra_prefix), enc(cagra_suffix), enc(global_graph),
                        enc(grid), enc(attrs), enc(cluster))
         h = C.c_void_p()
         _check(load().gf_index_open(C.byref(paths), C.byref(_opts(degree, f2h_factor, vec_dtype,
-                                                                    hist_contiguous, device)), C.byref(h)))
+                                                                    hist_contiguous, device, ref_ties)),
+                                    C.byref(h)))
         return cls(h)
 
     @classmethod
     def from_arrays(cls, vectors, attrs, grid_shape, l_q, r_q, global_pid, cell_graphs, cross,
                     labels=None, f2h_factor=1.0, vec_dtype=VEC_F32, hist_contiguous=False, device=0,
-                    degree=0):
+                    degree=0, ref_ties=False):
         """Arrays as in the files: vectors (N,D) point order, cell_graphs (N,R)
         concatenated per cell in cell order, cross (N, P*E) point order."""
         keep = dict(
@@ -206,7 +209,8 @@ class Index:
                      _ptr(keep["cross"]), _ptr(keep["labels"]))
         h = C.c_void_p()
         _check(load().gf_index_create(C.byref(host), C.byref(_opts(degree, f2h_factor, vec_dtype,
-                                                                     hist_contiguous, device)), C.byref(h)))
+                                                                     hist_contiguous, device, ref_ties)),
+                                      C.byref(h)))
         return cls(h)
 
     @staticmethod
@@ -457,6 +461,18 @@ def build_graphs(vectors, global_pid, P, R, E, device=0, graphs=True, cross=True
     _check(load().gf_build_graphs(_ptr(v), vt, n, d, _ptr(gp), P, R if graphs else 0, E if cross else 0,
                                   device, _ptr(g), _ptr(x), C.byref(st)))
     return g, x, st
+
+
+def optimize_graphs(knn_graphs, cell_sizes, R, device=0):
+    """gf_optimize_graphs: the kNN graphs (N, I) -> optimised graphs (N, R)
+    (rank-based reordering by detourable routes, then reverse edges)."""
+    g = _c(knn_graphs, np.uint32)
+    sz = _c(cell_sizes, np.uint32)
+    N, I = g.shape
+    out = np.empty((N, R), np.uint32)
+    ms = C.c_double()
+    _check(load().gf_optimize_graphs(_ptr(g), N, I, _ptr(sz), sz.size, R, device, _ptr(out), C.byref(ms)))
+    return out, ms.value
 
 
 def kmeans(vectors, ncent, iters, init_ids=None, seed=5, device=0):

@@ -289,6 +289,70 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
     }
 }
 
+void optimize_graphs(const uint32_t* knn, uint32_t N, uint32_t I, const uint32_t* cell_size, uint32_t P,
+                     uint32_t R, int32_t device, uint32_t* graphs, double* ms) {
+    const auto t0 = std::chrono::steady_clock::now();
+    GF_REQUIRE(knn && cell_size && graphs, GF_E_ARG, "null argument");
+    GF_REQUIRE(N > 0 && P > 0, GF_E_ARG, "empty graph");
+    GF_REQUIRE(I >= 1 && I <= 64, GF_E_UNSUPPORTED, "input degree must be in [1, 64]");
+    GF_REQUIRE(R >= 1 && R <= I, GF_E_ARG, "output degree must be in [1, input degree]");
+    std::vector<uint32_t> offset(P + 1, 0);
+    for (uint32_t c = 0; c < P; ++c) offset[c + 1] = offset[c] + cell_size[c];
+    GF_REQUIRE(offset[P] == N, GF_E_ARG, "cell sizes do not add up to N");
+    for (uint32_t c = 0; c < P; ++c)
+        for (size_t k = size_t(offset[c]) * I; k < size_t(offset[c + 1]) * I; ++k)
+            GF_REQUIRE(knn[k] < cell_size[c], GF_E_FORMAT, "kNN graph holds an id beyond its cell");
+    std::vector<uint32_t> ord(size_t(N) * I);
+    {
+        GF_HIP(hipSetDevice(device));
+        hipStream_t st = nullptr;
+        GF_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+        struct StreamGuard {
+            hipStream_t s;
+            ~StreamGuard() { (void)hipStreamDestroy(s); }
+        } guard{st};
+        DevBuf<uint32_t> dk, doff, dout;
+        dk.upload(knn, size_t(N) * I);
+        doff.upload(offset);
+        dout.alloc(size_t(N) * I);
+        GF_HIP(launch_prune(dk.p, N, I, doff.p, P, dout.p, st));
+        GF_HIP(hipMemcpyAsync(ord.data(), dout.p, ord.size() * 4, hipMemcpyDeviceToHost, st));
+        GF_HIP(hipStreamSynchronize(st));
+    }
+    // Reverse edges: for every rank k of the pruned lists (their first R
+    // entries), in node order, the edge A -> B adds A to B's reverse list
+    // (at most R, a node never lists itself).  Each row then keeps the first
+    // R / 2 pruned edges, appends reverse edges, then the rest of its
+    // reordered list, each id once; a row still short (a cell of fewer than
+    // R + 1 points) repeats its first entry.
+    const uint32_t keep = R / 2;
+    std::vector<uint32_t> mark;
+    for (uint32_t c = 0; c < P; ++c) {
+        const uint32_t off = offset[c], n = cell_size[c];
+        std::vector<uint32_t> rev(size_t(n) * R), rcnt(n, 0);
+        for (uint32_t k = 0; k < R; ++k)
+            for (uint32_t a = 0; a < n; ++a) {
+                const uint32_t b = ord[(size_t(off) + a) * I + k];
+                if (b != a && rcnt[b] < R) rev[size_t(b) * R + rcnt[b]++] = a;
+            }
+        mark.assign(n, 0);
+        for (uint32_t a = 0; a < n; ++a) {
+            const uint32_t* o = &ord[(size_t(off) + a) * I];
+            uint32_t* g = graphs + (size_t(off) + a) * R;
+            const uint32_t stamp = a + 1;
+            uint32_t m = 0;
+            auto put = [&](uint32_t x) {
+                if (m < R && mark[x] != stamp) { mark[x] = stamp; g[m++] = x; }
+            };
+            for (uint32_t k = 0; k < keep; ++k) put(o[k]);
+            for (uint32_t t = 0; t < rcnt[a]; ++t) put(rev[size_t(a) * R + t]);
+            for (uint32_t k = keep; k < I; ++k) put(o[k]);
+            for (; m < R; ++m) g[m] = g[0];
+        }
+    }
+    if (ms) *ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
 void kmeans_labels(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, uint32_t C, uint32_t iters,
                    const uint32_t* init_ids, int32_t device, int32_t* labels, uint8_t* centres, double* ms) {
     GF_REQUIRE(vectors && init_ids && labels && N > 0 && D > 0, GF_E_ARG, "kmeans: empty input");

@@ -114,7 +114,7 @@ int main(int argc, char** argv) {
 
     gf_index_paths paths{data_path.c_str(), cagra_prefix.c_str(), cagra_suffix.c_str(), global_graph.c_str(),
                          grid.c_str(),      attrs.c_str(),        cluster.empty() ? nullptr : cluster.c_str()};
-    gf_open_opts oo{degree, f2h_factor, vec_dtype, 0, device};
+    gf_open_opts oo{degree, f2h_factor, vec_dtype, 0, device, 0};
     gf_index* ix = nullptr;
     check(gf_index_open(&paths, &oo, &ix), "gf_index_open");
     gf_index_info info{};

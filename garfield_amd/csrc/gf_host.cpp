@@ -195,6 +195,7 @@ void map_cells(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix, s
     ix.device = opts ? opts->device : 0;
     ix.vdtype = opts ? opts->vec_dtype : GF_VEC_F32;
     ix.alpha = (opts && opts->f2h_factor != 0.0f) ? opts->f2h_factor : 1.0f;
+    ix.ref_ties = opts && opts->ref_ties;
     GF_REQUIRE(ix.vdtype == GF_VEC_F32 || ix.vdtype == GF_VEC_F16 || ix.vdtype == GF_VEC_U8, GF_E_ARG,
                "vec_dtype must be GF_VEC_F32, GF_VEC_F16 or GF_VEC_U8");
     GF_REQUIRE(!(opts && opts->degree) || opts->degree == h.R, GF_E_FORMAT, "--degree does not match the graph files");
@@ -713,14 +714,14 @@ gf_status gf_order_cells(gf_batch* b, uint32_t topc, double* ms) {
             GF_HIP(gf::launch_centroid_top(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp,
                                            ix->Cp, ix->Dp, topc, b->topk.p, st));
             GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, nullptr, ix->hist.p, b->cells.p, b->counts.p,
-                                    b->topk.p, st, true));
+                                    b->topk.p, st, true, ix->ref_ties));
             b->cdist_ready = false;
         } else {
             if (!b->cdist.p) b->cdist.alloc(size_t(b->Q) * ix->C);
             GF_HIP(gf::launch_centroid(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp, ix->Cp,
                                        ix->Dp, b->cdist.p, st));
             GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, b->cdist.p, ix->hist.p, b->cells.p, b->counts.p,
-                                    b->topk.p, st));
+                                    b->topk.p, st, false, ix->ref_ties));
             b->cdist_ready = true;
         }
         b->ordered = true;
@@ -1213,6 +1214,11 @@ gf_status gf_build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, ui
     return run_guarded([&] {
         gf::build_graphs(vectors, vec_dtype, N, D, global_pid, P, R, E, device, cell_graphs, cross, stats);
     });
+}
+
+gf_status gf_optimize_graphs(const uint32_t* knn_graphs, uint32_t N, uint32_t I, const uint32_t* cell_size,
+                             uint32_t P, uint32_t R, int32_t device, uint32_t* graphs, double* ms) {
+    return run_guarded([&] { gf::optimize_graphs(knn_graphs, N, I, cell_size, P, R, device, graphs, ms); });
 }
 
 gf_status gf_kmeans(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, uint32_t C, uint32_t iters,

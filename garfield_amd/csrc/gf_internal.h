@@ -154,6 +154,11 @@ struct KnnArgs {
     uint64_t* state;
 };
 hipError_t launch_knn_i8(const KnnArgs& a, uint32_t KS, uint32_t ncu, hipStream_t st);
+// Graph optimisation, first step: every row's I neighbours (cell-local ids,
+// rows cell-major, offset P + 1) rewritten in ascending (detourable routes,
+// rank) order.  I <= 64.
+hipError_t launch_prune(const uint32_t* knn, uint32_t N, uint32_t I, const uint32_t* offset, uint32_t P,
+                        uint32_t* out, hipStream_t st);
 // k-means update: cnt and fill (C each) must start at zero; start (C) and
 // mem (N) are scratch; centres (C x Dp u8) are rewritten where a cluster
 // has members.
@@ -363,9 +368,10 @@ hipError_t launch_centroid(const uint16_t* qh, const uint16_t* ch, const float* 
                            const float* cn, uint32_t Q, uint32_t C, uint32_t Qp, uint32_t Cp,
                            uint32_t Dp, float* dist, hipStream_t st);
 // chosen: topk already holds each query's topc nearest centres (dist unused).
+// ref_ties: equal scores keep the reference's sorting-network order.
 hipError_t launch_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc, const float* dist,
                         const uint32_t* hist, uint32_t* cells, const uint32_t* counts,
-                        uint32_t* topk, hipStream_t st, bool chosen = false);
+                        uint32_t* topk, hipStream_t st, bool chosen = false, bool ref_ties = false);
 // Each query's topc (<= 4) nearest centres without the distance matrix.
 hipError_t launch_centroid_top(const uint16_t* qh, const uint16_t* ch, const float* qn, const float* cn, uint32_t Q,
                                uint32_t C, uint32_t Qp, uint32_t Cp, uint32_t Dp, uint32_t topc, uint32_t* topk,

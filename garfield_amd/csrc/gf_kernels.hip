@@ -538,19 +538,33 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
     }
     if (cvalid(readlane64(rc, 0))) merge_into(A, L, rc, p.rl, nullptr);
 
-    // First K distinct ids (duplicates are adjacent: equal keys).
+    // First K distinct ids.  Copies of one row with equal keys are adjacent,
+    // but a row can also sit once with its distance and again at +inf (a
+    // neighbour met again after the visited set forgot it), so each candidate
+    // is checked against the earlier lanes of its chunk and against the rows
+    // already output (kept in S, free from here on).
     uint32_t n = 0;
     for (uint32_t base = 0; base < L && n < p.K; base += 64u) {
         const uint32_t i = base + lane;
         const uint64_t c = i < L ? A[i] : kCandSent;
+        const uint32_t row = crow(c);
         bool distinct = cvalid(c);
-        if (distinct && i > 0) distinct = crow(A[i - 1]) != crow(c);
+        for (uint32_t l2 = 0; l2 < 64u; ++l2) {
+            const uint32_t r2 = readlane32(row, l2);
+            if (l2 < lane && r2 == row) distinct = false;
+        }
+        const uint32_t nout = n < p.K ? n : p.K;
+        for (uint32_t t = 0; t < nout; ++t)
+            if (S[t] == row) distinct = false;
         const uint64_t m = ballot(distinct);
         const uint32_t idx = n + lanes_below(m);
+        wave_sync();
         if (distinct && idx < p.K) {
-            p.out_ids[size_t(q) * p.K + idx] = p.gidx[crow(c)];
+            p.out_ids[size_t(q) * p.K + idx] = p.gidx[row];
             p.out_dist[size_t(q) * p.K + idx] = cdist(c);
+            S[idx] = row;
         }
+        wave_sync();
         n += __popcll(m);
         if (!cvalid(readlane64(c, 63))) break;
     }
@@ -1242,10 +1256,13 @@ __global__ __launch_bounds__(64 * kCtW) void k_centroid_top(const uint16_t* qh, 
 // gpu_graph.cu:11343-11396): one wave per query picks its topc nearest centres
 // by (distance, index) -- NaN (empty cluster) counts as +inf -- scores every
 // selected cell by the sum of its histogram entries over those centres and
-// sorts the cells by (score descending, cell ascending).
+// sorts the cells by (score descending, cell ascending), or, with ref_ties, by
+// the reference's own network, bitonic_sort_id_by_num_int (gpu_graph.cu:123-141)
+// over the cells in their stage A order: a descending flip-bitonic network
+// whose order of equal scores is fixed by the network, not by the cells.
 __global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc,
                                               const float* dist, const uint32_t* hist, uint32_t* cells,
-                                              const uint32_t* counts, uint32_t* topk, bool chosen) {
+                                              const uint32_t* counts, uint32_t* topk, bool chosen, bool ref_ties) {
     extern __shared__ uint32_t so[];
     uint32_t* tk = so;             // topc
     uint32_t* sc = so + 16;        // P scores
@@ -1287,6 +1304,25 @@ __global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P
         cc[i] = cell;
     }
     __syncthreads();
+    if (ref_ties) {
+        // The pairs (u, d) of one (stride, step) pass are disjoint.
+        for (uint32_t stride = 1; stride < n; stride <<= 1)
+            for (uint32_t step = stride; step > 0; step >>= 1) {
+                for (uint32_t k = lane; k < n / 2; k += 64u) {
+                    const uint32_t a0 = 2 * step * (k / step), b0 = k % step;
+                    const uint32_t u = step == stride ? a0 + step - 1 - b0 : a0 + b0;
+                    const uint32_t d = a0 + b0 + step;
+                    if (d < n && int32_t(sc[u]) < int32_t(sc[d])) {
+                        const uint32_t ts = sc[u], tc = cc[u];
+                        sc[u] = sc[d]; cc[u] = cc[d];
+                        sc[d] = ts; cc[d] = tc;
+                    }
+                }
+                __syncthreads();
+            }
+        for (uint32_t i = lane; i < n; i += 64u) cl[i] = cc[i];
+        return;
+    }
     for (uint32_t i = lane; i < n; i += 64u) {
         const uint32_t s = sc[i], cell = cc[i];
         uint32_t rank = 0;
@@ -2567,7 +2603,57 @@ __global__ __launch_bounds__(256) void k_kmeans_mean(const uint8_t* vec, uint32_
     centres[size_t(c) * Dp + d] = uint8_t((2 * sum + n) / (2 * uint64_t(n)));
 }
 
+// Rank-based reordering of a kNN graph, the first step of CAGRA's graph
+// optimisation (Ootomo et al., "CAGRA: Highly Parallel Graph Construction and
+// Approximate Nearest Neighbor Search for GPUs", ICDE 2024): the edge A -> D
+// at rank k of A's list has a detour through every B at a rank below k in A's
+// list that lists D at a rank below k; A's edges are written in ascending
+// (detours, rank) order.  One wave per row: A's I neighbour lists are staged
+// in LDS (I x I ids) and lane k counts the detours of edge k.  Rows are
+// cell-major and ids cell-local (row = offset[cell] + id).
+__global__ __launch_bounds__(64) void k_prune(const uint32_t* knn, uint32_t N, uint32_t I, const uint32_t* offset,
+                                              uint32_t P, uint32_t* out) {
+    extern __shared__ uint32_t nl[];   // I x I
+    const uint32_t lane = lane_id(), row = blockIdx.x;
+    if (row >= N) return;
+    uint32_t lo = 0, hi = P;           // the cell: last c with offset[c] <= row
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (offset[mid] <= row) lo = mid; else hi = mid;
+    }
+    const uint32_t base = offset[lo];
+    const uint32_t d = lane < I ? knn[size_t(row) * I + lane] : kEmpty;
+    for (uint32_t k = 0; k < I; ++k) {
+        const uint32_t b = readlane32(d, k);
+        if (lane < I) nl[k * I + lane] = knn[(size_t(base) + b) * I + lane];
+    }
+    __syncthreads();
+    uint32_t cnt = 0;
+    if (lane < I) {
+        for (uint32_t kb = 0; kb < lane; ++kb) {
+            const uint32_t* lb = nl + kb * I;
+            bool f = false;
+            for (uint32_t j = 0; j < lane; ++j) f = f || lb[j] == d;
+            cnt += f ? 1u : 0u;
+        }
+    }
+    uint32_t pos = 0;
+    for (uint32_t k = 0; k < I; ++k) {
+        const uint32_t ck = readlane32(cnt, k);
+        pos += (ck < cnt || (ck == cnt && k < lane)) ? 1u : 0u;
+    }
+    if (lane < I) out[size_t(row) * I + pos] = d;
+}
+
 }  // namespace
+
+hipError_t launch_prune(const uint32_t* knn, uint32_t N, uint32_t I, const uint32_t* offset, uint32_t P,
+                        uint32_t* out, hipStream_t st) {
+    if (!N) return hipSuccess;
+    if (I < 1 || I > 64) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_prune, dim3(N), dim3(64), size_t(I) * I * sizeof(uint32_t), st, knn, N, I, offset, P, out);
+    return hipGetLastError();
+}
 
 template <int KS, int KT, int NB = 1>
 static hipError_t launch_knn_i8_t(const KnnArgs& a, uint32_t ncu, hipStream_t st) {
@@ -2963,10 +3049,11 @@ hipError_t launch_centroid(const uint16_t* qh, const uint16_t* ch, const float* 
 
 hipError_t launch_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc, const float* dist,
                         const uint32_t* hist, uint32_t* cells, const uint32_t* counts, uint32_t* topk,
-                        hipStream_t st, bool chosen) {
+                        hipStream_t st, bool chosen, bool ref_ties) {
     if (!Q) return hipSuccess;
     const uint32_t lds = (16 + 2 * P) * sizeof(uint32_t);
-    hipLaunchKernelGGL(k_order, dim3(Q), dim3(64), lds, st, Q, C, P, topc, dist, hist, cells, counts, topk, chosen);
+    hipLaunchKernelGGL(k_order, dim3(Q), dim3(64), lds, st, Q, C, P, topc, dist, hist, cells, counts, topk, chosen,
+                       ref_ties);
     return hipGetLastError();
 }
 

@@ -174,7 +174,8 @@ extern "C" gf_status gf_search_noalloc(gf_index* ix, const float* queries, uint3
         if (ix->C) {
             GF_HIP(gf::launch_centroid_top(s.q16, ix->centres.p, s.qnorm, ix->cnorm.p, Q, ix->C, Qp, ix->Cp, ix->Dp,
                                            o->topc, s.topk, st));
-            GF_HIP(gf::launch_order(Q, ix->C, P, o->topc, nullptr, ix->hist.p, s.cells, s.counts, s.topk, st, true));
+            GF_HIP(gf::launch_order(Q, ix->C, P, o->topc, nullptr, ix->hist.p, s.cells, s.counts, s.topk, st, true,
+                                    ix->ref_ties));
         }
 
         // Stage C (gf_search): schedule, traversal, gather brute force.

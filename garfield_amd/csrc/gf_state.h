@@ -153,6 +153,7 @@ struct gf_index {
     uint32_t N = 0, D = 0, a = 0, P = 0, R = 0, E = 0, C = 0;
     int32_t vdtype = GF_VEC_F32;
     float alpha = 1.0f;
+    bool ref_ties = false;   // stage B: equal cell scores in the reference's network order
     gf::RowShape rs{};
     uint32_t rowbytes = 0, Cp = 0, Dp = 0;
     std::vector<uint32_t> offset_h, grid_h;
@@ -383,6 +384,8 @@ void grid_scatter(const float* attrs, uint32_t N, uint32_t a, const uint32_t* gr
 void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, const uint32_t* global_pid,
                   uint32_t P, uint32_t R, uint32_t E, int32_t device, uint32_t* cell_graphs, uint32_t* cross,
                   gf_build_stats* stats);
+void optimize_graphs(const uint32_t* knn, uint32_t N, uint32_t I, const uint32_t* cell_size, uint32_t P,
+                     uint32_t R, int32_t device, uint32_t* graphs, double* ms);
 void kmeans_labels(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, uint32_t C, uint32_t iters,
                    const uint32_t* init_ids, int32_t device, int32_t* labels, uint8_t* centres, double* ms);
 }  // namespace gf

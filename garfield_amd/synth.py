@@ -223,12 +223,15 @@ def kmeans_labels(vectors, C, iters, seed, device="cpu", chunk=65536):
     return labels.cpu().numpy().astype(np.int32)
 
 
-def build_index(vectors, attrs, grid, R, E, C=0, kmeans_iters=8, seed=5, device="cpu", arith=None):
+def build_index(vectors, attrs, grid, R, E, C=0, kmeans_iters=8, seed=5, device="cpu", arith=None,
+                graph="knn", inter=64):
     """All index arrays, in the layout the files hold.  arith = (attr_min,
     attr_width) builds the cells on an arithmetic grid instead of rank quantiles.
     device "hip": the library's builder (gf_grid_scatter, the int8 MFMA
     gf_build_graphs and gf_kmeans; integer data only); else torch on that
-    device."""
+    device.  graph "cagra" (device "hip" only): exact kNN graphs of degree
+    `inter`, optimised to degree R by gf_optimize_graphs (the graph
+    cagra.build returns); "knn": exact kNN graphs of degree R."""
     grid = np.asarray(grid, np.int64)
     P = int(np.prod(grid))
     hip = device == "hip"
@@ -240,10 +243,18 @@ def build_index(vectors, attrs, grid, R, E, C=0, kmeans_iters=8, seed=5, device=
         global_pid = global_pid.astype(np.int32)
     else:
         l_q, r_q, pid_lists, global_pid = grid_scatter(attrs, grid)
+    if graph not in ("knn", "cagra") or (graph == "cagra" and not hip):
+        raise ValueError("graph must be 'knn', or 'cagra' with device 'hip'")
     if hip:
-        from ._lib import build_graphs
+        from ._lib import build_graphs, optimize_graphs
         v = vectors if vectors.dtype == np.uint8 else np.asarray(vectors, np.float32)
-        graphs, cross, _ = build_graphs(v, global_pid, P, R, E)
+        if graph == "cagra":
+            knn, cross, _ = build_graphs(v, global_pid, P, inter, E)
+            sizes = np.bincount(np.asarray(global_pid, np.int64), minlength=P)
+            graphs, _ = optimize_graphs(knn, sizes, R)
+            del knn
+        else:
+            graphs, cross, _ = build_graphs(v, global_pid, P, R, E)
     else:
         members = cell_members(global_pid, P)
         graphs = knn_cell_graphs(vectors, members, R, device=device)

@@ -62,6 +62,9 @@ typedef struct {
     int32_t hist_contiguous;  /* 1: cell x cluster histogram by i / ceil(N/P) as the
                                  reference (tools.cuh:587-590); 0: by grid cell */
     int32_t device;           /* HIP device ordinal */
+    int32_t ref_ties;         /* stage B, cells of equal score: 1 keeps the order of the reference's
+                                 sorting network (bitonic_sort_id_by_num_int, gpu_graph.cu:123-141,
+                                 11389); 0 orders them by ascending cell id */
 } gf_open_opts;
 
 /* The same content as the files, in host memory (no files needed). */
@@ -291,6 +294,22 @@ typedef struct {
 gf_status gf_build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D,
                           const uint32_t* global_pid, uint32_t P, uint32_t R, uint32_t E, int32_t device,
                           uint32_t* cell_graphs, uint32_t* cross, gf_build_stats* stats);
+
+/* The optimised per-cell graphs cagra.build returns (cagra_build.py:94-125
+ * saves index.graph; cuVS builds a kNN graph of a larger intermediate degree
+ * and optimises it), written from CAGRA's published algorithm (Ootomo et al.,
+ * ICDE 2024): each row of the kNN graph knn_graphs (N*I, per-cell graphs
+ * concatenated in cell order, cell-local ids, rows ordered by distance, e.g.
+ * gf_build_graphs with R = I) is reordered by ascending (number of detourable
+ * two-hop routes, rank): the edge at rank k to D has a detour through every
+ * B at a rank below k that lists D at a rank below k (GPU).  Then (host) every
+ * pruned edge A -> B among the first R adds A to B's reverse list (ranks in
+ * order, nodes in order, at most R per list), and the output row keeps the
+ * first R/2 reordered edges, then its reverse edges, then the rest of the
+ * reordered row, each id once (a row still short repeats its first id).
+ * I <= 64, R <= I; ms (wall time of the call) may be NULL. */
+gf_status gf_optimize_graphs(const uint32_t* knn_graphs, uint32_t N, uint32_t I, const uint32_t* cell_size,
+                             uint32_t P, uint32_t R, int32_t device, uint32_t* graphs /*N*R*/, double* ms);
 
 /* Per-point cluster labels for the index (the .cluster file; the reference
  * fits cuVS k-means and predicts, clustering.py:68-87).  Integer Lloyd

@@ -67,12 +67,88 @@ float canon_dist(const float* q, const float* x, uint32_t D, int vdtype) {
     return s[0];
 }
 
+// ---------------------------------------------------------------- REF_HFMA2
+// The reference's fp16 distance (gpu_graph.cu:3394-3403, 3508-3530; half4
+// loads tools.cuh:40-53): lane j of a 32-lane warp takes the 4-element chunks
+// j, j + 32, ... of the row; per chunk acc = hfma2(q.xy - x.xy, q.xy - x.xy,
+// acc) then the same for .zw, so acc.x sums elements 4c and 4c + 2 and acc.y
+// elements 4c + 1 and 4c + 3, in chunk order; then five hadd2 steps with
+// shfl_down 16, 8, 4, 2, 1 (a lane whose source is beyond the warp keeps its
+// own value); lane 0 returns float(acc.x) + float(acc.y) in fp32.  Every
+// half operation is its exact result rounded once to binary16 (nearest,
+// ties to even); hsub and hadd of two halves and the fma of two halves plus
+// a non-negative half are exact in double, or off by far less than a half
+// ulp where they are not (a tiny product next to a large accumulator).
+uint16_t half_rne(double v) {
+    if (v != v) return 0x7E00u;
+    const uint16_t sign = std::signbit(v) ? 0x8000u : 0u;
+    double a = std::fabs(v);
+    if (a >= 65520.0) return (uint16_t)(sign | 0x7C00u);   // beyond the largest half plus half an ulp
+    if (a < std::ldexp(1.0, -14)) {                          // subnormal: quantum 2^-24
+        const double m = std::nearbyint(a * std::ldexp(1.0, 24));
+        return (uint16_t)(sign | (uint16_t)m);               // m = 1024 is the smallest normal's encoding
+    }
+    int e;
+    (void)std::frexp(a, &e);                                 // a in [2^(e-1), 2^e)
+    const double q = std::ldexp(1.0, e - 11);
+    double m = std::nearbyint(a / q);                        // 1024 .. 2048
+    if (m >= 2048.0) { m /= 2.0; ++e; }
+    if (e - 1 + 15 >= 31) return (uint16_t)(sign | 0x7C00u);
+    return (uint16_t)(sign | (uint16_t)((e - 1 + 15) << 10) | (uint16_t)((uint32_t)m - 1024u));
+}
+double h2d(uint16_t h) { return (double)orc_h2f(h); }
+
+float hfma2_dist(const uint16_t* q, const uint16_t* x, uint32_t D) {
+    uint16_t ax[32], ay[32];
+    for (uint32_t l = 0; l < 32; ++l) { ax[l] = 0; ay[l] = 0; }
+    const uint32_t nc = D / 4;
+    for (uint32_t l = 0; l < 32; ++l)
+        for (uint32_t c = l; c < nc; c += 32) {
+            for (uint32_t p = 0; p < 2; ++p) {                // .xy then .zw
+                const uint32_t k = 4 * c + 2 * p;
+                const uint16_t dx = half_rne(h2d(q[k]) - h2d(x[k]));
+                const uint16_t dy = half_rne(h2d(q[k + 1]) - h2d(x[k + 1]));
+                ax[l] = half_rne(std::fma(h2d(dx), h2d(dx), h2d(ax[l])));
+                ay[l] = half_rne(std::fma(h2d(dy), h2d(dy), h2d(ay[l])));
+            }
+        }
+    for (uint32_t m = 16; m >= 1; m >>= 1) {
+        uint16_t nx[32], ny[32];
+        for (uint32_t l = 0; l < 32; ++l) {
+            const uint32_t s = l + m < 32 ? l + m : l;
+            nx[l] = half_rne(h2d(ax[l]) + h2d(ax[s]));
+            ny[l] = half_rne(h2d(ay[l]) + h2d(ay[s]));
+        }
+        std::memcpy(ax, nx, sizeof(ax));
+        std::memcpy(ay, ny, sizeof(ay));
+    }
+    return orc_h2f(ax[0]) + orc_h2f(ay[0]);
+}
+
+// Distance arithmetic of the fp16 path (orc_set_dist_mode): 0 binary16 values
+// accumulated in fp32 in the kernels' canonical order; 1 the reference's
+// REF_HFMA2 arithmetic above.
+int g_dist_mode = 0;
+
 struct Cand { float d; uint32_t id; };
+
+// Order of equal distances (orc_set_tie_mode):
+//   0  (distance, cell-major position), a total order, the HIP kernels' rule:
+//      every sort and merge then has one result;
+//   1  the reference's: distance alone, with its own sorting networks
+//      deciding between equal distances -- warpSort (gpu_graph.cu:144-159)
+//      for the R neighbours, bitonic_sort_id_by_dis_no_explore (:77-101) for
+//      the 128 cross slots and the final list -- and merge_top's ranks.
+int g_tie_mode = 0;
+// Planted mistakes (orc_set_mutation), for tests that show that the pinning
+// checks catch them; 0 in every other use.
+int g_mutation = 0;
 
 struct Ctx {
     const orc_index* ix;
     const uint32_t* cmpos;   // point id -> cell-major position (tie key)
     const uint32_t* cellof;  // point id -> cell
+    int tie;
 };
 
 inline uint32_t tiekey(const Ctx& c, uint32_t id) {
@@ -80,6 +156,7 @@ inline uint32_t tiekey(const Ctx& c, uint32_t id) {
 }
 inline bool cless(const Ctx& c, const Cand& x, const Cand& y) {
     if (x.d != y.d) return x.d < y.d;
+    if (c.tie == 1) return false;
     return tiekey(c, x.id) < tiekey(c, y.id);
 }
 
@@ -87,22 +164,87 @@ void sort_stable(const Ctx& c, Cand* v, size_t n) {
     std::stable_sort(v, v + n, [&](const Cand& x, const Cand& y) { return cless(c, x, y); });
 }
 
+// bitonic_sort_id_by_dis_no_explore (gpu_graph.cu:77-101): ascending by
+// distance; pairs (u, d) of one (stride, step) pass are disjoint, so the
+// sequential replay equals the block's.
+void bitonic_no_explore(float* dis, uint32_t* ids, uint32_t len) {
+    for (uint32_t stride = 1; stride < len; stride <<= 1)
+        for (uint32_t step = stride; step > 0; step >>= 1)
+            for (uint32_t k = 0; k < len / 2; ++k) {
+                const uint32_t a = 2 * step * (k / step), b = k % step;
+                const uint32_t u = step == stride ? a + step - 1 - b : a + b;
+                const uint32_t d = a + b + step;
+                if (d < len && dis[u] > dis[d]) { std::swap(dis[u], dis[d]); std::swap(ids[u], ids[d]); }
+            }
+}
+
+// warpSort (gpu_graph.cu:144-159) over len lanes: every lane reads its xor
+// partner's pair, then all lanes write; a lane takes its partner's pair only
+// when the keys differ.  A partner beyond len (not active) is never taken.
+void warp_sort(float* key, uint32_t* val, uint32_t len) {
+    std::vector<float> k1(len);
+    std::vector<uint32_t> v1(len);
+    for (uint32_t b = 1; b <= len; b <<= 1)
+        for (uint32_t cc = b / 2; cc >= 1; cc >>= 1) {
+            for (uint32_t l = 0; l < len; ++l) {
+                const uint32_t o = l ^ cc;
+                k1[l] = o < len ? key[o] : key[l];
+                v1[l] = o < len ? val[o] : val[l];
+            }
+            for (uint32_t l = 0; l < len; ++l) {
+                const bool p = ((l & b) != 0) == ((l & cc) != 0);
+                if (key[l] != k1[l] && ((key[l] < k1[l]) != p)) { key[l] = k1[l]; val[l] = v1[l]; }
+            }
+        }
+}
+
+// Sorts of the neighbour list (net = 0) and of the slots / final list (net = 1).
+void sort_cands(const Ctx& c, Cand* v, size_t n, int net) {
+    if (c.tie != 1) { sort_stable(c, v, n); return; }
+    std::vector<float> d(n);
+    std::vector<uint32_t> id(n);
+    for (size_t i = 0; i < n; ++i) { d[i] = v[i].d; id[i] = v[i].id; }
+    if (net == 0) warp_sort(d.data(), id.data(), (uint32_t)n);
+    else bitonic_no_explore(d.data(), id.data(), (uint32_t)n);
+    for (size_t i = 0; i < n; ++i) v[i] = {d[i], id[i]};
+}
+
+enum {
+    MUT_MERGE_A_FIRST = 1,        // merge ties put the list entry before the incoming one
+    MUT_RESET_EVERY_3 = 2,        // visited set rebuilt every 3 iterations, not 4
+    MUT_SLOT_HALF = 3,            // cross slot i follows candidate i / 2, not i % 64
+    MUT_RECYCLE_UNFILTERED = 4,   // evicted entries kept whether or not they pass the filter
+    MUT_NO_END_EXPLORE = 5,       // the end of a cell leaves the list's explored bits as they are
+    MUT_CROSS_LAST_FIRST = 6,     // cross edges tried from the last to the first
+    MUT_ENTRY_LOCAL_KEY = 7,      // first-cell entries enter the visited set by local id
+    MUT_DROP_SEEN = 8,            // neighbours seen before are dropped instead of entering at +inf
+    MUT_NO_POSTFILTER = 9,        // the final list is not filtered
+    MUT_ENTRIES_AFTER = 10,       // the next cell's entries are slots R..2R-1, not 0..R-1
+    MUT_RECYCLE_ENTRY_FIRST = 11, // recycle merge ties put the recycle entry before the evictee
+    MUT_SLOT_32 = 12,             // cross slot i follows candidate i % 32 (only the first 32 feed the slots)
+    MUT_CROSS_OWN_CELL = 13,      // cross edges read for the current cell instead of the next
+};
+// Per-cell iteration cap (gpu_graph.cu:39 MAX_ITER); tests lower it to reach
+// the end-of-cell step with unexplored entries left.
+uint32_t g_max_iter = MAX_ITER;
+
 // Merged position of every element of sorted X (n) and sorted Y (m):
-// X_i -> i + #{Y <= X_i}, Y_j -> j + #{X < Y_j}  (gpu_graph.cu:162-222).
+// X_i -> i + #{Y <= X_i}, Y_j -> j + #{X < Y_j}  (gpu_graph.cu:162-222): an
+// incoming Y entry goes before an equal X entry.
 void merge_positions(const Ctx& c, const Cand* X, size_t n, const Cand* Y, size_t m,
-                     std::vector<size_t>& px, std::vector<size_t>& py) {
+                     std::vector<size_t>& px, std::vector<size_t>& py, bool x_first = false) {
     px.resize(n); py.resize(m);
     auto lt = [&](const Cand& a, const Cand& b) { return cless(c, a, b); };
     for (size_t i = 0; i < n; ++i)
-        px[i] = i + (std::upper_bound(Y, Y + m, X[i], lt) - Y);
+        px[i] = i + (x_first ? std::lower_bound(Y, Y + m, X[i], lt) : std::upper_bound(Y, Y + m, X[i], lt)) - Y;
     for (size_t j = 0; j < m; ++j)
-        py[j] = j + (std::lower_bound(X, X + n, Y[j], lt) - X);
+        py[j] = j + (x_first ? std::upper_bound(X, X + n, Y[j], lt) : std::lower_bound(X, X + n, Y[j], lt)) - X;
 }
 
 // merge_top (gpu_graph.cu:162-222): X keeps the n smallest, Y the next m.
-void merge_plain(const Ctx& c, Cand* X, size_t n, Cand* Y, size_t m) {
+void merge_plain(const Ctx& c, Cand* X, size_t n, Cand* Y, size_t m, bool x_first = false) {
     std::vector<size_t> px, py;
-    merge_positions(c, X, n, Y, m, px, py);
+    merge_positions(c, X, n, Y, m, px, py, x_first || g_mutation == MUT_MERGE_A_FIRST);
     std::vector<Cand> out(n + m);
     for (size_t i = 0; i < n; ++i) out[px[i]] = X[i];
     for (size_t j = 0; j < m; ++j) out[py[j]] = Y[j];
@@ -113,6 +255,7 @@ void merge_plain(const Ctx& c, Cand* X, size_t n, Cand* Y, size_t m) {
 struct QueryState {
     const Ctx* c;
     const float* q;          // query as fp32 values (fp16 path: converted)
+    const uint16_t* qh;      // fp16 path: the query's binary16 values
     const float* lo;
     const float* hi;
     std::vector<float> xbuf;
@@ -133,6 +276,7 @@ float point_dist(QueryState& s, uint32_t gid) {
     const uint32_t D = ix->D;
     if (ix->vdtype != 1)
         return canon_dist(s.q, ix->vec_f32 + (size_t)gid * D, D, ix->vdtype);
+    if (g_dist_mode == 1) return hfma2_dist(s.qh, ix->vec_f16 + (size_t)gid * D, D);
     s.xbuf.resize(D);
     for (uint32_t i = 0; i < D; ++i) s.xbuf[i] = orc_h2f(ix->vec_f16[(size_t)gid * D + i]);
     return canon_dist(s.q, s.xbuf.data(), D, 1);
@@ -145,12 +289,13 @@ void merge_with_recycle(QueryState& s, Cand* A, size_t L, Cand* B, size_t R,
                         Cand* Rc, size_t rl) {
     const Ctx& c = *s.c;
     std::vector<size_t> px, py;
-    merge_positions(c, A, L, B, R, px, py);
+    merge_positions(c, A, L, B, R, px, py, g_mutation == MUT_MERGE_A_FIRST);
     std::vector<Cand> nA(L), nB(R);
     for (size_t i = 0; i < L; ++i) {
         if (px[i] < L) { nA[px[i]] = A[i]; continue; }
         Cand x = A[i];
-        if (x.id != SENT && !passes(s, x.id & 0x3FFFFFFFu)) x = {INF, SENT};
+        if (x.id != SENT && g_mutation != MUT_RECYCLE_UNFILTERED && !passes(s, x.id & 0x3FFFFFFFu))
+            x = {INF, SENT};
         nB[px[i] - L] = x;
     }
     for (size_t j = 0; j < R; ++j) {
@@ -159,28 +304,36 @@ void merge_with_recycle(QueryState& s, Cand* A, size_t L, Cand* B, size_t R,
     }
     std::copy(nA.begin(), nA.end(), A);
     std::copy(nB.begin(), nB.end(), B);
-    sort_stable(c, B, R);
-    if (B[0].id != SENT) merge_plain(c, Rc, rl, B, R);
+    sort_cands(c, B, R, 0);
+    if (B[0].id != SENT) merge_plain(c, Rc, rl, B, R, g_mutation == MUT_RECYCLE_ENTRY_FIRST);
 }
 
 bool in_cell(const Ctx& c, uint32_t gid, uint32_t cell) { return c.cellof[gid] == cell; }
+
+// Optional record of one query's traversal: the point ids it expands, in
+// order, the cell each expansion ran in, and the final recycle list.
+struct Trace {
+    std::vector<uint32_t> expanded, expanded_cell;
+    std::vector<Cand> recycle;
+};
 
 void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_all,
                 const float* hi_all, const uint32_t* cells, const uint32_t* counts,
                 const uint32_t* little, const uint32_t* entry, uint32_t L, uint32_t K,
                 uint32_t rl, uint32_t postfilter, uint32_t* out_ids, float* out_dist,
-                uint32_t* counters) {
+                uint32_t* counters, Trace* tr = nullptr) {
     const orc_index* ix = c.ix;
     const uint32_t D = ix->D, R = ix->R, E = ix->E, P = ix->P, a = ix->a;
     std::vector<float> qv(D);
+    const uint16_t* qh = nullptr;
     if (ix->vdtype != 1) {
         std::memcpy(qv.data(), (const float*)queries + (size_t)qi * D, sizeof(float) * D);
     } else {
-        const uint16_t* qh = (const uint16_t*)queries + (size_t)qi * D;
+        qh = (const uint16_t*)queries + (size_t)qi * D;
         for (uint32_t i = 0; i < D; ++i) qv[i] = orc_h2f(qh[i]);
     }
     QueryState s;
-    s.c = &c; s.q = qv.data(); s.lo = lo_all + (size_t)qi * a; s.hi = hi_all + (size_t)qi * a;
+    s.c = &c; s.q = qv.data(); s.qh = qh; s.lo = lo_all + (size_t)qi * a; s.hi = hi_all + (size_t)qi * a;
     std::memset(s.ctr, 0, sizeof(s.ctr));
 
     const uint32_t* cl = cells + (size_t)qi * P;
@@ -189,6 +342,7 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
     std::vector<Cand> out;
 
     auto cell_size = [&](uint32_t cc) { return ix->offset[cc + 1] - ix->offset[cc]; };
+    const uint32_t reset_every = g_mutation == MUT_RESET_EVERY_3 ? 3u : HASH_RESET;
 
     if (traverse) {
         s.ctr[ORC_C_ROUTE] = 1;
@@ -204,9 +358,10 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
         {
             const uint32_t c0 = cl[0], sz0 = cell_size(c0);
             for (uint32_t j = 0; j < R; ++j) {
-                uint32_t gid = ix->global_idx[ix->offset[c0] + entry[j] % sz0];
+                const uint32_t lid = entry[j] % sz0;
+                uint32_t gid = ix->global_idx[ix->offset[c0] + lid];
                 B[j] = {INF, gid};
-                H.insert(gid);
+                H.insert(g_mutation == MUT_ENTRY_LOCAL_KEY ? lid : gid);
             }
         }
         for (uint32_t p_i = 0; p_i < cnt; ++p_i) {
@@ -222,11 +377,11 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
                 B[j].d = point_dist(s, B[j].id);
                 s.ctr[ORC_C_DIST]++; s.ctr[ORC_C_ATTR]++;
             }
-            sort_stable(c, B.data(), R);
+            sort_cands(c, B.data(), R, 0);
             merge_with_recycle(s, A.data(), L, B.data(), R, Rc.data(), rl);
 
-            for (uint32_t it = 0; it < MAX_ITER; ++it) {
-                if ((it + 1) % HASH_RESET == 0) {            // gpu_graph.cu:3441-3454
+            for (uint32_t it = 0; it < g_max_iter; ++it) {
+                if ((it + 1) % reset_every == 0) {            // gpu_graph.cu:3441-3454
                     H.clear();
                     for (const auto* arr : {&A, &B})
                         for (const Cand& x : *arr) {
@@ -242,6 +397,7 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
                 if (sel == L) break;
                 A[sel].id |= EXPL;
                 s.ctr[ORC_C_EXPAND]++;
+                if (tr) { tr->expanded.push_back(A[sel].id & IDM); tr->expanded_cell.push_back(cur); }
                 const uint32_t tl = ix->local_idx[A[sel].id & IDM];
                 for (uint32_t j = 0; j < R; ++j) {           // gpu_graph.cu:3500-3530
                     uint32_t nl = ix->graph[(size_t)(base + tl) * R + j];
@@ -250,13 +406,15 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
                     B[j] = {INF, gid};
                     s.ctr[ORC_C_ATTR]++;
                     if (isnew) { B[j].d = point_dist(s, gid); s.ctr[ORC_C_DIST]++; }
+                    else if (g_mutation == MUT_DROP_SEEN) B[j].id = SENT;
                 }
-                sort_stable(c, B.data(), R);
+                sort_cands(c, B.data(), R, 0);
                 if (B[0].id != SENT)
                     merge_with_recycle(s, A.data(), L, B.data(), R, Rc.data(), rl);
             }
             // End of cell (gpu_graph.cu:3555-3560).
-            for (Cand& x : A) x.id |= EXPL;
+            if (g_mutation != MUT_NO_END_EXPLORE)
+                for (Cand& x : A) x.id |= EXPL;
             H.clear();
             if (p_i + 1 < cnt) {                             // gpu_graph.cu:3564-3642
                 const uint32_t nxt = cl[p_i + 1];
@@ -265,12 +423,14 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
                 for (uint32_t i = 0; i < std::min(XSTEP, L); ++i)
                     if (A[i].id != SENT) s.ctr[ORC_C_CROSS]++;
                 for (uint32_t i = 0; i < XSLOTS; ++i) {
-                    const uint32_t ci = i % XSTEP;
+                    const uint32_t ci = g_mutation == MUT_SLOT_HALF ? i / 2 : (g_mutation == MUT_SLOT_32 ? i % 32 : i % XSTEP);
                     if (ci >= L || A[ci].id == SENT) continue;  // in-bounds guard (the reference tests ci > L)
                     const uint32_t g = A[ci].id & IDM;
                     bool got = false;
-                    for (uint32_t j = 0; j < E && !got; ++j) {
-                        uint32_t nl = ix->cross[(size_t)g * P * E + (size_t)nxt * E + j];
+                    for (uint32_t jj = 0; jj < E && !got; ++jj) {
+                        const uint32_t j = g_mutation == MUT_CROSS_LAST_FIRST ? E - 1 - jj : jj;
+                        const uint32_t xc = g_mutation == MUT_CROSS_OWN_CELL ? cur : nxt;
+                        uint32_t nl = ix->cross[(size_t)g * P * E + (size_t)xc * E + j] % nsz;
                         if (H.insert(nl).second) { W[i].id = ix->global_idx[nbase + nl]; got = true; }
                     }
                     if (!got)                                // fallback: scan [0, |cell|), not [0, 62500)
@@ -282,9 +442,11 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
                     W[i].d = point_dist(s, W[i].id);
                     s.ctr[ORC_C_DIST]++; s.ctr[ORC_C_ATTR]++;
                 }
-                sort_stable(c, W.data(), XSLOTS);
+                sort_cands(c, W.data(), XSLOTS, 1);
                 H.clear();
-                for (uint32_t j = 0; j < R; ++j) B[j] = W[j];
+                const uint32_t e0 = g_mutation == MUT_ENTRIES_AFTER ? R : 0;
+                for (uint32_t j = 0; j < R; ++j) B[j] = W[e0 + j];
+                if (e0) for (uint32_t j = 0; j < R; ++j) W[R + j] = W[j];
                 for (uint32_t i = 0; i < XSLOTS; ++i)
                     if (W[i].id != SENT) H.insert(ix->local_idx[W[i].id]);
                 merge_plain(c, A.data(), L, W.data() + R, XSTEP);
@@ -297,9 +459,11 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
             }
         }
         // Post-filter + recycle merge (gpu_graph.cu:4025-4047).
-        for (Cand& x : A)
-            if (x.id != SENT && !passes(s, x.id & IDM)) x = {INF, SENT};
-        sort_stable(c, A.data(), L);
+        if (g_mutation != MUT_NO_POSTFILTER)
+            for (Cand& x : A)
+                if (x.id != SENT && !passes(s, x.id & IDM)) x = {INF, SENT};
+        sort_cands(c, A.data(), L, 1);
+        if (tr) tr->recycle = Rc;
         if (Rc[0].id != SENT) merge_plain(c, A.data(), L, Rc.data(), rl);
         out = A;
     } else {
@@ -319,22 +483,29 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
             }
         }
         size_t kk = std::min<size_t>(K, found.size());
+        Ctx ct = c;
+        ct.tie = 0;   // the brute force keeps (distance, cell-major position) order in both tie modes
         std::partial_sort(found.begin(), found.begin() + kk, found.end(),
-                          [&](const Cand& x, const Cand& y) { return cless(c, x, y); });
+                          [&](const Cand& x, const Cand& y) { return cless(ct, x, y); });
         found.resize(kk);
         out = found;
     }
     // Output: the first K distinct ids (the reference merges top and recycle
     // without deduplication and may repeat an id, gpu_graph.cu:4044-4047).
-    uint32_t n = 0, prev = SENT;
+    // In tie mode 0 the copies of one id are adjacent (equal keys) and every
+    // empty entry follows the valid ones; in mode 1 equal distances of other
+    // points, empty entries included, may sit between them.
+    uint32_t n = 0;
     for (const Cand& x : out) {
         if (n >= K) break;
-        if (x.id == SENT) break;
+        if (x.id == SENT) continue;
         uint32_t id = x.id & IDM;
-        if (n > 0 && id == prev) continue;
+        bool dup = false;
+        for (uint32_t t = 0; t < n && !dup; ++t) dup = out_ids[(size_t)qi * K + t] == id;
+        if (dup) continue;
         out_ids[(size_t)qi * K + n] = id;
         out_dist[(size_t)qi * K + n] = x.d;
-        prev = id; ++n;
+        ++n;
     }
     for (; n < K; ++n) {
         out_ids[(size_t)qi * K + n] = ORC_SENTINEL_ID;
@@ -608,10 +779,23 @@ void orc_sort_cells(uint32_t Q, uint32_t P, uint32_t C, uint32_t k, uint32_t* ce
             for (uint32_t t = 0; t < k; ++t) sc += hist[(size_t)cl[i] * C + topk[(size_t)q * k + t]];
             v[i] = {sc, cl[i]};
         }
-        std::sort(v.begin(), v.end(), [](const std::pair<int64_t, uint32_t>& x,
-                                         const std::pair<int64_t, uint32_t>& y) {
-            return x.first != y.first ? x.first > y.first : x.second < y.second;
-        });
+        if (g_tie_mode == 1) {
+            // bitonic_sort_id_by_num_int (gpu_graph.cu:123-141): descending,
+            // a swap when the upper score is smaller, over the stage A order
+            for (uint32_t stride = 1; stride < n; stride <<= 1)
+                for (uint32_t step = stride; step > 0; step >>= 1)
+                    for (uint32_t kk = 0; kk < n / 2; ++kk) {
+                        const uint32_t a0 = 2 * step * (kk / step), b0 = kk % step;
+                        const uint32_t u = step == stride ? a0 + step - 1 - b0 : a0 + b0;
+                        const uint32_t d = a0 + b0 + step;
+                        if (d < n && (int32_t)v[u].first < (int32_t)v[d].first) std::swap(v[u], v[d]);
+                    }
+        } else {
+            std::sort(v.begin(), v.end(), [](const std::pair<int64_t, uint32_t>& x,
+                                             const std::pair<int64_t, uint32_t>& y) {
+                return x.first != y.first ? x.first > y.first : x.second < y.second;
+            });
+        }
         for (uint32_t i = 0; i < n; ++i) cl[i] = v[i].second;
     }
 }
@@ -641,6 +825,7 @@ float orc_distance(const orc_index* ix, const void* q, uint32_t gid) {
     std::vector<float> qv(ix->D), xv(ix->D);
     if (ix->vdtype != 1)
         return canon_dist((const float*)q, ix->vec_f32 + (size_t)gid * ix->D, ix->D, ix->vdtype);
+    if (g_dist_mode == 1) return hfma2_dist((const uint16_t*)q, ix->vec_f16 + (size_t)gid * ix->D, ix->D);
     for (uint32_t i = 0; i < ix->D; ++i) {
         qv[i] = orc_h2f(((const uint16_t*)q)[i]);
         xv[i] = orc_h2f(ix->vec_f16[(size_t)gid * ix->D + i]);
@@ -660,11 +845,95 @@ void orc_search(const orc_index* ix, const void* queries, uint32_t Q,
             cmpos[ix->global_idx[r]] = r;
             cellof[ix->global_idx[r]] = c;
         }
-    Ctx c{ix, cmpos.data(), cellof.data()};
+    Ctx c{ix, cmpos.data(), cellof.data(), g_tie_mode};
 #pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads > 0 ? nthreads : omp_get_max_threads())
     for (int64_t q = 0; q < (int64_t)Q; ++q)
         search_one(c, queries, (uint32_t)q, lo, hi, cells, counts, little, entry, L, K, rl,
                    postfilter, out_ids, out_dist, counters);
+}
+
+void orc_set_tie_mode(int mode) { g_tie_mode = mode; }
+void orc_set_dist_mode(int mode) { g_dist_mode = mode; }
+uint16_t orc_half_rne(double v) { return half_rne(v); }
+float orc_hfma2_dist(const uint16_t* q, const uint16_t* x, uint32_t D) { return hfma2_dist(q, x, D); }
+void orc_set_mutation(int m) { g_mutation = m; }
+void orc_set_max_iter(uint32_t n) { g_max_iter = n ? n : MAX_ITER; }
+
+uint32_t orc_search_trace(const orc_index* ix, const void* queries, uint32_t qi, const float* lo, const float* hi,
+                          const uint32_t* cells, const uint32_t* counts, const uint32_t* entry, uint32_t L,
+                          uint32_t K, uint32_t rl, uint32_t* out_ids, float* out_dist, uint32_t* counters,
+                          uint32_t* expanded, uint32_t* expanded_cell, uint32_t cap, uint32_t* rec_ids,
+                          float* rec_dist) {
+    std::vector<uint32_t> cmpos(ix->N), cellof(ix->N);
+    for (uint32_t c = 0; c < ix->P; ++c)
+        for (uint32_t r = ix->offset[c]; r < ix->offset[c + 1]; ++r) {
+            cmpos[ix->global_idx[r]] = r;
+            cellof[ix->global_idx[r]] = c;
+        }
+    Ctx c{ix, cmpos.data(), cellof.data(), g_tie_mode};
+    Trace tr;
+    std::vector<uint32_t> little(qi + 1, 0);
+    std::vector<uint32_t> ids((size_t)(qi + 1) * K), ctr((size_t)(qi + 1) * ORC_NCNT);
+    std::vector<float> dist((size_t)(qi + 1) * K);
+    search_one(c, queries, qi, lo, hi, cells, counts, little.data(), entry, L, K, rl, 1u << 30, ids.data(),
+               dist.data(), ctr.data(), &tr);
+    std::memcpy(out_ids, &ids[(size_t)qi * K], K * sizeof(uint32_t));
+    std::memcpy(out_dist, &dist[(size_t)qi * K], K * sizeof(float));
+    std::memcpy(counters, &ctr[(size_t)qi * ORC_NCNT], ORC_NCNT * sizeof(uint32_t));
+    for (size_t i = 0; i < tr.expanded.size() && i < cap; ++i) {
+        expanded[i] = tr.expanded[i];
+        expanded_cell[i] = tr.expanded_cell[i];
+    }
+    for (uint32_t t = 0; t < rl; ++t) {
+        rec_ids[t] = tr.recycle.empty() || tr.recycle[t].id == SENT ? ORC_SENTINEL_ID : (tr.recycle[t].id & IDM);
+        rec_dist[t] = tr.recycle.empty() ? INF : tr.recycle[t].d;
+    }
+    return (uint32_t)tr.expanded.size();
+}
+
+void orc_bitonic_sort_dis(float* dis, uint32_t* ids, uint32_t len) { bitonic_no_explore(dis, ids, len); }
+void orc_warp_sort(float* key, uint32_t* val, uint32_t len) { warp_sort(key, val, len); }
+
+void orc_merge_top(float* d1, uint32_t* i1, uint32_t n, float* d2, uint32_t* i2, uint32_t m, int tie) {
+    std::vector<uint32_t> ident;
+    uint32_t mx = 0;
+    for (uint32_t i = 0; i < n; ++i) if (i1[i] != SENT) mx = std::max(mx, i1[i] & IDM);
+    for (uint32_t j = 0; j < m; ++j) if (i2[j] != SENT) mx = std::max(mx, i2[j] & IDM);
+    ident.resize((size_t)mx + 1);
+    for (uint32_t i = 0; i <= mx; ++i) ident[i] = i;
+    Ctx c{nullptr, ident.data(), nullptr, tie};
+    std::vector<Cand> X(n), Y(m);
+    for (uint32_t i = 0; i < n; ++i) X[i] = {d1[i], i1[i]};
+    for (uint32_t j = 0; j < m; ++j) Y[j] = {d2[j], i2[j]};
+    merge_plain(c, X.data(), n, Y.data(), m);
+    for (uint32_t i = 0; i < n; ++i) { d1[i] = X[i].d; i1[i] = X[i].id; }
+    for (uint32_t j = 0; j < m; ++j) { d2[j] = Y[j].d; i2[j] = Y[j].id; }
+}
+
+void orc_merge_recycle(const float* attrs, uint32_t a, const float* lo, const float* hi, float* dA, uint32_t* iA,
+                       uint32_t L, float* dB, uint32_t* iB, uint32_t R, float* dR, uint32_t* iR, uint32_t rl,
+                       int tie) {
+    std::vector<uint32_t> ident;
+    uint32_t mx = 0;
+    for (uint32_t i = 0; i < L; ++i) if (iA[i] != SENT) mx = std::max(mx, iA[i] & IDM);
+    for (uint32_t j = 0; j < R; ++j) if (iB[j] != SENT) mx = std::max(mx, iB[j] & IDM);
+    for (uint32_t j = 0; j < rl; ++j) if (iR[j] != SENT) mx = std::max(mx, iR[j] & IDM);
+    ident.resize((size_t)mx + 1);
+    for (uint32_t i = 0; i <= mx; ++i) ident[i] = i;
+    orc_index ix{};
+    ix.a = a;
+    ix.attrs = attrs;
+    Ctx c{&ix, ident.data(), nullptr, tie};
+    QueryState s;
+    s.c = &c; s.q = nullptr; s.lo = lo; s.hi = hi;
+    std::vector<Cand> A(L), B(R), Rc(rl);
+    for (uint32_t i = 0; i < L; ++i) A[i] = {dA[i], iA[i]};
+    for (uint32_t j = 0; j < R; ++j) B[j] = {dB[j], iB[j]};
+    for (uint32_t j = 0; j < rl; ++j) Rc[j] = {dR[j], iR[j]};
+    merge_with_recycle(s, A.data(), L, B.data(), R, Rc.data(), rl);
+    for (uint32_t i = 0; i < L; ++i) { dA[i] = A[i].d; iA[i] = A[i].id; }
+    for (uint32_t j = 0; j < R; ++j) { dB[j] = B[j].d; iB[j] = B[j].id; }
+    for (uint32_t j = 0; j < rl; ++j) { dR[j] = Rc[j].d; iR[j] = Rc[j].id; }
 }
 
 void orc_ground_truth(uint32_t N, uint32_t D, uint32_t a, const float* data,

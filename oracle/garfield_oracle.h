@@ -101,7 +101,8 @@ void orc_topk_clusters(uint32_t Q, uint32_t C, uint32_t k, const float* dist,
 
 /* gpu_graph.cu:11343-11396 sort_by_clustering_info_weighted: reorder each
  * query's cells by descending sum of hist[cell][c] over its top clusters;
- * ties by ascending cell id. */
+ * ties by ascending cell id (tie mode 0) or in the order of the reference's
+ * network bitonic_sort_id_by_num_int (gpu_graph.cu:123-141) (tie mode 1). */
 void orc_sort_cells(uint32_t Q, uint32_t P, uint32_t C, uint32_t k,
                     uint32_t* cells, const uint32_t* counts,
                     const uint32_t* topk, const uint32_t* hist);
@@ -132,6 +133,46 @@ void orc_search(const orc_index* ix, const void* queries, uint32_t Q,
                 const uint32_t* entry, uint32_t L, uint32_t K, uint32_t rl,
                 uint32_t postfilter, uint32_t* out_ids, float* out_dist,
                 uint32_t* counters, int nthreads);
+
+/* Order of equal distances in orc_search: 0 (default) (distance, cell-major
+ * position), the HIP kernels' total order; 1 the reference's -- distance
+ * alone, its sorting networks (warpSort gpu_graph.cu:144-159,
+ * bitonic_sort_id_by_dis_no_explore :77-101) and merge_top's ranks
+ * (:162-222) deciding between equal distances.  Process-wide. */
+void orc_set_tie_mode(int mode);
+/* Distance arithmetic of the fp16 path (vdtype 1): 0 (default) binary16
+ * values accumulated in fp32 in the kernels' canonical order; 1 REF_HFMA2,
+ * the reference's half arithmetic (hsub2 / hfma2 in its lane order, hadd2
+ * shfl_down tree, gpu_graph.cu:3394-3403) with every half operation rounded
+ * once to binary16.  Process-wide. */
+void orc_set_dist_mode(int mode);
+/* binary16 round-to-nearest-even of a double; the REF_HFMA2 distance of two
+ * binary16 rows (D a multiple of 4). */
+uint16_t orc_half_rne(double v);
+float orc_hfma2_dist(const uint16_t* q, const uint16_t* x, uint32_t D);
+/* Plants one numbered mistake in the traversal (0 = none), so that tests can
+ * show that their checks catch it; see MUT_* in garfield_oracle.cpp. */
+void orc_set_mutation(int m);
+/* Per-cell iteration cap of the traversal (0 restores the reference's 10000). */
+void orc_set_max_iter(uint32_t n);
+/* One traversal query (route forced to traversal) with its trajectory: the
+ * point ids expanded in order and the cell of each expansion (up to cap),
+ * and the recycle list before the final merge.  Returns the expansions. */
+uint32_t orc_search_trace(const orc_index* ix, const void* queries, uint32_t qi, const float* lo, const float* hi,
+                          const uint32_t* cells, const uint32_t* counts, const uint32_t* entry, uint32_t L,
+                          uint32_t K, uint32_t rl, uint32_t* out_ids, float* out_dist, uint32_t* counters,
+                          uint32_t* expanded, uint32_t* expanded_cell, uint32_t cap, uint32_t* rec_ids,
+                          float* rec_dist);
+/* The oracle's building blocks, for known-answer tests:
+ * bitonic_sort_id_by_dis_no_explore (gpu_graph.cu:77-101), warpSort
+ * (:144-159), merge_top (:162-222; tie 0 orders equal distances by id) and
+ * merge_top_with_recycle_list + the recycle merge (:224-315, 3412-3425). */
+void orc_bitonic_sort_dis(float* dis, uint32_t* ids, uint32_t len);
+void orc_warp_sort(float* key, uint32_t* val, uint32_t len);
+void orc_merge_top(float* d1, uint32_t* i1, uint32_t n, float* d2, uint32_t* i2, uint32_t m, int tie);
+void orc_merge_recycle(const float* attrs, uint32_t a, const float* lo, const float* hi, float* dA, uint32_t* iA,
+                       uint32_t L, float* dB, uint32_t* iB, uint32_t R, float* dR, uint32_t* iR, uint32_t rl,
+                       int tie);
 
 /* gpu_graph.cu:10782-10812 naive_brute_force_with_filter: exact filtered kNN
  * on fp32 (computed in fp64), ascending by (distance, id); missing entries are

@@ -212,10 +212,126 @@ class OracleIndex:
                           C.c_int(nthreads))
         return ids, dist, ctr
 
+    def trace(self, query, lo, hi, cells_, entry, L, K=10, rl=10, cap=100000):
+        """One traversal query over the ordered cells `cells_` with its
+        trajectory: (ids, dists, counters, expanded point ids, the cell of each
+        expansion, recycle ids, recycle distances)."""
+        dt = np.uint16 if self.vec_f16 is not None else np.float32
+        q = _c(np.atleast_2d(query), dt)
+        lo = _c(np.atleast_2d(lo), np.float32)
+        hi = _c(np.atleast_2d(hi), np.float32)
+        cl = np.zeros((1, self.P), np.uint32)
+        cl[0, :len(cells_)] = cells_
+        cnt = np.array([len(cells_)], np.uint32)
+        entry = _c(entry, np.uint32)
+        ids = np.empty(K, np.uint32)
+        dist = np.empty(K, np.float32)
+        ctr = np.empty(NCNT, np.uint32)
+        ex = np.empty(cap, np.uint32)
+        exc = np.empty(cap, np.uint32)
+        rid = np.empty(rl, np.uint32)
+        rd = np.empty(rl, np.float32)
+        n = load().orc_search_trace(C.byref(self.s), _p(q), C.c_uint32(0), _p(lo), _p(hi), _p(cl), _p(cnt),
+                                    _p(entry), C.c_uint32(L), C.c_uint32(K), C.c_uint32(rl), _p(ids), _p(dist),
+                                    _p(ctr), _p(ex), _p(exc), C.c_uint32(cap), _p(rid), _p(rd))
+        n = min(int(n), cap)
+        return ids, dist, ctr, ex[:n].copy(), exc[:n].copy(), rid, rd
+
     def distance(self, query, gid):
         dt = np.uint16 if self.vec_f16 is not None else np.float32
         q = _c(query, dt)
         return load().orc_distance(C.byref(self.s), _p(q), C.c_uint32(gid))
+
+
+def set_tie_mode(mode):
+    """0: equal distances ordered by cell-major position (the HIP kernels'
+    rule); 1: the reference's order (distance alone, its sorting networks)."""
+    load().orc_set_tie_mode(C.c_int(int(mode)))
+
+
+def set_dist_mode(mode):
+    """fp16 path distances: 0 binary16 values, fp32 accumulation (the HIP
+    kernels' arithmetic); 1 REF_HFMA2, the reference's half arithmetic."""
+    load().orc_set_dist_mode(C.c_int(int(mode)))
+
+
+def half_rne(v):
+    lib = load()
+    lib.orc_half_rne.restype = C.c_uint16
+    lib.orc_half_rne.argtypes = [C.c_double]
+    return int(lib.orc_half_rne(float(v)))
+
+
+def hfma2_dist(q, x):
+    q = _c(q, np.uint16)
+    x = _c(x, np.uint16)
+    lib = load()
+    lib.orc_hfma2_dist.restype = C.c_float
+    return float(lib.orc_hfma2_dist(_p(q), _p(x), C.c_uint32(q.size)))
+
+
+def set_mutation(m):
+    """Plant mistake number m in the traversal (0: none); test use only."""
+    load().orc_set_mutation(C.c_int(int(m)))
+
+
+MUTATIONS = {
+    1: "merge ties put the list entry before the incoming one",
+    2: "visited set rebuilt every 3 iterations, not 4",
+    3: "cross slot i follows candidate i / 2, not i % 64",
+    4: "evicted entries kept in the recycle list whether or not they pass the filter",
+    5: "the end of a cell leaves the list's explored bits as they are",
+    6: "cross edges tried from the last to the first",
+    7: "first-cell entries enter the visited set by local id, not point id",
+    8: "neighbours seen before are dropped instead of entering at +inf",
+    9: "the final list is not filtered",
+    10: "the next cell's entries are slots R..2R-1, not 0..R-1",
+    11: "recycle merge ties put the recycle entry before the evictee",
+    12: "cross slot i follows candidate i % 32 (only the first 32 candidates feed the slots)",
+    13: "cross edges read for the current cell instead of the next",
+}
+
+
+def set_max_iter(n):
+    """Per-cell iteration cap of the traversal (0: the reference's 10000)."""
+    load().orc_set_max_iter(C.c_uint32(int(n)))
+
+
+def bitonic_sort_dis(dis, ids):
+    d = _c(dis, np.float32).copy()
+    i = _c(ids, np.uint32).copy()
+    load().orc_bitonic_sort_dis(_p(d), _p(i), C.c_uint32(d.size))
+    return d, i
+
+
+def warp_sort(key, val):
+    k = _c(key, np.float32).copy()
+    v = _c(val, np.uint32).copy()
+    load().orc_warp_sort(_p(k), _p(v), C.c_uint32(k.size))
+    return k, v
+
+
+def merge_top(d1, i1, d2, i2, tie=1):
+    """merge_top on two sorted lists (tie 1: distance alone; 0: ties by id);
+    returns the lists' new contents."""
+    a = [_c(d1, np.float32).copy(), _c(i1, np.uint32).copy(), _c(d2, np.float32).copy(), _c(i2, np.uint32).copy()]
+    load().orc_merge_top(_p(a[0]), _p(a[1]), C.c_uint32(a[0].size), _p(a[2]), _p(a[3]), C.c_uint32(a[2].size),
+                         C.c_int(tie))
+    return a
+
+
+def merge_recycle(attrs, lo, hi, dA, iA, dB, iB, dR, iR, tie=1):
+    """merge_top_with_recycle_list + the evictee sort and recycle merge:
+    returns (A, B, recycle) as (distances, ids) pairs."""
+    attrs = _c(attrs, np.float32)
+    lo = _c(lo, np.float32)
+    hi = _c(hi, np.float32)
+    a = [_c(x, dt).copy() for x, dt in ((dA, np.float32), (iA, np.uint32), (dB, np.float32), (iB, np.uint32),
+                                         (dR, np.float32), (iR, np.uint32))]
+    load().orc_merge_recycle(_p(attrs), C.c_uint32(attrs.shape[1]), _p(lo), _p(hi), _p(a[0]), _p(a[1]),
+                             C.c_uint32(a[0].size), _p(a[2]), _p(a[3]), C.c_uint32(a[2].size), _p(a[4]), _p(a[5]),
+                             C.c_uint32(a[4].size), C.c_int(tie))
+    return (a[0], a[1]), (a[2], a[3]), (a[4], a[5])
 
 
 def ground_truth(data, attrs, queries, lo, hi, K, nthreads=0):
@@ -369,6 +485,56 @@ def cross_rows(vectors, global_pid, P, E, rows):
         o = np.argsort(d, axis=1, kind="stable")[:, :min(E, n)]
         out[:, c * E:c * E + o.shape[1]] = o
         out[:, c * E + o.shape[1]:(c + 1) * E] = o[:, :1]
+    return out
+
+
+def detour_order(knn_cell):
+    """One cell's kNN rows (n x I, local ids) in ascending (detourable
+    routes, rank) order, the reordering step of CAGRA's graph optimisation
+    (Ootomo et al., ICDE 2024): edge k of row a, to d = g[a, k], has a detour
+    through every b = g[a, j], j < k, whose own row lists d at a position
+    below k (first occurrence)."""
+    g = np.asarray(knn_cell, np.int64)
+    n, I = g.shape
+    pos = np.full((n, n), I, np.int64)           # pos[b, x]: first position of x in row b
+    for j in range(I - 1, -1, -1):
+        pos[np.arange(n), g[:, j]] = j
+    M = pos[g[:, :, None], g[:, None, :]]        # M[a, j, k] = position of g[a, k] in row g[a, j]
+    k = np.arange(I)
+    det = ((M < k[None, None, :]) & (k[None, :, None] < k[None, None, :])).sum(axis=1)
+    order = np.argsort(det * I + k[None, :], axis=1, kind="stable")
+    return np.take_along_axis(g, order, axis=1), det
+
+
+def optimize_graphs(knn_graphs, cell_sizes, R):
+    """gf_optimize_graphs restated: per cell, the detour order, then reverse
+    edges (for every rank k < R of the reordered rows, in row order, edge
+    a -> b appends a to b's reverse list, at most R, never b itself), then
+    each row = its first R // 2 reordered edges, its reverse edges, the rest
+    of its reordered row, each id once, padded with its first id."""
+    g = np.asarray(knn_graphs, np.int64)
+    I = g.shape[1]
+    out = np.empty((g.shape[0], R), np.uint32)
+    start = 0
+    for n in cell_sizes:
+        n = int(n)
+        if n == 0:
+            continue
+        o, _ = detour_order(g[start:start + n])
+        rev = [[] for _ in range(n)]
+        for k in range(R):
+            for a in range(n):
+                b = int(o[a, k])
+                if b != a and len(rev[b]) < R:
+                    rev[b].append(a)
+        for a in range(n):
+            row = []
+            for x in list(o[a, :R // 2]) + rev[a] + list(o[a, R // 2:]):
+                if len(row) < R and int(x) not in row:
+                    row.append(int(x))
+            row += [row[0]] * (R - len(row))
+            out[start + a] = row
+        start += n
     return out
 
 

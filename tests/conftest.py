@@ -48,24 +48,24 @@ def world_gauss():
     qv = synth.gaussian_unit_vectors(Q, 96, 42)
     sel = synth.log_uniform(Q, 0.001, 0.5, 43)
     lo, hi = synth.ranges_for_selectivity(Q, 3, sel, 44, hi=400)
-    cfg = dict(vectors=vec, attrs=att, grid=[4, 4, 4], R=16, E=2, C=16, queries=qv, lo=lo, hi=hi)
-    ix = synth.build_index(vec, att, cfg["grid"], 16, 2, 16, seed=6)
+    cfg = dict(vectors=vec, attrs=att, grid=[4, 4, 4], R=32, E=2, C=16, queries=qv, lo=lo, hi=hi)
+    ix = synth.build_index(vec, att, cfg["grid"], 32, 2, 16, seed=6)
     return cfg, ix
 
 
 @pytest.fixture(scope="session")
 def world_c4():
-    """Config-4-shaped (shrunk): 768-d Gaussian mixture (40 components,
+    """Config-4-shaped (shrunk): 768-d Gaussian mixture (1000 components,
     sigma 0.1 around unit centres) stored as fp16 (f2h_factor 1), 2 attributes
-    10 * component + U{0..9} on a 4x4 grid, queries at 10% selectivity."""
+    10 * component + U{0..9} on a 4x4 grid, R = 32, queries at 10% selectivity."""
     from garfield_amd import synth
-    N, Q, ncomp = 4000, 64, 40
+    N, Q, ncomp = 8000, 64, 1000
     vec, comp = synth.gmm_vectors(N, 768, ncomp, 70)
     att = synth.component_attrs(comp, 2, 71)
     qv, _ = synth.gmm_vectors(Q, 768, ncomp, 72)
     lo, hi = synth.ranges_for_selectivity(Q, 2, 0.1, 73, hi=10 * ncomp)
-    cfg = dict(vectors=vec, attrs=att, grid=[4, 4], R=16, E=2, C=16, queries=qv, lo=lo, hi=hi)
-    ix = synth.build_index(vec, att, cfg["grid"], 16, 2, 16, seed=74)
+    cfg = dict(vectors=vec, attrs=att, grid=[4, 4], R=32, E=2, C=16, queries=qv, lo=lo, hi=hi)
+    ix = synth.build_index(vec, att, cfg["grid"], 32, 2, 16, seed=74)
     return cfg, ix
 
 

@@ -1,0 +1,332 @@
+"""Sequential model of the reference's fused search kernel, traversal branch.
+
+TEST INFRASTRUCTURE ONLY: it checks the C++ oracle (oracle/garfield_oracle.cpp)
+on small inputs and nothing else uses it.
+
+It is written from the reference kernel's own control flow,
+select_path_contain_attr_filter_V2_without_output_with_post_pre_filter
+(indexsearch/gpu_graph.cu:3266-3643, 4025-4130), as one block run one step at a
+time: the shared arrays top_M_Cand / top_M_Cand_dis of TOPM + DEGREE entries
+with the explored bit 0x80000000 in the id, merge_top's bisection
+(gpu_graph.cu:162-222) and merge_top_with_recycle_list (:224-315) as written,
+the visited set as a set of keys (the reference's 2048-slot table, which the
+small inputs here never fill), and the 128 cross-edge slots of
+work_mem_unsigned / work_mem_float.  Its structure is the reference's, not the
+oracle's, so that a restatement mistake in either shows up as a difference.
+
+Tie modes: tie=1 orders equal distances as the reference does -- comparisons
+on distance alone and its sorting networks, warpSort (gpu_graph.cu:144-159)
+and bitonic_sort_id_by_dis_no_explore (:77-101); tie=0 breaks distance ties by
+cell-major position (the rule the oracle and the HIP kernels share), with
+every sort a stable sort on that key.
+
+Where the reference reads out of bounds, the model follows the oracle's
+documented in-bounds rules: a cross slot i whose candidate i % 64 lies at or
+beyond TOPM is empty (gpu_graph.cu:3572 tests TOPM < i % 64); the fallback scan
+stops at the cell's size instead of 62500 (:3583); an empty entry's distance
+is +inf (the reference leaves a stale value); entries are drawn below the first
+cell's size.  The reference's INF_DIS (1e9) is +inf here.
+"""
+import numpy as np
+
+SENT = 0xFFFFFFFF
+EXPL = 0x80000000
+IDM = 0x7FFFFFFF
+INF = float("inf")
+MAX_ITER = 10000
+HASH_RESET = 4
+HASHLEN = 2048
+
+
+def bitonic_no_explore(dis, ids, n):
+    """bitonic_sort_id_by_dis_no_explore (gpu_graph.cu:77-101) on dis[:n], ids[:n]."""
+    stride = 1
+    while stride < n:
+        step = stride
+        while step > 0:
+            for k in range(n // 2):
+                a = 2 * step * (k // step)
+                b = k % step
+                u = a + step - 1 - b if step == stride else a + b
+                d = a + b + step
+                if d < n and dis[u] > dis[d]:
+                    dis[u], dis[d] = dis[d], dis[u]
+                    ids[u], ids[d] = ids[d], ids[u]
+            step >>= 1
+        stride <<= 1
+
+
+def warp_sort(key, val, n):
+    """warpSort (gpu_graph.cu:144-159) on n lanes: each round every lane reads
+    its xor partner, then takes the partner's pair when the keys differ and
+    the partner belongs on its side."""
+    rng = 1
+    while rng <= n:
+        c = rng // 2
+        while c >= 1:
+            k1 = [key[l ^ c] if (l ^ c) < n else key[l] for l in range(n)]
+            v1 = [val[l ^ c] if (l ^ c) < n else val[l] for l in range(n)]
+            for l in range(n):
+                p = bool(l & rng) == bool(l & c)
+                if key[l] != k1[l] and ((key[l] < k1[l]) != p):
+                    key[l], val[l] = k1[l], v1[l]
+            c //= 2
+        rng <<= 1
+
+
+class KernelModel:
+    def __init__(self, vectors, attrs, global_pid, P, cell_graphs, cross, tie=0):
+        pid = [int(c) for c in global_pid]
+        N = len(pid)
+        self.P = P
+        # get_idx_mapper (tools.cuh:862-915): cell starts, then each cell's
+        # points in ascending point id
+        size = [0] * P
+        for c in pid:
+            size[c] += 1
+        self.seg = [0] * (P + 1)
+        for c in range(P):
+            self.seg[c + 1] = self.seg[c] + size[c]
+        self.gidx = [0] * N
+        self.lidx = [0] * N
+        self.cell = pid
+        fill = [0] * P
+        for i, c in enumerate(pid):
+            self.gidx[self.seg[c] + fill[c]] = i
+            self.lidx[i] = fill[c]
+            fill[c] += 1
+        self.graph = np.ascontiguousarray(cell_graphs, np.int64)
+        self.R = self.graph.shape[1]
+        self.cross = np.ascontiguousarray(cross, np.int64)
+        self.E = self.cross.shape[1] // P
+        self.vec = np.ascontiguousarray(vectors, np.float64)
+        self.attrs = np.ascontiguousarray(attrs, np.float64)
+        self.tie = tie
+
+    # ------------------------------------------------------------ order
+    def _k(self, d, i):
+        if self.tie == 1:
+            return (d,)
+        return (d, 0xFFFFFFFF if i == SENT else self.seg[self.cell[i & IDM]] + self.lidx[i & IDM])
+
+    def le(self, d1, i1, d2, i2):
+        return self._k(d1, i1) <= self._k(d2, i2)
+
+    def lt(self, d1, i1, d2, i2):
+        return self._k(d1, i1) < self._k(d2, i2)
+
+    def sort_b(self, ids, dis, lo, n):
+        """warpSort of entries [lo, lo + n) (tie 1) or a stable sort on the key."""
+        k, v = dis[lo:lo + n], ids[lo:lo + n]
+        if self.tie == 1:
+            warp_sort(k, v, n)
+        else:
+            order = sorted(range(n), key=lambda t: self._k(k[t], v[t]))
+            k, v = [k[t] for t in order], [v[t] for t in order]
+        dis[lo:lo + n], ids[lo:lo + n] = k, v
+
+    def sort_net(self, ids, dis, n):
+        if self.tie == 1:
+            bitonic_no_explore(dis, ids, n)
+        else:
+            order = sorted(range(n), key=lambda t: self._k(dis[t], ids[t]))
+            ids[:n], dis[:n] = [ids[t] for t in order], [dis[t] for t in order]
+
+    def _ranks(self, a_id, a_d, n, b_id, b_d, m):
+        """merge_top's destination of every entry (gpu_graph.cu:172-206): the
+        bisection over the other list as written, then the own index."""
+        out = []
+        for i in range(n):
+            v = (a_d[i], a_id[i])
+            r, tmp = 0, m
+            while tmp > 1:
+                half = tmp // 2
+                if self.le(b_d[r + half], b_id[r + half], *v):
+                    r += half
+                tmp -= half
+            r += 1 if self.le(b_d[r], b_id[r], *v) else 0
+            out.append(r + i)
+        for j in range(m):
+            v = (b_d[j], b_id[j])
+            r, tmp = 0, n
+            while tmp > 1:
+                half = tmp // 2
+                if self.lt(a_d[r + half], a_id[r + half], *v):
+                    r += half
+                tmp -= half
+            r += 1 if self.lt(a_d[r], a_id[r], *v) else 0
+            out.append(r + j)
+        return out
+
+    def merge_top(self, a_id, a_d, b_id, b_d):
+        """merge_top (gpu_graph.cu:162-222) on two lists, in place."""
+        n, m = len(a_id), len(b_id)
+        pos = self._ranks(a_id, a_d, n, b_id, b_d, m)
+        vals = [(a_id[i], a_d[i]) for i in range(n)] + [(b_id[j], b_d[j]) for j in range(m)]
+        for p, (i, d) in zip(pos, vals):
+            if p < n:
+                a_id[p], a_d[p] = i, d
+            elif p < n + m:
+                b_id[p - n], b_d[p - n] = i, d
+
+    # ------------------------------------------------------------ search
+    def _dist(self, q, g):
+        t = self.vec[g] - q
+        return float(np.dot(t, t))
+
+    def _passes(self, g, lo, hi):
+        a = self.attrs[g]
+        return bool(np.all((a >= lo) & (a <= hi)))
+
+    def search(self, q, lo, hi, cells, entry, L, K=10, rl=10, max_iter=MAX_ITER):
+        """One traversal query over the ordered cells; returns (ids, dists,
+        expansions, distance evaluations, expanded point ids, recycle list)."""
+        R, E, P = self.R, self.E, self.P
+        q = np.asarray(q, np.float64)
+        lo = np.asarray(lo, np.float64)
+        hi = np.asarray(hi, np.float64)
+        top = [SENT] * (L + R)
+        dis = [INF] * (L + R)
+        rec_id = [SENT] * rl
+        rec_d = [INF] * rl
+        H = set()
+        nexp = ndist = 0
+        expanded = []
+
+        def merge_with_recycle():
+            # merge_top_with_recycle_list (gpu_graph.cu:224-315); the ranks
+            # are a permutation of [0, L + R), so every entry is rewritten
+            newt = [SENT] * (L + R)
+            newd = [INF] * (L + R)
+            pos = self._ranks(top, dis, L, top[L:], dis[L:], R)
+            vals = [(top[i], dis[i]) for i in range(L + R)]
+            for k, (p, (i, d)) in enumerate(zip(pos, vals)):
+                if p >= L:
+                    if k < L and i != SENT:
+                        if not self._passes(i & 0x3FFFFFFF, lo, hi):
+                            i, d = SENT, INF
+                    elif k >= L:
+                        i, d = SENT, INF
+                if p < L + R:
+                    newt[p], newd[p] = i, d
+            top[:], dis[:] = newt, newd
+
+        def evict_to_recycle():
+            # gpu_graph.cu:3412-3425 / 3536-3546
+            self.sort_b(top, dis, L, R)
+            if top[L] != SENT:
+                b_id, b_d = top[L:], dis[L:]
+                self.merge_top(rec_id, rec_d, b_id, b_d)
+                top[L:], dis[L:] = b_id, b_d
+
+        for i in range(R):
+            top[L + i] = self.gidx[self.seg[cells[0]] + int(entry[i])]
+            H.add(top[L + i])           # the entry's point id (gpu_graph.cu:3349)
+        for p_i, pid in enumerate(cells):
+            base = self.seg[pid]
+            for i in range(R):
+                if top[L + i] == SENT:
+                    dis[L + i] = INF
+                    continue
+                dis[L + i] = self._dist(q, top[L + i])
+                if p_i == 0:
+                    ndist += 1
+            self.sort_b(top, dis, L, R)
+            merge_with_recycle()
+            evict_to_recycle()
+            for it in range(max_iter):
+                if (it + 1) % HASH_RESET == 0:
+                    H = set(self.lidx[t & IDM] for t in top if t != SENT)
+                assert len(H) < HASHLEN
+                to_explore = SENT
+                for j in range(L):
+                    if (top[j] & EXPL) == 0:
+                        to_explore = self.lidx[top[j]]
+                        expanded.append(top[j])
+                        top[j] |= EXPL
+                        break
+                if to_explore == SENT:
+                    break
+                nexp += 1
+                for j in range(R):
+                    nl = int(self.graph[base + to_explore, j])
+                    g = self.gidx[base + nl]
+                    if nl in H:
+                        dis[L + j] = INF
+                    else:
+                        H.add(nl)
+                        dis[L + j] = self._dist(q, g)
+                        ndist += 1
+                    top[L + j] = g
+                self.sort_b(top, dis, L, R)
+                if top[L] != SENT:
+                    merge_with_recycle()
+                    evict_to_recycle()
+            for i in range(L):
+                top[i] |= EXPL
+            H = set()
+            if p_i < len(cells) - 1:
+                nxt = cells[p_i + 1]
+                nbase, nsz = self.seg[nxt], self.seg[nxt + 1] - self.seg[nxt]
+                wid = [SENT] * 128
+                wd = [INF] * 128
+                for i in range(128):
+                    ci = i % 64
+                    if ci >= L or top[ci] == SENT:
+                        continue
+                    pure = top[ci] & IDM
+                    j = 0
+                    while j < E:
+                        nl = int(self.cross[pure, nxt * E + j])
+                        j += 1
+                        if nl not in H:
+                            H.add(nl)
+                            wid[i] = self.gidx[nbase + nl]
+                            break
+                        if j == E:
+                            for rp in range(min(62500, nsz)):
+                                if rp not in H:
+                                    H.add(rp)
+                                    wid[i] = self.gidx[nbase + rp]
+                                    break
+                for i in range(128):
+                    if wid[i] != SENT:
+                        wd[i] = self._dist(q, wid[i])
+                        ndist += 1
+                self.sort_net(wid, wd, 128)
+                H = set()
+                for i in range(R):
+                    top[L + i] = wid[i]
+                    if wid[i] != SENT:
+                        H.add(self.lidx[wid[i]])
+                for i in range(128 - R):
+                    if wid[R + i] != SENT:
+                        H.add(self.lidx[wid[R + i]])
+                a_id, a_d = top[:L], dis[:L]
+                b_id, b_d = wid[R:R + 64], wd[R:R + 64]
+                self.merge_top(a_id, a_d, b_id, b_d)
+                top[:L], dis[:L] = a_id, a_d
+            for i in range(L):
+                if top[i] != SENT:
+                    H.add(self.lidx[top[i] & IDM])
+        # post-filter, sort, recycle merge (gpu_graph.cu:4025-4047)
+        for i in range(L):
+            if top[i] != SENT and not self._passes(top[i] & IDM, lo, hi):
+                top[i], dis[i] = SENT, INF
+        a_id, a_d = top[:L], dis[:L]
+        self.sort_net(a_id, a_d, L)
+        recycle = list(zip(rec_id, rec_d))
+        if rec_id[0] != SENT:
+            self.merge_top(a_id, a_d, list(rec_id), list(rec_d))
+        ids, dists = [], []
+        for i, d in zip(a_id, a_d):
+            if len(ids) == K:
+                break
+            if i == SENT or (i & IDM) in ids:
+                continue
+            ids.append(i & IDM)
+            dists.append(d)
+        while len(ids) < K:
+            ids.append(0x7FFFFFFF)
+            dists.append(INF)
+        return ids, dists, nexp, ndist, [e & IDM for e in expanded], recycle

@@ -9,6 +9,7 @@ import pytest
 from garfield_amd import _lib
 from garfield_amd._lib import GarfieldError
 from oracle import oracle
+from oracle import oracle as orc
 
 
 # ---------------------------------------------------------------- grid
@@ -216,3 +217,54 @@ def test_builder_rejects_bad_input_before_device():
     with pytest.raises(GarfieldError) as e:
         _lib.kmeans(np.zeros((10, 64), np.uint8), 11, 2, init_ids=list(range(10)) + [0])
     assert e.value.status == 1   # more centres than points
+
+
+def test_graph_optimisation_hand_case():
+    """Points 0, 1, 2, 3 on a line, one cell, exact 3-NN rows by (distance, id):
+    [1 2 3] [0 2 3] [1 3 0] [2 1 0].  Detours (an earlier neighbour listing
+    the target at an earlier rank): row 0 -> 3 through 2 (2 lists 3 at rank 1
+    < 2); row 3 -> 1 through 2 (rank 0 < 1) and 3 -> 0 through 1 (rank 0 < 2):
+    counts [0 0 1] [0 0 1] [0 0 1] [0 1 1].  With R = 2 each row keeps its
+    first edge; reverse lists (rank 0 edges in row order, then rank 1):
+    rev[0] = [1], rev[1] = [0, 2], rev[2] = [3, 0], rev[3] = [2]; rows
+    [1 2] (rev 1 repeats, then the reordered rest), [0 2], [1 3], [2 1]."""
+    g = np.array([[1, 2, 3], [0, 2, 3], [1, 3, 0], [2, 1, 0]])
+    o, det = orc.detour_order(g)
+    assert det.tolist() == [[0, 0, 1], [0, 0, 1], [0, 0, 1], [0, 1, 1]]
+    assert o.tolist() == g.tolist()
+    assert orc.optimize_graphs(g, [4], 2).tolist() == [[1, 2], [0, 2], [1, 3], [2, 1]]
+
+
+def test_detour_counts_brute_force():
+    """detour_order against the definition evaluated by plain loops."""
+    rng = np.random.default_rng(8)
+    for n, I in ((30, 8), (12, 11), (50, 16)):
+        g = np.array([rng.choice([x for x in range(n) if x != a], I, replace=False) for a in range(n)])
+        o, det = orc.detour_order(g)
+        for a in range(n):
+            row = g[a].tolist()
+            for k, d in enumerate(row):
+                cnt = sum(1 for j in range(k) if d in g[row[j]].tolist()[:k])
+                assert det[a, k] == cnt
+            keyed = sorted(range(I), key=lambda k: (det[a, k], k))
+            assert o[a].tolist() == [row[k] for k in keyed]
+
+
+def test_optimised_graph_properties():
+    """Every row holds R distinct in-cell ids without itself, its first R/2
+    ids are its first R/2 reordered edges, and every node with an incoming
+    pruned edge among the first R ranks is reachable."""
+    rng = np.random.default_rng(9)
+    x = rng.integers(0, 256, (600, 16)).astype(np.uint8)
+    pid = rng.integers(0, 3, 600).astype(np.uint32)
+    knn = orc.knn_cell_graphs(x, pid, 3, 24)
+    sizes = np.bincount(pid, minlength=3)
+    out = orc.optimize_graphs(knn, sizes, 12)
+    start = 0
+    for c, n in enumerate(sizes):
+        o, _ = orc.detour_order(knn[start:start + n])
+        for a in range(n):
+            row = out[start + a].tolist()
+            assert len(set(row)) == 12 and a not in row and max(row) < n
+            assert row[:6] == o[a, :6].tolist()
+        start += n

@@ -128,3 +128,57 @@ def test_kmeans_headline_size_property():
     d = oracle._sq(v[pts], cen)
     assert np.array_equal(lab[pts], np.argmin(d, axis=1))
     assert len(np.unique(lab)) > C // 2
+
+
+@pytest.mark.parametrize("N,P,I,R,hi", [
+    (2400, 4, 64, 32, 256),    # the bench's shape: kNN of degree 64 optimised to 32
+    (1800, 3, 24, 16, 4),      # heavy distance ties in the kNN lists
+    (400, 6, 16, 8, 256),      # small cells (about 67 points)
+    (90, 3, 40, 32, 256),      # cells of about 30 points: rows repeat their nearest
+])
+def test_optimize_graphs_matches_oracle(N, P, I, R, hi):
+    """gf_optimize_graphs (GPU detour order, host reverse edges and merge) bit
+    for bit against oracle.optimize_graphs, from the library's exact kNN
+    graphs of degree I."""
+    _print_case("optimize", N=N, P=P, I=I, R=R, hi=hi)
+    rng = np.random.default_rng(N + I)
+    v = rng.integers(0, hi, (N, 64)).astype(np.uint8)
+    gp = rng.integers(0, P, N).astype(np.uint32)
+    knn, _, _ = _lib.build_graphs(v, gp, P, I, 1)
+    sizes = np.bincount(gp, minlength=P)
+    out, _ = _lib.optimize_graphs(knn, sizes, R)
+    assert np.array_equal(out, oracle.optimize_graphs(knn, sizes, R))
+
+
+def test_optimised_graph_search():
+    """An index whose per-cell graphs are optimised (degree 64 kNN -> 32) on a
+    config-2-shaped world (uniform 128-d integers, 4x4 cells): the traversal
+    on it is bit-exact against the oracle; the recall of both graphs at L = 64
+    is printed (on uniform 128-d data the two are within a few points)."""
+    import garfield_amd as gf
+    _print_case("optimized-search")
+    cfg = synth.config_headline(N=40_000, Q=400, R=32, C=64, seed=31)
+    lo, hi = cfg["lo"].astype(np.float32), cfg["hi"].astype(np.float32)
+    gt, gtd = oracle.ground_truth(cfg["vectors"], cfg["attrs"], cfg["queries"], lo, hi, 10)
+    rec = {}
+    for graph in ("knn", "cagra"):
+        ix = synth.build_index(cfg["vectors"], cfg["attrs"], cfg["grid"], 32, 2, 0, device="hip", graph=graph)
+        dev = synth.open_device_index(ix)
+        b = dev.batch(cfg["queries"], lo, hi)
+        b.mark_cells(0.0)
+        ent = gf.entry_points(40_000, ix["P"], 32)
+        ids, dist, _ = b.search(L=64, entry_points=ent)
+        if graph == "cagra":
+            cells, cnt, little, _ = b.get_cells()
+            O = oracle.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"],
+                                   ix["cross"])
+            oids, odist, _ = O.search(cfg["queries"], lo, hi, cells, cnt, little, ent, 64)
+            assert np.array_equal(ids, oids) and np.array_equal(dist.view(np.uint32), odist.view(np.uint32))
+        safe = np.where(ids == oracle.SENTINEL, 0, ids)
+        ex = ((cfg["vectors"][safe].astype(np.float64) - cfg["queries"][:, None, :]) ** 2).sum(-1)
+        ex[ids == oracle.SENTINEL] = np.inf
+        rec[graph] = oracle.recall(ids, gt, gtd, ex, tie_aware=True)
+        b.close()
+        dev.close()
+    print(f"recall at L=64: exact kNN {rec['knn']:.4f}, optimised {rec['cagra']:.4f}", flush=True)
+    assert abs(rec["cagra"] - rec["knn"]) < 0.1

@@ -92,6 +92,10 @@ def test_graph_replay_into_page_locked_arrays(monkeypatch, world_sub2):
         monkeypatch.delenv("GARFIELD_NO_GRAPH")
         for r in range(4):
             out = pinned if r % 2 == 0 else None
+            if out is not None:
+                # a replay must overwrite every entry of the caller's arrays
+                out[0].fill(0xFFFFFFFF)
+                out[1].fill(np.nan)
             ids, d, st = b.search(L=32, K=10, rl=10, out=out)
             assert st.graph == 1
             assert np.array_equal(ids, ids0), f"run {r}: ids differ"

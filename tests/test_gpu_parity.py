@@ -112,6 +112,37 @@ def test_centroid_order(small_world):
     dev.close()
 
 
+def test_centroid_order_reference_ties(small_world):
+    """ref_ties: equal cell scores keep the order of the reference's network
+    (bitonic_sort_id_by_num_int), bit for bit against the oracle's replay in
+    tie mode 1 on the GPU's own nearest centres; the order differs from the
+    default (ties by cell id) for some queries."""
+    from oracle import oracle as orc
+    cfg, ix = small_world
+    _print_case("centroid-ref-ties")
+    lo, hi, cells, cnt, sel, little = _oracle_pipeline(cfg, ix, 0.0)
+    _, hist = orc.centres_hist(ix["vectors"], ix["labels"], ix["global_pid"], ix["P"])
+    out = {}
+    for ref in (False, True):
+        dev = _device(ix, ref_ties=ref)
+        b = dev.batch(cfg["queries"], lo, hi)
+        b.mark_cells(0.0)
+        b.order_cells(4)
+        _, gtop = b.get_centroid()
+        gc, gcnt, _, _ = b.get_cells()
+        orc.set_tie_mode(1 if ref else 0)
+        try:
+            ocells = orc.sort_cells(cells, cnt, gtop, hist)
+        finally:
+            orc.set_tie_mode(0)
+        for q in range(len(cnt)):
+            assert np.array_equal(gc[q, :cnt[q]], ocells[q, :cnt[q]]), (ref, q)
+        out[ref] = gc
+        b.close()
+        dev.close()
+    assert any(not np.array_equal(out[False][q, :cnt[q]], out[True][q, :cnt[q]]) for q in range(len(cnt)))
+
+
 def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, postfilter=1 << 30, Q=None):
     import garfield_amd as gf
     from oracle import oracle as orc

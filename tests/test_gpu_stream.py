@@ -308,3 +308,51 @@ def test_stream_bruteforce_overflow_rerun():
     for ids, dists in out:
         assert np.array_equal(dists, gtd.astype(np.float32))
     assert np.array_equal(out[0][0], out[1][0])
+
+
+def test_c5_shaped_stream_matches_oracle():
+    """Config 5's own shape at 100k points: 128-d u8 vectors uniform in
+    [0, 255], 2 uniform attributes in [0, 10000) on a 16x16 arithmetic grid
+    (256 cells), R = 32 exact per-cell graphs and E = 2 cross edges (built by
+    the library's int8 MFMA builder, which test_gpu_build pins bit for bit),
+    queries with selectivity log-U[0.5 %, 20 %], the reference's plan of 16
+    consecutive cells per batch (bigdataset_experiment.cu:271-277), streamed
+    under a device budget below half the resident index.  Ids, distances and
+    counters against the oracle run batch by batch; the same routes mixed as
+    the out-of-core driver's little-cell threshold gives them."""
+    import garfield_amd as gf
+    from oracle import oracle as orc
+    N, D, Q, L = 100_000, 128, 160, 48
+    grid = [16, 16]
+    amin = np.zeros(2, np.float32)
+    width = np.full(2, 625.0, np.float32)
+    _print_case("c5-shaped", N=N, P=256, R=32)
+    vec = synth.uniform_int_vectors(N, D, 501).astype(np.uint8)
+    att = np.random.default_rng(502).integers(0, 10000, (N, 2)).astype(np.int32)
+    queries = synth.uniform_int_vectors(Q, D, 503).astype(np.float32)
+    sel = synth.log_uniform(Q, 0.005, 0.2, 504)
+    lo, hi = synth.ranges_for_selectivity(Q, 2, sel, 505)
+    ix = synth.build_index(vec, att, grid, 32, 2, 0, device="hip", arith=(amin, width))
+    ix["vectors"] = vec.astype(np.float32)
+    cfg = dict(queries=queries, lo=lo.astype(np.float32), hi=hi.astype(np.float32))
+    res = gl.Index.from_arrays(*_args(ix), vec_dtype=gl.VEC_U8)
+    budget = res.device_bytes // 2
+    res.close()
+    sx = gl.Index.create_streamed(*_args(ix), batch_cells=16, device_budget=budget)
+    assert sx.streamed and sx.nbatch == 16 and sx.device_bytes <= budget
+    b = sx.batch(cfg["queries"], cfg["lo"], cfg["hi"])
+    b.mark_cells_grid(amin, width, 0.3)
+    flags = b.get_cell_flags()
+    ids, dists, st = b.search(L=L, K=10, rl=10)
+    ctr = b.get_counters()
+    assert st.q_traverse > 0 and st.q_bruteforce > 0
+    sizes = synth.cell_sizes(ix)
+    ent = orc.entry_draw(int(sizes[sizes > 0].min()), 10 * L, ix["R"])
+    plan = [list(range(16 * i, 16 * i + 16)) for i in range(16)]
+    oids, od, oc = _oracle_stream(ix, plan, cfg, flags, ent, L, mfma=bool(st.bf_mfma))
+    bad = np.nonzero(np.any(ids != oids, axis=1))[0]
+    assert bad.size == 0, f"{bad.size} queries differ, first {bad[:5]}"
+    assert np.array_equal(dists.view(np.uint32), od.view(np.uint32))
+    assert np.array_equal(ctr.astype(np.int64), oc)
+    b.close()
+    sx.close()

@@ -1,0 +1,126 @@
+"""The oracle's REF_HFMA2 mode: the reference's own fp16 distance arithmetic
+(gpu_graph.cu:3394-3403), and how often the HIP fp16 route's ids (binary16
+values, fp32 accumulation) differ from it.
+
+Pinned by: numpy's binary16 conversion (round to nearest even from double) for
+every rounding step; a hand-computed case whose rounding is visible; exact
+agreement with the exact distance whenever every intermediate value is a
+small integer; and a numpy restatement of the lane and tree order.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+
+@pytest.fixture(autouse=True)
+def _modes():
+    orc.set_dist_mode(0)
+    orc.set_tie_mode(0)
+    yield
+    orc.set_dist_mode(0)
+    orc.set_tie_mode(0)
+
+
+def test_half_rounding_matches_numpy():
+    rng = np.random.default_rng(1)
+    vals = np.concatenate([
+        rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 5, 20000),
+        [0.0, -0.0, 65504.0, 65519.999, 65520.0, 1e6, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -14,
+         2.0 ** -14 - 2.0 ** -25, 2079.0, 2078.5, 2081.0, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, np.inf]])
+    for v in vals:
+        assert orc.half_rne(v) == int(np.float64(v).astype(np.float16).view(np.uint16)), v
+
+
+def test_hfma2_hand_case():
+    """q = 0, x = (45.5, 1, 3, 0): lane 0 alone; acc.x = round(45.5^2 =
+    2070.25) = 2070 (binary16 step 2 above 2048), then round(2070 + 9 = 2079)
+    = 2080 (a tie, to the even mantissa 16); acc.y = 1; the tree adds zeros;
+    the result is 2080 + 1 = 2081 where the exact distance is 2080.25."""
+    q = orc.f2h(np.zeros(4, np.float32))
+    x = orc.f2h(np.array([45.5, 1, 3, 0], np.float32))
+    assert orc.hfma2_dist(q, x) == 2081.0
+
+
+def test_hfma2_exact_on_small_integers():
+    """Integer rows whose squared differences and partial sums stay below
+    2048 are exact in binary16: the distance is the exact one."""
+    rng = np.random.default_rng(2)
+    for D in (96, 128, 768):
+        for _ in range(30):
+            q = rng.integers(0, 3, D).astype(np.float32)
+            x = rng.integers(0, 3, D).astype(np.float32)
+            assert orc.hfma2_dist(orc.f2h(q), orc.f2h(x)) == float(np.sum((q - x) ** 2))
+
+
+def _numpy_hfma2(q, x):
+    """The same arithmetic written with numpy: chunks of 4 as a (chunks, 4)
+    array, lane j = chunks j, j + 32, ...; each step rounded by numpy's
+    float64 -> float16 conversion."""
+    h = lambda v: np.float64(np.float16(v))
+    qc, xc = q.astype(np.float64).reshape(-1, 4), x.astype(np.float64).reshape(-1, 4)
+    acc = np.zeros((32, 2))
+    for c in range(qc.shape[0]):
+        lane = c % 32
+        for pair in (0, 2):
+            for comp in (0, 1):
+                d = h(qc[c, pair + comp] - xc[c, pair + comp])
+                acc[lane, comp] = h(d * d + acc[lane, comp])
+    for m in (16, 8, 4, 2, 1):
+        src = np.array([l + m if l + m < 32 else l for l in range(32)])
+        acc = np.vectorize(h)(acc + acc[src])
+    return float(np.float32(acc[0, 0]) + np.float32(acc[0, 1]))
+
+
+def test_hfma2_matches_numpy_restatement():
+    rng = np.random.default_rng(3)
+    for D in (96, 128, 256, 768):
+        for scale in (0.01, 1.0, 30.0):
+            for _ in range(8):
+                q = orc.f2h(rng.standard_normal(D).astype(np.float32) * scale)
+                x = orc.f2h(rng.standard_normal(D).astype(np.float32) * scale)
+                want = _numpy_hfma2(q.view(np.float16).astype(np.float64), x.view(np.float16).astype(np.float64))
+                assert orc.hfma2_dist(q, x) == want
+
+
+def test_fp16_route_against_ref_hfma2_report(world_c4, capsys):
+    """ID agreement of the HIP fp16 route (binary16 rows, fp32 accumulation;
+    the oracle's mode 0, which the GPU matches bit for bit) with the
+    reference's half arithmetic (REF_HFMA2), on the config-4-shaped world
+    (768-d Gaussian mixture, f2h_factor 1, R = 32) at L = 32, 64, 128.  The
+    half sums round at about 2^-11 relative, so near-equal candidates swap
+    places; the report gives the share of queries with identical ids and the
+    recall of each against the exact filtered ground truth."""
+    from garfield_amd import synth
+    cfg, ix = world_c4
+    l_q, r_q = synth.quantile_arrays(ix)
+    lo, hi = cfg["lo"].astype(np.float32), cfg["hi"].astype(np.float32)
+    cells, cnt = orc.cells(lo, hi, ix["grid"], l_q, r_q, synth.cell_sizes(ix))
+    vh = orc.f2h(ix["vectors"])
+    qh = orc.f2h(cfg["queries"])
+    O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"], ix["cross"],
+                        vec_f16=vh)
+    gt, gtd = orc.ground_truth(ix["vectors"], ix["attrs"], cfg["queries"], lo, hi, 10)
+    ent = orc.entry_points(ix["vectors"].shape[0], ix["P"], ix["R"])
+    z = np.zeros_like(cnt)
+    lines = []
+
+    def rec(ids):
+        safe = np.where(ids == orc.SENTINEL, 0, ids)
+        ex = ((ix["vectors"][safe].astype(np.float64) - cfg["queries"][:, None, :]) ** 2).sum(-1)
+        ex[ids == orc.SENTINEL] = np.inf
+        return orc.recall(ids, gt, gtd, ex, tie_aware=True)
+
+    for L in (32, 64, 128):
+        orc.set_dist_mode(0)
+        a, _, _ = O.search(qh, lo, hi, cells, cnt, z, ent, L)
+        orc.set_dist_mode(1)
+        b, _, _ = O.search(qh, lo, hi, cells, cnt, z, ent, L)
+        orc.set_dist_mode(0)
+        same = float(np.mean(np.all(a == b, axis=1)))
+        overlap = float(np.mean([len(set(x.tolist()) & set(y.tolist())) / 10 for x, y in zip(a, b)]))
+        lines.append(f"L={L}: identical ids {same:.3f} of queries, id overlap {overlap:.3f}, "
+                     f"recall fp32-accumulated {rec(a):.4f}, REF_HFMA2 {rec(b):.4f}")
+        assert overlap > 0.5
+    with capsys.disabled():
+        print("\n" + "\n".join(lines))

@@ -1,0 +1,450 @@
+"""Pinning the traversal oracle (orc_search, oracle/garfield_oracle.cpp).
+
+The reference is CUDA-only and cannot run here, and the GPU parity tests
+compare the HIP kernels bit for bit with this oracle, so the oracle itself is
+checked by tests that a plausible restatement mistake fails:
+
+1. known answers of its building blocks, derived by hand from the reference:
+   bitonic_sort_id_by_dis_no_explore (gpu_graph.cu:77-101, including
+   check.cu:752-804's sort_test, a reversed 200-array), warpSort (:144-159),
+   merge_top (:162-222) and merge_top_with_recycle_list with the recycle merge
+   (:224-315, 3412-3425);
+2. a closed form: a query over one cell whose graph is strongly connected, with
+   L above the cell's size, returns the filtered brute force of that cell;
+3. a two-cell, 16-point index whose whole trajectory (expansion order,
+   expansions, distance evaluations, cross slots, recycle list, results) is
+   derived by hand below;
+4. agreement with tests/kernel_model.py, a second restatement that follows the
+   reference kernel's own control flow (its arrays, explored bit, bisection
+   ranks and sorting networks), in both tie modes, on random small worlds and
+   with a lowered per-cell iteration cap;
+5. every planted mistake of orc_set_mutation turns at least one of 1-4 red
+   (two of them only under the reference's tie order, as
+   test_slot_order_is_invisible_under_a_total_order shows).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from kernel_model import KernelModel, bitonic_no_explore, warp_sort
+
+SENT = 0xFFFFFFFF
+INF = np.float32(np.inf)
+
+
+@pytest.fixture(autouse=True)
+def _reset_oracle():
+    orc.set_tie_mode(0)
+    orc.set_mutation(0)
+    orc.set_max_iter(0)
+    yield
+    orc.set_tie_mode(0)
+    orc.set_mutation(0)
+    orc.set_max_iter(0)
+
+
+# ------------------------------------------------------------------ 1. KATs
+def check_networks():
+    """Sorting networks: hand-traced answers and check.cu's sort_test."""
+    ok = True
+    # sort_test (check.cu:752-804): ids j, distances 200 - j, expect ascending
+    d, i = orc.bitonic_sort_dis(200.0 - np.arange(200, dtype=np.float32), np.arange(200, dtype=np.uint32))
+    ok &= bool(np.all(np.diff(d) >= 0)) and np.array_equal(i, np.arange(199, -1, -1))
+    # [1, 1, 0, 0] by the flip network (stride 2, step 2 swaps (1,2) then
+    # (0,3)): the equal keys come out in reverse order, ids [3, 2, 1, 0]
+    d, i = orc.bitonic_sort_dis([1, 1, 0, 0], [0, 1, 2, 3])
+    ok &= np.array_equal(i, [3, 2, 1, 0]) and np.array_equal(d, [0, 0, 1, 1])
+    # warpSort of [0, 1, 0, 1]: range 2 gives lanes [0, 1, 3, 2] (keys
+    # [0, 1, 1, 0]); range 4 / c 2 swaps lanes 1 and 3: values [0, 2, 3, 1]
+    k, v = orc.warp_sort([0, 1, 0, 1], [0, 1, 2, 3])
+    ok &= np.array_equal(v, [0, 2, 3, 1]) and np.array_equal(k, [0, 0, 1, 1])
+    return bool(ok)
+
+
+def check_merges():
+    """merge_top and the recycle merge on hand-derived cases."""
+    ok = True
+    # A = [a1, b3, c5], B = [x3, y4]: A_i -> i + #{B <= A_i} = 0, 2, 4;
+    # B_j -> j + #{A < B_j} = 1, 3: A = [a, x, b], B = [y, c] (the incoming
+    # x goes before the equal b)
+    a, b, x, y, c = 10, 11, 20, 21, 12
+    d1, i1, d2, i2 = orc.merge_top([1, 3, 5], [a, b, c], [3, 4], [x, y], tie=1)
+    ok &= np.array_equal(i1, [a, x, b]) and np.array_equal(i2, [y, c])
+    ok &= np.array_equal(d1, [1, 3, 3]) and np.array_equal(d2, [4, 5])
+    # merge_top_with_recycle_list: A = [a1, b2, c6], B = [x3, y7], recycle
+    # [r5, -]: positions a0 b1 x2 c3 y4; c is evicted (kept only if it passes
+    # the filter), y is rejected.  Attribute of point p is p; range [0, 100].
+    attrs = np.arange(200, dtype=np.float32)[:, None]
+    A, B, Rc = orc.merge_recycle(attrs, [0], [100], [1, 2, 6], [1, 2, 150], [3, 7], [3, 4],
+                                 [5, INF], [5, SENT], tie=1)
+    # c = 150 fails the range: the recycle list stays [r5, -]
+    ok &= np.array_equal(A[1], [1, 2, 3]) and np.array_equal(B[1], [SENT, SENT])
+    ok &= np.array_equal(Rc[1], [5, SENT])
+    A, B, Rc = orc.merge_recycle(attrs, [0], [100], [1, 2, 6], [1, 2, 6], [3, 7], [3, 4],
+                                 [5, INF], [5, SENT], tie=1)
+    # c = 6 passes: B = [c6, -] merges into [r5, -]: recycle [r5, c6]
+    ok &= np.array_equal(Rc[1], [5, 6]) and np.array_equal(Rc[0], [5, 6])
+    # equal distances: the evictee e (6) goes before the recycle entry r (6)
+    A, B, Rc = orc.merge_recycle(attrs, [0], [100], [1, 2, 6], [1, 2, 7], [3, 9], [3, 4],
+                                 [6, INF], [8, SENT], tie=1)
+    ok &= np.array_equal(Rc[1], [7, 8])
+    return bool(ok)
+
+
+def test_sorting_network_kats():
+    assert check_networks()
+    # the Python model's networks give the same answers
+    d, i = [1.0, 1.0, 0.0, 0.0], [0, 1, 2, 3]
+    bitonic_no_explore(d, i, 4)
+    assert i == [3, 2, 1, 0]
+    k, v = [0, 1, 0, 1], [0, 1, 2, 3]
+    warp_sort(k, v, 4)
+    assert v == [0, 2, 3, 1]
+
+
+def test_sorting_networks_sort_and_agree_with_model():
+    rng = np.random.default_rng(3)
+    for n in (16, 32, 64, 128, 200, 37):
+        for _ in range(20):
+            d = rng.integers(0, 5, n).astype(np.float32)          # many ties
+            ids = rng.permutation(n).astype(np.uint32)
+            od, oi = orc.bitonic_sort_dis(d, ids)
+            md, mi = [float(x) for x in d], [int(x) for x in ids]
+            bitonic_no_explore(md, mi, n)
+            assert np.all(np.diff(od) >= 0) and sorted(oi.tolist()) == sorted(ids.tolist())
+            assert oi.tolist() == mi
+            if n in (16, 32, 64):
+                ok, ov = orc.warp_sort(d, ids)
+                mk, mv = [float(x) for x in d], [int(x) for x in ids]
+                warp_sort(mk, mv, n)
+                assert np.all(np.diff(ok) >= 0) and ov.tolist() == mv
+
+
+def test_merge_kats():
+    assert check_merges()
+
+
+def test_merge_top_equals_std_merge():
+    """With distinct keys merge_top is std::merge split at n; at equal keys the
+    incoming list's entry goes first."""
+    rng = np.random.default_rng(4)
+    for _ in range(200):
+        n, m = int(rng.integers(1, 40)), int(rng.integers(1, 40))
+        d1 = np.sort(rng.integers(0, 30, n)).astype(np.float32)
+        d2 = np.sort(rng.integers(0, 30, m)).astype(np.float32)
+        i1, i2 = np.arange(n, dtype=np.uint32), np.arange(100, 100 + m, dtype=np.uint32)
+        a = orc.merge_top(d1, i1, d2, i2, tie=1)
+        ref = sorted([(float(d), 1, int(i)) for d, i in zip(d1, i1)] + [(float(d), 0, int(i)) for d, i in zip(d2, i2)])
+        got = [(float(d), int(i)) for d, i in zip(np.concatenate([a[0], a[2]]), np.concatenate([a[1], a[3]]))]
+        assert got == [(d, i) for d, _, i in ref]
+
+
+# --------------------------------------------------------- 2. closed form
+def _closed_world(n=40, R=4, D=8, seed=0):
+    """Two cells of n points; cell 1 holds point ids n..2n-1, so the entry ids
+    the reference inserts into the visited set (point ids) never equal a local
+    id of that cell.  Cell 1's graph: edge 0 is the ring l -> l+1, the others
+    random, so it is strongly connected."""
+    rng = np.random.default_rng(seed)
+    N = 2 * n
+    vec = rng.integers(0, 16, (N, D)).astype(np.float32)
+    att = rng.integers(0, 100, (N, 1)).astype(np.float32)
+    pid = np.array([0] * n + [1] * n, np.uint32)
+    g = rng.integers(0, n, (N, R)).astype(np.uint32)
+    g[:, 0] = (np.arange(N) + 1) % n
+    cross = rng.integers(0, n, (N, 2 * 2)).astype(np.uint32)
+    return vec, att, pid, g, cross
+
+
+def check_closed_form():
+    ok = True
+    n, R = 40, 4
+    vec, att, pid, g, cross = _closed_world(n, R)
+    O = orc.OracleIndex(vec, att, pid, 2, g, cross)
+    rng = np.random.default_rng(9)
+    members = np.arange(n, 2 * n)
+    for t in range(12):
+        q = rng.integers(0, 16, 8).astype(np.float32)
+        lo = np.array([rng.integers(0, 50)], np.float32)
+        hi = lo + np.float32(rng.integers(20, 60))
+        ent = rng.integers(0, n, R).astype(np.uint32)
+        for L in (n + R, 2 * n):
+            ids, dist, ctr, _, _, _, _ = O.trace(q, lo, hi, [1], ent, L, K=10)
+            inr = members[(att[members, 0] >= lo[0]) & (att[members, 0] <= hi[0])]
+            d = np.sum((vec[inr].astype(np.float64) - q) ** 2, axis=1)
+            order = np.lexsort((inr, d))[:10]       # cell-major position = id order in cell 1
+            exp = np.full(10, orc.SENTINEL, np.uint32)
+            exp[:len(order)] = inr[order]
+            ok &= np.array_equal(ids, exp)
+            ok &= np.array_equal(dist[:len(order)], d[order].astype(np.float32))
+    return bool(ok)
+
+
+def test_closed_form_single_cell():
+    assert check_closed_form()
+
+
+# ------------------------------------------------------ 3. hand-traced case
+def _hand_world():
+    """16 points on a line (dimension 0 of D = 4): cell 0 = ids 0..7 at
+    1, 6, 16, 19, 25, 31, 40, 60; cell 1 = ids 8..15 at 10, 13, 17, 22, 28, 35,
+    43, 52.  Attribute of id p is p.  Degree 2 (the two nearest in the cell,
+    by local id):
+      cell 0: [1,2] [0,2] [3,4] [2,4] [3,5] [4,6] [5,4] [6,5]
+      cell 1: [1,2] [0,2] [1,3] [2,4] [3,5] [4,6] [5,7] [6,5]
+    cross edges of cell 1's points into cell 0 (E = 2, local ids):
+      [1,2] [2,3] [2,3] [3,4] [4,5] [5,6] [6,5] [7,6]."""
+    N = 16
+    vec = np.zeros((N, 4), np.float32)
+    vec[:8, 0] = [1, 6, 16, 19, 25, 31, 40, 60]
+    vec[8:, 0] = [10, 13, 17, 22, 28, 35, 43, 52]
+    att = np.arange(N, dtype=np.float32)[:, None]
+    pid = np.array([0] * 8 + [1] * 8, np.uint32)
+    g = np.array([[1, 2], [0, 2], [3, 4], [2, 4], [3, 5], [4, 6], [5, 4], [6, 5],
+                  [1, 2], [0, 2], [1, 3], [2, 4], [3, 5], [4, 6], [5, 7], [6, 5]], np.uint32)
+    cross = np.zeros((N, 4), np.uint32)
+    cross[:, 1] = cross[:, 3] = 1
+    cross[8:, 0:2] = [[1, 2], [2, 3], [2, 3], [3, 4], [4, 5], [5, 6], [6, 5], [7, 6]]
+    return vec, att, pid, g, cross
+
+
+def check_hand_trace():
+    """Query x = 20, range [3, 12], cells [1, 0], entries local [7, 6] of
+    cell 1 (ids 15, 14), L = 4, R = 2, K = 3, rl = 2.  Squared distances:
+    ids 0-7: 361 196 16 1 25 121 400 1600; ids 8-15: 100 49 9 4 64 225 529 1024.
+
+    Cell 1.  Entries 15 (1024), 14 (529) enter the list; the visited set holds
+    their point ids 15, 14, not their local ids 7, 6 (gpu_graph.cu:3349).
+      it 0: expand 14 (local 6): neighbours 13 (new, 225) and 15 (local 7 is
+            not in the set: new again, 1024).  List [13, 14, 15, 15].
+      it 1: expand 13: 12 (new, 64), 14 (local 6 new again, 529).  List
+            [12, 13, 14, 14]; both 15s are evicted, fail the range: dropped.
+      it 2: expand 12: 11 (new, 4), 13 (seen: +inf, rejected).  List
+            [11, 12, 13, 14]; the explored 14 is evicted and fails the range.
+      it 3: visited set rebuilt from the list: local {3, 4, 5, 6}.  Expand 11:
+            10 (new, 9), 12 (seen).  List [11, 10, 12, 13]; 14 evicted, fails.
+      it 4: expand 10: 9 (new, 49), 11 (seen).  List [11, 10, 9, 12]; 13
+            evicted, fails.
+      it 5: expand 9: 8 (new, 100: beyond the list), 10 (seen).  No change.
+      it 6: nothing unexplored.
+    Cross slots into cell 0 (visited set emptied): slot i follows candidate
+    i % 64 of [11, 10, 9, 12]: slot 0 takes local 3 (11's first edge), slot 1
+    local 2, slot 2 (9: [2, 3] taken) the first free local 0, slot 3 local 4;
+    slots 64-67 fall back to 1, 5, 6, 7: all 8 points of cell 0, sorted
+    3 (1), 2 (16), 4 (25), 5, 1, 0, 6, 7.  Entries [3, 2]; slots 2.. merge
+    into the list: [11, 10, 4, 9].
+    Cell 0.  Entries merge: list [3, 11, 10, 2]; 4 (25) and 9 (49) are
+    evicted, pass the range and fill the recycle list [4, 9].  Expand 3 and 2:
+    every neighbour is in the visited set.
+    Post-filter drops 2 (attribute 2); the recycle merge gives [3, 11, 10, 4].
+    Results [3, 11, 10] at [1, 4, 9]; 8 expansions; 2 + 2 + 2 + 1 + 1 + 1 + 1
+    + 8 = 18 distance evaluations; expansion order 14 13 12 11 10 9 3 2."""
+    vec, att, pid, g, cross = _hand_world()
+    O = orc.OracleIndex(vec, att, pid, 2, g, cross)
+    ids, dist, ctr, ex, exc, rid, rd = O.trace(np.array([20, 0, 0, 0], np.float32), [3], [12], [1, 0],
+                                               np.array([7, 6], np.uint32), 4, K=3, rl=2)
+    return (ids.tolist() == [3, 11, 10] and dist.tolist() == [1, 4, 9] and int(ctr[0]) == 8
+            and int(ctr[1]) == 18 and ex.tolist() == [14, 13, 12, 11, 10, 9, 3, 2]
+            and exc.tolist() == [1, 1, 1, 1, 1, 1, 0, 0] and rid.tolist() == [4, 9] and rd.tolist() == [25, 49])
+
+
+@pytest.mark.parametrize("tie", [0, 1])
+def test_hand_traced_two_cells(tie):
+    orc.set_tie_mode(tie)
+    assert check_hand_trace()
+
+
+# ------------------------------------------------ 4. the kernel-shaped model
+def _random_world(seed, N=400, D=8, P=4, R=8, vmax=256):
+    rng = np.random.default_rng(seed)
+    v = rng.integers(0, vmax, (N, D)).astype(np.uint8)
+    pid = rng.integers(0, P, N).astype(np.uint32)
+    att = rng.integers(0, 100, (N, 2)).astype(np.float32)
+    g = orc.knn_cell_graphs(v, pid, P, R)
+    x = orc.cross_graph(v, pid, P, 2)
+    return v.astype(np.float32), att, pid, g, x
+
+
+_CASES = None
+
+
+def _model_cases():
+    """Random queries on three small worlds (one with heavy distance ties),
+    L = 8, 20, 70, both tie modes, and a per-cell iteration cap of 3 (the end
+    of a cell then finds unexplored entries); model results computed once."""
+    global _CASES
+    if _CASES is not None:
+        return _CASES
+    cases = []
+    for w, (seed, vmax, nq) in enumerate(((0, 256, 10), (1, 256, 10), (2, 16, 14))):
+        vec, att, pid, g, x = _random_world(seed, vmax=vmax)
+        sizes = np.bincount(pid, minlength=4)
+        rng = np.random.default_rng(100 + seed)
+        for qi in range(nq):
+            q = rng.integers(0, vmax, 8).astype(np.float32)
+            lo = rng.integers(0, 50, 2).astype(np.float32)
+            hi = lo + rng.integers(10, 60, 2).astype(np.float32)
+            cells = [int(c) for c in rng.permutation(4)[:rng.integers(1, 5)]]
+            ent = rng.integers(0, sizes[cells[0]], 8).astype(np.uint32)
+            for tie in (0, 1):
+                M = KernelModel(vec, att, pid, 4, g, x, tie=tie)
+                for L, cap in ((8, 10000), (20, 10000), (70, 10000), (20, 3)):
+                    cases.append((w, tie, cap, q, lo, hi, cells, ent, L,
+                                  M.search(q, lo, hi, cells, ent, L, max_iter=cap)))
+    worlds = [_random_world(s, vmax=v) for s, v in ((0, 256), (1, 256), (2, 16))]
+    _CASES = (worlds, cases)
+    return _CASES
+
+
+def check_model(stop_early=False):
+    worlds, cases = _model_cases()
+    idx = [orc.OracleIndex(v, a, p, 4, g, x) for v, a, p, g, x in worlds]
+    bad = 0
+    for w, tie, cap, q, lo, hi, cells, ent, L, m in cases:
+        orc.set_tie_mode(tie)
+        orc.set_max_iter(cap)
+        ids, dist, ctr, ex, _, _, _ = idx[w].trace(q, lo, hi, cells, ent, L)
+        same = (ids.tolist() == m[0] and dist.tolist() == [float(np.float32(d)) for d in m[1]]
+                and int(ctr[0]) == m[2] and int(ctr[1]) == m[3] and ex.tolist() == m[4])
+        bad += not same
+        if bad and stop_early:
+            break
+    orc.set_tie_mode(0)
+    orc.set_max_iter(0)
+    return bad == 0, bad, len(cases)
+
+
+def test_oracle_agrees_with_kernel_model():
+    ok, bad, n = check_model()
+    assert ok, f"{bad} of {n} cases differ"
+
+
+# ---------------------------------------------------------- 5. mutations
+CHECKS = {"networks": check_networks, "merges": check_merges, "closed form": check_closed_form,
+          "hand trace": check_hand_trace, "model": lambda: check_model(True)[0]}
+
+
+def _failing_checks(m):
+    orc.set_mutation(m)
+    failed = []
+    try:
+        for name, fn in CHECKS.items():
+            if not fn():
+                failed.append(name)
+    finally:
+        orc.set_mutation(0)
+    return failed
+
+
+@pytest.mark.parametrize("m", sorted(orc.MUTATIONS))
+def test_planted_mistake_is_caught(m):
+    failed = _failing_checks(m)
+    assert failed, f"mutation {m} ({orc.MUTATIONS[m]}) passes every check"
+
+
+@pytest.mark.parametrize("m", [3, 6])
+def test_slot_order_is_invisible_under_a_total_order(m):
+    """The order in which the 128 cross slots are filled (slot i following
+    candidate i / 2 instead of i % 64) and the order of a candidate's E = 2
+    cross edges change no result when equal distances are ordered by
+    cell-major position.  Each candidate owns two slots and each slot takes
+    the first of its candidate's edges not yet taken, else the smallest free
+    local id; so every candidate's two edge targets end up taken (by it or
+    earlier), and the fallbacks take the smallest ids outside them: the set of
+    points in the slots, which are then sorted, does not depend on the order.
+    The same argument shows that the reference's concurrent fill
+    (gpu_graph.cu:3569-3590) puts one set of points in the slots, which is why
+    the HIP kernel may fill them in slot order.  Under the reference's own tie
+    order the slot positions decide the network order of equal distances, so
+    there the two mutations are visible (test_planted_mistake_is_caught).
+    Checked here: identical results with and without the mutation in tie mode 0."""
+    worlds, cases = _model_cases()
+    idx = [orc.OracleIndex(v, a, p, 4, g, x) for v, a, p, g, x in worlds]
+    for w, tie, cap, q, lo, hi, cells, ent, L, _ in cases:
+        if tie != 0:
+            continue
+        orc.set_tie_mode(tie)
+        orc.set_max_iter(cap)
+        base = idx[w].trace(q, lo, hi, cells, ent, L)
+        orc.set_mutation(m)
+        mut = idx[w].trace(q, lo, hi, cells, ent, L)
+        orc.set_mutation(0)
+        for x, y in zip(base, mut):
+            assert np.array_equal(x, y)
+    orc.set_max_iter(0)
+    orc.set_mutation(m)
+    assert check_hand_trace()
+
+
+# ------------------------------------------- the reference's tie order, at scale
+@pytest.mark.parametrize("vmax,floor", [(256, 0.99), (4, 0.0)])
+def test_tie_order_agreement_report(vmax, floor, capsys):
+    """How often the kernels' tie rule (distance, cell-major position) changes
+    a query's ids against the reference's own tie order (tie mode 1), on a
+    config-1-shaped world (6000 x 128, 4x4 cells, R = 16, 256 queries at 30 %
+    selectivity) with integers 0..vmax-1.  On 0..255 data distinct points
+    almost never tie and the ids agree; on 0..3 data ties are everywhere and
+    the fraction is reported."""
+    from garfield_amd import synth
+    cfg = synth.config_small(N=6000, Q=256, R=16, C=24, sel=0.3, seed=7)
+    vec = (cfg["vectors"] % vmax).astype(np.float32)
+    q = (cfg["queries"] % vmax).astype(np.float32)
+    ix = synth.build_index(vec, cfg["attrs"], cfg["grid"], 16, 2, 24, seed=3)
+    l_q, r_q = synth.quantile_arrays(ix)
+    lo, hi = cfg["lo"].astype(np.float32), cfg["hi"].astype(np.float32)
+    cells, cnt = orc.cells(lo, hi, ix["grid"], l_q, r_q, synth.cell_sizes(ix))
+    O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"], ix["cross"])
+    ent = orc.entry_points(6000, ix["P"], 16)
+    z = np.zeros_like(cnt)
+    lines = []
+    for L in (16, 64, 256):
+        orc.set_tie_mode(0)
+        a, _, _ = O.search(q, lo, hi, cells, cnt, z, ent, L)
+        orc.set_tie_mode(1)
+        b, _, _ = O.search(q, lo, hi, cells, cnt, z, ent, L)
+        orc.set_tie_mode(0)
+        same = float(np.mean(np.all(a == b, axis=1)))
+        overlap = float(np.mean([len(set(x.tolist()) & set(y.tolist())) / len(set(x.tolist()))
+                                 for x, y in zip(a, b)]))
+        lines.append(f"vmax={vmax} L={L}: identical ids {same:.3f} of queries, id overlap {overlap:.4f}")
+        assert same >= floor
+    with capsys.disabled():
+        print("\n" + "\n".join(lines))
+
+
+def test_cell_sort_reference_network():
+    """sort_by_clustering_info_weighted's network (bitonic_sort_id_by_num_int,
+    gpu_graph.cu:123-141) on scores [1, 1, 2, 2] of cells [0, 1, 2, 3]: stride
+    2 / step 2 swaps positions (1, 2) then (0, 3), giving [3, 2, 1, 0]; tie
+    mode 0 orders equal scores by cell id: [2, 3, 0, 1]."""
+    hist = np.array([[1], [1], [2], [2]], np.uint32)
+    cells = np.array([[0, 1, 2, 3]], np.uint32)
+    topk = np.zeros((1, 1), np.uint32)
+    cnt = np.array([4], np.uint32)
+    assert orc.sort_cells(cells, cnt, topk, hist)[0].tolist() == [2, 3, 0, 1]
+    orc.set_tie_mode(1)
+    assert orc.sort_cells(cells, cnt, topk, hist)[0].tolist() == [3, 2, 1, 0]
+    # random scores with ties: a permutation, descending, and equal to the
+    # network replayed from the reference's loops
+    rng = np.random.default_rng(12)
+    for n in (3, 16, 37, 64):
+        hist = rng.integers(0, 4, (64, 1)).astype(np.uint32)
+        cl = np.zeros((1, 64), np.uint32)
+        cl[0, :n] = np.sort(rng.choice(64, n, replace=False))
+        out = orc.sort_cells(cl, np.array([n], np.uint32), topk, hist)[0, :n]
+        s = [int(hist[c, 0]) for c in cl[0, :n]]
+        ids = [int(c) for c in cl[0, :n]]
+        stride = 1
+        while stride < n:
+            step = stride
+            while step > 0:
+                for k in range(n // 2):
+                    a, b = 2 * step * (k // step), k % step
+                    u = a + step - 1 - b if step == stride else a + b
+                    d = a + b + step
+                    if d < n and s[u] < s[d]:
+                        s[u], s[d], ids[u], ids[d] = s[d], s[u], ids[d], ids[u]
+                step >>= 1
+            stride <<= 1
+        assert out.tolist() == ids and sorted(out.tolist()) == sorted(cl[0, :n].tolist())
+        assert all(hist[out[i], 0] >= hist[out[i + 1], 0] for i in range(n - 1))
