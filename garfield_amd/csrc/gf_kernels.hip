@@ -2189,29 +2189,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3
                 for (int j = 0; j < 4; ++j)
                     anyd |= max(max(acc[j][0], acc[j][1]), max(acc[j][2], acc[j][3])) >= tp[j];
                 if (!__builtin_amdgcn_ballot_w64(anyd)) continue;
-                bool anyl = !FILTER;   // lane-mask OR: no per-pair ballot
-                if constexpr (FILTER) {
+                // Pair positions (j, i) where some lane is within its bound: a
+                // tile step holds about two such pairs among its 1024, so the
+                // range test and the append run for those positions only.
+                bool full = false;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < 4; ++j)
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) anyl |= pass(j, i);
-                }
-                if (__builtin_amdgcn_ballot_w64(anyl)) {
-                    // Append: the owner adds |q'|^2 to nx - 2 q'.x' later.
-                    bool full = false;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            if (pass(j, i)) {
-                                const uint32_t ql = 16u * j + col;
-                                const int32_t v = cmn[i] - 2 * (acc[j][i] - cmh[i]);
-                                const uint32_t slot = atomicAdd(&cnt[ql], 1u);
-                                buf[ql * kBfBufQ + slot] = (uint64_t(uint32_t(v)) << 32) | uint32_t(cmr[i]);
-                                full |= slot + 1u >= kBfDrainAt;
-                            }
-                    if (__builtin_amdgcn_ballot_w64(full)) drain();
-                }
+                    for (int i = 0; i < 4; ++i) {
+                        const bool dok = acc[j][i] >= tp[j];
+                        if (!__builtin_amdgcn_ballot_w64(dok)) continue;
+                        if (pass(j, i)) {
+                            // Append: the owner adds |q'|^2 to nx - 2 q'.x' later.
+                            const uint32_t ql = 16u * j + col;
+                            const int32_t v = cmn[i] - 2 * (acc[j][i] - cmh[i]);
+                            const uint32_t slot = atomicAdd(&cnt[ql], 1u);
+                            buf[ql * kBfBufQ + slot] = (uint64_t(uint32_t(v)) << 32) | uint32_t(cmr[i]);
+                            full |= slot + 1u >= kBfDrainAt;
+                        }
+                    }
+                if (__builtin_amdgcn_ballot_w64(full)) drain();
             }
         };
         if (it.inside) tiles(std::false_type{});
