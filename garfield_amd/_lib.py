@@ -70,7 +70,8 @@ class SearchStats(C.Structure):
                 ("n_pass", C.c_uint64), ("bytes_traverse", C.c_double), ("bytes_bruteforce", C.c_double),
                 ("ops_bruteforce", C.c_double), ("bf_mfma", C.c_uint32), ("ms_bf_kernel", C.c_double),
                 ("n_batches", C.c_uint32), ("bytes_h2d", C.c_double), ("ms_h2d", C.c_double),
-                ("ms_stage_a", C.c_double), ("ms_stage_b", C.c_double), ("graph", C.c_uint32)]
+                ("ms_stage_a", C.c_double), ("ms_stage_b", C.c_double), ("graph", C.c_uint32),
+                ("q_fullgraph", C.c_uint32)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}

@@ -274,6 +274,31 @@ void entry_points_draw(uint32_t range, uint32_t ndraw, uint32_t R, uint32_t* out
     for (uint32_t j = 0; j < R; ++j) out[j] = j < want ? v[j] : j;
 }
 
+void entry_points_pair(uint32_t range1, uint32_t R, uint32_t range2, uint32_t BD, uint32_t* out1, uint32_t* out2) {
+    GF_REQUIRE(range1 >= 1 && range2 >= 1, GF_E_ARG, "no room for entry points");
+    std::mt19937 rng;
+    auto draw = [&](uint32_t range, uint32_t ndraw, std::vector<unsigned>& v) {
+        std::uniform_int_distribution<> intd(0, int(range) - 1);
+        const uint32_t want = std::min<uint32_t>(ndraw, range);
+        v.assign(want, 0);
+        std::unordered_set<unsigned> seen;
+        uint32_t k = 0;
+        while (k < want) {
+            const unsigned t = unsigned(intd(rng));
+            if (!seen.count(t)) { seen.insert(t); v[k++] = t; }
+        }
+    };
+    std::vector<unsigned> v;
+    draw(range1, 10 * R, v);
+    std::srand(1);
+    std::random_shuffle(v.begin(), v.end());
+    for (uint32_t j = 0; j < R; ++j) out1[j] = j < v.size() ? v[j] : j;
+    if (!BD) return;
+    draw(range2, 10 * BD, v);
+    std::random_shuffle(v.begin(), v.end());
+    for (uint32_t j = 0; j < BD; ++j) out2[j] = j < v.size() ? v[j] : j;
+}
+
 }  // namespace gf
 
 namespace {
@@ -343,15 +368,41 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
     std::vector<uint32_t> doff(a);
     for (uint32_t d = 0; d < a; ++d) { doff[d] = gsum; gsum += h.grid_shape[d]; }
     ix.l_q.upload(h.l_q, gsum);
-    // The reference's entry-point draw (gpu_graph.cu:12503-12526), made once
-    // per index; an index with no room for it (N <= (P - 1) * ceil(N / P))
-    // searches with the caller's entry points only.
+    // The full graph (P <= 64: FE = min(E, R, 64 / P) edges into each cell,
+    // at most 64 per row) and the reference's entry-point draws
+    // (gpu_graph.cu:12503-12539), made once per index: R entries for the
+    // traversal and FD distinct point ids below N, mapped to rows, for the
+    // full graph.  An index with no room for the first draw
+    // (N <= (P - 1) * ceil(N / P)) searches with the caller's entry points
+    // only; one with fewer than FD points has no full graph.
+    if (P <= 64 && E > 0 && N >= std::min(std::min(E, R), 64u / P) * P) {
+        ix.FE = std::min(std::min(E, R), 64u / P);
+        ix.FD = ix.FE * P;
+        std::vector<uint32_t> rowcell(N);
+        for (uint32_t c = 0; c < P; ++c)
+            for (uint32_t r = ix.offset_h[c]; r < ix.offset_h[c + 1]; ++r) rowcell[r] = c;
+        DevBuf<uint32_t> drc;
+        drc.upload(rowcell);
+        ix.fgraph.alloc(size_t(N) * ix.FD);
+        GF_HIP(gf::launch_assemble_full(ix.graph.p, ix.cross.p, ix.offset.p, drc.p, N, P, R, E, ix.FE, ix.fgraph.p,
+                                        ix.stream));
+        GF_HIP(hipStreamSynchronize(ix.stream));
+    }
     {
         const uint32_t avg = (N + P - 1) / P;
         if (N > (P - 1) * avg) {
-            std::vector<uint32_t> ent(R);
-            gf::entry_points_draw(N - (P - 1) * avg, R * 10, R, ent.data());
+            std::vector<uint32_t> ent(R), entf(std::max<uint32_t>(ix.FD, 1));
+            gf::entry_points_pair(N - (P - 1) * avg, R, N, ix.FD, ent.data(), entf.data());
             ix.entry_ref.upload(ent);
+            if (ix.FD) {
+                std::vector<uint32_t> rowof(N);
+                for (uint32_t r = 0; r < N; ++r) rowof[gidx[r]] = r;
+                for (auto& e : entf) e = rowof[e];
+                ix.fentry.upload(entf.data(), ix.FD);
+            }
+        } else {
+            ix.fgraph.release();
+            ix.FE = ix.FD = 0;
         }
     }
     ix.r_q.upload(h.r_q, gsum);
@@ -615,7 +666,7 @@ gf_status gf_batch_create(gf_index* ix, const float* queries, uint32_t Q, const 
         b->counts.alloc(Q);
         b->little.alloc(Q);
         b->selcount.alloc(Q);
-        b->tot.alloc(16);
+        b->tot.alloc(24);
         if (!ix->sub) {
             b->cellq.alloc(size_t(Q) * ix->P);
             b->ccount.alloc(ix->P);
@@ -779,8 +830,9 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         const uint32_t lds = Lpad * 8 + gf::kXSlots * 8 + 128 * 4 + hsize * 4;
         GF_REQUIRE(lds <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
 
-        // device scalars: tot[2] pairs, [3] fits, [4] items, [8..10] traversal /
-        // brute-force / empty counts, [12..13] traversal range, [14..15] brute-force range
+        // device scalars: tot[2] pairs, [3] fits, [4] items, [8..11] traversal /
+        // brute-force / empty / full-graph counts, [12..13] traversal range,
+        // [14..15] brute-force range, [16..17] full-graph range
         uint32_t* tot = b->tot.p;
         gf::TravArgs a{};
         a.vec = ix->vec.p;
@@ -814,6 +866,21 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         a.a = ix->a; a.P = ix->P; a.R = R; a.E = ix->E; a.L = L; a.K = K; a.rl = rl;
         a.hbits = hbits;
         a.Lpad = Lpad;
+        // The full-graph route: its own visited-set size (L + FD list and B
+        // region entries plus four expansions' FD between resets).
+        gf::TravArgs af = a;
+        uint32_t lds_f = 0;
+        if (ix->FD) {
+            const uint32_t hs = std::max<uint32_t>(256, next_pow2(2 * (L + 5 * ix->FD)));
+            af.hbits = 0;
+            while ((1u << af.hbits) < hs) ++af.hbits;
+            lds_f = Lpad * 8 + gf::kXSlots * 8 + 128 * 4 + hs * 4;
+            GF_REQUIRE(lds_f <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
+            af.fgraph = ix->fgraph.p;
+            af.fentry = ix->fentry.p;
+            af.FD = ix->FD;
+            af.frange = tot + 16;
+        }
 
         // Brute-force route on MFMA when vectors and queries are int8-exact:
         // work items of (sub-cell, <= 64 queries whose range reaches it),
@@ -947,7 +1014,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         // pinned staging with one synchronisation.
         const size_t nr = size_t(Q) * K;
         if (b->h_ids.n < nr) { b->h_ids.alloc(nr); b->h_dist.alloc(nr); }
-        if (!b->h_tot.n) { b->h_tot.alloc(16); b->h_stats.alloc(16); }
+        if (!b->h_tot.n) { b->h_tot.alloc(24); b->h_stats.alloc(16); }
         if (stats && b->stats.n < 16) b->stats.alloc(16);
         // Results go straight into the caller's arrays when HIP knows them as
         // page-locked host memory; otherwise through the batch's pinned
@@ -975,7 +1042,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
                 GF_HIP(hipMemcpyAsync(b->h_stats.p, b->stats.p, 16 * sizeof(unsigned long long), hipMemcpyDeviceToHost,
                                       st));
             }
-            GF_HIP(hipMemcpyAsync(b->h_tot.p, tot, 16 * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+            GF_HIP(hipMemcpyAsync(b->h_tot.p, tot, 24 * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
             GF_HIP(hipMemcpyAsync(b->h_stamps.p, b->stamps.p, 8 * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
             GF_HIP(hipMemcpyAsync(ids_dst, b->out_ids.p, nr * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
             if (dists) GF_HIP(hipMemcpyAsync(dist_dst, b->out_dist.p, nr * sizeof(float), hipMemcpyDeviceToHost, st));
@@ -990,12 +1057,16 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             gf::SchedArgs sa{};
             sa.Q = Q; sa.P = ix->P; sa.postfilter = opts->postfilter; sa.counts = b->counts.p; sa.little = b->little.p;
             sa.sched = b->sched.p; sa.tot = tot + 8; sa.ranges = tot + 12;
+            sa.full = ix->FD ? 1u : 0u;
+            sa.franges = ix->FD ? tot + 16 : nullptr;
             GF_HIP(gf::launch_reset_results(Q, K, b->out_ids.p, b->out_dist.p, b->counters.p, st));
             GF_HIP(gf::launch_sched(sa, st));
             GF_HIP(gf::launch_stamp(stamp + 0, st));
             gf::TravArgs at = a;
             at.srange = tot + 12;
             GF_HIP(gf::launch_traverse(ix->rs, at, lds, Q, st));
+            // queries with postfilter or more cells: the full graph
+            if (ix->FD && opts->postfilter <= ix->P) GF_HIP(gf::launch_fullgraph(ix->rs, af, lds_f, Q, st));
             GF_HIP(gf::launch_stamp(stamp + 1, st));
             if (gemm) {
                 launch_gemm();
@@ -1054,6 +1125,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             stats->q_traverse = dt[8];
             stats->q_bruteforce = dt[9];
             stats->q_empty = dt[10];
+            stats->q_fullgraph = ix->FD ? dt[11] : 0u;
             stats->n_expand = sm[0]; stats->n_dist = sm[1]; stats->n_attr = sm[2]; stats->n_cross = sm[3];
             stats->n_lrow = sm[4]; stats->n_scan = sm[5]; stats->n_pass = sm[6];
             // Algorithmic bytes: what each kernel must read from HBM given

@@ -67,6 +67,13 @@ struct TravArgs {
     float* out_dist;          // Q*K
     uint32_t* counters;       // Q*GF_NCOUNTERS
     uint32_t a, P, R, E, L, K, rl, hbits, Lpad;
+    // Full-graph route (queries with postfilter or more cells): the graph
+    // over every point, FD rows per row (cell-major rows, kEmpty = no edge),
+    // its FD entry rows and this launch's query range in sched.
+    const uint32_t* fgraph;
+    const uint32_t* fentry;
+    const uint32_t* frange;
+    uint32_t FD;
 };
 
 // Sub-cells: per cell a rank grid of attribute bins (host build in
@@ -269,10 +276,13 @@ struct BfSeedArgs {
     float* rhi;
 };
 // Query schedule (gpu_graph.cu:12485-12493): traversal queries by descending
-// cell count, then brute-force queries.  tot[0..2] = traversal, brute-force,
-// empty query counts; ranges[0..3] = traversal [begin, end), brute force [begin, end).
+// cell count, then brute-force queries, then full-graph queries.  tot[0..3] =
+// traversal, brute-force, empty, full-graph query counts; ranges[0..3] =
+// traversal [begin, end), brute force [begin, end); ranges[4..5] = full graph.
 struct SchedArgs {
     uint32_t Q, P, postfilter;
+    uint32_t full;            // 1: queries with postfilter or more cells (not all little) take the full graph
+    uint32_t* franges;        // ranges[4..5] (null when full is 0)
     const uint32_t* counts;
     const uint32_t* little;
     uint32_t* sched;
@@ -280,7 +290,7 @@ struct SchedArgs {
     uint32_t* ranges;
 };
 // Sums of the per-query counters and of the brute-force schedule for the
-// search statistics: out[0..6] counter sums, out[7] traversal DIST, out[8]
+// search statistics: out[0..6] counter sums, out[7] traversal and full-graph DIST, out[8]
 // brute-force DIST, out[9] sum of pairs x sub-cell size, out[10] sum of
 // items x tiles per item.
 struct StatsArgs {
@@ -299,6 +309,14 @@ struct StatsArgs {
 // The search launches take a grid of `grid` workgroups (an upper bound of
 // their query range, which is read on the device).
 hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds_bytes, uint32_t grid, hipStream_t st);
+// The full-graph route (fgraph, fentry, frange, FD of a), same LDS layout.
+hipError_t launch_fullgraph(const RowShape& rs, const TravArgs& a, uint32_t lds_bytes, uint32_t grid, hipStream_t st);
+// The full graph: row r, slot c * FE + e holds edge e of row r into cell c as a
+// cell-major row: the per-cell graph's edge e for r's own cell, the cross edge
+// e into c otherwise, kEmpty into an empty cell.
+hipError_t launch_assemble_full(const uint32_t* graph, const uint32_t* cross, const uint32_t* offset,
+                                const uint32_t* rowcell, uint32_t N, uint32_t P, uint32_t R, uint32_t E, uint32_t FE,
+                                uint32_t* out, hipStream_t st);
 hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, uint32_t grid, hipStream_t st);
 hipError_t launch_fill_results(uint32_t* ids, float* dist, uint32_t n, hipStream_t st);
 hipError_t launch_bf_i8(const BfGemmArgs& a, uint32_t ncu, hipStream_t st);   // grid: ncu x resident workgroups per CU

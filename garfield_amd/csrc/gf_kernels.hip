@@ -218,8 +218,12 @@ __device__ __forceinline__ uint32_t eval_lanes(const QReg<VT, CPL>& q, const Tra
 // (as themselves if valid and passing, else the sentinel; quirk of
 // merge_top_with_recycle_list, gpu_graph.cu:224-315); Bp has nb slots and is
 // pre-filled with sentinels.  Returns the first position that received an
-// incoming candidate (L if none).
-__device__ uint32_t merge_into(uint64_t* A, uint32_t L, uint64_t b, uint32_t nb, uint64_t* Bp) {
+// incoming candidate (L if none).  keep_all (merge_top, gpu_graph.cu:162-222,
+// whose B region keeps the n largest of both lists): Bp receives every
+// evicted A entry as itself and every incoming candidate that did not enter
+// A, each at its merged position minus L.
+__device__ uint32_t merge_into(uint64_t* A, uint32_t L, uint64_t b, uint32_t nb, uint64_t* Bp,
+                               bool keep_all = false) {
     const uint32_t lane = lane_id();
     const bool mine = lane < nb;
     const uint64_t kb = ckey(b);
@@ -237,6 +241,16 @@ __device__ uint32_t merge_into(uint64_t* A, uint32_t L, uint64_t b, uint32_t nb,
     }
     if (Bp && mine) Bp[lane] = kCandSent;
     wave_sync();
+    if (keep_all && Bp) {
+        // a rejected candidate sorts after all of A: merged position L + its
+        // stable rank among the incoming candidates
+        uint32_t ra = 0;
+        for (uint32_t k = 0; k < nb; ++k) {
+            const uint64_t kk = ckey(readlane64(b, k));
+            ra += (kk < kb) || (kk == kb && k < lane);
+        }
+        if (mine && r == L) Bp[ra] = b;
+    }
     const uint64_t ins = ballot(mine && r < L);
     if (ins == 0) return L;
     uint32_t rb = 0, rmin = L;
@@ -261,12 +275,13 @@ __device__ uint32_t merge_into(uint64_t* A, uint32_t L, uint64_t b, uint32_t nb,
         wave_sync();
         if (i < L) {
             if (np < L) A[np] = av;
-            else if (Bp) Bp[np - L] = (cvalid(av) && cpass(av)) ? av : kCandSent;
+            else if (Bp) Bp[np - L] = (keep_all || (cvalid(av) && cpass(av))) ? av : kCandSent;
         }
         wave_sync();
     }
     const uint32_t pos = rb + r;
     if (mine && r < L && pos < L) A[pos] = b;
+    else if (keep_all && Bp && mine && r < L) Bp[pos - L] = b;
     wave_sync();
     return rmin;
 }
@@ -585,6 +600,135 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
         ctr[C_PASS] = 0;
         ctr[C_ROUTE] = 1;
     }
+}
+
+// -------------------------------------------------------------- full graph
+// The full-graph post-filter branch (gpu_graph.cu:3644-3787; the reference
+// disables it with `&& false` and sends these queries to a brute force over
+// no cell): a graph search over every point's full-graph row (its own cell's
+// first edges and its cross edges into every other cell, assembled as
+// full_graph_search.cuh:984-997 does), from the FD entry points of the
+// reference's second draw (gpu_graph.cu:12527-12539), with the visited set
+// keyed by point (row), neighbours already in it dropped, and the plain
+// merge_top whose B region (the FD largest of both lists) is re-hashed at
+// every reset; no recycle list.  Then the common post-filter (gpu_graph.cu:
+// 4025-4047): passing entries in order, first K distinct.
+template <int VT, int LPR, int CPL>
+__global__ __launch_bounds__(64) void k_fullgraph(TravArgs p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint64_t* A = reinterpret_cast<uint64_t*>(smem);   // Lpad
+    uint64_t* W = A + p.Lpad;                           // the B region (FD <= 64)
+    uint32_t* S = reinterpret_cast<uint32_t*>(W + kXSlots);  // 128 row list
+    uint32_t* H = S + 128;                              // visited set
+    const uint32_t lane = lane_id();
+    const uint32_t si = p.frange[0] + blockIdx.x;
+    if (si >= p.frange[1]) return;
+    const uint32_t q = p.sched[si];
+    const uint32_t hsize = 1u << p.hbits;
+    const uint32_t L = p.L, FD = p.FD;
+
+    QReg<VT, CPL> qv;
+    load_query<VT, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
+    float lo[kMaxAttr], hi[kMaxAttr];
+#pragma unroll
+    for (uint32_t d = 0; d < kMaxAttr; ++d) {
+        lo[d] = d < p.a ? p.lo[size_t(q) * p.a + d] : 0.0f;
+        hi[d] = d < p.a ? p.hi[size_t(q) * p.a + d] : 0.0f;
+    }
+    for (uint32_t i = lane; i < L; i += 64u) A[i] = kCandSent;
+    hash_clear(H, hsize);
+    uint32_t n_expand = 0, n_dist = 0, n_attr = 0;
+    {
+        const bool mine = lane < FD;
+        const uint32_t row = mine ? p.fentry[lane] : 0u;
+        bool pass = false;
+        if (mine) {
+            hash_insert(H, p.hbits, row);
+            pass = row_pass(p.attrs, p.a, row, lo, hi);
+        }
+        wave_sync();
+        float d;
+        n_dist += eval_lanes<VT, LPR, CPL>(qv, p, S, row, mine, d);
+        n_attr += FD;
+        merge_into(A, L, mine ? make_cand(d, row, pass) : kCandSent, FD, W, true);
+    }
+    uint32_t scan = 0;
+    for (uint32_t it = 0; it < kMaxIter; ++it) {
+        if ((it + 1) % kHashReset == 0) {           // gpu_graph.cu:3690-3702
+            hash_clear(H, hsize);
+            for (uint32_t i = lane; i < L + FD; i += 64u) {
+                const uint64_t c = i < L ? A[i] : W[i - L];
+                if (cvalid(c)) hash_insert(H, p.hbits, crow(c));
+            }
+            wave_sync();
+        }
+        const uint32_t sel = first_unexplored(A, L, scan);
+        if (sel == L) break;
+        const uint64_t sc = A[sel];
+        wave_sync();
+        if (lane == 0) A[sel] = sc | 2u;
+        wave_sync();
+        ++n_expand;
+        scan = sel + 1;
+        const bool mine = lane < FD;
+        uint32_t nrow = kEmpty;
+        bool isnew = false, pass = false;
+        if (mine) {
+            nrow = p.fgraph[size_t(crow(sc)) * FD + lane];
+            isnew = nrow != kEmpty && hash_insert(H, p.hbits, nrow);
+            if (isnew) pass = row_pass(p.attrs, p.a, nrow, lo, hi);
+        }
+        n_attr += __popcll(ballot(isnew));
+        float d;
+        n_dist += eval_lanes<VT, LPR, CPL>(qv, p, S, nrow, isnew, d);
+        const uint32_t ip = merge_into(A, L, isnew ? make_cand(d, nrow, pass) : kCandSent, FD, W, true);
+        scan = ip < scan ? ip : scan;
+    }
+    // Post-filter (gpu_graph.cu:4025-4041): the passing entries, in order.
+    uint32_t wpos = 0;
+    for (uint32_t base = 0; base < L; base += 64u) {
+        const uint32_t i = base + lane;
+        wave_sync();
+        const uint64_t c = i < L ? A[i] : kCandSent;
+        const bool keep = i < L && cvalid(c) && cpass(c);
+        const uint64_t m = ballot(keep);
+        wave_sync();
+        if (keep) A[wpos + lanes_below(m)] = c;
+        wpos += __popcll(m);
+    }
+    wave_sync();
+    const uint32_t n = wpos < p.K ? wpos : p.K;     // rows of A are distinct
+    for (uint32_t j = lane; j < p.K; j += 64u) {
+        const uint64_t c = j < n ? A[j] : kCandSent;
+        p.out_ids[size_t(q) * p.K + j] = j < n ? p.gidx[crow(c)] : GF_NO_RESULT;
+        p.out_dist[size_t(q) * p.K + j] = j < n ? cdist(c) : __int_as_float(0x7F800000);
+    }
+    if (lane == 0) {
+        uint32_t* ctr = p.counters + size_t(q) * GF_NCOUNTERS;
+        ctr[C_EXPAND] = n_expand;
+        ctr[C_DIST] = n_dist;
+        ctr[C_ATTR] = n_attr;
+        ctr[C_CROSS] = 0;
+        ctr[C_LROW] = 0;
+        ctr[C_SCAN] = 0;
+        ctr[C_PASS] = 0;
+        ctr[C_ROUTE] = 3;
+    }
+}
+
+__global__ void k_assemble_full(const uint32_t* graph, const uint32_t* cross, const uint32_t* offset,
+                                const uint32_t* rowcell, uint32_t N, uint32_t P, uint32_t R, uint32_t E, uint32_t FE,
+                                uint32_t* out) {
+    const uint32_t FD = FE * P;
+    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= size_t(N) * FD) return;
+    const uint32_t r = uint32_t(i / FD), slot = uint32_t(i % FD), c = slot / FE, e = slot % FE;
+    const uint32_t own = rowcell[r], sz = offset[c + 1] - offset[c];
+    uint32_t v = kEmpty;
+    // local ids reduced modulo the cell size, the in-bounds rule of the
+    // traversal's cross-edge reads
+    if (sz) v = offset[c] + (c == own ? graph[size_t(r) * R + e] : cross[(size_t(r) * P + c) * E + e]) % sz;
+    out[i] = v;
 }
 
 // ----------------------------------------------------------- brute force
@@ -1862,26 +2006,35 @@ __global__ __launch_bounds__(1024) void k_sched(SchedArgs p) {
     for (uint32_t i = tid; i < nb; i += blockDim.x) bins[i] = 0;
     if (tid == 0) { nbf = 0; nempty = 0; bffill = 0; }
     __syncthreads();
+    // gpu_graph.cu:3377, 3644: traversal, the full graph (the reference's
+    // branch is disabled by `&& false`; here it runs when the index has a
+    // full graph), or the brute force over the first little cells
     auto route = [&](uint32_t q) -> uint32_t {
         const uint32_t c = p.counts[q], l = p.little[q];
         if (c < p.postfilter && c != l) return 1u;
+        if (p.full && c != l) return 3u;
         return l > 0 ? 2u : 0u;
     };
+    __shared__ uint32_t nfull, ffill;
+    if (tid == 0) { nfull = 0; ffill = 0; }
+    __syncthreads();
     for (uint32_t q = tid; q < p.Q; q += blockDim.x) {
         const uint32_t r = route(q);
         if (r == 1) atomicAdd(&bins[min(p.counts[q], p.P)], 1u);
         else if (r == 2) atomicAdd(&nbf, 1u);
+        else if (r == 3) atomicAdd(&nfull, 1u);
         else atomicAdd(&nempty, 1u);
     }
     __syncthreads();
     if (tid == 0) {
         uint32_t acc = 0;
         for (uint32_t i = nb; i-- > 0;) { off[i] = acc; acc += bins[i]; bins[i] = 0; }
-        p.tot[0] = acc; p.tot[1] = nbf; p.tot[2] = nempty;
+        p.tot[0] = acc; p.tot[1] = nbf; p.tot[2] = nempty; p.tot[3] = nfull;
         p.ranges[0] = 0; p.ranges[1] = acc; p.ranges[2] = acc; p.ranges[3] = acc + nbf;
+        if (p.franges) { p.franges[0] = acc + nbf; p.franges[1] = acc + nbf + nfull; }
     }
     __syncthreads();
-    const uint32_t ntrav = p.ranges[1];
+    const uint32_t ntrav = p.ranges[1], nfirstf = ntrav + nbf;
     for (uint32_t q = tid; q < p.Q; q += blockDim.x) {
         const uint32_t r = route(q);
         if (r == 1) {
@@ -1889,6 +2042,8 @@ __global__ __launch_bounds__(1024) void k_sched(SchedArgs p) {
             p.sched[off[c] + atomicAdd(&bins[c], 1u)] = q;
         } else if (r == 2) {
             p.sched[ntrav + atomicAdd(&bffill, 1u)] = q;
+        } else if (r == 3) {
+            p.sched[nfirstf + atomicAdd(&ffill, 1u)] = q;
         }
     }
 }
@@ -1905,7 +2060,7 @@ __global__ __launch_bounds__(256) void k_stats(StatsArgs p) {
 #pragma unroll
         for (int k = 0; k < 7; ++k)
             if (c[map[k]]) atomicAdd(&acc[k], (unsigned long long)c[map[k]]);
-        if (c[C_ROUTE] == 1) atomicAdd(&acc[7], (unsigned long long)c[C_DIST]);
+        if (c[C_ROUTE] == 1 || c[C_ROUTE] == 3) atomicAdd(&acc[7], (unsigned long long)c[C_DIST]);
         if (c[C_ROUTE] == 2) atomicAdd(&acc[8], (unsigned long long)c[C_DIST]);
     }
     if (p.bcnt && i < p.NS) {
@@ -2708,6 +2863,12 @@ hipError_t launch_trav_t(const TravArgs& a, uint32_t lds, uint32_t grid, hipStre
     return hipGetLastError();
 }
 template <int VT, int LPR, int CPL>
+hipError_t launch_full_t(const TravArgs& a, uint32_t lds, uint32_t grid, hipStream_t st) {
+    if (grid == 0) return hipSuccess;
+    hipLaunchKernelGGL((k_fullgraph<VT, LPR, CPL>), dim3(grid), dim3(64), lds, st, a);
+    return hipGetLastError();
+}
+template <int VT, int LPR, int CPL>
 hipError_t launch_bf_t(const TravArgs& a, uint32_t grid, hipStream_t st) {
     if (grid == 0) return hipSuccess;
     hipLaunchKernelGGL((k_bruteforce<VT, LPR, CPL>), dim3(grid), dim3(64), 0, st, a);
@@ -2753,6 +2914,25 @@ hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds, 
     GF_DISPATCH(CALL_T);
 #undef CALL_T
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_fullgraph(const RowShape& rs, const TravArgs& a, uint32_t lds, uint32_t grid, hipStream_t st) {
+    if (a.FD < 1 || a.FD > 64) return hipErrorInvalidValue;
+#define CALL_F(V, L_, C_) launch_full_t<V, L_, C_>(a, lds, grid, st)
+    GF_DISPATCH(CALL_F);
+#undef CALL_F
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_assemble_full(const uint32_t* graph, const uint32_t* cross, const uint32_t* offset,
+                                const uint32_t* rowcell, uint32_t N, uint32_t P, uint32_t R, uint32_t E, uint32_t FE,
+                                uint32_t* out, hipStream_t st) {
+    const size_t n = size_t(N) * FE * P;
+    if (!n) return hipSuccess;
+    if (FE > R || FE > E) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_assemble_full, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, st, graph, cross, offset,
+                       rowcell, N, P, R, E, FE, out);
+    return hipGetLastError();
 }
 
 hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, uint32_t grid, hipStream_t st) {

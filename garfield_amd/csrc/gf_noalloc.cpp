@@ -117,7 +117,7 @@ extern "C" gf_status gf_search_noalloc(gf_index* ix, const float* queries, uint3
                 s.cfill = c.take<uint32_t>(P);
             }
             s.sched = c.take<uint32_t>(Q);
-            s.tot = c.take<uint32_t>(16);
+            s.tot = c.take<uint32_t>(24);
             s.entry = c.take<uint32_t>(R);
             s.out_ids = c.take<uint32_t>(size_t(Q) * K);
             s.out_dist = c.take<float>(size_t(Q) * K);
@@ -214,11 +214,26 @@ extern "C" gf_status gf_search_noalloc(gf_index* ix, const float* queries, uint3
         gf::SchedArgs sa{};
         sa.Q = Q; sa.P = P; sa.postfilter = so.postfilter; sa.counts = s.counts; sa.little = s.little;
         sa.sched = s.sched; sa.tot = s.tot + 8; sa.ranges = s.tot + 12;
+        sa.full = ix->FD ? 1u : 0u;
+        sa.franges = ix->FD ? s.tot + 16 : nullptr;
         GF_HIP(gf::launch_reset_results(Q, K, s.out_ids, s.out_dist, s.counters, st));
         GF_HIP(gf::launch_sched(sa, st));
         gf::TravArgs tt = t;
         tt.srange = s.tot + 12;
         GF_HIP(gf::launch_traverse(ix->rs, tt, lds, Q, st));
+        if (ix->FD && so.postfilter <= P) {
+            gf::TravArgs tf = t;
+            const uint32_t hs = std::max<uint32_t>(256, next_pow2(2 * (L + 5 * ix->FD)));
+            tf.hbits = 0;
+            while ((1u << tf.hbits) < hs) ++tf.hbits;
+            const uint32_t lds_f = Lpad * 8 + gf::kXSlots * 8 + 128 * 4 + hs * 4;
+            GF_REQUIRE(lds_f <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
+            tf.fgraph = ix->fgraph.p;
+            tf.fentry = ix->fentry.p;
+            tf.FD = ix->FD;
+            tf.frange = s.tot + 16;
+            GF_HIP(gf::launch_fullgraph(ix->rs, tf, lds_f, Q, st));
+        }
         gf::TravArgs tb = t;
         tb.srange = s.tot + 14;
         GF_HIP(gf::launch_bruteforce(ix->rs, tb, Q, st));

@@ -161,6 +161,10 @@ struct gf_index {
     DevBuf<float> attrs, l_q, r_q, cnorm;
     DevBuf<uint32_t> graph, cross, offset, gidx, lrow, grid, doff, hist;
     DevBuf<uint32_t> entry_ref;   // the reference's entry-point draw (resident index: made when it is built)
+    // Full-graph route (P <= 64): every row's FE edges into each cell (FD =
+    // FE * P rows per row) and the FD entry rows of the reference's second draw.
+    uint32_t FE = 0, FD = 0;
+    DevBuf<uint32_t> fgraph, fentry;
     DevBuf<uint32_t> tile_cell, tile_row0, tile_n;
     DevBuf<uint16_t> centres;
     uint32_t ntiles = 0;
@@ -378,6 +382,11 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
 // Entry-point draws (mt19937 default seed, distinct uniform_int_distribution
 // draws in [0, range), std::random_shuffle after srand(1)): the first R.
 void entry_points_draw(uint32_t range, uint32_t ndraw, uint32_t R, uint32_t* out);
+// The resident search's two draws in one generator sequence
+// (gpu_graph.cu:12503-12539): 10 R distinct values below range1, shuffled,
+// the first R; then, continuing the same mt19937 and rand() streams, 10 BD
+// distinct values below range2, shuffled, the first BD (for the full graph).
+void entry_points_pair(uint32_t range1, uint32_t R, uint32_t range2, uint32_t BD, uint32_t* out1, uint32_t* out2);
 // Index builder (gf_build.cpp): the rank-quantile grid and the exact graphs.
 void grid_scatter(const float* attrs, uint32_t N, uint32_t a, const uint32_t* grid, float* l_q, float* r_q,
                   uint32_t* pid_lists, uint32_t* global_pid);

@@ -164,7 +164,11 @@ typedef struct {
     uint32_t L;            /* candidate list length (the reference's ef / TOPM) */
     uint32_t K;            /* results per query (reference: 10) */
     uint32_t rl;           /* recycle list length (reference: 10), <= 16 */
-    uint32_t postfilter;   /* --postfilter: queries with >= this many cells skip traversal */
+    uint32_t postfilter;   /* --postfilter: queries with >= this many cells (not all
+                              little) skip the cell-by-cell traversal; on a resident
+                              index of at most 64 cells they search its full graph
+                              (the branch gpu_graph.cu:3644-3787, which the reference
+                              disables with `&& false`), else they get no result */
     const uint32_t* entry_points;  /* R cell-local entry ids, or NULL for the
                                       reference's mt19937 draw (gpu_graph.cu:12503-12526;
                                       streamed: big_dataset_adapterV3.cuh:3862-3875) */
@@ -193,6 +197,10 @@ typedef struct {
     /* 1 if the search stage ran as a replayed HIP graph (a resident index's
        second and later searches of a batch with the same buffers and options) */
     uint32_t graph;
+    /* queries on the full-graph route (postfilter or more cells, not all
+       little; a resident index of at most 64 cells); their device time is in
+       ms_traverse */
+    uint32_t q_fullgraph;
 } gf_search_stats;
 
 gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids /*Q*K*/,

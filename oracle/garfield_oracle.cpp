@@ -223,6 +223,9 @@ enum {
     MUT_RECYCLE_ENTRY_FIRST = 11, // recycle merge ties put the recycle entry before the evictee
     MUT_SLOT_32 = 12,             // cross slot i follows candidate i % 32 (only the first 32 feed the slots)
     MUT_CROSS_OWN_CELL = 13,      // cross edges read for the current cell instead of the next
+    MUT_FULL_NO_B_REHASH = 14,    // full graph: the reset re-inserts the list only, not the B region
+    MUT_FULL_ENTRY_UNSEEN = 15,   // full graph: entry points are not put in the visited set
+    MUT_FULL_OWN_AS_CROSS = 16,   // full graph assembly: own-cell edges read from the cross edges
 };
 // Per-cell iteration cap (gpu_graph.cu:39 MAX_ITER); tests lower it to reach
 // the end-of-cell step with unexplored entries left.
@@ -339,6 +342,7 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
     const uint32_t* cl = cells + (size_t)qi * P;
     const uint32_t cnt = counts[qi], lit = little[qi];
     const bool traverse = (cnt < postfilter && cnt != lit);   // gpu_graph.cu:3377
+    const bool full = !traverse && ix->FD && cnt != lit;      // gpu_graph.cu:3644
     std::vector<Cand> out;
 
     auto cell_size = [&](uint32_t cc) { return ix->offset[cc + 1] - ix->offset[cc]; };
@@ -465,6 +469,57 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
         sort_cands(c, A.data(), L, 1);
         if (tr) tr->recycle = Rc;
         if (Rc[0].id != SENT) merge_plain(c, A.data(), L, Rc.data(), rl);
+        out = A;
+    } else if (full) {
+        // The full-graph branch (gpu_graph.cu:3644-3787, disabled in the
+        // reference by `&& false`): a graph search over the full graph from
+        // its FD entry points, visited set keyed by point id, neighbours seen
+        // before dropped, plain merge_top; every fourth iteration the visited
+        // set is rebuilt from the list and the B region.  Then the common
+        // post-filter (gpu_graph.cu:4025-4041); the recycle list is empty.
+        s.ctr[ORC_C_ROUTE] = 3;
+        const uint32_t FD = ix->FD;
+        std::vector<Cand> A(L, Cand{INF, SENT}), B(FD, Cand{INF, SENT});
+        std::unordered_set<uint32_t> H;
+        for (uint32_t j = 0; j < FD; ++j) {                  // gpu_graph.cu:3646-3683
+            const uint32_t g = ix->fentry[j];
+            if (g_mutation != MUT_FULL_ENTRY_UNSEEN) H.insert(g);
+            B[j] = {point_dist(s, g), g};
+            s.ctr[ORC_C_DIST]++; s.ctr[ORC_C_ATTR]++;
+        }
+        sort_cands(c, B.data(), FD, 1);
+        merge_plain(c, A.data(), L, B.data(), FD);
+        for (uint32_t it = 0; it < g_max_iter; ++it) {
+            if ((it + 1) % reset_every == 0) {            // gpu_graph.cu:3688-3702
+                H.clear();
+                for (const auto* arr : {&A, &B}) {
+                    if (arr == &B && g_mutation == MUT_FULL_NO_B_REHASH) continue;
+                    for (const Cand& x : *arr)
+                        if (x.id != SENT) H.insert(x.id & IDM);
+                }
+            }
+            uint32_t sel = L;                            // gpu_graph.cu:3704-3732
+            for (uint32_t j = 0; j < L; ++j)
+                if ((A[j].id & EXPL) == 0) { sel = j; break; }
+            if (sel == L) break;
+            A[sel].id |= EXPL;
+            s.ctr[ORC_C_EXPAND]++;
+            if (tr) { tr->expanded.push_back(A[sel].id & IDM); tr->expanded_cell.push_back(P); }
+            const uint32_t g = A[sel].id & IDM;
+            for (uint32_t j = 0; j < FD; ++j) {           // gpu_graph.cu:3741-3775
+                const uint32_t nb = ix->fgraph[(size_t)g * FD + j];
+                B[j] = {INF, SENT};
+                if (nb == SENT || !H.insert(nb).second) continue;
+                B[j] = {point_dist(s, nb), nb};
+                s.ctr[ORC_C_DIST]++; s.ctr[ORC_C_ATTR]++;
+            }
+            sort_cands(c, B.data(), FD, 1);
+            merge_plain(c, A.data(), L, B.data(), FD);
+        }
+        if (g_mutation != MUT_NO_POSTFILTER)
+            for (Cand& x : A)
+                if (x.id != SENT && !passes(s, x.id & IDM)) x = {INF, SENT};
+        sort_cands(c, A.data(), L, 1);
         out = A;
     } else {
         // Filtered brute force over the first `little` cells (gpu_graph.cu:3788-4022).
@@ -821,6 +876,53 @@ void orc_entry_points(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
     orc_entry_draw(N - (P - 1) * avg, R * 10, R, out);
 }
 
+void orc_entry_points_pair(uint32_t N, uint32_t P, uint32_t R, uint32_t FD, uint32_t* out, uint32_t* outf) {
+    // One mt19937 for both draws; random_shuffle's std::rand seeded once
+    // (gpu_graph.cu:12506-12537).
+    const uint32_t avg = (N + P - 1) / P;
+    std::mt19937 rng;
+    auto draw = [&](uint32_t range, uint32_t want, std::vector<unsigned>& v) {
+        std::uniform_int_distribution<> intd(0, (int)range - 1);
+        want = std::min(want, range);
+        v.assign(want, 0);
+        std::unordered_set<unsigned> seen;
+        for (uint32_t k = 0; k < want;) {
+            const unsigned t = (unsigned)intd(rng);
+            if (seen.insert(t).second) v[k++] = t;
+        }
+    };
+    std::vector<unsigned> v;
+    draw(N - (P - 1) * avg, 10 * R, v);
+    std::srand(1);
+    std::random_shuffle(v.begin(), v.end());
+    for (uint32_t j = 0; j < R; ++j) out[j] = j < v.size() ? v[j] : j;
+    if (!FD) return;
+    draw(N, 10 * FD, v);
+    std::random_shuffle(v.begin(), v.end());
+    for (uint32_t j = 0; j < FD; ++j) outf[j] = j < v.size() ? v[j] : j;
+}
+
+void orc_full_graph(const orc_index* ix, uint32_t FE, uint32_t* out) {
+    const uint32_t N = ix->N, P = ix->P, R = ix->R, E = ix->E, FD = FE * P;
+    std::vector<uint32_t> cellof(N);
+    for (uint32_t c = 0; c < P; ++c)
+        for (uint32_t r = ix->offset[c]; r < ix->offset[c + 1]; ++r) cellof[ix->global_idx[r]] = c;
+    for (uint32_t g = 0; g < N; ++g)
+        for (uint32_t c = 0; c < P; ++c) {
+            const uint32_t sz = ix->offset[c + 1] - ix->offset[c];
+            for (uint32_t e = 0; e < FE; ++e) {
+                uint32_t v = SENT;
+                if (sz) {
+                    const uint32_t l = c == cellof[g] && g_mutation != MUT_FULL_OWN_AS_CROSS
+                        ? ix->graph[(size_t)(ix->offset[c] + ix->local_idx[g]) * R + e]
+                        : ix->cross[(size_t)g * P * E + (size_t)c * E + e];
+                    v = ix->global_idx[ix->offset[c] + l % sz];
+                }
+                out[(size_t)g * FD + (size_t)c * FE + e] = v;
+            }
+        }
+}
+
 float orc_distance(const orc_index* ix, const void* q, uint32_t gid) {
     std::vector<float> qv(ix->D), xv(ix->D);
     if (ix->vdtype != 1)
@@ -863,7 +965,7 @@ uint32_t orc_search_trace(const orc_index* ix, const void* queries, uint32_t qi,
                           const uint32_t* cells, const uint32_t* counts, const uint32_t* entry, uint32_t L,
                           uint32_t K, uint32_t rl, uint32_t* out_ids, float* out_dist, uint32_t* counters,
                           uint32_t* expanded, uint32_t* expanded_cell, uint32_t cap, uint32_t* rec_ids,
-                          float* rec_dist) {
+                          float* rec_dist, uint32_t postfilter) {
     std::vector<uint32_t> cmpos(ix->N), cellof(ix->N);
     for (uint32_t c = 0; c < ix->P; ++c)
         for (uint32_t r = ix->offset[c]; r < ix->offset[c + 1]; ++r) {
@@ -875,7 +977,7 @@ uint32_t orc_search_trace(const orc_index* ix, const void* queries, uint32_t qi,
     std::vector<uint32_t> little(qi + 1, 0);
     std::vector<uint32_t> ids((size_t)(qi + 1) * K), ctr((size_t)(qi + 1) * ORC_NCNT);
     std::vector<float> dist((size_t)(qi + 1) * K);
-    search_one(c, queries, qi, lo, hi, cells, counts, little.data(), entry, L, K, rl, 1u << 30, ids.data(),
+    search_one(c, queries, qi, lo, hi, cells, counts, little.data(), entry, L, K, rl, postfilter, ids.data(),
                dist.data(), ctr.data(), &tr);
     std::memcpy(out_ids, &ids[(size_t)qi * K], K * sizeof(uint32_t));
     std::memcpy(out_dist, &dist[(size_t)qi * K], K * sizeof(float));

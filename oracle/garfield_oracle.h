@@ -42,7 +42,22 @@ typedef struct {
     const uint32_t* global_idx;   /* N: offset[c]+local -> point id */
     const uint32_t* local_idx;    /* N: point id -> local id in its cell */
     const uint32_t* cross;        /* N*P*E: cell-local ids, point-id order */
+    /* The full graph (FD = 0: none; orc_full_graph), point-id order and
+     * point ids, and its FD entry point ids (orc_entry_points_pair). */
+    uint32_t FD;
+    const uint32_t* fgraph;       /* N*FD */
+    const uint32_t* fentry;       /* FD */
 } orc_index;
+
+/* full_graph_search.cuh:984-997 assemble_edges: row g of the full graph
+ * holds, for every cell c in order, FE edges of g into c -- its own graph's
+ * first FE edges when c is g's cell, else its first FE cross edges into c --
+ * as point ids (local ids reduced modulo |c|; empty cells: 0xFFFFFFFF).
+ * out: N*FE*P, point-id order. */
+void orc_full_graph(const orc_index* ix, uint32_t FE, uint32_t* out);
+/* gpu_graph.cu:12503-12539: the R traversal entries (orc_entry_points) and,
+ * from the same generator, FD distinct full-graph entries drawn from [0, N). */
+void orc_entry_points_pair(uint32_t N, uint32_t P, uint32_t R, uint32_t FD, uint32_t* out, uint32_t* outf);
 
 /* tools.cuh:862-915 get_idx_mapper */
 void orc_idx_mapper(uint32_t N, uint32_t P, const uint32_t* global_pid,
@@ -155,14 +170,16 @@ float orc_hfma2_dist(const uint16_t* q, const uint16_t* x, uint32_t D);
 void orc_set_mutation(int m);
 /* Per-cell iteration cap of the traversal (0 restores the reference's 10000). */
 void orc_set_max_iter(uint32_t n);
-/* One traversal query (route forced to traversal) with its trajectory: the
- * point ids expanded in order and the cell of each expansion (up to cap),
- * and the recycle list before the final merge.  Returns the expansions. */
+/* One query (no little cells; postfilter as in orc_search: 1 << 30 forces
+ * the traversal, 0 the full graph of an index that has one) with its
+ * trajectory: the point ids expanded in order and the cell of each expansion
+ * (P on the full graph; up to cap), and the recycle list before the final
+ * merge.  Returns the expansions. */
 uint32_t orc_search_trace(const orc_index* ix, const void* queries, uint32_t qi, const float* lo, const float* hi,
                           const uint32_t* cells, const uint32_t* counts, const uint32_t* entry, uint32_t L,
                           uint32_t K, uint32_t rl, uint32_t* out_ids, float* out_dist, uint32_t* counters,
                           uint32_t* expanded, uint32_t* expanded_cell, uint32_t cap, uint32_t* rec_ids,
-                          float* rec_dist);
+                          float* rec_dist, uint32_t postfilter);
 /* The oracle's building blocks, for known-answer tests:
  * bitonic_sort_id_by_dis_no_explore (gpu_graph.cu:77-101), warpSort
  * (:144-159), merge_top (:162-222; tie 0 orders equal distances by id) and

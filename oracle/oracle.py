@@ -41,7 +41,8 @@ class _Index(C.Structure):
                 ("R", C.c_uint32), ("E", C.c_uint32), ("vdtype", C.c_int32),
                 ("vec_f32", C.c_void_p), ("vec_f16", C.c_void_p), ("attrs", C.c_void_p),
                 ("graph", C.c_void_p), ("offset", C.c_void_p), ("global_idx", C.c_void_p),
-                ("local_idx", C.c_void_p), ("cross", C.c_void_p)]
+                ("local_idx", C.c_void_p), ("cross", C.c_void_p),
+                ("FD", C.c_uint32), ("fgraph", C.c_void_p), ("fentry", C.c_void_p)]
 
 
 def _p(a):
@@ -168,6 +169,15 @@ def entry_points(N, P, R):
     return out
 
 
+def entry_points_pair(N, P, R, FD):
+    """The R traversal entries and the FD full-graph entries (point ids) of
+    one generator, as the reference draws them (gpu_graph.cu:12503-12539)."""
+    out = np.empty(R, np.uint32)
+    outf = np.empty(max(FD, 1), np.uint32)
+    load().orc_entry_points_pair(C.c_uint32(N), C.c_uint32(P), C.c_uint32(R), C.c_uint32(FD), _p(out), _p(outf))
+    return out, outf[:FD]
+
+
 def entry_draw(range_, ndraw, R):
     out = np.empty(R, np.uint32)
     load().orc_entry_draw(C.c_uint32(range_), C.c_uint32(ndraw), C.c_uint32(R), _p(out))
@@ -177,8 +187,12 @@ def entry_draw(range_, ndraw, R):
 class OracleIndex:
     """The index in the reference's representation (point-id order + idx mapper)."""
 
-    def __init__(self, vectors, attrs, global_pid, P, cell_graphs, cross, vec_f16=None, u8=False):
-        """u8=True: the HIP path's uint8 vector mode (vectors hold the integer values)."""
+    def __init__(self, vectors, attrs, global_pid, P, cell_graphs, cross, vec_f16=None, u8=False, full=True):
+        """u8=True: the HIP path's uint8 vector mode (vectors hold the integer values).
+        full=True: the full graph of the library's resident index (P <= 64
+        cells, FE = min(E, R, 64 // P) edges into each cell, entries from the
+        second draw), used by queries with postfilter or more cells; without
+        it they return no result."""
         self.vectors = _c(vectors, np.float32)
         self.vec_f16 = None if vec_f16 is None else _c(vec_f16, np.uint16)
         self.attrs = _c(attrs, np.float32)
@@ -190,7 +204,21 @@ class OracleIndex:
         self.s = _Index(N, D, self.attrs.shape[1], P, self.graph.shape[1], self.cross.shape[1] // P,
                         (2 if u8 else 0) if self.vec_f16 is None else 1, _p(self.vectors),
                         None if self.vec_f16 is None else _p(self.vec_f16), _p(self.attrs), _p(self.graph),
-                        _p(self.offset), _p(self.gidx), _p(self.lidx), _p(self.cross))
+                        _p(self.offset), _p(self.gidx), _p(self.lidx), _p(self.cross), 0, None, None)
+        R, E = self.graph.shape[1], self.cross.shape[1] // P
+        avg = (N + P - 1) // P
+        if full and P <= 64 and E > 0 and N > (P - 1) * avg and N >= min(E, R, 64 // P) * P:
+            self.FE = min(E, R, 64 // P)
+            self.FD = self.FE * P
+            self.fgraph = np.empty((N, self.FD), np.uint32)
+            load().orc_full_graph(C.byref(self.s), C.c_uint32(self.FE), _p(self.fgraph))
+            _, self.fentry = entry_points_pair(N, P, R, self.FD)
+            self.fentry = _c(self.fentry, np.uint32)
+            self.s.FD = self.FD
+            self.s.fgraph = _p(self.fgraph)
+            self.s.fentry = _p(self.fentry)
+        else:
+            self.FE = self.FD = 0
 
     def search(self, queries, lo, hi, cells_, counts, little, entry, L, K=10, rl=10, postfilter=1 << 30,
                nthreads=0):
@@ -212,8 +240,9 @@ class OracleIndex:
                           C.c_int(nthreads))
         return ids, dist, ctr
 
-    def trace(self, query, lo, hi, cells_, entry, L, K=10, rl=10, cap=100000):
-        """One traversal query over the ordered cells `cells_` with its
+    def trace(self, query, lo, hi, cells_, entry, L, K=10, rl=10, cap=100000, full=False):
+        """One traversal query over the ordered cells `cells_` (full=True: the
+        full-graph search, needs an index with a full graph) with its
         trajectory: (ids, dists, counters, expanded point ids, the cell of each
         expansion, recycle ids, recycle distances)."""
         dt = np.uint16 if self.vec_f16 is not None else np.float32
@@ -233,7 +262,8 @@ class OracleIndex:
         rd = np.empty(rl, np.float32)
         n = load().orc_search_trace(C.byref(self.s), _p(q), C.c_uint32(0), _p(lo), _p(hi), _p(cl), _p(cnt),
                                     _p(entry), C.c_uint32(L), C.c_uint32(K), C.c_uint32(rl), _p(ids), _p(dist),
-                                    _p(ctr), _p(ex), _p(exc), C.c_uint32(cap), _p(rid), _p(rd))
+                                    _p(ctr), _p(ex), _p(exc), C.c_uint32(cap), _p(rid), _p(rd),
+                                    C.c_uint32(0 if full else 1 << 30))
         n = min(int(n), cap)
         return ids, dist, ctr, ex[:n].copy(), exc[:n].copy(), rid, rd
 
@@ -289,6 +319,9 @@ MUTATIONS = {
     11: "recycle merge ties put the recycle entry before the evictee",
     12: "cross slot i follows candidate i % 32 (only the first 32 candidates feed the slots)",
     13: "cross edges read for the current cell instead of the next",
+    14: "full graph: the reset re-inserts the list only, not the B region",
+    15: "full graph: entry points are not put in the visited set",
+    16: "full graph assembly: own-cell edges read from the cross edges",
 }
 
 

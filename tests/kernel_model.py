@@ -330,3 +330,95 @@ class KernelModel:
             ids.append(0x7FFFFFFF)
             dists.append(INF)
         return ids, dists, nexp, ndist, [e & IDM for e in expanded], recycle
+
+    # ------------------------------------------------------- full graph
+    def full_graph(self, FE):
+        """assemble_edges (full_graph_search.cuh:984-997): for point b and
+        every cell pid in order, FE edges -- the own cell's graph row when pid
+        is b's cell, else b's cross edges into pid -- mapped to point ids
+        (local ids reduced modulo the cell size, the oracle's in-bounds rule;
+        an empty cell gives 0xFFFFFFFF)."""
+        N, P = len(self.cell), self.P
+        out = np.full((N, FE * P), SENT, np.uint32)
+        for b in range(N):
+            for i in range(FE * P):
+                pid, eid = i // FE, i % FE
+                sz = self.seg[pid + 1] - self.seg[pid]
+                if sz == 0:
+                    continue
+                if self.cell[b] == pid:
+                    v = int(self.graph[self.seg[pid] + self.lidx[b], eid])
+                else:
+                    v = int(self.cross[b, pid * self.E + eid])
+                out[b, i] = self.gidx[self.seg[pid] + v % sz]
+        return out
+
+    def search_full(self, q, lo, hi, fgraph, fentry, L, K=10, max_iter=MAX_ITER):
+        """The full-graph branch (gpu_graph.cu:3644-3787) and the common
+        post-filter (:4025-4047) for one query; returns (ids, dists,
+        expansions, distance evaluations, expanded point ids)."""
+        BD = fgraph.shape[1]
+        q = np.asarray(q, np.float64)
+        lo = np.asarray(lo, np.float64)
+        hi = np.asarray(hi, np.float64)
+        top = [SENT] * (L + BD)
+        dis = [INF] * (L + BD)
+        nexp = ndist = 0
+        expanded = []
+        H = set()
+        for i in range(BD):
+            top[L + i] = int(fentry[i])
+            H.add(top[L + i])
+        for j in range(BD):
+            dis[L + j] = self._dist(q, top[L + j])
+            ndist += 1
+
+        def sort_and_merge():
+            b_id, b_d = top[L:], dis[L:]
+            self.sort_net(b_id, b_d, BD)
+            a_id, a_d = top[:L], dis[:L]
+            self.merge_top(a_id, a_d, b_id, b_d)
+            top[:L], dis[:L] = a_id, a_d
+            top[L:], dis[L:] = b_id, b_d
+
+        sort_and_merge()
+        for it in range(max_iter):
+            if (it + 1) % HASH_RESET == 0:
+                H = set(t & IDM for t in top if t != SENT)
+            assert len(H) < HASHLEN
+            to_explore = SENT
+            for j in range(L):
+                if (top[j] & EXPL) == 0:
+                    to_explore = top[j]
+                    top[j] |= EXPL
+                    break
+            if to_explore == SENT:
+                break
+            nexp += 1
+            expanded.append(to_explore)
+            for j in range(BD):
+                g = int(fgraph[to_explore, j])
+                if g == SENT or g in H:
+                    top[L + j], dis[L + j] = SENT, INF
+                else:
+                    H.add(g)
+                    top[L + j], dis[L + j] = g, self._dist(q, g)
+                    ndist += 1
+            sort_and_merge()
+        for i in range(L):
+            if top[i] != SENT and not self._passes(top[i] & IDM, lo, hi):
+                top[i], dis[i] = SENT, INF
+        a_id, a_d = top[:L], dis[:L]
+        self.sort_net(a_id, a_d, L)
+        ids, dists = [], []
+        for i, d in zip(a_id, a_d):
+            if len(ids) == K:
+                break
+            if i == SENT or (i & IDM) in ids:
+                continue
+            ids.append(i & IDM)
+            dists.append(d)
+        while len(ids) < K:
+            ids.append(0x7FFFFFFF)
+            dists.append(INF)
+        return ids, dists, nexp, ndist, expanded

@@ -217,12 +217,35 @@ def test_bruteforce_parity(world32, prefilter):
     assert st.q_bruteforce > 0 and st.bf_mfma == 1
 
 
-def test_postfilter_routes_to_empty(small_world):
+@pytest.mark.parametrize("L", [16, 64, 300])
+def test_postfilter_full_graph_parity(small_world, L):
+    """Queries with postfilter or more cells run the full-graph search
+    (FD = 2 x 16 edges per row), bit-exact against the oracle."""
     cfg, ix = small_world
-    _print_case("postfilter")
-    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 32, postfilter=12)
+    _print_case("postfilter-full", L=L)
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, L, postfilter=12)
     _assert_same(ids, dists, ctr, oids, odist, octr, st)
-    assert st.q_empty > 0
+    assert st.q_fullgraph > 0 and st.q_traverse > 0
+    assert st.q_fullgraph == int(np.sum(octr[:, 7] == 3))
+
+
+def test_postfilter_full_graph_r32_fp16(world32):
+    cfg, ix = world32
+    _print_case("postfilter-full-fp16")
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 80, vec_dtype=1, f2h_factor=0.01,
+                                                             postfilter=6)
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+    assert st.q_fullgraph > 0
+
+
+def test_postfilter_full_graph_64_cells(world_gauss):
+    """4 x 4 x 4 cells: one edge into each cell, FD = 64 (a full wave); with
+    postfilter 1 every query that is not all little takes the full graph."""
+    cfg, ix = world_gauss
+    _print_case("postfilter-full-64")
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 128, postfilter=1)
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+    assert st.q_fullgraph > 0
 
 
 def test_recall_against_ground_truth(world32):

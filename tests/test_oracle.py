@@ -354,12 +354,38 @@ def test_traversal_deterministic_across_threads(tiny):
 
 
 def test_postfilter_and_empty_routes(tiny):
+    """Queries with postfilter or more cells: without a full graph no result
+    (the reference's full-graph branch is disabled and its brute force covers
+    no cell); with one, the full-graph search: filtered, ascending, distinct,
+    exact distances, and a recall that grows with L."""
     cfg, ix, lo, hi, cells, cnt, O, gt, gtd = tiny
     ent = orc.entry_points(4000, 16, 16)
     z = np.zeros_like(cnt)
-    ids, dist, ctr = O.search(cfg["queries"], lo, hi, cells, cnt, z, ent, 32, postfilter=int(cnt.min()))
-    routed = cnt >= cnt.min()
+    pf = int(np.median(cnt))
+    O0 = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], 16, ix["cell_graphs"], ix["cross"],
+                         full=False)
+    ids, dist, ctr = O0.search(cfg["queries"], lo, hi, cells, cnt, z, ent, 32, postfilter=pf)
+    routed = cnt >= pf
+    assert routed.any() and (~routed).any()
     assert np.all(ids[routed] == orc.SENTINEL) and np.all(ctr[routed, 7] == 0)
+    assert np.all(ctr[~routed, 7] == 1)
+    assert O.FD == 2 * 16
+    recs = []
+    for L in (16, 64, 256):
+        ids, dist, ctr = O.search(cfg["queries"], lo, hi, cells, cnt, z, ent, L, postfilter=pf)
+        assert np.all(ctr[routed, 7] == 3) and np.all(ctr[~routed, 7] == 1)
+        assert np.all(ctr[routed, 3] == 0) and np.all(ctr[routed, 0] > 0)
+        for q in np.nonzero(routed)[0]:
+            row = ids[q][ids[q] != orc.SENTINEL]
+            assert len(set(row.tolist())) == len(row)
+            assert np.all(np.diff(dist[q][:len(row)]) >= 0)
+            if len(row):
+                a = ix["attrs"][row]
+                assert np.all((a >= lo[q]) & (a <= hi[q]))
+            for j, i in enumerate(row):
+                assert dist[q, j] == np.sum((cfg["queries"][q].astype(np.float64) - ix["vectors"][i]) ** 2)
+        recs.append(orc.recall(ids[routed], gt[routed], gtd[routed]))
+    assert recs[0] < recs[2] and recs[2] > 0.5, recs
 
 
 def test_centres_hist_closed_form():

@@ -18,9 +18,14 @@ checked by tests that a plausible restatement mistake fails:
    reference kernel's own control flow (its arrays, explored bit, bisection
    ranks and sorting networks), in both tie modes, on random small worlds and
    with a lowered per-cell iteration cap;
-5. every planted mistake of orc_set_mutation turns at least one of 1-4 red
-   (two of them only under the reference's tie order, as
-   test_slot_order_is_invisible_under_a_total_order shows).
+5. every planted mistake of orc_set_mutation turns at least one of 1-4 or 6
+   red (two of them only under the reference's tie order, as
+   test_slot_order_is_invisible_under_a_total_order shows);
+6. the full-graph route (gpu_graph.cu:3644-3787, assemble_edges
+   full_graph_search.cuh:984-997, the entry draw :12527-12539): its assembly
+   and search against the kernel model's restatement in both tie modes, and a
+   closed form -- with L at least N nothing is evicted, so the result is the
+   filtered brute force over the points reachable from the entries.
 """
 import numpy as np
 import pytest
@@ -319,9 +324,137 @@ def test_oracle_agrees_with_kernel_model():
     assert ok, f"{bad} of {n} cases differ"
 
 
+# ------------------------------------------------- 6. the full-graph route
+_FCASES = None
+
+
+def _full_cases():
+    """Random queries on the three small worlds of section 4, L = 8, 20, 70
+    and a cap of 3 iterations, both tie modes; model results computed once."""
+    global _FCASES
+    if _FCASES is not None:
+        return _FCASES
+    worlds = [_random_world(s, vmax=v) for s, v in ((0, 256), (1, 256), (2, 16))]
+    cases = []
+    for w, (vec, att, pid, g, x) in enumerate(worlds):
+        O = orc.OracleIndex(vec, att, pid, 4, g, x)
+        fg, fe = O.fgraph.copy(), O.fentry.copy()
+        rng = np.random.default_rng(300 + w)
+        for qi in range(6):
+            q = rng.integers(0, 256 if w < 2 else 16, 8).astype(np.float32)
+            lo = rng.integers(0, 50, 2).astype(np.float32)
+            hi = lo + rng.integers(10, 60, 2).astype(np.float32)
+            for tie in (0, 1):
+                M = KernelModel(vec, att, pid, 4, g, x, tie=tie)
+                for L, cap in ((8, 10000), (20, 10000), (70, 10000), (20, 3)):
+                    cases.append((w, tie, cap, q, lo, hi, L, M.search_full(q, lo, hi, fg, fe, L, max_iter=cap)))
+    _FCASES = (worlds, cases)
+    return _FCASES
+
+
+def check_full_assembly():
+    worlds, _ = _full_cases()
+    ok = True
+    for vec, att, pid, g, x in worlds:
+        O = orc.OracleIndex(vec, att, pid, 4, g, x)
+        M = KernelModel(vec, att, pid, 4, g, x)
+        ok &= O.FE == 2 and np.array_equal(O.fgraph, M.full_graph(2))
+    return bool(ok)
+
+
+def check_full_model(stop_early=False):
+    worlds, cases = _full_cases()
+    idx = [orc.OracleIndex(v, a, p, 4, g, x) for v, a, p, g, x in worlds]
+    bad = 0
+    for w, tie, cap, q, lo, hi, L, m in cases:
+        orc.set_tie_mode(tie)
+        orc.set_max_iter(cap)
+        ids, dist, ctr, ex, exc, _, _ = idx[w].trace(q, lo, hi, [0, 1], [0] * 8, L, full=True)
+        same = (ids.tolist() == m[0] and dist.tolist() == [float(np.float32(d)) for d in m[1]]
+                and int(ctr[0]) == m[2] and int(ctr[1]) == m[3] and int(ctr[7]) == 3
+                and ex.tolist() == m[4] and np.all(exc == 4))
+        bad += not same
+        if bad and stop_early:
+            break
+    orc.set_tie_mode(0)
+    orc.set_max_iter(0)
+    return bad == 0, bad, len(cases)
+
+
+def _reach(fg, fe):
+    seen = set(int(e) for e in fe)
+    todo = list(seen)
+    while todo:
+        u = todo.pop()
+        for v in fg[u]:
+            v = int(v)
+            if v != SENT and v not in seen:
+                seen.add(v)
+                todo.append(v)
+    return np.array(sorted(seen), np.int64)
+
+
+def check_full_closed_form():
+    """L >= N: every point the search reaches stays in the list and is
+    expanded, so the answer is the exact filtered top-K over the reachable set
+    (computed here by a breadth-first search), in (distance, cell-major
+    position) order."""
+    ok = True
+    rng = np.random.default_rng(17)
+    N, P, D = 90, 3, 6
+    vec = rng.integers(0, 12, (N, D)).astype(np.float32)
+    att = rng.integers(0, 100, (N, 1)).astype(np.float32)
+    pid = rng.integers(0, P, N).astype(np.uint32)
+    g = orc.knn_cell_graphs(vec.astype(np.uint8), pid, P, 4)
+    x = orc.cross_graph(vec.astype(np.uint8), pid, P, 2)
+    O = orc.OracleIndex(vec, att, pid, P, g, x)
+    reach = _reach(O.fgraph, O.fentry)
+    ok &= O.FD == 6 and len(reach) > N // 2
+    cm = np.empty(N, np.int64)
+    cm[O.gidx] = np.arange(N)
+    for t in range(10):
+        q = rng.integers(0, 12, D).astype(np.float32)
+        lo = np.array([rng.integers(0, 40)], np.float32)
+        hi = lo + np.float32(rng.integers(10, 70))
+        ids, dist, ctr, ex, _, _, _ = O.trace(q, lo, hi, [0, 1], [0] * 4, 96, full=True)
+        inr = reach[(att[reach, 0] >= lo[0]) & (att[reach, 0] <= hi[0])]
+        d = np.sum((vec[inr].astype(np.float64) - q) ** 2, axis=1)
+        order = np.lexsort((cm[inr], d))[:10]
+        exp = np.full(10, orc.SENTINEL, np.uint32)
+        exp[:len(order)] = inr[order]
+        ok &= np.array_equal(ids, exp)
+        ok &= np.array_equal(dist[:len(order)], d[order].astype(np.float32))
+        ok &= sorted(ex.tolist()) == reach.tolist()      # each reachable point expanded once
+    return bool(ok)
+
+
+def test_full_graph_assembly_matches_model():
+    assert check_full_assembly()
+
+
+def test_full_graph_search_agrees_with_kernel_model():
+    ok, bad, n = check_full_model()
+    assert ok, f"{bad} of {n} cases differ"
+
+
+def test_full_graph_closed_form():
+    assert check_full_closed_form()
+
+
+def test_full_graph_entry_draw():
+    """The pair draw's first part is orc_entry_points' draw (one generator,
+    first use); the FD full-graph entries are distinct ids below N."""
+    for N, P, R, FD in ((4000, 16, 16, 32), (1000, 4, 8, 8), (200, 3, 4, 6)):
+        a, f = orc.entry_points_pair(N, P, R, FD)
+        assert np.array_equal(a, orc.entry_points(N, P, R))
+        assert len(f) == FD and len(set(f.tolist())) == FD and f.max() < N
+
+
 # ---------------------------------------------------------- 5. mutations
 CHECKS = {"networks": check_networks, "merges": check_merges, "closed form": check_closed_form,
-          "hand trace": check_hand_trace, "model": lambda: check_model(True)[0]}
+          "hand trace": check_hand_trace, "model": lambda: check_model(True)[0],
+          "full assembly": check_full_assembly, "full model": lambda: check_full_model(True)[0],
+          "full closed form": check_full_closed_form}
 
 
 def _failing_checks(m):

@@ -15,11 +15,11 @@ def _print_case(name, **kw):
     print(f"[case] {name} " + " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
 
 
-def _pipeline(dev, q, lo, hi, prefilter, topc, L, ent):
+def _pipeline(dev, q, lo, hi, prefilter, topc, L, ent, postfilter=1 << 30):
     b = dev.batch(q, lo, hi)
     b.mark_cells(prefilter)
     b.order_cells(topc)
-    ids, d, _ = b.search(L, entry_points=ent)
+    ids, d, _ = b.search(L, postfilter=postfilter, entry_points=ent)
     b.close()
     return ids, d
 
@@ -28,10 +28,13 @@ def _pipeline(dev, q, lo, hi, prefilter, topc, L, ent):
     ("world32", 0.05, 48, {}),                                  # MFMA route in the pipeline, gather here
     ("world_gauss", 0.02, 40, {}),                              # non-integer data, 3 attributes, 64 cells
     ("world_c4", 0.3, 32, dict(vec_dtype=1, f2h_factor=1.0)),   # fp16 rows, 768-d
+    ("world32", 0.05, 48, dict(postfilter=6)),                  # the full-graph route
 ])
 def test_noalloc_matches_batch_pipeline(request, world, prefilter, L, kw):
     import garfield_amd as gf
     cfg, ix = request.getfixturevalue(world)
+    kw = dict(kw)
+    pf = kw.pop("postfilter", 1 << 30)
     dev = synth.open_device_index(ix, **kw)
     q = cfg["queries"].astype(np.float32)
     lo = cfg["lo"].astype(np.float32)
@@ -40,11 +43,11 @@ def test_noalloc_matches_batch_pipeline(request, world, prefilter, L, kw):
     for call, n in enumerate((Q, Q // 2 + 3)):
         for ent in (None, gf.entry_points(ix["vectors"].shape[0], ix["P"], ix["R"])[::-1].copy()):
             _print_case("noalloc", world=world, call=call, Q=n, L=L, entry="ref" if ent is None else "given")
-            rids, rd = _pipeline(dev, q[:n], lo[:n], hi[:n], prefilter, 4, L, ent)
+            rids, rd = _pipeline(dev, q[:n], lo[:n], hi[:n], prefilter, 4, L, ent, pf)
             ids = np.full((n, 10), 0xFFFFFFFF, np.uint32)
             d = np.full((n, 10), np.nan, np.float32)
-            gids, gd = gf.search_noalloc(dev, q[:n], lo[:n], hi[:n], prefilter, topc=4, L=L, entry_points=ent,
-                                         out=(ids, d))
+            gids, gd = gf.search_noalloc(dev, q[:n], lo[:n], hi[:n], prefilter, topc=4, L=L, postfilter=pf,
+                                         entry_points=ent, out=(ids, d))
             assert gids is ids and gd is d
             assert np.array_equal(ids, rids), (world, call, np.argwhere(ids != rids)[:5])
             assert np.array_equal(d.view(np.uint32), rd.view(np.uint32)), (world, call)
