@@ -50,6 +50,10 @@ def main():
     ap.add_argument("--stream-q", type=int, default=10_000)
     ap.add_argument("--stream-budget-mb", type=int, default=64)
     ap.add_argument("--stream-thresholds", default="1.0,0.25,0.0")
+    ap.add_argument("--stream-plan", choices=["planned", "static"], default="planned",
+                    help="planned: batches planned from the query batch's cell lists (gf_stream_plan_cells), "
+                         "timed beside the reference's static plan of 16 consecutive cells per batch; "
+                         "static: that static plan only")
     ap.add_argument("--recall", type=float, default=0.95)
     ap.add_argument("--prefilters", default="1.0,0.3,0.2,0.1,0.05,0.0",
                     help="1.0 = every query to the filtered brute force; below 1, queries whose "
@@ -423,7 +427,9 @@ def build_bench(args):
 def stream_bench(args):
     """C5-shaped out-of-core search on one GPU: the index is streamed from
     pinned host memory under a device budget far below its size (config
-    synth.config_stream; plan: 4x4 blocks of cells).  A step is stage A on the
+    synth.config_stream).  Its batches are planned from the query batch's
+    stage A cell lists (gf_stream_plan_cells) and timed beside the reference's
+    static plan of 16 consecutive cells per batch.  A step is stage A on the
     arithmetic grid plus the streamed search of the whole query batch (every
     batch image crosses PCIe once per step)."""
     import torch
@@ -441,13 +447,39 @@ def stream_bench(args):
     gt_ids, gt_dist = synth.ground_truth_torch(cfg["vectors"], cfg["attrs"], cfg["queries"], lo, hi, 10)
     torch.cuda.empty_cache()
     log(f"stream workload built in {time.time() - t0:.1f}s: N={N} D={D} Q={Q} P={ix['P']}")
-    plan = synth.block_plan(cfg["grid"], 4)
+    P = ix["P"]
+    block = [list(range(i, min(P, i + 16))) for i in range(0, P, 16)]   # bigdataset_experiment.cu:271-277
     l_q, r_q = synth.quantile_arrays(ix)
     budget = args.stream_budget_mb << 20
+    sizes = synth.cell_sizes(ix)
+
+    def streamed(plan):
+        return gl.Index.create_streamed(ix["vectors"], ix["attrs"], ix["grid"], l_q, r_q, ix["global_pid"],
+                                        ix["cell_graphs"], ix["cross"], plan=plan, device_budget=budget,
+                                        vec_dtype=gl.VEC_U8)
+
+    # One streamed index is open at a time: each holds a compute and a copy
+    # stream, and with more streams than hardware queues (GPU_MAX_HW_QUEUES)
+    # a copy stream can share a queue with a compute stream, which
+    # serialises the copies with the kernels.
     t1 = time.time()
-    sx = gl.Index.create_streamed(ix["vectors"], ix["attrs"], ix["grid"], l_q, r_q, ix["global_pid"],
-                                  ix["cell_graphs"], ix["cross"], plan=plan, device_budget=budget,
-                                  vec_dtype=gl.VEC_U8)
+    plan, plan_kind = block, "16 consecutive cells per batch (static)"
+    if args.stream_plan == "planned":
+        # the batch plan from this query batch's stage A cell lists, under the
+        # static plan's largest batch (so the same device budget holds)
+        sx0 = streamed(block)
+        b0 = sx0.batch(cfg["queries"], lo, hi)
+        b0.mark_cells_grid(amin, width, 1.0)
+        c, n, _, _ = b0.get_cells()
+        b0.close()
+        sx0.close()
+        maxpts = max(int(sizes[bt].sum()) for bt in block)
+        t_plan = time.perf_counter()
+        plan, planned_active = gl.plan_cells(c, n, cfg["grid"], sizes, max_points=maxpts, max_cells=16)
+        log(f"plan: {len(plan)} batches, {planned_active} active (query, batch) pairs, "
+            f"{(time.perf_counter() - t_plan) * 1e3:.1f} ms on the host")
+        plan_kind = f"planned from the query batch's cell lists (gf_stream_plan_cells, <= {maxpts} points)"
+    sx = streamed(plan)
     resident_bytes = N * (D + ix["R"] * 4 + 2 * 4 + 8 + ix["P"] * ix["E"] * 4)
     log(f"streamed index packed in {time.time() - t1:.1f}s: {len(plan)} batches, device "
         f"{sx.device_bytes / 2**20:.1f} MiB (budget {args.stream_budget_mb} MiB; a resident copy needs "
@@ -489,6 +521,7 @@ def stream_bench(args):
     t = time.perf_counter()
     for _ in range(args.steps):
         ids, st, ms_a = step(thr, L)
+        n_active = st.n_active
         acc["a"] += ms_a
         acc["total"] += st.ms_total
         acc["h2d"] += st.ms_h2d
@@ -504,7 +537,40 @@ def stream_bench(args):
     h2d_gbs = acc["bytes"] / (acc["h2d"] / 1e3) / 1e9
     trav_gbs = acc["btr"] / (acc["tr"] / 1e3) / 1e9 if acc["tr"] > 0 else 0.0
     log(f"timed: {qps:.0f} QPS; per step: search {acc['total'] / K:.2f} ms, copies {acc['h2d'] / K:.2f} ms at "
-        f"{h2d_gbs:.1f} GB/s, traversal {acc['tr'] / K:.2f} ms, brute force {acc['bf'] / K:.2f} ms")
+        f"{h2d_gbs:.1f} GB/s, traversal {acc['tr'] / K:.2f} ms, brute force {acc['bf'] / K:.2f} ms, "
+        f"{n_active} active (query, batch) pairs")
+
+    def measure(thr_, L_, steps):
+        for _ in range(args.warmup):
+            step(thr_, L_)
+        torch.cuda.synchronize()
+        t_ = time.perf_counter()
+        for _ in range(steps):
+            mids, mst, _ = step(thr_, L_)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t_
+        m_strict, m_tie = recall(mids)
+        return {"little_threshold": thr_, "L": L_, "qps": round(Q * steps / el, 1), "n_active": mst.n_active,
+                "recall_at_10": round(m_tie, 4), "ms_search": round(mst.ms_total, 3),
+                "ms_traverse": round(mst.ms_traverse, 3)}
+
+    # the traversal route (every query traverses), where each active (query,
+    # batch) pair restarts a traversal
+    trav_L = args.traverse_L
+    planned_trav = measure(0.0, trav_L, max(2, args.steps // 2))
+    log(f"traversal at L={trav_L}: {planned_trav}")
+    device_bytes = sx.device_bytes
+    static = None
+    if args.stream_plan == "planned":
+        # the static plan at the same operating points, for comparison
+        b.close()
+        sx.close()
+        sx = streamed(block)
+        b = sx.batch(cfg["queries"], lo, hi)
+        static = {"plan": "16 consecutive cells per batch (bigdataset_experiment.cu:271-277)",
+                  "nbatch": len(block), **measure(thr, L, args.steps),
+                  "traversal": measure(0.0, trav_L, max(2, args.steps // 2))}
+        log(f"static plan at the same points: {static}")
     out = {
         "metric": "QPS at recall@10≥0.95, C5-shaped out-of-core streaming (scaled), 1 MI355X",
         "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1, "steps": K, "warmup": args.warmup,
@@ -514,11 +580,12 @@ def stream_bench(args):
         "config": {
             "workload": (f"C5-shaped, scaled: {N} x {D} u8 (integers 0-255), 2 uint32 attrs on a 16x16 arithmetic "
                          f"grid, R={ix['R']} exact per-cell kNN + E=2 cross edges, {Q} queries, selectivity "
-                         f"log-U[0.5%,20%], k=10, {len(plan)} batches of 4x4 cells, device budget "
+                         f"log-U[0.5%,20%], k=10, {len(plan)} batches: {plan_kind}, device budget "
                          f"{args.stream_budget_mb} MiB"),
+            "nbatch": len(plan), "n_active": n_active, "traversal": planned_trav, "static_plan": static,
             "N": N, "D": D, "Q": Q, "K": 10, "L": L, "little_threshold": thr,
             "recall_at_10": round(tie, 4), "recall_at_10_strict": round(strict, 4),
-            "device_bytes": sx.device_bytes, "resident_index_bytes": resident_bytes,
+            "device_bytes": device_bytes, "resident_index_bytes": resident_bytes,
             "ms_stage_a": round(acc["a"] / K, 3), "ms_search": round(acc["total"] / K, 3),
             "ms_h2d": round(acc["h2d"] / K, 3), "bytes_h2d": round(acc["bytes"] / K),
             "ms_traverse": round(acc["tr"] / K, 3), "ms_bruteforce": round(acc["bf"] / K, 3),

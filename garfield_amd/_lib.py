@@ -71,7 +71,7 @@ class SearchStats(C.Structure):
                 ("ops_bruteforce", C.c_double), ("bf_mfma", C.c_uint32), ("ms_bf_kernel", C.c_double),
                 ("n_batches", C.c_uint32), ("bytes_h2d", C.c_double), ("ms_h2d", C.c_double),
                 ("ms_stage_a", C.c_double), ("ms_stage_b", C.c_double), ("graph", C.c_uint32),
-                ("q_fullgraph", C.c_uint32)]
+                ("q_fullgraph", C.c_uint32), ("n_active", C.c_uint64)]
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -120,6 +120,8 @@ _SYMBOLS = {
                   C.c_void_p, C.c_void_p, C.POINTER(C.c_double)],
     "gf_search_noalloc": [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p, C.POINTER(_NoallocOpts),
                           C.c_void_p, C.c_void_p],
+    "gf_stream_plan_cells": [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_uint64,
+                             C.c_uint32, C.c_void_p, C.c_void_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)],
     "gf_host_alloc": [C.c_size_t, C.POINTER(C.c_void_p)],
     "gf_host_free": [C.c_void_p],
     "gf_status_str": [C.c_int32],
@@ -418,6 +420,36 @@ def entry_points(N, P, R):
     out = np.empty(R, np.uint32)
     _check(load().gf_entry_points(N, P, R, _ptr(out)))
     return out
+
+
+def plan_cells(cells, counts, grid, cell_size, max_points=0, max_cells=16):
+    """Batch plan for a streamed index from stage A cell lists (Q x P rows,
+    counts[q] ids each, as Batch.get_cells returns them) on a grid of shape
+    `grid` (gf_stream_plan_cells): returns (plan, active), plan a list of
+    batches of cell ids (the form Index.create_streamed takes), active the
+    plan's sum over batches of active queries."""
+    cl = _c(cells, np.uint32)
+    cn = _c(counts, np.uint32)
+    sz = _c(cell_size, np.uint32)
+    g = _c(grid, np.uint32).reshape(-1)
+    Q = cn.shape[0]
+    P = sz.shape[0]
+    if int(np.prod(g)) != P:
+        raise ValueError(f"grid {list(g)} does not hold {P} cells")
+    if Q and cl.shape != (Q, P):
+        raise ValueError(f"cells must be Q x P = {Q} x {P}, got {cl.shape}")
+    sizes = np.zeros(P, np.uint32)
+    flat = np.zeros(P, np.uint32)
+    nb = C.c_uint32(0)
+    act = C.c_uint64(0)
+    _check(load().gf_stream_plan_cells(_ptr(cl) if Q else None, _ptr(cn) if Q else None, Q, g.shape[0], _ptr(g),
+                                       _ptr(sz), int(max_points), int(max_cells), _ptr(sizes), _ptr(flat),
+                                       C.byref(nb), C.byref(act)))
+    plan, k = [], 0
+    for i in range(nb.value):
+        plan.append([int(c) for c in flat[k:k + sizes[i]]])
+        k += int(sizes[i])
+    return plan, int(act.value)
 
 
 def grid_scatter(attrs, grid):

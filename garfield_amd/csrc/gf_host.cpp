@@ -1314,6 +1314,26 @@ gf_status gf_host_free(void* ptr) {
     });
 }
 
+gf_status gf_stream_plan_cells(const uint32_t* cells, const uint32_t* counts, uint32_t Q, uint32_t a,
+                               const uint32_t* grid_shape, const uint32_t* cell_size, uint64_t max_points,
+                               uint32_t max_cells, uint32_t* sizes, uint32_t* plan_cells, uint32_t* nbatch,
+                               uint64_t* active) {
+    return run_guarded([&] {
+        GF_REQUIRE(grid_shape && cell_size && sizes && plan_cells && nbatch, GF_E_ARG,
+                   "gf_stream_plan_cells: null argument");
+        GF_REQUIRE(Q == 0 || (cells && counts), GF_E_ARG, "gf_stream_plan_cells: null cell lists");
+        std::vector<std::vector<uint32_t>> plan;
+        const uint64_t act = gf::plan_cells(cells, counts, Q, a, grid_shape, cell_size, max_points, max_cells, plan);
+        size_t k = 0;
+        for (size_t i = 0; i < plan.size(); ++i) {
+            sizes[i] = uint32_t(plan[i].size());
+            for (uint32_t c : plan[i]) plan_cells[k++] = c;
+        }
+        *nbatch = uint32_t(plan.size());
+        if (active) *active = act;
+    });
+}
+
 gf_status gf_entry_points(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
     return run_guarded([&] {
         GF_REQUIRE(out && P >= 1 && N >= P, GF_E_ARG, "invalid arguments");

@@ -377,6 +377,7 @@ hipError_t launch_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t*
 hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, hipStream_t st);
 hipError_t launch_zero_u32(uint32_t* x, uint32_t n, hipStream_t st);   // a kernel, so that it can sit in a graph
 hipError_t launch_stamp(uint64_t* t, hipStream_t st);                    // *t = device wall clock when it runs
+// need: 2 * nbatch entries, the need flags, then the active queries per batch
 hipError_t launch_batch_need(uint32_t Q, uint32_t P, uint32_t nbatch, const uint32_t* plan_cells,
                              const uint32_t* plan_off, const uint8_t* flags, uint32_t* need, hipStream_t st);
 hipError_t launch_merge_stream(uint32_t Q, uint32_t K, uint32_t* run_ids, float* run_dist, const uint32_t* ids,

@@ -1172,14 +1172,17 @@ __global__ void k_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* di
 // workgroup per batch): need[b] bit 0 = some query takes the brute force on
 // it (all its selected cells of the batch little), bit 1 = some query
 // traverses it; 0 = no query selects any of its cells.
+// need[b]: bit 0 = some query only brute-forces batch b, bit 1 = some query
+// traverses it; active[b] = queries with a selected cell in batch b.
 __global__ __launch_bounds__(256) void k_batch_need(uint32_t Q, uint32_t P, const uint32_t* plan_cells,
-                                                    const uint32_t* plan_off, const uint8_t* flags, uint32_t* need) {
-    __shared__ uint32_t acc;
+                                                    const uint32_t* plan_off, const uint8_t* flags, uint32_t* need,
+                                                    uint32_t* active) {
+    __shared__ uint32_t acc, nact;
     const uint32_t bi = blockIdx.x;
-    if (threadIdx.x == 0) acc = 0;
+    if (threadIdx.x == 0) { acc = 0; nact = 0; }
     __syncthreads();
     const uint32_t c0 = plan_off[bi], c1 = plan_off[bi + 1];
-    uint32_t mine = 0;
+    uint32_t mine = 0, na = 0;
     for (uint32_t q = blockIdx.y * blockDim.x + threadIdx.x; q < Q; q += gridDim.y * blockDim.x) {
         const uint8_t* fl = flags + size_t(q) * P;
         uint32_t n = 0;
@@ -1188,11 +1191,13 @@ __global__ __launch_bounds__(256) void k_batch_need(uint32_t Q, uint32_t P, cons
             const uint8_t f = fl[plan_cells[i]];
             if (f & 1u) { ++n; all = all && (f & 2u); }
         }
-        if (n) mine |= all ? 1u : 2u;
+        if (n) { mine |= all ? 1u : 2u; ++na; }
     }
     if (mine) atomicOr(&acc, mine);
+    if (na) atomicAdd(&nact, na);
     __syncthreads();
-    if (threadIdx.x == 0 && acc) atomicOr(&need[bi], acc);   // need[] zeroed before
+    if (threadIdx.x == 0 && acc) atomicOr(&need[bi], acc);   // need[] and active[] zeroed before
+    if (threadIdx.x == 0 && nact) atomicAdd(&active[bi], nact);
 }
 
 // Running top-K of a streamed search: merge the batch's sorted K results
@@ -3199,9 +3204,11 @@ hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* di
 hipError_t launch_batch_need(uint32_t Q, uint32_t P, uint32_t nbatch, const uint32_t* plan_cells,
                              const uint32_t* plan_off, const uint8_t* flags, uint32_t* need, hipStream_t st) {
     if (!nbatch) return hipSuccess;
-    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(256), 0, st, need, nbatch);
+    // need[0, nbatch) and the active counts need[nbatch, 2 nbatch)
+    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(256), 0, st, need, 2u * nbatch);
     const uint32_t gy = (Q + 255) / 256 < 64u ? (Q + 255) / 256 : 64u;
-    hipLaunchKernelGGL(k_batch_need, dim3(nbatch, gy), dim3(256), 0, st, Q, P, plan_cells, plan_off, flags, need);
+    hipLaunchKernelGGL(k_batch_need, dim3(nbatch, gy), dim3(256), 0, st, Q, P, plan_cells, plan_off, flags, need,
+                       need + nbatch);
     return hipGetLastError();
 }
 

@@ -379,6 +379,9 @@ void map_cells(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix, s
 // the device buffers; then the streamed stage C.
 void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_stream_plan* plan, gf_index& ix);
 void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* dists, gf_search_stats* stats);
+uint64_t plan_cells(const uint32_t* cells, const uint32_t* counts, uint32_t Q, uint32_t a, const uint32_t* grid,
+                    const uint32_t* cell_size, uint64_t max_points, uint32_t max_cells,
+                    std::vector<std::vector<uint32_t>>& plan);
 // Entry-point draws (mt19937 default seed, distinct uniform_int_distribution
 // draws in [0, range), std::random_shuffle after srand(1)): the first R.
 void entry_points_draw(uint32_t range, uint32_t ndraw, uint32_t R, uint32_t* out);

@@ -230,6 +230,233 @@ void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_s
     (void)N;
 }
 
+// Batch plan from a query batch's cell lists: the out-of-core pipeline's
+// cell scheduling (README.md:5: cells are grouped so that few queries are
+// active in each batch; the shipped driver fixes its batches by hand,
+// bigdataset_experiment.cu:271-277, 746-756).  A query is active in a batch
+// when it selects one of the batch's cells; each active (query, batch) pair
+// restarts the query's search on fresh entries and costs a pass of its
+// schedule, so the plan minimises the sum over batches of active queries.
+//
+// A range query selects a box of the grid (the Cartesian product of one
+// cell interval per attribute), so batches are boxes too: the plan is the
+// best guillotine partition of the grid into boxes that fit a batch (at most
+// max_cells non-empty cells and max_points points; 0 = no limit), found by
+// dynamic programming over every box of the grid.  Cutting a box X in two
+// between cells t-1 and t of axis d adds to the objective exactly the
+// queries that select cells on both sides: those whose interval on d holds
+// t-1 and t and whose box meets X on every other axis.  So
+//   cost(X) = 0 when X fits a batch, else
+//   min over (d, t) of cut(X, d, t) + cost(lower part) + cost(upper part),
+// compared as (cost, batches) with ties to the first (d, t) in ascending
+// order; a batch is a leaf box's non-empty cells in id order, leaves in
+// recursion order (lower part first), empty leaves dropped.  A query's
+// lists are read as their bounding box; the returned objective is recounted
+// from the lists themselves.
+namespace {
+
+struct PlanBox {
+    uint32_t x0[kMaxAttr], x1[kMaxAttr];
+};
+
+}  // namespace
+
+uint64_t plan_cells(const uint32_t* cells, const uint32_t* counts, uint32_t Q, uint32_t a, const uint32_t* grid,
+                    const uint32_t* cell_size, uint64_t max_points, uint32_t max_cells,
+                    std::vector<std::vector<uint32_t>>& plan) {
+    GF_REQUIRE(a >= 1 && a <= kMaxAttr, GF_E_ARG, "plan_cells: attribute count out of range");
+    uint64_t P = 1, nbox = 1;
+    uint32_t stride[kMaxAttr], bstride[kMaxAttr];
+    for (uint32_t d = 0; d < a; ++d) {
+        GF_REQUIRE(grid[d] >= 1, GF_E_ARG, "plan_cells: empty grid axis");
+        P *= grid[d];
+        nbox *= uint64_t(grid[d]) * grid[d];
+        GF_REQUIRE(nbox <= (uint64_t(1) << 22), GF_E_UNSUPPORTED, "plan_cells: grid too large to plan (more than 2^22 box slots)");
+    }
+    for (int d = int(a) - 1, s = 1, bs = 1; d >= 0; --d) {
+        stride[d] = uint32_t(s);
+        bstride[d] = uint32_t(bs);
+        s *= int(grid[d]);
+        bs *= int(grid[d] * grid[d]);
+    }
+    // Each query's box (bounding box of its listed cells).
+    std::vector<uint32_t> qlo, qhi;   // Qb x a
+    const size_t W = (size_t(Q) + 63) / 64;
+    std::vector<uint64_t> sel(size_t(P) * W, 0);
+    for (uint32_t q = 0; q < Q; ++q) {
+        GF_REQUIRE(counts[q] <= P, GF_E_ARG, "plan_cells: a query lists more cells than the grid holds");
+        if (!counts[q]) continue;
+        uint32_t lo[kMaxAttr], hi[kMaxAttr];
+        for (uint32_t d = 0; d < a; ++d) { lo[d] = grid[d]; hi[d] = 0; }
+        for (uint32_t i = 0; i < counts[q]; ++i) {
+            const uint32_t c = cells[size_t(q) * P + i];
+            GF_REQUIRE(c < P, GF_E_ARG, "plan_cells: cell id out of range");
+            sel[size_t(c) * W + q / 64] |= uint64_t(1) << (q % 64);
+            for (uint32_t d = 0; d < a; ++d) {
+                const uint32_t x = c / stride[d] % grid[d];
+                lo[d] = std::min(lo[d], x);
+                hi[d] = std::max(hi[d], x);
+            }
+        }
+        qlo.insert(qlo.end(), lo, lo + a);
+        qhi.insert(qhi.end(), hi, hi + a);
+    }
+    const size_t Qb = qlo.size() / a;
+    // cut(X, d, t).  Two attributes: per (d, t) a table over the other
+    // axis' [x0, x1] of the straddling queries whose interval meets it
+    // (prefix sums of a (lo, hi) histogram); one attribute: the straddle
+    // count; more: a scan of the straddling queries.
+    std::vector<std::vector<std::vector<uint32_t>>> strad(a);   // [d][t] query indices
+    std::vector<std::vector<std::vector<uint64_t>>> tab(a);     // [d][t] table (a <= 2)
+    for (uint32_t d = 0; d < a; ++d) {
+        strad[d].resize(grid[d]);
+        tab[d].resize(grid[d]);
+        for (size_t q = 0; q < Qb; ++q)
+            for (uint32_t t = qlo[q * a + d] + 1; t <= qhi[q * a + d]; ++t) strad[d][t].push_back(uint32_t(q));
+        if (a > 2) continue;
+        const uint32_t e = 1 - d, ge = a == 2 ? grid[e] : 1;
+        for (uint32_t t = 1; t < grid[d]; ++t) {
+            std::vector<uint64_t> h(size_t(ge) * ge, 0), T(size_t(ge) * ge, 0);
+            for (uint32_t q : strad[d][t]) {
+                if (a == 2) ++h[size_t(qlo[q * a + e]) * ge + qhi[q * a + e]];
+                else ++h[0];
+            }
+            // T[x0 * ge + x1] = #{lo <= x1, hi >= x0}
+            for (uint32_t x0 = 0; x0 < ge; ++x0)
+                for (uint32_t x1 = x0; x1 < ge; ++x1) {
+                    uint64_t n = 0;
+                    for (uint32_t lo = 0; lo <= x1; ++lo)
+                        for (uint32_t hi = std::max(lo, x0); hi < ge; ++hi) n += h[size_t(lo) * ge + hi];
+                    T[size_t(x0) * ge + x1] = n;
+                }
+            tab[d][t] = std::move(T);
+        }
+    }
+    auto cut = [&](const PlanBox& X, uint32_t d, uint32_t t) -> uint64_t {
+        if (a == 1) return tab[d][t][0];
+        if (a == 2) {
+            const uint32_t e = 1 - d;
+            return tab[d][t][size_t(X.x0[e]) * grid[e] + X.x1[e]];
+        }
+        uint64_t n = 0;
+        for (uint32_t q : strad[d][t]) {
+            bool meets = true;
+            for (uint32_t e = 0; e < a && meets; ++e)
+                if (e != d) meets = qlo[q * a + e] <= X.x1[e] && qhi[q * a + e] >= X.x0[e];
+            n += meets;
+        }
+        return n;
+    };
+    auto index = [&](const PlanBox& X) {
+        size_t i = 0;
+        for (uint32_t d = 0; d < a; ++d) i += size_t(X.x0[d] * grid[d] + X.x1[d]) * bstride[d];
+        return i;
+    };
+    // Every box, smaller extents first (both parts of a cut come before it).
+    std::vector<PlanBox> boxes;
+    {
+        PlanBox X{};
+        std::vector<uint32_t> pos(a, 0);   // enumerate (x0, x1) pairs per axis
+        std::vector<std::vector<std::pair<uint32_t, uint32_t>>> iv(a);
+        for (uint32_t d = 0; d < a; ++d)
+            for (uint32_t x0 = 0; x0 < grid[d]; ++x0)
+                for (uint32_t x1 = x0; x1 < grid[d]; ++x1) iv[d].push_back({x0, x1});
+        for (;;) {
+            for (uint32_t d = 0; d < a; ++d) { X.x0[d] = iv[d][pos[d]].first; X.x1[d] = iv[d][pos[d]].second; }
+            boxes.push_back(X);
+            uint32_t d = 0;
+            while (d < a && ++pos[d] == iv[d].size()) pos[d++] = 0;
+            if (d == a) break;
+        }
+        auto ext = [&](const PlanBox& B) {
+            uint32_t s = 0;
+            for (uint32_t d = 0; d < a; ++d) s += B.x1[d] - B.x0[d];
+            return s;
+        };
+        std::stable_sort(boxes.begin(), boxes.end(), [&](const PlanBox& u, const PlanBox& v) { return ext(u) < ext(v); });
+    }
+    std::vector<uint64_t> cost(nbox, 0), npts(nbox, 0);
+    std::vector<uint32_t> nleaf(nbox, 0), ncell(nbox, 0), split(nbox, 0);   // split: 0 = leaf, else d * 65536 + t
+    auto halves = [&](const PlanBox& X, uint32_t d, uint32_t t, PlanBox& A, PlanBox& B) {
+        A = X;
+        B = X;
+        A.x1[d] = t - 1;
+        B.x0[d] = t;
+    };
+    for (const PlanBox& X : boxes) {
+        const size_t i = index(X);
+        uint32_t d0 = a;
+        for (uint32_t d = 0; d < a; ++d)
+            if (X.x1[d] > X.x0[d]) { d0 = d; break; }
+        if (d0 == a) {   // one cell
+            uint32_t c = 0;
+            for (uint32_t d = 0; d < a; ++d) c += X.x0[d] * stride[d];
+            npts[i] = cell_size[c];
+            ncell[i] = cell_size[c] ? 1u : 0u;
+            nleaf[i] = ncell[i];
+            continue;
+        }
+        PlanBox A, B;
+        halves(X, d0, X.x0[d0] + 1, A, B);
+        npts[i] = npts[index(A)] + npts[index(B)];
+        ncell[i] = ncell[index(A)] + ncell[index(B)];
+        if ((max_cells == 0 || ncell[i] <= max_cells) && (max_points == 0 || npts[i] <= max_points)) {
+            nleaf[i] = ncell[i] ? 1u : 0u;
+            continue;
+        }
+        bool have = false;
+        for (uint32_t d = 0; d < a; ++d)
+            for (uint32_t t = X.x0[d] + 1; t <= X.x1[d]; ++t) {
+                halves(X, d, t, A, B);
+                const size_t ia = index(A), ib = index(B);
+                const uint64_t c = cut(X, d, t) + cost[ia] + cost[ib];
+                const uint32_t l = nleaf[ia] + nleaf[ib];
+                if (!have || c < cost[i] || (c == cost[i] && l < nleaf[i])) {
+                    have = true;
+                    cost[i] = c;
+                    nleaf[i] = l;
+                    split[i] = d * 65536u + t;
+                }
+            }
+    }
+    plan.clear();
+    std::vector<PlanBox> stack;
+    PlanBox all{};
+    for (uint32_t d = 0; d < a; ++d) { all.x0[d] = 0; all.x1[d] = grid[d] - 1; }
+    stack.push_back(all);
+    while (!stack.empty()) {
+        const PlanBox X = stack.back();
+        stack.pop_back();
+        const size_t i = index(X);
+        if (split[i]) {
+            PlanBox A, B;
+            halves(X, split[i] / 65536u, split[i] % 65536u, A, B);
+            stack.push_back(B);   // lower part first
+            stack.push_back(A);
+            continue;
+        }
+        std::vector<uint32_t> batch;
+        for (uint32_t c = 0; c < P; ++c) {
+            bool in = cell_size[c] > 0;
+            for (uint32_t d = 0; d < a && in; ++d) {
+                const uint32_t x = c / stride[d] % grid[d];
+                in = x >= X.x0[d] && x <= X.x1[d];
+            }
+            if (in) batch.push_back(c);
+        }
+        if (!batch.empty()) plan.push_back(std::move(batch));
+    }
+    uint64_t total = 0;
+    std::vector<uint64_t> act(W);
+    for (const auto& bt : plan) {
+        std::fill(act.begin(), act.end(), 0);
+        for (uint32_t c : bt)
+            for (size_t w = 0; w < W; ++w) act[w] |= sel[size_t(c) * W + w];
+        for (size_t w = 0; w < W; ++w) total += uint64_t(__builtin_popcountll(act[w]));
+    }
+    return total;
+}
+
 void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* dists, gf_search_stats* stats) {
     gf_index& ix = *b.ix;
     StreamIndex& S = *ix.sx;
@@ -435,11 +662,11 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     // Which batches this query batch needs, and which prefix of each image:
     // skipped batches cost nothing; a batch no query traverses moves only
     // its brute-force sections.
-    if (b.need.n < std::max<size_t>(nb, 1)) b.need.alloc(std::max<size_t>(nb, 1));
+    if (b.need.n < 2 * std::max<size_t>(nb, 1)) b.need.alloc(2 * std::max<size_t>(nb, 1));
     GF_HIP(launch_batch_need(Q, P, uint32_t(nb), S.plan_cells.p, S.plan_off.p, b.flags.p, b.need.p, st));
-    std::vector<uint32_t> need(nb, 0);
+    std::vector<uint32_t> need(2 * nb, 0);   // flags, then active queries per batch
     if (nb) {
-        GF_HIP(hipMemcpyAsync(need.data(), b.need.p, nb * 4, hipMemcpyDeviceToHost, st));
+        GF_HIP(hipMemcpyAsync(need.data(), b.need.p, 2 * nb * 4, hipMemcpyDeviceToHost, st));
         GF_HIP(hipStreamSynchronize(st));
     }
     if (gemm) {
@@ -525,6 +752,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         stats->ms_bf_kernel = g;
         stats->bf_mfma = gemm ? 1u : 0u;
         stats->n_batches = uint32_t(ran.size());
+        for (size_t bi : ran) stats->n_active += need[nb + bi];
         stats->bytes_h2d = bytes;
         stats->ms_h2d = h2d;
         uint64_t sum[GF_NCOUNTERS] = {0};

@@ -122,6 +122,26 @@ gf_status gf_index_create_streamed(const gf_index_host* host, const gf_open_opts
 gf_status gf_index_open_streamed(const gf_index_paths* paths, const gf_open_opts* opts,
                                  const gf_stream_plan* plan, gf_index** out);
 
+/* Batch plan for a streamed index from a query batch's stage A cell lists:
+ * the out-of-core pipeline's cell scheduling, which groups cells so that few
+ * queries are active per batch (README.md:5; the shipped driver writes its
+ * batches by hand, bigdataset_experiment.cu:271-277, 746-756).  The grid has
+ * a axes of grid_shape[d] cells (P = product, row-major, last axis fastest);
+ * cells/counts are gf_batch_get_cells' Q*P lists; cell_size holds the P cell
+ * sizes.  The plan is the guillotine partition of the grid into boxes of at
+ * most max_cells non-empty cells (0: no limit) and max_points points (0: no
+ * limit) that minimises the sum over batches of the queries selecting a cell
+ * of the batch (each query read as the bounding box of its cells), then the
+ * number of batches.  Writes nbatch batch sizes to sizes (room for P) and
+ * the cells batch after batch to plan_cells (room for P), in the form
+ * gf_stream_plan takes; empty cells are left out.  *active (may be NULL)
+ * receives the plan's objective counted from the lists.  Host only;
+ * GF_E_UNSUPPORTED for grids with more than 2^22 (x0, x1) box slots. */
+gf_status gf_stream_plan_cells(const uint32_t* cells, const uint32_t* counts, uint32_t Q, uint32_t a,
+                               const uint32_t* grid_shape, const uint32_t* cell_size, uint64_t max_points,
+                               uint32_t max_cells, uint32_t* sizes, uint32_t* plan_cells, uint32_t* nbatch,
+                               uint64_t* active);
+
 /* A query batch: Q query vectors (Q*D fp32) and closed ranges lo/hi (Q*a),
  * uploaded to the device (realdataset_search.cu:2198-2245 load + f2h). */
 gf_status gf_batch_create(gf_index* ix, const float* queries, uint32_t Q,
@@ -201,6 +221,10 @@ typedef struct {
        little; a resident index of at most 64 cells); their device time is in
        ms_traverse */
     uint32_t q_fullgraph;
+    /* streamed index: sum over the searched batches of the queries that
+       select a cell of the batch (each such pair restarts the query's search
+       in that batch) */
+    uint64_t n_active;
 } gf_search_stats;
 
 gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids /*Q*K*/,

@@ -589,3 +589,90 @@ def kmeans(vectors, C, iters, init_ids):
         np.add.at(sums, lab, x)
         nz = n > 0
         cen[nz] = (2 * sums[nz] + n[nz, None]) // (2 * n[nz, None])
+
+
+def plan_cells(cells_, counts, grid, cell_size, max_points=0, max_cells=16, mutation=0):
+    """Batch plan for out-of-core streaming from stage A cell lists, restated
+    as a memoised recursion over boxes of the grid.  The objective is the
+    out-of-core pipeline's cell scheduling (README.md:5: cells grouped so
+    that few queries are active per batch; the shipped driver fixes its
+    batches by hand, indexsearch/bigdataset/bigdataset_experiment.cu:271-277,
+    746-756): the sum over batches of the queries selecting one of the
+    batch's cells.  Batches are boxes (at most max_cells non-empty cells and
+    max_points points, 0 = no limit) of the best guillotine partition: a box
+    that fits is one batch; otherwise it is cut between cells t-1 and t of
+    axis d, minimising (queries selecting cells on both sides + the parts'
+    costs, then the number of batches), first (d, t) in ascending order on a
+    tie.  A query is the bounding box of its cells; grid cells are row-major,
+    last axis fastest.  Returns (plan, active) with active recounted from
+    the lists.  mutation (tests only): 1 counts a cut's straddling queries
+    without testing that they meet the box on the other axes, 2 compares
+    (batches, cost) instead of (cost, batches)."""
+    grid = [int(g) for g in grid]
+    a = len(grid)
+    P = int(np.prod(grid))
+    sizes = [int(x) for x in cell_size]
+    coords = np.array(np.unravel_index(np.arange(P), grid)).T          # P x a
+    boxes = []
+    for q in range(len(counts)):
+        n = int(counts[q])
+        if n:
+            cc = coords[np.asarray(cells_[q][:n], np.int64)]
+            boxes.append((cc.min(0), cc.max(0)))
+    qlo = np.array([b[0] for b in boxes], np.int64).reshape(-1, a)
+    qhi = np.array([b[1] for b in boxes], np.int64).reshape(-1, a)
+
+    def cells_in(x0, x1):
+        return [c for c in range(P) if sizes[c] and all(x0[d] <= coords[c][d] <= x1[d] for d in range(a))]
+
+    def cut(x0, x1, d, t):
+        m = (qlo[:, d] <= t - 1) & (qhi[:, d] >= t)
+        if mutation != 1:
+            for e in range(a):
+                if e != d:
+                    m &= (qlo[:, e] <= x1[e]) & (qhi[:, e] >= x0[e])
+        return int(m.sum())
+
+    memo = {}
+
+    def best(x0, x1):
+        key = (x0, x1)
+        if key in memo:
+            return memo[key]
+        inside = cells_in(x0, x1)
+        pts = sum(sizes[c] for c in inside)
+        unit = all(x0[d] == x1[d] for d in range(a))
+        if unit or ((max_cells == 0 or len(inside) <= max_cells) and (max_points == 0 or pts <= max_points)):
+            memo[key] = (0, 1 if inside else 0, None)
+            return memo[key]
+        res = None
+        for d in range(a):
+            for t in range(x0[d] + 1, x1[d] + 1):
+                lo_hi = x1[:d] + (t - 1,) + x1[d + 1:]
+                hi_lo = x0[:d] + (t,) + x0[d + 1:]
+                ca, la, _ = best(x0, lo_hi)
+                cb, lb, _ = best(hi_lo, x1)
+                c, l = cut(x0, x1, d, t) + ca + cb, la + lb
+                k = (l, c) if mutation == 2 else (c, l)
+                if res is None or k < res[0]:
+                    res = (k, c, l, (d, t))
+        memo[key] = (res[1], res[2], res[3])
+        return memo[key]
+
+    plan = []
+
+    def emit(x0, x1):
+        _, _, sp = best(x0, x1)
+        if sp is None:
+            inside = cells_in(x0, x1)
+            if inside:
+                plan.append(inside)
+            return
+        d, t = sp
+        emit(x0, x1[:d] + (t - 1,) + x1[d + 1:])
+        emit(x0[:d] + (t,) + x0[d + 1:], x1)
+
+    emit(tuple([0] * a), tuple(g - 1 for g in grid))
+    sets = [set(int(c) for c in cells_[q][:int(counts[q])]) for q in range(len(counts))]
+    active = sum(sum(1 for st in sets if st & set(bt)) for bt in plan)
+    return plan, active

@@ -356,3 +356,46 @@ def test_c5_shaped_stream_matches_oracle():
     assert np.array_equal(ctr.astype(np.int64), oc)
     b.close()
     sx.close()
+
+
+@pytest.mark.parametrize("thr,L", [(0.05, 48), (1.0, 32)])
+def test_planned_stream_matches_oracle(world_stream, thr, L):
+    """A plan made by gf_stream_plan_cells from the batch's own stage A cell
+    lists (at most 4 cells per batch): the streamed search over it is
+    bit-exact against the oracle run batch by batch, and the search's count
+    of active (query, batch) pairs is the planner's objective, at most the
+    static 2x2-block plan's (a partition the planner also considers)."""
+    from oracle import oracle as orc
+    cfg, ix = world_stream
+    _print_case("stream-planned", thr=thr, L=L)
+    P = ix["P"]
+    sizes = synth.cell_sizes(ix)
+    active = {}
+    plans = {"block": synth.block_plan(GRID, 2)}
+    probe = gl.Index.create_streamed(*_args(ix), plan=plans["block"])
+    b = probe.batch(cfg["queries"], cfg["lo"], cfg["hi"])
+    b.mark_cells_grid(AMIN, WIDTH, thr)
+    c, n, _, _ = b.get_cells()
+    plans["planned"], active["planned"] = gl.plan_cells(c, n, GRID, sizes, max_cells=4)
+    _, _, st = b.search(L=L, K=10, rl=10)
+    active["block"] = st.n_active
+    b.close()
+    probe.close()
+    assert sorted(x for bt in plans["planned"] for x in bt) == [x for x in range(P) if sizes[x]]
+    assert all(len(bt) <= 4 for bt in plans["planned"])
+    assert active["planned"] <= active["block"], active
+    sx = gl.Index.create_streamed(*_args(ix), plan=plans["planned"])
+    b = sx.batch(cfg["queries"], cfg["lo"], cfg["hi"])
+    b.mark_cells_grid(AMIN, WIDTH, thr)
+    flags = b.get_cell_flags()
+    ids, dists, st = b.search(L=L, K=10, rl=10)
+    ctr = b.get_counters()
+    assert st.n_active == active["planned"]
+    ent = orc.entry_draw(int(sizes[sizes > 0].min()), 10 * L, ix["R"])
+    oids, od, oc = _oracle_stream(ix, plans["planned"], cfg, flags, ent, L, mfma=bool(st.bf_mfma))
+    bad = np.nonzero(np.any(ids != oids, axis=1))[0]
+    assert bad.size == 0, f"{bad.size} queries differ, first {bad[:5]}"
+    assert np.array_equal(dists.view(np.uint32), od.view(np.uint32))
+    assert np.array_equal(ctr.astype(np.int64), oc)
+    b.close()
+    sx.close()
