@@ -75,17 +75,50 @@ __device__ __forceinline__ void hash_clear(uint32_t* H, uint32_t hsize) {
 // Vector types: VT 0 = fp32, 1 = binary16, 2 = uint8.  A row is read in
 // 16-byte chunks of kEpc<VT> elements; queries are fp32 rows for VT 2 and
 // rows of the data's type otherwise.
+//
+// Summation order (the canonical order the oracle restates): LPR "virtual"
+// lanes, virtual lane v accumulating chunks v, v + LPR, ... with fp32 fma in
+// element order, then an xor butterfly over the LPR partial sums.  The
+// virtual lanes are folded onto PL physical lanes per row (RowPlan), each
+// holding V = LPR / PL of them: the butterfly levels >= PL run inside a lane,
+// the levels < PL across lanes with DPP moves, so a row costs log2(PL)
+// cross-lane steps and 64 / PL rows are in flight per pass.  A physical lane
+// reads at most 4 chunks of a row (so a pass is a few 16-byte loads per lane)
+// and the loads of up to 16 chunks per lane are issued before the first
+// wait.
 template <int VT>
 constexpr int kEpc = VT == 0 ? 4 : (VT == 1 ? 8 : 16);
 
-template <int VT, int CPL>
-struct QReg {
-    float v[CPL][kEpc<VT>];
+template <int LPR, int CPL>
+struct RowPlan {
+    static constexpr int want = LPR * CPL / 4;
+    static constexpr int PL0 = want <= 8 ? 8 : (want <= 16 ? 16 : (want <= 32 ? 32 : 64));
+    static constexpr int PL = PL0 < LPR ? PL0 : LPR;   // physical lanes per row
+    static constexpr int V = LPR / PL;                   // virtual lanes per physical lane
+    static constexpr int RPP = 64 / PL;                  // rows per pass
+    static constexpr int NCH = V * CPL;                  // chunks per lane per row
+    static constexpr int NB = 16 / NCH > 0 ? 16 / NCH : 1;   // passes per batch of loads
 };
 
+template <int VT, int LPR, int CPL>
+struct QReg {
+    float v[RowPlan<LPR, CPL>::NCH][kEpc<VT>];
+};
+
+// Chunk k = j * CPL + m of physical lane l: virtual lane l + PL * j, its m-th
+// chunk l + PL * j + LPR * m.
+template <int LPR, int CPL>
+__device__ __forceinline__ uint32_t lane_chunk(uint32_t l, int k) {
+    using RP = RowPlan<LPR, CPL>;
+    return l + uint32_t(RP::PL * (k / CPL) + LPR * (k % CPL));
+}
+
+__device__ __forceinline__ uint4 load16(const char* base, uint32_t c) {
+    return *reinterpret_cast<const uint4*>(base + size_t(c) * 16u);
+}
+
 template <int VT>
-__device__ __forceinline__ void load_chunk(const char* base, uint32_t c, float (&x)[kEpc<VT>]) {
-    const uint4 u = *reinterpret_cast<const uint4*>(base + size_t(c) * 16u);
+__device__ __forceinline__ void decode_chunk(const uint4& u, float (&x)[kEpc<VT>]) {
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
     if constexpr (VT == 1) {
 #pragma unroll
@@ -105,78 +138,116 @@ __device__ __forceinline__ void load_chunk(const char* base, uint32_t c, float (
 }
 
 template <int VT, int LPR, int CPL>
-__device__ __forceinline__ void load_query(QReg<VT, CPL>& q, const char* qrow, uint32_t nch) {
-    const uint32_t l = lane_id() % LPR;
+__device__ __forceinline__ void load_query(QReg<VT, LPR, CPL>& q, const char* qrow, uint32_t nch) {
+    using RP = RowPlan<LPR, CPL>;
+    const uint32_t l = lane_id() % RP::PL;
 #pragma unroll
-    for (int m = 0; m < CPL; ++m) {
-        const uint32_t c = l + m * LPR;
+    for (int k = 0; k < RP::NCH; ++k) {
+        const uint32_t c = lane_chunk<LPR, CPL>(l, k);
         if (c < nch) {
             if constexpr (VT == 2) {
                 // fp32 query: one 16-element chunk is four 16-byte loads
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
+                for (int t = 0; t < 4; ++t) {
                     float x[4];
-                    load_chunk<0>(qrow, 4 * c + k, x);
+                    decode_chunk<0>(load16(qrow, 4 * c + t), x);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) q.v[m][4 * k + e] = x[e];
+                    for (int e = 0; e < 4; ++e) q.v[k][4 * t + e] = x[e];
                 }
             } else {
-                load_chunk<VT>(qrow, c, q.v[m]);
+                decode_chunk<VT>(load16(qrow, c), q.v[k]);
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < kEpc<VT>; ++e) q.v[m][e] = 0.0f;
+            for (int e = 0; e < kEpc<VT>; ++e) q.v[k][e] = 0.0f;
         }
     }
 }
 
-// Partial sum of one lane over its chunks l, l+LPR, ... in element order
-// (fp32 fma), the canonical order the oracle restates.
+// v + the value of lane (this lane + m): correct in every lane whose index
+// within its aligned group of 2m lanes is below m, which is all the
+// reduction below reads.
+template <int M>
+__device__ __forceinline__ float add_from_above(float v) {
+    if constexpr (M == 1) {
+        return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+    } else if constexpr (M == 2) {
+        return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+    } else if constexpr (M == 4 || M == 8) {
+        return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x100 + M, 0xF, 0xF, false));  // row_shl:M
+    } else {
+        return v + __shfl_down(v, M, 64);
+    }
+}
+
+// Distance of one row's chunks raw[0..NCH) (this lane's part) to the query:
+// per-virtual-lane fma chains, the in-lane butterfly levels, then the
+// cross-lane levels; the row's distance ends in the group's first lane.
 template <int VT, int LPR, int CPL>
-__device__ __forceinline__ float row_partial(const QReg<VT, CPL>& q, const char* row, uint32_t nch) {
-    const uint32_t l = lane_id() % LPR;
-    float acc = 0.0f;
+__device__ __forceinline__ float row_reduce(const QReg<VT, LPR, CPL>& q, const uint4 (&raw)[RowPlan<LPR, CPL>::NCH]) {
+    using RP = RowPlan<LPR, CPL>;
+    float s[RP::V];
 #pragma unroll
-    for (int m = 0; m < CPL; ++m) {
-        const uint32_t c = l + m * LPR;
-        if (c < nch) {
+    for (int j = 0; j < RP::V; ++j) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int m = 0; m < CPL; ++m) {
             float x[kEpc<VT>];
-            load_chunk<VT>(row, c, x);
+            decode_chunk<VT>(raw[j * CPL + m], x);
 #pragma unroll
             for (int e = 0; e < kEpc<VT>; ++e) {
-                const float d = q.v[m][e] - x[e];
+                const float d = q.v[j * CPL + m][e] - x[e];
                 acc = __builtin_fmaf(d, d, acc);
             }
         }
+        s[j] = acc;
     }
-    return acc;
+#pragma unroll
+    for (int mm = RP::V / 2; mm >= 1; mm >>= 1) {
+        float t[RP::V];
+#pragma unroll
+        for (int j = 0; j < RP::V; ++j) t[j] = s[j] + s[j ^ mm];
+#pragma unroll
+        for (int j = 0; j < RP::V; ++j) s[j] = t[j];
+    }
+    float v = s[0];
+    if constexpr (RP::PL >= 64) v = add_from_above<32>(v);
+    if constexpr (RP::PL >= 32) v = add_from_above<16>(v);
+    if constexpr (RP::PL >= 16) v = add_from_above<8>(v);
+    v = add_from_above<4>(v);
+    v = add_from_above<2>(v);
+    v = add_from_above<1>(v);
+    return v;
 }
 
 // Distances of the n rows listed in S[0..n) (LDS).  Lane j with compact
 // index ci (< n) receives the distance of row S[ci] in `dist`.
 template <int VT, int LPR, int CPL>
-__device__ __forceinline__ void eval_rows(const QReg<VT, CPL>& q, const char* vec, uint32_t rowbytes,
+__device__ __forceinline__ void eval_rows(const QReg<VT, LPR, CPL>& q, const char* vec, uint32_t rowbytes,
                                           uint32_t nch, const uint32_t* S, uint32_t n, uint32_t ci,
                                           float& dist) {
-    constexpr uint32_t RPI = 64 / LPR;                  // rows per pass
-    constexpr uint32_t NB = (8 / CPL) > 0 ? (8 / CPL) : 1;  // passes per batch
-    const uint32_t g = lane_id() / LPR;
-    const uint32_t npass = (n + RPI - 1) / RPI;
-    for (uint32_t k0 = 0; k0 < npass; k0 += NB) {
-        float acc[NB];
+    using RP = RowPlan<LPR, CPL>;
+    const uint32_t g = lane_id() / RP::PL, l = lane_id() % RP::PL;
+    const uint32_t npass = (n + RP::RPP - 1) / RP::RPP;
+    for (uint32_t k0 = 0; k0 < npass; k0 += RP::NB) {
+        uint4 raw[RP::NB][RP::NCH];
 #pragma unroll
-        for (uint32_t b = 0; b < NB; ++b) {
-            const uint32_t i = (k0 + b) * RPI + g;
-            acc[b] = 0.0f;
-            if (i < n) acc[b] = row_partial<VT, LPR, CPL>(q, vec + size_t(S[i]) * rowbytes, nch);
+        for (int b = 0; b < RP::NB; ++b) {
+            const uint32_t i = (k0 + b) * RP::RPP + g;
+            const char* row = i < n ? vec + size_t(S[i]) * rowbytes : nullptr;
+#pragma unroll
+            for (int k = 0; k < RP::NCH; ++k) {
+                const uint32_t c = lane_chunk<LPR, CPL>(l, k);
+                raw[b][k] = make_uint4(0u, 0u, 0u, 0u);
+                if (row && c < nch) raw[b][k] = load16(row, c);
+            }
         }
 #pragma unroll
-        for (uint32_t b = 0; b < NB; ++b) {
-            float v = acc[b];
-#pragma unroll
-            for (int m = LPR / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-            const float t = __shfl(v, int((ci % RPI) * LPR), 64);
-            if (ci < n && ci / RPI == k0 + b) dist = t;
+        for (int b = 0; b < RP::NB; ++b) {
+            if (k0 + b >= npass) break;
+            const float v = row_reduce<VT, LPR, CPL>(q, raw[b]);
+            const float t = __shfl(v, int((ci % RP::RPP) * RP::PL), 64);
+            if (ci < n && ci / RP::RPP == k0 + b) dist = t;
         }
     }
 }
@@ -195,18 +266,36 @@ __device__ __forceinline__ bool row_pass(const float* attrs, uint32_t a, uint32_
 }
 
 // Evaluate candidate rows held one per lane (lanes with need=false keep dist
-// = +inf).  Returns the number of rows gathered.
+// = +inf).  With lo/hi given, lanes with chk also test their row's attributes
+// into `pass`, loaded together with the rows (one wait for both).  Returns
+// the number of rows gathered.
 template <int VT, int LPR, int CPL>
-__device__ __forceinline__ uint32_t eval_lanes(const QReg<VT, CPL>& q, const TravArgs& p, uint32_t* S,
-                                               uint32_t row, bool need, float& dist) {
+__device__ __forceinline__ uint32_t eval_lanes(const QReg<VT, LPR, CPL>& q, const TravArgs& p, uint32_t* S,
+                                               uint32_t row, bool need, float& dist,
+                                               const float (*lo)[kMaxAttr] = nullptr,
+                                               const float (*hi)[kMaxAttr] = nullptr, bool chk = false,
+                                               bool* pass = nullptr) {
     const uint64_t m = ballot(need);
     const uint32_t ci = need ? lanes_below(m) : 0xFFFFFFFFu;
     wave_sync();
     if (need) S[ci] = row;
     wave_sync();
+    float av[kMaxAttr];
+    if (pass && chk) {
+#pragma unroll
+        for (uint32_t d = 0; d < kMaxAttr; ++d)
+            if (d < p.a) av[d] = p.attrs[size_t(row) * p.a + d];
+    }
     const uint32_t n = __popcll(m);
     dist = __int_as_float(0x7F800000);
     if (n) eval_rows<VT, LPR, CPL>(q, p.vec, p.rowbytes, p.nch, S, n, ci, dist);
+    if (pass) {
+        bool ok = chk;
+#pragma unroll
+        for (uint32_t d = 0; d < kMaxAttr; ++d)
+            if (d < p.a) ok = ok && (av[d] >= (*lo)[d]) && (av[d] <= (*hi)[d]);
+        *pass = ok;
+    }
     wave_sync();
     return n;
 }
@@ -382,7 +471,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
     const uint32_t hsize = 1u << p.hbits;
     const uint32_t L = p.L, R = p.R, P = p.P, E = p.E;
 
-    QReg<VT, CPL> qv;
+    QReg<VT, LPR, CPL> qv;
     load_query<VT, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
     float lo[kMaxAttr], hi[kMaxAttr];
 #pragma unroll
@@ -450,11 +539,11 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
                 const uint32_t nl = p.graph[size_t(srow) * R + lane];
                 nrow = off + nl;
                 isnew = hash_insert(H, p.hbits, nl);
-                pass = row_pass(p.attrs, p.a, nrow, lo, hi);
             }
             n_attr += R;
             float d;
-            n_dist += eval_lanes<VT, LPR, CPL>(qv, p, S, nrow, isnew, d);
+            // every neighbour's attributes are tested, loaded with the rows
+            n_dist += eval_lanes<VT, LPR, CPL>(qv, p, S, nrow, isnew, d, &lo, &hi, mine, &pass);
             b = mine ? make_cand(d, nrow, pass) : kCandSent;
             const uint32_t ip = merge_into(A, L, b, R, W);
             recycle_update(rc, p.rl, W, R, bleft, W);
@@ -627,7 +716,7 @@ __global__ __launch_bounds__(64) void k_fullgraph(TravArgs p) {
     const uint32_t hsize = 1u << p.hbits;
     const uint32_t L = p.L, FD = p.FD;
 
-    QReg<VT, CPL> qv;
+    QReg<VT, LPR, CPL> qv;
     load_query<VT, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
     float lo[kMaxAttr], hi[kMaxAttr];
 #pragma unroll
@@ -676,11 +765,10 @@ __global__ __launch_bounds__(64) void k_fullgraph(TravArgs p) {
         if (mine) {
             nrow = p.fgraph[size_t(crow(sc)) * FD + lane];
             isnew = nrow != kEmpty && hash_insert(H, p.hbits, nrow);
-            if (isnew) pass = row_pass(p.attrs, p.a, nrow, lo, hi);
         }
         n_attr += __popcll(ballot(isnew));
         float d;
-        n_dist += eval_lanes<VT, LPR, CPL>(qv, p, S, nrow, isnew, d);
+        n_dist += eval_lanes<VT, LPR, CPL>(qv, p, S, nrow, isnew, d, &lo, &hi, isnew, &pass);
         const uint32_t ip = merge_into(A, L, isnew ? make_cand(d, nrow, pass) : kCandSent, FD, W, true);
         scan = ip < scan ? ip : scan;
     }
@@ -745,7 +833,7 @@ __global__ __launch_bounds__(64) void k_bruteforce(TravArgs p) {
     if (si >= p.srange[1]) return;
     const uint32_t q = p.sched[si];
     const uint32_t K = p.K, P = p.P;
-    QReg<VT, CPL> qv;
+    QReg<VT, LPR, CPL> qv;
     load_query<VT, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
     float lo[kMaxAttr], hi[kMaxAttr];
 #pragma unroll
