@@ -827,7 +827,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         uint32_t hbits = 0;
         while ((1u << hbits) < hsize) ++hbits;
         const uint32_t Lpad = round_up(L, 2);
-        const uint32_t lds = Lpad * 8 + gf::kXSlots * 8 + 128 * 4 + hsize * 4;
+        const uint32_t lds = gf::trav_lds_bytes(Lpad, hsize, ix->P);
         GF_REQUIRE(lds <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
 
         // device scalars: tot[2] pairs, [3] fits, [4] items, [8..11] traversal /
@@ -865,6 +865,7 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         a.counters = b->counters.p;
         a.a = ix->a; a.P = ix->P; a.R = R; a.E = ix->E; a.L = L; a.K = K; a.rl = rl;
         a.hbits = hbits;
+        a.offl = gf::trav_offsets_in_lds(ix->P) ? 1u : 0u;
         a.Lpad = Lpad;
         // The full-graph route: its own visited-set size (L + FD list and B
         // region entries plus four expansions' FD between resets).
@@ -1130,11 +1131,13 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
             stats->n_lrow = sm[4]; stats->n_scan = sm[5]; stats->n_pass = sm[6];
             // Algorithmic bytes: what each kernel must read from HBM given
             // its counters (rows gathered, graph rows, attributes, cross-edge
-            // slices, local-id lookups) plus its result writes.
+            // slices, local-id lookups unless the offsets sit in LDS) plus
+            // its result writes.
             const double t_dist = double(sm[7]), b_dist = double(sm[8]);
+            const double lrow_bytes = gf::trav_offsets_in_lds(ix->P) ? 0.0 : 4.0;
             stats->bytes_traverse = t_dist * ix->rowbytes + double(stats->n_expand) * R * 4.0 +
                                     double(stats->n_attr) * ix->a * 4.0 + double(stats->n_cross) * ix->E * 4.0 +
-                                    double(stats->n_lrow) * 4.0 + double(dt[8]) * (K * 8.0 + ix->P * 4.0);
+                                    double(stats->n_lrow) * lrow_bytes + double(dt[8]) * (K * 8.0 + ix->P * 4.0);
             if (gemm && dt[9]) {
                 // Item schedule: every (query, sub-cell) pair costs 2 D ops per
                 // point; every item streams its sub-cell's tiles once; the final

@@ -15,6 +15,14 @@ constexpr uint32_t kMaxIter = 10000;  // per-cell iteration cap (gpu_graph.cu:39
 constexpr uint32_t kHashReset = 4;    // visited-set reset period (gpu_graph.cu:34)
 constexpr uint32_t kXSlots = 128;     // cross-cell entry slots (gpu_graph.cu:42)
 constexpr uint32_t kXStep = 64;       // candidates feeding the slots (gpu_graph.cu:3564)
+constexpr uint32_t kOffLds = 1024;    // cell offsets (P + 1) the traversal keeps in LDS
+
+// LDS bytes of the traversal kernel: candidate list, slot scratch, row list,
+// visited set of hsize keys, and the P + 1 cell offsets when they fit.
+inline bool trav_offsets_in_lds(uint32_t P) { return P + 1 <= kOffLds; }
+inline uint32_t trav_lds_bytes(uint32_t Lpad, uint32_t hsize, uint32_t P) {
+    return Lpad * 8 + kXSlots * 8 + 128 * 4 + hsize * 4 + (trav_offsets_in_lds(P) ? (P + 1) * 4 : 0);
+}
 constexpr uint32_t kMaxAttr = 8;      // attributes per point supported
 constexpr uint32_t kMaxE = 4;         // cross edges per (point, cell) supported
 constexpr uint32_t kSelTile = 1024;   // rows per selectivity tile
@@ -67,6 +75,7 @@ struct TravArgs {
     float* out_dist;          // Q*K
     uint32_t* counters;       // Q*GF_NCOUNTERS
     uint32_t a, P, R, E, L, K, rl, hbits, Lpad;
+    uint32_t offl;            // 1: the launch's LDS holds the P + 1 cell offsets (trav_lds_bytes)
     // Full-graph route (queries with postfilter or more cells): the graph
     // over every point, FD rows per row (cell-major rows, kEmpty = no edge),
     // its FD entry rows and this launch's query range in sched.

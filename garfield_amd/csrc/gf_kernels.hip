@@ -40,13 +40,16 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
 }
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
-// Lanes of one wave exchange data through LDS between the phases below.
-// Program order alone does not order one lane's LDS store before another
-// lane's load: the compiler assumes no cross-thread communication without
-// synchronisation and may move accesses.  Every hand-off therefore goes
-// through a workgroup barrier, which for these one-wave workgroups costs a
-// wait on outstanding LDS operations.
-__device__ __forceinline__ void wave_sync() { __syncthreads(); }
+// Lanes of one wave exchange data through LDS between the phases below
+// (one-wave workgroups only).  A wave's LDS instructions execute in issue
+// order, so the hardware already orders one lane's store before another
+// lane's later load; what must not happen is the compiler moving LDS
+// accesses across a hand-off (it assumes no communication between lanes
+// without synchronisation).  An empty asm with a memory clobber is that
+// fence.  A workgroup barrier would do it too, but it also waits for every
+// outstanding global load (the workgroup-scope release of the memory
+// model), which serialises the gathers with the LDS work around them.
+__device__ __forceinline__ void wave_sync() { __asm__ __volatile__("" ::: "memory"); }
 
 // ---------------------------------------------------------------- visited set
 // Open addressing with linear probing in LDS; set semantics identical to the
@@ -350,23 +353,46 @@ __device__ uint32_t merge_into(uint64_t* A, uint32_t L, uint64_t b, uint32_t nb,
         rb += (kk < kb) || (kk == kb && k < lane);
         rmin = rk < rmin ? rk : rmin;
     }
+    // The incoming positions in rank order (non-decreasing: a smaller key
+    // never lands after a larger one): lane t < nins holds the t-th.  A_i
+    // moves by #{positions <= i}, counted per 64-entry chunk from the
+    // positions before it and the few inside it.
+    const uint32_t nins = __popcll(ins);
+    const bool me_ins = (ins >> lane) & 1u;
+    const uint32_t dst = me_ins ? rb : nins + lanes_below(~ins);
+    const uint32_t rs = uint32_t(__builtin_amdgcn_ds_permute(int(dst * 4u), int(r)));
+    // Blocks of 4 chunks from the end: a block is read, then written; its
+    // writes land at or after its own start, which the blocks below never
+    // read, so one barrier per block orders it.
     const uint32_t nA = L - rmin;
-    for (int ch = int((nA + 63u) / 64u) - 1; ch >= 0; --ch) {
-        const uint32_t i = rmin + uint32_t(ch) * 64u + lane;
-        uint64_t av = 0;
-        uint32_t np = 0;
-        if (i < L) {
-            av = A[i];
-            uint32_t s = 0;
-            for (uint64_t m = ins; m; m &= m - 1) s += (readlane32(r, __builtin_ctzll(m)) <= i);
-            np = i + s;
+    const uint32_t nchunk = (nA + 63u) / 64u;
+    for (int blk = int((nchunk + 3u) / 4u) - 1; blk >= 0; --blk) {
+        uint64_t av[4];
+        uint32_t np[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t ch = uint32_t(blk) * 4u + u;
+            const uint32_t c0 = rmin + ch * 64u;
+            const uint32_t i = c0 + lane;
+            av[u] = 0;
+            np[u] = kEmpty;
+            if (ch < nchunk) {
+                uint32_t s = __popcll(ballot(lane < nins && rs < c0));
+                for (uint64_t m = ballot(lane < nins && rs >= c0 && rs < c0 + 64u); m; m &= m - 1)
+                    s += lane >= readlane32(rs, __builtin_ctzll(m)) - c0;
+                if (i < L) {
+                    av[u] = A[i];
+                    np[u] = i + s;
+                }
+            }
         }
         wave_sync();
-        if (i < L) {
-            if (np < L) A[np] = av;
-            else if (Bp) Bp[np - L] = (keep_all || (cvalid(av) && cpass(av))) ? av : kCandSent;
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            if (np[u] == kEmpty) continue;
+            if (np[u] < L) A[np[u]] = av[u];
+            else if (Bp) Bp[np[u] - L] = (keep_all || (cvalid(av[u]) && cpass(av[u]))) ? av[u] : kCandSent;
         }
-        wave_sync();
     }
     const uint32_t pos = rb + r;
     if (mine && r < L && pos < L) A[pos] = b;
@@ -418,21 +444,75 @@ __device__ __forceinline__ uint32_t first_unexplored(const uint64_t* A, uint32_t
     return L;
 }
 
-// Cell-local key of a candidate row for the visited set: arithmetic inside
-// the cell [off, offn), a gather of lrow[] for rows of other cells.
-__device__ __forceinline__ uint32_t local_key(const TravArgs& p, uint32_t row, uint32_t off, uint32_t offn,
-                                              uint32_t& nlrow) {
-    if (row >= off && row < offn) return row - off;
-    ++nlrow;
-    return p.lrow[row];
+// Cell offsets for the visited-set keys of other cells' rows: with at most
+// 16 cells, offset[0..15] in (wave-uniform) registers; with up to kOffLds - 1
+// cells, an LDS copy O of offset[0..P]; beyond, none (lrow[] is gathered).
+struct CellOffs {
+    const uint32_t* O;
+    uint32_t P;
+    uint32_t o[16];
+};
+
+__device__ __forceinline__ void cell_offs_init(CellOffs& co, const TravArgs& p, uint32_t* O) {
+    co.O = O;
+    co.P = p.P;
+#pragma unroll
+    for (uint32_t t = 0; t < 16; ++t) co.o[t] = t <= p.P ? p.offset[t] : 0u;
 }
 
-// Insert the keys of A[0..L) (and optionally one candidate per lane).
-__device__ void hash_add_list(const TravArgs& p, uint32_t* H, const uint64_t* A, uint32_t L,
+// Cell-local key of a candidate row for the visited set: arithmetic inside
+// the cell [off, offn); for rows of other cells, row - offset[c] for the
+// cell c holding it (rows are cell-major, so this is lrow[row]).
+__device__ __forceinline__ uint32_t local_key(const TravArgs& p, const CellOffs& co, uint32_t row, uint32_t off,
+                                              uint32_t offn, uint32_t& nlrow) {
+    if (row >= off && row < offn) return row - off;
+    ++nlrow;
+    if (co.P <= 16) {
+        // the largest offset <= row (offsets ascend; empty cells repeat one)
+        uint32_t base = 0;
+#pragma unroll
+        for (uint32_t t = 1; t < 16; ++t)
+            if (t < co.P && row >= co.o[t]) base = co.o[t];
+        return row - base;
+    }
+    if (!co.O) return p.lrow[row];
+    uint32_t lo = 0, hi = co.P;   // O[lo] <= row < O[hi]
+    while (hi - lo > 1u) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (co.O[mid] <= row) lo = mid; else hi = mid;
+    }
+    return row - co.O[lo];
+}
+
+// Insert the keys of A[0..L), four per lane at a time: their keys are
+// computed, then their first probes issued, before any probe's result is
+// awaited (a set: the insertion order does not change membership).
+__device__ void hash_add_list(const TravArgs& p, const CellOffs& co, uint32_t* H, const uint64_t* A, uint32_t L,
                               uint32_t off, uint32_t offn, uint32_t& nlrow) {
-    for (uint32_t i = lane_id(); i < L; i += 64u) {
-        const uint64_t c = A[i];
-        if (cvalid(c)) hash_insert(H, p.hbits, local_key(p, crow(c), off, offn, nlrow));
+    constexpr uint32_t U = 4;
+    const uint32_t mask = (1u << p.hbits) - 1u;
+    for (uint32_t base = 0; base < L; base += 64u * U) {
+        uint32_t key[U], h[U], old[U];
+        bool todo[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t i = base + u * 64u + lane_id();
+            const uint64_t c = i < L ? A[i] : kCandSent;
+            todo[u] = cvalid(c);
+            key[u] = todo[u] ? local_key(p, co, crow(c), off, offn, nlrow) : 0u;
+            h[u] = (key[u] * 2654435761u) >> (32u - p.hbits);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) old[u] = todo[u] ? atomicCAS(&H[h[u]], kEmpty, key[u]) : kEmpty;
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            if (!todo[u] || old[u] == kEmpty || old[u] == key[u]) continue;
+            for (uint32_t j = 0; j < mask; ++j) {
+                h[u] = (h[u] + 1u) & mask;
+                const uint32_t o2 = atomicCAS(&H[h[u]], kEmpty, key[u]);
+                if (o2 == kEmpty || o2 == key[u]) break;
+            }
+        }
     }
     wave_sync();
 }
@@ -470,6 +550,12 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
     const uint32_t q = p.sched[si];
     const uint32_t hsize = 1u << p.hbits;
     const uint32_t L = p.L, R = p.R, P = p.P, E = p.E;
+    // cell offsets for the visited-set keys of other cells' rows
+    uint32_t* O = p.offl ? H + hsize : nullptr;
+    if (O)
+        for (uint32_t i = lane; i <= P; i += 64u) O[i] = p.offset[i];
+    CellOffs co;
+    cell_offs_init(co, p, O);
 
     QReg<VT, LPR, CPL> qv;
     load_query<VT, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
@@ -517,9 +603,9 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
         for (uint32_t it = 0; it < kMaxIter; ++it) {
             if ((it + 1) % kHashReset == 0) {          // gpu_graph.cu:3441-3454
                 hash_clear(H, hsize);
-                hash_add_list(p, H, A, L, off, offn, n_lrow);
+                hash_add_list(p, co, H, A, L, off, offn, n_lrow);
                 if (lane < R && cvalid(bleft))
-                    hash_insert(H, p.hbits, local_key(p, crow(bleft), off, offn, n_lrow));
+                    hash_insert(H, p.hbits, local_key(p, co, crow(bleft), off, offn, n_lrow));
                 wave_sync();
             }
             const uint32_t sel = first_unexplored(A, L, scan);
@@ -617,7 +703,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
             }
             wave_sync();
             merge_into(A, L, y, 64u, nullptr);
-            hash_add_list(p, H, A, L, offx, offxn, n_lrow);
+            hash_add_list(p, co, H, A, L, offx, offxn, n_lrow);
         }
     }
 

@@ -84,7 +84,7 @@ extern "C" gf_status gf_search_noalloc(gf_index* ix, const float* queries, uint3
         uint32_t hbits = 0;
         while ((1u << hbits) < hsize) ++hbits;
         const uint32_t Lpad = gf::round_up(L, 2);
-        const uint32_t lds = Lpad * 8 + gf::kXSlots * 8 + 128 * 4 + hsize * 4;
+        const uint32_t lds = gf::trav_lds_bytes(Lpad, hsize, ix->P);
         GF_REQUIRE(lds <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
 
         // Sections, in the order gf_batch_create and the stage calls make them.
@@ -210,6 +210,7 @@ extern "C" gf_status gf_search_noalloc(gf_index* ix, const float* queries, uint3
         t.counters = s.counters;
         t.a = a; t.P = P; t.R = R; t.E = ix->E; t.L = L; t.K = K; t.rl = rl;
         t.hbits = hbits;
+        t.offl = gf::trav_offsets_in_lds(ix->P) ? 1u : 0u;
         t.Lpad = Lpad;
         gf::SchedArgs sa{};
         sa.Q = Q; sa.P = P; sa.postfilter = so.postfilter; sa.counts = s.counts; sa.little = s.little;

@@ -487,7 +487,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     uint32_t hbits = 0;
     while ((1u << hbits) < hsize) ++hbits;
     const uint32_t Lpad = round_up(L, 2);
-    const uint32_t lds = Lpad * 8 + kXSlots * 8 + 128 * 4 + hsize * 4;
+    const uint32_t lds = trav_lds_bytes(Lpad, hsize, Bm);
     GF_REQUIRE(lds <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
 
     TravArgs base{};
@@ -507,6 +507,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     base.counters = b.s_ctr.p;
     base.a = ix.a; base.R = R; base.E = ix.E; base.L = L; base.K = K; base.rl = o.rl;
     base.hbits = hbits;
+    base.offl = trav_offsets_in_lds(Bm) ? 1u : 0u;   // lds holds Bm + 1 >= B + 1 offsets
     base.Lpad = Lpad;
     uint32_t* tot = b.tot.p;
 
@@ -772,7 +773,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         stats->n_expand = sum[0]; stats->n_dist = sum[1]; stats->n_attr = sum[2]; stats->n_cross = sum[3];
         stats->n_lrow = sum[4]; stats->n_scan = sum[5]; stats->n_pass = sum[6];
         stats->bytes_traverse = t_dist * ix.rowbytes + double(sum[0]) * R * 4.0 + double(sum[2]) * ix.a * 4.0 +
-                                double(sum[3]) * ix.E * 4.0 + double(sum[4]) * 4.0;
+                                double(sum[3]) * ix.E * 4.0 + double(sum[4]) * (base.offl ? 0.0 : 4.0);
         stats->bytes_bruteforce = double(sum[5]) * ix.a * 4.0 + b_dist * ix.rowbytes;
         stats->ops_bruteforce = 3.0 * b_dist * ix.D;
     }
