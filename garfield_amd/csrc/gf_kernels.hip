@@ -2470,79 +2470,106 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3
             reload_tp();
         };
 
-        // Operands of tile t + 1 are loaded while tile t is computed.
-        v4i32_t A[KS], mh, mn, mr, ma[AW];
-        auto load_tile = [&](uint32_t t) {
-            const v4i32_t* vp = reinterpret_cast<const v4i32_t*>(p.vt + size_t(t) * KS * 1024u) + lane;
-            const int32_t* nt = p.tnorm + size_t(t) * 32u;
-            const uint32_t* mt = sa.tmeta + size_t(t) * MW;
-#pragma unroll
-            for (int k = 0; k < KS; ++k) A[k] = vp[k * 64];
-            mh = *reinterpret_cast<const v4i32_t*>(nt + 4u * grp);
-            mn = *reinterpret_cast<const v4i32_t*>(nt + 16u + 4u * grp);
-            mr = *reinterpret_cast<const v4i32_t*>(mt + 4u * grp);
-#pragma unroll
-            for (int w = 0; w < AW; ++w) ma[w] = *reinterpret_cast<const v4i32_t*>(mt + 16u * (1 + w) + 4u * grp);
+        // Operands of tile t + 1 are loaded while tile t is computed: the
+        // int8 tile A after tile t's MFMAs have read it, its norms and meta
+        // into the other of two register sets (M0, M1, alternating), so no
+        // register is copied from one tile to the next.  All loads are buffer
+        // loads from a descriptor based at the item's first tile: the tile
+        // offset is a scalar, the lane's offset a constant.
+        const uint32_t ntile = t1 - t0;
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int8_t*>(p.vt + size_t(t0) * KS * 1024u), 0, ntile * KS * 1024u, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int32_t*>(p.tnorm + size_t(t0) * 32u), 0, ntile * 128u, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint32_t*>(sa.tmeta + size_t(t0) * MW), 0, ntile * MW * 4u, 0x00020000);
+        struct TileMeta {
+            v4i32_t mh, mn, mr, ma[AW];
         };
-        // The tile loop, with the range test, or without it for an item
+        v4i32_t A[KS];
+        auto bload = [](__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+            return __builtin_bit_cast(v4i32_t, __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), 0));
+        };
+        auto load_a = [&](uint32_t t) {
+#pragma unroll
+            for (int k = 0; k < KS; ++k) A[k] = bload(rv, lane * 16u, (t - t0) * KS * 1024u + k * 1024u);
+        };
+        auto load_m = [&](TileMeta& M, uint32_t t) {
+            const uint32_t tt = t - t0;
+            M.mh = bload(rn, 16u * grp, tt * 128u);
+            M.mn = bload(rn, 16u * grp, tt * 128u + 64u);
+            M.mr = bload(rm, 16u * grp, tt * MW * 4u);
+#pragma unroll
+            for (int w = 0; w < AW; ++w) M.ma[w] = bload(rm, 16u * grp, tt * MW * 4u + 64u * (1 + w));
+        };
+        // One tile step, with the range test, or without it for an item
         // whose queries all contain the sub-cell's box (every point passes).
-        auto tiles = [&](auto filt) {
+        auto step = [&](auto filt, const TileMeta& M, TileMeta& Mn, uint32_t t) {
             constexpr bool FILTER = decltype(filt)::value;
-            load_tile(t0);
-            for (uint32_t t = t0; t < t1; ++t) {
-                // k-outer: the four column tiles' MFMAs are independent, so a
-                // dependent MFMA (same accumulator) issues three MFMAs later
-                v4i32_t acc[4];
+            // k-outer: the four column tiles' MFMAs are independent, so a
+            // dependent MFMA (same accumulator) issues three MFMAs later
+            v4i32_t acc[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B[j][0], mh, 0, 0, 0);
+            for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B[j][0], M.mh, 0, 0, 0);
 #pragma unroll
-                for (int k = 1; k < KS; ++k)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[k], B[j][k], acc[j], 0, 0, 0);
-                const v4i32_t cmh = mh, cmn = mn, cmr = mr, cma0 = ma[0], cma1 = ma[AW - 1];
-                if (t + 1 < t1) load_tile(t + 1);
-                // Branch-free test of one (point i, query column j) pair.
-                auto pass = [&](int j, int i) {
-                    bool ok = acc[j][i] >= tp[j];
-                    if constexpr (FILTER) {
-                        const uint32_t x0 = uint32_t(cma0[i]);
-                        ok &= clamp16(x0, blo[j][0], bhi[j][0]) == x0;
-                        if (AW > 1) {
-                            const uint32_t x1 = uint32_t(cma1[i]);
-                            ok &= clamp16(x1, blo[j][AW - 1], bhi[j][AW - 1]) == x1;
-                        }
-                    }
-                    return ok;
-                };
-                // Distance first, on the max of each column's four rows (one
-                // compare per column); the range test only runs for a tile
-                // where some pair is within the threshold.
-                bool anyd = false;
+            for (int k = 1; k < KS; ++k)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    anyd |= max(max(acc[j][0], acc[j][1]), max(acc[j][2], acc[j][3])) >= tp[j];
-                if (!__builtin_amdgcn_ballot_w64(anyd)) continue;
-                // Pair positions (j, i) where some lane is within its bound: a
-                // tile step holds about two such pairs among its 1024, so the
-                // range test and the append run for those positions only.
-                bool full = false;
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const bool dok = acc[j][i] >= tp[j];
-                        if (!__builtin_amdgcn_ballot_w64(dok)) continue;
-                        if (pass(j, i)) {
-                            // Append: the owner adds |q'|^2 to nx - 2 q'.x' later.
-                            const uint32_t ql = 16u * j + col;
-                            const int32_t v = cmn[i] - 2 * (acc[j][i] - cmh[i]);
-                            const uint32_t slot = atomicAdd(&cnt[ql], 1u);
-                            buf[ql * kBfBufQ + slot] = (uint64_t(uint32_t(v)) << 32) | uint32_t(cmr[i]);
-                            full |= slot + 1u >= kBfDrainAt;
-                        }
+                    acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[k], B[j][k], acc[j], 0, 0, 0);
+            if (t + 1 < t1) {
+                load_a(t + 1);
+                load_m(Mn, t + 1);
+            }
+            // Branch-free test of one (point i, query column j) pair.
+            auto pass = [&](int j, int i) {
+                bool ok = acc[j][i] >= tp[j];
+                if constexpr (FILTER) {
+                    const uint32_t x0 = uint32_t(M.ma[0][i]);
+                    ok &= clamp16(x0, blo[j][0], bhi[j][0]) == x0;
+                    if (AW > 1) {
+                        const uint32_t x1 = uint32_t(M.ma[AW - 1][i]);
+                        ok &= clamp16(x1, blo[j][AW - 1], bhi[j][AW - 1]) == x1;
                     }
-                if (__builtin_amdgcn_ballot_w64(full)) drain();
+                }
+                return ok;
+            };
+            // Distance first, on the max of each column's four rows (one
+            // compare per column); the range test only runs for a tile
+            // where some pair is within the threshold.
+            bool anyd = false;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                anyd |= max(max(acc[j][0], acc[j][1]), max(acc[j][2], acc[j][3])) >= tp[j];
+            if (!__builtin_amdgcn_ballot_w64(anyd)) return;
+            // Pair positions (j, i) where some lane is within its bound: a
+            // tile step holds about two such pairs among its 1024, so the
+            // range test and the append run for those positions only.
+            bool full = false;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const bool dok = acc[j][i] >= tp[j];
+                    if (!__builtin_amdgcn_ballot_w64(dok)) continue;
+                    if (pass(j, i)) {
+                        // Append: the owner adds |q'|^2 to nx - 2 q'.x' later.
+                        const uint32_t ql = 16u * j + col;
+                        const int32_t v = M.mn[i] - 2 * (acc[j][i] - M.mh[i]);
+                        const uint32_t slot = atomicAdd(&cnt[ql], 1u);
+                        buf[ql * kBfBufQ + slot] = (uint64_t(uint32_t(v)) << 32) | uint32_t(M.mr[i]);
+                        full |= slot + 1u >= kBfDrainAt;
+                    }
+                }
+            if (__builtin_amdgcn_ballot_w64(full)) drain();
+        };
+        auto tiles = [&](auto filt) {
+            TileMeta M0, M1;
+            load_a(t0);
+            load_m(M0, t0);
+            for (uint32_t t = t0; t < t1; t += 2) {
+                step(filt, M0, M1, t);
+                if (t + 1 >= t1) break;
+                step(filt, M1, M0, t + 1);
             }
         };
         if (it.inside) tiles(std::false_type{});
