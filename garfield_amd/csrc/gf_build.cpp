@@ -7,9 +7,13 @@
 // (indexbuild/cagra_build.py:94-127, cell-local ids) and, for the cross-cell
 // graph, a CAGRA search of every point against every cell's index
 // (indexbuild/global_graph_build.py:106-176, local ids, own cell included).
-// Here both graphs are exact: the distances are integer dot products on the
-// int8 MFMA units (k_knn_i8) over the brute force's tile layout, and every
-// list is ordered by (squared distance, cell-local id).
+// Here both graphs are exact nearest neighbours ordered by (squared
+// distance, cell-local id).  For integer data in [0, 255] the distances are
+// integer dot products on the int8 MFMA units (k_knn_i8) over the brute
+// force's tile layout.  Other float data runs the same kernels on a u8
+// quantisation of it (one scale for every dimension), keeping kFloatMargin
+// more candidates per list than it returns, and those candidates are
+// re-ranked by their exact fp32 distances (k_rerank).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -24,6 +28,48 @@
 namespace gf {
 
 namespace {
+
+constexpr uint32_t kFloatMargin = 16;   // extra candidates per list for the re-rank of float data
+
+// Float data that are not all integers in [0, 255].
+bool float_data(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D) {
+    if (vec_dtype != GF_VEC_F32) return false;
+    const float* s = static_cast<const float*>(vectors);
+    for (size_t i = 0; i < size_t(N) * D; ++i)
+        if (!(s[i] >= 0.0f && s[i] <= 255.0f && s[i] == std::floor(s[i]))) return true;
+    return false;
+}
+
+// The first N rows of v8 (Dp wide, padding left as it is) from the input:
+// u8 and integer float data as they are; other float data quantised as
+// rint((x - min) / s), s = (max - min) / 255 in double over all values (all
+// 0 when they are equal).
+void rows_u8(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, uint32_t Dp, bool fmode,
+             std::vector<uint8_t>& v8) {
+    if (vec_dtype == GF_VEC_U8) {
+        const uint8_t* s = static_cast<const uint8_t*>(vectors);
+        for (uint32_t i = 0; i < N; ++i) std::memcpy(&v8[size_t(i) * Dp], s + size_t(i) * D, D);
+        return;
+    }
+    const float* s = static_cast<const float*>(vectors);
+    if (!fmode) {
+        for (uint32_t i = 0; i < N; ++i)
+            for (uint32_t k = 0; k < D; ++k) v8[size_t(i) * Dp + k] = uint8_t(s[size_t(i) * D + k]);
+        return;
+    }
+    double lo = s[0], hi = s[0];
+    for (size_t i = 0; i < size_t(N) * D; ++i) {
+        lo = std::min(lo, double(s[i]));
+        hi = std::max(hi, double(s[i]));
+    }
+    GF_REQUIRE(std::isfinite(lo) && std::isfinite(hi), GF_E_UNSUPPORTED, "non-finite vectors");
+    const double sc = (hi - lo) / 255.0;
+    for (uint32_t i = 0; i < N; ++i)
+        for (uint32_t k = 0; k < D; ++k) {
+            const double q = sc > 0.0 ? std::nearbyint((double(s[size_t(i) * D + k]) - lo) / sc) : 0.0;
+            v8[size_t(i) * Dp + k] = uint8_t(std::min(255.0, std::max(0.0, q)));
+        }
+}
 
 // Stable ascending argsort of floats: LSD radix sort (three 11-bit digits)
 // of the order-preserving integer image of each value; -0 counts as +0, as
@@ -106,9 +152,19 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
                "build_graphs: E must be in [1, " + std::to_string(kKnnKMax) + "]");
     GF_REQUIRE(uint64_t(N) * P * (cross ? E : 0) < (uint64_t(1) << 40), GF_E_UNSUPPORTED,
                "build_graphs: cross-cell graph too large");
-    const uint32_t Dp = round_up(D, 64);
-    GF_REQUIRE(Dp <= 256, GF_E_UNSUPPORTED, "build_graphs: dimension above 256");
-    const uint32_t KS = Dp / 64;
+    const uint32_t KS = knn_ks(D);
+    GF_REQUIRE(KS > 0, GF_E_UNSUPPORTED, "build_graphs: dimension above 1024");
+    const uint32_t Dp = KS * 64, QT = knn_qt(KS);
+    // Float data that are not all integers in [0, 255]: candidates from a u8
+    // quantisation, kFloatMargin more per list, then the exact re-rank.
+    const bool fmode = float_data(vectors, vec_dtype, N, D);
+    uint32_t Rk = R, Ek = E;   // list sizes the kNN kernel keeps
+    if (fmode) {
+        GF_REQUIRE(!cell_graphs || R + 1 <= 64, GF_E_UNSUPPORTED, "build_graphs: float data supports R up to 63");
+        GF_REQUIRE(!cross || E <= 64, GF_E_UNSUPPORTED, "build_graphs: float data supports E up to 64");
+        Rk = std::min(R + kFloatMargin, 63u);
+        Ek = std::min(E + kFloatMargin, 64u);
+    }
 
     using clock = std::chrono::steady_clock;
     const auto c0 = clock::now();
@@ -116,25 +172,13 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
         return std::chrono::duration<double, std::milli>(clock::now() - a).count();
     };
     // Vectors as u8 rows of Dp (padding 128 is 0 after the -128 shift and
-    // adds nothing to norms or dot products); float input must hold integers
-    // in [0, 255], the data the int8 distances are exact for.  u8 rows of a
+    // adds nothing to norms or dot products): integer data as it is; other
+    // float data quantised as rint((x - min) / s), s = (max - min) / 255 in
+    // double over all values (all 0 when they are equal).  u8 rows of a
     // multiple of 64 are uploaded as they are.
     const bool direct = vec_dtype == GF_VEC_U8 && D == Dp;
     std::vector<uint8_t> v8(direct ? 0 : size_t(N) * Dp, uint8_t(128));
-    if (direct) {
-    } else if (vec_dtype == GF_VEC_U8) {
-        const uint8_t* s = static_cast<const uint8_t*>(vectors);
-        for (uint32_t i = 0; i < N; ++i) std::memcpy(&v8[size_t(i) * Dp], s + size_t(i) * D, D);
-    } else {
-        const float* s = static_cast<const float*>(vectors);
-        for (uint32_t i = 0; i < N; ++i)
-            for (uint32_t k = 0; k < D; ++k) {
-                const float x = s[size_t(i) * D + k];
-                GF_REQUIRE(x >= 0.0f && x <= 255.0f && x == std::floor(x), GF_E_UNSUPPORTED,
-                           "build_graphs: vectors must be integers in [0, 255]");
-                v8[size_t(i) * Dp + k] = uint8_t(x);
-            }
-    }
+    if (!direct) rows_u8(vectors, vec_dtype, N, D, Dp, fmode, v8);
 
     // Cells: members in ascending point id (the cell-local id order of the
     // index), each cell padded to whole 16-point tiles.
@@ -158,7 +202,7 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
     // cell outermost so that concurrent waves stream the same candidates.
     std::vector<KnnItem> gitems, citems;
     for (uint32_t c = 0; c < P; ++c)
-        for (uint32_t t = ctile[c]; t < ctile[c + 1]; t += 4) gitems.push_back(KnnItem{t, c, c});
+        for (uint32_t t = ctile[c]; t < ctile[c + 1]; t += QT) gitems.push_back(KnnItem{t, c, c});
     if (cross) {
         citems.reserve(gitems.size() * P);
         for (uint32_t tc = 0; tc < P; ++tc) {
@@ -205,9 +249,9 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
     dci.upload(citems);
     vt.alloc(size_t(ntile) * KS * 1024);
     tnorm.alloc(size_t(ntile) * 32);
-    if (cell_graphs) dout_g.alloc(size_t(N) * R);
+    if (cell_graphs) dout_g.alloc(size_t(N) * Rk);
     if (cross) {
-        dout_c.alloc(size_t(N) * P * E);
+        dout_c.alloc(size_t(N) * P * Ek);
         // rows into empty cells are never written by a kernel: zero them
         GF_HIP(hipMemsetAsync(dout_c.p, 0, dout_c.bytes(), st));
     }
@@ -227,7 +271,7 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
     for (uint32_t c = 0; c < P; ++c) tmax = std::max(tmax, ctile[c + 1] - ctile[c]);
     const uint32_t nchunk = (tmax + ctiles - 1) / ctiles;
     DevBuf<uint64_t> state;
-    state.alloc(std::max(cell_graphs ? size_t(N) * (R + 1) : 0, cross ? size_t(N) * P * E : 0));
+    state.alloc(std::max(cell_graphs ? size_t(N) * (Rk + 1) : 0, cross ? size_t(N) * P * Ek : 0));
     KnnArgs ka{};
     ka.vt = vt.p;
     ka.tnorm = tnorm.p;
@@ -240,8 +284,8 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
     if (cell_graphs) {
         ka.items = dgi.p;
         ka.nitems = uint32_t(gitems.size());
-        ka.K = R + 1;
-        ka.R = R;
+        ka.K = Rk + 1;
+        ka.R = Rk;
         ka.out = dout_g.p;
         for (ka.chunk = 0; ka.chunk < nchunk; ++ka.chunk) GF_HIP(launch_knn_i8(ka, KS, uint32_t(ncu), st));
     }
@@ -250,23 +294,75 @@ void build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D
         GF_REQUIRE(citems.size() < 0xFFFFFFFFull, GF_E_UNSUPPORTED, "build_graphs: too many cross items");
         ka.items = dci.p;
         ka.nitems = uint32_t(citems.size());
-        ka.K = E;
+        ka.K = Ek;
         ka.R = 0;
         ka.out = dout_c.p;
         for (ka.chunk = 0; ka.chunk < nchunk; ++ka.chunk) GF_HIP(launch_knn_i8(ka, KS, uint32_t(ncu), st));
     }
+    DevBuf<uint32_t> dfin_g, dfin_c;
+    if (fmode) {
+        // The candidates' exact fp32 distances: rows cell-major, zero padded
+        // to whole 16-byte chunks (the layout of the row-distance helpers).
+        const uint32_t nch = (D + 3) / 4, rw = nch * 4;
+        std::vector<float> rows(size_t(N) * rw, 0.0f);
+        std::vector<uint32_t> cmrow(N), rowcell(N);
+        const float* s = static_cast<const float*>(vectors);
+        std::vector<uint32_t> pos(coff.begin(), coff.end() - 1);
+        for (uint32_t i = 0; i < N; ++i) {
+            const uint32_t r = pos[global_pid[i]]++;
+            cmrow[i] = r;
+            rowcell[r] = global_pid[i];
+            std::memcpy(&rows[size_t(r) * rw], s + size_t(i) * D, size_t(D) * 4);
+        }
+        DevBuf<float> drows;
+        DevBuf<uint32_t> dcm, drc;
+        drows.upload(rows);
+        dcm.upload(cmrow);
+        drc.upload(rowcell);
+        RerankArgs ra{};
+        ra.vec = drows.p;
+        ra.rowbytes = rw * 4;
+        ra.nch = nch;
+        ra.coff = dcoff.p;
+        ra.rowcell = drc.p;
+        ra.cmrow = dcm.p;
+        ra.P = P;
+        if (cell_graphs) {
+            dfin_g.alloc(size_t(N) * R);
+            ra.cand = dout_g.p;
+            ra.nc = Rk;
+            ra.keep = R;
+            ra.graph = 1;
+            ra.out = dfin_g.p;
+            GF_HIP(launch_rerank(ra, D, N, st));
+        }
+        if (cross) {
+            dfin_c.alloc(size_t(N) * P * E);
+            GF_HIP(hipMemsetAsync(dfin_c.p, 0, dfin_c.bytes(), st));
+            ra.cand = dout_c.p;
+            ra.nc = Ek;
+            ra.keep = E;
+            ra.graph = 0;
+            ra.out = dfin_c.p;
+            GF_REQUIRE(uint64_t(N) * P < 0x80000000ull, GF_E_UNSUPPORTED, "build_graphs: too many cross lists");
+            GF_HIP(launch_rerank(ra, D, uint32_t(uint64_t(N) * P), st));
+        }
+        GF_HIP(hipStreamSynchronize(st));   // the row buffers go out of scope
+    }
+    const uint32_t* res_g = fmode ? dfin_g.p : dout_g.p;
+    const uint32_t* res_c = fmode ? dfin_c.p : dout_c.p;
     GF_HIP(hipEventRecord(ev[3], st));
     // The graphs travel to the caller on a second stream while the cross
     // edges are computed.
     if (cell_graphs) {
-        GF_HIP(hipStreamWaitEvent(st2, ev[2], 0));
-        GF_HIP(hipMemcpyAsync(cell_graphs, dout_g.p, dout_g.bytes(), hipMemcpyDeviceToHost, st2));
+        GF_HIP(hipStreamWaitEvent(st2, fmode ? ev[3] : ev[2], 0));
+        GF_HIP(hipMemcpyAsync(cell_graphs, res_g, size_t(N) * R * 4, hipMemcpyDeviceToHost, st2));
         GF_HIP(hipStreamSynchronize(st2));
     }
     GF_HIP(hipStreamSynchronize(st));
     const double ms_run = ms_since(c2);
     const auto c3 = clock::now();
-    if (cross) GF_HIP(hipMemcpy(cross, dout_c.p, dout_c.bytes(), hipMemcpyDeviceToHost));
+    if (cross) GF_HIP(hipMemcpy(cross, res_c, size_t(N) * P * E * 4, hipMemcpyDeviceToHost));
     if (stats) {
         stats->ms_prep = ms_prep;
         stats->ms_upload = ms_upload;
@@ -360,27 +456,17 @@ void kmeans_labels(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t 
                "kmeans: vectors must be GF_VEC_F32 or GF_VEC_U8");
     GF_REQUIRE(C > 0 && C <= N, GF_E_ARG, "kmeans: need 0 < C <= N");
     GF_REQUIRE(uint64_t(N) + C < 0xFFFFFFF0ull, GF_E_UNSUPPORTED, "kmeans: too many points");
-    const uint32_t Dp = round_up(D, 64);
-    GF_REQUIRE(Dp <= 256, GF_E_UNSUPPORTED, "kmeans: dimension above 256");
-    const uint32_t KS = Dp / 64;
+    const uint32_t KS = knn_ks(D);
+    GF_REQUIRE(KS > 0, GF_E_UNSUPPORTED, "kmeans: dimension above 1024");
+    const uint32_t Dp = KS * 64, QT = knn_qt(KS);
     for (uint32_t c = 0; c < C; ++c) GF_REQUIRE(init_ids[c] < N, GF_E_ARG, "kmeans: init id out of range");
     const auto c0 = std::chrono::steady_clock::now();
 
     // Rows: the N points, then the C centres (u8, Dp wide, padding 128).
+    // Float data that are not integers in [0, 255] are clustered in the u8
+    // quantisation the graph builder uses.
     std::vector<uint8_t> v8(size_t(N + C) * Dp, uint8_t(128));
-    if (vec_dtype == GF_VEC_U8) {
-        const uint8_t* s = static_cast<const uint8_t*>(vectors);
-        for (uint32_t i = 0; i < N; ++i) std::memcpy(&v8[size_t(i) * Dp], s + size_t(i) * D, D);
-    } else {
-        const float* s = static_cast<const float*>(vectors);
-        for (uint32_t i = 0; i < N; ++i)
-            for (uint32_t k = 0; k < D; ++k) {
-                const float x = s[size_t(i) * D + k];
-                GF_REQUIRE(x >= 0.0f && x <= 255.0f && x == std::floor(x), GF_E_UNSUPPORTED,
-                           "kmeans: vectors must be integers in [0, 255]");
-                v8[size_t(i) * Dp + k] = uint8_t(x);
-            }
-    }
+    rows_u8(vectors, vec_dtype, N, D, Dp, float_data(vectors, vec_dtype, N, D), v8);
     for (uint32_t c = 0; c < C; ++c)
         std::memcpy(&v8[size_t(N + c) * Dp], &v8[size_t(init_ids[c]) * Dp], Dp);
     // Two "cells": the points (queries) and the centres (candidates); an
@@ -392,7 +478,7 @@ void kmeans_labels(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t 
     for (uint32_t c = 0; c < C; ++c) trow[size_t(Tp) * 16 + c] = N + c;
     const std::vector<uint32_t> ctile{0, Tp, ntile}, coff{0, N, N + C};
     std::vector<KnnItem> items;
-    for (uint32_t t = 0; t < Tp; t += 4) items.push_back(KnnItem{t, 0, 1});
+    for (uint32_t t = 0; t < Tp; t += QT) items.push_back(KnnItem{t, 0, 1});
 
     GF_HIP(hipSetDevice(device));
     int ncu = 0;

@@ -170,6 +170,23 @@ struct KnnArgs {
     uint64_t* state;
 };
 hipError_t launch_knn_i8(const KnnArgs& a, uint32_t KS, uint32_t ncu, hipStream_t st);
+uint32_t knn_ks(uint32_t D);    // k-steps of 64 dimensions the kNN kernel runs for D (0: D too large)
+uint32_t knn_qt(uint32_t KS);   // query tiles per wave for KS (items group this many)
+
+// Exact fp32 re-rank of kNN candidate lists (float data): one wave per list.
+struct RerankArgs {
+    const float* vec;         // cell-major fp32 rows of rowbytes, zero padded to whole 16-byte chunks
+    uint32_t rowbytes, nch;
+    const uint32_t* coff;     // P + 1 cell starts (cell-major rows)
+    const uint32_t* rowcell;  // cell of each cell-major row
+    const uint32_t* cmrow;    // cell-major row of each point id
+    const uint32_t* cand;     // candidate lists of nc cell-local ids
+    uint32_t nc, keep, P;
+    uint32_t graph;           // 1: list i = cell-major row i's own-cell candidates (itself excluded);
+                              // 0: list i = point i / P's candidates in cell i % P
+    uint32_t* out;            // keep ids per list
+};
+hipError_t launch_rerank(const RerankArgs& a, uint32_t D, uint32_t nlists, hipStream_t st);
 // Graph optimisation, first step: every row's I neighbours (cell-local ids,
 // rows cell-major, offset P + 1) rewritten in ascending (detourable routes,
 // rank) order.  I <= 64.

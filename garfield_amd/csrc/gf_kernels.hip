@@ -2741,7 +2741,7 @@ __global__ __launch_bounds__(64) void k_q_i8(const float* q, uint32_t D, int8_t*
 // per-query accumulator threshold, queue in LDS and are merged by the query's
 // owner lane into a register top-K of (distance << 32 | cell-local id) keys:
 // the result is the K smallest keys, ties broken by the smaller local id.
-template <int KS, int KT, int NB>
+template <int KS, int KT, int NB, int QT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KT > 40 ? 1 : 2))) void k_knn_i8(KnnArgs p) {
     __shared__ uint64_t s_buf[4][kQB * kBfBufQ];
     __shared__ uint32_t s_cnt[4][kQB];
@@ -2763,7 +2763,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KT > 40 ? 1
     for (uint32_t item = i_lo + k8 * 4u + wave; item < i_hi; item += nwg_x * 4u) {
         const KnnItem it = p.items[item];
         const uint32_t qc = it.qcell, tc = it.tcell;
-        const uint32_t qt = it.qtile, qt_end = min(qt + 4u, p.ctile[qc + 1]);
+        const uint32_t qt = it.qtile, qt_end = min(qt + uint32_t(QT), p.ctile[qc + 1]);
         // candidates: this launch's chunk of the target cell's tiles
         const uint32_t t0 = p.ctile[tc], tn = p.ctile[tc + 1];
         const uint32_t tb = t0 + p.chunk * p.ctiles;
@@ -2771,7 +2771,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KT > 40 ? 1
         const uint32_t t1 = min(tn, tb + p.ctiles);
         const bool first = p.chunk == 0, last = t1 == tn;
         const uint32_t q_lid = (qt - p.ctile[qc]) * 16u + lane;   // the owner's query, cell-local
-        const bool own_live = q_lid < p.coff[qc + 1] - p.coff[qc];
+        const bool own_live = lane < 16u * QT && q_lid < p.coff[qc + 1] - p.coff[qc];
         const uint32_t own_t = own_live ? qt + grp : qt;
         const int32_t own_nq = p.tnorm[size_t(own_t) * 32u + 16u + col];
         // the query's keys so far (earlier chunks), cell-major row order
@@ -2788,10 +2788,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KT > 40 ? 1
         cnt[lane] = 0;
         stp[lane] = own_live ? acc_threshold(own_nq, own_thr) : INT32_MAX;
         wave_fence();
-        v4i32_t B[4][KS];
-        int32_t tp[4];
+        v4i32_t B[QT][KS];
+        int32_t tp[QT];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < QT; ++j) {
             const uint32_t t = qt + j < qt_end ? qt + j : qt;
 #pragma unroll
             for (int k = 0; k < KS; ++k)
@@ -2829,7 +2829,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KT > 40 ? 1
             }
             wave_fence();
 #pragma unroll
-            for (int j = 0; j < 4; ++j) tp[j] = stp[16u * j + col];
+            for (int j = 0; j < QT; ++j) tp[j] = stp[16u * j + col];
         };
         // Operands of the next NB - 1 tiles are in flight while a tile is
         // computed (a ring of NB register stages, indexed statically; a
@@ -2851,19 +2851,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KT > 40 ? 1
             for (int b = 0; b < NB; ++b) {
                 const uint32_t t = ts + b;
                 if (t >= t1) break;
-                v4i32_t acc[4];
+                v4i32_t acc[QT];
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < QT; ++j)
                     acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b][0], B[j][0], mh[b], 0, 0, 0);
 #pragma unroll
                 for (int k = 1; k < KS; ++k)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
+                    for (int j = 0; j < QT; ++j)
                         acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b][k], B[j][k], acc[j], 0, 0, 0);
                 // any pass in the tile: one compare per column on the max of its four rows
                 bool anyl = false;
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < QT; ++j)
                     anyl |= max(max(acc[j][0], acc[j][1]), max(acc[j][2], acc[j][3])) >= tp[j];
                 if (__builtin_amdgcn_ballot_w64(anyl)) {
                     // The owner adds |q'|^2 to |x'|^2 - 2 q'.x' when it merges.
@@ -2871,7 +2871,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KT > 40 ? 1
                     const v4i32_t cmh = mh[b], cmn = mn[b];
                     bool full = false;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
+                    for (int j = 0; j < QT; ++j)
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
                             if (acc[j][i] >= tp[j]) {
@@ -2920,6 +2920,51 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KT > 40 ? 1
     }
 }
 
+// Exact fp32 re-rank of the candidate lists of float data (the kNN kernel
+// ran on a u8 quantisation of it): distances in the canonical summation
+// order of the row-distance helpers, candidates ordered by (distance,
+// cell-local id), repeats dropped; the first `keep` are written and a list
+// with fewer distinct candidates repeats its nearest (a graph row with none:
+// the point itself).
+template <int LPR, int CPL>
+__global__ __launch_bounds__(64) void k_rerank(RerankArgs p) {
+    __shared__ uint32_t S[64];
+    const uint32_t li = blockIdx.x, lane = lane_id();
+    uint32_t qrow, tc, self = kEmpty;
+    if (p.graph) {
+        qrow = li;
+        tc = p.rowcell[li];
+        self = li - p.coff[tc];
+    } else {
+        qrow = p.cmrow[li / p.P];
+        tc = li % p.P;
+    }
+    const uint32_t base = p.coff[tc], size = p.coff[tc + 1] - base;
+    if (!size) return;   // lists into empty cells keep their zeros
+    QReg<0, LPR, CPL> qv;
+    const char* vec = reinterpret_cast<const char*>(p.vec);
+    load_query<0, LPR, CPL>(qv, vec + size_t(qrow) * p.rowbytes, p.nch);
+    const uint32_t lid = lane < p.nc ? p.cand[size_t(li) * p.nc + lane] : kEmpty;
+    bool ok = lid < size && lid != self;
+    for (uint32_t k = 0; k < 64u; ++k)
+        if (k < lane && readlane32(lid, k) == lid) ok = false;   // a repeat: its first lane keeps it
+    const uint64_t m = ballot(ok);
+    const uint32_t n = __popcll(m);
+    const uint32_t ci = ok ? lanes_below(m) : 0xFFFFFFFFu;
+    if (ok) S[ci] = base + lid;
+    wave_sync();
+    float d = __int_as_float(0x7F800000);
+    if (n) eval_rows<0, LPR, CPL>(qv, vec, p.rowbytes, p.nch, S, n, ci, d);
+    const uint64_t key = ok ? (uint64_t(__float_as_uint(d)) << 32) | lid : ~uint64_t(0);
+    uint32_t rk = 0;
+    for (uint32_t k = 0; k < 64u; ++k) rk += readlane64(key, k) < key;
+    uint32_t* o = p.out + size_t(li) * p.keep;
+    if (ok && rk < p.keep) o[rk] = lid;
+    const uint64_t nm = ballot(ok && rk == 0);
+    const uint32_t nearest = nm ? readlane32(lid, uint32_t(__builtin_ctzll(nm))) : (p.graph ? self : 0u);
+    for (uint32_t j = n + lane; j < p.keep; j += 64u) o[j] = nearest;
+}
+
 // k-means update of the index builder (integer Lloyd step): the members of
 // each cluster are listed (count, scan, scatter), then one workgroup per
 // cluster sums its members' u8 rows, a thread per dimension, and moves the
@@ -2941,24 +2986,26 @@ __global__ void k_kmeans_scatter(const uint32_t* lab2, uint32_t N, const uint32_
 
 __global__ __launch_bounds__(256) void k_kmeans_mean(const uint8_t* vec, uint32_t Dp, const uint32_t* cnt,
                                                      const uint32_t* start, const uint32_t* mem, uint8_t* centres) {
-    const uint32_t c = blockIdx.x, d = threadIdx.x;
+    const uint32_t c = blockIdx.x;
     const uint32_t n = cnt[c], s0 = start[c];
-    if (n == 0 || d >= Dp) return;
-    // eight members' rows in flight at a time
-    uint32_t sum8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    uint32_t k = 0;
-    for (; k + 8u <= n; k += 8u) {
-        uint32_t m[8];
+    if (n == 0) return;
+    for (uint32_t d = threadIdx.x; d < Dp; d += blockDim.x) {
+        // eight members' rows in flight at a time
+        uint32_t sum8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        uint32_t k = 0;
+        for (; k + 8u <= n; k += 8u) {
+            uint32_t m[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) m[i] = mem[s0 + k + i];
+            for (int i = 0; i < 8; ++i) m[i] = mem[s0 + k + i];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) sum8[i] += vec[size_t(m[i]) * Dp + d];
+            for (int i = 0; i < 8; ++i) sum8[i] += vec[size_t(m[i]) * Dp + d];
+        }
+        uint64_t sum = 0;
+        for (; k < n; ++k) sum += vec[size_t(mem[s0 + k]) * Dp + d];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum += sum8[i];
+        centres[size_t(c) * Dp + d] = uint8_t((2 * sum + n) / (2 * uint64_t(n)));
     }
-    uint64_t sum = 0;
-    for (; k < n; ++k) sum += vec[size_t(mem[s0 + k]) * Dp + d];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) sum += sum8[i];
-    centres[size_t(c) * Dp + d] = uint8_t((2 * sum + n) / (2 * uint64_t(n)));
 }
 
 // Rank-based reordering of a kNN graph, the first step of CAGRA's graph
@@ -3013,12 +3060,12 @@ hipError_t launch_prune(const uint32_t* knn, uint32_t N, uint32_t I, const uint3
     return hipGetLastError();
 }
 
-template <int KS, int KT, int NB = 1>
+template <int KS, int KT, int NB = 1, int QT = 4>
 static hipError_t launch_knn_i8_t(const KnnArgs& a, uint32_t ncu, hipStream_t st) {
     static int per_cu = 0;
     if (!per_cu) {
         int n = 0;
-        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_knn_i8<KS, KT, NB>, 256, 0);
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_knn_i8<KS, KT, NB, QT>, 256, 0);
         if (e != hipSuccess) return e;
         per_cu = n > 0 ? n : 1;
     }
@@ -3026,9 +3073,23 @@ static hipError_t launch_knn_i8_t(const KnnArgs& a, uint32_t ncu, hipStream_t st
     if (a.nitems == 0) return hipSuccess;
     const uint32_t need = ((a.nitems + 3u) / 4u + 7u) / 8u * 8u;
     const uint32_t grid = max(8u, min(ncu * uint32_t(per_cu), need));
-    hipLaunchKernelGGL((k_knn_i8<KS, KT, NB>), dim3(grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((k_knn_i8<KS, KT, NB, QT>), dim3(grid), dim3(256), 0, st, a);
     return hipGetLastError();
 }
+
+// KS (k-steps of 64 dimensions) 1 to 4: four query tiles per wave; 6, 8, 12
+// and 16 (dimensions up to 1024): one query tile per wave, so that the query
+// operand (QT x KS registers of 16 bytes) stays in registers.
+uint32_t knn_ks(uint32_t D) {
+    const uint32_t ks = (D + 63) / 64;
+    if (ks <= 4) return ks;
+    if (ks <= 6) return 6;
+    if (ks <= 8) return 8;
+    if (ks <= 12) return 12;
+    return ks <= 16 ? 16 : 0;
+}
+
+uint32_t knn_qt(uint32_t KS) { return KS <= 4 ? 4u : 1u; }
 
 hipError_t launch_knn_i8(const KnnArgs& a, uint32_t KS, uint32_t ncu, hipStream_t st) {
     if (a.K == 0 || a.K > kKnnKMax || ncu == 0 || (a.R && a.K != a.R + 1)) return hipErrorInvalidValue;
@@ -3039,18 +3100,30 @@ hipError_t launch_knn_i8(const KnnArgs& a, uint32_t KS, uint32_t ncu, hipStream_
         if (a.K <= 40) return launch_knn_i8_t<KS_, 40, 2>(a, ncu, st);   \
         return launch_knn_i8_t<KS_, 72>(a, ncu, st);                     \
     }
+#define KNN1(KS_)                                                          \
+    if (KS == KS_) {                                                       \
+        if (a.K <= 4) return launch_knn_i8_t<KS_, 4, 1, 1>(a, ncu, st);   \
+        if (a.K <= 16) return launch_knn_i8_t<KS_, 16, 1, 1>(a, ncu, st); \
+        if (a.K <= 40) return launch_knn_i8_t<KS_, 40, 1, 1>(a, ncu, st); \
+        return launch_knn_i8_t<KS_, 72, 1, 1>(a, ncu, st);                \
+    }
     KNN(1)
     KNN(2)
     KNN(3)
     KNN(4)
+    KNN1(6)
+    KNN1(8)
+    KNN1(12)
+    KNN1(16)
 #undef KNN
+#undef KNN1
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_kmeans_update(const uint8_t* vec, uint32_t Dp, const uint32_t* lab2, uint32_t N, uint32_t C,
                                 uint32_t* cnt, uint32_t* start, uint32_t* fill, uint32_t* mem, uint8_t* centres,
                                 hipStream_t st) {
-    if (N == 0 || C == 0 || Dp > 256) return N == 0 || C == 0 ? hipSuccess : hipErrorInvalidValue;
+    if (N == 0 || C == 0 || Dp > 1024) return N == 0 || C == 0 ? hipSuccess : hipErrorInvalidValue;
     const uint32_t g = (N + 255) / 256;
     hipLaunchKernelGGL(k_kmeans_count, dim3(g), dim3(256), 0, st, lab2, N, cnt);
     hipError_t e = launch_scan_small(cnt, C, start, st);
@@ -3147,6 +3220,23 @@ hipError_t launch_bruteforce(const RowShape& rs, const TravArgs& a, uint32_t gri
 #undef CALL_B
     return hipErrorInvalidValue;
 }
+
+template <int L_, int C_>
+static hipError_t launch_rerank_t(const RerankArgs& a, uint32_t nlists, hipStream_t st) {
+    hipLaunchKernelGGL((k_rerank<L_, C_>), dim3(nlists), dim3(64), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_rerank(const RerankArgs& a, uint32_t D, uint32_t nlists, hipStream_t st) {
+    if (!nlists) return hipSuccess;
+    if (a.nc == 0 || a.nc > 64 || a.keep == 0) return hipErrorInvalidValue;
+    const RowShape rs = row_shape(D, 0);
+#define CALL_R(V, L_, C_) launch_rerank_t<L_, C_>(a, nlists, st)
+    GF_DISPATCH_VT(0, CALL_R);
+#undef CALL_R
+    return hipErrorInvalidValue;
+}
+
 
 // The kernel's waves are persistent and split the items evenly, so the grid
 // is exactly the workgroups that fit on the device at once (a workgroup that

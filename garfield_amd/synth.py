@@ -228,8 +228,9 @@ def build_index(vectors, attrs, grid, R, E, C=0, kmeans_iters=8, seed=5, device=
     """All index arrays, in the layout the files hold.  arith = (attr_min,
     attr_width) builds the cells on an arithmetic grid instead of rank quantiles.
     device "hip": the library's builder (gf_grid_scatter, the int8 MFMA
-    gf_build_graphs and gf_kmeans; integer data only); else torch on that
-    device.  graph "cagra" (device "hip" only): exact kNN graphs of degree
+    gf_build_graphs and gf_kmeans; non-integer data through their u8
+    quantisation, graphs re-ranked by exact fp32 distances); else torch on
+    that device.  graph "cagra" (device "hip" only): exact kNN graphs of degree
     `inter`, optimised to degree R by gf_optimize_graphs (the graph
     cagra.build returns); "knn": exact kNN graphs of degree R."""
     grid = np.asarray(grid, np.int64)

@@ -320,9 +320,15 @@ typedef struct {
  * excludes the point itself; a row with fewer candidates than it holds
  * repeats its nearest (a point alone in its cell lists itself); edges into
  * an empty cell are 0.  vectors: N*D in point-id order, GF_VEC_U8 bytes or
- * GF_VEC_F32 integers in [0, 255] (other data is GF_E_UNSUPPORTED); D up to
- * 256; R + 1 and E up to 72.  cell_graphs (N*R) or cross (N*P*E) may be NULL
- * to skip that graph.  Runs on HIP device `device`; stats may be NULL. */
+ * GF_VEC_F32.  u8 data and floats that are all integers in [0, 255] get
+ * exact neighbours from int8 MFMA distances.  Other float data: the same
+ * kernels on the u8 quantisation rint((x - min) / s), s = (max - min) / 255
+ * over all values, keep 16 more candidates per list (at most 63 per graph
+ * row, 64 per cross list), which are then ordered by exact fp32 distance
+ * (the traversal's summation order), repeats dropped.  D up to 1024; R + 1
+ * and E up to 72 (float data: R up to 63, E up to 64).  cell_graphs (N*R)
+ * or cross (N*P*E) may be NULL to skip that graph.  Runs on HIP device
+ * `device`; stats may be NULL. */
 gf_status gf_build_graphs(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D,
                           const uint32_t* global_pid, uint32_t P, uint32_t R, uint32_t E, int32_t device,
                           uint32_t* cell_graphs, uint32_t* cross, gf_build_stats* stats);
@@ -350,8 +356,10 @@ gf_status gf_optimize_graphs(const uint32_t* knn_graphs, uint32_t N, uint32_t I,
  * distance (ties to the smaller centre index); an update moves each centre
  * to the rounded mean floor((2 sum + n) / (2 n)) of its n members (an empty
  * cluster keeps its centre).  `iters` assign + update rounds, then a final
- * assignment gives the labels.  Same data limits as gf_build_graphs;
- * centres (C*D bytes) may be NULL; ms (wall time of the call) may be NULL. */
+ * assignment gives the labels.  D up to 1024; float data that are not all
+ * integers in [0, 255] are clustered in gf_build_graphs' u8 quantisation
+ * (centres are then in its units).  centres (C*D bytes) may be NULL; ms
+ * (wall time of the call) may be NULL. */
 gf_status gf_kmeans(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, uint32_t C, uint32_t iters,
                     const uint32_t* init_ids, int32_t device, int32_t* labels /*N*/, uint8_t* centres /*C*D*/,
                     double* ms);

@@ -923,6 +923,10 @@ void orc_full_graph(const orc_index* ix, uint32_t FE, uint32_t* out) {
         }
 }
 
+void orc_canon_dists(const float* q, const float* X, uint32_t n, uint32_t D, float* out) {
+    for (uint32_t i = 0; i < n; ++i) out[i] = canon_dist(q, X + (size_t)i * D, D, 0);
+}
+
 float orc_distance(const orc_index* ix, const void* q, uint32_t gid) {
     std::vector<float> qv(ix->D), xv(ix->D);
     if (ix->vdtype != 1)

@@ -134,6 +134,9 @@ void orc_entry_draw(uint32_t range, uint32_t ndraw, uint32_t R, uint32_t* out);
 /* Canonical squared L2 distance between query q and point gid (the HIP
  * kernels' summation order). */
 float orc_distance(const orc_index* ix, const void* q, uint32_t gid);
+/* Canonical fp32 distances (the kernels' summation order for fp32 rows) of
+ * query q to the n rows of X (n*D). */
+void orc_canon_dists(const float* q, const float* X, uint32_t n, uint32_t D, float* out);
 
 /* gpu_graph.cu:3266-4131 fused kernel (+ host wrapper 12463-12616):
  * cell-by-cell traversal or filtered brute force per query.

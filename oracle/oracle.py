@@ -521,6 +521,88 @@ def cross_rows(vectors, global_pid, P, E, rows):
     return out
 
 
+def quantise_u8(vectors):
+    """The builder's u8 quantisation of float data for its candidate pass:
+    rint((x - min) / s), s = (max - min) / 255, in float64 over all values
+    (all 0 when they are equal)."""
+    v = np.asarray(vectors, np.float32).astype(np.float64)
+    lo, hi = v.min(), v.max()
+    s = (hi - lo) / 255.0
+    q = np.rint((v - lo) / s) if s > 0 else np.zeros_like(v)
+    return np.clip(q, 0, 255).astype(np.uint8)
+
+
+def canon_dists(q, X):
+    """Canonical fp32 distances of query q to the rows of X (the kernels'
+    summation order for fp32 rows, garfield_oracle.cpp canon_dist)."""
+    lib = load()
+    q = np.ascontiguousarray(q, np.float32)
+    X = np.ascontiguousarray(X, np.float32)
+    out = np.empty(X.shape[0], np.float32)
+    lib.orc_canon_dists(_p(q), _p(X), C.c_uint32(X.shape[0]), C.c_uint32(q.size), _p(out))
+    return out
+
+
+def _rerank(q, X, cand, keep, fill):
+    """Candidate local ids re-ranked by (canonical fp32 distance, id),
+    repeats and ids in `drop` removed; the first `keep`, a short list
+    repeating its nearest (or `fill` when empty)."""
+    ids = list(dict.fromkeys(int(c) for c in cand))
+    if not ids:
+        return [fill] * keep
+    d = canon_dists(q, X[ids])
+    order = sorted(range(len(ids)), key=lambda i: (d[i].view(np.uint32), ids[i]))
+    out = [ids[i] for i in order][:keep]
+    return out + [out[0]] * (keep - len(out))
+
+
+FLOAT_MARGIN = 16
+
+
+def float_graph_rows(vectors, global_pid, P, R, rows, margin=FLOAT_MARGIN, mutation=0):
+    """Per-cell graph rows of float data for the points `rows`: the
+    candidates are graph_rows of the u8 quantisation (quantise_u8) at degree
+    min(R + margin, 63); they are re-ranked by canonical fp32 distance (ties
+    by local id), repeats and the point itself dropped, and the first R kept
+    (a short row repeats its nearest; a point alone lists itself).
+    mutation (tests only): 1 re-ranks by the quantised order (no re-rank)."""
+    v = np.asarray(vectors, np.float32)
+    gp = np.asarray(global_pid)
+    Rk = min(R + margin, 63)
+    cand = graph_rows(quantise_u8(v), gp, P, Rk, rows)
+    mem = _members(gp, P)
+    out = np.empty((len(rows), R), np.uint32)
+    for i, p in enumerate(rows):
+        m = mem[gp[p]]
+        self_lid = int(np.searchsorted(m, p))
+        c = [x for x in cand[i] if x != self_lid]
+        if mutation == 1:
+            c = list(dict.fromkeys(int(x) for x in c))[:R]
+            out[i] = (c + [c[0]] * (R - len(c))) if c else [self_lid] * R
+            continue
+        out[i] = _rerank(v[p], v[m], c, R, self_lid)
+    return out
+
+
+def float_cross_rows(vectors, global_pid, P, E, rows, margin=FLOAT_MARGIN):
+    """Cross-cell rows of float data for the points `rows`: for every
+    non-empty cell, cross_rows of the u8 quantisation with min(E + margin,
+    64) candidates, re-ranked by canonical fp32 distance (ties by local id),
+    repeats dropped, the first E kept (a short list repeats its nearest);
+    edges into an empty cell are 0."""
+    v = np.asarray(vectors, np.float32)
+    gp = np.asarray(global_pid)
+    Ek = min(E + margin, 64)
+    cand = cross_rows(quantise_u8(v), gp, P, Ek, rows)
+    out = np.zeros((len(rows), P * E), np.uint32)
+    for c, m in enumerate(_members(gp, P)):
+        if len(m) == 0:
+            continue
+        for i, p in enumerate(rows):
+            out[i, c * E:(c + 1) * E] = _rerank(v[p], v[m], cand[i, c * Ek:(c + 1) * Ek], E, 0)
+    return out
+
+
 def detour_order(knn_cell):
     """One cell's kNN rows (n x I, local ids) in ascending (detourable
     routes, rank) order, the reordering step of CAGRA's graph optimisation

@@ -36,6 +36,13 @@ def world32():
     return cfg, ix
 
 
+def _float_index_device():
+    """Non-integer worlds are built by the library's builder where a GPU is
+    present (its float-data mode), by torch on the CPU otherwise."""
+    import torch
+    return "hip" if torch.cuda.is_available() else "cpu"
+
+
 @pytest.fixture(scope="session")
 def world_gauss():
     """Config-3-shaped (shrunk): 96-d Gaussian unit vectors, 3 Zipf attributes on
@@ -49,7 +56,7 @@ def world_gauss():
     sel = synth.log_uniform(Q, 0.001, 0.5, 43)
     lo, hi = synth.ranges_for_selectivity(Q, 3, sel, 44, hi=400)
     cfg = dict(vectors=vec, attrs=att, grid=[4, 4, 4], R=32, E=2, C=16, queries=qv, lo=lo, hi=hi)
-    ix = synth.build_index(vec, att, cfg["grid"], 32, 2, 16, seed=6)
+    ix = synth.build_index(vec, att, cfg["grid"], 32, 2, 16, seed=6, device=_float_index_device())
     return cfg, ix
 
 
@@ -65,7 +72,7 @@ def world_c4():
     qv, _ = synth.gmm_vectors(Q, 768, ncomp, 72)
     lo, hi = synth.ranges_for_selectivity(Q, 2, 0.1, 73, hi=10 * ncomp)
     cfg = dict(vectors=vec, attrs=att, grid=[4, 4], R=32, E=2, C=16, queries=qv, lo=lo, hi=hi)
-    ix = synth.build_index(vec, att, cfg["grid"], 32, 2, 16, seed=74)
+    ix = synth.build_index(vec, att, cfg["grid"], 32, 2, 16, seed=74, device=_float_index_device())
     return cfg, ix
 
 

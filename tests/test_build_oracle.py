@@ -199,14 +199,14 @@ def test_builder_rejects_bad_input_before_device():
     gp = np.zeros(10, np.uint32)
     v[3, 5] = 0.5
     with pytest.raises(GarfieldError) as e:
-        _lib.build_graphs(v, gp, 1, 4, 2)
-    assert e.value.status == 6   # GF_E_UNSUPPORTED: not integers in [0, 255]
+        _lib.build_graphs(v, gp, 1, 64, 2)
+    assert e.value.status == 6   # GF_E_UNSUPPORTED: float data (not integers in [0, 255]) with R above 63
     with pytest.raises(GarfieldError) as e:
         _lib.build_graphs(np.zeros((10, 64), np.uint8), gp, 1, 72, 2)
     assert e.value.status == 6   # R + 1 above 72
     with pytest.raises(GarfieldError) as e:
-        _lib.build_graphs(np.zeros((10, 300), np.uint8), gp, 1, 4, 2)
-    assert e.value.status == 6   # dimension above 256
+        _lib.build_graphs(np.zeros((10, 1100), np.uint8), gp, 1, 4, 2)
+    assert e.value.status == 6   # dimension above 1024
     with pytest.raises(GarfieldError) as e:
         _lib.build_graphs(np.zeros((10, 64), np.uint8), gp + 1, 1, 4, 2)
     assert e.value.status == 1   # a cell id >= P
@@ -268,3 +268,90 @@ def test_optimised_graph_properties():
             assert len(set(row)) == 12 and a not in row and max(row) < n
             assert row[:6] == o[a, :6].tolist()
         start += n
+
+
+# ------------------------------------------------------------ float data
+def test_quantise_u8_known_answers():
+    # s = 1: rint(x), halves to even (127.5 -> 128, 0.5 -> 0, 2.5 -> 2)
+    v = np.array([[0.0, 255.0, 127.5, 0.5, 2.5]], np.float32)
+    assert list(orc.quantise_u8(v)[0]) == [0, 255, 128, 0, 2]
+    assert list(orc.quantise_u8(np.full((2, 3), 7.0, np.float32)).ravel()) == [0] * 6
+    v = np.array([[-2.0, 2.0, 0.0]], np.float32)
+    assert list(orc.quantise_u8(v)[0]) == [0, 255, 128]
+
+
+def test_canon_dists_close_to_float64():
+    rng = np.random.default_rng(4)
+    X = rng.standard_normal((64, 768)).astype(np.float32)
+    d = orc.canon_dists(X[0], X)
+    ref = ((X.astype(np.float64) - X[0]) ** 2).sum(1)
+    assert d[0] == 0.0
+    assert np.allclose(d, ref, rtol=1e-5)
+
+
+def _exact_rows(v, gp, P, K, rows, cross):
+    """Brute force in float64: (distance, local id) order, a different form
+    (Python tuple sorts) from the oracle's re-rank."""
+    v64 = np.asarray(v, np.float64)
+    mem = [np.nonzero(gp == c)[0] for c in range(P)]
+    out = []
+    for p in rows:
+        cells = range(P) if cross else [gp[p]]
+        row = []
+        for c in cells:
+            m = mem[c]
+            items = sorted((float(((v64[x] - v64[p]) ** 2).sum()), l) for l, x in enumerate(m)
+                           if cross or x != p)
+            row.append([l for _, l in items[:K]])
+        out.append(row)
+    return out
+
+
+@pytest.mark.parametrize("D,mut", [(96, 0), (96, 1), (200, 0)])
+def test_float_rows_are_exact_neighbours(D, mut):
+    """On Gaussian, L2-normalised data (config 3's kind) the re-ranked rows
+    are the exact float64 nearest neighbours, except between distances within
+    1e-6 of each other; without the re-rank (mutation 1, the quantised order)
+    they are not."""
+    rng = np.random.default_rng(D)
+    N, P, R, E = 1200, 4, 16, 3
+    v = rng.standard_normal((N, D)).astype(np.float32)
+    v /= np.linalg.norm(v, axis=1, keepdims=True)
+    gp = rng.integers(0, P, N).astype(np.uint32)
+    rows = rng.choice(N, 40, replace=False)
+    g = orc.float_graph_rows(v, gp, P, R, rows, mutation=mut)
+    ex = _exact_rows(v, gp, P, R, rows, False)
+    v64 = v.astype(np.float64)
+    mem = [np.nonzero(gp == c)[0] for c in range(P)]
+    bad = 0
+    for i, p in enumerate(rows):
+        m = mem[gp[p]]
+        dg = ((v64[m[g[i]]] - v64[p]) ** 2).sum(1)
+        de = ((v64[m[ex[i][0]]] - v64[p]) ** 2).sum(1)
+        bad += not np.allclose(dg, de, rtol=0, atol=1e-6)
+    if mut:
+        assert bad > 0
+        return
+    assert bad == 0
+    x = orc.float_cross_rows(v, gp, P, E, rows[:10])
+    exc = _exact_rows(v, gp, P, E, rows[:10], True)
+    for i, p in enumerate(rows[:10]):
+        for c in range(P):
+            m = mem[c]
+            dx = ((v64[m[x[i, c * E:(c + 1) * E]]] - v64[p]) ** 2).sum(1)
+            de = ((v64[m[exc[i][c]]] - v64[p]) ** 2).sum(1)
+            assert np.allclose(dx, de, rtol=0, atol=1e-6), (p, c)
+
+
+def test_float_rows_short_cells():
+    """Cells smaller than the degree: rows repeat their nearest, a point
+    alone lists itself, cross edges into an empty cell are 0."""
+    rng = np.random.default_rng(9)
+    v = rng.standard_normal((7, 32)).astype(np.float32)
+    gp = np.array([0, 0, 0, 1, 2, 2, 2], np.uint32)   # cell 3 empty
+    g = orc.float_graph_rows(v, gp, 4, 4, [0, 3])
+    assert g[1].tolist() == [0, 0, 0, 0]              # alone: itself (local id 0)
+    assert len(set(g[0].tolist())) == 2 and g[0][2] == g[0][3] == g[0][0]
+    x = orc.float_cross_rows(v, gp, 4, 2, [3])
+    assert x[0, 6:8].tolist() == [0, 0]
+    assert x[0, 2:4].tolist() == [0, 0]               # cell 1 holds only the point itself

@@ -182,3 +182,73 @@ def test_optimised_graph_search():
         dev.close()
     print(f"recall at L=64: exact kNN {rec['knn']:.4f}, optimised {rec['cagra']:.4f}", flush=True)
     assert abs(rec["cagra"] - rec["knn"]) < 0.1
+
+
+def _float_check(v, gp, P, R, E):
+    """Float data: the library's graphs against the oracle's restatement
+    (candidates from the u8 quantisation, exact fp32 re-rank), every row."""
+    g, x, st = _lib.build_graphs(v, gp, P, R, E)
+    order = np.argsort(gp, kind="stable")          # cell-major row i = point order[i]
+    og = oracle.float_graph_rows(v, gp, P, R, order)
+    bad = np.nonzero(np.any(g != og, axis=1))[0]
+    assert bad.size == 0, f"{bad.size} graph rows differ, first {bad[:4]}: {g[bad[0]]} vs {og[bad[0]]}"
+    ox = oracle.float_cross_rows(v, gp, P, E, np.arange(v.shape[0]))
+    bad = np.nonzero(np.any(x != ox, axis=1))[0]
+    assert bad.size == 0, f"{bad.size} cross rows differ, first {bad[:4]}"
+    return st
+
+
+@pytest.mark.parametrize("N,D,grid,R,E,kind", [
+    (3000, 96, [2, 2], 16, 2, "gauss"),       # config 3's data: Gaussian, L2-normalised
+    (1200, 768, [2, 2], 32, 2, "gmm"),        # config 4's data: 768-d mixture (12 k-steps, one query tile per wave)
+    (1500, 300, [3, 1], 8, 4, "gauss"),       # D padded to 384 (6 k-steps)
+    (600, 64, [2, 3], 40, 20, "gmm"),         # cells of ~100 points: K' = 56 and 36 candidates
+])
+def test_build_float_matches_oracle(N, D, grid, R, E, kind):
+    _print_case("build-float", N=N, D=D, grid=grid, R=R, E=E, kind=kind)
+    rng = np.random.default_rng(N + D)
+    if kind == "gauss":
+        v = rng.standard_normal((N, D)).astype(np.float32)
+        v /= np.linalg.norm(v, axis=1, keepdims=True)
+    else:
+        cen = rng.standard_normal((20, D))
+        cen /= np.linalg.norm(cen, axis=1, keepdims=True)
+        v = (cen[rng.integers(0, 20, N)] + 0.1 * rng.standard_normal((N, D))).astype(np.float32)
+    att = rng.integers(0, 1000, (N, len(grid))).astype(np.float32)
+    _, _, _, gp = _lib.grid_scatter(att, grid)
+    _float_check(v, gp, int(np.prod(grid)), R, E)
+
+
+@pytest.mark.parametrize("D", [512, 1000])
+def test_build_wide_integer_rows(D):
+    """u8 rows of 512 and 1000 dimensions (8 and 16 k-steps, one query tile
+    per wave): exact integer neighbours, bit-exact against the oracle."""
+    _print_case("build-wide", D=D)
+    rng = np.random.default_rng(D)
+    v = rng.integers(0, 256, (900, D)).astype(np.uint8)
+    att = rng.integers(0, 1000, (900, 2)).astype(np.float32)
+    _, _, _, gp = _lib.grid_scatter(att, [2, 2])
+    st = _check(v, gp, 4, 12, 3)
+    assert st.dim == (512 if D == 512 else 1024)
+
+
+@pytest.mark.parametrize("N,D,C,kind", [(3000, 96, 24, "gauss"), (1500, 768, 12, "gmm"), (2000, 512, 20, "u8")])
+def test_kmeans_float_and_wide(N, D, C, kind):
+    """k-means of float data runs on the builder's u8 quantisation (the
+    oracle quantises, then runs its integer Lloyd rounds); 512 and 768
+    dimensions take the one-query-tile kernel."""
+    _print_case("kmeans-float", N=N, D=D, C=C, kind=kind)
+    rng = np.random.default_rng(N + D)
+    if kind == "u8":
+        v = rng.integers(0, 256, (N, D)).astype(np.uint8)
+        ref = v
+    else:
+        v = rng.standard_normal((N, D)).astype(np.float32)
+        if kind == "gauss":
+            v /= np.linalg.norm(v, axis=1, keepdims=True)
+        ref = oracle.quantise_u8(v)
+    init = rng.choice(N, C, replace=False)
+    lab, cen, _ = _lib.kmeans(v, C, 3, init_ids=init)
+    olab, ocen = oracle.kmeans(ref, C, 3, init)
+    assert np.array_equal(cen, ocen), "centres differ"
+    assert np.array_equal(lab, olab), "labels differ"
