@@ -50,6 +50,8 @@ def main():
     ap.add_argument("--stream-q", type=int, default=10_000)
     ap.add_argument("--stream-budget-mb", type=int, default=64)
     ap.add_argument("--stream-thresholds", default="1.0,0.25,0.0")
+    ap.add_argument("--cross-search-ef", type=int, default=32,
+                    help="build workload: list length of the search-based cross edges timed beside the exact ones")
     ap.add_argument("--stream-plan", choices=["planned", "static"], default="planned",
                     help="planned: batches planned from the query batch's cell lists (gf_stream_plan_cells), "
                          "timed beside the reference's static plan of 16 consecutive cells per batch; "
@@ -385,6 +387,18 @@ def build_bench(args):
         f"gf_build_graphs {acc['total'] / K:.1f} ms = prep {acc['prep'] / K:.1f} + upload {acc['upload'] / K:.1f} "
         f"+ run {acc['run'] / K:.1f} + download {acc['download'] / K:.1f}; gf_kmeans (C={cfg['C']}, 8 rounds) "
         f"{ms_kmeans / K:.1f} ms")
+    # Cross edges by per-cell graph search (global_graph_build.py's method,
+    # the route to indexes too large for N x N distances), on the same graphs:
+    # time and the share of the exact edges it finds.
+    from garfield_amd.global_graph import global_graph_build
+    t0 = time.perf_counter()
+    xs = global_graph_build(v, gp, P, g, E, ef=args.cross_search_ef, batch=1 << 17)
+    ms_xs = (time.perf_counter() - t0) * 1e3
+    samp = np.random.default_rng(1).choice(N, 2000, replace=False)
+    found = np.mean([len(set(xs[p, c * E:(c + 1) * E]) & set(x[p, c * E:(c + 1) * E])) / E
+                     for p in samp for c in range(P)])
+    log(f"cross edges by per-cell search (ef={args.cross_search_ef}): {ms_xs:.0f} ms, "
+        f"{found:.4f} of the exact edges found")
     cpu = None
     if not args.no_cpu:
         # the oracle's exact rows (numpy, float64 BLAS dot products) for a
@@ -415,7 +429,10 @@ def build_bench(args):
                    "ms_cross": round(ms_cross, 3), "pairs_cross": st.pairs_cross, "pairs_graph": st.pairs_graph,
                    "ms_call": round(acc["total"] / K, 3), "ms_host_prep": round(acc["prep"] / K, 3),
                    "ms_upload": round(acc["upload"] / K, 3), "ms_download": round(acc["download"] / K, 3),
-                   "C": cfg["C"], "kmeans_rounds": 8, "ms_kmeans": round(ms_kmeans / K, 3)},
+                   "C": cfg["C"], "kmeans_rounds": 8, "ms_kmeans": round(ms_kmeans / K, 3),
+                   "cross_by_search": {"ef": args.cross_search_ef, "ms": round(ms_xs, 1),
+                                       "exact_edges_found": round(float(found), 4),
+                                       "searches": N * P}},
         "roofline": {"bound": "mfma", "kernel": "k_knn_i8 (cross edges)", "achieved": round(tops, 1),
                      "peak": INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
                      "traffic": None, "ms_per_launch": round(ms_cross, 4)},

@@ -252,3 +252,43 @@ def test_kmeans_float_and_wide(N, D, C, kind):
     olab, ocen = oracle.kmeans(ref, C, 3, init)
     assert np.array_equal(cen, ocen), "centres differ"
     assert np.array_equal(lab, olab), "labels differ"
+
+
+def test_global_graph_by_search():
+    """Approximate cross edges by per-cell graph search (the method of
+    global_graph_build.py:106-176): bit-exact against the oracle's traversal
+    run the same way (one cell per query, no filter, list length ef, E
+    results, local ids), empty cells 0; and close to the exact cross edges."""
+    from garfield_amd.global_graph import global_graph_build
+    _print_case("global-graph-search")
+    rng = np.random.default_rng(31)
+    N, D, P, R, E, ef = 4000, 64, 16, 16, 2, 32
+    v = rng.integers(0, 256, (N, D)).astype(np.uint8)
+    att = rng.integers(0, 1000, (N, 2)).astype(np.float32)
+    _, _, _, gp = _lib.grid_scatter(att, [4, 4])
+    gp = gp.copy()
+    gp[gp == 5] = 6                                    # cell 5 empty
+    g, x_exact, _ = _lib.build_graphs(v, gp, P, R, E)
+    x = global_graph_build(v, gp, P, g, E, ef=ef, batch=1500)
+    O = oracle.OracleIndex(v.astype(np.float32), np.zeros((N, 1), np.float32), gp, P, g, np.zeros((N, P), np.uint32),
+                           u8=True)
+    ent = _lib.entry_points(N, P, R)
+    sizes = np.bincount(gp, minlength=P)
+    order = np.argsort(gp, kind="stable")
+    lrow = np.empty(N, np.int64)
+    lrow[order] = np.arange(N) - np.concatenate([[0], np.cumsum(sizes)])[gp[order]]
+    lo, hi = np.full((N, 1), -1.0, np.float32), np.full((N, 1), 1.0, np.float32)
+    for c in range(P):
+        if not sizes[c]:
+            assert not x[:, c * E:(c + 1) * E].any()
+            continue
+        cells = np.zeros((N, P), np.uint32)
+        cells[:, 0] = c
+        ids, _, _ = O.search(v.astype(np.float32), lo, hi, cells, np.ones(N, np.uint32), np.zeros(N, np.uint32),
+                             ent, ef, K=E)
+        assert np.all(ids != 0x7FFFFFFF)
+        assert np.array_equal(x[:, c * E:(c + 1) * E], lrow[ids]), c
+    hit = np.mean([len(set(x[p, c * E:(c + 1) * E]) & set(x_exact[p, c * E:(c + 1) * E])) / E
+                   for p in range(0, N, 7) for c in range(P) if sizes[c]])
+    print(f"[global-graph] exact cross edges found: {hit:.3f}", flush=True)
+    assert hit > 0.9
