@@ -15,8 +15,8 @@ All computation runs in the HIP library; every call raises if the library has
 not been built or cannot reach a GPU, and there is no CPU fallback.
 """
 from ._lib import (GarfieldError, Index, Batch, SearchStats, BuildStats, lib_path, f2h, row_norms_f16,
-                   entry_points, grid_scatter, plan_cells, build_graphs, optimize_graphs, kmeans, pinned_empty, search_noalloc, NO_RESULT, NCOUNTERS,
-                   VEC_F32, VEC_F16, VEC_U8)
+                   entry_points, grid_scatter, plan_cells, quantise_i8, build_graphs, optimize_graphs, kmeans, pinned_empty, search_noalloc, NO_RESULT, NCOUNTERS,
+                   VEC_F32, VEC_F16, VEC_U8, VEC_I8Q)
 
 
 def intersection_area_mark_little_seg_V2(batch, prefilter):

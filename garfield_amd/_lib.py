@@ -13,6 +13,7 @@ NCOUNTERS = 8
 VEC_F32 = 0
 VEC_F16 = 1
 VEC_U8 = 2
+VEC_I8Q = 3
 COUNTER_NAMES = ("expand", "dist", "attr", "cross", "lrow", "scan", "pass", "route")
 
 
@@ -122,6 +123,7 @@ _SYMBOLS = {
                           C.c_void_p, C.c_void_p],
     "gf_stream_plan_cells": [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_uint64,
                              C.c_uint32, C.c_void_p, C.c_void_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)],
+    "gf_quantise_i8": [C.c_void_p, C.c_uint64, C.c_uint32, C.c_float, C.c_void_p, C.c_void_p, C.c_void_p],
     "gf_host_alloc": [C.c_size_t, C.POINTER(C.c_void_p)],
     "gf_host_free": [C.c_void_p],
     "gf_status_str": [C.c_int32],
@@ -420,6 +422,20 @@ def entry_points(N, P, R):
     out = np.empty(R, np.uint32)
     _check(load().gf_entry_points(N, P, R, _ptr(out)))
     return out
+
+
+def quantise_i8(x, alpha=1.0):
+    """The int8 quantisation a VEC_I8Q index holds (gf_quantise_i8, host
+    code): returns (q (n x D int8), scale (D fp32), zero (D int32)), the
+    vector x dequantising to scale * (q - zero)."""
+    v = _c(x, np.float32)
+    n, D = v.shape
+    q = np.empty((n, D), np.int8)
+    s = np.empty(D, np.float32)
+    z = np.empty(D, np.int32)
+    _check(load().gf_quantise_i8(_ptr(v) if n else None, n, D, float(alpha), _ptr(s), _ptr(z),
+                                 _ptr(q) if n else None))
+    return q, s, z
 
 
 def plan_cells(cells, counts, grid, cell_size, max_points=0, max_cells=16):

@@ -58,7 +58,7 @@ void usage() {
         "usage: garfield_search --data_path F --query_path F --range F --cagra_prefix P --cagra_suffix S\n"
         "                       --global_graph F --grid F --attrs F [--cluster F] [--gt F] [--result F]\n"
         "                       [--prefilter x] [--postfilter n] [--f2h_factor x] [--degree n]\n"
-        "                       [--L l1,l2,...] [--vec_dtype f16|f32] [--device n]\n");
+        "                       [--L l1,l2,...] [--vec_dtype f16|f32|i8q] [--device n]\n");
 }
 
 }  // namespace
@@ -96,7 +96,8 @@ int main(int argc, char** argv) {
         else if (a == "--vec_dtype") {
             if (v == "f16") vec_dtype = GF_VEC_F16;
             else if (v == "f32") vec_dtype = GF_VEC_F32;
-            else die("--vec_dtype must be f16 or f32");
+            else if (v == "i8q") vec_dtype = GF_VEC_I8Q;
+            else die("--vec_dtype must be f16, f32 or i8q");
         } else if (a == "--L") {
             Ls.clear();
             std::stringstream ss(v);

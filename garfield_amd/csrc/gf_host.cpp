@@ -91,6 +91,38 @@ namespace gf {
 
 void set_last_error(const std::string& msg) { g_last_error = msg; }
 
+// Per-dimension int8 quantisation with the reference loader's host rules
+// (indexsearch/production_adapter.cuh:113-165), in fp32: x *= alpha; per
+// dimension min and max starting from 100000 and -100000; scale = (max - min)
+// / 255; zero point = round(-128 - min / scale) clamped to [-128, 127]; q =
+// round(x / scale) + zero point clamped to [-128, 127]; round() half away from
+// zero.  A dimension with max == min, where the reference divides by zero,
+// takes scale 1.
+void quantise_i8(const float* x, uint64_t n, uint32_t D, float alpha, std::vector<float>& scale,
+                 std::vector<int32_t>& zero, int8_t* out) {
+    scale.assign(D, 1.0f);
+    zero.assign(D, 0);
+    for (uint32_t d = 0; d < D; ++d) {
+        float mn = 100000.0f, mx = -100000.0f;
+        for (uint64_t i = 0; i < n; ++i) {
+            const float v = x[i * D + d] * alpha;
+            mn = std::min(mn, v);
+            mx = std::max(mx, v);
+        }
+        float s = (mx - mn) / 255.0f;
+        if (!(s > 0.0f)) s = 1.0f;
+        // clamped in double: the reference's int conversions overflow first
+        const double zr = std::round(float(-128) - mn / s);
+        const int z = int(std::max(-128.0, std::min(127.0, zr)));
+        for (uint64_t i = 0; i < n; ++i) {
+            const double q = double(std::round(x[i * D + d] * alpha / s)) + z;
+            out[i * D + d] = int8_t(std::max(-128.0, std::min(127.0, q)));
+        }
+        scale[d] = s;
+        zero[d] = z;
+    }
+}
+
 bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, const std::vector<uint32_t>& size,
                       const std::vector<uint32_t>& offset_h, uint32_t a, uint32_t P, SubHost& out) {
     if (a > 4) return false;
@@ -196,14 +228,15 @@ void map_cells(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix, s
     ix.vdtype = opts ? opts->vec_dtype : GF_VEC_F32;
     ix.alpha = (opts && opts->f2h_factor != 0.0f) ? opts->f2h_factor : 1.0f;
     ix.ref_ties = opts && opts->ref_ties;
-    GF_REQUIRE(ix.vdtype == GF_VEC_F32 || ix.vdtype == GF_VEC_F16 || ix.vdtype == GF_VEC_U8, GF_E_ARG,
-               "vec_dtype must be GF_VEC_F32, GF_VEC_F16 or GF_VEC_U8");
+    GF_REQUIRE(ix.vdtype == GF_VEC_F32 || ix.vdtype == GF_VEC_F16 || ix.vdtype == GF_VEC_U8 ||
+                   ix.vdtype == GF_VEC_I8Q, GF_E_ARG,
+               "vec_dtype must be GF_VEC_F32, GF_VEC_F16, GF_VEC_U8 or GF_VEC_I8Q");
     GF_REQUIRE(!(opts && opts->degree) || opts->degree == h.R, GF_E_FORMAT, "--degree does not match the graph files");
     const uint32_t elems = ix.vdtype == GF_VEC_F32 ? 4u : (ix.vdtype == GF_VEC_F16 ? 8u : 16u);
-    GF_REQUIRE(h.D % elems == 0, GF_E_UNSUPPORTED, "D must be a multiple of 4 (fp32), 8 (fp16) or 16 (u8)");
+    GF_REQUIRE(h.D % elems == 0, GF_E_UNSUPPORTED, "D must be a multiple of 4 (fp32), 8 (fp16) or 16 (u8, int8)");
     ix.rs = gf::row_shape(h.D, ix.vdtype);
     GF_REQUIRE(ix.rs.cpl <= gf::row_shape_max_cpl(ix.vdtype), GF_E_UNSUPPORTED, "D too large for this build");
-    ix.rowbytes = h.D * (ix.vdtype == GF_VEC_F32 ? 4u : (ix.vdtype == GF_VEC_F16 ? 2u : 1u));
+    ix.rowbytes = h.D * (ix.vdtype == GF_VEC_F32 ? 4u : (ix.vdtype == GF_VEC_F16 ? 2u : 1u));   // u8, int8: 1
 
     const uint32_t N = h.N, D = h.D, a = h.a, R = h.R, E = h.E;
     uint64_t P64 = 1;
@@ -343,6 +376,12 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
             ix.vec.alloc(v.size() * sizeof(uint16_t));
             GF_HIP(gf::launch_f2h(tmp.p, reinterpret_cast<uint16_t*>(ix.vec.p), v.size(), ix.alpha, ix.stream));
             vec_f32_dev = tmp.p;
+        } else if (ix.vdtype == GF_VEC_I8Q) {
+            std::vector<char> u(v.size());
+            gf::quantise_i8(v.data(), N, D, ix.alpha, ix.qscale, ix.qzero, reinterpret_cast<int8_t*>(u.data()));
+            ix.vec.upload(u);
+            tmp.upload(v);
+            vec_f32_dev = tmp.p;
         } else {
             std::vector<char> u(v.size());
             for (size_t i = 0; i < v.size(); ++i) u[i] = char(uint8_t(v[i]));
@@ -352,7 +391,7 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
         }
         build_subcells(h, gidx, size, ix);
         // Integer-valued data in [0, 255]: int8 tiles of the MFMA brute force.
-        bool ints = ix.sub && ix.vdtype != GF_VEC_F16 && D % 64 == 0 && D <= 256;
+        bool ints = ix.sub && ix.vdtype != GF_VEC_F16 && ix.vdtype != GF_VEC_I8Q && D % 64 == 0 && D <= 256;
         for (size_t i = 0; ints && i < v.size(); ++i) ints = v[i] >= 0.0f && v[i] <= 255.0f && v[i] == std::floor(v[i]);
         if (ints) {
             ix.vt.alloc(size_t(ix.ntile) * (D / 64) * 1024);
@@ -644,6 +683,19 @@ gf_status gf_batch_create(gf_index* ix, const float* queries, uint32_t Q, const 
             b->q16v.alloc(size_t(Q) * ix->D);
             GF_HIP(gf::launch_f2h(b->qf32.p, b->q16v.p, size_t(Q) * ix->D, ix->alpha, ix->stream));
         }
+        if (ix->vdtype == GF_VEC_I8Q) {
+            // rows [c | s]: c_d = fma(s_d, z_d, alpha q_d), the query less
+            // the dequantised offset, then the scales
+            const uint32_t D = ix->D;
+            std::vector<float> rows(size_t(Q) * 2 * D);
+            for (uint32_t q = 0; q < Q; ++q)
+                for (uint32_t d = 0; d < D; ++d) {
+                    const float x = queries[size_t(q) * D + d] * ix->alpha;
+                    rows[size_t(q) * 2 * D + d] = std::fmaf(ix->qscale[d], float(ix->qzero[d]), x);
+                    rows[size_t(q) * 2 * D + D + d] = ix->qscale[d];
+                }
+            b->qi8q.upload(rows);
+        }
         if (ix->C) {
             b->q16.alloc(size_t(b->Qp) * ix->Dp);
             GF_HIP(gf::launch_f2h_pad(b->qf32.p, Q, ix->D, b->q16.p, b->Qp, ix->Dp, ix->alpha, ix->stream));
@@ -849,6 +901,9 @@ gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, floa
         if (ix->vdtype == GF_VEC_F16) {
             a.queries = reinterpret_cast<const char*>(b->q16v.p);
             a.qbytes = ix->D * 2;
+        } else if (ix->vdtype == GF_VEC_I8Q) {
+            a.queries = reinterpret_cast<const char*>(b->qi8q.p);
+            a.qbytes = ix->D * 8;
         } else {
             a.queries = reinterpret_cast<const char*>(b->qf32.p);
             a.qbytes = ix->D * 4;
@@ -1300,6 +1355,18 @@ gf_status gf_kmeans(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t
                     const uint32_t* init_ids, int32_t device, int32_t* labels, uint8_t* centres, double* ms) {
     return run_guarded([&] {
         gf::kmeans_labels(vectors, vec_dtype, N, D, C, iters, init_ids, device, labels, centres, ms);
+    });
+}
+
+gf_status gf_quantise_i8(const float* x, uint64_t n, uint32_t D, float alpha, float* scale, int32_t* zero,
+                         int8_t* out) {
+    return run_guarded([&] {
+        GF_REQUIRE(D >= 1 && scale && zero && (n == 0 || (x && out)), GF_E_ARG, "gf_quantise_i8: bad argument");
+        std::vector<float> s;
+        std::vector<int32_t> z;
+        gf::quantise_i8(x, n, D, alpha, s, z, out);
+        std::memcpy(scale, s.data(), sizeof(float) * D);
+        std::memcpy(zero, z.data(), sizeof(int32_t) * D);
     });
 }
 

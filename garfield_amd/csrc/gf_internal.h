@@ -50,6 +50,8 @@ struct RowShape {
 };
 RowShape row_shape(uint32_t D, int vt);
 uint32_t row_shape_max_cpl(int vt);
+void quantise_i8(const float* x, uint64_t n, uint32_t D, float alpha, std::vector<float>& scale,
+                 std::vector<int32_t>& zero, int8_t* out);
 
 struct TravArgs {
     const char* vec;          // N rows of rowbytes, cell-major

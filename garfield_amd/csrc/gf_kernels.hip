@@ -75,9 +75,12 @@ __device__ __forceinline__ void hash_clear(uint32_t* H, uint32_t hsize) {
 }
 
 // ----------------------------------------------------------- row distances
-// Vector types: VT 0 = fp32, 1 = binary16, 2 = uint8.  A row is read in
-// 16-byte chunks of kEpc<VT> elements; queries are fp32 rows for VT 2 and
-// rows of the data's type otherwise.
+// Vector types: VT 0 = fp32, 1 = binary16, 2 = uint8, 3 = int8 quantised
+// per dimension (x = s_d (q - z_d)).  A row is read in 16-byte chunks of
+// kEpc<VT> elements; queries are fp32 rows for VT 2, rows [c | s] of 2 x
+// nch x 16 floats for VT 3 (c_d = fma(s_d, z_d, query_d)), and rows of the
+// data's type otherwise.  VT 3's element term is t = fma(-s_d, q, c_d), the
+// query minus the dequantised value, squared and summed as the others.
 //
 // Summation order (the canonical order the oracle restates): LPR "virtual"
 // lanes, virtual lane v accumulating chunks v, v + LPR, ... with fp32 fma in
@@ -106,6 +109,7 @@ struct RowPlan {
 template <int VT, int LPR, int CPL>
 struct QReg {
     float v[RowPlan<LPR, CPL>::NCH][kEpc<VT>];
+    float w[VT == 3 ? RowPlan<LPR, CPL>::NCH : 1][VT == 3 ? kEpc<VT> : 1];   // VT 3: per-dimension scales
 };
 
 // Chunk k = j * CPL + m of physical lane l: virtual lane l + PL * j, its m-th
@@ -134,6 +138,11 @@ __device__ __forceinline__ void decode_chunk(const uint4& u, float (&x)[kEpc<VT>
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int k = 0; k < 4; ++k) x[4 * i + k] = float((w[i] >> (8 * k)) & 0xFFu);
+    } else if constexpr (VT == 3) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) x[4 * i + k] = float(int8_t(uint8_t(w[i] >> (8 * k))));
     } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[i] = __uint_as_float(w[i]);
@@ -148,7 +157,7 @@ __device__ __forceinline__ void load_query(QReg<VT, LPR, CPL>& q, const char* qr
     for (int k = 0; k < RP::NCH; ++k) {
         const uint32_t c = lane_chunk<LPR, CPL>(l, k);
         if (c < nch) {
-            if constexpr (VT == 2) {
+            if constexpr (VT == 2 || VT == 3) {
                 // fp32 query: one 16-element chunk is four 16-byte loads
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
@@ -156,6 +165,11 @@ __device__ __forceinline__ void load_query(QReg<VT, LPR, CPL>& q, const char* qr
                     decode_chunk<0>(load16(qrow, 4 * c + t), x);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) q.v[k][4 * t + e] = x[e];
+                    if constexpr (VT == 3) {
+                        decode_chunk<0>(load16(qrow, 4 * (nch + c) + t), x);   // the scales follow the nch chunks
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) q.w[k][4 * t + e] = x[e];
+                    }
                 }
             } else {
                 decode_chunk<VT>(load16(qrow, c), q.v[k]);
@@ -163,6 +177,10 @@ __device__ __forceinline__ void load_query(QReg<VT, LPR, CPL>& q, const char* qr
         } else {
 #pragma unroll
             for (int e = 0; e < kEpc<VT>; ++e) q.v[k][e] = 0.0f;
+            if constexpr (VT == 3) {
+#pragma unroll
+                for (int e = 0; e < kEpc<VT>; ++e) q.w[k][e] = 0.0f;
+            }
         }
     }
 }
@@ -199,7 +217,9 @@ __device__ __forceinline__ float row_reduce(const QReg<VT, LPR, CPL>& q, const u
             decode_chunk<VT>(raw[j * CPL + m], x);
 #pragma unroll
             for (int e = 0; e < kEpc<VT>; ++e) {
-                const float d = q.v[j * CPL + m][e] - x[e];
+                float d;
+                if constexpr (VT == 3) d = __builtin_fmaf(-q.w[j * CPL + m][e], x[e], q.v[j * CPL + m][e]);
+                else d = q.v[j * CPL + m][e] - x[e];
                 acc = __builtin_fmaf(d, d, acc);
             }
         }
@@ -3159,7 +3179,7 @@ hipError_t launch_bf_t(const TravArgs& a, uint32_t grid, hipStream_t st) {
 RowShape row_shape(uint32_t D, int vt) {
     RowShape r;
     r.vt = vt;
-    const uint32_t elems = vt == 0 ? 4u : (vt == 1 ? 8u : 16u);
+    const uint32_t elems = vt == 0 ? 4u : (vt == 1 ? 8u : 16u);   // vt 2 and 3: 16 bytes
     r.nch = (D + elems - 1) / elems;
     r.lpr = 8;
     while (r.lpr < r.nch && r.lpr < 64) r.lpr <<= 1;
@@ -3186,6 +3206,7 @@ uint32_t row_shape_max_cpl(int vt) { return vt == 0 ? 4u : 2u; }
         if (rs.vt == 0) GF_DISPATCH_VT(0, CALL);   \
         if (rs.vt == 1) GF_DISPATCH_VT(1, CALL);   \
         if (rs.vt == 2) GF_DISPATCH_VT(2, CALL);   \
+        if (rs.vt == 3) GF_DISPATCH_VT(3, CALL);   \
     } while (0)
 
 hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds, uint32_t grid, hipStream_t st) {

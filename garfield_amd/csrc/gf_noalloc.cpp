@@ -72,6 +72,7 @@ extern "C" gf_status gf_search_noalloc(gf_index* ix, const float* queries, uint3
         GF_REQUIRE(ix && queries && lo && hi && o && ids, GF_E_ARG, "null argument");
         GF_REQUIRE(Q > 0, GF_E_ARG, "empty batch");
         GF_REQUIRE(!ix->sx, GF_E_UNSUPPORTED, "gf_search_noalloc needs a resident index");
+        GF_REQUIRE(ix->vdtype != GF_VEC_I8Q, GF_E_UNSUPPORTED, "gf_search_noalloc does not take GF_VEC_I8Q indexes");
         const gf_search_opts& so = o->search;
         const uint32_t L = so.L, K = so.K, rl = so.rl, R = ix->R, P = ix->P, a = ix->a, D = ix->D;
         GF_REQUIRE(L >= 1 && L < (1u << 16), GF_E_ARG, "L must be in [1, 65535]");

@@ -153,6 +153,8 @@ struct gf_index {
     uint32_t N = 0, D = 0, a = 0, P = 0, R = 0, E = 0, C = 0;
     int32_t vdtype = GF_VEC_F32;
     float alpha = 1.0f;
+    std::vector<float> qscale;      // GF_VEC_I8Q: per-dimension scale and zero point
+    std::vector<int32_t> qzero;
     bool ref_ties = false;   // stage B: equal cell scores in the reference's network order
     gf::RowShape rs{};
     uint32_t rowbytes = 0, Cp = 0, Dp = 0;
@@ -240,6 +242,7 @@ struct gf_batch {
     DevBuf<unsigned long long> stats;
     DevBuf<float> qf32, qnorm, lo, hi, cdist, out_dist;
     DevBuf<uint16_t> q16, q16v;
+    DevBuf<float> qi8q;   // GF_VEC_I8Q: query rows [c | s], c_d = fma(s_d, z_d, q_d)
     DevBuf<uint32_t> cells, counts, little, selcount, cellq, ccount, cstart, cfill, topk;
     DevBuf<uint32_t> out_ids, counters, sched, entry, gbound;
     // Per (query, cell) flags, 1 = selected | 2 = little: written by the

@@ -39,6 +39,12 @@ typedef int32_t gf_status;
 #define GF_VEC_F16 1        /* on binary16 copies half(x * f2h_factor), fp32 accumulation */
 #define GF_VEC_U8 2         /* on uint8 copies (vectors must be integers in [0, 255], as the
                                reference's u8 datasets, tools.cuh:134-150), fp32 accumulation */
+#define GF_VEC_I8Q 3        /* on int8 copies quantised per dimension as the reference's
+                               out-of-core loader does (production_adapter.cuh:108-165: scale
+                               (max - min) / 255, zero point round(-128 - min / scale), q =
+                               round(x / scale) + zero point in [-128, 127], after x *= f2h_factor);
+                               distances to the dequantised scale * (q - zero point) in fp32;
+                               resident indexes only */
 
 typedef struct gf_index gf_index;
 typedef struct gf_batch gf_batch;
@@ -363,6 +369,17 @@ gf_status gf_optimize_graphs(const uint32_t* knn_graphs, uint32_t N, uint32_t I,
 gf_status gf_kmeans(const void* vectors, int32_t vec_dtype, uint32_t N, uint32_t D, uint32_t C, uint32_t iters,
                     const uint32_t* init_ids, int32_t device, int32_t* labels /*N*/, uint8_t* centres /*C*D*/,
                     double* ms);
+
+/* The int8 quantisation a GF_VEC_I8Q index holds (replaces the reference
+ * loader's production_adapter.cuh:110-183 load_dataset_return_int8_arr, whose
+ * int8 array, scales and zero points it returns): x (n*D) times alpha, per
+ * dimension scale (max - min) / 255 with min and max starting from 100000
+ * and -100000, zero point round(-128 - min / scale) clamped to [-128, 127],
+ * out = round(x / scale) + zero point clamped to [-128, 127], fp32 arithmetic,
+ * round() half away from zero; a dimension with max == min takes scale 1.
+ * Host only (no device). */
+gf_status gf_quantise_i8(const float* x, uint64_t n, uint32_t D, float alpha, float* scale /*D*/,
+                         int32_t* zero /*D*/, int8_t* out /*n*D*/);
 
 const char* gf_status_str(gf_status s);
 const char* gf_last_error(void);

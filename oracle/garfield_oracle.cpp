@@ -43,8 +43,10 @@ uint32_t lanes_per_row(uint32_t D, int vdtype) {
 
 // Canonical distance: lane l of LPR accumulates chunks l, l+LPR, ... with fp32
 // fma in element order; the lane sums are combined by an xor butterfly.
-// Elements past D (row padding) are zero in both operands.
-float canon_dist(const float* q, const float* x, uint32_t D, int vdtype) {
+// Elements past D (row padding) are zero in both operands.  vdtype 3: q holds
+// c_k = fma(s_k, z_k, query_k) and the element term is fma(-s_k, x_k, c_k),
+// the query less the dequantised s_k (x_k - z_k).
+float canon_dist(const float* q, const float* x, uint32_t D, int vdtype, const float* s3 = nullptr) {
     const uint32_t ce = chunk_elems(vdtype);
     const uint32_t nch = (D + ce - 1) / ce;
     const uint32_t lpr = lanes_per_row(D, vdtype);
@@ -54,7 +56,7 @@ float canon_dist(const float* q, const float* x, uint32_t D, int vdtype) {
         for (uint32_t c = l; c < nch; c += lpr)
             for (uint32_t e = 0; e < ce; ++e) {
                 const uint32_t k = c * ce + e;
-                float d = k < D ? q[k] - x[k] : 0.0f;
+                float d = k >= D ? 0.0f : (vdtype == 3 ? std::fmaf(-s3[k], x[k], q[k]) : q[k] - x[k]);
                 acc = std::fmaf(d, d, acc);
             }
         s[l] = acc;
@@ -278,7 +280,7 @@ float point_dist(QueryState& s, uint32_t gid) {
     const orc_index* ix = s.c->ix;
     const uint32_t D = ix->D;
     if (ix->vdtype != 1)
-        return canon_dist(s.q, ix->vec_f32 + (size_t)gid * D, D, ix->vdtype);
+        return canon_dist(s.q, ix->vec_f32 + (size_t)gid * D, D, ix->vdtype, ix->qscale);
     if (g_dist_mode == 1) return hfma2_dist(s.qh, ix->vec_f16 + (size_t)gid * D, D);
     s.xbuf.resize(D);
     for (uint32_t i = 0; i < D; ++i) s.xbuf[i] = orc_h2f(ix->vec_f16[(size_t)gid * D + i]);
@@ -331,6 +333,8 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
     const uint16_t* qh = nullptr;
     if (ix->vdtype != 1) {
         std::memcpy(qv.data(), (const float*)queries + (size_t)qi * D, sizeof(float) * D);
+        if (ix->vdtype == 3)
+            for (uint32_t k = 0; k < D; ++k) qv[k] = std::fmaf(ix->qscale[k], float(ix->qzero[k]), qv[k]);
     } else {
         qh = (const uint16_t*)queries + (size_t)qi * D;
         for (uint32_t i = 0; i < D; ++i) qv[i] = orc_h2f(qh[i]);
@@ -929,6 +933,11 @@ void orc_canon_dists(const float* q, const float* X, uint32_t n, uint32_t D, flo
 
 float orc_distance(const orc_index* ix, const void* q, uint32_t gid) {
     std::vector<float> qv(ix->D), xv(ix->D);
+    if (ix->vdtype == 3) {
+        for (uint32_t k = 0; k < ix->D; ++k)
+            qv[k] = std::fmaf(ix->qscale[k], float(ix->qzero[k]), ((const float*)q)[k]);
+        return canon_dist(qv.data(), ix->vec_f32 + (size_t)gid * ix->D, ix->D, 3, ix->qscale);
+    }
     if (ix->vdtype != 1)
         return canon_dist((const float*)q, ix->vec_f32 + (size_t)gid * ix->D, ix->D, ix->vdtype);
     if (g_dist_mode == 1) return hfma2_dist((const uint16_t*)q, ix->vec_f16 + (size_t)gid * ix->D, ix->D);

@@ -33,8 +33,11 @@ extern "C" {
 /* Index in the reference's representation (point-id order, idx mapper). */
 typedef struct {
     uint32_t N, D, a, P, R, E;
-    int32_t vdtype;               /* 0: fp32 vectors, 1: fp16 bit patterns, 2: u8 values (in vec_f32) */
-    const float* vec_f32;         /* N*D, point-id order (vdtype 0 and 2) */
+    int32_t vdtype;               /* 0: fp32 vectors, 1: fp16 bit patterns, 2: u8 values (in vec_f32),
+                                     3: int8 values q (in vec_f32) of x = qscale (q - qzero) */
+    const float* vec_f32;         /* N*D, point-id order (vdtype 0, 2 and 3) */
+    const float* qscale;          /* D (vdtype 3) */
+    const int32_t* qzero;         /* D (vdtype 3) */
     const uint16_t* vec_f16;      /* N*D, point-id order, binary16 bits */
     const float* attrs;           /* N*a */
     const uint32_t* graph;        /* N*R, per-cell graphs concatenated in cell order */
@@ -140,7 +143,8 @@ void orc_canon_dists(const float* q, const float* X, uint32_t n, uint32_t D, flo
 
 /* gpu_graph.cu:3266-4131 fused kernel (+ host wrapper 12463-12616):
  * cell-by-cell traversal or filtered brute force per query.
- * queries: Q*D fp32 (vdtype 0) or binary16 bits (vdtype 1).
+ * queries: Q*D fp32 (vdtype 0, 2; vdtype 3: times the index's f2h_factor)
+ * or binary16 bits (vdtype 1).
  * cells: Q*P strided, already ordered.  counters: Q*ORC_NCNT. */
 #define ORC_NCNT 8
 enum { ORC_C_EXPAND = 0, ORC_C_DIST = 1, ORC_C_ATTR = 2, ORC_C_CROSS = 3,

@@ -39,7 +39,8 @@ def load():
 class _Index(C.Structure):
     _fields_ = [("N", C.c_uint32), ("D", C.c_uint32), ("a", C.c_uint32), ("P", C.c_uint32),
                 ("R", C.c_uint32), ("E", C.c_uint32), ("vdtype", C.c_int32),
-                ("vec_f32", C.c_void_p), ("vec_f16", C.c_void_p), ("attrs", C.c_void_p),
+                ("vec_f32", C.c_void_p), ("qscale", C.c_void_p), ("qzero", C.c_void_p),
+                ("vec_f16", C.c_void_p), ("attrs", C.c_void_p),
                 ("graph", C.c_void_p), ("offset", C.c_void_p), ("global_idx", C.c_void_p),
                 ("local_idx", C.c_void_p), ("cross", C.c_void_p),
                 ("FD", C.c_uint32), ("fgraph", C.c_void_p), ("fentry", C.c_void_p)]
@@ -187,8 +188,12 @@ def entry_draw(range_, ndraw, R):
 class OracleIndex:
     """The index in the reference's representation (point-id order + idx mapper)."""
 
-    def __init__(self, vectors, attrs, global_pid, P, cell_graphs, cross, vec_f16=None, u8=False, full=True):
+    def __init__(self, vectors, attrs, global_pid, P, cell_graphs, cross, vec_f16=None, u8=False, full=True,
+                 i8q=None):
         """u8=True: the HIP path's uint8 vector mode (vectors hold the integer values).
+        i8q=(scale, zero): the int8 per-dimension quantised mode (vectors hold
+        the int8 values q of scale * (q - zero), quantise_i8); queries are
+        then given times the index's f2h_factor.
         full=True: the full graph of the library's resident index (P <= 64
         cells, FE = min(E, R, 64 // P) edges into each cell, entries from the
         second draw), used by queries with postfilter or more cells; without
@@ -201,8 +206,15 @@ class OracleIndex:
         self.P = P
         self.gidx, self.lidx, self.offset = idx_mapper(global_pid, P)
         N, D = self.vectors.shape
+        vdt = (2 if u8 else 0) if self.vec_f16 is None else 1
+        self.qscale = self.qzero = None
+        if i8q is not None:
+            vdt = 3
+            self.qscale = _c(i8q[0], np.float32)
+            self.qzero = _c(i8q[1], np.int32)
         self.s = _Index(N, D, self.attrs.shape[1], P, self.graph.shape[1], self.cross.shape[1] // P,
-                        (2 if u8 else 0) if self.vec_f16 is None else 1, _p(self.vectors),
+                        vdt, _p(self.vectors), None if self.qscale is None else _p(self.qscale),
+                        None if self.qzero is None else _p(self.qzero),
                         None if self.vec_f16 is None else _p(self.vec_f16), _p(self.attrs), _p(self.graph),
                         _p(self.offset), _p(self.gidx), _p(self.lidx), _p(self.cross), 0, None, None)
         R, E = self.graph.shape[1], self.cross.shape[1] // P
@@ -519,6 +531,35 @@ def cross_rows(vectors, global_pid, P, E, rows):
         out[:, c * E:c * E + o.shape[1]] = o
         out[:, c * E + o.shape[1]:(c + 1) * E] = o[:, :1]
     return out
+
+
+def _round_half_away(v):
+    """C's round() of fp32 values: half away from zero (exact in float64)."""
+    v = np.asarray(v, np.float32).astype(np.float64)
+    return np.trunc(v + np.copysign(0.5, v))
+
+
+def quantise_i8(x, alpha=1.0, mutation=0):
+    """The reference's int8 quantisation of its out-of-core loader
+    (indexsearch/production_adapter.cuh:113-165), in fp32: x *= alpha; per
+    dimension min and max starting from 100000 and -100000; scale = (max -
+    min) / 255; zero point round(-128 - min / scale) clamped to [-128, 127];
+    q = round(x / scale) + zero point clamped to [-128, 127]; round() half
+    away from zero.  A dimension with max == min (the reference divides by
+    zero there) takes scale 1.  Returns (q int8, scale fp32, zero int32).
+    mutation 1: round half to even; 2: min and max from the data alone."""
+    v = np.asarray(x, np.float32) * np.float32(alpha)
+    if mutation == 2:
+        mn, mx = v.min(axis=0), v.max(axis=0)
+    else:
+        mn = np.minimum(np.float32(100000.0), v.min(axis=0))
+        mx = np.maximum(np.float32(-100000.0), v.max(axis=0))
+    s = (mx - mn) / np.float32(255.0)
+    s = np.where(s > 0, s, np.float32(1.0)).astype(np.float32)
+    rnd = np.rint if mutation == 1 else _round_half_away
+    z = np.clip(rnd(np.float32(-128.0) - mn / s), -128, 127).astype(np.int32)
+    q = np.clip(rnd(v / s) + z, -128, 127).astype(np.int8)
+    return q, s, z
 
 
 def quantise_u8(vectors):

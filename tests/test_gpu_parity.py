@@ -159,9 +159,17 @@ def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, post
     ids, dists, st = b.search(L=L, K=10, rl=10, postfilter=postfilter, entry_points=ent)
     ctr = b.get_counters()
     vec16 = orc.f2h(ix["vectors"], f2h_factor) if vec_dtype == 1 else None
-    O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"],
-                        ix["cross"], vec_f16=vec16)
-    oq = orc.f2h(queries, f2h_factor) if vec_dtype == 1 else queries
+    if vec_dtype == 3:
+        # the int8 values and per-dimension scales the index holds; queries
+        # scaled by f2h_factor as the library scales them
+        q8, qs, qz = orc.quantise_i8(ix["vectors"], f2h_factor)
+        O = orc.OracleIndex(q8.astype(np.float32), ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"],
+                            ix["cross"], i8q=(qs, qz))
+        oq = np.asarray(queries, np.float32) * np.float32(f2h_factor)
+    else:
+        O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"],
+                            ix["cross"], vec_f16=vec16)
+        oq = orc.f2h(queries, f2h_factor) if vec_dtype == 1 else queries
     oids, odist, octr = O.search(oq, lo, hi, gc, gcnt, glit, ent, L, K=10, rl=10, postfilter=postfilter)
     b.close()
     dev.close()
@@ -279,6 +287,66 @@ def test_gaussian_parity(world_gauss, L, prefilter):
     assert st.bf_mfma == 0
     if prefilter == 1.0:
         assert st.q_traverse == 0
+
+
+@pytest.mark.parametrize("L,prefilter", [(32, 0.0), (100, 0.0), (64, 0.01), (64, 1.0)])
+def test_i8q_parity(world_gauss, L, prefilter):
+    """int8 per-dimension quantised rows (GF_VEC_I8Q, the reference loader's
+    quantisation): traversal and gather brute force bit-exact against the
+    oracle's restatement of the same arithmetic."""
+    cfg, ix = world_gauss
+    _print_case("i8q", L=L, prefilter=prefilter)
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, L, prefilter=prefilter, vec_dtype=3)
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+    assert st.bf_mfma == 0
+    if prefilter == 1.0:
+        assert st.q_traverse == 0
+
+
+def test_i8q_768d_and_full_graph(world_c4):
+    """768-d rows (one 16-byte chunk per lane), f2h_factor 2, and the full
+    graph taking the queries with postfilter."""
+    cfg, ix = world_c4
+    _print_case("i8q-768")
+    _assert_same(*_traversal_case(cfg, ix, 64, vec_dtype=3, f2h_factor=2.0)[:6])
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 80, vec_dtype=3, postfilter=4)
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+    assert st.q_fullgraph > 0
+
+
+def test_i8q_recall(world_gauss):
+    """The quantised index still finds the fp32 neighbours: recall@10 against
+    exact fp32 ground truth at L = 200 stays within 0.05 of the fp32 index's."""
+    from oracle import oracle as orc
+    cfg, ix = world_gauss
+    _print_case("i8q-recall")
+    lo = cfg["lo"].astype(np.float32)
+    hi = cfg["hi"].astype(np.float32)
+    gt, gtd = orc.ground_truth(ix["vectors"], ix["attrs"], cfg["queries"], lo, hi, 10)
+    r8 = orc.recall(_traversal_case(cfg, ix, 200, vec_dtype=3)[0], gt, gtd)
+    r32 = orc.recall(_traversal_case(cfg, ix, 200)[0], gt, gtd)
+    assert r8 >= r32 - 0.05 and r8 > 0.8, (r8, r32)
+
+
+def test_i8q_rejected_where_unsupported(world_gauss):
+    """The no-allocation entry point and the streamed index take no
+    GF_VEC_I8Q index (status GF_E_UNSUPPORTED)."""
+    import garfield_amd as gf
+    cfg, ix = world_gauss
+    _print_case("i8q-reject")
+    dev = _device(ix, vec_dtype=3)
+    assert dev.vec_dtype == 3
+    lo = cfg["lo"].astype(np.float32)
+    hi = cfg["hi"].astype(np.float32)
+    with pytest.raises(gf.GarfieldError) as e:
+        gf.search_noalloc(dev, cfg["queries"][:4], lo[:4], hi[:4], 0.0, L=32, K=10)
+    assert e.value.status == 6
+    dev.close()
+    l_q, r_q = synth.quantile_arrays(ix)
+    with pytest.raises(gf.GarfieldError) as e:
+        gf.Index.create_streamed(ix["vectors"], ix["attrs"].astype(np.float32), ix["grid"], l_q, r_q,
+                                 ix["global_pid"], ix["cell_graphs"], ix["cross"], vec_dtype=3)
+    assert e.value.status == 6
 
 
 def test_mfma_bruteforce_all_queries(world32):
