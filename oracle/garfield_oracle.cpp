@@ -7,6 +7,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <limits>
@@ -20,6 +21,7 @@ namespace {
 const uint32_t SENT = 0xFFFFFFFFu;   // reference's empty candidate id
 const uint32_t EXPL = 0x80000000u;   // reference's "explored" bit
 const uint32_t IDM = 0x7FFFFFFFu;
+const uint32_t ID30 = 0x3FFFFFFFu;   // point id under the dual-channel traversal's two explored bits
 const float INF = std::numeric_limits<float>::infinity();
 const uint32_t MAX_ITER = 10000;     // gpu_graph.cu:39
 const uint32_t HASH_RESET = 4;       // gpu_graph.cu:34
@@ -154,7 +156,7 @@ struct Ctx {
 };
 
 inline uint32_t tiekey(const Ctx& c, uint32_t id) {
-    return id == SENT ? 0xFFFFFFFFu : c.cmpos[id & IDM];
+    return id == SENT ? 0xFFFFFFFFu : c.cmpos[id & ID30];
 }
 inline bool cless(const Ctx& c, const Cand& x, const Cand& y) {
     if (x.d != y.d) return x.d < y.d;
@@ -230,8 +232,22 @@ enum {
     MUT_FULL_OWN_AS_CROSS = 16,   // full graph assembly: own-cell edges read from the cross edges
 };
 // Per-cell iteration cap (gpu_graph.cu:39 MAX_ITER); tests lower it to reach
-// the end-of-cell step with unexplored entries left.
+// the end-of-cell step with unexplored entries left.  The dual-channel
+// traversal caps its epochs over all cells with the same value.
 uint32_t g_max_iter = MAX_ITER;
+// Traversal of the traversal-routed queries (orc_set_channels): 1 the
+// cell-by-cell search of the fused kernel, 2 the dual-channel search.
+int g_channels = 1;
+// Planted mistakes of the dual-channel search (orc_set_dual_mutation).
+int g_dual_mutation = 0;
+enum {
+    DMUT_NO_PARTNER = 1,          // the other channel gets no partner expansion
+    DMUT_PARTNER_LAST_EDGE = 2,   // the partner is sought from the last cross edge to the first
+    DMUT_NO_TURN = 3,             // the turn never passes to the other channel
+    DMUT_SWITCH_EDGE0 = 4,        // the cell switch reads cross edge 0 for all 128 slots
+    DMUT_ENTRY_SPLIT_HALF = 5,    // entries split at floor(L / 2) instead of ceil(L / 2)
+    DMUT_PEEK_ROW = 6,            // the partner test looks up the point id, not the local id's value
+};
 
 // Merged position of every element of sorted X (n) and sorted Y (m):
 // X_i -> i + #{Y <= X_i}, Y_j -> j + #{X < Y_j}  (gpu_graph.cu:162-222): an
@@ -352,7 +368,145 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
     auto cell_size = [&](uint32_t cc) { return ix->offset[cc + 1] - ix->offset[cc]; };
     const uint32_t reset_every = g_mutation == MUT_RESET_EVERY_3 ? 3u : HASH_RESET;
 
-    if (traverse) {
+    if (traverse && g_channels == 2) {
+        // Dual-channel traversal: the traversal of
+        // select_path_contain_attr_filter_V2_without_output_dual_channel_in_turn_with_prefilter
+        // (gpu_graph.cu:6249-6640; launched like batch_graph_search_gpu,
+        // gpu_graph.cu:12223-12300).  Two channels walk two cells of the
+        // query's list at once over one candidate list; an entry carries the
+        // reference's two explored bits (bit 31: channel 0, bit 30: channel
+        // 1), and a channel's own points enter with the other channel's bit
+        // set, so that each channel expands only its own.  Per epoch the
+        // channel `turn` expands its first unexplored entry and the other
+        // channel a partner: the first of that entry's cross edges into the
+        // other channel's cell whose local id is not in the visited set
+        // (which holds point ids: the reference tests the local id's value),
+        // expanded through R - 1 neighbours plus itself.  A channel with
+        // nothing left moves to the next cell of the list through 128
+        // cross-edge slots; with no cell left it joins the other channel.
+        s.ctr[ORC_C_ROUTE] = 4;
+        const uint32_t NONE = 0xFFFFFFFFu;
+        std::vector<Cand> A(L, Cand{INF, SENT}), T(2 * R, Cand{INF, SENT}), Rc(rl, Cand{INF, SENT});
+        std::unordered_set<uint32_t> H;
+        H.reserve(4 * (L + XSLOTS + 10 * R));
+        uint32_t pid[2] = {cl[0], cnt >= 2 ? cl[1] : cl[0]};
+        auto gid_of = [&](uint32_t cc, uint32_t lid) { return ix->global_idx[ix->offset[cc] + lid]; };
+        auto dist_of = [&](Cand& x) {
+            x.d = point_dist(s, x.id & ID30);
+            s.ctr[ORC_C_DIST]++; s.ctr[ORC_C_ATTR]++;
+        };
+        // Entries (gpu_graph.cu:6318-6329): entry i < ceil(L / 2) in channel
+        // 0's cell, the rest in channel 1's; entry[i] reduced modulo the cell
+        // size (the reference draws from [0, 62500)).  All L are evaluated
+        // and sorted (gpu_graph.cu:6338-6362).
+        const uint32_t L2 = g_dual_mutation == DMUT_ENTRY_SPLIT_HALF ? std::max(1u, L / 2) : (L + 1) / 2;
+        for (uint32_t i = 0; i < L; ++i) {
+            const uint32_t ch = std::min(1u, i / L2);
+            const uint32_t mask = pid[0] == pid[1] ? 0u : (1u << (30 + ch));
+            const uint32_t g = gid_of(pid[ch], entry[i] % cell_size(pid[ch]));
+            A[i] = {INF, g | mask};
+            H.insert(g);
+            dist_of(A[i]);
+        }
+        sort_cands(c, A.data(), L, 1);
+        uint32_t cur = cnt >= 2 ? 2 : 1, main_ch = 0, turn = 0;
+        for (uint32_t ep = 0; ep < g_max_iter; ++ep) {
+            if ((ep + 1) % reset_every == 0) {               // gpu_graph.cu:6364-6378
+                H.clear();
+                for (const auto* arr : {&A, &T})
+                    for (const Cand& x : *arr)
+                        if (x.id != SENT) H.insert(x.id & ID30);
+            }
+            // Selection (gpu_graph.cu:6380-6420).
+            uint32_t te[2] = {NONE, NONE};
+            {
+                const uint32_t mask = 1u << (pid[0] == pid[1] ? 31 - main_ch : 31 - turn);
+                for (uint32_t j = 0; j < L; ++j)
+                    if ((A[j].id & mask) == 0) {
+                        te[turn] = ix->local_idx[A[j].id & ID30];
+                        A[j].id |= mask;
+                        break;
+                    }
+                if (te[turn] != NONE && g_dual_mutation != DMUT_NO_PARTNER) {
+                    const uint32_t g = gid_of(pid[turn], te[turn]);
+                    const uint32_t ne = std::min(2u, E);
+                    for (uint32_t jj = 0; jj < ne; ++jj) {
+                        const uint32_t j = g_dual_mutation == DMUT_PARTNER_LAST_EDGE ? ne - 1 - jj : jj;
+                        const uint32_t v = ix->cross[(size_t)g * P * E + (size_t)pid[turn ^ 1] * E + j];
+                        const uint32_t key = g_dual_mutation == DMUT_PEEK_ROW ? gid_of(pid[turn ^ 1], v) : v;
+                        if (!H.count(key)) { te[turn ^ 1] = v; break; }
+                    }
+                }
+            }
+            if (te[turn] == NONE) {                          // gpu_graph.cu:6422-6547
+                if (cur == cnt && pid[0] == pid[1]) break;
+                if (cur == cnt) {                            // join the other channel's cell
+                    pid[turn] = pid[turn ^ 1];
+                    main_ch = turn ^ 1;
+                    continue;
+                }
+                // Move channel `turn` to the next cell: slot i follows entry
+                // i % 64 through its cross edge i / 64 (an edge index beyond E
+                // is skipped: the reference reads the next cell's edges there).
+                const uint32_t nxt = cl[cur];
+                const uint32_t mask = 1u << (30 + turn);
+                std::vector<Cand> W(XSLOTS, Cand{INF, SENT});
+                for (uint32_t i = 0; i < XSLOTS; ++i) {
+                    const uint32_t si = i % XSTEP;
+                    const uint32_t e = g_dual_mutation == DMUT_SWITCH_EDGE0 ? 0 : i / XSTEP;
+                    if (si >= L || A[si].id == SENT || e >= E) continue;
+                    const uint32_t nl = ix->cross[(size_t)(A[si].id & ID30) * P * E + (size_t)nxt * E + e];
+                    const uint32_t g = gid_of(nxt, nl);
+                    if (H.insert(g).second) { W[i] = {0.0f, g | mask}; s.ctr[ORC_C_CROSS]++; }
+                }
+                for (Cand& x : W)
+                    if (x.id != SENT) dist_of(x);
+                sort_cands(c, W.data(), XSLOTS, 1);
+                merge_with_recycle(s, A.data(), L, W.data(), XSLOTS, Rc.data(), rl);
+                pid[turn] = nxt;
+                ++cur;
+                continue;
+            }
+            // Expansion (gpu_graph.cu:6549-6581): R slots per channel, filled
+            // in slot order (the reference's two warps race on the visited
+            // set; here a lower slot takes a point first).
+            for (uint32_t ch = 0; ch < 2; ++ch) {
+                Cand* tc = T.data() + ch * R;
+                for (uint32_t j = 0; j < R; ++j) tc[j] = {INF, SENT};
+                if (te[ch] == NONE) continue;
+                if (te[ch] >= cell_size(pid[ch])) {
+                    // a channel's unexplored entries lie in its own cell (it
+                    // leaves a cell only when none is left there)
+                    std::fprintf(stderr, "orc dual: expansion outside the channel's cell\n");
+                    std::abort();
+                }
+                s.ctr[ORC_C_EXPAND]++;
+                const uint32_t mask = pid[0] == pid[1] ? 0u : (1u << (30 + ch));
+                const uint32_t base = ix->offset[pid[ch]];
+                const bool partner = ch != turn;
+                for (uint32_t j = 0, k = 0; j < R; ++j) {
+                    uint32_t g;
+                    if (partner && j == R - 1) g = gid_of(pid[ch], te[ch]);
+                    else g = gid_of(pid[ch], ix->graph[(size_t)(base + te[ch]) * R + k++]);
+                    if (H.insert(g).second) tc[j] = {0.0f, g | mask};
+                }
+            }
+            if (g_dual_mutation != DMUT_NO_TURN) turn ^= 1;
+            for (Cand& x : T)                                // gpu_graph.cu:6582-6602
+                if (x.id != SENT) dist_of(x);
+            // One sort of the 2R slots (the reference's warpSort over 2R
+            // lanes spans two 32-lane warps, whose halves it sorts apart).
+            sort_cands(c, T.data(), 2 * R, 0);
+            if (T[0].id != SENT)                             // gpu_graph.cu:6603-6616
+                merge_with_recycle(s, A.data(), L, T.data(), 2 * R, Rc.data(), rl);
+        }
+        // Post-filter + recycle merge (gpu_graph.cu:6618-6639).
+        for (Cand& x : A)
+            if (x.id != SENT && !passes(s, x.id & ID30)) x = {INF, SENT};
+        sort_cands(c, A.data(), L, 1);
+        if (Rc[0].id != SENT) merge_plain(c, A.data(), L, Rc.data(), rl);
+        out = A;
+    } else if (traverse) {
         s.ctr[ORC_C_ROUTE] = 1;
         std::vector<Cand> A(L, Cand{INF, SENT}), B(R, Cand{INF, SENT}), Rc(rl, Cand{INF, SENT});
         std::vector<Cand> W(XSLOTS);
@@ -558,7 +712,7 @@ void search_one(const Ctx& c, const void* queries, uint32_t qi, const float* lo_
     for (const Cand& x : out) {
         if (n >= K) break;
         if (x.id == SENT) continue;
-        uint32_t id = x.id & IDM;
+        uint32_t id = x.id & ID30;
         bool dup = false;
         for (uint32_t t = 0; t < n && !dup; ++t) dup = out_ids[(size_t)qi * K + t] == id;
         if (dup) continue;
@@ -973,6 +1127,8 @@ uint16_t orc_half_rne(double v) { return half_rne(v); }
 float orc_hfma2_dist(const uint16_t* q, const uint16_t* x, uint32_t D) { return hfma2_dist(q, x, D); }
 void orc_set_mutation(int m) { g_mutation = m; }
 void orc_set_max_iter(uint32_t n) { g_max_iter = n ? n : MAX_ITER; }
+void orc_set_channels(int n) { g_channels = n == 2 ? 2 : 1; }
+void orc_set_dual_mutation(int m) { g_dual_mutation = m; }
 
 uint32_t orc_search_trace(const orc_index* ix, const void* queries, uint32_t qi, const float* lo, const float* hi,
                           const uint32_t* cells, const uint32_t* counts, const uint32_t* entry, uint32_t L,

@@ -177,6 +177,13 @@ float orc_hfma2_dist(const uint16_t* q, const uint16_t* x, uint32_t D);
 void orc_set_mutation(int m);
 /* Per-cell iteration cap of the traversal (0 restores the reference's 10000). */
 void orc_set_max_iter(uint32_t n);
+/* Traversal of traversal-routed queries: 1 (default) the fused kernel's
+ * cell-by-cell search; 2 the dual-channel search of
+ * select_path_..._dual_channel_in_turn_with_prefilter (gpu_graph.cu:6249-6640),
+ * whose `entry` argument holds L entry ids (route counter 4). */
+void orc_set_channels(int n);
+/* Planted mistakes of the dual-channel search, for the pinning tests only. */
+void orc_set_dual_mutation(int m);
 /* One query (no little cells; postfilter as in orc_search: 1 << 30 forces
  * the traversal, 0 the full graph of an index that has one) with its
  * trajectory: the point ids expanded in order and the cell of each expansion

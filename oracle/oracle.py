@@ -342,6 +342,17 @@ def set_max_iter(n):
     load().orc_set_max_iter(C.c_uint32(int(n)))
 
 
+def set_channels(n):
+    """Traversal of traversal-routed queries: 1 the cell-by-cell search, 2 the
+    dual-channel search (entry points: L ids)."""
+    load().orc_set_channels(C.c_int(int(n)))
+
+
+def set_dual_mutation(m):
+    """Plant mistake number m in the dual-channel search (0: none); test use only."""
+    load().orc_set_dual_mutation(C.c_int(int(m)))
+
+
 def bitonic_sort_dis(dis, ids):
     d = _c(dis, np.float32).copy()
     i = _c(ids, np.uint32).copy()

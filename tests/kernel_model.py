@@ -32,6 +32,7 @@ import numpy as np
 SENT = 0xFFFFFFFF
 EXPL = 0x80000000
 IDM = 0x7FFFFFFF
+ID30 = 0x3FFFFFFF
 INF = float("inf")
 MAX_ITER = 10000
 HASH_RESET = 4
@@ -107,7 +108,7 @@ class KernelModel:
     def _k(self, d, i):
         if self.tie == 1:
             return (d,)
-        return (d, 0xFFFFFFFF if i == SENT else self.seg[self.cell[i & IDM]] + self.lidx[i & IDM])
+        return (d, 0xFFFFFFFF if i == SENT else self.seg[self.cell[i & ID30]] + self.lidx[i & ID30])
 
     def le(self, d1, i1, d2, i2):
         return self._k(d1, i1) <= self._k(d2, i2)
@@ -422,3 +423,175 @@ class KernelModel:
             ids.append(0x7FFFFFFF)
             dists.append(INF)
         return ids, dists, nexp, ndist, expanded
+
+    # ------------------------------------------------------- dual channel
+    def _merge_recycle_n(self, top, dis, L, n, lo, hi):
+        """merge_top_with_recycle_list (gpu_graph.cu:224-315) of the n entries
+        after top[:L] into top[:L]: list entries pushed out keep their place
+        in the tail only if they pass the filter; tail entries pushed out
+        become empty."""
+        newt = [SENT] * (L + n)
+        newd = [INF] * (L + n)
+        pos = self._ranks(top[:L], dis[:L], L, top[L:L + n], dis[L:L + n], n)
+        for k in range(L + n):
+            i, d, p = top[k], dis[k], pos[k]
+            if p >= L:
+                if k < L and i != SENT:
+                    if not self._passes(i & ID30, lo, hi):
+                        i, d = SENT, INF
+                elif k >= L:
+                    i, d = SENT, INF
+            newt[p], newd[p] = i, d
+        top[:L + n], dis[:L + n] = newt, newd
+
+    def search_dual(self, q, lo, hi, cells, entry, L, K=10, rl=10, max_iter=MAX_ITER):
+        """Traversal of select_path_contain_attr_filter_V2_without_output_
+        dual_channel_in_turn_with_prefilter (gpu_graph.cu:6249-6640) for one
+        query whose cells are not all little: top_M_Cand of TOPM + 2 DEGREE
+        entries, explored bits 31 (channel 0) and 30 (channel 1) in the id,
+        the visited set of point ids, `turn` and `main_channel` as in the
+        kernel.  In-bounds rules: entry[i] is reduced modulo its cell's size;
+        cross-edge indexes at or beyond E are skipped (the reference reads 2
+        edges per partner and per switch slot); equal keys met in one step
+        enter the visited set in slot order.  Returns (ids, dists,
+        expansions, distance evaluations, filled switch slots)."""
+        R, E = self.R, self.E
+        R2 = 2 * R
+        q = np.asarray(q, np.float64)
+        lo = np.asarray(lo, np.float64)
+        hi = np.asarray(hi, np.float64)
+        top = [SENT] * (L + R2)
+        dis = [INF] * (L + R2)
+        rec_id = [SENT] * rl
+        rec_d = [INF] * rl
+        H = set()
+        nexp = ndist = nslot = 0
+        psize = len(cells)
+        size = lambda c: self.seg[c + 1] - self.seg[c]
+        gid = lambda c, l: self.gidx[self.seg[c] + l]
+        pid = [cells[0], cells[1] if psize >= 2 else cells[0]]
+        L2 = (L + 1) // 2
+        for i in range(L):
+            mask = 0 if pid[0] == pid[1] else 1 << (30 + i // L2)
+            c = pid[i // L2]
+            top[i] = gid(c, int(entry[i]) % size(c)) | mask
+            H.add(top[i] & ID30)
+        cur = 2 if psize >= 2 else 1
+        main_channel = 0
+        turn = 0
+        for i in range(L):
+            if top[i] != SENT:
+                dis[i] = self._dist(q, top[i] & ID30)
+                ndist += 1
+        a_id, a_d = top[:L], dis[:L]
+        self.sort_net(a_id, a_d, L)
+        top[:L], dis[:L] = a_id, a_d
+        for epoch in range(max_iter):
+            if (epoch + 1) % HASH_RESET == 0:
+                H = set(t & ID30 for t in top[:L + R2] if t != SENT)
+            assert len(H) < HASHLEN
+            to_explore = [SENT, SENT]
+            shift = 31 - main_channel if pid[0] == pid[1] else 31 - turn
+            mask = 1 << shift
+            for j in range(L):
+                if (top[j] & mask) == 0:
+                    to_explore[turn] = self.lidx[top[j] & ID30]
+                    top[j] |= mask
+                    break
+            if to_explore[turn] != SENT:
+                g = gid(pid[turn], to_explore[turn])
+                for j in range(min(2, E)):
+                    v = int(self.cross[g, pid[turn ^ 1] * E + j])
+                    if v not in H:               # hash_peek of the local id's value
+                        to_explore[turn ^ 1] = v
+                        break
+            if to_explore[turn] == SENT:
+                if cur == psize and pid[0] == pid[1]:
+                    break
+                if cur == psize:
+                    pid[turn] = pid[turn ^ 1]
+                    main_channel = turn ^ 1
+                    continue
+                next_pid = cells[cur]
+                mask = 1 << (30 + turn)
+                wid = [SENT] * 128
+                wd = [INF] * 128
+                for i in range(128):
+                    if i % 64 >= L or top[i % 64] == SENT or i // 64 >= E:
+                        continue
+                    nl = int(self.cross[top[i % 64] & ID30, next_pid * E + i // 64])
+                    ng = gid(next_pid, nl)
+                    if ng not in H:
+                        H.add(ng)
+                        wid[i], wd[i] = ng | mask, 0.0
+                        nslot += 1
+                for i in range(128):
+                    if wid[i] != SENT:
+                        wd[i] = self._dist(q, wid[i] & ID30)
+                        ndist += 1
+                self.sort_net(wid, wd, 128)
+                t2, d2 = top[:L] + wid, dis[:L] + wd
+                self._merge_recycle_n(t2, d2, L, 128, lo, hi)
+                top[:L], dis[:L] = t2[:L], d2[:L]
+                wid, wd = t2[L:], d2[L:]
+                self.sort_net(wid, wd, 128)
+                if wid[0] != SENT:
+                    self.merge_top(rec_id, rec_d, wid, wd)
+                pid[turn] = next_pid
+                cur += 1
+                continue
+            for ch in (0, 1):
+                base = L + ch * R
+                if to_explore[ch] == SENT:
+                    for i in range(R):
+                        top[base + i], dis[base + i] = SENT, INF
+                    continue
+                nexp += 1
+                mask = 0 if pid[0] == pid[1] else 1 << (30 + ch)
+                for j in range(R - (0 if ch == turn else 1)):
+                    local = int(self.graph[self.seg[pid[ch]] + to_explore[ch], j])
+                    g = gid(pid[ch], local)
+                    if g in H:
+                        top[base + j], dis[base + j] = SENT, INF
+                    else:
+                        H.add(g)
+                        top[base + j], dis[base + j] = g | mask, 0.0
+                if ch != turn:
+                    g = gid(pid[ch], to_explore[ch])
+                    if g in H:
+                        top[base + R - 1], dis[base + R - 1] = SENT, INF
+                    else:
+                        H.add(g)
+                        top[base + R - 1], dis[base + R - 1] = g | mask, 0.0
+            turn ^= 1
+            for i in range(L, L + R2):
+                if top[i] != SENT:
+                    dis[i] = self._dist(q, top[i] & ID30)
+                    ndist += 1
+            self.sort_b(top, dis, L, R2)
+            if top[L] != SENT:
+                self._merge_recycle_n(top, dis, L, R2, lo, hi)
+                self.sort_b(top, dis, L, R2)
+                if top[L] != SENT:
+                    b_id, b_d = top[L:], dis[L:]
+                    self.merge_top(rec_id, rec_d, b_id, b_d)
+                    top[L:], dis[L:] = b_id, b_d
+        for i in range(L):
+            if top[i] != SENT and not self._passes(top[i] & ID30, lo, hi):
+                top[i], dis[i] = SENT, INF
+        a_id, a_d = top[:L], dis[:L]
+        self.sort_net(a_id, a_d, L)
+        if rec_id[0] != SENT:
+            self.merge_top(a_id, a_d, list(rec_id), list(rec_d))
+        ids, dists = [], []
+        for i, d in zip(a_id, a_d):
+            if len(ids) == K:
+                break
+            if i == SENT or (i & ID30) in ids:
+                continue
+            ids.append(i & ID30)
+            dists.append(d)
+        while len(ids) < K:
+            ids.append(0x7FFFFFFF)
+            dists.append(INF)
+        return ids, dists, nexp, ndist, nslot
