@@ -103,6 +103,7 @@ _SYMBOLS = {
     "gf_order_cells": [C.c_void_p, C.c_uint32, C.POINTER(C.c_double)],
     "gf_mark_cells_grid": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_double, C.POINTER(C.c_double)],
     "gf_search": [C.c_void_p, C.POINTER(_SearchOpts), C.c_void_p, C.c_void_p, C.POINTER(SearchStats)],
+    "gf_search_dual": [C.c_void_p, C.POINTER(_SearchOpts), C.c_void_p, C.c_void_p, C.POINTER(SearchStats)],
     "gf_batch_get_cells": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
     "gf_batch_set_cells": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
     "gf_batch_get_centroid": [C.c_void_p, C.c_void_p, C.c_void_p],
@@ -335,10 +336,12 @@ class Batch:
         self._topc = topc
         return ms.value if timed else None
 
-    def search(self, L, K=10, rl=10, postfilter=1 << 30, entry_points=None, out=None):
+    def search(self, L, K=10, rl=10, postfilter=1 << 30, entry_points=None, out=None, channels=1):
         """out: optional (ids, dists) arrays of shape (Q, K), uint32 and float32,
         C-contiguous, that receive the results (a caller searching in a loop
-        reuses them instead of touching fresh pages every call)."""
+        reuses them instead of touching fresh pages every call).  channels=2:
+        the dual-channel traversal (gf_search_dual; entry_points then holds
+        L ids)."""
         if out is None:
             ids = np.empty((self.Q, K), np.uint32)
             dists = np.empty((self.Q, K), np.float32)
@@ -350,7 +353,8 @@ class Batch:
         ent = None if entry_points is None else _c(entry_points, np.uint32)
         opts = _SearchOpts(L, K, rl, min(int(postfilter), 0xFFFFFFFF), _ptr(ent))
         st = SearchStats()
-        _check(load().gf_search(self._h, C.byref(opts), _ptr(ids), _ptr(dists), C.byref(st)))
+        fn = load().gf_search_dual if channels == 2 else load().gf_search
+        _check(fn(self._h, C.byref(opts), _ptr(ids), _ptr(dists), C.byref(st)))
         return ids, dists, st
 
     def get_cells(self):

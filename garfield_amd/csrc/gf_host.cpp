@@ -834,381 +834,408 @@ gf_status gf_order_cells(gf_batch* b, uint32_t topc, double* ms) {
     });
 }
 
-gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, float* dists,
-                    gf_search_stats* stats) {
-    return run_guarded([&] {
-        GF_REQUIRE(b && opts && ids, GF_E_ARG, "null argument");
-        GF_REQUIRE(b->marked, GF_E_STATE, "gf_search before gf_mark_cells");
-        gf_index* ix = b->ix;
-        const uint32_t L = opts->L, K = opts->K, rl = opts->rl;
-        GF_REQUIRE(L >= 1 && L < (1u << 16), GF_E_ARG, "L must be in [1, 65535]");
-        GF_REQUIRE(K >= 1 && K <= 64, GF_E_ARG, "K must be in [1, 64]");
-        GF_REQUIRE(rl >= 1 && rl <= 16, GF_E_ARG, "rl must be in [1, 16]");
-        set_device(ix);
-        // Device times of the latest stage calls (their events precede the
-        // search on the stream, which the search has waited for).
-        auto stage_times = [&]() {
-            if (!stats) return;
-            stats->ms_stage_a = b->sev_a ? b->stage_ms(0) : 0.0;
-            stats->ms_stage_b = b->sev_b ? b->stage_ms(2) : 0.0;
-        };
-        if (ix->sx) {
-            gf::stream_search(*b, *opts, ids, dists, stats);
-            stage_times();
-            return;
-        }
-        hipStream_t st = ix->stream;
-        const uint32_t Q = b->Q, R = ix->R;
+// gf_search and gf_search_dual: channels 1 runs the traversal-routed
+// queries through k_traverse, 2 through k_traverse_dual.
+static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, float* dists,
+                            gf_search_stats* stats, uint32_t channels) {
+    GF_REQUIRE(b && opts && ids, GF_E_ARG, "null argument");
+    GF_REQUIRE(b->marked, GF_E_STATE, "gf_search before gf_mark_cells");
+    gf_index* ix = b->ix;
+    const uint32_t L = opts->L, K = opts->K, rl = opts->rl;
+    GF_REQUIRE(L >= 1 && L < (1u << 16), GF_E_ARG, "L must be in [1, 65535]");
+    GF_REQUIRE(K >= 1 && K <= 64, GF_E_ARG, "K must be in [1, 64]");
+    GF_REQUIRE(rl >= 1 && rl <= 16, GF_E_ARG, "rl must be in [1, 16]");
+    set_device(ix);
+    // Device times of the latest stage calls (their events precede the
+    // search on the stream, which the search has waited for).
+    auto stage_times = [&]() {
+        if (!stats) return;
+        stats->ms_stage_a = b->sev_a ? b->stage_ms(0) : 0.0;
+        stats->ms_stage_b = b->sev_b ? b->stage_ms(2) : 0.0;
+    };
+    if (ix->sx) {
+        gf::stream_search(*b, *opts, ids, dists, stats);
+        stage_times();
+        return;
+    }
+    hipStream_t st = ix->stream;
+    const uint32_t Q = b->Q, R = ix->R;
 
-        // Entry points: the caller's, or the reference's draw (computed once per index).
-        if (opts->entry_points) {
-            b->entry.upload(opts->entry_points, R);
-        } else {
-            if (!ix->entry_ref.n) {
-                std::vector<uint32_t> ent(R);
-                entry_points_ref(ix->N, ix->P, R, ent.data());
-                ix->entry_ref.upload(ent);
-            }
-            if (b->entry.n < R) b->entry.alloc(R);
-            GF_HIP(hipMemcpyAsync(b->entry.p, ix->entry_ref.p, R * sizeof(uint32_t), hipMemcpyDeviceToDevice, st));
+    // Entry points: the caller's, or the reference's draw (computed once per
+    // index and count): R of them, L for the dual-channel traversal.
+    const uint32_t nent = channels == 2 ? L : R;
+    if (opts->entry_points) {
+        b->entry.upload(opts->entry_points, nent);
+    } else {
+        DevBuf<uint32_t>& ref = channels == 2 ? ix->entry_dual : ix->entry_ref;
+        if (ref.n != nent) {
+            std::vector<uint32_t> ent(nent);
+            entry_points_ref(ix->N, ix->P, nent, ent.data());
+            ref.upload(ent);
         }
-        ensure_out(*b, K);
-        if (b->sched.n < Q) b->sched.alloc(Q);
+        if (b->entry.n < nent) b->entry.alloc(nent);
+        GF_HIP(hipMemcpyAsync(b->entry.p, ref.p, nent * sizeof(uint32_t), hipMemcpyDeviceToDevice, st));
+    }
+    if (channels == 2 && ix->prow.n != ix->N) {
+        ix->prow.alloc(ix->N);
+        GF_HIP(gf::launch_invert_rows(ix->gidx.p, ix->N, ix->prow.p, st));
+    }
+    ensure_out(*b, K);
+    if (b->sched.n < Q) b->sched.alloc(Q);
 
-        const uint32_t hsize = std::max<uint32_t>(256, next_pow2(2 * (L + gf::kXSlots + 4 * R)));
-        uint32_t hbits = 0;
-        while ((1u << hbits) < hsize) ++hbits;
-        const uint32_t Lpad = round_up(L, 2);
-        const uint32_t lds = gf::trav_lds_bytes(Lpad, hsize, ix->P);
-        GF_REQUIRE(lds <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
+    // Visited-set size: twice the keys live between two resets (the list,
+    // the slots of four expansions and a cell's cross slots; the dual
+    // channel's expansions fill 2R slots).
+    const uint32_t hsize = std::max<uint32_t>(
+        256, next_pow2(2 * (L + gf::kXSlots + (channels == 2 ? 10 * R : 4 * R))));
+    uint32_t hbits = 0;
+    while ((1u << hbits) < hsize) ++hbits;
+    const uint32_t Lpad = round_up(L, 2);
+    const uint32_t lds = channels == 2 ? gf::trav_dual_lds_bytes(Lpad, hsize) : gf::trav_lds_bytes(Lpad, hsize, ix->P);
+    GF_REQUIRE(lds <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
 
-        // device scalars: tot[2] pairs, [3] fits, [4] items, [8..11] traversal /
-        // brute-force / empty / full-graph counts, [12..13] traversal range,
-        // [14..15] brute-force range, [16..17] full-graph range
-        uint32_t* tot = b->tot.p;
-        gf::TravArgs a{};
-        a.vec = ix->vec.p;
-        a.rowbytes = ix->rowbytes;
-        a.nch = ix->rs.nch;
-        a.attrs = ix->attrs.p;
-        a.graph = ix->graph.p;
-        a.cross = ix->cross.p;
-        a.xrow = uint64_t(ix->P) * ix->E;
-        a.xcell = ix->E;
-        a.offset = ix->offset.p;
-        a.gidx = ix->gidx.p;
-        a.lrow = ix->lrow.p;
-        if (ix->vdtype == GF_VEC_F16) {
-            a.queries = reinterpret_cast<const char*>(b->q16v.p);
-            a.qbytes = ix->D * 2;
-        } else if (ix->vdtype == GF_VEC_I8Q) {
-            a.queries = reinterpret_cast<const char*>(b->qi8q.p);
-            a.qbytes = ix->D * 8;
-        } else {
-            a.queries = reinterpret_cast<const char*>(b->qf32.p);
-            a.qbytes = ix->D * 4;
-        }
-        a.lo = b->lo.p;
-        a.hi = b->hi.p;
-        a.cells = b->cells.p;
-        a.counts = b->counts.p;
-        a.little = b->little.p;
-        a.sched = b->sched.p;
-        a.entry = b->entry.p;
-        a.out_ids = b->out_ids.p;
-        a.out_dist = b->out_dist.p;
-        a.counters = b->counters.p;
-        a.a = ix->a; a.P = ix->P; a.R = R; a.E = ix->E; a.L = L; a.K = K; a.rl = rl;
-        a.hbits = hbits;
-        a.offl = gf::trav_offsets_in_lds(ix->P) ? 1u : 0u;
-        a.Lpad = Lpad;
-        // The full-graph route: its own visited-set size (L + FD list and B
-        // region entries plus four expansions' FD between resets).
-        gf::TravArgs af = a;
-        uint32_t lds_f = 0;
-        if (ix->FD) {
-            const uint32_t hs = std::max<uint32_t>(256, next_pow2(2 * (L + 5 * ix->FD)));
-            af.hbits = 0;
-            while ((1u << af.hbits) < hs) ++af.hbits;
-            lds_f = Lpad * 8 + gf::kXSlots * 8 + 128 * 4 + hs * 4;
-            GF_REQUIRE(lds_f <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
-            af.fgraph = ix->fgraph.p;
-            af.fentry = ix->fentry.p;
-            af.FD = ix->FD;
-            af.frange = tot + 16;
-        }
+    // device scalars: tot[2] pairs, [3] fits, [4] items, [8..11] traversal /
+    // brute-force / empty / full-graph counts, [12..13] traversal range,
+    // [14..15] brute-force range, [16..17] full-graph range
+    uint32_t* tot = b->tot.p;
+    gf::TravArgs a{};
+    a.vec = ix->vec.p;
+    a.rowbytes = ix->rowbytes;
+    a.nch = ix->rs.nch;
+    a.attrs = ix->attrs.p;
+    a.graph = ix->graph.p;
+    a.cross = ix->cross.p;
+    a.xrow = uint64_t(ix->P) * ix->E;
+    a.xcell = ix->E;
+    a.offset = ix->offset.p;
+    a.gidx = ix->gidx.p;
+    a.lrow = ix->lrow.p;
+    a.prow = ix->prow.p;
+    if (ix->vdtype == GF_VEC_F16) {
+        a.queries = reinterpret_cast<const char*>(b->q16v.p);
+        a.qbytes = ix->D * 2;
+    } else if (ix->vdtype == GF_VEC_I8Q) {
+        a.queries = reinterpret_cast<const char*>(b->qi8q.p);
+        a.qbytes = ix->D * 8;
+    } else {
+        a.queries = reinterpret_cast<const char*>(b->qf32.p);
+        a.qbytes = ix->D * 4;
+    }
+    a.lo = b->lo.p;
+    a.hi = b->hi.p;
+    a.cells = b->cells.p;
+    a.counts = b->counts.p;
+    a.little = b->little.p;
+    a.sched = b->sched.p;
+    a.entry = b->entry.p;
+    a.out_ids = b->out_ids.p;
+    a.out_dist = b->out_dist.p;
+    a.counters = b->counters.p;
+    a.a = ix->a; a.P = ix->P; a.R = R; a.E = ix->E; a.L = L; a.K = K; a.rl = rl;
+    a.hbits = hbits;
+    a.offl = gf::trav_offsets_in_lds(ix->P) ? 1u : 0u;
+    a.Lpad = Lpad;
+    // The full-graph route: its own visited-set size (L + FD list and B
+    // region entries plus four expansions' FD between resets).
+    gf::TravArgs af = a;
+    uint32_t lds_f = 0;
+    if (ix->FD) {
+        const uint32_t hs = std::max<uint32_t>(256, next_pow2(2 * (L + 5 * ix->FD)));
+        af.hbits = 0;
+        while ((1u << af.hbits) < hs) ++af.hbits;
+        lds_f = Lpad * 8 + gf::kXSlots * 8 + 128 * 4 + hs * 4;
+        GF_REQUIRE(lds_f <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
+        af.fgraph = ix->fgraph.p;
+        af.fentry = ix->fentry.p;
+        af.FD = ix->FD;
+        af.frange = tot + 16;
+    }
 
-        // Brute-force route on MFMA when vectors and queries are int8-exact:
-        // work items of (sub-cell, <= 64 queries whose range reaches it),
-        // scheduled on the device.
-        const bool gemm = ix->i8 && b->i8 && K <= gf::kBfKMax;
-        const uint32_t NS = ix->NS;
-        b->pass_pending = gemm && !b->sel_exact;
-        if (gemm) {
-            if (!b->bcnt.n) {
-                b->bcnt.alloc(NS); b->bin.alloc(NS); b->bstart.alloc(NS); b->icnt.alloc(NS); b->ioff.alloc(NS);
-                b->nsub.alloc(Q); b->part_off.alloc(Q); b->pcnt.alloc(Q);
-            }
-            // item slots: a sub-cell adds up to two partial query blocks per
-            // tile chunk beyond pairs / 64
-            const size_t islots = size_t(NS) + ix->ntile / gf::kBfMaxItemTiles + 1;
-            if (!b->part.n) b->alloc_pairs(size_t(Q) * 64, K, Q, NS, islots);
-            if (b->rq.n < Q) {
-                b->rq.alloc(Q); b->rseed.alloc(Q);
-                b->rlo.alloc(size_t(Q) * ix->a); b->rhi.alloc(size_t(Q) * ix->a);
-            }
-            if (b->scnt.n < NS) {
-                b->scnt.alloc(NS);
-                // a seed sub-cell s with ns queries makes ceil(ns / 64) items per
-                // chunk of kBfSeedTiles tiles; every query seeds one sub-cell
-                uint32_t tmax = 0;
-                for (uint32_t s = 0; s < NS; ++s) tmax = std::max(tmax, ix->stile_h[s + 1] - ix->stile_h[s]);
-                const size_t chunks = (tmax + gf::kBfSeedTiles - 1) / gf::kBfSeedTiles;
-                b->sitems.alloc((size_t(Q) / gf::kBfQB + NS + 1) * std::max<size_t>(chunks, 1));
-            }
-            if (b->part.n < b->pair_cap * K) b->part.alloc(b->pair_cap * K);
-            if (b->gbound.n < Q) b->gbound.alloc(Q);
-            if (!b->bf_all && b->bfmask.n < size_t(Q) * ix->P) b->bfmask.alloc(size_t(Q) * ix->P);
+    // Brute-force route on MFMA when vectors and queries are int8-exact:
+    // work items of (sub-cell, <= 64 queries whose range reaches it),
+    // scheduled on the device.
+    const bool gemm = ix->i8 && b->i8 && K <= gf::kBfKMax;
+    const uint32_t NS = ix->NS;
+    b->pass_pending = gemm && !b->sel_exact;
+    if (gemm) {
+        if (!b->bcnt.n) {
+            b->bcnt.alloc(NS); b->bin.alloc(NS); b->bstart.alloc(NS); b->icnt.alloc(NS); b->ioff.alloc(NS);
+            b->nsub.alloc(Q); b->part_off.alloc(Q); b->pcnt.alloc(Q);
         }
-        // events: [0] search start, [1] after traversal, [2] end, [3..4] around the MFMA kernel alone
-        // Device timestamps (wall clock, kernels on the stream, so that they
-        // time a replayed graph too): [0] search start, [1] after traversal,
-        // [2] end, [3..4] around the MFMA brute-force launches.
-        if (!b->stamps.n) { b->stamps.alloc(8); b->h_stamps.alloc(8); }
-        uint64_t* stamp = b->stamps.p;
-        auto launch_gemm = [&]() {
-            gf::BfSchedArgs sc{};
-            sc.sa = sub_args(*ix);
-            sc.Q = Q; sc.postfilter = opts->postfilter; sc.counts = b->counts.p;
-            sc.little = b->little.p; sc.lo = b->lo.p; sc.hi = b->hi.p; sc.nsub = b->nsub.p; sc.bcnt = b->bcnt.p; sc.bin = b->bin.p;
-            sc.bstart = b->bstart.p; sc.bq = b->bq.p; sc.qcap = b->qcap;
-            sc.ok = tot + 3; sc.nbf = tot + 9;
-            sc.qlist = b->sched.p; sc.qrange = tot + 14;   // the brute-force queries of the schedule
-            sc.tch = gf::kBfMaxItemTiles;
-            if (!b->bf_all) {
-                GF_HIP(gf::launch_cell_flags(Q, ix->P, b->cells.p, b->counts.p, b->little.p, b->bfmask.p, st));
-                sc.bfm = b->bfmask.p;
-                sc.bP = ix->P;
-            }
-            // Seeds (one-pass lists): each query's best-filled sub-cell runs first.
-            const bool seeds = b->qcap != 0;
-            GF_HIP(gf::launch_bf_reset(Q, b->nsub.p, b->pcnt.p, b->gbound.p, st, seeds ? NS : 0,
-                                       seeds ? b->scnt.p : nullptr, seeds ? tot + 5 : nullptr));
+        // item slots: a sub-cell adds up to two partial query blocks per
+        // tile chunk beyond pairs / 64
+        const size_t islots = size_t(NS) + ix->ntile / gf::kBfMaxItemTiles + 1;
+        if (!b->part.n) b->alloc_pairs(size_t(Q) * 64, K, Q, NS, islots);
+        if (b->rq.n < Q) {
+            b->rq.alloc(Q); b->rseed.alloc(Q);
+            b->rlo.alloc(size_t(Q) * ix->a); b->rhi.alloc(size_t(Q) * ix->a);
+        }
+        if (b->scnt.n < NS) {
+            b->scnt.alloc(NS);
+            // a seed sub-cell s with ns queries makes ceil(ns / 64) items per
+            // chunk of kBfSeedTiles tiles; every query seeds one sub-cell
+            uint32_t tmax = 0;
+            for (uint32_t s = 0; s < NS; ++s) tmax = std::max(tmax, ix->stile_h[s + 1] - ix->stile_h[s]);
+            const size_t chunks = (tmax + gf::kBfSeedTiles - 1) / gf::kBfSeedTiles;
+            b->sitems.alloc((size_t(Q) / gf::kBfQB + NS + 1) * std::max<size_t>(chunks, 1));
+        }
+        if (b->part.n < b->pair_cap * K) b->part.alloc(b->pair_cap * K);
+        if (b->gbound.n < Q) b->gbound.alloc(Q);
+        if (!b->bf_all && b->bfmask.n < size_t(Q) * ix->P) b->bfmask.alloc(size_t(Q) * ix->P);
+    }
+    // events: [0] search start, [1] after traversal, [2] end, [3..4] around the MFMA kernel alone
+    // Device timestamps (wall clock, kernels on the stream, so that they
+    // time a replayed graph too): [0] search start, [1] after traversal,
+    // [2] end, [3..4] around the MFMA brute-force launches.
+    if (!b->stamps.n) { b->stamps.alloc(8); b->h_stamps.alloc(8); }
+    uint64_t* stamp = b->stamps.p;
+    auto launch_gemm = [&]() {
+        gf::BfSchedArgs sc{};
+        sc.sa = sub_args(*ix);
+        sc.Q = Q; sc.postfilter = opts->postfilter; sc.counts = b->counts.p;
+        sc.little = b->little.p; sc.lo = b->lo.p; sc.hi = b->hi.p; sc.nsub = b->nsub.p; sc.bcnt = b->bcnt.p; sc.bin = b->bin.p;
+        sc.bstart = b->bstart.p; sc.bq = b->bq.p; sc.qcap = b->qcap;
+        sc.ok = tot + 3; sc.nbf = tot + 9;
+        sc.qlist = b->sched.p; sc.qrange = tot + 14;   // the brute-force queries of the schedule
+        sc.tch = gf::kBfMaxItemTiles;
+        if (!b->bf_all) {
+            GF_HIP(gf::launch_cell_flags(Q, ix->P, b->cells.p, b->counts.p, b->little.p, b->bfmask.p, st));
+            sc.bfm = b->bfmask.p;
+            sc.bP = ix->P;
+        }
+        // Seeds (one-pass lists): each query's best-filled sub-cell runs first.
+        const bool seeds = b->qcap != 0;
+        GF_HIP(gf::launch_bf_reset(Q, b->nsub.p, b->pcnt.p, b->gbound.p, st, seeds ? NS : 0,
+                                   seeds ? b->scnt.p : nullptr, seeds ? tot + 5 : nullptr));
+        if (seeds) {
+            gf::BfSeedArgs sd{};
+            sd.sa = sc.sa; sd.Q = Q; sd.postfilter = sc.postfilter; sd.counts = sc.counts; sd.little = sc.little;
+            sd.cells = b->cells.p; sd.lo = sc.lo; sd.hi = sc.hi; sd.bfm = sc.bfm; sd.bP = sc.bP;
+            sd.qlist = sc.qlist; sd.qrange = sc.qrange; sd.qcap = b->qcap; sd.tch = gf::kBfSeedTiles;
+            sd.itch = gf::kBfMaxItemTiles;
+            sd.scnt = b->scnt.p; sd.bq = b->bq.p; sd.nsub = b->nsub.p;
+            sd.rq = b->rq.p; sd.rseed = b->rseed.p; sd.rlo = b->rlo.p; sd.rhi = b->rhi.p;
+            GF_HIP(gf::launch_bfseed(sd, Q, st));
+            sc.scnt = b->scnt.p;
+            sc.rq = b->rq.p; sc.rseed = b->rseed.p; sc.rlo = b->rlo.p; sc.rhi = b->rhi.p;
+        }
+        if (seeds) GF_HIP(gf::launch_bfsched_direct(sc, st));
+        else GF_HIP(gf::launch_bfsched(sc, false, st));
+        if (!b->qcap) GF_HIP(gf::launch_scan_small(b->bcnt.p, NS, b->bstart.p, st));
+        GF_HIP(gf::launch_scan_small(b->nsub.p, Q, b->part_off.p, st));
+        GF_HIP(gf::launch_total(b->nsub.p, b->part_off.p, Q, uint32_t(std::min<size_t>(b->pair_cap, UINT32_MAX)), K,
+                                b->part.n, tot + 2, st));
+        if (!b->qcap) GF_HIP(gf::launch_bfsched(sc, true, st));
+        // Two passes (resident index): the seeds and the items of the
+        // first-pass sub-cells, then a merge that lowers each query's
+        // bound to the K-th smallest distance found so far, then the rest
+        // of the items under those bounds.  Both k_bfitems launches take
+        // the sub-cells in the same order (counts, scan, fill).
+        const bool two = ix->sorder.n == NS && ix->ns1 > 0 && ix->ns1 < NS;
+        GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, b->qcap, ix->stile.p, gf::kBfMaxItemTiles, NS, b->icnt.p, b->ioff.p,
+                                  b->items.p, tot + 4, tot + 3, false, st, nullptr, nullptr, nullptr, 0,
+                                  two ? ix->sorder.p : nullptr, two ? ix->ns1 : 0u, nullptr));
+        GF_HIP(gf::launch_scan_small(b->icnt.p, NS, b->ioff.p, st));
+        const uint32_t scap = uint32_t(b->sitems.n);
+        GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, b->qcap, ix->stile.p, gf::kBfMaxItemTiles, NS, b->icnt.p, b->ioff.p,
+                                  b->items.p, tot + 4, tot + 3, true, st, seeds ? b->scnt.p : nullptr,
+                                  b->sitems.p, tot + 5, scap, two ? ix->sorder.p : nullptr, two ? ix->ns1 : 0u,
+                                  two ? tot + 6 : nullptr, gf::kBfSeedTiles));
+        gf::BfGemmArgs ga{};
+        ga.sa = sub_args(*ix);
+        ga.vt = ix->vt.p; ga.tnorm = ix->tnorm.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p;
+        ga.hi = b->hi.p; ga.items = b->items.p; ga.nitems = tot + 4; ga.bq = b->bq.p; ga.pcnt = b->pcnt.p;
+        ga.part_off = b->part_off.p; ga.part = b->part.p; ga.gbound = b->gbound.p;
+        ga.ok = tot + 3;
+        if (seeds) { ga.sitems = b->sitems.p; ga.nseed = tot + 5; ga.nseed_cap = scap; ga.seeds_on = 1; }
+        ga.K = K; ga.D = ix->D;
+        gf::BfFinalArgs fa{};
+        fa.gbound = b->gbound.p; fa.bfq = b->sched.p; fa.srange = tot + 14; fa.part_off = b->part_off.p; fa.pcnt = b->pcnt.p;
+        fa.ok = tot + 3; fa.part = b->part.p; fa.counts = b->counts.p; fa.cells = b->cells.p;
+        fa.offset = ix->offset.p; fa.selcount = b->selcount.p; fa.gidx = ix->gidx.p; fa.out_ids = b->out_ids.p;
+        fa.out_dist = b->out_dist.p; fa.counters = b->counters.p; fa.K = K; fa.P = ix->P;
+        GF_HIP(gf::launch_stamp(stamp + 3, st));
+        if (two) {
+            // the seeds alone, then a merge (each query's bound becomes the
+            // K-th of its seed sub-cell), the first pass under those
+            // bounds, a merge, the rest
+            ga.nitems_a = tot + 6;
             if (seeds) {
-                gf::BfSeedArgs sd{};
-                sd.sa = sc.sa; sd.Q = Q; sd.postfilter = sc.postfilter; sd.counts = sc.counts; sd.little = sc.little;
-                sd.cells = b->cells.p; sd.lo = sc.lo; sd.hi = sc.hi; sd.bfm = sc.bfm; sd.bP = sc.bP;
-                sd.qlist = sc.qlist; sd.qrange = sc.qrange; sd.qcap = b->qcap; sd.tch = gf::kBfSeedTiles;
-                sd.itch = gf::kBfMaxItemTiles;
-                sd.scnt = b->scnt.p; sd.bq = b->bq.p; sd.nsub = b->nsub.p;
-                sd.rq = b->rq.p; sd.rseed = b->rseed.p; sd.rlo = b->rlo.p; sd.rhi = b->rhi.p;
-                GF_HIP(gf::launch_bfseed(sd, Q, st));
-                sc.scnt = b->scnt.p;
-                sc.rq = b->rq.p; sc.rseed = b->rseed.p; sc.rlo = b->rlo.p; sc.rhi = b->rhi.p;
-            }
-            if (seeds) GF_HIP(gf::launch_bfsched_direct(sc, st));
-            else GF_HIP(gf::launch_bfsched(sc, false, st));
-            if (!b->qcap) GF_HIP(gf::launch_scan_small(b->bcnt.p, NS, b->bstart.p, st));
-            GF_HIP(gf::launch_scan_small(b->nsub.p, Q, b->part_off.p, st));
-            GF_HIP(gf::launch_total(b->nsub.p, b->part_off.p, Q, uint32_t(std::min<size_t>(b->pair_cap, UINT32_MAX)), K,
-                                    b->part.n, tot + 2, st));
-            if (!b->qcap) GF_HIP(gf::launch_bfsched(sc, true, st));
-            // Two passes (resident index): the seeds and the items of the
-            // first-pass sub-cells, then a merge that lowers each query's
-            // bound to the K-th smallest distance found so far, then the rest
-            // of the items under those bounds.  Both k_bfitems launches take
-            // the sub-cells in the same order (counts, scan, fill).
-            const bool two = ix->sorder.n == NS && ix->ns1 > 0 && ix->ns1 < NS;
-            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, b->qcap, ix->stile.p, gf::kBfMaxItemTiles, NS, b->icnt.p, b->ioff.p,
-                                      b->items.p, tot + 4, tot + 3, false, st, nullptr, nullptr, nullptr, 0,
-                                      two ? ix->sorder.p : nullptr, two ? ix->ns1 : 0u, nullptr));
-            GF_HIP(gf::launch_scan_small(b->icnt.p, NS, b->ioff.p, st));
-            const uint32_t scap = uint32_t(b->sitems.n);
-            GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, b->qcap, ix->stile.p, gf::kBfMaxItemTiles, NS, b->icnt.p, b->ioff.p,
-                                      b->items.p, tot + 4, tot + 3, true, st, seeds ? b->scnt.p : nullptr,
-                                      b->sitems.p, tot + 5, scap, two ? ix->sorder.p : nullptr, two ? ix->ns1 : 0u,
-                                      two ? tot + 6 : nullptr, gf::kBfSeedTiles));
-            gf::BfGemmArgs ga{};
-            ga.sa = sub_args(*ix);
-            ga.vt = ix->vt.p; ga.tnorm = ix->tnorm.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p;
-            ga.hi = b->hi.p; ga.items = b->items.p; ga.nitems = tot + 4; ga.bq = b->bq.p; ga.pcnt = b->pcnt.p;
-            ga.part_off = b->part_off.p; ga.part = b->part.p; ga.gbound = b->gbound.p;
-            ga.ok = tot + 3;
-            if (seeds) { ga.sitems = b->sitems.p; ga.nseed = tot + 5; ga.nseed_cap = scap; ga.seeds_on = 1; }
-            ga.K = K; ga.D = ix->D;
-            gf::BfFinalArgs fa{};
-            fa.gbound = b->gbound.p; fa.bfq = b->sched.p; fa.srange = tot + 14; fa.part_off = b->part_off.p; fa.pcnt = b->pcnt.p;
-            fa.ok = tot + 3; fa.part = b->part.p; fa.counts = b->counts.p; fa.cells = b->cells.p;
-            fa.offset = ix->offset.p; fa.selcount = b->selcount.p; fa.gidx = ix->gidx.p; fa.out_ids = b->out_ids.p;
-            fa.out_dist = b->out_dist.p; fa.counters = b->counters.p; fa.K = K; fa.P = ix->P;
-            GF_HIP(gf::launch_stamp(stamp + 3, st));
-            if (two) {
-                // the seeds alone, then a merge (each query's bound becomes the
-                // K-th of its seed sub-cell), the first pass under those
-                // bounds, a merge, the rest
-                ga.nitems_a = tot + 6;
-                if (seeds) {
-                    ga.irange = 3;
-                    GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu), st));
-                    fa.bound_only = 1;
-                    GF_HIP(gf::launch_bf_final(fa, Q, st));
-                    ga.seeds_on = 0;
-                }
-                ga.irange = 1;
+                ga.irange = 3;
                 GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu), st));
                 fa.bound_only = 1;
                 GF_HIP(gf::launch_bf_final(fa, Q, st));
-                fa.bound_only = 0;
-                ga.irange = 2;
+                ga.seeds_on = 0;
             }
+            ga.irange = 1;
             GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu), st));
-            GF_HIP(gf::launch_stamp(stamp + 4, st));
+            fa.bound_only = 1;
             GF_HIP(gf::launch_bf_final(fa, Q, st));
-        };
+            fa.bound_only = 0;
+            ga.irange = 2;
+        }
+        GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu), st));
+        GF_HIP(gf::launch_stamp(stamp + 4, st));
+        GF_HIP(gf::launch_bf_final(fa, Q, st));
+    };
 
-        // Results, statistics and the schedule's totals come back through
-        // pinned staging with one synchronisation.
-        const size_t nr = size_t(Q) * K;
-        if (b->h_ids.n < nr) { b->h_ids.alloc(nr); b->h_dist.alloc(nr); }
-        if (!b->h_tot.n) { b->h_tot.alloc(24); b->h_stats.alloc(16); }
-        if (stats && b->stats.n < 16) b->stats.alloc(16);
-        // Results go straight into the caller's arrays when HIP knows them as
-        // page-locked host memory; otherwise through the batch's pinned
-        // buffers and a host copy after the wait.
-        auto page_locked = [](const void* ptr) {
-            if (!ptr) return false;
-            hipPointerAttribute_t at{};
-            if (hipPointerGetAttributes(&at, ptr) != hipSuccess) {
-                (void)hipGetLastError();
-                return false;
-            }
-            return at.type == hipMemoryTypeHost;
-        };
-        const bool ids_direct = page_locked(ids), dist_direct = page_locked(dists);
-        uint32_t* ids_dst = ids_direct ? ids : b->h_ids.p;
-        float* dist_dst = dist_direct ? dists : b->h_dist.p;
-        auto enqueue_copies = [&]() {
-            if (stats) {
-                GF_HIP(gf::launch_zero_u32(reinterpret_cast<uint32_t*>(b->stats.p), 32, st));
-                gf::StatsArgs sa2{};
-                sa2.Q = Q; sa2.NS = gemm ? NS : 0; sa2.counters = b->counters.p; sa2.bcnt = gemm ? b->bcnt.p : nullptr;
-                sa2.bin = b->bin.p; sa2.split = b->qcap != 0; sa2.sseed = b->qcap ? b->scnt.p : nullptr;
-                sa2.ssize = ix->ssize.p; sa2.stile = ix->stile.p; sa2.out = b->stats.p;
-                GF_HIP(gf::launch_stats(sa2, st));
-                GF_HIP(hipMemcpyAsync(b->h_stats.p, b->stats.p, 16 * sizeof(unsigned long long), hipMemcpyDeviceToHost,
-                                      st));
-            }
-            GF_HIP(hipMemcpyAsync(b->h_tot.p, tot, 24 * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-            GF_HIP(hipMemcpyAsync(b->h_stamps.p, b->stamps.p, 8 * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
-            GF_HIP(hipMemcpyAsync(ids_dst, b->out_ids.p, nr * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-            if (dists) GF_HIP(hipMemcpyAsync(dist_dst, b->out_dist.p, nr * sizeof(float), hipMemcpyDeviceToHost, st));
-        };
-        auto enqueue_tail = [&]() {
-            enqueue_copies();
-            GF_HIP(hipStreamSynchronize(st));
-        };
-        // The whole stage, schedule to copies: no allocation, no host wait.
-        auto enqueue = [&]() {
-            // Schedule (gpu_graph.cu:12485-12493) on the device.
-            gf::SchedArgs sa{};
-            sa.Q = Q; sa.P = ix->P; sa.postfilter = opts->postfilter; sa.counts = b->counts.p; sa.little = b->little.p;
-            sa.sched = b->sched.p; sa.tot = tot + 8; sa.ranges = tot + 12;
-            sa.full = ix->FD ? 1u : 0u;
-            sa.franges = ix->FD ? tot + 16 : nullptr;
-            GF_HIP(gf::launch_reset_results(Q, K, b->out_ids.p, b->out_dist.p, b->counters.p, st));
-            GF_HIP(gf::launch_sched(sa, st));
-            GF_HIP(gf::launch_stamp(stamp + 0, st));
-            gf::TravArgs at = a;
-            at.srange = tot + 12;
-            GF_HIP(gf::launch_traverse(ix->rs, at, lds, Q, st));
-            // queries with postfilter or more cells: the full graph
-            if (ix->FD && opts->postfilter <= ix->P) GF_HIP(gf::launch_fullgraph(ix->rs, af, lds_f, Q, st));
-            GF_HIP(gf::launch_stamp(stamp + 1, st));
-            if (gemm) {
-                launch_gemm();
-            } else {
-                gf::TravArgs ab = a;
-                ab.srange = tot + 14;
-                GF_HIP(gf::launch_bruteforce(ix->rs, ab, Q, st));
-            }
-            GF_HIP(gf::launch_stamp(stamp + 2, st));
-            enqueue_copies();
-        };
-        // From a batch's second search on, the stage runs as a HIP graph,
-        // captured once per layout (buffers, options, route) and replayed:
-        // one launch instead of some twenty, no gaps between the kernels.
-        const uint64_t key[] = {uint64_t(L), K, rl, opts->postfilter, uint64_t(gemm), uint64_t(b->bf_all),
-                                uint64_t(b->qcap), uint64_t(stats != nullptr), uint64_t(dists != nullptr),
-                                uint64_t(uintptr_t(b->part.p)), uint64_t(uintptr_t(b->items.p)),
-                                uint64_t(uintptr_t(b->bq.p)), b->pair_cap, uint64_t(uintptr_t(b->out_ids.p)),
-                                uint64_t(uintptr_t(b->counters.p)), uint64_t(uintptr_t(b->sched.p)),
-                                uint64_t(uintptr_t(ids_dst)), uint64_t(uintptr_t(dist_dst)),
-                                uint64_t(uintptr_t(b->stats.p)), uint64_t(uintptr_t(b->bfmask.p)),
-                                uint64_t(uintptr_t(b->entry.p)), uint64_t(uintptr_t(b->sitems.p)),
-                                uint64_t(uintptr_t(b->out_dist.p)), uint64_t(uintptr_t(b->selcount.p)),
-                                uint64_t(uintptr_t(b->cells.p)), uint64_t(uintptr_t(b->gbound.p)),
-                                uint64_t(uintptr_t(b->scnt.p)), uint64_t(uintptr_t(b->rq.p)),
-                                uint64_t(uintptr_t(b->bcnt.p)), uint64_t(uintptr_t(b->h_tot.p)),
-                                uint64_t(uintptr_t(b->stamps.p)), uint64_t(uintptr_t(b->h_stamps.p))};
-        b->run_stage(std::vector<uint64_t>(std::begin(key), std::end(key)), st, enqueue);
-        GF_HIP(hipStreamSynchronize(st));
-        const uint32_t* dt = b->h_tot.p;
-        if (gemm && !dt[3]) {
-            // the pair lists outgrew their buffers: grow them and run the brute force again
-            b->alloc_pairs(size_t(dt[2]) + dt[2] / 4 + 1024, K, Q, NS, size_t(NS) + ix->ntile / gf::kBfMaxItemTiles + 1);
-            GF_HIP(gf::launch_stamp(stamp + 1, st));
-            launch_gemm();
-            GF_HIP(gf::launch_stamp(stamp + 2, st));
-            enqueue_tail();
-            GF_REQUIRE(dt[3], GF_E_STATE, "brute-force schedule does not fit after growing");
+    // Results, statistics and the schedule's totals come back through
+    // pinned staging with one synchronisation.
+    const size_t nr = size_t(Q) * K;
+    if (b->h_ids.n < nr) { b->h_ids.alloc(nr); b->h_dist.alloc(nr); }
+    if (!b->h_tot.n) { b->h_tot.alloc(24); b->h_stats.alloc(16); }
+    if (stats && b->stats.n < 16) b->stats.alloc(16);
+    // Results go straight into the caller's arrays when HIP knows them as
+    // page-locked host memory; otherwise through the batch's pinned
+    // buffers and a host copy after the wait.
+    auto page_locked = [](const void* ptr) {
+        if (!ptr) return false;
+        hipPointerAttribute_t at{};
+        if (hipPointerGetAttributes(&at, ptr) != hipSuccess) {
+            (void)hipGetLastError();
+            return false;
         }
-        if (!ids_direct) std::memcpy(ids, b->h_ids.p, nr * sizeof(uint32_t));
-        if (dists && !dist_direct) std::memcpy(dists, b->h_dist.p, nr * sizeof(float));
+        return at.type == hipMemoryTypeHost;
+    };
+    const bool ids_direct = page_locked(ids), dist_direct = page_locked(dists);
+    uint32_t* ids_dst = ids_direct ? ids : b->h_ids.p;
+    float* dist_dst = dist_direct ? dists : b->h_dist.p;
+    auto enqueue_copies = [&]() {
         if (stats) {
-            float t_tr = 0, t_bf = 0, t_g = 0;
-            const uint64_t* ts = b->h_stamps.p;
-            const double tick_ms = 1.0 / double(ix->wclk_khz);
-            t_tr = float(double(ts[1] - ts[0]) * tick_ms);
-            t_bf = float(double(ts[2] - ts[1]) * tick_ms);
-            if (gemm) t_g = float(double(ts[4] - ts[3]) * tick_ms);
-            const unsigned long long* sm = b->h_stats.p;
-            std::memset(stats, 0, sizeof(*stats));
-            stats->ms_traverse = t_tr;
-            stats->ms_bruteforce = t_bf;
-            stats->ms_total = double(t_tr) + double(t_bf);
-            stats->ms_bf_kernel = t_g;
-            stats->graph = b->graph_replayed ? 1u : 0u;
-            stats->q_traverse = dt[8];
-            stats->q_bruteforce = dt[9];
-            stats->q_empty = dt[10];
-            stats->q_fullgraph = ix->FD ? dt[11] : 0u;
-            stats->n_expand = sm[0]; stats->n_dist = sm[1]; stats->n_attr = sm[2]; stats->n_cross = sm[3];
-            stats->n_lrow = sm[4]; stats->n_scan = sm[5]; stats->n_pass = sm[6];
-            // Algorithmic bytes: what each kernel must read from HBM given
-            // its counters (rows gathered, graph rows, attributes, cross-edge
-            // slices, local-id lookups unless the offsets sit in LDS) plus
-            // its result writes.
-            const double t_dist = double(sm[7]), b_dist = double(sm[8]);
-            const double lrow_bytes = gf::trav_offsets_in_lds(ix->P) ? 0.0 : 4.0;
-            stats->bytes_traverse = t_dist * ix->rowbytes + double(stats->n_expand) * R * 4.0 +
-                                    double(stats->n_attr) * ix->a * 4.0 + double(stats->n_cross) * ix->E * 4.0 +
-                                    double(stats->n_lrow) * lrow_bytes + double(dt[8]) * (K * 8.0 + ix->P * 4.0);
-            if (gemm && dt[9]) {
-                // Item schedule: every (query, sub-cell) pair costs 2 D ops per
-                // point; every item streams its sub-cell's tiles once; the final
-                // merge reads the appended keys.
-                const double tile_bytes = (ix->D / 64) * 1024.0 + 32 * 4.0 + 16.0 * (1 + ix->AW) * 4.0;
-                stats->ops_bruteforce = 2.0 * ix->D * double(sm[9]);
-                stats->bytes_bruteforce = double(sm[10]) * tile_bytes + double(dt[9]) * K * 16.0;
-                stats->bf_mfma = 1;
-            } else {
-                stats->bytes_bruteforce = double(stats->n_scan) * ix->a * 4.0 + b_dist * ix->rowbytes +
-                                          double(dt[9]) * (K * 8.0 + ix->P * 4.0);
-                stats->ops_bruteforce = 3.0 * b_dist * ix->D;
-                stats->bf_mfma = 0;
-            }
-            stage_times();
+            GF_HIP(gf::launch_zero_u32(reinterpret_cast<uint32_t*>(b->stats.p), 32, st));
+            gf::StatsArgs sa2{};
+            sa2.Q = Q; sa2.NS = gemm ? NS : 0; sa2.counters = b->counters.p; sa2.bcnt = gemm ? b->bcnt.p : nullptr;
+            sa2.bin = b->bin.p; sa2.split = b->qcap != 0; sa2.sseed = b->qcap ? b->scnt.p : nullptr;
+            sa2.ssize = ix->ssize.p; sa2.stile = ix->stile.p; sa2.out = b->stats.p;
+            GF_HIP(gf::launch_stats(sa2, st));
+            GF_HIP(hipMemcpyAsync(b->h_stats.p, b->stats.p, 16 * sizeof(unsigned long long), hipMemcpyDeviceToHost,
+                                  st));
         }
+        GF_HIP(hipMemcpyAsync(b->h_tot.p, tot, 24 * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+        GF_HIP(hipMemcpyAsync(b->h_stamps.p, b->stamps.p, 8 * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
+        GF_HIP(hipMemcpyAsync(ids_dst, b->out_ids.p, nr * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+        if (dists) GF_HIP(hipMemcpyAsync(dist_dst, b->out_dist.p, nr * sizeof(float), hipMemcpyDeviceToHost, st));
+    };
+    auto enqueue_tail = [&]() {
+        enqueue_copies();
+        GF_HIP(hipStreamSynchronize(st));
+    };
+    // The whole stage, schedule to copies: no allocation, no host wait.
+    auto enqueue = [&]() {
+        // Schedule (gpu_graph.cu:12485-12493) on the device.
+        gf::SchedArgs sa{};
+        sa.Q = Q; sa.P = ix->P; sa.postfilter = opts->postfilter; sa.counts = b->counts.p; sa.little = b->little.p;
+        sa.sched = b->sched.p; sa.tot = tot + 8; sa.ranges = tot + 12;
+        sa.full = ix->FD ? 1u : 0u;
+        sa.franges = ix->FD ? tot + 16 : nullptr;
+        GF_HIP(gf::launch_reset_results(Q, K, b->out_ids.p, b->out_dist.p, b->counters.p, st));
+        GF_HIP(gf::launch_sched(sa, st));
+        GF_HIP(gf::launch_stamp(stamp + 0, st));
+        gf::TravArgs at = a;
+        at.srange = tot + 12;
+        if (channels == 2) GF_HIP(gf::launch_traverse_dual(ix->rs, at, lds, Q, st));
+        else GF_HIP(gf::launch_traverse(ix->rs, at, lds, Q, st));
+        // queries with postfilter or more cells: the full graph
+        if (ix->FD && opts->postfilter <= ix->P) GF_HIP(gf::launch_fullgraph(ix->rs, af, lds_f, Q, st));
+        GF_HIP(gf::launch_stamp(stamp + 1, st));
+        if (gemm) {
+            launch_gemm();
+        } else {
+            gf::TravArgs ab = a;
+            ab.srange = tot + 14;
+            GF_HIP(gf::launch_bruteforce(ix->rs, ab, Q, st));
+        }
+        GF_HIP(gf::launch_stamp(stamp + 2, st));
+        enqueue_copies();
+    };
+    // From a batch's second search on, the stage runs as a HIP graph,
+    // captured once per layout (buffers, options, route) and replayed:
+    // one launch instead of some twenty, no gaps between the kernels.
+    const uint64_t key[] = {uint64_t(L), K, rl, opts->postfilter, uint64_t(gemm), uint64_t(b->bf_all), channels,
+                            uint64_t(b->qcap), uint64_t(stats != nullptr), uint64_t(dists != nullptr),
+                            uint64_t(uintptr_t(b->part.p)), uint64_t(uintptr_t(b->items.p)),
+                            uint64_t(uintptr_t(b->bq.p)), b->pair_cap, uint64_t(uintptr_t(b->out_ids.p)),
+                            uint64_t(uintptr_t(b->counters.p)), uint64_t(uintptr_t(b->sched.p)),
+                            uint64_t(uintptr_t(ids_dst)), uint64_t(uintptr_t(dist_dst)),
+                            uint64_t(uintptr_t(b->stats.p)), uint64_t(uintptr_t(b->bfmask.p)),
+                            uint64_t(uintptr_t(b->entry.p)), uint64_t(uintptr_t(b->sitems.p)),
+                            uint64_t(uintptr_t(b->out_dist.p)), uint64_t(uintptr_t(b->selcount.p)),
+                            uint64_t(uintptr_t(b->cells.p)), uint64_t(uintptr_t(b->gbound.p)),
+                            uint64_t(uintptr_t(b->scnt.p)), uint64_t(uintptr_t(b->rq.p)),
+                            uint64_t(uintptr_t(b->bcnt.p)), uint64_t(uintptr_t(b->h_tot.p)),
+                            uint64_t(uintptr_t(b->stamps.p)), uint64_t(uintptr_t(b->h_stamps.p))};
+    b->run_stage(std::vector<uint64_t>(std::begin(key), std::end(key)), st, enqueue);
+    GF_HIP(hipStreamSynchronize(st));
+    const uint32_t* dt = b->h_tot.p;
+    if (gemm && !dt[3]) {
+        // the pair lists outgrew their buffers: grow them and run the brute force again
+        b->alloc_pairs(size_t(dt[2]) + dt[2] / 4 + 1024, K, Q, NS, size_t(NS) + ix->ntile / gf::kBfMaxItemTiles + 1);
+        GF_HIP(gf::launch_stamp(stamp + 1, st));
+        launch_gemm();
+        GF_HIP(gf::launch_stamp(stamp + 2, st));
+        enqueue_tail();
+        GF_REQUIRE(dt[3], GF_E_STATE, "brute-force schedule does not fit after growing");
+    }
+    if (!ids_direct) std::memcpy(ids, b->h_ids.p, nr * sizeof(uint32_t));
+    if (dists && !dist_direct) std::memcpy(dists, b->h_dist.p, nr * sizeof(float));
+    if (stats) {
+        float t_tr = 0, t_bf = 0, t_g = 0;
+        const uint64_t* ts = b->h_stamps.p;
+        const double tick_ms = 1.0 / double(ix->wclk_khz);
+        t_tr = float(double(ts[1] - ts[0]) * tick_ms);
+        t_bf = float(double(ts[2] - ts[1]) * tick_ms);
+        if (gemm) t_g = float(double(ts[4] - ts[3]) * tick_ms);
+        const unsigned long long* sm = b->h_stats.p;
+        std::memset(stats, 0, sizeof(*stats));
+        stats->ms_traverse = t_tr;
+        stats->ms_bruteforce = t_bf;
+        stats->ms_total = double(t_tr) + double(t_bf);
+        stats->ms_bf_kernel = t_g;
+        stats->graph = b->graph_replayed ? 1u : 0u;
+        stats->q_traverse = dt[8];
+        stats->q_bruteforce = dt[9];
+        stats->q_empty = dt[10];
+        stats->q_fullgraph = ix->FD ? dt[11] : 0u;
+        stats->n_expand = sm[0]; stats->n_dist = sm[1]; stats->n_attr = sm[2]; stats->n_cross = sm[3];
+        stats->n_lrow = sm[4]; stats->n_scan = sm[5]; stats->n_pass = sm[6];
+        // Algorithmic bytes: what each kernel must read from HBM given
+        // its counters (rows gathered, graph rows, attributes, cross-edge
+        // slices, local-id lookups unless the offsets sit in LDS) plus
+        // its result writes.
+        const double t_dist = double(sm[7]), b_dist = double(sm[8]);
+        const double lrow_bytes = gf::trav_offsets_in_lds(ix->P) ? 0.0 : 4.0;
+        stats->bytes_traverse = t_dist * ix->rowbytes + double(stats->n_expand) * R * 4.0 +
+                                double(stats->n_attr) * ix->a * 4.0 + double(stats->n_cross) * ix->E * 4.0 +
+                                double(stats->n_lrow) * lrow_bytes + double(dt[8]) * (K * 8.0 + ix->P * 4.0);
+        if (gemm && dt[9]) {
+            // Item schedule: every (query, sub-cell) pair costs 2 D ops per
+            // point; every item streams its sub-cell's tiles once; the final
+            // merge reads the appended keys.
+            const double tile_bytes = (ix->D / 64) * 1024.0 + 32 * 4.0 + 16.0 * (1 + ix->AW) * 4.0;
+            stats->ops_bruteforce = 2.0 * ix->D * double(sm[9]);
+            stats->bytes_bruteforce = double(sm[10]) * tile_bytes + double(dt[9]) * K * 16.0;
+            stats->bf_mfma = 1;
+        } else {
+            stats->bytes_bruteforce = double(stats->n_scan) * ix->a * 4.0 + b_dist * ix->rowbytes +
+                                      double(dt[9]) * (K * 8.0 + ix->P * 4.0);
+            stats->ops_bruteforce = 3.0 * b_dist * ix->D;
+            stats->bf_mfma = 0;
+        }
+        stage_times();
+    }
+}
+
+gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, float* dists,
+                    gf_search_stats* stats) {
+    return run_guarded([&] { search_resident(b, opts, ids, dists, stats, 1); });
+}
+
+gf_status gf_search_dual(gf_batch* b, const gf_search_opts* opts, uint32_t* ids, float* dists,
+                         gf_search_stats* stats) {
+    return run_guarded([&] {
+        GF_REQUIRE(b && !b->ix->sx, GF_E_UNSUPPORTED, "gf_search_dual needs a resident index");
+        GF_REQUIRE(b->ix->R <= 32, GF_E_UNSUPPORTED, "gf_search_dual supports R <= 32");
+        search_resident(b, opts, ids, dists, stats, 2);
     });
 }
 

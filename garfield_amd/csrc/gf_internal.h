@@ -23,6 +23,11 @@ inline bool trav_offsets_in_lds(uint32_t P) { return P + 1 <= kOffLds; }
 inline uint32_t trav_lds_bytes(uint32_t Lpad, uint32_t hsize, uint32_t P) {
     return Lpad * 8 + kXSlots * 8 + 128 * 4 + hsize * 4 + (trav_offsets_in_lds(P) ? (P + 1) * 4 : 0);
 }
+// LDS bytes of the dual-channel traversal: candidate list, switch slots and
+// evictees, row list, visited set.
+inline uint32_t trav_dual_lds_bytes(uint32_t Lpad, uint32_t hsize) {
+    return Lpad * 8 + 2 * kXSlots * 8 + 128 * 4 + hsize * 4;
+}
 constexpr uint32_t kMaxAttr = 8;      // attributes per point supported
 constexpr uint32_t kMaxE = 4;         // cross edges per (point, cell) supported
 constexpr uint32_t kSelTile = 1024;   // rows per selectivity tile
@@ -63,6 +68,7 @@ struct TravArgs {
     const uint32_t* offset;   // P+1
     const uint32_t* gidx;     // row -> point id
     const uint32_t* lrow;     // row -> cell-local id
+    const uint32_t* prow;     // point id -> row (dual-channel traversal)
     const char* queries;      // Q rows of qbytes (fp32, or fp16 in f16 mode)
     uint32_t qbytes;
     const float* lo;          // Q*a
@@ -337,6 +343,10 @@ struct StatsArgs {
 // The search launches take a grid of `grid` workgroups (an upper bound of
 // their query range, which is read on the device).
 hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds_bytes, uint32_t grid, hipStream_t st);
+// Dual-channel traversal: R <= 32, entry holds L ids, prow set.
+hipError_t launch_traverse_dual(const RowShape& rs, const TravArgs& a, uint32_t lds_bytes, uint32_t grid,
+                                hipStream_t st);
+hipError_t launch_invert_rows(const uint32_t* gidx, uint32_t N, uint32_t* prow, hipStream_t st);
 // The full-graph route (fgraph, fentry, frange, FD of a), same LDS layout.
 hipError_t launch_fullgraph(const RowShape& rs, const TravArgs& a, uint32_t lds_bytes, uint32_t grid, hipStream_t st);
 // The full graph: row r, slot c * FE + e holds edge e of row r into cell c as a

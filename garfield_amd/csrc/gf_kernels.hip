@@ -797,6 +797,319 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
     }
 }
 
+// ------------------------------------------------------ dual-channel search
+__device__ __forceinline__ bool hash_contains(const uint32_t* H, uint32_t hbits, uint32_t key) {
+    const uint32_t mask = (1u << hbits) - 1u;
+    uint32_t h = (key * 2654435761u) >> (32u - hbits);
+    for (uint32_t i = 0; i <= mask; ++i) {
+        const uint32_t v = H[h];
+        if (v == key) return true;
+        if (v == kEmpty) return false;
+        h = (h + 1u) & mask;
+    }
+    return false;
+}
+
+// Index of the first entry of A[0..L) that is unexplored and whose row lies
+// in [rlo, rhi) (L if none).  The sentinel carries the explored bit.
+__device__ __forceinline__ uint32_t first_unexplored_in(const uint64_t* A, uint32_t L, uint32_t rlo,
+                                                        uint32_t rhi) {
+    for (uint32_t base = 0; base < L; base += 64u) {
+        const uint32_t i = base + lane_id();
+        bool un = false;
+        if (i < L) {
+            const uint64_t c = A[i];
+            const uint32_t r = crow(c);
+            un = !cexpl(c) && r >= rlo && r < rhi;
+        }
+        const uint64_t m = ballot(un);
+        if (m) return base + __builtin_ctzll(m);
+    }
+    return L;
+}
+
+// One wavefront per query: the traversal of the reference's
+// select_path_contain_attr_filter_V2_without_output_dual_channel_in_turn_with_prefilter
+// (gpu_graph.cu:6249-6640).  Two channels walk two cells of the query's list
+// over one candidate list: per epoch the channel `turn` expands its first
+// unexplored entry (its R neighbours) and the other channel a partner, the
+// first of that entry's cross edges into the other channel's cell whose
+// local id, read as a point id, is not in the visited set (R - 1 neighbours
+// plus the partner itself); a channel with nothing left takes the next cell
+// of the list through 128 cross-edge slots, or, with none left, joins the
+// other channel.
+//
+// The reference marks entries with two explored bits, one per channel, and
+// gives a channel's own points the other channel's bit.  Here an entry has
+// one explored bit: a channel inserts only rows of its current cell and
+// leaves a cell only when none of its entries there is unexplored, so an
+// unexplored entry belongs to the channel whose current cell holds its row
+// (after a join, to the one channel left).  The visited set holds rows; the
+// partner test looks up the row of the point id (prow).  The 2R expansion
+// slots and the 128 switch slots are sorted before they are merged, so only
+// the set of rows new to the visited set matters, not which slot took one.
+template <int VT, int LPR, int CPL>
+__global__ __launch_bounds__(64) void k_traverse_dual(TravArgs p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint64_t* A = reinterpret_cast<uint64_t*>(smem);   // Lpad
+    uint64_t* W = A + p.Lpad;                           // 128: switch slots, merge scratch
+    uint64_t* X = W + kXSlots;                          // 128: switch evictees
+    uint32_t* S = reinterpret_cast<uint32_t*>(X + kXSlots);  // 128 row list
+    uint32_t* H = S + 128;                              // visited set (rows)
+    const uint32_t lane = lane_id();
+    const uint32_t si = p.srange[0] + blockIdx.x;
+    if (si >= p.srange[1]) return;
+    const uint32_t q = p.sched[si];
+    const uint32_t hsize = 1u << p.hbits;
+    const uint32_t L = p.L, R = p.R, P = p.P, E = p.E, R2 = 2u * p.R;
+
+    QReg<VT, LPR, CPL> qv;
+    load_query<VT, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
+    float lo[kMaxAttr], hi[kMaxAttr];
+#pragma unroll
+    for (uint32_t d = 0; d < kMaxAttr; ++d) {
+        lo[d] = d < p.a ? p.lo[size_t(q) * p.a + d] : 0.0f;
+        hi[d] = d < p.a ? p.hi[size_t(q) * p.a + d] : 0.0f;
+    }
+    for (uint32_t i = lane; i < L; i += 64u) A[i] = kCandSent;
+    hash_clear(H, hsize);   // ends with a wave_sync
+    uint32_t n_expand = 0, n_dist = 0, n_cross = 0;
+    uint64_t rc = kCandSent, bleft = kCandSent;
+
+    const uint32_t* cl = p.cells + size_t(q) * P;
+    const uint32_t cnt = p.counts[q];
+    // the two channels' cells as row ranges [off, end)
+    uint32_t c0 = cl[0], c1 = cnt >= 2 ? cl[1] : cl[0];
+    uint32_t off0 = p.offset[c0], end0 = p.offset[c0 + 1];
+    uint32_t off1 = p.offset[c1], end1 = p.offset[c1 + 1];
+    bool same = c0 == c1;
+
+    // Entries (gpu_graph.cu:6318-6362): entry i < ceil(L / 2) in channel 0's
+    // cell, the rest in channel 1's, reduced modulo the cell size; all L
+    // evaluated, then sorted.
+    {
+        const uint32_t L2 = (L + 1u) / 2u;
+        for (uint32_t base = 0; base < L; base += 64u) {
+            const uint32_t i = base + lane;
+            const bool mine = i < L;
+            uint32_t row = 0;
+            bool pass = false;
+            if (mine) {
+                const bool ch1 = i >= L2;
+                const uint32_t o = ch1 ? off1 : off0, sz = (ch1 ? end1 : end0) - o;
+                row = o + p.entry[i] % sz;
+                hash_insert(H, p.hbits, row);
+                pass = row_pass(p.attrs, p.a, row, lo, hi);
+            }
+            wave_sync();
+            float d;
+            n_dist += eval_lanes<VT, LPR, CPL>(qv, p, S, row, mine, d);
+            const uint64_t b = mine ? make_cand(d, row, pass) : kCandSent;
+            const uint32_t nb = L - base < 64u ? L - base : 64u;
+            merge_into(A, L, b, nb, nullptr);
+        }
+    }
+
+    uint32_t cur = cnt >= 2 ? 2u : 1u, turn = 0;
+    for (uint32_t ep = 0; ep < kMaxIter; ++ep) {
+        if ((ep + 1) % kHashReset == 0) {              // gpu_graph.cu:6364-6378
+            hash_clear(H, hsize);
+            for (uint32_t i = lane; i < L; i += 64u) {
+                const uint64_t c = A[i];
+                if (cvalid(c)) hash_insert(H, p.hbits, crow(c));
+            }
+            if (cvalid(bleft)) hash_insert(H, p.hbits, crow(bleft));
+            wave_sync();
+        }
+        // Selection and partner (gpu_graph.cu:6380-6420).
+        const uint32_t tlo = same ? 0u : (turn ? off1 : off0);
+        const uint32_t thi = same ? 0xFFFFFFFFu : (turn ? end1 : end0);
+        const uint32_t sel = first_unexplored_in(A, L, tlo, thi);
+        uint32_t te_row = kEmpty, pt_row = kEmpty;
+        if (sel < L) {
+            const uint64_t sc = A[sel];
+            wave_sync();
+            if (lane == 0) A[sel] = sc | 2u;
+            wave_sync();
+            te_row = crow(sc);
+            const uint32_t oc = turn ? c0 : c1, ooff = turn ? off0 : off1;
+            const uint32_t ne = E < 2u ? E : 2u;
+            uint32_t v = 0;
+            bool free = false;
+            if (lane < ne) {
+                v = p.cross[size_t(te_row) * p.xrow + size_t(oc) * p.xcell + lane];
+                free = !hash_contains(H, p.hbits, p.prow[v]);
+            }
+            const uint64_t m = ballot(free);
+            if (m) pt_row = ooff + readlane32(v, __builtin_ctzll(m));
+        }
+        if (sel == L) {                                 // gpu_graph.cu:6422-6547
+            if (cur == cnt && same) break;
+            if (cur == cnt) {                           // join the other channel's cell
+                if (turn) { c1 = c0; off1 = off0; end1 = end0; }
+                else { c0 = c1; off0 = off1; end0 = end1; }
+                same = true;
+                continue;
+            }
+            // Move channel `turn` to the next cell: slot h * 64 + j follows
+            // entry j through its cross edge h.
+            const uint32_t nxt = cl[cur];
+            const uint32_t offx = p.offset[nxt];
+            uint64_t w[2];
+#pragma unroll
+            for (uint32_t h = 0; h < 2; ++h) {
+                const uint64_t c = lane < L ? A[lane] : kCandSent;
+                const bool v = lane < L && cvalid(c) && h < E;
+                uint32_t row = 0;
+                if (v) row = offx + p.cross[size_t(crow(c)) * p.xrow + size_t(nxt) * p.xcell + h];
+                const bool isnew = v && hash_insert(H, p.hbits, row);
+                wave_sync();
+                n_cross += __popcll(ballot(isnew));
+                float d;
+                bool pass = false;
+                n_dist += eval_lanes<VT, LPR, CPL>(qv, p, S, row, isnew, d, &lo, &hi, isnew, &pass);
+                w[h] = isnew ? make_cand(d, row, pass) : kCandSent;
+            }
+            wave_sync();
+            W[lane] = w[0];
+            W[64u + lane] = w[1];
+            wave_sync();
+            sort128(W);
+            // merge_top_with_recycle_list of the 128 slots: the k slots that
+            // enter push out A's last k entries (slot rows are new to the
+            // visited set, which holds every row of A, so no slot equals an
+            // entry); those that pass the filter go to the recycle list.
+            uint32_t k = 0;
+#pragma unroll
+            for (uint32_t h = 0; h < 2; ++h) {
+                const uint64_t x = W[h * 64u + lane];
+                bool enter = false;
+                if (cvalid(x)) {
+                    const uint64_t kx = ckey(x);
+                    uint32_t a0 = 0, a1 = L;                 // first entry of A not below x
+                    while (a0 < a1) {
+                        const uint32_t mid = (a0 + a1) >> 1;
+                        if (ckey(A[mid]) < kx) a0 = mid + 1; else a1 = mid;
+                    }
+                    enter = h * 64u + lane + a0 < L;
+                }
+                k += __popcll(ballot(enter));
+            }
+            uint32_t nkeep = 0;
+            for (uint32_t base = 0; base < k; base += 64u) {
+                const uint32_t t = base + lane;
+                const uint64_t e = t < k ? A[L - k + t] : kCandSent;
+                const bool keep = t < k && cvalid(e) && cpass(e);
+                const uint64_t m = ballot(keep);
+                const uint32_t pos = nkeep + lanes_below(m);
+                wave_sync();
+                if (keep && pos < 64u) X[pos] = e;
+                nkeep += __popcll(m);
+            }
+            wave_sync();
+            merge_into(A, L, W[lane], 64u, nullptr);
+            merge_into(A, L, W[64u + lane], 64u, nullptr);
+            if (nkeep) {
+                uint64_t dummy;
+                recycle_update(rc, p.rl, X, nkeep < 64u ? nkeep : 64u, dummy, X);
+            }
+            if (turn) { c1 = nxt; off1 = offx; end1 = p.offset[nxt + 1]; }
+            else { c0 = nxt; off0 = offx; end0 = p.offset[nxt + 1]; }
+            ++cur;
+            continue;
+        }
+        // Expansion (gpu_graph.cu:6549-6616): slot j < R of channel 0, R + j
+        // of channel 1; the partner channel's last slot holds the partner.
+        uint32_t row = 0;
+        bool v = false;
+        if (lane < R2) {
+            const uint32_t ch = lane < R ? 0u : 1u, j = lane - ch * R;
+            const uint32_t erow = ch == turn ? te_row : pt_row;
+            if (erow != kEmpty) {
+                v = true;
+                if (ch != turn && j == R - 1u) row = erow;
+                else row = (ch ? off1 : off0) + p.graph[size_t(erow) * R + j];
+            }
+        }
+        const bool isnew = v && hash_insert(H, p.hbits, row);
+        n_expand += (te_row != kEmpty) + (pt_row != kEmpty);
+        float d;
+        bool pass = false;
+        n_dist += eval_lanes<VT, LPR, CPL>(qv, p, S, row, isnew, d, &lo, &hi, isnew, &pass);
+        const uint64_t b = isnew ? make_cand(d, row, pass) : kCandSent;
+        turn ^= 1u;
+        merge_into(A, L, b, R2, W);
+        recycle_update(rc, p.rl, W, R2, bleft, W);
+    }
+
+    // Post-filter, then merge the recycle list (gpu_graph.cu:6618-6639).
+    {
+        uint32_t wpos = 0;
+        for (uint32_t base = 0; base < L; base += 64u) {
+            const uint32_t i = base + lane;
+            wave_sync();
+            const uint64_t c = i < L ? A[i] : kCandSent;
+            const bool keep = i < L && cvalid(c) && cpass(c);
+            const uint64_t m = ballot(keep);
+            wave_sync();
+            if (keep) A[wpos + lanes_below(m)] = c;
+            wpos += __popcll(m);
+        }
+        wave_sync();
+        for (uint32_t i = wpos + lane; i < L; i += 64u) A[i] = kCandSent;
+        wave_sync();
+    }
+    if (cvalid(readlane64(rc, 0))) merge_into(A, L, rc, p.rl, nullptr);
+
+    // First K distinct ids (copies of one entry point are equal and adjacent).
+    uint32_t n = 0;
+    for (uint32_t base = 0; base < L && n < p.K; base += 64u) {
+        const uint32_t i = base + lane;
+        const uint64_t c = i < L ? A[i] : kCandSent;
+        const uint32_t row = crow(c);
+        bool distinct = cvalid(c);
+        for (uint32_t l2 = 0; l2 < 64u; ++l2) {
+            const uint32_t r2 = readlane32(row, l2);
+            if (l2 < lane && r2 == row) distinct = false;
+        }
+        const uint32_t nout = n < p.K ? n : p.K;
+        for (uint32_t t = 0; t < nout; ++t)
+            if (S[t] == row) distinct = false;
+        const uint64_t m = ballot(distinct);
+        const uint32_t idx = n + lanes_below(m);
+        wave_sync();
+        if (distinct && idx < p.K) {
+            p.out_ids[size_t(q) * p.K + idx] = p.gidx[row];
+            p.out_dist[size_t(q) * p.K + idx] = cdist(c);
+            S[idx] = row;
+        }
+        wave_sync();
+        n += __popcll(m);
+        if (!cvalid(readlane64(c, 63))) break;
+    }
+    for (uint32_t j = n + lane; j < p.K; j += 64u) {
+        p.out_ids[size_t(q) * p.K + j] = GF_NO_RESULT;
+        p.out_dist[size_t(q) * p.K + j] = __int_as_float(0x7F800000);
+    }
+    if (lane == 0) {
+        uint32_t* ctr = p.counters + size_t(q) * GF_NCOUNTERS;
+        ctr[C_EXPAND] = n_expand;
+        ctr[C_DIST] = n_dist;
+        ctr[C_ATTR] = n_dist;
+        ctr[C_CROSS] = n_cross;
+        ctr[C_LROW] = 0;
+        ctr[C_SCAN] = 0;
+        ctr[C_PASS] = 0;
+        ctr[C_ROUTE] = 4;
+    }
+}
+
+// prow[gidx[r]] = r: the row of each point id.
+__global__ void k_invert_rows(const uint32_t* gidx, uint32_t N, uint32_t* prow) {
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r < N) prow[gidx[r]] = r;
+}
+
 // -------------------------------------------------------------- full graph
 // The full-graph post-filter branch (gpu_graph.cu:3644-3787; the reference
 // disables it with `&& false` and sends these queries to a brute force over
@@ -3162,6 +3475,12 @@ hipError_t launch_trav_t(const TravArgs& a, uint32_t lds, uint32_t grid, hipStre
     return hipGetLastError();
 }
 template <int VT, int LPR, int CPL>
+hipError_t launch_dual_t(const TravArgs& a, uint32_t lds, uint32_t grid, hipStream_t st) {
+    if (grid == 0) return hipSuccess;
+    hipLaunchKernelGGL((k_traverse_dual<VT, LPR, CPL>), dim3(grid), dim3(64), lds, st, a);
+    return hipGetLastError();
+}
+template <int VT, int LPR, int CPL>
 hipError_t launch_full_t(const TravArgs& a, uint32_t lds, uint32_t grid, hipStream_t st) {
     if (grid == 0) return hipSuccess;
     hipLaunchKernelGGL((k_fullgraph<VT, LPR, CPL>), dim3(grid), dim3(64), lds, st, a);
@@ -3214,6 +3533,21 @@ hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds, 
     GF_DISPATCH(CALL_T);
 #undef CALL_T
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_traverse_dual(const RowShape& rs, const TravArgs& a, uint32_t lds, uint32_t grid,
+                                hipStream_t st) {
+    if (a.R < 1 || a.R > 32 || a.E < 1 || !a.prow) return hipErrorInvalidValue;
+#define CALL_D(V, L_, C_) launch_dual_t<V, L_, C_>(a, lds, grid, st)
+    GF_DISPATCH(CALL_D);
+#undef CALL_D
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_invert_rows(const uint32_t* gidx, uint32_t N, uint32_t* prow, hipStream_t st) {
+    if (N == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_invert_rows, dim3((N + 255) / 256), dim3(256), 0, st, gidx, N, prow);
+    return hipGetLastError();
 }
 
 hipError_t launch_fullgraph(const RowShape& rs, const TravArgs& a, uint32_t lds, uint32_t grid, hipStream_t st) {

@@ -163,6 +163,8 @@ struct gf_index {
     DevBuf<float> attrs, l_q, r_q, cnorm;
     DevBuf<uint32_t> graph, cross, offset, gidx, lrow, grid, doff, hist;
     DevBuf<uint32_t> entry_ref;   // the reference's entry-point draw (resident index: made when it is built)
+    DevBuf<uint32_t> entry_dual;  // the same draw of L entries for the dual-channel traversal
+    DevBuf<uint32_t> prow;        // point id -> row (dual-channel traversal, made at its first search)
     // Full-graph route (P <= 64): every row's FE edges into each cell (FD =
     // FE * P rows per row) and the FD entry rows of the reference's second draw.
     uint32_t FE = 0, FD = 0;

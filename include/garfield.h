@@ -236,6 +236,21 @@ typedef struct {
 gf_status gf_search(gf_batch* b, const gf_search_opts* opts, uint32_t* ids /*Q*K*/,
                     float* dists /*Q*K or NULL*/, gf_search_stats* stats /*or NULL*/);
 
+/* gf_search with the dual-channel traversal for the traversal-routed
+ * queries (replaces batch_graph_search_gpu, gpu_graph.cu:12223-12300, and
+ * the traversal of its kernel select_path_..._dual_channel_in_turn_with_prefilter,
+ * gpu_graph.cu:6249-6640): two channels walk two cells of a query's list at
+ * once over one candidate list of L entries, the channel in turn expanding
+ * its first unexplored entry and the other a partner reached through a
+ * cross edge; a channel with nothing left moves to the next cell through
+ * 128 cross-edge slots, or joins the other channel.  opts->entry_points
+ * holds L cell-local ids (the first ceil(L/2) for the first cell, the rest
+ * for the second, each reduced modulo its cell's size), or NULL for the
+ * reference's draw of L.  Other routes (brute force, full graph) as
+ * gf_search.  Resident indexes with R <= 32; route counter 4. */
+gf_status gf_search_dual(gf_batch* b, const gf_search_opts* opts, uint32_t* ids /*Q*K*/,
+                         float* dists /*Q*K or NULL*/, gf_search_stats* stats /*or NULL*/);
+
 /* Inspection / injection of the batch's intermediate state, for parity
  * tests and for callers that compute cell lists themselves.
  * cells is Q*P (row q holds counts[q] cell ids), the reference's

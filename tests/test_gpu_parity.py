@@ -143,7 +143,8 @@ def test_centroid_order_reference_ties(small_world):
     assert any(not np.array_equal(out[False][q, :cnt[q]], out[True][q, :cnt[q]]) for q in range(len(cnt)))
 
 
-def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, postfilter=1 << 30, Q=None):
+def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, postfilter=1 << 30, Q=None,
+                    channels=1):
     import garfield_amd as gf
     from oracle import oracle as orc
     dev = _device(ix, vec_dtype=vec_dtype, f2h_factor=f2h_factor)
@@ -155,8 +156,8 @@ def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, post
     if ix["labels"] is not None:
         b.order_cells(4)
     gc, gcnt, glit, _ = b.get_cells()
-    ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], ix["R"])
-    ids, dists, st = b.search(L=L, K=10, rl=10, postfilter=postfilter, entry_points=ent)
+    ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], L if channels == 2 else ix["R"])
+    ids, dists, st = b.search(L=L, K=10, rl=10, postfilter=postfilter, entry_points=ent, channels=channels)
     ctr = b.get_counters()
     vec16 = orc.f2h(ix["vectors"], f2h_factor) if vec_dtype == 1 else None
     if vec_dtype == 3:
@@ -170,7 +171,11 @@ def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, post
         O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"],
                             ix["cross"], vec_f16=vec16)
         oq = orc.f2h(queries, f2h_factor) if vec_dtype == 1 else queries
-    oids, odist, octr = O.search(oq, lo, hi, gc, gcnt, glit, ent, L, K=10, rl=10, postfilter=postfilter)
+    orc.set_channels(channels)
+    try:
+        oids, odist, octr = O.search(oq, lo, hi, gc, gcnt, glit, ent, L, K=10, rl=10, postfilter=postfilter)
+    finally:
+        orc.set_channels(1)
     b.close()
     dev.close()
     dump = os.environ.get("GF_DUMP_DIR")
@@ -347,6 +352,54 @@ def test_i8q_rejected_where_unsupported(world_gauss):
         gf.Index.create_streamed(ix["vectors"], ix["attrs"].astype(np.float32), ix["grid"], l_q, r_q,
                                  ix["global_pid"], ix["cell_graphs"], ix["cross"], vec_dtype=3)
     assert e.value.status == 6
+
+
+@pytest.mark.parametrize("L", [16, 64, 200])
+def test_dual_channel_parity_r16(small_world, L):
+    """The dual-channel traversal (gf_search_dual): ids, distances and
+    counters bit-exact against the oracle's restatement."""
+    cfg, ix = small_world
+    _print_case("dual-r16", L=L)
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, L, channels=2)
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+    assert np.sum(octr[:, 7] == 4) == st.q_traverse > 0
+
+
+@pytest.mark.parametrize("L,prefilter", [(33, 0.0), (100, 0.05)])
+def test_dual_channel_parity_r32(world32, L, prefilter):
+    """R = 32 (64 expansion slots per epoch), odd L, mixed routes."""
+    cfg, ix = world32
+    _print_case("dual-r32", L=L, prefilter=prefilter)
+    _assert_same(*_traversal_case(cfg, ix, L, prefilter=prefilter, channels=2))
+
+
+@pytest.mark.parametrize("vec_dtype", [0, 1, 3])
+def test_dual_channel_row_types(world_gauss, vec_dtype):
+    """fp32, fp16 and int8-quantised rows of non-integer data, 64 cells of 3
+    attributes; and the full graph beside it for queries with postfilter."""
+    cfg, ix = world_gauss
+    _print_case("dual-rows", vec_dtype=vec_dtype)
+    f = 0.5 if vec_dtype == 1 else 1.0
+    _assert_same(*_traversal_case(cfg, ix, 64, vec_dtype=vec_dtype, f2h_factor=f, channels=2))
+    # most of these queries select one cell: postfilter 2 sends the others
+    # to the full graph
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 48, vec_dtype=vec_dtype, f2h_factor=f,
+                                                             postfilter=2, channels=2)
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+    assert st.q_fullgraph > 0 and np.sum(octr[:, 7] == 4) > 0
+
+
+def test_dual_channel_recall(world32):
+    """Recall@10 of the dual-channel route against exact ground truth at
+    L = 200, and every returned distance exact."""
+    from oracle import oracle as orc
+    cfg, ix = world32
+    _print_case("dual-recall")
+    ids, dists, *_ = _traversal_case(cfg, ix, 200, channels=2)
+    lo = cfg["lo"].astype(np.float32)
+    hi = cfg["hi"].astype(np.float32)
+    gt, gtd = orc.ground_truth(ix["vectors"], ix["attrs"], cfg["queries"], lo, hi, 10)
+    assert orc.recall(ids, gt, gtd) > 0.8
 
 
 def test_mfma_bruteforce_all_queries(world32):
