@@ -68,6 +68,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traverse", action="store_true", help="skip the traversal roofline line")
     ap.add_argument("--traverse-L", type=int, default=100)
+    ap.add_argument("--channels", default="1,2",
+                    help="traversals swept: 1 cell-by-cell (gf_search), 2 dual-channel (gf_search_dual)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="after the run, stream this many MiB through y = x + 1 (fp32) three times: a kernel "
                          "of known traffic (reads and writes that many bytes) to scale rocprofv3's "
@@ -118,30 +120,30 @@ def main():
     # page-locked result arrays: the search copies into them directly
     out = (gf.pinned_empty((Q, 10), np.uint32), gf.pinned_empty((Q, 10), np.float32))
 
-    def step(prefilter, L):
+    def step(prefilter, L, ch=1):
         # Stages A and B are enqueued without waiting; the search reports
         # their device times after its one synchronisation.  The result
         # arrays are reused from step to step, page-locked, so the search's
         # device-to-host copies land in them directly.
         b.mark_cells(prefilter, timed=False)
         b.order_cells(4, timed=False)
-        ids, dists, st = b.search(L=L, K=10, rl=10, postfilter=args.postfilter, out=out)
+        ids, dists, st = b.search(L=L, K=10, rl=10, postfilter=args.postfilter, out=out, channels=ch)
         return ids, dists, st, st.ms_stage_a, st.ms_stage_b
 
     def recall(ids):
         ex = synth.exact_result_dist(cfg["vectors"], cfg["queries"], ids)
         return synth.recall_at_k(ids, ex, gt_ids, gt_dist)
 
-    def timed(prefilter, L, steps, warmup):
+    def timed(prefilter, L, steps, warmup, ch=1):
         """steps timed passes after warmup; sums of the device times and the
         algorithmic work the search statistics report."""
         for _ in range(warmup):
-            step(prefilter, L)
+            step(prefilter, L, ch)
         torch.cuda.synchronize()
         acc = dict(a=0.0, b=0.0, tr=0.0, bf=0.0, bfk=0.0, btr=0.0, bbf=0.0, obf=0.0)
         t = time.perf_counter()
         for _ in range(steps):
-            ids, dists, st, ms_a, ms_b = step(prefilter, L)
+            ids, dists, st, ms_a, ms_b = step(prefilter, L, ch)
             acc["a"] += ms_a
             acc["b"] += ms_b
             acc["tr"] += st.ms_traverse
@@ -159,20 +161,26 @@ def main():
     # prefilter, the smallest L of the reference's sweep reaching the target,
     # read off a full sweep (no early stop), which is reported as the
     # traversal curve.
+    # Traversal curves are keyed by prefilter, with "dual:" before the
+    # prefilter for the dual-channel traversal.
+    channels = [int(x) for x in args.channels.split(",")]
     candidates = []
     curves = {}
-    for pf in [float(x) for x in args.prefilters.split(",")]:
+    for pf, ch in [(float(x), c) for x in args.prefilters.split(",") for c in channels]:
         if pf >= 1.0:
+            if ch != channels[0]:
+                continue
             ids, dists, st, _, _ = step(pf, 10)
             strict, tie = recall(ids)
             log(f"prefilter={pf}: recall={tie:.4f} (strict {strict:.4f}) q_bf={st.q_bruteforce}")
             if tie >= args.recall:
-                candidates.append(dict(prefilter=pf, L=10, recall=tie, strict=strict, route="bruteforce"))
+                candidates.append(dict(prefilter=pf, L=10, recall=tie, strict=strict, route="bruteforce",
+                                       channels=1))
             continue
         curve = []
         for L in ([args.L] if args.L else L_SWEEP):
             t = time.perf_counter()
-            ids, dists, st, ms_a, ms_b = step(pf, L)
+            ids, dists, st, ms_a, ms_b = step(pf, L, ch)
             wall = time.perf_counter() - t
             strict, tie = recall(ids)
             gbs = st.bytes_traverse / max(st.ms_traverse, 1e-9) / 1e6
@@ -181,26 +189,27 @@ def main():
                           "ms_bruteforce": round(st.ms_bruteforce, 3), "traverse_GBs": round(gbs, 1),
                           "traverse_frac": round(gbs / HBM_PEAK_GBS, 4), "q_traverse": st.q_traverse,
                           "q_bruteforce": st.q_bruteforce})
-            log(f"prefilter={pf} L={L}: recall={tie:.4f} (strict {strict:.4f}) step={wall * 1e3:.1f}ms "
+            log(f"{'dual ' if ch == 2 else ''}prefilter={pf} L={L}: recall={tie:.4f} (strict {strict:.4f}) step={wall * 1e3:.1f}ms "
                 f"trav={st.ms_traverse:.1f}ms ({gbs:.0f} GB/s) bf={st.ms_bruteforce:.1f}ms A={ms_a:.2f}ms "
                 f"B={ms_b:.2f}ms q_trav={st.q_traverse} q_bf={st.q_bruteforce}")
-        curves[str(pf)] = curve
+        curves[("dual:" if ch == 2 else "") + str(pf)] = curve
         reach = [c for c in curve if c["recall"] >= args.recall]
         if reach:
             c = reach[0]
             candidates.append(dict(prefilter=pf, L=c["L"], recall=c["recall"], strict=c["recall_strict"],
-                                   route="traversal"))
+                                   route="traversal", channels=ch))
     if not candidates:
         raise SystemExit("no operating point reached the recall target")
     for c in candidates:
-        _, _, acc = timed(c["prefilter"], c["L"], max(3, args.steps // 4), 1)
+        _, _, acc = timed(c["prefilter"], c["L"], max(3, args.steps // 4), 1, c["channels"])
         c["qps"] = Q * max(3, args.steps // 4) / acc["elapsed"]
-        log(f"candidate {c['route']} prefilter={c['prefilter']} L={c['L']}: {c['qps']:.0f} QPS")
+        log(f"candidate {c['route']} channels={c['channels']} prefilter={c['prefilter']} L={c['L']}: "
+            f"{c['qps']:.0f} QPS")
     best = max(candidates, key=lambda c: c["qps"])
-    pf, L = best["prefilter"], best["L"]
-    log(f"operating point: {best['route']} prefilter={pf} L={L} recall={best['recall']:.4f}")
+    pf, L, bch = best["prefilter"], best["L"], best["channels"]
+    log(f"operating point: {best['route']} channels={bch} prefilter={pf} L={L} recall={best['recall']:.4f}")
 
-    ids, last, acc = timed(pf, L, args.steps, args.warmup)
+    ids, last, acc = timed(pf, L, args.steps, args.warmup, bch)
     elapsed = acc["elapsed"]
     K = args.steps
     strict, tie = recall(ids)
@@ -211,7 +220,7 @@ def main():
     # Dominant kernel: the one with the larger device time in the timed steps.
     traffic = profiled_traffic()
     if ms_tr >= ms_bf:
-        dom, dom_bytes, dom_ms, mfma = "k_traverse", acc["btr"], ms_tr, False
+        dom, dom_bytes, dom_ms, mfma = ("k_traverse_dual" if bch == 2 else "k_traverse"), acc["btr"], ms_tr, False
     else:
         mfma = bool(last.bf_mfma)
         # the MFMA kernel alone (its schedule and the final merge are timed in ms_bruteforce)
@@ -257,29 +266,31 @@ def main():
         tc = [c for c in candidates if c["route"] == "traversal"]
         if tc:
             tp = max(tc, key=lambda c: c["qps"])
-            tpf, tL, trec = tp["prefilter"], tp["L"], tp["recall"]
+            tpf, tL, trec, tch = tp["prefilter"], tp["L"], tp["recall"], tp["channels"]
         else:
-            tpf, tL, trec = 0.0, args.traverse_L, None
+            tpf, tL, trec, tch = 0.0, args.traverse_L, None, 1
         tsteps = max(3, args.steps // 4)
-        tids, stt, tacc = timed(tpf, tL, tsteps, 1)
+        tids, stt, tacc = timed(tpf, tL, tsteps, 1, tch)
         ms_t = tacc["tr"] / tsteps
         gbs = tacc["btr"] / tsteps / (ms_t / 1e3) / 1e9 if ms_t > 0 else 0.0
-        tr = traffic.get(f"k_traverse@{tpf}:{tL}")
-        trav = {"bound": "hbm", "kernel": "k_traverse", "prefilter": tpf, "L": tL,
+        tkern = "k_traverse_dual" if tch == 2 else "k_traverse"
+        tr = traffic.get(f"{tkern}@{tpf}:{tL}")
+        trav = {"bound": "hbm", "kernel": tkern, "channels": tch, "prefilter": tpf, "L": tL,
                 "recall_at_10": round(recall(tids)[1], 4), "reaches_target": trec is not None,
                 "qps": round(Q * tsteps / tacc["elapsed"], 1), "queries_traversed": stt.q_traverse,
                 "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": round(tacc["btr"] / tsteps),
                 "ms_per_launch": round(ms_t, 4), "traffic": tr["bytes"] if tr else None,
                 "traffic_source": tr["source"] if tr else None}
-        log(f"traversal route: prefilter={tpf} L={tL}: {trav['qps']:.0f} QPS, recall {trav['recall_at_10']}, "
-            f"k_traverse {ms_t:.2f} ms, {gbs:.0f} GB/s algorithmic ({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+        log(f"traversal route: channels={tch} prefilter={tpf} L={tL}: {trav['qps']:.0f} QPS, recall "
+            f"{trav['recall_at_10']}, {tkern} {ms_t:.2f} ms, {gbs:.0f} GB/s algorithmic "
+            f"({gbs / HBM_PEAK_GBS:.1%} of HBM)")
 
     cpu = cpu_trav = None
     if not args.no_cpu:
-        cpu = cpu_baseline(cfg, ix, b, L, pf, args)
+        cpu = cpu_baseline(cfg, ix, b, L, pf, args, bch)
         if trav is not None and best["route"] != "traversal":
-            cpu_trav = cpu_baseline(cfg, ix, b, trav["L"], trav["prefilter"], args)
+            cpu_trav = cpu_baseline(cfg, ix, b, trav["L"], trav["prefilter"], args, trav["channels"])
 
     out = {
         "metric": METRIC,
@@ -297,8 +308,9 @@ def main():
         "config": {
             "workload": workload,
             "route": ("filtered brute force (int8 MFMA query-batch kernel)" if best["route"] == "bruteforce"
-                      else "cell-by-cell graph traversal (queries at or below the prefilter selectivity "
-                           "to filtered brute force)"),
+                      else ("dual-channel" if bch == 2 else "cell-by-cell") +
+                      " graph traversal (queries at or below the prefilter selectivity to filtered brute force)"),
+            "channels": bch,
             "N": N, "D": D, "Q": Q, "K": 10, "L": L,
             "prefilter": pf, "postfilter": args.postfilter, "f2h_factor": 1.0, "degree": cfg["R"],
             "graph": args.graph,
@@ -620,16 +632,17 @@ def stream_bench(args):
     print(json.dumps(out), flush=True)
 
 
-def cpu_baseline(cfg, ix, batch, L, prefilter, args):
+def cpu_baseline(cfg, ix, batch, L, prefilter, args, channels=1):
     """The oracle's traversal / brute force (OpenMP over queries) on a sample of
-    the same batch, same routing, same L, on the host's cores."""
+    the same batch, same routing, same L, same traversal, on the host's cores."""
     from oracle import oracle as orc
     import garfield_amd as gf
     batch.mark_cells(prefilter)          # the operating point's cells and routing
     batch.order_cells(4)
     cells, counts, little, _ = batch.get_cells()
     O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"], ix["cross"])
-    ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], ix["R"])
+    ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], L if channels == 2 else ix["R"])
+    orc.set_channels(channels)
     # The GPU box allots 16 host cores to its one GPU (OMP_NUM_THREADS is
     # set to that share there); os.cpu_count() sees the whole host.
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
@@ -648,10 +661,13 @@ def cpu_baseline(cfg, ix, batch, L, prefilter, args):
         if dt >= args.cpu_seconds or n >= Q:
             break
         n = min(Q, max(n * 2, int(n * args.cpu_seconds / max(dt, 1e-3) * 1.1)))
+    orc.set_channels(1)
     routed = int(np.sum((little[sel] == counts[sel]) & (counts[sel] > 0)))
-    log(f"cpu baseline (prefilter {prefilter}, L {L}): {n} queries in {dt:.1f}s on {threads} threads")
+    log(f"cpu baseline (prefilter {prefilter}, L {L}, channels {channels}): {n} queries in {dt:.1f}s on "
+        f"{threads} threads")
     return {"value": round(n / dt, 1), "unit": "queries/s", "cores": threads, "kind": "port",
-            "route": "filtered brute force" if prefilter >= 1.0 else "traversal (+ brute force below the prefilter)",
+            "route": "filtered brute force" if prefilter >= 1.0 else
+                     ("dual-channel " if channels == 2 else "") + "traversal (+ brute force below the prefilter)",
             "host_cpu": host_cpu_model(), "host_nproc": os.cpu_count(),
             "sample": f"{n} random queries of the same batch ({routed} on the brute force; same cells, routing, "
                       f"L={L}, prefilter={prefilter}), search stage only (stages A/B not timed), OpenMP over "

@@ -504,6 +504,37 @@ __device__ __forceinline__ uint32_t local_key(const TravArgs& p, const CellOffs&
     return row - co.O[lo];
 }
 
+// Insert the rows of the valid entries of A[0..L), four per lane at a time,
+// their first probes issued before any is awaited.
+__device__ void hash_add_rows(uint32_t* H, uint32_t hbits, const uint64_t* A, uint32_t L) {
+    constexpr uint32_t U = 4;
+    const uint32_t mask = (1u << hbits) - 1u;
+    for (uint32_t base = 0; base < L; base += 64u * U) {
+        uint32_t key[U], h[U], old[U];
+        bool todo[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t i = base + u * 64u + lane_id();
+            const uint64_t c = i < L ? A[i] : kCandSent;
+            todo[u] = cvalid(c);
+            key[u] = crow(c);
+            h[u] = (key[u] * 2654435761u) >> (32u - hbits);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) old[u] = todo[u] ? atomicCAS(&H[h[u]], kEmpty, key[u]) : kEmpty;
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            if (!todo[u] || old[u] == kEmpty || old[u] == key[u]) continue;
+            for (uint32_t j = 0; j < mask; ++j) {
+                h[u] = (h[u] + 1u) & mask;
+                const uint32_t o2 = atomicCAS(&H[h[u]], kEmpty, key[u]);
+                if (o2 == kEmpty || o2 == key[u]) break;
+            }
+        }
+    }
+    wave_sync();
+}
+
 // Insert the keys of A[0..L), four per lane at a time: their keys are
 // computed, then their first probes issued, before any probe's result is
 // awaited (a set: the insertion order does not change membership).
@@ -810,11 +841,11 @@ __device__ __forceinline__ bool hash_contains(const uint32_t* H, uint32_t hbits,
     return false;
 }
 
-// Index of the first entry of A[0..L) that is unexplored and whose row lies
-// in [rlo, rhi) (L if none).  The sentinel carries the explored bit.
-__device__ __forceinline__ uint32_t first_unexplored_in(const uint64_t* A, uint32_t L, uint32_t rlo,
-                                                        uint32_t rhi) {
-    for (uint32_t base = 0; base < L; base += 64u) {
+// Index of the first entry of A[start..L) that is unexplored and whose row
+// lies in [rlo, rhi) (L if none).  The sentinel carries the explored bit.
+__device__ __forceinline__ uint32_t first_unexplored_in(const uint64_t* A, uint32_t L, uint32_t start,
+                                                        uint32_t rlo, uint32_t rhi) {
+    for (uint32_t base = start; base < L; base += 64u) {
         const uint32_t i = base + lane_id();
         bool un = false;
         if (i < L) {
@@ -910,27 +941,29 @@ __global__ __launch_bounds__(64) void k_traverse_dual(TravArgs p) {
         }
     }
 
-    uint32_t cur = cnt >= 2 ? 2u : 1u, turn = 0;
+    // scan0 / scan1: no entry of channel 0 / 1 before it is unexplored (an
+    // insertion at position i moves entries at i and after to the right)
+    uint32_t cur = cnt >= 2 ? 2u : 1u, turn = 0, scan0 = 0, scan1 = 0;
     for (uint32_t ep = 0; ep < kMaxIter; ++ep) {
         if ((ep + 1) % kHashReset == 0) {              // gpu_graph.cu:6364-6378
             hash_clear(H, hsize);
-            for (uint32_t i = lane; i < L; i += 64u) {
-                const uint64_t c = A[i];
-                if (cvalid(c)) hash_insert(H, p.hbits, crow(c));
-            }
+            hash_add_rows(H, p.hbits, A, L);
             if (cvalid(bleft)) hash_insert(H, p.hbits, crow(bleft));
             wave_sync();
         }
         // Selection and partner (gpu_graph.cu:6380-6420).
         const uint32_t tlo = same ? 0u : (turn ? off1 : off0);
         const uint32_t thi = same ? 0xFFFFFFFFu : (turn ? end1 : end0);
-        const uint32_t sel = first_unexplored_in(A, L, tlo, thi);
+        const uint32_t sel = first_unexplored_in(A, L, turn ? scan1 : scan0, tlo, thi);
         uint32_t te_row = kEmpty, pt_row = kEmpty;
         if (sel < L) {
             const uint64_t sc = A[sel];
             wave_sync();
             if (lane == 0) A[sel] = sc | 2u;
             wave_sync();
+            if (same) scan0 = scan1 = sel + 1;
+            else if (turn) scan1 = sel + 1;
+            else scan0 = sel + 1;
             te_row = crow(sc);
             const uint32_t oc = turn ? c0 : c1, ooff = turn ? off0 : off1;
             const uint32_t ne = E < 2u ? E : 2u;
@@ -949,6 +982,7 @@ __global__ __launch_bounds__(64) void k_traverse_dual(TravArgs p) {
                 if (turn) { c1 = c0; off1 = off0; end1 = end0; }
                 else { c0 = c1; off0 = off1; end0 = end1; }
                 same = true;
+                scan0 = scan1 = scan0 < scan1 ? scan0 : scan1;
                 continue;
             }
             // Move channel `turn` to the next cell: slot h * 64 + j follows
@@ -1007,8 +1041,11 @@ __global__ __launch_bounds__(64) void k_traverse_dual(TravArgs p) {
                 nkeep += __popcll(m);
             }
             wave_sync();
-            merge_into(A, L, W[lane], 64u, nullptr);
-            merge_into(A, L, W[64u + lane], 64u, nullptr);
+            const uint32_t ip0 = merge_into(A, L, W[lane], 64u, nullptr);
+            const uint32_t ip1 = merge_into(A, L, W[64u + lane], 64u, nullptr);
+            const uint32_t ip = ip0 < ip1 ? ip0 : ip1;
+            scan0 = ip < scan0 ? ip : scan0;
+            scan1 = ip < scan1 ? ip : scan1;
             if (nkeep) {
                 uint64_t dummy;
                 recycle_update(rc, p.rl, X, nkeep < 64u ? nkeep : 64u, dummy, X);
@@ -1038,8 +1075,10 @@ __global__ __launch_bounds__(64) void k_traverse_dual(TravArgs p) {
         n_dist += eval_lanes<VT, LPR, CPL>(qv, p, S, row, isnew, d, &lo, &hi, isnew, &pass);
         const uint64_t b = isnew ? make_cand(d, row, pass) : kCandSent;
         turn ^= 1u;
-        merge_into(A, L, b, R2, W);
+        const uint32_t ip = merge_into(A, L, b, R2, W);
         recycle_update(rc, p.rl, W, R2, bleft, W);
+        scan0 = ip < scan0 ? ip : scan0;
+        scan1 = ip < scan1 ? ip : scan1;
     }
 
     // Post-filter, then merge the recycle list (gpu_graph.cu:6618-6639).
@@ -2572,7 +2611,8 @@ __global__ __launch_bounds__(256) void k_stats(StatsArgs p) {
 #pragma unroll
         for (int k = 0; k < 7; ++k)
             if (c[map[k]]) atomicAdd(&acc[k], (unsigned long long)c[map[k]]);
-        if (c[C_ROUTE] == 1 || c[C_ROUTE] == 3) atomicAdd(&acc[7], (unsigned long long)c[C_DIST]);
+        if (c[C_ROUTE] == 1 || c[C_ROUTE] == 3 || c[C_ROUTE] == 4)
+            atomicAdd(&acc[7], (unsigned long long)c[C_DIST]);
         if (c[C_ROUTE] == 2) atomicAdd(&acc[8], (unsigned long long)c[C_DIST]);
     }
     if (p.bcnt && i < p.NS) {
