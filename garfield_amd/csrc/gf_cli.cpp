@@ -58,7 +58,7 @@ void usage() {
         "usage: garfield_search --data_path F --query_path F --range F --cagra_prefix P --cagra_suffix S\n"
         "                       --global_graph F --grid F --attrs F [--cluster F] [--gt F] [--result F]\n"
         "                       [--prefilter x] [--postfilter n] [--f2h_factor x] [--degree n]\n"
-        "                       [--L l1,l2,...] [--vec_dtype f16|f32|i8q] [--device n]\n");
+        "                       [--L l1,l2,...] [--vec_dtype f16|f32|i8q] [--channels 1|2] [--device n]\n");
 }
 
 }  // namespace
@@ -68,7 +68,7 @@ int main(int argc, char** argv) {
         cluster, result;
     float prefilter = 0.0f, f2h_factor = 1.0f;
     uint32_t postfilter = 0xFFFFFFFFu, degree = 0;
-    int32_t vec_dtype = GF_VEC_F16, device = 0;
+    int32_t vec_dtype = GF_VEC_F16, device = 0, channels = 1;
     // the reference's sweep (realdataset_search.cu:2757), ascending
     std::vector<uint32_t> Ls = {10,  15,  20,  25,  30,  35,  40,  45,  50,  55,  60,  70,   80,   90,   100,  120,
                                 140, 160, 180, 200, 250, 300, 400, 500, 600, 700, 800, 900, 1000, 1100, 1400, 1700};
@@ -93,6 +93,10 @@ int main(int argc, char** argv) {
         else if (a == "--f2h_factor") f2h_factor = std::stof(v);
         else if (a == "--degree") degree = uint32_t(std::stoul(v));
         else if (a == "--device") device = std::stoi(v);
+        else if (a == "--channels") {
+            channels = std::stoi(v);
+            if (channels != 1 && channels != 2) die("--channels must be 1 or 2");
+        }
         else if (a == "--vec_dtype") {
             if (v == "f16") vec_dtype = GF_VEC_F16;
             else if (v == "f32") vec_dtype = GF_VEC_F32;
@@ -169,7 +173,8 @@ int main(int argc, char** argv) {
     for (uint32_t L : Ls) {
         gf_search_opts so{L, K, 10, postfilter, nullptr};
         gf_search_stats st{};
-        check(gf_search(b, &so, ids.data(), nullptr, &st), "gf_search");
+        if (channels == 2) check(gf_search_dual(b, &so, ids.data(), nullptr, &st), "gf_search_dual");
+        else check(gf_search(b, &so, ids.data(), nullptr, &st), "gf_search");
         double recall = -1.0;
         if (!gt.empty()) {
             double sum = 0;

@@ -519,15 +519,17 @@ def test_index_opened_from_files(small_world, tmp_path):
         assert np.array_equal(x, y)
 
 
-def test_cli_matches_library(small_world, tmp_path):
+@pytest.mark.parametrize("channels", [1, 2])
+def test_cli_matches_library(small_world, tmp_path, channels):
     """garfield_search on the index files: the reference's CSV, and the same
-    recall as the library on the same batch."""
+    recall as the library on the same batch (channels 2: the dual-channel
+    traversal)."""
     import csv
     import subprocess
     from garfield_amd import formats
     from oracle import oracle as orc
     cfg, ix = small_world
-    _print_case("cli")
+    _print_case("cli", channels=channels)
     p = synth.write_index(ix, str(tmp_path / "w"))
     formats.write_fvecs(str(tmp_path / "q.fvecs"), cfg["queries"])
     formats.write_ranges(str(tmp_path / "q.range"), cfg["lo"], cfg["hi"])
@@ -541,7 +543,7 @@ def test_cli_matches_library(small_world, tmp_path):
             "--cagra_suffix", p["cagra_suffix"], "--global_graph", p["global_graph"], "--grid", p["grid"],
             "--attrs", p["attrs"], "--cluster", p["cluster"], "--result", str(tmp_path / "r.csv"),
             "--prefilter", "0.05", "--f2h_factor", "1.0", "--degree", str(ix["R"]), "--L", "32,64",
-            "--vec_dtype", "f32"]
+            "--vec_dtype", "f32", "--channels", str(channels)]
     r = subprocess.run(args, capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
     rows = list(csv.DictReader(open(tmp_path / "r.csv")))
@@ -555,7 +557,7 @@ def test_cli_matches_library(small_world, tmp_path):
     b.mark_cells(0.05)
     b.order_cells(4)
     for x in rows:
-        ids, _, _ = b.search(L=int(x["ef"]), K=10, rl=10)
+        ids, _, _ = b.search(L=int(x["ef"]), K=10, rl=10, channels=channels)
         rec = np.mean([len(set(ids[q]) & set(gt[q][gt[q] != 0x7FFFFFFF])) / max(1, np.sum(gt[q] != 0x7FFFFFFF))
                        if np.any(gt[q] != 0x7FFFFFFF) else 1.0 for q in range(len(gt))])
         assert abs(rec - float(x["recall"])) < 1e-5, (x, rec)
