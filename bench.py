@@ -42,7 +42,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", choices=["headline", "small"], default="headline")
+    ap.add_argument("--config", choices=["headline", "small", "c3", "c4"], default="headline",
+                    help="headline: C2 (the metric's config); c3, c4: the non-integer configs, each with its own "
+                         "metric string (the fp32 and fp16 distance paths)")
     ap.add_argument("--workload", choices=["resident", "stream", "build"], default="resident",
                     help="stream: the C5-shaped out-of-core workload; build: the index builder on the "
                          "headline index (each its own JSON line, not the headline)")
@@ -95,25 +97,43 @@ def main():
         workload = ("C2 headline: 1M x 128 fp32 (integers 0-255), 2 uint32 attrs on a 4x4 grid, "
                     f"R=32 per-cell graphs ({'exact 64-NN optimised to 32 (pruned + reverse edges)' if args.graph == 'cagra' else 'exact 32-NN'})"
                     " + E=2 exact cross edges, C=1000, 10k queries, selectivity log-U[1%,50%], k=10")
+    elif args.config == "c3":
+        cfg = synth.config_c3()
+        workload = ("C3: 1M x 96 fp32 Gaussian unit vectors, 3 Zipf(1.1) attrs on a 4x4x4 grid, R=32 per-cell "
+                    "graphs (exact 48-NN of the builder's float mode optimised to 32) + E=2 cross edges, C=1000, "
+                    "10k queries, selectivity log-U[0.1%,50%], k=10")
+    elif args.config == "c4":
+        cfg = synth.config_c4()
+        workload = ("C4: 1M x 768 Gaussian mixture (1000 components, sigma 0.1) stored as fp16 (f2h_factor 1), "
+                    "2 attrs 10*component+U{0..9} on 4x4, R=32 per-cell graphs (exact 48-NN of the builder's "
+                    "float mode optimised to 32) + E=2 cross edges, C=1000, 10k queries at 10%, k=10")
     else:
         cfg = synth.config_small()
         workload = "C1: 100k x 128 fp32 (integers 0-255), 2 attrs on 4x4, R=16, E=2, C=100, 1k queries at 30%, k=10"
+    metric = {"c3": "QPS at recall@10≥0.95, 1M×96 fp32, 3-attr range filter, 1 MI355X",
+              "c4": "QPS at recall@10≥0.95, 1M×768 fp16, 2-attr range filter, 1 MI355X"}.get(args.config, METRIC)
+    floatcfg = args.config in ("c3", "c4")
+    vec_dtype = gf.VEC_F16 if args.config == "c4" else gf.VEC_F32
     N, D = cfg["vectors"].shape
     Q = cfg["queries"].shape[0]
     log(f"data generated N={N} D={D} Q={Q} ({time.time() - t0:.1f}s)")
     t1 = time.time()
+    # float data: the builder's candidate lists hold at most 63 entries
     ix = synth.build_index(cfg["vectors"], cfg["attrs"], cfg["grid"], cfg["R"], cfg["E"], cfg["C"],
-                           device="hip", graph=args.graph)
+                           device="hip", graph=args.graph, inter=48 if floatcfg else 64)
     log(f"index built on GPU in {time.time() - t1:.1f}s ({args.graph} graphs)")
     lo = cfg["lo"].astype(np.float32)
     hi = cfg["hi"].astype(np.float32)
     t1 = time.time()
     gt_ids, gt_dist = synth.ground_truth_torch(cfg["vectors"], cfg["attrs"], cfg["queries"], lo, hi, 10)
+    # the tie test compares float64 distances: the ground truth's own in
+    # float64 too (exact for integer data either way)
+    gt_dist = synth.exact_result_dist(cfg["vectors"], cfg["queries"], gt_ids)
     log(f"ground truth in {time.time() - t1:.1f}s")
     torch.cuda.empty_cache()
 
     t1 = time.time()
-    dev = synth.open_device_index(ix)
+    dev = synth.open_device_index(ix, vec_dtype=vec_dtype, f2h_factor=1.0)
     b = dev.batch(cfg["queries"], lo, hi)
     log(f"library index resident ({dev.device_bytes / 2**30:.2f} GiB) in {time.time() - t1:.1f}s")
 
@@ -218,7 +238,7 @@ def main():
     ms_a_sum, ms_b_sum, ms_tr, ms_bf, ms_bfk = acc["a"], acc["b"], acc["tr"], acc["bf"], acc["bfk"]
     qps_ref = Q / ((ms_a_sum + ms_b_sum + ms_tr + ms_bf) / K / 1e3)
     # Dominant kernel: the one with the larger device time in the timed steps.
-    traffic = profiled_traffic()
+    traffic = profiled_traffic() if args.config == "headline" else {}
     if ms_tr >= ms_bf:
         dom, dom_bytes, dom_ms, mfma = ("k_traverse_dual" if bch == 2 else "k_traverse"), acc["btr"], ms_tr, False
     else:
@@ -288,12 +308,13 @@ def main():
 
     cpu = cpu_trav = None
     if not args.no_cpu:
-        cpu = cpu_baseline(cfg, ix, b, L, pf, args, bch)
+        f16 = vec_dtype == gf.VEC_F16
+        cpu = cpu_baseline(cfg, ix, b, L, pf, args, bch, f16)
         if trav is not None and best["route"] != "traversal":
-            cpu_trav = cpu_baseline(cfg, ix, b, trav["L"], trav["prefilter"], args, trav["channels"])
+            cpu_trav = cpu_baseline(cfg, ix, b, trav["L"], trav["prefilter"], args, trav["channels"], f16)
 
     out = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(qps, 1),
         "unit": "queries/s",
         "n_gpus": 1,
@@ -303,7 +324,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "i8" if (last.bf_mfma and ms_bf > ms_tr) else "f32",
+        "dtype": "i8" if (last.bf_mfma and ms_bf > ms_tr) else ("f16" if vec_dtype == gf.VEC_F16 else "f32"),
         "data": "synthetic (generated in bench.py; index built on the GPU by the library's builder)",
         "config": {
             "workload": workload,
@@ -632,15 +653,18 @@ def stream_bench(args):
     print(json.dumps(out), flush=True)
 
 
-def cpu_baseline(cfg, ix, batch, L, prefilter, args, channels=1):
+def cpu_baseline(cfg, ix, batch, L, prefilter, args, channels=1, f16=False):
     """The oracle's traversal / brute force (OpenMP over queries) on a sample of
-    the same batch, same routing, same L, same traversal, on the host's cores."""
+    the same batch, same routing, same L, same traversal and row type (f16:
+    binary16 rows and queries), on the host's cores."""
     from oracle import oracle as orc
     import garfield_amd as gf
     batch.mark_cells(prefilter)          # the operating point's cells and routing
     batch.order_cells(4)
     cells, counts, little, _ = batch.get_cells()
-    O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"], ix["cross"])
+    O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"], ix["cross"],
+                        vec_f16=orc.f2h(ix["vectors"], 1.0) if f16 else None)
+    queries = orc.f2h(cfg["queries"], 1.0) if f16 else cfg["queries"]
     ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], L if channels == 2 else ix["R"])
     orc.set_channels(channels)
     # The GPU box allots 16 host cores to its one GPU (OMP_NUM_THREADS is
@@ -655,7 +679,7 @@ def cpu_baseline(cfg, ix, batch, L, prefilter, args, channels=1):
     while True:
         sel = np.sort(order[:n])
         t = time.perf_counter()
-        O.search(cfg["queries"][sel], lo[sel], hi[sel], cells[sel], counts[sel], little[sel], ent, L,
+        O.search(queries[sel], lo[sel], hi[sel], cells[sel], counts[sel], little[sel], ent, L,
                  postfilter=args.postfilter, nthreads=threads)
         dt = time.perf_counter() - t
         if dt >= args.cpu_seconds or n >= Q:

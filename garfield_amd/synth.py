@@ -81,6 +81,24 @@ def ranges_for_selectivity(q, a, sel, seed, hi=DOMAIN):
     return lo.astype(np.int32), hi_.astype(np.int32)
 
 
+def ranges_for_selectivity_ranked(attrs, q, sel, seed):
+    """Closed ranges that each hold a sel**(1/a) fraction of the points'
+    values on every attribute (a random window of the sorted values), for
+    skewed attributes; equal values at a window's ends widen it."""
+    rng = np.random.default_rng(seed)
+    n, a = attrs.shape
+    sel = np.broadcast_to(np.asarray(sel, np.float64), (q,))
+    w = np.clip(np.round(n * sel ** (1.0 / a)), 1, n).astype(np.int64)
+    lo = np.empty((q, a), np.int64)
+    hi = np.empty((q, a), np.int64)
+    for d in range(a):
+        s = np.sort(attrs[:, d])
+        r0 = (rng.random(q) * (n - w + 1)).astype(np.int64)
+        lo[:, d] = s[r0]
+        hi[:, d] = s[r0 + w - 1]
+    return lo.astype(np.int32), hi.astype(np.int32)
+
+
 def log_uniform(q, lo, hi, seed):
     rng = np.random.default_rng(seed)
     return np.exp(rng.uniform(math.log(lo), math.log(hi), size=q))
@@ -321,6 +339,34 @@ def config_headline(N=1_000_000, Q=10_000, R=32, C=1000, seed=11):
     sel = log_uniform(Q, 0.01, 0.5, seed + 3)
     lo, hi = ranges_for_selectivity(Q, 2, sel, seed + 4)
     return dict(vectors=vec, attrs=att, grid=[4, 4], R=R, E=2, C=C, queries=qv, lo=lo, hi=hi, sel=sel)
+
+
+def config_c3(N=1_000_000, Q=10_000, R=32, C=1000, seed=31):
+    """Config C3: N x 96 Gaussian unit vectors, 3 Zipf(1.1) attributes on a
+    4x4x4 rank grid (64 cells), selectivity log-U[0.1%, 50%] (ranges drawn
+    in rank space, as the skewed values need)."""
+    vec = gaussian_unit_vectors(N, 96, seed)
+    att = zipf_attrs(N, 3, seed + 1)
+    qv = gaussian_unit_vectors(Q, 96, seed + 2)
+    sel = log_uniform(Q, 0.001, 0.5, seed + 3)
+    lo, hi = ranges_for_selectivity_ranked(att, Q, sel, seed + 4)
+    return dict(vectors=vec, attrs=att, grid=[4, 4, 4], R=R, E=2, C=C, queries=qv, lo=lo, hi=hi, sel=sel)
+
+
+def config_c4(N=1_000_000, Q=10_000, R=32, C=1000, ncomp=1000, seed=41):
+    """Config C4: N x 768 vectors of a Gaussian mixture (ncomp components,
+    sigma 0.1 around unit centres; the queries from the same mixture), 2
+    attributes 10 * component + U{0..9} on a 4x4 grid, 10% selectivity."""
+    vec, comp = gmm_vectors(N, 768, ncomp, seed)
+    att = component_attrs(comp, 2, seed + 1)
+    rng = np.random.default_rng(seed)
+    cen = rng.standard_normal((ncomp, 768))
+    cen /= np.linalg.norm(cen, axis=1, keepdims=True)     # the same centres as gmm_vectors draws
+    qr = np.random.default_rng(seed + 2)
+    qc = qr.integers(0, ncomp, size=Q)
+    qv = (cen[qc] + 0.1 * qr.standard_normal((Q, 768))).astype(np.float32)
+    lo, hi = ranges_for_selectivity(Q, 2, 0.1, seed + 3, hi=10 * ncomp)
+    return dict(vectors=vec, attrs=att, grid=[4, 4], R=R, E=2, C=C, queries=qv, lo=lo, hi=hi)
 
 
 def config_stream(N=1_000_000, Q=10_000, R=32, seed=21):
