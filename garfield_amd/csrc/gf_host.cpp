@@ -400,6 +400,27 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
                                       ix.stream));
             ix.i8 = true;
         }
+        // Binary16 rows with sub-cells: |x|^2 per row (fp32, as k_norms_f16
+        // sums the binary16 values) and the largest |x| for the fp16 MFMA
+        // brute force's error bound (each binary16 value is within 2^-11 of
+        // x * alpha).
+        if (ix.sub && ix.vdtype == GF_VEC_F16 && gf::bf_f16_supported(D, ix.AW, 1)) {
+            ix.xnorm16.alloc(N);
+            GF_HIP(gf::launch_norms_f16(reinterpret_cast<const uint16_t*>(ix.vec.p), N, D, D, ix.xnorm16.p,
+                                        ix.stream));
+            double xm = 0.0;
+            for (uint32_t r = 0; r < N; ++r) {
+                double s = 0.0;
+                for (uint32_t d = 0; d < D; ++d) {
+                    const double x = double(v[size_t(r) * D + d]) * ix.alpha;
+                    s += x * x;
+                }
+                xm = std::max(xm, s);
+            }
+            // binary16 rounding: within 2^-11 relative, 2^-25 absolute (subnormals)
+            ix.xmax16 = std::sqrt(xm) * (1.0 + 1.0 / 1024.0) + std::sqrt(double(D)) * std::ldexp(1.0, -24);
+            ix.h16 = true;
+        }
         GF_HIP(hipStreamSynchronize(ix.stream));
     }
     // Grid (real_dataset_adapter.cuh:563-619).
@@ -682,6 +703,31 @@ gf_status gf_batch_create(gf_index* ix, const float* queries, uint32_t Q, const 
         if (ix->vdtype == GF_VEC_F16) {
             b->q16v.alloc(size_t(Q) * ix->D);
             GF_HIP(gf::launch_f2h(b->qf32.p, b->q16v.p, size_t(Q) * ix->D, ix->alpha, ix->stream));
+            if (ix->h16) {
+                // |q|^2 of the binary16 query, and the bound eps_q of |d' - d|
+                // for the fp16 MFMA brute force: d' = |q|^2 + |x|^2 - 2 q.x
+                // and the canonical d each hold fp32 sums of D terms, within
+                // gamma_{D+2} (|q| + |x|)^2 of the exact distance between the
+                // binary16 vectors (plus two roundings of the combination);
+                // doubled for margin, with a floor for subnormal products.
+                const uint32_t D = ix->D;
+                b->qn16.alloc(Q);
+                GF_HIP(gf::launch_norms_f16(b->q16v.p, Q, D, D, b->qn16.p, ix->stream));
+                const double u = std::ldexp(1.0, -24), gam = (D + 2) * u / (1.0 - (D + 2) * u);
+                std::vector<float> eps(Q);
+                for (uint32_t q = 0; q < Q; ++q) {
+                    double s = 0.0;
+                    for (uint32_t d = 0; d < D; ++d) {
+                        const double x = double(queries[size_t(q) * D + d]) * ix->alpha;
+                        s += x * x;
+                    }
+                    const double nq = std::sqrt(s) * (1.0 + 1.0 / 1024.0) + std::sqrt(double(D)) * std::ldexp(1.0, -24);
+                    const double e = 2.0 * (3.0 * gam + 2.0 * u) * (nq + ix->xmax16) * (nq + ix->xmax16) +
+                                     D * std::ldexp(1.0, -40);
+                    eps[q] = float(e * (1.0 + 1e-6));
+                }
+                b->heps.upload(eps);
+            }
         }
         if (ix->vdtype == GF_VEC_I8Q) {
             // rows [c | s]: c_d = fma(s_d, z_d, alpha q_d), the query less
@@ -955,9 +1001,14 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     // work items of (sub-cell, <= 64 queries whose range reaches it),
     // scheduled on the device.
     const bool gemm = ix->i8 && b->i8 && K <= gf::kBfKMax;
+    // Binary16 rows: the same items on fp16 MFMA, candidates within the
+    // distances' error bound re-ranked exactly (k_bf_f16, k_bf_f16_final).
+    const bool gemm_h = !gemm && ix->h16 && b->qn16.n == Q && gf::bf_f16_supported(ix->D, ix->AW, K);
+    const bool sched_bf = gemm || gemm_h;
+    const uint32_t KP = gemm_h ? gf::kBfHKT : K;   // keys per (query, item) in the partial area
     const uint32_t NS = ix->NS;
-    b->pass_pending = gemm && !b->sel_exact;
-    if (gemm) {
+    b->pass_pending = sched_bf && !b->sel_exact;
+    if (sched_bf) {
         if (!b->bcnt.n) {
             b->bcnt.alloc(NS); b->bin.alloc(NS); b->bstart.alloc(NS); b->icnt.alloc(NS); b->ioff.alloc(NS);
             b->nsub.alloc(Q); b->part_off.alloc(Q); b->pcnt.alloc(Q);
@@ -965,7 +1016,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         // item slots: a sub-cell adds up to two partial query blocks per
         // tile chunk beyond pairs / 64
         const size_t islots = size_t(NS) + ix->ntile / gf::kBfMaxItemTiles + 1;
-        if (!b->part.n) b->alloc_pairs(size_t(Q) * 64, K, Q, NS, islots);
+        if (!b->part.n) b->alloc_pairs(size_t(Q) * 64, KP, Q, NS, islots);
         if (b->rq.n < Q) {
             b->rq.alloc(Q); b->rseed.alloc(Q);
             b->rlo.alloc(size_t(Q) * ix->a); b->rhi.alloc(size_t(Q) * ix->a);
@@ -979,8 +1030,9 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
             const size_t chunks = (tmax + gf::kBfSeedTiles - 1) / gf::kBfSeedTiles;
             b->sitems.alloc((size_t(Q) / gf::kBfQB + NS + 1) * std::max<size_t>(chunks, 1));
         }
-        if (b->part.n < b->pair_cap * K) b->part.alloc(b->pair_cap * K);
+        if (b->part.n < b->pair_cap * KP) b->part.alloc(b->pair_cap * KP);
         if (b->gbound.n < Q) b->gbound.alloc(Q);
+        if (gemm_h && b->hover.n < Q) b->hover.alloc(Q);
         if (!b->bf_all && b->bfmask.n < size_t(Q) * ix->P) b->bfmask.alloc(size_t(Q) * ix->P);
     }
     // events: [0] search start, [1] after traversal, [2] end, [3..4] around the MFMA kernel alone
@@ -1023,7 +1075,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         else GF_HIP(gf::launch_bfsched(sc, false, st));
         if (!b->qcap) GF_HIP(gf::launch_scan_small(b->bcnt.p, NS, b->bstart.p, st));
         GF_HIP(gf::launch_scan_small(b->nsub.p, Q, b->part_off.p, st));
-        GF_HIP(gf::launch_total(b->nsub.p, b->part_off.p, Q, uint32_t(std::min<size_t>(b->pair_cap, UINT32_MAX)), K,
+        GF_HIP(gf::launch_total(b->nsub.p, b->part_off.p, Q, uint32_t(std::min<size_t>(b->pair_cap, UINT32_MAX)), KP,
                                 b->part.n, tot + 2, st));
         if (!b->qcap) GF_HIP(gf::launch_bfsched(sc, true, st));
         // Two passes (resident index): the seeds and the items of the
@@ -1041,6 +1093,26 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
                                   b->items.p, tot + 4, tot + 3, true, st, seeds ? b->scnt.p : nullptr,
                                   b->sitems.p, tot + 5, scap, two ? ix->sorder.p : nullptr, two ? ix->ns1 : 0u,
                                   two ? tot + 6 : nullptr, gf::kBfSeedTiles));
+        if (gemm_h) {
+            GF_HIP(gf::launch_zero_u32(b->hover.p, Q, st));
+            gf::BfHArgs ha{};
+            ha.sa = sub_args(*ix);
+            ha.vec = reinterpret_cast<const uint16_t*>(ix->vec.p); ha.xnorm = ix->xnorm16.p;
+            ha.q16 = b->q16v.p; ha.qnorm = b->qn16.p; ha.eps = b->heps.p; ha.lo = b->lo.p; ha.hi = b->hi.p;
+            ha.items = b->items.p; ha.nitems = tot + 4; ha.bq = b->bq.p; ha.part_off = b->part_off.p;
+            ha.pcnt = b->pcnt.p; ha.part = b->part.p; ha.gbound = b->gbound.p; ha.over = b->hover.p;
+            ha.ok = tot + 3;
+            if (seeds) { ha.sitems = b->sitems.p; ha.nseed = tot + 5; ha.nseed_cap = scap; }
+            ha.K = K; ha.D = ix->D;
+            GF_HIP(gf::launch_stamp(stamp + 3, st));
+            GF_HIP(gf::launch_bf_f16(ha, ix->AW, uint32_t(ix->ncu), st));
+            GF_HIP(gf::launch_stamp(stamp + 4, st));
+            gf::TravArgs ab = a;
+            ab.srange = tot + 14;
+            const gf::BfHFinal hf{tot + 3, b->hover.p, b->pcnt.p, b->part_off.p, b->part.p, b->heps.p, b->selcount.p};
+            GF_HIP(gf::launch_bf_f16_final(ix->rs, ab, hf, Q, st));
+            return;
+        }
         gf::BfGemmArgs ga{};
         ga.sa = sub_args(*ix);
         ga.vt = ix->vt.p; ga.tnorm = ix->tnorm.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p;
@@ -1104,7 +1176,8 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         if (stats) {
             GF_HIP(gf::launch_zero_u32(reinterpret_cast<uint32_t*>(b->stats.p), 32, st));
             gf::StatsArgs sa2{};
-            sa2.Q = Q; sa2.NS = gemm ? NS : 0; sa2.counters = b->counters.p; sa2.bcnt = gemm ? b->bcnt.p : nullptr;
+            sa2.Q = Q; sa2.NS = sched_bf ? NS : 0; sa2.counters = b->counters.p;
+            sa2.bcnt = sched_bf ? b->bcnt.p : nullptr;
             sa2.bin = b->bin.p; sa2.split = b->qcap != 0; sa2.sseed = b->qcap ? b->scnt.p : nullptr;
             sa2.ssize = ix->ssize.p; sa2.stile = ix->stile.p; sa2.out = b->stats.p;
             GF_HIP(gf::launch_stats(sa2, st));
@@ -1138,7 +1211,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         // queries with postfilter or more cells: the full graph
         if (ix->FD && opts->postfilter <= ix->P) GF_HIP(gf::launch_fullgraph(ix->rs, af, lds_f, Q, st));
         GF_HIP(gf::launch_stamp(stamp + 1, st));
-        if (gemm) {
+        if (sched_bf) {
             launch_gemm();
         } else {
             gf::TravArgs ab = a;
@@ -1151,7 +1224,8 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     // From a batch's second search on, the stage runs as a HIP graph,
     // captured once per layout (buffers, options, route) and replayed:
     // one launch instead of some twenty, no gaps between the kernels.
-    const uint64_t key[] = {uint64_t(L), K, rl, opts->postfilter, uint64_t(gemm), uint64_t(b->bf_all), channels,
+    const uint64_t key[] = {uint64_t(L), K, rl, opts->postfilter, uint64_t(gemm) | uint64_t(gemm_h) << 1,
+                            uint64_t(b->bf_all), channels, uint64_t(uintptr_t(b->hover.p)),
                             uint64_t(b->qcap), uint64_t(stats != nullptr), uint64_t(dists != nullptr),
                             uint64_t(uintptr_t(b->part.p)), uint64_t(uintptr_t(b->items.p)),
                             uint64_t(uintptr_t(b->bq.p)), b->pair_cap, uint64_t(uintptr_t(b->out_ids.p)),
@@ -1167,9 +1241,9 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     b->run_stage(std::vector<uint64_t>(std::begin(key), std::end(key)), st, enqueue);
     GF_HIP(hipStreamSynchronize(st));
     const uint32_t* dt = b->h_tot.p;
-    if (gemm && !dt[3]) {
+    if (sched_bf && !dt[3]) {
         // the pair lists outgrew their buffers: grow them and run the brute force again
-        b->alloc_pairs(size_t(dt[2]) + dt[2] / 4 + 1024, K, Q, NS, size_t(NS) + ix->ntile / gf::kBfMaxItemTiles + 1);
+        b->alloc_pairs(size_t(dt[2]) + dt[2] / 4 + 1024, KP, Q, NS, size_t(NS) + ix->ntile / gf::kBfMaxItemTiles + 1);
         GF_HIP(gf::launch_stamp(stamp + 1, st));
         launch_gemm();
         GF_HIP(gf::launch_stamp(stamp + 2, st));
@@ -1184,7 +1258,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         const double tick_ms = 1.0 / double(ix->wclk_khz);
         t_tr = float(double(ts[1] - ts[0]) * tick_ms);
         t_bf = float(double(ts[2] - ts[1]) * tick_ms);
-        if (gemm) t_g = float(double(ts[4] - ts[3]) * tick_ms);
+        if (sched_bf) t_g = float(double(ts[4] - ts[3]) * tick_ms);
         const unsigned long long* sm = b->h_stats.p;
         std::memset(stats, 0, sizeof(*stats));
         stats->ms_traverse = t_tr;
@@ -1215,6 +1289,14 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
             stats->ops_bruteforce = 2.0 * ix->D * double(sm[9]);
             stats->bytes_bruteforce = double(sm[10]) * tile_bytes + double(dt[9]) * K * 16.0;
             stats->bf_mfma = 1;
+        } else if (gemm_h && dt[9]) {
+            // fp16 items: every (query, sub-cell) pair costs 2 D flops per
+            // point; every item streams its sub-cell's rows and meta; the
+            // final re-rank gathers the candidates' rows
+            const double tile_bytes = 16.0 * ix->D * 2.0 + 16.0 * (2 + ix->AW) * 4.0;
+            stats->ops_bruteforce = 2.0 * ix->D * double(sm[9]);
+            stats->bytes_bruteforce = double(sm[10]) * tile_bytes + b_dist * ix->rowbytes + double(dt[9]) * K * 16.0;
+            stats->bf_mfma = 2;
         } else {
             stats->bytes_bruteforce = double(stats->n_scan) * ix->a * 4.0 + b_dist * ix->rowbytes +
                                       double(dt[9]) * (K * 8.0 + ix->P * 4.0);

@@ -152,6 +152,49 @@ struct BfGemmArgs {
     uint32_t irange;
     const uint32_t* nitems_a;
 };
+// Query-batch brute force of binary16 rows on fp16 MFMA (k_bf_f16):
+// candidate keys within the distances' error bound, re-ranked exactly by
+// k_bf_f16_final.  Items and tiles as k_bf_i8's.
+constexpr uint32_t kBfHKT = 16;       // keys an item keeps per query
+struct BfHArgs {
+    SubArgs sa;
+    const uint16_t* vec;       // binary16 rows, cell-major, D per row
+    const float* xnorm;        // per row |x|^2
+    const uint16_t* q16;       // Q*D binary16 queries
+    const float* qnorm;        // per query |q|^2
+    const float* eps;          // per query bound of |d' - d|
+    const float* lo;
+    const float* hi;
+    const BfItem* items;
+    const uint32_t* nitems;
+    const uint32_t* bq;
+    const uint32_t* part_off;  // per query: first pair (its area holds pairs * kBfHKT keys)
+    uint32_t* pcnt;
+    uint64_t* part;            // kept keys (d' bits << 32) | row
+    uint32_t* gbound;          // per query: bits of the smallest K-th d' of any item so far
+    uint32_t* over;            // per query: 1 if an item may have dropped a candidate
+    const uint32_t* ok;
+    const BfItem* sitems;
+    const uint32_t* nseed;
+    uint32_t nseed_cap;
+    uint32_t K, D;
+};
+struct BfHFinal {
+    const uint32_t* ok;
+    const uint32_t* over;
+    const uint32_t* pcnt;
+    const uint32_t* part_off;
+    const uint64_t* part;
+    const float* eps;
+    const uint32_t* selcount;
+};
+// D a multiple of 32 in [64, 1024], AW 1 or 2, K <= 10.
+bool bf_f16_supported(uint32_t D, uint32_t AW, uint32_t K);
+hipError_t launch_bf_f16(const BfHArgs& a, uint32_t AW, uint32_t ncu, hipStream_t st);
+// Brute-force queries of the schedule range srange in a.sched (binary16 rows).
+hipError_t launch_bf_f16_final(const RowShape& rs, const TravArgs& a, const BfHFinal& f, uint32_t grid,
+                               hipStream_t st);
+
 // Index build: exact nearest neighbours over int8 tiles (k_knn_i8).
 constexpr uint32_t kKnnKMax = 72;   // largest K (R + 1 for graphs, E for cross edges)
 struct KnnItem {

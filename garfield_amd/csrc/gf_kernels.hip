@@ -1281,31 +1281,13 @@ __global__ void k_assemble_full(const uint32_t* graph, const uint32_t* cross, co
 // Filtered brute force over the query's cells (gpu_graph.cu:3788-4022): an
 // attribute scan of each cell's contiguous rows, compaction of the passing
 // rows, distance evaluation and a wave-held top-K keyed by (distance, row).
+// Exact distances of the rows S[0..nrows) to the query, merged into the
+// top-K (lane t < K: t-th best by (distance, row)).
 template <int VT, int LPR, int CPL>
-__global__ __launch_bounds__(64) void k_bruteforce(TravArgs p) {
-    constexpr uint32_t U = 4;                 // 64-row chunks scanned per step
-    __shared__ uint32_t S[64 * U + 64];
-    __shared__ uint64_t T[64];
-    const uint32_t lane = lane_id();
-    const uint32_t si = p.srange[0] + blockIdx.x;
-    if (si >= p.srange[1]) return;
-    const uint32_t q = p.sched[si];
-    const uint32_t K = p.K, P = p.P;
-    QReg<VT, LPR, CPL> qv;
-    load_query<VT, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
-    float lo[kMaxAttr], hi[kMaxAttr];
-#pragma unroll
-    for (uint32_t d = 0; d < kMaxAttr; ++d) {
-        lo[d] = d < p.a ? p.lo[size_t(q) * p.a + d] : 0.0f;
-        hi[d] = d < p.a ? p.hi[size_t(q) * p.a + d] : 0.0f;
-    }
-    uint64_t top = kCandSent;                 // lane t < K: t-th best
-    uint32_t n_scan = 0, n_pass = 0;
-    const uint32_t* cl = p.cells + size_t(q) * P;
-    const uint32_t lit = p.little[q];
-    uint32_t ns = 0;
-
-    auto flush = [&](uint32_t nrows) {
+__device__ void bf_flush(const QReg<VT, LPR, CPL>& qv, const TravArgs& p, const uint32_t* S, uint32_t nrows,
+                         uint64_t& top, uint64_t* T) {
+    const uint32_t lane = lane_id(), K = p.K;
+    {
         for (uint32_t base = 0; base < nrows; base += 64u) {
             const uint32_t nb = nrows - base < 64u ? nrows - base : 64u;
             const bool mine = lane < nb;
@@ -1331,7 +1313,31 @@ __global__ __launch_bounds__(64) void k_bruteforce(TravArgs p) {
             wave_sync();
             top = lane < K ? T[lane] : kCandSent;
         }
-    };
+    }
+}
+
+// Filtered brute force of query q over the first little[q] cells of its
+// list: the passing rows are gathered 64 at a time and ranked exactly.
+// Results and counters are written for q.
+template <int VT, int LPR, int CPL>
+__device__ void bf_scan_query(const TravArgs& p, uint32_t q, uint32_t* S, uint64_t* T) {
+    constexpr uint32_t U = 4;                 // 64-row chunks scanned per step (S holds 64 U + 64)
+    const uint32_t lane = lane_id();
+    const uint32_t K = p.K, P = p.P;
+    QReg<VT, LPR, CPL> qv;
+    load_query<VT, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
+    float lo[kMaxAttr], hi[kMaxAttr];
+#pragma unroll
+    for (uint32_t d = 0; d < kMaxAttr; ++d) {
+        lo[d] = d < p.a ? p.lo[size_t(q) * p.a + d] : 0.0f;
+        hi[d] = d < p.a ? p.hi[size_t(q) * p.a + d] : 0.0f;
+    }
+    uint64_t top = kCandSent;                 // lane t < K: t-th best
+    uint32_t n_scan = 0, n_pass = 0;
+    const uint32_t* cl = p.cells + size_t(q) * P;
+    const uint32_t lit = p.little[q];
+    uint32_t ns = 0;
+    auto flush = [&](uint32_t nrows) { bf_flush<VT, LPR, CPL>(qv, p, S, nrows, top, T); };
 
     for (uint32_t g = 0; g < lit; ++g) {
         const uint32_t cc = cl[g];
@@ -1380,6 +1386,15 @@ __global__ __launch_bounds__(64) void k_bruteforce(TravArgs p) {
         ctr[C_PASS] = n_pass;
         ctr[C_ROUTE] = lit ? 2u : 0u;
     }
+}
+
+template <int VT, int LPR, int CPL>
+__global__ __launch_bounds__(64) void k_bruteforce(TravArgs p) {
+    __shared__ uint32_t S[64 * 4 + 64];
+    __shared__ uint64_t T[64];
+    const uint32_t si = p.srange[0] + blockIdx.x;
+    if (si >= p.srange[1]) return;
+    bf_scan_query<VT, LPR, CPL>(p, p.sched[si], S, T);
 }
 
 __global__ void k_fill_results(uint32_t* ids, float* dist, uint32_t n) {
@@ -2967,6 +2982,273 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3
     }
 }
 
+// ------------------------------------------- fp16 query-batch brute force
+// Brute force of binary16 rows for a batch of queries on fp16 MFMA
+// (v_mfma_f32_16x16x32_f16).  Items and sub-cell tiles are k_bf_i8's; a
+// wave takes an item's queries 16 at a time (queries as the B operand, D / 32
+// k-steps held in registers) and streams the sub-cell's tiles, 16 rows each,
+// as A, gathered from the cell-major rows.  The MFMA distance
+// d' = |q|^2 + |x|^2 - 2 q.x differs from the canonical fp32 distance d by at
+// most eps_q (a bound from the fp32 error of both), so every point whose d
+// is among the K smallest has d' within the query's smallest K-th d' plus
+// 2 eps_q; k_bf_f16_final re-ranks exactly the keys within that limit.  An
+// owner lane keeps its query's 16 smallest keys per item; if the 16th lies
+// within the item's K-th plus 2 eps_q, keys may have been dropped, and the
+// query is flagged for an exact scan.
+template <int KS, int AW>
+__global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
+    __shared__ uint64_t s_buf[4][16 * kBfBufQ];
+    __shared__ uint32_t s_cnt[4][16];
+    __shared__ float s_tp[4][16];
+    __shared__ uint32_t s_bnd[4][2 * AW][16];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
+    const SubArgs& sa = p.sa;
+    const uint32_t nwg = gridDim.x, xcd = blockIdx.x & 7u, k8 = blockIdx.x >> 3;
+    const uint32_t nwg_x = (nwg - xcd + 7u) >> 3;
+    const uint32_t i_e = *p.ok ? *p.nitems : 0u;
+    const uint32_t i_lo = uint32_t(uint64_t(i_e) * xcd / 8u), i_hi = uint32_t(uint64_t(i_e) * (xcd + 1u) / 8u);
+    uint64_t* buf = s_buf[wave];
+    uint32_t* cnt = s_cnt[wave];
+    float* stp = s_tp[wave];
+    const uint32_t K = p.K;
+    const uint32_t col = lane & 15u, grp = lane >> 4;
+    constexpr uint32_t MW = 16u * (1u + AW);
+    const float kInf = __int_as_float(0x7F800000);
+    const uint32_t n_seed = p.sitems && *p.ok ? min(*p.nseed, p.nseed_cap) : 0u;
+    uint32_t seed_id = blockIdx.x * 4u + wave, item_id = i_lo + k8 * 4u + wave;
+    for (;;) {
+        BfItem it;
+        if (seed_id < n_seed) {
+            it = p.sitems[seed_id];
+            seed_id += nwg * 4u;
+        } else if (item_id < i_hi) {
+            it = p.items[item_id];
+            item_id += nwg_x * 4u;
+        } else {
+            break;
+        }
+        const uint32_t cell = sa.scell[it.sub];
+        for (uint32_t qb = 0; qb < it.nq; qb += 16u) {
+            const uint32_t nqb = min(16u, it.nq - qb);
+            // Owner state: lane < nqb owns query qb + lane; its sorted 16
+            // smallest (d' << 32 | row) keys live in registers.
+            const bool own_live = lane < nqb;
+            const uint32_t own_q = p.bq[it.qbase + qb + (own_live ? lane : 0u)];
+            const float own_eps2 = own_live ? 2.0f * p.eps[own_q] : 0.0f;
+            const uint32_t gb =
+                own_live ? __hip_atomic_load(&p.gbound[own_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                         : 0xFFFFFFFFu;
+            const float own_bnd = gb == 0xFFFFFFFFu ? kInf : __uint_as_float(gb);
+            uint64_t tk[kBfHKT];
+#pragma unroll
+            for (uint32_t k = 0; k < kBfHKT; ++k) tk[k] = kKeySent;
+            float kth = kInf;
+            wave_fence();
+            if (lane < 16u) {
+                cnt[lane] = 0;
+                stp[lane] = own_live ? own_bnd + own_eps2 : -1.0f;
+            }
+#pragma unroll
+            for (int w = 0; w < AW; ++w) {
+                uint32_t l0 = 65534u, h0 = 65534u, l1 = 0u, h1 = 0u;
+                if (own_live) {
+                    const uint32_t d0 = 2u * w, d1 = 2u * w + 1u;
+                    range16(p.lo[size_t(own_q) * sa.a + d0], p.hi[size_t(own_q) * sa.a + d0],
+                            sa.abase[cell * sa.a + d0], l0, h0);
+                    if (d1 < sa.a)
+                        range16(p.lo[size_t(own_q) * sa.a + d1], p.hi[size_t(own_q) * sa.a + d1],
+                                sa.abase[cell * sa.a + d1], l1, h1);
+                }
+                if (lane < 16u) {
+                    s_bnd[wave][2 * w][lane] = l0 | (l1 << 16);
+                    s_bnd[wave][2 * w + 1][lane] = h0 | (h1 << 16);
+                }
+            }
+            wave_fence();
+            // Column data: query qb + col (a dead column repeats the first
+            // query; its threshold -1 keeps it from producing survivors).
+            const uint32_t qc = p.bq[it.qbase + qb + (col < nqb ? col : 0u)];
+            half8_t B[KS];
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
+                B[k] = *reinterpret_cast<const half8_t*>(p.q16 + size_t(qc) * p.D + k * 32 + grp * 8);
+            const float qn = p.qnorm[qc];
+            uint32_t blo[AW], bhi[AW];
+#pragma unroll
+            for (int w = 0; w < AW; ++w) {
+                blo[w] = s_bnd[wave][2 * w][col];
+                bhi[w] = s_bnd[wave][2 * w + 1][col];
+            }
+            float tp = stp[col];
+            // Owner: merge the buffered survivors of its query and publish
+            // the new threshold min(bound, K-th) + 2 eps.
+            auto drain = [&]() {
+                wave_fence();
+                if (lane < 16u) {
+                    const uint32_t n = cnt[lane];
+                    for (uint32_t e = 0; e < n; ++e) {
+                        uint64_t c = buf[lane * kBfBufQ + e];
+                        if (c < tk[kBfHKT - 1]) {
+#pragma unroll
+                            for (uint32_t k = 0; k < kBfHKT; ++k) {
+                                const bool lt = c < tk[k];
+                                const uint64_t v = tk[k];
+                                tk[k] = lt ? c : v;
+                                c = lt ? v : c;
+                            }
+                        }
+                    }
+                    cnt[lane] = 0;
+#pragma unroll
+                    for (uint32_t k = 0; k < kBfHKT; ++k)
+                        if (k == K - 1u && tk[k] != kKeySent) kth = __uint_as_float(uint32_t(tk[k] >> 32));
+                    if (own_live) stp[lane] = fminf(own_bnd, kth) + own_eps2;
+                }
+                wave_fence();
+                tp = stp[col];
+            };
+            for (uint32_t t = it.tb; t < it.te; ++t) {
+                const uint32_t* meta = sa.tmeta + size_t(t) * MW;
+                const uint32_t ra = meta[col];                 // the row of this lane's A operand
+                const uint16_t* arow = p.vec + size_t(ra == kEmpty ? 0u : ra) * p.D + grp * 8u;
+                half8_t A[KS];
+#pragma unroll
+                for (int k = 0; k < KS; ++k) A[k] = *reinterpret_cast<const half8_t*>(arow + k * 32);
+                uint32_t mr[4];
+                float xn[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    mr[i] = meta[4u * grp + i];
+                    xn[i] = mr[i] != kEmpty ? p.xnorm[mr[i]] : 0.0f;
+                }
+                float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int k = 0; k < KS; ++k) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[k], B[k], acc, 0, 0, 0);
+                bool full = false;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    // point 4 grp + i, query column col
+                    const float d = fmaxf(__fsub_rn(__fadd_rn(qn, xn[i]), __fmul_rn(2.0f, acc[i])), 0.0f);
+                    bool ok = d <= tp && mr[i] != kEmpty;
+                    if (!__builtin_amdgcn_ballot_w64(ok)) continue;
+                    if (!it.inside) {
+#pragma unroll
+                        for (int w = 0; w < AW; ++w) {
+                            const uint32_t x = meta[16u * (1u + w) + 4u * grp + i];
+                            ok &= clamp16(x, blo[w], bhi[w]) == x;
+                        }
+                    }
+                    if (ok) {
+                        const uint32_t slot = atomicAdd(&cnt[col], 1u);
+                        buf[col * kBfBufQ + slot] = (uint64_t(__float_as_uint(d)) << 32) | mr[i];
+                        full |= slot + 1u >= kBfDrainAt;
+                    }
+                }
+                if (__builtin_amdgcn_ballot_w64(full)) drain();
+            }
+            drain();
+            if (own_live) {
+                if (kth != kInf) atomicMin(&p.gbound[own_q], __float_as_uint(kth));
+                const float lim = fminf(own_bnd, kth) + own_eps2;
+                uint32_t keep = 0;
+#pragma unroll
+                for (uint32_t k = 0; k < kBfHKT; ++k)
+                    keep += (tk[k] != kKeySent && __uint_as_float(uint32_t(tk[k] >> 32)) <= lim) ? 1u : 0u;
+                if (tk[kBfHKT - 1] != kKeySent && __uint_as_float(uint32_t(tk[kBfHKT - 1] >> 32)) <= kth + own_eps2)
+                    p.over[own_q] = 1u;
+                if (keep) {
+                    const size_t slot = size_t(p.part_off[own_q]) * kBfHKT + atomicAdd(&p.pcnt[own_q], keep);
+#pragma unroll
+                    for (uint32_t k = 0; k < kBfHKT; ++k)
+                        if (k < keep) p.part[slot + k] = tk[k];
+                }
+            }
+        }
+    }
+}
+
+// Per query of the fp16 brute force: the K-th smallest d' of the keys its
+// items kept, then the exact (canonical) distances of the keys within that
+// plus 2 eps, ranked by (distance, row).  A flagged query is scanned exactly.
+template <int VT, int LPR, int CPL>
+__global__ __launch_bounds__(64) void k_bf_f16_final(TravArgs p, BfHFinal f) {
+    __shared__ uint32_t S[64 * 4 + 64];
+    __shared__ uint64_t T[64];
+    const uint32_t lane = lane_id();
+    if (!*f.ok) return;
+    const uint32_t si = p.srange[0] + blockIdx.x;
+    if (si >= p.srange[1]) return;
+    const uint32_t q = p.sched[si];
+    if (f.over[q]) {
+        bf_scan_query<VT, LPR, CPL>(p, q, S, T);
+        return;
+    }
+    const uint32_t K = p.K;
+    const uint32_t n = f.pcnt[q];
+    const uint64_t* part = f.part + size_t(f.part_off[q]) * kBfHKT;
+    // K-th smallest key (a running top-K over chunks of 64)
+    uint64_t top = kKeySent;
+    for (uint32_t s0 = 0; s0 < n; s0 += 64u) {
+        const uint64_t c = s0 + lane < n ? part[s0 + lane] : kKeySent;
+        const bool surv = c < readlane64(top, K - 1);
+        const uint64_t sm = ballot(surv);
+        if (!sm) continue;
+        uint32_t rs = 0, rt = lane;
+        for (uint64_t m = sm; m; m &= m - 1) {
+            const uint64_t kk = readlane64(c, __builtin_ctzll(m));
+            rs += kk < c;
+            rt += kk < top;
+        }
+        for (uint32_t t = 0; t < K; ++t) rs += readlane64(top, t) < c;
+        wave_sync();
+        if (surv && rs < K) T[rs] = c;
+        if (lane < K && rt < K) T[rt] = top;
+        wave_sync();
+        top = lane < K ? T[lane] : kKeySent;
+        wave_sync();
+    }
+    const uint64_t kk = readlane64(top, K - 1);
+    const float lim = kk == kKeySent ? __int_as_float(0x7F800000)
+                                     : __uint_as_float(uint32_t(kk >> 32)) + 2.0f * f.eps[q];
+    QReg<VT, LPR, CPL> qv;
+    load_query<VT, LPR, CPL>(qv, p.queries + size_t(q) * p.qbytes, p.nch);
+    uint64_t best = kCandSent;
+    uint32_t ncand = 0;
+    for (uint32_t s0 = 0; s0 < n; s0 += 64u) {
+        const uint64_t c = s0 + lane < n ? part[s0 + lane] : kKeySent;
+        const bool in = c != kKeySent && __uint_as_float(uint32_t(c >> 32)) <= lim;
+        const uint64_t m = ballot(in);
+        wave_sync();
+        if (in) S[lanes_below(m)] = uint32_t(c);
+        wave_sync();
+        const uint32_t nb = __popcll(m);
+        if (nb) bf_flush<VT, LPR, CPL>(qv, p, S, nb, best, T);
+        ncand += nb;
+    }
+    if (lane < K) {
+        p.out_ids[size_t(q) * K + lane] = cvalid(best) ? p.gidx[crow(best)] : GF_NO_RESULT;
+        p.out_dist[size_t(q) * K + lane] = cdist(best);
+    }
+    uint32_t scan = 0;
+    for (uint32_t i = lane; i < p.little[q]; i += 64u) {
+        const uint32_t c = p.cells[size_t(q) * p.P + i];
+        scan += p.offset[c + 1] - p.offset[c];
+    }
+#pragma unroll
+    for (uint32_t o = 32; o; o >>= 1) scan += uint32_t(__shfl_xor(int(scan), int(o)));
+    if (lane == 0) {
+        uint32_t* ctr = p.counters + size_t(q) * GF_NCOUNTERS;
+        ctr[C_EXPAND] = 0;
+        ctr[C_DIST] = ncand;
+        ctr[C_ATTR] = 0;
+        ctr[C_CROSS] = 0;
+        ctr[C_LROW] = 0;
+        ctr[C_SCAN] = scan;
+        ctr[C_PASS] = f.selcount[q];
+        ctr[C_ROUTE] = 2;
+    }
+}
+
 // Per-query merge of the keys the brute-force items appended for the query.
 __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
     __shared__ uint64_t T[64];
@@ -3567,6 +3849,54 @@ uint32_t row_shape_max_cpl(int vt) { return vt == 0 ? 4u : 2u; }
         if (rs.vt == 2) GF_DISPATCH_VT(2, CALL);   \
         if (rs.vt == 3) GF_DISPATCH_VT(3, CALL);   \
     } while (0)
+
+namespace {
+template <int KS, int AW>
+hipError_t launch_bf_f16_t(const BfHArgs& a, uint32_t ncu, hipStream_t st) {
+    static int per_cu = 0;
+    if (!per_cu) {
+        int n = 0;
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_bf_f16<KS, AW>, 256, 0);
+        if (e != hipSuccess) return e;
+        per_cu = n > 0 ? n : 1;
+    }
+    hipLaunchKernelGGL((k_bf_f16<KS, AW>), dim3(ncu * uint32_t(per_cu)), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+template <int VT, int LPR, int CPL>
+hipError_t launch_bf_f16_final_t(const TravArgs& a, const BfHFinal& f, uint32_t grid, hipStream_t st) {
+    if (grid == 0) return hipSuccess;
+    hipLaunchKernelGGL((k_bf_f16_final<VT, LPR, CPL>), dim3(grid), dim3(64), 0, st, a, f);
+    return hipGetLastError();
+}
+}  // namespace
+
+bool bf_f16_supported(uint32_t D, uint32_t AW, uint32_t K) {
+    const uint32_t ks = D / 32;
+    return D % 32 == 0 && (AW == 1 || AW == 2) && K >= 1 && K <= 10 &&
+           (ks == 2 || ks == 3 || ks == 4 || ks == 8 || ks == 16 || ks == 24);
+}
+
+hipError_t launch_bf_f16(const BfHArgs& a, uint32_t AW, uint32_t ncu, hipStream_t st) {
+    if (!bf_f16_supported(a.D, AW, a.K) || ncu == 0) return hipErrorInvalidValue;
+#define BFH(KS_)                                                                  \
+    case KS_:                                                                     \
+        return AW == 1 ? launch_bf_f16_t<KS_, 1>(a, ncu, st) : launch_bf_f16_t<KS_, 2>(a, ncu, st);
+    switch (a.D / 32) {
+        BFH(2) BFH(3) BFH(4) BFH(8) BFH(16) BFH(24)
+        default: return hipErrorInvalidValue;
+    }
+#undef BFH
+}
+
+hipError_t launch_bf_f16_final(const RowShape& rs, const TravArgs& a, const BfHFinal& f, uint32_t grid,
+                               hipStream_t st) {
+    if (rs.vt != 1) return hipErrorInvalidValue;
+#define CALL_H(V, L_, C_) launch_bf_f16_final_t<V, L_, C_>(a, f, grid, st)
+    GF_DISPATCH_VT(1, CALL_H);
+#undef CALL_H
+    return hipErrorInvalidValue;
+}
 
 hipError_t launch_traverse(const RowShape& rs, const TravArgs& a, uint32_t lds, uint32_t grid, hipStream_t st) {
 #define CALL_T(V, L_, C_) launch_trav_t<V, L_, C_>(a, lds, grid, st)

@@ -144,7 +144,7 @@ def test_centroid_order_reference_ties(small_world):
 
 
 def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, postfilter=1 << 30, Q=None,
-                    channels=1):
+                    channels=1, K=10):
     import garfield_amd as gf
     from oracle import oracle as orc
     dev = _device(ix, vec_dtype=vec_dtype, f2h_factor=f2h_factor)
@@ -157,7 +157,7 @@ def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, post
         b.order_cells(4)
     gc, gcnt, glit, _ = b.get_cells()
     ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], L if channels == 2 else ix["R"])
-    ids, dists, st = b.search(L=L, K=10, rl=10, postfilter=postfilter, entry_points=ent, channels=channels)
+    ids, dists, st = b.search(L=L, K=K, rl=10, postfilter=postfilter, entry_points=ent, channels=channels)
     ctr = b.get_counters()
     vec16 = orc.f2h(ix["vectors"], f2h_factor) if vec_dtype == 1 else None
     if vec_dtype == 3:
@@ -173,7 +173,7 @@ def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, post
         oq = orc.f2h(queries, f2h_factor) if vec_dtype == 1 else queries
     orc.set_channels(channels)
     try:
-        oids, odist, octr = O.search(oq, lo, hi, gc, gcnt, glit, ent, L, K=10, rl=10, postfilter=postfilter)
+        oids, odist, octr = O.search(oq, lo, hi, gc, gcnt, glit, ent, L, K=K, rl=10, postfilter=postfilter)
     finally:
         orc.set_channels(1)
     b.close()
@@ -188,12 +188,18 @@ def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, post
 
 
 def _assert_same(ids, dists, ctr, oids, odist, octr, st=None):
-    if st is not None and st.bf_mfma:
+    if st is not None and st.bf_mfma == 1:
         # the MFMA brute force evaluates every scanned point, the oracle only
         # the passing ones
         octr = octr.copy()
         rows = octr[:, 7] == 2
         octr[rows, 1] = octr[rows, 5]
+    if st is not None and st.bf_mfma == 2:
+        # the fp16 MFMA brute force evaluates exactly the candidates its
+        # error bound keeps, the oracle every passing point
+        octr = octr.copy()
+        rows = octr[:, 7] == 2
+        octr[rows, 1] = ctr[rows, 1]
     bad = np.nonzero(np.any(ids != oids, axis=1))[0]
     assert bad.size == 0, f"{bad.size} queries differ, first q={bad[:5]}: gpu={ids[bad[0]]} oracle={oids[bad[0]]}"
     assert np.array_equal(dists.view(np.uint32), odist.view(np.uint32))
@@ -402,6 +408,34 @@ def test_dual_channel_recall(world32):
     assert orc.recall(ids, gt, gtd) > 0.8
 
 
+@pytest.mark.parametrize("prefilter,K", [(1.0, 10), (1.0, 5), (0.05, 10)])
+def test_f16_mfma_bruteforce_768d(world_c4, prefilter, K):
+    """Binary16 rows (768-d): the fp16 MFMA brute force keeps the candidates
+    within its error bound and re-ranks them exactly, so ids, distances and
+    counters equal the oracle's brute force (DIST aside: it counts the
+    candidates re-ranked)."""
+    cfg, ix = world_c4
+    _print_case("f16-bf", prefilter=prefilter, K=K)
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 32, prefilter=prefilter, vec_dtype=1,
+                                                             K=K)
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+    assert st.bf_mfma == 2 and st.q_bruteforce > 0
+    rows = octr[:, 7] == 2
+    assert np.all(ctr[rows, 1] <= octr[rows, 1])       # never more than the passing points
+
+
+@pytest.mark.parametrize("prefilter", [1.0, 0.01])
+def test_f16_mfma_bruteforce_three_attributes(world_gauss, prefilter):
+    """96-d binary16 rows (three k-steps), three attributes (two packed
+    words), f2h_factor 0.5."""
+    cfg, ix = world_gauss
+    _print_case("f16-bf-3a", prefilter=prefilter)
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 32, prefilter=prefilter, vec_dtype=1,
+                                                             f2h_factor=0.5)
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+    assert st.bf_mfma == 2 and st.q_bruteforce > 0
+
+
 def test_mfma_bruteforce_all_queries(world32):
     """Every query on the int8 MFMA brute force: exact filtered top-10."""
     from oracle import oracle as orc
@@ -483,14 +517,16 @@ def test_c4_fp16_768d_traversal(world_c4, L):
     _assert_same(*_traversal_case(cfg, ix, L, vec_dtype=1, f2h_factor=1.0)[:6])
 
 
-def test_c4_fp16_768d_bruteforce_and_order(world_c4):
-    """The gather brute force on 768-d fp16 rows (prefilter 1: every query),
-    after the cluster-guided order of stage B on 768-d centres."""
+@pytest.mark.parametrize("K", [10, 16])
+def test_c4_fp16_768d_bruteforce_and_order(world_c4, K):
+    """The brute force on 768-d fp16 rows (prefilter 1: every query), after
+    the cluster-guided order of stage B on 768-d centres: the fp16 MFMA route
+    at K = 10, the gather kernel at K = 16 (beyond the MFMA route's K)."""
     cfg, ix = world_c4
-    _print_case("c4-bruteforce")
+    _print_case("c4-bruteforce", K=K)
     ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 32, prefilter=1.0, vec_dtype=1,
-                                                             f2h_factor=1.0)
-    assert st.bf_mfma == 0 and st.q_bruteforce > 0
+                                                             f2h_factor=1.0, K=K)
+    assert st.bf_mfma == (2 if K <= 10 else 0) and st.q_bruteforce > 0
     _assert_same(ids, dists, ctr, oids, odist, octr, st)
 
 
