@@ -31,6 +31,7 @@ L_SWEEP = [10, 15, 20, 25, 30, 35, 40, 45, 50, 55, 60, 70, 80, 90, 100, 120, 140
            300, 400, 500, 600, 700, 800, 900, 1000, 1100, 1400, 1700]
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POP/s
+FP16_PEAK_TFLOPS = 2500.0 # MI355X dense fp16 MFMA, 2.5 PFLOP/s
 
 
 def log(*a):
@@ -244,7 +245,8 @@ def main():
     else:
         mfma = bool(last.bf_mfma)
         # the MFMA kernel alone (its schedule and the final merge are timed in ms_bruteforce)
-        dom, dom_bytes, dom_ms = ("k_bf_i8" if mfma else "k_bruteforce"), acc["bbf"], (ms_bfk if mfma else ms_bf)
+        dom = {1: "k_bf_i8", 2: "k_bf_f16"}.get(int(last.bf_mfma), "k_bruteforce")
+        dom_bytes, dom_ms = acc["bbf"], (ms_bfk if mfma else ms_bf)
     if mfma:
         # Algorithmic work of the int8 brute force: D multiply-adds (2 D ops)
         # per (query, point) pair that passes the query's filter.  The
@@ -256,17 +258,22 @@ def main():
         n_pass = int(ctr[ctr[:, 7] == 2, 6].sum(dtype=np.int64))
         ops_alg = 2.0 * D * n_pass
         achieved = ops_alg / (dom_ms / K / 1e3) / 1e12 if dom_ms > 0 else 0.0
-        tr = traffic.get("k_bf_i8")
+        tr = traffic.get(dom)
+        f16 = dom == "k_bf_f16"
+        peak = FP16_PEAK_TFLOPS if f16 else INT8_PEAK_TOPS
         roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
-                    "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "op_kind": "int8 MAC x2 (TOP/s)",
-                    "frac": round(achieved / INT8_PEAK_TOPS, 4),
+                    "peak": peak, "unit": "TFLOP/s",
+                    "op_kind": "fp16 MAC x2 (TFLOP/s)" if f16 else "int8 MAC x2 (TOP/s)",
+                    "frac": round(achieved / peak, 4),
                     "traffic": tr["bytes"] if tr else None,
                     "traffic_source": tr["source"] if tr else None,
                     "ops_per_launch": round(ops_alg), "pairs_passing": n_pass,
                     "ops_scheduled_per_launch": round(acc["obf"] / K),
                     "bytes_per_launch": round(dom_bytes / K), "ms_per_launch": round(dom_ms / K, 4),
-                    "launch": "one search: three k_bf_i8 launches and the two bound merges between them"}
-        dom_desc = f"{achieved:.1f} TOP/s"
+                    "launch": ("one search: one k_bf_f16 launch (the exact re-rank k_bf_f16_final is not in it)"
+                               if f16 else
+                               "one search: three k_bf_i8 launches and the two bound merges between them")}
+        dom_desc = f"{achieved:.1f} {'TFLOP/s' if f16 else 'TOP/s'}"
     else:
         achieved = (dom_bytes / K) / (dom_ms / K / 1e3) / 1e9 if dom_ms > 0 else 0.0
         tr = traffic.get(dom)

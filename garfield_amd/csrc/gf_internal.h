@@ -155,7 +155,7 @@ struct BfGemmArgs {
 // Query-batch brute force of binary16 rows on fp16 MFMA (k_bf_f16):
 // candidate keys within the distances' error bound, re-ranked exactly by
 // k_bf_f16_final.  Items and tiles as k_bf_i8's.
-constexpr uint32_t kBfHKT = 16;       // keys an item keeps per query
+constexpr uint32_t kBfHKT = 32;       // keys an item keeps per query
 struct BfHArgs {
     SubArgs sa;
     const uint16_t* vec;       // binary16 rows, cell-major, D per row

@@ -2992,15 +2992,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3
 // most eps_q (a bound from the fp32 error of both), so every point whose d
 // is among the K smallest has d' within the query's smallest K-th d' plus
 // 2 eps_q; k_bf_f16_final re-ranks exactly the keys within that limit.  An
-// owner lane keeps its query's 16 smallest keys per item; if the 16th lies
-// within the item's K-th plus 2 eps_q, keys may have been dropped, and the
-// query is flagged for an exact scan.
+// owner lane keeps its query's 32 smallest keys per item (in LDS); if all 32
+// lie within min(bound, the item's K-th) plus 2 eps_q, keys may have been
+// dropped, and the query is flagged for an exact scan.
 template <int KS, int AW>
 __global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
     __shared__ uint64_t s_buf[4][16 * kBfBufQ];
+    __shared__ uint64_t s_tk[4][16][kBfHKT];   // per owner: its kept keys, ascending
     __shared__ uint32_t s_cnt[4][16];
     __shared__ float s_tp[4][16];
     __shared__ uint32_t s_bnd[4][2 * AW][16];
+    // k-steps per load group: with more than 4, row loads are issued a
+    // group ahead of the MFMAs that use them (two group buffers)
+    constexpr int G = KS > 4 ? 4 : KS;
+    constexpr int NG = KS / G;
+    static_assert(KS % G == 0 && (NG == 1 || NG % 2 == 0), "k-step groups");
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
     const SubArgs& sa = p.sa;
     const uint32_t nwg = gridDim.x, xcd = blockIdx.x & 7u, k8 = blockIdx.x >> 3;
@@ -3030,8 +3036,8 @@ __global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
         const uint32_t cell = sa.scell[it.sub];
         for (uint32_t qb = 0; qb < it.nq; qb += 16u) {
             const uint32_t nqb = min(16u, it.nq - qb);
-            // Owner state: lane < nqb owns query qb + lane; its sorted 16
-            // smallest (d' << 32 | row) keys live in registers.
+            // Owner state: lane < nqb owns query qb + lane; its kept keys
+            // (d' << 32 | row, ascending) live in s_tk.
             const bool own_live = lane < nqb;
             const uint32_t own_q = p.bq[it.qbase + qb + (own_live ? lane : 0u)];
             const float own_eps2 = own_live ? 2.0f * p.eps[own_q] : 0.0f;
@@ -3039,14 +3045,14 @@ __global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
                 own_live ? __hip_atomic_load(&p.gbound[own_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                          : 0xFFFFFFFFu;
             const float own_bnd = gb == 0xFFFFFFFFu ? kInf : __uint_as_float(gb);
-            uint64_t tk[kBfHKT];
-#pragma unroll
-            for (uint32_t k = 0; k < kBfHKT; ++k) tk[k] = kKeySent;
+            uint64_t* tk = s_tk[wave][col];
             float kth = kInf;
             wave_fence();
             if (lane < 16u) {
                 cnt[lane] = 0;
                 stp[lane] = own_live ? own_bnd + own_eps2 : -1.0f;
+#pragma unroll
+                for (uint32_t k = 0; k < kBfHKT; ++k) tk[k] = kKeySent;
             }
 #pragma unroll
             for (int w = 0; w < AW; ++w) {
@@ -3080,40 +3086,45 @@ __global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
                 bhi[w] = s_bnd[wave][2 * w + 1][col];
             }
             float tp = stp[col];
-            // Owner: merge the buffered survivors of its query and publish
-            // the new threshold min(bound, K-th) + 2 eps.
+            // Owner: insert the buffered survivors of its query into its kept
+            // keys and publish the new threshold min(bound, K-th) + 2 eps.
             auto drain = [&]() {
                 wave_fence();
                 if (lane < 16u) {
                     const uint32_t n = cnt[lane];
                     for (uint32_t e = 0; e < n; ++e) {
-                        uint64_t c = buf[lane * kBfBufQ + e];
-                        if (c < tk[kBfHKT - 1]) {
-#pragma unroll
-                            for (uint32_t k = 0; k < kBfHKT; ++k) {
-                                const bool lt = c < tk[k];
-                                const uint64_t v = tk[k];
-                                tk[k] = lt ? c : v;
-                                c = lt ? v : c;
-                            }
+                        const uint64_t c = buf[lane * kBfBufQ + e];
+                        if (c >= tk[kBfHKT - 1]) continue;
+                        uint32_t j = kBfHKT - 1;
+                        while (j > 0 && tk[j - 1] > c) {
+                            tk[j] = tk[j - 1];
+                            --j;
                         }
+                        tk[j] = c;
                     }
                     cnt[lane] = 0;
-#pragma unroll
-                    for (uint32_t k = 0; k < kBfHKT; ++k)
-                        if (k == K - 1u && tk[k] != kKeySent) kth = __uint_as_float(uint32_t(tk[k] >> 32));
+                    const uint64_t kk = tk[K - 1];
+                    if (kk != kKeySent) kth = __uint_as_float(uint32_t(kk >> 32));
                     if (own_live) stp[lane] = fminf(own_bnd, kth) + own_eps2;
                 }
                 wave_fence();
                 tp = stp[col];
             };
+            // A operand rows: lane's row of tile t is meta[col]; groups of G
+            // k-steps are loaded into alternating buffers a group ahead.
+            auto arow_of = [&](uint32_t t) {
+                const uint32_t ra = sa.tmeta[size_t(t) * MW + col];
+                return p.vec + size_t(ra == kEmpty ? 0u : ra) * p.D + grp * 8u;
+            };
+            half8_t Ab[NG == 1 ? 1 : 2][G];
+            auto load_group = [&](half8_t (&dst)[G], const uint16_t* arow, int g) {
+#pragma unroll
+                for (int k = 0; k < G; ++k) dst[k] = *reinterpret_cast<const half8_t*>(arow + (g * G + k) * 32);
+            };
+            const uint16_t* arow = it.tb < it.te ? arow_of(it.tb) : p.vec;
+            if (it.tb < it.te) load_group(Ab[0], arow, 0);
             for (uint32_t t = it.tb; t < it.te; ++t) {
                 const uint32_t* meta = sa.tmeta + size_t(t) * MW;
-                const uint32_t ra = meta[col];                 // the row of this lane's A operand
-                const uint16_t* arow = p.vec + size_t(ra == kEmpty ? 0u : ra) * p.D + grp * 8u;
-                half8_t A[KS];
-#pragma unroll
-                for (int k = 0; k < KS; ++k) A[k] = *reinterpret_cast<const half8_t*>(arow + k * 32);
                 uint32_t mr[4];
                 float xn[4];
 #pragma unroll
@@ -3121,9 +3132,25 @@ __global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
                     mr[i] = meta[4u * grp + i];
                     xn[i] = mr[i] != kEmpty ? p.xnorm[mr[i]] : 0.0f;
                 }
+                const uint16_t* anext = t + 1 < it.te ? arow_of(t + 1) : arow;
                 float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+                if constexpr (NG == 1) {
 #pragma unroll
-                for (int k = 0; k < KS; ++k) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[k], B[k], acc, 0, 0, 0);
+                    for (int k = 0; k < KS; ++k)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab[0][k], B[k], acc, 0, 0, 0);
+                    if (t + 1 < it.te) load_group(Ab[0], anext, 0);
+                } else {
+#pragma unroll
+                    for (int g = 0; g < NG; ++g) {
+                        // the next group: of this tile, or the next tile's first
+                        if (g + 1 < NG) load_group(Ab[(g + 1) & 1], arow, g + 1);
+                        else if (t + 1 < it.te) load_group(Ab[0], anext, 0);
+#pragma unroll
+                        for (int k = 0; k < G; ++k)
+                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab[g & 1][k], B[g * G + k], acc, 0, 0, 0);
+                    }
+                }
+                arow = anext;
                 bool full = false;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -3149,20 +3176,19 @@ __global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
             drain();
             if (own_live) {
                 if (kth != kInf) atomicMin(&p.gbound[own_q], __float_as_uint(kth));
+                // keys within the query's limit; if the last kept key is
+                // within it too, keys beyond may have been dropped
                 const float lim = fminf(own_bnd, kth) + own_eps2;
                 uint32_t keep = 0;
-#pragma unroll
-                for (uint32_t k = 0; k < kBfHKT; ++k)
-                    keep += (tk[k] != kKeySent && __uint_as_float(uint32_t(tk[k] >> 32)) <= lim) ? 1u : 0u;
-                if (tk[kBfHKT - 1] != kKeySent && __uint_as_float(uint32_t(tk[kBfHKT - 1] >> 32)) <= kth + own_eps2)
-                    p.over[own_q] = 1u;
+                while (keep < kBfHKT && tk[keep] != kKeySent && __uint_as_float(uint32_t(tk[keep] >> 32)) <= lim)
+                    ++keep;
+                if (keep == kBfHKT) p.over[own_q] = 1u;
                 if (keep) {
                     const size_t slot = size_t(p.part_off[own_q]) * kBfHKT + atomicAdd(&p.pcnt[own_q], keep);
-#pragma unroll
-                    for (uint32_t k = 0; k < kBfHKT; ++k)
-                        if (k < keep) p.part[slot + k] = tk[k];
+                    for (uint32_t k = 0; k < keep; ++k) p.part[slot + k] = tk[k];
                 }
             }
+            wave_fence();
         }
     }
 }
