@@ -331,11 +331,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "i8" if (last.bf_mfma and ms_bf > ms_tr) else ("f16" if vec_dtype == gf.VEC_F16 else "f32"),
+        "dtype": "i8" if (last.bf_mfma == 1 and ms_bf > ms_tr) else ("f16" if vec_dtype == gf.VEC_F16 else "f32"),
         "data": "synthetic (generated in bench.py; index built on the GPU by the library's builder)",
         "config": {
             "workload": workload,
-            "route": ("filtered brute force (int8 MFMA query-batch kernel)" if best["route"] == "bruteforce"
+            "route": ({1: "filtered brute force (int8 MFMA query-batch kernel)",
+                       2: "filtered brute force (fp16 MFMA query-batch kernel, candidates re-ranked exactly)"}.get(
+                           int(last.bf_mfma), "filtered brute force (gather kernel)") if best["route"] == "bruteforce"
                       else ("dual-channel" if bch == 2 else "cell-by-cell") +
                       " graph traversal (queries at or below the prefilter selectivity to filtered brute force)"),
             "channels": bch,
