@@ -32,6 +32,7 @@ L_SWEEP = [10, 15, 20, 25, 30, 35, 40, 45, 50, 55, 60, 70, 80, 90, 100, 120, 140
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POP/s
 FP16_PEAK_TFLOPS = 2500.0 # MI355X dense fp16 MFMA, 2.5 PFLOP/s
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 
 
 def log(*a):
@@ -245,7 +246,8 @@ def main():
     else:
         mfma = bool(last.bf_mfma)
         # the MFMA kernel alone (its schedule and the final merge are timed in ms_bruteforce)
-        dom = {1: "k_bf_i8", 2: "k_bf_f16"}.get(int(last.bf_mfma), "k_bruteforce")
+        dom = {1: "k_bf_i8", 2: "k_bf_f16" if vec_dtype == gf.VEC_F16 else "k_bf_f32"}.get(int(last.bf_mfma),
+                                                                                         "k_bruteforce")
         dom_bytes, dom_ms = acc["bbf"], (ms_bfk if mfma else ms_bf)
     if mfma:
         # Algorithmic work of the int8 brute force: D multiply-adds (2 D ops)
@@ -259,18 +261,19 @@ def main():
         ops_alg = 2.0 * D * n_pass
         achieved = ops_alg / (dom_ms / K / 1e3) / 1e12 if dom_ms > 0 else 0.0
         tr = traffic.get(dom)
-        f16 = dom == "k_bf_f16"
-        peak = FP16_PEAK_TFLOPS if f16 else INT8_PEAK_TOPS
+        f16 = dom in ("k_bf_f16", "k_bf_f32")
+        peak = {"k_bf_f16": FP16_PEAK_TFLOPS, "k_bf_f32": FP32_PEAK_TFLOPS}.get(dom, INT8_PEAK_TOPS)
         roofline = {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                     "peak": peak, "unit": "TFLOP/s",
-                    "op_kind": "fp16 MAC x2 (TFLOP/s)" if f16 else "int8 MAC x2 (TOP/s)",
+                    "op_kind": {"k_bf_f16": "fp16 MAC x2 (TFLOP/s)", "k_bf_f32": "fp32 MAC x2 (TFLOP/s)"}.get(
+                        dom, "int8 MAC x2 (TOP/s)"),
                     "frac": round(achieved / peak, 4),
                     "traffic": tr["bytes"] if tr else None,
                     "traffic_source": tr["source"] if tr else None,
                     "ops_per_launch": round(ops_alg), "pairs_passing": n_pass,
                     "ops_scheduled_per_launch": round(acc["obf"] / K),
                     "bytes_per_launch": round(dom_bytes / K), "ms_per_launch": round(dom_ms / K, 4),
-                    "launch": ("one search: one k_bf_f16 launch (the exact re-rank k_bf_f16_final is not in it)"
+                    "launch": (f"one search: one {dom} launch (the exact re-rank k_bf_f16_final is not in it)"
                                if f16 else
                                "one search: three k_bf_i8 launches and the two bound merges between them")}
         dom_desc = f"{achieved:.1f} {'TFLOP/s' if f16 else 'TOP/s'}"
@@ -336,7 +339,7 @@ def main():
         "config": {
             "workload": workload,
             "route": ({1: "filtered brute force (int8 MFMA query-batch kernel)",
-                       2: "filtered brute force (fp16 MFMA query-batch kernel, candidates re-ranked exactly)"}.get(
+                       2: "filtered brute force (float MFMA query-batch kernel, candidates re-ranked exactly)"}.get(
                            int(last.bf_mfma), "filtered brute force (gather kernel)") if best["route"] == "bruteforce"
                       else ("dual-channel" if bch == 2 else "cell-by-cell") +
                       " graph traversal (queries at or below the prefilter selectivity to filtered brute force)"),

@@ -400,26 +400,34 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
                                       ix.stream));
             ix.i8 = true;
         }
-        // Binary16 rows with sub-cells: |x|^2 per row (fp32, as k_norms_f16
-        // sums the binary16 values) and the largest |x| for the fp16 MFMA
-        // brute force's error bound (each binary16 value is within 2^-11 of
-        // x * alpha).
-        if (ix.sub && ix.vdtype == GF_VEC_F16 && gf::bf_f16_supported(D, ix.AW, 1)) {
-            ix.xnorm16.alloc(N);
-            GF_HIP(gf::launch_norms_f16(reinterpret_cast<const uint16_t*>(ix.vec.p), N, D, D, ix.xnorm16.p,
-                                        ix.stream));
+        // Float rows with sub-cells and no int8 route: |x|^2 per row (fp32:
+        // binary16 rows as k_norms_f16 sums their values, fp32 rows from a
+        // float64 sum) and the largest |x| for the MFMA brute force's error
+        // bound (a binary16 value is within 2^-11 of x * alpha, or 2^-25 for
+        // subnormals).
+        const int fvt = ix.vdtype == GF_VEC_F16 ? 1 : (ix.vdtype == GF_VEC_F32 ? 0 : -1);
+        if (ix.sub && !ix.i8 && fvt >= 0 && gf::bf_float_supported(fvt, D, ix.AW, 1)) {
+            std::vector<float> xn(fvt == 0 ? N : 0);
             double xm = 0.0;
             for (uint32_t r = 0; r < N; ++r) {
                 double s = 0.0;
                 for (uint32_t d = 0; d < D; ++d) {
-                    const double x = double(v[size_t(r) * D + d]) * ix.alpha;
+                    const double x = double(v[size_t(r) * D + d]) * (fvt == 1 ? ix.alpha : 1.0f);
                     s += x * x;
                 }
                 xm = std::max(xm, s);
+                if (fvt == 0) xn[r] = float(s);
             }
-            // binary16 rounding: within 2^-11 relative, 2^-25 absolute (subnormals)
-            ix.xmax16 = std::sqrt(xm) * (1.0 + 1.0 / 1024.0) + std::sqrt(double(D)) * std::ldexp(1.0, -24);
-            ix.h16 = true;
+            if (fvt == 1) {
+                ix.xnormf.alloc(N);
+                GF_HIP(gf::launch_norms_f16(reinterpret_cast<const uint16_t*>(ix.vec.p), N, D, D, ix.xnormf.p,
+                                            ix.stream));
+                ix.xmaxf = std::sqrt(xm) * (1.0 + 1.0 / 1024.0) + std::sqrt(double(D)) * std::ldexp(1.0, -24);
+            } else {
+                ix.xnormf.upload(xn);
+                ix.xmaxf = std::sqrt(xm) * (1.0 + 1e-6);
+            }
+            ix.hf = true;
         }
         GF_HIP(hipStreamSynchronize(ix.stream));
     }
@@ -703,31 +711,39 @@ gf_status gf_batch_create(gf_index* ix, const float* queries, uint32_t Q, const 
         if (ix->vdtype == GF_VEC_F16) {
             b->q16v.alloc(size_t(Q) * ix->D);
             GF_HIP(gf::launch_f2h(b->qf32.p, b->q16v.p, size_t(Q) * ix->D, ix->alpha, ix->stream));
-            if (ix->h16) {
-                // |q|^2 of the binary16 query, and the bound eps_q of |d' - d|
-                // for the fp16 MFMA brute force: d' = |q|^2 + |x|^2 - 2 q.x
-                // and the canonical d each hold fp32 sums of D terms, within
-                // gamma_{D+2} (|q| + |x|)^2 of the exact distance between the
-                // binary16 vectors (plus two roundings of the combination);
-                // doubled for margin, with a floor for subnormal products.
-                const uint32_t D = ix->D;
-                b->qn16.alloc(Q);
-                GF_HIP(gf::launch_norms_f16(b->q16v.p, Q, D, D, b->qn16.p, ix->stream));
-                const double u = std::ldexp(1.0, -24), gam = (D + 2) * u / (1.0 - (D + 2) * u);
-                std::vector<float> eps(Q);
-                for (uint32_t q = 0; q < Q; ++q) {
-                    double s = 0.0;
-                    for (uint32_t d = 0; d < D; ++d) {
-                        const double x = double(queries[size_t(q) * D + d]) * ix->alpha;
-                        s += x * x;
-                    }
-                    const double nq = std::sqrt(s) * (1.0 + 1.0 / 1024.0) + std::sqrt(double(D)) * std::ldexp(1.0, -24);
-                    const double e = 2.0 * (3.0 * gam + 2.0 * u) * (nq + ix->xmax16) * (nq + ix->xmax16) +
-                                     D * std::ldexp(1.0, -40);
-                    eps[q] = float(e * (1.0 + 1e-6));
+        }
+        if (ix->hf) {
+            // |q|^2 of the query as the rows hold it (binary16 or fp32), and
+            // the bound eps_q of |d' - d| for the MFMA brute force of float
+            // rows: d' = |q|^2 + |x|^2 - 2 q.x and the canonical d each hold
+            // fp32 sums of D terms, within gamma_{D+2} (|q| + |x|)^2 of the
+            // exact distance of the rows' vectors (plus two roundings of the
+            // combination); doubled for margin, with a floor for subnormal
+            // products.
+            const uint32_t D = ix->D;
+            const bool h = ix->vdtype == GF_VEC_F16;
+            const double u = std::ldexp(1.0, -24), gam = (D + 2) * u / (1.0 - (D + 2) * u);
+            std::vector<float> eps(Q), qn(h ? 0 : Q);
+            for (uint32_t q = 0; q < Q; ++q) {
+                double s = 0.0;
+                for (uint32_t d = 0; d < D; ++d) {
+                    const double x = double(queries[size_t(q) * D + d]) * (h ? ix->alpha : 1.0f);
+                    s += x * x;
                 }
-                b->heps.upload(eps);
+                if (!h) qn[q] = float(s);
+                const double nq = h ? std::sqrt(s) * (1.0 + 1.0 / 1024.0) + std::sqrt(double(D)) * std::ldexp(1.0, -24)
+                                    : std::sqrt(s) * (1.0 + 1e-6);
+                const double e = 2.0 * (3.0 * gam + 2.0 * u) * (nq + ix->xmaxf) * (nq + ix->xmaxf) +
+                                 D * std::ldexp(1.0, -40);
+                eps[q] = float(e * (1.0 + 1e-6));
             }
+            if (h) {
+                b->qnf.alloc(Q);
+                GF_HIP(gf::launch_norms_f16(b->q16v.p, Q, D, D, b->qnf.p, ix->stream));
+            } else {
+                b->qnf.upload(qn);
+            }
+            b->heps.upload(eps);
         }
         if (ix->vdtype == GF_VEC_I8Q) {
             // rows [c | s]: c_d = fma(s_d, z_d, alpha q_d), the query less
@@ -1003,7 +1019,8 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     const bool gemm = ix->i8 && b->i8 && K <= gf::kBfKMax;
     // Binary16 rows: the same items on fp16 MFMA, candidates within the
     // distances' error bound re-ranked exactly (k_bf_f16, k_bf_f16_final).
-    const bool gemm_h = !gemm && ix->h16 && b->qn16.n == Q && gf::bf_f16_supported(ix->D, ix->AW, K);
+    const int fvt = ix->vdtype == GF_VEC_F16 ? 1 : 0;
+    const bool gemm_h = !gemm && ix->hf && b->qnf.n == Q && gf::bf_float_supported(fvt, ix->D, ix->AW, K);
     const bool sched_bf = gemm || gemm_h;
     const uint32_t KP = gemm_h ? gf::kBfHKT : K;   // keys per (query, item) in the partial area
     const uint32_t NS = ix->NS;
@@ -1097,15 +1114,16 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
             GF_HIP(gf::launch_zero_u32(b->hover.p, Q, st));
             gf::BfHArgs ha{};
             ha.sa = sub_args(*ix);
-            ha.vec = reinterpret_cast<const uint16_t*>(ix->vec.p); ha.xnorm = ix->xnorm16.p;
-            ha.q16 = b->q16v.p; ha.qnorm = b->qn16.p; ha.eps = b->heps.p; ha.lo = b->lo.p; ha.hi = b->hi.p;
+            ha.vec = ix->vec.p; ha.xnorm = ix->xnormf.p;
+            ha.q16 = fvt == 1 ? static_cast<const void*>(b->q16v.p) : static_cast<const void*>(b->qf32.p);
+            ha.qnorm = b->qnf.p; ha.eps = b->heps.p; ha.lo = b->lo.p; ha.hi = b->hi.p;
             ha.items = b->items.p; ha.nitems = tot + 4; ha.bq = b->bq.p; ha.part_off = b->part_off.p;
             ha.pcnt = b->pcnt.p; ha.part = b->part.p; ha.gbound = b->gbound.p; ha.over = b->hover.p;
             ha.ok = tot + 3;
             if (seeds) { ha.sitems = b->sitems.p; ha.nseed = tot + 5; ha.nseed_cap = scap; }
             ha.K = K; ha.D = ix->D;
             GF_HIP(gf::launch_stamp(stamp + 3, st));
-            GF_HIP(gf::launch_bf_f16(ha, ix->AW, uint32_t(ix->ncu), st));
+            GF_HIP(gf::launch_bf_float(ha, fvt, ix->AW, uint32_t(ix->ncu), st));
             GF_HIP(gf::launch_stamp(stamp + 4, st));
             gf::TravArgs ab = a;
             ab.srange = tot + 14;

@@ -152,15 +152,16 @@ struct BfGemmArgs {
     uint32_t irange;
     const uint32_t* nitems_a;
 };
-// Query-batch brute force of binary16 rows on fp16 MFMA (k_bf_f16):
-// candidate keys within the distances' error bound, re-ranked exactly by
-// k_bf_f16_final.  Items and tiles as k_bf_i8's.
+// Query-batch brute force of float rows on MFMA (k_bf_f16: binary16 rows,
+// fp16 MFMA; k_bf_f32: fp32 rows, fp32 MFMA): candidate keys within the
+// distances' error bound, re-ranked exactly by k_bf_f16_final.  Items and
+// tiles as k_bf_i8's.
 constexpr uint32_t kBfHKT = 32;       // keys an item keeps per query
 struct BfHArgs {
     SubArgs sa;
-    const uint16_t* vec;       // binary16 rows, cell-major, D per row
+    const void* vec;           // rows (binary16 or fp32), cell-major, D per row
     const float* xnorm;        // per row |x|^2
-    const uint16_t* q16;       // Q*D binary16 queries
+    const void* q16;           // Q*D queries of the rows' type
     const float* qnorm;        // per query |q|^2
     const float* eps;          // per query bound of |d' - d|
     const float* lo;
@@ -188,10 +189,11 @@ struct BfHFinal {
     const float* eps;
     const uint32_t* selcount;
 };
-// D a multiple of 32 in [64, 1024], AW 1 or 2, K <= 10.
-bool bf_f16_supported(uint32_t D, uint32_t AW, uint32_t K);
-hipError_t launch_bf_f16(const BfHArgs& a, uint32_t AW, uint32_t ncu, hipStream_t st);
-// Brute-force queries of the schedule range srange in a.sched (binary16 rows).
+// vt 1 (binary16 rows): D in {64, 96, 128, 256, 512, 768}; vt 0 (fp32
+// rows): D in {64, 96, 128, 256}; AW 1 or 2; K <= 10.
+bool bf_float_supported(int vt, uint32_t D, uint32_t AW, uint32_t K);
+hipError_t launch_bf_float(const BfHArgs& a, int vt, uint32_t AW, uint32_t ncu, hipStream_t st);
+// Brute-force queries of the schedule range srange in a.sched (binary16 or fp32 rows).
 hipError_t launch_bf_f16_final(const RowShape& rs, const TravArgs& a, const BfHFinal& f, uint32_t grid,
                                hipStream_t st);
 

@@ -2995,18 +2995,53 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3
 // owner lane keeps its query's 32 smallest keys per item (in LDS); if all 32
 // lie within min(bound, the item's K-th) plus 2 eps_q, keys may have been
 // dropped, and the query is flagged for an exact scan.
-template <int KS, int AW>
-__global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
+// Operand chunks of the two row types.  Binary16 rows (VT 1): a chunk is
+// one v_mfma_f32_16x16x32_f16 k-step, 8 halves per lane (lane group g holds
+// dims 32 c + 8 g .. + 8).  fp32 rows (VT 0): a chunk is four
+// v_mfma_f32_16x16x4_f32 k-steps, 4 floats per lane; lane group g supplies
+// k-slot g, so it holds dims g D/4 + 4 c .. + 4 (a permutation of the dims,
+// the same for rows and queries, which the dot product does not see).
+template <int VT> struct BfChunk;
+template <> struct BfChunk<1> {
+    typedef half8_t T;
+    typedef uint16_t E;
+    static __device__ __forceinline__ const E* at(const E* row, uint32_t D, uint32_t g, int c) {
+        return row + c * 32 + g * 8u;
+    }
+    static __device__ __forceinline__ float4_t mma(const T& a, const T& b, float4_t acc) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+    }
+};
+template <> struct BfChunk<0> {
+    typedef float4_t T;
+    typedef float E;
+    static __device__ __forceinline__ const E* at(const E* row, uint32_t D, uint32_t g, int c) {
+        return row + g * (D / 4u) + c * 4;
+    }
+    static __device__ __forceinline__ float4_t mma(const T& a, const T& b, float4_t acc) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc, 0, 0, 0);
+        return acc;
+    }
+};
+
+template <int VT, int KS, int AW>
+__device__ void bf_float_items(const BfHArgs& p) {
+    typedef BfChunk<VT> CH;
+    typedef typename CH::T ChunkT;
+    typedef typename CH::E ElemT;
     __shared__ uint64_t s_buf[4][16 * kBfBufQ];
     __shared__ uint64_t s_tk[4][16][kBfHKT];   // per owner: its kept keys, ascending
     __shared__ uint32_t s_cnt[4][16];
     __shared__ float s_tp[4][16];
     __shared__ uint32_t s_bnd[4][2 * AW][16];
-    // k-steps per load group: with more than 4, row loads are issued a
-    // group ahead of the MFMAs that use them (two group buffers)
-    constexpr int G = KS > 4 ? 4 : KS;
+    // chunks per load group: with more than 4, row loads are issued a group
+    // ahead of the MFMAs that use them (two group buffers)
+    constexpr int G = KS <= 4 ? KS : (KS == 6 ? 3 : 4);
     constexpr int NG = KS / G;
-    static_assert(KS % G == 0 && (NG == 1 || NG % 2 == 0), "k-step groups");
+    static_assert(KS % G == 0 && (NG == 1 || NG % 2 == 0), "chunk groups");
+    const ElemT* vec = reinterpret_cast<const ElemT*>(p.vec);
+    const ElemT* qrows = reinterpret_cast<const ElemT*>(p.q16);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
     const SubArgs& sa = p.sa;
     const uint32_t nwg = gridDim.x, xcd = blockIdx.x & 7u, k8 = blockIdx.x >> 3;
@@ -3074,10 +3109,10 @@ __global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
             // Column data: query qb + col (a dead column repeats the first
             // query; its threshold -1 keeps it from producing survivors).
             const uint32_t qc = p.bq[it.qbase + qb + (col < nqb ? col : 0u)];
-            half8_t B[KS];
+            ChunkT B[KS];
 #pragma unroll
             for (int k = 0; k < KS; ++k)
-                B[k] = *reinterpret_cast<const half8_t*>(p.q16 + size_t(qc) * p.D + k * 32 + grp * 8);
+                B[k] = *reinterpret_cast<const ChunkT*>(CH::at(qrows + size_t(qc) * p.D, p.D, grp, k));
             const float qn = p.qnorm[qc];
             uint32_t blo[AW], bhi[AW];
 #pragma unroll
@@ -3114,14 +3149,15 @@ __global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
             // k-steps are loaded into alternating buffers a group ahead.
             auto arow_of = [&](uint32_t t) {
                 const uint32_t ra = sa.tmeta[size_t(t) * MW + col];
-                return p.vec + size_t(ra == kEmpty ? 0u : ra) * p.D + grp * 8u;
+                return vec + size_t(ra == kEmpty ? 0u : ra) * p.D;
             };
-            half8_t Ab[NG == 1 ? 1 : 2][G];
-            auto load_group = [&](half8_t (&dst)[G], const uint16_t* arow, int g) {
+            ChunkT Ab[NG == 1 ? 1 : 2][G];
+            auto load_group = [&](ChunkT (&dst)[G], const ElemT* arow, int g) {
 #pragma unroll
-                for (int k = 0; k < G; ++k) dst[k] = *reinterpret_cast<const half8_t*>(arow + (g * G + k) * 32);
+                for (int k = 0; k < G; ++k)
+                    dst[k] = *reinterpret_cast<const ChunkT*>(CH::at(arow, p.D, grp, g * G + k));
             };
-            const uint16_t* arow = it.tb < it.te ? arow_of(it.tb) : p.vec;
+            const ElemT* arow = it.tb < it.te ? arow_of(it.tb) : vec;
             if (it.tb < it.te) load_group(Ab[0], arow, 0);
             for (uint32_t t = it.tb; t < it.te; ++t) {
                 const uint32_t* meta = sa.tmeta + size_t(t) * MW;
@@ -3132,12 +3168,11 @@ __global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
                     mr[i] = meta[4u * grp + i];
                     xn[i] = mr[i] != kEmpty ? p.xnorm[mr[i]] : 0.0f;
                 }
-                const uint16_t* anext = t + 1 < it.te ? arow_of(t + 1) : arow;
+                const ElemT* anext = t + 1 < it.te ? arow_of(t + 1) : arow;
                 float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
                 if constexpr (NG == 1) {
 #pragma unroll
-                    for (int k = 0; k < KS; ++k)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab[0][k], B[k], acc, 0, 0, 0);
+                    for (int k = 0; k < KS; ++k) acc = CH::mma(Ab[0][k], B[k], acc);
                     if (t + 1 < it.te) load_group(Ab[0], anext, 0);
                 } else {
 #pragma unroll
@@ -3146,8 +3181,7 @@ __global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
                         if (g + 1 < NG) load_group(Ab[(g + 1) & 1], arow, g + 1);
                         else if (t + 1 < it.te) load_group(Ab[0], anext, 0);
 #pragma unroll
-                        for (int k = 0; k < G; ++k)
-                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab[g & 1][k], B[g * G + k], acc, 0, 0, 0);
+                        for (int k = 0; k < G; ++k) acc = CH::mma(Ab[g & 1][k], B[g * G + k], acc);
                     }
                 }
                 arow = anext;
@@ -3191,6 +3225,15 @@ __global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
             wave_fence();
         }
     }
+}
+
+template <int KS, int AW>
+__global__ __launch_bounds__(256) void k_bf_f16(BfHArgs p) {
+    bf_float_items<1, KS, AW>(p);
+}
+template <int KS, int AW>
+__global__ __launch_bounds__(256) void k_bf_f32(BfHArgs p) {
+    bf_float_items<0, KS, AW>(p);
 }
 
 // Per query of the fp16 brute force: the K-th smallest d' of the keys its
@@ -3877,16 +3920,17 @@ uint32_t row_shape_max_cpl(int vt) { return vt == 0 ? 4u : 2u; }
     } while (0)
 
 namespace {
-template <int KS, int AW>
-hipError_t launch_bf_f16_t(const BfHArgs& a, uint32_t ncu, hipStream_t st) {
+template <int VT, int KS, int AW>
+hipError_t launch_bf_float_t(const BfHArgs& a, uint32_t ncu, hipStream_t st) {
     static int per_cu = 0;
+    const auto kern = VT == 1 ? k_bf_f16<KS, AW> : k_bf_f32<KS, AW>;
     if (!per_cu) {
         int n = 0;
-        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_bf_f16<KS, AW>, 256, 0);
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 256, 0);
         if (e != hipSuccess) return e;
         per_cu = n > 0 ? n : 1;
     }
-    hipLaunchKernelGGL((k_bf_f16<KS, AW>), dim3(ncu * uint32_t(per_cu)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(kern, dim3(ncu * uint32_t(per_cu)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 template <int VT, int LPR, int CPL>
@@ -3897,19 +3941,32 @@ hipError_t launch_bf_f16_final_t(const TravArgs& a, const BfHFinal& f, uint32_t 
 }
 }  // namespace
 
-bool bf_f16_supported(uint32_t D, uint32_t AW, uint32_t K) {
-    const uint32_t ks = D / 32;
-    return D % 32 == 0 && (AW == 1 || AW == 2) && K >= 1 && K <= 10 &&
-           (ks == 2 || ks == 3 || ks == 4 || ks == 8 || ks == 16 || ks == 24);
+bool bf_float_supported(int vt, uint32_t D, uint32_t AW, uint32_t K) {
+    if (!(AW == 1 || AW == 2) || K < 1 || K > 10) return false;
+    if (vt == 1) {
+        const uint32_t ks = D / 32;
+        return D % 32 == 0 && (ks == 2 || ks == 3 || ks == 4 || ks == 8 || ks == 16 || ks == 24);
+    }
+    if (vt == 0) {
+        const uint32_t ks = D / 16;
+        return D % 16 == 0 && (ks == 4 || ks == 6 || ks == 8 || ks == 16);
+    }
+    return false;
 }
 
-hipError_t launch_bf_f16(const BfHArgs& a, uint32_t AW, uint32_t ncu, hipStream_t st) {
-    if (!bf_f16_supported(a.D, AW, a.K) || ncu == 0) return hipErrorInvalidValue;
-#define BFH(KS_)                                                                  \
-    case KS_:                                                                     \
-        return AW == 1 ? launch_bf_f16_t<KS_, 1>(a, ncu, st) : launch_bf_f16_t<KS_, 2>(a, ncu, st);
-    switch (a.D / 32) {
-        BFH(2) BFH(3) BFH(4) BFH(8) BFH(16) BFH(24)
+hipError_t launch_bf_float(const BfHArgs& a, int vt, uint32_t AW, uint32_t ncu, hipStream_t st) {
+    if (!bf_float_supported(vt, a.D, AW, a.K) || ncu == 0) return hipErrorInvalidValue;
+#define BFH(VT_, KS_)                                                                        \
+    case KS_:                                                                                \
+        return AW == 1 ? launch_bf_float_t<VT_, KS_, 1>(a, ncu, st) : launch_bf_float_t<VT_, KS_, 2>(a, ncu, st);
+    if (vt == 1) {
+        switch (a.D / 32) {
+            BFH(1, 2) BFH(1, 3) BFH(1, 4) BFH(1, 8) BFH(1, 16) BFH(1, 24)
+            default: return hipErrorInvalidValue;
+        }
+    }
+    switch (a.D / 16) {
+        BFH(0, 4) BFH(0, 6) BFH(0, 8) BFH(0, 16)
         default: return hipErrorInvalidValue;
     }
 #undef BFH
@@ -3917,9 +3974,9 @@ hipError_t launch_bf_f16(const BfHArgs& a, uint32_t AW, uint32_t ncu, hipStream_
 
 hipError_t launch_bf_f16_final(const RowShape& rs, const TravArgs& a, const BfHFinal& f, uint32_t grid,
                                hipStream_t st) {
-    if (rs.vt != 1) return hipErrorInvalidValue;
 #define CALL_H(V, L_, C_) launch_bf_f16_final_t<V, L_, C_>(a, f, grid, st)
-    GF_DISPATCH_VT(1, CALL_H);
+    if (rs.vt == 1) GF_DISPATCH_VT(1, CALL_H);
+    if (rs.vt == 0) GF_DISPATCH_VT(0, CALL_H);
 #undef CALL_H
     return hipErrorInvalidValue;
 }

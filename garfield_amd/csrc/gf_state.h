@@ -187,11 +187,12 @@ struct gf_index {
     // [0, 255], D a multiple of 64 up to 256): int8 tiles and norms.
     bool i8 = false;
     DevBuf<int8_t> vt;
-    // Binary16 rows with sub-cells (D a multiple of 32): the fp16 MFMA brute
-    // force, with |x|^2 per row and the largest |x| over the index.
-    bool h16 = false;
-    DevBuf<float> xnorm16;
-    double xmax16 = 0.0;
+    // Float rows with sub-cells (binary16 or fp32, shapes of
+    // bf_float_supported) and no int8 route: the MFMA brute force of float
+    // rows, with |x|^2 per row and the largest |x| over the index.
+    bool hf = false;
+    DevBuf<float> xnormf;
+    double xmaxf = 0.0;
     DevBuf<int32_t> tnorm;
     int ncu = 0;
     int wclk_khz = 100000;   // rate of the device wall clock the search's timestamps read
@@ -250,7 +251,7 @@ struct gf_batch {
     DevBuf<float> qf32, qnorm, lo, hi, cdist, out_dist;
     DevBuf<uint16_t> q16, q16v;
     DevBuf<float> qi8q;   // GF_VEC_I8Q: query rows [c | s], c_d = fma(s_d, z_d, q_d)
-    DevBuf<float> qn16, heps;   // binary16 rows: |q|^2 of the binary16 query, bound of |d' - d|
+    DevBuf<float> qnf, heps;   // float MFMA brute force: |q|^2 of the query as the rows hold it, bound of |d' - d|
     DevBuf<uint32_t> hover;     // fp16 brute force: queries whose kept keys may miss a candidate
     DevBuf<uint32_t> cells, counts, little, selcount, cellq, ccount, cstart, cfill, topk;
     DevBuf<uint32_t> out_ids, counters, sched, entry, gbound;

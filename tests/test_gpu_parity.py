@@ -290,14 +290,26 @@ def test_recall_against_ground_truth(world32):
 
 @pytest.mark.parametrize("L,prefilter", [(32, 0.0), (100, 0.0), (64, 0.01), (64, 1.0)])
 def test_gaussian_parity(world_gauss, L, prefilter):
-    """Non-integer 96-d data: canonical fp32 summation order, gather brute force, 3 attributes."""
+    """Non-integer 96-d data: canonical fp32 summation order, the fp32 MFMA
+    brute force with its exact re-rank, 3 attributes."""
     cfg, ix = world_gauss
     _print_case("gauss", L=L, prefilter=prefilter)
     ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, L, prefilter=prefilter)
     _assert_same(ids, dists, ctr, oids, odist, octr, st)
-    assert st.bf_mfma == 0
+    assert st.bf_mfma == (2 if st.q_bruteforce else 0)
     if prefilter == 1.0:
         assert st.q_traverse == 0
+
+
+@pytest.mark.parametrize("K", [5, 10, 16])
+def test_f32_mfma_bruteforce(world_gauss, K):
+    """fp32 rows (96-d, six chunks of four fp32 MFMA k-steps): the float
+    MFMA route for K <= 10, the gather kernel beyond; bit-exact either way."""
+    cfg, ix = world_gauss
+    _print_case("f32-bf", K=K)
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, 32, prefilter=1.0, K=K)
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+    assert st.q_bruteforce > 0 and st.bf_mfma == (2 if K <= 10 else 0)
 
 
 @pytest.mark.parametrize("L,prefilter", [(32, 0.0), (100, 0.0), (64, 0.01), (64, 1.0)])
