@@ -74,6 +74,9 @@ def main():
     ap.add_argument("--traverse-L", type=int, default=100)
     ap.add_argument("--channels", default="1,2",
                     help="traversals swept: 1 cell-by-cell (gf_search), 2 dual-channel (gf_search_dual)")
+    ap.add_argument("--rows", choices=["auto", "f32", "u8", "f16"], default="auto",
+                    help="row storage of the resident index (auto: f16 for c4, else f32; u8 is exact for the "
+                         "integer-valued configs C1 and C2)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="after the run, stream this many MiB through y = x + 1 (fp32) three times: a kernel "
                          "of known traffic (reads and writes that many bytes) to scale rocprofv3's "
@@ -115,7 +118,11 @@ def main():
     metric = {"c3": "QPS at recall@10≥0.95, 1M×96 fp32, 3-attr range filter, 1 MI355X",
               "c4": "QPS at recall@10≥0.95, 1M×768 fp16, 2-attr range filter, 1 MI355X"}.get(args.config, METRIC)
     floatcfg = args.config in ("c3", "c4")
-    vec_dtype = gf.VEC_F16 if args.config == "c4" else gf.VEC_F32
+    # C1 / C2 hold integers in [0, 255]: u8 rows (--rows u8) give the same
+    # distances as fp32 rows bit for bit (every partial sum is an integer
+    # below 2^24) at a quarter of the bytes per row gather
+    rows = args.rows if args.rows != "auto" else ("f16" if args.config == "c4" else "f32")
+    vec_dtype = {"f32": gf.VEC_F32, "u8": gf.VEC_U8, "f16": gf.VEC_F16}[rows]
     N, D = cfg["vectors"].shape
     Q = cfg["queries"].shape[0]
     log(f"data generated N={N} D={D} Q={Q} ({time.time() - t0:.1f}s)")
@@ -304,8 +311,8 @@ def main():
         ms_t = tacc["tr"] / tsteps
         gbs = tacc["btr"] / tsteps / (ms_t / 1e3) / 1e9 if ms_t > 0 else 0.0
         tkern = "k_traverse_dual" if tch == 2 else "k_traverse"
-        tr = traffic.get(f"{tkern}@{tpf}:{tL}")
-        trav = {"bound": "hbm", "kernel": tkern, "channels": tch, "prefilter": tpf, "L": tL,
+        tr = traffic.get(f"{tkern}@{tpf}:{tL}" + ("" if rows == "f32" else f":{rows}"))
+        trav = {"bound": "hbm", "kernel": tkern, "rows": rows, "channels": tch, "prefilter": tpf, "L": tL,
                 "recall_at_10": round(recall(tids)[1], 4), "reaches_target": trec is not None,
                 "qps": round(Q * tsteps / tacc["elapsed"], 1), "queries_traversed": stt.q_traverse,
                 "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -344,6 +351,7 @@ def main():
                       else ("dual-channel" if bch == 2 else "cell-by-cell") +
                       " graph traversal (queries at or below the prefilter selectivity to filtered brute force)"),
             "channels": bch,
+            "rows": rows,
             "N": N, "D": D, "Q": Q, "K": 10, "L": L,
             "prefilter": pf, "postfilter": args.postfilter, "f2h_factor": 1.0, "degree": cfg["R"],
             "graph": args.graph,
