@@ -21,9 +21,6 @@ _RECALL = {}
 
 @pytest.fixture(scope="module")
 def c1_world():
-    import torch
-    if not torch.cuda.is_available():
-        pytest.skip("needs a GPU")
     from oracle import oracle as orc
     cfg = synth.config_small()
     assert cfg["vectors"].shape == (100_000, 128) and cfg["queries"].shape[0] == 1000
