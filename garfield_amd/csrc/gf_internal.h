@@ -257,9 +257,9 @@ struct BfFinalArgs {
     const uint32_t* bfq;       // schedule
     const uint32_t* srange;    // device [begin, end) of the brute-force queries in bfq
     const uint32_t* part_off;  // per query: first pair (partial area = pairs * K keys)
-    const uint32_t* pcnt;      // keys appended for each query
+    uint32_t* pcnt;            // keys appended for each query (bound_only: reset to the kept keys)
     const uint32_t* ok;
-    const uint64_t* part;
+    uint64_t* part;            // bound_only: each query's area compacted to its K smallest keys
     const uint32_t* counts;
     const uint32_t* cells;
     const uint32_t* offset;

@@ -3328,7 +3328,7 @@ __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
     const uint32_t q = p.bfq[si];
     const uint32_t K = p.K;
     const uint32_t n = p.pcnt[q];
-    const uint64_t* part = p.part + size_t(p.part_off[q]) * K;
+    uint64_t* part = p.part + size_t(p.part_off[q]) * K;
     // The query's final bound: some item held K keys within it, so no key
     // beyond it reaches the top K.
     const uint32_t g = p.gbound ? p.gbound[q] : 0xFFFFFFFFu;
@@ -3358,6 +3358,15 @@ __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
     if (p.bound_only) {
         const uint64_t t_k = readlane64(top, K - 1);
         if (lane == 0 && t_k != kKeySent && uint32_t(t_k >> 32) < g) p.gbound[q] = uint32_t(t_k >> 32);
+        // The K smallest keys so far stand for every key read here: the next
+        // merge reads them and the keys appended after them (the K smallest
+        // of the union are the K smallest of all).  Every key read above was
+        // consumed before these writes (top depends on all of them).
+        const uint32_t nt = uint32_t(__popcll(ballot(lane < K && top != kKeySent)));
+        if (nt < n) {
+            if (lane < nt) part[lane] = top;
+            if (lane == 0) p.pcnt[q] = nt;
+        }
         return;
     }
     if (lane < K) {
