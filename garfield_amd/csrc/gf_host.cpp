@@ -1190,25 +1190,25 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     const bool ids_direct = page_locked(ids), dist_direct = page_locked(dists);
     uint32_t* ids_dst = ids_direct ? ids : b->h_ids.p;
     float* dist_dst = dist_direct ? dists : b->h_dist.p;
-    auto enqueue_copies = [&]() {
+    // zero_stats: the sums start from zero here (in the whole stage,
+    // k_reset_results has zeroed them)
+    auto enqueue_copies = [&](bool zero_stats) {
         if (stats) {
-            GF_HIP(gf::launch_zero_u32(reinterpret_cast<uint32_t*>(b->stats.p), 32, st));
+            if (zero_stats) GF_HIP(gf::launch_zero_u32(reinterpret_cast<uint32_t*>(b->stats.p), 32, st));
             gf::StatsArgs sa2{};
             sa2.Q = Q; sa2.NS = sched_bf ? NS : 0; sa2.counters = b->counters.p;
             sa2.bcnt = sched_bf ? b->bcnt.p : nullptr;
             sa2.bin = b->bin.p; sa2.split = b->qcap != 0; sa2.sseed = b->qcap ? b->scnt.p : nullptr;
             sa2.ssize = ix->ssize.p; sa2.stile = ix->stile.p; sa2.out = b->stats.p;
             GF_HIP(gf::launch_stats(sa2, st));
-            GF_HIP(hipMemcpyAsync(b->h_stats.p, b->stats.p, 16 * sizeof(unsigned long long), hipMemcpyDeviceToHost,
-                                  st));
         }
-        GF_HIP(hipMemcpyAsync(b->h_tot.p, tot, 24 * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-        GF_HIP(hipMemcpyAsync(b->h_stamps.p, b->stamps.p, 8 * sizeof(uint64_t), hipMemcpyDeviceToHost, st));
+        GF_HIP(gf::launch_gather_meta(stats ? b->stats.p : nullptr, tot, b->stamps.p, b->h_stats.p, b->h_tot.p,
+                                      b->h_stamps.p, st));
         GF_HIP(hipMemcpyAsync(ids_dst, b->out_ids.p, nr * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
         if (dists) GF_HIP(hipMemcpyAsync(dist_dst, b->out_dist.p, nr * sizeof(float), hipMemcpyDeviceToHost, st));
     };
     auto enqueue_tail = [&]() {
-        enqueue_copies();
+        enqueue_copies(true);
         GF_HIP(hipStreamSynchronize(st));
     };
     // The whole stage, schedule to copies: no allocation, no host wait.
@@ -1219,7 +1219,8 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         sa.sched = b->sched.p; sa.tot = tot + 8; sa.ranges = tot + 12;
         sa.full = ix->FD ? 1u : 0u;
         sa.franges = ix->FD ? tot + 16 : nullptr;
-        GF_HIP(gf::launch_reset_results(Q, K, b->out_ids.p, b->out_dist.p, b->counters.p, st));
+        GF_HIP(gf::launch_reset_results(Q, K, b->out_ids.p, b->out_dist.p, b->counters.p, st,
+                                        stats ? reinterpret_cast<uint32_t*>(b->stats.p) : nullptr, stats ? 32u : 0u));
         GF_HIP(gf::launch_sched(sa, st));
         GF_HIP(gf::launch_stamp(stamp + 0, st));
         gf::TravArgs at = a;
@@ -1237,7 +1238,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
             GF_HIP(gf::launch_bruteforce(ix->rs, ab, Q, st));
         }
         GF_HIP(gf::launch_stamp(stamp + 2, st));
-        enqueue_copies();
+        enqueue_copies(false);
     };
     // From a batch's second search on, the stage runs as a HIP graph,
     // captured once per layout (buffers, options, route) and replayed:

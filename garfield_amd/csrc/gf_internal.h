@@ -457,7 +457,12 @@ hipError_t launch_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_
 // Also zeroes scnt (NS entries) and *nseed when given.
 hipError_t launch_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t* gbound, hipStream_t st,
                           uint32_t NS = 0, uint32_t* scnt = nullptr, uint32_t* nseed = nullptr);
-hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, hipStream_t st);
+// Also zeroes z[0, nz) (a search's statistics sums, for one kernel less).
+hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, hipStream_t st,
+                                uint32_t* z = nullptr, uint32_t nz = 0);
+// stats (16, optional), tot (24) and stamps (8) to page-locked host buffers.
+hipError_t launch_gather_meta(const unsigned long long* stats, const uint32_t* tot, const uint64_t* stamps,
+                              unsigned long long* h_stats, uint32_t* h_tot, uint64_t* h_stamps, hipStream_t st);
 hipError_t launch_zero_u32(uint32_t* x, uint32_t n, hipStream_t st);   // a kernel, so that it can sit in a graph
 hipError_t launch_stamp(uint64_t* t, hipStream_t st);                    // *t = device wall clock when it runs
 // need: 2 * nbatch entries, the need flags, then the active queries per batch

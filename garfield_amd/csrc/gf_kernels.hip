@@ -1723,10 +1723,23 @@ __global__ void k_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t*
 }
 
 // Sentinel results and zero counters for a batch's searches.
-__global__ void k_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr) {
+__global__ void k_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, uint32_t* z,
+                                uint32_t nz) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < Q * K) { ids[i] = GF_NO_RESULT; dist[i] = __int_as_float(0x7F800000); }
     if (i < Q * GF_NCOUNTERS) ctr[i] = 0;
+    if (i < nz) z[i] = 0;
+}
+
+// A search's small host-side outputs in one kernel instead of three copies:
+// the statistics sums (optional), the schedule totals and the timestamps,
+// written to page-locked host memory.
+__global__ void k_gather_meta(const unsigned long long* stats, const uint32_t* tot, const uint64_t* stamps,
+                              unsigned long long* h_stats, uint32_t* h_tot, uint64_t* h_stamps) {
+    const uint32_t t = threadIdx.x;
+    if (stats && t < 16u) h_stats[t] = stats[t];
+    if (t < 24u) h_tot[t] = tot[t];
+    if (t < 8u) h_stamps[t] = stamps[t];
 }
 
 // What each batch of a streamed plan must do for this query batch (one
@@ -4303,9 +4316,17 @@ hipError_t launch_zero_u32(uint32_t* x, uint32_t n, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, hipStream_t st) {
-    const uint32_t n = Q * (K > GF_NCOUNTERS ? K : GF_NCOUNTERS);
-    hipLaunchKernelGGL(k_reset_results, dim3((n + 255) / 256), dim3(256), 0, st, Q, K, ids, dist, ctr);
+hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, hipStream_t st,
+                                uint32_t* z, uint32_t nz) {
+    uint32_t n = Q * (K > GF_NCOUNTERS ? K : GF_NCOUNTERS);
+    n = n > nz ? n : nz;
+    hipLaunchKernelGGL(k_reset_results, dim3((n + 255) / 256), dim3(256), 0, st, Q, K, ids, dist, ctr, z, nz);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_meta(const unsigned long long* stats, const uint32_t* tot, const uint64_t* stamps,
+                              unsigned long long* h_stats, uint32_t* h_tot, uint64_t* h_stamps, hipStream_t st) {
+    hipLaunchKernelGGL(k_gather_meta, dim3(1), dim3(64), 0, st, stats, tot, stamps, h_stats, h_tot, h_stamps);
     return hipGetLastError();
 }
 
