@@ -462,6 +462,7 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
             std::vector<uint32_t> ent(R), entf(std::max<uint32_t>(ix.FD, 1));
             gf::entry_points_pair(N - (P - 1) * avg, R, N, ix.FD, ent.data(), entf.data());
             ix.entry_ref.upload(ent);
+            ++ix.entry_gen;
             if (ix.FD) {
                 std::vector<uint32_t> rowof(N);
                 for (uint32_t r = 0; r < N; ++r) rowof[gidx[r]] = r;
@@ -928,15 +929,25 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     const uint32_t nent = channels == 2 ? L : R;
     if (opts->entry_points) {
         b->entry.upload(opts->entry_points, nent);
+        b->entry_src = nullptr;
     } else {
         DevBuf<uint32_t>& ref = channels == 2 ? ix->entry_dual : ix->entry_ref;
         if (ref.n != nent) {
             std::vector<uint32_t> ent(nent);
             entry_points_ref(ix->N, ix->P, nent, ent.data());
             ref.upload(ent);
+            ++ix->entry_gen;
         }
-        if (b->entry.n < nent) b->entry.alloc(nent);
-        GF_HIP(hipMemcpyAsync(b->entry.p, ref.p, nent * sizeof(uint32_t), hipMemcpyDeviceToDevice, st));
+        if (b->entry.n < nent) {
+            b->entry.alloc(nent);
+            b->entry_src = nullptr;
+        }
+        if (b->entry_src != ref.p || b->entry_src_n != nent || b->entry_src_gen != ix->entry_gen) {
+            GF_HIP(hipMemcpyAsync(b->entry.p, ref.p, nent * sizeof(uint32_t), hipMemcpyDeviceToDevice, st));
+            b->entry_src = ref.p;
+            b->entry_src_n = nent;
+            b->entry_src_gen = ix->entry_gen;
+        }
     }
     if (channels == 2 && ix->prow.n != ix->N) {
         ix->prow.alloc(ix->N);

@@ -164,6 +164,7 @@ struct gf_index {
     DevBuf<uint32_t> graph, cross, offset, gidx, lrow, grid, doff, hist;
     DevBuf<uint32_t> entry_ref;   // the reference's entry-point draw (resident index: made when it is built)
     DevBuf<uint32_t> entry_dual;  // the same draw of L entries for the dual-channel traversal
+    uint32_t entry_gen = 0;       // bumped whenever entry_ref or entry_dual is (re)written
     DevBuf<uint32_t> prow;        // point id -> row (dual-channel traversal, made at its first search)
     // Full-graph route (P <= 64): every row's FE edges into each cell (FD =
     // FE * P rows per row) and the FD entry rows of the reference's second draw.
@@ -255,6 +256,10 @@ struct gf_batch {
     DevBuf<uint32_t> hover;     // fp16 brute force: queries whose kept keys may miss a candidate
     DevBuf<uint32_t> cells, counts, little, selcount, cellq, ccount, cstart, cfill, topk;
     DevBuf<uint32_t> out_ids, counters, sched, entry, gbound;
+    // What entry holds when it is a copy of the index's draw (source buffer,
+    // count, generation), so that a search with the same draw skips the copy.
+    const uint32_t* entry_src = nullptr;
+    uint32_t entry_src_n = 0, entry_src_gen = 0;
     // Per (query, cell) flags, 1 = selected | 2 = little: written by the
     // arithmetic-grid stage A, else derived from the cell lists on use.
     DevBuf<uint8_t> flags;

@@ -471,6 +471,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     if (o.entry_points) std::copy(o.entry_points, o.entry_points + R, ent.begin());
     else entry_points_draw(std::max(S.min_cell, 1u), 10 * L, R, ent.data());
     b.entry.upload(ent);
+    b.entry_src = nullptr;
 
     if (!b.flags_ready) {
         if (b.flags.n < size_t(Q) * P) b.flags.alloc(size_t(Q) * P);
