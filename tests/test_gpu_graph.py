@@ -106,3 +106,52 @@ def test_graph_replay_into_page_locked_arrays(monkeypatch, world_sub2):
     finally:
         b.close()
         dev.close()
+
+
+def test_reused_batch_switches_entries_and_channels(world32):
+    """One batch searched with the index's entry draw, the dual-channel
+    traversal (its own draw of L entries), caller-given entry points and the
+    draw again, in that order and replayed: every search equals the same
+    search on a fresh batch (ids, distances, counters, statistics sums), so a
+    skipped entry-point copy never leaves stale entries behind."""
+    import garfield_amd as gf
+    cfg, ix = world32
+    lo, hi = cfg["lo"].astype(np.float32), cfg["hi"].astype(np.float32)
+    dev = synth.open_device_index(ix)
+    N, P, R = ix["vectors"].shape[0], ix["P"], ix["R"]
+    rng = np.random.default_rng(5)
+    own = rng.integers(0, 10**6, R).astype(np.uint32)
+    plan = [dict(L=64, channels=1), dict(L=33, channels=2), dict(L=64, channels=1, entry_points=own),
+            dict(L=64, channels=1), dict(L=33, channels=2), dict(L=64, channels=1)]
+
+    def fresh(kw):
+        b = dev.batch(cfg["queries"], lo, hi)
+        try:
+            b.mark_cells(0.0)
+            b.order_cells(4)
+            ids, d, st = b.search(K=10, rl=10, **kw)
+            return ids, d, b.get_counters(), (st.n_expand, st.n_dist, st.q_traverse, st.q_bruteforce)
+        finally:
+            b.close()
+
+    want = [fresh(kw) for kw in plan]
+    b = dev.batch(cfg["queries"], lo, hi)
+    try:
+        b.mark_cells(0.0)
+        b.order_cells(4)
+        for rep in range(2):
+            for i, kw in enumerate(plan):
+                _print_case("reuse", rep=rep, step=i, L=kw["L"], channels=kw["channels"])
+                ids, d, st = b.search(K=10, rl=10, **kw)
+                w = want[i]
+                assert np.array_equal(ids, w[0]), (rep, i)
+                assert np.array_equal(d.view(np.uint32), w[1].view(np.uint32)), (rep, i)
+                assert np.array_equal(b.get_counters(), w[2]), (rep, i)
+                assert (st.n_expand, st.n_dist, st.q_traverse, st.q_bruteforce) == w[3], (rep, i)
+    finally:
+        b.close()
+        dev.close()
+    # the caller's entries and the draw give different trajectories, so the
+    # comparison above would see a stale copy
+    assert not np.array_equal(want[2][2], want[3][2])
+    assert gf.entry_points(N, P, R).shape == (R,)
