@@ -33,10 +33,46 @@ HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POP/s
 FP16_PEAK_TFLOPS = 2500.0 # MI355X dense fp16 MFMA, 2.5 PFLOP/s
 FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA
+# The result line is read back from the tail of the run's combined output,
+# which holds about 16 KB: the line and everything logged to stderr must fit.
+MAX_LINE_BYTES = 6000
+DEFAULT_CURVES = os.path.join("gpurun_out", "bench_curves.json")
+
+VERBOSE = False
 
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def vlog(*a):
+    """Per-point progress (every L of a sweep): only with --verbose, so the
+    default run's stderr stays a few KB."""
+    if VERBOSE:
+        log(*a)
+
+
+def result_line(out):
+    """The one stdout JSON line.  Raises if it would not fit the tail the
+    driver parses (bulky per-L curves belong in the side file)."""
+    s = json.dumps(out, separators=(",", ":"))
+    if len(s.encode()) > MAX_LINE_BYTES:
+        raise ValueError(f"result line is {len(s.encode())} bytes (> {MAX_LINE_BYTES}); "
+                         f"largest keys: {sorted(out, key=lambda k: -len(json.dumps(out[k])))[:3]}")
+    return s
+
+
+def write_curves(path, curves, meta):
+    """Full recall / QPS sweeps, keyed like the operating points, to a side
+    file (created with its folder)."""
+    if not path:
+        return
+    d = os.path.dirname(path)
+    if d:
+        os.makedirs(d, exist_ok=True)
+    with open(path, "w") as f:
+        json.dump({"meta": meta, "curves": curves}, f)
+    log(f"sweep curves written to {path}")
 
 
 def main():
@@ -81,7 +117,12 @@ def main():
                     help="after the run, stream this many MiB through y = x + 1 (fp32) three times: a kernel "
                          "of known traffic (reads and writes that many bytes) to scale rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--curves-out", default=DEFAULT_CURVES,
+                    help="file for the full per-L sweep curves ('' = do not write)")
+    ap.add_argument("--verbose", action="store_true", help="log every point of the sweeps to stderr")
     args = ap.parse_args()
+    global VERBOSE
+    VERBOSE = args.verbose
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the query path shards over "
               "queries with no exchange between GPUs", file=sys.stderr)
@@ -218,11 +259,15 @@ def main():
                           "ms_bruteforce": round(st.ms_bruteforce, 3), "traverse_GBs": round(gbs, 1),
                           "traverse_frac": round(gbs / HBM_PEAK_GBS, 4), "q_traverse": st.q_traverse,
                           "q_bruteforce": st.q_bruteforce})
-            log(f"{'dual ' if ch == 2 else ''}prefilter={pf} L={L}: recall={tie:.4f} (strict {strict:.4f}) step={wall * 1e3:.1f}ms "
-                f"trav={st.ms_traverse:.1f}ms ({gbs:.0f} GB/s) bf={st.ms_bruteforce:.1f}ms A={ms_a:.2f}ms "
-                f"B={ms_b:.2f}ms q_trav={st.q_traverse} q_bf={st.q_bruteforce}")
+            vlog(f"{'dual ' if ch == 2 else ''}prefilter={pf} L={L}: recall={tie:.4f} (strict {strict:.4f}) step={wall * 1e3:.1f}ms "
+                 f"trav={st.ms_traverse:.1f}ms ({gbs:.0f} GB/s) bf={st.ms_bruteforce:.1f}ms A={ms_a:.2f}ms "
+                 f"B={ms_b:.2f}ms q_trav={st.q_traverse} q_bf={st.q_bruteforce}")
         curves[("dual:" if ch == 2 else "") + str(pf)] = curve
         reach = [c for c in curve if c["recall"] >= args.recall]
+        sel = [c for c in curve if c["L"] in (100, 600, 1100, 1700)]
+        log(f"sweep channels={ch} prefilter={pf}: " +
+            " ".join(f"L{c['L']}:{c['recall']:.3f}@{c['traverse_frac']:.2f}HBM" for c in sel) +
+            (f"; target at L={reach[0]['L']}" if reach else "; target not reached"))
         if reach:
             c = reach[0]
             candidates.append(dict(prefilter=pf, L=c["L"], recall=c["recall"], strict=c["recall_strict"],
@@ -360,16 +405,18 @@ def main():
             "ms_stage_a": round(ms_a_sum / K, 3), "ms_stage_b": round(ms_b_sum / K, 3),
             "ms_traverse": round(ms_tr / K, 3), "ms_bruteforce": round(ms_bf / K, 3),
             "q_traverse": last.q_traverse, "q_bruteforce": last.q_bruteforce, "q_empty": last.q_empty,
-            "candidates": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in c.items()}
-                           for c in candidates],
+            "candidates": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in c.items()
+                            if k != "strict"} for c in candidates],
+            "curves_file": args.curves_out or None,
         },
         "roofline": roofline,
         "traverse_operating_point": trav,
-        "traverse_curve": curves,
         "cpu_baseline": cpu,
         "cpu_baseline_traverse": cpu_trav,
     }
-    print(json.dumps(out), flush=True)
+    write_curves(args.curves_out, curves, {"config": args.config, "graph": args.graph, "rows": rows,
+                                           "recall_target": args.recall, "Q": Q})
+    print(result_line(out), flush=True)
     if args.calib_copy_mb:
         n = args.calib_copy_mb * (1 << 20) // 4
         x = torch.zeros(n, dtype=torch.float32, device="cuda")
@@ -491,7 +538,7 @@ def build_bench(args):
                      "traffic": None, "ms_per_launch": round(ms_cross, 4)},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(out), flush=True)
+    print(result_line(out), flush=True)
 
 
 def stream_bench(args):
@@ -572,7 +619,7 @@ def stream_bench(args):
             ids, st, ms_a = step(thr, L)
             wall = time.perf_counter() - t
             strict, tie = recall(ids)
-            log(f"threshold={thr} L={L}: recall={tie:.4f} step={wall * 1e3:.1f}ms total={st.ms_total:.1f}ms "
+            vlog(f"threshold={thr} L={L}: recall={tie:.4f} step={wall * 1e3:.1f}ms total={st.ms_total:.1f}ms "
                 f"h2d={st.ms_h2d:.1f}ms ({st.bytes_h2d / max(st.ms_h2d, 1e-9) / 1e6:.1f} GB/s) "
                 f"trav={st.ms_traverse:.1f}ms bf={st.ms_bruteforce:.1f}ms")
             if tie >= args.recall or args.L:
@@ -670,7 +717,7 @@ def stream_bench(args):
                               "ms_per_launch": round(acc["tr"] / K, 4)},
         "cpu_baseline": None,
     }
-    print(json.dumps(out), flush=True)
+    print(result_line(out), flush=True)
 
 
 def cpu_baseline(cfg, ix, batch, L, prefilter, args, channels=1, f16=False):
@@ -715,7 +762,10 @@ def cpu_baseline(cfg, ix, batch, L, prefilter, args, channels=1, f16=False):
             "host_cpu": host_cpu_model(), "host_nproc": os.cpu_count(),
             "sample": f"{n} random queries of the same batch ({routed} on the brute force; same cells, routing, "
                       f"L={L}, prefilter={prefilter}), search stage only (stages A/B not timed), OpenMP over "
-                      f"queries on {threads} threads (the GPU box's host-core share for one GPU)"}
+                      f"queries on {threads} threads (the GPU box's host-core share for one GPU)",
+            "note": "the oracle: plain C++ (-O3 -march=x86-64-v3 -ffp-contract=off, no hand vectorisation, "
+                    "one query per thread), a checker rather than an optimised CPU index, so the GPU/CPU ratio "
+                    "is not a measure of kernel quality"}
 
 
 def host_cpu_model():

@@ -169,6 +169,31 @@ def _opts(degree, f2h_factor, vec_dtype, hist_contiguous, device, ref_ties=False
                      hist_contiguous=int(hist_contiguous), device=device, ref_ties=int(ref_ties))
 
 
+def _out_arrays(out, Q, K):
+    """Result arrays for a search: fresh ones, or the caller's (ids, dists),
+    checked to be C-contiguous (Q, K) uint32 and float32, since the library
+    writes Q * K * 4 bytes into each."""
+    if out is None:
+        return np.empty((Q, K), np.uint32), np.empty((Q, K), np.float32)
+    ids, dists = out
+    for arr, dt in ((ids, np.uint32), (dists, np.float32)):
+        if (not isinstance(arr, np.ndarray) or arr.shape != (Q, K) or arr.dtype != dt
+                or not arr.flags.c_contiguous or not arr.flags.writeable):
+            raise ValueError(f"out arrays must be writeable C-contiguous ({Q}, {K}) uint32 and float32")
+    return ids, dists
+
+
+def _entry_arg(entry_points, n, what):
+    """The caller's entry-point draw, which the library reads n ids from
+    (R for a cell-by-cell search, L for a dual-channel one)."""
+    if entry_points is None:
+        return None
+    ent = _c(entry_points, np.uint32).reshape(-1)
+    if ent.size != n:
+        raise ValueError(f"entry_points must hold {what} = {n} ids, got {ent.size}")
+    return ent
+
+
 class Index:
     """A GMG index resident on one GPU."""
 
@@ -342,15 +367,9 @@ class Batch:
         reuses them instead of touching fresh pages every call).  channels=2:
         the dual-channel traversal (gf_search_dual; entry_points then holds
         L ids)."""
-        if out is None:
-            ids = np.empty((self.Q, K), np.uint32)
-            dists = np.empty((self.Q, K), np.float32)
-        else:
-            ids, dists = out
-            for arr, dt in ((ids, np.uint32), (dists, np.float32)):
-                if arr.shape != (self.Q, K) or arr.dtype != dt or not arr.flags.c_contiguous:
-                    raise ValueError("out arrays must be C-contiguous (Q, K) uint32 and float32")
-        ent = None if entry_points is None else _c(entry_points, np.uint32)
+        ids, dists = _out_arrays(out, self.Q, K)
+        ent = _entry_arg(entry_points, L if channels == 2 else self.index.R,
+                         "L (dual-channel)" if channels == 2 else "R")
         opts = _SearchOpts(L, K, rl, min(int(postfilter), 0xFFFFFFFF), _ptr(ent))
         st = SearchStats()
         fn = load().gf_search_dual if channels == 2 else load().gf_search
@@ -395,12 +414,8 @@ def search_noalloc(index, queries, lo, hi, prefilter, topc=4, L=64, K=10, rl=10,
     if q.ndim != 2 or q.shape[1] != index.D or lo.shape != (q.shape[0], index.a) or hi.shape != lo.shape:
         raise ValueError("queries must be (Q, D) and lo/hi (Q, a)")
     Q = q.shape[0]
-    if out is None:
-        ids = np.empty((Q, K), np.uint32)
-        dists = np.empty((Q, K), np.float32)
-    else:
-        ids, dists = out
-    ent = None if entry_points is None else _c(entry_points, np.uint32)
+    ids, dists = _out_arrays(out, Q, K)
+    ent = _entry_arg(entry_points, index.R, "R")
     opts = _NoallocOpts(float(prefilter), int(topc),
                         _SearchOpts(L, K, rl, min(int(postfilter), 0xFFFFFFFF), _ptr(ent)))
     _check(load().gf_search_noalloc(index._h, _ptr(q), Q, _ptr(lo), _ptr(hi), C.byref(opts), _ptr(ids),

@@ -269,8 +269,9 @@ gf_status gf_batch_get_counters(const gf_batch* b, uint32_t* counters /*Q*GF_NCO
 
 /* One query batch through stages A, B and C in one call that allocates
  * nothing.  No counterpart in the reference: it is for callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc).  It runs the kernels of gf_batch_create,
+ * allocate device memory (tight serving loops, harnesses that forbid
+ * hipMalloc).  The call is synchronous (it copies the host arrays and waits
+ * for its stream), so it cannot be recorded under HIP graph capture.  It runs the kernels of gf_batch_create,
  * gf_mark_cells(prefilter), gf_order_cells(topc) and gf_search(search) on a
  * resident index and returns the same ids and distances; routed queries take
  * the gather brute force, whose results equal the MFMA route's.  Every

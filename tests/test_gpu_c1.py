@@ -73,6 +73,31 @@ def test_c1_dual_channel_parity(c1_world):
     _RECALL[("dual", 128)] = _recall(ids, gt)
 
 
+@pytest.mark.parametrize("channels", [1, 2])
+@pytest.mark.parametrize("prefilter", [0.0, 0.3])
+@pytest.mark.parametrize("L", [600, 1100, 1700])
+def test_c1_operating_point_L_parity(c1_world, L, prefilter, channels):
+    """The list lengths the recall target needs (L = 600-1700), where the
+    kernels run their largest configurations: a 2048- (L = 600) or 4096-slot
+    visited set (L >= 1100), lists past 512 entries and 20-32 KB of LDS per
+    workgroup.  Ids, distances and counters bit for bit against the oracle,
+    which keeps its visited set as an exact set, so a table that filled up
+    (an insert reported as 'seen') would show as a difference.  64 queries of
+    the batch; cells of 6,250 points, larger than L."""
+    cfg, ix, gt = c1_world
+    _print_case("c1-high-L", L=L, prefilter=prefilter, channels=channels, Q=64)
+    ids, dists, ctr, oids, odist, octr, st = _traversal_case(cfg, ix, L, prefilter=prefilter, Q=64,
+                                                             channels=channels)
+    assert st.q_traverse > 0
+    if prefilter == 0.0:
+        assert st.q_traverse == 64
+    _assert_same(ids, dists, ctr, oids, odist, octr, st)
+    # some query expanded more than 512 nodes (counter 0; route 1 is the
+    # cell-by-cell traversal, 4 the dual-channel one), so lists this long ran
+    trav = np.isin(ctr[:, 7], (1, 4))
+    assert ctr[trav, 0].max() > 512
+
+
 def test_c1_recall_grows_with_L(c1_world):
     """Against the CPU ground truth: more candidates give more recall, and the
     dual-channel traversal is not worse than the cell-by-cell one at equal L."""
