@@ -394,9 +394,8 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
         bool ints = ix.sub && ix.vdtype != GF_VEC_F16 && ix.vdtype != GF_VEC_I8Q && D % 64 == 0 && D <= 256;
         for (size_t i = 0; ints && i < v.size(); ++i) ints = v[i] >= 0.0f && v[i] <= 255.0f && v[i] == std::floor(v[i]);
         if (ints) {
-            ix.vt.alloc(size_t(ix.ntile) * (D / 64) * 1024);
-            ix.tnorm.alloc(size_t(ix.ntile) * 32);
-            GF_HIP(gf::launch_tile_i8(vec_f32_dev, false, D, ix.tmeta.p, ix.AW, ix.ntile, ix.vt.p, ix.tnorm.p,
+            ix.trec.alloc(size_t(ix.ntile) * gf::bf_rec_bytes(D, ix.AW));
+            GF_HIP(gf::launch_tile_rec(vec_f32_dev, false, D, ix.tmeta.p, ix.AW, ix.ntile, ix.trec.p,
                                       ix.stream));
             ix.i8 = true;
         }
@@ -1144,7 +1143,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         }
         gf::BfGemmArgs ga{};
         ga.sa = sub_args(*ix);
-        ga.vt = ix->vt.p; ga.tnorm = ix->tnorm.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p;
+        ga.rec = ix->trec.p; ga.q8 = b->q8.p; ga.nq = b->nq.p; ga.lo = b->lo.p;
         ga.hi = b->hi.p; ga.items = b->items.p; ga.nitems = tot + 4; ga.bq = b->bq.p; ga.pcnt = b->pcnt.p;
         ga.part_off = b->part_off.p; ga.part = b->part.p; ga.gbound = b->gbound.p;
         ga.ok = tot + 3;

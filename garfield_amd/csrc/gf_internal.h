@@ -112,7 +112,10 @@ struct SubArgs {
 // are stored shifted by -128 as int8 in the sub-cell tile order, each tile in
 // MFMA operand order: tile t, k-step s holds 64 lanes x 16 bytes, lane l
 // carrying bytes [64 s + 16 (l / 16), +16) of point l % 16.  tnorm holds per
-// tile [-floor(|x'|^2 / 2) x 16][|x'|^2 x 16].
+// tile [-floor(|x'|^2 / 2) x 16][|x'|^2 x 16].  The brute force reads one
+// record per tile (bf_rec_bytes): the D / 64 k-steps, the tile's norms, then
+// its meta (rows, AW attribute words x 16), records back to back in tile
+// order, so consecutive tiles are one contiguous range.
 constexpr uint32_t kBfTile = 16;      // points per tile
 constexpr uint32_t kBfKMax = 16;      // largest K of the MFMA route
 constexpr uint32_t kBfQB = 64;        // queries per work item
@@ -124,10 +127,10 @@ struct BfItem {
     uint32_t tb, te;                   // tiles [tb, te) of the sub-cell
     uint32_t inside;                   // 1: every query's range contains the sub-cell's box
 };
+__host__ __device__ inline uint32_t bf_rec_bytes(uint32_t D, uint32_t AW) { return (D / 64u) * 1024u + 128u + 64u * (1u + AW); }
 struct BfGemmArgs {
     SubArgs sa;
-    const int8_t* vt;          // tiled int8 vectors
-    const int32_t* tnorm;      // per tile norms
+    const uint8_t* rec;        // tile records (bf_rec_bytes each)
     const int8_t* q8;          // Q*D queries shifted by -128
     const int32_t* nq;         // |q - 128|^2
     const float* lo;
@@ -406,6 +409,9 @@ hipError_t launch_bf_i8(const BfGemmArgs& a, uint32_t ncu, hipStream_t st);   //
 hipError_t launch_bf_final(const BfFinalArgs& a, uint32_t grid, hipStream_t st);
 hipError_t launch_tile_i8(const void* vec_cm, bool u8, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
                           int8_t* vt, int32_t* tnorm, hipStream_t st);
+// The brute force's tile records (bf_rec_bytes each) from the same inputs.
+hipError_t launch_tile_rec(const void* vec_cm, bool u8, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
+                           uint8_t* rec, hipStream_t st);
 hipError_t launch_note_bf(const uint32_t* tot, uint32_t* note, hipStream_t st);
 hipError_t launch_subsel(const SubSelArgs& a, hipStream_t st);
 hipError_t launch_bfsched(const BfSchedArgs& a, bool fill, hipStream_t st);

@@ -2677,7 +2677,7 @@ __global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint3
     const uint32_t ns = qcap && scnt ? scnt[s] : 0u;   // seeds: the front of the region
     if (fill && ns) {
         // seed items go to their own list (order is free: each is one
-        // sub-cell), in chunks of stch tiles
+        // sub-cell), in chunks of stch tiles, one wave per item (no padding)
         const uint32_t nc = tile_chunks(stile, s, stch), gs = (ns + kBfQB - 1) / kBfQB;
         const uint32_t t0 = stile[s], t1 = stile[s + 1], step = stch ? stch : (t1 - t0);
         uint32_t k = atomicAdd(nseed, gs * nc);
@@ -2737,17 +2737,223 @@ __global__ void k_note_bf(const uint32_t* tot, uint32_t* note) {
     }
 }
 
+// Per-wave state of the int8 brute force over one work item (a sub-cell's
+// tiles and up to 64 of its queries): lane q owns query q of the item, with
+// its sorted top-K of (distance << 32 | row) keys in registers, its survivor
+// buffer (BUFQ slots) and its accumulator threshold in LDS; B holds the
+// item's queries as four 16-query column tiles (a dead column repeats the
+// first query, whose empty range keeps it from producing survivors).  A lane
+// reserves the buffer slots of its survivors of a tile with one LDS atomic
+// per column tile (at most four per tile, issued together).
+template <int KS, int AW, int KT, uint32_t BUFQ>
+struct BfWave {
+    static constexpr uint32_t DRAIN_AT = BUFQ - 15u;   // one tile adds at most 16 per query
+    uint64_t* buf;
+    uint32_t* cnt;
+    int32_t* stp;
+    uint32_t lane, col, grp, K;
+    bool own_live;
+    uint32_t own_q, own_thr, thr0;   // the item's bound, and the query's bound when the item began
+    int32_t own_nq;
+    uint64_t tk[KT];
+    uint64_t kth;
+    v4i32_t B[4][KS];
+    uint32_t blo[4][AW], bhi[4][AW];
+    int32_t tp[4];
+
+    __device__ __forceinline__ void begin(const BfGemmArgs& p, const BfItem& it, uint32_t cell) {
+        const SubArgs& sa = p.sa;
+        own_live = lane < it.nq;
+        own_q = p.bq[it.qbase + (own_live ? lane : 0u)];
+        own_nq = p.nq[own_q];
+        own_thr = own_live ? __hip_atomic_load(&p.gbound[own_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        thr0 = own_thr;
+#pragma unroll
+        for (int k = 0; k < KT; ++k) tk[k] = kKeySent;
+        kth = kKeySent;
+        wave_fence();
+        cnt[lane] = 0;
+        stp[lane] = own_live ? acc_threshold(own_nq, own_thr) : INT32_MAX;
+        // the owner's packed range bounds, then each column lane takes
+        // those of its four queries (owner lane 16 j + col)
+        uint32_t lw[AW], hw[AW];
+#pragma unroll
+        for (int w = 0; w < AW; ++w) {
+            uint32_t l0 = 65534u, h0 = 65534u, l1 = 0u, h1 = 0u;
+            if (own_live) {
+                const uint32_t d0 = 2u * w, d1 = 2u * w + 1u;
+                range16(p.lo[size_t(own_q) * sa.a + d0], p.hi[size_t(own_q) * sa.a + d0],
+                        sa.abase[cell * sa.a + d0], l0, h0);
+                if (d1 < sa.a)
+                    range16(p.lo[size_t(own_q) * sa.a + d1], p.hi[size_t(own_q) * sa.a + d1],
+                            sa.abase[cell * sa.a + d1], l1, h1);
+            }
+            lw[w] = l0 | (l1 << 16);
+            hw[w] = h0 | (h1 << 16);
+        }
+        wave_fence();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t ql = 16u * j + col;
+            const uint32_t q = p.bq[it.qbase + (ql < it.nq ? ql : 0u)];
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
+                B[j][k] = *reinterpret_cast<const v4i32_t*>(p.q8 + size_t(q) * p.D + k * 64 + grp * 16);
+#pragma unroll
+            for (int w = 0; w < AW; ++w) {
+                blo[j][w] = uint32_t(__shfl(int(lw[w]), int(ql), 64));
+                bhi[j][w] = uint32_t(__shfl(int(hw[w]), int(ql), 64));
+            }
+            tp[j] = stp[ql];
+        }
+    }
+
+    __device__ __forceinline__ void reload_tp() {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) tp[j] = stp[16u * j + col];
+    }
+    // Owner: merge the buffered survivors of its query, publish the new
+    // threshold and lower the query's bound.
+    __device__ __forceinline__ void drain() {
+        wave_fence();
+        const uint32_t n = cnt[lane];
+        if (n) {
+            uint64_t nxt = buf[lane * BUFQ];
+            for (uint32_t e = 0; e < n; ++e) {
+                const uint64_t cur = nxt;
+                if (e + 1 < n) nxt = buf[lane * BUFQ + e + 1];
+                const int32_t d = own_nq + int32_t(uint32_t(cur >> 32));
+                uint64_t c = (uint64_t(uint32_t(d)) << 32) | uint32_t(cur);
+                if (c < kth) {
+#pragma unroll
+                    for (int k = 0; k < KT; ++k) {
+                        const bool lt = c < tk[k];
+                        const uint64_t v = tk[k];
+                        tk[k] = lt ? c : v;
+                        c = lt ? v : c;
+                    }
+#pragma unroll
+                    for (int k = 0; k < KT; ++k)
+                        if (uint32_t(k) == K - 1) kth = tk[k];
+                }
+            }
+            cnt[lane] = 0;
+            if (kth != kKeySent && uint32_t(kth >> 32) < own_thr) {
+                own_thr = uint32_t(kth >> 32);
+                stp[lane] = acc_threshold(own_nq, own_thr);
+            }
+        }
+        wave_fence();
+        reload_tp();
+    }
+    // One tile: A (KS k-steps) and mh (-floor(|x'|^2 / 2) of the lane's four
+    // points) as operands; meta(mn, mr, ma) fetches the tile's |x'|^2, rows
+    // and attribute words for the lane's points when some pair is within its
+    // threshold (about two of a tile's 1024 pairs once thresholds settle).
+    __device__ __forceinline__ void mma(const v4i32_t (&A)[KS], const v4i32_t& mh, v4i32_t (&acc)[4]) const {
+        // k-outer: the four column tiles' MFMAs are independent, so a
+        // dependent MFMA (same accumulator) issues three MFMAs later
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B[j][0], mh, 0, 0, 0);
+#pragma unroll
+        for (int k = 1; k < KS; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[k], B[j][k], acc[j], 0, 0, 0);
+    }
+    template <class Meta>
+    __device__ __forceinline__ void tile(const v4i32_t (&A)[KS], const v4i32_t& mh, Meta meta) {
+        v4i32_t acc[4];
+        mma(A, mh, acc);
+        epilogue(acc, mh, meta);
+    }
+    template <class Meta>
+    __device__ __forceinline__ void epilogue(const v4i32_t (&acc)[4], const v4i32_t& mh, Meta meta) {
+        // Distance first, on the max of each column tile's four rows: jm
+        // has bit j when some lane holds a pair of column tile j within its
+        // query's threshold (about two of a tile's 1024 pairs once settled,
+        // often failing the range test).
+        uint32_t jm = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            jm |= __builtin_amdgcn_ballot_w64(max(max(acc[j][0], acc[j][1]), max(acc[j][2], acc[j][3])) >= tp[j])
+                      ? 1u << j : 0u;
+        if (!jm) return;
+        v4i32_t mn, mr, ma[AW];
+        meta(mn, mr, ma);
+        bool full = false;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (!(jm & (1u << j))) continue;
+            // pairs (j, i) of this lane within the threshold and the range
+            uint32_t okm = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                bool ok = acc[j][i] >= tp[j];
+                const uint32_t x0 = uint32_t(ma[0][i]);
+                ok &= clamp16(x0, blo[j][0], bhi[j][0]) == x0;
+                if (AW > 1) {
+                    const uint32_t x1 = uint32_t(ma[AW - 1][i]);
+                    ok &= clamp16(x1, blo[j][AW - 1], bhi[j][AW - 1]) == x1;
+                }
+                okm |= ok ? 1u << i : 0u;
+            }
+            if (!__builtin_amdgcn_ballot_w64(okm != 0u)) continue;
+            // one LDS atomic reserves this lane's slots; the lane holding
+            // the last reservation sees the query's new count
+            const uint32_t ql = 16u * j + col;
+            uint32_t slot = okm ? atomicAdd(&cnt[ql], uint32_t(__builtin_popcount(okm))) : 0u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (okm & (1u << i)) {
+                    // the owner adds |q'|^2 to |x'|^2 - 2 q'.x' later
+                    const int32_t v = mn[i] - 2 * (acc[j][i] - mh[i]);
+                    buf[ql * BUFQ + slot++] = (uint64_t(uint32_t(v)) << 32) | uint32_t(mr[i]);
+                }
+            full |= okm && slot >= DRAIN_AT;
+        }
+        if (__builtin_amdgcn_ballot_w64(full)) drain();
+    }
+    // End of the item: lower the query's global bound (read at the item's
+    // start: a store inside the tile loop would make the compiler wait for
+    // every load in flight before the next tile's operands) if the item
+    // improved on it, and append the keys within it for the final merge.
+    __device__ __forceinline__ void finish(const BfGemmArgs& p) {
+        drain();
+        if (!own_live) return;
+        const bool lower = own_thr < thr0;
+        if (lower) atomicMin(&p.gbound[own_q], own_thr);
+        uint32_t keep = 0;
+#pragma unroll
+        for (int k = 0; k < KT; ++k)
+            keep += (uint32_t(k) < K && tk[k] != kKeySent && uint32_t(tk[k] >> 32) <= own_thr) ? 1u : 0u;
+        if (keep) {
+            const size_t slot = size_t(p.part_off[own_q]) * K + atomicAdd(&p.pcnt[own_q], keep);
+#pragma unroll
+            for (int k = 0; k < KT; ++k)
+                if (uint32_t(k) < keep) p.part[slot + k] = tk[k];
+        }
+    }
+};
+
+// The MFMA kernel, one wave per item: the seed items (seeds_on), then the
+// launch's range of the item list (irange).  Persistent
+// waves, XCD-aware: workgroups go round-robin to the 8 XCDs and XCD x works
+// through the x-th eighth of the item list (items of one sub-cell are
+// adjacent, so its tiles stay in that XCD's L2).  The operands of tile t + 1
+// are loaded while tile t is computed: the int8 k-steps after tile t's MFMAs
+// have read them, its norms and meta into the other of two register sets.
 template <int KS, int AW, int KT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3 : 2))) void k_bf_i8(BfGemmArgs p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 && KS <= 2 && KT <= 10 ? 3 : 2))) void k_bf_i8(BfGemmArgs p) {
     __shared__ uint64_t s_buf[4][kQB * kBfBufQ];
     __shared__ uint32_t s_cnt[4][kQB];
     __shared__ int32_t s_tp[4][kQB];
-    __shared__ uint32_t s_bnd[4][2 * AW][kQB];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
     const SubArgs& sa = p.sa;
-    // Persistent waves, XCD-aware: workgroups go round-robin to the 8 XCDs and
-    // XCD x works through the x-th eighth of the item list (items of one
-    // sub-cell are adjacent, so its tiles stay in that XCD's L2).
+    const uint32_t RB = bf_rec_bytes(p.D, AW), KB = KS * 1024u;
+    BfWave<KS, AW, KT, kBfBufQ> w;
+    w.buf = s_buf[wave]; w.cnt = s_cnt[wave]; w.stp = s_tp[wave];
+    w.lane = lane; w.col = lane & 15u; w.grp = lane >> 4; w.K = p.K;
+    const uint32_t n_seed = p.sitems && *p.ok && p.seeds_on ? min(*p.nseed, p.nseed_cap) : 0u;
     const uint32_t nwg = gridDim.x, xcd = blockIdx.x & 7u, k8 = blockIdx.x >> 3;
     const uint32_t nwg_x = (nwg - xcd + 7u) >> 3;
     uint32_t i_b = 0, i_e = *p.ok && p.irange != 3u ? *p.nitems : 0u;
@@ -2756,16 +2962,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3
     const uint32_t n_items = i_e - i_b;
     const uint32_t i_lo = i_b + uint32_t(uint64_t(n_items) * xcd / 8u);
     const uint32_t i_hi = i_b + uint32_t(uint64_t(n_items) * (xcd + 1u) / 8u);
-    uint64_t* buf = s_buf[wave];
-    uint32_t* cnt = s_cnt[wave];
-    int32_t* stp = s_tp[wave];
-    const uint32_t K = p.K;
-    const uint32_t col = lane & 15u, grp = lane >> 4;
-    constexpr uint32_t MW = 16u * (1u + AW);
-
-    // Seed items first (strided over every wave of the grid), then the XCD's
-    // range of the item list.
-    const uint32_t n_seed = p.sitems && *p.ok && p.seeds_on ? min(*p.nseed, p.nseed_cap) : 0u;
     uint32_t seed_id = blockIdx.x * 4u + wave, item_id = i_lo + k8 * 4u + wave;
     for (;;) {
         BfItem it;
@@ -2778,220 +2974,52 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 ? 3
         } else {
             break;
         }
-        const uint32_t s = it.sub, cell = sa.scell[s];
-        const uint32_t t0 = it.tb, t1 = it.te;
-
-        // Owner state: lane q owns query q of the block; its sorted top-K of
-        // (distance << 32 | row) keys lives in registers.
-        const bool own_live = lane < it.nq;
-        const uint32_t own_q = p.bq[it.qbase + (own_live ? lane : 0u)];
-        const int32_t own_nq = p.nq[own_q];
-        uint32_t own_thr =
-            own_live ? __hip_atomic_load(&p.gbound[own_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
-        uint64_t tk[KT];
-#pragma unroll
-        for (int k = 0; k < KT; ++k) tk[k] = kKeySent;
-        uint64_t kth = kKeySent;
-        wave_fence();
-        cnt[lane] = 0;
-        stp[lane] = own_live ? acc_threshold(own_nq, own_thr) : INT32_MAX;
-#pragma unroll
-        for (int w = 0; w < AW; ++w) {
-            uint32_t l0 = 65534u, h0 = 65534u, l1 = 0u, h1 = 0u;
-            if (own_live) {
-                const uint32_t d0 = 2u * w, d1 = 2u * w + 1u;
-                range16(p.lo[size_t(own_q) * sa.a + d0], p.hi[size_t(own_q) * sa.a + d0],
-                        sa.abase[cell * sa.a + d0], l0, h0);
-                if (d1 < sa.a)
-                    range16(p.lo[size_t(own_q) * sa.a + d1], p.hi[size_t(own_q) * sa.a + d1],
-                            sa.abase[cell * sa.a + d1], l1, h1);
-            }
-            s_bnd[wave][2 * w][lane] = l0 | (l1 << 16);
-            s_bnd[wave][2 * w + 1][lane] = h0 | (h1 << 16);
-        }
-        wave_fence();
-
-        // Column data: query 16 j + col of the block (a dead column repeats
-        // the first query; its empty range keeps it from producing survivors).
-        v4i32_t B[4][KS];
-        uint32_t blo[4][AW], bhi[4][AW];
-        int32_t tp[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t ql = 16u * j + col;
-            const uint32_t q = p.bq[it.qbase + (ql < it.nq ? ql : 0u)];
-#pragma unroll
-            for (int k = 0; k < KS; ++k)
-                B[j][k] = *reinterpret_cast<const v4i32_t*>(p.q8 + size_t(q) * p.D + k * 64 + grp * 16);
-#pragma unroll
-            for (int w = 0; w < AW; ++w) {
-                blo[j][w] = s_bnd[wave][2 * w][ql];
-                bhi[j][w] = s_bnd[wave][2 * w + 1][ql];
-            }
-            tp[j] = stp[ql];
-        }
-
-        auto reload_tp = [&]() {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) tp[j] = stp[16u * j + col];
-        };
-        auto set_thr = [&](uint32_t thr) {
-            own_thr = thr;
-            stp[lane] = acc_threshold(own_nq, own_thr);
-        };
-        // Owner: merge the buffered survivors of its query, publish the new
-        // threshold and lower the query's global bound.
-        auto drain = [&]() {
-            wave_fence();
-            const uint32_t n = cnt[lane];
-            if (n) {
-                uint64_t nxt = buf[lane * kBfBufQ];
-                for (uint32_t e = 0; e < n; ++e) {
-                    const uint64_t cur = nxt;
-                    if (e + 1 < n) nxt = buf[lane * kBfBufQ + e + 1];
-                    const int32_t d = own_nq + int32_t(uint32_t(cur >> 32));
-                    uint64_t c = (uint64_t(uint32_t(d)) << 32) | uint32_t(cur);
-                    if (c < kth) {
-#pragma unroll
-                        for (int k = 0; k < KT; ++k) {
-                            const bool lt = c < tk[k];
-                            const uint64_t v = tk[k];
-                            tk[k] = lt ? c : v;
-                            c = lt ? v : c;
-                        }
-#pragma unroll
-                        for (int k = 0; k < KT; ++k)
-                            if (uint32_t(k) == K - 1) kth = tk[k];
-                    }
-                }
-                cnt[lane] = 0;
-                if (kth != kKeySent && uint32_t(kth >> 32) < own_thr) set_thr(uint32_t(kth >> 32));
-            }
-            wave_fence();
-            reload_tp();
-        };
-
-        // Operands of tile t + 1 are loaded while tile t is computed: the
-        // int8 tile A after tile t's MFMAs have read it, its norms and meta
-        // into the other of two register sets (M0, M1, alternating), so no
-        // register is copied from one tile to the next.  All loads are buffer
-        // loads from a descriptor based at the item's first tile: the tile
-        // offset is a scalar, the lane's offset a constant.
-        const uint32_t ntile = t1 - t0;
-        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<int8_t*>(p.vt + size_t(t0) * KS * 1024u), 0, ntile * KS * 1024u, 0x00020000);
-        const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<int32_t*>(p.tnorm + size_t(t0) * 32u), 0, ntile * 128u, 0x00020000);
-        const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint32_t*>(sa.tmeta + size_t(t0) * MW), 0, ntile * MW * 4u, 0x00020000);
+        w.begin(p, it, sa.scell[it.sub]);
+        const uint32_t t0 = it.tb, t1 = it.te, ntile = t1 - t0;
+        const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(p.rec + size_t(t0) * RB), 0, ntile * RB, 0x00020000);
         struct TileMeta {
             v4i32_t mh, mn, mr, ma[AW];
         };
         v4i32_t A[KS];
-        auto bload = [](__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-            return __builtin_bit_cast(v4i32_t, __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), 0));
+        auto bload = [&](uint32_t voff, uint32_t soff) __attribute__((always_inline)) {
+            return __builtin_bit_cast(v4i32_t, __builtin_amdgcn_raw_buffer_load_b128(rr, int(voff), int(soff), 0));
         };
-        auto load_a = [&](uint32_t t) {
+        auto load_a = [&](uint32_t t) __attribute__((always_inline)) {
 #pragma unroll
-            for (int k = 0; k < KS; ++k) A[k] = bload(rv, lane * 16u, (t - t0) * KS * 1024u + k * 1024u);
+            for (int k = 0; k < KS; ++k) A[k] = bload(lane * 16u, (t - t0) * RB + k * 1024u);
         };
-        auto load_m = [&](TileMeta& M, uint32_t t) {
-            const uint32_t tt = t - t0;
-            M.mh = bload(rn, 16u * grp, tt * 128u);
-            M.mn = bload(rn, 16u * grp, tt * 128u + 64u);
-            M.mr = bload(rm, 16u * grp, tt * MW * 4u);
+        auto load_m = [&](TileMeta& M, uint32_t t) __attribute__((always_inline)) {
+            const uint32_t o = (t - t0) * RB + KB;
+            M.mh = bload(16u * w.grp, o);
+            M.mn = bload(16u * w.grp, o + 64u);
+            M.mr = bload(16u * w.grp, o + 128u);
 #pragma unroll
-            for (int w = 0; w < AW; ++w) M.ma[w] = bload(rm, 16u * grp, tt * MW * 4u + 64u * (1 + w));
+            for (int a = 0; a < AW; ++a) M.ma[a] = bload(16u * w.grp, o + 128u + 64u * (1 + a));
         };
-        // One tile step, with the range test, or without it for an item
-        // whose queries all contain the sub-cell's box (every point passes).
-        auto step = [&](auto filt, const TileMeta& M, TileMeta& Mn, uint32_t t) {
-            constexpr bool FILTER = decltype(filt)::value;
-            // k-outer: the four column tiles' MFMAs are independent, so a
-            // dependent MFMA (same accumulator) issues three MFMAs later
+        auto step = [&](const TileMeta& M, TileMeta& Mn, uint32_t t) __attribute__((always_inline)) {
             v4i32_t acc[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B[j][0], M.mh, 0, 0, 0);
-#pragma unroll
-            for (int k = 1; k < KS; ++k)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[k], B[j][k], acc[j], 0, 0, 0);
+            w.mma(A, M.mh, acc);
             if (t + 1 < t1) {
                 load_a(t + 1);
                 load_m(Mn, t + 1);
             }
-            // Branch-free test of one (point i, query column j) pair.
-            auto pass = [&](int j, int i) {
-                bool ok = acc[j][i] >= tp[j];
-                if constexpr (FILTER) {
-                    const uint32_t x0 = uint32_t(M.ma[0][i]);
-                    ok &= clamp16(x0, blo[j][0], bhi[j][0]) == x0;
-                    if (AW > 1) {
-                        const uint32_t x1 = uint32_t(M.ma[AW - 1][i]);
-                        ok &= clamp16(x1, blo[j][AW - 1], bhi[j][AW - 1]) == x1;
-                    }
-                }
-                return ok;
-            };
-            // Distance first, on the max of each column's four rows (one
-            // compare per column); the range test only runs for a tile
-            // where some pair is within the threshold.
-            bool anyd = false;
+            w.epilogue(acc, M.mh, [&](v4i32_t& mn, v4i32_t& mr, v4i32_t (&ma)[AW]) __attribute__((always_inline)) {
+                mn = M.mn;
+                mr = M.mr;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                anyd |= max(max(acc[j][0], acc[j][1]), max(acc[j][2], acc[j][3])) >= tp[j];
-            if (!__builtin_amdgcn_ballot_w64(anyd)) return;
-            // Pair positions (j, i) where some lane is within its bound: a
-            // tile step holds about two such pairs among its 1024, so the
-            // range test and the append run for those positions only.
-            bool full = false;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const bool dok = acc[j][i] >= tp[j];
-                    if (!__builtin_amdgcn_ballot_w64(dok)) continue;
-                    if (pass(j, i)) {
-                        // Append: the owner adds |q'|^2 to nx - 2 q'.x' later.
-                        const uint32_t ql = 16u * j + col;
-                        const int32_t v = M.mn[i] - 2 * (acc[j][i] - M.mh[i]);
-                        const uint32_t slot = atomicAdd(&cnt[ql], 1u);
-                        buf[ql * kBfBufQ + slot] = (uint64_t(uint32_t(v)) << 32) | uint32_t(M.mr[i]);
-                        full |= slot + 1u >= kBfDrainAt;
-                    }
-                }
-            if (__builtin_amdgcn_ballot_w64(full)) drain();
+                for (int a = 0; a < AW; ++a) ma[a] = M.ma[a];
+            });
         };
-        auto tiles = [&](auto filt) {
-            TileMeta M0, M1;
-            load_a(t0);
-            load_m(M0, t0);
-            for (uint32_t t = t0; t < t1; t += 2) {
-                step(filt, M0, M1, t);
-                if (t + 1 >= t1) break;
-                step(filt, M1, M0, t + 1);
-            }
-        };
-        if (it.inside) tiles(std::false_type{});
-        else tiles(std::true_type{});
-        drain();
-        if (own_live) {
-            // The query's bound is read at item start and lowered at item end:
-            // device-scope atomics inside the tile loop would stall its loads.
-            if (own_thr != 0xFFFFFFFFu) atomicMin(&p.gbound[own_q], own_thr);
-            // Only keys within the query's bound can reach its final top-K.
-            uint32_t keep = 0;
-#pragma unroll
-            for (int k = 0; k < KT; ++k)
-                keep += (uint32_t(k) < K && tk[k] != kKeySent && uint32_t(tk[k] >> 32) <= own_thr) ? 1u : 0u;
-            if (keep) {
-                const size_t slot = size_t(p.part_off[own_q]) * K + atomicAdd(&p.pcnt[own_q], keep);
-#pragma unroll
-                for (int k = 0; k < KT; ++k)
-                    if (uint32_t(k) < keep) p.part[slot + k] = tk[k];
-            }
+        TileMeta M0, M1;
+        load_a(t0);
+        load_m(M0, t0);
+        for (uint32_t t = t0; t < t1; t += 2) {
+            step(M0, M1, t);
+            if (t + 1 >= t1) break;
+            step(M1, M0, t + 1);
         }
+        w.finish(p);
     }
 }
 
@@ -3412,12 +3440,17 @@ __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
 // points are all zero).
 template <typename T>
 __global__ __launch_bounds__(64) void k_tile_i8(const T* vec, uint32_t D, const uint32_t* tmeta, uint32_t AW,
-                                               int8_t* vt, int32_t* tnorm) {
+                                               int8_t* vt, size_t vstride, int32_t* tnorm, size_t nstride,
+                                               uint32_t* mdst, size_t mstride) {
+    // Tile t's k-steps at vt + t vstride, its norms at tnorm + t nstride and,
+    // with mdst, a copy of its meta (16 (1 + AW) words) at mdst + t mstride.
     const uint32_t t = blockIdx.x, lane = lane_id();
     const uint32_t col = lane & 15u;
-    const uint32_t row = tmeta[size_t(t) * 16u * (1u + AW) + col];
+    const uint32_t MW = 16u * (1u + AW);
+    const uint32_t row = tmeta[size_t(t) * MW + col];
     const bool valid = row != 0xFFFFFFFFu;
     const uint32_t KS = D / 64u;
+    if (mdst && lane < MW) mdst[size_t(t) * mstride + lane] = tmeta[size_t(t) * MW + lane];
     if constexpr (sizeof(T) == 1) {
         // u8 rows: each lane moves its 16 bytes of a k-step with one load and
         // one store (x - 128 as int8 is x ^ 0x80); the norm of a point is the
@@ -3427,7 +3460,7 @@ __global__ __launch_bounds__(64) void k_tile_i8(const T* vec, uint32_t D, const 
             uint4 v = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
             if (valid) v = *reinterpret_cast<const uint4*>(vec + size_t(row) * D + s * 64u + (lane >> 4) * 16u);
             v.x ^= 0x80808080u; v.y ^= 0x80808080u; v.z ^= 0x80808080u; v.w ^= 0x80808080u;
-            *reinterpret_cast<uint4*>(vt + (size_t(t) * KS + s) * 1024u + lane * 16u) = v;
+            *reinterpret_cast<uint4*>(vt + size_t(t) * vstride + s * 1024u + lane * 16u) = v;
             const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -3440,13 +3473,13 @@ __global__ __launch_bounds__(64) void k_tile_i8(const T* vec, uint32_t D, const 
         n += __shfl_xor(n, 16, 64);
         n += __shfl_xor(n, 32, 64);
         if (lane < 16) {
-            tnorm[size_t(t) * 32u + col] = valid ? -(n >> 1) : kPadSeed;
-            tnorm[size_t(t) * 32u + 16u + col] = n;
+            tnorm[size_t(t) * nstride + col] = valid ? -(n >> 1) : kPadSeed;
+            tnorm[size_t(t) * nstride + 16u + col] = n;
         }
         return;
     }
     for (uint32_t s = 0; s < KS; ++s) {
-        int8_t* dst = vt + (size_t(t) * KS + s) * 1024u + lane * 16u;
+        int8_t* dst = vt + size_t(t) * vstride + s * 1024u + lane * 16u;
         for (uint32_t j = 0; j < 16; ++j) {
             const uint32_t k = s * 64u + (lane >> 4) * 16u + j;
             dst[j] = valid ? int8_t(int32_t(vec[size_t(row) * D + k]) - 128) : int8_t(0);
@@ -3459,8 +3492,8 @@ __global__ __launch_bounds__(64) void k_tile_i8(const T* vec, uint32_t D, const 
                 const int32_t v = int32_t(vec[size_t(row) * D + k]) - 128;
                 n += v * v;
             }
-        tnorm[size_t(t) * 32u + col] = valid ? -(n >> 1) : kPadSeed;
-        tnorm[size_t(t) * 32u + 16u + col] = n;
+        tnorm[size_t(t) * nstride + col] = valid ? -(n >> 1) : kPadSeed;
+        tnorm[size_t(t) * nstride + 16u + col] = n;
     }
 }
 
@@ -4133,12 +4166,29 @@ hipError_t launch_stats(const StatsArgs& a, hipStream_t st) {
 hipError_t launch_tile_i8(const void* vec_cm, bool u8, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
                           int8_t* vt, int32_t* tnorm, hipStream_t st) {
     if (!ntile) return hipSuccess;
+    const size_t vs = size_t(D / 64) * 1024u;
     if (u8)
         hipLaunchKernelGGL(k_tile_i8<uint8_t>, dim3(ntile), dim3(64), 0, st, static_cast<const uint8_t*>(vec_cm), D,
-                           tmeta, AW, vt, tnorm);
+                           tmeta, AW, vt, vs, tnorm, size_t(32), static_cast<uint32_t*>(nullptr), size_t(0));
     else
         hipLaunchKernelGGL(k_tile_i8<float>, dim3(ntile), dim3(64), 0, st, static_cast<const float*>(vec_cm), D,
-                           tmeta, AW, vt, tnorm);
+                           tmeta, AW, vt, vs, tnorm, size_t(32), static_cast<uint32_t*>(nullptr), size_t(0));
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_rec(const void* vec_cm, bool u8, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
+                           uint8_t* rec, hipStream_t st) {
+    if (!ntile) return hipSuccess;
+    const size_t rb = bf_rec_bytes(D, AW), ks = size_t(D / 64) * 1024u;
+    int8_t* vt = reinterpret_cast<int8_t*>(rec);
+    int32_t* tn = reinterpret_cast<int32_t*>(rec + ks);
+    uint32_t* md = reinterpret_cast<uint32_t*>(rec + ks + 128u);
+    if (u8)
+        hipLaunchKernelGGL(k_tile_i8<uint8_t>, dim3(ntile), dim3(64), 0, st, static_cast<const uint8_t*>(vec_cm), D,
+                           tmeta, AW, vt, rb, tn, rb / 4u, md, rb / 4u);
+    else
+        hipLaunchKernelGGL(k_tile_i8<float>, dim3(ntile), dim3(64), 0, st, static_cast<const float*>(vec_cm), D,
+                           tmeta, AW, vt, rb, tn, rb / 4u, md, rb / 4u);
     return hipGetLastError();
 }
 

@@ -127,11 +127,10 @@ struct StreamIndex {
     size_t max_bytes = 0;
     uint64_t budget = 0;
     uint32_t Bmax = 0, min_cell = 0;
-    // MFMA brute force: int8 tiles of the batch being searched
+    // MFMA brute force: int8 tile records of the batch being searched
     bool i8 = false;
     uint32_t AW = 0, NSmax = 0, tmax = 0;
-    DevBuf<int8_t> vt;
-    DevBuf<int32_t> tnorm;
+    DevBuf<uint8_t> trec;
     // the plan on the device (cells batch after batch, first of each batch)
     DevBuf<uint32_t> plan_cells, plan_off;
     hipStream_t copy = nullptr;
@@ -187,14 +186,13 @@ struct gf_index {
     // Query-batch MFMA brute force (additionally: vectors integers in
     // [0, 255], D a multiple of 64 up to 256): int8 tiles and norms.
     bool i8 = false;
-    DevBuf<int8_t> vt;
+    DevBuf<uint8_t> trec;   // MFMA brute force: int8 tile records (gf::bf_rec_bytes each)
     // Float rows with sub-cells (binary16 or fp32, shapes of
     // bf_float_supported) and no int8 route: the MFMA brute force of float
     // rows, with |x|^2 per row and the largest |x| over the index.
     bool hf = false;
     DevBuf<float> xnormf;
     double xmaxf = 0.0;
-    DevBuf<int32_t> tnorm;
     int ncu = 0;
     int wclk_khz = 100000;   // rate of the device wall clock the search's timestamps read
     // Streamed index (gf_index_create_streamed / gf_index_open_streamed):
@@ -209,8 +207,8 @@ struct gf_index {
                cross.bytes() + offset.bytes() + gidx.bytes() + lrow.bytes() + grid.bytes() + doff.bytes() +
                hist.bytes() + tile_cell.bytes() + tile_row0.bytes() + tile_n.bytes() + centres.bytes() +
                sbase.bytes() + scell.bytes() + ssize.bytes() + stile.bytes() + tmeta.bytes() + sbox.bytes() +
-               sorder.bytes() + abase.bytes() + vt.bytes() + tnorm.bytes() +
-               (sx ? sx->turn[0].bytes() + sx->turn[1].bytes() + sx->vt.bytes() + sx->tnorm.bytes() : 0);
+               sorder.bytes() + abase.bytes() + trec.bytes() +
+               (sx ? sx->turn[0].bytes() + sx->turn[1].bytes() + sx->trec.bytes() : 0);
     }
 };
 

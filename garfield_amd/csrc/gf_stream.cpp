@@ -220,8 +220,7 @@ void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_s
         sx->plan_off.upload(po);
     }
     if (sx->i8) {
-        sx->vt.alloc(size_t(std::max(sx->tmax, 1u)) * (D / 64) * 1024);
-        sx->tnorm.alloc(size_t(std::max(sx->tmax, 1u)) * 32);
+        sx->trec.alloc(size_t(std::max(sx->tmax, 1u)) * bf_rec_bytes(D, sx->AW));
         ix.i8 = true;   // gf_batch_create keeps int8 queries
     }
     GF_HIP(hipDeviceGetAttribute(&ix.ncu, hipDeviceAttributeMultiprocessorCount, ix.device));
@@ -564,7 +563,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         sa.tmeta = reinterpret_cast<const uint32_t*>(dev + sb.o_tmeta);
         sa.abase = reinterpret_cast<const int32_t*>(dev + sb.o_abase);
         sa.a = ix.a; sa.AW = S.AW; sa.P = sb.B; sa.NS = sb.NS;
-        GF_HIP(launch_tile_i8(dev + sb.o_vec, true, ix.D, sa.tmeta, S.AW, sb.ntile, S.vt.p, S.tnorm.p, st));
+        GF_HIP(launch_tile_rec(dev + sb.o_vec, true, ix.D, sa.tmeta, S.AW, sb.ntile, S.trec.p, st));
         GF_HIP(launch_cell_flags(Q, sb.B, b.slist.p, b.scount.p, b.slittle.p, b.bfmask.p, st));
         BfSchedArgs sc{};
         sc.sa = sa;
@@ -594,7 +593,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         }
         BfGemmArgs ga{};
         ga.sa = sa;
-        ga.vt = S.vt.p; ga.tnorm = S.tnorm.p; ga.q8 = b.q8.p; ga.nq = b.nq.p; ga.lo = b.lo.p; ga.hi = b.hi.p;
+        ga.rec = S.trec.p; ga.q8 = b.q8.p; ga.nq = b.nq.p; ga.lo = b.lo.p; ga.hi = b.hi.p;
         ga.items = b.items.p; ga.nitems = tot + 4; ga.bq = b.bq.p; ga.pcnt = b.pcnt.p; ga.part_off = b.part_off.p;
         ga.part = b.part.p; ga.gbound = b.gbound.p; ga.ok = tot + 3; ga.K = K; ga.D = ix.D;
         GF_HIP(hipEventRecord(ge[2 * bi], st));
