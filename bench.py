@@ -110,9 +110,10 @@ def main():
     ap.add_argument("--traverse-L", type=int, default=100)
     ap.add_argument("--channels", default="1,2",
                     help="traversals swept: 1 cell-by-cell (gf_search), 2 dual-channel (gf_search_dual)")
-    ap.add_argument("--rows", choices=["auto", "f32", "u8", "f16"], default="auto",
+    ap.add_argument("--rows", choices=["auto", "f32", "u8", "f16", "f16ref"], default="auto",
                     help="row storage of the resident index (auto: f16 for c4, else f32; u8 is exact for the "
-                         "integer-valued configs C1 and C2)")
+                         "integer-valued configs C1 and C2; f16ref: binary16 rows with the reference's "
+                         "binary16 distance arithmetic)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="after the run, stream this many MiB through y = x + 1 (fp32) three times: a kernel "
                          "of known traffic (reads and writes that many bytes) to scale rocprofv3's "
@@ -163,7 +164,7 @@ def main():
     # distances as fp32 rows bit for bit (every partial sum is an integer
     # below 2^24) at a quarter of the bytes per row gather
     rows = args.rows if args.rows != "auto" else ("f16" if args.config == "c4" else "f32")
-    vec_dtype = {"f32": gf.VEC_F32, "u8": gf.VEC_U8, "f16": gf.VEC_F16}[rows]
+    vec_dtype = {"f32": gf.VEC_F32, "u8": gf.VEC_U8, "f16": gf.VEC_F16, "f16ref": gf.VEC_F16_REF}[rows]
     N, D = cfg["vectors"].shape
     Q = cfg["queries"].shape[0]
     log(f"data generated N={N} D={D} Q={Q} ({time.time() - t0:.1f}s)")
@@ -370,10 +371,11 @@ def main():
 
     cpu = cpu_trav = None
     if not args.no_cpu:
-        f16 = vec_dtype == gf.VEC_F16
-        cpu = cpu_baseline(cfg, ix, b, L, pf, args, bch, f16)
+        f16 = vec_dtype in (gf.VEC_F16, gf.VEC_F16_REF)
+        ref16 = vec_dtype == gf.VEC_F16_REF
+        cpu = cpu_baseline(cfg, ix, b, L, pf, args, bch, f16, ref16)
         if trav is not None and best["route"] != "traversal":
-            cpu_trav = cpu_baseline(cfg, ix, b, trav["L"], trav["prefilter"], args, trav["channels"], f16)
+            cpu_trav = cpu_baseline(cfg, ix, b, trav["L"], trav["prefilter"], args, trav["channels"], f16, ref16)
 
     out = {
         "metric": metric,
@@ -386,7 +388,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "i8" if (last.bf_mfma == 1 and ms_bf > ms_tr) else ("f16" if vec_dtype == gf.VEC_F16 else "f32"),
+        "dtype": "i8" if (last.bf_mfma == 1 and ms_bf > ms_tr) else (
+            "f16" if vec_dtype in (gf.VEC_F16, gf.VEC_F16_REF) else "f32"),
         "data": "synthetic (generated in bench.py; index built on the GPU by the library's builder)",
         "config": {
             "workload": workload,
@@ -720,10 +723,11 @@ def stream_bench(args):
     print(result_line(out), flush=True)
 
 
-def cpu_baseline(cfg, ix, batch, L, prefilter, args, channels=1, f16=False):
+def cpu_baseline(cfg, ix, batch, L, prefilter, args, channels=1, f16=False, ref16=False):
     """The oracle's traversal / brute force (OpenMP over queries) on a sample of
     the same batch, same routing, same L, same traversal and row type (f16:
-    binary16 rows and queries), on the host's cores."""
+    binary16 rows and queries; ref16: with the reference's binary16
+    arithmetic), on the host's cores."""
     from oracle import oracle as orc
     import garfield_amd as gf
     batch.mark_cells(prefilter)          # the operating point's cells and routing
@@ -734,6 +738,7 @@ def cpu_baseline(cfg, ix, batch, L, prefilter, args, channels=1, f16=False):
     queries = orc.f2h(cfg["queries"], 1.0) if f16 else cfg["queries"]
     ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], L if channels == 2 else ix["R"])
     orc.set_channels(channels)
+    orc.set_dist_mode(1 if ref16 else 0)
     # The GPU box allots 16 host cores to its one GPU (OMP_NUM_THREADS is
     # set to that share there); os.cpu_count() sees the whole host.
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(os.cpu_count() or 1, 16)
@@ -753,6 +758,7 @@ def cpu_baseline(cfg, ix, batch, L, prefilter, args, channels=1, f16=False):
             break
         n = min(Q, max(n * 2, int(n * args.cpu_seconds / max(dt, 1e-3) * 1.1)))
     orc.set_channels(1)
+    orc.set_dist_mode(0)
     routed = int(np.sum((little[sel] == counts[sel]) & (counts[sel] > 0)))
     log(f"cpu baseline (prefilter {prefilter}, L {L}, channels {channels}): {n} queries in {dt:.1f}s on "
         f"{threads} threads")

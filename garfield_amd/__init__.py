@@ -16,7 +16,7 @@ not been built or cannot reach a GPU, and there is no CPU fallback.
 """
 from ._lib import (GarfieldError, Index, Batch, SearchStats, BuildStats, lib_path, f2h, row_norms_f16,
                    entry_points, grid_scatter, plan_cells, quantise_i8, build_graphs, optimize_graphs, kmeans, pinned_empty, search_noalloc, NO_RESULT, NCOUNTERS,
-                   VEC_F32, VEC_F16, VEC_U8, VEC_I8Q)
+                   VEC_F32, VEC_F16, VEC_U8, VEC_I8Q, VEC_F16_REF)
 
 
 def intersection_area_mark_little_seg_V2(batch, prefilter):
@@ -58,7 +58,7 @@ def grid_scatter_V2(attrs, grid):
 
 __all__ = [
     "GarfieldError", "Index", "Batch", "SearchStats", "BuildStats", "lib_path", "f2h", "row_norms_f16",
-    "entry_points", "grid_scatter", "grid_scatter_V2", "build_graphs", "kmeans", "pinned_empty", "NO_RESULT", "NCOUNTERS", "VEC_F32", "VEC_F16", "VEC_U8",
+    "entry_points", "grid_scatter", "grid_scatter_V2", "build_graphs", "kmeans", "pinned_empty", "NO_RESULT", "NCOUNTERS", "VEC_F32", "VEC_F16", "VEC_F16_REF", "VEC_U8",
     "intersection_area_mark_little_seg_V2", "get_partitions_access_order_V2",
     "batch_graph_search_gpu_with_prefilter_and_postfilter",
     "intersection_area_mark_little_seg_batch_process",

@@ -14,6 +14,7 @@ VEC_F32 = 0
 VEC_F16 = 1
 VEC_U8 = 2
 VEC_I8Q = 3
+VEC_F16_REF = 4   # binary16 rows, the reference's binary16 distance arithmetic
 COUNTER_NAMES = ("expand", "dist", "attr", "cross", "lrow", "scan", "pass", "route")
 
 

@@ -101,7 +101,8 @@ int main(int argc, char** argv) {
             if (v == "f16") vec_dtype = GF_VEC_F16;
             else if (v == "f32") vec_dtype = GF_VEC_F32;
             else if (v == "i8q") vec_dtype = GF_VEC_I8Q;
-            else die("--vec_dtype must be f16, f32 or i8q");
+            else if (v == "f16ref") vec_dtype = GF_VEC_F16_REF;
+            else die("--vec_dtype must be f16, f16ref, f32 or i8q");
         } else if (a == "--L") {
             Ls.clear();
             std::stringstream ss(v);

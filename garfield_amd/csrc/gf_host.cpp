@@ -229,14 +229,15 @@ void map_cells(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix, s
     ix.alpha = (opts && opts->f2h_factor != 0.0f) ? opts->f2h_factor : 1.0f;
     ix.ref_ties = opts && opts->ref_ties;
     GF_REQUIRE(ix.vdtype == GF_VEC_F32 || ix.vdtype == GF_VEC_F16 || ix.vdtype == GF_VEC_U8 ||
-                   ix.vdtype == GF_VEC_I8Q, GF_E_ARG,
-               "vec_dtype must be GF_VEC_F32, GF_VEC_F16, GF_VEC_U8 or GF_VEC_I8Q");
+                   ix.vdtype == GF_VEC_I8Q || ix.vdtype == GF_VEC_F16_REF, GF_E_ARG,
+               "vec_dtype must be GF_VEC_F32, GF_VEC_F16, GF_VEC_U8, GF_VEC_I8Q or GF_VEC_F16_REF");
+    const bool half_rows = gf::half_rows(ix.vdtype);
     GF_REQUIRE(!(opts && opts->degree) || opts->degree == h.R, GF_E_FORMAT, "--degree does not match the graph files");
-    const uint32_t elems = ix.vdtype == GF_VEC_F32 ? 4u : (ix.vdtype == GF_VEC_F16 ? 8u : 16u);
+    const uint32_t elems = ix.vdtype == GF_VEC_F32 ? 4u : (half_rows ? 8u : 16u);
     GF_REQUIRE(h.D % elems == 0, GF_E_UNSUPPORTED, "D must be a multiple of 4 (fp32), 8 (fp16) or 16 (u8, int8)");
     ix.rs = gf::row_shape(h.D, ix.vdtype);
     GF_REQUIRE(ix.rs.cpl <= gf::row_shape_max_cpl(ix.vdtype), GF_E_UNSUPPORTED, "D too large for this build");
-    ix.rowbytes = h.D * (ix.vdtype == GF_VEC_F32 ? 4u : (ix.vdtype == GF_VEC_F16 ? 2u : 1u));   // u8, int8: 1
+    ix.rowbytes = h.D * (ix.vdtype == GF_VEC_F32 ? 4u : (half_rows ? 2u : 1u));   // u8, int8: 1
 
     const uint32_t N = h.N, D = h.D, a = h.a, R = h.R, E = h.E;
     uint64_t P64 = 1;
@@ -371,7 +372,7 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
         if (ix.vdtype == GF_VEC_F32) {
             ix.vec.upload(reinterpret_cast<const char*>(v.data()), v.size() * sizeof(float));
             vec_f32_dev = reinterpret_cast<const float*>(ix.vec.p);
-        } else if (ix.vdtype == GF_VEC_F16) {
+        } else if (gf::half_rows(ix.vdtype)) {
             tmp.upload(v);
             ix.vec.alloc(v.size() * sizeof(uint16_t));
             GF_HIP(gf::launch_f2h(tmp.p, reinterpret_cast<uint16_t*>(ix.vec.p), v.size(), ix.alpha, ix.stream));
@@ -391,7 +392,7 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
         }
         build_subcells(h, gidx, size, ix);
         // Integer-valued data in [0, 255]: int8 tiles of the MFMA brute force.
-        bool ints = ix.sub && ix.vdtype != GF_VEC_F16 && ix.vdtype != GF_VEC_I8Q && D % 64 == 0 && D <= 256;
+        bool ints = ix.sub && !gf::half_rows(ix.vdtype) && ix.vdtype != GF_VEC_I8Q && D % 64 == 0 && D <= 256;
         for (size_t i = 0; ints && i < v.size(); ++i) ints = v[i] >= 0.0f && v[i] <= 255.0f && v[i] == std::floor(v[i]);
         if (ints) {
             ix.trec.alloc(size_t(ix.ntile) * gf::bf_rec_bytes(D, ix.AW));
@@ -708,7 +709,7 @@ gf_status gf_batch_create(gf_index* ix, const float* queries, uint32_t Q, const 
         b->qf32.upload(queries, size_t(Q) * ix->D);
         b->lo.upload(lo, size_t(Q) * ix->a);
         b->hi.upload(hi, size_t(Q) * ix->a);
-        if (ix->vdtype == GF_VEC_F16) {
+        if (gf::half_rows(ix->vdtype)) {
             b->q16v.alloc(size_t(Q) * ix->D);
             GF_HIP(gf::launch_f2h(b->qf32.p, b->q16v.p, size_t(Q) * ix->D, ix->alpha, ix->stream));
         }
@@ -983,7 +984,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     a.gidx = ix->gidx.p;
     a.lrow = ix->lrow.p;
     a.prow = ix->prow.p;
-    if (ix->vdtype == GF_VEC_F16) {
+    if (gf::half_rows(ix->vdtype)) {
         a.queries = reinterpret_cast<const char*>(b->q16v.p);
         a.qbytes = ix->D * 2;
     } else if (ix->vdtype == GF_VEC_I8Q) {

@@ -49,6 +49,9 @@ enum { C_EXPAND = 0, C_DIST = 1, C_ATTR = 2, C_CROSS = 3, C_LROW = 4, C_SCAN = 5
 // per row (power of two in [8, 64]), CPL chunks per lane.
 // Row layout of the distance kernels: vt 0 = fp32, 1 = binary16, 2 = uint8
 // vectors; a row is nch 16-byte chunks, LPR lanes per row, cpl chunks per lane.
+// Row types stored as binary16 (GF_VEC_F16, GF_VEC_F16_REF).
+inline bool half_rows(int vdtype) { return vdtype == GF_VEC_F16 || vdtype == GF_VEC_F16_REF; }
+
 struct RowShape {
     int vt;
     uint32_t nch, lpr, cpl;

@@ -93,7 +93,7 @@ __device__ __forceinline__ void hash_clear(uint32_t* H, uint32_t hsize) {
 // and the loads of up to 16 chunks per lane are issued before the first
 // wait.
 template <int VT>
-constexpr int kEpc = VT == 0 ? 4 : (VT == 1 ? 8 : 16);
+constexpr int kEpc = VT == 0 ? 4 : ((VT == 1 || VT == 4) ? 8 : 16);
 
 template <int LPR, int CPL>
 struct RowPlan {
@@ -110,6 +110,12 @@ template <int VT, int LPR, int CPL>
 struct QReg {
     float v[RowPlan<LPR, CPL>::NCH][kEpc<VT>];
     float w[VT == 3 ? RowPlan<LPR, CPL>::NCH : 1][VT == 3 ? kEpc<VT> : 1];   // VT 3: per-dimension scales
+};
+// VT 4: binary16 rows with the reference's half arithmetic; the query stays
+// in binary16 (its 16-byte chunks as loaded).
+template <int LPR, int CPL>
+struct QReg<4, LPR, CPL> {
+    uint4 h[RowPlan<LPR, CPL>::NCH];
 };
 
 // Chunk k = j * CPL + m of physical lane l: virtual lane l + PL * j, its m-th
@@ -153,33 +159,41 @@ template <int VT, int LPR, int CPL>
 __device__ __forceinline__ void load_query(QReg<VT, LPR, CPL>& q, const char* qrow, uint32_t nch) {
     using RP = RowPlan<LPR, CPL>;
     const uint32_t l = lane_id() % RP::PL;
+    if constexpr (VT == 4) {
 #pragma unroll
-    for (int k = 0; k < RP::NCH; ++k) {
-        const uint32_t c = lane_chunk<LPR, CPL>(l, k);
-        if (c < nch) {
-            if constexpr (VT == 2 || VT == 3) {
-                // fp32 query: one 16-element chunk is four 16-byte loads
+        for (int k = 0; k < RP::NCH; ++k) {
+            const uint32_t c = lane_chunk<LPR, CPL>(l, k);
+            q.h[k] = c < nch ? load16(qrow, c) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    } else {
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    float x[4];
-                    decode_chunk<0>(load16(qrow, 4 * c + t), x);
+        for (int k = 0; k < RP::NCH; ++k) {
+            const uint32_t c = lane_chunk<LPR, CPL>(l, k);
+            if (c < nch) {
+                if constexpr (VT == 2 || VT == 3) {
+                    // fp32 query: one 16-element chunk is four 16-byte loads
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) q.v[k][4 * t + e] = x[e];
-                    if constexpr (VT == 3) {
-                        decode_chunk<0>(load16(qrow, 4 * (nch + c) + t), x);   // the scales follow the nch chunks
+                    for (int t = 0; t < 4; ++t) {
+                        float x[4];
+                        decode_chunk<0>(load16(qrow, 4 * c + t), x);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) q.w[k][4 * t + e] = x[e];
+                        for (int e = 0; e < 4; ++e) q.v[k][4 * t + e] = x[e];
+                        if constexpr (VT == 3) {
+                            decode_chunk<0>(load16(qrow, 4 * (nch + c) + t), x);   // the scales follow the nch chunks
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) q.w[k][4 * t + e] = x[e];
+                        }
                     }
+                } else {
+                    decode_chunk<VT>(load16(qrow, c), q.v[k]);
                 }
             } else {
-                decode_chunk<VT>(load16(qrow, c), q.v[k]);
-            }
-        } else {
 #pragma unroll
-            for (int e = 0; e < kEpc<VT>; ++e) q.v[k][e] = 0.0f;
-            if constexpr (VT == 3) {
+                for (int e = 0; e < kEpc<VT>; ++e) q.v[k][e] = 0.0f;
+                if constexpr (VT == 3) {
 #pragma unroll
-                for (int e = 0; e < kEpc<VT>; ++e) q.w[k][e] = 0.0f;
+                    for (int e = 0; e < kEpc<VT>; ++e) q.w[k][e] = 0.0f;
+                }
             }
         }
     }
@@ -201,11 +215,79 @@ __device__ __forceinline__ float add_from_above(float v) {
     }
 }
 
+// Binary16 arithmetic of the reference's fp16 distance
+// (gpu_graph.cu:3394-3403, 3508-3530): lane r of a 32-lane warp takes the
+// 4-element chunks r, r + 32, ... of the row and, per chunk, acc =
+// hfma2(q.xy - x.xy, q.xy - x.xy, acc) then the same for .zw (so acc.x sums
+// elements 4c, 4c + 2 and acc.y elements 4c + 1, 4c + 3, in chunk order),
+// every operation rounded once to binary16; then hadd2 steps with shfl_down
+// 16, 8, 4, 2, 1 and float(acc.x) + float(acc.y) in fp32 on lane 0.  Here
+// (LPR = 16) virtual lane v takes our 16-byte chunks v, v + 16, ...: chunk c
+// is the reference's chunks 2c and 2c + 1, so v accumulates reference lanes
+// 2v (a0) and 2v + 1 (a1) in their own order.  Steps 16..2 of the tree pair
+// reference lanes of the same parity (v ^ 8 .. v ^ 1, a0 and a1 apart: in
+// the lane for the virtual lanes a physical lane folds, then across lanes),
+// step 1 adds a1 to a0; for the value that ends in lane 0 the xor pairing
+// adds the same operands as shfl_down's, and a binary16 sum does not depend
+// on operand order.
+__device__ __forceinline__ __half2 h2(uint32_t u) { return __builtin_bit_cast(__half2, u); }
+__device__ __forceinline__ uint32_t u2(__half2 h) { return __builtin_bit_cast(uint32_t, h); }
+template <int M>
+__device__ __forceinline__ uint32_t hadd_from_above(uint32_t v) {
+    uint32_t o;
+    if constexpr (M == 1) o = uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0xB1, 0xF, 0xF, false));
+    else if constexpr (M == 2) o = uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x4E, 0xF, 0xF, false));
+    else if constexpr (M == 4 || M == 8) o = uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x100 + M, 0xF, 0xF, false));
+    else o = uint32_t(__shfl_down(int(v), M, 64));
+    return u2(__hadd2(h2(v), h2(o)));
+}
+template <int LPR, int CPL>
+__device__ __forceinline__ float row_reduce_ref(const QReg<4, LPR, CPL>& q, const uint4 (&raw)[RowPlan<LPR, CPL>::NCH]) {
+    using RP = RowPlan<LPR, CPL>;
+    static_assert(LPR == 16, "the reference's 32 lanes as 16 virtual lanes of two");
+    // virtual lane l + PL j of this physical lane: reference lanes 2 v and 2 v + 1
+    __half2 a0[RP::V], a1[RP::V];
+#pragma unroll
+    for (int j = 0; j < RP::V; ++j) {
+        a0[j] = h2(0u);
+        a1[j] = h2(0u);
+#pragma unroll
+        for (int m = 0; m < CPL; ++m) {
+            const uint4& qc = q.h[j * CPL + m];
+            const uint4& xc = raw[j * CPL + m];
+            __half2 d = __hsub2(h2(qc.x), h2(xc.x));
+            a0[j] = __hfma2(d, d, a0[j]);
+            d = __hsub2(h2(qc.y), h2(xc.y));
+            a0[j] = __hfma2(d, d, a0[j]);
+            d = __hsub2(h2(qc.z), h2(xc.z));
+            a1[j] = __hfma2(d, d, a1[j]);
+            d = __hsub2(h2(qc.w), h2(xc.w));
+            a1[j] = __hfma2(d, d, a1[j]);
+        }
+    }
+    // tree levels on the virtual lane index, highest first: in-lane (the
+    // folded virtual lanes), then across lanes
+#pragma unroll
+    for (int mm = RP::V / 2; mm >= 1; mm >>= 1)
+#pragma unroll
+        for (int j = 0; j < mm; ++j) {
+            a0[j] = __hadd2(a0[j], a0[j + mm]);
+            a1[j] = __hadd2(a1[j], a1[j + mm]);
+        }
+    uint32_t v0 = u2(a0[0]), v1 = u2(a1[0]);
+    if constexpr (RP::PL >= 16) { v0 = hadd_from_above<8>(v0); v1 = hadd_from_above<8>(v1); }
+    v0 = hadd_from_above<4>(v0); v1 = hadd_from_above<4>(v1);
+    v0 = hadd_from_above<2>(v0); v1 = hadd_from_above<2>(v1);
+    v0 = hadd_from_above<1>(v0); v1 = hadd_from_above<1>(v1);
+    const __half2 r = __hadd2(h2(v0), h2(v1));
+    return __half2float(__low2half(r)) + __half2float(__high2half(r));
+}
+
 // Distance of one row's chunks raw[0..NCH) (this lane's part) to the query:
 // per-virtual-lane fma chains, the in-lane butterfly levels, then the
 // cross-lane levels; the row's distance ends in the group's first lane.
 template <int VT, int LPR, int CPL>
-__device__ __forceinline__ float row_reduce(const QReg<VT, LPR, CPL>& q, const uint4 (&raw)[RowPlan<LPR, CPL>::NCH]) {
+__device__ __forceinline__ float row_reduce_gen(const QReg<VT, LPR, CPL>& q, const uint4 (&raw)[RowPlan<LPR, CPL>::NCH]) {
     using RP = RowPlan<LPR, CPL>;
     float s[RP::V];
 #pragma unroll
@@ -241,6 +323,12 @@ __device__ __forceinline__ float row_reduce(const QReg<VT, LPR, CPL>& q, const u
     v = add_from_above<2>(v);
     v = add_from_above<1>(v);
     return v;
+}
+
+template <int VT, int LPR, int CPL>
+__device__ __forceinline__ float row_reduce(const QReg<VT, LPR, CPL>& q, const uint4 (&raw)[RowPlan<LPR, CPL>::NCH]) {
+    if constexpr (VT == 4) return row_reduce_ref<LPR, CPL>(q, raw);
+    else return row_reduce_gen<VT, LPR, CPL>(q, raw);
 }
 
 // Distances of the n rows listed in S[0..n) (LDS).  Lane j with compact
@@ -3944,15 +4032,25 @@ hipError_t launch_bf_t(const TravArgs& a, uint32_t grid, hipStream_t st) {
 RowShape row_shape(uint32_t D, int vt) {
     RowShape r;
     r.vt = vt;
-    const uint32_t elems = vt == 0 ? 4u : (vt == 1 ? 8u : 16u);   // vt 2 and 3: 16 bytes
+    const uint32_t elems = vt == 0 ? 4u : ((vt == 1 || vt == 4) ? 8u : 16u);   // vt 2 and 3: 16 bytes
     r.nch = (D + elems - 1) / elems;
+    if (vt == 4) {
+        // the reference's 32 lanes: 16 virtual lanes of two (row_reduce_ref),
+        // chunks per lane rounded up to an instantiated count
+        r.lpr = 16;
+        r.cpl = (r.nch + 15) / 16;
+        if (r.cpl == 3) r.cpl = 4;
+        else if (r.cpl == 5) r.cpl = 6;
+        else if (r.cpl == 7) r.cpl = 8;
+        return r;
+    }
     r.lpr = 8;
     while (r.lpr < r.nch && r.lpr < 64) r.lpr <<= 1;
     r.cpl = (r.nch + r.lpr - 1) / r.lpr;
     return r;
 }
 
-uint32_t row_shape_max_cpl(int vt) { return vt == 0 ? 4u : 2u; }
+uint32_t row_shape_max_cpl(int vt) { return vt == 0 ? 4u : (vt == 4 ? 8u : 2u); }
 
 // Instantiated shapes: LPR 8..64 with one chunk per lane, and 64 lanes with
 // up to 4 (fp32) or 2 (fp16, u8) chunks per lane.
@@ -3966,12 +4064,22 @@ uint32_t row_shape_max_cpl(int vt) { return vt == 0 ? 4u : 2u; }
         if (VT_ == 0 && rs.lpr == 64 && rs.cpl == 3) return CALL(0, 64, 3);         \
         if (VT_ == 0 && rs.lpr == 64 && rs.cpl == 4) return CALL(0, 64, 4);         \
     } while (0)
+// VT 4 (binary16, the reference's arithmetic): 16 lanes, 1..8 chunks each.
+#define GF_DISPATCH_VT4(CALL)                                  \
+    do {                                                       \
+        if (rs.lpr == 16 && rs.cpl == 1) return CALL(4, 16, 1); \
+        if (rs.lpr == 16 && rs.cpl == 2) return CALL(4, 16, 2); \
+        if (rs.lpr == 16 && rs.cpl == 4) return CALL(4, 16, 4); \
+        if (rs.lpr == 16 && rs.cpl == 6) return CALL(4, 16, 6); \
+        if (rs.lpr == 16 && rs.cpl == 8) return CALL(4, 16, 8); \
+    } while (0)
 #define GF_DISPATCH(CALL)                          \
     do {                                           \
         if (rs.vt == 0) GF_DISPATCH_VT(0, CALL);   \
         if (rs.vt == 1) GF_DISPATCH_VT(1, CALL);   \
         if (rs.vt == 2) GF_DISPATCH_VT(2, CALL);   \
         if (rs.vt == 3) GF_DISPATCH_VT(3, CALL);   \
+        if (rs.vt == 4) GF_DISPATCH_VT4(CALL);     \
     } while (0)
 
 namespace {

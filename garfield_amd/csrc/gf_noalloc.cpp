@@ -101,7 +101,7 @@ extern "C" gf_status gf_search_noalloc(gf_index* ix, const float* queries, uint3
             s.qf32 = c.take<float>(size_t(Q) * D);
             s.lo = c.take<float>(size_t(Q) * a);
             s.hi = c.take<float>(size_t(Q) * a);
-            if (ix->vdtype == GF_VEC_F16) s.q16v = c.take<uint16_t>(size_t(Q) * D);
+            if (gf::half_rows(ix->vdtype)) s.q16v = c.take<uint16_t>(size_t(Q) * D);
             if (ix->C) {
                 s.q16 = c.take<uint16_t>(size_t(Qp) * ix->Dp);
                 s.qnorm = c.take<float>(Qp);
@@ -196,9 +196,10 @@ extern "C" gf_status gf_search_noalloc(gf_index* ix, const float* queries, uint3
         t.offset = ix->offset.p;
         t.gidx = ix->gidx.p;
         t.lrow = ix->lrow.p;
-        t.queries = ix->vdtype == GF_VEC_F16 ? reinterpret_cast<const char*>(s.q16v)
+        const bool hq = gf::half_rows(ix->vdtype);
+        t.queries = hq ? reinterpret_cast<const char*>(s.q16v)
                                              : reinterpret_cast<const char*>(s.qf32);
-        t.qbytes = ix->vdtype == GF_VEC_F16 ? D * 2 : D * 4;
+        t.qbytes = hq ? D * 2 : D * 4;
         t.lo = s.lo;
         t.hi = s.hi;
         t.cells = s.cells;

@@ -42,7 +42,7 @@ void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_s
     GF_REQUIRE(plan, GF_E_ARG, "null stream plan");
     std::vector<uint32_t> size, gidx, lrow;
     map_cells(h, opts, ix, size, gidx, lrow);
-    GF_REQUIRE(ix.vdtype != GF_VEC_F16 && ix.vdtype != GF_VEC_I8Q, GF_E_UNSUPPORTED,
+    GF_REQUIRE(ix.vdtype != GF_VEC_F16 && ix.vdtype != GF_VEC_I8Q && ix.vdtype != GF_VEC_F16_REF, GF_E_UNSUPPORTED,
                "a streamed index holds GF_VEC_F32 or GF_VEC_U8 vectors");
     const uint32_t P = ix.P, R = ix.R, E = ix.E, a = ix.a, D = ix.D, N = ix.N;
 

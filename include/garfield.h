@@ -45,6 +45,12 @@ typedef int32_t gf_status;
                                round(x / scale) + zero point in [-128, 127], after x *= f2h_factor);
                                distances to the dequantised scale * (q - zero point) in fp32;
                                resident indexes only */
+#define GF_VEC_F16_REF 4    /* binary16 copies as GF_VEC_F16, distances in the reference's binary16
+                               arithmetic: per 4-element chunk, in its 32-lane chunk order,
+                               acc = __hfma2(q - x, q - x, acc) rounded to binary16 at every step,
+                               then its shfl_down 16..1 __hadd2 tree and float(acc.x) + float(acc.y)
+                               (gpu_graph.cu:3394-3403, 3508-3530); the brute force runs on the
+                               gather kernel; resident indexes only */
 
 typedef struct gf_index gf_index;
 typedef struct gf_batch gf_batch;
@@ -64,7 +70,7 @@ typedef struct {
 typedef struct {
     uint32_t degree;          /* --degree: per-cell graph degree R; 0 = from the files */
     float f2h_factor;         /* --f2h_factor: scale before fp16 conversion (0 means 1) */
-    int32_t vec_dtype;        /* GF_VEC_F32, GF_VEC_F16 or GF_VEC_U8 */
+    int32_t vec_dtype;        /* GF_VEC_F32, GF_VEC_F16, GF_VEC_U8, GF_VEC_I8Q or GF_VEC_F16_REF */
     int32_t hist_contiguous;  /* 1: cell x cluster histogram by i / ceil(N/P) as the
                                  reference (tools.cuh:587-590); 0: by grid cell */
     int32_t device;           /* HIP device ordinal */

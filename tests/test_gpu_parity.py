@@ -159,7 +159,9 @@ def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, post
     ent = gf.entry_points(ix["vectors"].shape[0], ix["P"], L if channels == 2 else ix["R"])
     ids, dists, st = b.search(L=L, K=K, rl=10, postfilter=postfilter, entry_points=ent, channels=channels)
     ctr = b.get_counters()
-    vec16 = orc.f2h(ix["vectors"], f2h_factor) if vec_dtype == 1 else None
+    # binary16 rows: 1 with fp32 accumulation (the oracle's distance mode
+    # 0), 4 with the reference's binary16 arithmetic (mode 1)
+    vec16 = orc.f2h(ix["vectors"], f2h_factor) if vec_dtype in (1, 4) else None
     if vec_dtype == 3:
         # the int8 values and per-dimension scales the index holds; queries
         # scaled by f2h_factor as the library scales them
@@ -170,12 +172,14 @@ def _traversal_case(cfg, ix, L, prefilter=0.0, vec_dtype=0, f2h_factor=1.0, post
     else:
         O = orc.OracleIndex(ix["vectors"], ix["attrs"], ix["global_pid"], ix["P"], ix["cell_graphs"],
                             ix["cross"], vec_f16=vec16)
-        oq = orc.f2h(queries, f2h_factor) if vec_dtype == 1 else queries
+        oq = orc.f2h(queries, f2h_factor) if vec_dtype in (1, 4) else queries
     orc.set_channels(channels)
+    orc.set_dist_mode(1 if vec_dtype == 4 else 0)
     try:
         oids, odist, octr = O.search(oq, lo, hi, gc, gcnt, glit, ent, L, K=K, rl=10, postfilter=postfilter)
     finally:
         orc.set_channels(1)
+        orc.set_dist_mode(0)
     b.close()
     dev.close()
     dump = os.environ.get("GF_DUMP_DIR")

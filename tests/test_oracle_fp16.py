@@ -1,6 +1,7 @@
 """The oracle's REF_HFMA2 mode: the reference's own fp16 distance arithmetic
-(gpu_graph.cu:3394-3403), and how often the HIP fp16 route's ids (binary16
-values, fp32 accumulation) differ from it.
+(gpu_graph.cu:3394-3403), and how often the fp32-accumulated fp16 route's ids
+(GF_VEC_F16: binary16 values, fp32 accumulation) differ from it; the
+GF_VEC_F16_REF route computes it on the GPU (tests/test_gpu_fp16_ref.py).
 
 Pinned by: numpy's binary16 conversion (round to nearest even from double) for
 every rounding step; a hand-computed case whose rounding is visible; exact
@@ -121,6 +122,10 @@ def test_fp16_route_against_ref_hfma2_report(world_c4, capsys):
         overlap = float(np.mean([len(set(x.tolist()) & set(y.tolist())) / 10 for x, y in zip(a, b)]))
         lines.append(f"L={L}: identical ids {same:.3f} of queries, id overlap {overlap:.3f}, "
                      f"recall fp32-accumulated {rec(a):.4f}, REF_HFMA2 {rec(b):.4f}")
-        assert overlap > 0.5
+        # measured on this world: identical ids for 0.61-0.64 of queries,
+        # id overlap 0.80-0.82; a drift beyond these floors is a change in
+        # either arithmetic (GF_VEC_F16_REF gives the reference's ids bit for
+        # bit, tests/test_gpu_fp16_ref.py)
+        assert same >= 0.55 and overlap >= 0.75, (L, same, overlap)
     with capsys.disabled():
         print("\n" + "\n".join(lines))
