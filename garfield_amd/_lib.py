@@ -125,6 +125,10 @@ _SYMBOLS = {
                           C.c_void_p, C.c_void_p],
     "gf_stream_plan_cells": [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_uint64,
                              C.c_uint32, C.c_void_p, C.c_void_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)],
+    "gf_batch_plan_stream": [C.c_void_p, C.c_uint64, C.c_uint32, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
+                             C.POINTER(C.c_double)],
+    "gf_batch_set_stream_plan": [C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p],
+    "gf_batch_get_stream_plan": [C.c_void_p, C.POINTER(C.c_uint32), C.c_void_p, C.c_void_p],
     "gf_quantise_i8": [C.c_void_p, C.c_uint64, C.c_uint32, C.c_float, C.c_void_p, C.c_void_p, C.c_void_p],
     "gf_host_alloc": [C.c_size_t, C.POINTER(C.c_void_p)],
     "gf_host_free": [C.c_void_p],
@@ -205,7 +209,6 @@ class Index:
         self.N, self.D, self.a, self.P = info.N, info.D, info.a, info.P
         self.R, self.E, self.C = info.R, info.E, info.C
         self.vec_dtype, self.f2h_factor = info.vec_dtype, info.f2h_factor
-        self.device_bytes = info.device_bytes
         self.streamed, self.nbatch = bool(info.streamed), info.nbatch
 
     @classmethod
@@ -291,6 +294,14 @@ class Index:
         _check(load().gf_index_open_streamed(C.byref(paths), C.byref(_opts(degree, 1.0, vec_dtype, False, device)),
                                              C.byref(sp), C.byref(h)))
         return cls(h)
+
+    @property
+    def device_bytes(self):
+        """Device memory the index holds now (a streamed index's batch
+        buffers grow for a query batch's larger plan)."""
+        info = _Info()
+        _check(load().gf_index_get_info(self._h, C.byref(info)))
+        return info.device_bytes
 
     def close(self):
         if self._h:
@@ -397,6 +408,39 @@ class Batch:
         topk = np.empty((self.Q, self._topc), np.uint32)
         _check(load().gf_batch_get_centroid(self._h, _ptr(dist), _ptr(topk)))
         return dist, topk
+
+    def plan_stream(self, max_points=0, max_cells=0):
+        """Streamed index: plan this batch's batches from its stage A cell
+        lists (gf_batch_plan_stream); its next searches use the plan.
+        Returns (plan, active, ms): the batches of cell ids, the plan's
+        active (query, batch) pairs, the call's host wall time."""
+        nb = C.c_uint32(0)
+        act = C.c_uint64(0)
+        ms = C.c_double(0.0)
+        _check(load().gf_batch_plan_stream(self._h, int(max_points), int(max_cells), C.byref(nb), C.byref(act),
+                                           C.byref(ms)))
+        return self.stream_plan(), int(act.value), ms.value
+
+    def set_stream_plan(self, plan):
+        """Streamed index: the batches this batch's searches use (a list of
+        lists of cell ids); None or [] returns to the index's build-time plan."""
+        plan = plan or []
+        sizes = _c([len(b) for b in plan] or [0], np.uint32)
+        cells = _c([c for b in plan for c in b] or [0], np.uint32)
+        _check(load().gf_batch_set_stream_plan(self._h, len(plan), _ptr(sizes), _ptr(cells)))
+
+    def stream_plan(self):
+        """The plan this batch's next streamed search uses."""
+        P = self.index.P
+        nb = C.c_uint32(0)
+        sizes = np.zeros(P, np.uint32)
+        cells = np.zeros(P, np.uint32)
+        _check(load().gf_batch_get_stream_plan(self._h, C.byref(nb), _ptr(sizes), _ptr(cells)))
+        plan, k = [], 0
+        for i in range(nb.value):
+            plan.append([int(c) for c in cells[k:k + sizes[i]]])
+            k += int(sizes[i])
+        return plan
 
     def get_counters(self):
         c = np.empty((self.Q, NCOUNTERS), np.uint32)

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <functional>
 #include <cmath>
 #include <cstdlib>
@@ -691,7 +692,7 @@ gf_status gf_index_get_info(const gf_index* ix, gf_index_info* out) {
         out->f2h_factor = ix->alpha;
         out->device_bytes = ix->device_bytes();
         out->streamed = ix->sx ? 1u : 0u;
-        out->nbatch = ix->sx ? uint32_t(ix->sx->batches.size()) : 0u;
+        out->nbatch = ix->sx ? uint32_t(ix->sx->plan->batches.size()) : 0u;
     });
 }
 
@@ -1540,6 +1541,57 @@ gf_status gf_stream_plan_cells(const uint32_t* cells, const uint32_t* counts, ui
         }
         *nbatch = uint32_t(plan.size());
         if (active) *active = act;
+    });
+}
+
+gf_status gf_batch_plan_stream(gf_batch* b, uint64_t max_points, uint32_t max_cells, uint32_t* nbatch,
+                               uint64_t* active, double* ms) {
+    return run_guarded([&] {
+        const auto t0 = std::chrono::steady_clock::now();
+        GF_REQUIRE(b, GF_E_ARG, "null batch");
+        GF_REQUIRE(b->ix->sx, GF_E_UNSUPPORTED, "gf_batch_plan_stream: not a streamed index");
+        GF_REQUIRE(b->marked, GF_E_STATE, "cells not marked");
+        set_device(b->ix);
+        const uint64_t act = gf::stream_plan_batch(*b, max_points, max_cells);
+        if (nbatch) *nbatch = uint32_t(b->splan->batches.size());
+        if (active) *active = act;
+        if (ms) *ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    });
+}
+
+gf_status gf_batch_set_stream_plan(gf_batch* b, uint32_t nbatch, const uint32_t* sizes, const uint32_t* cells) {
+    return run_guarded([&] {
+        GF_REQUIRE(b, GF_E_ARG, "null batch");
+        GF_REQUIRE(b->ix->sx, GF_E_UNSUPPORTED, "gf_batch_set_stream_plan: not a streamed index");
+        GF_REQUIRE(nbatch == 0 || (sizes && cells), GF_E_ARG, "null plan");
+        const uint32_t P = b->ix->P;
+        std::vector<std::vector<uint32_t>> plan;
+        size_t k = 0;
+        for (uint32_t i = 0; i < nbatch; ++i) {
+            GF_REQUIRE(sizes[i] >= 1 && sizes[i] <= P, GF_E_ARG, "stream plan batch size out of range");
+            GF_REQUIRE(k + sizes[i] <= P, GF_E_ARG, "stream plan holds more cells than the grid");
+            plan.emplace_back(cells + k, cells + k + sizes[i]);
+            k += sizes[i];
+        }
+        set_device(b->ix);
+        gf::stream_set_plan(*b, std::move(plan));
+    });
+}
+
+gf_status gf_batch_get_stream_plan(const gf_batch* b, uint32_t* nbatch, uint32_t* sizes, uint32_t* cells) {
+    return run_guarded([&] {
+        GF_REQUIRE(b && nbatch, GF_E_ARG, "null argument");
+        GF_REQUIRE(b->ix->sx, GF_E_UNSUPPORTED, "gf_batch_get_stream_plan: not a streamed index");
+        const gf::StreamPlan& pl = b->splan ? *b->splan : *b->ix->sx->plan;
+        *nbatch = uint32_t(pl.cells.size());
+        size_t k = 0;
+        for (size_t i = 0; i < pl.cells.size(); ++i) {
+            if (sizes) sizes[i] = uint32_t(pl.cells[i].size());
+            for (uint32_t c : pl.cells[i]) {
+                if (cells) cells[k] = c;
+                ++k;
+            }
+        }
     });
 }
 

@@ -477,6 +477,20 @@ hipError_t launch_stamp(uint64_t* t, hipStream_t st);                    // *t =
 // need: 2 * nbatch entries, the need flags, then the active queries per batch
 hipError_t launch_batch_need(uint32_t Q, uint32_t P, uint32_t nbatch, const uint32_t* plan_cells,
                              const uint32_t* plan_off, const uint8_t* flags, uint32_t* need, hipStream_t st);
+hipError_t launch_cell_boxes(uint32_t Q, uint32_t P, uint32_t a, const uint32_t* grid, const uint32_t* cells,
+                             const uint32_t* counts, uint32_t* box, hipStream_t st);
+// One piece of a streamed batch image, read by k_stream_gather from pinned
+// host memory: nrow rows of width bytes, source rows spitch apart from byte
+// src of the arena (base 0) or of the plan's header block (base 1), image
+// rows dpitch apart from byte dst.  mw != 0: tile metadata of mw words per
+// tile, whose words w with w % mw < 16 (rows) gain add unless 0xFFFFFFFF.
+struct GatherDesc {
+    uint64_t src, dst, spitch, dpitch;
+    uint32_t width, nrow, base, add, mw;
+    uint32_t pad[3];
+};
+hipError_t launch_stream_gather(const GatherDesc* desc, uint32_t n, const char* arena, const char* head, char* img,
+                                hipStream_t st);
 hipError_t launch_merge_stream(uint32_t Q, uint32_t K, uint32_t* run_ids, float* run_dist, const uint32_t* ids,
                                const float* dist, uint32_t* run_ctr, const uint32_t* ctr, bool first,
                                hipStream_t st);

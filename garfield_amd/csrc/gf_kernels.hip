@@ -1833,9 +1833,8 @@ __global__ void k_gather_meta(const unsigned long long* stats, const uint32_t* t
 // What each batch of a streamed plan must do for this query batch (one
 // workgroup per batch): need[b] bit 0 = some query takes the brute force on
 // it (all its selected cells of the batch little), bit 1 = some query
-// traverses it; 0 = no query selects any of its cells.
-// need[b]: bit 0 = some query only brute-forces batch b, bit 1 = some query
-// traverses it; active[b] = queries with a selected cell in batch b.
+// traverses it; 0 = no query selects any of its cells.  active[b] = queries
+// with a selected cell in batch b.
 __global__ __launch_bounds__(256) void k_batch_need(uint32_t Q, uint32_t P, const uint32_t* plan_cells,
                                                     const uint32_t* plan_off, const uint8_t* flags, uint32_t* need,
                                                     uint32_t* active) {
@@ -1860,6 +1859,101 @@ __global__ __launch_bounds__(256) void k_batch_need(uint32_t Q, uint32_t P, cons
     __syncthreads();
     if (threadIdx.x == 0 && acc) atomicOr(&need[bi], acc);   // need[] and active[] zeroed before
     if (threadIdx.x == 0 && nact) atomicAdd(&active[bi], nact);
+}
+
+// Bounding box of each query's listed cells on a grid of a axes (row-major,
+// last axis fastest): box[q * 2a + d] = lowest coordinate on axis d,
+// box[q * 2a + a + d] = highest; a query with no cell gets lo = grid, hi = 0.
+__global__ __launch_bounds__(256) void k_cell_boxes(uint32_t Q, uint32_t P, uint32_t a, const uint32_t* grid,
+                                                    const uint32_t* cells, const uint32_t* counts, uint32_t* box) {
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= Q) return;
+    uint32_t lo[kMaxAttr], hi[kMaxAttr], g[kMaxAttr];
+#pragma unroll
+    for (uint32_t d = 0; d < kMaxAttr; ++d) {
+        g[d] = d < a ? grid[d] : 1u;
+        lo[d] = g[d];
+        hi[d] = 0;
+    }
+    const uint32_t n = counts[q] < P ? counts[q] : P;
+    for (uint32_t i = 0; i < n; ++i) {
+        uint32_t c = cells[size_t(q) * P + i];
+        if (c >= P) continue;
+#pragma unroll
+        for (int d = kMaxAttr - 1; d >= 0; --d) {
+            if (uint32_t(d) >= a) continue;
+            const uint32_t x = c % g[d];
+            c /= g[d];
+            lo[d] = x < lo[d] ? x : lo[d];
+            hi[d] = x > hi[d] ? x : hi[d];
+        }
+    }
+    for (uint32_t d = 0; d < a; ++d) {
+        box[size_t(q) * 2 * a + d] = lo[d];
+        box[size_t(q) * 2 * a + a + d] = hi[d];
+    }
+}
+
+// A streamed batch's image assembled from pinned host memory over PCIe: the
+// pieces of GatherDesc in order, every thread striding over each piece in
+// chunks of the widest of 16, 8, 4 or 1 bytes that source, image, pitches
+// and width allow, four chunks in flight per thread.  Tile metadata pieces
+// get their rows rebased on the way (mw != 0).
+template <typename V>
+__device__ inline void gather_fix(V& v, uint64_t byte, uint32_t add, uint32_t mw) {
+    if (uint32_t((byte / 4) % mw) >= 16u) return;
+    uint32_t* w = reinterpret_cast<uint32_t*>(&v);
+#pragma unroll
+    for (uint32_t k = 0; k < sizeof(V) / 4; ++k)
+        if (w[k] != 0xFFFFFFFFu) w[k] += add;
+}
+
+template <typename V>
+__device__ inline void gather_piece(const char* src, char* dst, uint64_t spitch, uint64_t dpitch, uint32_t width,
+                                    uint32_t nrow, uint32_t add, uint32_t mw, uint32_t tid, uint32_t nt) {
+    const uint64_t wc = width / sizeof(V), total = wc * nrow;
+    for (uint64_t i = tid; i < total; i += 4ull * nt) {
+        V v[4];
+        uint64_t so[4], dof[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint64_t j = i + uint64_t(u) * nt;
+            if (j >= total) break;
+            const uint64_t r = nrow == 1 ? 0 : j / wc, c = j - r * wc;
+            so[u] = r * spitch + c * sizeof(V);
+            dof[u] = r * dpitch + c * sizeof(V);
+            v[u] = *reinterpret_cast<const V*>(src + so[u]);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+            const uint64_t j = i + uint64_t(u) * nt;
+            if (j >= total) break;
+            if constexpr (sizeof(V) >= 4) {
+                if (mw) gather_fix(v[u], so[u], add, mw);
+            }
+            *reinterpret_cast<V*>(dst + dof[u]) = v[u];
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_stream_gather(const GatherDesc* __restrict__ desc, uint32_t n,
+                                                       const char* arena, const char* head, char* img) {
+    const uint32_t tid = blockIdx.x * blockDim.x + threadIdx.x, nt = gridDim.x * blockDim.x;
+    for (uint32_t k = 0; k < n; ++k) {
+        const GatherDesc g = desc[k];
+        const char* src = (g.base ? head : arena) + g.src;
+        char* dst = img + g.dst;
+        const uint64_t al = reinterpret_cast<uint64_t>(src) | reinterpret_cast<uint64_t>(dst) | g.width |
+                            (g.nrow > 1 ? (g.spitch | g.dpitch) : 0);
+        if ((al & 15u) == 0)
+            gather_piece<uint4>(src, dst, g.spitch, g.dpitch, g.width, g.nrow, g.add, g.mw, tid, nt);
+        else if ((al & 7u) == 0)
+            gather_piece<uint2>(src, dst, g.spitch, g.dpitch, g.width, g.nrow, g.add, g.mw, tid, nt);
+        else if ((al & 3u) == 0)
+            gather_piece<uint32_t>(src, dst, g.spitch, g.dpitch, g.width, g.nrow, g.add, g.mw, tid, nt);
+        else
+            gather_piece<uint8_t>(src, dst, g.spitch, g.dpitch, g.width, g.nrow, 0u, 0u, tid, nt);
+    }
 }
 
 // Running top-K of a streamed search: merge the batch's sorted K results
@@ -4496,6 +4590,25 @@ hipError_t launch_batch_need(uint32_t Q, uint32_t P, uint32_t nbatch, const uint
     const uint32_t gy = (Q + 255) / 256 < 64u ? (Q + 255) / 256 : 64u;
     hipLaunchKernelGGL(k_batch_need, dim3(nbatch, gy), dim3(256), 0, st, Q, P, plan_cells, plan_off, flags, need,
                        need + nbatch);
+    return hipGetLastError();
+}
+
+hipError_t launch_cell_boxes(uint32_t Q, uint32_t P, uint32_t a, const uint32_t* grid, const uint32_t* cells,
+                             const uint32_t* counts, uint32_t* box, hipStream_t st) {
+    if (!Q) return hipSuccess;
+    hipLaunchKernelGGL(k_cell_boxes, dim3((Q + 255) / 256), dim3(256), 0, st, Q, P, a, grid, cells, counts, box);
+    return hipGetLastError();
+}
+
+hipError_t launch_stream_gather(const GatherDesc* desc, uint32_t n, const char* arena, const char* head, char* img,
+                                hipStream_t st) {
+    if (!n) return hipSuccess;
+    // 16 workgroups keep enough reads in flight for the PCIe link (56 GB/s
+    // alone, 52 GB/s beside a latency-bound kernel, measured) and slow the
+    // compute stream's kernels by 5-12 %; 64 reach no more and slow them by
+    // up to 75 % (their long-latency host reads hold the memory pipelines of
+    // the CUs they share).
+    hipLaunchKernelGGL(k_stream_gather, dim3(16), dim3(256), 0, st, desc, n, arena, head, img);
     return hipGetLastError();
 }
 

@@ -75,10 +75,10 @@ struct PinBuf {
         p = nullptr;
         n = 0;
     }
-    void alloc(size_t count) {
+    void alloc(size_t count, unsigned flags = hipHostMallocDefault) {
         release();
         if (count == 0) return;
-        hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&p), count * sizeof(T), hipHostMallocDefault);
+        hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&p), count * sizeof(T), flags);
         if (e != hipSuccess) {
             p = nullptr;
             throw gf::Error{GF_E_NOMEM, "hipHostMalloc of " + std::to_string(count * sizeof(T)) + " bytes failed"};
@@ -88,51 +88,132 @@ struct PinBuf {
     size_t bytes() const { return n * sizeof(T); }
 };
 
-// A streamed index keeps no per-point array on the device.  Its static plan
-// groups cells into batches; each batch is stored in pinned host memory as
-// one packed image that hipMemcpyAsync moves into one of two device buffers
-// ("turns"), laid out as a small index of the batch's cells, with the
-// sections the brute force needs first so that a batch none of whose queries
-// traverses crosses PCIe as a prefix of its image:
-//   vec    rows x rowbytes (the batch's cells in plan order, cell-major rows)
-//   gidx   rows       point id of each row
-//   offset B + 1      first row of each batch cell
-//   bcell  B          cell id of each batch cell
-//   sub-cells (when the MFMA brute force applies: u8 vectors, D a multiple
-//   of 64 up to 256): sbase B + 1, scell / ssize NS, stile NS + 1,
-//   sbox NS * 2a, abase B * a, tmeta tiles * 16 (1 + AW), batch-local rows
-//   and cells; the int8 tiles are built on the device from the rows
-//                                      <- end of the MFMA brute-force prefix
-//   attrs  rows x a   fp32             <- end of the gather brute-force prefix
-//   graph  rows x R   cell-local neighbour ids
-//   lrow   rows       cell-local id of each row
+// Sub-cells of every cell, host arrays (compute_subcells).
+struct SubHost {
+    uint32_t AW = 0, NS = 0, ntile = 0;
+    // Brute-force pass order: the ns1 sub-cells of the first pass (about one
+    // in eight of each cell's rank grid, spread over it), then the rest.
+    uint32_t ns1 = 0;
+    std::vector<uint32_t> sorder;
+    std::vector<uint32_t> sbase, scell, ssize, stile, tmeta;
+    std::vector<int32_t> sbox, abase;
+};
+
+// A streamed index keeps no per-point array on the device.  Its rows stay in
+// pinned host memory, in one arena laid out in the resident row order (cells
+// in id order, each cell's rows consecutive), whatever the plan:
+//   vec    N x rowbytes
+//   gidx   N          point id of each row
+//   attrs  N x a      fp32
+//   graph  N x R      cell-local neighbour ids
+//   lrow   N          cell-local id of each row
+//   cross  P x N x E  target-major: edge e of row g into cell c' at
+//          (c' * N + g) * E + e.  The rows of one cell into c' are the
+//          reference's per-pair "T" slice (big_dataset_adapterV3.cuh:3539-3541),
+//          and the slices of a run of consecutive cells into c' are adjacent.
+//   sub-cells (MFMA brute force: u8 vectors, D a multiple of 64 up to 256):
+//          ssize NS, sbox NS x 2a, tmeta tiles x 16 (1 + AW) with resident rows
+// A plan groups cells into batches.  A search assembles each batch's image in
+// one of two device buffers ("turns") on a side stream, from pieces: per run
+// of consecutive cell ids in the batch one piece of each array it needs, per
+// (source run, target run) one two-dimensional piece of cross edges, and the
+// batch header, which the plan builds on the host.  The large 1-D pieces
+// (rows of vectors and graphs) move by DMA; one k_stream_gather launch reads
+// the others from the pinned memory over PCIe.  The image is a small
+// index of the batch's cells, the sections the brute force needs first, so
+// that a batch none of whose queries traverses moves only a prefix:
+//   header offset B + 1 (first row of each batch cell), bcell B (cell ids);
+//          with sub-cells sbase B + 1, scell NS, stile NS + 1 (batch-local),
+//          abase B x a
+//   ssize NS, sbox NS x 2a, tmeta tiles x MW (rows made batch rows on the
+//          way: a run's rows all move by the same amount)
+//   vec    rows x rowbytes (the batch's cells in plan order)
+//   gidx   rows                        <- end of the MFMA brute-force prefix
+//   attrs  rows x a                    <- end of the gather brute-force prefix
+//   graph  rows x R, lrow rows
 //   cross  B x rows x E: edge e of row r into the batch's i-th cell at
-//          (i * rows + r) * E + e (the reference's per-pair "T" slices,
-//          big_dataset_adapterV3.cuh:3539-3541)
+//          (i * rows + r) * E + e
 // Every section starts on a 256-byte boundary.
+struct StreamRun {            // a maximal run of consecutive cell ids in a batch
+    uint32_t i0 = 0, n = 0;   // first batch cell, cells
+    uint32_t c0 = 0;          // cell id of the first
+    uint32_t g0 = 0, r0 = 0, rows = 0;   // first resident row, first batch row, rows
+    uint32_t s0 = 0, sb0 = 0, ns = 0;    // first resident / batch sub-cell, sub-cells
+    uint32_t t0 = 0, tb0 = 0, nt = 0;    // first resident / batch tile, tiles
+};
+
 struct StreamBatch {
     uint32_t B = 0, rows = 0, NS = 0, ntile = 0;
-    size_t o_vec = 0, o_graph = 0, o_attrs = 0, o_gidx = 0, o_lrow = 0, o_cross = 0, o_offset = 0, o_bcell = 0;
-    size_t o_sbase = 0, o_scell = 0, o_ssize = 0, o_stile = 0, o_sbox = 0, o_abase = 0, o_tmeta = 0;
-    size_t bytes = 0;      // image size
+    size_t o_offset = 0, o_bcell = 0, o_sbase = 0, o_scell = 0, o_stile = 0, o_abase = 0;
+    size_t head = 0;        // header bytes (image prefix copied from the plan's pinned block)
+    size_t o_ssize = 0, o_sbox = 0, o_tmeta = 0, o_vec = 0, o_gidx = 0, o_attrs = 0, o_graph = 0, o_lrow = 0,
+           o_cross = 0;
+    size_t bytes = 0;       // image size
     size_t bytes_mfma = 0;  // prefix the MFMA brute force reads
     size_t bytes_bf = 0;    // prefix the gather brute force reads
-    size_t host_off = 0;   // image start in the pinned arena
+    size_t head_off = 0;    // header in the plan's pinned block
+    uint32_t run0 = 0, nrun = 0;   // the batch's runs in StreamPlan::runs
+    // its pieces: in StreamPlan::desc from desc0 (k_stream_gather) and in
+    // StreamPlan::dma from dma0 (hipMemcpyAsync, the large 1-D ones); the
+    // first ndesc[w] and ndma[w], bytes moved[w], make the MFMA brute
+    // force's prefix (w = 0), the gather brute force's (1), the image (2)
+    uint32_t desc0 = 0, ndesc[3] = {0, 0, 0};
+    uint32_t dma0 = 0, ndma[3] = {0, 0, 0};
+    size_t moved[3] = {0, 0, 0};
+};
+
+struct StreamCopy {   // a 1-D piece of a batch image moved by DMA from the arena
+    size_t src, dst, bytes;
+};
+
+// A batch plan of a streamed index: the index's build-time plan, or one a
+// query batch sets (gf_batch_plan_stream / gf_batch_set_stream_plan).
+struct StreamPlan {
+    std::vector<std::vector<uint32_t>> cells;
+    std::vector<StreamBatch> batches;
+    std::vector<StreamRun> runs;
+    PinBuf<char> head;         // coherent pinned memory, read by k_stream_gather
+    DevBuf<GatherDesc> desc;   // every batch's gathered pieces
+    std::vector<StreamCopy> dma;   // every batch's DMA pieces
+    // cells batch after batch and the first of each batch, for k_batch_need
+    DevBuf<uint32_t> plan_cells, plan_off;
+    size_t max_bytes = 0;
+    uint32_t Bmax = 0, NSmax = 0, tmax = 0;
+};
+
+// The part of the batch planner's dynamic program that depends on the grid,
+// the cell sizes and the batch limits only (plan_boxes): the boxes that do
+// not fit a batch, ordered so that both parts of any cut of a box come before
+// it, and each box's batch count when it is a leaf.
+struct PlanFrame {
+    uint32_t a = 0;
+    std::vector<uint32_t> grid;
+    uint64_t max_points = 0;
+    uint32_t max_cells = 0;
+    uint32_t stride[kMaxAttr] = {}, bstride[kMaxAttr] = {};
+    size_t nbox = 0;
+    std::vector<uint32_t> order;   // boxes that do not fit
+    std::vector<uint8_t> leaf;     // per box: 0 / 1 batches when it is a leaf; 2 = not a leaf
 };
 
 struct StreamIndex {
-    std::vector<StreamBatch> batches;
-    PinBuf<char> host;
+    PinBuf<char> host;   // the arena (coherent pinned memory, read by k_stream_gather)
+    size_t arena_bytes = 0;
+    size_t a_vec = 0, a_gidx = 0, a_attrs = 0, a_graph = 0, a_lrow = 0, a_cross = 0, a_ssize = 0, a_sbox = 0,
+           a_tmeta = 0;
+    uint32_t rows = 0;            // N
+    std::vector<uint32_t> size;   // points per cell
+    SubHost sh;                   // sub-cell offsets (the arena holds ssize, sbox, tmeta)
+    std::unique_ptr<PlanFrame> frame;   // the planner's frame for the latest batch limits
+    std::unique_ptr<StreamPlan> plan;   // the build-time plan
     DevBuf<char> turn[2];
-    size_t max_bytes = 0;
     uint64_t budget = 0;
-    uint32_t Bmax = 0, min_cell = 0;
+    uint32_t min_cell = 0;
     // MFMA brute force: int8 tile records of the batch being searched
     bool i8 = false;
-    uint32_t AW = 0, NSmax = 0, tmax = 0;
+    uint32_t AW = 0;
+    size_t trec_tiles = 0;
     DevBuf<uint8_t> trec;
-    // the plan on the device (cells batch after batch, first of each batch)
-    DevBuf<uint32_t> plan_cells, plan_off;
     hipStream_t copy = nullptr;
     hipEvent_t ready[2] = {nullptr, nullptr}, freed[2] = {nullptr, nullptr};
     ~StreamIndex() {
@@ -237,10 +318,20 @@ struct gf_batch {
     DevBuf<gf::BfItem> sitems;
     // slots: (sub-cell, tile chunk) combinations, bounding the items beyond
     // one per 64 pairs.
+    // The sub-cells and slots (and queries) the buffers were sized for: a
+    // schedule over more must call alloc_pairs again.
+    uint32_t ns_cap = 0, q_cap = 0;
+    size_t slot_cap = 0;
+    bool pairs_fit(uint32_t Q, uint32_t NS, size_t slots) const {
+        return part.n && Q <= q_cap && NS <= ns_cap && slots <= slot_cap;
+    }
     void alloc_pairs(size_t pairs, uint32_t K, uint32_t Q, uint32_t NS, size_t slots) {
         const bool direct = size_t(NS) * Q <= gf::kDirectListMax;
         qcap = direct ? Q : 0u;
         pair_cap = pairs;
+        ns_cap = NS;
+        q_cap = Q;
+        slot_cap = slots;
         const size_t nbq = direct ? size_t(NS) * Q : pairs;
         if (bq.n < nbq) bq.alloc(nbq);
         part.alloc(pairs * K);
@@ -273,9 +364,12 @@ struct gf_batch {
     // search's MFMA brute force reported PASS from counts not made yet.
     bool sel_exact = true;
     bool pass_pending = false;
-    // Streamed search: per-batch cell lists and results.
+    // Streamed search: per-batch cell lists and results, and the batch plan
+    // this query batch set (none: the index's build-time plan).
     DevBuf<uint32_t> slist, scount, slittle, s_ids, s_ctr, note, need;
     DevBuf<float> s_dist;
+    std::unique_ptr<gf::StreamPlan> splan;
+    DevBuf<uint32_t> qbox;   // per query: bounding box of its cells on the grid (planning)
     // pinned staging of a resident search's results, totals and timestamps
     gf::PinBuf<uint32_t> h_ids, h_tot;
     gf::PinBuf<float> h_dist;
@@ -374,15 +468,6 @@ namespace gf {
 // Sub-cells of every cell (host arrays; see build_subcells in gf_host.cpp):
 // false when the attributes do not allow them (a > 4, non-integer values, or
 // a spread of 65534 or more inside a cell).
-struct SubHost {
-    uint32_t AW = 0, NS = 0, ntile = 0;
-    // Brute-force pass order: the ns1 sub-cells of the first pass (about one
-    // in eight of each cell's rank grid, spread over it), then the rest.
-    uint32_t ns1 = 0;
-    std::vector<uint32_t> sorder;
-    std::vector<uint32_t> sbase, scell, ssize, stile, tmeta;
-    std::vector<int32_t> sbox, abase;
-};
 bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, const std::vector<uint32_t>& size,
                       const std::vector<uint32_t>& offset_h, uint32_t a, uint32_t P, SubHost& out);
 // Checks shared by resident and streamed indexes, and the idx mapper
@@ -391,13 +476,31 @@ bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx,
 // is validated here, before any device call.
 void map_cells(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix, std::vector<uint32_t>& size,
                std::vector<uint32_t>& gidx, std::vector<uint32_t>& lrow);
-// Streamed index (gf_stream.cpp): packs the plan's batch images and sizes
-// the device buffers; then the streamed stage C.
+// Streamed index (gf_stream.cpp): fills the pinned arena, makes the
+// build-time plan and sizes the device buffers; then the streamed stage C.
 void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_stream_plan* plan, gf_index& ix);
+// A plan of a streamed index over the given batches of cell ids (each cell at
+// most once): image layouts, runs and headers; the index's turn buffers and
+// tile scratch grow to hold its largest batch within the device budget.
+// reuse (may be null): a plan whose host and device buffers the new one may
+// take over (it is left without them).
+std::unique_ptr<StreamPlan> make_stream_plan(gf_index& ix, std::vector<std::vector<uint32_t>> cells,
+                                             StreamPlan* reuse);
+// gf_batch_plan_stream (returns the plan's active (query, batch) pairs) and
+// gf_batch_set_stream_plan (no batches: back to the build-time plan).
+uint64_t stream_plan_batch(gf_batch& b, uint64_t max_points, uint32_t max_cells);
+void stream_set_plan(gf_batch& b, std::vector<std::vector<uint32_t>> cells);
 void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* dists, gf_search_stats* stats);
 uint64_t plan_cells(const uint32_t* cells, const uint32_t* counts, uint32_t Q, uint32_t a, const uint32_t* grid,
                     const uint32_t* cell_size, uint64_t max_points, uint32_t max_cells,
                     std::vector<std::vector<uint32_t>>& plan);
+// The planner's dynamic program on query boxes (qlo / qhi: a grid coordinates
+// per query, lo <= hi), without the objective count.  cache (may be null):
+// a frame kept for these cell sizes, reused when grid and limits match, else
+// rebuilt into it.
+void plan_boxes(const std::vector<uint32_t>& qlo, const std::vector<uint32_t>& qhi, uint32_t a, const uint32_t* grid,
+                const uint32_t* cell_size, uint64_t max_points, uint32_t max_cells,
+                std::vector<std::vector<uint32_t>>& plan, std::unique_ptr<PlanFrame>* cache = nullptr);
 // Entry-point draws (mt19937 default seed, distinct uniform_int_distribution
 // draws in [0, range), std::random_shuffle after srand(1)): the first R.
 void entry_points_draw(uint32_t range, uint32_t ndraw, uint32_t R, uint32_t* out);

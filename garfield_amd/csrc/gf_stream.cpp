@@ -1,24 +1,30 @@
 // Streamed (out-of-core) index and search: the reference's out-of-core
 // scheduler batch_graph_search_gpu_with_prefilter_batch_process_compressed_graph_T_dataset_resident_u8
-// (big_dataset_adapterV3.cuh:3719-4117), rebuilt around one packed pinned
-// image per batch.
+// (big_dataset_adapterV3.cuh:3719-4117), rebuilt around a pinned arena and
+// per-plan batch images.
 //
 // The reference issues one cudaMemcpyAsync per cell graph and per (cell,
 // cell') cross-edge slice of a batch (big_dataset_adapterV3.cuh:3925-3946),
 // then serialises the pipeline with cudaDeviceSynchronize (:4010) and
 // re-ranks L candidates per query on 9 host threads (:3741-3797).  Here the
-// plan is fixed when the index is built, so each batch is packed once, at
-// build time, into a contiguous image in pinned memory laid out as a small
-// index of the batch's cells (gf_state.h, StreamBatch).  A search then moves
-// each image with one hipMemcpyAsync on a side stream into one of two device
-// buffers, while the compute stream searches the previous batch; events
-// order buffer reuse, and no host synchronisation happens inside the loop.
-// Distances are exact on the device (fp32 or u8 data), so the per-batch top
-// K merges into a running top K on the device instead of a host re-rank.
+// index's rows sit in one pinned arena in resident row order, the cross
+// edges target-major (gf_state.h, StreamIndex), so that a batch's image is
+// assembled from a few pieces per run of consecutive cell ids in the batch
+// (the cross edges of a pair of runs in one two-dimensional piece), whatever
+// the plan: the index's build-time plan, or one a query batch makes from its
+// own stage A cell lists, with no re-pack.  Large pieces move by DMA, the
+// rest by one gather kernel that reads the pinned memory over PCIe (one DMA
+// command per piece would cost more than moving the small ones).  The copies
+// run on a side stream into one of two device buffers while the compute
+// stream searches the previous batch; events order buffer reuse, and no host synchronisation
+// happens inside the loop.  Distances are exact on the device (fp32 or u8
+// data), so the per-batch top K merges into a running top K on the device
+// instead of a host re-rank.
 #include <algorithm>
 #include <cstring>
 #include <memory>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "gf_state.h"
@@ -28,6 +34,10 @@ namespace {
 
 constexpr size_t kAlign = 256;
 constexpr uint32_t kStreamTileChunk = 16;   // tiles per MFMA brute-force item on a streamed batch
+constexpr int kCopyCore = 0, kCopyAttrs = 1, kCopyAll = 2;   // sections of a batch image to copy
+// 1-D pieces of at least this many bytes move by DMA (a few us of command
+// overhead each, no CU time); smaller and 2-D ones by k_stream_gather
+constexpr size_t kDmaPiece = size_t(256) << 10;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 uint32_t next_pow2(uint32_t x) {
@@ -36,7 +46,281 @@ uint32_t next_pow2(uint32_t x) {
     return p;
 }
 
+// Runs body(lo, hi) over [0, n) on up to 16 host threads.
+template <class F>
+void parallel_for(size_t n, size_t grain, F&& body) {
+    const size_t hw = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    const size_t nt = std::min(hw, std::max<size_t>(1, n / std::max<size_t>(grain, 1)));
+    if (nt <= 1) {
+        body(size_t(0), n);
+        return;
+    }
+    std::vector<std::thread> th;
+    for (size_t t = 0; t < nt; ++t) th.emplace_back([&, t] { body(n * t / nt, n * (t + 1) / nt); });
+    for (auto& x : th) x.join();
+}
+
+// Device bytes a streamed index holds for turn buffers of `turn` bytes and
+// tile records for `tiles` tiles.
+uint64_t stream_device_need(const gf_index& ix, const StreamIndex& S, size_t turn, size_t tiles) {
+    return 2 * uint64_t(turn) + (S.i8 ? uint64_t(tiles) * bf_rec_bytes(ix.D, S.AW) : 0);
+}
+
 }  // namespace
+
+std::unique_ptr<StreamPlan> make_stream_plan(gf_index& ix, std::vector<std::vector<uint32_t>> cells,
+                                             StreamPlan* reuse) {
+    StreamIndex& S = *ix.sx;
+    const uint32_t P = ix.P, a = ix.a, E = ix.E, R = ix.R;
+    const uint32_t MW = 16 * (1 + S.AW);
+    const SubHost& sh = S.sh;
+    std::unique_ptr<StreamPlan> pl(new StreamPlan());
+    {
+        std::vector<char> seen(P, 0);
+        for (const auto& bt : cells) {
+            GF_REQUIRE(!bt.empty(), GF_E_ARG, "empty batch in the stream plan");
+            for (uint32_t c : bt) {
+                GF_REQUIRE(c < P, GF_E_ARG, "stream plan cell id out of range");
+                GF_REQUIRE(!seen[c], GF_E_ARG, "cell " + std::to_string(c) + " appears twice in the stream plan");
+                seen[c] = 1;
+            }
+        }
+    }
+    size_t head_total = 0;
+    for (const auto& cl : cells) {
+        StreamBatch sb;
+        sb.B = uint32_t(cl.size());
+        uint64_t rows = 0;
+        for (uint32_t c : cl) rows += S.size[c];
+        sb.rows = uint32_t(rows);
+        if (S.i8)
+            for (uint32_t c : cl) {
+                sb.NS += sh.sbase[c + 1] - sh.sbase[c];
+                sb.ntile += sh.stile[sh.sbase[c + 1]] - sh.stile[sh.sbase[c]];
+            }
+        // runs of consecutive cell ids
+        sb.run0 = uint32_t(pl->runs.size());
+        uint32_t r = 0, sbi = 0, tbi = 0;
+        for (uint32_t i = 0; i < sb.B; ++i) {
+            const uint32_t c = cl[i];
+            if (i == 0 || c != cl[i - 1] + 1) {
+                StreamRun u;
+                u.i0 = i;
+                u.c0 = c;
+                u.g0 = ix.offset_h[c];
+                u.r0 = r;
+                if (S.i8) {
+                    u.s0 = sh.sbase[c];
+                    u.sb0 = sbi;
+                    u.t0 = sh.stile[u.s0];
+                    u.tb0 = tbi;
+                }
+                pl->runs.push_back(u);
+            }
+            StreamRun& u = pl->runs.back();
+            ++u.n;
+            u.rows += S.size[c];
+            r += S.size[c];
+            if (S.i8) {
+                const uint32_t ns = sh.sbase[c + 1] - sh.sbase[c];
+                const uint32_t nt = sh.stile[sh.sbase[c + 1]] - sh.stile[sh.sbase[c]];
+                u.ns += ns;
+                u.nt += nt;
+                sbi += ns;
+                tbi += nt;
+            }
+        }
+        sb.nrun = uint32_t(pl->runs.size()) - sb.run0;
+        // image layout
+        size_t o = 0;
+        auto take = [&](size_t bytes) {
+            const size_t at = o;
+            o = align_up(o + bytes);
+            return at;
+        };
+        sb.o_offset = take((size_t(sb.B) + 1) * 4);
+        sb.o_bcell = take(size_t(sb.B) * 4);
+        if (S.i8) {
+            sb.o_sbase = take((size_t(sb.B) + 1) * 4);
+            sb.o_scell = take(size_t(sb.NS) * 4);
+            sb.o_stile = take((size_t(sb.NS) + 1) * 4);
+            sb.o_abase = take(size_t(sb.B) * a * 4);
+        }
+        sb.head = o;
+        if (S.i8) {
+            sb.o_ssize = take(size_t(sb.NS) * 4);
+            sb.o_sbox = take(size_t(sb.NS) * 2 * a * 4);
+            sb.o_tmeta = take(size_t(sb.ntile) * MW * 4);
+        }
+        sb.o_vec = take(rows * ix.rowbytes);
+        sb.o_gidx = take(rows * 4);
+        sb.bytes_mfma = o;
+        sb.o_attrs = take(rows * a * 4);
+        sb.bytes_bf = o;
+        sb.o_graph = take(rows * R * 4);
+        sb.o_lrow = take(rows * 4);
+        sb.o_cross = take(size_t(sb.B) * rows * E * 4);
+        sb.bytes = o;
+        sb.head_off = head_total;
+        head_total += sb.head;
+        pl->max_bytes = std::max(pl->max_bytes, sb.bytes);
+        pl->Bmax = std::max(pl->Bmax, sb.B);
+        pl->NSmax = std::max(pl->NSmax, sb.NS);
+        pl->tmax = std::max(pl->tmax, sb.ntile);
+        pl->batches.push_back(sb);
+    }
+    // room on the device for the plan's largest batch (checked before any
+    // device call)
+    const size_t turn = std::max(S.turn[0].n, pl->max_bytes);
+    const size_t tiles = std::max(S.trec_tiles, size_t(std::max(pl->tmax, 1u)));
+    const bool grow = turn > S.turn[0].n || (S.i8 && tiles > S.trec_tiles);
+    if (grow) {
+        const uint64_t need = stream_device_need(ix, S, turn, tiles);
+        GF_REQUIRE(S.budget == 0 || need <= S.budget, GF_E_UNSUPPORTED,
+                   "the plan's largest batch needs " + std::to_string(need) + " device bytes (two images" +
+                       (S.i8 ? std::string(" and its int8 tiles") : std::string()) + "), over the device budget of " +
+                       std::to_string(S.budget));
+    }
+    GF_HIP(hipSetDevice(ix.device));
+    // headers (in the previous plan's buffers when they are large enough)
+    if (reuse && reuse->head.n >= std::max<size_t>(head_total, 1)) {
+        std::swap(pl->head.p, reuse->head.p);
+        std::swap(pl->head.n, reuse->head.n);
+    } else {
+        pl->head.alloc(std::max<size_t>(head_total, 1), hipHostMallocCoherent);
+    }
+    std::memset(pl->head.p, 0, std::max<size_t>(head_total, 1));
+    for (size_t bi = 0; bi < cells.size(); ++bi) {
+        const auto& cl = cells[bi];
+        const StreamBatch& sb = pl->batches[bi];
+        char* h = pl->head.p + sb.head_off;
+        uint32_t* offset = reinterpret_cast<uint32_t*>(h + sb.o_offset);
+        offset[0] = 0;
+        for (uint32_t i = 0; i < sb.B; ++i) offset[i + 1] = offset[i] + S.size[cl[i]];
+        std::memcpy(h + sb.o_bcell, cl.data(), cl.size() * 4);
+        if (!S.i8) continue;
+        uint32_t* sbase = reinterpret_cast<uint32_t*>(h + sb.o_sbase);
+        uint32_t* scell = reinterpret_cast<uint32_t*>(h + sb.o_scell);
+        uint32_t* stile = reinterpret_cast<uint32_t*>(h + sb.o_stile);
+        int32_t* abase = reinterpret_cast<int32_t*>(h + sb.o_abase);
+        uint32_t ns = 0, nt = 0;
+        for (uint32_t i = 0; i < sb.B; ++i) {
+            const uint32_t c = cl[i];
+            sbase[i] = ns;
+            for (uint32_t d = 0; d < a; ++d) abase[size_t(i) * a + d] = sh.abase[size_t(c) * a + d];
+            for (uint32_t s0 = sh.sbase[c]; s0 < sh.sbase[c + 1]; ++s0, ++ns) {
+                scell[ns] = i;
+                stile[ns] = nt;
+                nt += sh.stile[s0 + 1] - sh.stile[s0];
+            }
+        }
+        sbase[sb.B] = ns;
+        stile[ns] = nt;
+    }
+    // The pieces of each batch image (k_stream_gather), checked against the
+    // image, the arena and the header block.
+    {
+        std::vector<GatherDesc> ds;
+        pl->dma.clear();
+        const size_t arena = S.arena_bytes, rb = ix.rowbytes;
+        for (auto& sb : pl->batches) {
+            sb.desc0 = uint32_t(ds.size());
+            sb.dma0 = uint32_t(pl->dma.size());
+            size_t moved = 0;
+            auto put = [&](uint32_t base, size_t src, size_t dst, size_t width, uint32_t nrow = 1, size_t spitch = 0,
+                           size_t dpitch = 0, uint32_t add = 0, uint32_t mw = 0) {
+                if (!width || !nrow) return;
+                const size_t send = src + (nrow - 1) * spitch + width, dend = dst + (nrow - 1) * dpitch + width;
+                GF_REQUIRE(send <= (base ? head_total : arena) && dend <= sb.bytes && width <= UINT32_MAX, GF_E_STATE,
+                           "internal: a streamed batch piece out of bounds");
+                moved += width * nrow;
+                if (base == 0 && nrow == 1 && !mw && width >= kDmaPiece) {
+                    pl->dma.push_back(StreamCopy{src, dst, width});
+                    return;
+                }
+                GatherDesc g{};
+                g.src = src; g.dst = dst; g.spitch = spitch; g.dpitch = dpitch;
+                g.width = uint32_t(width); g.nrow = nrow; g.base = base; g.add = add; g.mw = mw;
+                ds.push_back(g);
+            };
+            auto level = [&](int w) {
+                sb.ndesc[w] = uint32_t(ds.size()) - sb.desc0;
+                sb.ndma[w] = uint32_t(pl->dma.size()) - sb.dma0;
+                sb.moved[w] = moved;
+            };
+            const StreamRun* runs = pl->runs.data() + sb.run0;
+            put(1, sb.head_off, 0, sb.head);
+            for (uint32_t k = 0; k < sb.nrun; ++k) {
+                const StreamRun& u = runs[k];
+                if (S.i8) {
+                    put(0, S.a_ssize + size_t(u.s0) * 4, sb.o_ssize + size_t(u.sb0) * 4, size_t(u.ns) * 4);
+                    put(0, S.a_sbox + size_t(u.s0) * 2 * a * 4, sb.o_sbox + size_t(u.sb0) * 2 * a * 4,
+                        size_t(u.ns) * 2 * a * 4);
+                    // rows of a run move by one amount: batch row - resident row (mod 2^32)
+                    put(0, S.a_tmeta + size_t(u.t0) * MW * 4, sb.o_tmeta + size_t(u.tb0) * MW * 4, size_t(u.nt) * MW * 4,
+                        1, 0, 0, u.r0 - u.g0, MW);
+                }
+                put(0, S.a_vec + size_t(u.g0) * rb, sb.o_vec + size_t(u.r0) * rb, size_t(u.rows) * rb);
+                put(0, S.a_gidx + size_t(u.g0) * 4, sb.o_gidx + size_t(u.r0) * 4, size_t(u.rows) * 4);
+            }
+            level(0);
+            for (uint32_t k = 0; k < sb.nrun; ++k) {
+                const StreamRun& u = runs[k];
+                put(0, S.a_attrs + size_t(u.g0) * a * 4, sb.o_attrs + size_t(u.r0) * a * 4, size_t(u.rows) * a * 4);
+            }
+            level(1);
+            for (uint32_t k = 0; k < sb.nrun; ++k) {
+                const StreamRun& u = runs[k];
+                put(0, S.a_graph + size_t(u.g0) * R * 4, sb.o_graph + size_t(u.r0) * R * 4, size_t(u.rows) * R * 4);
+                put(0, S.a_lrow + size_t(u.g0) * 4, sb.o_lrow + size_t(u.r0) * 4, size_t(u.rows) * 4);
+                // cross edges of run u's rows into the cells of run v: image rows
+                // (v.i0 + j) * rows + u.r0, arena rows (v.c0 + j) * N + u.g0
+                for (uint32_t k2 = 0; k2 < sb.nrun; ++k2) {
+                    const StreamRun& v = runs[k2];
+                    put(0, S.a_cross + (size_t(v.c0) * S.rows + u.g0) * E * 4,
+                        sb.o_cross + (size_t(v.i0) * sb.rows + u.r0) * E * 4, size_t(u.rows) * E * 4, v.n,
+                        size_t(S.rows) * E * 4, size_t(sb.rows) * E * 4);
+                }
+            }
+            level(2);
+        }
+        if (ds.empty()) ds.push_back(GatherDesc{});
+        if (reuse && reuse->desc.n >= ds.size()) {
+            std::swap(pl->desc.p, reuse->desc.p);
+            std::swap(pl->desc.n, reuse->desc.n);
+        } else {
+            pl->desc.alloc(ds.size());
+        }
+        GF_HIP(hipMemcpy(pl->desc.p, ds.data(), ds.size() * sizeof(GatherDesc), hipMemcpyHostToDevice));
+    }
+    {
+        // sized for any plan (P cells, P batches) so that a later plan reuses them
+        std::vector<uint32_t> pc, po(1, 0);
+        for (const auto& cl : cells) {
+            pc.insert(pc.end(), cl.begin(), cl.end());
+            po.push_back(uint32_t(pc.size()));
+        }
+        if (reuse && reuse->plan_cells.n == size_t(P) + 1 && reuse->plan_off.n == size_t(P) + 1) {
+            std::swap(pl->plan_cells.p, reuse->plan_cells.p);
+            std::swap(pl->plan_cells.n, reuse->plan_cells.n);
+            std::swap(pl->plan_off.p, reuse->plan_off.p);
+            std::swap(pl->plan_off.n, reuse->plan_off.n);
+        } else {
+            pl->plan_cells.alloc(size_t(P) + 1);
+            pl->plan_off.alloc(size_t(P) + 1);
+        }
+        if (!pc.empty()) GF_HIP(hipMemcpy(pl->plan_cells.p, pc.data(), pc.size() * 4, hipMemcpyHostToDevice));
+        GF_HIP(hipMemcpy(pl->plan_off.p, po.data(), po.size() * 4, hipMemcpyHostToDevice));
+    }
+    if (turn > S.turn[0].n)
+        for (int t = 0; t < 2; ++t) S.turn[t].alloc(turn);
+    if (S.i8 && tiles > S.trec_tiles) {
+        S.trec.alloc(tiles * bf_rec_bytes(ix.D, S.AW));
+        S.trec_tiles = tiles;
+    }
+    pl->cells = std::move(cells);
+    return pl;
+}
 
 void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_stream_plan* plan, gf_index& ix) {
     GF_REQUIRE(plan, GF_E_ARG, "null stream plan");
@@ -44,9 +328,10 @@ void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_s
     map_cells(h, opts, ix, size, gidx, lrow);
     GF_REQUIRE(ix.vdtype != GF_VEC_F16 && ix.vdtype != GF_VEC_I8Q && ix.vdtype != GF_VEC_F16_REF, GF_E_UNSUPPORTED,
                "a streamed index holds GF_VEC_F32 or GF_VEC_U8 vectors");
-    const uint32_t P = ix.P, R = ix.R, E = ix.E, a = ix.a, D = ix.D, N = ix.N;
+    const uint32_t P = ix.P, R = ix.R, E = ix.E, a = ix.a, D = ix.D;
+    const uint32_t N = ix.offset_h[P];
 
-    // The static plan: explicit batches, or consecutive cells.
+    // The build-time plan: explicit batches, or consecutive cells.
     std::vector<std::vector<uint32_t>> plan_cells;
     if (plan->nbatch == 0) {
         const uint32_t bc = plan->batch_cells ? plan->batch_cells : 16u;
@@ -57,177 +342,107 @@ void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_s
         }
     } else {
         GF_REQUIRE(plan->sizes && plan->cells, GF_E_ARG, "stream plan without sizes or cells");
-        std::vector<char> seen(P, 0);
         size_t k = 0;
         for (uint32_t i = 0; i < plan->nbatch; ++i) {
             GF_REQUIRE(plan->sizes[i] >= 1, GF_E_ARG, "empty batch in the stream plan");
-            std::vector<uint32_t> v;
-            for (uint32_t j = 0; j < plan->sizes[i]; ++j, ++k) {
-                const uint32_t c = plan->cells[k];
-                GF_REQUIRE(c < P, GF_E_ARG, "stream plan cell id out of range");
-                GF_REQUIRE(!seen[c], GF_E_ARG, "cell " + std::to_string(c) + " appears twice in the stream plan");
-                seen[c] = 1;
-                v.push_back(c);
-            }
-            plan_cells.push_back(v);
+            GF_REQUIRE(plan->sizes[i] <= P, GF_E_ARG, "stream plan batch larger than the grid");
+            plan_cells.emplace_back(plan->cells + k, plan->cells + k + plan->sizes[i]);
+            k += plan->sizes[i];
         }
     }
 
     std::unique_ptr<StreamIndex> sx(new StreamIndex());
-    sx->budget = plan->device_budget;
+    StreamIndex& S = *sx;
+    S.budget = plan->device_budget;
+    S.rows = N;
+    S.size = size;
     // Sub-cells for the MFMA brute force (u8 vectors, D a multiple of 64 up to 256).
-    SubHost sh;
-    sx->i8 = ix.vdtype == GF_VEC_U8 && D % 64 == 0 && D <= 256 &&
-             compute_subcells(h, gidx, size, ix.offset_h, a, P, sh);
-    sx->AW = sh.AW;
-    const uint32_t MW = 16 * (1 + sh.AW);
-    size_t total = 0;
-    for (const auto& cl : plan_cells) {
-        StreamBatch sb;
-        sb.B = uint32_t(cl.size());
-        uint64_t rows = 0;
-        for (uint32_t c : cl) rows += size[c];
-        sb.rows = uint32_t(rows);
-        if (sx->i8)
-            for (uint32_t c : cl) {
-                sb.NS += sh.sbase[c + 1] - sh.sbase[c];
-                sb.ntile += sh.stile[sh.sbase[c + 1]] - sh.stile[sh.sbase[c]];
-            }
-        sb.o_vec = 0;
-        sb.o_gidx = align_up(sb.o_vec + rows * ix.rowbytes);
-        sb.o_offset = align_up(sb.o_gidx + rows * 4);
-        sb.o_bcell = align_up(sb.o_offset + (size_t(sb.B) + 1) * 4);
-        size_t end = sb.o_bcell + size_t(sb.B) * 4;
-        if (sx->i8) {
-            sb.o_sbase = align_up(end);
-            sb.o_scell = align_up(sb.o_sbase + (size_t(sb.B) + 1) * 4);
-            sb.o_ssize = align_up(sb.o_scell + size_t(sb.NS) * 4);
-            sb.o_stile = align_up(sb.o_ssize + size_t(sb.NS) * 4);
-            sb.o_sbox = align_up(sb.o_stile + (size_t(sb.NS) + 1) * 4);
-            sb.o_abase = align_up(sb.o_sbox + size_t(sb.NS) * 2 * a * 4);
-            sb.o_tmeta = align_up(sb.o_abase + size_t(sb.B) * a * 4);
-            end = sb.o_tmeta + size_t(sb.ntile) * MW * 4;
-        }
-        sb.bytes_mfma = align_up(end);
-        sb.o_attrs = sb.bytes_mfma;
-        sb.bytes_bf = align_up(sb.o_attrs + rows * a * 4);
-        sb.o_graph = sb.bytes_bf;
-        sb.o_lrow = align_up(sb.o_graph + rows * R * 4);
-        sb.o_cross = align_up(sb.o_lrow + rows * 4);
-        sb.bytes = align_up(sb.o_cross + size_t(sb.B) * rows * E * 4);
-        sb.host_off = total;
-        total += sb.bytes;
-        sx->max_bytes = std::max(sx->max_bytes, sb.bytes);
-        sx->Bmax = std::max(sx->Bmax, sb.B);
-        sx->NSmax = std::max(sx->NSmax, sb.NS);
-        sx->tmax = std::max(sx->tmax, sb.ntile);
-        sx->batches.push_back(sb);
-    }
-    const size_t tile_bytes = size_t(D / 64) * 1024 + 32 * 4;
-    const uint64_t need = 2 * uint64_t(sx->max_bytes) + (sx->i8 ? uint64_t(sx->tmax) * tile_bytes : 0);
-    GF_REQUIRE(sx->budget == 0 || need <= sx->budget, GF_E_UNSUPPORTED,
-               "the largest batch needs " + std::to_string(need) + " device bytes (two images" +
-                   (sx->i8 ? std::string(" and its int8 tiles") : std::string()) + "), over the device budget of " +
-                   std::to_string(sx->budget));
-    sx->min_cell = 0;
+    S.i8 = ix.vdtype == GF_VEC_U8 && D % 64 == 0 && D <= 256 &&
+           compute_subcells(h, gidx, size, ix.offset_h, a, P, S.sh);
+    S.AW = S.sh.AW;
+    const uint32_t MW = 16 * (1 + S.AW);
+    S.min_cell = 0;
     for (uint32_t c = 0; c < P; ++c)
-        if (size[c] && (sx->min_cell == 0 || size[c] < sx->min_cell)) sx->min_cell = size[c];
+        if (size[c] && (S.min_cell == 0 || size[c] < S.min_cell)) S.min_cell = size[c];
 
+    // The arena.
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o = align_up(o + bytes);
+        return at;
+    };
+    S.a_vec = take(size_t(N) * ix.rowbytes);
+    S.a_gidx = take(size_t(N) * 4);
+    S.a_attrs = take(size_t(N) * a * 4);
+    S.a_graph = take(size_t(N) * R * 4);
+    S.a_lrow = take(size_t(N) * 4);
+    S.a_cross = take(size_t(P) * N * E * 4);
+    if (S.i8) {
+        S.a_ssize = take(size_t(S.sh.NS) * 4);
+        S.a_sbox = take(size_t(S.sh.NS) * 2 * a * 4);
+        S.a_tmeta = take(size_t(S.sh.ntile) * MW * 4);
+    }
+
+    S.arena_bytes = o;
+    ix.sx = std::move(sx);
+    // the build-time plan sizes the device buffers (and checks the plan and
+    // the budget before any device call)
+    S.plan = make_stream_plan(ix, std::move(plan_cells), nullptr);
     GF_HIP(hipSetDevice(ix.device));
-    sx->host.alloc(total);
-    // Pack the images.
-    for (size_t bi = 0; bi < plan_cells.size(); ++bi) {
-        const auto& cl = plan_cells[bi];
-        const StreamBatch& sb = sx->batches[bi];
-        char* img = sx->host.p + sb.host_off;
-        std::memset(img, 0, sb.bytes);
-        std::vector<uint32_t> boff(sb.B + 1, 0);
-        for (uint32_t i = 0; i < sb.B; ++i) boff[i + 1] = boff[i] + size[cl[i]];
-        uint32_t* g_graph = reinterpret_cast<uint32_t*>(img + sb.o_graph);
-        float* g_attrs = reinterpret_cast<float*>(img + sb.o_attrs);
-        uint32_t* g_gidx = reinterpret_cast<uint32_t*>(img + sb.o_gidx);
-        uint32_t* g_lrow = reinterpret_cast<uint32_t*>(img + sb.o_lrow);
-        uint32_t* g_cross = reinterpret_cast<uint32_t*>(img + sb.o_cross);
-        for (uint32_t i = 0; i < sb.B; ++i) {
-            const uint32_t c = cl[i], n = size[c], r0 = ix.offset_h[c];
-            std::memcpy(g_graph + size_t(boff[i]) * R, h.cell_graphs + size_t(r0) * R, size_t(n) * R * 4);
-            for (uint32_t l = 0; l < n; ++l) {
-                const uint32_t r = boff[i] + l, pt = gidx[r0 + l];
-                const float* x = h.vectors + size_t(pt) * D;
-                if (ix.vdtype == GF_VEC_U8) {
-                    uint8_t* y = reinterpret_cast<uint8_t*>(img + sb.o_vec) + size_t(r) * ix.rowbytes;
-                    for (uint32_t j = 0; j < D; ++j) y[j] = uint8_t(x[j]);
-                } else {
-                    std::memcpy(img + sb.o_vec + size_t(r) * ix.rowbytes, x, size_t(D) * 4);
-                }
-                for (uint32_t d = 0; d < a; ++d) g_attrs[size_t(r) * a + d] = h.attrs[size_t(pt) * a + d];
-                g_gidx[r] = pt;
-                g_lrow[r] = l;
-                for (uint32_t t = 0; t < sb.B; ++t)
-                    for (uint32_t e = 0; e < E; ++e)
-                        g_cross[(size_t(t) * sb.rows + r) * E + e] = h.cross[(size_t(pt) * P + cl[t]) * E + e];
-            }
-        }
-        std::memcpy(img + sb.o_offset, boff.data(), boff.size() * 4);
-        std::memcpy(img + sb.o_bcell, cl.data(), cl.size() * 4);
-        if (sx->i8) {
-            uint32_t* g_sbase = reinterpret_cast<uint32_t*>(img + sb.o_sbase);
-            uint32_t* g_scell = reinterpret_cast<uint32_t*>(img + sb.o_scell);
-            uint32_t* g_ssize = reinterpret_cast<uint32_t*>(img + sb.o_ssize);
-            uint32_t* g_stile = reinterpret_cast<uint32_t*>(img + sb.o_stile);
-            int32_t* g_sbox = reinterpret_cast<int32_t*>(img + sb.o_sbox);
-            int32_t* g_abase = reinterpret_cast<int32_t*>(img + sb.o_abase);
-            uint32_t* g_tmeta = reinterpret_cast<uint32_t*>(img + sb.o_tmeta);
-            uint32_t ns = 0, nt = 0;
-            for (uint32_t i = 0; i < sb.B; ++i) {
-                const uint32_t c = cl[i];
-                g_sbase[i] = ns;
-                for (uint32_t d = 0; d < a; ++d) g_abase[size_t(i) * a + d] = sh.abase[size_t(c) * a + d];
-                for (uint32_t s0 = sh.sbase[c]; s0 < sh.sbase[c + 1]; ++s0, ++ns) {
-                    g_scell[ns] = i;
-                    g_ssize[ns] = sh.ssize[s0];
-                    g_stile[ns] = nt;
-                    for (uint32_t k = 0; k < 2 * a; ++k) g_sbox[size_t(ns) * 2 * a + k] = sh.sbox[size_t(s0) * 2 * a + k];
-                    for (uint32_t t = sh.stile[s0]; t < sh.stile[s0 + 1]; ++t, ++nt) {
-                        const uint32_t* src = &sh.tmeta[size_t(t) * MW];
-                        uint32_t* dst = g_tmeta + size_t(nt) * MW;
-                        std::memcpy(dst, src, MW * 4);
-                        for (uint32_t j = 0; j < 16; ++j)   // rows become batch rows
-                            if (src[j] != 0xFFFFFFFFu) dst[j] = src[j] - ix.offset_h[c] + boff[i];
-                    }
-                }
-            }
-            g_sbase[sb.B] = ns;
-            g_stile[ns] = nt;
-        }
+    GF_HIP(hipStreamCreateWithFlags(&ix.stream, hipStreamNonBlocking));
+    GF_HIP(hipStreamCreateWithFlags(&S.copy, hipStreamNonBlocking));
+    for (int t = 0; t < 2; ++t) {
+        GF_HIP(hipEventCreateWithFlags(&S.ready[t], hipEventDisableTiming));
+        GF_HIP(hipEventCreateWithFlags(&S.freed[t], hipEventDisableTiming));
     }
 
-    GF_HIP(hipStreamCreateWithFlags(&ix.stream, hipStreamNonBlocking));
-    GF_HIP(hipStreamCreateWithFlags(&sx->copy, hipStreamNonBlocking));
-    for (int t = 0; t < 2; ++t) {
-        GF_HIP(hipEventCreateWithFlags(&sx->ready[t], hipEventDisableTiming));
-        GF_HIP(hipEventCreateWithFlags(&sx->freed[t], hipEventDisableTiming));
-        sx->turn[t].alloc(sx->max_bytes);
-    }
-    {
-        std::vector<uint32_t> pc, po(1, 0);
-        for (const auto& cl : plan_cells) {
-            pc.insert(pc.end(), cl.begin(), cl.end());
-            po.push_back(uint32_t(pc.size()));
+    S.host.alloc(std::max<size_t>(S.arena_bytes, 1), hipHostMallocCoherent);
+    char* A = S.host.p;
+    parallel_for(N, 4096, [&](size_t lo, size_t hi) {
+        for (size_t g = lo; g < hi; ++g) {
+            const uint32_t pt = gidx[g];
+            const float* x = h.vectors + size_t(pt) * D;
+            if (ix.vdtype == GF_VEC_U8) {
+                uint8_t* y = reinterpret_cast<uint8_t*>(A + S.a_vec) + g * ix.rowbytes;
+                for (uint32_t j = 0; j < D; ++j) y[j] = uint8_t(x[j]);
+            } else {
+                std::memcpy(A + S.a_vec + g * ix.rowbytes, x, size_t(D) * 4);
+            }
+            float* at = reinterpret_cast<float*>(A + S.a_attrs) + g * a;
+            for (uint32_t d = 0; d < a; ++d) at[d] = h.attrs[size_t(pt) * a + d];
         }
-        if (pc.empty()) pc.push_back(0);
-        sx->plan_cells.upload(pc);
-        sx->plan_off.upload(po);
-    }
-    if (sx->i8) {
-        sx->trec.alloc(size_t(std::max(sx->tmax, 1u)) * bf_rec_bytes(D, sx->AW));
+    });
+    std::memcpy(A + S.a_gidx, gidx.data(), size_t(N) * 4);
+    std::memcpy(A + S.a_graph, h.cell_graphs, size_t(N) * R * 4);
+    std::memcpy(A + S.a_lrow, lrow.data(), size_t(N) * 4);
+    // cross edges, point-major in the input, target-major in the arena;
+    // blocks of rows so that a block's input rows stay in cache
+    parallel_for((size_t(N) + 255) / 256, 4, [&](size_t lo, size_t hi) {
+        uint32_t* X = reinterpret_cast<uint32_t*>(A + S.a_cross);
+        for (size_t blk = lo; blk < hi; ++blk) {
+            const size_t g0 = blk * 256, g1 = std::min<size_t>(N, g0 + 256);
+            for (uint32_t c = 0; c < P; ++c)
+                for (size_t g = g0; g < g1; ++g)
+                    for (uint32_t e = 0; e < E; ++e)
+                        X[(size_t(c) * N + g) * E + e] = h.cross[(size_t(gidx[g]) * P + c) * E + e];
+        }
+    });
+    if (S.i8) {
+        std::memcpy(A + S.a_ssize, S.sh.ssize.data(), S.sh.ssize.size() * 4);
+        std::memcpy(A + S.a_sbox, S.sh.sbox.data(), S.sh.sbox.size() * 4);
+        std::memcpy(A + S.a_tmeta, S.sh.tmeta.data(), S.sh.tmeta.size() * 4);
+        // the plans need the offsets only
+        std::vector<uint32_t>().swap(S.sh.ssize);
+        std::vector<int32_t>().swap(S.sh.sbox);
+        std::vector<uint32_t>().swap(S.sh.tmeta);
+        std::vector<uint32_t>().swap(S.sh.sorder);
+        std::vector<uint32_t>().swap(S.sh.scell);
         ix.i8 = true;   // gf_batch_create keeps int8 queries
     }
     GF_HIP(hipDeviceGetAttribute(&ix.ncu, hipDeviceAttributeMultiprocessorCount, ix.device));
     ix.offset.upload(ix.offset_h);
     ix.grid.upload(ix.grid_h);
-    ix.sx = std::move(sx);
-    (void)N;
 }
 
 // Batch plan from a query batch's cell lists: the out-of-core pipeline's
@@ -253,31 +468,21 @@ void build_streamed(const gf_index_host& h, const gf_open_opts* opts, const gf_s
 // recursion order (lower part first), empty leaves dropped.  A query's
 // lists are read as their bounding box; the returned objective is recounted
 // from the lists themselves.
-namespace {
-
-struct PlanBox {
-    uint32_t x0[kMaxAttr], x1[kMaxAttr];
-};
-
-}  // namespace
-
 uint64_t plan_cells(const uint32_t* cells, const uint32_t* counts, uint32_t Q, uint32_t a, const uint32_t* grid,
                     const uint32_t* cell_size, uint64_t max_points, uint32_t max_cells,
                     std::vector<std::vector<uint32_t>>& plan) {
     GF_REQUIRE(a >= 1 && a <= kMaxAttr, GF_E_ARG, "plan_cells: attribute count out of range");
     uint64_t P = 1, nbox = 1;
-    uint32_t stride[kMaxAttr], bstride[kMaxAttr];
+    uint32_t stride[kMaxAttr];
     for (uint32_t d = 0; d < a; ++d) {
         GF_REQUIRE(grid[d] >= 1, GF_E_ARG, "plan_cells: empty grid axis");
         P *= grid[d];
         nbox *= uint64_t(grid[d]) * grid[d];
         GF_REQUIRE(nbox <= (uint64_t(1) << 22), GF_E_UNSUPPORTED, "plan_cells: grid too large to plan (more than 2^22 box slots)");
     }
-    for (int d = int(a) - 1, s = 1, bs = 1; d >= 0; --d) {
+    for (int d = int(a) - 1, s = 1; d >= 0; --d) {
         stride[d] = uint32_t(s);
-        bstride[d] = uint32_t(bs);
         s *= int(grid[d]);
-        bs *= int(grid[d] * grid[d]);
     }
     // Each query's box (bounding box of its listed cells).
     std::vector<uint32_t> qlo, qhi;   // Qb x a
@@ -301,151 +506,7 @@ uint64_t plan_cells(const uint32_t* cells, const uint32_t* counts, uint32_t Q, u
         qlo.insert(qlo.end(), lo, lo + a);
         qhi.insert(qhi.end(), hi, hi + a);
     }
-    const size_t Qb = qlo.size() / a;
-    // cut(X, d, t).  Two attributes: per (d, t) a table over the other
-    // axis' [x0, x1] of the straddling queries whose interval meets it
-    // (prefix sums of a (lo, hi) histogram); one attribute: the straddle
-    // count; more: a scan of the straddling queries.
-    std::vector<std::vector<std::vector<uint32_t>>> strad(a);   // [d][t] query indices
-    std::vector<std::vector<std::vector<uint64_t>>> tab(a);     // [d][t] table (a <= 2)
-    for (uint32_t d = 0; d < a; ++d) {
-        strad[d].resize(grid[d]);
-        tab[d].resize(grid[d]);
-        for (size_t q = 0; q < Qb; ++q)
-            for (uint32_t t = qlo[q * a + d] + 1; t <= qhi[q * a + d]; ++t) strad[d][t].push_back(uint32_t(q));
-        if (a > 2) continue;
-        const uint32_t e = 1 - d, ge = a == 2 ? grid[e] : 1;
-        for (uint32_t t = 1; t < grid[d]; ++t) {
-            std::vector<uint64_t> h(size_t(ge) * ge, 0), T(size_t(ge) * ge, 0);
-            for (uint32_t q : strad[d][t]) {
-                if (a == 2) ++h[size_t(qlo[q * a + e]) * ge + qhi[q * a + e]];
-                else ++h[0];
-            }
-            // T[x0 * ge + x1] = #{lo <= x1, hi >= x0}
-            for (uint32_t x0 = 0; x0 < ge; ++x0)
-                for (uint32_t x1 = x0; x1 < ge; ++x1) {
-                    uint64_t n = 0;
-                    for (uint32_t lo = 0; lo <= x1; ++lo)
-                        for (uint32_t hi = std::max(lo, x0); hi < ge; ++hi) n += h[size_t(lo) * ge + hi];
-                    T[size_t(x0) * ge + x1] = n;
-                }
-            tab[d][t] = std::move(T);
-        }
-    }
-    auto cut = [&](const PlanBox& X, uint32_t d, uint32_t t) -> uint64_t {
-        if (a == 1) return tab[d][t][0];
-        if (a == 2) {
-            const uint32_t e = 1 - d;
-            return tab[d][t][size_t(X.x0[e]) * grid[e] + X.x1[e]];
-        }
-        uint64_t n = 0;
-        for (uint32_t q : strad[d][t]) {
-            bool meets = true;
-            for (uint32_t e = 0; e < a && meets; ++e)
-                if (e != d) meets = qlo[q * a + e] <= X.x1[e] && qhi[q * a + e] >= X.x0[e];
-            n += meets;
-        }
-        return n;
-    };
-    auto index = [&](const PlanBox& X) {
-        size_t i = 0;
-        for (uint32_t d = 0; d < a; ++d) i += size_t(X.x0[d] * grid[d] + X.x1[d]) * bstride[d];
-        return i;
-    };
-    // Every box, smaller extents first (both parts of a cut come before it).
-    std::vector<PlanBox> boxes;
-    {
-        PlanBox X{};
-        std::vector<uint32_t> pos(a, 0);   // enumerate (x0, x1) pairs per axis
-        std::vector<std::vector<std::pair<uint32_t, uint32_t>>> iv(a);
-        for (uint32_t d = 0; d < a; ++d)
-            for (uint32_t x0 = 0; x0 < grid[d]; ++x0)
-                for (uint32_t x1 = x0; x1 < grid[d]; ++x1) iv[d].push_back({x0, x1});
-        for (;;) {
-            for (uint32_t d = 0; d < a; ++d) { X.x0[d] = iv[d][pos[d]].first; X.x1[d] = iv[d][pos[d]].second; }
-            boxes.push_back(X);
-            uint32_t d = 0;
-            while (d < a && ++pos[d] == iv[d].size()) pos[d++] = 0;
-            if (d == a) break;
-        }
-        auto ext = [&](const PlanBox& B) {
-            uint32_t s = 0;
-            for (uint32_t d = 0; d < a; ++d) s += B.x1[d] - B.x0[d];
-            return s;
-        };
-        std::stable_sort(boxes.begin(), boxes.end(), [&](const PlanBox& u, const PlanBox& v) { return ext(u) < ext(v); });
-    }
-    std::vector<uint64_t> cost(nbox, 0), npts(nbox, 0);
-    std::vector<uint32_t> nleaf(nbox, 0), ncell(nbox, 0), split(nbox, 0);   // split: 0 = leaf, else d * 65536 + t
-    auto halves = [&](const PlanBox& X, uint32_t d, uint32_t t, PlanBox& A, PlanBox& B) {
-        A = X;
-        B = X;
-        A.x1[d] = t - 1;
-        B.x0[d] = t;
-    };
-    for (const PlanBox& X : boxes) {
-        const size_t i = index(X);
-        uint32_t d0 = a;
-        for (uint32_t d = 0; d < a; ++d)
-            if (X.x1[d] > X.x0[d]) { d0 = d; break; }
-        if (d0 == a) {   // one cell
-            uint32_t c = 0;
-            for (uint32_t d = 0; d < a; ++d) c += X.x0[d] * stride[d];
-            npts[i] = cell_size[c];
-            ncell[i] = cell_size[c] ? 1u : 0u;
-            nleaf[i] = ncell[i];
-            continue;
-        }
-        PlanBox A, B;
-        halves(X, d0, X.x0[d0] + 1, A, B);
-        npts[i] = npts[index(A)] + npts[index(B)];
-        ncell[i] = ncell[index(A)] + ncell[index(B)];
-        if ((max_cells == 0 || ncell[i] <= max_cells) && (max_points == 0 || npts[i] <= max_points)) {
-            nleaf[i] = ncell[i] ? 1u : 0u;
-            continue;
-        }
-        bool have = false;
-        for (uint32_t d = 0; d < a; ++d)
-            for (uint32_t t = X.x0[d] + 1; t <= X.x1[d]; ++t) {
-                halves(X, d, t, A, B);
-                const size_t ia = index(A), ib = index(B);
-                const uint64_t c = cut(X, d, t) + cost[ia] + cost[ib];
-                const uint32_t l = nleaf[ia] + nleaf[ib];
-                if (!have || c < cost[i] || (c == cost[i] && l < nleaf[i])) {
-                    have = true;
-                    cost[i] = c;
-                    nleaf[i] = l;
-                    split[i] = d * 65536u + t;
-                }
-            }
-    }
-    plan.clear();
-    std::vector<PlanBox> stack;
-    PlanBox all{};
-    for (uint32_t d = 0; d < a; ++d) { all.x0[d] = 0; all.x1[d] = grid[d] - 1; }
-    stack.push_back(all);
-    while (!stack.empty()) {
-        const PlanBox X = stack.back();
-        stack.pop_back();
-        const size_t i = index(X);
-        if (split[i]) {
-            PlanBox A, B;
-            halves(X, split[i] / 65536u, split[i] % 65536u, A, B);
-            stack.push_back(B);   // lower part first
-            stack.push_back(A);
-            continue;
-        }
-        std::vector<uint32_t> batch;
-        for (uint32_t c = 0; c < P; ++c) {
-            bool in = cell_size[c] > 0;
-            for (uint32_t d = 0; d < a && in; ++d) {
-                const uint32_t x = c / stride[d] % grid[d];
-                in = x >= X.x0[d] && x <= X.x1[d];
-            }
-            if (in) batch.push_back(c);
-        }
-        if (!batch.empty()) plan.push_back(std::move(batch));
-    }
+    plan_boxes(qlo, qhi, a, grid, cell_size, max_points, max_cells, plan);
     uint64_t total = 0;
     std::vector<uint64_t> act(W);
     for (const auto& bt : plan) {
@@ -457,10 +518,287 @@ uint64_t plan_cells(const uint32_t* cells, const uint32_t* counts, uint32_t Q, u
     return total;
 }
 
+namespace {
+
+// Grid coordinates of box i: (x0, x1) per axis; false for an empty slot
+// (x0 > x1).
+inline bool box_coords(const PlanFrame& F, size_t i, uint32_t* x0, uint32_t* x1) {
+    for (uint32_t d = 0; d < F.a; ++d) {
+        const uint32_t g = F.grid[d], v = uint32_t((i / F.bstride[d]) % (size_t(g) * g));
+        x0[d] = v / g;
+        x1[d] = v % g;
+        if (x0[d] > x1[d]) return false;
+    }
+    return true;
+}
+
+void build_frame(PlanFrame& F, uint32_t a, const uint32_t* grid, const uint32_t* cell_size, uint64_t max_points,
+                 uint32_t max_cells) {
+    F.a = a;
+    F.grid.assign(grid, grid + a);
+    F.max_points = max_points;
+    F.max_cells = max_cells;
+    F.nbox = 1;
+    for (uint32_t d = 0; d < a; ++d) F.nbox *= size_t(grid[d]) * grid[d];
+    for (int d = int(a) - 1, s = 1, bs = 1; d >= 0; --d) {
+        F.stride[d] = uint32_t(s);
+        F.bstride[d] = uint32_t(bs);
+        s *= int(grid[d]);
+        bs *= int(grid[d] * grid[d]);
+    }
+    // boxes by total extent (counting sort): both parts of a cut come first
+    uint32_t emax = 0;
+    for (uint32_t d = 0; d < a; ++d) emax += grid[d] - 1;
+    std::vector<uint32_t> ext(F.nbox, UINT32_MAX), count(emax + 2, 0);
+    uint32_t x0[kMaxAttr], x1[kMaxAttr];
+    for (size_t i = 0; i < F.nbox; ++i) {
+        if (!box_coords(F, i, x0, x1)) continue;
+        uint32_t e = 0;
+        for (uint32_t d = 0; d < a; ++d) e += x1[d] - x0[d];
+        ext[i] = e;
+        ++count[e + 1];
+    }
+    for (uint32_t e = 1; e <= emax + 1; ++e) count[e] += count[e - 1];
+    std::vector<uint32_t> byext(count[emax + 1]);
+    for (size_t i = 0; i < F.nbox; ++i)
+        if (ext[i] != UINT32_MAX) byext[count[ext[i]]++] = uint32_t(i);
+    std::vector<uint64_t> npts(F.nbox, 0);
+    std::vector<uint32_t> ncell(F.nbox, 0);
+    F.leaf.assign(F.nbox, 0);
+    F.order.clear();
+    for (uint32_t i : byext) {
+        box_coords(F, i, x0, x1);
+        uint32_t d0 = a;
+        for (uint32_t d = 0; d < a; ++d)
+            if (x1[d] > x0[d]) { d0 = d; break; }
+        if (d0 == a) {   // one cell
+            uint32_t c = 0;
+            for (uint32_t d = 0; d < a; ++d) c += x0[d] * F.stride[d];
+            npts[i] = cell_size[c];
+            ncell[i] = cell_size[c] ? 1u : 0u;
+            F.leaf[i] = uint8_t(ncell[i]);
+            continue;
+        }
+        // the slab x0 of axis d0 and the rest
+        const size_t ia = i - size_t(x1[d0] - x0[d0]) * F.bstride[d0];
+        const size_t ib = i + size_t(grid[d0]) * F.bstride[d0];
+        npts[i] = npts[ia] + npts[ib];
+        ncell[i] = ncell[ia] + ncell[ib];
+        if ((max_cells == 0 || ncell[i] <= max_cells) && (max_points == 0 || npts[i] <= max_points)) {
+            F.leaf[i] = ncell[i] ? 1u : 0u;
+        } else {
+            F.leaf[i] = 2;
+            F.order.push_back(i);
+        }
+    }
+}
+
+}  // namespace
+
+void plan_boxes(const std::vector<uint32_t>& qlo, const std::vector<uint32_t>& qhi, uint32_t a, const uint32_t* grid,
+                const uint32_t* cell_size, uint64_t max_points, uint32_t max_cells,
+                std::vector<std::vector<uint32_t>>& plan, std::unique_ptr<PlanFrame>* cache) {
+    GF_REQUIRE(a >= 1 && a <= kMaxAttr, GF_E_ARG, "plan_cells: attribute count out of range");
+    GF_REQUIRE(qlo.size() == qhi.size() && qlo.size() % a == 0, GF_E_ARG, "plan_cells: malformed query boxes");
+    uint64_t nbox = 1;
+    for (uint32_t d = 0; d < a; ++d) {
+        GF_REQUIRE(grid[d] >= 1, GF_E_ARG, "plan_cells: empty grid axis");
+        nbox *= uint64_t(grid[d]) * grid[d];
+        GF_REQUIRE(nbox <= (uint64_t(1) << 22), GF_E_UNSUPPORTED, "plan_cells: grid too large to plan (more than 2^22 box slots)");
+    }
+    for (size_t k = 0; k < qlo.size(); ++k)
+        GF_REQUIRE(qlo[k] <= qhi[k] && qhi[k] < grid[k % a], GF_E_ARG, "plan_cells: query box outside the grid");
+    std::unique_ptr<PlanFrame> local;
+    std::unique_ptr<PlanFrame>& slot = cache ? *cache : local;
+    if (!slot || slot->a != a || !std::equal(grid, grid + a, slot->grid.begin()) || slot->max_points != max_points ||
+        slot->max_cells != max_cells) {
+        slot.reset(new PlanFrame());
+        build_frame(*slot, a, grid, cell_size, max_points, max_cells);
+    }
+    const PlanFrame& F = *slot;
+    const size_t Qb = qlo.size() / a;
+    // cut(X, d, t).  One attribute: the queries straddling t; two: per (d,
+    // t) a table over the other axis' [x0, x1] of the straddling queries
+    // whose interval meets it (suffix sums over hi, prefix sums over lo of a
+    // (lo, hi) histogram); more: a scan of the straddling queries.
+    std::vector<std::vector<std::vector<uint32_t>>> strad(a);   // [d][t] query indices (a > 2)
+    std::vector<std::vector<uint64_t>> tab(a);                  // [d] (t * ge + x0) * ge + x1 (a <= 2)
+    for (uint32_t d = 0; d < a; ++d) {
+        const uint32_t e = a == 2 ? 1 - d : d, ge = a == 2 ? grid[e] : 1;
+        if (a > 2) {
+            strad[d].resize(grid[d]);
+            for (size_t q = 0; q < Qb; ++q)
+                for (uint32_t t = qlo[q * a + d] + 1; t <= qhi[q * a + d]; ++t) strad[d][t].push_back(uint32_t(q));
+            continue;
+        }
+        std::vector<uint64_t>& T = tab[d];
+        T.assign(size_t(grid[d]) * ge * ge, 0);
+        // histogram of straddlers per t over (lo_e, hi_e)
+        for (size_t q = 0; q < Qb; ++q) {
+            const size_t key = a == 2 ? size_t(qlo[q * a + e]) * ge + qhi[q * a + e] : 0;
+            for (uint32_t t = qlo[q * a + d] + 1; t <= qhi[q * a + d]; ++t) ++T[size_t(t) * ge * ge + key];
+        }
+        std::vector<uint64_t> h(size_t(ge) * ge);
+        for (uint32_t t = 1; t < grid[d]; ++t) {
+            uint64_t* Tt = &T[size_t(t) * ge * ge];
+            std::copy(Tt, Tt + size_t(ge) * ge, h.begin());
+            // T[x0 * ge + x1] = #{lo <= x1, hi >= x0}
+            for (uint32_t lo = 0; lo < ge; ++lo)
+                for (uint32_t hi = ge - 1; hi-- > 0;) h[size_t(lo) * ge + hi] += h[size_t(lo) * ge + hi + 1];
+            for (uint32_t x0 = 0; x0 < ge; ++x0) {
+                uint64_t n = 0;
+                for (uint32_t x1 = 0; x1 < ge; ++x1) {
+                    n += h[size_t(x1) * ge + x0];
+                    Tt[size_t(x0) * ge + x1] = x1 >= x0 ? n : 0;
+                }
+            }
+        }
+    }
+    // (cost, batches) of each box as one key, cost << 12 | batches (a box of
+    // this size has fewer than 2^11 cells): adding two keys adds both parts,
+    // and comparing keys compares (cost, batches) in that order
+    constexpr uint32_t kLeafBits = 12;
+    std::vector<uint64_t> key(F.nbox);
+    std::vector<uint32_t> split(F.nbox, 0);   // 0 = leaf, else d * 65536 + t
+    for (size_t i = 0; i < F.nbox; ++i) key[i] = F.leaf[i] == 2 ? 0u : F.leaf[i];
+    uint32_t x0[kMaxAttr], x1[kMaxAttr];
+    for (uint32_t i : F.order) {
+        box_coords(F, i, x0, x1);
+        uint64_t best = UINT64_MAX;
+        uint32_t bs = 0;
+        for (uint32_t d = 0; d < a; ++d) {
+            const size_t bd = F.bstride[d], gbd = size_t(grid[d]) * bd;
+            // cut at t: lower part i - (x1 - t + 1) bd, upper part i + (t - x0) g bd
+            const uint64_t* ka = key.data() + (i - size_t(x1[d] - x0[d]) * bd);
+            const uint64_t* kb = key.data() + (i + gbd);
+            const uint32_t n = x1[d] - x0[d];
+            if (a <= 2) {
+                const uint32_t e = a == 2 ? 1 - d : 0, ge = a == 2 ? grid[e] : 1;
+                const size_t row = a == 2 ? size_t(x0[e]) * ge + x1[e] : 0, tstep = size_t(ge) * ge;
+                const uint64_t* T = tab[d].data() + size_t(x0[d] + 1) * tstep + row;
+                for (uint32_t k = 0; k < n; ++k) {
+                    const uint64_t c = (T[k * tstep] << kLeafBits) + ka[k * bd] + kb[k * gbd];
+                    if (c < best) { best = c; bs = d * 65536u + x0[d] + 1 + k; }
+                }
+            } else {
+                for (uint32_t k = 0; k < n; ++k) {
+                    const uint32_t t = x0[d] + 1 + k;
+                    uint64_t cut = 0;
+                    for (uint32_t q : strad[d][t]) {
+                        bool meets = true;
+                        for (uint32_t e = 0; e < a && meets; ++e)
+                            if (e != d) meets = qlo[q * a + e] <= x1[e] && qhi[q * a + e] >= x0[e];
+                        cut += meets;
+                    }
+                    const uint64_t c = (cut << kLeafBits) + ka[k * bd] + kb[k * gbd];
+                    if (c < best) { best = c; bs = d * 65536u + t; }
+                }
+            }
+        }
+        key[i] = best;
+        split[i] = bs;
+    }
+    // the leaves, lower parts first; a leaf's non-empty cells in id order
+    plan.clear();
+    size_t all = 0;
+    for (uint32_t d = 0; d < a; ++d) all += size_t(grid[d] - 1) * F.bstride[d];   // x0 = 0, x1 = g - 1
+    std::vector<size_t> stack(1, all);
+    while (!stack.empty()) {
+        const size_t i = stack.back();
+        stack.pop_back();
+        box_coords(F, i, x0, x1);
+        if (split[i]) {
+            const uint32_t d = split[i] / 65536u, t = split[i] % 65536u;
+            const size_t bd = F.bstride[d];
+            stack.push_back(i + size_t(t - x0[d]) * grid[d] * bd);   // upper part
+            stack.push_back(i - size_t(x1[d] - t + 1) * bd);          // lower part, popped first
+            continue;
+        }
+        std::vector<uint32_t> batch;
+        uint32_t x[kMaxAttr];
+        for (uint32_t d = 0; d < a; ++d) x[d] = x0[d];
+        for (;;) {
+            uint32_t c = 0;
+            for (uint32_t d = 0; d < a; ++d) c += x[d] * F.stride[d];
+            if (cell_size[c]) batch.push_back(c);
+            int d = int(a) - 1;
+            while (d >= 0 && ++x[d] > x1[d]) { x[d] = x0[d]; --d; }
+            if (d < 0) break;
+        }
+        if (!batch.empty()) plan.push_back(std::move(batch));
+    }
+}
+
+namespace {
+
+// A new plan for b in the buffers of its current one; a failure after the
+// buffers moved (a device error) leaves b on the index's build-time plan.
+std::unique_ptr<StreamPlan> plan_reusing(gf_batch& b, std::vector<std::vector<uint32_t>> cells) {
+    try {
+        return make_stream_plan(*b.ix, std::move(cells), b.splan.get());
+    } catch (...) {
+        if (b.splan && (!b.splan->head.p || !b.splan->plan_cells.p)) b.splan.reset();
+        throw;
+    }
+}
+
+}  // namespace
+
+// The plan of a query batch from its own stage A cell lists: each query's
+// bounding box on the device (k_cell_boxes), the boxes to the host, the
+// planner's dynamic program (plan_boxes), the plan's headers; the batch's
+// active (query, batch) pairs counted on the device from its cell flags.
+uint64_t stream_plan_batch(gf_batch& b, uint64_t max_points, uint32_t max_cells) {
+    gf_index& ix = *b.ix;
+    StreamIndex& S = *ix.sx;
+    const uint32_t Q = b.Q, P = ix.P, a = ix.a;
+    hipStream_t st = ix.stream;
+    if (b.qbox.n < size_t(Q) * 2 * a) b.qbox.alloc(size_t(Q) * 2 * a);
+    GF_HIP(launch_cell_boxes(Q, P, a, ix.grid.p, b.cells.p, b.counts.p, b.qbox.p, st));
+    std::vector<uint32_t> box(size_t(Q) * 2 * a);
+    if (Q) GF_HIP(hipMemcpyAsync(box.data(), b.qbox.p, box.size() * 4, hipMemcpyDeviceToHost, st));
+    GF_HIP(hipStreamSynchronize(st));
+    std::vector<uint32_t> qlo, qhi;
+    for (uint32_t q = 0; q < Q; ++q) {
+        const uint32_t* x = &box[size_t(q) * 2 * a];
+        if (x[0] > x[a]) continue;   // no cell
+        qlo.insert(qlo.end(), x, x + a);
+        qhi.insert(qhi.end(), x + a, x + 2 * a);
+    }
+    std::vector<std::vector<uint32_t>> cells;
+    plan_boxes(qlo, qhi, a, ix.grid_h.data(), S.size.data(), max_points, max_cells, cells, &S.frame);
+    std::unique_ptr<StreamPlan> pl = plan_reusing(b, std::move(cells));
+    const size_t nb = pl->batches.size();
+    if (!b.flags_ready) {
+        if (b.flags.n < size_t(Q) * P) b.flags.alloc(size_t(Q) * P);
+        GF_HIP(launch_cell_flags(Q, P, b.cells.p, b.counts.p, b.little.p, b.flags.p, st));
+    }
+    if (b.need.n < 2 * std::max<size_t>(nb, 1)) b.need.alloc(2 * std::max<size_t>(nb, 1));
+    GF_HIP(launch_batch_need(Q, P, uint32_t(nb), pl->plan_cells.p, pl->plan_off.p, b.flags.p, b.need.p, st));
+    std::vector<uint32_t> act(nb);
+    if (nb) GF_HIP(hipMemcpyAsync(act.data(), b.need.p + nb, nb * 4, hipMemcpyDeviceToHost, st));
+    GF_HIP(hipStreamSynchronize(st));
+    b.splan = std::move(pl);
+    uint64_t total = 0;
+    for (uint32_t x : act) total += x;
+    return total;
+}
+
+void stream_set_plan(gf_batch& b, std::vector<std::vector<uint32_t>> cells) {
+    if (cells.empty()) {
+        b.splan.reset();
+        return;
+    }
+    b.splan = plan_reusing(b, std::move(cells));
+}
+
 void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* dists, gf_search_stats* stats) {
     gf_index& ix = *b.ix;
     StreamIndex& S = *ix.sx;
-    const uint32_t Q = b.Q, K = o.K, L = o.L, R = ix.R, P = ix.P, Bm = std::max<uint32_t>(S.Bmax, 1u);
+    const StreamPlan& pl = b.splan ? *b.splan : *S.plan;
+    GF_REQUIRE(pl.max_bytes <= S.turn[0].n && (!S.i8 || pl.tmax <= S.trec_tiles), GF_E_STATE,
+               "the stream plan's largest batch does not fit the index's device buffers");
+    const uint32_t Q = b.Q, K = o.K, L = o.L, R = ix.R, P = ix.P, Bm = std::max<uint32_t>(pl.Bmax, 1u);
     hipStream_t st = ix.stream;
 
     // Entry points: the caller's, or the out-of-core host's draw: 10 L
@@ -512,7 +850,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     base.Lpad = Lpad;
     uint32_t* tot = b.tot.p;
 
-    const size_t nb = S.batches.size();
+    const size_t nb = pl.batches.size();
     // per batch: copy start/end (copy stream), traversal start, brute-force start/end (compute stream)
     std::vector<hipEvent_t> ce(5 * nb, nullptr);
     hipEvent_t t0 = nullptr, t1 = nullptr;
@@ -534,11 +872,14 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     // route's limit; schedule buffers sized like the resident path's.
     const bool gemm = S.i8 && b.i8 && K <= kBfKMax;
     if (gemm) {
-        const uint32_t NS = std::max(S.NSmax, 1u);
+        const uint32_t NS = std::max(pl.NSmax, 1u);
         if (b.bcnt.n < NS) { b.bcnt.alloc(NS); b.bin.alloc(NS); b.bstart.alloc(NS); b.icnt.alloc(NS); b.ioff.alloc(NS); }
         if (b.nsub.n < Q) { b.nsub.alloc(Q); b.part_off.alloc(Q); b.pcnt.alloc(Q); b.gbound.alloc(Q); }
         // items <= pairs x chunks / 64 + (sub-cell, chunk) slots (k_bfitems)
-        if (!b.part.n) b.alloc_pairs(size_t(Q) * 64, K, Q, NS, S.tmax / kStreamTileChunk + NS);
+        // sized for this plan's largest batch (a batch's plan may change
+        // between searches)
+        const size_t slots = pl.tmax / kStreamTileChunk + NS;
+        if (!b.pairs_fit(Q, NS, slots)) b.alloc_pairs(std::max<size_t>(b.pair_cap, size_t(Q) * 64), K, Q, NS, slots);
         if (b.part.n < b.pair_cap * K) b.part.alloc(b.pair_cap * K);
         if (b.bfmask.n < size_t(Q) * Bm) b.bfmask.alloc(size_t(Q) * Bm);
         if (b.note.n < 2 * std::max<size_t>(nb, 1)) b.note.alloc(2 * std::max<size_t>(nb, 1));
@@ -609,20 +950,30 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         GF_HIP(launch_note_bf(tot, b.note.p + 2 * bi, st));
     };
 
+    // A batch's image from the arena and the plan's header block, on the
+    // copy stream: DMA for the large pieces, then one k_stream_gather for the
+    // rest; the pieces the MFMA brute force reads (kCopyCore), and the
+    // attributes (kCopyAttrs, the gather brute force), and the graph and
+    // cross edges (kCopyAll, the traversal).
     double bytes = 0.0;
-    auto enqueue_copy = [&](size_t bi, int t, size_t nbytes) {
-        const StreamBatch& sb = S.batches[bi];
-        GF_HIP(hipStreamWaitEvent(S.copy, S.freed[t], 0));
-        GF_HIP(hipEventRecord(ce[5 * bi], S.copy));
-        GF_HIP(hipMemcpyAsync(S.turn[t].p, S.host.p + sb.host_off, nbytes, hipMemcpyHostToDevice, S.copy));
-        GF_HIP(hipEventRecord(ce[5 * bi + 1], S.copy));
-        GF_HIP(hipEventRecord(S.ready[t], S.copy));
-        bytes += double(nbytes);
+    auto enqueue_copy = [&](size_t bi, int t, int what) {
+        const StreamBatch& sb = pl.batches[bi];
+        hipStream_t cs = S.copy;
+        GF_HIP(hipStreamWaitEvent(cs, S.freed[t], 0));
+        GF_HIP(hipEventRecord(ce[5 * bi], cs));
+        for (uint32_t k = 0; k < sb.ndma[what]; ++k) {
+            const StreamCopy& c = pl.dma[sb.dma0 + k];
+            GF_HIP(hipMemcpyAsync(S.turn[t].p + c.dst, S.host.p + c.src, c.bytes, hipMemcpyHostToDevice, cs));
+        }
+        GF_HIP(launch_stream_gather(pl.desc.p + sb.desc0, sb.ndesc[what], S.host.p, pl.head.p, S.turn[t].p, cs));
+        bytes += double(sb.moved[what]);
+        GF_HIP(hipEventRecord(ce[5 * bi + 1], cs));
+        GF_HIP(hipEventRecord(S.ready[t], cs));
     };
     // One batch on the compute stream: its cell lists and routes, the
     // traversal (unless skipped), the brute force, the merge.
     auto enqueue_compute = [&](size_t bi, int t, bool traverse, bool first) {
-        const StreamBatch& sb = S.batches[bi];
+        const StreamBatch& sb = pl.batches[bi];
         char* dev = S.turn[t].p;
         GF_HIP(hipStreamWaitEvent(st, S.ready[t], 0));
         const uint32_t* bcell = reinterpret_cast<const uint32_t*>(dev + sb.o_bcell);
@@ -665,7 +1016,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     // skipped batches cost nothing; a batch no query traverses moves only
     // its brute-force sections.
     if (b.need.n < 2 * std::max<size_t>(nb, 1)) b.need.alloc(2 * std::max<size_t>(nb, 1));
-    GF_HIP(launch_batch_need(Q, P, uint32_t(nb), S.plan_cells.p, S.plan_off.p, b.flags.p, b.need.p, st));
+    GF_HIP(launch_batch_need(Q, P, uint32_t(nb), pl.plan_cells.p, pl.plan_off.p, b.flags.p, b.need.p, st));
     std::vector<uint32_t> need(2 * nb, 0);   // flags, then active queries per batch
     if (nb) {
         GF_HIP(hipMemcpyAsync(need.data(), b.need.p, 2 * nb * 4, hipMemcpyDeviceToHost, st));
@@ -684,10 +1035,9 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     std::vector<size_t> ran;
     for (size_t bi = 0; bi < nb; ++bi) {
         if (!need[bi]) continue;
-        const StreamBatch& sb = S.batches[bi];
         const bool trav = (need[bi] & 2u) != 0;
         const int t = int(ran.size() & 1);
-        enqueue_copy(bi, t, trav ? sb.bytes : (gemm ? sb.bytes_mfma : sb.bytes_bf));
+        enqueue_copy(bi, t, trav ? kCopyAll : (gemm ? kCopyCore : kCopyAttrs));
         enqueue_compute(bi, t, trav, ran.empty());
         ran.push_back(bi);
     }
@@ -706,11 +1056,11 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
         for (size_t bi = 0; bi < nb; ++bi)
             if (!note[2 * bi]) need = std::max<size_t>(need, note[2 * bi + 1]);
         if (need) {
-            const uint32_t NS = std::max(S.NSmax, 1u);
-            b.alloc_pairs(need + need / 4 + 1024, K, Q, NS, S.tmax / kStreamTileChunk + NS);
+            const uint32_t NS = std::max(pl.NSmax, 1u);
+            b.alloc_pairs(need + need / 4 + 1024, K, Q, NS, pl.tmax / kStreamTileChunk + NS);
             for (size_t bi = 0; bi < nb; ++bi)
                 if (!note[2 * bi]) {
-                    enqueue_copy(bi, 0, S.batches[bi].bytes_mfma);
+                    enqueue_copy(bi, 0, kCopyCore);
                     enqueue_compute(bi, 0, false, false);
                 }
             GF_HIP(hipStreamSynchronize(st));

@@ -112,14 +112,21 @@ gf_status gf_index_close(gf_index* ix);
 gf_status gf_index_get_info(const gf_index* ix, gf_index_info* out);
 
 /* Streamed (out-of-core) index: the cells' graphs, vectors, attributes and
- * the cross edges between cells of one batch stay in pinned host memory, in
- * one packed image per batch of a static plan, and gf_search streams the
- * batches through two device buffers with hipMemcpyAsync on a side stream,
- * overlapped with the search of the previous batch.  Replaces the
- * out-of-core driver's host-pinned loaders (get_graph_info_host,
- * check.cu:572-623; load_result_pined, tools.cuh:241-255), its static batch
- * plan (bigdataset_experiment.cu:271-277, 746-756) and the device buffers it
- * sizes from the largest batch (bigdataset_experiment.cu:776-793). */
+ * every (cell, cell') slice of cross edges (the reference's "T" layout,
+ * big_dataset_adapterV3.cuh:3539-3541) stay in pinned host memory in the
+ * resident row order, whatever the batch plan.  gf_search streams the
+ * batches of a plan through two device buffers: DMA copies on a side stream
+ * assemble each batch's image (a few per run of consecutive cell ids, the
+ * cross edges of two runs in one 2-D copy), overlapped with the search of the
+ * previous batch.  The plan given here is the index's build-time plan; a
+ * query batch may replace it (gf_batch_plan_stream, gf_batch_set_stream_plan)
+ * without a re-pack.  Replaces the out-of-core driver's host-pinned loaders
+ * (get_graph_info_host, check.cu:572-623; load_result_pined,
+ * tools.cuh:241-255), its static batch plan (bigdataset_experiment.cu:271-277,
+ * 746-756), its per-slice copies (big_dataset_adapterV3.cuh:3925-3946) and
+ * the device buffers it sizes from the largest batch
+ * (bigdataset_experiment.cu:776-793).  Host memory: N * (rowbytes + 4 * (2 +
+ * a + R + P * E)) bytes plus the sub-cell metadata. */
 typedef struct {
     uint64_t device_budget;   /* bytes the two batch buffers may use (the device cap); 0 = no cap */
     uint32_t nbatch;          /* batches in cells/sizes; 0 = consecutive cells, batch_cells per batch */
@@ -153,6 +160,33 @@ gf_status gf_stream_plan_cells(const uint32_t* cells, const uint32_t* counts, ui
                                const uint32_t* grid_shape, const uint32_t* cell_size, uint64_t max_points,
                                uint32_t max_cells, uint32_t* sizes, uint32_t* plan_cells, uint32_t* nbatch,
                                uint64_t* active);
+
+/* The batch plan a streamed index's gf_search uses for this query batch,
+ * made from the batch's stage A cell lists (the out-of-core pipeline's
+ * dynamic cell scheduling, README.md:5; the reference's driver fixes its
+ * batches by hand, bigdataset_experiment.cu:271-277, 746-756): each query's
+ * bounding box of cells on the device, gf_stream_plan_cells' dynamic program
+ * on the host (max_points, max_cells as there), the batches' headers; the
+ * plan's active (query, batch) pairs counted on the device.  The index's
+ * rows are not re-packed.  The batch keeps the plan for its next searches
+ * (until the next call, gf_batch_set_stream_plan or gf_batch_free); a plan
+ * whose largest batch needs more device memory than the index's two batch
+ * buffers hold grows them within the index's device budget, else
+ * GF_E_UNSUPPORTED.  Synchronous; *ms (may be NULL) receives the call's host
+ * wall time, *nbatch and *active (may be NULL) the plan's batches and its
+ * active pairs.  GF_E_UNSUPPORTED on a resident index, GF_E_STATE before
+ * stage A. */
+gf_status gf_batch_plan_stream(gf_batch* b, uint64_t max_points, uint32_t max_cells, uint32_t* nbatch,
+                               uint64_t* active, double* ms);
+/* Sets this query batch's plan explicitly: nbatch batches of sizes[i] cell
+ * ids in cells, batch after batch, each cell at most once (a cell in no
+ * batch is never searched), the form gf_stream_plan takes; nbatch = 0 goes
+ * back to the index's build-time plan.  Buffers grow as for
+ * gf_batch_plan_stream. */
+gf_status gf_batch_set_stream_plan(gf_batch* b, uint32_t nbatch, const uint32_t* sizes, const uint32_t* cells);
+/* The plan this batch's next search uses: *nbatch, then (each may be NULL;
+ * room for P) the batch sizes and the cells batch after batch. */
+gf_status gf_batch_get_stream_plan(const gf_batch* b, uint32_t* nbatch, uint32_t* sizes, uint32_t* cells);
 
 /* A query batch: Q query vectors (Q*D fp32) and closed ranges lo/hi (Q*a),
  * uploaded to the device (realdataset_search.cu:2198-2245 load + f2h). */

@@ -399,3 +399,84 @@ def test_planned_stream_matches_oracle(world_stream, thr, L):
     assert np.array_equal(ctr.astype(np.int64), oc)
     b.close()
     sx.close()
+
+
+@pytest.mark.parametrize("thr,L,K", [(0.05, 48, 10), (1.0, 32, 10), (0.1, 32, 20)])
+def test_plans_on_one_index(world_stream, thr, L, K):
+    """One streamed index, four plans in turn on one query batch, with no
+    re-pack: the build-time plan (shuffled, 4 cells per batch), the plan
+    gf_batch_plan_stream makes from the batch's own cell lists, an explicit
+    plan with a batch of 10 cells (larger than any build-time batch: the
+    device buffers grow), and the build-time plan again.  Each search is
+    bit-exact (ids, distances, counters) against the oracle run batch by
+    batch over that plan; the planned plan's active (query, batch) pairs, as
+    the planner counts them, are the search's."""
+    import garfield_amd as gf
+    from oracle import oracle as orc
+    cfg, ix = world_stream
+    _print_case("plans-one-index", thr=thr, L=L, K=K)
+    P = ix["P"]
+    plan0 = _shuffled_plan(P, 4, seed=3)
+    sx = gl.Index.create_streamed(*_args(ix), plan=plan0)
+    bytes0 = sx.device_bytes
+    b = sx.batch(cfg["queries"], cfg["lo"], cfg["hi"])
+    gf.intersection_area_mark_little_seg_batch_process(b, AMIN, WIDTH, thr)
+    flags = b.get_cell_flags()
+    sizes = synth.cell_sizes(ix)
+    ent = orc.entry_draw(int(sizes[sizes > 0].min()), 10 * L, ix["R"])
+    assert b.stream_plan() == plan0
+
+    def check(plan, tag):
+        ids, dists, st = b.search(L=L, K=K, rl=10)
+        ctr = b.get_counters()
+        assert st.bf_mfma == (K <= 16)
+        oids, od, oc = _oracle_stream(ix, plan, cfg, flags, ent, L, K=K, mfma=bool(st.bf_mfma))
+        bad = np.nonzero(np.any(ids != oids, axis=1))[0]
+        assert bad.size == 0, f"{tag}: {bad.size} queries differ, first {bad[:5]}"
+        assert np.array_equal(dists.view(np.uint32), od.view(np.uint32)), tag
+        assert np.array_equal(ctr.astype(np.int64), oc), tag
+        return ids, dists, st
+
+    r0 = check(plan0, "build-time")
+    planned, active, ms = b.plan_stream(max_cells=4)
+    assert ms > 0 and b.stream_plan() == planned
+    assert sorted(c for bt in planned for c in bt) == [c for c in range(P) if sizes[c]]
+    assert all(len(bt) <= 4 for bt in planned)
+    _, _, st = check(planned, "planned")
+    assert st.n_active == active
+    big = [[0, 1, 2, 5], [3, 4], [6, 7, 8, 9, 10, 11, 12, 13, 14, 15]]
+    b.set_stream_plan(big)
+    assert b.stream_plan() == big
+    check(big, "explicit")
+    assert sx.device_bytes > bytes0      # the turn buffers grew for the 10-cell batch
+    b.set_stream_plan(None)
+    assert b.stream_plan() == plan0
+    r3 = check(plan0, "build-time again")
+    assert np.array_equal(r0[0], r3[0])
+    b.close()
+    sx.close()
+
+
+def test_plan_over_budget_refused(world_stream):
+    """A plan whose largest batch does not fit the index's device budget is
+    refused (GF_E_UNSUPPORTED) and the batch keeps its previous plan."""
+    cfg, ix = world_stream
+    _print_case("plan-over-budget")
+    P = ix["P"]
+    plan0 = _shuffled_plan(P, 2, seed=9)
+    probe = gl.Index.create_streamed(*_args(ix), plan=plan0)
+    budget = probe.device_bytes + 4096
+    probe.close()
+    sx = gl.Index.create_streamed(*_args(ix), plan=plan0, device_budget=budget)
+    b = sx.batch(cfg["queries"], cfg["lo"], cfg["hi"])
+    b.mark_cells_grid(AMIN, WIDTH, 0.05)
+    with pytest.raises(gl.GarfieldError) as e:
+        b.set_stream_plan([list(range(P))])
+    assert e.value.status == 6
+    assert b.stream_plan() == plan0
+    with pytest.raises(gl.GarfieldError):
+        b.plan_stream(max_cells=16)          # one batch of every cell: over the budget
+    ids, _, st = b.search(L=32, K=10, rl=10)
+    assert st.n_batches > 0 and sx.device_bytes <= budget
+    b.close()
+    sx.close()
