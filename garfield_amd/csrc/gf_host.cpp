@@ -544,11 +544,6 @@ gf::SubArgs sub_args(const gf_index& ix) {
     return sa;
 }
 
-uint32_t next_pow2(uint32_t x) {
-    uint32_t p = 1;
-    while (p < x) p <<= 1;
-    return p;
-}
 
 void entry_points_ref(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
     const uint32_t avg = (N + P - 1) / P;
@@ -957,13 +952,10 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     ensure_out(*b, K);
     if (b->sched.n < Q) b->sched.alloc(Q);
 
-    // Visited-set size: twice the keys live between two resets (the list,
-    // the slots of four expansions and a cell's cross slots; the dual
-    // channel's expansions fill 2R slots).
-    const uint32_t hsize = std::max<uint32_t>(
-        256, next_pow2(2 * (L + gf::kXSlots + (channels == 2 ? 10 * R : 4 * R))));
-    uint32_t hbits = 0;
-    while ((1u << hbits) < hsize) ++hbits;
+    // Visited-set size for the keys live between two resets (the list, the
+    // slots of four expansions and a cell's cross slots; the dual channel's
+    // expansions fill 2R slots).
+    const uint32_t hsize = gf::visited_slots(L + gf::kXSlots + (channels == 2 ? 10 * R : 4 * R));
     const uint32_t Lpad = round_up(L, 2);
     const uint32_t lds = channels == 2 ? gf::trav_dual_lds_bytes(Lpad, hsize) : gf::trav_lds_bytes(Lpad, hsize, ix->P);
     GF_REQUIRE(lds <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
@@ -1006,7 +998,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     a.out_dist = b->out_dist.p;
     a.counters = b->counters.p;
     a.a = ix->a; a.P = ix->P; a.R = R; a.E = ix->E; a.L = L; a.K = K; a.rl = rl;
-    a.hbits = hbits;
+    a.hsize = hsize;
     a.offl = gf::trav_offsets_in_lds(ix->P) ? 1u : 0u;
     a.Lpad = Lpad;
     // The full-graph route: its own visited-set size (L + FD list and B
@@ -1014,9 +1006,8 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     gf::TravArgs af = a;
     uint32_t lds_f = 0;
     if (ix->FD) {
-        const uint32_t hs = std::max<uint32_t>(256, next_pow2(2 * (L + 5 * ix->FD)));
-        af.hbits = 0;
-        while ((1u << af.hbits) < hs) ++af.hbits;
+        const uint32_t hs = gf::visited_slots(L + 5 * ix->FD);
+        af.hsize = hs;
         lds_f = Lpad * 8 + gf::kXSlots * 8 + 128 * 4 + hs * 4;
         GF_REQUIRE(lds_f <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
         af.fgraph = ix->fgraph.p;

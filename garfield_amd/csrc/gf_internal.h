@@ -20,6 +20,15 @@ constexpr uint32_t kOffLds = 1024;    // cell offsets (P + 1) the traversal keep
 // LDS bytes of the traversal kernel: candidate list, slot scratch, row list,
 // visited set of hsize keys, and the P + 1 cell offsets when they fit.
 inline bool trav_offsets_in_lds(uint32_t P) { return P + 1 <= kOffLds; }
+// Visited-set slots for at most `live` keys between two clears: a load
+// factor of at most 0.6 (linear probing then needs about 3.6 probes for a new
+// key at the worst load, 1.75 for a present one), a multiple of 64, at least
+// 256.  The table never fills, so its set semantics are exact.
+inline uint32_t visited_slots(uint32_t live) {
+    const uint32_t s = (live * 5u + 2u) / 3u;
+    const uint32_t r = (s + 63u) / 64u * 64u;
+    return r < 256u ? 256u : r;
+}
 inline uint32_t trav_lds_bytes(uint32_t Lpad, uint32_t hsize, uint32_t P) {
     return Lpad * 8 + kXSlots * 8 + 128 * 4 + hsize * 4 + (trav_offsets_in_lds(P) ? (P + 1) * 4 : 0);
 }
@@ -85,7 +94,7 @@ struct TravArgs {
     uint32_t* out_ids;        // Q*K
     float* out_dist;          // Q*K
     uint32_t* counters;       // Q*GF_NCOUNTERS
-    uint32_t a, P, R, E, L, K, rl, hbits, Lpad;
+    uint32_t a, P, R, E, L, K, rl, hsize, Lpad;   // hsize: visited-set slots (visited_slots)
     uint32_t offl;            // 1: the launch's LDS holds the P + 1 cell offsets (trav_lds_bytes)
     // Full-graph route (queries with postfilter or more cells): the graph
     // over every point, FD rows per row (cell-major rows, kEmpty = no edge),

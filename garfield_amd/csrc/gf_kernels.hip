@@ -52,18 +52,24 @@ __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 __device__ __forceinline__ void wave_sync() { __asm__ __volatile__("" ::: "memory"); }
 
 // ---------------------------------------------------------------- visited set
-// Open addressing with linear probing in LDS; set semantics identical to the
-// reference's 2048-slot table (gpu_graph.cu:677-711) as long as the table does
-// not fill up, which the host guarantees by sizing it to twice the keys that
-// can be live between two resets.
-__device__ __forceinline__ bool hash_insert(uint32_t* H, uint32_t hbits, uint32_t key) {
-    const uint32_t mask = (1u << hbits) - 1u;
-    uint32_t h = (key * 2654435761u) >> (32u - hbits);
-    for (uint32_t i = 0; i <= mask; ++i) {
+// Open addressing with linear probing in LDS over hsize slots (any multiple
+// of 64); set semantics identical to the reference's 2048-slot table
+// (gpu_graph.cu:677-711) as long as the table does not fill up, which the
+// host guarantees by sizing it for a load factor of at most 0.6 of the keys
+// that can be live between two resets.  A key's first slot is the high word
+// of (key * 2654435761 mod 2^32) * hsize: for hsize = 2^b, the top b bits of
+// the multiplicative hash.
+__device__ __forceinline__ uint32_t hash_slot(uint32_t key, uint32_t hsize) {
+    return __umulhi(key * 2654435761u, hsize);
+}
+__device__ __forceinline__ uint32_t hash_next(uint32_t h, uint32_t hsize) { return h + 1u == hsize ? 0u : h + 1u; }
+__device__ __forceinline__ bool hash_insert(uint32_t* H, uint32_t hsize, uint32_t key) {
+    uint32_t h = hash_slot(key, hsize);
+    for (uint32_t i = 0; i < hsize; ++i) {
         uint32_t old = atomicCAS(&H[h], kEmpty, key);
         if (old == kEmpty) return true;
         if (old == key) return false;
-        h = (h + 1u) & mask;
+        h = hash_next(h, hsize);
     }
     return false;
 }
@@ -594,9 +600,8 @@ __device__ __forceinline__ uint32_t local_key(const TravArgs& p, const CellOffs&
 
 // Insert the rows of the valid entries of A[0..L), four per lane at a time,
 // their first probes issued before any is awaited.
-__device__ void hash_add_rows(uint32_t* H, uint32_t hbits, const uint64_t* A, uint32_t L) {
+__device__ void hash_add_rows(uint32_t* H, uint32_t hsize, const uint64_t* A, uint32_t L) {
     constexpr uint32_t U = 4;
-    const uint32_t mask = (1u << hbits) - 1u;
     for (uint32_t base = 0; base < L; base += 64u * U) {
         uint32_t key[U], h[U], old[U];
         bool todo[U];
@@ -606,15 +611,15 @@ __device__ void hash_add_rows(uint32_t* H, uint32_t hbits, const uint64_t* A, ui
             const uint64_t c = i < L ? A[i] : kCandSent;
             todo[u] = cvalid(c);
             key[u] = crow(c);
-            h[u] = (key[u] * 2654435761u) >> (32u - hbits);
+            h[u] = hash_slot(key[u], hsize);
         }
 #pragma unroll
         for (uint32_t u = 0; u < U; ++u) old[u] = todo[u] ? atomicCAS(&H[h[u]], kEmpty, key[u]) : kEmpty;
 #pragma unroll
         for (uint32_t u = 0; u < U; ++u) {
             if (!todo[u] || old[u] == kEmpty || old[u] == key[u]) continue;
-            for (uint32_t j = 0; j < mask; ++j) {
-                h[u] = (h[u] + 1u) & mask;
+            for (uint32_t j = 0; j + 1u < hsize; ++j) {
+                h[u] = hash_next(h[u], hsize);
                 const uint32_t o2 = atomicCAS(&H[h[u]], kEmpty, key[u]);
                 if (o2 == kEmpty || o2 == key[u]) break;
             }
@@ -629,7 +634,7 @@ __device__ void hash_add_rows(uint32_t* H, uint32_t hbits, const uint64_t* A, ui
 __device__ void hash_add_list(const TravArgs& p, const CellOffs& co, uint32_t* H, const uint64_t* A, uint32_t L,
                               uint32_t off, uint32_t offn, uint32_t& nlrow) {
     constexpr uint32_t U = 4;
-    const uint32_t mask = (1u << p.hbits) - 1u;
+    const uint32_t hsize = p.hsize;
     for (uint32_t base = 0; base < L; base += 64u * U) {
         uint32_t key[U], h[U], old[U];
         bool todo[U];
@@ -639,15 +644,15 @@ __device__ void hash_add_list(const TravArgs& p, const CellOffs& co, uint32_t* H
             const uint64_t c = i < L ? A[i] : kCandSent;
             todo[u] = cvalid(c);
             key[u] = todo[u] ? local_key(p, co, crow(c), off, offn, nlrow) : 0u;
-            h[u] = (key[u] * 2654435761u) >> (32u - p.hbits);
+            h[u] = hash_slot(key[u], hsize);
         }
 #pragma unroll
         for (uint32_t u = 0; u < U; ++u) old[u] = todo[u] ? atomicCAS(&H[h[u]], kEmpty, key[u]) : kEmpty;
 #pragma unroll
         for (uint32_t u = 0; u < U; ++u) {
             if (!todo[u] || old[u] == kEmpty || old[u] == key[u]) continue;
-            for (uint32_t j = 0; j < mask; ++j) {
-                h[u] = (h[u] + 1u) & mask;
+            for (uint32_t j = 0; j + 1u < hsize; ++j) {
+                h[u] = hash_next(h[u], hsize);
                 const uint32_t o2 = atomicCAS(&H[h[u]], kEmpty, key[u]);
                 if (o2 == kEmpty || o2 == key[u]) break;
             }
@@ -687,7 +692,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
     const uint32_t si = p.srange[0] + blockIdx.x;
     if (si >= p.srange[1]) return;
     const uint32_t q = p.sched[si];
-    const uint32_t hsize = 1u << p.hbits;
+    const uint32_t hsize = p.hsize;
     const uint32_t L = p.L, R = p.R, P = p.P, E = p.E;
     // cell offsets for the visited-set keys of other cells' rows
     uint32_t* O = p.offl ? H + hsize : nullptr;
@@ -723,7 +728,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
         bool pass = false;
         if (mine) {
             row = off0 + p.entry[lane] % sz0;
-            hash_insert(H, p.hbits, p.gidx[row]);
+            hash_insert(H, p.hsize, p.gidx[row]);
             pass = row_pass(p.attrs, p.a, row, lo, hi);
         }
         wave_sync();
@@ -744,7 +749,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
                 hash_clear(H, hsize);
                 hash_add_list(p, co, H, A, L, off, offn, n_lrow);
                 if (lane < R && cvalid(bleft))
-                    hash_insert(H, p.hbits, local_key(p, co, crow(bleft), off, offn, n_lrow));
+                    hash_insert(H, p.hsize, local_key(p, co, crow(bleft), off, offn, n_lrow));
                 wave_sync();
             }
             const uint32_t sel = first_unexplored(A, L, scan);
@@ -763,7 +768,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
             if (mine) {
                 const uint32_t nl = p.graph[size_t(srow) * R + lane];
                 nrow = off + nl;
-                isnew = hash_insert(H, p.hbits, nl);
+                isnew = hash_insert(H, p.hsize, nl);
             }
             n_attr += R;
             float d;
@@ -838,7 +843,7 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
             const uint64_t y = W[R + lane];
             for (uint32_t h = 0; h < 2; ++h) {
                 const uint64_t c = W[h * 64u + lane];
-                if (cvalid(c)) hash_insert(H, p.hbits, crow(c) - offx);
+                if (cvalid(c)) hash_insert(H, p.hsize, crow(c) - offx);
             }
             wave_sync();
             merge_into(A, L, y, 64u, nullptr);
@@ -917,14 +922,13 @@ __global__ __launch_bounds__(64) void k_traverse(TravArgs p) {
 }
 
 // ------------------------------------------------------ dual-channel search
-__device__ __forceinline__ bool hash_contains(const uint32_t* H, uint32_t hbits, uint32_t key) {
-    const uint32_t mask = (1u << hbits) - 1u;
-    uint32_t h = (key * 2654435761u) >> (32u - hbits);
-    for (uint32_t i = 0; i <= mask; ++i) {
+__device__ __forceinline__ bool hash_contains(const uint32_t* H, uint32_t hsize, uint32_t key) {
+    uint32_t h = hash_slot(key, hsize);
+    for (uint32_t i = 0; i < hsize; ++i) {
         const uint32_t v = H[h];
         if (v == key) return true;
         if (v == kEmpty) return false;
-        h = (h + 1u) & mask;
+        h = hash_next(h, hsize);
     }
     return false;
 }
@@ -979,7 +983,7 @@ __global__ __launch_bounds__(64) void k_traverse_dual(TravArgs p) {
     const uint32_t si = p.srange[0] + blockIdx.x;
     if (si >= p.srange[1]) return;
     const uint32_t q = p.sched[si];
-    const uint32_t hsize = 1u << p.hbits;
+    const uint32_t hsize = p.hsize;
     const uint32_t L = p.L, R = p.R, P = p.P, E = p.E, R2 = 2u * p.R;
 
     QReg<VT, LPR, CPL> qv;
@@ -1017,7 +1021,7 @@ __global__ __launch_bounds__(64) void k_traverse_dual(TravArgs p) {
                 const bool ch1 = i >= L2;
                 const uint32_t o = ch1 ? off1 : off0, sz = (ch1 ? end1 : end0) - o;
                 row = o + p.entry[i] % sz;
-                hash_insert(H, p.hbits, row);
+                hash_insert(H, p.hsize, row);
                 pass = row_pass(p.attrs, p.a, row, lo, hi);
             }
             wave_sync();
@@ -1035,8 +1039,8 @@ __global__ __launch_bounds__(64) void k_traverse_dual(TravArgs p) {
     for (uint32_t ep = 0; ep < kMaxIter; ++ep) {
         if ((ep + 1) % kHashReset == 0) {              // gpu_graph.cu:6364-6378
             hash_clear(H, hsize);
-            hash_add_rows(H, p.hbits, A, L);
-            if (cvalid(bleft)) hash_insert(H, p.hbits, crow(bleft));
+            hash_add_rows(H, p.hsize, A, L);
+            if (cvalid(bleft)) hash_insert(H, p.hsize, crow(bleft));
             wave_sync();
         }
         // Selection and partner (gpu_graph.cu:6380-6420).
@@ -1059,7 +1063,7 @@ __global__ __launch_bounds__(64) void k_traverse_dual(TravArgs p) {
             bool free = false;
             if (lane < ne) {
                 v = p.cross[size_t(te_row) * p.xrow + size_t(oc) * p.xcell + lane];
-                free = !hash_contains(H, p.hbits, p.prow[v]);
+                free = !hash_contains(H, p.hsize, p.prow[v]);
             }
             const uint64_t m = ballot(free);
             if (m) pt_row = ooff + readlane32(v, __builtin_ctzll(m));
@@ -1084,7 +1088,7 @@ __global__ __launch_bounds__(64) void k_traverse_dual(TravArgs p) {
                 const bool v = lane < L && cvalid(c) && h < E;
                 uint32_t row = 0;
                 if (v) row = offx + p.cross[size_t(crow(c)) * p.xrow + size_t(nxt) * p.xcell + h];
-                const bool isnew = v && hash_insert(H, p.hbits, row);
+                const bool isnew = v && hash_insert(H, p.hsize, row);
                 wave_sync();
                 n_cross += __popcll(ballot(isnew));
                 float d;
@@ -1156,7 +1160,7 @@ __global__ __launch_bounds__(64) void k_traverse_dual(TravArgs p) {
                 else row = (ch ? off1 : off0) + p.graph[size_t(erow) * R + j];
             }
         }
-        const bool isnew = v && hash_insert(H, p.hbits, row);
+        const bool isnew = v && hash_insert(H, p.hsize, row);
         n_expand += (te_row != kEmpty) + (pt_row != kEmpty);
         float d;
         bool pass = false;
@@ -1259,7 +1263,7 @@ __global__ __launch_bounds__(64) void k_fullgraph(TravArgs p) {
     const uint32_t si = p.frange[0] + blockIdx.x;
     if (si >= p.frange[1]) return;
     const uint32_t q = p.sched[si];
-    const uint32_t hsize = 1u << p.hbits;
+    const uint32_t hsize = p.hsize;
     const uint32_t L = p.L, FD = p.FD;
 
     QReg<VT, LPR, CPL> qv;
@@ -1278,7 +1282,7 @@ __global__ __launch_bounds__(64) void k_fullgraph(TravArgs p) {
         const uint32_t row = mine ? p.fentry[lane] : 0u;
         bool pass = false;
         if (mine) {
-            hash_insert(H, p.hbits, row);
+            hash_insert(H, p.hsize, row);
             pass = row_pass(p.attrs, p.a, row, lo, hi);
         }
         wave_sync();
@@ -1293,7 +1297,7 @@ __global__ __launch_bounds__(64) void k_fullgraph(TravArgs p) {
             hash_clear(H, hsize);
             for (uint32_t i = lane; i < L + FD; i += 64u) {
                 const uint64_t c = i < L ? A[i] : W[i - L];
-                if (cvalid(c)) hash_insert(H, p.hbits, crow(c));
+                if (cvalid(c)) hash_insert(H, p.hsize, crow(c));
             }
             wave_sync();
         }
@@ -1310,7 +1314,7 @@ __global__ __launch_bounds__(64) void k_fullgraph(TravArgs p) {
         bool isnew = false, pass = false;
         if (mine) {
             nrow = p.fgraph[size_t(crow(sc)) * FD + lane];
-            isnew = nrow != kEmpty && hash_insert(H, p.hbits, nrow);
+            isnew = nrow != kEmpty && hash_insert(H, p.hsize, nrow);
         }
         n_attr += __popcll(ballot(isnew));
         float d;

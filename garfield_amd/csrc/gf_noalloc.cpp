@@ -58,11 +58,6 @@ struct Carve {
     }
 };
 
-uint32_t next_pow2(uint32_t x) {
-    uint32_t p = 1;
-    while (p < x) p <<= 1;
-    return p;
-}
 
 }  // namespace
 
@@ -81,9 +76,7 @@ extern "C" gf_status gf_search_noalloc(gf_index* ix, const float* queries, uint3
         GF_REQUIRE(!ix->C || (o->topc >= 1 && o->topc <= 4), GF_E_ARG, "topc must be in [1, 4]");
         GF_REQUIRE(so.entry_points || ix->entry_ref.n == R, GF_E_ARG,
                    "the index has no room for the reference's entry-point draw: pass entry_points");
-        const uint32_t hsize = std::max<uint32_t>(256, next_pow2(2 * (L + gf::kXSlots + 4 * R)));
-        uint32_t hbits = 0;
-        while ((1u << hbits) < hsize) ++hbits;
+        const uint32_t hsize = gf::visited_slots(L + gf::kXSlots + 4 * R);
         const uint32_t Lpad = gf::round_up(L, 2);
         const uint32_t lds = gf::trav_lds_bytes(Lpad, hsize, ix->P);
         GF_REQUIRE(lds <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
@@ -211,7 +204,7 @@ extern "C" gf_status gf_search_noalloc(gf_index* ix, const float* queries, uint3
         t.out_dist = s.out_dist;
         t.counters = s.counters;
         t.a = a; t.P = P; t.R = R; t.E = ix->E; t.L = L; t.K = K; t.rl = rl;
-        t.hbits = hbits;
+        t.hsize = hsize;
         t.offl = gf::trav_offsets_in_lds(ix->P) ? 1u : 0u;
         t.Lpad = Lpad;
         gf::SchedArgs sa{};
@@ -226,9 +219,8 @@ extern "C" gf_status gf_search_noalloc(gf_index* ix, const float* queries, uint3
         GF_HIP(gf::launch_traverse(ix->rs, tt, lds, Q, st));
         if (ix->FD && so.postfilter <= P) {
             gf::TravArgs tf = t;
-            const uint32_t hs = std::max<uint32_t>(256, next_pow2(2 * (L + 5 * ix->FD)));
-            tf.hbits = 0;
-            while ((1u << tf.hbits) < hs) ++tf.hbits;
+            const uint32_t hs = gf::visited_slots(L + 5 * ix->FD);
+            tf.hsize = hs;
             const uint32_t lds_f = Lpad * 8 + gf::kXSlots * 8 + 128 * 4 + hs * 4;
             GF_REQUIRE(lds_f <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
             tf.fgraph = ix->fgraph.p;

@@ -40,11 +40,6 @@ constexpr int kCopyCore = 0, kCopyAttrs = 1, kCopyAll = 2;   // sections of a ba
 constexpr size_t kDmaPiece = size_t(256) << 10;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
-uint32_t next_pow2(uint32_t x) {
-    uint32_t p = 1;
-    while (p < x) p <<= 1;
-    return p;
-}
 
 // Runs body(lo, hi) over [0, n) on up to 16 host threads.
 template <class F>
@@ -822,9 +817,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     if (b.out_ids.n < size_t(Q) * K) { b.out_ids.alloc(size_t(Q) * K); b.out_dist.alloc(size_t(Q) * K); }
     if (b.counters.n < size_t(Q) * GF_NCOUNTERS) b.counters.alloc(size_t(Q) * GF_NCOUNTERS);
 
-    const uint32_t hsize = std::max<uint32_t>(256, next_pow2(2 * (L + kXSlots + 4 * R)));
-    uint32_t hbits = 0;
-    while ((1u << hbits) < hsize) ++hbits;
+    const uint32_t hsize = visited_slots(L + kXSlots + 4 * R);
     const uint32_t Lpad = round_up(L, 2);
     const uint32_t lds = trav_lds_bytes(Lpad, hsize, Bm);
     GF_REQUIRE(lds <= 64 * 1024, GF_E_UNSUPPORTED, "L too large for the LDS budget");
@@ -845,7 +838,7 @@ void stream_search(gf_batch& b, const gf_search_opts& o, uint32_t* ids, float* d
     base.out_dist = b.s_dist.p;
     base.counters = b.s_ctr.p;
     base.a = ix.a; base.R = R; base.E = ix.E; base.L = L; base.K = K; base.rl = o.rl;
-    base.hbits = hbits;
+    base.hsize = hsize;
     base.offl = trav_offsets_in_lds(Bm) ? 1u : 0u;   // lds holds Bm + 1 >= B + 1 offsets
     base.Lpad = Lpad;
     uint32_t* tot = b.tot.p;
