@@ -205,6 +205,19 @@ def main():
         ex = synth.exact_result_dist(cfg["vectors"], cfg["queries"], ids)
         return synth.recall_at_k(ids, ex, gt_ids, gt_dist)
 
+    def recall_by_selectivity(ids):
+        """Tie-aware recall of the queries in each band of their selectivity."""
+        ex = synth.exact_result_dist(cfg["vectors"], cfg["queries"], ids)
+        _, tie = synth.recall_at_k(ids, ex, gt_ids, gt_dist, per_query=True)
+        sel = np.asarray(cfg["sel"])
+        edges = [0.0, 0.02, 0.05, 0.1, 0.2, 1.0]
+        out = []
+        for a, b in zip(edges[:-1], edges[1:]):
+            m = (sel >= a) & (sel < b)
+            if m.any():
+                out.append(f"sel[{a:g},{b:g}):{tie[m].mean():.3f}(n={int(m.sum())})")
+        return " ".join(out)
+
     def timed(prefilter, L, steps, warmup, ch=1):
         """steps timed passes after warmup; sums of the device times and the
         algorithmic work the search statistics report."""
@@ -263,6 +276,8 @@ def main():
             vlog(f"{'dual ' if ch == 2 else ''}prefilter={pf} L={L}: recall={tie:.4f} (strict {strict:.4f}) step={wall * 1e3:.1f}ms "
                  f"trav={st.ms_traverse:.1f}ms ({gbs:.0f} GB/s) bf={st.ms_bruteforce:.1f}ms A={ms_a:.2f}ms "
                  f"B={ms_b:.2f}ms q_trav={st.q_traverse} q_bf={st.q_bruteforce}")
+            if VERBOSE and pf == 0.0 and "sel" in cfg and L in (100, 600, 1100, 1700):
+                vlog(f"  recall by selectivity: {recall_by_selectivity(ids)}")
         curves[("dual:" if ch == 2 else "") + str(pf)] = curve
         reach = [c for c in curve if c["recall"] >= args.recall]
         sel = [c for c in curve if c["L"] in (100, 600, 1100, 1700)]

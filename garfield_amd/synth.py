@@ -423,10 +423,11 @@ def ground_truth_torch(vectors, attrs, queries, lo, hi, K, device="cuda", chunk=
     return ids, dist
 
 
-def recall_at_k(res_ids, res_exact_dist, gt_ids, gt_dist):
+def recall_at_k(res_ids, res_exact_dist, gt_ids, gt_dist, per_query=False):
     """(strict, tie-aware) recall: strict is |res ∩ gt| / |gt| (tools.cuh:384-453,
     1 when the filter passes nothing); tie-aware also counts a result whose exact
-    distance is <= the K-th ground-truth distance."""
+    distance is <= the K-th ground-truth distance.  per_query: the two arrays
+    of per-query recalls instead of their means."""
     Q, K = gt_ids.shape
     strict = np.empty(Q)
     tie = np.empty(Q)
@@ -443,6 +444,8 @@ def recall_at_k(res_ids, res_exact_dist, gt_ids, gt_dist):
         uniq = np.zeros(K, bool)
         uniq[first] = True
         tie[q] = min(np.count_nonzero(valid & uniq & (res_exact_dist[q] <= kth)), g.size) / g.size
+    if per_query:
+        return strict, tie
     return float(strict.mean()), float(tie.mean())
 
 
