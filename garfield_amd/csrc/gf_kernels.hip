@@ -3212,9 +3212,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 && 
 // ------------------------------------------- fp16 query-batch brute force
 // Brute force of binary16 rows for a batch of queries on fp16 MFMA
 // (v_mfma_f32_16x16x32_f16).  Items and sub-cell tiles are k_bf_i8's; a
-// wave takes an item's queries 16 at a time (queries as the B operand, D / 32
-// k-steps held in registers) and streams the sub-cell's tiles, 16 rows each,
-// as A, gathered from the cell-major rows.  The MFMA distance
+// workgroup takes an item, each of its four waves 16 of the item's queries
+// (queries as the B operand, D / 32 k-steps held in registers), and streams
+// the sub-cell's tiles, 16 rows each, through LDS as the A operand of all
+// four, gathered once from the cell-major rows.  The MFMA distance
 // d' = |q|^2 + |x|^2 - 2 q.x differs from the canonical fp32 distance d by at
 // most eps_q (a bound from the fp32 error of both), so every point whose d
 // is among the K smallest has d' within the query's smallest K-th d' plus
@@ -3252,24 +3253,55 @@ template <> struct BfChunk<0> {
     }
 };
 
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return uint32_t(uintptr_t((const __attribute__((address_space(3))) void*)p));
+}
+// Asynchronous global-to-LDS copies: 16 (4) bytes per active lane from src to
+// LDS at lds_base + 16 (4) x lane, lds_base wave-uniform (in m0).  They count
+// in vmcnt and the compiler does not see them: the caller waits
+// (wait_vmcnt) and synchronises before the data is read.
+__device__ __forceinline__ void lds_copy16(const void* src, uint32_t lds_base) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
+}
+__device__ __forceinline__ void lds_copy4(const void* src, uint32_t lds_base) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
+}
+// s_waitcnt vmcnt(N), the other counters unconstrained (gfx9 encoding).
+template <uint32_t N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N < 64u, "vmcnt");
+    __builtin_amdgcn_s_waitcnt(int((N & 15u) | ((N >> 4) << 14) | (7u << 4) | (15u << 8)));
+}
+
 template <int VT, int KS, int AW>
 __device__ void bf_float_items(const BfHArgs& p) {
     typedef BfChunk<VT> CH;
     typedef typename CH::T ChunkT;
     typedef typename CH::E ElemT;
+    static_assert(sizeof(ChunkT) == 16, "16-byte operand chunks");
+    // A workgroup takes an item; wave w takes its queries 16 w .. 16 w + 15.
+    // The sub-cell's tiles pass through LDS once for all of them, copied by
+    // asynchronous global-to-LDS loads a tile ahead: tile t is staged in
+    // MFMA operand order (chunk k: 64 lanes x 16 bytes, lane l holding row
+    // l % 16's dims of lane group l / 16), double buffered, with its meta
+    // record (rows, attribute words) and its rows' norms; each wave reads
+    // its A operands and the epilogue's data from there.
+    constexpr uint32_t NSLOT = uint32_t(KS) * 64u;
+    constexpr uint32_t NL = (NSLOT + 255u) / 256u;    // 16-byte copies per thread per tile
+    constexpr uint32_t MW = 16u * (1u + AW);
+    __shared__ uint4 s_tile[2][NSLOT];
+    __shared__ uint32_t s_meta[2][MW];
+    __shared__ float s_xn[2][16];
     __shared__ uint64_t s_buf[4][16 * kBfBufQ];
     __shared__ uint64_t s_tk[4][16][kBfHKT];   // per owner: its kept keys, ascending
     __shared__ uint32_t s_cnt[4][16];
     __shared__ float s_tp[4][16];
     __shared__ uint32_t s_bnd[4][2 * AW][16];
-    // chunks per load group: with more than 4, row loads are issued a group
-    // ahead of the MFMAs that use them (two group buffers)
-    constexpr int G = KS <= 4 ? KS : (KS == 6 ? 3 : 4);
-    constexpr int NG = KS / G;
-    static_assert(KS % G == 0 && (NG == 1 || NG % 2 == 0), "chunk groups");
     const ElemT* vec = reinterpret_cast<const ElemT*>(p.vec);
     const ElemT* qrows = reinterpret_cast<const ElemT*>(p.q16);
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = lane_id();
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = lane_id();
     const SubArgs& sa = p.sa;
     const uint32_t nwg = gridDim.x, xcd = blockIdx.x & 7u, k8 = blockIdx.x >> 3;
     const uint32_t nwg_x = (nwg - xcd + 7u) >> 3;
@@ -3280,35 +3312,37 @@ __device__ void bf_float_items(const BfHArgs& p) {
     float* stp = s_tp[wave];
     const uint32_t K = p.K;
     const uint32_t col = lane & 15u, grp = lane >> 4;
-    constexpr uint32_t MW = 16u * (1u + AW);
     const float kInf = __int_as_float(0x7F800000);
     const uint32_t n_seed = p.sitems && *p.ok ? min(*p.nseed, p.nseed_cap) : 0u;
-    uint32_t seed_id = blockIdx.x * 4u + wave, item_id = i_lo + k8 * 4u + wave;
+    // this thread's share of a tile: row tid % 16, lane group (tid % 64) / 16,
+    // chunks wave, wave + 4, ...
+    const uint32_t ld_row = tid & 15u, ld_grp = (tid & 63u) >> 4;
+    uint32_t seed_id = blockIdx.x, item_id = i_lo + k8;
     for (;;) {
         BfItem it;
         if (seed_id < n_seed) {
             it = p.sitems[seed_id];
-            seed_id += nwg * 4u;
+            seed_id += nwg;
         } else if (item_id < i_hi) {
             it = p.items[item_id];
-            item_id += nwg_x * 4u;
+            item_id += nwg_x;
         } else {
             break;
         }
         const uint32_t cell = sa.scell[it.sub];
-        for (uint32_t qb = 0; qb < it.nq; qb += 16u) {
-            const uint32_t nqb = min(16u, it.nq - qb);
-            // Owner state: lane < nqb owns query qb + lane; its kept keys
-            // (d' << 32 | row, ascending) live in s_tk.
-            const bool own_live = lane < nqb;
-            const uint32_t own_q = p.bq[it.qbase + qb + (own_live ? lane : 0u)];
-            const float own_eps2 = own_live ? 2.0f * p.eps[own_q] : 0.0f;
-            const uint32_t gb =
-                own_live ? __hip_atomic_load(&p.gbound[own_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                         : 0xFFFFFFFFu;
-            const float own_bnd = gb == 0xFFFFFFFFu ? kInf : __uint_as_float(gb);
-            uint64_t* tk = s_tk[wave][col];
-            float kth = kInf;
+        const uint32_t qb = 16u * wave;
+        const uint32_t nqb = it.nq > qb ? min(16u, it.nq - qb) : 0u;   // wave-uniform
+        // Owner state: lane < nqb owns query qb + lane; its kept keys
+        // (d' << 32 | row, ascending) live in s_tk.
+        const bool own_live = lane < nqb;
+        const uint32_t own_q = own_live ? p.bq[it.qbase + qb + lane] : 0u;
+        const float own_eps2 = own_live ? 2.0f * p.eps[own_q] : 0.0f;
+        const uint32_t gb =
+            own_live ? __hip_atomic_load(&p.gbound[own_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0xFFFFFFFFu;
+        const float own_bnd = gb == 0xFFFFFFFFu ? kInf : __uint_as_float(gb);
+        uint64_t* tk = s_tk[wave][col];
+        float kth = kInf;
+        if (nqb) {
             wave_fence();
             if (lane < 16u) {
                 cnt[lane] = 0;
@@ -3333,91 +3367,93 @@ __device__ void bf_float_items(const BfHArgs& p) {
                 }
             }
             wave_fence();
-            // Column data: query qb + col (a dead column repeats the first
-            // query; its threshold -1 keeps it from producing survivors).
-            const uint32_t qc = p.bq[it.qbase + qb + (col < nqb ? col : 0u)];
-            ChunkT B[KS];
+        }
+        // Column data: query qb + col (a dead column repeats the wave's
+        // first query, or the item's; its threshold -1 keeps it from
+        // producing survivors).
+        const uint32_t qc = p.bq[it.qbase + (nqb ? qb + (col < nqb ? col : 0u) : 0u)];
+        ChunkT B[KS];
+        if (nqb) {
 #pragma unroll
             for (int k = 0; k < KS; ++k)
                 B[k] = *reinterpret_cast<const ChunkT*>(CH::at(qrows + size_t(qc) * p.D, p.D, grp, k));
-            const float qn = p.qnorm[qc];
-            uint32_t blo[AW], bhi[AW];
+        }
+        const float qn = p.qnorm[qc];
+        uint32_t blo[AW], bhi[AW];
 #pragma unroll
-            for (int w = 0; w < AW; ++w) {
-                blo[w] = s_bnd[wave][2 * w][col];
-                bhi[w] = s_bnd[wave][2 * w + 1][col];
+        for (int w = 0; w < AW; ++w) {
+            blo[w] = nqb ? s_bnd[wave][2 * w][col] : 0u;
+            bhi[w] = nqb ? s_bnd[wave][2 * w + 1][col] : 0u;
+        }
+        float tp = nqb ? stp[col] : -1.0f;
+        // Owner: insert the buffered survivors of its query into its kept
+        // keys and publish the new threshold min(bound, K-th) + 2 eps.
+        auto drain = [&]() {
+            wave_fence();
+            if (lane < 16u) {
+                const uint32_t n = cnt[lane];
+                for (uint32_t e = 0; e < n; ++e) {
+                    const uint64_t c = buf[lane * kBfBufQ + e];
+                    if (c >= tk[kBfHKT - 1]) continue;
+                    uint32_t j = kBfHKT - 1;
+                    while (j > 0 && tk[j - 1] > c) {
+                        tk[j] = tk[j - 1];
+                        --j;
+                    }
+                    tk[j] = c;
+                }
+                cnt[lane] = 0;
+                const uint64_t kk = tk[K - 1];
+                if (kk != kKeySent) kth = __uint_as_float(uint32_t(kk >> 32));
+                if (own_live) stp[lane] = fminf(own_bnd, kth) + own_eps2;
             }
-            float tp = stp[col];
-            // Owner: insert the buffered survivors of its query into its kept
-            // keys and publish the new threshold min(bound, K-th) + 2 eps.
-            auto drain = [&]() {
-                wave_fence();
-                if (lane < 16u) {
-                    const uint32_t n = cnt[lane];
-                    for (uint32_t e = 0; e < n; ++e) {
-                        const uint64_t c = buf[lane * kBfBufQ + e];
-                        if (c >= tk[kBfHKT - 1]) continue;
-                        uint32_t j = kBfHKT - 1;
-                        while (j > 0 && tk[j - 1] > c) {
-                            tk[j] = tk[j - 1];
-                            --j;
-                        }
-                        tk[j] = c;
-                    }
-                    cnt[lane] = 0;
-                    const uint64_t kk = tk[K - 1];
-                    if (kk != kKeySent) kth = __uint_as_float(uint32_t(kk >> 32));
-                    if (own_live) stp[lane] = fminf(own_bnd, kth) + own_eps2;
-                }
-                wave_fence();
-                tp = stp[col];
-            };
-            // A operand rows: lane's row of tile t is meta[col]; groups of G
-            // k-steps are loaded into alternating buffers a group ahead.
-            auto arow_of = [&](uint32_t t) {
-                const uint32_t ra = sa.tmeta[size_t(t) * MW + col];
-                return vec + size_t(ra == kEmpty ? 0u : ra) * p.D;
-            };
-            ChunkT Ab[NG == 1 ? 1 : 2][G];
-            auto load_group = [&](ChunkT (&dst)[G], const ElemT* arow, int g) {
+            wave_fence();
+            tp = stp[col];
+        };
+        // Copy tile t into LDS buffer b (ra: this thread's row of the tile,
+        // loaded a tile ahead); wave 0 also copies the meta record and, lane
+        // l < 16, the norm of row l.
+        auto stage = [&](uint32_t t, uint32_t b, uint32_t ra) {
+            const ElemT* row = vec + size_t(ra == kEmpty ? 0u : ra) * p.D;
 #pragma unroll
-                for (int k = 0; k < G; ++k)
-                    dst[k] = *reinterpret_cast<const ChunkT*>(CH::at(arow, p.D, grp, g * G + k));
-            };
-            const ElemT* arow = it.tb < it.te ? arow_of(it.tb) : vec;
-            if (it.tb < it.te) load_group(Ab[0], arow, 0);
-            for (uint32_t t = it.tb; t < it.te; ++t) {
-                const uint32_t* meta = sa.tmeta + size_t(t) * MW;
-                uint32_t mr[4];
-                float xn[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    mr[i] = meta[4u * grp + i];
-                    xn[i] = mr[i] != kEmpty ? p.xnorm[mr[i]] : 0.0f;
-                }
-                const ElemT* anext = t + 1 < it.te ? arow_of(t + 1) : arow;
+            for (uint32_t j = 0; j < NL; ++j)
+                if (j * 4u + wave < uint32_t(KS))
+                    lds_copy16(CH::at(row, p.D, ld_grp, int(j * 4u + wave)),
+                               __builtin_amdgcn_readfirstlane(lds_addr(&s_tile[b][j * 256u + wave * 64u])));
+            if (wave == 0) {
+                if (lane < MW / 4u)
+                    lds_copy16(sa.tmeta + size_t(t) * MW + 4u * lane, lds_addr(&s_meta[b][0]));
+                if (lane < 16u) lds_copy4(p.xnorm + (ra == kEmpty ? 0u : ra), lds_addr(&s_xn[b][0]));
+            }
+        };
+        uint32_t ra_next = kEmpty;
+        if (it.tb < it.te) {
+            const uint32_t ra0 = sa.tmeta[size_t(it.tb) * MW + ld_row];
+            stage(it.tb, 0, ra0);
+            if (it.tb + 1 < it.te) ra_next = sa.tmeta[size_t(it.tb + 1) * MW + ld_row];
+        }
+        wait_vmcnt<0>();
+        __syncthreads();
+        for (uint32_t t = it.tb; t < it.te; ++t) {
+            const uint32_t cur = (t - it.tb) & 1u;
+            if (t + 1 < it.te) {
+                stage(t + 1, cur ^ 1u, ra_next);
+                if (t + 2 < it.te) ra_next = sa.tmeta[size_t(t + 2) * MW + ld_row];
+            }
+            if (nqb) {
                 float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-                if constexpr (NG == 1) {
 #pragma unroll
-                    for (int k = 0; k < KS; ++k) acc = CH::mma(Ab[0][k], B[k], acc);
-                    if (t + 1 < it.te) load_group(Ab[0], anext, 0);
-                } else {
-#pragma unroll
-                    for (int g = 0; g < NG; ++g) {
-                        // the next group: of this tile, or the next tile's first
-                        if (g + 1 < NG) load_group(Ab[(g + 1) & 1], arow, g + 1);
-                        else if (t + 1 < it.te) load_group(Ab[0], anext, 0);
-#pragma unroll
-                        for (int k = 0; k < G; ++k) acc = CH::mma(Ab[g & 1][k], B[g * G + k], acc);
-                    }
-                }
-                arow = anext;
+                for (int k = 0; k < KS; ++k)
+                    acc = CH::mma(*reinterpret_cast<const ChunkT*>(&s_tile[cur][uint32_t(k) * 64u + lane]), B[k], acc);
+                const uint32_t* meta = s_meta[cur];
                 bool full = false;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     // point 4 grp + i, query column col
-                    const float d = fmaxf(__fsub_rn(__fadd_rn(qn, xn[i]), __fmul_rn(2.0f, acc[i])), 0.0f);
-                    bool ok = d <= tp && mr[i] != kEmpty;
+                    const uint32_t mr = meta[4u * grp + i];
+                    const float xn = s_xn[cur][4u * grp + i];
+                    const float d = fmaxf(__fsub_rn(__fadd_rn(qn, xn), __fmul_rn(2.0f, acc[i])), 0.0f);
+                    bool ok = d <= tp && mr != kEmpty;
                     if (!__builtin_amdgcn_ballot_w64(ok)) continue;
                     if (!it.inside) {
 #pragma unroll
@@ -3428,12 +3464,16 @@ __device__ void bf_float_items(const BfHArgs& p) {
                     }
                     if (ok) {
                         const uint32_t slot = atomicAdd(&cnt[col], 1u);
-                        buf[col * kBfBufQ + slot] = (uint64_t(__float_as_uint(d)) << 32) | mr[i];
+                        buf[col * kBfBufQ + slot] = (uint64_t(__float_as_uint(d)) << 32) | mr;
                         full |= slot + 1u >= kBfDrainAt;
                     }
                 }
                 if (__builtin_amdgcn_ballot_w64(full)) drain();
             }
+            wait_vmcnt<0>();
+            __syncthreads();
+        }
+        if (nqb) {
             drain();
             if (own_live) {
                 if (kth != kInf) atomicMin(&p.gbound[own_q], __float_as_uint(kth));
