@@ -428,6 +428,12 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
                 ix.xnormf.upload(xn);
                 ix.xmaxf = std::sqrt(xm) * (1.0 + 1e-6);
             }
+            // the brute force's tile records: its tiles' rows in MFMA operand
+            // order, contiguous per tile, with their meta records and norms
+            const uint32_t KS = fvt == 1 ? D / 32 : D / 16;
+            ix.frec.alloc(size_t(ix.ntile) * gf::bf_frec_bytes(KS, ix.AW));
+            GF_HIP(gf::launch_tile_frec(ix.vec.p, fvt, D, ix.tmeta.p, ix.xnormf.p, ix.AW, ix.ntile, ix.frec.p,
+                                        ix.stream));
             ix.hf = true;
         }
         GF_HIP(hipStreamSynchronize(ix.stream));
@@ -1117,7 +1123,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
             GF_HIP(gf::launch_zero_u32(b->hover.p, Q, st));
             gf::BfHArgs ha{};
             ha.sa = sub_args(*ix);
-            ha.vec = ix->vec.p; ha.xnorm = ix->xnormf.p;
+            ha.rec = ix->frec.p;
             ha.q16 = fvt == 1 ? static_cast<const void*>(b->q16v.p) : static_cast<const void*>(b->qf32.p);
             ha.qnorm = b->qnf.p; ha.eps = b->heps.p; ha.lo = b->lo.p; ha.hi = b->hi.p;
             ha.items = b->items.p; ha.nitems = tot + 4; ha.bq = b->bq.p; ha.part_off = b->part_off.p;

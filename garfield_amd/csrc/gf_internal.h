@@ -140,6 +140,10 @@ struct BfItem {
     uint32_t inside;                   // 1: every query's range contains the sub-cell's box
 };
 __host__ __device__ inline uint32_t bf_rec_bytes(uint32_t D, uint32_t AW) { return (D / 64u) * 1024u + 128u + 64u * (1u + AW); }
+// Float tile record of the float MFMA brute force (KS operand chunks of 64
+// lanes x 16 bytes in MFMA operand order, then the tile's meta record of
+// 16 (1 + AW) words, then its 16 rows' |x|^2 as fp32).
+__host__ __device__ inline uint32_t bf_frec_bytes(uint32_t KS, uint32_t AW) { return KS * 1024u + 64u * (2u + AW); }
 struct BfGemmArgs {
     SubArgs sa;
     const uint8_t* rec;        // tile records (bf_rec_bytes each)
@@ -174,8 +178,7 @@ struct BfGemmArgs {
 constexpr uint32_t kBfHKT = 32;       // keys an item keeps per query
 struct BfHArgs {
     SubArgs sa;
-    const void* vec;           // rows (binary16 or fp32), cell-major, D per row
-    const float* xnorm;        // per row |x|^2
+    const uint8_t* rec;        // tile records (bf_frec_bytes each)
     const void* q16;           // Q*D queries of the rows' type
     const float* qnorm;        // per query |q|^2
     const float* eps;          // per query bound of |d' - d|
@@ -422,6 +425,10 @@ hipError_t launch_bf_final(const BfFinalArgs& a, uint32_t grid, hipStream_t st);
 hipError_t launch_tile_i8(const void* vec_cm, bool u8, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
                           int8_t* vt, int32_t* tnorm, hipStream_t st);
 // The brute force's tile records (bf_rec_bytes each) from the same inputs.
+// Float tile records (bf_frec_bytes) of ntile tiles from cell-major rows of
+// type vt (1 binary16, 0 fp32) and their norms.
+hipError_t launch_tile_frec(const void* vec, int vt, uint32_t D, const uint32_t* tmeta, const float* xnorm,
+                            uint32_t AW, uint32_t ntile, uint8_t* rec, hipStream_t st);
 hipError_t launch_tile_rec(const void* vec_cm, bool u8, uint32_t D, const uint32_t* tmeta, uint32_t AW, uint32_t ntile,
                            uint8_t* rec, hipStream_t st);
 hipError_t launch_note_bf(const uint32_t* tot, uint32_t* note, hipStream_t st);

@@ -3281,24 +3281,30 @@ __device__ void bf_float_items(const BfHArgs& p) {
     typedef typename CH::E ElemT;
     static_assert(sizeof(ChunkT) == 16, "16-byte operand chunks");
     // A workgroup takes an item; wave w takes its queries 16 w .. 16 w + 15.
-    // The sub-cell's tiles pass through LDS once for all of them, copied by
-    // asynchronous global-to-LDS loads a tile ahead: tile t is staged in
-    // MFMA operand order (chunk k: 64 lanes x 16 bytes, lane l holding row
-    // l % 16's dims of lane group l / 16), double buffered, with its meta
-    // record (rows, attribute words) and its rows' norms; each wave reads
-    // its A operands and the epilogue's data from there.
+    // The sub-cell's tile records (bf_frec_bytes: operand chunks in MFMA
+    // operand order, chunk k = 64 lanes x 16 bytes, lane l holding row
+    // l % 16's dims of lane group l / 16; then the meta record and the
+    // rows' norms) pass through LDS once for all of them, each copied whole
+    // by asynchronous global-to-LDS loads a tile ahead into a double buffer
+    // (a third buffer, two tiles ahead, measured slower: it leaves room for
+    // one workgroup per CU instead of two); each wave reads its A operands
+    // and the epilogue's data from there.
     constexpr uint32_t NSLOT = uint32_t(KS) * 64u;
     constexpr uint32_t NL = (NSLOT + 255u) / 256u;    // 16-byte copies per thread per tile
     constexpr uint32_t MW = 16u * (1u + AW);
+    constexpr uint32_t NTAIL = (MW + 16u) / 4u;       // 16-byte chunks of meta record and norms
+    constexpr uint32_t RB = uint32_t(KS) * 1024u + 64u * (2u + AW);
+    static_assert(RB == NSLOT * 16u + NTAIL * 16u, "record layout");
     __shared__ uint4 s_tile[2][NSLOT];
-    __shared__ uint32_t s_meta[2][MW];
-    __shared__ float s_xn[2][16];
-    __shared__ uint64_t s_buf[4][16 * kBfBufQ];
-    __shared__ uint64_t s_tk[4][16][kBfHKT];   // per owner: its kept keys, ascending
+    __shared__ uint32_t s_tail[2][MW + 16u];   // meta words, then the norms
+    // Per-owner lists padded by one key, so that the 16 owners' lists start
+    // on different LDS banks (the drain's accesses go to all 16 at once).
+    constexpr uint32_t BQ = kBfBufQ + 1u, TK = kBfHKT + 1u;
+    __shared__ uint64_t s_buf[4][16 * BQ];
+    __shared__ uint64_t s_tk[4][16][TK];   // per owner: its kept keys, ascending
     __shared__ uint32_t s_cnt[4][16];
     __shared__ float s_tp[4][16];
     __shared__ uint32_t s_bnd[4][2 * AW][16];
-    const ElemT* vec = reinterpret_cast<const ElemT*>(p.vec);
     const ElemT* qrows = reinterpret_cast<const ElemT*>(p.q16);
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = lane_id();
@@ -3314,9 +3320,6 @@ __device__ void bf_float_items(const BfHArgs& p) {
     const uint32_t col = lane & 15u, grp = lane >> 4;
     const float kInf = __int_as_float(0x7F800000);
     const uint32_t n_seed = p.sitems && *p.ok ? min(*p.nseed, p.nseed_cap) : 0u;
-    // this thread's share of a tile: row tid % 16, lane group (tid % 64) / 16,
-    // chunks wave, wave + 4, ...
-    const uint32_t ld_row = tid & 15u, ld_grp = (tid & 63u) >> 4;
     uint32_t seed_id = blockIdx.x, item_id = i_lo + k8;
     for (;;) {
         BfItem it;
@@ -3393,7 +3396,7 @@ __device__ void bf_float_items(const BfHArgs& p) {
             if (lane < 16u) {
                 const uint32_t n = cnt[lane];
                 for (uint32_t e = 0; e < n; ++e) {
-                    const uint64_t c = buf[lane * kBfBufQ + e];
+                    const uint64_t c = buf[lane * BQ + e];
                     if (c >= tk[kBfHKT - 1]) continue;
                     uint32_t j = kBfHKT - 1;
                     while (j > 0 && tk[j - 1] > c) {
@@ -3410,48 +3413,36 @@ __device__ void bf_float_items(const BfHArgs& p) {
             wave_fence();
             tp = stp[col];
         };
-        // Copy tile t into LDS buffer b (ra: this thread's row of the tile,
-        // loaded a tile ahead); wave 0 also copies the meta record and, lane
-        // l < 16, the norm of row l.
-        auto stage = [&](uint32_t t, uint32_t b, uint32_t ra) {
-            const ElemT* row = vec + size_t(ra == kEmpty ? 0u : ra) * p.D;
+        // Copy tile t's record into LDS buffer b: thread tid its 16-byte
+        // chunks j * 256 + tid of the operand (chunk 4 j + wave: a
+        // wave-uniform bound), wave 0 the meta record and norms.
+        auto stage = [&](uint32_t t, uint32_t b) {
+            const uint8_t* src = p.rec + size_t(t) * RB;
 #pragma unroll
             for (uint32_t j = 0; j < NL; ++j)
                 if (j * 4u + wave < uint32_t(KS))
-                    lds_copy16(CH::at(row, p.D, ld_grp, int(j * 4u + wave)),
+                    lds_copy16(src + (j * 256u + tid) * 16u,
                                __builtin_amdgcn_readfirstlane(lds_addr(&s_tile[b][j * 256u + wave * 64u])));
-            if (wave == 0) {
-                if (lane < MW / 4u)
-                    lds_copy16(sa.tmeta + size_t(t) * MW + 4u * lane, lds_addr(&s_meta[b][0]));
-                if (lane < 16u) lds_copy4(p.xnorm + (ra == kEmpty ? 0u : ra), lds_addr(&s_xn[b][0]));
-            }
+            if (wave == 0 && lane < NTAIL) lds_copy16(src + NSLOT * 16u + lane * 16u, lds_addr(&s_tail[b][0]));
         };
-        uint32_t ra_next = kEmpty;
-        if (it.tb < it.te) {
-            const uint32_t ra0 = sa.tmeta[size_t(it.tb) * MW + ld_row];
-            stage(it.tb, 0, ra0);
-            if (it.tb + 1 < it.te) ra_next = sa.tmeta[size_t(it.tb + 1) * MW + ld_row];
-        }
+        if (it.tb < it.te) stage(it.tb, 0);
         wait_vmcnt<0>();
         __syncthreads();
         for (uint32_t t = it.tb; t < it.te; ++t) {
             const uint32_t cur = (t - it.tb) & 1u;
-            if (t + 1 < it.te) {
-                stage(t + 1, cur ^ 1u, ra_next);
-                if (t + 2 < it.te) ra_next = sa.tmeta[size_t(t + 2) * MW + ld_row];
-            }
+            if (t + 1 < it.te) stage(t + 1, cur ^ 1u);
             if (nqb) {
                 float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int k = 0; k < KS; ++k)
                     acc = CH::mma(*reinterpret_cast<const ChunkT*>(&s_tile[cur][uint32_t(k) * 64u + lane]), B[k], acc);
-                const uint32_t* meta = s_meta[cur];
+                const uint32_t* meta = s_tail[cur];
                 bool full = false;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     // point 4 grp + i, query column col
                     const uint32_t mr = meta[4u * grp + i];
-                    const float xn = s_xn[cur][4u * grp + i];
+                    const float xn = __uint_as_float(meta[MW + 4u * grp + i]);
                     const float d = fmaxf(__fsub_rn(__fadd_rn(qn, xn), __fmul_rn(2.0f, acc[i])), 0.0f);
                     bool ok = d <= tp && mr != kEmpty;
                     if (!__builtin_amdgcn_ballot_w64(ok)) continue;
@@ -3464,7 +3455,7 @@ __device__ void bf_float_items(const BfHArgs& p) {
                     }
                     if (ok) {
                         const uint32_t slot = atomicAdd(&cnt[col], 1u);
-                        buf[col * kBfBufQ + slot] = (uint64_t(__float_as_uint(d)) << 32) | mr;
+                        buf[col * BQ + slot] = (uint64_t(__float_as_uint(d)) << 32) | mr;
                         full |= slot + 1u >= kBfDrainAt;
                     }
                 }
@@ -3492,6 +3483,30 @@ __device__ void bf_float_items(const BfHArgs& p) {
             wave_fence();
         }
     }
+}
+
+// Float tile records (bf_frec_bytes) for the float MFMA brute force: one
+// wave per tile copies its 16 rows' operand chunks into MFMA operand order
+// (BfChunk<VT>::at), then the meta record and the rows' norms; an empty slot
+// (row kEmpty) gets zero operands and norm.
+template <int VT>
+__global__ __launch_bounds__(64) void k_tile_frec(const void* vec, uint32_t D, const uint32_t* tmeta,
+                                                  const float* xnorm, uint32_t AW, uint8_t* rec) {
+    typedef BfChunk<VT> CH;
+    typedef typename CH::E ElemT;
+    const uint32_t t = blockIdx.x, lane = lane_id();
+    const uint32_t KS = VT == 1 ? D / 32u : D / 16u, MW = 16u * (1u + AW);
+    uint8_t* dst = rec + size_t(t) * bf_frec_bytes(KS, AW);
+    const uint32_t row = tmeta[size_t(t) * MW + (lane & 15u)];
+    const ElemT* src = reinterpret_cast<const ElemT*>(vec) + size_t(row == kEmpty ? 0u : row) * D;
+    for (uint32_t k = 0; k < KS; ++k) {
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (row != kEmpty) v = *reinterpret_cast<const uint4*>(CH::at(src, D, lane >> 4, int(k)));
+        *reinterpret_cast<uint4*>(dst + k * 1024u + lane * 16u) = v;
+    }
+    uint32_t* tail = reinterpret_cast<uint32_t*>(dst + KS * 1024u);
+    for (uint32_t w = lane; w < MW; w += 64u) tail[w] = tmeta[size_t(t) * MW + w];
+    if (lane < 16u) tail[MW + lane] = row != kEmpty ? __float_as_uint(xnorm[row]) : 0u;
 }
 
 template <int KS, int AW>
@@ -4419,6 +4434,16 @@ hipError_t launch_tile_i8(const void* vec_cm, bool u8, uint32_t D, const uint32_
     else
         hipLaunchKernelGGL(k_tile_i8<float>, dim3(ntile), dim3(64), 0, st, static_cast<const float*>(vec_cm), D,
                            tmeta, AW, vt, vs, tnorm, size_t(32), static_cast<uint32_t*>(nullptr), size_t(0));
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_frec(const void* vec, int vt, uint32_t D, const uint32_t* tmeta, const float* xnorm,
+                            uint32_t AW, uint32_t ntile, uint8_t* rec, hipStream_t st) {
+    if (!ntile) return hipSuccess;
+    if (vt == 1)
+        hipLaunchKernelGGL(k_tile_frec<1>, dim3(ntile), dim3(64), 0, st, vec, D, tmeta, xnorm, AW, rec);
+    else
+        hipLaunchKernelGGL(k_tile_frec<0>, dim3(ntile), dim3(64), 0, st, vec, D, tmeta, xnorm, AW, rec);
     return hipGetLastError();
 }
 

@@ -273,6 +273,7 @@ struct gf_index {
     // rows, with |x|^2 per row and the largest |x| over the index.
     bool hf = false;
     DevBuf<float> xnormf;
+    DevBuf<uint8_t> frec;   // its tile records (gf::bf_frec_bytes each)
     double xmaxf = 0.0;
     int ncu = 0;
     int wclk_khz = 100000;   // rate of the device wall clock the search's timestamps read
@@ -288,7 +289,7 @@ struct gf_index {
                cross.bytes() + offset.bytes() + gidx.bytes() + lrow.bytes() + grid.bytes() + doff.bytes() +
                hist.bytes() + tile_cell.bytes() + tile_row0.bytes() + tile_n.bytes() + centres.bytes() +
                sbase.bytes() + scell.bytes() + ssize.bytes() + stile.bytes() + tmeta.bytes() + sbox.bytes() +
-               sorder.bytes() + abase.bytes() + trec.bytes() +
+               sorder.bytes() + abase.bytes() + trec.bytes() + xnormf.bytes() + frec.bytes() +
                (sx ? sx->turn[0].bytes() + sx->turn[1].bytes() + sx->trec.bytes() : 0);
     }
 };
