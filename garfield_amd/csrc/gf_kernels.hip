@@ -3046,13 +3046,11 @@ struct BfWave {
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[k], B[j][k], acc[j], 0, 0, 0);
     }
-    template <class Meta>
-    __device__ __forceinline__ void tile(const v4i32_t (&A)[KS], const v4i32_t& mh, Meta meta) {
-        v4i32_t acc[4];
-        mma(A, mh, acc);
-        epilogue(acc, mh, meta);
-    }
-    template <class Meta>
+    // RANGE false: every query of the item contains the sub-cell's box, so
+    // every point is in range and only the distance test runs (padding and
+    // dead columns still fail it: their accumulator is INT32_MIN, their
+    // threshold INT32_MAX).
+    template <bool RANGE, class Meta>
     __device__ __forceinline__ void epilogue(const v4i32_t (&acc)[4], const v4i32_t& mh, Meta meta) {
         // Distance first, on the max of each column tile's four rows: jm
         // has bit j when some lane holds a pair of column tile j within its
@@ -3075,11 +3073,13 @@ struct BfWave {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 bool ok = acc[j][i] >= tp[j];
-                const uint32_t x0 = uint32_t(ma[0][i]);
-                ok &= clamp16(x0, blo[j][0], bhi[j][0]) == x0;
-                if (AW > 1) {
-                    const uint32_t x1 = uint32_t(ma[AW - 1][i]);
-                    ok &= clamp16(x1, blo[j][AW - 1], bhi[j][AW - 1]) == x1;
+                if constexpr (RANGE) {
+                    const uint32_t x0 = uint32_t(ma[0][i]);
+                    ok &= clamp16(x0, blo[j][0], bhi[j][0]) == x0;
+                    if (AW > 1) {
+                        const uint32_t x1 = uint32_t(ma[AW - 1][i]);
+                        ok &= clamp16(x1, blo[j][AW - 1], bhi[j][AW - 1]) == x1;
+                    }
                 }
                 okm |= ok ? 1u << i : 0u;
             }
@@ -3175,36 +3175,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 && 
 #pragma unroll
             for (int k = 0; k < KS; ++k) A[k] = bload(lane * 16u, (t - t0) * RB + k * 1024u);
         };
-        auto load_m = [&](TileMeta& M, uint32_t t) __attribute__((always_inline)) {
-            const uint32_t o = (t - t0) * RB + KB;
-            M.mh = bload(16u * w.grp, o);
-            M.mn = bload(16u * w.grp, o + 64u);
-            M.mr = bload(16u * w.grp, o + 128u);
+        // the tile loop, with the range test (rg true) or without it (an
+        // inside item: its attribute words are not even loaded)
+        auto run = [&](auto rg) __attribute__((always_inline)) {
+            constexpr bool RANGE = decltype(rg)::value;
+            auto load_m = [&](TileMeta& M, uint32_t t) __attribute__((always_inline)) {
+                const uint32_t o = (t - t0) * RB + KB;
+                M.mh = bload(16u * w.grp, o);
+                M.mn = bload(16u * w.grp, o + 64u);
+                M.mr = bload(16u * w.grp, o + 128u);
+                if constexpr (RANGE) {
 #pragma unroll
-            for (int a = 0; a < AW; ++a) M.ma[a] = bload(16u * w.grp, o + 128u + 64u * (1 + a));
-        };
-        auto step = [&](const TileMeta& M, TileMeta& Mn, uint32_t t) __attribute__((always_inline)) {
-            v4i32_t acc[4];
-            w.mma(A, M.mh, acc);
-            if (t + 1 < t1) {
-                load_a(t + 1);
-                load_m(Mn, t + 1);
+                    for (int a = 0; a < AW; ++a) M.ma[a] = bload(16u * w.grp, o + 128u + 64u * (1 + a));
+                }
+            };
+            auto step = [&](const TileMeta& M, TileMeta& Mn, uint32_t t) __attribute__((always_inline)) {
+                v4i32_t acc[4];
+                w.mma(A, M.mh, acc);
+                if (t + 1 < t1) {
+                    load_a(t + 1);
+                    load_m(Mn, t + 1);
+                }
+                w.template epilogue<RANGE>(
+                    acc, M.mh, [&](v4i32_t& mn, v4i32_t& mr, v4i32_t (&ma)[AW]) __attribute__((always_inline)) {
+                        mn = M.mn;
+                        mr = M.mr;
+                        if constexpr (RANGE) {
+#pragma unroll
+                            for (int a = 0; a < AW; ++a) ma[a] = M.ma[a];
+                        }
+                    });
+            };
+            TileMeta M0, M1;
+            load_a(t0);
+            load_m(M0, t0);
+            for (uint32_t t = t0; t < t1; t += 2) {
+                step(M0, M1, t);
+                if (t + 1 >= t1) break;
+                step(M1, M0, t + 1);
             }
-            w.epilogue(acc, M.mh, [&](v4i32_t& mn, v4i32_t& mr, v4i32_t (&ma)[AW]) __attribute__((always_inline)) {
-                mn = M.mn;
-                mr = M.mr;
-#pragma unroll
-                for (int a = 0; a < AW; ++a) ma[a] = M.ma[a];
-            });
         };
-        TileMeta M0, M1;
-        load_a(t0);
-        load_m(M0, t0);
-        for (uint32_t t = t0; t < t1; t += 2) {
-            step(M0, M1, t);
-            if (t + 1 >= t1) break;
-            step(M1, M0, t + 1);
-        }
+        if (__builtin_amdgcn_readfirstlane(it.inside)) run(std::false_type{});
+        else run(std::true_type{});
         w.finish(p);
     }
 }
