@@ -3018,9 +3018,14 @@ struct BfWave {
                         tk[k] = lt ? c : v;
                         c = lt ? v : c;
                     }
+                    // the K-th key (a move when K is the template's KT)
+                    if (K == uint32_t(KT)) {
+                        kth = tk[KT - 1];
+                    } else {
 #pragma unroll
-                    for (int k = 0; k < KT; ++k)
-                        if (uint32_t(k) == K - 1) kth = tk[k];
+                        for (int k = 0; k < KT; ++k)
+                            if (uint32_t(k) == K - 1) kth = tk[k];
+                    }
                 }
             }
             cnt[lane] = 0;
@@ -3160,7 +3165,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 && 
         } else {
             break;
         }
-        w.begin(p, it, sa.scell[it.sub]);
         const uint32_t t0 = it.tb, t1 = it.te, ntile = t1 - t0;
         const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint8_t*>(p.rec + size_t(t0) * RB), 0, ntile * RB, 0x00020000);
@@ -3206,9 +3210,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 && 
                         }
                     });
             };
+            // the first tile's loads fly while the item's queries load
             TileMeta M0, M1;
             load_a(t0);
             load_m(M0, t0);
+            w.begin(p, it, sa.scell[it.sub]);
             for (uint32_t t = t0; t < t1; t += 2) {
                 step(M0, M1, t);
                 if (t + 1 >= t1) break;
