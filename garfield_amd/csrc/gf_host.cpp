@@ -563,15 +563,15 @@ void entry_points_ref(uint32_t N, uint32_t P, uint32_t R, uint32_t* out) {
 // partially covered ones are scanned; without sub-cells, per-cell tiles.
 void count_selectivity(gf_batch& b, hipStream_t st) {
     gf_index* ix = b.ix;
-    GF_HIP(hipMemsetAsync(b.selcount.p, 0, b.Q * sizeof(uint32_t), st));
+    GF_HIP(gf::launch_zero_u32(b.selcount.p, b.Q, st));
     if (ix->sub) {
         gf::SubSelArgs sl{};
         sl.sa = sub_args(*ix);
         sl.Q = b.Q; sl.lo = b.lo.p; sl.hi = b.hi.p; sl.selcount = b.selcount.p;
         GF_HIP(gf::launch_subsel(sl, st));
     } else {
-        GF_HIP(hipMemsetAsync(b.ccount.p, 0, ix->P * sizeof(uint32_t), st));
-        GF_HIP(hipMemsetAsync(b.cfill.p, 0, ix->P * sizeof(uint32_t), st));
+        GF_HIP(gf::launch_zero_u32(b.ccount.p, ix->P, st));
+        GF_HIP(gf::launch_zero_u32(b.cfill.p, ix->P, st));
         GF_HIP(gf::launch_cellq_count(b.Q, ix->P, b.cells.p, b.counts.p, b.ccount.p, st));
         GF_HIP(gf::launch_scan_small(b.ccount.p, ix->P, b.cstart.p, st));
         GF_HIP(gf::launch_cellq_fill(b.Q, ix->P, b.cells.p, b.counts.p, b.cstart.p, b.cfill.p, b.cellq.p, st));
@@ -813,23 +813,36 @@ gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms) {
         b->bf_all = true;
         set_device(ix);
         hipStream_t st = ix->stream;
-        b->stage_event(0, st);
-        GF_HIP(gf::launch_cells(b->Q, ix->a, b->lo.p, b->hi.p, ix->grid.p, ix->doff.p, ix->l_q.p, ix->r_q.p, ix->P,
-                                ix->offset.p, b->cells.p, b->counts.p, st));
-        if (prefilter >= 1.0f) {
-            // count / N <= prefilter holds for every count: every query is
-            // routed to the brute force without counting (the routing is the
-            // reference's); the exact counts are made when they are asked for.
-            GF_HIP(hipMemsetAsync(b->selcount.p, 0, b->Q * sizeof(uint32_t), st));
-            b->sel_exact = false;
-        } else {
-            count_selectivity(*b, st);
-            b->sel_exact = true;
+        b->ensure_stamps();
+        const bool count = prefilter < 1.0f;
+        auto enqueue = [&]() {
+            GF_HIP(gf::launch_stamp(b->stamps.p + gf_batch::kStampA, st));
+            GF_HIP(gf::launch_cells(b->Q, ix->a, b->lo.p, b->hi.p, ix->grid.p, ix->doff.p, ix->l_q.p, ix->r_q.p,
+                                    ix->P, ix->offset.p, b->cells.p, b->counts.p, st));
+            // prefilter >= 1: count / N <= prefilter holds for every count,
+            // so every query is routed to the brute force without counting
+            // (the routing is the reference's); the exact counts are made
+            // when they are asked for.
+            if (count) count_selectivity(*b, st);
+            else GF_HIP(gf::launch_zero_u32(b->selcount.p, b->Q, st));
+            GF_HIP(gf::launch_route(b->Q, ix->N, prefilter, b->selcount.p, b->counts.p, b->little.p, st));
+            GF_HIP(gf::launch_stamp(b->stamps.p + gf_batch::kStampA + 1, st));
+        };
+        uint32_t pf = 0;
+        std::memcpy(&pf, &prefilter, sizeof(pf));
+        const uint64_t key[] = {uint64_t(uintptr_t(ix)), pf, b->Q, uint64_t(uintptr_t(b->lo.p)),
+                                uint64_t(uintptr_t(b->hi.p)), uint64_t(uintptr_t(b->cells.p)),
+                                uint64_t(uintptr_t(b->counts.p)), uint64_t(uintptr_t(b->selcount.p)),
+                                uint64_t(uintptr_t(b->little.p)), uint64_t(uintptr_t(b->ccount.p)),
+                                uint64_t(uintptr_t(b->cfill.p)), uint64_t(uintptr_t(b->cstart.p)),
+                                uint64_t(uintptr_t(b->cellq.p)), uint64_t(uintptr_t(b->stamps.p))};
+        b->sg[gf_batch::kGraphA].run(std::vector<uint64_t>(std::begin(key), std::end(key)), st, enqueue);
+        b->sel_exact = count;
+        b->time_a = gf_batch::kTimeStamps;
+        if (ms) {
+            b->fetch_stamps(gf_batch::kStampA, 2, st);
+            *ms = b->stamp_ms(gf_batch::kStampA);
         }
-        GF_HIP(gf::launch_route(b->Q, ix->N, prefilter, b->selcount.p, b->counts.p, b->little.p, st));
-        b->stage_event(1, st);
-        b->sev_a = true;
-        if (ms) *ms = b->stage_ms(0);
         b->marked = true;
     });
 }
@@ -853,9 +866,9 @@ gf_status gf_mark_cells_grid(gf_batch* b, const float* attr_min, const float* at
                                      threshold, b->cells.p, b->counts.p, b->little.p, b->flags.p, st));
         GF_HIP(hipMemsetAsync(b->selcount.p, 0, b->Q * sizeof(uint32_t), st));
         b->stage_event(1, st);
-        b->sev_a = true;
+        b->time_a = gf_batch::kTimeEvents;
         // amin and width are freed on return: their reads must be done first
-        const double el = b->stage_ms(0);
+        const double el = b->event_ms();
         if (ms) *ms = el;
         b->marked = true;
         b->flags_ready = true;
@@ -871,31 +884,42 @@ gf_status gf_order_cells(gf_batch* b, uint32_t topc, double* ms) {
         GF_REQUIRE(topc >= 1 && topc <= 16, GF_E_ARG, "topc must be in [1, 16]");
         gf_index* ix = b->ix;
         set_device(ix);
-        if (!ix->C) { if (ms) *ms = 0.0; b->sev_b = false; return; }
+        if (!ix->C) { if (ms) *ms = 0.0; b->time_b = gf_batch::kTimeNone; return; }
         hipStream_t st = ix->stream;
         if (b->topk.n < size_t(b->Q) * topc) b->topk.alloc(size_t(b->Q) * topc);
+        const bool top = topc <= 4;
+        if (!top && !b->cdist.p) b->cdist.alloc(size_t(b->Q) * ix->C);
         b->topc = topc;
-        b->stage_event(2, st);
-        if (topc <= 4) {
-            // nearest centres straight from the MFMA tiles; the distance
-            // matrix is made only if gf_batch_get_centroid asks for it
-            GF_HIP(gf::launch_centroid_top(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp,
-                                           ix->Cp, ix->Dp, topc, b->topk.p, st));
-            GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, nullptr, ix->hist.p, b->cells.p, b->counts.p,
-                                    b->topk.p, st, true, ix->ref_ties));
-            b->cdist_ready = false;
-        } else {
-            if (!b->cdist.p) b->cdist.alloc(size_t(b->Q) * ix->C);
-            GF_HIP(gf::launch_centroid(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp, ix->Cp,
-                                       ix->Dp, b->cdist.p, st));
-            GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, b->cdist.p, ix->hist.p, b->cells.p, b->counts.p,
-                                    b->topk.p, st, false, ix->ref_ties));
-            b->cdist_ready = true;
-        }
+        b->ensure_stamps();
+        auto enqueue = [&]() {
+            GF_HIP(gf::launch_stamp(b->stamps.p + gf_batch::kStampB, st));
+            if (top) {
+                // nearest centres straight from the MFMA tiles; the distance
+                // matrix is made only if gf_batch_get_centroid asks for it
+                GF_HIP(gf::launch_centroid_top(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp,
+                                               ix->Cp, ix->Dp, topc, b->topk.p, st));
+                GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, nullptr, ix->hist.p, b->cells.p, b->counts.p,
+                                        b->topk.p, st, true, ix->ref_ties));
+            } else {
+                GF_HIP(gf::launch_centroid(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp,
+                                           ix->Cp, ix->Dp, b->cdist.p, st));
+                GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, b->cdist.p, ix->hist.p, b->cells.p, b->counts.p,
+                                        b->topk.p, st, false, ix->ref_ties));
+            }
+            GF_HIP(gf::launch_stamp(b->stamps.p + gf_batch::kStampB + 1, st));
+        };
+        const uint64_t key[] = {uint64_t(uintptr_t(ix)), topc, b->Q, uint64_t(uintptr_t(b->topk.p)),
+                                uint64_t(uintptr_t(b->cdist.p)), uint64_t(uintptr_t(b->q16.p)),
+                                uint64_t(uintptr_t(b->qnorm.p)), uint64_t(uintptr_t(b->cells.p)),
+                                uint64_t(uintptr_t(b->counts.p)), uint64_t(uintptr_t(b->stamps.p))};
+        b->sg[gf_batch::kGraphB].run(std::vector<uint64_t>(std::begin(key), std::end(key)), st, enqueue);
+        b->cdist_ready = !top;
         b->ordered = true;
-        b->stage_event(3, st);
-        b->sev_b = true;
-        if (ms) *ms = b->stage_ms(2);
+        b->time_b = gf_batch::kTimeStamps;
+        if (ms) {
+            b->fetch_stamps(gf_batch::kStampB, 2, st);
+            *ms = b->stamp_ms(gf_batch::kStampB);
+        }
     });
 }
 
@@ -911,16 +935,21 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     GF_REQUIRE(K >= 1 && K <= 64, GF_E_ARG, "K must be in [1, 64]");
     GF_REQUIRE(rl >= 1 && rl <= 16, GF_E_ARG, "rl must be in [1, 16]");
     set_device(ix);
-    // Device times of the latest stage calls (their events precede the
-    // search on the stream, which the search has waited for).
-    auto stage_times = [&]() {
+    // Device times of the latest stage calls (their events and timestamps
+    // precede the search on the stream, which the search has waited for;
+    // gathered: the resident search copied the timestamps with its results).
+    auto stage_times = [&](bool gathered) {
         if (!stats) return;
-        stats->ms_stage_a = b->sev_a ? b->stage_ms(0) : 0.0;
-        stats->ms_stage_b = b->sev_b ? b->stage_ms(2) : 0.0;
+        if (!gathered && (b->time_a == gf_batch::kTimeStamps || b->time_b == gf_batch::kTimeStamps))
+            b->fetch_stamps(gf_batch::kStampA, 4, ix->stream);
+        stats->ms_stage_a = b->time_a == gf_batch::kTimeEvents   ? b->event_ms()
+                            : b->time_a == gf_batch::kTimeStamps ? b->stamp_ms(gf_batch::kStampA)
+                                                                 : 0.0;
+        stats->ms_stage_b = b->time_b == gf_batch::kTimeStamps ? b->stamp_ms(gf_batch::kStampB) : 0.0;
     };
     if (ix->sx) {
         gf::stream_search(*b, *opts, ids, dists, stats);
-        stage_times();
+        stage_times(false);
         return;
     }
     hipStream_t st = ix->stream;
@@ -1065,7 +1094,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     // Device timestamps (wall clock, kernels on the stream, so that they
     // time a replayed graph too): [0] search start, [1] after traversal,
     // [2] end, [3..4] around the MFMA brute-force launches.
-    if (!b->stamps.n) { b->stamps.alloc(8); b->h_stamps.alloc(8); }
+    b->ensure_stamps();
     uint64_t* stamp = b->stamps.p;
     auto launch_gemm = [&]() {
         gf::BfSchedArgs sc{};
@@ -1293,7 +1322,8 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         stats->ms_bruteforce = t_bf;
         stats->ms_total = double(t_tr) + double(t_bf);
         stats->ms_bf_kernel = t_g;
-        stats->graph = b->graph_replayed ? 1u : 0u;
+        stats->graph = (b->graph_replayed() ? 1u : 0u) | (b->sg[gf_batch::kGraphA].replayed ? 2u : 0u) |
+                       (b->sg[gf_batch::kGraphB].replayed ? 4u : 0u);
         stats->q_traverse = dt[8];
         stats->q_bruteforce = dt[9];
         stats->q_empty = dt[10];
@@ -1331,7 +1361,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
             stats->ops_bruteforce = 3.0 * b_dist * ix->D;
             stats->bf_mfma = 0;
         }
-        stage_times();
+        stage_times(true);
     }
 }
 
@@ -1355,6 +1385,8 @@ gf_status gf_batch_get_cells(const gf_batch* b, uint32_t* cells, uint32_t* count
         GF_REQUIRE(b, GF_E_ARG, "null batch");
         GF_REQUIRE(b->marked, GF_E_STATE, "cells not marked");
         set_device(b->ix);
+        // the stage calls return once enqueued: wait for them
+        GF_HIP(hipStreamSynchronize(b->ix->stream));
         if (selcount) ensure_selcount(*const_cast<gf_batch*>(b));
         const size_t Q = b->Q;
         if (cells) GF_HIP(hipMemcpy(cells, b->cells.p, Q * b->ix->P * 4, hipMemcpyDeviceToHost));
@@ -1379,6 +1411,8 @@ gf_status gf_batch_set_cells(gf_batch* b, const uint32_t* cells, const uint32_t*
             }
         }
         const size_t Q = b->Q;
+        // an earlier stage call may still be writing these buffers
+        GF_HIP(hipStreamSynchronize(b->ix->stream));
         GF_HIP(hipMemcpy(b->cells.p, cells, Q * P * 4, hipMemcpyHostToDevice));
         GF_HIP(hipMemcpy(b->counts.p, counts, Q * 4, hipMemcpyHostToDevice));
         GF_HIP(hipMemcpy(b->little.p, little, Q * 4, hipMemcpyHostToDevice));
@@ -1394,6 +1428,7 @@ gf_status gf_batch_get_centroid(const gf_batch* b, float* dist, uint32_t* topc) 
         GF_REQUIRE(b->ordered, GF_E_STATE, "gf_order_cells has not run");
         set_device(b->ix);
         const gf_index* ix = b->ix;
+        GF_HIP(hipStreamSynchronize(ix->stream));
         if (dist && !b->cdist_ready) {
             // the matrix the nearest centres were chosen from (same tiles, same rounding)
             gf_batch* mb = const_cast<gf_batch*>(b);
@@ -1414,6 +1449,7 @@ gf_status gf_batch_get_cell_flags(const gf_batch* b, uint8_t* flags) {
         GF_REQUIRE(b->marked, GF_E_STATE, "cells not marked");
         gf_batch* mb = const_cast<gf_batch*>(b);
         set_device(b->ix);
+        GF_HIP(hipStreamSynchronize(b->ix->stream));
         const size_t n = size_t(b->Q) * b->ix->P;
         if (!b->flags_ready) {
             if (mb->flags.n < n) mb->flags.alloc(n);
@@ -1430,6 +1466,7 @@ gf_status gf_batch_get_counters(const gf_batch* b, uint32_t* counters) {
         GF_REQUIRE(b && counters, GF_E_ARG, "null argument");
         GF_REQUIRE(b->counters.p, GF_E_STATE, "gf_search has not run");
         set_device(b->ix);
+        GF_HIP(hipStreamSynchronize(b->ix->stream));
         GF_HIP(hipMemcpy(counters, b->counters.p, size_t(b->Q) * GF_NCOUNTERS * 4, hipMemcpyDeviceToHost));
         if (b->pass_pending) {
             // the MFMA brute force reports the exact count as PASS; it was

@@ -1831,7 +1831,7 @@ __global__ void k_gather_meta(const unsigned long long* stats, const uint32_t* t
     const uint32_t t = threadIdx.x;
     if (stats && t < 16u) h_stats[t] = stats[t];
     if (t < 24u) h_tot[t] = tot[t];
-    if (t < 8u) h_stamps[t] = stamps[t];
+    if (t < 12u) h_stamps[t] = stamps[t];   // the search's [0..4], stages A [5..6] and B [7..8]
 }
 
 // What each batch of a streamed plan must do for this query batch (one

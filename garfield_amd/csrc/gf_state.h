@@ -294,6 +294,74 @@ struct gf_index {
     }
 };
 
+namespace gf {
+// One stage of the query path as a HIP graph: captured on its second call
+// and replayed while its key (the buffers it touches, the options, the
+// route) is unchanged; one launch instead of several, no host gaps between
+// the kernels.  If capture or instantiation fails the stage runs eagerly from
+// then on.  GARFIELD_NO_GRAPH=1 turns replay off.
+struct StageGraph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    std::vector<uint64_t> gkey;
+    uint32_t nruns = 0;
+    bool off = false, replayed = false;
+    StageGraph() = default;
+    StageGraph(const StageGraph&) = delete;
+    StageGraph& operator=(const StageGraph&) = delete;
+    void drop() {
+        if (gexec) (void)hipGraphExecDestroy(gexec);
+        if (graph) (void)hipGraphDestroy(graph);
+        gexec = nullptr;
+        graph = nullptr;
+        gkey.clear();
+    }
+    // Enqueues the stage on st: replays the graph, captures and launches a
+    // new one, or calls enqueue() directly.  enqueue must not allocate or
+    // wait on the host.
+    template <class F>
+    void run(const std::vector<uint64_t>& key, hipStream_t st, F&& enqueue) {
+        replayed = false;
+        ++nruns;
+        const char* env = std::getenv("GARFIELD_NO_GRAPH");
+        if (off || nruns < 2 || (env && env[0] == '1')) {
+            enqueue();
+            return;
+        }
+        if (!(gexec && key == gkey)) {
+            drop();
+            if (hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed) != hipSuccess) {
+                (void)hipGetLastError();
+                off = true;
+                enqueue();
+                return;
+            }
+            bool ok = true;
+            try {
+                enqueue();
+            } catch (...) {
+                ok = false;
+            }
+            hipGraph_t g = nullptr;
+            const hipError_t e = hipStreamEndCapture(st, &g);
+            if (!ok || e != hipSuccess || !g || hipGraphInstantiate(&gexec, g, nullptr, nullptr, 0) != hipSuccess) {
+                if (g) (void)hipGraphDestroy(g);
+                gexec = nullptr;
+                (void)hipGetLastError();
+                off = true;
+                enqueue();
+                return;
+            }
+            graph = g;
+            gkey = key;
+        }
+        GF_HIP(hipGraphLaunch(gexec, st));
+        replayed = true;
+    }
+    ~StageGraph() { drop(); }
+};
+}  // namespace gf
+
 struct gf_batch {
     gf_index* ix = nullptr;
     uint32_t Q = 0, Qp = 0, topc = 0;
@@ -379,81 +447,47 @@ struct gf_batch {
     gf::PinBuf<uint64_t> h_stamps;
     // Stage B ran; cdist holds the query x centre matrix of that run.
     bool ordered = false, cdist_ready = false;
-    // Around the latest stage A ([0], [1]) and stage B ([2], [3]) calls.
-    hipEvent_t sev[4] = {nullptr, nullptr, nullptr, nullptr};
-    bool sev_a = false, sev_b = false;
+    // Device times of the latest stage A and B calls: events sev[0..1]
+    // (stage A on an arithmetic grid) or device timestamps in stamps[5..6]
+    // (stage A) and stamps[7..8] (stage B), which the search gathers.
+    enum : uint8_t { kTimeNone = 0, kTimeEvents = 1, kTimeStamps = 2 };
+    static constexpr uint32_t kStampA = 5, kStampB = 7, kNStamps = 12;
+    hipEvent_t sev[2] = {nullptr, nullptr};
+    uint8_t time_a = kTimeNone, time_b = kTimeNone;
     // Records event i of sev (created on first use).
     void stage_event(int i, hipStream_t st) {
         if (!sev[i]) GF_HIP(hipEventCreate(&sev[i]));
         GF_HIP(hipEventRecord(sev[i], st));
     }
-    // Device time between sev[i] and sev[i + 1] (waits for the latter).
-    double stage_ms(int i) {
-        GF_HIP(hipEventSynchronize(sev[i + 1]));
+    // Device time between sev[0] and sev[1] (waits for the latter).
+    double event_ms() {
+        GF_HIP(hipEventSynchronize(sev[1]));
         float ms = 0;
-        GF_HIP(hipEventElapsedTime(&ms, sev[i], sev[i + 1]));
+        GF_HIP(hipEventElapsedTime(&ms, sev[0], sev[1]));
         return ms;
     }
-    // The search stage as a HIP graph: captured on a batch's second search
-    // and replayed while its key (the buffers it touches, the options, the
-    // route) is unchanged.  If capture or instantiation fails the batch runs
-    // every later search eagerly.  GARFIELD_NO_GRAPH=1 turns replay off.
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t gexec = nullptr;
-    std::vector<uint64_t> gkey;
-    uint32_t nruns = 0;
-    bool graph_off = false, graph_replayed = false;
-    void drop_graph() {
-        if (gexec) (void)hipGraphExecDestroy(gexec);
-        if (graph) (void)hipGraphDestroy(graph);
-        gexec = nullptr;
-        graph = nullptr;
-        gkey.clear();
+    void ensure_stamps() {
+        if (!stamps.n) { stamps.alloc(kNStamps); h_stamps.alloc(kNStamps); }
     }
-    // Enqueues the stage on st: replays the graph, captures and launches a
-    // new one, or calls enqueue() directly.  enqueue must not allocate or
-    // wait on the host.
+    // Milliseconds between the host copies of stamps i and i + 1.
+    double stamp_ms(uint32_t i) const {
+        const uint64_t* t = h_stamps.p;
+        return t[i + 1] >= t[i] ? double(t[i + 1] - t[i]) / double(ix->wclk_khz) : 0.0;
+    }
+    // Waits for the stream and copies stamps [i, i + n) to the host.
+    void fetch_stamps(uint32_t i, uint32_t n, hipStream_t st) {
+        GF_HIP(hipStreamSynchronize(st));
+        GF_HIP(hipMemcpy(h_stamps.p + i, stamps.p + i, n * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    }
+    // Stage A, stage B and the search stage as HIP graphs.
+    gf::StageGraph sg[3];
+    static constexpr int kGraphA = 0, kGraphB = 1, kGraphSearch = 2;
+    bool graph_replayed() const { return sg[kGraphSearch].replayed; }
     template <class F>
     void run_stage(const std::vector<uint64_t>& key, hipStream_t st, F&& enqueue) {
-        graph_replayed = false;
-        ++nruns;
-        const char* off = std::getenv("GARFIELD_NO_GRAPH");
-        if (graph_off || nruns < 2 || (off && off[0] == '1')) {
-            enqueue();
-            return;
-        }
-        if (!(gexec && key == gkey)) {
-            drop_graph();
-            if (hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed) != hipSuccess) {
-                (void)hipGetLastError();
-                graph_off = true;
-                enqueue();
-                return;
-            }
-            bool ok = true;
-            try {
-                enqueue();
-            } catch (...) {
-                ok = false;
-            }
-            hipGraph_t g = nullptr;
-            const hipError_t e = hipStreamEndCapture(st, &g);
-            if (!ok || e != hipSuccess || !g || hipGraphInstantiate(&gexec, g, nullptr, nullptr, 0) != hipSuccess) {
-                if (g) (void)hipGraphDestroy(g);
-                gexec = nullptr;
-                (void)hipGetLastError();
-                graph_off = true;
-                enqueue();
-                return;
-            }
-            graph = g;
-            gkey = key;
-        }
-        GF_HIP(hipGraphLaunch(gexec, st));
-        graph_replayed = true;
+        sg[kGraphSearch].run(key, st, enqueue);
     }
     ~gf_batch() {
-        drop_graph();
         for (auto& e : sev) if (e) (void)hipEventDestroy(e);
     }
 };

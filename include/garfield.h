@@ -260,8 +260,10 @@ typedef struct {
        gf_mark_cells_grid) and stage B (gf_order_cells) calls; 0 if none ran */
     double ms_stage_a;
     double ms_stage_b;
-    /* 1 if the search stage ran as a replayed HIP graph (a resident index's
-       second and later searches of a batch with the same buffers and options) */
+    /* HIP graph replays: bit 0 the search stage (a resident index's second
+       and later searches of a batch with the same buffers and options), bit 1
+       the latest gf_mark_cells call and bit 2 the latest gf_order_cells call
+       (their second and later calls with the same arguments) */
     uint32_t graph;
     /* queries on the full-graph route (postfilter or more cells, not all
        little; a resident index of at most 64 cells); their device time is in

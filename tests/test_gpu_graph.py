@@ -1,11 +1,13 @@
-"""The resident search stage replayed as a HIP graph gives the eager bits.
+"""The resident query path's stages replayed as HIP graphs give the eager bits.
 
 A batch's second and later searches run the stage (schedule, traversal,
-brute force, merges, statistics, result copies) as one captured graph.  Each
-case runs the stage once eagerly (GARFIELD_NO_GRAPH=1), then replays it
-several times with other eager work on the stream in between (stage A again,
-reading the cells back), and compares every replay's ids, distances and
-counters with the eager run; a change of options recaptures.
+brute force, merges, statistics, result copies) as one captured graph, and
+the second and later stage A and B calls with the same arguments replay
+theirs.  Each case runs the stages once eagerly (GARFIELD_NO_GRAPH=1), then
+replays them several times with other eager work on the stream in between
+(reading the cells back, exact selectivity counts), and compares every
+replay's cells, ids, distances and counters with the eager run; a change of
+options recaptures.
 """
 import numpy as np
 import pytest
@@ -30,12 +32,12 @@ def _replays(monkeypatch, cfg, ix, prefilter, Ls, reps=3, **dev_kw):
             monkeypatch.setenv("GARFIELD_NO_GRAPH", "1")
             ids0, d0, st0 = b.search(L=L, K=10, rl=10)
             c0 = b.get_counters()
-            assert st0.graph == 0
+            assert (st0.graph & 1) == 0
             monkeypatch.delenv("GARFIELD_NO_GRAPH")
             for r in range(reps):
                 ids, d, st = b.search(L=L, K=10, rl=10)
                 c = b.get_counters()
-                assert st.graph == 1, f"L={L} run {r}: the search did not run as a graph"
+                assert st.graph & 1, f"L={L} run {r}: the search did not run as a graph"
                 assert np.array_equal(ids, ids0), f"L={L} replay {r}: ids differ"
                 assert np.array_equal(d.view(np.uint32), d0.view(np.uint32)), f"L={L} replay {r}: distances differ"
                 assert np.array_equal(c, c0), f"L={L} replay {r}: counters differ"
@@ -97,7 +99,7 @@ def test_graph_replay_into_page_locked_arrays(monkeypatch, world_sub2):
                 out[0].fill(0xFFFFFFFF)
                 out[1].fill(np.nan)
             ids, d, st = b.search(L=32, K=10, rl=10, out=out)
-            assert st.graph == 1
+            assert st.graph & 1
             assert np.array_equal(ids, ids0), f"run {r}: ids differ"
             assert np.array_equal(d.view(np.uint32), d0.view(np.uint32)), f"run {r}: distances differ"
             if out is not None:
@@ -155,3 +157,57 @@ def test_reused_batch_switches_entries_and_channels(world32):
     # comparison above would see a stale copy
     assert not np.array_equal(want[2][2], want[3][2])
     assert gf.entry_points(N, P, R).shape == (R,)
+
+
+@pytest.mark.parametrize("prefilters", [(1.0, 0.05), (0.0, 0.05)])
+def test_stage_a_b_graph_replays(monkeypatch, world_sub2, world32, prefilters):
+    """Stages A (with and without the exact selectivity counts) and B as
+    replayed graphs: the cell lists, counts, routing and the searches equal
+    the eager run on every replay; timed and untimed calls alternate, the
+    reported stage times are positive, and switching the prefilter
+    recaptures stage A."""
+    cfg, ix = world32 if prefilters[0] == 0.0 else world_sub2
+    _print_case("graph-stage-ab", prefilters=prefilters)
+    dev = synth.open_device_index(ix)
+    b = dev.batch(cfg["queries"], cfg["lo"].astype(np.float32), cfg["hi"].astype(np.float32))
+    labels = ix["labels"] is not None
+    try:
+        want = {}
+        monkeypatch.setenv("GARFIELD_NO_GRAPH", "1")
+        for pf in prefilters:
+            b.mark_cells(pf, timed=False)
+            if labels:
+                b.order_cells(4, timed=False)
+            cells = b.get_cells()
+            ids, d, st = b.search(L=40, K=10, rl=10)
+            assert st.graph == 0
+            want[pf] = (cells, ids, d, b.get_counters())
+        monkeypatch.delenv("GARFIELD_NO_GRAPH")
+        for r in range(4):
+            for pf in prefilters:
+                timed = (r + int(pf * 100)) % 2 == 0
+                ms_a = b.mark_cells(pf, timed=timed)
+                ms_b = b.order_cells(4, timed=not timed) if labels else None
+                ids, d, st = b.search(L=40, K=10, rl=10)
+                cells = b.get_cells()
+                w = want[pf]
+                for k, (x, y) in enumerate(zip(cells, w[0])):
+                    assert np.array_equal(x, y), f"replay {r} prefilter {pf}: cell array {k} differs"
+                assert np.array_equal(ids, w[1]), f"replay {r} prefilter {pf}: ids differ"
+                assert np.array_equal(d.view(np.uint32), w[2].view(np.uint32)), f"replay {r} prefilter {pf}: dists"
+                assert np.array_equal(b.get_counters(), w[3]), f"replay {r} prefilter {pf}: counters differ"
+                # from the second round on, stage A (and B) replay their graphs
+                if r >= 1:
+                    assert st.graph & 2, f"replay {r} prefilter {pf}: stage A did not replay"
+                    if labels:
+                        assert st.graph & 4, f"replay {r} prefilter {pf}: stage B did not replay"
+                assert st.ms_stage_a > 0.0
+                if labels:
+                    assert st.ms_stage_b > 0.0
+                if timed:
+                    assert ms_a is not None and ms_a > 0.0
+                elif labels:
+                    assert ms_b is not None and ms_b > 0.0
+    finally:
+        b.close()
+        dev.close()
