@@ -838,6 +838,7 @@ gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms) {
                                 uint64_t(uintptr_t(b->cellq.p)), uint64_t(uintptr_t(b->stamps.p))};
         b->sg[gf_batch::kGraphA].run(std::vector<uint64_t>(std::begin(key), std::end(key)), st, enqueue);
         b->sel_exact = count;
+        b->route_bf = !count;
         b->time_a = gf_batch::kTimeStamps;
         if (ms) {
             b->fetch_stamps(gf_batch::kStampA, 2, st);
@@ -873,6 +874,7 @@ gf_status gf_mark_cells_grid(gf_batch* b, const float* attr_min, const float* at
         b->marked = true;
         b->flags_ready = true;
         b->bf_all = false;
+        b->route_bf = false;
         b->sel_exact = true;   // the arithmetic-grid stage A counts nothing: selcount stays 0
     });
 }
@@ -1249,6 +1251,9 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         enqueue_copies(true);
         GF_HIP(hipStreamSynchronize(st));
     };
+    // prefilter >= 1 in the latest stage A: k_sched routes no query to the
+    // traversal or the full graph, so neither is launched
+    const bool route_bf = b->route_bf;
     // The whole stage, schedule to copies: no allocation, no host wait.
     auto enqueue = [&]() {
         // Schedule (gpu_graph.cu:12485-12493) on the device.
@@ -1260,14 +1265,19 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         GF_HIP(gf::launch_reset_results(Q, K, b->out_ids.p, b->out_dist.p, b->counters.p, st,
                                         stats ? reinterpret_cast<uint32_t*>(b->stats.p) : nullptr, stats ? 32u : 0u));
         GF_HIP(gf::launch_sched(sa, st));
-        GF_HIP(gf::launch_stamp(stamp + 0, st));
-        gf::TravArgs at = a;
-        at.srange = tot + 12;
-        if (channels == 2) GF_HIP(gf::launch_traverse_dual(ix->rs, at, lds, Q, st));
-        else GF_HIP(gf::launch_traverse(ix->rs, at, lds, Q, st));
-        // queries with postfilter or more cells: the full graph
-        if (ix->FD && opts->postfilter <= ix->P) GF_HIP(gf::launch_fullgraph(ix->rs, af, lds_f, Q, st));
-        GF_HIP(gf::launch_stamp(stamp + 1, st));
+        if (route_bf) {
+            // every query takes the brute force (or has no cell): no traversal
+            GF_HIP(gf::launch_stamp(stamp + 0, st, 2));
+        } else {
+            GF_HIP(gf::launch_stamp(stamp + 0, st));
+            gf::TravArgs at = a;
+            at.srange = tot + 12;
+            if (channels == 2) GF_HIP(gf::launch_traverse_dual(ix->rs, at, lds, Q, st));
+            else GF_HIP(gf::launch_traverse(ix->rs, at, lds, Q, st));
+            // queries with postfilter or more cells: the full graph
+            if (ix->FD && opts->postfilter <= ix->P) GF_HIP(gf::launch_fullgraph(ix->rs, af, lds_f, Q, st));
+            GF_HIP(gf::launch_stamp(stamp + 1, st));
+        }
         if (sched_bf) {
             launch_gemm();
         } else {
@@ -1281,7 +1291,8 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     // From a batch's second search on, the stage runs as a HIP graph,
     // captured once per layout (buffers, options, route) and replayed:
     // one launch instead of some twenty, no gaps between the kernels.
-    const uint64_t key[] = {uint64_t(L), K, rl, opts->postfilter, uint64_t(gemm) | uint64_t(gemm_h) << 1,
+    const uint64_t key[] = {uint64_t(L), K, rl, opts->postfilter,
+                            uint64_t(gemm) | uint64_t(gemm_h) << 1 | uint64_t(route_bf) << 2,
                             uint64_t(b->bf_all), channels, uint64_t(uintptr_t(b->hover.p)),
                             uint64_t(b->qcap), uint64_t(stats != nullptr), uint64_t(dists != nullptr),
                             uint64_t(uintptr_t(b->part.p)), uint64_t(uintptr_t(b->items.p)),
@@ -1419,6 +1430,7 @@ gf_status gf_batch_set_cells(gf_batch* b, const uint32_t* cells, const uint32_t*
         b->marked = true;
         b->flags_ready = false;
         b->bf_all = false;
+        b->route_bf = false;
     });
 }
 

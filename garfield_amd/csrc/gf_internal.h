@@ -489,7 +489,7 @@ hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* di
 hipError_t launch_gather_meta(const unsigned long long* stats, const uint32_t* tot, const uint64_t* stamps,
                               unsigned long long* h_stats, uint32_t* h_tot, uint64_t* h_stamps, hipStream_t st);
 hipError_t launch_zero_u32(uint32_t* x, uint32_t n, hipStream_t st);   // a kernel, so that it can sit in a graph
-hipError_t launch_stamp(uint64_t* t, hipStream_t st);                    // *t = device wall clock when it runs
+hipError_t launch_stamp(uint64_t* t, hipStream_t st, uint32_t n = 1);   // t[0..n) = device wall clock when it runs
 // need: 2 * nbatch entries, the need flags, then the active queries per batch
 hipError_t launch_batch_need(uint32_t Q, uint32_t P, uint32_t nbatch, const uint32_t* plan_cells,
                              const uint32_t* plan_off, const uint8_t* flags, uint32_t* need, hipStream_t st);

@@ -1600,37 +1600,65 @@ __global__ void k_cellq_fill(uint32_t Q, uint32_t P, const uint32_t* cells, cons
     }
 }
 
-// Exclusive scan of a short array (n <= a few thousand) by one workgroup.
-__global__ __launch_bounds__(1024) void k_scan_small(const uint32_t* in, uint32_t n, uint32_t* out) {
-    // Chunks of 1024 elements: wave scans, then a scan of the 16 wave sums,
-    // carried across chunks.  Each chunk reads its inputs before any thread
-    // writes its outputs, so in and out may alias.
-    __shared__ uint32_t wsum[16];
+// Exclusive scan of a short array by one workgroup.  Up to kScanLds
+// elements: staged in LDS with coalesced loads, each thread scans a
+// contiguous run of them, one block-wide scan of the run totals (wave
+// shuffles, then the 16 wave sums), coalesced stores.  Longer arrays: chunks
+// of 1024 elements with a carry.  Every output is written after every input
+// was read, so in and out may alias.
+constexpr uint32_t kScanLds = 16384;
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wsum, uint32_t& total) {
     const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (uint32_t o = 1; o < 64u; o <<= 1) {
+        const uint32_t y = uint32_t(__shfl_up(int(x), o));
+        x += lane >= o ? y : 0u;
+    }
+    if (lane == 63u) wsum[w] = x;
+    __syncthreads();
+    if (w == 0) {
+        uint32_t z = lane < 16u ? wsum[lane] : 0u;
+#pragma unroll
+        for (uint32_t o = 1; o < 16u; o <<= 1) {
+            const uint32_t y = uint32_t(__shfl_up(int(z), o));
+            z += lane >= o ? y : 0u;
+        }
+        if (lane < 16u) wsum[lane] = z;
+    }
+    __syncthreads();
+    total = wsum[15];
+    return (w ? wsum[w - 1] : 0u) + x - v;
+}
+__global__ __launch_bounds__(1024) void k_scan_small(const uint32_t* in, uint32_t n, uint32_t* out) {
+    __shared__ uint32_t wsum[16];
+    __shared__ uint32_t buf[kScanLds];
+    const uint32_t t = threadIdx.x;
+    if (n <= kScanLds) {
+        for (uint32_t i = t; i < n; i += 1024u) buf[i] = in[i];
+        __syncthreads();
+        const uint32_t per = (n + 1023u) / 1024u, b0 = min(n, t * per), b1 = min(n, b0 + per);
+        uint32_t sum = 0;
+        for (uint32_t i = b0; i < b1; ++i) sum += buf[i];
+        uint32_t total;
+        uint32_t run = block_exclusive_scan(sum, wsum, total);
+        for (uint32_t i = b0; i < b1; ++i) {
+            const uint32_t v = buf[i];
+            buf[i] = run;
+            run += v;
+        }
+        __syncthreads();
+        for (uint32_t i = t; i < n; i += 1024u) out[i] = buf[i];
+        return;
+    }
     uint32_t carry = 0;
     for (uint32_t base = 0; base < n; base += 1024u) {
         const uint32_t i = base + t;
         const uint32_t v = i < n ? in[i] : 0u;
-        uint32_t x = v;
-#pragma unroll
-        for (uint32_t o = 1; o < 64u; o <<= 1) {
-            const uint32_t y = uint32_t(__shfl_up(int(x), o));
-            x += lane >= o ? y : 0u;
-        }
-        if (lane == 63u) wsum[w] = x;
-        __syncthreads();
-        if (w == 0) {
-            uint32_t z = lane < 16u ? wsum[lane] : 0u;
-#pragma unroll
-            for (uint32_t o = 1; o < 16u; o <<= 1) {
-                const uint32_t y = uint32_t(__shfl_up(int(z), o));
-                z += lane >= o ? y : 0u;
-            }
-            if (lane < 16u) wsum[lane] = z;
-        }
-        __syncthreads();
-        if (i < n) out[i] = carry + (w ? wsum[w - 1] : 0u) + x - v;
-        carry += wsum[15];
+        uint32_t total;
+        const uint32_t ex = block_exclusive_scan(v, wsum, total);
+        if (i < n) out[i] = carry + ex;
+        carry += total;
         __syncthreads();
     }
 }
@@ -1792,9 +1820,9 @@ __global__ void k_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_
 }
 
 // The device wall clock (constant rate, hipDeviceAttributeWallClockRate).
-__global__ void k_stamp(uint64_t* t) {
+__global__ void k_stamp(uint64_t* t, uint32_t n) {
     const uint64_t now = __builtin_amdgcn_s_memrealtime();
-    if (threadIdx.x == 0) *t = now;
+    if (threadIdx.x < n) t[threadIdx.x] = now;
 }
 
 __global__ void k_zero_u32(uint32_t* x, uint32_t n) {
@@ -2783,12 +2811,23 @@ __global__ __launch_bounds__(1024) void k_sched(SchedArgs p) {
     __shared__ uint32_t nfull, ffill;
     if (tid == 0) { nfull = 0; ffill = 0; }
     __syncthreads();
-    for (uint32_t q = tid; q < p.Q; q += blockDim.x) {
-        const uint32_t r = route(q);
+    // routes other than the traversal count with one LDS atomic per wave
+    // (ballots), not one per query
+    const uint32_t lane = lane_id();
+    auto wave_add = [&](uint32_t* ctr, bool x) -> uint32_t {
+        const uint64_t m = __builtin_amdgcn_ballot_w64(x);
+        const uint32_t below = __builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u));
+        uint32_t base = 0;
+        if (lane == 0 && m) base = atomicAdd(ctr, uint32_t(__builtin_popcountll(m)));
+        return uint32_t(__shfl(int(base), 0, 64)) + below;
+    };
+    for (uint32_t q0 = tid & ~63u; q0 < p.Q; q0 += blockDim.x) {
+        const uint32_t q = q0 + lane;
+        const uint32_t r = q < p.Q ? route(q) : 4u;
         if (r == 1) atomicAdd(&bins[min(p.counts[q], p.P)], 1u);
-        else if (r == 2) atomicAdd(&nbf, 1u);
-        else if (r == 3) atomicAdd(&nfull, 1u);
-        else atomicAdd(&nempty, 1u);
+        wave_add(&nbf, r == 2);
+        wave_add(&nfull, r == 3);
+        wave_add(&nempty, r == 0);
     }
     __syncthreads();
     if (tid == 0) {
@@ -2800,16 +2839,17 @@ __global__ __launch_bounds__(1024) void k_sched(SchedArgs p) {
     }
     __syncthreads();
     const uint32_t ntrav = p.ranges[1], nfirstf = ntrav + nbf;
-    for (uint32_t q = tid; q < p.Q; q += blockDim.x) {
-        const uint32_t r = route(q);
+    for (uint32_t q0 = tid & ~63u; q0 < p.Q; q0 += blockDim.x) {
+        const uint32_t q = q0 + lane;
+        const uint32_t r = q < p.Q ? route(q) : 4u;
         if (r == 1) {
             const uint32_t c = min(p.counts[q], p.P);
             p.sched[off[c] + atomicAdd(&bins[c], 1u)] = q;
-        } else if (r == 2) {
-            p.sched[ntrav + atomicAdd(&bffill, 1u)] = q;
-        } else if (r == 3) {
-            p.sched[nfirstf + atomicAdd(&ffill, 1u)] = q;
         }
+        const uint32_t sb = wave_add(&bffill, r == 2);
+        const uint32_t sf = wave_add(&ffill, r == 3);
+        if (r == 2) p.sched[ntrav + sb] = q;
+        if (r == 3) p.sched[nfirstf + sf] = q;
     }
 }
 
@@ -2819,25 +2859,36 @@ __global__ __launch_bounds__(256) void k_stats(StatsArgs p) {
     const uint32_t tid = threadIdx.x, i = blockIdx.x * 256u + tid;
     if (tid < 11) acc[tid] = 0;
     __syncthreads();
+    uint64_t v[11] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     if (i < p.Q) {
         const uint32_t* c = p.counters + size_t(i) * GF_NCOUNTERS;
         const uint32_t map[7] = {C_EXPAND, C_DIST, C_ATTR, C_CROSS, C_LROW, C_SCAN, C_PASS};
 #pragma unroll
-        for (int k = 0; k < 7; ++k)
-            if (c[map[k]]) atomicAdd(&acc[k], (unsigned long long)c[map[k]]);
-        if (c[C_ROUTE] == 1 || c[C_ROUTE] == 3 || c[C_ROUTE] == 4)
-            atomicAdd(&acc[7], (unsigned long long)c[C_DIST]);
-        if (c[C_ROUTE] == 2) atomicAdd(&acc[8], (unsigned long long)c[C_DIST]);
+        for (int k = 0; k < 7; ++k) v[k] = c[map[k]];
+        if (c[C_ROUTE] == 1 || c[C_ROUTE] == 3 || c[C_ROUTE] == 4) v[7] = c[C_DIST];
+        if (c[C_ROUTE] == 2) v[8] = c[C_DIST];
     }
     if (p.bcnt && i < p.NS) {
         const uint32_t ns = p.sseed ? p.sseed[i] : 0u, n = p.bcnt[i] + ns;
         if (n) {
-            atomicAdd(&acc[9], (unsigned long long)n * p.ssize[i]);
+            v[9] = uint64_t(n) * p.ssize[i];
             const uint32_t ni = p.split ? p.bin[i] : 0u;
             const uint32_t nb = (ns + kBfQB - 1) / kBfQB + (ni + kBfQB - 1) / kBfQB +
                                 (n - ns - ni + kBfQB - 1) / kBfQB;
-            atomicAdd(&acc[10], (unsigned long long)nb * (p.stile[i + 1] - p.stile[i]));
+            v[10] = uint64_t(nb) * (p.stile[i + 1] - p.stile[i]);
         }
+    }
+    // sums over the wave, then one LDS atomic per wave and counter
+#pragma unroll
+    for (int k = 0; k < 11; ++k) {
+        uint64_t x = v[k];
+#pragma unroll
+        for (uint32_t o = 32; o; o >>= 1) {
+            const uint32_t lo = uint32_t(__shfl_xor(int(uint32_t(x)), int(o), 64));
+            const uint32_t hi = uint32_t(__shfl_xor(int(uint32_t(x >> 32)), int(o), 64));
+            x += (uint64_t(hi) << 32) | lo;
+        }
+        if ((tid & 63u) == 0 && x) atomicAdd(&acc[k], (unsigned long long)x);
     }
     __syncthreads();
     if (tid < 11 && acc[tid]) atomicAdd(&p.out[tid], acc[tid]);
@@ -2847,17 +2898,20 @@ __global__ __launch_bounds__(256) void k_stats(StatsArgs p) {
 // of 64, times its tiles in chunks of tch (0: one chunk).  Sub-cells are
 // taken in the order sorder (identity if null), so the items of its first
 // ns1 sub-cells come first: *nitems_a of them.
-__global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart, uint32_t qcap,
-                          const uint32_t* stile, uint32_t tch, uint32_t NS, uint32_t* icnt, const uint32_t* ioff,
-                          BfItem* items, uint32_t* nitems, const uint32_t* ok, bool fill, const uint32_t* scnt,
-                          BfItem* sitems, uint32_t* nseed, uint32_t scap, const uint32_t* sorder, uint32_t ns1,
-                          uint32_t* nitems_a, uint32_t stch) {
-    const uint32_t ks = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(256) void k_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint32_t* bstart,
+                                                 uint32_t qcap, const uint32_t* stile, uint32_t tch, uint32_t NS,
+                                                 uint32_t* icnt, const uint32_t* ioff, BfItem* items,
+                                                 uint32_t* nitems, const uint32_t* ok, bool fill, const uint32_t* scnt,
+                                                 BfItem* sitems, uint32_t* nseed, uint32_t scap,
+                                                 const uint32_t* sorder, uint32_t ns1, uint32_t* nitems_a,
+                                                 uint32_t stch) {
+    // one wave per sub-cell; its lanes write the sub-cell's items in parallel
+    const uint32_t ks = blockIdx.x * 4u + (threadIdx.x >> 6), lane = lane_id();
     if (ks >= NS) return;
     const uint32_t s = sorder ? sorder[ks] : ks;
     if (fill && !*ok) {
-        if (ks == NS - 1) *nitems = 0;
-        if (nitems_a && ks == 0) *nitems_a = 0;
+        if (lane == 0 && ks == NS - 1) *nitems = 0;
+        if (lane == 0 && nitems_a && ks == 0) *nitems_a = 0;
         return;
     }
     const uint32_t ns = qcap && scnt ? scnt[s] : 0u;   // seeds: the front of the region
@@ -2866,11 +2920,13 @@ __global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint3
         // sub-cell), in chunks of stch tiles, one wave per item (no padding)
         const uint32_t nc = tile_chunks(stile, s, stch), gs = (ns + kBfQB - 1) / kBfQB;
         const uint32_t t0 = stile[s], t1 = stile[s + 1], step = stch ? stch : (t1 - t0);
-        uint32_t k = atomicAdd(nseed, gs * nc);
-        for (uint32_t c = 0; c < nc; ++c) {
+        uint32_t k0 = 0;
+        if (lane == 0) k0 = atomicAdd(nseed, gs * nc);
+        k0 = uint32_t(__shfl(int(k0), 0, 64));
+        for (uint32_t j = lane; j < gs * nc; j += 64u) {
+            const uint32_t c = j / gs, b = j - c * gs, k = k0 + j;
             const uint32_t tb = t0 + c * step, te = min(t1, tb + step);
-            for (uint32_t b = 0; b < gs; ++b, ++k)
-                if (k < scap) sitems[k] = BfItem{s, s * qcap + b * kBfQB, min(kBfQB, ns - b * kBfQB), tb, te, 0u};
+            if (k < scap) sitems[k] = BfItem{s, s * qcap + b * kBfQB, min(kBfQB, ns - b * kBfQB), tb, te, 0u};
         }
     }
     const uint32_t n = bcnt[s], ni = bin[s];
@@ -2878,30 +2934,34 @@ __global__ void k_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint3
     // grouped by 64 each; else one run whose first ni entries are inside
     const uint32_t gi = qcap ? (ni + kBfQB - 1) / kBfQB : 0u;
     const uint32_t gp = qcap ? (n - ni + kBfQB - 1) / kBfQB : (n + kBfQB - 1) / kBfQB;
-    const uint32_t nc = n ? tile_chunks(stile, s, tch) : 0u;
-    if (!fill) { icnt[ks] = (gi + gp) * nc; return; }
+    const uint32_t nc = n ? tile_chunks(stile, s, tch) : 0u, g = gi + gp;
+    if (!fill) {
+        if (lane == 0) icnt[ks] = g * nc;
+        return;
+    }
     const uint32_t t0 = stile[s], t1 = stile[s + 1], step = tch ? tch : (t1 - t0);
-    uint32_t k = ioff[ks];
-    if (nitems_a) {
-        if (ks + 1 == ns1) *nitems_a = ioff[ks] + (gi + gp) * nc;
+    const uint32_t k0 = ioff[ks];
+    if (lane == 0 && nitems_a) {
+        if (ks + 1 == ns1) *nitems_a = k0 + g * nc;
         else if (ns1 == 0 && ks == 0) *nitems_a = 0;
     }
-    for (uint32_t c = 0; c < nc; ++c) {
+    // item k0 + c g + b: chunk c of the tiles, group b (inside groups first)
+    for (uint32_t j = lane; j < g * nc; j += 64u) {
+        const uint32_t c = j / g, b = j - c * g;
         const uint32_t tb = t0 + c * step, te = min(t1, tb + step);
+        BfItem it;
         if (qcap) {
             const uint32_t np = n - ni;
-            for (uint32_t b = 0; b < gi; ++b)
-                items[k++] = BfItem{s, s * qcap + ns + b * kBfQB, min(kBfQB, ni - b * kBfQB), tb, te, 1u};
-            for (uint32_t b = 0; b < gp; ++b)
-                items[k++] = BfItem{s, s * qcap + qcap - np + b * kBfQB, min(kBfQB, np - b * kBfQB), tb, te, 0u};
+            it = b < gi ? BfItem{s, s * qcap + ns + b * kBfQB, min(kBfQB, ni - b * kBfQB), tb, te, 1u}
+                        : BfItem{s, s * qcap + qcap - np + (b - gi) * kBfQB, min(kBfQB, np - (b - gi) * kBfQB), tb,
+                                 te, 0u};
         } else {
-            for (uint32_t b = 0; b < gp; ++b) {
-                const uint32_t m = min(kBfQB, n - b * kBfQB);
-                items[k++] = BfItem{s, bstart[s] + b * kBfQB, m, tb, te, b * kBfQB + m <= ni ? 1u : 0u};
-            }
+            const uint32_t m = min(kBfQB, n - b * kBfQB);
+            it = BfItem{s, bstart[s] + b * kBfQB, m, tb, te, b * kBfQB + m <= ni ? 1u : 0u};
         }
+        items[k0 + j] = it;
     }
-    if (ks == NS - 1) *nitems = ioff[ks] + (gi + gp) * nc;
+    if (lane == 0 && ks == NS - 1) *nitems = k0 + g * nc;
 }
 
 // out[0] = start[n-1] + cnt[n-1], the total of an exclusive scan; out[1] =
@@ -4515,7 +4575,7 @@ hipError_t launch_bfitems(const uint32_t* bcnt, const uint32_t* bin, const uint3
     if (!NS) return hipSuccess;
     if (scnt && (!sitems || !nseed)) return hipErrorInvalidValue;
     if (sorder && ns1 > NS) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_bfitems, dim3((NS + 255) / 256), dim3(256), 0, st, bcnt, bin, bstart, qcap, stile, tch, NS,
+    hipLaunchKernelGGL(k_bfitems, dim3((NS + 3) / 4), dim3(256), 0, st, bcnt, bin, bstart, qcap, stile, tch, NS,
                        icnt, ioff, items, nitems, ok, fill, scnt, sitems, nseed, scap, sorder, ns1, nitems_a,
                        scnt ? stch : tch);
     return hipGetLastError();
@@ -4644,8 +4704,9 @@ hipError_t launch_bfseed(const BfSeedArgs& a, uint32_t Q, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_stamp(uint64_t* t, hipStream_t st) {
-    hipLaunchKernelGGL(k_stamp, dim3(1), dim3(64), 0, st, t);
+hipError_t launch_stamp(uint64_t* t, hipStream_t st, uint32_t n) {
+    if (n < 1 || n > 64) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_stamp, dim3(1), dim3(64), 0, st, t, n);
     return hipGetLastError();
 }
 

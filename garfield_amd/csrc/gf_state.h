@@ -366,6 +366,8 @@ struct gf_batch {
     gf_index* ix = nullptr;
     uint32_t Q = 0, Qp = 0, topc = 0;
     bool marked = false;
+    // the latest stage A sent every query to the brute force (prefilter >= 1)
+    bool route_bf = false;
     bool i8 = false;
     DevBuf<int8_t> q8;
     DevBuf<int32_t> nq;
