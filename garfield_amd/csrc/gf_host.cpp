@@ -816,17 +816,29 @@ gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms) {
         b->ensure_stamps();
         const bool count = prefilter < 1.0f;
         auto enqueue = [&]() {
-            GF_HIP(gf::launch_stamp(b->stamps.p + gf_batch::kStampA, st));
+            // the stage's kernels take its timestamps: the cell kernel when it
+            // starts, the last kernel (ticket) when it ends
+            gf::CellsTail tl;
+            tl.st_entry = b->stamps.p + gf_batch::kStampA;
+            uint32_t* const ticket = b->ticket(gf_batch::kTicketA);
+            uint64_t* const st_end = b->stamps.p + gf_batch::kStampA + 1;
+            if (!count) {
+                // prefilter >= 1: count / N <= prefilter holds for every
+                // count, so every query is routed to the brute force without
+                // counting (the routing is the reference's), in the cell
+                // kernel itself; the exact counts are made when asked for.
+                tl.selcount = b->selcount.p;
+                tl.little = b->little.p;
+                tl.ticket = ticket;
+                tl.st_exit = st_end;
+            }
             GF_HIP(gf::launch_cells(b->Q, ix->a, b->lo.p, b->hi.p, ix->grid.p, ix->doff.p, ix->l_q.p, ix->r_q.p,
-                                    ix->P, ix->offset.p, b->cells.p, b->counts.p, st));
-            // prefilter >= 1: count / N <= prefilter holds for every count,
-            // so every query is routed to the brute force without counting
-            // (the routing is the reference's); the exact counts are made
-            // when they are asked for.
-            if (count) count_selectivity(*b, st);
-            else GF_HIP(gf::launch_zero_u32(b->selcount.p, b->Q, st));
-            GF_HIP(gf::launch_route(b->Q, ix->N, prefilter, b->selcount.p, b->counts.p, b->little.p, st));
-            GF_HIP(gf::launch_stamp(b->stamps.p + gf_batch::kStampA + 1, st));
+                                    ix->P, ix->offset.p, b->cells.p, b->counts.p, st, tl));
+            if (count) {
+                count_selectivity(*b, st);
+                GF_HIP(gf::launch_route(b->Q, ix->N, prefilter, b->selcount.p, b->counts.p, b->little.p, st, ticket,
+                                        st_end));
+            }
         };
         uint32_t pf = 0;
         std::memcpy(&pf, &prefilter, sizeof(pf));
@@ -894,21 +906,24 @@ gf_status gf_order_cells(gf_batch* b, uint32_t topc, double* ms) {
         b->topc = topc;
         b->ensure_stamps();
         auto enqueue = [&]() {
-            GF_HIP(gf::launch_stamp(b->stamps.p + gf_batch::kStampB, st));
+            // timestamps: the centre kernel when it starts, a stamp kernel at
+            // the end (k_order runs one workgroup per query: a ticket over
+            // that many workgroups costs more than a kernel)
+            uint64_t* const st0 = b->stamps.p + gf_batch::kStampB;
             if (top) {
                 // nearest centres straight from the MFMA tiles; the distance
                 // matrix is made only if gf_batch_get_centroid asks for it
                 GF_HIP(gf::launch_centroid_top(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp,
-                                               ix->Cp, ix->Dp, topc, b->topk.p, st));
+                                               ix->Cp, ix->Dp, topc, b->topk.p, st, st0));
                 GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, nullptr, ix->hist.p, b->cells.p, b->counts.p,
                                         b->topk.p, st, true, ix->ref_ties));
             } else {
                 GF_HIP(gf::launch_centroid(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp,
-                                           ix->Cp, ix->Dp, b->cdist.p, st));
+                                           ix->Cp, ix->Dp, b->cdist.p, st, st0));
                 GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, b->cdist.p, ix->hist.p, b->cells.p, b->counts.p,
                                         b->topk.p, st, false, ix->ref_ties));
             }
-            GF_HIP(gf::launch_stamp(b->stamps.p + gf_batch::kStampB + 1, st));
+            GF_HIP(gf::launch_stamp(st0 + 1, st));
         };
         const uint64_t key[] = {uint64_t(uintptr_t(ix)), topc, b->Q, uint64_t(uintptr_t(b->topk.p)),
                                 uint64_t(uintptr_t(b->cdist.p)), uint64_t(uintptr_t(b->q16.p)),
@@ -1184,7 +1199,9 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         fa.ok = tot + 3; fa.part = b->part.p; fa.counts = b->counts.p; fa.cells = b->cells.p;
         fa.offset = ix->offset.p; fa.selcount = b->selcount.p; fa.gidx = ix->gidx.p; fa.out_ids = b->out_ids.p;
         fa.out_dist = b->out_dist.p; fa.counters = b->counters.p; fa.K = K; fa.P = ix->P;
-        GF_HIP(gf::launch_stamp(stamp + 3, st));
+        // timestamps [3] and [4]: the first MFMA launch when it starts, the
+        // final merge when it starts
+        ga.stamp = stamp + 3;
         if (two) {
             // the seeds alone, then a merge (each query's bound becomes the
             // K-th of its seed sub-cell), the first pass under those
@@ -1193,19 +1210,21 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
             if (seeds) {
                 ga.irange = 3;
                 GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu), st));
+                ga.stamp = nullptr;
                 fa.bound_only = 1;
                 GF_HIP(gf::launch_bf_final(fa, Q, st));
                 ga.seeds_on = 0;
             }
             ga.irange = 1;
             GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu), st));
+            ga.stamp = nullptr;
             fa.bound_only = 1;
             GF_HIP(gf::launch_bf_final(fa, Q, st));
             fa.bound_only = 0;
             ga.irange = 2;
         }
         GF_HIP(gf::launch_bf_i8(ga, uint32_t(ix->ncu), st));
-        GF_HIP(gf::launch_stamp(stamp + 4, st));
+        fa.stamp = stamp + 4;
         GF_HIP(gf::launch_bf_final(fa, Q, st));
     };
 
@@ -1262,14 +1281,15 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         sa.sched = b->sched.p; sa.tot = tot + 8; sa.ranges = tot + 12;
         sa.full = ix->FD ? 1u : 0u;
         sa.franges = ix->FD ? tot + 16 : nullptr;
+        // timestamps: [0] (and [1] with no traversal) when the reset starts,
+        // [2] when the gather of the results starts (k_gather_meta)
         GF_HIP(gf::launch_reset_results(Q, K, b->out_ids.p, b->out_dist.p, b->counters.p, st,
-                                        stats ? reinterpret_cast<uint32_t*>(b->stats.p) : nullptr, stats ? 32u : 0u));
+                                        stats ? reinterpret_cast<uint32_t*>(b->stats.p) : nullptr, stats ? 32u : 0u,
+                                        stamp + 0, route_bf ? 2u : 1u));
         GF_HIP(gf::launch_sched(sa, st));
-        if (route_bf) {
-            // every query takes the brute force (or has no cell): no traversal
-            GF_HIP(gf::launch_stamp(stamp + 0, st, 2));
-        } else {
-            GF_HIP(gf::launch_stamp(stamp + 0, st));
+        if (!route_bf) {
+            // (with route_bf every query takes the brute force or has no
+            // cell: no traversal is launched)
             gf::TravArgs at = a;
             at.srange = tot + 12;
             if (channels == 2) GF_HIP(gf::launch_traverse_dual(ix->rs, at, lds, Q, st));
@@ -1285,7 +1305,6 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
             ab.srange = tot + 14;
             GF_HIP(gf::launch_bruteforce(ix->rs, ab, Q, st));
         }
-        GF_HIP(gf::launch_stamp(stamp + 2, st));
         enqueue_copies(false);
     };
     // From a batch's second search on, the stage runs as a HIP graph,
@@ -1314,7 +1333,6 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         b->alloc_pairs(size_t(dt[2]) + dt[2] / 4 + 1024, KP, Q, NS, size_t(NS) + ix->ntile / gf::kBfMaxItemTiles + 1);
         GF_HIP(gf::launch_stamp(stamp + 1, st));
         launch_gemm();
-        GF_HIP(gf::launch_stamp(stamp + 2, st));
         enqueue_tail();
         GF_REQUIRE(dt[3], GF_E_STATE, "brute-force schedule does not fit after growing");
     }

@@ -170,6 +170,7 @@ struct BfGemmArgs {
     uint32_t seeds_on;
     uint32_t irange;
     const uint32_t* nitems_a;
+    uint64_t* stamp = nullptr;   // optional: the device wall clock when the launch starts
 };
 // Query-batch brute force of float rows on MFMA (k_bf_f16: binary16 rows,
 // fp16 MFMA; k_bf_f32: fp32 rows, fp32 MFMA): candidate keys within the
@@ -290,6 +291,7 @@ struct BfFinalArgs {
     // Bound only: lower each query's gbound to the K-th smallest key appended
     // so far and leave the keys, results and counters as they are.
     uint32_t bound_only;
+    uint64_t* stamp = nullptr;   // optional: the device wall clock when the launch starts
 };
 // Stage A on sub-cells: one workgroup per sub-cell over all queries.  A point
 // that passes a range lies in a cell the range selects, so the relation of a
@@ -454,10 +456,21 @@ hipError_t launch_f2h_pad(const float* x, uint32_t rows, uint32_t D, uint16_t* o
                           uint32_t rows_pad, uint32_t Dp, float alpha, hipStream_t st);
 hipError_t launch_norms_f16(const uint16_t* x, uint32_t n, uint32_t D, uint32_t ld, float* out,
                             hipStream_t st);
+// Optional parts of stage A's cell kernel: with little (and selcount) also
+// the routing of a prefilter >= 1 (selcount 0 and every selected cell little,
+// as k_route computes it then); st_entry, the device wall clock when the
+// launch starts; st_exit (with ticket, a zeroed counter), when it ends.
+struct CellsTail {
+    uint32_t* selcount = nullptr;
+    uint32_t* little = nullptr;
+    uint64_t* st_entry = nullptr;
+    uint32_t* ticket = nullptr;
+    uint64_t* st_exit = nullptr;
+};
 hipError_t launch_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi,
                         const uint32_t* grid, const uint32_t* doff, const float* l_q,
                         const float* r_q, uint32_t P, const uint32_t* offset, uint32_t* cells,
-                        uint32_t* counts, hipStream_t st);
+                        uint32_t* counts, hipStream_t st, const CellsTail& tl = CellsTail{});
 hipError_t launch_cellq_count(uint32_t Q, uint32_t P, const uint32_t* cells,
                               const uint32_t* counts, uint32_t* ccount, hipStream_t st);
 hipError_t launch_scan_small(const uint32_t* in, uint32_t n, uint32_t* out_excl, hipStream_t st);
@@ -470,7 +483,8 @@ hipError_t launch_selcount(uint32_t ntiles, const uint32_t* tile_cell, const uin
                            const uint32_t* cellq, const float* lo, const float* hi,
                            uint32_t* selcount, hipStream_t st);
 hipError_t launch_route(uint32_t Q, uint32_t N, float thr, const uint32_t* selcount,
-                        const uint32_t* counts, uint32_t* little, hipStream_t st);
+                        const uint32_t* counts, uint32_t* little, hipStream_t st, uint32_t* ticket = nullptr,
+                        uint64_t* st_exit = nullptr);   // st_exit: the end of the launch (stamp_exit)
 hipError_t launch_cells_grid(uint32_t Q, uint32_t a, const float* lo, const float* hi, const float* amin,
                              const float* width, const uint32_t* grid, uint32_t P, const uint32_t* offset,
                              double thr, uint32_t* cells, uint32_t* counts, uint32_t* little, uint8_t* flags,
@@ -484,8 +498,9 @@ hipError_t launch_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t*
                           uint32_t NS = 0, uint32_t* scnt = nullptr, uint32_t* nseed = nullptr);
 // Also zeroes z[0, nz) (a search's statistics sums, for one kernel less).
 hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, hipStream_t st,
-                                uint32_t* z = nullptr, uint32_t nz = 0);
-// stats (16, optional), tot (24) and stamps (8) to page-locked host buffers.
+                                uint32_t* z = nullptr, uint32_t nz = 0, uint64_t* stp = nullptr, uint32_t nst = 0);
+// stats (16, optional), tot (24) and stamps (12) to page-locked host buffers;
+// stamps[2], the search's end, is taken by this kernel when it starts.
 hipError_t launch_gather_meta(const unsigned long long* stats, const uint32_t* tot, const uint64_t* stamps,
                               unsigned long long* h_stats, uint32_t* h_tot, uint64_t* h_stamps, hipStream_t st);
 hipError_t launch_zero_u32(uint32_t* x, uint32_t n, hipStream_t st);   // a kernel, so that it can sit in a graph
@@ -512,7 +527,7 @@ hipError_t launch_merge_stream(uint32_t Q, uint32_t K, uint32_t* run_ids, float*
                                hipStream_t st);
 hipError_t launch_centroid(const uint16_t* qh, const uint16_t* ch, const float* qn,
                            const float* cn, uint32_t Q, uint32_t C, uint32_t Qp, uint32_t Cp,
-                           uint32_t Dp, float* dist, hipStream_t st);
+                           uint32_t Dp, float* dist, hipStream_t st, uint64_t* st_entry = nullptr);
 // chosen: topk already holds each query's topc nearest centres (dist unused).
 // ref_ties: equal scores keep the reference's sorting-network order.
 hipError_t launch_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc, const float* dist,
@@ -521,7 +536,7 @@ hipError_t launch_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc, const
 // Each query's topc (<= 4) nearest centres without the distance matrix.
 hipError_t launch_centroid_top(const uint16_t* qh, const uint16_t* ch, const float* qn, const float* cn, uint32_t Q,
                                uint32_t C, uint32_t Qp, uint32_t Cp, uint32_t Dp, uint32_t topc, uint32_t* topk,
-                               hipStream_t st);
+                               hipStream_t st, uint64_t* st_entry = nullptr);
 
 // Host-side file readers (gf_io.cpp).  Each throws gf::Error on failure.
 struct Error {

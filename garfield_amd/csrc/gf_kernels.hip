@@ -18,6 +18,31 @@ namespace {
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x & 63u; }
 
+// Timestamps taken by the kernels of a stage themselves, so that a stage needs
+// no kernel of its own for them: stamp_entry -- the first workgroup writes
+// st[0..n) when it starts; stamp_exit -- the last workgroup of the launch to
+// finish writes *st (ticket: a counter at zero, which that workgroup returns
+// to zero, so that the next launch or replay starts from zero).  stamp_exit
+// costs one device-scope atomic per workgroup, all on one word: only for
+// launches of a few hundred workgroups at most.
+__device__ __forceinline__ void stamp_entry(uint64_t* st, uint32_t n) {
+    if (st && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x < n)
+        st[threadIdx.x] = __builtin_amdgcn_s_memrealtime();
+}
+__device__ __forceinline__ void stamp_exit(uint32_t* ticket, uint64_t* st) {
+    if (!st) return;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        const uint32_t nb = gridDim.x * gridDim.y * gridDim.z;
+        if (atomicAdd(ticket, 1u) == nb - 1u) {
+            *st = __builtin_amdgcn_s_memrealtime();
+            atomicExch(ticket, 0u);
+        }
+    }
+}
+
+
 __device__ __forceinline__ uint64_t make_cand(float d, uint32_t row, bool pass) {
     return (uint64_t(__float_as_uint(d)) << 32) | (row << 2) | (pass ? 1u : 0u);
 }
@@ -1543,11 +1568,10 @@ __global__ __launch_bounds__(64) void k_norms_f16(const uint16_t* x, uint32_t n,
 // (the reference computes cell -1 or g there) selects nothing; an empty interval between two cells selects
 // the next cell, as the reference's do-while does.  Cells holding no point
 // are never selected (the reference would read past them).
-__global__ void k_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi, const uint32_t* grid,
-                        const uint32_t* doff, const float* l_q, const float* r_q, uint32_t P,
-                        const uint32_t* offset, uint32_t* cells, uint32_t* counts) {
-    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= Q) return;
+__device__ __forceinline__ uint32_t cells_of_query(uint32_t q, uint32_t a, const float* lo, const float* hi,
+                                                   const uint32_t* grid, const uint32_t* doff, const float* l_q,
+                                                   const float* r_q, uint32_t P, const uint32_t* offset,
+                                                   uint32_t* cells) {
     uint32_t cl[kMaxAttr], ch[kMaxAttr], idx[kMaxAttr], g[kMaxAttr];
     bool empty = false;
 #pragma unroll
@@ -1580,7 +1604,22 @@ __global__ void k_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi
             if (d < 0) break;
         }
     }
-    counts[q] = n;
+    return n;
+}
+__global__ void k_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi, const uint32_t* grid,
+                        const uint32_t* doff, const float* l_q, const float* r_q, uint32_t P,
+                        const uint32_t* offset, uint32_t* cells, uint32_t* counts, CellsTail tl) {
+    stamp_entry(tl.st_entry, 1);
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q < Q) {
+        const uint32_t n = cells_of_query(q, a, lo, hi, grid, doff, l_q, r_q, P, offset, cells);
+        counts[q] = n;
+        if (tl.little) {
+            tl.selcount[q] = 0;
+            tl.little[q] = n;
+        }
+    }
+    stamp_exit(tl.ticket, tl.st_exit);
 }
 
 __global__ void k_cellq_count(uint32_t Q, uint32_t P, const uint32_t* cells, const uint32_t* counts,
@@ -1708,11 +1747,13 @@ __global__ __launch_bounds__(256) void k_selcount(const uint32_t* tile_cell, con
 // Prefilter routing (real_dataset_adapter.cuh:374-381): the selectivity is
 // computed in double, stored as float and compared with the threshold.
 __global__ void k_route(uint32_t Q, uint32_t N, float thr, const uint32_t* selcount, const uint32_t* counts,
-                        uint32_t* little) {
+                        uint32_t* little, uint32_t* ticket, uint64_t* st_exit) {
     const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= Q) return;
-    const float proportion = float((1.0 * selcount[q]) / (1.0 * N));
-    little[q] = proportion <= thr ? counts[q] : 0u;
+    if (q < Q) {
+        const float proportion = float((1.0 * selcount[q]) / (1.0 * N));
+        little[q] = proportion <= thr ? counts[q] : 0u;
+    }
+    stamp_exit(ticket, st_exit);
 }
 
 // Arithmetic-grid cells (intersection_area_batch_mark_little_seg,
@@ -1844,7 +1885,8 @@ __global__ void k_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t*
 
 // Sentinel results and zero counters for a batch's searches.
 __global__ void k_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, uint32_t* z,
-                                uint32_t nz) {
+                                uint32_t nz, uint64_t* st, uint32_t nst) {
+    stamp_entry(st, nst);
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < Q * K) { ids[i] = GF_NO_RESULT; dist[i] = __int_as_float(0x7F800000); }
     if (i < Q * GF_NCOUNTERS) ctr[i] = 0;
@@ -1856,10 +1898,12 @@ __global__ void k_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* di
 // written to page-locked host memory.
 __global__ void k_gather_meta(const unsigned long long* stats, const uint32_t* tot, const uint64_t* stamps,
                               unsigned long long* h_stats, uint32_t* h_tot, uint64_t* h_stamps) {
+    // the search ends here: its timestamp [2] is taken now
+    const uint64_t now = __builtin_amdgcn_s_memrealtime();
     const uint32_t t = threadIdx.x;
     if (stats && t < 16u) h_stats[t] = stats[t];
     if (t < 24u) h_tot[t] = tot[t];
-    if (t < 12u) h_stamps[t] = stamps[t];   // the search's [0..4], stages A [5..6] and B [7..8]
+    if (t < 12u) h_stamps[t] = t == 2u ? now : stamps[t];   // the search's [0..4], stages A [5..6] and B [7..8]
 }
 
 // What each batch of a streamed plan must do for this query batch (one
@@ -2036,7 +2080,8 @@ __device__ __forceinline__ float centre_dist(float qn, float cn, float dot) {
 
 __global__ __launch_bounds__(256) void k_centroid(const uint16_t* qh, const uint16_t* ch, const float* qn,
                                                   const float* cn, uint32_t Q, uint32_t C, uint32_t Dp,
-                                                  float* dist) {
+                                                  float* dist, uint64_t* st_entry) {
+    stamp_entry(st_entry, 1);
     const uint32_t lane = lane_id(), wave = threadIdx.x >> 6;
     const uint32_t q0 = blockIdx.x * 16u;
     const uint32_t c0 = (blockIdx.y * 4u + wave) * 16u;
@@ -2091,7 +2136,9 @@ __device__ __forceinline__ void merge4(float (&ad)[4], uint32_t (&ai)[4], const 
 constexpr uint32_t kCtW = 4;
 __global__ __launch_bounds__(64 * kCtW) void k_centroid_top(const uint16_t* qh, const uint16_t* ch, const float* qn,
                                                             const float* cn, uint32_t Q, uint32_t C, uint32_t Cp,
-                                                            uint32_t Dp, uint32_t topc, uint32_t* topk) {
+                                                            uint32_t Dp, uint32_t topc, uint32_t* topk,
+                                                            uint64_t* st_entry) {
+    stamp_entry(st_entry, 1);
     __shared__ float sd[kCtW][16][4];
     __shared__ uint32_t si[kCtW][16][4];
     const uint32_t lane = lane_id(), wave = threadIdx.x >> 6;
@@ -2197,9 +2244,9 @@ __global__ __launch_bounds__(64 * kCtW) void k_centroid_top(const uint16_t* qh, 
 // the reference's own network, bitonic_sort_id_by_num_int (gpu_graph.cu:123-141)
 // over the cells in their stage A order: a descending flip-bitonic network
 // whose order of equal scores is fixed by the network, not by the cells.
-__global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc,
-                                              const float* dist, const uint32_t* hist, uint32_t* cells,
-                                              const uint32_t* counts, uint32_t* topk, bool chosen, bool ref_ties) {
+__device__ __forceinline__ void order_query(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc,
+                                            const float* dist, const uint32_t* hist, uint32_t* cells,
+                                            const uint32_t* counts, uint32_t* topk, bool chosen, bool ref_ties) {
     extern __shared__ uint32_t so[];
     uint32_t* tk = so;             // topc
     uint32_t* sc = so + 16;        // P scores
@@ -2266,6 +2313,11 @@ __global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P
         for (uint32_t j = 0; j < n; ++j) rank += (sc[j] > s) || (sc[j] == s && cc[j] < cell);
         cl[rank] = cell;
     }
+}
+__global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc,
+                                              const float* dist, const uint32_t* hist, uint32_t* cells,
+                                              const uint32_t* counts, uint32_t* topk, bool chosen, bool ref_ties) {
+    order_query(Q, C, P, topc, dist, hist, cells, counts, topk, chosen, ref_ties);
 }
 
 // ------------------------------------------ query-batch brute force (MFMA)
@@ -3195,6 +3247,7 @@ struct BfWave {
 // have read them, its norms and meta into the other of two register sets.
 template <int KS, int AW, int KT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 && KS <= 2 && KT <= 10 ? 3 : 2))) void k_bf_i8(BfGemmArgs p) {
+    stamp_entry(p.stamp, 1);
     __shared__ uint64_t s_buf[4][kQB * kBfBufQ];
     __shared__ uint32_t s_cnt[4][kQB];
     __shared__ int32_t s_tp[4][kQB];
@@ -3680,6 +3733,7 @@ __global__ __launch_bounds__(64) void k_bf_f16_final(TravArgs p, BfHFinal f) {
 
 // Per-query merge of the keys the brute-force items appended for the query.
 __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
+    stamp_entry(p.stamp, 1);
     __shared__ uint64_t T[64];
     const uint32_t lane = lane_id();
     if (!*p.ok) return;
@@ -4624,10 +4678,13 @@ hipError_t launch_norms_f16(const uint16_t* x, uint32_t n, uint32_t D, uint32_t 
 
 hipError_t launch_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi, const uint32_t* grid,
                         const uint32_t* doff, const float* l_q, const float* r_q, uint32_t P,
-                        const uint32_t* offset, uint32_t* cells, uint32_t* counts, hipStream_t st) {
+                        const uint32_t* offset, uint32_t* cells, uint32_t* counts, hipStream_t st,
+                        const CellsTail& tl) {
     if (!Q) return hipSuccess;
+    if (tl.little && !tl.selcount) return hipErrorInvalidValue;
+    if (tl.st_exit && !tl.ticket) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_cells, dim3((Q + 63) / 64), dim3(64), 0, st, Q, a, lo, hi, grid, doff, l_q, r_q,
-                       P, offset, cells, counts);
+                       P, offset, cells, counts, tl);
     return hipGetLastError();
 }
 
@@ -4663,9 +4720,11 @@ hipError_t launch_selcount(uint32_t ntiles, const uint32_t* tile_cell, const uin
 }
 
 hipError_t launch_route(uint32_t Q, uint32_t N, float thr, const uint32_t* selcount, const uint32_t* counts,
-                        uint32_t* little, hipStream_t st) {
+                        uint32_t* little, hipStream_t st, uint32_t* ticket, uint64_t* st_exit) {
+    if (st_exit && !ticket) return hipErrorInvalidValue;
     if (!Q) return hipSuccess;
-    hipLaunchKernelGGL(k_route, dim3((Q + 255) / 256), dim3(256), 0, st, Q, N, thr, selcount, counts, little);
+    hipLaunchKernelGGL(k_route, dim3((Q + 255) / 256), dim3(256), 0, st, Q, N, thr, selcount, counts, little, ticket,
+                       st_exit);
     return hipGetLastError();
 }
 
@@ -4717,10 +4776,12 @@ hipError_t launch_zero_u32(uint32_t* x, uint32_t n, hipStream_t st) {
 }
 
 hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, hipStream_t st,
-                                uint32_t* z, uint32_t nz) {
+                                uint32_t* z, uint32_t nz, uint64_t* stp, uint32_t nst) {
+    if (nst > 64) return hipErrorInvalidValue;
     uint32_t n = Q * (K > GF_NCOUNTERS ? K : GF_NCOUNTERS);
     n = n > nz ? n : nz;
-    hipLaunchKernelGGL(k_reset_results, dim3((n + 255) / 256), dim3(256), 0, st, Q, K, ids, dist, ctr, z, nz);
+    hipLaunchKernelGGL(k_reset_results, dim3((n + 255) / 256), dim3(256), 0, st, Q, K, ids, dist, ctr, z, nz, stp,
+                       stp ? nst : 0u);
     return hipGetLastError();
 }
 
@@ -4771,11 +4832,12 @@ hipError_t launch_merge_stream(uint32_t Q, uint32_t K, uint32_t* run_ids, float*
 
 hipError_t launch_centroid(const uint16_t* qh, const uint16_t* ch, const float* qn, const float* cn,
                            uint32_t Q, uint32_t C, uint32_t Qp, uint32_t Cp, uint32_t Dp, float* dist,
-                           hipStream_t st) {
+                           hipStream_t st, uint64_t* st_entry) {
     if (!Q || !C) return hipSuccess;
     // Cp is a multiple of 64 and Qp of 16, so every tile read stays inside the
     // zero-padded operands.
-    hipLaunchKernelGGL(k_centroid, dim3(Qp / 16, Cp / 64), dim3(256), 0, st, qh, ch, qn, cn, Q, C, Dp, dist);
+    hipLaunchKernelGGL(k_centroid, dim3(Qp / 16, Cp / 64), dim3(256), 0, st, qh, ch, qn, cn, Q, C, Dp, dist,
+                       st_entry);
     return hipGetLastError();
 }
 
@@ -4791,11 +4853,11 @@ hipError_t launch_order(uint32_t Q, uint32_t C, uint32_t P, uint32_t topc, const
 
 hipError_t launch_centroid_top(const uint16_t* qh, const uint16_t* ch, const float* qn, const float* cn, uint32_t Q,
                                uint32_t C, uint32_t Qp, uint32_t Cp, uint32_t Dp, uint32_t topc, uint32_t* topk,
-                               hipStream_t st) {
+                               hipStream_t st, uint64_t* st_entry) {
     if (!Q || !C) return hipSuccess;
     if (topc < 1 || topc > 4) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_centroid_top, dim3(Qp / 16), dim3(64 * kCtW), 0, st, qh, ch, qn, cn, Q, C, Cp, Dp, topc,
-                       topk);
+                       topk, st_entry);
     return hipGetLastError();
 }
 

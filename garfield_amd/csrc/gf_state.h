@@ -453,7 +453,9 @@ struct gf_batch {
     // (stage A on an arithmetic grid) or device timestamps in stamps[5..6]
     // (stage A) and stamps[7..8] (stage B), which the search gathers.
     enum : uint8_t { kTimeNone = 0, kTimeEvents = 1, kTimeStamps = 2 };
-    static constexpr uint32_t kStampA = 5, kStampB = 7, kNStamps = 12;
+    // kNStamps gathered; then the zeroed counter of stamp_exit for stage A
+    // (kTicketA: a u64 slot holding a u32 counter)
+    static constexpr uint32_t kStampA = 5, kStampB = 7, kNStamps = 12, kTicketA = 12;
     hipEvent_t sev[2] = {nullptr, nullptr};
     uint8_t time_a = kTimeNone, time_b = kTimeNone;
     // Records event i of sev (created on first use).
@@ -469,8 +471,13 @@ struct gf_batch {
         return ms;
     }
     void ensure_stamps() {
-        if (!stamps.n) { stamps.alloc(kNStamps); h_stamps.alloc(kNStamps); }
+        if (!stamps.n) {
+            stamps.alloc(kNStamps + 4);
+            h_stamps.alloc(kNStamps);
+            GF_HIP(hipMemset(stamps.p, 0, (kNStamps + 4) * sizeof(uint64_t)));
+        }
     }
+    uint32_t* ticket(uint32_t i) { return reinterpret_cast<uint32_t*>(stamps.p + i); }
     // Milliseconds between the host copies of stamps i and i + 1.
     double stamp_ms(uint32_t i) const {
         const uint64_t* t = h_stamps.p;
