@@ -1113,7 +1113,8 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     // [2] end, [3..4] around the MFMA brute-force launches.
     b->ensure_stamps();
     uint64_t* stamp = b->stamps.p;
-    auto launch_gemm = [&]() {
+    // reset_done: k_reset_results already did k_bf_reset's work
+    auto launch_gemm = [&](bool reset_done) {
         gf::BfSchedArgs sc{};
         sc.sa = sub_args(*ix);
         sc.Q = Q; sc.postfilter = opts->postfilter; sc.counts = b->counts.p;
@@ -1129,8 +1130,9 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         }
         // Seeds (one-pass lists): each query's best-filled sub-cell runs first.
         const bool seeds = b->qcap != 0;
-        GF_HIP(gf::launch_bf_reset(Q, b->nsub.p, b->pcnt.p, b->gbound.p, st, seeds ? NS : 0,
-                                   seeds ? b->scnt.p : nullptr, seeds ? tot + 5 : nullptr));
+        if (!reset_done)
+            GF_HIP(gf::launch_bf_reset(Q, b->nsub.p, b->pcnt.p, b->gbound.p, st, seeds ? NS : 0,
+                                       seeds ? b->scnt.p : nullptr, seeds ? tot + 5 : nullptr));
         if (seeds) {
             gf::BfSeedArgs sd{};
             sd.sa = sc.sa; sd.Q = Q; sd.postfilter = sc.postfilter; sd.counts = sc.counts; sd.little = sc.little;
@@ -1146,9 +1148,8 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         if (seeds) GF_HIP(gf::launch_bfsched_direct(sc, st));
         else GF_HIP(gf::launch_bfsched(sc, false, st));
         if (!b->qcap) GF_HIP(gf::launch_scan_small(b->bcnt.p, NS, b->bstart.p, st));
-        GF_HIP(gf::launch_scan_small(b->nsub.p, Q, b->part_off.p, st));
-        GF_HIP(gf::launch_total(b->nsub.p, b->part_off.p, Q, uint32_t(std::min<size_t>(b->pair_cap, UINT32_MAX)), KP,
-                                b->part.n, tot + 2, st));
+        GF_HIP(gf::launch_scan_total(b->nsub.p, Q, b->part_off.p, uint32_t(std::min<size_t>(b->pair_cap, UINT32_MAX)),
+                                     KP, b->part.n, tot + 2, st));
         if (!b->qcap) GF_HIP(gf::launch_bfsched(sc, true, st));
         // Two passes (resident index): the seeds and the items of the
         // first-pass sub-cells, then a merge that lowers each query's
@@ -1283,9 +1284,21 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         sa.franges = ix->FD ? tot + 16 : nullptr;
         // timestamps: [0] (and [1] with no traversal) when the reset starts,
         // [2] when the gather of the results starts (k_gather_meta)
+        // with the brute-force schedule, the reset also does k_bf_reset's work
+        gf::BfReset br;
+        if (sched_bf) {
+            br.nsub = b->nsub.p;
+            br.pcnt = b->pcnt.p;
+            br.gbound = b->gbound.p;
+            if (b->qcap) {
+                br.NS = NS;
+                br.scnt = b->scnt.p;
+                br.nseed = tot + 5;
+            }
+        }
         GF_HIP(gf::launch_reset_results(Q, K, b->out_ids.p, b->out_dist.p, b->counters.p, st,
                                         stats ? reinterpret_cast<uint32_t*>(b->stats.p) : nullptr, stats ? 32u : 0u,
-                                        stamp + 0, route_bf ? 2u : 1u));
+                                        stamp + 0, route_bf ? 2u : 1u, br));
         GF_HIP(gf::launch_sched(sa, st));
         if (!route_bf) {
             // (with route_bf every query takes the brute force or has no
@@ -1299,7 +1312,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
             GF_HIP(gf::launch_stamp(stamp + 1, st));
         }
         if (sched_bf) {
-            launch_gemm();
+            launch_gemm(true);
         } else {
             gf::TravArgs ab = a;
             ab.srange = tot + 14;
@@ -1332,7 +1345,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         // the pair lists outgrew their buffers: grow them and run the brute force again
         b->alloc_pairs(size_t(dt[2]) + dt[2] / 4 + 1024, KP, Q, NS, size_t(NS) + ix->ntile / gf::kBfMaxItemTiles + 1);
         GF_HIP(gf::launch_stamp(stamp + 1, st));
-        launch_gemm();
+        launch_gemm(false);
         enqueue_tail();
         GF_REQUIRE(dt[3], GF_E_STATE, "brute-force schedule does not fit after growing");
     }

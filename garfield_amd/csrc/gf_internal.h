@@ -474,6 +474,9 @@ hipError_t launch_cells(uint32_t Q, uint32_t a, const float* lo, const float* hi
 hipError_t launch_cellq_count(uint32_t Q, uint32_t P, const uint32_t* cells,
                               const uint32_t* counts, uint32_t* ccount, hipStream_t st);
 hipError_t launch_scan_small(const uint32_t* in, uint32_t n, uint32_t* out_excl, hipStream_t st);
+// The scan and launch_total's outputs (tot[0..1]) in one kernel.
+hipError_t launch_scan_total(const uint32_t* in, uint32_t n, uint32_t* out_excl, uint32_t cap, uint32_t mul,
+                             uint64_t cap2, uint32_t* tot, hipStream_t st);
 hipError_t launch_cellq_fill(uint32_t Q, uint32_t P, const uint32_t* cells,
                              const uint32_t* counts, const uint32_t* cstart, uint32_t* cfill,
                              uint32_t* cellq, hipStream_t st);
@@ -497,8 +500,20 @@ hipError_t launch_stream_lists(uint32_t Q, uint32_t P, uint32_t B, const uint32_
 hipError_t launch_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t* gbound, hipStream_t st,
                           uint32_t NS = 0, uint32_t* scnt = nullptr, uint32_t* nseed = nullptr);
 // Also zeroes z[0, nz) (a search's statistics sums, for one kernel less).
+// The brute force's per-query state as k_bf_reset sets it (nsub and pcnt
+// 0, gbound open; scnt[0..NS) and *nseed 0 when given), for a reset that
+// does it too.
+struct BfReset {
+    uint32_t* nsub = nullptr;
+    uint32_t* pcnt = nullptr;
+    uint32_t* gbound = nullptr;
+    uint32_t NS = 0;
+    uint32_t* scnt = nullptr;
+    uint32_t* nseed = nullptr;
+};
 hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, hipStream_t st,
-                                uint32_t* z = nullptr, uint32_t nz = 0, uint64_t* stp = nullptr, uint32_t nst = 0);
+                                uint32_t* z = nullptr, uint32_t nz = 0, uint64_t* stp = nullptr, uint32_t nst = 0,
+                                const BfReset& br = BfReset{});
 // stats (16, optional), tot (24) and stamps (12) to page-locked host buffers;
 // stamps[2], the search's end, is taken by this kernel when it starts.
 hipError_t launch_gather_meta(const unsigned long long* stats, const uint32_t* tot, const uint64_t* stamps,

@@ -1669,7 +1669,16 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
     total = wsum[15];
     return (w ? wsum[w - 1] : 0u) + x - v;
 }
-__global__ __launch_bounds__(1024) void k_scan_small(const uint32_t* in, uint32_t n, uint32_t* out) {
+// tot (optional): tot[0] = the total, tot[1] = whether it fits cap entries
+// (and, times mul, cap2 when cap2 != 0) -- k_total's outputs.
+__device__ __forceinline__ void scan_total(uint32_t* tot, uint32_t total, uint32_t cap, uint32_t mul, uint64_t cap2) {
+    if (tot && threadIdx.x == 0) {
+        tot[0] = total;
+        tot[1] = (total <= cap && (cap2 == 0 || uint64_t(total) * mul <= cap2)) ? 1u : 0u;
+    }
+}
+__global__ __launch_bounds__(1024) void k_scan_small(const uint32_t* in, uint32_t n, uint32_t* out, uint32_t* tot,
+                                                     uint32_t cap, uint32_t mul, uint64_t cap2) {
     __shared__ uint32_t wsum[16];
     __shared__ uint32_t buf[kScanLds];
     const uint32_t t = threadIdx.x;
@@ -1688,6 +1697,7 @@ __global__ __launch_bounds__(1024) void k_scan_small(const uint32_t* in, uint32_
         }
         __syncthreads();
         for (uint32_t i = t; i < n; i += 1024u) out[i] = buf[i];
+        scan_total(tot, total, cap, mul, cap2);
         return;
     }
     uint32_t carry = 0;
@@ -1700,6 +1710,7 @@ __global__ __launch_bounds__(1024) void k_scan_small(const uint32_t* in, uint32_
         carry += total;
         __syncthreads();
     }
+    scan_total(tot, carry, cap, mul, cap2);
 }
 
 // Exact selectivity counts (real_dataset_adapter.cuh:346-383), tiled: a tile
@@ -1885,12 +1896,22 @@ __global__ void k_bf_reset(uint32_t Q, uint32_t* nsub, uint32_t* pcnt, uint32_t*
 
 // Sentinel results and zero counters for a batch's searches.
 __global__ void k_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, uint32_t* z,
-                                uint32_t nz, uint64_t* st, uint32_t nst) {
+                                uint32_t nz, uint64_t* st, uint32_t nst, BfReset br) {
     stamp_entry(st, nst);
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < Q * K) { ids[i] = GF_NO_RESULT; dist[i] = __int_as_float(0x7F800000); }
     if (i < Q * GF_NCOUNTERS) ctr[i] = 0;
     if (i < nz) z[i] = 0;
+    // k_bf_reset's work when br.nsub is set
+    if (br.nsub) {
+        if (br.scnt && i < br.NS) br.scnt[i] = 0;
+        if (br.nseed && i == 0) *br.nseed = 0;
+        if (i < Q) {
+            br.nsub[i] = 0;
+            br.pcnt[i] = 0;
+            br.gbound[i] = 0xFFFFFFFFu;
+        }
+    }
 }
 
 // A search's small host-side outputs in one kernel instead of three copies:
@@ -4696,7 +4717,14 @@ hipError_t launch_cellq_count(uint32_t Q, uint32_t P, const uint32_t* cells, con
 }
 
 hipError_t launch_scan_small(const uint32_t* in, uint32_t n, uint32_t* out, hipStream_t st) {
-    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, st, in, n, out);
+    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, st, in, n, out, nullptr, 0u, 0u, uint64_t(0));
+    return hipGetLastError();
+}
+
+hipError_t launch_scan_total(const uint32_t* in, uint32_t n, uint32_t* out, uint32_t cap, uint32_t mul, uint64_t cap2,
+                             uint32_t* tot, hipStream_t st) {
+    if (!tot) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_scan_small, dim3(1), dim3(1024), 0, st, in, n, out, tot, cap, mul, cap2);
     return hipGetLastError();
 }
 
@@ -4776,12 +4804,14 @@ hipError_t launch_zero_u32(uint32_t* x, uint32_t n, hipStream_t st) {
 }
 
 hipError_t launch_reset_results(uint32_t Q, uint32_t K, uint32_t* ids, float* dist, uint32_t* ctr, hipStream_t st,
-                                uint32_t* z, uint32_t nz, uint64_t* stp, uint32_t nst) {
+                                uint32_t* z, uint32_t nz, uint64_t* stp, uint32_t nst, const BfReset& br) {
     if (nst > 64) return hipErrorInvalidValue;
+    if (br.nsub && (!br.pcnt || !br.gbound || (br.scnt && !br.nseed))) return hipErrorInvalidValue;
     uint32_t n = Q * (K > GF_NCOUNTERS ? K : GF_NCOUNTERS);
     n = n > nz ? n : nz;
+    if (br.nsub) n = n > br.NS ? n : br.NS;
     hipLaunchKernelGGL(k_reset_results, dim3((n + 255) / 256), dim3(256), 0, st, Q, K, ids, dist, ctr, z, nz, stp,
-                       stp ? nst : 0u);
+                       stp ? nst : 0u, br);
     return hipGetLastError();
 }
 
