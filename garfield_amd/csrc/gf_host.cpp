@@ -588,6 +588,87 @@ void ensure_selcount(gf_batch& b) {
     b.sel_exact = true;
 }
 
+// Stage A's kernels (gf_mark_cells) on st.  The stage's kernels take its
+// timestamps: the cell kernel when it starts, the last kernel (ticket) when
+// it ends.
+void stage_a_enqueue(gf_batch* b, float prefilter, hipStream_t st) {
+    gf_index* ix = b->ix;
+    const bool count = prefilter < 1.0f;
+    gf::CellsTail tl;
+    tl.st_entry = b->stamps.p + gf_batch::kStampA;
+    uint32_t* const ticket = b->ticket(gf_batch::kTicketA);
+    uint64_t* const st_end = b->stamps.p + gf_batch::kStampA + 1;
+    if (!count) {
+        // prefilter >= 1: count / N <= prefilter holds for every count, so
+        // every query is routed to the brute force without counting (the
+        // routing is the reference's), in the cell kernel itself; the exact
+        // counts are made when asked for.
+        tl.selcount = b->selcount.p;
+        tl.little = b->little.p;
+        tl.ticket = ticket;
+        tl.st_exit = st_end;
+    }
+    GF_HIP(gf::launch_cells(b->Q, ix->a, b->lo.p, b->hi.p, ix->grid.p, ix->doff.p, ix->l_q.p, ix->r_q.p, ix->P,
+                            ix->offset.p, b->cells.p, b->counts.p, st, tl));
+    if (count) {
+        count_selectivity(*b, st);
+        GF_HIP(gf::launch_route(b->Q, ix->N, prefilter, b->selcount.p, b->counts.p, b->little.p, st, ticket,
+                                st_end));
+    }
+}
+std::vector<uint64_t> stage_a_key(const gf_batch* b, float prefilter) {
+    uint32_t pf = 0;
+    std::memcpy(&pf, &prefilter, sizeof(pf));
+    return {uint64_t(uintptr_t(b->ix)), pf, b->Q, uint64_t(uintptr_t(b->lo.p)), uint64_t(uintptr_t(b->hi.p)),
+            uint64_t(uintptr_t(b->cells.p)), uint64_t(uintptr_t(b->counts.p)), uint64_t(uintptr_t(b->selcount.p)),
+            uint64_t(uintptr_t(b->little.p)), uint64_t(uintptr_t(b->ccount.p)), uint64_t(uintptr_t(b->cfill.p)),
+            uint64_t(uintptr_t(b->cstart.p)), uint64_t(uintptr_t(b->cellq.p)), uint64_t(uintptr_t(b->stamps.p))};
+}
+// Stage B's kernels (gf_order_cells, b->topc centres) on st.  Timestamps:
+// the centre kernel when it starts, a stamp kernel at the end (k_order runs
+// one workgroup per query: a ticket over that many workgroups costs more
+// than a kernel).
+void stage_b_enqueue(gf_batch* b, hipStream_t st) {
+    gf_index* ix = b->ix;
+    const uint32_t topc = b->topc;
+    uint64_t* const st0 = b->stamps.p + gf_batch::kStampB;
+    if (topc <= 4) {
+        // nearest centres straight from the MFMA tiles; the distance matrix
+        // is made only if gf_batch_get_centroid asks for it
+        GF_HIP(gf::launch_centroid_top(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp, ix->Cp,
+                                       ix->Dp, topc, b->topk.p, st, st0));
+        GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, nullptr, ix->hist.p, b->cells.p, b->counts.p, b->topk.p,
+                                st, true, ix->ref_ties));
+    } else {
+        GF_HIP(gf::launch_centroid(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp, ix->Cp,
+                                   ix->Dp, b->cdist.p, st, st0));
+        GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, b->cdist.p, ix->hist.p, b->cells.p, b->counts.p,
+                                b->topk.p, st, false, ix->ref_ties));
+    }
+    GF_HIP(gf::launch_stamp(st0 + 1, st));
+}
+std::vector<uint64_t> stage_b_key(const gf_batch* b) {
+    return {uint64_t(uintptr_t(b->ix)), b->topc, b->Q, uint64_t(uintptr_t(b->topk.p)), uint64_t(uintptr_t(b->cdist.p)),
+            uint64_t(uintptr_t(b->q16.p)), uint64_t(uintptr_t(b->qnorm.p)), uint64_t(uintptr_t(b->cells.p)),
+            uint64_t(uintptr_t(b->counts.p)), uint64_t(uintptr_t(b->stamps.p))};
+}
+// Enqueues the stage calls recorded without ms (gf_mark_cells, then
+// gf_order_cells), each as its own graph.  Every call that reads or writes
+// the stage buffers, other than the search (which takes them into its own
+// graph), flushes first.
+void flush_stages(gf_batch* b) {
+    hipStream_t st = b->ix->stream;
+    if (b->pend_a) {
+        b->pend_a = false;
+        const float pf = b->pend_pf;
+        b->sg[gf_batch::kGraphA].run(stage_a_key(b, pf), st, [&]() { stage_a_enqueue(b, pf, st); });
+    }
+    if (b->pend_b) {
+        b->pend_b = false;
+        b->sg[gf_batch::kGraphB].run(stage_b_key(b), st, [&]() { stage_b_enqueue(b, st); });
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -809,54 +890,29 @@ gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms) {
         gf_index* ix = b->ix;
         GF_REQUIRE(!ix->sx, GF_E_UNSUPPORTED,
                    "a streamed index has no resident attributes: use gf_mark_cells_grid or gf_batch_set_cells");
-        b->flags_ready = false;
-        b->bf_all = true;
         set_device(ix);
         hipStream_t st = ix->stream;
         b->ensure_stamps();
+        // a stage B recorded before this call runs first
+        if (b->pend_b) flush_stages(b);
         const bool count = prefilter < 1.0f;
-        auto enqueue = [&]() {
-            // the stage's kernels take its timestamps: the cell kernel when it
-            // starts, the last kernel (ticket) when it ends
-            gf::CellsTail tl;
-            tl.st_entry = b->stamps.p + gf_batch::kStampA;
-            uint32_t* const ticket = b->ticket(gf_batch::kTicketA);
-            uint64_t* const st_end = b->stamps.p + gf_batch::kStampA + 1;
-            if (!count) {
-                // prefilter >= 1: count / N <= prefilter holds for every
-                // count, so every query is routed to the brute force without
-                // counting (the routing is the reference's), in the cell
-                // kernel itself; the exact counts are made when asked for.
-                tl.selcount = b->selcount.p;
-                tl.little = b->little.p;
-                tl.ticket = ticket;
-                tl.st_exit = st_end;
-            }
-            GF_HIP(gf::launch_cells(b->Q, ix->a, b->lo.p, b->hi.p, ix->grid.p, ix->doff.p, ix->l_q.p, ix->r_q.p,
-                                    ix->P, ix->offset.p, b->cells.p, b->counts.p, st, tl));
-            if (count) {
-                count_selectivity(*b, st);
-                GF_HIP(gf::launch_route(b->Q, ix->N, prefilter, b->selcount.p, b->counts.p, b->little.p, st, ticket,
-                                        st_end));
-            }
-        };
-        uint32_t pf = 0;
-        std::memcpy(&pf, &prefilter, sizeof(pf));
-        const uint64_t key[] = {uint64_t(uintptr_t(ix)), pf, b->Q, uint64_t(uintptr_t(b->lo.p)),
-                                uint64_t(uintptr_t(b->hi.p)), uint64_t(uintptr_t(b->cells.p)),
-                                uint64_t(uintptr_t(b->counts.p)), uint64_t(uintptr_t(b->selcount.p)),
-                                uint64_t(uintptr_t(b->little.p)), uint64_t(uintptr_t(b->ccount.p)),
-                                uint64_t(uintptr_t(b->cfill.p)), uint64_t(uintptr_t(b->cstart.p)),
-                                uint64_t(uintptr_t(b->cellq.p)), uint64_t(uintptr_t(b->stamps.p))};
-        b->sg[gf_batch::kGraphA].run(std::vector<uint64_t>(std::begin(key), std::end(key)), st, enqueue);
+        b->flags_ready = false;
+        b->bf_all = true;
         b->sel_exact = count;
         b->route_bf = !count;
         b->time_a = gf_batch::kTimeStamps;
-        if (ms) {
-            b->fetch_stamps(gf_batch::kStampA, 2, st);
-            *ms = b->stamp_ms(gf_batch::kStampA);
-        }
         b->marked = true;
+        if (!ms) {
+            // recorded: the next search enqueues it in its own graph (another
+            // call that needs the stage's outputs enqueues it first)
+            b->pend_a = true;
+            b->pend_pf = prefilter;
+            return;
+        }
+        b->pend_a = false;
+        b->sg[gf_batch::kGraphA].run(stage_a_key(b, prefilter), st, [&]() { stage_a_enqueue(b, prefilter, st); });
+        b->fetch_stamps(gf_batch::kStampA, 2, st);
+        *ms = b->stamp_ms(gf_batch::kStampA);
     });
 }
 
@@ -870,6 +926,7 @@ gf_status gf_mark_cells_grid(gf_batch* b, const float* attr_min, const float* at
                        "attr_width must be positive and finite, attr_min finite");
         set_device(ix);
         hipStream_t st = ix->stream;
+        flush_stages(b);
         if (b->flags.n < size_t(b->Q) * ix->P) b->flags.alloc(size_t(b->Q) * ix->P);
         DevBuf<float> amin, width;
         amin.upload(attr_min, ix->a);
@@ -900,43 +957,25 @@ gf_status gf_order_cells(gf_batch* b, uint32_t topc, double* ms) {
         set_device(ix);
         if (!ix->C) { if (ms) *ms = 0.0; b->time_b = gf_batch::kTimeNone; return; }
         hipStream_t st = ix->stream;
+        // a stage B recorded before runs first: the stage reorders the cell
+        // lists in place, so two of them are not one
+        if (b->pend_b) flush_stages(b);
         if (b->topk.n < size_t(b->Q) * topc) b->topk.alloc(size_t(b->Q) * topc);
         const bool top = topc <= 4;
         if (!top && !b->cdist.p) b->cdist.alloc(size_t(b->Q) * ix->C);
         b->topc = topc;
         b->ensure_stamps();
-        auto enqueue = [&]() {
-            // timestamps: the centre kernel when it starts, a stamp kernel at
-            // the end (k_order runs one workgroup per query: a ticket over
-            // that many workgroups costs more than a kernel)
-            uint64_t* const st0 = b->stamps.p + gf_batch::kStampB;
-            if (top) {
-                // nearest centres straight from the MFMA tiles; the distance
-                // matrix is made only if gf_batch_get_centroid asks for it
-                GF_HIP(gf::launch_centroid_top(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp,
-                                               ix->Cp, ix->Dp, topc, b->topk.p, st, st0));
-                GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, nullptr, ix->hist.p, b->cells.p, b->counts.p,
-                                        b->topk.p, st, true, ix->ref_ties));
-            } else {
-                GF_HIP(gf::launch_centroid(b->q16.p, ix->centres.p, b->qnorm.p, ix->cnorm.p, b->Q, ix->C, b->Qp,
-                                           ix->Cp, ix->Dp, b->cdist.p, st, st0));
-                GF_HIP(gf::launch_order(b->Q, ix->C, ix->P, topc, b->cdist.p, ix->hist.p, b->cells.p, b->counts.p,
-                                        b->topk.p, st, false, ix->ref_ties));
-            }
-            GF_HIP(gf::launch_stamp(st0 + 1, st));
-        };
-        const uint64_t key[] = {uint64_t(uintptr_t(ix)), topc, b->Q, uint64_t(uintptr_t(b->topk.p)),
-                                uint64_t(uintptr_t(b->cdist.p)), uint64_t(uintptr_t(b->q16.p)),
-                                uint64_t(uintptr_t(b->qnorm.p)), uint64_t(uintptr_t(b->cells.p)),
-                                uint64_t(uintptr_t(b->counts.p)), uint64_t(uintptr_t(b->stamps.p))};
-        b->sg[gf_batch::kGraphB].run(std::vector<uint64_t>(std::begin(key), std::end(key)), st, enqueue);
         b->cdist_ready = !top;
         b->ordered = true;
         b->time_b = gf_batch::kTimeStamps;
-        if (ms) {
-            b->fetch_stamps(gf_batch::kStampB, 2, st);
-            *ms = b->stamp_ms(gf_batch::kStampB);
+        if (!ms) {
+            b->pend_b = true;   // recorded, as gf_mark_cells without ms
+            return;
         }
+        flush_stages(b);   // a recorded stage A
+        b->sg[gf_batch::kGraphB].run(stage_b_key(b), st, [&]() { stage_b_enqueue(b, st); });
+        b->fetch_stamps(gf_batch::kStampB, 2, st);
+        *ms = b->stamp_ms(gf_batch::kStampB);
     });
 }
 
@@ -965,10 +1004,14 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         stats->ms_stage_b = b->time_b == gf_batch::kTimeStamps ? b->stamp_ms(gf_batch::kStampB) : 0.0;
     };
     if (ix->sx) {
+        flush_stages(b);
         gf::stream_search(*b, *opts, ids, dists, stats);
         stage_times(false);
         return;
     }
+    // stage calls recorded without ms run at the start of this stage's graph
+    const bool pend_a = b->pend_a, pend_b = b->pend_b;
+    const float pend_pf = b->pend_pf;
     hipStream_t st = ix->stream;
     const uint32_t Q = b->Q, R = ix->R;
 
@@ -1276,6 +1319,8 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     const bool route_bf = b->route_bf;
     // The whole stage, schedule to copies: no allocation, no host wait.
     auto enqueue = [&]() {
+        if (pend_a) stage_a_enqueue(b, pend_pf, st);
+        if (pend_b) stage_b_enqueue(b, st);
         // Schedule (gpu_graph.cu:12485-12493) on the device.
         gf::SchedArgs sa{};
         sa.Q = Q; sa.P = ix->P; sa.postfilter = opts->postfilter; sa.counts = b->counts.p; sa.little = b->little.p;
@@ -1338,7 +1383,20 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
                             uint64_t(uintptr_t(b->scnt.p)), uint64_t(uintptr_t(b->rq.p)),
                             uint64_t(uintptr_t(b->bcnt.p)), uint64_t(uintptr_t(b->h_tot.p)),
                             uint64_t(uintptr_t(b->stamps.p)), uint64_t(uintptr_t(b->h_stamps.p))};
-    b->run_stage(std::vector<uint64_t>(std::begin(key), std::end(key)), st, enqueue);
+    std::vector<uint64_t> gkey(std::begin(key), std::end(key));
+    uint32_t ppf = 0;
+    std::memcpy(&ppf, &pend_pf, sizeof(ppf));
+    gkey.push_back(uint64_t(pend_a) | uint64_t(pend_b) << 1 | uint64_t(pend_a ? ppf : 0u) << 2);
+    if (pend_a) {
+        const auto ka = stage_a_key(b, pend_pf);
+        gkey.insert(gkey.end(), ka.begin(), ka.end());
+    }
+    if (pend_b) {
+        const auto kb = stage_b_key(b);
+        gkey.insert(gkey.end(), kb.begin(), kb.end());
+    }
+    b->pend_a = b->pend_b = false;
+    b->run_stage(gkey, st, enqueue);
     GF_HIP(hipStreamSynchronize(st));
     const uint32_t* dt = b->h_tot.p;
     if (sched_bf && !dt[3]) {
@@ -1364,8 +1422,10 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         stats->ms_bruteforce = t_bf;
         stats->ms_total = double(t_tr) + double(t_bf);
         stats->ms_bf_kernel = t_g;
-        stats->graph = (b->graph_replayed() ? 1u : 0u) | (b->sg[gf_batch::kGraphA].replayed ? 2u : 0u) |
-                       (b->sg[gf_batch::kGraphB].replayed ? 4u : 0u);
+        // a recorded stage ran in the search's graph
+        const bool ra = pend_a ? b->graph_replayed() : b->sg[gf_batch::kGraphA].replayed;
+        const bool rb = pend_b ? b->graph_replayed() : b->sg[gf_batch::kGraphB].replayed;
+        stats->graph = (b->graph_replayed() ? 1u : 0u) | (ra ? 2u : 0u) | (rb ? 4u : 0u);
         stats->q_traverse = dt[8];
         stats->q_bruteforce = dt[9];
         stats->q_empty = dt[10];
@@ -1427,7 +1487,8 @@ gf_status gf_batch_get_cells(const gf_batch* b, uint32_t* cells, uint32_t* count
         GF_REQUIRE(b, GF_E_ARG, "null batch");
         GF_REQUIRE(b->marked, GF_E_STATE, "cells not marked");
         set_device(b->ix);
-        // the stage calls return once enqueued: wait for them
+        // the stage calls return once recorded or enqueued: run and wait for them
+        flush_stages(const_cast<gf_batch*>(b));
         GF_HIP(hipStreamSynchronize(b->ix->stream));
         if (selcount) ensure_selcount(*const_cast<gf_batch*>(b));
         const size_t Q = b->Q;
@@ -1454,6 +1515,7 @@ gf_status gf_batch_set_cells(gf_batch* b, const uint32_t* cells, const uint32_t*
         }
         const size_t Q = b->Q;
         // an earlier stage call may still be writing these buffers
+        flush_stages(b);
         GF_HIP(hipStreamSynchronize(b->ix->stream));
         GF_HIP(hipMemcpy(b->cells.p, cells, Q * P * 4, hipMemcpyHostToDevice));
         GF_HIP(hipMemcpy(b->counts.p, counts, Q * 4, hipMemcpyHostToDevice));
@@ -1471,6 +1533,7 @@ gf_status gf_batch_get_centroid(const gf_batch* b, float* dist, uint32_t* topc) 
         GF_REQUIRE(b->ordered, GF_E_STATE, "gf_order_cells has not run");
         set_device(b->ix);
         const gf_index* ix = b->ix;
+        flush_stages(const_cast<gf_batch*>(b));
         GF_HIP(hipStreamSynchronize(ix->stream));
         if (dist && !b->cdist_ready) {
             // the matrix the nearest centres were chosen from (same tiles, same rounding)
@@ -1492,6 +1555,7 @@ gf_status gf_batch_get_cell_flags(const gf_batch* b, uint8_t* flags) {
         GF_REQUIRE(b->marked, GF_E_STATE, "cells not marked");
         gf_batch* mb = const_cast<gf_batch*>(b);
         set_device(b->ix);
+        flush_stages(mb);
         GF_HIP(hipStreamSynchronize(b->ix->stream));
         const size_t n = size_t(b->Q) * b->ix->P;
         if (!b->flags_ready) {
@@ -1509,6 +1573,7 @@ gf_status gf_batch_get_counters(const gf_batch* b, uint32_t* counters) {
         GF_REQUIRE(b && counters, GF_E_ARG, "null argument");
         GF_REQUIRE(b->counters.p, GF_E_STATE, "gf_search has not run");
         set_device(b->ix);
+        flush_stages(const_cast<gf_batch*>(b));
         GF_HIP(hipStreamSynchronize(b->ix->stream));
         GF_HIP(hipMemcpy(counters, b->counters.p, size_t(b->Q) * GF_NCOUNTERS * 4, hipMemcpyDeviceToHost));
         if (b->pass_pending) {
@@ -1629,6 +1694,7 @@ gf_status gf_batch_plan_stream(gf_batch* b, uint64_t max_points, uint32_t max_ce
         GF_REQUIRE(b->ix->sx, GF_E_UNSUPPORTED, "gf_batch_plan_stream: not a streamed index");
         GF_REQUIRE(b->marked, GF_E_STATE, "cells not marked");
         set_device(b->ix);
+        flush_stages(b);
         const uint64_t act = gf::stream_plan_batch(*b, max_points, max_cells);
         if (nbatch) *nbatch = uint32_t(b->splan->batches.size());
         if (active) *active = act;

@@ -368,6 +368,11 @@ struct gf_batch {
     bool marked = false;
     // the latest stage A sent every query to the brute force (prefilter >= 1)
     bool route_bf = false;
+    // Stage calls made without ms on a resident index, not yet enqueued:
+    // the search enqueues them in its own graph; any other call that reads
+    // or writes the stage buffers enqueues them first (flush_stages).
+    bool pend_a = false, pend_b = false;
+    float pend_pf = 0.0f;
     bool i8 = false;
     DevBuf<int8_t> q8;
     DevBuf<int32_t> nq;
