@@ -200,9 +200,12 @@ gf_status gf_batch_free(gf_batch* b);
  * to filtered brute force.  With prefilter >= 1 every query is routed there
  * without counting (count / N <= 1 always holds); the exact counts are then
  * made when gf_batch_get_cells asks for selcount or counters are read.
- * ms (may be NULL) receives the device time; with ms NULL the call returns
- * once the stage is enqueued, and gf_search_stats.ms_stage_a reports the
- * device time after the search (the same holds for the other stage calls). */
+ * ms (may be NULL) receives the device time.  With ms NULL the call only
+ * records the stage: the next gf_search runs it at the start of its own HIP
+ * graph and gf_search_stats.ms_stage_a reports its device time; a call that
+ * reads or writes the stage's outputs (the batch getters, gf_batch_set_cells,
+ * gf_mark_cells_grid, gf_batch_plan_stream) runs it first.  The same holds
+ * for gf_order_cells. */
 gf_status gf_mark_cells(gf_batch* b, float prefilter, double* ms);
 
 /* Stage B -- get_partitions_access_order_V2 (gpu_graph.cu:11742-11845):
