@@ -957,8 +957,8 @@ gf_status gf_order_cells(gf_batch* b, uint32_t topc, double* ms) {
         set_device(ix);
         if (!ix->C) { if (ms) *ms = 0.0; b->time_b = gf_batch::kTimeNone; return; }
         hipStream_t st = ix->stream;
-        // a stage B recorded before runs first: the stage reorders the cell
-        // lists in place, so two of them are not one
+        // a stage B recorded before runs first, so that the calls run in the
+        // order they were made (the stage reorders the cell lists in place)
         if (b->pend_b) flush_stages(b);
         if (b->topk.n < size_t(b->Q) * topc) b->topk.alloc(size_t(b->Q) * topc);
         const bool top = topc <= 4;

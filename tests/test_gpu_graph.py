@@ -211,3 +211,44 @@ def test_stage_a_b_graph_replays(monkeypatch, world_sub2, world32, prefilters):
     finally:
         b.close()
         dev.close()
+
+
+def test_recorded_stage_calls_keep_their_order(world32):
+    """Stage calls without ms are recorded and run later (at the next search,
+    or first thing in a call that reads the stage buffers), in the order they
+    were made: every sequence of calls made without ms gives the cells, ids
+    and counters of the same sequence made with ms (each call run at once),
+    here with the reference's tie order (ref_ties)."""
+    cfg, ix = world32
+    lo, hi = cfg["lo"].astype(np.float32), cfg["hi"].astype(np.float32)
+    dev = synth.open_device_index(ix, ref_ties=True)
+    seqs = [["A", "B", "B", "cells"],
+            ["A", "B", "A", "B", "B", "search", "cells"],
+            ["A", "B", "search", "B", "search", "cells"],
+            ["A", "A", "B", "cells", "B", "cells", "search"]]
+    try:
+        for n, seq in enumerate(seqs):
+            _print_case("recorded-order", seq=n)
+            got = {}
+            for timed in (True, False):
+                b = dev.batch(cfg["queries"], lo, hi)
+                out = []
+                try:
+                    for op in seq:
+                        if op == "A":
+                            b.mark_cells(0.05, timed=timed)
+                        elif op == "B":
+                            b.order_cells(4, timed=timed)
+                        elif op == "cells":
+                            out.append(b.get_cells()[:3])
+                        else:
+                            ids, d, _ = b.search(L=48, K=10, rl=10)
+                            out.append((ids.copy(), d.view(np.uint32).copy(), b.get_counters()))
+                finally:
+                    b.close()
+                got[timed] = out
+            for i, (x, y) in enumerate(zip(got[True], got[False])):
+                for k, (u, v) in enumerate(zip(x, y)):
+                    assert np.array_equal(u, v), f"sequence {n} ({seq}): output {i} part {k} differs"
+    finally:
+        dev.close()
