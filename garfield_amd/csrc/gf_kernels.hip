@@ -2355,8 +2355,10 @@ __global__ __launch_bounds__(64) void k_order(uint32_t Q, uint32_t C, uint32_t P
 // 4 (l / 16) + i, i < 4, of query 16 j + l % 16 for each column tile j.  The
 // accumulator starts at -floor(|x'|^2 / 2), so "d <= thr" becomes the single
 // compare acc >= ceil((|q'|^2 - thr) / 2) (exact up to the parity of |x'|^2,
-// which the owner's exact test settles).  The range test runs on every pair as
-// a packed u16 clamp: per cell, attributes are stored as value - base in
+// which the owner's exact test settles).  The range test runs, where some pair
+// of a column tile is within its bound, on that column tile's pairs as a
+// packed u16 clamp (not at all in an item whose queries all contain the
+// sub-cell): per cell, attributes are stored as value - base in
 // [0, 65533] (tile padding 65535) and a query's range becomes [lo', hi'] in the
 // same units (an empty range is [65534, 65534]); a point passes iff clamping
 // its packed word leaves it unchanged.  Survivors (rare once the threshold has
@@ -3061,7 +3063,8 @@ __global__ void k_note_bf(const uint32_t* tot, uint32_t* note) {
 // its sorted top-K of (distance << 32 | row) keys in registers, its survivor
 // buffer (BUFQ slots) and its accumulator threshold in LDS; B holds the
 // item's queries as four 16-query column tiles (a dead column repeats the
-// first query, whose empty range keeps it from producing survivors).  A lane
+// first query; its threshold INT32_MAX and its empty range keep it from
+// producing survivors).  A lane
 // reserves the buffer slots of its survivors of a tile with one LDS atomic
 // per column tile (at most four per tile, issued together).
 template <int KS, int AW, int KT, uint32_t BUFQ>
