@@ -1219,9 +1219,29 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
             ha.items = b->items.p; ha.nitems = tot + 4; ha.bq = b->bq.p; ha.part_off = b->part_off.p;
             ha.pcnt = b->pcnt.p; ha.part = b->part.p; ha.gbound = b->gbound.p; ha.over = b->hover.p;
             ha.ok = tot + 3;
-            if (seeds) { ha.sitems = b->sitems.p; ha.nseed = tot + 5; ha.nseed_cap = scap; }
+            if (seeds) { ha.sitems = b->sitems.p; ha.nseed = tot + 5; ha.nseed_cap = scap; ha.seeds_on = 1; }
             ha.K = K; ha.D = ix->D;
             GF_HIP(gf::launch_stamp(stamp + 3, st));
+            // Binary16 rows: the seeds alone, then (two passes) the
+            // first-pass sub-cells' items, then the rest, each launch
+            // starting from the bounds the earlier ones left in gbound
+            // (C4, 768-d: 6.1 ms against 7.8 ms in one launch).  fp32 rows:
+            // one launch, seeds first in each workgroup (C3, 96-d: 6.0 ms
+            // against 7.4 ms in three).
+            const bool split = fvt == 1;
+            if (seeds && split) {
+                ha.irange = 3;
+                GF_HIP(gf::launch_bf_float(ha, fvt, ix->AW, uint32_t(ix->ncu), st));
+                ha.seeds_on = 0;
+            }
+            if (two && split) {
+                ha.nitems_a = tot + 6;
+                ha.irange = 1;
+                GF_HIP(gf::launch_bf_float(ha, fvt, ix->AW, uint32_t(ix->ncu), st));
+                ha.irange = 2;
+            } else {
+                ha.irange = 0;
+            }
             GF_HIP(gf::launch_bf_float(ha, fvt, ix->AW, uint32_t(ix->ncu), st));
             GF_HIP(gf::launch_stamp(stamp + 4, st));
             gf::TravArgs ab = a;

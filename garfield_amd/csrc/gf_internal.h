@@ -197,6 +197,12 @@ struct BfHArgs {
     const BfItem* sitems;
     const uint32_t* nseed;
     uint32_t nseed_cap;
+    // What a launch runs, as BfGemmArgs: the seed items if seeds_on, and of
+    // the item list all (irange 0), the first *nitems_a (1), the rest (2)
+    // or none (3).
+    uint32_t seeds_on;
+    uint32_t irange;
+    const uint32_t* nitems_a;
     uint32_t K, D;
 };
 struct BfHFinal {

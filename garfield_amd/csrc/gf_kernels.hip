@@ -64,6 +64,12 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
     return __builtin_amdgcn_mbcnt_hi(uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0u));
 }
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+// v of lane src (any lane, not necessarily active-uniform).
+__device__ __forceinline__ uint64_t shfl64(uint64_t v, uint32_t src) {
+    const uint32_t lo = uint32_t(__shfl(int(uint32_t(v)), int(src), 64));
+    const uint32_t hi = uint32_t(__shfl(int(uint32_t(v >> 32)), int(src), 64));
+    return (uint64_t(hi) << 32) | lo;
+}
 
 // Lanes of one wave exchange data through LDS between the phases below
 // (one-wave workgroups only).  A wave's LDS instructions execute in issue
@@ -1418,12 +1424,15 @@ __device__ void bf_flush(const QReg<VT, LPR, CPL>& qv, const TravArgs& p, const 
             if (sm == 0) continue;
             const uint64_t kc = ckey(c), kt = ckey(top);
             uint32_t rs = 0, rt = lane;
+            // ranks in the merged order, ties to the top entry, then to the
+            // lower lane: a permutation even if a key repeats
             for (uint64_t m = sm; m; m &= m - 1) {
-                const uint64_t kk = readlane64(kc, __builtin_ctzll(m));
-                rs += kk < kc;
+                const uint32_t j = __builtin_ctzll(m);
+                const uint64_t kk = readlane64(kc, j);
+                rs += kk < kc || (kk == kc && j < lane);
                 rt += kk < kt;
             }
-            for (uint32_t t = 0; t < K; ++t) rs += readlane64(kt, t) < kc;
+            for (uint32_t t = 0; t < K; ++t) rs += readlane64(kt, t) <= kc;
             wave_sync();
             if (surv && rs < K) T[rs] = c;
             if (lane < K && rt < K) T[rt] = top;
@@ -3374,10 +3383,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AW == 1 && 
 // d' = |q|^2 + |x|^2 - 2 q.x differs from the canonical fp32 distance d by at
 // most eps_q (a bound from the fp32 error of both), so every point whose d
 // is among the K smallest has d' within the query's smallest K-th d' plus
-// 2 eps_q; k_bf_f16_final re-ranks exactly the keys within that limit.  An
-// owner lane keeps its query's 32 smallest keys per item (in LDS); if all 32
-// lie within min(bound, the item's K-th) plus 2 eps_q, keys may have been
-// dropped, and the query is flagged for an exact scan.
+// 2 eps_q; k_bf_f16_final re-ranks exactly the keys within that limit.  Per
+// item a query keeps its 32 smallest keys (in registers, 8 in each of the
+// four lanes of its column); if all 32 lie within min(bound, the item's
+// K-th) plus 2 eps_q, keys may have been dropped, and the query is flagged
+// for an exact scan.
 // Operand chunks of the two row types.  Binary16 rows (VT 1): a chunk is
 // one v_mfma_f32_16x16x32_f16 k-step, 8 halves per lane (lane group g holds
 // dims 32 c + 8 g .. + 8).  fp32 rows (VT 0): a chunk is four
@@ -3452,11 +3462,11 @@ __device__ void bf_float_items(const BfHArgs& p) {
     static_assert(RB == NSLOT * 16u + NTAIL * 16u, "record layout");
     __shared__ uint4 s_tile[2][NSLOT];
     __shared__ uint32_t s_tail[2][MW + 16u];   // meta words, then the norms
-    // Per-owner lists padded by one key, so that the 16 owners' lists start
-    // on different LDS banks (the drain's accesses go to all 16 at once).
-    constexpr uint32_t BQ = kBfBufQ + 1u, TK = kBfHKT + 1u;
+    // Per-owner survivor buffers padded by one key, so that the 16 owners'
+    // buffers start on different LDS banks (the drain reads all 16 at once).
+    constexpr uint32_t BQ = kBfBufQ + 1u;
+    static_assert(kBfHKT == 32u, "kept keys: 8 per lane of the owner's 4 lanes");
     __shared__ uint64_t s_buf[4][16 * BQ];
-    __shared__ uint64_t s_tk[4][16][TK];   // per owner: its kept keys, ascending
     __shared__ uint32_t s_cnt[4][16];
     __shared__ float s_tp[4][16];
     __shared__ uint32_t s_bnd[4][2 * AW][16];
@@ -3466,15 +3476,18 @@ __device__ void bf_float_items(const BfHArgs& p) {
     const SubArgs& sa = p.sa;
     const uint32_t nwg = gridDim.x, xcd = blockIdx.x & 7u, k8 = blockIdx.x >> 3;
     const uint32_t nwg_x = (nwg - xcd + 7u) >> 3;
-    const uint32_t i_e = *p.ok ? *p.nitems : 0u;
-    const uint32_t i_lo = uint32_t(uint64_t(i_e) * xcd / 8u), i_hi = uint32_t(uint64_t(i_e) * (xcd + 1u) / 8u);
+    uint32_t i_b = 0, i_e = *p.ok && p.irange != 3u ? *p.nitems : 0u;
+    if (p.irange == 1u) i_e = min(i_e, *p.nitems_a);
+    if (p.irange == 2u) i_b = min(i_e, *p.nitems_a);
+    const uint32_t i_lo = i_b + uint32_t(uint64_t(i_e - i_b) * xcd / 8u);
+    const uint32_t i_hi = i_b + uint32_t(uint64_t(i_e - i_b) * (xcd + 1u) / 8u);
     uint64_t* buf = s_buf[wave];
     uint32_t* cnt = s_cnt[wave];
     float* stp = s_tp[wave];
     const uint32_t K = p.K;
     const uint32_t col = lane & 15u, grp = lane >> 4;
     const float kInf = __int_as_float(0x7F800000);
-    const uint32_t n_seed = p.sitems && *p.ok ? min(*p.nseed, p.nseed_cap) : 0u;
+    const uint32_t n_seed = p.sitems && *p.ok && p.seeds_on ? min(*p.nseed, p.nseed_cap) : 0u;
     uint32_t seed_id = blockIdx.x, item_id = i_lo + k8;
     for (;;) {
         BfItem it;
@@ -3490,23 +3503,24 @@ __device__ void bf_float_items(const BfHArgs& p) {
         const uint32_t cell = sa.scell[it.sub];
         const uint32_t qb = 16u * wave;
         const uint32_t nqb = it.nq > qb ? min(16u, it.nq - qb) : 0u;   // wave-uniform
-        // Owner state: lane < nqb owns query qb + lane; its kept keys
-        // (d' << 32 | row, ascending) live in s_tk.
+        // Owner state: lane < nqb owns query qb + lane.  Its kept keys
+        // (d' << 32 | row, ascending, kBfHKT of them) are spread over the
+        // four lanes of its column: lane col + 16 g holds keys 8 g .. 8 g + 7.
         const bool own_live = lane < nqb;
         const uint32_t own_q = own_live ? p.bq[it.qbase + qb + lane] : 0u;
         const float own_eps2 = own_live ? 2.0f * p.eps[own_q] : 0.0f;
         const uint32_t gb =
             own_live ? __hip_atomic_load(&p.gbound[own_q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0xFFFFFFFFu;
         const float own_bnd = gb == 0xFFFFFFFFu ? kInf : __uint_as_float(gb);
-        uint64_t* tk = s_tk[wave][col];
+        uint64_t tk[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) tk[k] = kKeySent;
         float kth = kInf;
         if (nqb) {
             wave_fence();
             if (lane < 16u) {
                 cnt[lane] = 0;
                 stp[lane] = own_live ? own_bnd + own_eps2 : -1.0f;
-#pragma unroll
-                for (uint32_t k = 0; k < kBfHKT; ++k) tk[k] = kKeySent;
             }
 #pragma unroll
             for (int w = 0; w < AW; ++w) {
@@ -3544,24 +3558,44 @@ __device__ void bf_float_items(const BfHArgs& p) {
             bhi[w] = nqb ? s_bnd[wave][2 * w + 1][col] : 0u;
         }
         float tp = nqb ? stp[col] : -1.0f;
-        // Owner: insert the buffered survivors of its query into its kept
-        // keys and publish the new threshold min(bound, K-th) + 2 eps.
+        // Insert the buffered survivors of every column's query into its
+        // kept keys, and the owner publishes the new threshold
+        // min(bound, K-th) + 2 eps.  A cascade over the column's four
+        // lanes: at step s lane col + 16 g inserts into its 8 keys what lane
+        // col + 16 (g - 1) pushed out at step s - 1 (lane col: the buffer's
+        // entry s), and pushes out its largest; what the last lane pushes
+        // out is dropped.  Each segment sees the entries in buffer order, so
+        // the result is the sequential insertion's: the kBfHKT smallest.
         auto drain = [&]() {
             wave_fence();
-            if (lane < 16u) {
-                const uint32_t n = cnt[lane];
-                for (uint32_t e = 0; e < n; ++e) {
-                    const uint64_t c = buf[lane * BQ + e];
-                    if (c >= tk[kBfHKT - 1]) continue;
-                    uint32_t j = kBfHKT - 1;
-                    while (j > 0 && tk[j - 1] > c) {
-                        tk[j] = tk[j - 1];
-                        --j;
-                    }
-                    tk[j] = c;
+            const uint32_t n = cnt[col];
+            uint32_t nm = n;
+#pragma unroll
+            for (uint32_t o = 1; o < 16u; o <<= 1) nm = max(nm, uint32_t(__shfl_xor(int(nm), int(o), 64)));
+            nm = __builtin_amdgcn_readfirstlane(nm);
+            uint64_t pass = kKeySent;
+            uint64_t nxt = grp == 0u && n ? buf[col * BQ] : kKeySent;
+            for (uint32_t st = 0; st < nm + 3u; ++st) {
+                uint64_t c = grp == 0u ? nxt : pass;
+                if (grp == 0u) nxt = st + 1u < n ? buf[col * BQ + st + 1u] : kKeySent;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const bool lt = c < tk[k];
+                    const uint64_t v = tk[k];
+                    tk[k] = lt ? c : v;
+                    c = lt ? v : c;
                 }
+                pass = shfl64(c, (lane - 16u) & 63u);
+            }
+            // the K-th key: key K - 1 of the column, in lane col + 16 ((K - 1) / 8)
+            uint64_t kl = tk[0];
+#pragma unroll
+            for (int k = 1; k < 8; ++k)
+                if (uint32_t(k) == ((K - 1u) & 7u)) kl = tk[k];
+            const uint64_t kk = shfl64(kl, col + 16u * ((K - 1u) >> 3));
+            wave_fence();
+            if (lane < 16u) {
                 cnt[lane] = 0;
-                const uint64_t kk = tk[K - 1];
                 if (kk != kKeySent) kth = __uint_as_float(uint32_t(kk >> 32));
                 if (own_live) stp[lane] = fminf(own_bnd, kth) + own_eps2;
             }
@@ -3621,19 +3655,29 @@ __device__ void bf_float_items(const BfHArgs& p) {
         }
         if (nqb) {
             drain();
+            // Keys within the query's limit (a prefix of the ascending
+            // keys: the lane's count is 8 in the segments before the last
+            // one that has any); if all kBfHKT are within it, keys beyond
+            // may have been dropped.
+            const float lim = __shfl(fminf(own_bnd, kth) + own_eps2, int(col), 64);
+            uint32_t kseg = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                kseg += tk[k] != kKeySent && __uint_as_float(uint32_t(tk[k] >> 32)) <= lim ? 1u : 0u;
+            uint32_t keep = kseg + uint32_t(__shfl_xor(int(kseg), 16, 64));
+            keep += uint32_t(__shfl_xor(int(keep), 32, 64));
+            uint64_t base = 0;
             if (own_live) {
                 if (kth != kInf) atomicMin(&p.gbound[own_q], __float_as_uint(kth));
-                // keys within the query's limit; if the last kept key is
-                // within it too, keys beyond may have been dropped
-                const float lim = fminf(own_bnd, kth) + own_eps2;
-                uint32_t keep = 0;
-                while (keep < kBfHKT && tk[keep] != kKeySent && __uint_as_float(uint32_t(tk[keep] >> 32)) <= lim)
-                    ++keep;
                 if (keep == kBfHKT) p.over[own_q] = 1u;
-                if (keep) {
-                    const size_t slot = size_t(p.part_off[own_q]) * kBfHKT + atomicAdd(&p.pcnt[own_q], keep);
-                    for (uint32_t k = 0; k < keep; ++k) p.part[slot + k] = tk[k];
-                }
+                if (keep) base = uint64_t(p.part_off[own_q]) * kBfHKT + atomicAdd(&p.pcnt[own_q], keep);
+            }
+            base = shfl64(base, col);
+            if (col < nqb) {
+                uint64_t* dst = p.part + base + 8u * grp;
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    if (uint32_t(k) < kseg) dst[k] = tk[k];
             }
             wave_fence();
         }
@@ -3700,12 +3744,15 @@ __global__ __launch_bounds__(64) void k_bf_f16_final(TravArgs p, BfHFinal f) {
         const uint64_t sm = ballot(surv);
         if (!sm) continue;
         uint32_t rs = 0, rt = lane;
+        // ranks in the merged order, ties to the top entry, then to the
+        // lower lane: a permutation even if a key repeats
         for (uint64_t m = sm; m; m &= m - 1) {
-            const uint64_t kk = readlane64(c, __builtin_ctzll(m));
-            rs += kk < c;
+            const uint32_t j = __builtin_ctzll(m);
+            const uint64_t kk = readlane64(c, j);
+            rs += kk < c || (kk == c && j < lane);
             rt += kk < top;
         }
-        for (uint32_t t = 0; t < K; ++t) rs += readlane64(top, t) < c;
+        for (uint32_t t = 0; t < K; ++t) rs += readlane64(top, t) <= c;
         wave_sync();
         if (surv && rs < K) T[rs] = c;
         if (lane < K && rt < K) T[rt] = top;
@@ -3780,12 +3827,15 @@ __global__ __launch_bounds__(64) void k_bf_final(BfFinalArgs p) {
         const uint64_t sm = ballot(surv);
         if (!sm) continue;
         uint32_t rs = 0, rt = lane;
+        // ranks in the merged order, ties to the top entry, then to the
+        // lower lane: a permutation even if a key repeats
         for (uint64_t m = sm; m; m &= m - 1) {
-            const uint64_t kk = readlane64(c, __builtin_ctzll(m));
-            rs += kk < c;
+            const uint32_t j = __builtin_ctzll(m);
+            const uint64_t kk = readlane64(c, j);
+            rs += kk < c || (kk == c && j < lane);
             rt += kk < top;
         }
-        for (uint32_t t = 0; t < K; ++t) rs += readlane64(top, t) < c;
+        for (uint32_t t = 0; t < K; ++t) rs += readlane64(top, t) <= c;
         __syncthreads();
         if (surv && rs < K) T[rs] = c;
         if (lane < K && rt < K) T[rt] = top;
