@@ -1121,6 +1121,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
     const bool gemm_h = !gemm && ix->hf && b->qnf.n == Q && gf::bf_float_supported(fvt, ix->D, ix->AW, K);
     const bool sched_bf = gemm || gemm_h;
     const uint32_t KP = gemm_h ? gf::kBfHKT : K;   // keys per (query, item) in the partial area
+    const uint32_t seed_tiles = gemm_h ? gf::kBfHSeedTiles : gf::kBfSeedTiles;
     const uint32_t NS = ix->NS;
     b->pass_pending = sched_bf && !b->sel_exact;
     if (sched_bf) {
@@ -1139,10 +1140,12 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         if (b->scnt.n < NS) {
             b->scnt.alloc(NS);
             // a seed sub-cell s with ns queries makes ceil(ns / 64) items per
-            // chunk of kBfSeedTiles tiles; every query seeds one sub-cell
+            // chunk of seed tiles (sized for the smaller chunk of the two
+            // routes); every query seeds one sub-cell
             uint32_t tmax = 0;
             for (uint32_t s = 0; s < NS; ++s) tmax = std::max(tmax, ix->stile_h[s + 1] - ix->stile_h[s]);
-            const size_t chunks = (tmax + gf::kBfSeedTiles - 1) / gf::kBfSeedTiles;
+            const uint32_t sch = std::min(gf::kBfSeedTiles, gf::kBfHSeedTiles);
+            const size_t chunks = (tmax + sch - 1) / sch;
             b->sitems.alloc((size_t(Q) / gf::kBfQB + NS + 1) * std::max<size_t>(chunks, 1));
         }
         if (b->part.n < b->pair_cap * KP) b->part.alloc(b->pair_cap * KP);
@@ -1180,7 +1183,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
             gf::BfSeedArgs sd{};
             sd.sa = sc.sa; sd.Q = Q; sd.postfilter = sc.postfilter; sd.counts = sc.counts; sd.little = sc.little;
             sd.cells = b->cells.p; sd.lo = sc.lo; sd.hi = sc.hi; sd.bfm = sc.bfm; sd.bP = sc.bP;
-            sd.qlist = sc.qlist; sd.qrange = sc.qrange; sd.qcap = b->qcap; sd.tch = gf::kBfSeedTiles;
+            sd.qlist = sc.qlist; sd.qrange = sc.qrange; sd.qcap = b->qcap; sd.tch = seed_tiles;
             sd.itch = gf::kBfMaxItemTiles;
             sd.scnt = b->scnt.p; sd.bq = b->bq.p; sd.nsub = b->nsub.p;
             sd.rq = b->rq.p; sd.rseed = b->rseed.p; sd.rlo = b->rlo.p; sd.rhi = b->rhi.p;
@@ -1208,7 +1211,7 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
         GF_HIP(gf::launch_bfitems(b->bcnt.p, b->bin.p, b->bstart.p, b->qcap, ix->stile.p, gf::kBfMaxItemTiles, NS, b->icnt.p, b->ioff.p,
                                   b->items.p, tot + 4, tot + 3, true, st, seeds ? b->scnt.p : nullptr,
                                   b->sitems.p, tot + 5, scap, two ? ix->sorder.p : nullptr, two ? ix->ns1 : 0u,
-                                  two ? tot + 6 : nullptr, gf::kBfSeedTiles));
+                                  two ? tot + 6 : nullptr, seed_tiles));
         if (gemm_h) {
             GF_HIP(gf::launch_zero_u32(b->hover.p, Q, st));
             gf::BfHArgs ha{};
