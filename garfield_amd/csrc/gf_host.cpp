@@ -1228,9 +1228,9 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
             // Binary16 rows: the seeds alone, then (two passes) the
             // first-pass sub-cells' items, then the rest, each launch
             // starting from the bounds the earlier ones left in gbound
-            // (C4, 768-d: 6.1 ms against 7.8 ms in one launch).  fp32 rows:
-            // one launch, seeds first in each workgroup (C3, 96-d: 6.0 ms
-            // against 7.4 ms in three).
+            // (C4, 768-d: 5.5 ms against 7.6 ms in one launch).  fp32 rows:
+            // one launch, seeds first in each workgroup (C3, 96-d: 5.9 ms
+            // against 7.3 ms in three).
             const bool split = fvt == 1;
             if (seeds && split) {
                 ha.irange = 3;
