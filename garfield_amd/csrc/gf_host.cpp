@@ -83,6 +83,7 @@ void build_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, c
     ix.tmeta.upload(sh.tmeta);
     ix.sorder.upload(sh.sorder);
     ix.ns1 = sh.ns1;
+    ix.shash_h = std::move(sh.shash);
     ix.sub = true;
 }
 
@@ -124,6 +125,16 @@ void quantise_i8(const float* x, uint64_t n, uint32_t D, float alpha, std::vecto
     }
 }
 
+void first_pass_order(const std::vector<uint32_t>& shash, uint32_t m, std::vector<uint32_t>& order, uint32_t& ns1) {
+    const uint32_t NS = uint32_t(shash.size());
+    order.clear();
+    for (uint32_t s = 0; s < NS; ++s)
+        if (shash[s] % m == 0u) order.push_back(s);
+    ns1 = uint32_t(order.size());
+    for (uint32_t s = 0; s < NS; ++s)
+        if (shash[s] % m != 0u) order.push_back(s);
+}
+
 bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, const std::vector<uint32_t>& size,
                       const std::vector<uint32_t>& offset_h, uint32_t a, uint32_t P, SubHost& out) {
     if (a > 4) return false;
@@ -141,7 +152,8 @@ bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx,
             abase[size_t(c) * a + d] = int32_t(mn);
         }
     const uint32_t AW = (a + 1) / 2, MW = 16 * (1 + AW);
-    std::vector<uint32_t> sbase(P + 1, 0), scell, ssize, stile, tmeta, first;
+    std::vector<uint32_t> sbase(P + 1, 0), scell, ssize, stile, tmeta;
+    out.shash.clear();
     std::vector<int32_t> sbox;
     auto attr = [&](uint32_t r, uint32_t d) { return int32_t(h.attrs[size_t(gidx[r]) * a + d]); };
     for (uint32_t c = 0; c < P; ++c) {
@@ -162,11 +174,12 @@ bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx,
         for (uint32_t k = 0; k < nsc; ++k) {
             const auto& m = members[k];
             // First-pass sub-cells: grid coordinates (s_0, ..., s_{a-1}) with
-            // s_0 + 3 s_1 + 5 s_2 + 7 s_3 = 0 (mod 8), one in eight of the grid
-            // and spread over every row and column of it.
+            // h = s_0 + 3 s_1 + 5 s_2 + 7 s_3 = 0 (mod 8), one in eight of the
+            // grid and spread over every row and column of it (the float
+            // route takes h = 0 mod 4: first_pass_order).
             uint32_t h = 0;
             for (uint32_t d = 0, kk = k; d < a; ++d, kk /= S) h += (2u * (a - 1u - d) + 1u) * (kk % S);
-            first.push_back(h % 8u == 0u ? 1u : 0u);
+            out.shash.push_back(h);
             scell.push_back(c);
             ssize.push_back(uint32_t(m.size()));
             stile.push_back(uint32_t(tmeta.size() / MW));
@@ -199,12 +212,7 @@ bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx,
     stile.push_back(uint32_t(tmeta.size() / MW));
     out.AW = AW;
     out.NS = sbase[P];
-    out.sorder.clear();
-    for (uint32_t s = 0; s < out.NS; ++s)
-        if (first[s]) out.sorder.push_back(s);
-    out.ns1 = uint32_t(out.sorder.size());
-    for (uint32_t s = 0; s < out.NS; ++s)
-        if (!first[s]) out.sorder.push_back(s);
+    first_pass_order(out.shash, 8, out.sorder, out.ns1);
     out.ntile = stile.back();
     out.sbase = std::move(sbase);
     out.scell = std::move(scell);
@@ -435,6 +443,18 @@ void build_index(const gf_index_host& h, const gf_open_opts* opts, gf_index& ix)
             GF_HIP(gf::launch_tile_frec(ix.vec.p, fvt, D, ix.tmeta.p, ix.xnormf.p, ix.AW, ix.ntile, ix.frec.p,
                                         ix.stream));
             ix.hf = true;
+            // Binary16 rows' first pass (a launch of its own): one in four
+            // sub-cells (C4: 4.1-4.2 ms per search against 5.5-5.7 ms at one
+            // in eight; one in two as fast as one in four, one in sixteen
+            // 6.5 ms).  fp32 rows run one launch and keep one in eight (C3:
+            // 5.9 ms against 6.05 ms at one in four).
+            if (fvt == 1) {
+                std::vector<uint32_t> order;
+                uint32_t ns1 = 0;
+                gf::first_pass_order(ix.shash_h, gf::kBfHFirstPass, order, ns1);
+                ix.sorder.upload(order);
+                ix.ns1 = ns1;
+            }
         }
         GF_HIP(hipStreamSynchronize(ix.stream));
     }
@@ -1228,7 +1248,8 @@ static void search_resident(gf_batch* b, const gf_search_opts* opts, uint32_t* i
             // Binary16 rows: the seeds alone, then (two passes) the
             // first-pass sub-cells' items, then the rest, each launch
             // starting from the bounds the earlier ones left in gbound
-            // (C4, 768-d: 5.5 ms against 7.6 ms in one launch).  fp32 rows:
+            // (C4, 768-d, one in eight sub-cells in the first pass: 5.5 ms
+            // against 7.6 ms in one launch).  fp32 rows:
             // one launch, seeds first in each workgroup (C3, 96-d: 5.9 ms
             // against 7.3 ms in three).
             const bool split = fvt == 1;

@@ -133,6 +133,7 @@ constexpr uint32_t kBfKMax = 16;      // largest K of the MFMA route
 constexpr uint32_t kBfQB = 64;        // queries per work item
 constexpr uint32_t kBfMaxItemTiles = 65536;   // tiles per MFMA work item (keeps buffer offsets below 2^31)
 constexpr uint32_t kBfSeedTiles = 16;         // tiles per seed item: a seed sub-cell spreads over several waves
+constexpr uint32_t kBfHFirstPass = 4;         // binary16 rows' first pass: sub-cells with grid hash % 4 == 0
 constexpr uint32_t kBfHSeedTiles = 128;       // the same for the float MFMA route (measured: C4 5.6 ms at 128, 6.0 at 16)
 constexpr size_t kDirectListMax = size_t(64) << 20;   // NS x Q bound of one-pass sub-cell lists (256 MiB)
 struct BfItem {

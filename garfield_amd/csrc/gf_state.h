@@ -93,8 +93,9 @@ struct SubHost {
     uint32_t AW = 0, NS = 0, ntile = 0;
     // Brute-force pass order: the ns1 sub-cells of the first pass (about one
     // in eight of each cell's rank grid, spread over it), then the rest.
+    // shash: per sub-cell the grid hash that picks them (first_pass_order).
     uint32_t ns1 = 0;
-    std::vector<uint32_t> sorder;
+    std::vector<uint32_t> sorder, shash;
     std::vector<uint32_t> sbase, scell, ssize, stile, tmeta;
     std::vector<int32_t> sbox, abase;
 };
@@ -259,7 +260,7 @@ struct gf_index {
     // cell-major row and the packed 16-bit attribute offsets of each point.
     bool sub = false;
     uint32_t AW = 0, NS = 0, ntile = 0;
-    std::vector<uint32_t> ssize_h, stile_h;
+    std::vector<uint32_t> ssize_h, stile_h, shash_h;
     DevBuf<uint32_t> sbase, scell, ssize, stile, tmeta;
     DevBuf<uint32_t> sorder;   // sub-cells of the brute force's first pass (ns1 of them), then the rest
     uint32_t ns1 = 0;
@@ -517,6 +518,8 @@ namespace gf {
 // Sub-cells of every cell (host arrays; see build_subcells in gf_host.cpp):
 // false when the attributes do not allow them (a > 4, non-integer values, or
 // a spread of 65534 or more inside a cell).
+// The first-pass sub-cells (grid hash divisible by m), then the rest.
+void first_pass_order(const std::vector<uint32_t>& shash, uint32_t m, std::vector<uint32_t>& order, uint32_t& ns1);
 bool compute_subcells(const gf_index_host& h, const std::vector<uint32_t>& gidx, const std::vector<uint32_t>& size,
                       const std::vector<uint32_t>& offset_h, uint32_t a, uint32_t P, SubHost& out);
 // Checks shared by resident and streamed indexes, and the idx mapper
